@@ -1,0 +1,193 @@
+/*
+ * sdca_hip.h - C ABI of the MI355X (gfx950) batched prox + evaluation path.
+ *
+ * Plain C: pointers, sizes and enums only.  Every entry point replaces one
+ * loop of libsdca v0.3.1 (header-only C++11); the reference interface each
+ * one stands in for is cited beside it.  The C++ drop-in overloads with the
+ * reference's own names and signatures live in sdca_hip.hpp.
+ *
+ * Memory: by default every pointer argument is a device pointer
+ * (hipMalloc'ed or torch CUDA memory) and the work is enqueued on `stream`
+ * (a hipStream_t, NULL = the default stream) without a host synchronisation.
+ * With SDCA_HOST_PTR the arrays are host memory: the library stages them
+ * through device buffers and returns after the results are copied back.
+ *
+ * Errors: every function returns an sdca_status; the message of the last
+ * failure on the calling thread is returned by sdca_last_error().  Nothing
+ * aborts.  Argument checks mirror the Matlab front end
+ * (src/matlab/mex_prox.cpp:132-136): rhs >= 0, rho >= 0, alpha > 0,
+ * 1 <= k <= m, 1 <= p <= m - 1 (p only for the two-block operator).
+ */
+#ifndef SDCA_HIP_H
+#define SDCA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SDCA_HIP_ABI_VERSION 1
+
+typedef enum sdca_status {
+  SDCA_OK = 0,
+  SDCA_ERR_ARG_NULL = 1,        /* a required pointer is NULL */
+  SDCA_ERR_ARG_RANGE = 2,       /* LIBSDCA:outOfRange (mex_util.h) */
+  SDCA_ERR_PRECISION = 3,       /* LIBSDCA:precision: unknown dtype */
+  SDCA_ERR_NOT_IMPLEMENTED = 4, /* e.g. long double, or an op not on this path */
+  SDCA_ERR_OUT_OF_MEMORY = 5,
+  SDCA_ERR_HIP = 6,             /* a HIP runtime call failed */
+  SDCA_ERR_PROX = 7,            /* LIBSDCA:prox: unknown operator */
+  SDCA_ERR_LABELS = 8           /* invalid labels / offsets (output.h:169-208) */
+} sdca_status;
+
+typedef enum sdca_dtype {
+  SDCA_F32 = 0,
+  SDCA_F64 = 1,
+  SDCA_LONG_DOUBLE = 2 /* valid in the reference (mex_prox.cpp:195); not on the GPU */
+} sdca_dtype;
+
+/* Operators of the Matlab prox front end (mex_prox.cpp:145-172). */
+typedef enum sdca_prox_op {
+  SDCA_PROX_KNAPSACK_EQ = 0,   /* knapsack_eq.h:143-157 */
+  SDCA_PROX_KNAPSACK_LE = 1,   /* knapsack_le.h:250-295 */
+  SDCA_PROX_TOPK_SIMPLEX = 2,  /* topk_simplex.h:100-113 */
+  SDCA_PROX_TOPK_CONE = 3,     /* topk_cone.h:187-199 */
+  SDCA_PROX_ENTROPY = 4,       /* entropy.h:85-98 */
+  SDCA_PROX_ENTROPY_NORM = 5,  /* entropy_norm.h:315-328 */
+  SDCA_PROX_TOPK_ENTROPY = 6,  /* topk_entropy.h:306-318 */
+  SDCA_PROX_TWO_SIMPLEX = 7,   /* two_simplex.h:183-196 */
+  SDCA_PROX_LAMBERT_W_EXP = 8, /* apply(dim, ..., lambert_w_exp_map), proxdef.h:386-400 */
+  /* Operators of the same front end that are not on this path yet:
+   * they return SDCA_ERR_NOT_IMPLEMENTED. */
+  SDCA_PROX_KNAPSACK_LE_BIASED = 9,
+  SDCA_PROX_TOPK_SIMPLEX_BIASED = 10,
+  SDCA_PROX_TOPK_CONE_BIASED = 11,
+  SDCA_PROX_TOPK_ENTROPY_BIASED = 12,
+  SDCA_PROX_TWO_SIMPLEX_SORT = 13
+} sdca_prox_op;
+
+/* Operator parameters; defaults as in mex_prox.cpp:121-127. */
+typedef struct sdca_prox_params {
+  double lo, hi, rhs, rho, alpha;
+  int64_t k, p;
+} sdca_prox_params;
+
+/* Per-column threshold record (proxdef.h:29-67): x <- clamp(map(x - t), lo, hi).
+ * For the two-block operator, two records per column (block a, then b). */
+typedef struct sdca_thresholds {
+  double t, lo, hi;
+} sdca_thresholds;
+
+#define SDCA_DEVICE_PTR 0u
+#define SDCA_HOST_PTR 1u
+
+/* Fills the defaults lo=0, hi=1, rhs=1, rho=1, alpha=1, k=1, p=1. */
+void sdca_prox_params_default(sdca_prox_params* params);
+
+/*
+ * Batched prox over the n contiguous columns of an m x n column-major
+ * matrix: replaces the loop prox(dim, first, last, aux, compute, params...)
+ * (proxdef.h:279-298) and its two-block form (proxdef.h:301-324).
+ *   data:   element type of in/out;
+ *   result: the reference's Result template argument (internal precision);
+ *   in/out: m*n elements each; out == in works in place like the reference;
+ *   col_p:  for SDCA_PROX_TWO_SIMPLEX, optional per-column split p (n int64
+ *           values in [1, m-1]); NULL uses params->p for every column;
+ *   thresholds: optional, n records (2n for the two-block operator) with the
+ *           computed thresholds, in double.
+ * The reference's `aux` scratch has no counterpart: scratch lives in
+ * registers and LDS.
+ */
+int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result,
+              int64_t m, int64_t n, const void* in, void* out,
+              const sdca_prox_params* params, const int64_t* col_p,
+              sdca_thresholds* thresholds, unsigned flags, void* stream);
+
+/* Objectives of the evaluation pass (objective.h:55-160). */
+typedef enum sdca_objective_kind {
+  SDCA_OBJ_HINGE_TOPK = 0,             /* l2_hinge_topk.h:11-88 */
+  SDCA_OBJ_HINGE_TOPK_SMOOTH = 1,      /* l2_hinge_topk.h:90-194 */
+  SDCA_OBJ_TOPK_HINGE = 2,             /* l2_topk_hinge.h:10-88 */
+  SDCA_OBJ_TOPK_HINGE_SMOOTH = 3,      /* l2_topk_hinge.h:90-198 */
+  SDCA_OBJ_ENTROPY = 4,                /* l2_entropy.h:15-116 */
+  SDCA_OBJ_ENTROPY_TOPK = 5,           /* l2_entropy_topk.h:11-109 */
+  SDCA_OBJ_MULTILABEL_HINGE = 6,       /* l2_multilabel_hinge.h:10-98 */
+  SDCA_OBJ_MULTILABEL_HINGE_SMOOTH = 7,/* l2_multilabel_hinge.h:100-210 */
+  SDCA_OBJ_MULTILABEL_ENTROPY = 8      /* l2_multilabel_entropy.h:10-111 */
+} sdca_objective_kind;
+
+typedef struct sdca_objective {
+  int32_t kind;   /* sdca_objective_kind */
+  int32_t reserved;
+  double c;       /* loss weight c = 1 / (lambda n) */
+  double gamma;   /* smoothing (smooth objectives) */
+  int64_t k;      /* top-k (top-k objectives) */
+} sdca_objective;
+
+/* One eval record (eval/types.h:219-332) without the timing fields. */
+typedef struct sdca_eval_record {
+  double primal, dual;
+  double primal_loss, dual_loss;
+  double primal_regularizer, dual_regularizer;
+  double rank_loss;   /* multilabel only (eval/types.h:317-332) */
+} sdca_eval_record;
+
+/*
+ * Whole-dataset evaluation for feature input: replaces evaluate_dataset
+ * (eval.h:15-51) for feature_input with multiclass or multilabel output.
+ * Computes scores = W' X (W: d x m, X: d x n, both column-major), then per
+ * example the dual loss, the top-k count histogram (multiclass) or rank loss
+ * (multilabel) and the primal loss of each of the n_obj objectives, and
+ * finishes each record as eval_end does (eval/core.h:43-95).
+ *   A:       m x n dual variables, or NULL for all zeros;
+ *   W0:      d x m initial primal variables (prox mode), or NULL;
+ *   labels:  multiclass: n labels in [0, m); multilabel: CSR labels;
+ *   offsets: NULL for multiclass; n+1 CSR offsets for multilabel;
+ *   records: n_obj host records;
+ *   accuracy: optional host array of m: top-(i+1) accuracy (after
+ *           partial_sum and 1/n, eval/core.h:65-68), multiclass only;
+ *   per_example: optional, n * n_obj * 2 doubles: (primal, dual) loss of
+ *           each example and objective before the loss coefficient.
+ * The objectives must all be multiclass or all multilabel.
+ */
+int sdca_eval_features(const sdca_objective* objs, int n_obj,
+                       sdca_dtype data, sdca_dtype result,
+                       int64_t d, int64_t m, int64_t n,
+                       const void* X, const void* W, const void* A,
+                       const void* W0, const int64_t* labels,
+                       const int64_t* offsets, sdca_eval_record* records,
+                       double* accuracy, double* per_example,
+                       unsigned flags, void* stream);
+
+/*
+ * The same evaluation from precomputed scores S (m x n column-major), with
+ * the primal regularizer 0.5 <W, W> (- <W0, W>) supplied by the caller:
+ * the per-example part of evaluate_dataset (eval.h:36-47).  Used to check
+ * the epilogue bit for bit on identical scores.
+ */
+int sdca_eval_scores(const sdca_objective* objs, int n_obj,
+                     sdca_dtype data, sdca_dtype result,
+                     int64_t m, int64_t n, const void* S, const void* A,
+                     const int64_t* labels, const int64_t* offsets,
+                     double primal_regularizer, double dual_regularizer,
+                     sdca_eval_record* records, double* accuracy,
+                     double* per_example, unsigned flags, void* stream);
+
+/* scores = W' X on the matrix cores (eval/scores.h:21-26 for all i at once). */
+int sdca_scores(sdca_dtype data, int64_t d, int64_t m, int64_t n,
+                const void* X, const void* W, void* S,
+                unsigned flags, void* stream);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* sdca_last_error(void);
+
+/* ABI version (SDCA_HIP_ABI_VERSION). */
+int sdca_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDCA_HIP_H */

@@ -1,0 +1,202 @@
+"""ctypes binding of the CPU checker (TEST INFRASTRUCTURE ONLY).
+
+Loads oracle/liboracle.so (the restatement) and, when it was built,
+oracle/_ref/libsdca_ref.so (our shim over the reference headers).  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module; the product package never does.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libsdca_ref.so")
+REFERENCE_TREE = "/root/reference"
+
+F32, F64 = 0, 1
+OPS = {
+    "knapsack_eq": 0, "knapsack_le": 1, "topk_simplex": 2, "topk_cone": 3,
+    "entropy": 4, "entropy_norm": 5, "topk_entropy": 6, "two_simplex": 7,
+    "lambert_w_exp": 8,
+}
+OBJECTIVES = {
+    "hinge_topk": 0, "hinge_topk_smooth": 1, "topk_hinge": 2,
+    "topk_hinge_smooth": 3, "entropy": 4, "entropy_topk": 5,
+    "multilabel_hinge": 6, "multilabel_hinge_smooth": 7,
+    "multilabel_entropy": 8,
+}
+
+
+class ProxParams(ctypes.Structure):
+    _fields_ = [("lo", ctypes.c_double), ("hi", ctypes.c_double),
+                ("rhs", ctypes.c_double), ("rho", ctypes.c_double),
+                ("alpha", ctypes.c_double), ("k", ctypes.c_int64),
+                ("p", ctypes.c_int64)]
+
+
+class Objective(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("c", ctypes.c_double), ("gamma", ctypes.c_double),
+                ("k", ctypes.c_int64)]
+
+
+class EvalRecord(ctypes.Structure):
+    _fields_ = [("primal", ctypes.c_double), ("dual", ctypes.c_double),
+                ("primal_loss", ctypes.c_double), ("dual_loss", ctypes.c_double),
+                ("primal_regularizer", ctypes.c_double),
+                ("dual_regularizer", ctypes.c_double),
+                ("rank_loss", ctypes.c_double)]
+
+
+def build(with_reference=True):
+    """Compile liboracle.so, and the reference shim when the tree exists."""
+    subprocess.check_call(["make", "-s", "-B", "-C", HERE, "all"])
+    if with_reference and os.path.isdir(os.path.join(REFERENCE_TREE, "include")):
+        subprocess.check_call(["make", "-s", "-B", "-C", HERE, "ref"])
+
+
+_libs = {}
+
+
+def _load(path):
+    if path not in _libs:
+        lib = ctypes.CDLL(path)
+        _libs[path] = lib
+    return _libs[path]
+
+
+def oracle():
+    if not os.path.exists(ORACLE_SO):
+        build(with_reference=False)
+    return Library(_load(ORACLE_SO), "oracle")
+
+
+def reference():
+    """The reference shim, or None when it was not built."""
+    if not os.path.exists(REF_SO):
+        return None
+    return Library(_load(REF_SO), "ref")
+
+
+def make_params(lo=0.0, hi=1.0, rhs=1.0, rho=1.0, alpha=1.0, k=1, p=1):
+    return ProxParams(lo, hi, rhs, rho, alpha, k, p)
+
+
+def make_objectives(objs):
+    """objs: list of (name, c, gamma, k)."""
+    arr = (Objective * len(objs))()
+    for i, (name, c, gamma, k) in enumerate(objs):
+        arr[i] = Objective(OBJECTIVES[name], 0, c, gamma, k)
+    return arr
+
+
+def _dt(a):
+    return F32 if a.dtype == np.float32 else F64
+
+
+class Library:
+    def __init__(self, lib, prefix):
+        self.lib = lib
+        self.prefix = prefix
+        self._prox = getattr(lib, prefix + "_prox")
+        self._prox.restype = ctypes.c_int
+        self._prox.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                               ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                               ctypes.POINTER(ProxParams), ctypes.c_void_p,
+                               ctypes.c_void_p, ctypes.c_int]
+        self._eval = getattr(lib, prefix + "_eval_scores")
+        self._eval.restype = ctypes.c_int
+        self._lw64 = getattr(lib, prefix + "_lambert_w_exp_f64")
+        self._lw64.restype = ctypes.c_double
+        self._lw64.argtypes = [ctypes.c_double]
+        self._lw32 = getattr(lib, prefix + "_lambert_w_exp_f32")
+        self._lw32.restype = ctypes.c_float
+        self._lw32.argtypes = [ctypes.c_float]
+
+    def prox(self, op, x, result=None, params=None, col_p=None,
+             thresholds=False, nthreads=1):
+        """In-place batched prox over the columns of x (m x n, Fortran order,
+        given as an (n, m) C-contiguous array: row j = column j)."""
+        assert x.flags.c_contiguous
+        n, m = x.shape
+        data = _dt(x)
+        result = data if result is None else result
+        params = params or make_params()
+        thr = None
+        if thresholds:
+            cnt = 2 * n if op == "two_simplex" else n
+            thr = np.zeros((cnt, 3), dtype=np.float64)
+        cp = None
+        if col_p is not None:
+            cp = np.ascontiguousarray(col_p, dtype=np.int64)
+        rc = self._prox(OPS[op], data, result, m, n, x.ctypes.data,
+                        ctypes.byref(params),
+                        cp.ctypes.data if cp is not None else None,
+                        thr.ctypes.data if thr is not None else None, nthreads)
+        if rc != 0:
+            raise RuntimeError(f"{self.prefix}_prox failed: {rc}")
+        return thr
+
+    def eval_scores(self, objs, S, A, labels, offsets=None, preg=0.0, dreg=0.0,
+                    result=None, per_example=False, nthreads=1):
+        """S, A: (n, m) C-contiguous (row i = example i's m scores)."""
+        n, m = S.shape
+        data = _dt(S)
+        result = data if result is None else result
+        objarr = make_objectives(objs)
+        recs = (EvalRecord * len(objs))()
+        acc = np.zeros(m, dtype=np.float64)
+        pe = np.zeros((n, len(objs), 2), dtype=np.float64) if per_example else None
+        labels = np.ascontiguousarray(labels, dtype=np.int64)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
+        args = [objarr, ctypes.c_int(len(objs)), ctypes.c_int(data), ctypes.c_int(result),
+                ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(S.ctypes.data),
+                ctypes.c_void_p(A.ctypes.data if A is not None else None),
+                ctypes.c_void_p(labels.ctypes.data),
+                ctypes.c_void_p(off.ctypes.data if off is not None else None),
+                ctypes.c_double(preg), ctypes.c_double(dreg), recs,
+                ctypes.c_void_p(acc.ctypes.data),
+                ctypes.c_void_p(pe.ctypes.data if pe is not None else None)]
+        if self.prefix == "oracle":
+            args.append(ctypes.c_int(nthreads))
+        rc = self._eval(*args)
+        if rc != 0:
+            raise RuntimeError(f"{self.prefix}_eval_scores failed: {rc}")
+        out = [{f: getattr(r, f) for f, _ in EvalRecord._fields_} for r in recs]
+        return out, acc, pe
+
+    def lambert_w_exp(self, x):
+        if np.asarray(x).dtype == np.float32:
+            return np.array([self._lw32(float(v)) for v in np.ravel(x)], dtype=np.float32)
+        return np.array([self._lw64(float(v)) for v in np.ravel(x)], dtype=np.float64)
+
+    # Only the restatement has these two.
+    def scores(self, X, W, nthreads=1):
+        """X: (n, d), W: (m, d) C-contiguous -> S (n, m)."""
+        n, d = X.shape
+        m = W.shape[0]
+        S = np.zeros((n, m), dtype=X.dtype)
+        f = self.lib.oracle_scores
+        f.restype = ctypes.c_int
+        rc = f(ctypes.c_int(_dt(X)), ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+               ctypes.c_void_p(X.ctypes.data), ctypes.c_void_p(W.ctypes.data),
+               ctypes.c_void_p(S.ctypes.data), ctypes.c_int(nthreads))
+        assert rc == 0
+        return S
+
+    def regularizers(self, W, W0=None, result=None):
+        data = _dt(W)
+        result = data if result is None else result
+        preg = ctypes.c_double()
+        dreg = ctypes.c_double()
+        f = self.lib.oracle_regularizers
+        f.restype = ctypes.c_int
+        rc = f(ctypes.c_int(data), ctypes.c_int(result), ctypes.c_int64(W.size),
+               ctypes.c_void_p(W.ctypes.data),
+               ctypes.c_void_p(W0.ctypes.data if W0 is not None else None),
+               ctypes.byref(preg), ctypes.byref(dreg))
+        assert rc == 0
+        return preg.value, dreg.value

@@ -1,0 +1,571 @@
+// CPU restatement of libsdca's batched prox operators and evaluation pass.
+//
+// TEST INFRASTRUCTURE ONLY.  This header (and liboracle.so built from it) is
+// the checker that the HIP path is compared against.  Only tests/,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
+// product library (libsdca_amd) never links or calls it.
+//
+// Every function restates one reference function step by step, with the same
+// element types, comparison predicates and STL partition/selection calls, so
+// that the results match the reference headers bit for bit when compiled with
+// the same standard library.  Citations are relative to the reference tree
+// (libsdca v0.3.1).  The build is -O3 without -ffast-math and without
+// SDCA_ACCURATE_MATH, which is the reference's shipped macro set.
+//
+// Pins (tests/test_oracle_*.py):
+//   * against the reference headers themselves (oracle/_ref, built from
+//     /root/reference where that tree exists) on random and edge inputs;
+//   * against committed golden vectors made from the same build
+//     (tests/golden/);
+//   * against closed forms and brute force: sort-based simplex projection,
+//     KKT checks by enumeration of (|U|, |M|) for the top-k cone/simplex,
+//     softmax for the entropic projection, mpmath Lambert W, the Omega known
+//     answer and the two-simplex regression vector of the reference tests.
+#ifndef SDCA_ORACLE_HPP
+#define SDCA_ORACLE_HPP
+
+#include <algorithm>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <iterator>
+#include <limits>
+#include <numeric>
+#include <utility>
+#include <vector>
+
+namespace orc {
+
+// ---------------------------------------------------------------------------
+// Threshold record (proxdef.h:29-67).  Over the permuted scratch copy,
+// [begin, first) is fixed at hi, [first, last) is free and [last, end) is
+// fixed at lo.  `kind` selects the elementwise map of the clamp pass
+// (proxdef.h:164-196): 0 = identity, 1 = exp, 2 = lambert_w_exp.
+// ---------------------------------------------------------------------------
+template <class R, class It>
+struct thr {
+  R t, lo, hi;
+  It first, last;
+  int kind;
+};
+
+template <class R, class It>
+inline thr<R, It> make_thr(R t, R lo, R hi, It first, It last, int kind = 0) {
+  thr<R, It> r;
+  r.t = t; r.lo = lo; r.hi = hi; r.first = first; r.last = last; r.kind = kind;
+  return r;
+}
+
+// exp_traits (log_exp.h:27-60): smallest argument with a normal exp().
+template <class T> struct exp_min_arg;
+template <> struct exp_min_arg<float> {
+  static float get() { return -8.733654022216796875000000e+01f; }
+};
+template <> struct exp_min_arg<double> {
+  static double get() { return std::log(std::numeric_limits<double>::min()); }
+};
+template <> struct exp_min_arg<long double> {
+  static long double get() { return -1.135513711193302405799699e+04L; }
+};
+
+// x * log(x) with 0 log 0 = 0 (log_exp.h:76-80).
+template <class T> inline T x_log_x(T x) { return (x > 0) ? x * std::log(x) : 0; }
+
+// ---------------------------------------------------------------------------
+// Lambert W of exp(x) (lambert.h:31-203).
+// ---------------------------------------------------------------------------
+template <class T>
+inline T lw_step5(T w, T y) {  // order-5 Householder step, lambert.h:31-42
+  T f0 = w - y, f1 = 1 + y;
+  T f11 = f1 * f1, f0y = f0 * y;
+  T f00y = f0 * f0y;
+  return w - 4 * f0 * (6 * f1 * (f11 + f0y) + f00y)
+    / (f11 * (24 * f11 + 36 * f0y) + f00y * (14 * y + f0 + 8));
+}
+
+template <class T>
+inline T exp_approx(T x) {  // (1 + x/1024)^1024, lambert.h:53-62
+  T y = 1 + x / static_cast<T>(1024);
+  for (int i = 0; i < 10; ++i) y *= y;
+  return y;
+}
+
+inline float lambert_w_exp(float x) {  // lambert.h:77-106
+  float w;
+  if (x > -1) {
+    if (x <= 8) {
+      w = lw_step5(x, 1.0f);
+    } else {
+      return (x <= 536870912) ? lw_step5(x - std::log(x), x) : x;
+    }
+  } else {
+    if (x > -18) {
+      w = exp_approx(x);
+    } else {
+      return (x > -104) ? std::exp(x) : 0.0f;
+    }
+  }
+  return lw_step5(w, std::exp(x - w));
+}
+
+template <class T>
+inline T lambert_w_exp_wide(T x) {  // double and long double, lambert.h:121-203
+  T w;
+  if (x > 0) {
+    if (x <= 4) {
+      w = lw_step5(x, static_cast<T>(1));
+    } else if (x <= static_cast<T>(576460752303423488.0L)) {
+      w = x - std::log(x);
+      w = lw_step5(w, x);
+    } else {
+      return x;
+    }
+  } else {
+    if (x > -36) {
+      w = exp_approx(x);
+      if (x > -20) w = lw_step5(w, exp_approx(x - w));
+    } else {
+      return (x > -746) ? std::exp(x) : static_cast<T>(0);
+    }
+  }
+  return lw_step5(w, std::exp(x - w));
+}
+inline double lambert_w_exp(double x) { return lambert_w_exp_wide(x); }
+inline long double lambert_w_exp(long double x) { return lambert_w_exp_wide(x); }
+
+// ---------------------------------------------------------------------------
+// log-sum-exp family (log_exp.h:88-338).
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline R lse_at(It first, It last, It mx, R& s) {  // log_exp.h:134-152
+  s = 0;
+  R m = static_cast<R>(*mx);
+  for (It a = first; a != mx; ++a) s += std::exp(static_cast<R>(*a) - m);
+  for (It a = mx + 1; a != last; ++a) s += std::exp(static_cast<R>(*a) - m);
+  return m + std::log1p(s);
+}
+
+template <class R, class It>
+inline R lse(It first, It last) {  // log_exp.h:112-122
+  if (first == last) return 0;
+  R s;
+  return lse_at<R>(first, last, std::max_element(first, last), s);
+}
+
+template <class R, class It>
+inline R lse_both(It first, It last, It mx, R& l, R& l1) {  // log_exp.h:287-308
+  R s;
+  l = lse_at<R>(first, last, mx, s);
+  R m = static_cast<R>(*mx);
+  l1 = std::exp(-m);
+  l1 = std::isfinite(l1) ? m + std::log1p(s + l1) : 0;
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// Continuous quadratic knapsack, Kiwiel variable fixing (knapsack_eq.h:25-109).
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline thr<R, It> knapsack_eq(It first, It last, R lo, R hi, R rhs) {
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), std::abs(rhs));
+  auto m = std::distance(first, last);
+  R t = (std::accumulate(first, last, static_cast<R>(0)) - rhs)
+        / static_cast<R>(m);
+  It free_first(first), free_last(last);
+  for (;;) {
+    R cut = lo + t;
+    It lo_begin = std::partition(free_first, free_last,
+                                 [=](const R x) { return x > cut; });
+    R sum_lo = std::accumulate(lo_begin, free_last, static_cast<R>(0));
+    auto n_lo = std::distance(lo_begin, free_last);
+    cut = hi + t;
+    It hi_end = std::partition(free_first, lo_begin,
+                               [=](const R x) { return x > cut; });
+    R sum_hi = std::accumulate(free_first, hi_end, static_cast<R>(0));
+    auto n_hi = std::distance(free_first, hi_end);
+
+    R s_hi = static_cast<R>(n_hi) * hi;
+    R s_lo = static_cast<R>(n_lo) * lo;
+    R infeas = sum_hi + sum_lo - (s_hi + s_lo) - static_cast<R>(n_hi + n_lo) * t;
+    R next;
+    if (n_hi > 0 && infeas > eps) {
+      free_first = hi_end;
+      next = static_cast<R>(m) * t - sum_hi + s_hi;
+      m -= n_hi;
+    } else if (n_lo > 0 && infeas < -eps) {
+      free_last = lo_begin;
+      next = static_cast<R>(m) * t - sum_lo + s_lo;
+      m -= n_lo;
+    } else {
+      free_first = hi_end;
+      free_last = lo_begin;
+      break;
+    }
+    if (m > 0) {
+      t = next / static_cast<R>(m);
+    } else {
+      break;
+    }
+  }
+  return make_thr(t, lo, hi, free_first, free_last);
+}
+
+// Inequality knapsack (knapsack_le.h:17-44).
+template <class R, class It>
+inline thr<R, It> knapsack_le(It first, It last, R lo, R hi, R rhs) {
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), std::abs(rhs));
+  It mid_first = std::partition(first, last, [=](const R x) { return x >= hi; });
+  It mid_last = std::partition(mid_first, last, [=](const R x) { return x > lo; });
+  R s = std::accumulate(mid_first, mid_last, static_cast<R>(0))
+      + hi * static_cast<R>(std::distance(first, mid_first))
+      + lo * static_cast<R>(std::distance(mid_last, last));
+  if (s > rhs + eps) return knapsack_eq(first, last, lo, hi, rhs);
+  return make_thr(static_cast<R>(0), lo, hi, mid_first, mid_last);
+}
+
+// ---------------------------------------------------------------------------
+// Top-k cone (topk_cone.h:18-157).
+// ---------------------------------------------------------------------------
+enum class proj { zero, constant, general };
+
+template <class R, class It>
+inline proj cone_special_cases(It first, It last, std::ptrdiff_t k, R div,
+                               thr<R, It>& out) {
+  typedef typename std::iterator_traits<It>::value_type D;
+  It k_last = first + k;
+  std::nth_element(first, k_last - 1, last, std::greater<D>());
+  const R eps = 16 * std::numeric_limits<R>::epsilon();
+  R sum_k = std::accumulate(first, k_last, static_cast<R>(0));
+  if (sum_k <= eps) {
+    out = make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                   first, first);
+    return proj::zero;
+  }
+  R hi = sum_k / div;
+  R t = static_cast<R>(*(k_last - 1)) - hi;
+  if (k == std::distance(first, last) ||
+      t >= static_cast<R>(*std::max_element(k_last, last)) - eps) {
+    out = make_thr(t, static_cast<R>(0), hi, k_last, k_last);
+    return proj::constant;
+  }
+  return proj::general;
+}
+
+template <class R, class It>
+inline thr<R, It> cone_search(It first, It last, std::ptrdiff_t k) {
+  typedef typename std::iterator_traits<It>::value_type D;
+  std::sort(first, last, std::greater<D>());
+  It k_last = first + k;
+  R k_u = static_cast<R>(k);
+  R min_u = +std::numeric_limits<R>::infinity();
+  R num_u = 0, sum_u = 0;
+  const R eps = 16 * std::numeric_limits<R>::epsilon();
+  for (It mf = first;;) {
+    R min_m = +std::numeric_limits<R>::infinity();
+    R max_m = -std::numeric_limits<R>::infinity();
+    R sum_m = 0, num_m_sum_u = 0;
+    R den = k_u * k_u;
+    R k_u_sum_u = k_u * sum_u;
+    for (It ml = mf;;) {
+      R t = (num_u * sum_m - k_u_sum_u) / den;
+      R hi = (num_m_sum_u + k_u * sum_m) / den;
+      R tt = hi + t;
+      if (max_m - eps <= tt && tt <= min_u + eps) {
+        if (t <= min_m + eps &&
+            ((ml == last) || static_cast<R>(*ml) - eps <= t)) {
+          return make_thr(t, static_cast<R>(0), hi, mf, ml);
+        }
+      }
+      if (ml == last) break;
+      min_m = static_cast<R>(*ml);
+      max_m = static_cast<R>(*mf);
+      sum_m += min_m;
+      num_m_sum_u += sum_u;
+      den += num_u;
+      ++ml;
+    }
+    if (mf == k_last) break;
+    min_u = static_cast<R>(*mf);
+    sum_u += min_u;
+    --k_u;
+    ++num_u;
+    ++mf;
+  }
+  return make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                  first, first);
+}
+
+template <class R, class It>
+inline thr<R, It> topk_cone(It first, It last, std::ptrdiff_t k) {
+  thr<R, It> out;
+  if (cone_special_cases(first, last, k, static_cast<R>(k), out) == proj::general)
+    return cone_search<R>(first, last, k);
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k simplex (topk_simplex.h:9-68).
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline bool topk_simplex_lt(It u_first, It u_last, R t, R k, R rhs, R eps) {
+  if (u_first == u_last) return t < -eps;
+  R num_u = static_cast<R>(std::distance(u_first, u_last));
+  R sum_u = std::accumulate(u_first, u_last, static_cast<R>(0));
+  return k * (sum_u + (k - num_u) * t) < rhs * num_u - eps;
+}
+
+template <class R, class It>
+inline thr<R, It> topk_simplex(It first, It last, std::ptrdiff_t k, R rhs) {
+  const R K = static_cast<R>(k), lo = 0;
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), std::abs(rhs));
+  thr<R, It> out;
+  switch (cone_special_cases(first, last, k, K, out)) {
+    case proj::zero:
+      break;
+    case proj::constant:
+      if (K * out.hi > rhs + eps) return knapsack_eq(first, last, lo, rhs / K, rhs);
+      break;
+    case proj::general: {
+      thr<R, It> t = knapsack_eq(first, last, lo, rhs / K, rhs);
+      if (topk_simplex_lt(first, t.first, t.t, K, rhs, eps))
+        return cone_search<R>(first, last, k);
+      return t;
+    }
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Entropic projections (entropy.h:19-53, entropy_norm.h:15-183).
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline thr<R, It> entropy(It first, It last, R hi, R rhs) {
+  const R eps = 16 * std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), rhs);
+  R lo(0), r(rhs), u = std::log(hi) + eps;
+  R t = lse<R>(first, last) - std::log(rhs);
+  It mf = first;
+  for (;;) {
+    R cut = t + u;
+    It it = std::partition(mf, last, [=](R a) { return a > cut; });
+    if (it == mf) break;
+    r -= hi * static_cast<R>(std::distance(mf, it));
+    mf = it;
+    if (it == last) break;
+    if (r <= eps) {
+      t = static_cast<R>(*std::max_element(mf, last)) - exp_min_arg<R>::get() + 1;
+      break;
+    }
+    t = lse<R>(mf, last) - std::log(r);
+  }
+  return make_thr(t, lo, hi, mf, last, 1);
+}
+
+template <class R, class It>
+inline R sum_w_exp_step4(It first, It last, R rhs, R t) {  // entropy_norm.h:161-176
+  R f0(0), f1(0), f2(0), f3(0);
+  const R mt = -t;
+  for (It a = first; a != last; ++a) {  // lambert.h:311-332
+    R v = lambert_w_exp(static_cast<R>(*a) + mt);
+    R d = 1 + v;
+    R d3 = d * d * d;
+    f0 += v;
+    f1 += v / d;
+    f2 += v / d3;
+    f3 += v * (1 - 2 * v) / (d3 * d * d);
+  }
+  f0 -= rhs;
+  R f02 = f0 * f2, f11 = f1 * f1;
+  return t - 3 * f0 * (2 * f11 - f02) / (6 * f1 * (f02 - f11) - f0 * (f0 * f3));
+}
+
+template <class R, class It>
+inline R solve_sum_w_exp(It first, It last, R rhs) {  // entropy_norm.h:183-236
+  R t = (std::accumulate(first, last, static_cast<R>(0)) - rhs)
+        / static_cast<R>(std::distance(first, last));
+  It u_last = last;
+  for (;;) {
+    It it = std::partition(first, u_last, [=](R a) { return a > t; });
+    if (it == u_last || it == first) break;
+    u_last = it;
+    t = (std::accumulate(first, u_last, static_cast<R>(0)) - rhs)
+        / static_cast<R>(std::distance(first, u_last));
+  }
+  const R ub = static_cast<R>(*std::max_element(first, last)) - exp_min_arg<R>::get();
+  const R eps = 16 * std::numeric_limits<R>::epsilon();
+  for (std::size_t iter = 0; iter < 32; ++iter) {
+    R prev(t);
+    t = sum_w_exp_step4(first, last, rhs, std::min(t, ub));
+    if (std::abs(prev - t) <= eps) break;
+  }
+  return t;
+}
+
+template <class R, class It>
+inline thr<R, It> entropy_norm(It first, It last, R hi, R rhs) {
+  const R eps = 16 * std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), rhs);
+  R lo(0), r(rhs), u = hi + std::log(hi) + eps;
+  R t = solve_sum_w_exp(first, last, rhs);
+  It mf = first;
+  for (;;) {
+    R cut = t + u;
+    It it = std::partition(mf, last, [=](R a) { return a > cut; });
+    if (it == mf) break;
+    r -= hi * static_cast<R>(std::distance(mf, it));
+    mf = it;
+    if (it == last) break;
+    if (r <= eps) {
+      t = static_cast<R>(*std::max_element(mf, last)) - exp_min_arg<R>::get() + 1;
+      break;
+    }
+    t = solve_sum_w_exp(mf, last, r);
+  }
+  return make_thr(t, lo, hi, mf, last, 2);
+}
+
+// Top-k entropy (topk_entropy.h:20-76).
+template <class R, class It>
+inline thr<R, It> topk_entropy(It first, It last, std::ptrdiff_t k) {
+  const R eps = 16 * std::numeric_limits<R>::epsilon();
+  const R K = static_cast<R>(k);
+  It mx = std::max_element(first, last);
+  R log_z, log_z_1;
+  lse_both(first, last, mx, log_z, log_z_1);
+  R t(log_z_1), lo(0), hi(1);
+  if (k <= 1 || static_cast<R>(*mx) - eps <= log_z - std::log(K))
+    return make_thr(t, lo, hi, first, last, 1);
+  R min_u(0), sum_u(0), k_u(K), z(0);
+  It mf = first;
+  for (std::ptrdiff_t num_u = 1; num_u < k; ++num_u) {
+    min_u = static_cast<R>(*mx);
+    sum_u += min_u;
+    std::swap(*mf, *mx);
+    ++mf;
+    --k_u;
+    mx = std::max_element(mf, last);
+    log_z = lse_at(mf, last, mx, z);
+    R tt = log_z - std::log(k_u);
+    if (static_cast<R>(*mx) - eps <= tt && tt <= min_u + eps) break;
+  }
+  R tmp = ((K - k_u) * log_z + k_u * std::log(k_u) - sum_u) / K;
+  R mxv = static_cast<R>(*mx);
+  if (tmp > mxv) {
+    R a = (1 + z) * std::exp(mxv - tmp);
+    t = tmp + std::log1p(a * K) - std::log(k_u);
+    hi = a / (1 + a * K);
+  } else {
+    R a = std::exp(tmp - mxv) / K;
+    t = mxv + std::log1p(z + a) - std::log(k_u / K);
+    hi = (1 + z) / ((1 + z + a) * K);
+  }
+  return make_thr(t, lo, hi, mf, last, 1);
+}
+
+// Two-block simplex, <1,x> = <1,y> <= rhs (two_simplex.h:18-119).
+template <class R, class It>
+inline std::pair<thr<R, It>, thr<R, It>>
+two_simplex(It a_first, It a_last, It b_first, It b_last, R rhs) {
+  R t, s, lo(0), hi(rhs);
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), rhs);
+  It x_last(a_last);
+  for (;;) {
+    t = (std::accumulate(a_first, x_last, static_cast<R>(0)) - rhs)
+        / static_cast<R>(std::distance(a_first, x_last));
+    It it = std::partition(a_first, x_last, [=](const R x) { return x > t; });
+    if (it == x_last) break;
+    x_last = it;
+  }
+  It y_last(b_last);
+  for (;;) {
+    s = (std::accumulate(b_first, y_last, static_cast<R>(0)) - rhs)
+        / static_cast<R>(std::distance(b_first, y_last));
+    It it = std::partition(b_first, y_last, [=](const R y) { return y > s; });
+    if (it == y_last) break;
+    y_last = it;
+  }
+  if (t + s >= -eps) {
+    return std::make_pair(make_thr(t, lo, hi, a_first, x_last),
+                          make_thr(s, lo, hi, b_first, y_last));
+  }
+  auto m = std::distance(a_first, x_last) + std::distance(b_first, y_last);
+  t = (+std::accumulate(a_first, x_last, static_cast<R>(0))
+       - std::accumulate(b_first, y_last, static_cast<R>(0))) / static_cast<R>(m);
+  for (;;) {
+    It x_it = std::partition(a_first, x_last, [=](const R x) { return x > t; });
+    R sum_x = std::accumulate(x_it, x_last, static_cast<R>(0));
+    auto n_x = std::distance(x_it, x_last);
+    It y_it = std::partition(b_first, y_last, [=](const R y) { return y > -t; });
+    R sum_y = std::accumulate(y_it, y_last, static_cast<R>(0));
+    auto n_y = std::distance(y_it, y_last);
+    R next, infeas = sum_x - sum_y - static_cast<R>(n_x + n_y) * t;
+    if (n_y > 0 && infeas > eps) {
+      y_last = y_it;
+      next = static_cast<R>(m) * t + sum_y;
+      m -= n_y;
+    } else if (n_x > 0 && infeas < -eps) {
+      x_last = x_it;
+      next = static_cast<R>(m) * t - sum_x;
+      m -= n_x;
+    } else {
+      x_last = x_it;
+      y_last = y_it;
+      break;
+    }
+    if (m > 0) {
+      t = next / static_cast<R>(m);
+    } else {
+      break;
+    }
+  }
+  return std::make_pair(make_thr(t, lo, hi, a_first, x_last),
+                        make_thr(-t, lo, hi, b_first, y_last));
+}
+
+// ---------------------------------------------------------------------------
+// Clamp/map pass (proxdef.h:164-196): thresholds are cast to Data first.
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline void clamp(const thr<R, It>& th, It first, It last) {
+  typedef typename std::iterator_traits<It>::value_type D;
+  const D t = static_cast<D>(th.t), lo = static_cast<D>(th.lo),
+          hi = static_cast<D>(th.hi);
+  for (It x = first; x != last; ++x) {
+    D v = *x - t;
+    if (th.kind == 1) v = std::exp(v);
+    else if (th.kind == 2) v = lambert_w_exp(v);
+    *x = std::max(lo, std::min(v, hi));
+  }
+}
+
+// <prox(x), prox(x)> and <x, prox(x)> from the threshold sets (proxdef.h:332-370).
+template <class R, class It>
+inline R dot_prox_prox(const thr<R, It>& t, It first, It last) {
+  R num_hi = static_cast<R>(std::distance(first, t.first));
+  R num_mi = static_cast<R>(std::distance(t.first, t.last));
+  R num_lo = static_cast<R>(std::distance(t.last, last));
+  R sum_mi = std::accumulate(t.first, t.last, static_cast<R>(0));
+  R dot_mi(0);
+  for (It a = t.first; a != t.last; ++a) { R x = *a; dot_mi += x * x; }
+  return t.hi * t.hi * num_hi + t.t * t.t * num_mi + t.lo * t.lo * num_lo
+       + dot_mi - static_cast<R>(2) * t.t * sum_mi;
+}
+
+template <class R, class It>
+inline R dot_x_prox(const thr<R, It>& t, It first, It last) {
+  R sum_hi = std::accumulate(first, t.first, static_cast<R>(0));
+  R sum_mi = std::accumulate(t.first, t.last, static_cast<R>(0));
+  R sum_lo = std::accumulate(t.last, last, static_cast<R>(0));
+  R dot_mi(0);
+  for (It a = t.first; a != t.last; ++a) { R x = *a; dot_mi += x * x; }
+  return t.hi * sum_hi - t.t * sum_mi + t.lo * sum_lo + dot_mi;
+}
+
+}  // namespace orc
+
+#endif

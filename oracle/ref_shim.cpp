@@ -1,0 +1,335 @@
+// C entry points over the reference headers themselves (TEST INFRASTRUCTURE
+// ONLY).  This file is our own wrapper; it is compiled with
+// -I/root/reference/include by oracle/Makefile into oracle/_ref/, which is
+// never committed.  It exists to pin the oracle restatement and to time the
+// reference CPU path for the bench's cpu_baseline.
+//
+// What is not built: the BLAS-backed parts of the evaluation (the scores
+// gemv, the regularizer dot products and the smooth objectives' dual losses,
+// math/blas.h:191-319) need an external CBLAS library, which this build does
+// not link; those entries report NaN and are pinned by closed forms instead.
+#include <cmath>
+#include <cstdint>
+#include <limits>
+#include <thread>
+#include <vector>
+
+#include "sdca/prox.h"
+#include "sdca/solver/eval/dual.h"
+#include "sdca/solver/eval/primal.h"
+#include "sdca/solver/eval/types.h"
+#include "sdca/solver/objective/l2_entropy.h"
+#include "sdca/solver/objective/l2_entropy_topk.h"
+#include "sdca/solver/objective/l2_hinge_topk.h"
+#include "sdca/solver/objective/l2_multilabel_entropy.h"
+#include "sdca/solver/objective/l2_multilabel_hinge.h"
+#include "sdca/solver/objective/l2_topk_hinge.h"
+
+#include "../include/sdca_hip.h"
+
+namespace {
+
+template <class F>
+void parallel_for(int64_t n, int nthreads, F f) {
+  if (nthreads <= 1 || n < 2 * nthreads) {
+    f(static_cast<int64_t>(0), n);
+    return;
+  }
+  std::vector<std::thread> pool;
+  int64_t chunk = (n + nthreads - 1) / nthreads;
+  for (int w = 0; w < nthreads; ++w) {
+    int64_t b = w * chunk, e = std::min(n, b + chunk);
+    if (b >= e) break;
+    pool.emplace_back(f, b, e);
+  }
+  for (auto& t : pool) t.join();
+}
+
+template <class T>
+void put(sdca_thresholds* out, int64_t j, const T& th) {
+  out[j].t = static_cast<double>(th.t);
+  out[j].lo = static_cast<double>(th.lo);
+  out[j].hi = static_cast<double>(th.hi);
+}
+
+// The reference's own batched entry points (the Matlab dispatch,
+// src/matlab/mex_prox.cpp:145-172), on columns [b, e).
+template <class D, class R>
+void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_params* p,
+             const int64_t* col_p) {
+  const R lo = static_cast<R>(p->lo), hi = static_cast<R>(p->hi), rhs = static_cast<R>(p->rhs);
+  const std::ptrdiff_t k = static_cast<std::ptrdiff_t>(p->k);
+  switch (op) {
+    case SDCA_PROX_KNAPSACK_EQ: sdca::prox_knapsack_eq(m, first, last, aux, lo, hi, rhs); break;
+    case SDCA_PROX_KNAPSACK_LE: sdca::prox_knapsack_le(m, first, last, aux, lo, hi, rhs); break;
+    case SDCA_PROX_TOPK_SIMPLEX: sdca::prox_topk_simplex(m, first, last, aux, k, rhs); break;
+    case SDCA_PROX_TOPK_CONE: sdca::prox_topk_cone<R>(m, first, last, aux, k); break;
+    case SDCA_PROX_ENTROPY: sdca::prox_entropy(m, first, last, aux, hi, rhs); break;
+    case SDCA_PROX_ENTROPY_NORM: sdca::prox_entropy_norm(m, first, last, aux, hi, rhs); break;
+    case SDCA_PROX_TOPK_ENTROPY: sdca::prox_topk_entropy<R>(m, first, last, aux, k); break;
+    case SDCA_PROX_TWO_SIMPLEX:
+      if (!col_p) {
+        sdca::prox_two_simplex(m, static_cast<std::ptrdiff_t>(p->p), first, last, aux, rhs);
+      } else {
+        // Per-column split: one batch call per column.
+        for (int64_t j = 0; first + j * m < last; ++j)
+          sdca::prox_two_simplex(m, static_cast<std::ptrdiff_t>(col_p[j]), first + j * m,
+                                 first + (j + 1) * m, aux, rhs);
+      }
+      break;
+    case SDCA_PROX_LAMBERT_W_EXP: sdca::apply(m, first, last, sdca::lambert_w_exp_map<D>()); break;
+    default: break;
+  }
+}
+
+// Per-column loop with the threshold records (same steps as proxdef.h:279-298).
+template <class D, class R>
+void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
+                     const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* out) {
+  const R lo = static_cast<R>(p->lo), hi = static_cast<R>(p->hi), rhs = static_cast<R>(p->rhs);
+  const std::ptrdiff_t k = static_cast<std::ptrdiff_t>(p->k);
+  for (int64_t j = b; j < e; ++j) {
+    D* col = x + j * m;
+    std::copy(col, col + m, aux);
+    D* al = aux + m;
+    switch (op) {
+      case SDCA_PROX_KNAPSACK_EQ: {
+        auto t = sdca::thresholds_knapsack_eq(aux, al, lo, hi, rhs);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_KNAPSACK_LE: {
+        auto t = sdca::thresholds_knapsack_le(aux, al, lo, hi, rhs);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_TOPK_SIMPLEX: {
+        auto t = sdca::thresholds_topk_simplex(aux, al, k, rhs);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_TOPK_CONE: {
+        auto t = sdca::thresholds_topk_cone<R>(aux, al, k);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_ENTROPY: {
+        auto t = sdca::thresholds_entropy(aux, al, hi, rhs);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_ENTROPY_NORM: {
+        auto t = sdca::thresholds_entropy_norm(aux, al, hi, rhs);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_TOPK_ENTROPY: {
+        auto t = sdca::thresholds_topk_entropy<R>(aux, al, k);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_TWO_SIMPLEX: {
+        std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])
+                                  : static_cast<std::ptrdiff_t>(p->p);
+        auto t = sdca::thresholds_two_simplex(aux, aux + pj, aux + pj, al, rhs);
+        sdca::prox(t.first, col, col + pj);
+        sdca::prox(t.second, col + pj, col + m);
+        put(out, 2 * j, t.first);
+        put(out, 2 * j + 1, t.second);
+        break;
+      }
+      default: break;
+    }
+  }
+}
+
+template <class D, class R>
+int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
+              const int64_t* col_p, sdca_thresholds* out, int nthreads) {
+  if (op == SDCA_PROX_LAMBERT_W_EXP) {
+    parallel_for(n, nthreads, [&](int64_t b, int64_t e) {
+      batched<D, R>(op, m, x + b * m, x + e * m, nullptr, p, nullptr);
+    });
+    return 0;
+  }
+  parallel_for(n, nthreads, [&](int64_t b, int64_t e) {
+    std::vector<D> aux(static_cast<size_t>(m));
+    if (out) {
+      with_thresholds<D, R>(op, m, b, e, x, aux.data(), p, col_p, out);
+    } else {
+      batched<D, R>(op, m, x + b * m, x + e * m, aux.data(), p, col_p ? col_p + b : nullptr);
+    }
+  });
+  return 0;
+}
+
+template <class R>
+void init_record(sdca::eval_train<R, sdca::multiclass_output>& e, int64_t m) {
+  e.accuracy.assign(static_cast<size_t>(m), 0);
+}
+template <class R>
+void init_record(sdca::eval_train<R, sdca::multilabel_output>&, int64_t) {}
+template <class R>
+void merge_record(sdca::eval_train<R, sdca::multiclass_output>& e,
+                  const sdca::eval_train<R, sdca::multiclass_output>& one) {
+  for (size_t j = 0; j < e.accuracy.size(); ++j) e.accuracy[j] += one.accuracy[j];
+}
+template <class R>
+void merge_record(sdca::eval_train<R, sdca::multilabel_output>& e,
+                  const sdca::eval_train<R, sdca::multilabel_output>& one) {
+  e.rank_loss += one.rank_loss;
+}
+
+// Per-example evaluation with the reference's eval_primal_loss /
+// eval_dual_loss (eval/primal.h, eval/dual.h) for one objective.  When
+// per-example values are requested, each example runs on a fresh record whose
+// loss fields are then added to the running totals: the same single
+// additions the reference makes, so the totals are unchanged.
+template <class Obj, class Out, class Ev, bool HasDual>
+void eval_loop(const Obj& obj, const Out& out, Ev& ev, int64_t m, int64_t n,
+               const typename Obj::data_type* S, const typename Obj::data_type* A,
+               int o, int no, double* per_example) {
+  typedef typename Obj::data_type D;
+  std::vector<D> s(static_cast<size_t>(m)), v(static_cast<size_t>(m));
+  for (int64_t i = 0; i < n; ++i) {
+    std::copy(S + i * m, S + (i + 1) * m, s.begin());
+    if (A) std::copy(A + i * m, A + (i + 1) * m, v.begin());
+    else std::fill(v.begin(), v.end(), static_cast<D>(0));
+    const sdca::size_type ii = static_cast<sdca::size_type>(i);
+    if (!per_example) {
+      if (HasDual) sdca::eval_dual_loss(ii, out, obj, v.data(), ev);
+      sdca::eval_primal_loss(ii, out, obj, s.data(), ev);
+      continue;
+    }
+    Ev one;
+    init_record(one, m);
+    if (HasDual) sdca::eval_dual_loss(ii, out, obj, v.data(), one);
+    sdca::eval_primal_loss(ii, out, obj, s.data(), one);
+    per_example[(i * no + o) * 2] = static_cast<double>(one.primal_loss);
+    per_example[(i * no + o) * 2 + 1] =
+        HasDual ? static_cast<double>(one.dual_loss) : std::numeric_limits<double>::quiet_NaN();
+    ev.primal_loss += one.primal_loss;
+    ev.dual_loss += one.dual_loss;
+    merge_record(ev, one);
+  }
+}
+
+template <class Obj, class D, class R, bool HasDual>
+void eval_one(std::false_type, const Obj& obj, int64_t m, int64_t n, const D* S,
+              const D* A, const int64_t* labels, const int64_t*, int o, int no,
+              sdca_eval_record* rec, std::vector<R>* hist, double* per_example) {
+  std::vector<sdca::size_type> lab(labels, labels + n);
+  sdca::multiclass_output out(static_cast<sdca::size_type>(m), lab);
+  sdca::eval_train<R, sdca::multiclass_output> ev;
+  init_record(ev, m);
+  eval_loop<Obj, sdca::multiclass_output, decltype(ev), HasDual>(
+      obj, out, ev, m, n, S, A, o, no, per_example);
+  obj.update_primal_loss(ev.primal_loss);
+  rec[o].primal_loss = static_cast<double>(ev.primal_loss);
+  rec[o].dual_loss = HasDual ? static_cast<double>(ev.dual_loss)
+                             : std::numeric_limits<double>::quiet_NaN();
+  rec[o].rank_loss = 0;
+  if (hist) *hist = ev.accuracy;
+}
+
+template <class Obj, class D, class R, bool HasDual>
+void eval_one(std::true_type, const Obj& obj, int64_t m, int64_t n, const D* S,
+              const D* A, const int64_t* labels, const int64_t* offsets, int o, int no,
+              sdca_eval_record* rec, std::vector<R>*, double* per_example) {
+  std::vector<sdca::size_type> lab(labels, labels + offsets[n]);
+  std::vector<sdca::size_type> off(offsets, offsets + n + 1);
+  sdca::multilabel_output out(static_cast<sdca::size_type>(m), lab, off);
+  sdca::eval_train<R, sdca::multilabel_output> ev;
+  eval_loop<Obj, sdca::multilabel_output, decltype(ev), HasDual>(
+      obj, out, ev, m, n, S, A, o, no, per_example);
+  obj.update_primal_loss(ev.primal_loss);
+  rec[o].primal_loss = static_cast<double>(ev.primal_loss);
+  rec[o].dual_loss = HasDual ? static_cast<double>(ev.dual_loss)
+                             : std::numeric_limits<double>::quiet_NaN();
+  rec[o].rank_loss = static_cast<double>(ev.rank_loss / static_cast<R>(n));
+}
+
+#define SDCA_REF_EVAL(ML, HASDUAL, OBJ)                                              \
+  eval_one<decltype(OBJ), D, R, HASDUAL>(std::integral_constant<bool, ML>(), OBJ, m, n, \
+                                         S, A, labels, offsets, o, n_obj, rec, h,     \
+                                         per_example)
+
+template <class D, class R>
+int eval_impl(const sdca_objective* objs, int n_obj, int64_t m, int64_t n, const D* S,
+              const D* A, const int64_t* labels, const int64_t* offsets, double preg,
+              double dreg, sdca_eval_record* rec, double* accuracy, double* per_example) {
+  std::vector<R> hist;
+  for (int o = 0; o < n_obj; ++o) {
+    const sdca_objective& ob = objs[o];
+    const R c = static_cast<R>(ob.c), g = static_cast<R>(ob.gamma);
+    const sdca::size_type k = static_cast<sdca::size_type>(ob.k);
+    std::vector<R>* h = (o == 0 && accuracy && !offsets) ? &hist : nullptr;
+    rec[o].rank_loss = 0;
+    switch (ob.kind) {
+      case SDCA_OBJ_HINGE_TOPK:
+        SDCA_REF_EVAL(false, true, (sdca::l2_hinge_topk<D, R>(c, k))); break;
+      case SDCA_OBJ_HINGE_TOPK_SMOOTH:
+        SDCA_REF_EVAL(false, false, (sdca::l2_hinge_topk_smooth<D, R>(c, g, k))); break;
+      case SDCA_OBJ_TOPK_HINGE:
+        SDCA_REF_EVAL(false, true, (sdca::l2_topk_hinge<D, R>(c, k))); break;
+      case SDCA_OBJ_TOPK_HINGE_SMOOTH:
+        SDCA_REF_EVAL(false, false, (sdca::l2_topk_hinge_smooth<D, R>(c, g, k))); break;
+      case SDCA_OBJ_ENTROPY:
+        SDCA_REF_EVAL(false, true, (sdca::l2_entropy<D, R>(c))); break;
+      case SDCA_OBJ_ENTROPY_TOPK:
+        SDCA_REF_EVAL(false, true, (sdca::l2_entropy_topk<D, R>(c, k))); break;
+      case SDCA_OBJ_MULTILABEL_HINGE:
+        SDCA_REF_EVAL(true, true, (sdca::l2_multilabel_hinge<D, R>(c))); break;
+      case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
+        SDCA_REF_EVAL(true, false, (sdca::l2_multilabel_hinge_smooth<D, R>(c, g))); break;
+      case SDCA_OBJ_MULTILABEL_ENTROPY:
+        SDCA_REF_EVAL(true, true, (sdca::l2_multilabel_entropy<D, R>(c))); break;
+      default: return SDCA_ERR_ARG_RANGE;
+    }
+    // objective_base::update_all (objective_base.h:116-128)
+    rec[o].primal_regularizer = preg;
+    rec[o].dual_regularizer = dreg;
+    rec[o].primal = static_cast<double>(static_cast<R>(rec[o].primal_loss) + static_cast<R>(preg));
+    rec[o].dual = static_cast<double>(static_cast<R>(rec[o].dual_loss) - static_cast<R>(dreg));
+  }
+  if (accuracy && !offsets && !hist.empty()) {
+    // eval_end: partial_sum and scaling by 1/n (eval/core.h:65-68)
+    std::partial_sum(hist.begin(), hist.end(), hist.begin());
+    R coeff(1 / static_cast<R>(n));
+    for (int64_t j = 0; j < m; ++j) accuracy[j] = static_cast<double>(hist[j] * coeff);
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ref_prox(int op, int data, int result, int64_t m, int64_t n, void* x,
+             const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* out,
+             int nthreads) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return prox_impl<float, float>(op, m, n, static_cast<float*>(x), p, col_p, out, nthreads);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return prox_impl<float, double>(op, m, n, static_cast<float*>(x), p, col_p, out, nthreads);
+  if (data == SDCA_F64 && result == SDCA_F32)
+    return prox_impl<double, float>(op, m, n, static_cast<double*>(x), p, col_p, out, nthreads);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return prox_impl<double, double>(op, m, n, static_cast<double*>(x), p, col_p, out, nthreads);
+  return SDCA_ERR_PRECISION;
+}
+
+int ref_eval_scores(const sdca_objective* objs, int n_obj, int data, int result,
+                    int64_t m, int64_t n, const void* S, const void* A,
+                    const int64_t* labels, const int64_t* offsets, double preg,
+                    double dreg, sdca_eval_record* rec, double* accuracy,
+                    double* per_example) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return eval_impl<float, float>(objs, n_obj, m, n, static_cast<const float*>(S),
+        static_cast<const float*>(A), labels, offsets, preg, dreg, rec, accuracy, per_example);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return eval_impl<float, double>(objs, n_obj, m, n, static_cast<const float*>(S),
+        static_cast<const float*>(A), labels, offsets, preg, dreg, rec, accuracy, per_example);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return eval_impl<double, double>(objs, n_obj, m, n, static_cast<const double*>(S),
+        static_cast<const double*>(A), labels, offsets, preg, dreg, rec, accuracy, per_example);
+  return SDCA_ERR_PRECISION;
+}
+
+double ref_lambert_w_exp_f64(double x) { return sdca::lambert_w_exp(x); }
+float ref_lambert_w_exp_f32(float x) { return sdca::lambert_w_exp(x); }
+
+}  // extern "C"
