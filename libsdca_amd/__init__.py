@@ -1,0 +1,204 @@
+"""libsdca_amd - MI355X (gfx950) batched prox operators and evaluation pass.
+
+Python host side of the C ABI in include/sdca_hip.h.  The functions keep the
+names and argument meaning of libsdca's batched C++ API
+(include/sdca/prox/*.h, the `dim` overloads) and of the Matlab front end's
+operator table (src/matlab/mex_prox.cpp:145-172):
+
+    prox_knapsack_eq(dim, A, lo=0, hi=1, rhs=1)
+    prox_knapsack_le(dim, A, lo=0, hi=1, rhs=1)
+    prox_topk_simplex(dim, A, k=1, rhs=1)
+    prox_topk_cone(dim, A, k=1)
+    prox_entropy(dim, A, hi=1, rhs=1)
+    prox_entropy_norm(dim, A, hi=1, rhs=1)
+    prox_topk_entropy(dim, A, k=1)
+    prox_two_simplex(dim, p, A, rhs=1)
+    lambert_w_exp(A)
+
+`A` holds n columns of length dim, contiguous (a C-contiguous (n, dim) array
+or tensor, i.e. the column-major dim x n matrix of the reference).  A torch
+CUDA tensor is processed in place on the device (stream-ordered on torch's
+current stream); a numpy array is staged through device memory and updated in
+place.  There is no CPU fallback: without the built HIP library every call
+raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+__all__ = [
+    "SdcaError", "library", "prox", "prox_knapsack_eq", "prox_knapsack_le",
+    "prox_topk_simplex", "prox_topk_cone", "prox_entropy", "prox_entropy_norm",
+    "prox_topk_entropy", "prox_two_simplex", "lambert_w_exp", "OPS", "F32", "F64",
+]
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsdca_hip.so")
+
+F32, F64, LONG_DOUBLE = 0, 1, 2
+HOST_PTR = 1
+OPS = {
+    "knapsack_eq": 0, "knapsack": 0, "knapsack_le": 1, "topk_simplex": 2,
+    "topk_cone": 3, "entropy": 4, "entropy_norm": 5, "topk_entropy": 6,
+    "two_simplex": 7, "lambert_w_exp": 8, "knapsack_le_biased": 9,
+    "topk_simplex_biased": 10, "topk_cone_biased": 11,
+    "topk_entropy_biased": 12, "two_simplex_sort": 13,
+}
+STATUS = {
+    0: "OK", 1: "ARG_NULL", 2: "ARG_RANGE", 3: "PRECISION", 4: "NOT_IMPLEMENTED",
+    5: "OUT_OF_MEMORY", 6: "HIP", 7: "PROX", 8: "LABELS",
+}
+
+
+class SdcaError(RuntimeError):
+    """A failed C ABI call; .status is the sdca_status code."""
+
+    def __init__(self, status, message):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+class ProxParams(ctypes.Structure):
+    _fields_ = [("lo", ctypes.c_double), ("hi", ctypes.c_double),
+                ("rhs", ctypes.c_double), ("rho", ctypes.c_double),
+                ("alpha", ctypes.c_double), ("k", ctypes.c_int64),
+                ("p", ctypes.c_int64)]
+
+
+class Thresholds(ctypes.Structure):
+    _fields_ = [("t", ctypes.c_double), ("lo", ctypes.c_double), ("hi", ctypes.c_double)]
+
+
+_lib = None
+
+
+def library():
+    """The loaded libsdca_hip.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise SdcaError(6, f"{LIB_PATH} is missing: build it with "
+                               "`python -c 'import __graft_entry__ as g; g.build()'`")
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.sdca_prox.restype = ctypes.c_int
+        lib.sdca_prox.argtypes = [
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ProxParams), ctypes.c_void_p,
+            ctypes.c_void_p, ctypes.c_uint, ctypes.c_void_p]
+        lib.sdca_last_error.restype = ctypes.c_char_p
+        lib.sdca_abi_version.restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        msg = library().sdca_last_error().decode(errors="replace")
+        raise SdcaError(rc, msg)
+
+
+def _is_torch(x):
+    return type(x).__module__.startswith("torch")
+
+
+def _dtype_code(x):
+    if _is_torch(x):
+        import torch
+        return {torch.float32: F32, torch.float64: F64}.get(x.dtype, -1)
+    return {np.dtype(np.float32): F32, np.dtype(np.float64): F64}.get(x.dtype, -1)
+
+
+def _stream_ptr():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
+         alpha=1.0, k=1, p=1, col_p=None, thresholds=False):
+    """Batched prox over the rows of A (each row is one column of the
+    reference's dim x n matrix).  Returns out (A itself when out is None) and,
+    with thresholds=True, an (n, 3) (or (2n, 3) for two_simplex) array of
+    (t, lo, hi) per column/block."""
+    lib = library()
+    code = OPS[op] if isinstance(op, str) else int(op)
+    data = _dtype_code(A)
+    if data < 0:
+        raise SdcaError(3, f"unsupported element type {A.dtype}")
+    res = data if result is None else ({"float": F32, "single": F32, "double": F64,
+                                        "long double": LONG_DOUBLE}.get(result, result))
+    if A.ndim == 1:
+        A = A.reshape(1, -1)
+    n, m = int(A.shape[0]), int(A.shape[1])
+    if out is None:
+        out = A
+    params = ProxParams(lo, hi, rhs, rho, alpha, int(k), int(p))
+    nthr = 2 * n if code == OPS["two_simplex"] else n
+    if _is_torch(A):
+        import torch
+        if not A.is_cuda or not A.is_contiguous() or not out.is_contiguous():
+            raise SdcaError(2, "torch inputs must be contiguous CUDA tensors")
+        thr = torch.zeros((nthr, 3), dtype=torch.float64, device=A.device) if thresholds else None
+        cp = None
+        if col_p is not None:
+            cp = torch.as_tensor(col_p, dtype=torch.int64, device=A.device).contiguous()
+        check(lib.sdca_prox(code, data, res, m, n, A.data_ptr(), out.data_ptr(),
+                            ctypes.byref(params), cp.data_ptr() if cp is not None else None,
+                            thr.data_ptr() if thr is not None else None, 0, _stream_ptr()))
+        return (out, thr) if thresholds else out
+    if not A.flags.c_contiguous or not out.flags.c_contiguous:
+        raise SdcaError(2, "numpy inputs must be C-contiguous")
+    thr = np.zeros((nthr, 3), dtype=np.float64) if thresholds else None
+    cp = None if col_p is None else np.ascontiguousarray(col_p, dtype=np.int64)
+    check(lib.sdca_prox(code, data, res, m, n, A.ctypes.data, out.ctypes.data,
+                        ctypes.byref(params), cp.ctypes.data if cp is not None else None,
+                        thr.ctypes.data if thr is not None else None, HOST_PTR, None))
+    return (out, thr) if thresholds else out
+
+
+def _rows(dim, A):
+    if A.ndim == 2 and A.shape[1] == dim:
+        return A
+    return A.reshape(-1, dim)
+
+
+# The reference's batched overloads (`dim` first).  Result follows the
+# reference: deduced from the floating parameter's type in C++; here the
+# element type unless `result` is given.  prox_topk_cone / prox_topk_entropy
+# default to double, as their C++ templates do (topk_cone.h:187-199,
+# topk_entropy.h:306-318).
+def prox_knapsack_eq(dim, A, lo=0.0, hi=1.0, rhs=1.0, result=None):
+    return prox("knapsack_eq", _rows(dim, A), lo=lo, hi=hi, rhs=rhs, result=result)
+
+
+def prox_knapsack_le(dim, A, lo=0.0, hi=1.0, rhs=1.0, result=None):
+    return prox("knapsack_le", _rows(dim, A), lo=lo, hi=hi, rhs=rhs, result=result)
+
+
+def prox_topk_simplex(dim, A, k=1, rhs=1.0, result=None):
+    return prox("topk_simplex", _rows(dim, A), k=k, rhs=rhs, result=result)
+
+
+def prox_topk_cone(dim, A, k=1, result="double"):
+    return prox("topk_cone", _rows(dim, A), k=k, result=result)
+
+
+def prox_entropy(dim, A, hi=1.0, rhs=1.0, result=None):
+    return prox("entropy", _rows(dim, A), hi=hi, rhs=rhs, result=result)
+
+
+def prox_entropy_norm(dim, A, hi=1.0, rhs=1.0, result=None):
+    return prox("entropy_norm", _rows(dim, A), hi=hi, rhs=rhs, result=result)
+
+
+def prox_topk_entropy(dim, A, k=1, result="double"):
+    return prox("topk_entropy", _rows(dim, A), k=k, result=result)
+
+
+def prox_two_simplex(dim, p, A, rhs=1.0, result=None):
+    return prox("two_simplex", _rows(dim, A), p=p, rhs=rhs, result=result)
+
+
+def lambert_w_exp(A):
+    """Elementwise W(exp(x)) in place (apply(dim, ..., lambert_w_exp_map))."""
+    return prox("lambert_w_exp", A if A.ndim == 2 else A.reshape(1, -1))

@@ -1,0 +1,168 @@
+// Device-side building blocks shared by the prox and evaluation kernels
+// (gfx950, wave64).  Numeric semantics follow libsdca v0.3.1: comparisons and
+// threshold arithmetic in the Result type R, element storage and the final
+// clamp in the Data type D.
+#ifndef SDCA_HIP_COMMON_HPP
+#define SDCA_HIP_COMMON_HPP
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sdca_gpu {
+
+template <class T> struct num;
+template <> struct num<float> {
+  __device__ __host__ static constexpr float eps() { return 1.19209290e-07f; }
+  __device__ __host__ static constexpr float inf() { return __builtin_huge_valf(); }
+  // exp_traits<float>::min_arg (math/log_exp.h:46-52)
+  __device__ __host__ static constexpr float exp_min_arg() { return -8.733654022216796875000000e+01f; }
+};
+template <> struct num<double> {
+  __device__ __host__ static constexpr double eps() { return 2.2204460492503131e-16; }
+  __device__ __host__ static constexpr double inf() { return __builtin_huge_val(); }
+  // exp_traits<double>::min_arg = log(DBL_MIN) (math/log_exp.h:27-34)
+  __device__ __host__ static constexpr double exp_min_arg() { return -0x1.6232bdd7abcd2p+9; }
+};
+
+__device__ inline float dexp(float x) { return expf(x); }
+__device__ inline double dexp(double x) { return exp(x); }
+__device__ inline float dlog(float x) { return logf(x); }
+__device__ inline double dlog(double x) { return log(x); }
+__device__ inline float dlog1p(float x) { return log1pf(x); }
+__device__ inline double dlog1p(double x) { return log1p(x); }
+__device__ inline float dmax(float a, float b) { return fmaxf(a, b); }
+__device__ inline double dmax(double a, double b) { return fmax(a, b); }
+__device__ inline float dmin(float a, float b) { return fminf(a, b); }
+__device__ inline double dmin(double a, double b) { return fmin(a, b); }
+
+// std::max(lo, std::min(x, hi)) with the argument order of proxdef.h:177:
+// min(x, hi) returns x unless hi < x; max(lo, y) returns lo unless lo < y.
+template <class D>
+__device__ inline D clamp_ref(D x, D lo, D hi) {
+  D y = (hi < x) ? hi : x;
+  return (lo < y) ? y : lo;
+}
+
+// x log x with 0 log 0 = 0 (math/log_exp.h:76-80).
+template <class T>
+__device__ inline T x_log_x(T x) { return (x > 0) ? x * dlog(x) : T(0); }
+
+// ---------------------------------------------------------------------------
+// Lambert W(exp(x)) (math/lambert.h:31-157): same intervals, same
+// initialisation and the same order-5 Householder step.
+// ---------------------------------------------------------------------------
+template <class T>
+__device__ inline T lw_step5(T w, T y) {
+  T f0 = w - y, f1 = T(1) + y;
+  T f11 = f1 * f1, f0y = f0 * y;
+  T f00y = f0 * f0y;
+  return w - T(4) * f0 * (T(6) * f1 * (f11 + f0y) + f00y)
+    / (f11 * (T(24) * f11 + T(36) * f0y) + f00y * (T(14) * y + f0 + T(8)));
+}
+
+template <class T>
+__device__ inline T exp_approx(T x) {
+  T y = T(1) + x / T(1024);
+#pragma unroll
+  for (int i = 0; i < 10; ++i) y *= y;
+  return y;
+}
+
+__device__ inline float lambert_w_exp(float x) {
+  float w;
+  if (x > -1.0f) {
+    if (x <= 8.0f) {
+      w = lw_step5(x, 1.0f);
+    } else {
+      return (x <= 536870912.0f) ? lw_step5(x - logf(x), x) : x;
+    }
+  } else {
+    if (x > -18.0f) {
+      w = exp_approx(x);
+    } else {
+      return (x > -104.0f) ? expf(x) : 0.0f;
+    }
+  }
+  return lw_step5(w, expf(x - w));
+}
+
+__device__ inline double lambert_w_exp(double x) {
+  double w;
+  if (x > 0.0) {
+    if (x <= 4.0) {
+      w = lw_step5(x, 1.0);
+    } else if (x <= 576460752303423488.0) {
+      w = x - log(x);
+      w = lw_step5(w, x);
+    } else {
+      return x;
+    }
+  } else {
+    if (x > -36.0) {
+      w = exp_approx(x);
+      if (x > -20.0) w = lw_step5(w, exp_approx(x - w));
+    } else {
+      return (x > -746.0) ? exp(x) : 0.0;
+    }
+  }
+  return lw_step5(w, exp(x - w));
+}
+
+// ---------------------------------------------------------------------------
+// Reductions over a group of G adjacent lanes of a wave (G a power of two,
+// groups aligned to G).  Every lane of the group receives the result.
+// ---------------------------------------------------------------------------
+template <int G, class T>
+__device__ inline T group_sum(T x) {
+#pragma unroll
+  for (int off = G / 2; off >= 1; off /= 2) x += __shfl_xor(x, off, 64);
+  return x;
+}
+template <int G, class T>
+__device__ inline T group_max(T x) {
+#pragma unroll
+  for (int off = G / 2; off >= 1; off /= 2) {
+    T y = __shfl_xor(x, off, 64);
+    x = (y > x) ? y : x;
+  }
+  return x;
+}
+template <int G, class T>
+__device__ inline T group_min(T x) {
+#pragma unroll
+  for (int off = G / 2; off >= 1; off /= 2) {
+    T y = __shfl_xor(x, off, 64);
+    x = (y < x) ? y : x;
+  }
+  return x;
+}
+
+// Sorted (descending) top list of L values, insertion of one value:
+// new[i] = max(old[i], min(old[i-1], x)) = median(old[i-1], old[i], x).
+template <int L, class D>
+__device__ inline void top_insert(D (&top)[L], D x) {
+#pragma unroll
+  for (int i = L - 1; i >= 1; --i) {
+    D lo = (top[i - 1] < x) ? top[i - 1] : x;
+    top[i] = (top[i] < lo) ? lo : top[i];
+  }
+  top[0] = (top[0] < x) ? x : top[0];
+}
+
+// Merge the top lists of the G lanes of a group (every lane ends with the
+// top L values of the union, as a multiset).
+template <int G, int L, class D>
+__device__ inline void top_merge(D (&top)[L]) {
+#pragma unroll
+  for (int off = G / 2; off >= 1; off /= 2) {
+    D other[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) other[i] = __shfl_xor(top[i], off, 64);
+#pragma unroll
+    for (int i = 0; i < L; ++i) top_insert(top, other[i]);
+  }
+}
+
+}  // namespace sdca_gpu
+
+#endif

@@ -1,0 +1,711 @@
+// Batched column prox kernels for gfx950 (one template, five operator
+// families).  Replaces the batch loop prox(dim, first, last, aux, ...)
+// (proxdef.h:279-324) of libsdca v0.3.1.
+//
+// Layout.  The input is an m x n column-major matrix; columns are contiguous.
+// A 256-thread workgroup owns B = 256 / G consecutive columns: it copies their
+// B*m contiguous elements into LDS with 16-byte loads (fully coalesced), then
+// each group of G adjacent lanes takes one column, lane g holding elements
+// g, g+G, g+2G, ... in C registers (slots past m hold -inf, which every pass
+// below ignores by construction).  Thresholds are found in registers with
+// group reductions over the G lanes; the clamp/map result goes back through
+// LDS and out with 16-byte stores.  HBM traffic is one read and one write of
+// the matrix.
+//
+// Semantics.  Each family restates the reference algorithm on register
+// values: the same threshold formulas, the same case tests and epsilons and
+// the same arithmetic type (Result R) for every quantity, with the partitions
+// of the reference expressed as value cuts (a partition by `x > c` keeps a
+// set {x > cut}).  Sums run in a different order than the reference's
+// std::accumulate, so thresholds agree to rounding.  Columns whose case needs
+// the reference's full sort (topk_cone_search with |U| > 0, ties at zero,
+// k beyond the register list) are flagged into a list that the
+// workgroup-per-column kernel in prox_slow.hpp finishes.
+#ifndef SDCA_HIP_PROX_IMPL_HPP
+#define SDCA_HIP_PROX_IMPL_HPP
+
+#include "common.hpp"
+#include "prox_launch.hpp"
+
+namespace sdca_gpu {
+
+enum Family { FAM_KNAP = 0, FAM_TOPK = 1, FAM_ENT = 2, FAM_TOPKENT = 3, FAM_TWO = 4 };
+
+template <class R>
+struct ProxParamsT {
+  R lo, hi, rhs;
+  int k;
+  int op;
+  int p;
+};
+
+// Result of the threshold search for one column.
+template <class R>
+struct ColThr {
+  R t, lo, hi;     // first (or only) block
+  R t2, lo2, hi2;  // second block (two-block operator)
+  int kind;        // elementwise map of the clamp: 0 identity, 1 exp, 2 W(exp)
+  bool slow;       // column deferred to the workgroup-per-column kernel
+};
+
+template <class R>
+__device__ inline ColThr<R> make_thr(R t, R lo, R hi, int kind = 0) {
+  ColThr<R> r;
+  r.t = t; r.lo = lo; r.hi = hi;
+  r.t2 = t; r.lo2 = lo; r.hi2 = hi;
+  r.kind = kind;
+  r.slow = false;
+  return r;
+}
+
+template <class R>
+__device__ inline ColThr<R> slow_thr() {
+  ColThr<R> r = make_thr<R>(R(0), R(0), R(0));
+  r.slow = true;
+  return r;
+}
+
+// Sum of the valid slots (padding holds -inf).
+template <int G, int C, class D, class R>
+__device__ inline R total_sum(const D (&v)[C], int nvalid) {
+  R s = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    if (c < nvalid) s += static_cast<R>(v[c]);
+  return group_sum<G>(s);
+}
+
+// ---------------------------------------------------------------------------
+// Kiwiel variable fixing (knapsack_eq.h:25-109).  The free set of the
+// reference is the value interval (lo_cut, hi_cut]: fixing the upper
+// candidates {x > hi + t} lowers hi_cut, fixing the lower candidates
+// {x <= lo + t} raises lo_cut.  On exit the final candidates are folded into
+// the fixed sets exactly as the reference's last partition does.
+// ---------------------------------------------------------------------------
+template <class R>
+struct KnapState {
+  R t;
+  R lo_cut, hi_cut;  // fixed sets: x <= lo_cut at lo, x > hi_cut at hi
+  R c_lo, c_hi;      // final candidate cuts inside the free interval
+  int n_u;           // |U| = number at hi (fixed + final candidates)
+  R sum_u;           // sum over U
+};
+
+template <int G, int C, class D, class R>
+__device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, R total,
+                                                R lo, R hi, R rhs) {
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  int mc = m;
+  R t = (total - rhs) / static_cast<R>(m);
+  KnapState<R> st;
+  st.lo_cut = -num<R>::inf();
+  st.hi_cut = num<R>::inf();
+  st.c_lo = -num<R>::inf();
+  st.c_hi = num<R>::inf();
+  st.n_u = 0;
+  st.sum_u = 0;
+  for (int iter = 0; iter <= m; ++iter) {
+    const R c_lo = lo + t, c_hi = hi + t;
+    R s_lo = 0, s_hi = 0;
+    int n_lo = 0, n_hi = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      const bool fr = (x > st.lo_cut) && !(x > st.hi_cut);
+      const bool gl = x > c_lo;
+      if (fr && !gl) { s_lo += x; ++n_lo; }
+      if (fr && gl && x > c_hi) { s_hi += x; ++n_hi; }
+    }
+    s_lo = group_sum<G>(s_lo);
+    s_hi = group_sum<G>(s_hi);
+    n_lo = group_sum<G>(n_lo);
+    n_hi = group_sum<G>(n_hi);
+    const R sh = static_cast<R>(n_hi) * hi;
+    const R sl = static_cast<R>(n_lo) * lo;
+    const R infeas = s_hi + s_lo - (sh + sl) - static_cast<R>(n_hi + n_lo) * t;
+    R next;
+    if (n_hi > 0 && infeas > eps) {
+      st.hi_cut = dmin(st.hi_cut, dmax(c_lo, c_hi));
+      next = static_cast<R>(mc) * t - s_hi + sh;
+      mc -= n_hi;
+      st.n_u += n_hi;
+      st.sum_u += s_hi;
+    } else if (n_lo > 0 && infeas < -eps) {
+      st.lo_cut = dmax(st.lo_cut, c_lo);
+      next = static_cast<R>(mc) * t - s_lo + sl;
+      mc -= n_lo;
+    } else {
+      st.c_lo = c_lo;
+      st.c_hi = c_hi;
+      st.n_u += n_hi;
+      st.sum_u += s_hi;
+      break;
+    }
+    if (mc > 0) {
+      t = next / static_cast<R>(mc);
+    } else {
+      break;
+    }
+  }
+  st.t = t;
+  return st;
+}
+
+// ---------------------------------------------------------------------------
+// Knapsack family: knapsack_eq (knapsack_eq.h:25-109) and knapsack_le
+// (knapsack_le.h:17-44).
+// ---------------------------------------------------------------------------
+template <int G, int C, class D, class R>
+__device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
+                                        const ProxParamsT<R>& pp) {
+  const R lo = pp.lo, hi = pp.hi, rhs = pp.rhs;
+  if (pp.op == OP_KNAPSACK_LE) {
+    const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+    R s_mid = 0;
+    int n_hi = 0, n_mid = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      if (x >= hi) ++n_hi;
+      else if (x > lo) { s_mid += x; ++n_mid; }
+    }
+    s_mid = group_sum<G>(s_mid);
+    n_hi = group_sum<G>(n_hi);
+    n_mid = group_sum<G>(n_mid);
+    const int n_lo = m - n_hi - n_mid;
+    const R s = s_mid + hi * static_cast<R>(n_hi) + lo * static_cast<R>(n_lo);
+    if (!(s > rhs + eps)) return make_thr<R>(R(0), lo, hi);
+  }
+  const R total = total_sum<G, C, D, R>(v, nvalid);
+  KnapState<R> st = knapsack_eq_regs<G, C, D, R>(v, m, total, lo, hi, rhs);
+  return make_thr<R>(st.t, lo, hi);
+}
+
+// ---------------------------------------------------------------------------
+// Top-k family: topk_cone (topk_cone.h:18-157) and topk_simplex
+// (topk_simplex.h:9-68).  The k largest values come from a sorted register
+// list of KM + 1 entries per lane (median-of-three insertion), merged across
+// the group; k <= KM.
+// ---------------------------------------------------------------------------
+template <class R>
+struct TopkSel {
+  R sum_k;   // sum of the k largest (in descending order)
+  R kth;     // k-th largest
+  R next;    // (k+1)-th largest, -inf if k == m
+  R first;   // largest
+};
+
+template <int G, int C, int KM, class D, class R>
+__device__ inline TopkSel<R> topk_select(const D (&v)[C], int k) {
+  constexpr int L = KM + 1;
+  D top[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) top[i] = -num<D>::inf();
+#pragma unroll
+  for (int c = 0; c < C; ++c) top_insert(top, v[c]);
+  top_merge<G>(top);
+  TopkSel<R> s;
+  s.sum_k = 0;
+  s.kth = static_cast<R>(top[0]);
+  s.next = -num<R>::inf();
+  s.first = static_cast<R>(top[0]);
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    if (i < k) s.sum_k += static_cast<R>(top[i]);
+    if (i == k - 1) s.kth = static_cast<R>(top[i]);
+    if (i == k) s.next = static_cast<R>(top[i]);
+  }
+  return s;
+}
+
+// topk_cone_search (topk_cone.h:58-133) when the answer has U empty: then
+// t = 0 exactly, M = {x > 16 eps} and hi = k sum(M) / k^2; valid if
+// hi >= max(M) - 16 eps.  Any other outcome (U non-empty, or values within
+// 16 eps of zero that the reference may place in M) goes to the slow path.
+template <int G, int C, class D, class R>
+__device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
+  const R eps16 = R(16) * num<R>::eps();
+  R s_p = 0;
+  int n_p = 0, n_z = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(v[c]);
+    if (x > eps16) { s_p += x; ++n_p; }
+    else if (x >= -eps16) ++n_z;
+  }
+  s_p = group_sum<G>(s_p);
+  n_p = group_sum<G>(n_p);
+  n_z = group_sum<G>(n_z);
+  if (n_z > 0) return slow_thr<R>();
+  const R den = K * K;
+  const R t = (R(0) * s_p - K * R(0)) / den;
+  const R hi = (R(0) + K * s_p) / den;
+  const R max_m = (n_p > 0) ? largest : -num<R>::inf();
+  const R tt = hi + t;
+  if (max_m - eps16 <= tt) return make_thr<R>(t, R(0), hi);
+  return slow_thr<R>();
+}
+
+template <int G, int C, int KM, class D, class R>
+__device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
+                                        const ProxParamsT<R>& pp) {
+  const int k = pp.k;
+  const R K = static_cast<R>(k);
+  const R eps16 = R(16) * num<R>::eps();
+  TopkSel<R> sel = topk_select<G, C, KM, D, R>(v, k);
+  // topk_cone_special_cases (topk_cone.h:18-55)
+  if (sel.sum_k <= eps16) return make_thr<R>(R(0), R(0), R(0));
+  const R hi_c = sel.sum_k / K;
+  const R t_c = sel.kth - hi_c;
+  const bool constant = (k == m) || (t_c >= sel.next - eps16);
+  if (pp.op == OP_TOPK_CONE) {
+    if (constant) return make_thr<R>(t_c, R(0), hi_c);
+    return cone_search_u0<G, C, D, R>(v, K, sel.first);
+  }
+  // thresholds_topk_simplex (topk_simplex.h:39-68)
+  const R rhs = pp.rhs;
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  if (constant && !(K * hi_c > rhs + eps)) return make_thr<R>(t_c, R(0), hi_c);
+  const R total = total_sum<G, C, D, R>(v, nvalid);
+  KnapState<R> st = knapsack_eq_regs<G, C, D, R>(v, m, total, R(0), rhs / K, rhs);
+  if (!constant) {
+    // is_topk_simplex_lt (topk_simplex.h:9-27) over U = [first, t.first)
+    bool lt;
+    if (st.n_u == 0) {
+      lt = st.t < -eps;
+    } else {
+      const R num_u = static_cast<R>(st.n_u);
+      lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * num_u - eps;
+    }
+    if (lt) return cone_search_u0<G, C, D, R>(v, K, sel.first);
+  }
+  return make_thr<R>(st.t, R(0), rhs / K);
+}
+
+// ---------------------------------------------------------------------------
+// log-sum-exp over the slots in `mask`, excluding exactly one maximum element
+// (the first in lane/slot order), as log_sum_exp(first, last, max, s)
+// (math/log_exp.h:134-152) excludes its `max` iterator.  Returns s.
+// ---------------------------------------------------------------------------
+template <int G, int C, class D, class R>
+__device__ inline R lse_sum_excl(const D (&v)[C], const bool (&mask)[C], R mx) {
+  int first_c = C;
+#pragma unroll
+  for (int c = C - 1; c >= 0; --c)
+    if (mask[c] && static_cast<R>(v[c]) == mx) first_c = c;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const int owner = group_min<G>(first_c < C ? g : G);
+  R s = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const bool skip = (g == owner) && (c == first_c);
+    if (mask[c] && !skip) s += dexp(static_cast<R>(v[c]) - mx);
+  }
+  return group_sum<G>(s);
+}
+
+template <int G, int C, class D, class R>
+__device__ inline R masked_max(const D (&v)[C], const bool (&mask)[C]) {
+  R mx = -num<R>::inf();
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    if (mask[c]) mx = dmax(mx, static_cast<R>(v[c]));
+  return group_max<G>(mx);
+}
+
+// solve_sum_w_exp (entropy_norm.h:183-236) over the slots in `range`
+// (count valid elements, all with values > -inf unless padding).
+template <int G, int C, class D, class R>
+__device__ inline R solve_sum_w_exp_regs(const D (&v)[C], const bool (&range)[C],
+                                         int count, R rhs) {
+  R s = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    if (range[c] && static_cast<R>(v[c]) > -num<R>::inf()) s += static_cast<R>(v[c]);
+  s = group_sum<G>(s);
+  R t = (s - rhs) / static_cast<R>(count);
+  // Heuristic refinement: U = {a > t} shrinks while it stays non-trivial.
+  R u_cut = -num<R>::inf();
+  int u_count = count;
+  for (int it = 0; it < count + 1; ++it) {
+    R su = 0;
+    int cu = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      if (range[c] && x > u_cut && x > t) { su += x; ++cu; }
+    }
+    su = group_sum<G>(su);
+    cu = group_sum<G>(cu);
+    if (cu == u_count || cu == 0) break;
+    u_cut = dmax(u_cut, t);
+    u_count = cu;
+    t = (su - rhs) / static_cast<R>(cu);
+  }
+  // Householder iterations of order 4 (entropy_norm.h:161-204).
+  const R ub = masked_max<G, C, D, R>(v, range) - num<R>::exp_min_arg();
+  const R eps16 = R(16) * num<R>::eps();
+  for (int iter = 0; iter < 32; ++iter) {
+    const R prev = t;
+    const R tc = dmin(t, ub);
+    const R mt = -tc;
+    R f0 = 0, f1 = 0, f2 = 0, f3 = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (range[c]) {
+        const R w = lambert_w_exp(static_cast<R>(v[c]) + mt);
+        const R d = R(1) + w;
+        const R d3 = d * d * d;
+        f0 += w;
+        f1 += w / d;
+        f2 += w / d3;
+        f3 += w * (R(1) - R(2) * w) / (d3 * d * d);
+      }
+    }
+    f0 = group_sum<G>(f0);
+    f1 = group_sum<G>(f1);
+    f2 = group_sum<G>(f2);
+    f3 = group_sum<G>(f3);
+    f0 -= rhs;
+    const R f02 = f0 * f2, f11 = f1 * f1;
+    t = tc - R(3) * f0 * (R(2) * f11 - f02) / (R(6) * f1 * (f02 - f11) - f0 * (f0 * f3));
+    if (fabs(prev - t) <= eps16) break;
+  }
+  return t;
+}
+
+// ---------------------------------------------------------------------------
+// Entropic family: entropy (entropy.h:19-53) and entropy_norm
+// (entropy_norm.h:246-283).  Elements fixed at hi are {x > hi_cut}.
+// ---------------------------------------------------------------------------
+template <int G, int C, class D, class R>
+__device__ inline ColThr<R> ent_family(const D (&v)[C], int m, int nvalid,
+                                       const ProxParamsT<R>& pp) {
+  const bool norm = pp.op == OP_ENTROPY_NORM;
+  const R hi = pp.hi, rhs = pp.rhs;
+  const R eps = R(16) * num<R>::eps() * dmax(R(1), rhs);
+  const R u = norm ? hi + dlog(hi) + eps : dlog(hi) + eps;
+  R r = rhs;
+  bool freem[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) freem[c] = c < nvalid;
+  R t;
+  if (norm) {
+    t = solve_sum_w_exp_regs<G, C, D, R>(v, freem, m, rhs);
+  } else {
+    const R mx = masked_max<G, C, D, R>(v, freem);
+    t = mx + dlog1p(lse_sum_excl<G, C, D, R>(v, freem, mx)) - dlog(rhs);
+  }
+  int nfixed = 0;
+  for (int iter = 0; iter <= m; ++iter) {
+    const R cut = t + u;
+    int cnt = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (freem[c] && static_cast<R>(v[c]) > cut) { ++cnt; freem[c] = false; }
+    }
+    cnt = group_sum<G>(cnt);
+    if (cnt == 0) break;
+    r -= hi * static_cast<R>(cnt);
+    nfixed += cnt;
+    if (nfixed == m) break;
+    if (r <= eps) {
+      t = masked_max<G, C, D, R>(v, freem) - num<R>::exp_min_arg() + R(1);
+      break;
+    }
+    if (norm) {
+      t = solve_sum_w_exp_regs<G, C, D, R>(v, freem, m - nfixed, r);
+    } else {
+      const R mx = masked_max<G, C, D, R>(v, freem);
+      t = mx + dlog1p(lse_sum_excl<G, C, D, R>(v, freem, mx)) - dlog(r);
+    }
+  }
+  return make_thr<R>(t, R(0), hi, norm ? 2 : 1);
+}
+
+// ---------------------------------------------------------------------------
+// Top-k entropy (topk_entropy.h:20-76).  U grows by removing the current
+// maximum; membership is a per-lane slot mask.
+// ---------------------------------------------------------------------------
+template <int G, int C, class D, class R>
+__device__ inline void masked_argmax(const D (&v)[C], const bool (&mask)[C], R& mx,
+                                     int& owner, int& slot) {
+  R lm = -num<R>::inf();
+  int lc = C;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(v[c]);
+    if (mask[c] && (lc == C || x > lm)) { lm = x; lc = c; }
+  }
+  mx = group_max<G>(lm);
+  const int g = static_cast<int>(threadIdx.x) % G;
+  owner = group_min<G>((lc < C && lm == mx) ? g : G);
+  slot = lc;
+}
+
+template <int G, int C, class D, class R>
+__device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
+                                           const ProxParamsT<R>& pp) {
+  (void)m;
+  const int k = pp.k;
+  const R eps = R(16) * num<R>::eps();
+  const R K = static_cast<R>(k);
+  const int g = static_cast<int>(threadIdx.x) % G;
+  bool rest[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) rest[c] = c < nvalid;
+  R mx;
+  int owner, slot;
+  masked_argmax<G, C, D, R>(v, rest, mx, owner, slot);
+  R z = lse_sum_excl<G, C, D, R>(v, rest, mx);
+  R log_z = mx + dlog1p(z);
+  R l1 = dexp(-mx);
+  R log_z_1 = isfinite(l1) ? mx + dlog1p(z + l1) : R(0);
+  if (k <= 1 || mx - eps <= log_z - dlog(K)) return make_thr<R>(log_z_1, R(0), R(1), 1);
+  R sum_u = 0, k_u = K;
+  for (int num_u = 1; num_u < k; ++num_u) {
+    const R min_u = mx;
+    sum_u += min_u;
+    if (g == owner) {
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (c == slot) rest[c] = false;
+    }
+    k_u -= R(1);
+    masked_argmax<G, C, D, R>(v, rest, mx, owner, slot);
+    z = lse_sum_excl<G, C, D, R>(v, rest, mx);
+    log_z = mx + dlog1p(z);
+    const R tt = log_z - dlog(k_u);
+    if (mx - eps <= tt && tt <= min_u + eps) break;
+  }
+  const R tmp = ((K - k_u) * log_z + k_u * dlog(k_u) - sum_u) / K;
+  R t, hi;
+  if (tmp > mx) {
+    const R a = (R(1) + z) * dexp(mx - tmp);
+    t = tmp + dlog1p(a * K) - dlog(k_u);
+    hi = a / (R(1) + a * K);
+  } else {
+    const R a = dexp(tmp - mx) / K;
+    t = mx + dlog1p(z + a) - dlog(k_u / K);
+    hi = (R(1) + z) / ((R(1) + z + a) * K);
+  }
+  return make_thr<R>(t, R(0), hi, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Two-block simplex (two_simplex.h:18-119).  Block a = rows [0, p), block
+// b = rows [p, m); the sets kept by the reference's partitions are
+// {x > x_cut} and {y > y_cut}.
+// ---------------------------------------------------------------------------
+template <int G, int C, class D, class R>
+__device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const ProxParamsT<R>& pp) {
+  const R rhs = pp.rhs;
+  const R eps = num<R>::eps() * dmax(R(1), rhs);
+  const int g = static_cast<int>(threadIdx.x) % G;
+  bool in_a[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) in_a[c] = (g + G * c) < p;
+  R cuts[2];
+  R res[2];
+  int cnt[2] = {p, m - p};
+  // Phase 1: each block on its own simplex <1, x> = rhs.
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    R cut = -num<R>::inf();
+    R tb = 0;
+    for (int it = 0; it <= m; ++it) {
+      R s = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(v[c]);
+        if (in_a[c] == (b == 0) && x > cut) s += x;
+      }
+      s = group_sum<G>(s);
+      tb = (s - rhs) / static_cast<R>(cnt[b]);
+      int above = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(v[c]);
+        if (in_a[c] == (b == 0) && x > cut && x > tb) ++above;
+      }
+      above = group_sum<G>(above);
+      if (above == cnt[b]) break;
+      cut = dmax(cut, tb);
+      cnt[b] = above;
+    }
+    cuts[b] = cut;
+    res[b] = tb;
+  }
+  R t = res[0];
+  const R s = res[1];
+  if (t + s >= -eps) {
+    ColThr<R> r = make_thr<R>(t, R(0), rhs);
+    r.t2 = s;
+    return r;
+  }
+  // Phase 2: joint variable fixing with s = -t.
+  int mc = cnt[0] + cnt[1];
+  {
+    R sa = 0, sb = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      if (in_a[c] && x > cuts[0]) sa += x;
+      if (!in_a[c] && x > cuts[1]) sb += x;
+    }
+    sa = group_sum<G>(sa);
+    sb = group_sum<G>(sb);
+    t = (+sa - sb) / static_cast<R>(mc);
+  }
+  for (int it = 0; it <= m; ++it) {
+    R sum_x = 0, sum_y = 0;
+    int n_x = 0, n_y = 0;
+    const R mt = -t;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      if (in_a[c]) {
+        if (x > cuts[0] && !(x > t)) { sum_x += x; ++n_x; }
+      } else {
+        if (x > cuts[1] && !(x > mt)) { sum_y += x; ++n_y; }
+      }
+    }
+    sum_x = group_sum<G>(sum_x);
+    sum_y = group_sum<G>(sum_y);
+    n_x = group_sum<G>(n_x);
+    n_y = group_sum<G>(n_y);
+    const R infeas = sum_x - sum_y - static_cast<R>(n_x + n_y) * t;
+    R next;
+    if (n_y > 0 && infeas > eps) {
+      cuts[1] = dmax(cuts[1], mt);
+      next = static_cast<R>(mc) * t + sum_y;
+      mc -= n_y;
+    } else if (n_x > 0 && infeas < -eps) {
+      cuts[0] = dmax(cuts[0], t);
+      next = static_cast<R>(mc) * t - sum_x;
+      mc -= n_x;
+    } else {
+      break;
+    }
+    if (mc > 0) {
+      t = next / static_cast<R>(mc);
+    } else {
+      break;
+    }
+  }
+  ColThr<R> r = make_thr<R>(t, R(0), rhs);
+  r.t2 = -t;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Tile copies between global memory and LDS, 16 bytes per lane when both
+// sides are 16-byte aligned.
+// ---------------------------------------------------------------------------
+template <class D>
+__device__ inline void tile_copy(D* __restrict__ dst, const D* __restrict__ src,
+                                 int64_t count) {
+  const int64_t bytes = count * static_cast<int64_t>(sizeof(D));
+  const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+  if (vec) {
+    const int64_t nv = bytes / 16;
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    uint4* d4 = reinterpret_cast<uint4*>(dst);
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) d4[i] = s4[i];
+    const int64_t done = nv * 16 / static_cast<int64_t>(sizeof(D));
+    for (int64_t i = done + threadIdx.x; i < count; i += blockDim.x) dst[i] = src[i];
+  } else {
+    for (int64_t i = threadIdx.x; i < count; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
+template <class D, class R>
+__device__ inline D apply_map(D x, D t, D lo, D hi, int kind) {
+  D y = x - t;
+  if (kind == 1) y = dexp(y);
+  else if (kind == 2) y = lambert_w_exp(y);
+  return clamp_ref(y, lo, hi);
+}
+
+// ---------------------------------------------------------------------------
+// The batched kernel.  Block = 256 threads = B columns of G lanes.
+// ---------------------------------------------------------------------------
+template <int FAM, int KM, class D, class R, int G, int C>
+__global__ void __launch_bounds__(256)
+prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
+                    int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
+                    sdca_thresholds* __restrict__ thr, int* __restrict__ slow) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  D* tile = reinterpret_cast<D*>(smem_raw);
+  constexpr int B = 256 / G;
+  const int m = static_cast<int>(m64);
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * B;
+  const int ncols = static_cast<int>(min(static_cast<int64_t>(B), n - col0));
+  const int64_t count = static_cast<int64_t>(ncols) * m;
+  tile_copy(tile, in + col0 * m64, count);
+  __syncthreads();
+
+  const int lc = static_cast<int>(threadIdx.x) / G;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const bool active = lc < ncols;
+  const int nvalid = active ? (m - g + G - 1) / G : 0;
+  D v[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    v[c] = (c < nvalid) ? tile[lc * m + g + G * c] : -num<D>::inf();
+
+  ColThr<R> th;
+  int p = pp.p;
+  if constexpr (FAM == FAM_KNAP) {
+    th = knap_family<G, C, D, R>(v, m, nvalid, pp);
+  } else if constexpr (FAM == FAM_TOPK) {
+    th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp);
+  } else if constexpr (FAM == FAM_ENT) {
+    th = ent_family<G, C, D, R>(v, m, nvalid, pp);
+  } else if constexpr (FAM == FAM_TOPKENT) {
+    th = topkent_family<G, C, D, R>(v, m, nvalid, pp);
+  } else {
+    if (col_p && active) p = static_cast<int>(col_p[col0 + lc]);
+    th = two_family<G, C, D, R>(v, m, p, pp);
+  }
+
+  if (active) {
+    const D t1 = static_cast<D>(th.t), lo1 = static_cast<D>(th.lo), hi1 = static_cast<D>(th.hi);
+    const D t2 = static_cast<D>(th.t2), lo2 = static_cast<D>(th.lo2), hi2 = static_cast<D>(th.hi2);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (c < nvalid && !th.slow) {
+        const int idx = g + G * c;
+        const bool second = (FAM == FAM_TWO) && idx >= p;
+        tile[lc * m + idx] = second ? apply_map<D, R>(v[c], t2, lo2, hi2, 0)
+                                    : apply_map<D, R>(v[c], t1, lo1, hi1, th.kind);
+      }
+    }
+    if (g == 0) {
+      const int64_t j = col0 + lc;
+      if (th.slow) {
+        const int pos = atomicAdd(slow, 1);
+        slow[1 + pos] = static_cast<int>(j);
+      } else if (thr) {
+        if (FAM == FAM_TWO) {
+          thr[2 * j].t = static_cast<double>(th.t);
+          thr[2 * j].lo = static_cast<double>(th.lo);
+          thr[2 * j].hi = static_cast<double>(th.hi);
+          thr[2 * j + 1].t = static_cast<double>(th.t2);
+          thr[2 * j + 1].lo = static_cast<double>(th.lo2);
+          thr[2 * j + 1].hi = static_cast<double>(th.hi2);
+        } else {
+          thr[j].t = static_cast<double>(th.t);
+          thr[j].lo = static_cast<double>(th.lo);
+          thr[j].hi = static_cast<double>(th.hi);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  tile_copy(out + col0 * m64, tile, count);
+}
+
+}  // namespace sdca_gpu
+
+#endif

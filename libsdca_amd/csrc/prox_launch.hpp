@@ -1,0 +1,62 @@
+// Host-side launch interface of the prox kernels (internal to the library).
+#ifndef SDCA_HIP_PROX_LAUNCH_HPP
+#define SDCA_HIP_PROX_LAUNCH_HPP
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sdca_hip.h"
+
+namespace sdca_gpu {
+
+enum {
+  OP_KNAPSACK_EQ = SDCA_PROX_KNAPSACK_EQ,
+  OP_KNAPSACK_LE = SDCA_PROX_KNAPSACK_LE,
+  OP_TOPK_SIMPLEX = SDCA_PROX_TOPK_SIMPLEX,
+  OP_TOPK_CONE = SDCA_PROX_TOPK_CONE,
+  OP_ENTROPY = SDCA_PROX_ENTROPY,
+  OP_ENTROPY_NORM = SDCA_PROX_ENTROPY_NORM,
+  OP_TOPK_ENTROPY = SDCA_PROX_TOPK_ENTROPY,
+  OP_TWO_SIMPLEX = SDCA_PROX_TWO_SIMPLEX,
+  OP_LAMBERT_W_EXP = SDCA_PROX_LAMBERT_W_EXP
+};
+
+// Largest m handled by the register kernels.
+constexpr int64_t kRegMaxM = 2048;
+// Top-k operators keep k <= kTopkMaxK in registers; larger k takes the
+// workgroup-per-column kernel.
+constexpr int64_t kTopkMaxK = 8;
+
+struct ProxLaunch {
+  int op;
+  int data;    // sdca_dtype of the elements
+  int result;  // sdca_dtype of the internal arithmetic
+  int64_t m, n;
+  const void* in;
+  void* out;
+  double lo, hi, rhs;
+  int64_t k, p;
+  const int64_t* col_p;     // device, or NULL
+  sdca_thresholds* thr;     // device, or NULL
+  int* slow;                // device: [0] = count, [1..n] = column list
+  hipStream_t stream;
+};
+
+// Register kernels, one per operator family (prox_*.hip).
+hipError_t launch_knap(const ProxLaunch& a);
+hipError_t launch_topk(const ProxLaunch& a);
+hipError_t launch_ent(const ProxLaunch& a);
+hipError_t launch_topkent(const ProxLaunch& a);
+hipError_t launch_two(const ProxLaunch& a);
+// Workgroup-per-column kernel over the flagged list (all_columns: every column).
+hipError_t launch_slow(const ProxLaunch& a, bool all_columns);
+// Largest m the workgroup-per-column kernel accepts for this element type.
+int64_t slow_max_m(int data);
+// Elementwise lambert_w_exp over m*n elements.
+hipError_t launch_lambert(const ProxLaunch& a);
+// Zero the slow-column counter.
+hipError_t launch_clear(int* p, int count, hipStream_t stream);
+
+}  // namespace sdca_gpu
+
+#endif

@@ -1,0 +1,308 @@
+// Workgroup-per-column prox kernel: the columns the register kernel defers
+// (topk_cone_search with U non-empty, zero-band ties, k > kTopkMaxK) and the
+// knapsack operators for m beyond the register kernel.
+//
+// The column is sorted in LDS (bitonic, descending, the order the reference's
+// std::sort(greater) produces), then one lane runs the reference's sequential
+// steps on the sorted values - the special cases (topk_cone.h:18-55), the
+// Kiwiel loop (knapsack_eq.h:25-109) whose partitions are contiguous ranges
+// of the sorted column, the top-k simplex test (topk_simplex.h:9-68) and the
+// O(k m) search topk_cone_search (topk_cone.h:58-133) in the same order and
+// with the same sums - and the workgroup clamps the column from global memory.
+// Columns come from a device list written by the register kernel, so no host
+// round trip is needed; every workgroup exits after the list is drained.
+#include "common.hpp"
+#include "prox_impl.hpp"
+#include "prox_launch.hpp"
+
+namespace sdca_gpu {
+
+namespace {
+
+template <class R, class D>
+__device__ R sum_range(const D* s, int b, int e) {
+  R acc = 0;
+  for (int i = b; i < e; ++i) acc += static_cast<R>(s[i]);
+  return acc;
+}
+
+// Kiwiel variable fixing on a column sorted in descending order.
+template <class D, class R>
+__device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  int mc = m;
+  R t = (sum_range<R>(s, 0, m) - rhs) / static_cast<R>(m);
+  int f = 0, l = m;  // free range [f, l)
+  KnapState<R> st;
+  st.n_u = 0;
+  st.sum_u = 0;
+  for (int iter = 0; iter <= m; ++iter) {
+    const R c_lo = lo + t, c_hi = hi + t;
+    int p_lo = f;  // first free index with !(x > c_lo)
+    while (p_lo < l && static_cast<R>(s[p_lo]) > c_lo) ++p_lo;
+    int p_hi = f;  // end of the prefix with x > c_hi (within [f, p_lo))
+    while (p_hi < p_lo && static_cast<R>(s[p_hi]) > c_hi) ++p_hi;
+    const R s_lo = sum_range<R>(s, p_lo, l);
+    const int n_lo = l - p_lo;
+    const R s_hi = sum_range<R>(s, f, p_hi);
+    const int n_hi = p_hi - f;
+    const R sh = static_cast<R>(n_hi) * hi;
+    const R sl = static_cast<R>(n_lo) * lo;
+    const R infeas = s_hi + s_lo - (sh + sl) - static_cast<R>(n_hi + n_lo) * t;
+    R next;
+    if (n_hi > 0 && infeas > eps) {
+      f = p_hi;
+      next = static_cast<R>(mc) * t - s_hi + sh;
+      mc -= n_hi;
+    } else if (n_lo > 0 && infeas < -eps) {
+      l = p_lo;
+      next = static_cast<R>(mc) * t - s_lo + sl;
+      mc -= n_lo;
+    } else {
+      f = p_hi;
+      l = p_lo;
+      break;
+    }
+    if (mc > 0) {
+      t = next / static_cast<R>(mc);
+    } else {
+      break;
+    }
+  }
+  st.t = t;
+  st.n_u = f;
+  st.sum_u = sum_range<R>(s, 0, f);
+  return st;
+}
+
+// topk_cone_search (topk_cone.h:58-133) on the sorted column.
+template <class D, class R>
+__device__ void cone_search_sorted(const D* s, int m, int k, R& t_out, R& hi_out) {
+  R k_u = static_cast<R>(k);
+  R min_u = num<R>::inf();
+  R num_u = 0, sum_u = 0;
+  const R eps = R(16) * num<R>::eps();
+  for (int mf = 0;;) {
+    R min_m = num<R>::inf();
+    R max_m = -num<R>::inf();
+    R sum_m = 0, num_m_sum_u = 0;
+    R den = k_u * k_u;
+    const R k_u_sum_u = k_u * sum_u;
+    for (int ml = mf;;) {
+      const R t = (num_u * sum_m - k_u_sum_u) / den;
+      const R hi = (num_m_sum_u + k_u * sum_m) / den;
+      const R tt = hi + t;
+      if (max_m - eps <= tt && tt <= min_u + eps) {
+        if (t <= min_m + eps && (ml == m || static_cast<R>(s[ml]) - eps <= t)) {
+          t_out = t;
+          hi_out = hi;
+          return;
+        }
+      }
+      if (ml == m) break;
+      min_m = static_cast<R>(s[ml]);
+      max_m = static_cast<R>(s[mf]);
+      sum_m += min_m;
+      num_m_sum_u += sum_u;
+      den += num_u;
+      ++ml;
+    }
+    if (mf == k) break;
+    min_u = static_cast<R>(s[mf]);
+    sum_u += min_u;
+    k_u -= R(1);
+    num_u += R(1);
+    ++mf;
+  }
+  t_out = 0;
+  hi_out = 0;
+}
+
+template <class D, class R>
+__device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, int k,
+                                  R& t_out, R& lo_out, R& hi_out) {
+  if (op == OP_KNAPSACK_EQ || op == OP_KNAPSACK_LE) {
+    lo_out = lo;
+    hi_out = hi;
+    if (op == OP_KNAPSACK_LE) {
+      // knapsack_le.h:30-46 on the sorted column
+      const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+      int n_hi = 0;
+      while (n_hi < m && static_cast<R>(s[n_hi]) >= hi) ++n_hi;
+      int e_mid = n_hi;
+      while (e_mid < m && static_cast<R>(s[e_mid]) > lo) ++e_mid;
+      const R sum = sum_range<R>(s, n_hi, e_mid) + hi * static_cast<R>(n_hi)
+                  + lo * static_cast<R>(m - e_mid);
+      if (!(sum > rhs + eps)) {
+        t_out = 0;
+        return;
+      }
+    }
+    t_out = knapsack_sorted<D, R>(s, m, lo, hi, rhs).t;
+    return;
+  }
+  const R K = static_cast<R>(k);
+  const R eps16 = R(16) * num<R>::eps();
+  const R sum_k = sum_range<R>(s, 0, k);
+  if (sum_k <= eps16) {
+    t_out = 0; lo_out = 0; hi_out = 0;
+    return;
+  }
+  const R hi_c = sum_k / K;
+  const R t_c = static_cast<R>(s[k - 1]) - hi_c;
+  const bool constant = (k == m) || (t_c >= static_cast<R>(s[k]) - eps16);
+  lo_out = 0;
+  if (op == OP_TOPK_CONE) {
+    if (constant) {
+      t_out = t_c;
+      hi_out = hi_c;
+    } else {
+      cone_search_sorted<D, R>(s, m, k, t_out, hi_out);
+    }
+    return;
+  }
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  if (constant && !(K * hi_c > rhs + eps)) {
+    t_out = t_c;
+    hi_out = hi_c;
+    return;
+  }
+  KnapState<R> st = knapsack_sorted<D, R>(s, m, R(0), rhs / K, rhs);
+  if (!constant) {
+    bool lt;
+    if (st.n_u == 0) {
+      lt = st.t < -eps;
+    } else {
+      const R num_u = static_cast<R>(st.n_u);
+      lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * num_u - eps;
+    }
+    if (lt) {
+      cone_search_sorted<D, R>(s, m, k, t_out, hi_out);
+      return;
+    }
+  }
+  t_out = st.t;
+  hi_out = rhs / K;
+}
+
+template <class D, class R>
+__global__ void __launch_bounds__(256)
+prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
+                 ProxParamsT<R> pp, sdca_thresholds* __restrict__ thr,
+                 const int* __restrict__ slow, int all_columns, int pow2) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  D* s = reinterpret_cast<D*>(smem_raw);
+  __shared__ R sh_t, sh_lo, sh_hi;
+  const int m = static_cast<int>(m64);
+  const int64_t count = all_columns ? n : static_cast<int64_t>(slow[0]);
+  for (int64_t w = blockIdx.x; w < count; w += gridDim.x) {
+    const int64_t j = all_columns ? w : static_cast<int64_t>(slow[1 + w]);
+    const D* col = in + j * m64;
+    for (int i = threadIdx.x; i < pow2; i += blockDim.x)
+      s[i] = (i < m) ? col[i] : -num<D>::inf();
+    __syncthreads();
+    // Bitonic sort, descending.
+    for (int size = 2; size <= pow2; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = threadIdx.x; i < pow2; i += blockDim.x) {
+          const int partner = i ^ stride;
+          if (partner > i) {
+            const bool desc = (i & size) == 0;
+            const D a = s[i], b = s[partner];
+            if (desc ? (a < b) : (b < a)) {
+              s[i] = b;
+              s[partner] = a;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (threadIdx.x == 0) {
+      R t, lo, hi;
+      thresholds_sorted<D, R>(s, m, pp.op, pp.lo, pp.hi, pp.rhs, pp.k, t, lo, hi);
+      sh_t = t;
+      sh_lo = lo;
+      sh_hi = hi;
+      if (thr) {
+        thr[j].t = static_cast<double>(t);
+        thr[j].lo = static_cast<double>(lo);
+        thr[j].hi = static_cast<double>(hi);
+      }
+    }
+    __syncthreads();
+    const D t = static_cast<D>(sh_t), lo = static_cast<D>(sh_lo), hi = static_cast<D>(sh_hi);
+    D* dst = out + j * m64;
+    for (int i = threadIdx.x; i < m; i += blockDim.x) dst[i] = clamp_ref(col[i] - t, lo, hi);
+    __syncthreads();
+  }
+}
+
+template <class D, class R>
+hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
+  ProxParamsT<R> pp;
+  pp.lo = static_cast<R>(a.lo);
+  pp.hi = static_cast<R>(a.hi);
+  pp.rhs = static_cast<R>(a.rhs);
+  pp.k = static_cast<int>(a.k);
+  pp.op = a.op;
+  pp.p = static_cast<int>(a.p);
+  int pow2 = 1;
+  while (pow2 < a.m) pow2 <<= 1;
+  const int64_t cap = all_columns ? 4096 : 512;
+  const int64_t grid = a.n < cap ? a.n : cap;
+  hipLaunchKernelGGL((prox_slow_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
+                     dim3(256), static_cast<size_t>(pow2) * sizeof(D), a.stream,
+                     static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
+                     a.thr, a.slow, all_columns ? 1 : 0, pow2);
+  return hipGetLastError();
+}
+
+__global__ void clear_kernel(int* p, int count) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) p[i] = 0;
+}
+
+template <class D>
+__global__ void __launch_bounds__(256) lambert_kernel(const D* __restrict__ in, D* __restrict__ out,
+                                                      int64_t count) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride)
+    out[i] = lambert_w_exp(in[i]);
+}
+
+}  // namespace
+
+int64_t slow_max_m(int data) {
+  // Sorted column in at most 32 KiB of LDS.
+  return data == SDCA_F32 ? 8192 : 4096;
+}
+
+hipError_t launch_slow(const ProxLaunch& a, bool all_columns) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_slow_t<float, float>(a, all_columns);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_slow_t<float, double>(a, all_columns);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_slow_t<double, double>(a, all_columns);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_clear(int* p, int count, hipStream_t stream) {
+  hipLaunchKernelGGL(clear_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, p, count);
+  return hipGetLastError();
+}
+
+hipError_t launch_lambert(const ProxLaunch& a) {
+  const int64_t count = a.m * a.n;
+  int64_t blocks = (count + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  if (a.data == SDCA_F32) {
+    hipLaunchKernelGGL(lambert_kernel<float>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       a.stream, static_cast<const float*>(a.in), static_cast<float*>(a.out), count);
+  } else {
+    hipLaunchKernelGGL(lambert_kernel<double>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       a.stream, static_cast<const double*>(a.in), static_cast<double*>(a.out), count);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sdca_gpu

@@ -1,0 +1,204 @@
+"""GPU parity of the batched prox operators against the CPU oracle.
+
+Every case runs the HIP path through the C ABI (libsdca_amd.prox on torch
+CUDA tensors, or numpy through the host-staging path) and the oracle
+restatement on the same seeded input, and compares the projected columns
+elementwise:
+
+    |gpu - oracle| <= rtol * max(1, max|a|)   per column
+
+with rtol = 1e-5 when the arithmetic (Result) type is float and 1e-12 when it
+is double (the tolerances of the north star).  The scale max(1, max|a|) is
+the magnitude of the column, because thresholds come from sums whose
+rounding depends on summation order.
+"""
+import numpy as np
+import pytest
+
+from tests import inputs
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = 0, 1
+RTOL = {F32: 1e-5, F64: 1e-12}
+
+
+def run_gpu(op, x, result, cuda, **kw):
+    import torch
+    import libsdca_amd as sd
+    t = torch.from_numpy(x).to(cuda)
+    out, thr = sd.prox(op, t, result=result, thresholds=True, **kw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), thr.cpu().numpy()
+
+
+def run_oracle(oracle, op, x, result, **kw):
+    from oracle import binding
+    y = x.copy()
+    col_p = kw.pop("col_p", None)
+    thr = oracle.prox(op, y, result=result, params=binding.make_params(**kw), col_p=col_p,
+                      thresholds=True)
+    return y, thr
+
+
+def assert_close(x, got, want, result, what):
+    scale = np.maximum(1.0, np.abs(x.astype(np.float64)).max(axis=1, keepdims=True))
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64)) / scale
+    bad = np.argwhere(err > RTOL[result])
+    assert bad.size == 0, (
+        f"{what}: {len(np.unique(bad[:, 0]))} columns differ, max scaled err "
+        f"{err.max():.3e}; first column {bad[0, 0]}: got {got[bad[0, 0]][:8]} want {want[bad[0, 0]][:8]}")
+
+
+DTYPES = [(np.float32, F32), (np.float32, F64), (np.float64, F64)]
+# One m per register configuration (G lanes x C slots), plus the sizes of the
+# benchmark configurations.
+MS = [1, 3, 10, 16, 17, 64, 100, 128, 200, 512, 999, 1000, 2048]
+
+
+def cases(m, dtype, seed):
+    n = 300
+    yield "normal", inputs.normal(n, m, dtype, seed)
+    yield "label+2", inputs.label_shifted(n, m, dtype, seed + 1)
+    yield "pos", inputs.decades(n, m, dtype, seed + 2, -3, 3)
+    yield "neg", inputs.decades(n, m, dtype, seed + 3, -3, 3, sign=-1.0)
+    yield "mixed", inputs.mixed_signs(n, m, dtype, seed + 4, -3, 3)
+    yield "edge", inputs.edge_columns(m, dtype, seed + 5)
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", MS)
+@pytest.mark.parametrize("op,kw", [
+    ("knapsack_eq", dict(lo=0.0, hi=1.0, rhs=1.0)),
+    ("knapsack_eq", dict(lo=-0.5, hi=0.25, rhs=0.7)),
+    ("knapsack_le", dict(lo=0.0, hi=0.3, rhs=1.0)),
+])
+def test_knapsack(cuda, oracle, op, kw, m, dtype, result):
+    if kw["hi"] * m < kw["rhs"] or kw["lo"] * m > kw["rhs"]:
+        pytest.skip("infeasible bounds for this m")
+    for name, x in cases(m, dtype, 10 + m):
+        got, _ = run_gpu(op, x, result, cuda, **kw)
+        want, _ = run_oracle(oracle, op, x, result, **kw)
+        assert_close(x, got, want, result, f"{op} {name} m={m}")
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", MS)
+@pytest.mark.parametrize("op", ["topk_simplex", "topk_cone"])
+@pytest.mark.parametrize("k", [1, 2, 5, 8, 11])
+def test_topk(cuda, oracle, op, k, m, dtype, result):
+    if k > m:
+        pytest.skip("k > m")
+    kw = dict(k=k, rhs=1.0)
+    for name, x in cases(m, dtype, 20 + m + k):
+        got, _ = run_gpu(op, x, result, cuda, **kw)
+        want, _ = run_oracle(oracle, op, x, result, **kw)
+        assert_close(x, got, want, result, f"{op} k={k} {name} m={m}")
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [1, 10, 100, 200, 1000, 2048])
+@pytest.mark.parametrize("op,kw", [
+    ("entropy", dict(hi=1.0, rhs=1.0)),
+    ("entropy", dict(hi=0.1, rhs=0.5)),
+    ("entropy_norm", dict(hi=1.0, rhs=1.0)),
+    ("entropy_norm", dict(hi=0.2, rhs=0.9)),
+])
+def test_entropic(cuda, oracle, op, kw, m, dtype, result):
+    if kw["hi"] * m < kw["rhs"]:
+        pytest.skip("infeasible bounds for this m")
+    n = 200
+    for name, x in [("uniform", inputs.uniform(n, m, dtype, 30 + m, -10, 10)),
+                    ("normal", inputs.normal(n, m, dtype, 31 + m, 3.0)),
+                    ("edge", inputs.edge_columns(m, dtype, 32 + m))]:
+        got, _ = run_gpu(op, x, result, cuda, **kw)
+        want, _ = run_oracle(oracle, op, x, result, **kw)
+        assert_close(x, got, want, result, f"{op} {name} m={m}")
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [2, 10, 100, 999])
+@pytest.mark.parametrize("k", [1, 3, 5, 12])
+def test_topk_entropy(cuda, oracle, k, m, dtype, result):
+    if k > m:
+        pytest.skip("k > m")
+    n = 200
+    for name, x in [("normal", inputs.normal(n, m, dtype, 40 + m, 2.0)),
+                    ("label+2", inputs.label_shifted(n, m, dtype, 41 + m)),
+                    ("edge", inputs.edge_columns(m, dtype, 42 + m))]:
+        got, _ = run_gpu("topk_entropy", x, result, cuda, k=k)
+        want, _ = run_oracle(oracle, "topk_entropy", x, result, k=k)
+        assert_close(x, got, want, result, f"topk_entropy k={k} {name} m={m}")
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [2, 10, 159, 200, 1000])
+def test_two_simplex(cuda, oracle, m, dtype, result):
+    n = 300
+    rng = np.random.default_rng(50 + m)
+    col_p = rng.integers(1, min(m - 1, 5) + 1, n)
+    for rhs in [1.0, 2.0]:
+        for name, x in [("normal", inputs.normal(n, m, dtype, 51 + m)),
+                        ("mixed", inputs.mixed_signs(n, m, dtype, 52 + m, -2, 2))]:
+            got, _ = run_gpu("two_simplex", x, result, cuda, rhs=rhs, col_p=col_p)
+            want, _ = run_oracle(oracle, "two_simplex", x, result, rhs=rhs, col_p=col_p)
+            assert_close(x, got, want, result, f"two_simplex rhs={rhs} {name} m={m}")
+            # scalar p for every column
+            got, _ = run_gpu("two_simplex", x, result, cuda, rhs=rhs, p=1)
+            want, _ = run_oracle(oracle, "two_simplex", x, result, rhs=rhs, p=1)
+            assert_close(x, got, want, result, f"two_simplex p=1 rhs={rhs} {name} m={m}")
+
+
+def test_two_simplex_regression_vector(cuda, oracle):
+    """The hard-coded vector of test/prox/two_simplex.cpp:55-64 (p=1, rhs=2)."""
+    x = np.array([[-0.49371069182389915] + [0.49371069182390021] * 158], dtype=np.float64)
+    got, _ = run_gpu("two_simplex", x, F64, cuda, rhs=2.0, p=1)
+    want, _ = run_oracle(oracle, "two_simplex", x, F64, rhs=2.0, p=1)
+    assert_close(x, got, want, F64, "two_simplex regression vector")
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_lambert_w_exp(cuda, oracle, dtype):
+    rng = np.random.default_rng(60)
+    x = rng.uniform(-50, 50, (1, 100000)).astype(dtype)
+    edges = np.array([-1e4, -746, -745.9, -104, -36, -20, -18, -1, 0, 4, 8, 2.0**29, 2.0**59,
+                      1e20, 36.5, -0.5], dtype=dtype)
+    x = np.concatenate([x, edges[None, :]], axis=1)
+    got, _ = run_gpu_plain("lambert_w_exp", x, cuda)
+    want = oracle.lambert_w_exp(x).reshape(x.shape)
+    r = F32 if dtype == np.float32 else F64
+    tol = {F32: 4e-7, F64: 4e-16}[r]
+    err = np.abs(got.astype(np.float64) - want) / np.maximum(1.0, np.abs(want))
+    assert err.max() <= tol, f"max rel err {err.max():.3e}"
+
+
+def run_gpu_plain(op, x, cuda):
+    import torch
+    import libsdca_amd as sd
+    t = torch.from_numpy(x).to(cuda)
+    sd.prox(op, t)
+    torch.cuda.synchronize()
+    return t.cpu().numpy(), None
+
+
+def test_host_pointer_path(oracle):
+    """numpy in, numpy out through the library's own staging."""
+    import libsdca_amd as sd
+    x = inputs.label_shifted(1000, 100, np.float32, 70)
+    got = x.copy()
+    sd.prox_topk_simplex(100, got, k=5, rhs=1.0)
+    want, _ = run_oracle(oracle, "topk_simplex", x, F32, k=5, rhs=1.0)
+    assert_close(x, got, want, F32, "host path topk_simplex")
+
+
+def test_out_of_place(cuda, oracle):
+    import torch
+    import libsdca_amd as sd
+    x = inputs.normal(5000, 10, np.float64, 71)
+    t = torch.from_numpy(x).to(cuda)
+    o = torch.empty_like(t)
+    sd.prox("knapsack_eq", t, out=o)
+    torch.cuda.synchronize()
+    assert np.array_equal(t.cpu().numpy(), x), "input modified by an out-of-place call"
+    want, _ = run_oracle(oracle, "knapsack_eq", x, F64)
+    assert_close(x, o.cpu().numpy(), want, F64, "out of place knapsack_eq")
