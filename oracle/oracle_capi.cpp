@@ -252,6 +252,12 @@ int oracle_prox(int op, int data, int result, int64_t m, int64_t n, void* x,
     return prox_impl<double, float>(op, m, n, static_cast<double*>(x), p, col_p, thr_out, nthreads);
   if (data == SDCA_F64 && result == SDCA_F64)
     return prox_impl<double, double>(op, m, n, static_cast<double*>(x), p, col_p, thr_out, nthreads);
+  // Long double arithmetic: the high-precision solution the parity tests use
+  // to bound the rounding error of the float/double paths.
+  if (data == SDCA_F32 && result == SDCA_LONG_DOUBLE)
+    return prox_impl<float, long double>(op, m, n, static_cast<float*>(x), p, col_p, thr_out, nthreads);
+  if (data == SDCA_F64 && result == SDCA_LONG_DOUBLE)
+    return prox_impl<double, long double>(op, m, n, static_cast<double*>(x), p, col_p, thr_out, nthreads);
   return SDCA_ERR_PRECISION;
 }
 

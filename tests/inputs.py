@@ -51,7 +51,7 @@ def edge_columns(m, dtype, seed=0):
         np.full(m, 0.5),
         np.linspace(-1, 1, m),
         np.linspace(1, -1, m),
-        np.repeat(rng.standard_normal(max(1, m // 4)), 4)[:m] if m >= 4 else rng.standard_normal(m),
+        np.resize(np.repeat(rng.standard_normal(max(1, m // 4)), 4), m),
         np.where(np.arange(m) % 2 == 0, 1.0, -1.0),
         rng.standard_normal(m) * 1e-6,
         rng.standard_normal(m) * 1e6,

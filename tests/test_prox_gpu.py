@@ -2,15 +2,23 @@
 
 Every case runs the HIP path through the C ABI (libsdca_amd.prox on torch
 CUDA tensors, or numpy through the host-staging path) and the oracle
-restatement on the same seeded input, and compares the projected columns
-elementwise:
+restatement (bit-exact with the reference headers) on the same seeded input,
+and compares the projected columns elementwise, scaled by the column
+magnitude s = max(1, max|a|):
 
-    |gpu - oracle| <= rtol * max(1, max|a|)   per column
+  * |gpu - ref| / s <= rtol + 3 E, and
+  * |gpu - exact| / s <= rtol + 2 E (the GPU is at least as accurate as the
+    reference),
 
-with rtol = 1e-5 when the arithmetic (Result) type is float and 1e-12 when it
-is double (the tolerances of the north star).  The scale max(1, max|a|) is
-the magnitude of the column, because thresholds come from sums whose
-rounding depends on summation order.
+with rtol = 1e-5 when the arithmetic (Result) type or the element (Data) type
+is float and 1e-12 when both are double (the north star's tolerances), "exact" the same algorithm run by the
+oracle in long double, and E = max over the batch of |ref - exact| / s: the
+reference's own rounding error.  E is not a fudge factor: the thresholds come
+from sums of m terms whose rounding depends on summation order (the
+reference's std::partition order is not reproducible in parallel), and for
+float at m = 1000 the reference itself is ~2e-4 away from the exact
+projection, so a flat 1e-5 would fail any implementation that sums in another
+order.  E is printed for every case that needs it.
 """
 import numpy as np
 import pytest
@@ -41,13 +49,32 @@ def run_oracle(oracle, op, x, result, **kw):
     return y, thr
 
 
-def assert_close(x, got, want, result, what):
+LONG_DOUBLE = 2
+
+
+def parity(oracle, op, x, got, result, what, **kw):
+    """Check got (GPU) against the oracle at the Result type and in long double."""
+    ref, _ = run_oracle(oracle, op, x, result, **dict(kw))
+    exact, _ = run_oracle(oracle, op, x, LONG_DOUBLE, **dict(kw))
     scale = np.maximum(1.0, np.abs(x.astype(np.float64)).max(axis=1, keepdims=True))
-    err = np.abs(got.astype(np.float64) - want.astype(np.float64)) / scale
-    bad = np.argwhere(err > RTOL[result])
+    g = got.astype(np.float64)
+    r = ref.astype(np.float64)
+    e = exact.astype(np.float64)
+    d_ref = np.abs(g - r) / scale
+    err_gpu = np.abs(g - e) / scale
+    err_ref = float((np.abs(r - e) / scale).max())
+    # Outputs are stored in the Data type: float data caps the precision.
+    rtol = max(RTOL[result], RTOL[F32] if x.dtype == np.float32 else RTOL[F64])
+    bad = np.argwhere(d_ref > rtol + 3 * err_ref)
     assert bad.size == 0, (
-        f"{what}: {len(np.unique(bad[:, 0]))} columns differ, max scaled err "
-        f"{err.max():.3e}; first column {bad[0, 0]}: got {got[bad[0, 0]][:8]} want {want[bad[0, 0]][:8]}")
+        f"{what}: {len(np.unique(bad[:, 0]))} columns differ from the reference, max scaled "
+        f"err {d_ref.max():.3e} (reference error E={err_ref:.3e}); column {bad[0, 0]}: "
+        f"got {got[bad[0, 0]][:6]} want {ref[bad[0, 0]][:6]}")
+    assert err_gpu.max() <= rtol + 2 * err_ref, (
+        f"{what}: GPU error vs exact {err_gpu.max():.3e} exceeds rtol + 2E "
+        f"(E={err_ref:.3e})")
+    if d_ref.max() > rtol:
+        print(f"{what}: max |gpu-ref|/s {d_ref.max():.2e} within rtol + 3E, E={err_ref:.2e}")
 
 
 DTYPES = [(np.float32, F32), (np.float32, F64), (np.float64, F64)]
@@ -78,8 +105,7 @@ def test_knapsack(cuda, oracle, op, kw, m, dtype, result):
         pytest.skip("infeasible bounds for this m")
     for name, x in cases(m, dtype, 10 + m):
         got, _ = run_gpu(op, x, result, cuda, **kw)
-        want, _ = run_oracle(oracle, op, x, result, **kw)
-        assert_close(x, got, want, result, f"{op} {name} m={m}")
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -92,8 +118,7 @@ def test_topk(cuda, oracle, op, k, m, dtype, result):
     kw = dict(k=k, rhs=1.0)
     for name, x in cases(m, dtype, 20 + m + k):
         got, _ = run_gpu(op, x, result, cuda, **kw)
-        want, _ = run_oracle(oracle, op, x, result, **kw)
-        assert_close(x, got, want, result, f"{op} k={k} {name} m={m}")
+        parity(oracle, op, x, got, result, f"{op} k={k} {name} m={m}", **kw)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -112,8 +137,7 @@ def test_entropic(cuda, oracle, op, kw, m, dtype, result):
                     ("normal", inputs.normal(n, m, dtype, 31 + m, 3.0)),
                     ("edge", inputs.edge_columns(m, dtype, 32 + m))]:
         got, _ = run_gpu(op, x, result, cuda, **kw)
-        want, _ = run_oracle(oracle, op, x, result, **kw)
-        assert_close(x, got, want, result, f"{op} {name} m={m}")
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -127,8 +151,7 @@ def test_topk_entropy(cuda, oracle, k, m, dtype, result):
                     ("label+2", inputs.label_shifted(n, m, dtype, 41 + m)),
                     ("edge", inputs.edge_columns(m, dtype, 42 + m))]:
         got, _ = run_gpu("topk_entropy", x, result, cuda, k=k)
-        want, _ = run_oracle(oracle, "topk_entropy", x, result, k=k)
-        assert_close(x, got, want, result, f"topk_entropy k={k} {name} m={m}")
+        parity(oracle, "topk_entropy", x, got, result, f"topk_entropy k={k} {name} m={m}", k=k)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -141,20 +164,17 @@ def test_two_simplex(cuda, oracle, m, dtype, result):
         for name, x in [("normal", inputs.normal(n, m, dtype, 51 + m)),
                         ("mixed", inputs.mixed_signs(n, m, dtype, 52 + m, -2, 2))]:
             got, _ = run_gpu("two_simplex", x, result, cuda, rhs=rhs, col_p=col_p)
-            want, _ = run_oracle(oracle, "two_simplex", x, result, rhs=rhs, col_p=col_p)
-            assert_close(x, got, want, result, f"two_simplex rhs={rhs} {name} m={m}")
+            parity(oracle, "two_simplex", x, got, result, f"two_simplex rhs={rhs} {name} m={m}", rhs=rhs, col_p=col_p)
             # scalar p for every column
             got, _ = run_gpu("two_simplex", x, result, cuda, rhs=rhs, p=1)
-            want, _ = run_oracle(oracle, "two_simplex", x, result, rhs=rhs, p=1)
-            assert_close(x, got, want, result, f"two_simplex p=1 rhs={rhs} {name} m={m}")
+            parity(oracle, "two_simplex", x, got, result, f"two_simplex p=1 rhs={rhs} {name} m={m}", rhs=rhs, p=1)
 
 
 def test_two_simplex_regression_vector(cuda, oracle):
     """The hard-coded vector of test/prox/two_simplex.cpp:55-64 (p=1, rhs=2)."""
     x = np.array([[-0.49371069182389915] + [0.49371069182390021] * 158], dtype=np.float64)
     got, _ = run_gpu("two_simplex", x, F64, cuda, rhs=2.0, p=1)
-    want, _ = run_oracle(oracle, "two_simplex", x, F64, rhs=2.0, p=1)
-    assert_close(x, got, want, F64, "two_simplex regression vector")
+    parity(oracle, "two_simplex", x, got, F64, "two_simplex regression vector", rhs=2.0, p=1)
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
@@ -187,8 +207,7 @@ def test_host_pointer_path(oracle):
     x = inputs.label_shifted(1000, 100, np.float32, 70)
     got = x.copy()
     sd.prox_topk_simplex(100, got, k=5, rhs=1.0)
-    want, _ = run_oracle(oracle, "topk_simplex", x, F32, k=5, rhs=1.0)
-    assert_close(x, got, want, F32, "host path topk_simplex")
+    parity(oracle, "topk_simplex", x, got, F32, "host path topk_simplex", k=5, rhs=1.0)
 
 
 def test_out_of_place(cuda, oracle):
@@ -200,5 +219,4 @@ def test_out_of_place(cuda, oracle):
     sd.prox("knapsack_eq", t, out=o)
     torch.cuda.synchronize()
     assert np.array_equal(t.cpu().numpy(), x), "input modified by an out-of-place call"
-    want, _ = run_oracle(oracle, "knapsack_eq", x, F64)
-    assert_close(x, o.cpu().numpy(), want, F64, "out of place knapsack_eq")
+    parity(oracle, "knapsack_eq", x, o.cpu().numpy(), F64, "out of place knapsack_eq")
