@@ -109,41 +109,109 @@ __device__ inline double lambert_w_exp(double x) {
 }
 
 // ---------------------------------------------------------------------------
+// Cross-lane exchange lane <-> lane ^ OFF inside a wave: DPP quad
+// permutations for OFF = 1, 2 (a VALU operand modifier, no LDS traffic),
+// ds_swizzle in xor mode for OFF = 4, 8, 16, ds_bpermute for 32.
+// ---------------------------------------------------------------------------
+template <int OFF>
+__device__ inline int xor_lane(int v) {
+  if constexpr (OFF == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (OFF == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (OFF < 32) {
+    return __builtin_amdgcn_ds_swizzle(v, (OFF << 10) | 0x1F);  // and 0x1F, xor OFF
+  } else {
+    return __shfl_xor(v, OFF, 64);
+  }
+}
+template <int OFF>
+__device__ inline float xor_lane(float v) {
+  return __int_as_float(xor_lane<OFF>(__float_as_int(v)));
+}
+template <int OFF>
+__device__ inline double xor_lane(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = xor_lane<OFF>(static_cast<int>(b & 0xffffffffll));
+  const int hi = xor_lane<OFF>(static_cast<int>(b >> 32));
+  return __longlong_as_double((static_cast<long long>(hi) << 32) |
+                              (static_cast<long long>(static_cast<unsigned>(lo))));
+}
+
+// ---------------------------------------------------------------------------
 // Reductions over a group of G adjacent lanes of a wave (G a power of two,
 // groups aligned to G).  Every lane of the group receives the result.
 // ---------------------------------------------------------------------------
 template <int G, class T>
 __device__ inline T group_sum(T x) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off /= 2) x += __shfl_xor(x, off, 64);
+  if constexpr (G >= 64) x += xor_lane<32>(x);
+  if constexpr (G >= 32) x += xor_lane<16>(x);
+  if constexpr (G >= 16) x += xor_lane<8>(x);
+  if constexpr (G >= 8) x += xor_lane<4>(x);
+  if constexpr (G >= 4) x += xor_lane<2>(x);
+  if constexpr (G >= 2) x += xor_lane<1>(x);
   return x;
+}
+template <int OFF, class T>
+__device__ inline T max_step(T x) {
+  T y = xor_lane<OFF>(x);
+  return (y > x) ? y : x;
+}
+template <int OFF, class T>
+__device__ inline T min_step(T x) {
+  T y = xor_lane<OFF>(x);
+  return (y < x) ? y : x;
 }
 template <int G, class T>
 __device__ inline T group_max(T x) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off /= 2) {
-    T y = __shfl_xor(x, off, 64);
-    x = (y > x) ? y : x;
-  }
+  if constexpr (G >= 64) x = max_step<32>(x);
+  if constexpr (G >= 32) x = max_step<16>(x);
+  if constexpr (G >= 16) x = max_step<8>(x);
+  if constexpr (G >= 8) x = max_step<4>(x);
+  if constexpr (G >= 4) x = max_step<2>(x);
+  if constexpr (G >= 2) x = max_step<1>(x);
   return x;
 }
 template <int G, class T>
 __device__ inline T group_min(T x) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off /= 2) {
-    T y = __shfl_xor(x, off, 64);
-    x = (y < x) ? y : x;
-  }
+  if constexpr (G >= 64) x = min_step<32>(x);
+  if constexpr (G >= 32) x = min_step<16>(x);
+  if constexpr (G >= 16) x = min_step<8>(x);
+  if constexpr (G >= 8) x = min_step<4>(x);
+  if constexpr (G >= 4) x = min_step<2>(x);
+  if constexpr (G >= 2) x = min_step<1>(x);
   return x;
+}
+// Exclusive prefix sum over the group (lane order g = 0..G-1).
+template <int G>
+__device__ inline int group_exclusive_scan(int x, int g) {
+  int incl = x;
+  if constexpr (G >= 2) { int y = xor_lane<1>(incl); if (g & 1) incl += y; }
+  // After step s every lane holds the inclusive sum of its aligned block of
+  // 2^(s+1) lanes restricted to lanes <= itself; the xor partner supplies the
+  // lower half's total.
+  if constexpr (G >= 4) { int t = __shfl(incl, (threadIdx.x & ~3) | 1, 64); if (g & 2) incl += t; }
+  if constexpr (G >= 8) { int t = __shfl(incl, (threadIdx.x & ~7) | 3, 64); if (g & 4) incl += t; }
+  if constexpr (G >= 16) { int t = __shfl(incl, (threadIdx.x & ~15) | 7, 64); if (g & 8) incl += t; }
+  if constexpr (G >= 32) { int t = __shfl(incl, (threadIdx.x & ~31) | 15, 64); if (g & 16) incl += t; }
+  if constexpr (G >= 64) { int t = __shfl(incl, (threadIdx.x & ~63) | 31, 64); if (g & 32) incl += t; }
+  return incl - x;
 }
 
 // Sorted (descending) top list of L values, insertion of one value:
-// new[i] = max(old[i], min(old[i-1], x)) = median(old[i-1], old[i], x).
-template <int L, class D>
-__device__ inline void top_insert(D (&top)[L], D x) {
+// new[i] = max(old[i], min(old[i-1], x)) = median(old[i-1], old[i], x), one
+// v_med3_f32 per level for float.
+template <int L>
+__device__ inline void top_insert(float (&top)[L], float x) {
+#pragma unroll
+  for (int i = L - 1; i >= 1; --i) top[i] = __builtin_amdgcn_fmed3f(top[i - 1], top[i], x);
+  top[0] = fmaxf(top[0], x);
+}
+template <int L>
+__device__ inline void top_insert(double (&top)[L], double x) {
 #pragma unroll
   for (int i = L - 1; i >= 1; --i) {
-    D lo = (top[i - 1] < x) ? top[i - 1] : x;
+    double lo = (top[i - 1] < x) ? top[i - 1] : x;
     top[i] = (top[i] < lo) ? lo : top[i];
   }
   top[0] = (top[0] < x) ? x : top[0];
@@ -151,16 +219,22 @@ __device__ inline void top_insert(D (&top)[L], D x) {
 
 // Merge the top lists of the G lanes of a group (every lane ends with the
 // top L values of the union, as a multiset).
+template <int OFF, int L, class D>
+__device__ inline void top_merge_step(D (&top)[L]) {
+  D other[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) other[i] = xor_lane<OFF>(top[i]);
+#pragma unroll
+  for (int i = 0; i < L; ++i) top_insert(top, other[i]);
+}
 template <int G, int L, class D>
 __device__ inline void top_merge(D (&top)[L]) {
-#pragma unroll
-  for (int off = G / 2; off >= 1; off /= 2) {
-    D other[L];
-#pragma unroll
-    for (int i = 0; i < L; ++i) other[i] = __shfl_xor(top[i], off, 64);
-#pragma unroll
-    for (int i = 0; i < L; ++i) top_insert(top, other[i]);
-  }
+  if constexpr (G >= 64) top_merge_step<32>(top);
+  if constexpr (G >= 32) top_merge_step<16>(top);
+  if constexpr (G >= 16) top_merge_step<8>(top);
+  if constexpr (G >= 8) top_merge_step<4>(top);
+  if constexpr (G >= 4) top_merge_step<2>(top);
+  if constexpr (G >= 2) top_merge_step<1>(top);
 }
 
 }  // namespace sdca_gpu

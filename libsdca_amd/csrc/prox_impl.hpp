@@ -92,7 +92,7 @@ struct KnapState {
 };
 
 template <int G, int C, class D, class R>
-__device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, R total,
+__device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nvalid, R total,
                                                 R lo, R hi, R rhs) {
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   int mc = m;
@@ -110,6 +110,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, R total,
     int n_lo = 0, n_hi = 0;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
+      if (c >= nvalid) continue;
       const R x = static_cast<R>(v[c]);
       const bool fr = (x > st.lo_cut) && !(x > st.hi_cut);
       const bool gl = x > c_lo;
@@ -151,6 +152,71 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, R total,
   return st;
 }
 
+// The same variable fixing over a short list b[0, cnt) held in LDS, run by
+// every lane of the group on identical data (no divergence, no broadcast).
+template <class D, class R>
+__device__ inline KnapState<R> knapsack_list(const D* b, int cnt, R lo, R hi, R rhs) {
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  R total = 0;
+  for (int i = 0; i < cnt; ++i) total += static_cast<R>(b[i]);
+  int mc = cnt;
+  R t = (total - rhs) / static_cast<R>(cnt);
+  KnapState<R> st;
+  st.lo_cut = -num<R>::inf();
+  st.hi_cut = num<R>::inf();
+  st.c_lo = -num<R>::inf();
+  st.c_hi = num<R>::inf();
+  st.n_u = 0;
+  st.sum_u = 0;
+  for (int iter = 0; iter <= cnt; ++iter) {
+    const R c_lo = lo + t, c_hi = hi + t;
+    R s_lo = 0, s_hi = 0;
+    int n_lo = 0, n_hi = 0;
+    for (int i = 0; i < cnt; ++i) {
+      const R x = static_cast<R>(b[i]);
+      const bool fr = (x > st.lo_cut) && !(x > st.hi_cut);
+      const bool gl = x > c_lo;
+      if (fr && !gl) { s_lo += x; ++n_lo; }
+      if (fr && gl && x > c_hi) { s_hi += x; ++n_hi; }
+    }
+    const R sh = static_cast<R>(n_hi) * hi;
+    const R sl = static_cast<R>(n_lo) * lo;
+    const R infeas = s_hi + s_lo - (sh + sl) - static_cast<R>(n_hi + n_lo) * t;
+    R next;
+    if (n_hi > 0 && infeas > eps) {
+      st.hi_cut = dmin(st.hi_cut, dmax(c_lo, c_hi));
+      next = static_cast<R>(mc) * t - s_hi + sh;
+      mc -= n_hi;
+      st.n_u += n_hi;
+      st.sum_u += s_hi;
+    } else if (n_lo > 0 && infeas < -eps) {
+      st.lo_cut = dmax(st.lo_cut, c_lo);
+      next = static_cast<R>(mc) * t - s_lo + sl;
+      mc -= n_lo;
+    } else {
+      st.c_lo = c_lo;
+      st.c_hi = c_hi;
+      st.n_u += n_hi;
+      st.sum_u += s_hi;
+      break;
+    }
+    if (mc > 0) {
+      t = next / static_cast<R>(mc);
+    } else {
+      break;
+    }
+  }
+  st.t = t;
+  return st;
+}
+
+// Make LDS writes of this wave visible to its own later reads.
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---------------------------------------------------------------------------
 // Knapsack family: knapsack_eq (knapsack_eq.h:25-109) and knapsack_le
 // (knapsack_le.h:17-44).
@@ -177,7 +243,7 @@ __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
     if (!(s > rhs + eps)) return make_thr<R>(R(0), lo, hi);
   }
   const R total = total_sum<G, C, D, R>(v, nvalid);
-  KnapState<R> st = knapsack_eq_regs<G, C, D, R>(v, m, total, lo, hi, rhs);
+  KnapState<R> st = knapsack_eq_regs<G, C, D, R>(v, m, nvalid, total, lo, hi, rhs);
   return make_thr<R>(st.t, lo, hi);
 }
 
@@ -196,13 +262,14 @@ struct TopkSel {
 };
 
 template <int G, int C, int KM, class D, class R>
-__device__ inline TopkSel<R> topk_select(const D (&v)[C], int k) {
+__device__ inline TopkSel<R> topk_select(const D (&v)[C], int nvalid, int k) {
   constexpr int L = KM + 1;
   D top[L];
 #pragma unroll
   for (int i = 0; i < L; ++i) top[i] = -num<D>::inf();
 #pragma unroll
-  for (int c = 0; c < C; ++c) top_insert(top, v[c]);
+  for (int c = 0; c < C; ++c)
+    if (c < nvalid) top_insert(top, v[c]);
   top_merge<G>(top);
   TopkSel<R> s;
   s.sum_k = 0;
@@ -246,13 +313,47 @@ __device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
   return slow_thr<R>();
 }
 
+// Columns with more candidates than this run the variable fixing over all
+// register slots instead of the compacted list.
+constexpr int kCandMax = 64;
+
+// Variable fixing for the top-k simplex's knapsack (lo = 0, hi = rhs / k):
+// its root t* satisfies sum_i clamp(a_i - t*, 0, hi) = k hi, hence
+// a_(k) - hi <= t* < a_(k) (the k largest each give hi at t = a_(k) - hi;
+// fewer than k can be positive at t = a_(k)).  Elements at or below a_(k) - hi
+// end at the lower bound whatever the iteration does, so the fixing runs over
+// the few values above that cut, compacted into the column's LDS slots; the
+// cut is widened by a few ulps so that rounding of hi = rhs / k cannot drop a
+// contributor.
+template <int G, int C, class D, class R>
+__device__ inline KnapState<R> topk_knapsack(const D (&v)[C], int m, int nvalid, R kth, R hi,
+                                             R rhs, D* lds_col) {
+  const R cut = kth - hi - (fabs(kth) + hi) * (R(16) * num<R>::eps());
+  int cn = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    if (c < nvalid && static_cast<R>(v[c]) > cut) ++cn;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const int total = group_sum<G>(cn);
+  if (total >= 1 && total <= kCandMax) {
+    int pos = group_exclusive_scan<G>(cn, g);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      if (c < nvalid && static_cast<R>(v[c]) > cut) lds_col[pos++] = v[c];
+    wave_lds_sync();
+    return knapsack_list<D, R>(lds_col, total, R(0), hi, rhs);
+  }
+  const R all = total_sum<G, C, D, R>(v, nvalid);
+  return knapsack_eq_regs<G, C, D, R>(v, m, nvalid, all, R(0), hi, rhs);
+}
+
 template <int G, int C, int KM, class D, class R>
 __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
-                                        const ProxParamsT<R>& pp) {
+                                        const ProxParamsT<R>& pp, D* lds_col) {
   const int k = pp.k;
   const R K = static_cast<R>(k);
   const R eps16 = R(16) * num<R>::eps();
-  TopkSel<R> sel = topk_select<G, C, KM, D, R>(v, k);
+  TopkSel<R> sel = topk_select<G, C, KM, D, R>(v, nvalid, k);
   // topk_cone_special_cases (topk_cone.h:18-55)
   if (sel.sum_k <= eps16) return make_thr<R>(R(0), R(0), R(0));
   const R hi_c = sel.sum_k / K;
@@ -266,8 +367,8 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   const R rhs = pp.rhs;
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   if (constant && !(K * hi_c > rhs + eps)) return make_thr<R>(t_c, R(0), hi_c);
-  const R total = total_sum<G, C, D, R>(v, nvalid);
-  KnapState<R> st = knapsack_eq_regs<G, C, D, R>(v, m, total, R(0), rhs / K, rhs);
+  const R hi = rhs / K;
+  KnapState<R> st = topk_knapsack<G, C, D, R>(v, m, nvalid, sel.kth, hi, rhs, lds_col);
   if (!constant) {
     // is_topk_simplex_lt (topk_simplex.h:9-27) over U = [first, t.first)
     bool lt;
@@ -279,7 +380,7 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
     }
     if (lt) return cone_search_u0<G, C, D, R>(v, K, sel.first);
   }
-  return make_thr<R>(st.t, R(0), rhs / K);
+  return make_thr<R>(st.t, R(0), hi);
 }
 
 // ---------------------------------------------------------------------------
@@ -659,7 +760,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   if constexpr (FAM == FAM_KNAP) {
     th = knap_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPK) {
-    th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp);
+    th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, tile + lc * m);
   } else if constexpr (FAM == FAM_ENT) {
     th = ent_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPKENT) {
@@ -672,12 +773,16 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   if (active) {
     const D t1 = static_cast<D>(th.t), lo1 = static_cast<D>(th.lo), hi1 = static_cast<D>(th.hi);
     const D t2 = static_cast<D>(th.t2), lo2 = static_cast<D>(th.lo2), hi2 = static_cast<D>(th.hi2);
+    // Deferred columns put their input back: the threshold search may have
+    // used the column's LDS slots as scratch, and the workgroup-per-column
+    // kernel reads the input again (in place when in == out).
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      if (c < nvalid && !th.slow) {
+      if (c < nvalid) {
         const int idx = g + G * c;
         const bool second = (FAM == FAM_TWO) && idx >= p;
-        tile[lc * m + idx] = second ? apply_map<D, R>(v[c], t2, lo2, hi2, 0)
+        tile[lc * m + idx] = th.slow ? v[c]
+                           : second ? apply_map<D, R>(v[c], t2, lo2, hi2, 0)
                                     : apply_map<D, R>(v[c], t1, lo1, hi1, th.kind);
       }
     }

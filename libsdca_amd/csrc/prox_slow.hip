@@ -19,11 +19,19 @@ namespace sdca_gpu {
 
 namespace {
 
+// Sums over ranges of the sorted column.  Summing a sorted sequence in order
+// is the worst case for rounding (all positives, then the cancelling
+// negatives), so the sum is compensated (Neumaier) in double.
 template <class R, class D>
 __device__ R sum_range(const D* s, int b, int e) {
-  R acc = 0;
-  for (int i = b; i < e; ++i) acc += static_cast<R>(s[i]);
-  return acc;
+  double acc = 0, comp = 0;
+  for (int i = b; i < e; ++i) {
+    const double x = static_cast<double>(static_cast<R>(s[i]));
+    const double t = acc + x;
+    comp += (fabs(acc) >= fabs(x)) ? (acc - t) + x : (x - t) + acc;
+    acc = t;
+  }
+  return static_cast<R>(acc + comp);
 }
 
 // Kiwiel variable fixing on a column sorted in descending order.
