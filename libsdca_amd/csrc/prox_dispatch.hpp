@@ -9,7 +9,11 @@ namespace sdca_gpu {
 
 template <int FAM, int KM, class D, class R, int G, int C>
 hipError_t launch_one(const ProxLaunch& a) {
-  constexpr int B = 256 / G;
+#ifndef SDCA_PROX_BT
+#define SDCA_PROX_BT 64
+#endif
+  constexpr int BT = SDCA_PROX_BT;  // threads per workgroup (default: one wave)
+  constexpr int B = BT / G;
   ProxParamsT<R> pp;
   pp.lo = static_cast<R>(a.lo);
   pp.hi = static_cast<R>(a.hi);
@@ -18,18 +22,25 @@ hipError_t launch_one(const ProxLaunch& a) {
   pp.op = a.op;
   pp.p = static_cast<int>(a.p);
   const int64_t blocks = (a.n + B - 1) / B;
-  const size_t shmem = static_cast<size_t>(B) * static_cast<size_t>(a.m) * sizeof(D);
-  hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(256), shmem, a.stream, static_cast<const D*>(a.in),
-                     static_cast<D*>(a.out), a.m, a.n, pp, a.col_p, a.thr, a.slow);
+  // B*m tile, G*C words of slack for branch-free slot reads, BT dummy words.
+  const size_t shmem = (static_cast<size_t>(B) * static_cast<size_t>(a.m) + G * C + BT) * sizeof(D);
+  hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
+                     static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp, a.col_p,
+                     a.thr, a.slow);
   return hipGetLastError();
 }
 
-// m -> (G, C): the fewest lanes per column whose C slots hold the column.
+// m -> (G lanes per column, C slots per lane): the fewest lanes whose C
+// slots hold the column (C = 25 fits m = 100 exactly on four lanes).
 template <int FAM, int KM, class D, class R>
 hipError_t launch_by_m(const ProxLaunch& a) {
   if (a.m <= 16) return launch_one<FAM, KM, D, R, 1, 16>(a);
   if (a.m <= 64) return launch_one<FAM, KM, D, R, 4, 16>(a);
+#ifndef SDCA_M100_G
+#define SDCA_M100_G 4
+#endif
+  if (a.m <= 100) return launch_one<FAM, KM, D, R, SDCA_M100_G, 100 / SDCA_M100_G>(a);
   if (a.m <= 128) return launch_one<FAM, KM, D, R, 4, 32>(a);
   if (a.m <= 256) return launch_one<FAM, KM, D, R, 16, 16>(a);
   if (a.m <= 512) return launch_one<FAM, KM, D, R, 16, 32>(a);

@@ -3,7 +3,7 @@
 // (proxdef.h:279-324) of libsdca v0.3.1.
 //
 // Layout.  The input is an m x n column-major matrix; columns are contiguous.
-// A 256-thread workgroup owns B = 256 / G consecutive columns: it copies their
+// A one-wave workgroup owns B = 64 / G consecutive columns: it copies their
 // B*m contiguous elements into LDS with 16-byte loads (fully coalesced), then
 // each group of G adjacent lanes takes one column, lane g holding elements
 // g, g+G, g+2G, ... in C registers (slots past m hold -inf, which every pass
@@ -70,8 +70,7 @@ template <int G, int C, class D, class R>
 __device__ inline R total_sum(const D (&v)[C], int nvalid) {
   R s = 0;
 #pragma unroll
-  for (int c = 0; c < C; ++c)
-    if (c < nvalid) s += static_cast<R>(v[c]);
+  for (int c = 0; c < C; ++c) s += (c < nvalid) ? static_cast<R>(v[c]) : R(0);
   return group_sum<G>(s);
 }
 
@@ -110,8 +109,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
     int n_lo = 0, n_hi = 0;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      if (c >= nvalid) continue;
-      const R x = static_cast<R>(v[c]);
+      const R x = static_cast<R>(v[c]);  // padding (-inf) is never free
       const bool fr = (x > st.lo_cut) && !(x > st.hi_cut);
       const bool gl = x > c_lo;
       if (fr && !gl) { s_lo += x; ++n_lo; }
@@ -268,8 +266,7 @@ __device__ inline TopkSel<R> topk_select(const D (&v)[C], int nvalid, int k) {
 #pragma unroll
   for (int i = 0; i < L; ++i) top[i] = -num<D>::inf();
 #pragma unroll
-  for (int c = 0; c < C; ++c)
-    if (c < nvalid) top_insert(top, v[c]);
+  for (int c = 0; c < C; ++c) top_insert(top, v[c]);  // -inf padding leaves it unchanged
   top_merge<G>(top);
   TopkSel<R> s;
   s.sum_k = 0;
@@ -297,8 +294,10 @@ __device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const R x = static_cast<R>(v[c]);
-    if (x > eps16) { s_p += x; ++n_p; }
-    else if (x >= -eps16) ++n_z;
+    const bool pos = x > eps16;
+    s_p += pos ? x : R(0);
+    n_p += pos ? 1 : 0;
+    n_z += (!pos && x >= -eps16) ? 1 : 0;
   }
   s_p = group_sum<G>(s_p);
   n_p = group_sum<G>(n_p);
@@ -313,6 +312,69 @@ __device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
   return slow_thr<R>();
 }
 
+// Variable fixing over the first cnt entries of a sorted register list
+// (compile-time length L, so the list stays in registers).
+template <int L, class D, class R>
+__device__ inline KnapState<R> knapsack_top(const D (&b)[L], int cnt, R lo, R hi, R rhs) {
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  R total = 0;
+#pragma unroll
+  for (int i = 0; i < L; ++i) total += (i < cnt) ? static_cast<R>(b[i]) : R(0);
+  int mc = cnt;
+  R t = (total - rhs) / static_cast<R>(cnt);
+  KnapState<R> st;
+  st.lo_cut = -num<R>::inf();
+  st.hi_cut = num<R>::inf();
+  st.c_lo = -num<R>::inf();
+  st.c_hi = num<R>::inf();
+  st.n_u = 0;
+  st.sum_u = 0;
+  for (int iter = 0; iter <= L; ++iter) {
+    const R c_lo = lo + t, c_hi = hi + t;
+    R s_lo = 0, s_hi = 0;
+    int n_lo = 0, n_hi = 0;
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      const R x = static_cast<R>(b[i]);
+      const bool fr = (i < cnt) && (x > st.lo_cut) && !(x > st.hi_cut);
+      const bool gl = x > c_lo;
+      const bool lo_c = fr && !gl, hi_c = fr && gl && x > c_hi;
+      s_lo += lo_c ? x : R(0);
+      n_lo += lo_c ? 1 : 0;
+      s_hi += hi_c ? x : R(0);
+      n_hi += hi_c ? 1 : 0;
+    }
+    const R sh = static_cast<R>(n_hi) * hi;
+    const R sl = static_cast<R>(n_lo) * lo;
+    const R infeas = s_hi + s_lo - (sh + sl) - static_cast<R>(n_hi + n_lo) * t;
+    R next;
+    if (n_hi > 0 && infeas > eps) {
+      st.hi_cut = dmin(st.hi_cut, dmax(c_lo, c_hi));
+      next = static_cast<R>(mc) * t - s_hi + sh;
+      mc -= n_hi;
+      st.n_u += n_hi;
+      st.sum_u += s_hi;
+    } else if (n_lo > 0 && infeas < -eps) {
+      st.lo_cut = dmax(st.lo_cut, c_lo);
+      next = static_cast<R>(mc) * t - s_lo + sl;
+      mc -= n_lo;
+    } else {
+      st.c_lo = c_lo;
+      st.c_hi = c_hi;
+      st.n_u += n_hi;
+      st.sum_u += s_hi;
+      break;
+    }
+    if (mc > 0) {
+      t = next / static_cast<R>(mc);
+    } else {
+      break;
+    }
+  }
+  st.t = t;
+  return st;
+}
+
 // Columns with more candidates than this run the variable fixing over all
 // register slots instead of the compacted list.
 constexpr int kCandMax = 64;
@@ -325,23 +387,41 @@ constexpr int kCandMax = 64;
 // the few values above that cut, compacted into the column's LDS slots; the
 // cut is widened by a few ulps so that rounding of hi = rhs / k cannot drop a
 // contributor.
-template <int G, int C, class D, class R>
-__device__ inline KnapState<R> topk_knapsack(const D (&v)[C], int m, int nvalid, R kth, R hi,
-                                             R rhs, D* lds_col) {
+template <int G, int C, int L, class D, class R>
+__device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L], int m,
+                                             int nvalid, R kth, R hi, R rhs, D* lds_col,
+                                             D* lds_dummy) {
   const R cut = kth - hi - (fabs(kth) + hi) * (R(16) * num<R>::eps());
-  int cn = 0;
+#ifndef SDCA_TOPK_LIST_KNAPSACK
+#define SDCA_TOPK_LIST_KNAPSACK 0
+#endif
+  // When every value above the cut is in the sorted top list, solve there.
+  if (SDCA_TOPK_LIST_KNAPSACK && !(static_cast<R>(top[L - 1]) > cut)) {
+    int cnt = 0;
 #pragma unroll
-  for (int c = 0; c < C; ++c)
-    if (c < nvalid && static_cast<R>(v[c]) > cut) ++cn;
-  const int g = static_cast<int>(threadIdx.x) % G;
-  const int total = group_sum<G>(cn);
-  if (total >= 1 && total <= kCandMax) {
-    int pos = group_exclusive_scan<G>(cn, g);
+    for (int i = 0; i < L; ++i) cnt += (static_cast<R>(top[i]) > cut) ? 1 : 0;
+    return knapsack_top<L, D, R>(top, cnt, R(0), hi, rhs);
+  }
+  if (lds_col != nullptr) {
+    int cn = 0;
 #pragma unroll
-    for (int c = 0; c < C; ++c)
-      if (c < nvalid && static_cast<R>(v[c]) > cut) lds_col[pos++] = v[c];
-    wave_lds_sync();
-    return knapsack_list<D, R>(lds_col, total, R(0), hi, rhs);
+    for (int c = 0; c < C; ++c) cn += (static_cast<R>(v[c]) > cut) ? 1 : 0;
+    const int g = static_cast<int>(threadIdx.x) % G;
+    const int total = group_sum<G>(cn);
+    if (total <= kCandMax) {
+      // Branch-free compaction: every slot is stored, non-candidates to the
+      // lane's own dummy word (distinct per lane, so no bank serialisation).
+      int pos = group_exclusive_scan<G>(cn, g);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const bool pr = static_cast<R>(v[c]) > cut;
+        D* dst = pr ? lds_col + pos : lds_dummy;
+        *dst = v[c];
+        pos += pr ? 1 : 0;
+      }
+      wave_lds_sync();
+      return knapsack_list<D, R>(lds_col, total, R(0), hi, rhs);
+    }
   }
   const R all = total_sum<G, C, D, R>(v, nvalid);
   return knapsack_eq_regs<G, C, D, R>(v, m, nvalid, all, R(0), hi, rhs);
@@ -349,26 +429,41 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], int m, int nvalid,
 
 template <int G, int C, int KM, class D, class R>
 __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
-                                        const ProxParamsT<R>& pp, D* lds_col) {
+                                        const ProxParamsT<R>& pp, D* lds_col, D* lds_dummy) {
   const int k = pp.k;
   const R K = static_cast<R>(k);
   const R eps16 = R(16) * num<R>::eps();
-  TopkSel<R> sel = topk_select<G, C, KM, D, R>(v, nvalid, k);
+  constexpr int L = KM + 1;
+  D top[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) top[i] = -num<D>::inf();
+#pragma unroll
+  for (int c = 0; c < C; ++c) top_insert(top, v[c]);  // -inf padding leaves it unchanged
+  top_merge<G>(top);
+  R sum_k = 0, kth = static_cast<R>(top[0]), next = -num<R>::inf();
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    if (i < k) sum_k += static_cast<R>(top[i]);
+    if (i == k - 1) kth = static_cast<R>(top[i]);
+    if (i == k) next = static_cast<R>(top[i]);
+  }
+  const R largest = static_cast<R>(top[0]);
   // topk_cone_special_cases (topk_cone.h:18-55)
-  if (sel.sum_k <= eps16) return make_thr<R>(R(0), R(0), R(0));
-  const R hi_c = sel.sum_k / K;
-  const R t_c = sel.kth - hi_c;
-  const bool constant = (k == m) || (t_c >= sel.next - eps16);
+  if (sum_k <= eps16) return make_thr<R>(R(0), R(0), R(0));
+  const R hi_c = sum_k / K;
+  const R t_c = kth - hi_c;
+  const bool constant = (k == m) || (t_c >= next - eps16);
   if (pp.op == OP_TOPK_CONE) {
     if (constant) return make_thr<R>(t_c, R(0), hi_c);
-    return cone_search_u0<G, C, D, R>(v, K, sel.first);
+    return cone_search_u0<G, C, D, R>(v, K, largest);
   }
   // thresholds_topk_simplex (topk_simplex.h:39-68)
   const R rhs = pp.rhs;
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   if (constant && !(K * hi_c > rhs + eps)) return make_thr<R>(t_c, R(0), hi_c);
   const R hi = rhs / K;
-  KnapState<R> st = topk_knapsack<G, C, D, R>(v, m, nvalid, sel.kth, hi, rhs, lds_col);
+  KnapState<R> st = topk_knapsack<G, C, L, D, R>(v, top, m, nvalid, kth, hi, rhs, lds_col,
+                                                  lds_dummy);
   if (!constant) {
     // is_topk_simplex_lt (topk_simplex.h:9-27) over U = [first, t.first)
     bool lt;
@@ -378,7 +473,7 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
       const R num_u = static_cast<R>(st.n_u);
       lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * num_u - eps;
     }
-    if (lt) return cone_search_u0<G, C, D, R>(v, K, sel.first);
+    if (lt) return cone_search_u0<G, C, D, R>(v, K, largest);
   }
   return make_thr<R>(st.t, R(0), hi);
 }
@@ -703,7 +798,7 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
 // Tile copies between global memory and LDS, 16 bytes per lane when both
 // sides are 16-byte aligned.
 // ---------------------------------------------------------------------------
-template <class D>
+template <int BT, class D>
 __device__ inline void tile_copy(D* __restrict__ dst, const D* __restrict__ src,
                                  int64_t count) {
   const int64_t bytes = count * static_cast<int64_t>(sizeof(D));
@@ -712,11 +807,62 @@ __device__ inline void tile_copy(D* __restrict__ dst, const D* __restrict__ src,
     const int64_t nv = bytes / 16;
     const uint4* s4 = reinterpret_cast<const uint4*>(src);
     uint4* d4 = reinterpret_cast<uint4*>(dst);
-    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) d4[i] = s4[i];
+    for (int64_t i = threadIdx.x; i < nv; i += BT) d4[i] = s4[i];
     const int64_t done = nv * 16 / static_cast<int64_t>(sizeof(D));
-    for (int64_t i = done + threadIdx.x; i < count; i += blockDim.x) dst[i] = src[i];
+    for (int64_t i = done + threadIdx.x; i < count; i += BT) dst[i] = src[i];
   } else {
-    for (int64_t i = threadIdx.x; i < count; i += blockDim.x) dst[i] = src[i];
+    for (int64_t i = threadIdx.x; i < count; i += BT) dst[i] = src[i];
+  }
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Global -> LDS copy of a column tile with every 16-byte load of the thread
+// issued before the first LDS store (NV = the most loads a thread can have
+// for this configuration), so the whole tile is in flight at once.  Blocks
+// are one wave, so a tile is a few KiB: HBM streams best when many small
+// blocks each touch a short contiguous range (a 32 KiB-per-block copy runs
+// ~30% slower than a 4 KiB one on MI355X).
+template <int NV, int BT, class D>
+__device__ inline void tile_load(D* __restrict__ dst, const D* __restrict__ src, int64_t count) {
+  const int64_t bytes = count * static_cast<int64_t>(sizeof(D));
+  const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+  if (!vec || bytes % 16 != 0) {
+    tile_copy<BT>(dst, src, count);
+    return;
+  }
+  const int nv = static_cast<int>(bytes / 16);
+  const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+  u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+  u32x4 r[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = i * BT + static_cast<int>(threadIdx.x);
+    if (idx < nv) r[i] = __builtin_nontemporal_load(s4 + idx);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = i * BT + static_cast<int>(threadIdx.x);
+    if (idx < nv) d4[idx] = r[i];
+  }
+}
+
+// LDS -> global copy; stores are fire-and-forget, streamed past the caches.
+template <int NV, int BT, class D>
+__device__ inline void tile_store(D* __restrict__ dst, const D* __restrict__ src, int64_t count) {
+  const int64_t bytes = count * static_cast<int64_t>(sizeof(D));
+  const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+  if (!vec || bytes % 16 != 0) {
+    tile_copy<BT>(dst, src, count);
+    return;
+  }
+  const int nv = static_cast<int>(bytes / 16);
+  const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+  u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = i * BT + static_cast<int>(threadIdx.x);
+    if (idx < nv) __builtin_nontemporal_store(s4[idx], d4 + idx);
   }
 }
 
@@ -729,65 +875,90 @@ __device__ inline D apply_map(D x, D t, D lo, D hi, int kind) {
 }
 
 // ---------------------------------------------------------------------------
-// The batched kernel.  Block = 256 threads = B columns of G lanes.
+// The batched kernel.  Block = BT threads (one wave) = BT / G columns of G
+// lanes each.
 // ---------------------------------------------------------------------------
-template <int FAM, int KM, class D, class R, int G, int C>
-__global__ void __launch_bounds__(256)
+template <int FAM, int KM, class D, class R, int G, int C, int BT>
+__global__ void __launch_bounds__(BT)
 prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
                     int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
                     sdca_thresholds* __restrict__ thr, int* __restrict__ slow) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* tile = reinterpret_cast<D*>(smem_raw);
-  constexpr int B = 256 / G;
+  constexpr int B = BT / G;
+  // Most 16-byte transfers per thread: B m sizeof(D) / (16 BT) <= C sizeof(D) / 16.
+  constexpr int NV = (C * static_cast<int>(sizeof(D)) + 15) / 16;
   const int m = static_cast<int>(m64);
   const int64_t col0 = static_cast<int64_t>(blockIdx.x) * B;
   const int ncols = static_cast<int>(min(static_cast<int64_t>(B), n - col0));
   const int64_t count = static_cast<int64_t>(ncols) * m;
-  tile_copy(tile, in + col0 * m64, count);
-  __syncthreads();
-
   const int lc = static_cast<int>(threadIdx.x) / G;
   const int g = static_cast<int>(threadIdx.x) % G;
   const bool active = lc < ncols;
+  const int64_t j = col0 + lc;
+
+  tile_load<NV, BT>(tile, in + col0 * m64, count);
+  __syncthreads();
   const int nvalid = active ? (m - g + G - 1) / G : 0;
+  // The tile has G*C words of slack after the B*m elements, so every slot
+  // read stays inside the allocation and the loop needs no branch; past the
+  // tile sit BT per-lane dummy words for predicated stores.
+  D* const lds_dummy = tile + B * m + G * C + threadIdx.x;
   D v[C];
 #pragma unroll
-  for (int c = 0; c < C; ++c)
-    v[c] = (c < nvalid) ? tile[lc * m + g + G * c] : -num<D>::inf();
+  for (int c = 0; c < C; ++c) {
+    const D x = tile[lc * m + g + G * c];
+    v[c] = (c < nvalid) ? x : -num<D>::inf();
+  }
 
   ColThr<R> th;
   int p = pp.p;
   if constexpr (FAM == FAM_KNAP) {
     th = knap_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPK) {
-    th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, tile + lc * m);
+    th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, tile + lc * m, lds_dummy);
   } else if constexpr (FAM == FAM_ENT) {
     th = ent_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPKENT) {
     th = topkent_family<G, C, D, R>(v, m, nvalid, pp);
   } else {
-    if (col_p && active) p = static_cast<int>(col_p[col0 + lc]);
+    if (col_p && active) p = static_cast<int>(col_p[j]);
     th = two_family<G, C, D, R>(v, m, p, pp);
   }
 
+  // The threshold search may have used the column's LDS slots as scratch.
+  __syncthreads();
   if (active) {
     const D t1 = static_cast<D>(th.t), lo1 = static_cast<D>(th.lo), hi1 = static_cast<D>(th.hi);
     const D t2 = static_cast<D>(th.t2), lo2 = static_cast<D>(th.lo2), hi2 = static_cast<D>(th.hi2);
-    // Deferred columns put their input back: the threshold search may have
-    // used the column's LDS slots as scratch, and the workgroup-per-column
-    // kernel reads the input again (in place when in == out).
+    // The elementwise map is fixed per family (and per launch for the
+    // entropic family, from the uniform op argument), so the slot loop has no
+    // per-lane branch.  Deferred columns keep their input: the
+    // workgroup-per-column kernel reads it again (in place when in == out).
+    auto write_slots = [&](auto map) {
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      if (c < nvalid) {
-        const int idx = g + G * c;
-        const bool second = (FAM == FAM_TWO) && idx >= p;
-        tile[lc * m + idx] = th.slow ? v[c]
-                           : second ? apply_map<D, R>(v[c], t2, lo2, hi2, 0)
-                                    : apply_map<D, R>(v[c], t1, lo1, hi1, th.kind);
+      for (int c = 0; c < C; ++c) {
+        const D y = th.slow ? v[c] : map(c);
+        D* dst = (c < nvalid) ? tile + lc * m + g + G * c : lds_dummy;
+        *dst = y;
       }
+    };
+    if constexpr (FAM == FAM_ENT) {
+      if (pp.op == OP_ENTROPY) {
+        write_slots([&](int c) { return clamp_ref(dexp(v[c] - t1), lo1, hi1); });
+      } else {
+        write_slots([&](int c) { return clamp_ref(lambert_w_exp(v[c] - t1), lo1, hi1); });
+      }
+    } else if constexpr (FAM == FAM_TOPKENT) {
+      write_slots([&](int c) { return clamp_ref(dexp(v[c] - t1), lo1, hi1); });
+    } else if constexpr (FAM == FAM_TWO) {
+      write_slots([&](int c) {
+        return (g + G * c >= p) ? clamp_ref(v[c] - t2, lo2, hi2) : clamp_ref(v[c] - t1, lo1, hi1);
+      });
+    } else {
+      write_slots([&](int c) { return clamp_ref(v[c] - t1, lo1, hi1); });
     }
     if (g == 0) {
-      const int64_t j = col0 + lc;
       if (th.slow) {
         const int pos = atomicAdd(slow, 1);
         slow[1 + pos] = static_cast<int>(j);
@@ -808,7 +979,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
     }
   }
   __syncthreads();
-  tile_copy(out + col0 * m64, tile, count);
+  tile_store<NV, BT>(out + col0 * m64, tile, count);
 }
 
 }  // namespace sdca_gpu
