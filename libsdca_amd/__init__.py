@@ -31,6 +31,7 @@ __all__ = [
     "SdcaError", "library", "prox", "prox_knapsack_eq", "prox_knapsack_le",
     "prox_topk_simplex", "prox_topk_cone", "prox_entropy", "prox_entropy_norm",
     "prox_topk_entropy", "prox_two_simplex", "lambert_w_exp", "OPS", "F32", "F64",
+    "OBJECTIVES", "objective", "scores", "eval_features", "eval_scores",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -69,6 +70,33 @@ class ProxParams(ctypes.Structure):
 
 class Thresholds(ctypes.Structure):
     _fields_ = [("t", ctypes.c_double), ("lo", ctypes.c_double), ("hi", ctypes.c_double)]
+
+
+class Objective(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("c", ctypes.c_double), ("gamma", ctypes.c_double), ("k", ctypes.c_int64)]
+
+
+class EvalRecord(ctypes.Structure):
+    _fields_ = [("primal", ctypes.c_double), ("dual", ctypes.c_double),
+                ("primal_loss", ctypes.c_double), ("dual_loss", ctypes.c_double),
+                ("primal_regularizer", ctypes.c_double),
+                ("dual_regularizer", ctypes.c_double), ("rank_loss", ctypes.c_double)]
+
+
+# Objectives of the evaluation pass, named after the reference's makers
+# (objective.h:55-160: make_objective_l2_hinge_topk, ...).
+OBJECTIVES = {
+    "l2_hinge_topk": 0, "l2_hinge_topk_smooth": 1, "l2_topk_hinge": 2,
+    "l2_topk_hinge_smooth": 3, "l2_entropy": 4, "l2_entropy_topk": 5,
+    "l2_multilabel_hinge": 6, "l2_multilabel_hinge_smooth": 7,
+    "l2_multilabel_entropy": 8,
+}
+
+
+def objective(name, c=1.0, gamma=1.0, k=1):
+    """An objective for eval_features / eval_scores (c = 1 / (lambda n))."""
+    return (name, float(c), float(gamma), int(k))
 
 
 _lib = None
@@ -203,3 +231,124 @@ def prox_two_simplex(dim, p, A, rhs=1.0, result=None):
 def lambert_w_exp(A):
     """Elementwise W(exp(x)) in place (apply(dim, ..., lambert_w_exp_map))."""
     return prox("lambert_w_exp", A if A.ndim == 2 else A.reshape(1, -1))
+
+
+# ---------------------------------------------------------------------------
+# Evaluation pass (evaluate_dataset, eval.h:15-51, for feature input).
+# X: (n, d) examples, W: (m, d) classes, S/A: (n, m); all C-contiguous, i.e.
+# the reference's column-major d x n, d x m and m x n matrices.
+# ---------------------------------------------------------------------------
+def _objs(objs):
+    arr = (Objective * len(objs))()
+    for i, (name, c, gamma, k) in enumerate(objs):
+        arr[i] = Objective(OBJECTIVES[name], 0, c, gamma, k)
+    return arr
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    return x.data_ptr() if _is_torch(x) else x.ctypes.data
+
+
+def scores(X, W, out=None):
+    """S = X W^T (scores of every example for every class)."""
+    lib = library()
+    n, d = int(X.shape[0]), int(X.shape[1])
+    m = int(W.shape[0])
+    data = _dtype_code(X)
+    if _is_torch(X):
+        import torch
+        S = out if out is not None else torch.empty((n, m), dtype=X.dtype, device=X.device)
+        check(lib.sdca_scores(data, ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+                              ctypes.c_void_p(X.data_ptr()), ctypes.c_void_p(W.data_ptr()),
+                              ctypes.c_void_p(S.data_ptr()), ctypes.c_uint(0), _stream_ptr()))
+        return S
+    S = out if out is not None else np.zeros((n, m), dtype=X.dtype)
+    check(lib.sdca_scores(data, ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+                          ctypes.c_void_p(X.ctypes.data), ctypes.c_void_p(W.ctypes.data),
+                          ctypes.c_void_p(S.ctypes.data), ctypes.c_uint(HOST_PTR), None))
+    return S
+
+
+def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_example, torch_mode,
+          data, tail_args=()):
+    lib = library()
+    res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
+    objarr = _objs(objs)
+    recs = (EvalRecord * len(objs))()
+    acc = np.zeros(m, dtype=np.float64)
+    pe = None
+    if torch_mode:
+        import torch
+        dev = lead_args[0].device
+        lab = torch.as_tensor(labels, dtype=torch.int64, device=dev).contiguous()
+        off = None if offsets is None else torch.as_tensor(offsets, dtype=torch.int64, device=dev).contiguous()
+        if per_example:
+            pe = torch.zeros((n, len(objs), 2), dtype=torch.float64, device=dev)
+        flags, stream = 0, _stream_ptr()
+    else:
+        lab = np.ascontiguousarray(labels, dtype=np.int64)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
+        if per_example:
+            pe = np.zeros((n, len(objs), 2), dtype=np.float64)
+        flags, stream = HOST_PTR, None
+    fn = getattr(lib, fn_name)
+    fn.restype = ctypes.c_int
+    args = [objarr, ctypes.c_int(len(objs)), ctypes.c_int(data), ctypes.c_int(res)]
+    args += list(lead_args[1])
+    args += [ctypes.c_void_p(_ptr(A)), *tail_args, ctypes.c_void_p(_ptr(lab)),
+             ctypes.c_void_p(_ptr(off)), recs, ctypes.c_void_p(acc.ctypes.data),
+             ctypes.c_void_p(_ptr(pe)), ctypes.c_uint(flags), stream]
+    check(fn(*args))
+    records = [{f: getattr(r, f) for f, _ in EvalRecord._fields_} for r in recs]
+    return records, acc, pe
+
+
+def eval_features(objs, X, W, labels, A=None, W0=None, offsets=None, result=None,
+                  per_example=False):
+    """evaluate_dataset for feature input.  objs: list of objective(...).
+    Returns (records, accuracy, per_example): one eval record per objective
+    (primal, dual, primal_loss, dual_loss, primal/dual regularizer, rank_loss),
+    the top-(i+1) accuracies (multiclass) and optionally the (n, n_obj, 2)
+    per-example (primal, dual) losses before the loss coefficient."""
+    n, d = int(X.shape[0]), int(X.shape[1])
+    m = int(W.shape[0])
+    lead = (X, [ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+                ctypes.c_void_p(_ptr(X)), ctypes.c_void_p(_ptr(W))])
+    return _eval("sdca_eval_features", objs, lead, m, n, labels, offsets, A, result, per_example,
+                 _is_torch(X), _dtype_code(X), tail_args=(ctypes.c_void_p(_ptr(W0)),))
+
+
+def eval_scores(objs, S, labels, A=None, offsets=None, primal_regularizer=0.0,
+                dual_regularizer=0.0, result=None, per_example=False):
+    """The per-example part of evaluate_dataset on precomputed scores S."""
+    n, m = int(S.shape[0]), int(S.shape[1])
+    lead = (S, [ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(_ptr(S))])
+    lib = library()
+    res = _dtype_code(S) if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
+    torch_mode = _is_torch(S)
+    objarr = _objs(objs)
+    recs = (EvalRecord * len(objs))()
+    acc = np.zeros(m, dtype=np.float64)
+    if torch_mode:
+        import torch
+        lab = torch.as_tensor(labels, dtype=torch.int64, device=S.device).contiguous()
+        off = None if offsets is None else torch.as_tensor(offsets, dtype=torch.int64, device=S.device).contiguous()
+        pe = torch.zeros((n, len(objs), 2), dtype=torch.float64, device=S.device) if per_example else None
+        flags, stream = 0, _stream_ptr()
+    else:
+        lab = np.ascontiguousarray(labels, dtype=np.int64)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
+        pe = np.zeros((n, len(objs), 2), dtype=np.float64) if per_example else None
+        flags, stream = HOST_PTR, None
+    lib.sdca_eval_scores.restype = ctypes.c_int
+    check(lib.sdca_eval_scores(objarr, ctypes.c_int(len(objs)), ctypes.c_int(_dtype_code(S)),
+                               ctypes.c_int(res), ctypes.c_int64(m), ctypes.c_int64(n),
+                               ctypes.c_void_p(_ptr(S)), ctypes.c_void_p(_ptr(A)),
+                               ctypes.c_void_p(_ptr(lab)), ctypes.c_void_p(_ptr(off)),
+                               ctypes.c_double(primal_regularizer), ctypes.c_double(dual_regularizer),
+                               recs, ctypes.c_void_p(acc.ctypes.data), ctypes.c_void_p(_ptr(pe)),
+                               ctypes.c_uint(flags), stream))
+    records = [{f: getattr(r, f) for f, _ in EvalRecord._fields_} for r in recs]
+    return records, acc, pe

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/sdca_hip.h"
+#include "eval_launch.hpp"
 #include "prox_launch.hpp"
 
 namespace {
@@ -262,6 +263,317 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
   }
   return SDCA_OK;
+}
+
+
+}  // extern "C"
+
+namespace {
+
+bool is_multilabel(int kind) { return kind >= SDCA_OBJ_MULTILABEL_HINGE; }
+bool uses_k(int kind) {
+  return kind == SDCA_OBJ_HINGE_TOPK || kind == SDCA_OBJ_HINGE_TOPK_SMOOTH ||
+         kind == SDCA_OBJ_TOPK_HINGE || kind == SDCA_OBJ_TOPK_HINGE_SMOOTH ||
+         kind == SDCA_OBJ_ENTROPY_TOPK;
+}
+bool uses_gamma(int kind) {
+  return kind == SDCA_OBJ_HINGE_TOPK_SMOOTH || kind == SDCA_OBJ_TOPK_HINGE_SMOOTH ||
+         kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH;
+}
+// objective_base::coeff_primal_loss of each objective (objective/*.h).
+double loss_coeff(const sdca_objective& o) {
+  switch (o.kind) {
+    case SDCA_OBJ_HINGE_TOPK:
+    case SDCA_OBJ_TOPK_HINGE: return o.c / static_cast<double>(o.k);
+    case SDCA_OBJ_HINGE_TOPK_SMOOTH:
+    case SDCA_OBJ_TOPK_HINGE_SMOOTH:
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH: return o.c / o.gamma;
+    default: return o.c;
+  }
+}
+
+int check_objectives(const sdca_objective* objs, int n_obj, int64_t m, bool multilabel) {
+  if (!objs) return fail(SDCA_ERR_ARG_NULL, "objectives must not be NULL");
+  if (n_obj < 1 || n_obj > sdca_gpu::kMaxObjectives)
+    return fail(SDCA_ERR_ARG_RANGE, "n_obj must be in [1, %d] (got %d)", sdca_gpu::kMaxObjectives, n_obj);
+  for (int o = 0; o < n_obj; ++o) {
+    const sdca_objective& ob = objs[o];
+    if (ob.kind < SDCA_OBJ_HINGE_TOPK || ob.kind > SDCA_OBJ_MULTILABEL_ENTROPY)
+      return fail(SDCA_ERR_ARG_RANGE, "unknown objective kind %d", ob.kind);
+    if (is_multilabel(ob.kind) != multilabel)
+      return fail(SDCA_ERR_ARG_RANGE, "objective %d does not match the %s labels", o,
+                  multilabel ? "multilabel" : "multiclass");
+    if (!(ob.c > 0)) return fail(SDCA_ERR_ARG_RANGE, "c must be > 0 (got %g)", ob.c);
+    if (uses_gamma(ob.kind) && !(ob.gamma > 0))
+      return fail(SDCA_ERR_ARG_RANGE, "gamma must be > 0 (got %g)", ob.gamma);
+    if (uses_k(ob.kind)) {
+      if (ob.k < 1 || ob.k > m - 1)
+        return fail(SDCA_ERR_ARG_RANGE, "k must be in [1, %lld] (got %lld)", (long long)(m - 1),
+                    (long long)ob.k);
+      if (ob.k > sdca_gpu::kEvalMaxK)
+        return fail(SDCA_ERR_NOT_IMPLEMENTED, "top-k objectives support k <= %lld on the GPU",
+                    (long long)sdca_gpu::kEvalMaxK);
+    }
+  }
+  return SDCA_OK;
+}
+
+// Host-side label checks (data/output.h:169-208), when labels are host memory.
+int check_labels(const int64_t* labels, const int64_t* offsets, int64_t m, int64_t n) {
+  if (!offsets) {
+    for (int64_t i = 0; i < n; ++i)
+      if (labels[i] < 0 || labels[i] >= m)
+        return fail(SDCA_ERR_LABELS, "label %lld of example %lld is outside [0, %lld)",
+                    (long long)labels[i], (long long)i, (long long)m);
+    return SDCA_OK;
+  }
+  if (offsets[0] != 0) return fail(SDCA_ERR_LABELS, "The first offset must be 0.");
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t p = offsets[i + 1] - offsets[i];
+    if (p < 1 || p >= m)
+      return fail(SDCA_ERR_LABELS, "Each example must have between 1 and num_classes - 1 labels.");
+    for (int64_t q = offsets[i]; q < offsets[i + 1]; ++q) {
+      if (labels[q] < 0 || labels[q] >= m)
+        return fail(SDCA_ERR_LABELS, "label %lld is outside [0, %lld)", (long long)labels[q], (long long)m);
+      if (q > offsets[i] && !(labels[q - 1] < labels[q]))
+        return fail(SDCA_ERR_LABELS, "All labels for every example must be distinct and sorted.");
+    }
+  }
+  return SDCA_OK;
+}
+
+// The shared part of sdca_eval_scores / sdca_eval_features: epilogue,
+// reductions and eval_end (eval/core.h:43-95) on device pointers.
+int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, int64_t m,
+                   int64_t n, const void* dS, const void* dA, const int64_t* dlabels,
+                   const int64_t* doffsets, const void* dW, const void* dW0, int64_t dm,
+                   double preg_in, double dreg_in, sdca_eval_record* records, double* accuracy,
+                   double* per_example, bool per_example_host, hipStream_t stream) {
+  using namespace sdca_gpu;
+  const bool multilabel = doffsets != nullptr;
+  // Scratch layout: per-example losses, counts, rank, slow list, sums, hist, reg.
+  const size_t pe_bytes = static_cast<size_t>(n) * n_obj * 2 * sizeof(double);
+  const size_t cnt_bytes = static_cast<size_t>(n) * sizeof(int);
+  const size_t rank_bytes = static_cast<size_t>(n) * sizeof(double);
+  const size_t slow_bytes = (1 + 2 * static_cast<size_t>(n) * n_obj) * sizeof(int);
+  const size_t sums_bytes = (2 * kMaxObjectives + 2) * sizeof(double);
+  const size_t hist_bytes = static_cast<size_t>(m) * sizeof(unsigned long long);
+  const size_t reg_bytes = (2 * 512 + 2) * sizeof(double);
+  auto align = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t total = align(pe_bytes) + align(cnt_bytes) + align(rank_bytes) + align(slow_bytes) +
+                       align(sums_bytes) + align(hist_bytes) + align(reg_bytes);
+  void* ws = nullptr;
+  int rc = workspace(stream, 2, total, &ws);
+  if (rc) return rc;
+  char* p = static_cast<char*>(ws);
+  double* d_pe = reinterpret_cast<double*>(p); p += align(pe_bytes);
+  int* d_cnt = reinterpret_cast<int*>(p); p += align(cnt_bytes);
+  double* d_rank = reinterpret_cast<double*>(p); p += align(rank_bytes);
+  int* d_slow = reinterpret_cast<int*>(p); p += align(slow_bytes);
+  double* d_sums = reinterpret_cast<double*>(p); p += align(sums_bytes);
+  unsigned long long* d_hist = reinterpret_cast<unsigned long long*>(p); p += align(hist_bytes);
+  double* d_reg = reinterpret_cast<double*>(p);
+
+  EvalLaunch a;
+  a.data = data;
+  a.result = result;
+  a.m = m;
+  a.n = n;
+  a.S = dS;
+  a.A = dA;
+  a.labels = dlabels;
+  a.offsets = doffsets;
+  a.objs.n = n_obj;
+  for (int o = 0; o < n_obj; ++o) {
+    a.objs.o[o].kind = objs[o].kind;
+    a.objs.o[o].k = static_cast<int>(objs[o].k);
+    a.objs.o[o].c = objs[o].c;
+    a.objs.o[o].gamma = objs[o].gamma;
+  }
+  a.per_example = d_pe;
+  a.counts = multilabel ? nullptr : d_cnt;
+  a.rank = multilabel ? d_rank : nullptr;
+  a.slow = d_slow;
+  a.stream = stream;
+  SDCA_HIP_TRY(launch_clear(d_slow, 1, stream), "clear kernel");
+  SDCA_HIP_TRY(launch_eval_epilogue(a), "evaluation epilogue kernel");
+  if (!multilabel) SDCA_HIP_TRY(launch_eval_slow(a), "evaluation epilogue (deferred examples)");
+  SDCA_HIP_TRY(launch_eval_reduce(a, d_sums, multilabel ? d_sums + 2 * kMaxObjectives : nullptr,
+                                  multilabel ? nullptr : d_hist),
+               "evaluation reduction kernels");
+  if (dW) SDCA_HIP_TRY(launch_regularizer(data, dW, dW0, dm, d_reg + 2, d_reg, stream),
+                       "regularizer kernel");
+
+  std::vector<double> sums(2 * kMaxObjectives + 2, 0.0), reg(2, 0.0);
+  std::vector<unsigned long long> hist(static_cast<size_t>(m), 0ull);
+  SDCA_HIP_TRY(hipMemcpyAsync(sums.data(), d_sums, sums_bytes, hipMemcpyDeviceToHost, stream),
+               "hipMemcpyAsync(D2H)");
+  if (!multilabel && accuracy)
+    SDCA_HIP_TRY(hipMemcpyAsync(hist.data(), d_hist, hist_bytes, hipMemcpyDeviceToHost, stream),
+                 "hipMemcpyAsync(D2H)");
+  if (dW) SDCA_HIP_TRY(hipMemcpyAsync(reg.data(), d_reg, 2 * sizeof(double), hipMemcpyDeviceToHost,
+                                      stream), "hipMemcpyAsync(D2H)");
+  if (per_example) {
+    SDCA_HIP_TRY(hipMemcpyAsync(per_example, d_pe, pe_bytes,
+                                per_example_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice,
+                                stream), "hipMemcpyAsync(per_example)");
+  }
+  SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+
+  // eval_end: primal_loss *= coeff; primal = loss + reg; dual = loss - reg;
+  // accuracy = partial_sum(hist) / n; rank_loss /= n (eval/core.h:43-95).
+  double preg = preg_in, dreg = dreg_in;
+  if (dW) {
+    preg = reg[0] - (dW0 ? reg[1] : 0.0);
+    dreg = reg[0];
+  }
+  for (int o = 0; o < n_obj; ++o) {
+    sdca_eval_record& r = records[o];
+    r.primal_loss = loss_coeff(objs[o]) * sums[2 * o];
+    r.dual_loss = sums[2 * o + 1];
+    r.primal_regularizer = preg;
+    r.dual_regularizer = dreg;
+    r.primal = r.primal_loss + preg;
+    r.dual = r.dual_loss - dreg;
+    r.rank_loss = multilabel ? sums[2 * kMaxObjectives] / static_cast<double>(n) : 0.0;
+  }
+  if (!multilabel && accuracy) {
+    unsigned long long run = 0;
+    for (int64_t j = 0; j < m; ++j) {
+      run += hist[j];
+      accuracy[j] = static_cast<double>(run) / static_cast<double>(n);
+    }
+  }
+  return SDCA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sdca_scores(sdca_dtype data, int64_t d, int64_t m, int64_t n, const void* X, const void* W,
+                void* S, unsigned flags, void* stream_ptr) {
+  using namespace sdca_gpu;
+  g_last_error.clear();
+  int rc = check_dtypes(data, data);
+  if (rc) return rc;
+  if (d < 1 || m < 1 || n < 0) return fail(SDCA_ERR_ARG_RANGE, "need d >= 1, m >= 1, n >= 0");
+  if (n == 0) return SDCA_OK;
+  if (!X || !W || !S) return fail(SDCA_ERR_ARG_NULL, "X, W and S must not be NULL");
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const size_t es = dtype_size(data);
+  DeviceBuffer dx, dw, ds;
+  const void* pX = X;
+  const void* pW = W;
+  void* pS = S;
+  if (flags & SDCA_HOST_PTR) {
+    if ((rc = stage_in(X, es * d * n, dx, stream))) return rc;
+    if ((rc = stage_in(W, es * d * m, dw, stream))) return rc;
+    SDCA_HIP_TRY(hipMalloc(&ds.ptr, es * m * n), "hipMalloc(staging)");
+    pX = dx.ptr;
+    pW = dw.ptr;
+    pS = ds.ptr;
+  }
+  if (data == SDCA_F32)
+    SDCA_HIP_TRY(launch_scores_gemm(static_cast<const float*>(pX), static_cast<const float*>(pW),
+                                    static_cast<float*>(pS), n, m, d, stream), "scores kernel");
+  else
+    SDCA_HIP_TRY(launch_scores_gemm_f64(static_cast<const double*>(pX), static_cast<const double*>(pW),
+                                        static_cast<double*>(pS), n, m, d, stream), "scores kernel");
+  if (flags & SDCA_HOST_PTR) {
+    SDCA_HIP_TRY(hipMemcpyAsync(S, pS, es * m * n, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
+    SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  }
+  return SDCA_OK;
+}
+
+static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,
+                       int64_t d, int64_t m, int64_t n, const void* X, const void* W,
+                       const void* S, const void* A, const void* W0, const int64_t* labels,
+                       const int64_t* offsets, double preg, double dreg,
+                       sdca_eval_record* records, double* accuracy, double* per_example,
+                       unsigned flags, void* stream_ptr) {
+  using namespace sdca_gpu;
+  g_last_error.clear();
+  int rc = check_dtypes(data, result);
+  if (rc) return rc;
+  if (m < 2) return fail(SDCA_ERR_ARG_RANGE, "m must be >= 2 (got %lld)", (long long)m);
+  if (n < 1) return fail(SDCA_ERR_ARG_RANGE, "n must be >= 1 (got %lld)", (long long)n);
+  if (m > kEvalMaxM)
+    return fail(SDCA_ERR_NOT_IMPLEMENTED, "the evaluation supports m <= %lld on the GPU",
+                (long long)kEvalMaxM);
+  if (n > INT32_MAX / 2) return fail(SDCA_ERR_ARG_RANGE, "n too large");
+  const bool multilabel = offsets != nullptr;
+  if ((rc = check_objectives(objs, n_obj, m, multilabel))) return rc;
+  if (!records) return fail(SDCA_ERR_ARG_NULL, "records must not be NULL");
+  if (!labels) return fail(SDCA_ERR_ARG_NULL, "labels must not be NULL");
+  const bool host = (flags & SDCA_HOST_PTR) != 0;
+  if (host && (rc = check_labels(labels, offsets, m, n))) return rc;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const size_t es = dtype_size(data);
+  DeviceBuffer dx, dw, ds, da, dw0, dl, doff;
+  const void* pX = X;
+  const void* pW = W;
+  const void* pS = S;
+  const void* pA = A;
+  const void* pW0 = W0;
+  const int64_t* pl = labels;
+  const int64_t* poff = offsets;
+  if (host) {
+    const int64_t nlab = multilabel ? offsets[n] : n;
+    if (X && (rc = stage_in(X, es * d * n, dx, stream))) return rc;
+    if (W && (rc = stage_in(W, es * d * m, dw, stream))) return rc;
+    if (S && (rc = stage_in(S, es * m * n, ds, stream))) return rc;
+    if (A && (rc = stage_in(A, es * m * n, da, stream))) return rc;
+    if (W0 && (rc = stage_in(W0, es * d * m, dw0, stream))) return rc;
+    if ((rc = stage_in(labels, sizeof(int64_t) * nlab, dl, stream))) return rc;
+    if (offsets && (rc = stage_in(offsets, sizeof(int64_t) * (n + 1), doff, stream))) return rc;
+    pX = X ? dx.ptr : nullptr;
+    pW = W ? dw.ptr : nullptr;
+    pS = S ? ds.ptr : nullptr;
+    pA = A ? da.ptr : nullptr;
+    pW0 = W0 ? dw0.ptr : nullptr;
+    pl = static_cast<const int64_t*>(dl.ptr);
+    poff = offsets ? static_cast<const int64_t*>(doff.ptr) : nullptr;
+  }
+  if (!pS) {
+    // scores = W' X into the stream's workspace
+    void* sbuf = nullptr;
+    if ((rc = workspace(stream, 1, es * static_cast<size_t>(m) * static_cast<size_t>(n), &sbuf))) return rc;
+    if (data == SDCA_F32)
+      SDCA_HIP_TRY(launch_scores_gemm(static_cast<const float*>(pX), static_cast<const float*>(pW),
+                                      static_cast<float*>(sbuf), n, m, d, stream), "scores kernel");
+    else
+      SDCA_HIP_TRY(launch_scores_gemm_f64(static_cast<const double*>(pX),
+                                          static_cast<const double*>(pW), static_cast<double*>(sbuf),
+                                          n, m, d, stream), "scores kernel");
+    pS = sbuf;
+  }
+  return eval_on_device(objs, n_obj, data, result, m, n, pS, pA, pl, poff, X ? pW : nullptr,
+                        X ? pW0 : nullptr, d * m, preg, dreg, records, accuracy, per_example, host,
+                        stream);
+}
+
+int sdca_eval_features(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,
+                       int64_t d, int64_t m, int64_t n, const void* X, const void* W,
+                       const void* A, const void* W0, const int64_t* labels,
+                       const int64_t* offsets, sdca_eval_record* records, double* accuracy,
+                       double* per_example, unsigned flags, void* stream) {
+  if (!X || !W) return fail(SDCA_ERR_ARG_NULL, "X and W must not be NULL");
+  if (d < 1) return fail(SDCA_ERR_ARG_RANGE, "d must be >= 1 (got %lld)", (long long)d);
+  return eval_common(objs, n_obj, data, result, d, m, n, X, W, nullptr, A, W0, labels, offsets,
+                     0.0, 0.0, records, accuracy, per_example, flags, stream);
+}
+
+int sdca_eval_scores(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,
+                     int64_t m, int64_t n, const void* S, const void* A, const int64_t* labels,
+                     const int64_t* offsets, double primal_regularizer, double dual_regularizer,
+                     sdca_eval_record* records, double* accuracy, double* per_example,
+                     unsigned flags, void* stream) {
+  if (!S) return fail(SDCA_ERR_ARG_NULL, "S must not be NULL");
+  return eval_common(objs, n_obj, data, result, 0, m, n, nullptr, nullptr, S, A, nullptr, labels,
+                     offsets, primal_regularizer, dual_regularizer, records, accuracy, per_example,
+                     flags, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,995 @@
+// Per-example epilogue of the evaluation pass (eval.h:36-47) on the score
+// matrix: dual loss, top-k count / rank loss and the primal loss of every
+// requested objective, one group of G lanes per example.
+//
+// Per example the scores row (m contiguous floats) is read straight into C
+// register slots per lane (lane g holds classes g, g+G, ...; coalesced), and
+// each objective restates its reference primal_loss / dual_loss:
+//   multiclass (label y; the reference swaps s_y to the front, eval/primal.h:217-237)
+//     count      #{j != y : s_j >= s_y}                          (ties count against)
+//     hinge_topk max(0, sum of the k largest h_j), h_j = s_j + (1 - s_y)  (l2_hinge_topk.h:71-86)
+//     topk_hinge sum of the positive h_j among the k largest              (l2_topk_hinge.h:72-87)
+//     *_smooth   <h, p> - <p, p> / 2 with p the top-k simplex / knapsack_le projection of h
+//                (l2_hinge_topk.h:162-179, l2_topk_hinge.h:166-183), from the threshold sets
+//                as dot_x_prox / dot_prox_prox do (proxdef.h:332-370)
+//     entropy    lse(s) - s_y                                              (l2_entropy.h:77-91)
+//     entropy_topk  via the top-k entropy thresholds of s_j - s_y          (l2_entropy_topk.h:74-94)
+//   multilabel (positives P, eval/primal.h:246-271)
+//     rank loss  #{(p, n): s_n >= s_p} / (|P| |N|)
+//     hinge      max(0, max_N s - min_P s + 1)                             (l2_multilabel_hinge.h:69-84)
+//     smooth     two-simplex projection of (1/2 - s_P, 1/2 + s_N)          (l2_multilabel_hinge.h:168-191)
+//     entropy    lse(s) - mean_P s                                         (l2_multilabel_entropy.h:72-86)
+// Losses are written per example (in double) and reduced afterwards in a
+// fixed order, so the totals are deterministic.  Examples whose top-k
+// simplex needs the reference's full topk_cone_search are listed and
+// finished by the workgroup-per-example kernel at the end of this file.
+#include "eval_launch.hpp"
+#include "prox_impl.hpp"
+
+namespace sdca_gpu {
+
+namespace {
+
+template <class R>
+struct SetStats {
+  R sum_u, sum_m, dot_m;
+  int n_u, n_m;
+};
+
+// <h, p> - <p, p> / 2 from the threshold sets with lo = 0
+// (dot_x_prox - dot_prox_prox / 2, proxdef.h:332-370).
+template <class R>
+__device__ inline R smooth_loss(R t, R hi, const SetStats<R>& st) {
+  const R hp = hi * st.sum_u - t * st.sum_m + st.dot_m;
+  const R pp = hi * hi * static_cast<R>(st.n_u) + t * t * static_cast<R>(st.n_m) + st.dot_m
+             - R(2) * t * st.sum_m;
+  return hp - R(0.5) * pp;
+}
+
+// Set statistics of a Kiwiel result (knapsack_eq.h:46-85): U = fixed at hi
+// plus the final upper candidates, M = the remaining free elements, L = the
+// rest; `cand` restricts the sets to values above the candidate cut.
+template <int G, int C, class D, class R>
+__device__ inline SetStats<R> knap_sets(const D (&h)[C], const KnapState<R>& st, R cand_cut) {
+  SetStats<R> r;
+  r.sum_u = r.sum_m = r.dot_m = 0;
+  r.n_u = r.n_m = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(h[c]);
+    const bool cand = x > cand_cut;
+    const bool fixed_hi = x > st.hi_cut;
+    const bool fr = (x > st.lo_cut) && !fixed_hi;
+    const bool gl = x > st.c_lo;
+    const bool in_u = cand && (fixed_hi || (fr && gl && x > st.c_hi));
+    const bool in_m = cand && fr && gl && !(x > st.c_hi);
+    r.sum_u += in_u ? x : R(0);
+    r.n_u += in_u ? 1 : 0;
+    r.sum_m += in_m ? x : R(0);
+    r.dot_m += in_m ? x * x : R(0);
+    r.n_m += in_m ? 1 : 0;
+  }
+  r.sum_u = group_sum<G>(r.sum_u);
+  r.sum_m = group_sum<G>(r.sum_m);
+  r.dot_m = group_sum<G>(r.dot_m);
+  r.n_u = group_sum<G>(r.n_u);
+  r.n_m = group_sum<G>(r.n_m);
+  return r;
+}
+
+// Smooth top-k hinge loss (l2_hinge_topk.h:162-179) of the m' = m - 1 values
+// h (padding and the label's slot hold -inf).  Returns false when the
+// example needs the full topk_cone_search.
+template <int G, int C, int KM, class D, class R>
+__device__ inline bool smooth_topk_hinge(const D (&h)[C], int mp, int k, R gamma, D* lds_col,
+                                         D* lds_dummy, R& loss) {
+  constexpr int L = KM + 1;
+  const R K = static_cast<R>(k);
+  const R eps16 = R(16) * num<R>::eps();
+  D top[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) top[i] = -num<D>::inf();
+#pragma unroll
+  for (int c = 0; c < C; ++c) top_insert(top, h[c]);
+  top_merge<G>(top);
+  R sum_k = 0, kth = static_cast<R>(top[0]), next = -num<R>::inf();
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    if (i < k) sum_k += static_cast<R>(top[i]);
+    if (i == k - 1) kth = static_cast<R>(top[i]);
+    if (i == k) next = static_cast<R>(top[i]);
+  }
+  const R largest = static_cast<R>(top[0]);
+  // thresholds_topk_simplex(h, k, gamma) (topk_simplex.h:39-68)
+  if (sum_k <= eps16) {  // zero projection
+    loss = 0;
+    return true;
+  }
+  const R hi_c = sum_k / K;
+  const R t_c = kth - hi_c;
+  const bool constant = (k == mp) || (t_c >= next - eps16);
+  const R eps = num<R>::eps() * dmax(R(1), fabs(gamma));
+  if (constant && !(K * hi_c > gamma + eps)) {
+    // U = the k largest, M empty (topk_cone.h:43-51)
+    const R hp = hi_c * sum_k;
+    const R pp = hi_c * hi_c * K;
+    loss = hp - R(0.5) * pp;
+    return true;
+  }
+  const R hi = gamma / K;
+  KnapState<R> st = topk_knapsack<G, C, L, D, R>(h, top, mp, C, kth, hi, gamma, lds_col,
+                                                  lds_dummy);
+  if (!constant) {
+    bool lt;
+    if (st.n_u == 0) {
+      lt = st.t < -eps;
+    } else {
+      const R num_u = static_cast<R>(st.n_u);
+      lt = K * (st.sum_u + (K - num_u) * st.t) < gamma * num_u - eps;
+    }
+    if (lt) {
+      // topk_cone_search with U empty: t = 0, M = {h > 16 eps}; else defer.
+      ColThr<R> cs = cone_search_u0<G, C, D, R>(h, K, largest);
+      if (cs.slow) return false;
+      R dot = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(h[c]);
+        dot += (x > eps16) ? x * x : R(0);
+      }
+      dot = group_sum<G>(dot);
+      loss = R(0.5) * dot;
+      return true;
+    }
+  }
+  // The candidate cut used by topk_knapsack: values at or below it are in L.
+  const R cut = kth - hi - (fabs(kth) + hi) * (R(16) * num<R>::eps());
+  const SetStats<R> ss = knap_sets<G, C, D, R>(h, st, cut);
+  loss = smooth_loss(st.t, hi, ss);
+  return true;
+}
+
+// Smooth top-k hinge beta (l2_topk_hinge.h:166-183): knapsack_le(h, 0, gamma/k, gamma).
+template <int G, int C, class D, class R>
+__device__ inline R smooth_topk_hinge_beta(const D (&h)[C], int mp, int k, R gamma) {
+  const R lo = 0, hi = gamma / static_cast<R>(k), rhs = gamma;
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  // knapsack_le.h:30-46: U = {x >= hi}, M = {lo < x < hi}, L = the rest
+  SetStats<R> s;
+  s.sum_u = s.sum_m = s.dot_m = 0;
+  s.n_u = s.n_m = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(h[c]);
+    const bool u = x >= hi;
+    const bool mm = !u && x > lo;
+    s.sum_u += u ? x : R(0);
+    s.n_u += u ? 1 : 0;
+    s.sum_m += mm ? x : R(0);
+    s.dot_m += mm ? x * x : R(0);
+    s.n_m += mm ? 1 : 0;
+  }
+  s.sum_u = group_sum<G>(s.sum_u);
+  s.sum_m = group_sum<G>(s.sum_m);
+  s.dot_m = group_sum<G>(s.dot_m);
+  s.n_u = group_sum<G>(s.n_u);
+  s.n_m = group_sum<G>(s.n_m);
+  const int n_l = mp - s.n_u - s.n_m;
+  const R sum = s.sum_m + hi * static_cast<R>(s.n_u) + lo * static_cast<R>(n_l);
+  if (!(sum > rhs + eps)) {
+    // thresholds (0, lo, hi): <h,p> = hi sum_U + dot_M, <p,p> = hi^2 |U| + dot_M
+    return smooth_loss(R(0), hi, s);
+  }
+  R total = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(h[c]);
+    total += (x > -num<R>::inf()) ? x : R(0);
+  }
+  total = group_sum<G>(total);
+  KnapState<R> st = knapsack_eq_regs<G, C, D, R>(h, mp, C, total, lo, hi, rhs);
+  const SetStats<R> ss = knap_sets<G, C, D, R>(h, st, -num<R>::inf());
+  return smooth_loss(st.t, hi, ss);
+}
+
+template <int G, int C, class D, class R>
+__device__ inline R lse_all(const D (&v)[C], int nvalid) {
+  bool mask[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) mask[c] = c < nvalid;
+  const R mx = masked_max<G, C, D, R>(v, mask);
+  return mx + dlog1p(lse_sum_excl<G, C, D, R>(v, mask, mx));
+}
+
+template <int G, int C, int KM, class D, class R>
+__global__ void __launch_bounds__(64)
+eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
+                       const int64_t* __restrict__ labels, int64_t m64, int64_t n, EvalObjs objs,
+                       double* __restrict__ per_example, int* __restrict__ counts,
+                       int* __restrict__ slow) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  D* lds = reinterpret_cast<D*>(smem_raw);
+  constexpr int B = 64 / G;
+  const int m = static_cast<int>(m64);
+  const int lc = static_cast<int>(threadIdx.x) / G;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * B + lc;
+  const bool active = i < n;
+  const int64_t ii = active ? i : 0;  // inactive groups compute on example 0, store nothing
+  D* const lds_col = lds + lc * m;
+  D* const lds_dummy = lds + B * m + threadIdx.x;
+
+  const D* srow = S + ii * m64;
+  const int y = static_cast<int>(labels[ii]);
+  const D sy = srow[y];
+  const int nvalid = (m - g + G - 1) / G;
+  D s[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) s[c] = (c < nvalid) ? srow[g + G * c] : -num<D>::inf();
+
+  // eval_primal_loss: count of j != y with s_j >= s_y (eval/primal.h:228-233)
+  int cnt = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int idx = g + G * c;
+    cnt += (c < nvalid && idx != y && s[c] >= sy) ? 1 : 0;
+  }
+  cnt = group_sum<G>(cnt);
+  if (active && g == 0) counts[i] = cnt;
+
+  // Dual variables of the example.
+  D a[C];
+  D ay = 0;
+  if (A) {
+    const D* arow = A + ii * m64;
+    ay = arow[y];
+#pragma unroll
+    for (int c = 0; c < C; ++c) a[c] = (c < nvalid) ? arow[g + G * c] : D(0);
+  } else {
+#pragma unroll
+    for (int c = 0; c < C; ++c) a[c] = 0;
+  }
+
+  for (int o = 0; o < objs.n; ++o) {
+    const EvalObj ob = objs.o[o];
+    const R c_ = static_cast<R>(ob.c), gamma = static_cast<R>(ob.gamma);
+    const int k = ob.k;
+    R primal = 0, dual = 0;
+    bool deferred = false;
+    // h_j = s_j + (1 - s_y) for j != y, in the Data type (l2_hinge_topk.h:73-74)
+    const D shift1 = D(1) - sy;
+    D h[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int idx = g + G * c;
+      h[c] = (c < nvalid && idx != y) ? s[c] + shift1 : -num<D>::inf();
+    }
+    switch (ob.kind) {
+      case SDCA_OBJ_HINGE_TOPK:
+      case SDCA_OBJ_TOPK_HINGE: {
+        constexpr int L = KM + 1;
+        D top[L];
+#pragma unroll
+        for (int q = 0; q < L; ++q) top[q] = -num<D>::inf();
+#pragma unroll
+        for (int c = 0; c < C; ++c) top_insert(top, h[c]);
+        top_merge<G>(top);
+        R sum = 0;
+#pragma unroll
+        for (int q = 0; q < L; ++q) {
+          const R x = static_cast<R>(top[q]);
+          if (q < k) sum += (ob.kind == SDCA_OBJ_HINGE_TOPK || top[q] > D(0)) ? x : R(0);
+        }
+        primal = (ob.kind == SDCA_OBJ_HINGE_TOPK) ? dmax(R(0), sum) : sum;
+        dual = static_cast<R>(ay);
+        break;
+      }
+      case SDCA_OBJ_HINGE_TOPK_SMOOTH: {
+        deferred = !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, k, gamma, lds_col, lds_dummy, primal);
+        break;
+      }
+      case SDCA_OBJ_TOPK_HINGE_SMOOTH: {
+        primal = smooth_topk_hinge_beta<G, C, D, R>(h, m - 1, k, gamma);
+        break;
+      }
+      case SDCA_OBJ_ENTROPY: {
+        primal = lse_all<G, C, D, R>(s, nvalid) - static_cast<R>(sy);
+        break;
+      }
+      case SDCA_OBJ_ENTROPY_TOPK: {
+        // a_j = s_j - s_y (l2_entropy_topk.h:78-80), then the top-k entropy thresholds
+        const D shift0 = -sy;
+        D v[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const int idx = g + G * c;
+          v[c] = (c < nvalid && idx != y) ? s[c] + shift0 : -num<D>::inf();
+        }
+        ProxParamsT<R> pp;
+        pp.lo = 0; pp.hi = 1; pp.rhs = 1; pp.k = k; pp.op = OP_TOPK_ENTROPY; pp.p = 0;
+        int n_u = 0;
+        R sum_u = 0;
+        ColThr<R> th = topkent_family<G, C, D, R>(v, m - 1, C, pp, &n_u, &sum_u);
+        if (n_u == 0) {
+          primal = th.t;  // t = log(1 + sum exp) when U stays empty
+        } else {
+          const R num_hi = static_cast<R>(n_u);
+          const R sk = th.hi * static_cast<R>(k);
+          primal = th.hi * (sum_u + th.t * (static_cast<R>(k) - num_hi)) - x_log_x(R(1) - sk)
+                 - num_hi * x_log_x(th.hi);
+        }
+        break;
+      }
+      default:
+        break;
+    }
+    // Dual losses with the ground truth at position 0 (eval/dual.h:303-319).
+    switch (ob.kind) {
+      case SDCA_OBJ_HINGE_TOPK_SMOOTH:
+      case SDCA_OBJ_TOPK_HINGE_SMOOTH: {  // l2_hinge_topk.h:182-192
+        R sq = 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const int idx = g + G * c;
+          const R x = static_cast<R>(a[c]);
+          sq += (c < nvalid && idx != y) ? x * x : R(0);
+        }
+        sq = group_sum<G>(sq);
+        dual = static_cast<R>(ay) - (gamma / (R(2) * c_)) * sq;
+        break;
+      }
+      case SDCA_OBJ_ENTROPY:
+      case SDCA_OBJ_ENTROPY_TOPK: {  // l2_entropy.h:94-114, l2_entropy_topk.h:97-107
+        R acc = 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const int idx = g + G * c;
+          acc += (c < nvalid && idx != y) ? x_log_x(-static_cast<R>(a[c])) : R(0);
+        }
+        acc = group_sum<G>(acc);
+        dual = x_log_x(c_) - x_log_x(c_ - static_cast<R>(ay)) - acc;
+        break;
+      }
+      default:
+        dual = static_cast<R>(ay);
+        break;
+    }
+    if (active && g == 0) {
+      per_example[(i * objs.n + o) * 2] = static_cast<double>(primal);
+      per_example[(i * objs.n + o) * 2 + 1] = static_cast<double>(dual);
+      if (deferred) {
+        const int pos = atomicAdd(slow, 1);
+        slow[1 + 2 * pos] = static_cast<int>(i);
+        slow[2 + 2 * pos] = o;
+      }
+    }
+  }
+}
+
+// Two-block simplex sets (two_simplex.h:18-119) with block a = the slots in
+// `in_a`: the projection of (a, b) onto {x, y >= 0, <1,x> = <1,y> <= rhs}.
+// Returns the smooth multilabel loss <h, p> - <p, p> / 2 summed over both
+// blocks (lo = 0 and U is empty in both, so only the free sets count).
+template <int G, int C, class D, class R>
+__device__ inline R smooth_two_simplex_loss(const D (&v)[C], const bool (&in_a)[C], int p, int mn,
+                                            R rhs) {
+  const R eps = num<R>::eps() * dmax(R(1), rhs);
+  R cuts[2];
+  R res[2];
+  int cnt[2] = {p, mn};
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    R cut = -num<R>::inf();
+    R tb = 0;
+    for (int it = 0; it <= p + mn; ++it) {
+      R s = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(v[c]);
+        s += (in_a[c] == (b == 0) && x > cut) ? x : R(0);
+      }
+      s = group_sum<G>(s);
+      tb = (s - rhs) / static_cast<R>(cnt[b]);
+      int above = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(v[c]);
+        above += (in_a[c] == (b == 0) && x > cut && x > tb) ? 1 : 0;
+      }
+      above = group_sum<G>(above);
+      if (above == cnt[b]) break;
+      cut = dmax(cut, tb);
+      cnt[b] = above;
+    }
+    cuts[b] = cut;
+    res[b] = tb;
+  }
+  R t = res[0], s2 = res[1];
+  if (!(t + s2 >= -eps)) {
+    int mc = cnt[0] + cnt[1];
+    R sa = 0, sb = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      sa += (in_a[c] && x > cuts[0]) ? x : R(0);
+      sb += (!in_a[c] && x > cuts[1]) ? x : R(0);
+    }
+    sa = group_sum<G>(sa);
+    sb = group_sum<G>(sb);
+    t = (+sa - sb) / static_cast<R>(mc);
+    for (int it = 0; it <= p + mn; ++it) {
+      R sum_x = 0, sum_y = 0;
+      int n_x = 0, n_y = 0;
+      const R mt = -t;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(v[c]);
+        const bool lx = in_a[c] && x > cuts[0] && !(x > t);
+        const bool ly = !in_a[c] && x > cuts[1] && !(x > mt);
+        sum_x += lx ? x : R(0);
+        n_x += lx ? 1 : 0;
+        sum_y += ly ? x : R(0);
+        n_y += ly ? 1 : 0;
+      }
+      sum_x = group_sum<G>(sum_x);
+      sum_y = group_sum<G>(sum_y);
+      n_x = group_sum<G>(n_x);
+      n_y = group_sum<G>(n_y);
+      const R infeas = sum_x - sum_y - static_cast<R>(n_x + n_y) * t;
+      R next;
+      if (n_y > 0 && infeas > eps) {
+        cuts[1] = dmax(cuts[1], mt);
+        next = static_cast<R>(mc) * t + sum_y;
+        mc -= n_y;
+      } else if (n_x > 0 && infeas < -eps) {
+        cuts[0] = dmax(cuts[0], t);
+        next = static_cast<R>(mc) * t - sum_x;
+        mc -= n_x;
+      } else {
+        cuts[0] = dmax(cuts[0], t);
+        cuts[1] = dmax(cuts[1], mt);
+        break;
+      }
+      if (mc > 0) {
+        t = next / static_cast<R>(mc);
+      } else {
+        break;
+      }
+    }
+    s2 = -t;
+  }
+  // Free sets: {x in a: x > cuts[0]} with threshold t, {y in b: y > cuts[1]} with s2.
+  R sm[2] = {0, 0}, dm[2] = {0, 0};
+  int nm[2] = {0, 0};
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(v[c]);
+    const bool fa = in_a[c] && x > cuts[0];
+    const bool fb = !in_a[c] && x > cuts[1];
+    sm[0] += fa ? x : R(0);
+    dm[0] += fa ? x * x : R(0);
+    nm[0] += fa ? 1 : 0;
+    sm[1] += fb ? x : R(0);
+    dm[1] += fb ? x * x : R(0);
+    nm[1] += fb ? 1 : 0;
+  }
+  R loss = 0;
+  const R th[2] = {t, s2};
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    SetStats<R> st;
+    st.sum_u = 0;
+    st.n_u = 0;
+    st.sum_m = group_sum<G>(sm[b]);
+    st.dot_m = group_sum<G>(dm[b]);
+    st.n_m = group_sum<G>(nm[b]);
+    loss += smooth_loss(th[b], rhs, st);
+  }
+  return loss;
+}
+
+template <int G, int C, class D, class R>
+__global__ void __launch_bounds__(64)
+eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
+                       const int64_t* __restrict__ labels, const int64_t* __restrict__ offsets,
+                       int64_t m64, int64_t n, EvalObjs objs, double* __restrict__ per_example,
+                       double* __restrict__ rank) {
+  constexpr int B = 64 / G;
+  const int m = static_cast<int>(m64);
+  const int lc = static_cast<int>(threadIdx.x) / G;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * B + lc;
+  const bool active = i < n;
+  const int64_t ii = active ? i : 0;
+  const int64_t off0 = offsets[ii];
+  const int p = static_cast<int>(offsets[ii + 1] - off0);
+  const int nvalid = (m - g + G - 1) / G;
+  const D* srow = S + ii * m64;
+  D s[C];
+  bool pos[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    s[c] = (c < nvalid) ? srow[g + G * c] : -num<D>::inf();
+    pos[c] = false;
+  }
+  for (int q = 0; q < p; ++q) {
+    const int lab = static_cast<int>(labels[off0 + q]);
+#pragma unroll
+    for (int c = 0; c < C; ++c) pos[c] = pos[c] || (g + G * c == lab);
+  }
+  // Rank loss (eval/primal.h:259-267): for each positive, the negatives >= it.
+  R rl = 0;
+  for (int q = 0; q < p; ++q) {
+    const int lab = static_cast<int>(labels[off0 + q]);
+    const D sp = srow[lab];
+    int cn = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) cn += (c < nvalid && !pos[c] && s[c] >= sp) ? 1 : 0;
+    rl += static_cast<R>(group_sum<G>(cn));
+  }
+  const R rank_i = rl / static_cast<R>(p * (m - p));
+  if (active && g == 0) rank[i] = static_cast<double>(rank_i);
+
+  D a[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) a[c] = (A && c < nvalid) ? A[ii * m64 + g + G * c] : D(0);
+
+  for (int o = 0; o < objs.n; ++o) {
+    const EvalObj ob = objs.o[o];
+    const R c_ = static_cast<R>(ob.c), gamma = static_cast<R>(ob.gamma);
+    R primal = 0, dual = 0;
+    switch (ob.kind) {
+      case SDCA_OBJ_MULTILABEL_HINGE: {  // l2_multilabel_hinge.h:69-84
+        D mn = num<D>::inf(), mx = -num<D>::inf();
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          if (c < nvalid) {
+            mn = pos[c] ? ((s[c] < mn) ? s[c] : mn) : mn;
+            mx = !pos[c] ? ((mx < s[c]) ? s[c] : mx) : mx;
+          }
+        }
+        mn = group_min<G>(mn);
+        mx = group_max<G>(mx);
+        primal = dmax(R(0), static_cast<R>(mx - mn + D(1)));
+        break;
+      }
+      case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH: {  // l2_multilabel_hinge.h:168-191
+        const D half(0.5);
+        D v[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          v[c] = (c < nvalid) ? (pos[c] ? half - s[c] : s[c] + half) : -num<D>::inf();
+        primal = smooth_two_simplex_loss<G, C, D, R>(v, pos, p, m - p, gamma);
+        break;
+      }
+      case SDCA_OBJ_MULTILABEL_ENTROPY: {  // l2_multilabel_entropy.h:72-86
+        R sp = 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c) sp += (c < nvalid && pos[c]) ? static_cast<R>(s[c]) : R(0);
+        sp = group_sum<G>(sp);
+        primal = lse_all<G, C, D, R>(s, nvalid) - sp / static_cast<R>(p);
+        break;
+      }
+      default:
+        break;
+    }
+    R s_pos = 0, s_neg = 0, sq = 0, xl_pos = 0, xl_neg = 0;
+    const R pr = static_cast<R>(p);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      if (c < nvalid) {
+        const R x = static_cast<R>(a[c]);
+        s_pos += pos[c] ? x : R(0);
+        s_neg += pos[c] ? R(0) : x;
+        sq += x * x;
+        xl_pos += pos[c] ? x_log_x(c_ - pr * x) : R(0);
+        xl_neg += pos[c] ? R(0) : x_log_x(-x);
+      }
+    }
+    s_pos = group_sum<G>(s_pos);
+    s_neg = group_sum<G>(s_neg);
+    sq = group_sum<G>(sq);
+    xl_pos = group_sum<G>(xl_pos);
+    xl_neg = group_sum<G>(xl_neg);
+    switch (ob.kind) {
+      case SDCA_OBJ_MULTILABEL_HINGE: dual = s_pos; break;  // l2_multilabel_hinge.h:87-96
+      case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:                 // l2_multilabel_hinge.h:194-208
+        dual = R(0.5) * (s_pos - s_neg - (gamma / c_) * sq);
+        break;
+      case SDCA_OBJ_MULTILABEL_ENTROPY:                      // l2_multilabel_entropy.h:89-109
+        dual = -xl_pos / pr - xl_neg + x_log_x(c_) + dlog(pr) * (c_ - s_pos);
+        break;
+      default: break;
+    }
+    if (active && g == 0) {
+      per_example[(i * objs.n + o) * 2] = static_cast<double>(primal);
+      per_example[(i * objs.n + o) * 2 + 1] = static_cast<double>(dual);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Deferred smooth top-k hinge examples: the h values of the example are
+// sorted in LDS and one lane runs the reference's thresholds_topk_simplex on
+// them (special cases, Kiwiel on contiguous ranges, topk_cone_search), then
+// the loss from the sorted threshold sets.
+// ---------------------------------------------------------------------------
+template <class D, class R>
+__device__ R sorted_sum(const D* s, int b, int e) {
+  double acc = 0, comp = 0;
+  for (int q = b; q < e; ++q) {
+    const double x = static_cast<double>(static_cast<R>(s[q]));
+    const double t = acc + x;
+    comp += (fabs(acc) >= fabs(x)) ? (acc - t) + x : (x - t) + acc;
+    acc = t;
+  }
+  return static_cast<R>(acc + comp);
+}
+
+template <class D, class R>
+__device__ R sorted_dot(const D* s, int b, int e) {
+  double acc = 0;
+  for (int q = b; q < e; ++q) {
+    const double x = static_cast<double>(static_cast<R>(s[q]));
+    acc += x * x;
+  }
+  return static_cast<R>(acc);
+}
+
+template <class D, class R>
+__device__ R smooth_topk_sorted(const D* s, int mp, int k, R gamma) {
+  const R K = static_cast<R>(k);
+  const R eps16 = R(16) * num<R>::eps();
+  const R sum_k = sorted_sum<D, R>(s, 0, k);
+  if (sum_k <= eps16) return R(0);
+  const R hi_c = sum_k / K;
+  const R t_c = static_cast<R>(s[k - 1]) - hi_c;
+  const bool constant = (k == mp) || (t_c >= static_cast<R>(s[k]) - eps16);
+  const R eps = num<R>::eps() * dmax(R(1), fabs(gamma));
+  if (constant && !(K * hi_c > gamma + eps)) return hi_c * sum_k - R(0.5) * hi_c * hi_c * K;
+  // Kiwiel on the sorted values: U = [0, f), M = [f, l), L = [l, mp)
+  const R hi = gamma / K;
+  int mc = mp, f = 0, l = mp;
+  R t = (sorted_sum<D, R>(s, 0, mp) - gamma) / static_cast<R>(mp);
+  for (int iter = 0; iter <= mp; ++iter) {
+    const R c_lo = t, c_hi = hi + t;
+    int p_lo = f;
+    while (p_lo < l && static_cast<R>(s[p_lo]) > c_lo) ++p_lo;
+    int p_hi = f;
+    while (p_hi < p_lo && static_cast<R>(s[p_hi]) > c_hi) ++p_hi;
+    const R s_lo = sorted_sum<D, R>(s, p_lo, l);
+    const int n_lo = l - p_lo;
+    const R s_hi = sorted_sum<D, R>(s, f, p_hi);
+    const int n_hi = p_hi - f;
+    const R sh = static_cast<R>(n_hi) * hi;
+    const R infeas = s_hi + s_lo - sh - static_cast<R>(n_hi + n_lo) * t;
+    R next;
+    if (n_hi > 0 && infeas > eps) {
+      f = p_hi;
+      next = static_cast<R>(mc) * t - s_hi + sh;
+      mc -= n_hi;
+    } else if (n_lo > 0 && infeas < -eps) {
+      l = p_lo;
+      next = static_cast<R>(mc) * t - s_lo;
+      mc -= n_lo;
+    } else {
+      f = p_hi;
+      l = p_lo;
+      break;
+    }
+    if (mc > 0) t = next / static_cast<R>(mc);
+    else break;
+  }
+  bool lt = false;
+  if (!constant) {
+    if (f == 0) {
+      lt = t < -eps;
+    } else {
+      const R num_u = static_cast<R>(f);
+      lt = K * (sorted_sum<D, R>(s, 0, f) + (K - num_u) * t) < gamma * num_u - eps;
+    }
+  }
+  R th = hi;
+  if (lt) {
+    // topk_cone_search (topk_cone.h:58-133) on the sorted values
+    R k_u = K, min_u = num<R>::inf(), num_u = 0, sum_u = 0;
+    bool found = false;
+    for (int mf = 0; !found;) {
+      R min_m = num<R>::inf(), max_m = -num<R>::inf(), sum_m = 0, num_m_sum_u = 0;
+      R den = k_u * k_u;
+      const R k_u_sum_u = k_u * sum_u;
+      for (int ml = mf;;) {
+        const R tt_ = (num_u * sum_m - k_u_sum_u) / den;
+        const R hh = (num_m_sum_u + k_u * sum_m) / den;
+        const R tt = hh + tt_;
+        if (max_m - eps16 <= tt && tt <= min_u + eps16 && tt_ <= min_m + eps16 &&
+            (ml == mp || static_cast<R>(s[ml]) - eps16 <= tt_)) {
+          t = tt_;
+          th = hh;
+          f = mf;
+          l = ml;
+          found = true;
+          break;
+        }
+        if (ml == mp) break;
+        min_m = static_cast<R>(s[ml]);
+        max_m = static_cast<R>(s[mf]);
+        sum_m += min_m;
+        num_m_sum_u += sum_u;
+        den += num_u;
+        ++ml;
+      }
+      if (found || mf == k) break;
+      min_u = static_cast<R>(s[mf]);
+      sum_u += min_u;
+      k_u -= R(1);
+      num_u += R(1);
+      ++mf;
+    }
+    if (!found) return R(0);  // default zero thresholds
+  }
+  SetStats<R> st;
+  st.sum_u = sorted_sum<D, R>(s, 0, f);
+  st.n_u = f;
+  st.sum_m = sorted_sum<D, R>(s, f, l);
+  st.dot_m = sorted_dot<D, R>(s, f, l);
+  st.n_m = l - f;
+  return smooth_loss(t, th, st);
+}
+
+template <class D, class R>
+__global__ void __launch_bounds__(256)
+eval_slow_kernel(const D* __restrict__ S, const int64_t* __restrict__ labels, int64_t m64,
+                 EvalObjs objs, double* __restrict__ per_example, const int* __restrict__ slow,
+                 int pow2) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  D* s = reinterpret_cast<D*>(smem_raw);
+  const int m = static_cast<int>(m64);
+  const int count = slow[0];
+  for (int w = blockIdx.x; w < count; w += gridDim.x) {
+    const int64_t i = slow[1 + 2 * w];
+    const int o = slow[2 + 2 * w];
+    const D* srow = S + i * m64;
+    const int y = static_cast<int>(labels[i]);
+    const D shift1 = D(1) - srow[y];
+    // h over j != y, compacted: positions after y move down by one.
+    for (int q = threadIdx.x; q < pow2; q += blockDim.x) {
+      D v = -num<D>::inf();
+      if (q < m - 1) v = srow[q < y ? q : q + 1] + shift1;
+      s[q] = v;
+    }
+    __syncthreads();
+    for (int size = 2; size <= pow2; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int q = threadIdx.x; q < pow2; q += blockDim.x) {
+          const int partner = q ^ stride;
+          if (partner > q) {
+            const bool desc = (q & size) == 0;
+            const D a = s[q], b = s[partner];
+            if (desc ? (a < b) : (b < a)) {
+              s[q] = b;
+              s[partner] = a;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (threadIdx.x == 0) {
+      const EvalObj ob = objs.o[o];
+      per_example[(i * objs.n + o) * 2] = static_cast<double>(
+          smooth_topk_sorted<D, R>(s, m - 1, ob.k, static_cast<R>(ob.gamma)));
+    }
+    __syncthreads();
+  }
+}
+
+template <class D, class R, int G, int C, int KM>
+hipError_t launch_mc(const EvalLaunch& a) {
+  constexpr int B = 64 / G;
+  const int64_t blocks = (a.n + B - 1) / B;
+  const size_t shmem = (static_cast<size_t>(B) * a.m + 64) * sizeof(D);
+  hipLaunchKernelGGL((eval_multiclass_kernel<G, C, KM, D, R>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(64), shmem, a.stream, static_cast<const D*>(a.S),
+                     static_cast<const D*>(a.A), a.labels, a.m, a.n, a.objs, a.per_example,
+                     a.counts, a.slow);
+  return hipGetLastError();
+}
+
+template <class D, class R, int G, int C>
+hipError_t launch_ml(const EvalLaunch& a) {
+  constexpr int B = 64 / G;
+  const int64_t blocks = (a.n + B - 1) / B;
+  hipLaunchKernelGGL((eval_multilabel_kernel<G, C, D, R>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(64), 0, a.stream, static_cast<const D*>(a.S), static_cast<const D*>(a.A),
+                     a.labels, a.offsets, a.m, a.n, a.objs, a.per_example, a.rank);
+  return hipGetLastError();
+}
+
+template <class D, class R>
+hipError_t launch_typed(const EvalLaunch& a) {
+  if (a.offsets) {
+    if (a.m <= 64) return launch_ml<D, R, 4, 16>(a);
+    if (a.m <= 256) return launch_ml<D, R, 16, 16>(a);
+    if (a.m <= 1024) return launch_ml<D, R, 64, 16>(a);
+    return launch_ml<D, R, 64, 32>(a);
+  }
+  int kmax = 1;
+  for (int o = 0; o < a.objs.n; ++o) kmax = a.objs.o[o].k > kmax ? a.objs.o[o].k : kmax;
+  if (kmax <= 5) {
+    if (a.m <= 64) return launch_mc<D, R, 4, 16, 5>(a);
+    if (a.m <= 256) return launch_mc<D, R, 16, 16, 5>(a);
+    if (a.m <= 1024) return launch_mc<D, R, 64, 16, 5>(a);
+    return launch_mc<D, R, 64, 32, 5>(a);
+  }
+  if (a.m <= 64) return launch_mc<D, R, 4, 16, 8>(a);
+  if (a.m <= 256) return launch_mc<D, R, 16, 16, 8>(a);
+  if (a.m <= 1024) return launch_mc<D, R, 64, 16, 8>(a);
+  return launch_mc<D, R, 64, 32, 8>(a);
+}
+
+template <class D, class R>
+hipError_t launch_slow_typed(const EvalLaunch& a) {
+  int pow2 = 1;
+  while (pow2 < a.m) pow2 <<= 1;
+  hipLaunchKernelGGL((eval_slow_kernel<D, R>), dim3(256), dim3(256),
+                     static_cast<size_t>(pow2) * sizeof(D), a.stream, static_cast<const D*>(a.S),
+                     a.labels, a.m, a.objs, a.per_example, a.slow, pow2);
+  return hipGetLastError();
+}
+
+// Deterministic sums: one workgroup per output, fixed strided order plus a
+// fixed LDS tree.
+__global__ void __launch_bounds__(256)
+reduce_kernel(const double* __restrict__ per_example, int64_t n, int n_obj,
+              const double* __restrict__ rank, double* __restrict__ sums,
+              double* __restrict__ rank_sum) {
+  __shared__ double part[256];
+  const int out = blockIdx.x;  // 0 .. 2 n_obj - 1: (objective, primal/dual); 2 n_obj: rank
+  double acc = 0;
+  if (out < 2 * n_obj) {
+    for (int64_t i = threadIdx.x; i < n; i += 256) acc += per_example[i * 2 * n_obj + out];
+  } else if (rank) {
+    for (int64_t i = threadIdx.x; i < n; i += 256) acc += rank[i];
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (out < 2 * n_obj) sums[out] = part[0];
+    else if (rank_sum) *rank_sum = part[0];
+  }
+}
+
+__global__ void __launch_bounds__(256)
+hist_kernel(const int* __restrict__ counts, int64_t n, unsigned long long* __restrict__ hist) {
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    atomicAdd(hist + counts[i], 1ull);
+}
+
+__global__ void zero_u64_kernel(unsigned long long* p, int64_t count) {
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < count; i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = 0;
+}
+
+template <class D>
+__global__ void __launch_bounds__(256)
+regularizer_kernel(const D* __restrict__ W, const D* __restrict__ W0, int64_t count,
+                   double* __restrict__ partials) {
+  __shared__ double p0[256], p1[256];
+  double a0 = 0, a1 = 0;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < count; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const double w = static_cast<double>(W[i]);
+    a0 += w * w;
+    if (W0) a1 += static_cast<double>(W0[i]) * w;
+  }
+  p0[threadIdx.x] = a0;
+  p1[threadIdx.x] = a1;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) {
+      p0[threadIdx.x] += p0[threadIdx.x + w];
+      p1[threadIdx.x] += p1[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    partials[2 * blockIdx.x] = p0[0];
+    partials[2 * blockIdx.x + 1] = p1[0];
+  }
+}
+
+__global__ void regularizer_final(const double* __restrict__ partials, int nb, double* out) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    double a0 = 0, a1 = 0;
+    for (int b = 0; b < nb; ++b) {
+      a0 += partials[2 * b];
+      a1 += partials[2 * b + 1];
+    }
+    out[0] = 0.5 * a0;
+    out[1] = a1;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+gemm_f64_kernel(const double* __restrict__ X, const double* __restrict__ W, double* __restrict__ S,
+                int64_t n, int64_t m, int64_t d) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= n * m) return;
+  const int64_t i = idx / m, j = idx % m;
+  const double* x = X + i * d;
+  const double* w = W + j * d;
+  double acc = 0;
+  for (int64_t q = 0; q < d; ++q) acc += w[q] * x[q];
+  S[idx] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_eval_epilogue(const EvalLaunch& a) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_typed<float, float>(a);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_typed<float, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_typed<double, double>(a);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_eval_slow(const EvalLaunch& a) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_slow_typed<float, float>(a);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_slow_typed<float, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_slow_typed<double, double>(a);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_eval_reduce(const EvalLaunch& a, double* sums, double* rank_sum,
+                              unsigned long long* hist) {
+  hipLaunchKernelGGL(reduce_kernel, dim3(2 * a.objs.n + 1), dim3(256), 0, a.stream,
+                     a.per_example, a.n, a.objs.n, a.rank, sums, rank_sum);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (hist && a.counts) {
+    hipLaunchKernelGGL(zero_u64_kernel, dim3(static_cast<unsigned>((a.m + 255) / 256)), dim3(256), 0,
+                       a.stream, hist, a.m);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    int64_t blocks = (a.n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(hist_kernel, dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)), dim3(256),
+                       0, a.stream, a.counts, a.n, hist);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+hipError_t launch_regularizer(int data, const void* W, const void* W0, int64_t count,
+                              double* partials, double* out, hipStream_t stream) {
+  int64_t blocks = (count + 255) / 256;
+  if (blocks > 512) blocks = 512;
+  if (blocks < 1) blocks = 1;
+  if (data == SDCA_F32) {
+    hipLaunchKernelGGL(regularizer_kernel<float>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, static_cast<const float*>(W), static_cast<const float*>(W0), count,
+                       partials);
+  } else {
+    hipLaunchKernelGGL(regularizer_kernel<double>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, static_cast<const double*>(W), static_cast<const double*>(W0), count,
+                       partials);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(regularizer_final, dim3(1), dim3(64), 0, stream, partials,
+                     static_cast<int>(blocks), out);
+  return hipGetLastError();
+}
+
+hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, int64_t n,
+                                  int64_t m, int64_t d, hipStream_t stream) {
+  const int64_t total = n * m;
+  hipLaunchKernelGGL(gemm_f64_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                     stream, X, W, S, n, m, d);
+  return hipGetLastError();
+}
+
+}  // namespace sdca_gpu

@@ -1,0 +1,64 @@
+// Host-side launch interface of the evaluation kernels (internal).
+#ifndef SDCA_HIP_EVAL_LAUNCH_HPP
+#define SDCA_HIP_EVAL_LAUNCH_HPP
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sdca_hip.h"
+
+namespace sdca_gpu {
+
+constexpr int kMaxObjectives = 8;
+// Top-k objectives keep k <= kEvalMaxK in registers.
+constexpr int64_t kEvalMaxK = 8;
+// Largest m the per-example kernels hold in registers.
+constexpr int64_t kEvalMaxM = 2048;
+
+// One objective as the kernels see it.
+struct EvalObj {
+  int kind;
+  int k;
+  double c, gamma;
+};
+
+struct EvalObjs {
+  int n;
+  EvalObj o[kMaxObjectives];
+};
+
+struct EvalLaunch {
+  int data, result;
+  int64_t m, n;
+  const void* S;           // n x m scores (device)
+  const void* A;           // n x m dual variables or NULL (device)
+  const int64_t* labels;   // device
+  const int64_t* offsets;  // device, multilabel CSR or NULL
+  EvalObjs objs;
+  double* per_example;     // device: n x n_obj x 2 (primal, dual) before the coefficient
+  int* counts;             // device: n (multiclass top-k counts), or NULL
+  double* rank;            // device: n (multilabel rank loss per example), or NULL
+  int* slow;               // device: [0] = count, then (example, objective) pairs
+  hipStream_t stream;
+};
+
+// S = X W^T for fp32 on the matrix cores; X: n x d, W: m x d, S: n x m (row-major).
+hipError_t launch_scores_gemm(const float* X, const float* W, float* S, int64_t n, int64_t m,
+                              int64_t d, hipStream_t stream);
+// The same contraction in double (plain FMA kernel).
+hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, int64_t n,
+                                  int64_t m, int64_t d, hipStream_t stream);
+// Per-example epilogue (losses, counts, rank loss) and its deferred examples.
+hipError_t launch_eval_epilogue(const EvalLaunch& a);
+hipError_t launch_eval_slow(const EvalLaunch& a);
+// Deterministic reductions: sums[o*2+{0,1}] = sum_i per_example; rank sum;
+// hist[c] = #{i: counts[i] == c}.
+hipError_t launch_eval_reduce(const EvalLaunch& a, double* sums, double* rank_sum,
+                              unsigned long long* hist);
+// 0.5 <W, W> and <W0, W> in double (out[0], out[1]); `partials` holds 1024 doubles.
+hipError_t launch_regularizer(int data, const void* W, const void* W0, int64_t count,
+                              double* partials, double* out, hipStream_t stream);
+
+}  // namespace sdca_gpu
+
+#endif

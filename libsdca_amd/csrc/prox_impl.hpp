@@ -65,12 +65,15 @@ __device__ inline ColThr<R> slow_thr() {
   return r;
 }
 
-// Sum of the valid slots (padding holds -inf).
+// Sum of the valid slots (padding, and excluded slots, hold -inf).
 template <int G, int C, class D, class R>
 __device__ inline R total_sum(const D (&v)[C], int nvalid) {
   R s = 0;
 #pragma unroll
-  for (int c = 0; c < C; ++c) s += (c < nvalid) ? static_cast<R>(v[c]) : R(0);
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(v[c]);
+    s += (c < nvalid && x > -num<R>::inf()) ? x : R(0);
+  }
   return group_sum<G>(s);
 }
 
@@ -641,7 +644,8 @@ __device__ inline void masked_argmax(const D (&v)[C], const bool (&mask)[C], R& 
 
 template <int G, int C, class D, class R>
 __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
-                                           const ProxParamsT<R>& pp) {
+                                           const ProxParamsT<R>& pp, int* n_u_out = nullptr,
+                                           R* sum_u_out = nullptr) {
   (void)m;
   const int k = pp.k;
   const R eps = R(16) * num<R>::eps();
@@ -657,11 +661,15 @@ __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
   R log_z = mx + dlog1p(z);
   R l1 = dexp(-mx);
   R log_z_1 = isfinite(l1) ? mx + dlog1p(z + l1) : R(0);
+  if (n_u_out) *n_u_out = 0;
+  if (sum_u_out) *sum_u_out = R(0);
   if (k <= 1 || mx - eps <= log_z - dlog(K)) return make_thr<R>(log_z_1, R(0), R(1), 1);
   R sum_u = 0, k_u = K;
+  int n_u = 0;
   for (int num_u = 1; num_u < k; ++num_u) {
     const R min_u = mx;
     sum_u += min_u;
+    ++n_u;
     if (g == owner) {
 #pragma unroll
       for (int c = 0; c < C; ++c)
@@ -674,6 +682,8 @@ __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
     const R tt = log_z - dlog(k_u);
     if (mx - eps <= tt && tt <= min_u + eps) break;
   }
+  if (n_u_out) *n_u_out = n_u;
+  if (sum_u_out) *sum_u_out = sum_u;
   const R tmp = ((K - k_u) * log_z + k_u * dlog(k_u) - sum_u) / K;
   R t, hi;
   if (tmp > mx) {

@@ -275,6 +275,14 @@ int oracle_eval_scores(const sdca_objective* objs, int n_obj, int data, int resu
   if (data == SDCA_F64 && result == SDCA_F64)
     return eval_scores_impl<double, double>(objs, n_obj, m, n, static_cast<const double*>(S),
         static_cast<const double*>(A), labels, offsets, preg, dreg, rec, accuracy, per_example, nthreads);
+  // Long double arithmetic: the high-precision losses the parity tests use to
+  // bound the rounding error of the float/double paths.
+  if (data == SDCA_F32 && result == SDCA_LONG_DOUBLE)
+    return eval_scores_impl<float, long double>(objs, n_obj, m, n, static_cast<const float*>(S),
+        static_cast<const float*>(A), labels, offsets, preg, dreg, rec, accuracy, per_example, nthreads);
+  if (data == SDCA_F64 && result == SDCA_LONG_DOUBLE)
+    return eval_scores_impl<double, long double>(objs, n_obj, m, n, static_cast<const double*>(S),
+        static_cast<const double*>(A), labels, offsets, preg, dreg, rec, accuracy, per_example, nthreads);
   return SDCA_ERR_PRECISION;
 }
 

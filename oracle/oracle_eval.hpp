@@ -5,7 +5,8 @@
 // feature-input objectives (objective/*.h), the per-example epilogue of
 // evaluate_dataset (eval.h:36-47, eval/primal.h:27-87, eval/dual.h:23-63) and
 // eval_end (eval/core.h:43-95).  The BLAS dot products of the reference
-// (math/blas.h:191-219) are restated as sequential loops in the Data type.
+// (math/blas.h:191-219) are modelled as exact dot products rounded to the Data
+// type (see blas_dot).
 #ifndef SDCA_ORACLE_EVAL_HPP
 #define SDCA_ORACLE_EVAL_HPP
 
@@ -14,11 +15,15 @@
 
 namespace orc {
 
+// cblas_?dot (math/blas.h:191-219).  The reference links whatever CBLAS the
+// build selects (MKL, Accelerate, ...; cmake/SelectBLAS.cmake), so its
+// accumulation order is unpinned; the oracle models it as the exact dot
+// product rounded once to the Data type (accumulated in long double).
 template <class D>
 inline D blas_dot(std::ptrdiff_t n, const D* x, const D* y) {
-  D s = 0;
-  for (std::ptrdiff_t i = 0; i < n; ++i) s += x[i] * y[i];
-  return s;
+  long double s = 0;
+  for (std::ptrdiff_t i = 0; i < n; ++i) s += static_cast<long double>(x[i]) * y[i];
+  return static_cast<D>(s);
 }
 
 template <class D, class R>

@@ -1,0 +1,222 @@
+"""GPU parity of the evaluation pass against the CPU oracle.
+
+* scores: the MFMA GEMM against a float64 product; the bound is the fp32
+  dot-product forward error, sqrt(d) eps sum|x_l w_l| (a d-term sum).
+* epilogue on identical scores: per-example primal and dual losses of every
+  objective against the oracle (bit-exact with the reference on these
+  inputs), top-k counts exactly, totals after eval_end.
+* end to end: eval_features against the oracle run on the GPU's own scores
+  (so that the integer counts can be compared exactly) and against the
+  oracle's own float scores within the fp32 score tolerance.
+
+Tolerance for per-example losses, relative to max(1, |loss|): rtol = 1e-5
+when the arithmetic (Result) type or the data type is float and 1e-12 when
+both are double, plus the reference's own rounding error E, measured per
+batch as max |ref - exact| with "exact" the oracle in long double:
+|gpu - ref| <= rtol + 3 E and |gpu - exact| <= rtol + 2 E.  As for the prox
+operators, E is needed because the smooth losses go through a Kiwiel
+projection of m - 1 values: in float the reference's own loss at m = 1000 is
+~1e-2 away from the long-double value, and any other summation order rounds
+differently.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = 0, 1
+RTOL = {F32: 1e-5, F64: 1e-12}
+
+MC_OBJS = [("l2_hinge_topk", 1.0, 1.0, 5), ("l2_hinge_topk_smooth", 1.0, 1.0, 5),
+           ("l2_topk_hinge", 1.0, 1.0, 3), ("l2_topk_hinge_smooth", 0.5, 0.7, 3),
+           ("l2_entropy", 1.0, 1.0, 1), ("l2_entropy_topk", 1.0, 1.0, 3)]
+ML_OBJS = [("l2_multilabel_hinge", 1.0, 1.0, 1), ("l2_multilabel_hinge_smooth", 1.0, 1.0, 1),
+           ("l2_multilabel_entropy", 1.0, 1.0, 1)]
+ORACLE_NAME = {"l2_hinge_topk": "hinge_topk", "l2_hinge_topk_smooth": "hinge_topk_smooth",
+               "l2_topk_hinge": "topk_hinge", "l2_topk_hinge_smooth": "topk_hinge_smooth",
+               "l2_entropy": "entropy", "l2_entropy_topk": "entropy_topk",
+               "l2_multilabel_hinge": "multilabel_hinge",
+               "l2_multilabel_hinge_smooth": "multilabel_hinge_smooth",
+               "l2_multilabel_entropy": "multilabel_entropy"}
+
+
+def oracle_objs(objs):
+    return [(ORACLE_NAME[n], c, g, k) for (n, c, g, k) in objs]
+
+
+def multilabel_labels(rng, n, m, pmax=5):
+    off = [0]
+    lab = []
+    for _ in range(n):
+        p = int(rng.integers(1, min(pmax, m - 1) + 1))
+        lab += sorted(rng.choice(m, p, replace=False).tolist())
+        off.append(len(lab))
+    return np.array(lab, dtype=np.int64), np.array(off, dtype=np.int64)
+
+
+@pytest.mark.parametrize("n,m,d", [(3000, 300, 1000), (517, 1000, 4096), (1000, 200, 1024),
+                                   (64, 5, 37), (130, 129, 16)])
+def test_scores_gemm(cuda, n, m, d):
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(n + m + d)
+    X = rng.standard_normal((n, d)).astype(np.float32)
+    W = (rng.standard_normal((m, d)) * 0.01).astype(np.float32)
+    S = sd.scores(torch.from_numpy(X).to(cuda), torch.from_numpy(W).to(cuda))
+    torch.cuda.synchronize()
+    got = S.cpu().numpy().astype(np.float64)
+    want = X.astype(np.float64) @ W.astype(np.float64).T
+    bound = np.sqrt(d) * np.finfo(np.float32).eps * (np.abs(X).astype(np.float64) @ np.abs(W).astype(np.float64).T)
+    err = np.abs(got - want)
+    assert (err <= 4 * bound + 1e-30).all(), f"max err/bound {(err / (bound + 1e-30)).max():.2f}"
+
+
+LONG_DOUBLE = 2
+
+
+def compare_per_example(got, want, rtol, what, exact=None):
+    """Per objective (last axis): |got - want| / s <= rtol + 3 E, and with the
+    long-double values `exact`, |got - exact| / s <= rtol + 2 E."""
+    scale = np.maximum(1.0, np.abs(want))
+    err = np.abs(got - want) / scale
+    E = np.zeros(want.shape[-1])
+    if exact is not None:
+        E = np.nanmax(np.abs(want - exact) / scale, axis=0)
+    ok = np.isnan(want) | (err <= rtol + 3 * E)
+    bad = np.argwhere(~ok)
+    assert bad.size == 0, (f"{what}: {len(bad)} entries differ, max scaled err "
+                           f"{np.nanmax(err):.3e} (E per objective {E}); first {bad[0]}: got "
+                           f"{got[tuple(bad[0])]} want {want[tuple(bad[0])]}")
+    if exact is not None:
+        e_gpu = np.nanmax(np.abs(got - exact) / scale, axis=0)
+        assert (e_gpu <= rtol + 2 * E).all(), f"{what}: GPU error vs exact {e_gpu} > rtol + 2E ({E})"
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float32, F64), (np.float64, F64)])
+@pytest.mark.parametrize("m", [2, 10, 100, 257, 1000])
+@pytest.mark.parametrize("with_a", [False, True])
+def test_epilogue_multiclass(cuda, oracle, dtype, result, m, with_a):
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(m + 7)
+    n = 700
+    S = (rng.standard_normal((n, m)) * 2).astype(dtype)
+    y = rng.integers(0, m, n)
+    # some exact ties with the label score
+    S[: n // 10, 0] = S[np.arange(n // 10), y[: n // 10]]
+    A = (rng.standard_normal((n, m)) * 0.01).astype(dtype) if with_a else None
+    if A is not None:
+        A[np.arange(n), y] = np.abs(A[np.arange(n), y])
+        mask = np.ones_like(A, dtype=bool)
+        mask[np.arange(n), y] = False
+        A[mask] = -np.abs(A[mask])
+    objs = [o for o in MC_OBJS if o[3] <= m - 1]
+    recs, acc, pe = sd.eval_scores(objs, torch.from_numpy(S).to(cuda), y,
+                                   A=None if A is None else torch.from_numpy(A).to(cuda),
+                                   result=result, per_example=True)
+    torch.cuda.synchronize()
+    pe = pe.cpu().numpy()
+    o_recs, o_acc, o_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, result=result,
+                                             per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, result=LONG_DOUBLE,
+                                    per_example=True)
+    rtol = RTOL[result]
+    if dtype == np.float32:
+        rtol = max(rtol, RTOL[F32])
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], rtol, f"primal m={m}", x_pe[:, :, 0])
+    compare_per_example(pe[:, :, 1], o_pe[:, :, 1], rtol, f"dual m={m}", x_pe[:, :, 1])
+    # top-k counts are integers: accuracy must match exactly
+    assert np.array_equal(acc * n, o_acc * n) or np.allclose(acc, o_acc, rtol=0, atol=0.5 / n), \
+        f"accuracy differs: {acc[:5]} vs {o_acc[:5]}"
+    # Totals after eval_end: the per-example bound summed over the batch (the
+    # coefficient scales the primal loss), plus the reference's own
+    # accumulation error in the Result type.
+    eps_r = np.finfo(np.float32 if result == F32 else np.float64).eps
+    for oi, (r, o, ob) in enumerate(zip(recs, o_recs, objs)):
+        for key, col in (("primal_loss", 0), ("dual_loss", 1)):
+            coeff = r["primal_loss"] / pe[:, oi, 0].sum() if col == 0 and pe[:, oi, 0].sum() else 1.0
+            scale = np.maximum(1.0, np.abs(o_pe[:, oi, col]))
+            E = np.nanmax(np.abs(o_pe[:, oi, col] - x_pe[:, oi, col]) / scale)
+            tol = abs(coeff) * (np.sum(scale) * (rtol + 3 * E) + n * eps_r * np.abs(o_pe[:, oi, col]).sum())
+            assert abs(r[key] - o[key]) <= tol + 1e-300, f"{ob[0]} {key}: {r[key]} vs {o[key]} (tol {tol})"
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float64, F64)])
+@pytest.mark.parametrize("m", [3, 20, 200, 1000])
+def test_epilogue_multilabel(cuda, oracle, dtype, result, m):
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(m + 11)
+    n = 500
+    S = (rng.standard_normal((n, m)) * 2).astype(dtype)
+    lab, off = multilabel_labels(rng, n, m)
+    A = (rng.standard_normal((n, m)) * 0.01).astype(dtype)
+    recs, _, pe = sd.eval_scores(ML_OBJS, torch.from_numpy(S).to(cuda), lab,
+                                 A=torch.from_numpy(A).to(cuda), offsets=off, result=result,
+                                 per_example=True)
+    torch.cuda.synchronize()
+    pe = pe.cpu().numpy()
+    o_recs, _, o_pe = oracle.eval_scores(oracle_objs(ML_OBJS), S, A, lab, off, result=result,
+                                         per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(ML_OBJS), S, A, lab, off, result=LONG_DOUBLE,
+                                    per_example=True)
+    rtol = RTOL[result]
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], rtol, f"multilabel primal m={m}", x_pe[:, :, 0])
+    compare_per_example(pe[:, :, 1], o_pe[:, :, 1], rtol, f"multilabel dual m={m}", x_pe[:, :, 1])
+    for r, o in zip(recs, o_recs):
+        assert abs(r["rank_loss"] - o["rank_loss"]) <= 1e-6 * max(1, abs(o["rank_loss"]))
+
+
+@pytest.mark.parametrize("m,d", [(1000, 4096), (200, 1024), (37, 100)])
+def test_eval_features_end_to_end(cuda, oracle, m, d):
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(m + d)
+    n = 1500
+    X = rng.standard_normal((n, d)).astype(np.float32)
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    W = (rng.standard_normal((m, d)) * 0.01).astype(np.float32)
+    W0 = (rng.standard_normal((m, d)) * 0.01).astype(np.float32)
+    y = rng.integers(0, m, n)
+    objs = [("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)]
+    tX, tW = torch.from_numpy(X).to(cuda), torch.from_numpy(W).to(cuda)
+    recs, acc, pe = sd.eval_features(objs, tX, tW, y, W0=torch.from_numpy(W0).to(cuda),
+                                     per_example=True)
+    S = sd.scores(tX, tW)
+    torch.cuda.synchronize()
+    S = S.cpu().numpy()
+    pe = pe.cpu().numpy()
+    preg, dreg = oracle.regularizers(W, W0)
+    o_recs, o_acc, o_pe = oracle.eval_scores(oracle_objs(objs), S, None, y, preg=preg, dreg=dreg,
+                                             per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), S, None, y, result=LONG_DOUBLE,
+                                    per_example=True)
+    # Same scores: counts exact, losses within the fp32 tolerance.
+    assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n)
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], 1e-5, "features primal", x_pe[:, :, 0])
+    # Regularizers 0.5 <W, W> - <W0, W> and 0.5 <W, W>, against float64.
+    W64, W064 = W.astype(np.float64), W0.astype(np.float64)
+    preg64 = 0.5 * np.sum(W64 * W64) - np.sum(W064 * W64)
+    dreg64 = 0.5 * np.sum(W64 * W64)
+    for r, o in zip(recs, o_recs):
+        assert abs(r["primal_regularizer"] - preg64) <= 1e-6 * max(1, abs(preg64))
+        assert abs(r["dual_regularizer"] - dreg64) <= 1e-6 * max(1, abs(dreg64))
+        assert abs(r["primal"] - o["primal"]) <= 1e-4 * max(1, abs(o["primal"]))
+
+
+def test_eval_host_pointers(oracle):
+    """numpy in, records out through the library's staging."""
+    import libsdca_amd as sd
+    rng = np.random.default_rng(5)
+    n, m, d = 300, 50, 64
+    X = rng.standard_normal((n, d)).astype(np.float32)
+    W = (rng.standard_normal((m, d)) * 0.1).astype(np.float32)
+    y = rng.integers(0, m, n)
+    objs = [("l2_hinge_topk", 1.0, 1.0, 2), ("l2_entropy", 2.0, 1.0, 1)]
+    recs, acc, _ = sd.eval_features(objs, X, W, y)
+    S = sd.scores(X, W)
+    preg, dreg = oracle.regularizers(W)
+    o_recs, o_acc, _ = oracle.eval_scores(oracle_objs(objs), S, None, y, preg=preg, dreg=dreg)
+    assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n)
+    for r, o in zip(recs, o_recs):
+        assert abs(r["primal"] - o["primal"]) <= 1e-4 * max(1, abs(o["primal"]))
