@@ -15,7 +15,9 @@ duration used for the roofline.
 Other workloads (--config): c1 (knapsack_eq f64 m=10 n=1e5), c2cone (top-k
 cone on the headline input), c3 (entropy f64 m=1000 n=2e5), c3norm
 (entropy_norm f64), lambert (W(exp(x)) f64 on 10M points), c5prox
-(two_simplex f32 m=200 n=5e5, per-column p).
+(two_simplex f32 m=200 n=5e5, per-column p), c4 (evaluation pass d=4096
+m=1000 n=1e5: examples/s, roofline on the fp32 MFMA score GEMM), c5eval
+(multilabel evaluation d=1024 m=200 n=5e5).
 
 cpu_baseline: the reference's own prox loop (oracle/_ref, built from the
 reference headers with -O3) - or the oracle restatement when that library is
@@ -61,7 +63,20 @@ CONFIGS = {
                    gen="normal", seed=4105, col_p=True,
                    desc="batched two-block simplex prox, m=200, n=500,000, fp32, N(0,1), "
                         "per-column p in [1,5]"),
+    "c4": dict(op="eval", d=4096, m=1000, n=100_000, dtype="f32", result="f32", seed=104,
+               objs=[("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)],
+               desc="evaluation pass, fp32: X d=4096 x n=100,000 (N(0,1), unit columns), "
+                    "W d x m=1000 (N(0,0.01^2)), scores W'X, smooth top-5 hinge (gamma=1) and "
+                    "softmax cross-entropy with c=1 (lambda=1/n), top-1/top-5 accuracy"),
+    "c5eval": dict(op="eval", d=1024, m=200, n=500_000, dtype="f32", result="f32", seed=105,
+                   multilabel=True,
+                   objs=[("l2_multilabel_hinge_smooth", 1.0, 1.0, 1),
+                         ("l2_multilabel_entropy", 1.0, 1.0, 1)],
+                   desc="multilabel evaluation pass, fp32: d=1024, m=200, n=500,000, 1-5 "
+                        "positive labels per example, smooth multilabel hinge and multilabel "
+                        "cross-entropy with c=1, rank loss"),
 }
+MFMA_F32_PEAK_TFLOPS = 157.3
 
 
 def parse():
@@ -147,6 +162,127 @@ def cpu_baseline(cfg, x_sample, col_p_sample, seconds):
             "sample": f"first {total_cols} columns of the same input, 1 thread, {elapsed:.1f} s"}
 
 
+def make_eval_input(cfg, torch, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(cfg["seed"])
+    n, m, d = cfg["n"], cfg["m"], cfg["d"]
+    X = torch.randn((n, d), generator=g, device=dev, dtype=torch.float32)
+    X /= X.norm(dim=1, keepdim=True)
+    W = torch.randn((m, d), generator=g, device=dev, dtype=torch.float32) * 0.01
+    if cfg.get("multilabel"):
+        # 1-5 distinct sorted labels per example, drawn uniformly without replacement.
+        p = torch.randint(1, 6, (n,), generator=g, device=dev)
+        keys = torch.rand((n, m), generator=g, device=dev)
+        order = keys.argsort(dim=1)[:, :5]
+        ar = torch.arange(5, device=dev)[None, :]
+        chosen = torch.where(ar < p[:, None], order, torch.full_like(order, m))
+        chosen, _ = chosen.sort(dim=1)
+        labels = chosen[chosen < m].contiguous()
+        offsets = torch.zeros(n + 1, dtype=torch.int64, device=dev)
+        offsets[1:] = torch.cumsum(p, 0)
+        return X, W, labels, offsets
+    labels = torch.randint(0, m, (n,), generator=g, device=dev)
+    return X, W, labels, None
+
+
+def bench_eval(cfg, args, torch, sd):
+    dev = torch.device("cuda:0")
+    X, W, labels, offsets = make_eval_input(cfg, torch, dev)
+    objs = cfg["objs"]
+    stream = torch.cuda.current_stream()
+
+    def step():
+        return sd.eval_features(objs, X, W, labels, offsets=offsets)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        recs, acc, _ = step()  # each call ends with a host synchronisation
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    # The dominant kernel is the score GEMM: time it on its own, event-timed
+    # on the stream it runs on.
+    S = torch.empty((cfg["n"], cfg["m"]), dtype=torch.float32, device=dev)
+    for _ in range(2):
+        sd.scores(X, W, out=S)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        a.record(stream)
+        sd.scores(X, W, out=S)
+        b.record(stream)
+    torch.cuda.synchronize()
+    gemm_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    flops = 2.0 * cfg["n"] * cfg["m"] * cfg["d"]
+    achieved = flops / (gemm_ms / 1e3) / 1e12
+    value = cfg["n"] / (ms_per_step / 1e3)
+    extra = {"records": recs}
+    if not cfg.get("multilabel"):
+        extra["top1"] = float(acc[0])
+        extra["top5"] = float(acc[4])
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "examples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded on the device)",
+        "config": {"workload": cfg["desc"], "d": cfg["d"], "m": cfg["m"], "n": cfg["n"],
+                   "objectives": [o[0] for o in objs]},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS, "traffic": None,
+                     "note": f"score GEMM 2 n m d = {flops:.3e} flop / mean event-timed launch "
+                             f"{gemm_ms:.3f} ms; full pass {ms_per_step:.3f} ms"},
+        "eval": extra,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_eval(cfg, X, W, labels, offsets, args.cpu_seconds)
+    print(json.dumps(result))
+
+
+def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds):
+    """The oracle's evaluation (gemv loop + epilogue, single thread, as the
+    reference's evaluate_dataset runs) on a bounded sample of examples."""
+    import numpy as np
+    from oracle import binding
+    lib = binding.oracle()
+    oname = {"l2_hinge_topk_smooth": "hinge_topk_smooth", "l2_entropy": "entropy",
+             "l2_multilabel_hinge_smooth": "multilabel_hinge_smooth",
+             "l2_multilabel_entropy": "multilabel_entropy"}
+    objs = [(oname[o[0]], o[1], o[2], o[3]) for o in cfg["objs"]]
+    Wh = W.cpu().numpy()
+    lab = labels.cpu().numpy()
+    off = None if offsets is None else offsets.cpu().numpy()
+
+    def run(ne):
+        Xs = X[:ne].cpu().numpy()
+        t0 = time.perf_counter()
+        S = lib.scores(Xs, Wh)
+        if off is None:
+            lib.eval_scores(objs, S, None, lab[:ne])
+        else:
+            lib.eval_scores(objs, S, None, lab[: off[ne]], off[: ne + 1])
+        return time.perf_counter() - t0
+
+    probe = 200
+    dt = run(probe)
+    ne = int(min(cfg["n"], max(probe, seconds / max(dt / probe, 1e-9))))
+    dt = run(ne)
+    return {"value": ne / dt, "unit": "examples/s", "cores": 1, "kind": "port",
+            "sample": f"first {ne} examples, 1 thread ({dt:.1f} s): the oracle's per-example "
+                      f"gemv loop plus the restated epilogue (the reference's BLAS is not built here)"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -159,6 +295,9 @@ def main():
     import libsdca_amd as sd
 
     cfg = CONFIGS[args.config]
+    if cfg["op"] == "eval":
+        bench_eval(cfg, args, torch, sd)
+        return
     dev = torch.device("cuda:0")
     x, col_p = make_input(cfg, torch, dev)
     rotate = cfg.get("rotate", 1)
