@@ -1,0 +1,339 @@
+"""What the mathematics fixes, checked against the oracle (CPU only).
+
+These pins do not retype the oracle's formulas: each one certifies the
+result by a property that characterises it independently.
+
+* Projections are certified by first-order optimality over the vertices of
+  the (polyhedral) feasible set: x = P_K(a) iff x in K and
+  <a - x, v - x> <= 0 for every vertex v.  The top-k cone
+  {0 <= x_i <= sum(x)/k} is the cone over the vertices 1_S/k (|S| = k) of the
+  capped simplex, so the condition is: sum of the k largest of (a - x) <= 0
+  and <a - x, x> = 0.  The top-k simplex {x in cone, sum(x) <= r} has the
+  vertices 0 and r 1_S / k.
+* The knapsack / entropic thresholds are checked against a bisection on the
+  monotone constraint function in float64 (with W(e^x) from scipy).
+* Lambert W against scipy.special.lambertw, the Omega known answer and the
+  inverse identities of the reference tests (test/prox/lambert.cpp:5-157).
+* The two-block simplex and top-k entropy against scipy's SLSQP on small
+  problems, plus the regression vector of test/prox/two_simplex.cpp:55-64.
+* Evaluation: losses against closed forms (max over the projection set of
+  <h,p> - |p|^2/2 = (|h|^2 - |h - P(h)|^2) / 2), counts against numpy.
+"""
+import numpy as np
+import pytest
+import scipy.optimize
+import scipy.special
+
+from oracle import binding
+from tests import inputs
+
+F64, LD = 1, 2
+
+
+def prox(oracle, op, x, result=F64, **kw):
+    y = np.array(x, dtype=np.float64, copy=True)
+    if y.ndim == 1:
+        y = y[None, :]
+    col_p = kw.pop("col_p", None)
+    thr = oracle.prox(op, y, result=result, params=binding.make_params(**kw), col_p=col_p,
+                      thresholds=op != "lambert_w_exp")
+    return y, thr
+
+
+def topk_sum(v, k):
+    return np.sort(v)[::-1][:k].sum()
+
+
+def cases(m, seed):
+    x = np.concatenate([inputs.normal(40, m, np.float64, seed),
+                        inputs.label_shifted(40, m, np.float64, seed + 1),
+                        inputs.mixed_signs(40, m, np.float64, seed + 2, -2, 2),
+                        inputs.decades(20, m, np.float64, seed + 3, -2, 2),
+                        inputs.decades(20, m, np.float64, seed + 4, -2, 2, sign=-1.0)])
+    return x
+
+
+@pytest.mark.parametrize("m,k", [(2, 1), (5, 1), (5, 2), (10, 3), (30, 5), (100, 5), (7, 7)])
+def test_topk_cone_optimality(oracle, m, k):
+    X = cases(m, 10 + m + k)
+    P, _ = prox(oracle, "topk_cone", X, k=k)
+    for a, x in zip(X, P):
+        scale = max(1.0, np.abs(a).max())
+        tol = 1e-10 * scale * m
+        assert x.min() >= -tol
+        assert x.max() <= x.sum() / k + tol
+        r = a - x
+        assert topk_sum(r, k) <= tol, "polar cone condition"
+        assert abs(np.dot(r, x)) <= tol * max(1.0, np.abs(x).sum())
+
+
+@pytest.mark.parametrize("m,k,rhs", [(2, 1, 1.0), (5, 2, 1.0), (10, 3, 2.0), (30, 5, 1.0),
+                                     (100, 5, 1.0), (6, 6, 1.0)])
+def test_topk_simplex_optimality(oracle, m, k, rhs):
+    X = cases(m, 20 + m + k)
+    P, _ = prox(oracle, "topk_simplex", X, k=k, rhs=rhs)
+    for a, x in zip(X, P):
+        scale = max(1.0, np.abs(a).max())
+        tol = 1e-10 * scale * m
+        assert x.min() >= -tol and x.sum() <= rhs + tol and x.max() <= x.sum() / k + tol
+        r = a - x
+        rx = np.dot(r, x)
+        assert rx >= -tol * max(1, np.abs(x).sum()), "vertex 0"
+        assert (rhs / k) * topk_sum(r, k) <= rx + tol * max(1, rhs), "vertices r 1_S / k"
+
+
+def test_topk_closed_forms(oracle):
+    X = cases(12, 5)
+    P, _ = prox(oracle, "topk_cone", X, k=1)
+    assert np.allclose(P, np.maximum(X, 0), atol=1e-12)
+    P, _ = prox(oracle, "topk_cone", X, k=12)  # k = m: all entries equal
+    assert np.allclose(P, np.maximum(X.mean(axis=1, keepdims=True), 0) * np.ones_like(X), atol=1e-12)
+
+
+def bisect(f, lo, hi, it=200):
+    for _ in range(it):
+        mid = 0.5 * (lo + hi)
+        if f(mid) > 0:
+            lo = mid
+        else:
+            hi = mid
+    return 0.5 * (lo + hi)
+
+
+@pytest.mark.parametrize("lo,hi,rhs", [(0.0, 1.0, 1.0), (-0.5, 0.25, 0.7), (0.0, 0.2, 1.0),
+                                       (-1.0, 2.0, -3.0)])
+@pytest.mark.parametrize("m", [1, 5, 10, 50])
+def test_knapsack_eq_bisection(oracle, lo, hi, rhs, m):
+    if hi * m < rhs or lo * m > rhs:
+        pytest.skip("infeasible")
+    X = cases(m, 30 + m)
+    P, thr = prox(oracle, "knapsack_eq", X, result=LD, lo=lo, hi=hi, rhs=rhs)
+    for a, x in zip(X, P):
+        t = bisect(lambda t: np.clip(a - t, lo, hi).sum() - rhs, a.min() - hi - 1, a.max() - lo + 1)
+        want = np.clip(a - t, lo, hi)
+        assert np.allclose(x, want, atol=1e-9 * max(1, np.abs(a).max()))
+        assert abs(x.sum() - rhs) <= 1e-9 * max(1, np.abs(a).sum())
+
+
+def test_simplex_sort_based(oracle):
+    """knapsack_eq with lo=0, hi >= rhs is the Euclidean simplex projection:
+    the sort-based threshold of Held-Wolfe-Crowder / Duchi et al. / Condat."""
+    X = cases(10, 40)
+    P, _ = prox(oracle, "knapsack_eq", X, result=LD, lo=0.0, hi=1.0, rhs=1.0)
+    for a, x in zip(X, P):
+        u = np.sort(a)[::-1]
+        css = np.cumsum(u) - 1.0
+        rho = np.nonzero(u - css / np.arange(1, len(a) + 1) > 0)[0][-1]
+        t = css[rho] / (rho + 1)
+        assert np.allclose(x, np.maximum(a - t, 0), atol=1e-12)
+
+
+@pytest.mark.parametrize("lo,hi,rhs", [(0.0, 0.3, 1.0), (0.0, 1.0, 0.5), (-1.0, 0.5, 0.2)])
+def test_knapsack_le(oracle, lo, hi, rhs):
+    X = cases(20, 50)
+    P, _ = prox(oracle, "knapsack_le", X, result=LD, lo=lo, hi=hi, rhs=rhs)
+    for a, x in zip(X, P):
+        c = np.clip(a, lo, hi)
+        if c.sum() <= rhs:
+            want = c
+        else:
+            t = bisect(lambda t: np.clip(a - t, lo, hi).sum() - rhs, a.min() - hi - 1, a.max() - lo + 1)
+            want = np.clip(a - t, lo, hi)
+        assert np.allclose(x, want, atol=1e-9 * max(1, np.abs(a).max()))
+
+
+@pytest.mark.parametrize("hi,rhs", [(1.0, 1.0), (0.1, 0.5), (0.3, 2.0)])
+@pytest.mark.parametrize("m", [1, 10, 200])
+def test_entropy_exp_map(oracle, hi, rhs, m):
+    if hi * m < rhs:
+        pytest.skip("infeasible")
+    X = inputs.uniform(30, m, np.float64, 60 + m, -10, 10)
+    P, _ = prox(oracle, "entropy", X, hi=hi, rhs=rhs)
+    for a, x in zip(X, P):
+        if hi >= rhs:  # closed form: rhs * softmax(a)
+            want = rhs * scipy.special.softmax(a)
+        else:
+            t = bisect(lambda t: np.minimum(np.exp(a - t), hi).sum() - rhs, a.min() - 50, a.max() + 50)
+            want = np.minimum(np.exp(a - t), hi)
+        assert np.allclose(x, want, atol=1e-12, rtol=1e-10)
+
+
+def w_exp(x):
+    """W(e^x) independently: scipy's principal branch, or x - log x for large x
+    (where e^x overflows) refined by Newton on w + log w = x."""
+    x = np.asarray(x, dtype=np.float64)
+    out = np.empty_like(x)
+    small = x < 700
+    out[small] = scipy.special.lambertw(np.exp(x[small])).real
+    w = x[~small] - np.log(x[~small])
+    for _ in range(5):
+        w = w - (w + np.log(w) - x[~small]) / (1 + 1 / w)
+    out[~small] = w
+    return out
+
+
+@pytest.mark.parametrize("hi,rhs", [(1.0, 1.0), (0.2, 0.9)])
+@pytest.mark.parametrize("m", [1, 10, 100])
+def test_entropy_norm_lambert_map(oracle, hi, rhs, m):
+    if hi * m < rhs:
+        pytest.skip("infeasible")
+    X = inputs.uniform(20, m, np.float64, 70 + m, -10, 10)
+    P, _ = prox(oracle, "entropy_norm", X, hi=hi, rhs=rhs)
+    for a, x in zip(X, P):
+        t = bisect(lambda t: np.minimum(w_exp(a - t), hi).sum() - rhs, a.min() - 60, a.max() + 60)
+        want = np.minimum(w_exp(a - t), hi)
+        assert np.allclose(x, want, atol=1e-10, rtol=1e-9)
+
+
+def test_lambert_known_answer(oracle):
+    """W(e^0) = Omega (test/prox/lambert.cpp:144-157, lambert.h:15-16)."""
+    omega = 0.5671432904097838729999686622103555497538157871865125081351310792230457930866
+    assert oracle.lambert_w_exp(np.array([0.0]))[0] == np.float64(omega)
+    assert oracle.lambert_w_exp(np.array([0.0], dtype=np.float32))[0] == np.float32(omega)
+
+
+def test_lambert_identities_and_scipy(oracle):
+    rng = np.random.default_rng(80)
+    x = np.concatenate([rng.uniform(-50, 50, 20000), np.linspace(-745, 700, 2000),
+                        [-746, -745.9, -36, -20, 0, 4, 2.0**59, 1e300]])
+    w = oracle.lambert_w_exp(x)
+    eps = np.finfo(np.float64).eps
+    pos = x > 0
+    # test/prox/lambert.cpp:5-41: w + log w = x (x > 0), w e^w = e^x (x < 0)
+    assert np.all(np.abs(w[pos] + np.log(w[pos]) - x[pos]) <= 4 * eps * np.maximum(1, x[pos]))
+    neg = (x < 0) & (x > -745)
+    assert np.all(np.abs(w[neg] * np.exp(w[neg]) - np.exp(x[neg])) <= 4 * eps)
+    # Against scipy: the reference's branches stop after a fixed number of
+    # Householder steps; (-36, 0] (one or two steps from exp_approx) is
+    # accurate to ~20 eps relative, the other branches to ~2 eps.
+    mid = np.abs(x) < 700
+    rel = np.abs(w[mid] - w_exp(x[mid])) / w_exp(x[mid])
+    band = (x[mid] > -36) & (x[mid] <= 0)
+    assert rel[band].max() <= 32 * eps
+    assert rel[~band].max() <= 4 * eps
+
+
+def test_lambert_float(oracle):
+    rng = np.random.default_rng(81)
+    x = np.concatenate([rng.uniform(-50, 50, 5000), [-104, -18, -1, 8, 2.0**29]]).astype(np.float32)
+    w = oracle.lambert_w_exp(x).astype(np.float64)
+    want = w_exp(x.astype(np.float64))
+    assert np.allclose(w, want, rtol=8 * np.finfo(np.float32).eps, atol=1e-38)
+
+
+def test_topk_entropy_k1_closed_form(oracle):
+    """k = 1: x = e^a / (1 + sum e^a), t = log(1 + sum e^a) (topk_entropy.h:37-41)."""
+    X = inputs.normal(30, 15, np.float64, 90, 2.0)
+    P, thr = prox(oracle, "topk_entropy", X, k=1)
+    for a, x, th in zip(X, P, thr):
+        z = np.log1p(np.exp(a).sum())
+        assert abs(th[0] - z) <= 1e-12 * max(1, z)
+        assert np.allclose(x, np.exp(a) / (1 + np.exp(a).sum()), rtol=1e-11)
+
+
+def test_topk_entropy_slsqp(oracle):
+    """min <x, log x> + (1 - s) log(1 - s) - <a, x>, s = sum x <= 1, 0 <= x <= s / k."""
+    X = inputs.normal(8, 6, np.float64, 91, 2.0)
+    k = 3
+    P, _ = prox(oracle, "topk_entropy", X, k=k)
+
+    def solve(a):
+        def f(x):
+            s = x.sum()
+            xl = np.where(x > 0, x * np.log(np.maximum(x, 1e-300)), 0.0)
+            return xl.sum() + (1 - s) * np.log(max(1 - s, 1e-300)) - a @ x
+        cons = [{"type": "ineq", "fun": lambda x: 1 - x.sum()},
+                {"type": "ineq", "fun": lambda x: x.sum() / k - x}]
+        r = scipy.optimize.minimize(f, np.full(len(a), 0.5 / len(a)), method="SLSQP",
+                                    bounds=[(0, 1)] * len(a), constraints=cons,
+                                    options={"ftol": 1e-14, "maxiter": 500})
+        return r.x
+
+    for a, x in zip(X, P):
+        assert np.allclose(x, solve(a), atol=2e-5)
+
+
+def test_two_simplex_slsqp(oracle):
+    """Projection of (a, b) onto {x, y >= 0, sum x = sum y <= r}."""
+    rng = np.random.default_rng(92)
+    for trial in range(12):
+        m = int(rng.integers(3, 9))
+        p = int(rng.integers(1, m))
+        r = float(rng.uniform(0.5, 3))
+        a = rng.standard_normal(m) * 2
+        P, _ = prox(oracle, "two_simplex", a, p=p, rhs=r)
+        cons = [{"type": "eq", "fun": lambda z: z[:p].sum() - z[p:].sum()},
+                {"type": "ineq", "fun": lambda z: r - z[:p].sum()}]
+        sol = scipy.optimize.minimize(lambda z: 0.5 * np.sum((z - a) ** 2), np.zeros(m),
+                                      method="SLSQP", bounds=[(0, None)] * m, constraints=cons,
+                                      options={"ftol": 1e-15, "maxiter": 500})
+        assert np.allclose(P[0], sol.x, atol=1e-6), (trial, P[0], sol.x)
+
+
+def test_two_simplex_regression_vector(oracle):
+    """test/prox/two_simplex.cpp:55-64: p = 1, rhs = 2, feasible output."""
+    a = np.array([-0.49371069182389915] + [0.49371069182390021] * 158)
+    P, _ = prox(oracle, "two_simplex", a, p=1, rhs=2.0)
+    x, y = P[0, :1], P[0, 1:]
+    eps = 4 * np.finfo(np.float64).eps * 159
+    assert x.min() >= 0 and y.min() >= 0
+    assert abs(x.sum() - y.sum()) <= 64 * eps and x.sum() <= 2 + 64 * eps
+
+
+# ---------------------------------------------------------------------------
+# Evaluation pass
+# ---------------------------------------------------------------------------
+def test_eval_multiclass_closed_forms(oracle):
+    rng = np.random.default_rng(100)
+    n, m, k, gamma = 300, 40, 5, 0.8
+    S = rng.standard_normal((n, m)) * 2
+    y = rng.integers(0, m, n)
+    A = rng.standard_normal((n, m)) * 0.01
+    objs = [("hinge_topk", 1.0, 1.0, k), ("topk_hinge", 1.0, 1.0, k), ("entropy", 1.0, 1.0, 1),
+            ("hinge_topk_smooth", 1.0, gamma, k)]
+    recs, acc, pe = oracle.eval_scores(objs, S, A, y, result=F64, per_example=True)
+    for i in range(n):
+        s = S[i]
+        h = np.delete(s + 1 - s[y[i]], y[i])
+        top = np.sort(h)[::-1][:k]
+        assert abs(pe[i, 0, 0] - max(0.0, top.sum())) <= 1e-12
+        assert abs(pe[i, 1, 0] - np.maximum(top, 0).sum()) <= 1e-12
+        assert abs(pe[i, 2, 0] - (scipy.special.logsumexp(s) - s[y[i]])) <= 1e-12
+        # smooth: (|h|^2 - |h - P(h)|^2) / 2 with P the top-k simplex projection (rhs = gamma),
+        # P(h) certified by the vertex conditions of test_topk_simplex_optimality
+        p, _ = prox(oracle, "topk_simplex", h, k=k, rhs=gamma)
+        p = p[0]
+        r = h - p
+        assert (gamma / k) * topk_sum(r, k) <= np.dot(r, p) + 1e-10
+        want = 0.5 * (h @ h - r @ r)
+        assert abs(pe[i, 3, 0] - want) <= 1e-10 * max(1, abs(want))
+        # duals: A_y for the hinge losses
+        assert pe[i, 0, 1] == A[i, y[i]]
+    # accuracy: fraction of examples with fewer than j+1 other scores >= s_y
+    cnt = np.array([(np.delete(S[i], y[i]) >= S[i, y[i]]).sum() for i in range(n)])
+    want_acc = np.array([(cnt <= j).mean() for j in range(m)])
+    assert np.allclose(acc, want_acc, atol=1e-15)
+    assert abs(recs[0]["primal_loss"] - pe[:, 0, 0].sum() / k) <= 1e-9
+
+
+def test_eval_multilabel_closed_forms(oracle):
+    rng = np.random.default_rng(101)
+    n, m = 200, 25
+    S = rng.standard_normal((n, m)) * 2
+    off = [0]
+    lab = []
+    for _ in range(n):
+        p = int(rng.integers(1, 6))
+        lab += sorted(rng.choice(m, p, replace=False).tolist())
+        off.append(len(lab))
+    objs = [("multilabel_hinge", 1.0, 1.0, 1), ("multilabel_entropy", 1.0, 1.0, 1)]
+    recs, _, pe = oracle.eval_scores(objs, S, None, lab, off, result=F64, per_example=True)
+    rank = 0.0
+    for i in range(n):
+        P = np.array(lab[off[i]:off[i + 1]])
+        N = np.setdiff1d(np.arange(m), P)
+        s = S[i]
+        assert abs(pe[i, 0, 0] - max(0.0, s[N].max() - s[P].min() + 1)) <= 1e-12
+        assert abs(pe[i, 1, 0] - (scipy.special.logsumexp(s) - s[P].mean())) <= 1e-12
+        rank += (s[N][None, :] >= s[P][:, None]).sum() / (len(P) * len(N))
+    assert abs(recs[0]["rank_loss"] - rank / n) <= 1e-12
