@@ -27,6 +27,7 @@ on the host cores of the GPU box.
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -87,7 +88,45 @@ def parse():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="time a plain device copy of the headline input's size instead "
+                         "(the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def traffic_of(config):
+    """HBM bytes per launch of the config's dominant kernel, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes summarised in profiles/hbm_traffic.md (each
+    counter scaled by what it reads for a plain copy of known size); None when
+    that workload has not been profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"^- (\w+): traffic ([0-9.eE+]+) B per launch", line)
+        if m and m.group(1) == config:
+            return float(m.group(2))
+    return None
+
+
+def copy_calibration(args, torch):
+    """A device-to-device copy of the headline input (n x m fp32), timed like a
+    prox step: the known-size kernel that calibrates the HBM byte counters."""
+    cfg = CONFIGS["c2"]
+    dev = torch.device("cuda:0")
+    x = torch.empty((cfg["n"], cfg["m"]), dtype=torch.float32, device=dev).normal_()
+    out = torch.empty_like(x)
+    for _ in range(args.warmup):
+        out.copy_(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out.copy_(x)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    nbytes = x.numel() * x.element_size()
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                      "ms_per_copy": dt * 1e3, "GB/s": 2 * nbytes / dt / 1e9}))
 
 
 def make_input(cfg, torch, dev):
@@ -123,8 +162,9 @@ def kwargs_of(cfg):
 
 
 def cpu_baseline(cfg, x_sample, col_p_sample, seconds):
-    """Time the reference (or oracle) prox loop single-threaded on a sample."""
-    import numpy as np
+    """Time the reference's (or the oracle's) prox loop single-threaded on a
+    sample of the same input: a first slice sized to ~`seconds` of work, run
+    again until that much time has been measured."""
     from oracle import binding
     lib = binding.reference()
     kind = "reference"
@@ -134,32 +174,30 @@ def cpu_baseline(cfg, x_sample, col_p_sample, seconds):
     op = cfg["op"]
     res = 0 if cfg["result"] == "f32" else 1
     params = binding.make_params(**kwargs_of(cfg))
-    total_cols = 0
-    elapsed = 0.0
-    if op == "lambert_w_exp":
-        unit_count = x_sample.size
     n_avail = x_sample.shape[0]
-    # Calibrate on a small slice, then run ~`seconds` of work.
-    probe = max(1, min(n_avail, 2000 if op != "lambert_w_exp" else 1))
-    work = x_sample[:probe].copy()
-    t0 = time.perf_counter()
-    lib.prox(op, work, result=res, params=params,
-             col_p=None if col_p_sample is None else col_p_sample[:probe])
-    dt_probe = time.perf_counter() - t0
-    if op == "lambert_w_exp":
-        units_per_s = x_sample.size / max(dt_probe, 1e-9)
-        return {"value": units_per_s, "unit": "points/s", "cores": 1, "kind": kind,
-                "sample": f"{x_sample.size} points of the same input, 1 thread"}
-    per_col = dt_probe / probe
+
+    def timed(ncols):
+        work = x_sample[:ncols].copy()
+        cp = None if col_p_sample is None else col_p_sample[:ncols]
+        t0 = time.perf_counter()
+        lib.prox(op, work, result=res, params=params, col_p=cp)
+        return time.perf_counter() - t0
+
+    probe = max(1, min(n_avail, 2000))
+    per_col = timed(probe) / probe
     ncols = int(min(n_avail, max(probe, seconds / max(per_col, 1e-12))))
-    work = x_sample[:ncols].copy()
-    t0 = time.perf_counter()
-    lib.prox(op, work, result=res, params=params,
-             col_p=None if col_p_sample is None else col_p_sample[:ncols])
-    elapsed = time.perf_counter() - t0
-    total_cols = ncols
-    return {"value": total_cols / elapsed, "unit": "columns/s", "cores": 1, "kind": kind,
-            "sample": f"first {total_cols} columns of the same input, 1 thread, {elapsed:.1f} s"}
+    elapsed, passes = 0.0, 0
+    while elapsed < 0.8 * seconds and passes < 200:
+        elapsed += timed(ncols)
+        passes += 1
+    if op == "lambert_w_exp":
+        pts = ncols * x_sample.shape[1] * passes
+        return {"value": pts / elapsed, "unit": "points/s", "cores": 1, "kind": kind,
+                "sample": f"{x_sample.shape[1]} points of the same input x {passes} passes, "
+                          f"1 thread, {elapsed:.1f} s"}
+    return {"value": ncols * passes / elapsed, "unit": "columns/s", "cores": 1, "kind": kind,
+            "sample": f"first {ncols} columns of the same input x {passes} passes, 1 thread, "
+                      f"{elapsed:.1f} s"}
 
 
 def make_eval_input(cfg, torch, dev):
@@ -240,7 +278,8 @@ def bench_eval(cfg, args, torch, sd):
         "config": {"workload": cfg["desc"], "d": cfg["d"], "m": cfg["m"], "n": cfg["n"],
                    "objectives": [o[0] for o in objs]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS,
+                     "traffic": traffic_of(args.config),
                      "note": f"score GEMM 2 n m d = {flops:.3e} flop / mean event-timed launch "
                              f"{gemm_ms:.3f} ms; full pass {ms_per_step:.3f} ms"},
         "eval": extra,
@@ -287,13 +326,16 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the prox columns and evaluation examples shard across GPUs without exchange; "
-              "see DESIGN.md)", file=sys.stderr)
+              "(prox columns and evaluation examples shard across GPUs with no exchange "
+              "other than a final sum of the evaluation records)", file=sys.stderr)
         sys.exit(2)
     import torch
 
     import libsdca_amd as sd
 
+    if args.copy_calibration:
+        copy_calibration(args, torch)
+        return
     cfg = CONFIGS[args.config]
     if cfg["op"] == "eval":
         bench_eval(cfg, args, torch, sd)
@@ -355,7 +397,7 @@ def main():
         "config": {"workload": cfg["desc"], "op": cfg["op"], "m": cfg["m"], "n": cfg["n"],
                    "result": cfg["result"], **kw},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_of(args.config),
                      "note": f"algorithmic {bytes_per_unit} B per unit x {units} units per launch "
                              f"/ mean event-timed launch {avg_ms:.4f} ms"},
     }
@@ -364,7 +406,7 @@ def main():
         if cfg["op"] == "lambert_w_exp":
             sample = x.reshape(-1)[:1_000_000].cpu().numpy().reshape(1, -1)
         else:
-            sample = x[: min(cfg["n"], 2_000_000)].cpu().numpy()
+            sample = x[: min(cfg["n"], 4_000_000)].cpu().numpy()
         cps = None if col_p is None else col_p[: sample.shape[0]].cpu().numpy()
         result["cpu_baseline"] = cpu_baseline(cfg, np.ascontiguousarray(sample), cps,
                                               args.cpu_seconds)

@@ -51,12 +51,12 @@ typedef enum sdca_dtype {
 /* Operators of the Matlab prox front end (mex_prox.cpp:145-172). */
 typedef enum sdca_prox_op {
   SDCA_PROX_KNAPSACK_EQ = 0,   /* knapsack_eq.h:143-157 */
-  SDCA_PROX_KNAPSACK_LE = 1,   /* knapsack_le.h:250-295 */
+  SDCA_PROX_KNAPSACK_LE = 1,   /* knapsack_le.h:78-92 */
   SDCA_PROX_TOPK_SIMPLEX = 2,  /* topk_simplex.h:100-113 */
   SDCA_PROX_TOPK_CONE = 3,     /* topk_cone.h:187-199 */
   SDCA_PROX_ENTROPY = 4,       /* entropy.h:85-98 */
-  SDCA_PROX_ENTROPY_NORM = 5,  /* entropy_norm.h:315-328 */
-  SDCA_PROX_TOPK_ENTROPY = 6,  /* topk_entropy.h:306-318 */
+  SDCA_PROX_ENTROPY_NORM = 5,  /* entropy_norm.h:213-226 */
+  SDCA_PROX_TOPK_ENTROPY = 6,  /* topk_entropy.h:106-118 */
   SDCA_PROX_TWO_SIMPLEX = 7,   /* two_simplex.h:183-196 */
   SDCA_PROX_LAMBERT_W_EXP = 8, /* apply(dim, ..., lambert_w_exp_map), proxdef.h:386-400 */
   /* Operators of the same front end that are not on this path yet:
@@ -126,12 +126,12 @@ typedef struct sdca_objective {
   int64_t k;      /* top-k (top-k objectives) */
 } sdca_objective;
 
-/* One eval record (eval/types.h:219-332) without the timing fields. */
+/* One eval record (eval/types.h:12-20, 84-125) without the timing fields. */
 typedef struct sdca_eval_record {
   double primal, dual;
   double primal_loss, dual_loss;
   double primal_regularizer, dual_regularizer;
-  double rank_loss;   /* multilabel only (eval/types.h:317-332) */
+  double rank_loss;   /* multilabel only (eval/types.h:110-125) */
 } sdca_eval_record;
 
 /*

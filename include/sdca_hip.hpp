@@ -1,0 +1,201 @@
+// sdca_hip.hpp - C++11 drop-in overloads for libsdca's batched prox calls and
+// the feature-input evaluation pass, running on the MI355X through the C ABI
+// of sdca_hip.h.
+//
+// The names, template parameters, argument order and defaults are those of
+// the reference's batched (`dim`) overloads, so a caller switches by
+// replacing `sdca::` with `sdca::hip::`:
+//
+//   sdca::prox_topk_simplex(m, A, A + m * n, aux, k, rhs);        // reference
+//   sdca::hip::prox_topk_simplex(m, A, A + m * n, aux, k, rhs);   // MI355X
+//
+// As in the reference, Result is deduced from the floating parameter (lo,
+// hi, rhs) or defaults to double where there is none (prox_topk_cone,
+// prox_topk_entropy).  Iterators must be float* or double* to contiguous
+// host memory; the batch is staged through device memory and updated in
+// place.  `aux` (the reference's m-element scratch) is accepted and unused.
+// For device-resident data call the C ABI (sdca_prox) directly.  Errors throw
+// sdca::hip::error (the reference asserts instead).
+#ifndef SDCA_HIP_HPP
+#define SDCA_HIP_HPP
+
+#include <cstdint>
+#include <iterator>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+#include "sdca_hip.h"
+
+namespace sdca {
+namespace hip {
+
+class error : public std::runtime_error {
+ public:
+  error(int status, const std::string& what) : std::runtime_error(what), status_(status) {}
+  int status() const { return status_; }
+
+ private:
+  int status_;
+};
+
+namespace detail {
+
+template <typename T> struct dtype;
+template <> struct dtype<float> { static const sdca_dtype value = SDCA_F32; };
+template <> struct dtype<double> { static const sdca_dtype value = SDCA_F64; };
+template <> struct dtype<long double> { static const sdca_dtype value = SDCA_LONG_DOUBLE; };
+
+inline void check(int rc) {
+  if (rc != SDCA_OK) throw error(rc, sdca_last_error());
+}
+
+template <typename Result, typename Data>
+inline void run(sdca_prox_op op, std::ptrdiff_t dim, Data* first, Data* last,
+                const sdca_prox_params& p, const int64_t* col_p = nullptr) {
+  static_assert(std::is_same<Data, float>::value || std::is_same<Data, double>::value,
+                "sdca::hip works on float* or double* ranges");
+  if (dim <= 0) throw error(SDCA_ERR_ARG_RANGE, "dim must be positive");
+  const std::ptrdiff_t total = last - first;
+  if (total % dim != 0) throw error(SDCA_ERR_ARG_RANGE, "range is not a whole number of columns");
+  check(sdca_prox(op, dtype<Data>::value, dtype<Result>::value, dim, total / dim, first, first,
+                  &p, col_p, nullptr, SDCA_HOST_PTR, nullptr));
+}
+
+inline sdca_prox_params params() {
+  sdca_prox_params p;
+  sdca_prox_params_default(&p);
+  return p;
+}
+
+}  // namespace detail
+
+// knapsack_eq.h:143-157
+template <typename Result = double, typename Data>
+inline void prox_knapsack_eq(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                             const Result lo = 0, const Result hi = 1, const Result rhs = 1) {
+  sdca_prox_params p = detail::params();
+  p.lo = static_cast<double>(lo);
+  p.hi = static_cast<double>(hi);
+  p.rhs = static_cast<double>(rhs);
+  detail::run<Result>(SDCA_PROX_KNAPSACK_EQ, dim, first, last, p);
+}
+
+// knapsack_le.h:78-92
+template <typename Result = double, typename Data>
+inline void prox_knapsack_le(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                             const Result lo = 0, const Result hi = 1, const Result rhs = 1) {
+  sdca_prox_params p = detail::params();
+  p.lo = static_cast<double>(lo);
+  p.hi = static_cast<double>(hi);
+  p.rhs = static_cast<double>(rhs);
+  detail::run<Result>(SDCA_PROX_KNAPSACK_LE, dim, first, last, p);
+}
+
+// topk_simplex.h:100-113
+template <typename Result = double, typename Data>
+inline void prox_topk_simplex(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                              const std::ptrdiff_t k = 1, const Result rhs = 1) {
+  sdca_prox_params p = detail::params();
+  p.k = k;
+  p.rhs = static_cast<double>(rhs);
+  detail::run<Result>(SDCA_PROX_TOPK_SIMPLEX, dim, first, last, p);
+}
+
+// topk_cone.h:187-199 (Result is not deducible: double by default)
+template <typename Result = double, typename Data>
+inline void prox_topk_cone(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                           const std::ptrdiff_t k = 1) {
+  sdca_prox_params p = detail::params();
+  p.k = k;
+  detail::run<Result>(SDCA_PROX_TOPK_CONE, dim, first, last, p);
+}
+
+// entropy.h:85-98
+template <typename Result = double, typename Data>
+inline void prox_entropy(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                         const Result hi = 1, const Result rhs = 1) {
+  sdca_prox_params p = detail::params();
+  p.hi = static_cast<double>(hi);
+  p.rhs = static_cast<double>(rhs);
+  detail::run<Result>(SDCA_PROX_ENTROPY, dim, first, last, p);
+}
+
+// entropy_norm.h:213-226
+template <typename Result = double, typename Data>
+inline void prox_entropy_norm(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                              const Result hi = 1, const Result rhs = 1) {
+  sdca_prox_params p = detail::params();
+  p.hi = static_cast<double>(hi);
+  p.rhs = static_cast<double>(rhs);
+  detail::run<Result>(SDCA_PROX_ENTROPY_NORM, dim, first, last, p);
+}
+
+// topk_entropy.h:106-118 (Result is not deducible: double by default)
+template <typename Result = double, typename Data>
+inline void prox_topk_entropy(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                              const std::ptrdiff_t k = 1) {
+  sdca_prox_params p = detail::params();
+  p.k = k;
+  detail::run<Result>(SDCA_PROX_TOPK_ENTROPY, dim, first, last, p);
+}
+
+// two_simplex.h:183-196
+template <typename Result = double, typename Data>
+inline void prox_two_simplex(std::ptrdiff_t dim, std::ptrdiff_t p_split, Data* first, Data* last,
+                             Data* /*aux*/, const Result rhs = 1) {
+  sdca_prox_params p = detail::params();
+  p.p = p_split;
+  p.rhs = static_cast<double>(rhs);
+  detail::run<Result>(SDCA_PROX_TWO_SIMPLEX, dim, first, last, p);
+}
+
+// apply(dim, first, last, lambert_w_exp_map<Data>()) (proxdef.h:386-400)
+template <typename Data>
+inline void apply_lambert_w_exp(std::ptrdiff_t dim, Data* first, Data* last) {
+  detail::run<Data>(SDCA_PROX_LAMBERT_W_EXP, dim, first, last, detail::params());
+}
+
+// One evaluation record (eval/types.h:12-20, 84-125) without the timing fields.
+struct eval_record {
+  double primal, dual, primal_loss, dual_loss, primal_regularizer, dual_regularizer;
+  double rank_loss;            // multilabel
+  std::vector<double> accuracy;  // multiclass: top-(i+1) accuracy after partial_sum / n
+};
+
+// evaluate_dataset (eval.h:15-51) for feature_input: X is d x n and W is
+// d x m, column-major (num_dimensions fastest), labels 0-based; offsets is
+// empty for multiclass and holds the n + 1 CSR offsets for multilabel.
+// A (m x n dual variables) and W0 (prox mode) may be null.
+template <typename Data, typename Result = double>
+inline std::vector<eval_record> evaluate_features(
+    const std::vector<sdca_objective>& objectives, std::int64_t d, std::int64_t m,
+    std::int64_t n, const Data* X, const Data* W, const std::vector<std::int64_t>& labels,
+    const std::vector<std::int64_t>& offsets = std::vector<std::int64_t>(),
+    const Data* A = nullptr, const Data* W0 = nullptr) {
+  std::vector<sdca_eval_record> recs(objectives.size());
+  std::vector<double> acc(static_cast<size_t>(m), 0.0);
+  detail::check(sdca_eval_features(
+      objectives.data(), static_cast<int>(objectives.size()), detail::dtype<Data>::value,
+      detail::dtype<Result>::value, d, m, n, X, W, A, W0, labels.data(),
+      offsets.empty() ? nullptr : offsets.data(), recs.data(),
+      offsets.empty() ? acc.data() : nullptr, nullptr, SDCA_HOST_PTR, nullptr));
+  std::vector<eval_record> out(recs.size());
+  for (size_t i = 0; i < recs.size(); ++i) {
+    out[i].primal = recs[i].primal;
+    out[i].dual = recs[i].dual;
+    out[i].primal_loss = recs[i].primal_loss;
+    out[i].dual_loss = recs[i].dual_loss;
+    out[i].primal_regularizer = recs[i].primal_regularizer;
+    out[i].dual_regularizer = recs[i].dual_regularizer;
+    out[i].rank_loss = recs[i].rank_loss;
+    if (offsets.empty()) out[i].accuracy = acc;
+  }
+  return out;
+}
+
+}  // namespace hip
+}  // namespace sdca
+
+#endif  // SDCA_HIP_HPP

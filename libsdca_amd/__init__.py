@@ -195,7 +195,7 @@ def _rows(dim, A):
 # reference: deduced from the floating parameter's type in C++; here the
 # element type unless `result` is given.  prox_topk_cone / prox_topk_entropy
 # default to double, as their C++ templates do (topk_cone.h:187-199,
-# topk_entropy.h:306-318).
+# topk_entropy.h:106-118).
 def prox_knapsack_eq(dim, A, lo=0.0, hi=1.0, rhs=1.0, result=None):
     return prox("knapsack_eq", _rows(dim, A), lo=lo, hi=hi, rhs=rhs, result=result)
 

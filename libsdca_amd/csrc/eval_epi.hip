@@ -5,7 +5,7 @@
 // Per example the scores row (m contiguous floats) is read straight into C
 // register slots per lane (lane g holds classes g, g+G, ...; coalesced), and
 // each objective restates its reference primal_loss / dual_loss:
-//   multiclass (label y; the reference swaps s_y to the front, eval/primal.h:217-237)
+//   multiclass (label y; the reference swaps s_y to the front, eval/primal.h:27-53)
 //     count      #{j != y : s_j >= s_y}                          (ties count against)
 //     hinge_topk max(0, sum of the k largest h_j), h_j = s_j + (1 - s_y)  (l2_hinge_topk.h:71-86)
 //     topk_hinge sum of the positive h_j among the k largest              (l2_topk_hinge.h:72-87)
@@ -14,7 +14,7 @@
 //                as dot_x_prox / dot_prox_prox do (proxdef.h:332-370)
 //     entropy    lse(s) - s_y                                              (l2_entropy.h:77-91)
 //     entropy_topk  via the top-k entropy thresholds of s_j - s_y          (l2_entropy_topk.h:74-94)
-//   multilabel (positives P, eval/primal.h:246-271)
+//   multilabel (positives P, eval/primal.h:56-87)
 //     rank loss  #{(p, n): s_n >= s_p} / (|P| |N|)
 //     hinge      max(0, max_N s - min_P s + 1)                             (l2_multilabel_hinge.h:69-84)
 //     smooth     two-simplex projection of (1/2 - s_P, 1/2 + s_N)          (l2_multilabel_hinge.h:168-191)
@@ -227,7 +227,7 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
 #pragma unroll
   for (int c = 0; c < C; ++c) s[c] = (c < nvalid) ? srow[g + G * c] : -num<D>::inf();
 
-  // eval_primal_loss: count of j != y with s_j >= s_y (eval/primal.h:228-233)
+  // eval_primal_loss: count of j != y with s_j >= s_y (eval/primal.h:44-49)
   int cnt = 0;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -323,7 +323,7 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
       default:
         break;
     }
-    // Dual losses with the ground truth at position 0 (eval/dual.h:303-319).
+    // Dual losses with the ground truth at position 0 (eval/dual.h:23-44).
     switch (ob.kind) {
       case SDCA_OBJ_HINGE_TOPK_SMOOTH:
       case SDCA_OBJ_TOPK_HINGE_SMOOTH: {  // l2_hinge_topk.h:182-192
@@ -517,7 +517,7 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
 #pragma unroll
     for (int c = 0; c < C; ++c) pos[c] = pos[c] || (g + G * c == lab);
   }
-  // Rank loss (eval/primal.h:259-267): for each positive, the negatives >= it.
+  // Rank loss (eval/primal.h:70-79): for each positive, the negatives >= it.
   R rl = 0;
   for (int q = 0; q < p; ++q) {
     const int lab = static_cast<int>(labels[off0 + q]);

@@ -20,7 +20,7 @@
 // std::accumulate, so thresholds agree to rounding.  Columns whose case needs
 // the reference's full sort (topk_cone_search with |U| > 0, ties at zero,
 // k beyond the register list) are flagged into a list that the
-// workgroup-per-column kernel in prox_slow.hpp finishes.
+// workgroup-per-column kernel in prox_slow.hip finishes.
 #ifndef SDCA_HIP_PROX_IMPL_HPP
 #define SDCA_HIP_PROX_IMPL_HPP
 
@@ -512,7 +512,7 @@ __device__ inline R masked_max(const D (&v)[C], const bool (&mask)[C]) {
   return group_max<G>(mx);
 }
 
-// solve_sum_w_exp (entropy_norm.h:183-236) over the slots in `range`
+// solve_sum_w_exp (entropy_norm.h:110-134) over the slots in `range`
 // (count valid elements, all with values > -inf unless padding).
 template <int G, int C, class D, class R>
 __device__ inline R solve_sum_w_exp_regs(const D (&v)[C], const bool (&range)[C],
@@ -575,7 +575,7 @@ __device__ inline R solve_sum_w_exp_regs(const D (&v)[C], const bool (&range)[C]
 
 // ---------------------------------------------------------------------------
 // Entropic family: entropy (entropy.h:19-53) and entropy_norm
-// (entropy_norm.h:246-283).  Elements fixed at hi are {x > hi_cut}.
+// (entropy_norm.h:146-181).  Elements fixed at hi are {x > hi_cut}.
 // ---------------------------------------------------------------------------
 template <int G, int C, class D, class R>
 __device__ inline ColThr<R> ent_family(const D (&v)[C], int m, int nvalid,

@@ -384,7 +384,7 @@ inline R sum_w_exp_step4(It first, It last, R rhs, R t) {  // entropy_norm.h:161
 }
 
 template <class R, class It>
-inline R solve_sum_w_exp(It first, It last, R rhs) {  // entropy_norm.h:183-236
+inline R solve_sum_w_exp(It first, It last, R rhs) {  // entropy_norm.h:110-134
   R t = (std::accumulate(first, last, static_cast<R>(0)) - rhs)
         / static_cast<R>(std::distance(first, last));
   It u_last = last;

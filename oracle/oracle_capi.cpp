@@ -116,14 +116,14 @@ void eval_range(const std::vector<orc::objective<D, R>>& objs, int64_t m,
     else std::fill(v.begin(), v.end(), static_cast<D>(0));
     if (!offsets) {
       const int64_t y = labels[i];
-      // eval_dual_loss: move_front, dual_loss, move_back (eval/dual.h:303-319)
+      // eval_dual_loss: move_front, dual_loss, move_back (eval/dual.h:23-44)
       std::swap(v[0], v[y]);
       for (size_t o = 0; o < no; ++o) {
         R dl = objs[o].dual_loss(m, v.data());
         dual[o] += dl;
         if (per_example) per_example[(i * no + o) * 2 + 1] = static_cast<double>(dl);
       }
-      // eval_primal_loss (eval/primal.h:217-237)
+      // eval_primal_loss (eval/primal.h:27-53)
       std::swap(s[0], s[y]);
       D* it = std::partition(s.data() + 1, s.data() + m,
                              [&](const D& x) { return x >= s[0]; });
@@ -144,7 +144,7 @@ void eval_range(const std::vector<orc::objective<D, R>>& objs, int64_t m,
         dual[o] += dl;
         if (per_example) per_example[(i * no + o) * 2 + 1] = static_cast<double>(dl);
       }
-      // eval_primal_loss multilabel (eval/primal.h:246-271)
+      // eval_primal_loss multilabel (eval/primal.h:56-87)
       orc::ml_move_front(lab, p, s.data());
       D* neg_first = s.data() + p;
       D* neg_last = s.data() + m;
@@ -208,7 +208,7 @@ int eval_scores_impl(const sdca_objective* objs_in, int n_obj, int64_t m,
   return 0;
 }
 
-// Regularizers for feature input (eval/regularizer.h:364-386,
+// Regularizers for feature input (eval/regularizer.h:22-44,
 // objective_base.h:59-89), with the dot in the Data type.
 template <class D, class R>
 void regularizers(int64_t dm, const D* W, const D* W0, double& preg, double& dreg) {

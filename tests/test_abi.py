@@ -91,3 +91,50 @@ def test_eval_argument_checks():
         sd.eval_features([sd.objective("l2_multilabel_entropy")], X, W, [2, 1, 0, 1, 2, 3],
                          offsets=[0, 2, 3, 4, 6])
     assert e.value.status == 8
+
+
+HPP_PROGRAM = r"""
+#include "sdca_hip.hpp"
+#include <vector>
+int main() {
+  std::vector<float> a(100 * 8, 0.f), aux(100);
+  std::vector<double> b(10 * 4, 0.0), bux(10);
+  float* f = a.data();
+  double* d = b.data();
+  // the reference's batched call shapes (topk_simplex.h, topk_cone.h, ...)
+  sdca::hip::prox_topk_simplex(100, f, f + a.size(), aux.data(), 5, 1.0f);
+  sdca::hip::prox_topk_cone(100, f, f + a.size(), aux.data(), 5);
+  sdca::hip::prox_knapsack_eq(10, d, d + b.size(), bux.data(), 0.0, 1.0, 1.0);
+  sdca::hip::prox_knapsack_le(10, d, d + b.size(), bux.data(), 0.0, 1.0, 1.0);
+  sdca::hip::prox_entropy(10, d, d + b.size(), bux.data(), 1.0, 1.0);
+  sdca::hip::prox_entropy_norm(10, d, d + b.size(), bux.data(), 1.0, 1.0);
+  sdca::hip::prox_topk_entropy(10, d, d + b.size(), bux.data(), 2);
+  sdca::hip::prox_two_simplex(10, 3, d, d + b.size(), bux.data(), 1.0);
+  sdca::hip::apply_lambert_w_exp(10, d, d + b.size());
+  std::vector<sdca_objective> objs(1);
+  objs[0].kind = SDCA_OBJ_ENTROPY; objs[0].c = 1; objs[0].gamma = 1; objs[0].k = 1;
+  std::vector<int64_t> y(4, 0);
+  std::vector<float> X(3 * 4), W(3 * 5);
+  std::vector<sdca::hip::eval_record> r =
+      sdca::hip::evaluate_features<float>(objs, 3, 5, 4, X.data(), W.data(), y);
+  return r.empty();
+}
+"""
+
+
+def test_cpp_header_compiles_and_links(tmp_path):
+    """include/sdca_hip.hpp is plain C++11 and links against the C ABI library."""
+    import shutil
+    import subprocess
+    import libsdca_amd as sd
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not found")
+    src = tmp_path / "use_hpp.cpp"
+    src.write_text(HPP_PROGRAM)
+    libdir = os.path.dirname(sd.LIB_PATH)
+    cmd = [gxx, "-std=c++11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src),
+           "-o", str(tmp_path / "use_hpp"), "-L", libdir, "-l:" + os.path.basename(sd.LIB_PATH),
+           "-Wl,--allow-shlib-undefined"]
+    out = subprocess.run(cmd, capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr

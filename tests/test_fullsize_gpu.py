@@ -1,0 +1,278 @@
+"""Parity at the full sizes of the benchmark workloads.
+
+Each test builds the bench's own seeded input (bench.make_input /
+bench.make_eval_input, so the tested workload is the timed one), runs the HIP
+path once through the C ABI, and checks
+
+  * every column against the CPU oracle, in chunks, with the error-aware
+    criterion of test_prox_gpu.parity (rtol 1e-5 for fp32, 1e-12 for fp64,
+    plus the reference's own rounding error E), where the oracle finishes in
+    seconds; a seeded sample of columns where it does not (the Lambert-map
+    entropic projection);
+  * size-independent properties on every column, computed independently on
+    the GPU in float64: feasibility of the projection (bounds, sums), the
+    optimality certificate of the top-k cone/simplex projections, the softmax
+    closed form of the entropic projection (hi >= rhs), idempotence;
+  * for the evaluation pass, the top-k accuracy counts recomputed exactly from
+    the GPU's own scores, the rank loss recomputed from them, and the
+    per-example losses of a sample against the oracle on the same scores.
+"""
+import numpy as np
+import pytest
+
+from tests.test_eval_gpu import LONG_DOUBLE, compare_per_example, oracle_objs
+from tests.test_prox_gpu import parity
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = 0, 1
+CHUNK = 250_000
+
+
+def bench_input(name, cuda):
+    import torch
+    import bench
+    cfg = bench.CONFIGS[name]
+    x, col_p = bench.make_input(cfg, torch, cuda)
+    return cfg, x, col_p
+
+
+def run(cfg, x, col_p=None):
+    import torch
+    import bench
+    import libsdca_amd as sd
+    out = torch.empty_like(x)
+    res = "float" if cfg["result"] == "f32" else "double"
+    sd.prox(cfg["op"], x, out=out, result=res, col_p=col_p, **bench.kwargs_of(cfg))
+    torch.cuda.synchronize()
+    return out
+
+
+def chunked_parity(oracle, cfg, x, out, col_p=None, stride=1):
+    """Every `stride`-th chunk of CHUNK columns against the oracle."""
+    import bench
+    res = F32 if cfg["result"] == "f32" else F64
+    kw = bench.kwargs_of(cfg)
+    n = x.shape[0]
+    starts = list(range(0, n, CHUNK))[::stride]
+    for b in starts:
+        e = min(n, b + CHUNK)
+        xs = x[b:e].cpu().numpy()
+        got = out[b:e].cpu().numpy()
+        ckw = dict(kw)
+        if col_p is not None:
+            ckw["col_p"] = col_p[b:e].cpu().numpy()
+        parity(oracle, cfg["op"], xs, got, res, f"{cfg['op']} columns {b}:{e}", **ckw)
+    return len(starts)
+
+
+def scale_of(x64):
+    return x64.abs().amax(dim=1).clamp_min(1.0)
+
+
+def test_c2_topk_simplex_full(cuda, oracle):
+    """m=100, k=5, rhs=1, fp32, n=4,000,000: every column."""
+    import torch
+    cfg, x, _ = bench_input("c2", cuda)
+    out = run(cfg, x)
+    k, rhs, rtol = cfg["k"], cfg["rhs"], 1e-5
+    for b in range(0, x.shape[0], 1_000_000):
+        a = x[b:b + 1_000_000].double()
+        p = out[b:b + 1_000_000].double()
+        s = scale_of(a)
+        tot = p.sum(dim=1)
+        assert (p >= 0).all()
+        assert (tot <= rhs + rtol * s).all()
+        assert (p <= (tot / k)[:, None] + rtol * s[:, None]).all()
+        # Optimality: <r, y - p> <= 0 over the vertices y of the top-k simplex,
+        # 0 and (rhs/j) 1_S with |S| = j >= k, whose maximum is
+        # max(0, (rhs/k) * sum of the k largest r).
+        r = a - p
+        lhs = torch.clamp((rhs / k) * r.topk(k, dim=1).values.sum(dim=1), min=0)
+        rp = (r * p).sum(dim=1)
+        cert_tol = 64 * 100 * 1.2e-7 * s * s
+        assert (lhs <= rp + cert_tol).all(), f"certificate fails: {(lhs - rp - cert_tol).max()}"
+    chunked_parity(oracle, cfg, x, out)
+
+
+def test_c2_topk_simplex_idempotent(cuda):
+    """The projection of a projected batch is itself (to fp32 rounding)."""
+    import torch
+    cfg, x, _ = bench_input("c2", cuda)
+    p = run(cfg, x)
+    q = run(cfg, p)
+    err = (q.double() - p.double()).abs().amax()
+    assert err <= 1e-6, f"max |P(P(a)) - P(a)| = {err}"
+
+
+def test_c2_topk_cone_full(cuda, oracle):
+    """Top-k cone on the headline input, every column."""
+    import torch
+    cfg, x, _ = bench_input("c2cone", cuda)
+    out = run(cfg, x)
+    k, rtol = cfg["k"], 1e-5
+    for b in range(0, x.shape[0], 1_000_000):
+        a = x[b:b + 1_000_000].double()
+        p = out[b:b + 1_000_000].double()
+        s = scale_of(a)
+        tot = p.sum(dim=1)
+        assert (p >= 0).all()
+        assert (p <= (tot / k)[:, None] + rtol * s[:, None]).all()
+        # The cone's extreme rays are 1_S / |S| with |S| >= k, and p is the
+        # projection iff <r, p> = 0 and the k largest r sum to <= 0.
+        r = a - p
+        cert_tol = 64 * 100 * 1.2e-7 * s * s
+        assert (r.topk(k, dim=1).values.sum(dim=1) <= cert_tol).all()
+        assert ((r * p).sum(dim=1).abs() <= cert_tol).all()
+    chunked_parity(oracle, cfg, x, out)
+
+
+def test_c1_knapsack_eq_full(cuda, oracle):
+    """Simplex projection m=10, n=100,000, fp64: every column, plus sum = 1."""
+    cfg, x, _ = bench_input("c1", cuda)
+    out = run(cfg, x)
+    tot = out.sum(dim=1)
+    assert ((tot - 1).abs() <= 1e-12 * 10).all()
+    assert ((out >= 0) & (out <= 1)).all()
+    chunked_parity(oracle, cfg, x, out)
+
+
+@pytest.mark.timeout(300)
+def test_c3_entropy_full(cuda, oracle):
+    """Entropic projection m=1000, n=200,000, fp64, hi = rhs = 1: the exact
+    solution is softmax(a) on every column; the oracle on one chunk."""
+    import torch
+    cfg, x, _ = bench_input("c3", cuda)
+    out = run(cfg, x)
+    want = torch.softmax(x, dim=1)
+    err = (out - want).abs().amax()
+    assert err <= 1e-12, f"max |x - softmax(a)| = {err}"
+    chunked_parity(oracle, cfg, x, out, stride=100)
+
+
+@pytest.mark.timeout(300)
+def test_c3_entropy_norm_full(cuda, oracle):
+    """Lambert-map entropic projection m=1000, n=200,000, fp64: feasibility on
+    every column, the oracle on a seeded sample of 5,000 columns."""
+    import torch
+    cfg, x, _ = bench_input("c3norm", cuda)
+    out = run(cfg, x)
+    tot = out.sum(dim=1)
+    assert ((tot - cfg["rhs"]).abs() <= 1e-12 * 1000).all()
+    assert ((out >= 0) & (out <= cfg["hi"])).all()
+    idx = torch.from_numpy(np.sort(np.random.default_rng(7).choice(x.shape[0], 5000, replace=False))).to(cuda)
+    xs = x.index_select(0, idx).cpu().numpy()
+    got = out.index_select(0, idx).cpu().numpy()
+    parity(oracle, "entropy_norm", xs, got, F64, "entropy_norm sample", hi=cfg["hi"], rhs=cfg["rhs"])
+
+
+def test_lambert_full(cuda, oracle):
+    """W(exp(x)) on 10,000,000 points x ~ U(-50, 50), fp64: every point."""
+    cfg, x, _ = bench_input("lambert", cuda)
+    out = run(cfg, x)
+    xs = x.cpu().numpy()
+    got = out.cpu().numpy()
+    want = oracle.lambert_w_exp(xs.copy())
+    rel = np.abs(got - want) / np.maximum(1.0, np.abs(want))
+    assert rel.max() <= 1e-12, f"max rel err {rel.max():.3e} at x = {xs.reshape(-1)[rel.argmax()]}"
+
+
+def test_c5_two_simplex_full(cuda, oracle):
+    """Multilabel dual prox: two-block simplex m=200, n=500,000, fp32,
+    per-column split p in [1, 5]: every column, plus sum(x_P) = sum(x_N) <= 1."""
+    import torch
+    cfg, x, col_p = bench_input("c5prox", cuda)
+    out = run(cfg, x, col_p)
+    o = out.double()
+    ar = torch.arange(x.shape[1], device=cuda)[None, :]
+    pos = ar < col_p[:, None]
+    sp = torch.where(pos, o, 0).sum(dim=1)
+    sn = torch.where(pos, 0, o).sum(dim=1)
+    s = scale_of(x.double())
+    assert (out >= 0).all()
+    assert ((sp - sn).abs() <= 1e-5 * s).all()
+    assert (sp <= cfg["rhs"] + 1e-5 * s).all()
+    chunked_parity(oracle, cfg, x, out, col_p)
+
+
+@pytest.mark.timeout(300)
+def test_c4_eval_full(cuda, oracle):
+    """Evaluation pass d=4096, m=1000, n=100,000 (smooth top-5 hinge, softmax
+    cross-entropy): accuracy counts exact on every example from the GPU's own
+    scores, per-example losses of 5,000 examples against the oracle."""
+    import torch
+    import bench
+    import libsdca_amd as sd
+    cfg = bench.CONFIGS["c4"]
+    X, W, labels, _ = bench.make_eval_input(cfg, torch, cuda)
+    objs = cfg["objs"]
+    recs, acc, pe = sd.eval_features(objs, X, W, labels, per_example=True)
+    S = sd.scores(X, W)
+    torch.cuda.synchronize()
+    n, m = S.shape
+    sy = S.gather(1, labels[:, None])
+    cnt = (S >= sy).sum(dim=1) - 1  # other classes scoring >= the label (ties count against)
+    hist = torch.bincount(cnt, minlength=m).double()
+    want_acc = (hist.cumsum(0) / n).cpu().numpy()
+    assert np.array_equal(acc, want_acc) or np.abs(acc - want_acc).max() <= 1e-15
+    idx = np.sort(np.random.default_rng(11).choice(n, 5000, replace=False))
+    it = torch.from_numpy(idx).to(cuda)
+    Ss = S.index_select(0, it).cpu().numpy()
+    ys = labels.index_select(0, it).cpu().numpy()
+    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, ys, result=F32, per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, ys, result=LONG_DOUBLE,
+                                    per_example=True)
+    got = pe.index_select(0, it).cpu().numpy()
+    compare_per_example(got[:, :, 0], o_pe[:, :, 0], 1e-5, "c4 primal", exact=x_pe[:, :, 0])
+    compare_per_example(got[:, :, 1], o_pe[:, :, 1], 1e-5, "c4 dual", exact=x_pe[:, :, 1])
+    # eval_end: primal_loss = coeff * sum (objective_base.h:116-128)
+    tot = pe.sum(dim=0).cpu().numpy()
+    coeff = [c / g for (_, c, g, _) in objs[:1]] + [objs[1][1]]
+    for o in range(len(objs)):
+        assert abs(recs[o]["primal_loss"] - coeff[o] * tot[o, 0]) <= 1e-9 * max(1, abs(recs[o]["primal_loss"]))
+
+
+@pytest.mark.timeout(300)
+def test_c5_eval_full(cuda, oracle):
+    """Multilabel evaluation d=1024, m=200, n=500,000: rank loss recomputed on
+    every example from the GPU's own scores, per-example losses of 5,000
+    examples against the oracle."""
+    import torch
+    import bench
+    import libsdca_amd as sd
+    cfg = bench.CONFIGS["c5eval"]
+    X, W, labels, offsets = bench.make_eval_input(cfg, torch, cuda)
+    objs = cfg["objs"]
+    recs, _, pe = sd.eval_features(objs, X, W, labels, offsets=offsets, per_example=True)
+    S = sd.scores(X, W)
+    torch.cuda.synchronize()
+    n, m = S.shape
+    npos = offsets[1:] - offsets[:-1]
+    row = torch.repeat_interleave(torch.arange(n, device=cuda), npos)
+    posmask = torch.zeros((n, m), dtype=torch.bool, device=cuda)
+    posmask[row, labels] = True
+    slot = torch.arange(labels.numel(), device=cuda) - offsets[:-1][row]
+    lab5 = torch.zeros((n, 5), dtype=torch.int64, device=cuda)
+    lab5[row, slot] = labels
+    rank = torch.zeros(n, dtype=torch.float64, device=cuda)
+    for j in range(5):
+        valid = j < npos
+        sp = S.gather(1, lab5[:, j:j + 1])
+        c = ((S >= sp) & ~posmask).sum(dim=1).double()
+        rank += torch.where(valid, c, 0.0)
+    rank /= (npos * (m - npos)).double()
+    want = float(rank.sum()) / n
+    for r in recs:
+        assert abs(r["rank_loss"] - want) <= 1e-12 * max(1.0, want), (r["rank_loss"], want)
+    idx = np.sort(np.random.default_rng(12).choice(n, 5000, replace=False))
+    off = offsets.cpu().numpy()
+    lab = labels.cpu().numpy()
+    Ss = S.index_select(0, torch.from_numpy(idx).to(cuda)).cpu().numpy()
+    sl = [lab[off[i]:off[i + 1]] for i in idx]
+    so = np.concatenate([[0], np.cumsum([len(v) for v in sl])]).astype(np.int64)
+    sl = np.concatenate(sl).astype(np.int64)
+    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, sl, so, result=F32, per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, sl, so, result=LONG_DOUBLE,
+                                    per_example=True)
+    got = pe.index_select(0, torch.from_numpy(idx).to(cuda)).cpu().numpy()
+    compare_per_example(got[:, :, 0], o_pe[:, :, 0], 1e-5, "c5 primal", exact=x_pe[:, :, 0])

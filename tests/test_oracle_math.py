@@ -337,3 +337,37 @@ def test_eval_multilabel_closed_forms(oracle):
         assert abs(pe[i, 1, 0] - (scipy.special.logsumexp(s) - s[P].mean())) <= 1e-12
         rank += (s[N][None, :] >= s[P][:, None]).sum() / (len(P) * len(N))
     assert abs(recs[0]["rank_loss"] - rank / n) <= 1e-12
+
+
+def test_eval_smooth_dual_losses(oracle):
+    """The three dual losses whose reference code calls CBLAS (so the
+    reference shim cannot evaluate them here): A_0 - gamma/(2c) sum_{j>=1} A_j^2
+    for both smooth multiclass hinges (l2_hinge_topk.h:182-192,
+    l2_topk_hinge.h:186-196) and (sum_P A - sum_N A - (gamma/c) |A|^2) / 2 for
+    the smooth multilabel hinge (l2_multilabel_hinge.h:194-208), with the
+    ground truth / positives moved to the front first (data/output.h:42-71,
+    120-165)."""
+    rng = np.random.default_rng(102)
+    n, m, c, gamma = 150, 30, 1.7, 0.6
+    S = rng.standard_normal((n, m))
+    A = rng.standard_normal((n, m)) * 0.1
+    y = rng.integers(0, m, n)
+    objs = [("hinge_topk_smooth", c, gamma, 3), ("topk_hinge_smooth", c, gamma, 3)]
+    _, _, pe = oracle.eval_scores(objs, S, A, y, result=F64, per_example=True)
+    for i in range(n):
+        rest = np.delete(A[i], y[i])
+        want = A[i, y[i]] - gamma / (2 * c) * (rest @ rest)
+        assert abs(pe[i, 0, 1] - want) <= 1e-13 and abs(pe[i, 1, 1] - want) <= 1e-13
+    off, lab = [0], []
+    for _ in range(n):
+        p = int(rng.integers(1, 6))
+        lab += sorted(rng.choice(m, p, replace=False).tolist())
+        off.append(len(lab))
+    _, _, pe = oracle.eval_scores([("multilabel_hinge_smooth", c, gamma, 1)], S, A, lab, off,
+                                  result=F64, per_example=True)
+    for i in range(n):
+        P = np.array(lab[off[i]:off[i + 1]])
+        mask = np.zeros(m, bool)
+        mask[P] = True
+        want = 0.5 * (A[i, mask].sum() - A[i, ~mask].sum() - gamma / c * (A[i] @ A[i]))
+        assert abs(pe[i, 0, 1] - want) <= 1e-13
