@@ -43,6 +43,16 @@ __device__ inline D clamp_ref(D x, D lo, D hi) {
   return (lo < y) ? y : lo;
 }
 
+// clamp_ref for lo <= hi' with hi' = max(lo, hi) precomputed per column (then
+// clamp_ref(x, lo, hi) == clamp_med3(x, lo, hi') for every x that is not NaN,
+// including lo > hi, where both give lo): one v_med3_f32 for float.
+__device__ inline float clamp_med3(float x, float lo, float hi_eff) {
+  return __builtin_amdgcn_fmed3f(x, lo, hi_eff);
+}
+__device__ inline double clamp_med3(double x, double lo, double hi_eff) {
+  return clamp_ref(x, lo, hi_eff);
+}
+
 // x log x with 0 log 0 = 0 (math/log_exp.h:76-80).
 template <class T>
 __device__ inline T x_log_x(T x) { return (x > 0) ? x * dlog(x) : T(0); }
@@ -201,14 +211,23 @@ __device__ inline int group_exclusive_scan(int x, int g) {
 // Sorted (descending) top list of L values, insertion of one value:
 // new[i] = max(old[i], min(old[i-1], x)) = median(old[i-1], old[i], x), one
 // v_med3_f32 per level for float.
+// +inf in a register the compiler cannot see through: a median with it is
+// max(), issued as v_med3_f32 instead of a v_max_f32 that needs its inputs
+// canonicalised first (one extra instruction per loaded value).
+__device__ inline float opaque_inf() {
+  float x = __builtin_inff();
+  asm("" : "+v"(x));
+  return x;
+}
+
 template <int L>
-__device__ inline void top_insert(float (&top)[L], float x) {
+__device__ inline void top_insert(float (&top)[L], float x, float pinf = opaque_inf()) {
 #pragma unroll
   for (int i = L - 1; i >= 1; --i) top[i] = __builtin_amdgcn_fmed3f(top[i - 1], top[i], x);
-  top[0] = fmaxf(top[0], x);
+  top[0] = __builtin_amdgcn_fmed3f(top[0], x, pinf);
 }
 template <int L>
-__device__ inline void top_insert(double (&top)[L], double x) {
+__device__ inline void top_insert(double (&top)[L], double x, double = 0) {
 #pragma unroll
   for (int i = L - 1; i >= 1; --i) {
     double lo = (top[i - 1] < x) ? top[i - 1] : x;

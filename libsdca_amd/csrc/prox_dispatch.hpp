@@ -24,10 +24,19 @@ hipError_t launch_one(const ProxLaunch& a) {
   const int64_t blocks = (a.n + B - 1) / B;
   // B*m tile, G*C words of slack for branch-free slot reads, BT dummy words.
   const size_t shmem = (static_cast<size_t>(B) * static_cast<size_t>(a.m) + G * C + BT) * sizeof(D);
-  hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT>),
-                     dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
-                     static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp, a.col_p,
-                     a.thr, a.slow);
+  // m == G * C (the configuration's exact size) gets the variant without
+  // per-slot validity tests.
+  if (a.m == static_cast<int64_t>(G) * C) {
+    hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, true>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
+                       static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
+                       a.col_p, a.thr, a.slow);
+  } else {
+    hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, false>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
+                       static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
+                       a.col_p, a.thr, a.slow);
+  }
   return hipGetLastError();
 }
 

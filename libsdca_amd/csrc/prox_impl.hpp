@@ -153,64 +153,6 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
   return st;
 }
 
-// The same variable fixing over a short list b[0, cnt) held in LDS, run by
-// every lane of the group on identical data (no divergence, no broadcast).
-template <class D, class R>
-__device__ inline KnapState<R> knapsack_list(const D* b, int cnt, R lo, R hi, R rhs) {
-  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
-  R total = 0;
-  for (int i = 0; i < cnt; ++i) total += static_cast<R>(b[i]);
-  int mc = cnt;
-  R t = (total - rhs) / static_cast<R>(cnt);
-  KnapState<R> st;
-  st.lo_cut = -num<R>::inf();
-  st.hi_cut = num<R>::inf();
-  st.c_lo = -num<R>::inf();
-  st.c_hi = num<R>::inf();
-  st.n_u = 0;
-  st.sum_u = 0;
-  for (int iter = 0; iter <= cnt; ++iter) {
-    const R c_lo = lo + t, c_hi = hi + t;
-    R s_lo = 0, s_hi = 0;
-    int n_lo = 0, n_hi = 0;
-    for (int i = 0; i < cnt; ++i) {
-      const R x = static_cast<R>(b[i]);
-      const bool fr = (x > st.lo_cut) && !(x > st.hi_cut);
-      const bool gl = x > c_lo;
-      if (fr && !gl) { s_lo += x; ++n_lo; }
-      if (fr && gl && x > c_hi) { s_hi += x; ++n_hi; }
-    }
-    const R sh = static_cast<R>(n_hi) * hi;
-    const R sl = static_cast<R>(n_lo) * lo;
-    const R infeas = s_hi + s_lo - (sh + sl) - static_cast<R>(n_hi + n_lo) * t;
-    R next;
-    if (n_hi > 0 && infeas > eps) {
-      st.hi_cut = dmin(st.hi_cut, dmax(c_lo, c_hi));
-      next = static_cast<R>(mc) * t - s_hi + sh;
-      mc -= n_hi;
-      st.n_u += n_hi;
-      st.sum_u += s_hi;
-    } else if (n_lo > 0 && infeas < -eps) {
-      st.lo_cut = dmax(st.lo_cut, c_lo);
-      next = static_cast<R>(mc) * t - s_lo + sl;
-      mc -= n_lo;
-    } else {
-      st.c_lo = c_lo;
-      st.c_hi = c_hi;
-      st.n_u += n_hi;
-      st.sum_u += s_hi;
-      break;
-    }
-    if (mc > 0) {
-      t = next / static_cast<R>(mc);
-    } else {
-      break;
-    }
-  }
-  st.t = t;
-  return st;
-}
-
 // Make LDS writes of this wave visible to its own later reads.
 __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -378,18 +320,22 @@ __device__ inline KnapState<R> knapsack_top(const D (&b)[L], int cnt, R lo, R hi
   return st;
 }
 
-// Columns with more candidates than this run the variable fixing over all
-// register slots instead of the compacted list.
-constexpr int kCandMax = 64;
+// Candidate slots per lane for the top-k simplex's knapsack: the group holds
+// up to G * kCandSlots<G> candidates in registers; columns with more run the
+// variable fixing over all register slots instead.
+template <int G>
+constexpr int kCandSlots = (G <= 4) ? 4 : (G <= 16) ? 2 : 1;
 
 // Variable fixing for the top-k simplex's knapsack (lo = 0, hi = rhs / k):
 // its root t* satisfies sum_i clamp(a_i - t*, 0, hi) = k hi, hence
 // a_(k) - hi <= t* < a_(k) (the k largest each give hi at t = a_(k) - hi;
 // fewer than k can be positive at t = a_(k)).  Elements at or below a_(k) - hi
 // end at the lower bound whatever the iteration does, so the fixing runs over
-// the few values above that cut, compacted into the column's LDS slots; the
-// cut is widened by a few ulps so that rounding of hi = rhs / k cannot drop a
-// contributor.
+// the few values above that cut only.  The candidates are compacted through
+// the column's LDS slots into kCandSlots registers per lane (candidate i to
+// lane i % G), and the register variable fixing runs on them with group sums.
+// The cut is widened by a few ulps so that rounding of hi = rhs / k cannot
+// drop a contributor.
 template <int G, int C, int L, class D, class R>
 __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L], int m,
                                              int nvalid, R kth, R hi, R rhs, D* lds_col,
@@ -405,13 +351,14 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
     for (int i = 0; i < L; ++i) cnt += (static_cast<R>(top[i]) > cut) ? 1 : 0;
     return knapsack_top<L, D, R>(top, cnt, R(0), hi, rhs);
   }
-  if (lds_col != nullptr) {
+  if constexpr (G > 1) {
+    constexpr int CC = kCandSlots<G>;
     int cn = 0;
 #pragma unroll
     for (int c = 0; c < C; ++c) cn += (static_cast<R>(v[c]) > cut) ? 1 : 0;
     const int g = static_cast<int>(threadIdx.x) % G;
     const int total = group_sum<G>(cn);
-    if (total <= kCandMax) {
+    if (total <= G * CC) {
       // Branch-free compaction: every slot is stored, non-candidates to the
       // lane's own dummy word (distinct per lane, so no bank serialisation).
       int pos = group_exclusive_scan<G>(cn, g);
@@ -423,7 +370,19 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
         pos += pr ? 1 : 0;
       }
       wave_lds_sync();
-      return knapsack_list<D, R>(lds_col, total, R(0), hi, rhs);
+      // Candidate i sits at lds_col[i]; lane g takes i = g, g + G, ...  The
+      // reads stay inside the tile (G * CC <= G * C words of slack follow it).
+      D cand[CC];
+      R csum = 0;
+#pragma unroll
+      for (int c = 0; c < CC; ++c) {
+        const D x = lds_col[g + G * c];
+        const bool ok = g + G * c < total;
+        cand[c] = ok ? x : -num<D>::inf();
+        csum += ok ? static_cast<R>(x) : R(0);
+      }
+      csum = group_sum<G>(csum);
+      return knapsack_eq_regs<G, CC, D, R>(cand, total, total, csum, R(0), hi, rhs);
     }
   }
   const R all = total_sum<G, C, D, R>(v, nvalid);
@@ -832,7 +791,9 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // for this configuration), so the whole tile is in flight at once.  Blocks
 // are one wave, so a tile is a few KiB: HBM streams best when many small
 // blocks each touch a short contiguous range (a 32 KiB-per-block copy runs
-// ~30% slower than a 4 KiB one on MI355X).
+// ~30% slower than a 4 KiB one on MI355X).  Lanes past the tile's last
+// 16-byte word repeat that word (same address, same value), so the copy has
+// no per-load branch.
 template <int NV, int BT, class D>
 __device__ inline void tile_load(D* __restrict__ dst, const D* __restrict__ src, int64_t count) {
   const int64_t bytes = count * static_cast<int64_t>(sizeof(D));
@@ -841,19 +802,19 @@ __device__ inline void tile_load(D* __restrict__ dst, const D* __restrict__ src,
     tile_copy<BT>(dst, src, count);
     return;
   }
-  const int nv = static_cast<int>(bytes / 16);
+  const int last = static_cast<int>(bytes / 16) - 1;
   const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
   u32x4* d4 = reinterpret_cast<u32x4*>(dst);
   u32x4 r[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = i * BT + static_cast<int>(threadIdx.x);
-    if (idx < nv) r[i] = __builtin_nontemporal_load(s4 + idx);
+    const int idx = min(i * BT + static_cast<int>(threadIdx.x), last);
+    r[i] = __builtin_nontemporal_load(s4 + idx);
   }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = i * BT + static_cast<int>(threadIdx.x);
-    if (idx < nv) d4[idx] = r[i];
+    const int idx = min(i * BT + static_cast<int>(threadIdx.x), last);
+    d4[idx] = r[i];
   }
 }
 
@@ -866,13 +827,13 @@ __device__ inline void tile_store(D* __restrict__ dst, const D* __restrict__ src
     tile_copy<BT>(dst, src, count);
     return;
   }
-  const int nv = static_cast<int>(bytes / 16);
+  const int last = static_cast<int>(bytes / 16) - 1;
   const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
   u32x4* d4 = reinterpret_cast<u32x4*>(dst);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = i * BT + static_cast<int>(threadIdx.x);
-    if (idx < nv) __builtin_nontemporal_store(s4[idx], d4 + idx);
+    const int idx = min(i * BT + static_cast<int>(threadIdx.x), last);
+    __builtin_nontemporal_store(s4[idx], d4 + idx);
   }
 }
 
@@ -886,9 +847,9 @@ __device__ inline D apply_map(D x, D t, D lo, D hi, int kind) {
 
 // ---------------------------------------------------------------------------
 // The batched kernel.  Block = BT threads (one wave) = BT / G columns of G
-// lanes each.
+// lanes each.  FULL: m == G * C, so every slot of an active lane is valid.
 // ---------------------------------------------------------------------------
-template <int FAM, int KM, class D, class R, int G, int C, int BT>
+template <int FAM, int KM, class D, class R, int G, int C, int BT, bool FULL>
 __global__ void __launch_bounds__(BT)
 prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
                     int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
@@ -898,7 +859,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   constexpr int B = BT / G;
   // Most 16-byte transfers per thread: B m sizeof(D) / (16 BT) <= C sizeof(D) / 16.
   constexpr int NV = (C * static_cast<int>(sizeof(D)) + 15) / 16;
-  const int m = static_cast<int>(m64);
+  const int m = FULL ? G * C : static_cast<int>(m64);
   const int64_t col0 = static_cast<int64_t>(blockIdx.x) * B;
   const int ncols = static_cast<int>(min(static_cast<int64_t>(B), n - col0));
   const int64_t count = static_cast<int64_t>(ncols) * m;
@@ -907,18 +868,27 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   const bool active = lc < ncols;
   const int64_t j = col0 + lc;
 
-  tile_load<NV, BT>(tile, in + col0 * m64, count);
+  tile_load<NV, BT>(tile, in + col0 * m, count);
   __syncthreads();
-  const int nvalid = active ? (m - g + G - 1) / G : 0;
+  const int nvalid = active ? (FULL ? C : (m - g + G - 1) / G) : 0;
+  // Slot c of this lane is tile word lc * m + g + G c: a per-lane base and a
+  // compile-time offset, so every slot access is one LDS instruction.
+  D* const col = tile + lc * m;
+  D* const mine = col + g;
   // The tile has G*C words of slack after the B*m elements, so every slot
   // read stays inside the allocation and the loop needs no branch; past the
   // tile sit BT per-lane dummy words for predicated stores.
   D* const lds_dummy = tile + B * m + G * C + threadIdx.x;
   D v[C];
+  if (FULL && ncols == B) {
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
-    const D x = tile[lc * m + g + G * c];
-    v[c] = (c < nvalid) ? x : -num<D>::inf();
+    for (int c = 0; c < C; ++c) v[c] = mine[G * c];
+  } else {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const D x = mine[G * c];
+      v[c] = (c < nvalid) ? x : -num<D>::inf();
+    }
   }
 
   ColThr<R> th;
@@ -926,7 +896,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   if constexpr (FAM == FAM_KNAP) {
     th = knap_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPK) {
-    th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, tile + lc * m, lds_dummy);
+    th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, col, lds_dummy);
   } else if constexpr (FAM == FAM_ENT) {
     th = ent_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPKENT) {
@@ -939,34 +909,50 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   // The threshold search may have used the column's LDS slots as scratch.
   __syncthreads();
   if (active) {
+    // Deferred columns keep their input: the workgroup-per-column kernel
+    // reads it again (in place when in == out).  For the clamp-only families
+    // that is the clamp with t = 0, lo = -inf, hi = +inf; the entropic maps
+    // select the input instead.
+    constexpr bool kClampOnly = FAM == FAM_KNAP || FAM == FAM_TOPK || FAM == FAM_TWO;
+    if (kClampOnly && th.slow) {
+      th.t = th.t2 = R(0);
+      th.lo = th.lo2 = -num<R>::inf();
+      th.hi = th.hi2 = num<R>::inf();
+    }
     const D t1 = static_cast<D>(th.t), lo1 = static_cast<D>(th.lo), hi1 = static_cast<D>(th.hi);
     const D t2 = static_cast<D>(th.t2), lo2 = static_cast<D>(th.lo2), hi2 = static_cast<D>(th.hi2);
+    const D he1 = lo1 < hi1 ? hi1 : lo1, he2 = lo2 < hi2 ? hi2 : lo2;
     // The elementwise map is fixed per family (and per launch for the
     // entropic family, from the uniform op argument), so the slot loop has no
-    // per-lane branch.  Deferred columns keep their input: the
-    // workgroup-per-column kernel reads it again (in place when in == out).
+    // per-lane branch.
     auto write_slots = [&](auto map) {
 #pragma unroll
       for (int c = 0; c < C; ++c) {
-        const D y = th.slow ? v[c] : map(c);
-        D* dst = (c < nvalid) ? tile + lc * m + g + G * c : lds_dummy;
-        *dst = y;
+        const D y = map(c);
+        if (FULL) {
+          mine[G * c] = y;
+        } else {
+          D* dst = (c < nvalid) ? mine + G * c : lds_dummy;
+          *dst = y;
+        }
       }
     };
     if constexpr (FAM == FAM_ENT) {
       if (pp.op == OP_ENTROPY) {
-        write_slots([&](int c) { return clamp_ref(dexp(v[c] - t1), lo1, hi1); });
+        write_slots([&](int c) { return th.slow ? v[c] : clamp_ref(dexp(v[c] - t1), lo1, hi1); });
       } else {
-        write_slots([&](int c) { return clamp_ref(lambert_w_exp(v[c] - t1), lo1, hi1); });
+        write_slots([&](int c) {
+          return th.slow ? v[c] : clamp_ref(lambert_w_exp(v[c] - t1), lo1, hi1);
+        });
       }
     } else if constexpr (FAM == FAM_TOPKENT) {
-      write_slots([&](int c) { return clamp_ref(dexp(v[c] - t1), lo1, hi1); });
+      write_slots([&](int c) { return th.slow ? v[c] : clamp_ref(dexp(v[c] - t1), lo1, hi1); });
     } else if constexpr (FAM == FAM_TWO) {
       write_slots([&](int c) {
-        return (g + G * c >= p) ? clamp_ref(v[c] - t2, lo2, hi2) : clamp_ref(v[c] - t1, lo1, hi1);
+        return (g + G * c >= p) ? clamp_med3(v[c] - t2, lo2, he2) : clamp_med3(v[c] - t1, lo1, he1);
       });
     } else {
-      write_slots([&](int c) { return clamp_ref(v[c] - t1, lo1, hi1); });
+      write_slots([&](int c) { return clamp_med3(v[c] - t1, lo1, he1); });
     }
     if (g == 0) {
       if (th.slow) {
@@ -989,7 +975,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
     }
   }
   __syncthreads();
-  tile_store<NV, BT>(out + col0 * m64, tile, count);
+  tile_store<NV, BT>(out + col0 * m, tile, count);
 }
 
 }  // namespace sdca_gpu

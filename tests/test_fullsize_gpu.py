@@ -17,6 +17,8 @@ path once through the C ABI, and checks
     the GPU's own scores, the rank loss recomputed from them, and the
     per-example losses of a sample against the oracle on the same scores.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -27,6 +29,7 @@ pytestmark = pytest.mark.gpu
 
 F32, F64 = 0, 1
 CHUNK = 250_000
+THREADS = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
 
 
 def bench_input(name, cuda):
@@ -48,21 +51,21 @@ def run(cfg, x, col_p=None):
     return out
 
 
-def chunked_parity(oracle, cfg, x, out, col_p=None, stride=1):
-    """Every `stride`-th chunk of CHUNK columns against the oracle."""
+def chunked_parity(oracle, cfg, x, out, col_p=None, chunk=CHUNK, stride=1):
+    """Every `stride`-th chunk of `chunk` columns against the oracle."""
     import bench
     res = F32 if cfg["result"] == "f32" else F64
     kw = bench.kwargs_of(cfg)
     n = x.shape[0]
-    starts = list(range(0, n, CHUNK))[::stride]
+    starts = list(range(0, n, chunk))[::stride]
     for b in starts:
-        e = min(n, b + CHUNK)
+        e = min(n, b + chunk)
         xs = x[b:e].cpu().numpy()
         got = out[b:e].cpu().numpy()
         ckw = dict(kw)
         if col_p is not None:
             ckw["col_p"] = col_p[b:e].cpu().numpy()
-        parity(oracle, cfg["op"], xs, got, res, f"{cfg['op']} columns {b}:{e}", **ckw)
+        parity(oracle, cfg["op"], xs, got, res, f"{cfg['op']} columns {b}:{e}", THREADS, **ckw)
     return len(starts)
 
 
@@ -96,13 +99,13 @@ def test_c2_topk_simplex_full(cuda, oracle):
 
 
 def test_c2_topk_simplex_idempotent(cuda):
-    """The projection of a projected batch is itself (to fp32 rounding)."""
-    import torch
+    """The projection of a projected batch is itself, within the fp32
+    tolerance 1e-5 (s = max(1, max|p|) = 1 for these columns)."""
     cfg, x, _ = bench_input("c2", cuda)
     p = run(cfg, x)
     q = run(cfg, p)
     err = (q.double() - p.double()).abs().amax()
-    assert err <= 1e-6, f"max |P(P(a)) - P(a)| = {err}"
+    assert err <= 1e-5, f"max |P(P(a)) - P(a)| = {err}"
 
 
 def test_c2_topk_cone_full(cuda, oracle):
@@ -147,7 +150,7 @@ def test_c3_entropy_full(cuda, oracle):
     want = torch.softmax(x, dim=1)
     err = (out - want).abs().amax()
     assert err <= 1e-12, f"max |x - softmax(a)| = {err}"
-    chunked_parity(oracle, cfg, x, out, stride=100)
+    chunked_parity(oracle, cfg, x, out, chunk=20_000, stride=10)
 
 
 @pytest.mark.timeout(300)
@@ -163,16 +166,18 @@ def test_c3_entropy_norm_full(cuda, oracle):
     idx = torch.from_numpy(np.sort(np.random.default_rng(7).choice(x.shape[0], 5000, replace=False))).to(cuda)
     xs = x.index_select(0, idx).cpu().numpy()
     got = out.index_select(0, idx).cpu().numpy()
-    parity(oracle, "entropy_norm", xs, got, F64, "entropy_norm sample", hi=cfg["hi"], rhs=cfg["rhs"])
+    parity(oracle, "entropy_norm", xs, got, F64, "entropy_norm sample", THREADS, hi=cfg["hi"],
+           rhs=cfg["rhs"])
 
 
 def test_lambert_full(cuda, oracle):
     """W(exp(x)) on 10,000,000 points x ~ U(-50, 50), fp64: every point."""
     cfg, x, _ = bench_input("lambert", cuda)
     out = run(cfg, x)
-    xs = x.cpu().numpy()
-    got = out.cpu().numpy()
-    want = oracle.lambert_w_exp(xs.copy())
+    xs = x.cpu().numpy().reshape(-1, 1000)  # elementwise: any (n, m) view of the points
+    got = out.cpu().numpy().reshape(-1, 1000)
+    want = xs.copy()
+    oracle.prox("lambert_w_exp", want, result=F64, nthreads=THREADS)
     rel = np.abs(got - want) / np.maximum(1.0, np.abs(want))
     assert rel.max() <= 1e-12, f"max rel err {rel.max():.3e} at x = {xs.reshape(-1)[rel.argmax()]}"
 
@@ -219,9 +224,10 @@ def test_c4_eval_full(cuda, oracle):
     it = torch.from_numpy(idx).to(cuda)
     Ss = S.index_select(0, it).cpu().numpy()
     ys = labels.index_select(0, it).cpu().numpy()
-    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, ys, result=F32, per_example=True)
+    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, ys, result=F32, per_example=True,
+                                    nthreads=THREADS)
     _, _, x_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, ys, result=LONG_DOUBLE,
-                                    per_example=True)
+                                    per_example=True, nthreads=THREADS)
     got = pe.index_select(0, it).cpu().numpy()
     compare_per_example(got[:, :, 0], o_pe[:, :, 0], 1e-5, "c4 primal", exact=x_pe[:, :, 0])
     compare_per_example(got[:, :, 1], o_pe[:, :, 1], 1e-5, "c4 dual", exact=x_pe[:, :, 1])
@@ -262,8 +268,10 @@ def test_c5_eval_full(cuda, oracle):
         rank += torch.where(valid, c, 0.0)
     rank /= (npos * (m - npos)).double()
     want = float(rank.sum()) / n
+    # Result is float: the reference forms each example's rank term in float
+    # (eval/primal.h:70-79), so the total carries fp32 rounding: rtol 1e-5.
     for r in recs:
-        assert abs(r["rank_loss"] - want) <= 1e-12 * max(1.0, want), (r["rank_loss"], want)
+        assert abs(r["rank_loss"] - want) <= 1e-5 * max(1.0, want), (r["rank_loss"], want)
     idx = np.sort(np.random.default_rng(12).choice(n, 5000, replace=False))
     off = offsets.cpu().numpy()
     lab = labels.cpu().numpy()
@@ -271,8 +279,9 @@ def test_c5_eval_full(cuda, oracle):
     sl = [lab[off[i]:off[i + 1]] for i in idx]
     so = np.concatenate([[0], np.cumsum([len(v) for v in sl])]).astype(np.int64)
     sl = np.concatenate(sl).astype(np.int64)
-    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, sl, so, result=F32, per_example=True)
+    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, sl, so, result=F32,
+                                    per_example=True, nthreads=THREADS)
     _, _, x_pe = oracle.eval_scores(oracle_objs(objs), Ss, None, sl, so, result=LONG_DOUBLE,
-                                    per_example=True)
+                                    per_example=True, nthreads=THREADS)
     got = pe.index_select(0, torch.from_numpy(idx).to(cuda)).cpu().numpy()
     compare_per_example(got[:, :, 0], o_pe[:, :, 0], 1e-5, "c5 primal", exact=x_pe[:, :, 0])

@@ -40,22 +40,22 @@ def run_gpu(op, x, result, cuda, **kw):
     return out.cpu().numpy(), thr.cpu().numpy()
 
 
-def run_oracle(oracle, op, x, result, **kw):
+def run_oracle(oracle, op, x, result, nthreads=1, **kw):
     from oracle import binding
     y = x.copy()
     col_p = kw.pop("col_p", None)
     thr = oracle.prox(op, y, result=result, params=binding.make_params(**kw), col_p=col_p,
-                      thresholds=True)
+                      thresholds=op != "lambert_w_exp", nthreads=nthreads)
     return y, thr
 
 
 LONG_DOUBLE = 2
 
 
-def parity(oracle, op, x, got, result, what, **kw):
+def parity(oracle, op, x, got, result, what, nthreads=1, **kw):
     """Check got (GPU) against the oracle at the Result type and in long double."""
-    ref, _ = run_oracle(oracle, op, x, result, **dict(kw))
-    exact, _ = run_oracle(oracle, op, x, LONG_DOUBLE, **dict(kw))
+    ref, _ = run_oracle(oracle, op, x, result, nthreads, **dict(kw))
+    exact, _ = run_oracle(oracle, op, x, LONG_DOUBLE, nthreads, **dict(kw))
     scale = np.maximum(1.0, np.abs(x.astype(np.float64)).max(axis=1, keepdims=True))
     g = got.astype(np.float64)
     r = ref.astype(np.float64)
