@@ -52,18 +52,24 @@ size_t dtype_size(int dt) { return dt == SDCA_F32 ? 4 : 8; }
 struct Workspace {
   void* ptr[4] = {nullptr, nullptr, nullptr, nullptr};
   size_t cap[4] = {0, 0, 0, 0};
+  // The deferred-column list's two counters are zero (the deferred-column
+  // kernel of the last call on this stream was launched and resets them).
+  bool list_zeroed = false;
 };
 
 std::mutex g_ws_mutex;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-// Returns slot `slot` of the calling stream's workspace with at least `bytes`.
-int workspace(hipStream_t stream, int slot, size_t bytes, void** out) {
+// Returns slot `slot` of the calling stream's workspace with at least `bytes`
+// (and, with `ws`, the stream's workspace record).
+int workspace(hipStream_t stream, int slot, size_t bytes, void** out, Workspace** ws = nullptr) {
   int dev = 0;
   SDCA_HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
   Workspace& w = g_ws[std::make_pair(dev, stream)];
+  if (ws) *ws = &w;
   if (w.cap[slot] < bytes) {
+    if (slot == 0) w.list_zeroed = false;
     if (w.ptr[slot]) {
       SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
       SDCA_HIP_TRY(hipFree(w.ptr[slot]), "hipFree");
@@ -232,12 +238,18 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   } else if ((topk || knap) && (!reg_ok || (topk && p.k > kTopkMaxK))) {
     SDCA_HIP_TRY(launch_slow(a, true), "prox kernel (workgroup per column)");
   } else {
+    // Deferred-column list: [count, done, column ids...].  The deferred-column
+    // kernel zeroes both counters when its last workgroup finishes, so a
+    // clear is launched only for a new list or after a call that did not
+    // reach that kernel.
+    Workspace* wsr = nullptr;
     if (topk) {
       void* ws = nullptr;
-      rc = workspace(stream, 0, static_cast<size_t>(n + 1) * sizeof(int), &ws);
+      rc = workspace(stream, 0, static_cast<size_t>(n + 2) * sizeof(int), &ws, &wsr);
       if (rc) return rc;
       a.slow = static_cast<int*>(ws);
-      SDCA_HIP_TRY(launch_clear(a.slow, 1, stream), "clear kernel");
+      if (!wsr->list_zeroed) SDCA_HIP_TRY(launch_clear(a.slow, 2, stream), "clear kernel");
+      wsr->list_zeroed = false;
     }
     hipError_t e = hipSuccess;
     switch (op) {
@@ -252,7 +264,10 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
       default: break;
     }
     SDCA_HIP_TRY(e, "prox kernel");
-    if (topk) SDCA_HIP_TRY(launch_slow(a, false), "prox kernel (deferred columns)");
+    if (topk) {
+      SDCA_HIP_TRY(launch_slow(a, false), "prox kernel (deferred columns)");
+      wsr->list_zeroed = true;
+    }
   }
 
   if (host) {

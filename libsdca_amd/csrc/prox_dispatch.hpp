@@ -22,11 +22,14 @@ hipError_t launch_one(const ProxLaunch& a) {
   pp.op = a.op;
   pp.p = static_cast<int>(a.p);
   const int64_t blocks = (a.n + B - 1) / B;
-  // B*m tile, G*C words of slack for branch-free slot reads, BT dummy words.
-  const size_t shmem = (static_cast<size_t>(B) * static_cast<size_t>(a.m) + G * C + BT) * sizeof(D);
+  // B*m tile, G*C words of slack for branch-free slot reads (not needed when
+  // m == G*C), BT dummy words.
+  const bool full = a.m == static_cast<int64_t>(G) * C;
+  const size_t shmem =
+      (static_cast<size_t>(B) * static_cast<size_t>(a.m) + (full ? 0 : G * C) + BT) * sizeof(D);
   // m == G * C (the configuration's exact size) gets the variant without
   // per-slot validity tests.
-  if (a.m == static_cast<int64_t>(G) * C) {
+  if (full) {
     hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, true>),
                        dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
                        static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,

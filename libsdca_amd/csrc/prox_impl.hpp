@@ -144,7 +144,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
       break;
     }
     if (mc > 0) {
-      t = next / static_cast<R>(mc);
+      t = div_near(next, static_cast<R>(mc));
     } else {
       break;
     }
@@ -324,7 +324,10 @@ __device__ inline KnapState<R> knapsack_top(const D (&b)[L], int cnt, R lo, R hi
 // up to G * kCandSlots<G> candidates in registers; columns with more run the
 // variable fixing over all register slots instead.
 template <int G>
-constexpr int kCandSlots = (G <= 4) ? 4 : (G <= 16) ? 2 : 1;
+#ifndef SDCA_CAND_G4
+#define SDCA_CAND_G4 4
+#endif
+constexpr int kCandSlots = (G <= 2) ? 8 : (G <= 4) ? SDCA_CAND_G4 : (G <= 16) ? 2 : 1;
 
 // Variable fixing for the top-k simplex's knapsack (lo = 0, hi = rhs / k):
 // its root t* satisfies sum_i clamp(a_i - t*, 0, hi) = k hi, hence
@@ -371,7 +374,8 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
       }
       wave_lds_sync();
       // Candidate i sits at lds_col[i]; lane g takes i = g, g + G, ...  The
-      // reads stay inside the tile (G * CC <= G * C words of slack follow it).
+      // reads stay inside the tile: G * CC <= 16 <= m for G = 4 and 2, and
+      // G * CC <= G <= m for larger G.
       D cand[CC];
       R csum = 0;
 #pragma unroll
@@ -875,10 +879,10 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   // compile-time offset, so every slot access is one LDS instruction.
   D* const col = tile + lc * m;
   D* const mine = col + g;
-  // The tile has G*C words of slack after the B*m elements, so every slot
-  // read stays inside the allocation and the loop needs no branch; past the
-  // tile sit BT per-lane dummy words for predicated stores.
-  D* const lds_dummy = tile + B * m + G * C + threadIdx.x;
+  // Unless FULL, the tile has G*C words of slack after the B*m elements, so
+  // every slot read stays inside the allocation and the loop needs no branch;
+  // past that sit BT per-lane dummy words for predicated stores.
+  D* const lds_dummy = tile + B * m + (FULL ? 0 : G * C) + threadIdx.x;
   D v[C];
   if (FULL && ncols == B) {
 #pragma unroll
@@ -957,7 +961,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
     if (g == 0) {
       if (th.slow) {
         const int pos = atomicAdd(slow, 1);
-        slow[1 + pos] = static_cast<int>(j);
+        slow[2 + pos] = static_cast<int>(j);
       } else if (thr) {
         if (FAM == FAM_TWO) {
           thr[2 * j].t = static_cast<double>(th.t);

@@ -197,14 +197,14 @@ template <class D, class R>
 __global__ void __launch_bounds__(256)
 prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
                  ProxParamsT<R> pp, sdca_thresholds* __restrict__ thr,
-                 const int* __restrict__ slow, int all_columns, int pow2) {
+                 int* __restrict__ slow, int all_columns, int pow2) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* s = reinterpret_cast<D*>(smem_raw);
   __shared__ R sh_t, sh_lo, sh_hi;
   const int m = static_cast<int>(m64);
   const int64_t count = all_columns ? n : static_cast<int64_t>(slow[0]);
   for (int64_t w = blockIdx.x; w < count; w += gridDim.x) {
-    const int64_t j = all_columns ? w : static_cast<int64_t>(slow[1 + w]);
+    const int64_t j = all_columns ? w : static_cast<int64_t>(slow[2 + w]);
     const D* col = in + j * m64;
     for (int i = threadIdx.x; i < pow2; i += blockDim.x)
       s[i] = (i < m) ? col[i] : -num<D>::inf();
@@ -243,6 +243,16 @@ prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int
     D* dst = out + j * m64;
     for (int i = threadIdx.x; i < m; i += blockDim.x) dst[i] = clamp_ref(col[i] - t, lo, hi);
     __syncthreads();
+  }
+  // List mode: the last workgroup to finish zeroes the list's counters
+  // [count, done] for the next call on the stream (every workgroup has read
+  // the count before it increments done).
+  if (!all_columns && threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(slow + 1, 1) == static_cast<int>(gridDim.x) - 1) {
+      atomicExch(slow, 0);
+      atomicExch(slow + 1, 0);
+    }
   }
 }
 
