@@ -93,55 +93,80 @@ struct KnapState {
   R sum_u;           // sum over U
 };
 
+// The fixing may start with the n_u0 values above hi_cut0 (sum sum_u0)
+// already at the upper bound, when those are known to end there; the
+// iteration is then Kiwiel's on the remaining problem.
+//
+// Each lane keeps a working copy w of its slots in which every fixed value
+// (and padding) is NaN: both candidate tests (w <= lo + t, w > hi + t) are
+// false for NaN, so a slot costs two compares and the fixing of a set is one
+// select.  The low and high counts travel in one integer (n_lo + 2^16 n_hi;
+// at most m <= 2048 each) through the group sum.
 template <int G, int C, class D, class R>
 __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nvalid, R total,
-                                                R lo, R hi, R rhs) {
+                                                R lo, R hi, R rhs, R hi_cut0 = num<R>::inf(),
+                                                int n_u0 = 0, R sum_u0 = 0) {
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
-  int mc = m;
-  R t = (total - rhs) / static_cast<R>(m);
+  const R qnan = num<R>::quiet_nan();
+  int mc = m - n_u0;
+  R t = div_near(total - sum_u0 - rhs + static_cast<R>(n_u0) * hi, static_cast<R>(mc));
   KnapState<R> st;
   st.lo_cut = -num<R>::inf();
-  st.hi_cut = num<R>::inf();
+  st.hi_cut = hi_cut0;
   st.c_lo = -num<R>::inf();
   st.c_hi = num<R>::inf();
-  st.n_u = 0;
-  st.sum_u = 0;
+  st.n_u = n_u0;
+  st.sum_u = sum_u0;
+  R w[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(v[c]);
+    w[c] = (x > -num<R>::inf() && !(x > hi_cut0)) ? x : qnan;
+  }
   for (int iter = 0; iter <= m; ++iter) {
     const R c_lo = lo + t, c_hi = hi + t;
     R s_lo = 0, s_hi = 0;
-    int n_lo = 0, n_hi = 0;
+    int n_lh = 0;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const R x = static_cast<R>(v[c]);  // padding (-inf) is never free
-      const bool fr = (x > st.lo_cut) && !(x > st.hi_cut);
-      const bool gl = x > c_lo;
-      if (fr && !gl) { s_lo += x; ++n_lo; }
-      if (fr && gl && x > c_hi) { s_hi += x; ++n_hi; }
+      const bool lo_c = w[c] <= c_lo;
+      const bool hi_c = w[c] > c_hi;
+      s_lo += lo_c ? w[c] : R(0);
+      s_hi += hi_c ? w[c] : R(0);
+      n_lh += (lo_c ? 1 : 0) + (hi_c ? 0x10000 : 0);
     }
     s_lo = group_sum<G>(s_lo);
     s_hi = group_sum<G>(s_hi);
-    n_lo = group_sum<G>(n_lo);
-    n_hi = group_sum<G>(n_hi);
+    n_lh = group_sum<G>(n_lh);
+    const int n_lo = n_lh & 0xffff, n_hi = n_lh >> 16;
     const R sh = static_cast<R>(n_hi) * hi;
     const R sl = static_cast<R>(n_lo) * lo;
     const R infeas = s_hi + s_lo - (sh + sl) - static_cast<R>(n_hi + n_lo) * t;
-    R next;
-    if (n_hi > 0 && infeas > eps) {
-      st.hi_cut = dmin(st.hi_cut, dmax(c_lo, c_hi));
-      next = static_cast<R>(mc) * t - s_hi + sh;
-      mc -= n_hi;
-      st.n_u += n_hi;
-      st.sum_u += s_hi;
-    } else if (n_lo > 0 && infeas < -eps) {
-      st.lo_cut = dmax(st.lo_cut, c_lo);
-      next = static_cast<R>(mc) * t - s_lo + sl;
-      mc -= n_lo;
-    } else {
+    const bool fix_hi = n_hi > 0 && infeas > eps;
+    const bool fix_lo = !fix_hi && n_lo > 0 && infeas < -eps;
+    if (!fix_hi && !fix_lo) {
       st.c_lo = c_lo;
       st.c_hi = c_hi;
       st.n_u += n_hi;
       st.sum_u += s_hi;
       break;
+    }
+    R next;
+    if (fix_hi) {
+      st.hi_cut = dmin(st.hi_cut, dmax(c_lo, c_hi));
+      next = static_cast<R>(mc) * t - s_hi + sh;
+      mc -= n_hi;
+      st.n_u += n_hi;
+      st.sum_u += s_hi;
+    } else {
+      st.lo_cut = dmax(st.lo_cut, c_lo);
+      next = static_cast<R>(mc) * t - s_lo + sl;
+      mc -= n_lo;
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const bool fixed = fix_hi ? (w[c] > c_hi) : (w[c] <= c_lo);
+      w[c] = fixed ? qnan : w[c];
     }
     if (mc > 0) {
       t = div_near(next, static_cast<R>(mc));
@@ -343,7 +368,8 @@ template <int G, int C, int L, class D, class R>
 __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L], int m,
                                              int nvalid, R kth, R hi, R rhs, D* lds_col,
                                              D* lds_dummy) {
-  const R cut = kth - hi - (fabs(kth) + hi) * (R(16) * num<R>::eps());
+  const R slack = (fabs(kth) + hi) * (R(16) * num<R>::eps());
+  const R cut = kth - hi - slack;
 #ifndef SDCA_TOPK_LIST_KNAPSACK
 #define SDCA_TOPK_LIST_KNAPSACK 0
 #endif
@@ -386,7 +412,20 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
         csum += ok ? static_cast<R>(x) : R(0);
       }
       csum = group_sum<G>(csum);
-      return knapsack_eq_regs<G, CC, D, R>(cand, total, total, csum, R(0), hi, rhs);
+      // Values at or above a_(k) + hi end at the upper bound (t* < a_(k)), so
+      // the fixing starts with them fixed; they are among the k - 1 largest,
+      // i.e. in the sorted top list every lane of the group holds.
+      const R ucut = kth + hi + slack;
+      int n_u0 = 0;
+      R sum_u0 = 0;
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        const bool u = static_cast<R>(top[i]) > ucut;
+        n_u0 += u ? 1 : 0;
+        sum_u0 += u ? static_cast<R>(top[i]) : R(0);
+      }
+      return knapsack_eq_regs<G, CC, D, R>(cand, total, total, csum, R(0), hi, rhs, ucut, n_u0,
+                                           sum_u0);
     }
   }
   const R all = total_sum<G, C, D, R>(v, nvalid);
