@@ -44,7 +44,8 @@ hipError_t launch_one(const ProxLaunch& a) {
 }
 
 // m -> (G lanes per column, C slots per lane): the fewest lanes whose C
-// slots hold the column (C = 25 fits m = 100 exactly on four lanes).
+// slots hold the column (C = 25 fits m = 100 exactly on four lanes and
+// m = 200 on eight).
 template <int FAM, int KM, class D, class R>
 hipError_t launch_by_m(const ProxLaunch& a) {
   if (a.m <= 16) return launch_one<FAM, KM, D, R, 1, 16>(a);
@@ -54,6 +55,7 @@ hipError_t launch_by_m(const ProxLaunch& a) {
 #endif
   if (a.m <= 100) return launch_one<FAM, KM, D, R, SDCA_M100_G, 100 / SDCA_M100_G>(a);
   if (a.m <= 128) return launch_one<FAM, KM, D, R, 4, 32>(a);
+  if (a.m <= 200) return launch_one<FAM, KM, D, R, 8, 25>(a);
   if (a.m <= 256) return launch_one<FAM, KM, D, R, 16, 16>(a);
   if (a.m <= 512) return launch_one<FAM, KM, D, R, 16, 32>(a);
   if (a.m <= 1024) return launch_one<FAM, KM, D, R, 64, 16>(a);

@@ -715,33 +715,55 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
   for (int c = 0; c < C; ++c) in_a[c] = (g + G * c) < p;
   R cuts[2];
   R res[2];
-  int cnt[2] = {p, m - p};
-  // Phase 1: each block on its own simplex <1, x> = rhs.
+  int cnt[2];
+  // Phase 1: each block on its own simplex <1, x> = rhs, by the reference's
+  // iteration t = (sum(S) - rhs) / |S|, S <- {x in S : x > t} until S stays.
+  // Its fixed point depends only on starting from a superset of the final
+  // S, so S starts at {x > max - rhs} (a final member x has x > t and the
+  // block maximum satisfies max - t <= rhs) instead of the whole block; each
+  // pass gives the sum and count for the next threshold and the test.
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    R cut = -num<R>::inf();
+    R mx = -num<R>::inf();
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      mx = (in_a[c] == (b == 0) && x > mx) ? x : mx;
+    }
+    mx = group_max<G>(mx);
+    R cut = mx - rhs;
+    R sb = 0;
+    int nb = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const R x = static_cast<R>(v[c]);
+      const bool in = in_a[c] == (b == 0) && x > cut;
+      sb += in ? x : R(0);
+      nb += in ? 1 : 0;
+    }
+    sb = group_sum<G>(sb);
+    nb = group_sum<G>(nb);
     R tb = 0;
     for (int it = 0; it <= m; ++it) {
-      R s = 0;
+      tb = div_near(sb - rhs, static_cast<R>(nb));
+      R s2 = 0;
+      int n2 = 0;
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const R x = static_cast<R>(v[c]);
-        if (in_a[c] == (b == 0) && x > cut) s += x;
+        const bool in = in_a[c] == (b == 0) && x > cut && x > tb;
+        s2 += in ? x : R(0);
+        n2 += in ? 1 : 0;
       }
-      s = group_sum<G>(s);
-      tb = (s - rhs) / static_cast<R>(cnt[b]);
-      int above = 0;
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const R x = static_cast<R>(v[c]);
-        if (in_a[c] == (b == 0) && x > cut && x > tb) ++above;
-      }
-      above = group_sum<G>(above);
-      if (above == cnt[b]) break;
+      s2 = group_sum<G>(s2);
+      n2 = group_sum<G>(n2);
+      if (n2 == nb) break;
       cut = dmax(cut, tb);
-      cnt[b] = above;
+      sb = s2;
+      nb = n2;
     }
     cuts[b] = cut;
+    cnt[b] = nb;
     res[b] = tb;
   }
   R t = res[0];

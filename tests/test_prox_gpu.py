@@ -80,7 +80,7 @@ def parity(oracle, op, x, got, result, what, nthreads=1, **kw):
 DTYPES = [(np.float32, F32), (np.float32, F64), (np.float64, F64)]
 # One m per register configuration (G lanes x C slots), plus the sizes of the
 # benchmark configurations.
-MS = [1, 3, 10, 16, 17, 64, 100, 128, 200, 512, 999, 1000, 2048]
+MS = [1, 3, 10, 16, 17, 64, 100, 101, 128, 150, 200, 512, 999, 1000, 2048]
 
 
 def cases(m, dtype, seed):
