@@ -65,7 +65,13 @@ __device__ inline float div_near(float n, float d) {
   const float e = __builtin_fmaf(-d, q, n);
   return __builtin_fmaf(e, r, q);
 }
-__device__ inline double div_near(double n, double d) { return n / d; }
+// Double: reciprocal, one Newton step on it, then one on the quotient.
+__device__ inline double div_near(double n, double d) {
+  const double r0 = __builtin_amdgcn_rcp(d);
+  const double r = __builtin_fma(__builtin_fma(-d, r0, 1.0), r0, r0);
+  const double q = n * r;
+  return __builtin_fma(__builtin_fma(-d, q, n), r, q);
+}
 
 // x log x with 0 log 0 = 0 (math/log_exp.h:76-80).
 template <class T>
@@ -73,15 +79,17 @@ __device__ inline T x_log_x(T x) { return (x > 0) ? x * dlog(x) : T(0); }
 
 // ---------------------------------------------------------------------------
 // Lambert W(exp(x)) (math/lambert.h:31-157): same intervals, same
-// initialisation and the same order-5 Householder step.
+// initialisation and the same order-5 Householder step.  The step's
+// quotient uses div_near: its error scales the (small) correction, so W keeps
+// full precision.
 // ---------------------------------------------------------------------------
 template <class T>
 __device__ inline T lw_step5(T w, T y) {
   T f0 = w - y, f1 = T(1) + y;
   T f11 = f1 * f1, f0y = f0 * y;
   T f00y = f0 * f0y;
-  return w - T(4) * f0 * (T(6) * f1 * (f11 + f0y) + f00y)
-    / (f11 * (T(24) * f11 + T(36) * f0y) + f00y * (T(14) * y + f0 + T(8)));
+  return w - div_near(T(4) * f0 * (T(6) * f1 * (f11 + f0y) + f00y),
+                      f11 * (T(24) * f11 + T(36) * f0y) + f00y * (T(14) * y + f0 + T(8)));
 }
 
 template <class T>
@@ -92,44 +100,44 @@ __device__ inline T exp_approx(T x) {
   return y;
 }
 
+// The reference's branches (lambert.h:81-105 float, :125-156 double) give
+// every x an initial w (with at most one intermediate step) and then the
+// same final step lw_step5(w, exp(x - w)), or a closed form at the extremes.
+// Here only the initial part is branch-specific; the exponential and the
+// final step are issued once for the whole wave, so a wave whose lanes span
+// several intervals pays for the costly part once instead of per branch.
+// Each lane still computes exactly its branch's sequence.
 __device__ inline float lambert_w_exp(float x) {
-  float w;
-  if (x > -1.0f) {
-    if (x <= 8.0f) {
-      w = lw_step5(x, 1.0f);
-    } else {
-      return (x <= 536870912.0f) ? lw_step5(x - logf(x), x) : x;
-    }
-  } else {
-    if (x > -18.0f) {
-      w = exp_approx(x);
-    } else {
-      return (x > -104.0f) ? expf(x) : 0.0f;
-    }
+  const int br = x > -1.0f ? (x <= 8.0f ? 0 : (x <= 536870912.0f ? 1 : 2))
+                           : (x > -18.0f ? 3 : 4);
+  float w = 0.0f;
+  if (br == 0) {
+    w = lw_step5(x, 1.0f);
+  } else if (br == 1) {
+    w = x - logf(x);  // (8, 2^29]: the result is lw_step5(x - log x, x)
+  } else if (br == 3) {
+    w = exp_approx(x);
   }
-  return lw_step5(w, expf(x - w));
+  const float e = expf(br == 4 ? x : x - w);
+  const float r = lw_step5(w, br == 1 ? x : e);
+  return br == 2 ? x : (br == 4 ? ((x > -104.0f) ? e : 0.0f) : r);
 }
 
 __device__ inline double lambert_w_exp(double x) {
-  double w;
-  if (x > 0.0) {
-    if (x <= 4.0) {
-      w = lw_step5(x, 1.0);
-    } else if (x <= 576460752303423488.0) {
-      w = x - log(x);
-      w = lw_step5(w, x);
-    } else {
-      return x;
-    }
-  } else {
-    if (x > -36.0) {
-      w = exp_approx(x);
-      if (x > -20.0) w = lw_step5(w, exp_approx(x - w));
-    } else {
-      return (x > -746.0) ? exp(x) : 0.0;
-    }
+  const int br = x > 0.0 ? (x <= 4.0 ? 0 : (x <= 576460752303423488.0 ? 1 : 2))
+                         : (x > -20.0 ? 3 : (x > -36.0 ? 4 : 5));
+  double w = 0.0;
+  if (br == 0) {
+    w = lw_step5(x, 1.0);
+  } else if (br == 1) {
+    w = lw_step5(x - log(x), x);
+  } else if (br == 3 || br == 4) {
+    w = exp_approx(x);
+    if (br == 3) w = lw_step5(w, exp_approx(x - w));
   }
-  return lw_step5(w, exp(x - w));
+  const double e = exp(br == 5 ? x : x - w);
+  const double r = lw_step5(w, e);
+  return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
 }
 
 // ---------------------------------------------------------------------------

@@ -514,15 +514,56 @@ __device__ inline R masked_max(const D (&v)[C], const bool (&mask)[C]) {
   return group_max<G>(mx);
 }
 
-// solve_sum_w_exp (entropy_norm.h:110-134) over the slots in `range`
-// (count valid elements, all with values > -inf unless padding).
+// ---------------------------------------------------------------------------
+// Entropic family: entropy (entropy.h:19-53) and entropy_norm
+// (entropy_norm.h:146-181), on the column's LDS copy.  Slot c of the lane is
+// x[G c]; the free set is a bit mask over the lane's slots.  Every pass is a
+// rolled loop that reads its slot from LDS: with C slots unrolled and held in
+// registers, C exp / Lambert evaluations would be live at once (in double,
+// more than 150 VGPRs and two waves per SIMD).
+// ---------------------------------------------------------------------------
+template <int C>
+__device__ inline unsigned slot_bits(int nvalid) {
+  return nvalid >= 32 ? 0xffffffffu : ((1u << nvalid) - 1u);
+}
+
 template <int G, int C, class D, class R>
-__device__ inline R solve_sum_w_exp_regs(const D (&v)[C], const bool (&range)[C],
-                                         int count, R rhs) {
+__device__ inline R lds_masked_max(const D* x, unsigned bits) {
+  R mx = -num<R>::inf();
+#pragma unroll 4
+  for (int c = 0; c < C; ++c) {
+    const R y = static_cast<R>(x[G * c]);
+    mx = (((bits >> c) & 1u) && y > mx) ? y : mx;
+  }
+  return group_max<G>(mx);
+}
+
+// sum of exp(x - mx) over the free slots except exactly one maximum element
+// (the first in lane/slot order), as log_sum_exp(first, last, max, s)
+// (math/log_exp.h:134-152) excludes its `max` iterator.
+template <int G, int C, class D, class R>
+__device__ inline R lds_lse_sum_excl(const D* x, unsigned bits, R mx) {
+  int first_c = C;
+#pragma unroll 4
+  for (int c = C - 1; c >= 0; --c)
+    first_c = (((bits >> c) & 1u) && static_cast<R>(x[G * c]) == mx) ? c : first_c;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const int owner = group_min<G>(first_c < C ? g : G);
+  if (g == owner) bits &= ~(1u << first_c);
   R s = 0;
-#pragma unroll
+#pragma unroll 4
   for (int c = 0; c < C; ++c)
-    if (range[c] && static_cast<R>(v[c]) > -num<R>::inf()) s += static_cast<R>(v[c]);
+    if ((bits >> c) & 1u) s += dexp(static_cast<R>(x[G * c]) - mx);
+  return group_sum<G>(s);
+}
+
+// solve_sum_w_exp (entropy_norm.h:110-134) over the free slots (count of
+// them in the column).
+template <int G, int C, class D, class R>
+__device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int count, R rhs) {
+  R s = 0;
+#pragma unroll 4
+  for (int c = 0; c < C; ++c) s += ((bits >> c) & 1u) ? static_cast<R>(x[G * c]) : R(0);
   s = group_sum<G>(s);
   R t = (s - rhs) / static_cast<R>(count);
   // Heuristic refinement: U = {a > t} shrinks while it stays non-trivial.
@@ -531,10 +572,12 @@ __device__ inline R solve_sum_w_exp_regs(const D (&v)[C], const bool (&range)[C]
   for (int it = 0; it < count + 1; ++it) {
     R su = 0;
     int cu = 0;
-#pragma unroll
+#pragma unroll 4
     for (int c = 0; c < C; ++c) {
-      const R x = static_cast<R>(v[c]);
-      if (range[c] && x > u_cut && x > t) { su += x; ++cu; }
+      const R y = static_cast<R>(x[G * c]);
+      const bool in = ((bits >> c) & 1u) && y > u_cut && y > t;
+      su += in ? y : R(0);
+      cu += in ? 1 : 0;
     }
     su = group_sum<G>(su);
     cu = group_sum<G>(cu);
@@ -543,24 +586,27 @@ __device__ inline R solve_sum_w_exp_regs(const D (&v)[C], const bool (&range)[C]
     u_count = cu;
     t = (su - rhs) / static_cast<R>(cu);
   }
-  // Householder iterations of order 4 (entropy_norm.h:161-204).
-  const R ub = masked_max<G, C, D, R>(v, range) - num<R>::exp_min_arg();
+  // Householder iterations of order 4 (entropy_norm.h:84-102).
+  const R ub = lds_masked_max<G, C, D, R>(x, bits) - num<R>::exp_min_arg();
   const R eps16 = R(16) * num<R>::eps();
   for (int iter = 0; iter < 32; ++iter) {
     const R prev = t;
     const R tc = dmin(t, ub);
     const R mt = -tc;
     R f0 = 0, f1 = 0, f2 = 0, f3 = 0;
-#pragma unroll
+#pragma unroll 1
     for (int c = 0; c < C; ++c) {
-      if (range[c]) {
-        const R w = lambert_w_exp(static_cast<R>(v[c]) + mt);
-        const R d = R(1) + w;
-        const R d3 = d * d * d;
+      if ((bits >> c) & 1u) {
+        const R w = lambert_w_exp(static_cast<R>(x[G * c]) + mt);
+        // The derivative sums steer the step only (the root is f0 = rhs),
+        // so they share one reciprocal of 1 + w.
+        const R rd = div_near(R(1), R(1) + w);
+        const R rd2 = rd * rd;
+        const R rd3 = rd2 * rd;
         f0 += w;
-        f1 += w / d;
-        f2 += w / d3;
-        f3 += w * (R(1) - R(2) * w) / (d3 * d * d);
+        f1 += w * rd;
+        f2 += w * rd3;
+        f3 += w * (R(1) - R(2) * w) * (rd3 * rd2);
       }
     }
     f0 = group_sum<G>(f0);
@@ -575,35 +621,34 @@ __device__ inline R solve_sum_w_exp_regs(const D (&v)[C], const bool (&range)[C]
   return t;
 }
 
-// ---------------------------------------------------------------------------
-// Entropic family: entropy (entropy.h:19-53) and entropy_norm
-// (entropy_norm.h:146-181).  Elements fixed at hi are {x > hi_cut}.
-// ---------------------------------------------------------------------------
-template <int G, int C, class D, class R>
-__device__ inline ColThr<R> ent_family(const D (&v)[C], int m, int nvalid,
-                                       const ProxParamsT<R>& pp) {
-  const bool norm = pp.op == OP_ENTROPY_NORM;
+// Forced inline: outlined, the call convention alone costs the kernel ~80
+// VGPRs (three waves per SIMD instead of eight).
+template <bool NORM, int G, int C, class D, class R>
+__device__ __forceinline__ ColThr<R> ent_family(const D* x, int m, int nvalid,
+                                                const ProxParamsT<R>& pp) {
   const R hi = pp.hi, rhs = pp.rhs;
   const R eps = R(16) * num<R>::eps() * dmax(R(1), rhs);
-  const R u = norm ? hi + dlog(hi) + eps : dlog(hi) + eps;
+  const R u = NORM ? hi + dlog(hi) + eps : dlog(hi) + eps;
   R r = rhs;
-  bool freem[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) freem[c] = c < nvalid;
-  R t;
-  if (norm) {
-    t = solve_sum_w_exp_regs<G, C, D, R>(v, freem, m, rhs);
-  } else {
-    const R mx = masked_max<G, C, D, R>(v, freem);
-    t = mx + dlog1p(lse_sum_excl<G, C, D, R>(v, freem, mx)) - dlog(rhs);
-  }
+  unsigned freeb = slot_bits<C>(nvalid);
+  R t = 0;
   int nfixed = 0;
+  // Threshold over the free set, then fix {x > t + u} at hi and repeat
+  // (entropy.h:30-49, entropy_norm.h:157-178).
   for (int iter = 0; iter <= m; ++iter) {
+    if constexpr (NORM) {
+      t = lds_solve_sum_w_exp<G, C, D, R>(x, freeb, m - nfixed, r);
+    } else {
+      const R mx = lds_masked_max<G, C, D, R>(x, freeb);
+      t = mx + dlog1p(lds_lse_sum_excl<G, C, D, R>(x, freeb, mx)) - dlog(r);
+    }
     const R cut = t + u;
     int cnt = 0;
-#pragma unroll
+#pragma unroll 4
     for (int c = 0; c < C; ++c) {
-      if (freem[c] && static_cast<R>(v[c]) > cut) { ++cnt; freem[c] = false; }
+      const bool fix = ((freeb >> c) & 1u) && static_cast<R>(x[G * c]) > cut;
+      cnt += fix ? 1 : 0;
+      freeb &= fix ? ~(1u << c) : ~0u;
     }
     cnt = group_sum<G>(cnt);
     if (cnt == 0) break;
@@ -611,17 +656,11 @@ __device__ inline ColThr<R> ent_family(const D (&v)[C], int m, int nvalid,
     nfixed += cnt;
     if (nfixed == m) break;
     if (r <= eps) {
-      t = masked_max<G, C, D, R>(v, freem) - num<R>::exp_min_arg() + R(1);
+      t = lds_masked_max<G, C, D, R>(x, freeb) - num<R>::exp_min_arg() + R(1);
       break;
     }
-    if (norm) {
-      t = solve_sum_w_exp_regs<G, C, D, R>(v, freem, m - nfixed, r);
-    } else {
-      const R mx = masked_max<G, C, D, R>(v, freem);
-      t = mx + dlog1p(lse_sum_excl<G, C, D, R>(v, freem, mx)) - dlog(r);
-    }
   }
-  return make_thr<R>(t, R(0), hi, norm ? 2 : 1);
+  return make_thr<R>(t, R(0), hi, NORM ? 2 : 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -902,14 +941,6 @@ __device__ inline void tile_store(D* __restrict__ dst, const D* __restrict__ src
   }
 }
 
-template <class D, class R>
-__device__ inline D apply_map(D x, D t, D lo, D hi, int kind) {
-  D y = x - t;
-  if (kind == 1) y = dexp(y);
-  else if (kind == 2) y = lambert_w_exp(y);
-  return clamp_ref(y, lo, hi);
-}
-
 // ---------------------------------------------------------------------------
 // The batched kernel.  Block = BT threads (one wave) = BT / G columns of G
 // lanes each.  FULL: m == G * C, so every slot of an active lane is valid.
@@ -963,7 +994,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   } else if constexpr (FAM == FAM_TOPK) {
     th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, col, lds_dummy);
   } else if constexpr (FAM == FAM_ENT) {
-    th = ent_family<G, C, D, R>(v, m, nvalid, pp);
+    th = ent_family<KM == 1, G, C, D, R>(mine, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPKENT) {
     th = topkent_family<G, C, D, R>(v, m, nvalid, pp);
   } else {
@@ -1002,16 +1033,23 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
         }
       }
     };
+    // The exp / Lambert maps run in a rolled loop over the LDS copy of the
+    // slots (in place), for the same register reason as above.
+    auto write_rolled = [&](auto map) {
+      if (th.slow) return;
+#pragma unroll 2
+      for (int c = 0; c < C; ++c) {
+        if (c < nvalid) mine[G * c] = map(mine[G * c]);
+      }
+    };
     if constexpr (FAM == FAM_ENT) {
-      if (pp.op == OP_ENTROPY) {
-        write_slots([&](int c) { return th.slow ? v[c] : clamp_ref(dexp(v[c] - t1), lo1, hi1); });
+      if constexpr (KM == 0) {
+        write_rolled([&](D x) { return clamp_ref(dexp(x - t1), lo1, hi1); });
       } else {
-        write_slots([&](int c) {
-          return th.slow ? v[c] : clamp_ref(lambert_w_exp(v[c] - t1), lo1, hi1);
-        });
+        write_rolled([&](D x) { return clamp_ref(lambert_w_exp(x - t1), lo1, hi1); });
       }
     } else if constexpr (FAM == FAM_TOPKENT) {
-      write_slots([&](int c) { return th.slow ? v[c] : clamp_ref(dexp(v[c] - t1), lo1, hi1); });
+      write_rolled([&](D x) { return clamp_ref(dexp(x - t1), lo1, hi1); });
     } else if constexpr (FAM == FAM_TWO) {
       write_slots([&](int c) {
         return (g + G * c >= p) ? clamp_med3(v[c] - t2, lo2, he2) : clamp_med3(v[c] - t1, lo1, he1);

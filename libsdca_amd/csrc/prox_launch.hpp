@@ -46,6 +46,7 @@ struct ProxLaunch {
 hipError_t launch_knap(const ProxLaunch& a);
 hipError_t launch_topk(const ProxLaunch& a);
 hipError_t launch_ent(const ProxLaunch& a);
+hipError_t launch_ent_norm(const ProxLaunch& a);
 hipError_t launch_topkent(const ProxLaunch& a);
 hipError_t launch_two(const ProxLaunch& a);
 // Workgroup-per-column kernel over the flagged list (all_columns: every column).
