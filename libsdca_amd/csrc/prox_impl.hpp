@@ -623,22 +623,47 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
 
 // Forced inline: outlined, the call convention alone costs the kernel ~80
 // VGPRs (three waves per SIMD instead of eight).
+// For the exp map the first threshold pass also keeps e_c = exp(x_c - mx0)
+// (mx0 the column maximum) in registers, and when t >= mx0 the clamp pass
+// writes e_c * exp(mx0 - t) instead of evaluating exp(x_c - t) again (the
+// same value to a few ulps; with t >= mx0 an underflowed e_c means an
+// underflowed result).
 template <bool NORM, int G, int C, class D, class R>
 __device__ __forceinline__ ColThr<R> ent_family(const D* x, int m, int nvalid,
-                                                const ProxParamsT<R>& pp) {
+                                                const ProxParamsT<R>& pp, R (&e)[C],
+                                                R& scale) {
   const R hi = pp.hi, rhs = pp.rhs;
   const R eps = R(16) * num<R>::eps() * dmax(R(1), rhs);
   const R u = NORM ? hi + dlog(hi) + eps : dlog(hi) + eps;
   R r = rhs;
   unsigned freeb = slot_bits<C>(nvalid);
   R t = 0;
+  R mx0 = 0;
   int nfixed = 0;
+  if constexpr (!NORM) {
+    // log_sum_exp with the first maximum excluded (math/log_exp.h:134-152).
+    mx0 = lds_masked_max<G, C, D, R>(x, freeb);
+    int first_c = C;
+#pragma unroll
+    for (int c = C - 1; c >= 0; --c)
+      first_c = (((freeb >> c) & 1u) && static_cast<R>(x[G * c]) == mx0) ? c : first_c;
+    const int g = static_cast<int>(threadIdx.x) % G;
+    const int owner = group_min<G>(first_c < C ? g : G);
+    R sum = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const bool ok = (freeb >> c) & 1u;
+      e[c] = ok ? dexp(static_cast<R>(x[G * c]) - mx0) : R(0);
+      sum += (ok && !(g == owner && c == first_c)) ? e[c] : R(0);
+    }
+    t = mx0 + dlog1p(group_sum<G>(sum)) - dlog(r);
+  }
   // Threshold over the free set, then fix {x > t + u} at hi and repeat
   // (entropy.h:30-49, entropy_norm.h:157-178).
   for (int iter = 0; iter <= m; ++iter) {
     if constexpr (NORM) {
       t = lds_solve_sum_w_exp<G, C, D, R>(x, freeb, m - nfixed, r);
-    } else {
+    } else if (iter > 0) {
       const R mx = lds_masked_max<G, C, D, R>(x, freeb);
       t = mx + dlog1p(lds_lse_sum_excl<G, C, D, R>(x, freeb, mx)) - dlog(r);
     }
@@ -660,6 +685,7 @@ __device__ __forceinline__ ColThr<R> ent_family(const D* x, int m, int nvalid,
       break;
     }
   }
+  if constexpr (!NORM) scale = dexp(mx0 - t);
   return make_thr<R>(t, R(0), hi, NORM ? 2 : 1);
 }
 
@@ -989,12 +1015,15 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
 
   ColThr<R> th;
   int p = pp.p;
+  // exp(x - mx0) per slot and exp(mx0 - t) from the exp-map family.
+  R ecache[C];
+  R escale = 0;
   if constexpr (FAM == FAM_KNAP) {
     th = knap_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPK) {
     th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, col, lds_dummy);
   } else if constexpr (FAM == FAM_ENT) {
-    th = ent_family<KM == 1, G, C, D, R>(mine, m, nvalid, pp);
+    th = ent_family<KM == 1, G, C, D, R>(mine, m, nvalid, pp, ecache, escale);
   } else if constexpr (FAM == FAM_TOPKENT) {
     th = topkent_family<G, C, D, R>(v, m, nvalid, pp);
   } else {
@@ -1044,7 +1073,18 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
     };
     if constexpr (FAM == FAM_ENT) {
       if constexpr (KM == 0) {
-        write_rolled([&](D x) { return clamp_ref(dexp(x - t1), lo1, hi1); });
+        // The cached exp(x - mx0) may have underflowed where exp(x - t) does
+        // not when t < mx0 (after fixing, or for a large rhs); then the map
+        // is evaluated directly.
+        if (!th.slow && escale <= R(1)) {
+#pragma unroll
+          for (int c = 0; c < C; ++c) {
+            if (c < nvalid)
+              mine[G * c] = clamp_ref(static_cast<D>(ecache[c] * escale), lo1, hi1);
+          }
+        } else {
+          write_rolled([&](D x) { return clamp_ref(dexp(x - t1), lo1, hi1); });
+        }
       } else {
         write_rolled([&](D x) { return clamp_ref(lambert_w_exp(x - t1), lo1, hi1); });
       }
