@@ -589,6 +589,48 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
   // Householder iterations of order 4 (entropy_norm.h:84-102).
   const R ub = lds_masked_max<G, C, D, R>(x, bits) - num<R>::exp_min_arg();
   const R eps16 = R(16) * num<R>::eps();
+  if constexpr (sizeof(R) == 8) {
+    // The iteration converges to the root of sum W(exp(x - t)) = rhs from
+    // any start near it, and its stopping rule |dt| <= 16 eps is checked in
+    // double below; single-precision steps (about a third of the cost) bring
+    // t within ~1e-6 first, so the double loop needs two Lambert passes
+    // instead of about five.  The single-precision estimate is used only if
+    // its own steps settled.
+    float tf = static_cast<float>(t);
+    const float ubf = static_cast<float>(ub);
+    bool settled = false;
+    for (int iter = 0; iter < 4; ++iter) {
+      const float prev = tf;
+      const float tc = fminf(tf, ubf);
+      float f0 = 0, f1 = 0, f2 = 0, f3 = 0;
+#pragma unroll 1
+      for (int c = 0; c < C; ++c) {
+        if ((bits >> c) & 1u) {
+          const float w = lambert_w_exp(static_cast<float>(x[G * c]) - tc);
+          const float rd = div_near(1.0f, 1.0f + w);
+          const float rd2 = rd * rd;
+          const float rd3 = rd2 * rd;
+          f0 += w;
+          f1 += w * rd;
+          f2 += w * rd3;
+          f3 += w * (1.0f - 2.0f * w) * (rd3 * rd2);
+        }
+      }
+      f0 = group_sum<G>(f0);
+      f1 = group_sum<G>(f1);
+      f2 = group_sum<G>(f2);
+      f3 = group_sum<G>(f3);
+      f0 -= static_cast<float>(rhs);
+      const float f02 = f0 * f2, f11 = f1 * f1;
+      tf = tc - 3.0f * f0 * (2.0f * f11 - f02) / (6.0f * f1 * (f02 - f11) - f0 * (f0 * f3));
+      if (!(fabsf(tf) <= 3.0e38f)) break;
+      if (fabsf(prev - tf) <= 4.0e-6f * fmaxf(1.0f, fabsf(tf))) {
+        settled = true;
+        break;
+      }
+    }
+    if (settled) t = static_cast<R>(tf);
+  }
   for (int iter = 0; iter < 32; ++iter) {
     const R prev = t;
     const R tc = dmin(t, ub);
