@@ -48,7 +48,10 @@ hipError_t launch_one(const ProxLaunch& a) {
 // m = 200 on eight).
 template <int FAM, int KM, class D, class R>
 hipError_t launch_by_m(const ProxLaunch& a) {
-  if (a.m <= 16) return launch_one<FAM, KM, D, R, 1, 16>(a);
+#ifndef SDCA_M16_G
+#define SDCA_M16_G 1
+#endif
+  if (a.m <= 16) return launch_one<FAM, KM, D, R, SDCA_M16_G, 16 / SDCA_M16_G>(a);
   if (a.m <= 64) return launch_one<FAM, KM, D, R, 4, 16>(a);
 #ifndef SDCA_M100_G
 #define SDCA_M100_G 4

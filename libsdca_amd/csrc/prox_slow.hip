@@ -244,12 +244,15 @@ prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int
     for (int i = threadIdx.x; i < m; i += blockDim.x) dst[i] = clamp_ref(col[i] - t, lo, hi);
     __syncthreads();
   }
-  // List mode: the last workgroup to finish zeroes the list's counters
-  // [count, done] for the next call on the stream (every workgroup has read
-  // the count before it increments done).
-  if (!all_columns && threadIdx.x == 0) {
+  // List mode: the list's counters [count, done] must be zero for the next
+  // call on the stream.  With an empty list they already are; otherwise the
+  // min(grid, count) workgroups that took columns count themselves out and
+  // the last of them zeroes both (each has read the count before it
+  // increments done).
+  const int64_t workers = count < static_cast<int64_t>(gridDim.x) ? count : gridDim.x;
+  if (!all_columns && static_cast<int64_t>(blockIdx.x) < workers && threadIdx.x == 0) {
     __threadfence();
-    if (atomicAdd(slow + 1, 1) == static_cast<int>(gridDim.x) - 1) {
+    if (atomicAdd(slow + 1, 1) == static_cast<int>(workers) - 1) {
       atomicExch(slow, 0);
       atomicExch(slow + 1, 0);
     }

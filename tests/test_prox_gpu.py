@@ -220,3 +220,19 @@ def test_out_of_place(cuda, oracle):
     torch.cuda.synchronize()
     assert np.array_equal(t.cpu().numpy(), x), "input modified by an out-of-place call"
     parity(oracle, "knapsack_eq", x, o.cpu().numpy(), F64, "out of place knapsack_eq")
+
+
+def test_deferred_list_reuse(cuda, oracle):
+    """Consecutive calls on one stream share the deferred-column list, whose
+    counters the deferred-column kernel resets: a call with many deferred
+    columns (top-k cone with one dominant entry per column: the cone search
+    with U non-empty), a smaller one, then one with none, each against the
+    oracle."""
+    rng = np.random.default_rng(77)
+    for n in (5000, 300, 4000):
+        x = rng.standard_normal((n, 50)).astype(np.float32)
+        if n != 4000:
+            x[np.arange(n), rng.integers(0, 50, n)] += 40.0
+        for op in ("topk_cone", "topk_simplex"):
+            got, _ = run_gpu(op, x, F32, cuda, k=5)
+            parity(oracle, op, x, got, F32, f"{op} n={n}", k=5)
