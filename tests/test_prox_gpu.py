@@ -236,3 +236,35 @@ def test_deferred_list_reuse(cuda, oracle):
         for op in ("topk_cone", "topk_simplex"):
             got, _ = run_gpu(op, x, F32, cuda, k=5)
             parity(oracle, op, x, got, F32, f"{op} n={n}", k=5)
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [2049, 3000, 4096])
+@pytest.mark.parametrize("op,kw", [
+    ("knapsack_eq", dict(lo=0.0, hi=1.0, rhs=1.0)),
+    ("knapsack_le", dict(lo=-0.5, hi=0.3, rhs=2.0)),
+    ("topk_simplex", dict(k=5, rhs=1.0)),
+    ("topk_cone", dict(k=3)),
+])
+def test_large_m_workgroup_per_column(cuda, oracle, op, kw, m, dtype, result):
+    """m beyond the register kernel (2048): one workgroup per column, the
+    column sorted in LDS."""
+    n = 40
+    for name, x in [("normal", inputs.normal(n, m, dtype, 90 + m)),
+                    ("label+2", inputs.label_shifted(n, m, dtype, 91 + m)),
+                    ("edge", inputs.edge_columns(m, dtype, 92 + m))]:
+        got, _ = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
+
+
+def test_large_m_limits(cuda):
+    """Sizes past the workgroup-per-column kernel's LDS, and the operators
+    without it, are refused with SDCA_ERR_NOT_IMPLEMENTED (4)."""
+    import torch
+    import libsdca_amd as sd
+    for op, m, dt in [("topk_simplex", 8193, torch.float32), ("knapsack_eq", 4097, torch.float64),
+                      ("entropy", 2049, torch.float64), ("two_simplex", 2049, torch.float32)]:
+        x = torch.zeros((3, m), dtype=dt, device=cuda)
+        with pytest.raises(sd.SdcaError) as e:
+            sd.prox(op, x, k=5, p=1)
+        assert e.value.status == 4, op
