@@ -221,37 +221,6 @@ __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
 // list of KM + 1 entries per lane (median-of-three insertion), merged across
 // the group; k <= KM.
 // ---------------------------------------------------------------------------
-template <class R>
-struct TopkSel {
-  R sum_k;   // sum of the k largest (in descending order)
-  R kth;     // k-th largest
-  R next;    // (k+1)-th largest, -inf if k == m
-  R first;   // largest
-};
-
-template <int G, int C, int KM, class D, class R>
-__device__ inline TopkSel<R> topk_select(const D (&v)[C], int nvalid, int k) {
-  constexpr int L = KM + 1;
-  D top[L];
-#pragma unroll
-  for (int i = 0; i < L; ++i) top[i] = -num<D>::inf();
-#pragma unroll
-  for (int c = 0; c < C; ++c) top_insert(top, v[c]);  // -inf padding leaves it unchanged
-  top_merge<G>(top);
-  TopkSel<R> s;
-  s.sum_k = 0;
-  s.kth = static_cast<R>(top[0]);
-  s.next = -num<R>::inf();
-  s.first = static_cast<R>(top[0]);
-#pragma unroll
-  for (int i = 0; i < L; ++i) {
-    if (i < k) s.sum_k += static_cast<R>(top[i]);
-    if (i == k - 1) s.kth = static_cast<R>(top[i]);
-    if (i == k) s.next = static_cast<R>(top[i]);
-  }
-  return s;
-}
-
 // topk_cone_search (topk_cone.h:58-133) when the answer has U empty: then
 // t = 0 exactly, M = {x > 16 eps} and hi = k sum(M) / k^2; valid if
 // hi >= max(M) - 16 eps.  Any other outcome (U non-empty, or values within
@@ -282,69 +251,6 @@ __device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
   return slow_thr<R>();
 }
 
-// Variable fixing over the first cnt entries of a sorted register list
-// (compile-time length L, so the list stays in registers).
-template <int L, class D, class R>
-__device__ inline KnapState<R> knapsack_top(const D (&b)[L], int cnt, R lo, R hi, R rhs) {
-  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
-  R total = 0;
-#pragma unroll
-  for (int i = 0; i < L; ++i) total += (i < cnt) ? static_cast<R>(b[i]) : R(0);
-  int mc = cnt;
-  R t = (total - rhs) / static_cast<R>(cnt);
-  KnapState<R> st;
-  st.lo_cut = -num<R>::inf();
-  st.hi_cut = num<R>::inf();
-  st.c_lo = -num<R>::inf();
-  st.c_hi = num<R>::inf();
-  st.n_u = 0;
-  st.sum_u = 0;
-  for (int iter = 0; iter <= L; ++iter) {
-    const R c_lo = lo + t, c_hi = hi + t;
-    R s_lo = 0, s_hi = 0;
-    int n_lo = 0, n_hi = 0;
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const R x = static_cast<R>(b[i]);
-      const bool fr = (i < cnt) && (x > st.lo_cut) && !(x > st.hi_cut);
-      const bool gl = x > c_lo;
-      const bool lo_c = fr && !gl, hi_c = fr && gl && x > c_hi;
-      s_lo += lo_c ? x : R(0);
-      n_lo += lo_c ? 1 : 0;
-      s_hi += hi_c ? x : R(0);
-      n_hi += hi_c ? 1 : 0;
-    }
-    const R sh = static_cast<R>(n_hi) * hi;
-    const R sl = static_cast<R>(n_lo) * lo;
-    const R infeas = s_hi + s_lo - (sh + sl) - static_cast<R>(n_hi + n_lo) * t;
-    R next;
-    if (n_hi > 0 && infeas > eps) {
-      st.hi_cut = dmin(st.hi_cut, dmax(c_lo, c_hi));
-      next = static_cast<R>(mc) * t - s_hi + sh;
-      mc -= n_hi;
-      st.n_u += n_hi;
-      st.sum_u += s_hi;
-    } else if (n_lo > 0 && infeas < -eps) {
-      st.lo_cut = dmax(st.lo_cut, c_lo);
-      next = static_cast<R>(mc) * t - s_lo + sl;
-      mc -= n_lo;
-    } else {
-      st.c_lo = c_lo;
-      st.c_hi = c_hi;
-      st.n_u += n_hi;
-      st.sum_u += s_hi;
-      break;
-    }
-    if (mc > 0) {
-      t = next / static_cast<R>(mc);
-    } else {
-      break;
-    }
-  }
-  st.t = t;
-  return st;
-}
-
 // Candidate slots per lane for the top-k simplex's knapsack: the group holds
 // up to G * kCandSlots<G> candidates in registers; columns with more run the
 // variable fixing over all register slots instead.
@@ -370,16 +276,6 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
                                              D* lds_dummy) {
   const R slack = (fabs(kth) + hi) * (R(16) * num<R>::eps());
   const R cut = kth - hi - slack;
-#ifndef SDCA_TOPK_LIST_KNAPSACK
-#define SDCA_TOPK_LIST_KNAPSACK 0
-#endif
-  // When every value above the cut is in the sorted top list, solve there.
-  if (SDCA_TOPK_LIST_KNAPSACK && !(static_cast<R>(top[L - 1]) > cut)) {
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < L; ++i) cnt += (static_cast<R>(top[i]) > cut) ? 1 : 0;
-    return knapsack_top<L, D, R>(top, cnt, R(0), hi, rhs);
-  }
   if constexpr (G > 1) {
     constexpr int CC = kCandSlots<G>;
     int cn = 0;
