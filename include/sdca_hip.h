@@ -59,11 +59,11 @@ typedef enum sdca_prox_op {
   SDCA_PROX_TOPK_ENTROPY = 6,  /* topk_entropy.h:106-118 */
   SDCA_PROX_TWO_SIMPLEX = 7,   /* two_simplex.h:183-196 */
   SDCA_PROX_LAMBERT_W_EXP = 8, /* apply(dim, ..., lambert_w_exp_map), proxdef.h:386-400 */
+  SDCA_PROX_KNAPSACK_LE_BIASED = 9,   /* knapsack_le_biased.h:165-180 (uses rho) */
+  SDCA_PROX_TOPK_SIMPLEX_BIASED = 10, /* topk_simplex_biased.h:105-119 (uses rho) */
+  SDCA_PROX_TOPK_CONE_BIASED = 11,    /* topk_cone_biased.h:145-158 (uses rho) */
   /* Operators of the same front end that are not on this path yet:
    * they return SDCA_ERR_NOT_IMPLEMENTED. */
-  SDCA_PROX_KNAPSACK_LE_BIASED = 9,
-  SDCA_PROX_TOPK_SIMPLEX_BIASED = 10,
-  SDCA_PROX_TOPK_CONE_BIASED = 11,
   SDCA_PROX_TOPK_ENTROPY_BIASED = 12,
   SDCA_PROX_TWO_SIMPLEX_SORT = 13
 } sdca_prox_op;

@@ -151,6 +151,41 @@ inline void prox_two_simplex(std::ptrdiff_t dim, std::ptrdiff_t p_split, Data* f
   detail::run<Result>(SDCA_PROX_TWO_SIMPLEX, dim, first, last, p);
 }
 
+// knapsack_le_biased.h:165-180
+template <typename Result = double, typename Data>
+inline void prox_knapsack_le_biased(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                                    const Result lo = 0, const Result hi = 1,
+                                    const Result rhs = 1, const Result rho = 1) {
+  sdca_prox_params p = detail::params();
+  p.lo = static_cast<double>(lo);
+  p.hi = static_cast<double>(hi);
+  p.rhs = static_cast<double>(rhs);
+  p.rho = static_cast<double>(rho);
+  detail::run<Result>(SDCA_PROX_KNAPSACK_LE_BIASED, dim, first, last, p);
+}
+
+// topk_simplex_biased.h:105-119
+template <typename Result = double, typename Data>
+inline void prox_topk_simplex_biased(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                                     const std::ptrdiff_t k = 1, const Result rhs = 1,
+                                     const Result rho = 1) {
+  sdca_prox_params p = detail::params();
+  p.k = k;
+  p.rhs = static_cast<double>(rhs);
+  p.rho = static_cast<double>(rho);
+  detail::run<Result>(SDCA_PROX_TOPK_SIMPLEX_BIASED, dim, first, last, p);
+}
+
+// topk_cone_biased.h:145-158
+template <typename Result = double, typename Data>
+inline void prox_topk_cone_biased(std::ptrdiff_t dim, Data* first, Data* last, Data* /*aux*/,
+                                  const std::ptrdiff_t k = 1, const Result rho = 1) {
+  sdca_prox_params p = detail::params();
+  p.k = k;
+  p.rho = static_cast<double>(rho);
+  detail::run<Result>(SDCA_PROX_TOPK_CONE_BIASED, dim, first, last, p);
+}
+
 // apply(dim, first, last, lambert_w_exp_map<Data>()) (proxdef.h:386-400)
 template <typename Data>
 inline void apply_lambert_w_exp(std::ptrdiff_t dim, Data* first, Data* last) {

@@ -228,6 +228,18 @@ def prox_two_simplex(dim, p, A, rhs=1.0, result=None):
     return prox("two_simplex", _rows(dim, A), p=p, rhs=rhs, result=result)
 
 
+def prox_knapsack_le_biased(dim, A, lo=0.0, hi=1.0, rhs=1.0, rho=1.0, result=None):
+    return prox("knapsack_le_biased", _rows(dim, A), lo=lo, hi=hi, rhs=rhs, rho=rho, result=result)
+
+
+def prox_topk_simplex_biased(dim, A, k=1, rhs=1.0, rho=1.0, result=None):
+    return prox("topk_simplex_biased", _rows(dim, A), k=k, rhs=rhs, rho=rho, result=result)
+
+
+def prox_topk_cone_biased(dim, A, k=1, rho=1.0, result=None):
+    return prox("topk_cone_biased", _rows(dim, A), k=k, rho=rho, result=result)
+
+
 def lambert_w_exp(A):
     """Elementwise W(exp(x)) in place (apply(dim, ..., lambert_w_exp_map))."""
     return prox("lambert_w_exp", A if A.ndim == 2 else A.reshape(1, -1))

@@ -139,9 +139,11 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   else sdca_prox_params_default(&p);
   if (static_cast<int>(op) < 0 || op > SDCA_PROX_TWO_SIMPLEX_SORT)
     return fail(SDCA_ERR_PROX, "unknown prox operator %d", static_cast<int>(op));
-  if (op > SDCA_PROX_LAMBERT_W_EXP)
+  if (op == SDCA_PROX_TOPK_ENTROPY_BIASED || op == SDCA_PROX_TWO_SIMPLEX_SORT)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "prox operator %d is not implemented on the GPU",
                 static_cast<int>(op));
+  const bool biased = op == SDCA_PROX_KNAPSACK_LE_BIASED || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
+                      op == SDCA_PROX_TOPK_CONE_BIASED;
   int rc = check_dtypes(data, result);
   if (rc) return rc;
   if (m < 1) return fail(SDCA_ERR_ARG_RANGE, "m must be >= 1 (got %lld)", (long long)m);
@@ -153,7 +155,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   if (!(p.rho >= 0)) return fail(SDCA_ERR_ARG_RANGE, "rho must be >= 0 (got %g)", p.rho);
   if (!(p.alpha > 0)) return fail(SDCA_ERR_ARG_RANGE, "alpha must be > 0 (got %g)", p.alpha);
   const bool uses_k = op == SDCA_PROX_TOPK_SIMPLEX || op == SDCA_PROX_TOPK_CONE ||
-                      op == SDCA_PROX_TOPK_ENTROPY;
+                      op == SDCA_PROX_TOPK_ENTROPY || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
+                      op == SDCA_PROX_TOPK_CONE_BIASED;
   if (uses_k && (p.k < 1 || p.k > m))
     return fail(SDCA_ERR_ARG_RANGE, "k must be in [1, %lld] (got %lld)", (long long)m, (long long)p.k);
   if (op == SDCA_PROX_TWO_SIMPLEX) {
@@ -176,10 +179,13 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   const bool reg_ok = m <= kRegMaxM;
   const bool topk = op == SDCA_PROX_TOPK_SIMPLEX || op == SDCA_PROX_TOPK_CONE;
   const bool knap = op == SDCA_PROX_KNAPSACK_EQ || op == SDCA_PROX_KNAPSACK_LE;
-  if (!reg_ok && !(topk || knap) && op != SDCA_PROX_LAMBERT_W_EXP)
+  if (!reg_ok && !(topk || knap || biased) && op != SDCA_PROX_LAMBERT_W_EXP)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "operator %d supports m <= %lld on the GPU (got %lld)",
                 static_cast<int>(op), (long long)kRegMaxM, (long long)m);
   if ((topk || knap) && m > slow_max_m(data) && (!reg_ok || (topk && p.k > kTopkMaxK)))
+    return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
+                (long long)m, (long long)slow_max_m(data));
+  if (biased && m > slow_max_m(data))
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
                 (long long)m, (long long)slow_max_m(data));
 
@@ -226,6 +232,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   a.lo = p.lo;
   a.hi = p.hi;
   a.rhs = p.rhs;
+  a.rho = p.rho;
   a.k = p.k;
   a.p = p.p;
   a.col_p = d_colp;
@@ -235,7 +242,10 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
 
   if (op == SDCA_PROX_LAMBERT_W_EXP) {
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
-  } else if ((topk || knap) && (!reg_ok || (topk && p.k > kTopkMaxK))) {
+  } else if (biased || ((topk || knap) && (!reg_ok || (topk && p.k > kTopkMaxK)))) {
+    // The biased operators' searches need the sorted column: one workgroup
+    // per column (knapsack_le_biased.h, topk_simplex_biased.h,
+    // topk_cone_biased.h).
     SDCA_HIP_TRY(launch_slow(a, true), "prox kernel (workgroup per column)");
   } else {
     // Deferred-column list: [count, done, column ids...].  The deferred-column

@@ -18,6 +18,7 @@ hipError_t launch_one(const ProxLaunch& a) {
   pp.lo = static_cast<R>(a.lo);
   pp.hi = static_cast<R>(a.hi);
   pp.rhs = static_cast<R>(a.rhs);
+  pp.rho = R(0);
   pp.k = static_cast<int>(a.k);
   pp.op = a.op;
   pp.p = static_cast<int>(a.p);

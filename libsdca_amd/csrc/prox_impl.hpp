@@ -34,6 +34,7 @@ enum Family { FAM_KNAP = 0, FAM_TOPK = 1, FAM_ENT = 2, FAM_TOPKENT = 3, FAM_TWO 
 template <class R>
 struct ProxParamsT {
   R lo, hi, rhs;
+  R rho;  // biased operators only (0 for the others)
   int k;
   int op;
   int p;

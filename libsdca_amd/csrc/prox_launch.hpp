@@ -18,7 +18,10 @@ enum {
   OP_ENTROPY_NORM = SDCA_PROX_ENTROPY_NORM,
   OP_TOPK_ENTROPY = SDCA_PROX_TOPK_ENTROPY,
   OP_TWO_SIMPLEX = SDCA_PROX_TWO_SIMPLEX,
-  OP_LAMBERT_W_EXP = SDCA_PROX_LAMBERT_W_EXP
+  OP_LAMBERT_W_EXP = SDCA_PROX_LAMBERT_W_EXP,
+  OP_KNAPSACK_LE_BIASED = SDCA_PROX_KNAPSACK_LE_BIASED,
+  OP_TOPK_SIMPLEX_BIASED = SDCA_PROX_TOPK_SIMPLEX_BIASED,
+  OP_TOPK_CONE_BIASED = SDCA_PROX_TOPK_CONE_BIASED
 };
 
 // Largest m handled by the register kernels.
@@ -34,7 +37,7 @@ struct ProxLaunch {
   int64_t m, n;
   const void* in;
   void* out;
-  double lo, hi, rhs;
+  double lo, hi, rhs, rho;
   int64_t k, p;
   const int64_t* col_p;     // device, or NULL
   sdca_thresholds* thr;     // device, or NULL

@@ -83,12 +83,15 @@ __device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
   return st;
 }
 
-// topk_cone_search (topk_cone.h:58-133) on the sorted column.
+// topk_cone_search (topk_cone.h:58-133) and its biased form
+// thresholds_topk_cone_biased_search (topk_cone_biased.h:9-106) on the sorted
+// column: the latter starts the |U| + rho k^2 term at rho k^2 (rho = 0 gives
+// the former's steps exactly).
 template <class D, class R>
-__device__ void cone_search_sorted(const D* s, int m, int k, R& t_out, R& hi_out) {
+__device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R& hi_out) {
   R k_u = static_cast<R>(k);
   R min_u = num<R>::inf();
-  R num_u = 0, sum_u = 0;
+  R num_u = rho * static_cast<R>(k) * static_cast<R>(k), sum_u = 0;
   const R eps = R(16) * num<R>::eps();
   for (int mf = 0;;) {
     R min_m = num<R>::inf();
@@ -126,13 +129,75 @@ __device__ void cone_search_sorted(const D* s, int m, int k, R& t_out, R& hi_out
   hi_out = 0;
 }
 
+// thresholds_knapsack_le_biased_search (knapsack_le_biased.h:10-92) on the
+// sorted column: grow U, and for each U grow M, until the candidate t
+// satisfies the reference's interval tests; default 0.
 template <class D, class R>
-__device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, int k,
+__device__ void knapsack_le_biased_sorted(const D* s, int m, R lo, R hi, R rhs, R rho,
+                                          R& t_out, R& lo_out, R& hi_out) {
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  const R rho_rhs = rho * rhs;
+  const R rho_inv = R(1) / rho;
+  const R num_x = static_cast<R>(m);
+  R num_u = 0, min_u = num<R>::inf();
+  for (int mf = 0;;) {
+    R min_m = num<R>::inf();
+    R max_m = -num<R>::inf();
+    R num_m = 0, sum_m = 0;
+    R num_l = num_x - num_u;
+    for (int ml = mf;;) {
+      const R t = (lo * num_l + hi * num_u + sum_m) / (rho_inv + num_m);
+      if (t <= rho_rhs + eps) {
+        R tt = hi + t;
+        if (max_m - eps <= tt && tt <= min_u + eps) {
+          tt = lo + t;
+          if (tt <= min_m + eps && (ml == m || static_cast<R>(s[ml]) - eps <= tt)) {
+            t_out = t;
+            lo_out = lo;
+            hi_out = hi;
+            return;
+          }
+        }
+      }
+      if (ml == m) break;
+      min_m = static_cast<R>(s[ml]);
+      max_m = static_cast<R>(s[mf]);
+      sum_m += min_m;
+      num_l -= R(1);
+      num_m += R(1);
+      ++ml;
+    }
+    if (mf == m) break;
+    min_u = static_cast<R>(s[mf]);
+    num_u += R(1);
+    ++mf;
+  }
+  t_out = 0;
+  lo_out = 0;
+  hi_out = 0;
+}
+
+template <class D, class R>
+__device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, R rho, int k,
                                   R& t_out, R& lo_out, R& hi_out) {
-  if (op == OP_KNAPSACK_EQ || op == OP_KNAPSACK_LE) {
+  if (op == OP_KNAPSACK_LE_BIASED && rho != R(0)) {
+    // knapsack_le_biased.h:102-130: the equality solution if its t is at
+    // least rho rhs, else the search.
     lo_out = lo;
     hi_out = hi;
-    if (op == OP_KNAPSACK_LE) {
+    const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+    const R t = knapsack_sorted<D, R>(s, m, lo, hi, rhs).t;
+    if (t >= rho * rhs - eps) {
+      t_out = t;
+      return;
+    }
+    knapsack_le_biased_sorted<D, R>(s, m, lo, hi, rhs, rho, t_out, lo_out, hi_out);
+    return;
+  }
+  if (op == OP_KNAPSACK_EQ || op == OP_KNAPSACK_LE || op == OP_KNAPSACK_LE_BIASED) {
+    lo_out = lo;
+    hi_out = hi;
+    if (op != OP_KNAPSACK_EQ) {  // knapsack_le, and knapsack_le_biased with rho = 0
       // knapsack_le.h:30-46 on the sorted column
       const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
       int n_hi = 0;
@@ -156,16 +221,18 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
     t_out = 0; lo_out = 0; hi_out = 0;
     return;
   }
-  const R hi_c = sum_k / K;
+  // topk_cone_special_cases with divisor K (+ rho K^2 for the biased forms,
+  // topk_cone_biased.h:117, topk_simplex_biased.h:53).
+  const R hi_c = sum_k / (K + rho * K * K);
   const R t_c = static_cast<R>(s[k - 1]) - hi_c;
   const bool constant = (k == m) || (t_c >= static_cast<R>(s[k]) - eps16);
   lo_out = 0;
-  if (op == OP_TOPK_CONE) {
+  if (op == OP_TOPK_CONE || op == OP_TOPK_CONE_BIASED) {
     if (constant) {
       t_out = t_c;
       hi_out = hi_c;
     } else {
-      cone_search_sorted<D, R>(s, m, k, t_out, hi_out);
+      cone_search_sorted<D, R>(s, m, k, rho, t_out, hi_out);
     }
     return;
   }
@@ -177,15 +244,17 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
   }
   KnapState<R> st = knapsack_sorted<D, R>(s, m, R(0), rhs / K, rhs);
   if (!constant) {
+    // is_topk_simplex_lt (topk_simplex.h:9-27) / is_topk_simplex_biased_lt
+    // (topk_simplex_biased.h:9-28); rho = 0 gives the former exactly.
     bool lt;
     if (st.n_u == 0) {
-      lt = st.t < -eps;
+      lt = st.t < rho * rhs - eps;
     } else {
       const R num_u = static_cast<R>(st.n_u);
-      lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * num_u - eps;
+      lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * (num_u + rho * K * K) - eps;
     }
     if (lt) {
-      cone_search_sorted<D, R>(s, m, k, t_out, hi_out);
+      cone_search_sorted<D, R>(s, m, k, rho, t_out, hi_out);
       return;
     }
   }
@@ -228,7 +297,7 @@ prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int
     }
     if (threadIdx.x == 0) {
       R t, lo, hi;
-      thresholds_sorted<D, R>(s, m, pp.op, pp.lo, pp.hi, pp.rhs, pp.k, t, lo, hi);
+      thresholds_sorted<D, R>(s, m, pp.op, pp.lo, pp.hi, pp.rhs, pp.rho, pp.k, t, lo, hi);
       sh_t = t;
       sh_lo = lo;
       sh_hi = hi;
@@ -265,6 +334,9 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   pp.lo = static_cast<R>(a.lo);
   pp.hi = static_cast<R>(a.hi);
   pp.rhs = static_cast<R>(a.rhs);
+  const bool biased = a.op == OP_KNAPSACK_LE_BIASED || a.op == OP_TOPK_SIMPLEX_BIASED ||
+                      a.op == OP_TOPK_CONE_BIASED;
+  pp.rho = biased ? static_cast<R>(a.rho) : R(0);
   pp.k = static_cast<int>(a.k);
   pp.op = a.op;
   pp.p = static_cast<int>(a.p);

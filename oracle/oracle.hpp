@@ -340,6 +340,152 @@ inline thr<R, It> topk_simplex(It first, It last, std::ptrdiff_t k, R rhs) {
 }
 
 // ---------------------------------------------------------------------------
+// Biased top-k cone and simplex, min 0.5 (<x,x> + rho <1,x>^2) - <a,x>
+// (topk_cone_biased.h:9-137, topk_simplex_biased.h:9-71).
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline thr<R, It> cone_biased_search(It first, It last, std::ptrdiff_t k, R rho) {
+  typedef typename std::iterator_traits<It>::value_type D;
+  std::sort(first, last, std::greater<D>());
+  It k_last = first + k;
+  R k_u = static_cast<R>(k);                                  // k - |U|
+  R nu_rho = rho * static_cast<R>(k) * static_cast<R>(k);     // |U| + rho k^2
+  R min_u = +std::numeric_limits<R>::infinity();
+  R sum_u = 0;
+  const R eps = 16 * std::numeric_limits<R>::epsilon();
+  for (It mf = first;;) {
+    R min_m = +std::numeric_limits<R>::infinity();
+    R max_m = -std::numeric_limits<R>::infinity();
+    R sum_m = 0, num_m_sum_u = 0;
+    R den = k_u * k_u;
+    R k_u_sum_u = k_u * sum_u;
+    for (It ml = mf;;) {
+      R t = (nu_rho * sum_m - k_u_sum_u) / den;
+      R hi = (num_m_sum_u + k_u * sum_m) / den;
+      R tt = hi + t;
+      if (max_m - eps <= tt && tt <= min_u + eps) {
+        if (t <= min_m + eps &&
+            ((ml == last) || static_cast<R>(*ml) - eps <= t)) {
+          return make_thr(t, static_cast<R>(0), hi, mf, ml);
+        }
+      }
+      if (ml == last) break;
+      min_m = static_cast<R>(*ml);
+      max_m = static_cast<R>(*mf);
+      sum_m += min_m;
+      num_m_sum_u += sum_u;
+      den += nu_rho;
+      ++ml;
+    }
+    if (mf == k_last) break;
+    min_u = static_cast<R>(*mf);
+    sum_u += min_u;
+    --k_u;
+    ++nu_rho;
+    ++mf;
+  }
+  return make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                  first, first);
+}
+
+template <class R, class It>
+inline thr<R, It> topk_cone_biased(It first, It last, std::ptrdiff_t k, R rho) {
+  const R K = static_cast<R>(k);
+  thr<R, It> out;
+  if (cone_special_cases(first, last, k, K + rho * K * K, out) == proj::general)
+    return cone_biased_search<R>(first, last, k, rho);
+  return out;
+}
+
+template <class R, class It>
+inline bool topk_simplex_biased_lt(It u_first, It u_last, R t, R k, R rhs, R rho, R eps) {
+  if (u_first == u_last) return t < rho * rhs - eps;
+  R num_u = static_cast<R>(std::distance(u_first, u_last));
+  R sum_u = std::accumulate(u_first, u_last, static_cast<R>(0));
+  return k * (sum_u + (k - num_u) * t) < rhs * (num_u + rho * k * k) - eps;
+}
+
+template <class R, class It>
+inline thr<R, It> topk_simplex_biased(It first, It last, std::ptrdiff_t k, R rhs, R rho) {
+  const R K = static_cast<R>(k), lo = 0;
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), std::abs(rhs));
+  thr<R, It> out;
+  switch (cone_special_cases(first, last, k, K + rho * K * K, out)) {
+    case proj::zero:
+      break;
+    case proj::constant:
+      if (K * out.hi > rhs + eps) return knapsack_eq(first, last, lo, rhs / K, rhs);
+      break;
+    case proj::general: {
+      thr<R, It> t = knapsack_eq(first, last, lo, rhs / K, rhs);
+      if (topk_simplex_biased_lt(first, t.first, t.t, K, rhs, rho, eps))
+        return cone_biased_search<R>(first, last, k, rho);
+      return t;
+    }
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Biased inequality knapsack, min 0.5 (<x,x> + rho <1,x>^2) - <a,x>,
+// <1,x> <= rhs, lo <= x <= hi (knapsack_le_biased.h:10-130).
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline thr<R, It> knapsack_le_biased_search(It first, It last, R lo, R hi, R rhs, R rho) {
+  typedef typename std::iterator_traits<It>::value_type D;
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), std::abs(rhs));
+  std::sort(first, last, std::greater<D>());
+  const R rho_rhs = rho * rhs;
+  const R rho_inv = static_cast<R>(1) / rho;
+  const R num_x = static_cast<R>(std::distance(first, last));
+  R num_u = 0, min_u = +std::numeric_limits<R>::infinity();
+  for (It mf = first;;) {
+    R min_m = +std::numeric_limits<R>::infinity();
+    R max_m = -std::numeric_limits<R>::infinity();
+    R num_m = 0, sum_m = 0;
+    R num_l = num_x - num_u;
+    for (It ml = mf;;) {
+      R t = (lo * num_l + hi * num_u + sum_m) / (rho_inv + num_m);
+      if (t <= rho_rhs + eps) {
+        R tt = hi + t;
+        if (max_m - eps <= tt && tt <= min_u + eps) {
+          tt = lo + t;
+          if (tt <= min_m + eps &&
+              ((ml == last) || static_cast<R>(*ml) - eps <= tt)) {
+            return make_thr(t, lo, hi, mf, ml);
+          }
+        }
+      }
+      if (ml == last) break;
+      min_m = static_cast<R>(*ml);
+      max_m = static_cast<R>(*mf);
+      sum_m += min_m;
+      --num_l;
+      ++num_m;
+      ++ml;
+    }
+    if (mf == last) break;
+    min_u = static_cast<R>(*mf);
+    ++num_u;
+    ++mf;
+  }
+  return make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                  first, first);
+}
+
+template <class R, class It>
+inline thr<R, It> knapsack_le_biased(It first, It last, R lo, R hi, R rhs, R rho) {
+  if (rho == 0) return knapsack_le(first, last, lo, hi, rhs);
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), std::abs(rhs));
+  thr<R, It> t = knapsack_eq(first, last, lo, hi, rhs);
+  if (t.t >= rho * rhs - eps) return t;
+  return knapsack_le_biased_search(first, last, lo, hi, rhs, rho);
+}
+
+// ---------------------------------------------------------------------------
 // Entropic projections (entropy.h:19-53, entropy_norm.h:15-183).
 // ---------------------------------------------------------------------------
 template <class R, class It>

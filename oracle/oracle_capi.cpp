@@ -45,7 +45,7 @@ template <class D, class R>
 int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
               const int64_t* col_p, sdca_thresholds* thr_out, int nthreads) {
   const R lo = static_cast<R>(p->lo), hi = static_cast<R>(p->hi),
-          rhs = static_cast<R>(p->rhs);
+          rhs = static_cast<R>(p->rhs), rho = static_cast<R>(p->rho);
   const std::ptrdiff_t k = static_cast<std::ptrdiff_t>(p->k);
   if (op == SDCA_PROX_LAMBERT_W_EXP) {  // apply(dim, ..., lambert_w_exp_map<Data>)
     parallel_for(m * n, nthreads, [&](int64_t b, int64_t e, int) {
@@ -84,6 +84,11 @@ int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
         case SDCA_PROX_ENTROPY: t = orc::entropy(a, a_end, hi, rhs); break;
         case SDCA_PROX_ENTROPY_NORM: t = orc::entropy_norm(a, a_end, hi, rhs); break;
         case SDCA_PROX_TOPK_ENTROPY: t = orc::topk_entropy<R>(a, a_end, k); break;
+        case SDCA_PROX_KNAPSACK_LE_BIASED:
+          t = orc::knapsack_le_biased(a, a_end, lo, hi, rhs, rho); break;
+        case SDCA_PROX_TOPK_SIMPLEX_BIASED:
+          t = orc::topk_simplex_biased<R>(a, a_end, k, rhs, rho); break;
+        case SDCA_PROX_TOPK_CONE_BIASED: t = orc::topk_cone_biased<R>(a, a_end, k, rho); break;
         default: break;
       }
       orc::clamp(t, col, col + m);

@@ -58,6 +58,7 @@ template <class D, class R>
 void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_params* p,
              const int64_t* col_p) {
   const R lo = static_cast<R>(p->lo), hi = static_cast<R>(p->hi), rhs = static_cast<R>(p->rhs);
+  const R rho = static_cast<R>(p->rho);
   const std::ptrdiff_t k = static_cast<std::ptrdiff_t>(p->k);
   switch (op) {
     case SDCA_PROX_KNAPSACK_EQ: sdca::prox_knapsack_eq(m, first, last, aux, lo, hi, rhs); break;
@@ -78,6 +79,11 @@ void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_param
       }
       break;
     case SDCA_PROX_LAMBERT_W_EXP: sdca::apply(m, first, last, sdca::lambert_w_exp_map<D>()); break;
+    case SDCA_PROX_KNAPSACK_LE_BIASED:
+      sdca::prox_knapsack_le_biased(m, first, last, aux, lo, hi, rhs, rho); break;
+    case SDCA_PROX_TOPK_SIMPLEX_BIASED:
+      sdca::prox_topk_simplex_biased(m, first, last, aux, k, rhs, rho); break;
+    case SDCA_PROX_TOPK_CONE_BIASED: sdca::prox_topk_cone_biased(m, first, last, aux, k, rho); break;
     default: break;
   }
 }
@@ -87,6 +93,7 @@ template <class D, class R>
 void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
                      const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* out) {
   const R lo = static_cast<R>(p->lo), hi = static_cast<R>(p->hi), rhs = static_cast<R>(p->rhs);
+  const R rho = static_cast<R>(p->rho);
   const std::ptrdiff_t k = static_cast<std::ptrdiff_t>(p->k);
   for (int64_t j = b; j < e; ++j) {
     D* col = x + j * m;
@@ -130,6 +137,18 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
         put(out, 2 * j, t.first);
         put(out, 2 * j + 1, t.second);
         break;
+      }
+      case SDCA_PROX_KNAPSACK_LE_BIASED: {
+        auto t = sdca::thresholds_knapsack_le_biased(aux, al, lo, hi, rhs, rho);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_TOPK_SIMPLEX_BIASED: {
+        auto t = sdca::thresholds_topk_simplex_biased(aux, al, k, rhs, rho);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_TOPK_CONE_BIASED: {
+        auto t = sdca::thresholds_topk_cone_biased(aux, al, k, rho);
+        sdca::prox(t, col, col + m); put(out, j, t); break;
       }
       default: break;
     }

@@ -111,6 +111,9 @@ int main() {
   sdca::hip::prox_topk_entropy(10, d, d + b.size(), bux.data(), 2);
   sdca::hip::prox_two_simplex(10, 3, d, d + b.size(), bux.data(), 1.0);
   sdca::hip::apply_lambert_w_exp(10, d, d + b.size());
+  sdca::hip::prox_knapsack_le_biased(10, d, d + b.size(), bux.data(), 0.0, 1.0, 1.0, 0.5);
+  sdca::hip::prox_topk_simplex_biased(100, f, f + a.size(), aux.data(), 5, 1.0f, 0.5f);
+  sdca::hip::prox_topk_cone_biased(100, f, f + a.size(), aux.data(), 5, 0.5f);
   std::vector<sdca_objective> objs(1);
   objs[0].kind = SDCA_OBJ_ENTROPY; objs[0].c = 1; objs[0].gamma = 1; objs[0].k = 1;
   std::vector<int64_t> y(4, 0);

@@ -371,3 +371,71 @@ def test_eval_smooth_dual_losses(oracle):
         mask[P] = True
         want = 0.5 * (A[i, mask].sum() - A[i, ~mask].sum() - gamma / c * (A[i] @ A[i]))
         assert abs(pe[i, 0, 1] - want) <= 1e-13
+
+
+# ---------------------------------------------------------------------------
+# Biased operators: min 0.5 (<x,x> + rho <1,x>^2) - <a,x> over the same sets.
+# With s = <1,x>, the negative gradient is r = a - x - rho s 1, and x is
+# optimal iff <r, v - x> <= 0 for every vertex (or extreme ray) v of the set.
+# ---------------------------------------------------------------------------
+def lp_max_box_budget(r, lo, hi, rhs):
+    """max <r, y> over lo <= y <= hi, sum(y) <= rhs (greedy is exact: unit
+    weights), or None when the set is empty."""
+    m = len(r)
+    if lo * m > rhs:
+        return None
+    y = np.full(m, lo)
+    budget = rhs - lo * m
+    for i in np.argsort(-r):
+        if r[i] <= 0 or budget <= 0:
+            break
+        step = min(hi - lo, budget)
+        y[i] += step
+        budget -= step
+    return float(np.dot(r, y))
+
+
+@pytest.mark.parametrize("m,k,rho", [(2, 1, 1.0), (5, 2, 0.5), (10, 3, 2.0), (30, 5, 1.0),
+                                     (6, 6, 0.3)])
+def test_topk_cone_biased_optimality(oracle, m, k, rho):
+    X = cases(m, 60 + m + k)
+    P, _ = prox(oracle, "topk_cone_biased", X, k=k, rho=rho)
+    for a, x in zip(X, P):
+        scale = max(1.0, np.abs(a).max())
+        tol = 1e-10 * scale * m
+        assert x.min() >= -tol and x.max() <= x.sum() / k + tol
+        r = a - x - rho * x.sum()
+        assert topk_sum(r, k) <= tol, "extreme rays 1_S, |S| = k"
+        assert abs(np.dot(r, x)) <= tol * max(1.0, np.abs(x).sum())
+
+
+@pytest.mark.parametrize("m,k,rhs,rho", [(2, 1, 1.0, 1.0), (5, 2, 1.0, 0.5), (10, 3, 2.0, 2.0),
+                                         (30, 5, 1.0, 1.0), (6, 6, 1.0, 0.3)])
+def test_topk_simplex_biased_optimality(oracle, m, k, rhs, rho):
+    X = cases(m, 70 + m + k)
+    P, _ = prox(oracle, "topk_simplex_biased", X, k=k, rhs=rhs, rho=rho)
+    for a, x in zip(X, P):
+        scale = max(1.0, np.abs(a).max())
+        tol = 1e-10 * scale * m
+        assert x.min() >= -tol and x.sum() <= rhs + tol and x.max() <= x.sum() / k + tol
+        r = a - x - rho * x.sum()
+        rx = np.dot(r, x)
+        assert rx >= -tol * max(1, np.abs(x).sum()), "vertex 0"
+        assert (rhs / k) * topk_sum(r, k) <= rx + tol * max(1, rhs), "vertices r 1_S / k"
+
+
+@pytest.mark.parametrize("lo,hi,rhs,rho", [(0.0, 1.0, 1.0, 1.0), (-0.5, 0.3, 2.0, 0.5),
+                                           (0.0, 0.2, 0.5, 3.0), (-1.0, 1.0, -2.0, 1.0)])
+def test_knapsack_le_biased_optimality(oracle, lo, hi, rhs, rho):
+    for m in (3, 10, 30):
+        X = cases(m, 80 + m)
+        P, _ = prox(oracle, "knapsack_le_biased", X, lo=lo, hi=hi, rhs=rhs, rho=rho)
+        for a, x in zip(X, P):
+            if lo * m > rhs:
+                continue
+            scale = max(1.0, np.abs(a).max())
+            tol = 1e-10 * scale * m
+            assert x.min() >= lo - tol and x.max() <= hi + tol and x.sum() <= rhs + tol
+            r = a - x - rho * x.sum()
+            best = lp_max_box_budget(r, lo, hi, rhs)
+            assert best <= np.dot(r, x) + tol * max(1.0, np.abs(x).sum()), "LP over the set"

@@ -33,6 +33,14 @@ OPS = [
     ("two_simplex", dict(p=1)),
     ("two_simplex", dict(p=3, rhs=2.0)),
     ("lambert_w_exp", dict()),
+    ("knapsack_le_biased", dict(rho=1.0)),
+    ("knapsack_le_biased", dict(lo=-0.5, hi=0.3, rhs=2.0, rho=0.5)),
+    ("knapsack_le_biased", dict(lo=0.0, hi=1.0, rhs=1.0, rho=0.0)),
+    ("topk_simplex_biased", dict(k=1, rho=1.0)),
+    ("topk_simplex_biased", dict(k=5, rhs=1.0, rho=0.5)),
+    ("topk_simplex_biased", dict(k=3, rhs=2.5, rho=2.0)),
+    ("topk_cone_biased", dict(k=1, rho=1.0)),
+    ("topk_cone_biased", dict(k=3, rho=0.25)),
 ]
 DTYPES = [(np.float32, 0), (np.float32, 1), (np.float64, 1), (np.float64, 0)]
 
@@ -59,7 +67,8 @@ def columns(m, dtype, seed):
 def test_prox_bit_exact(oracle, reference, op, kw, m, dtype, result):
     if op == "two_simplex" and (m < 2 or kw["p"] >= m):
         pytest.skip("p must be in [1, m-1]")
-    if op in ("topk_simplex", "topk_cone", "topk_entropy") and kw["k"] > m:
+    if op in ("topk_simplex", "topk_cone", "topk_entropy", "topk_simplex_biased",
+              "topk_cone_biased") and kw["k"] > m:
         pytest.skip("k > m")
     if op in ("knapsack_eq",) and (kw.get("hi", 1.0) * m < kw.get("rhs", 1.0) or kw.get("lo", 0.0) * m > kw.get("rhs", 1.0)):
         pytest.skip("infeasible")

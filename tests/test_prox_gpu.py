@@ -268,3 +268,24 @@ def test_large_m_limits(cuda):
         with pytest.raises(sd.SdcaError) as e:
             sd.prox(op, x, k=5, p=1)
         assert e.value.status == 4, op
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [1, 5, 17, 100, 1000])
+@pytest.mark.parametrize("op,kw", [
+    ("knapsack_le_biased", dict(lo=0.0, hi=1.0, rhs=1.0, rho=1.0)),
+    ("knapsack_le_biased", dict(lo=-0.5, hi=0.3, rhs=2.0, rho=0.5)),
+    ("knapsack_le_biased", dict(lo=0.0, hi=1.0, rhs=1.0, rho=0.0)),
+    ("topk_simplex_biased", dict(k=1, rhs=1.0, rho=1.0)),
+    ("topk_simplex_biased", dict(k=5, rhs=1.0, rho=0.5)),
+    ("topk_cone_biased", dict(k=1, rho=1.0)),
+    ("topk_cone_biased", dict(k=3, rho=0.25)),
+])
+def test_biased(cuda, oracle, op, kw, m, dtype, result):
+    """The biased operators (rho <1,x>^2 / 2 added to the objective), one
+    workgroup per sorted column."""
+    if kw.get("k", 1) > m:
+        pytest.skip("k > m")
+    for name, x in cases(m, dtype, 110 + m):
+        got, thr = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
