@@ -62,10 +62,9 @@ typedef enum sdca_prox_op {
   SDCA_PROX_KNAPSACK_LE_BIASED = 9,   /* knapsack_le_biased.h:165-180 (uses rho) */
   SDCA_PROX_TOPK_SIMPLEX_BIASED = 10, /* topk_simplex_biased.h:105-119 (uses rho) */
   SDCA_PROX_TOPK_CONE_BIASED = 11,    /* topk_cone_biased.h:145-158 (uses rho) */
-  /* Operators of the same front end that are not on this path yet:
-   * they return SDCA_ERR_NOT_IMPLEMENTED. */
+  /* Not on this path yet: returns SDCA_ERR_NOT_IMPLEMENTED. */
   SDCA_PROX_TOPK_ENTROPY_BIASED = 12,
-  SDCA_PROX_TWO_SIMPLEX_SORT = 13
+  SDCA_PROX_TWO_SIMPLEX_SORT = 13     /* two_simplex_sort.h:175-190 (uses p / col_p) */
 } sdca_prox_op;
 
 /* Operator parameters; defaults as in mex_prox.cpp:121-127. */
@@ -93,7 +92,7 @@ void sdca_prox_params_default(sdca_prox_params* params);
  *   data:   element type of in/out;
  *   result: the reference's Result template argument (internal precision);
  *   in/out: m*n elements each; out == in works in place like the reference;
- *   col_p:  for SDCA_PROX_TWO_SIMPLEX, optional per-column split p (n int64
+ *   col_p:  for the two-block operators, optional per-column split p (n int64
  *           values in [1, m-1]); NULL uses params->p for every column;
  *   thresholds: optional, n records (2n for the two-block operator) with the
  *           computed thresholds, in double.

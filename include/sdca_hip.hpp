@@ -186,6 +186,16 @@ inline void prox_topk_cone_biased(std::ptrdiff_t dim, Data* first, Data* last, D
   detail::run<Result>(SDCA_PROX_TOPK_CONE_BIASED, dim, first, last, p);
 }
 
+// two_simplex_sort.h:175-190
+template <typename Result = double, typename Data>
+inline void prox_two_simplex_sort(std::ptrdiff_t dim, std::ptrdiff_t p_split, Data* first,
+                                  Data* last, Data* /*aux*/, const Result rhs = 1) {
+  sdca_prox_params p = detail::params();
+  p.p = p_split;
+  p.rhs = static_cast<double>(rhs);
+  detail::run<Result>(SDCA_PROX_TWO_SIMPLEX_SORT, dim, first, last, p);
+}
+
 // apply(dim, first, last, lambert_w_exp_map<Data>()) (proxdef.h:386-400)
 template <typename Data>
 inline void apply_lambert_w_exp(std::ptrdiff_t dim, Data* first, Data* last) {

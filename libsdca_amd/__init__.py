@@ -162,7 +162,7 @@ def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
     if out is None:
         out = A
     params = ProxParams(lo, hi, rhs, rho, alpha, int(k), int(p))
-    nthr = 2 * n if code == OPS["two_simplex"] else n
+    nthr = 2 * n if code in (OPS["two_simplex"], OPS["two_simplex_sort"]) else n
     if _is_torch(A):
         import torch
         if not A.is_cuda or not A.is_contiguous() or not out.is_contiguous():
@@ -238,6 +238,10 @@ def prox_topk_simplex_biased(dim, A, k=1, rhs=1.0, rho=1.0, result=None):
 
 def prox_topk_cone_biased(dim, A, k=1, rho=1.0, result=None):
     return prox("topk_cone_biased", _rows(dim, A), k=k, rho=rho, result=result)
+
+
+def prox_two_simplex_sort(dim, p, A, rhs=1.0, result=None):
+    return prox("two_simplex_sort", _rows(dim, A), p=p, rhs=rhs, result=result)
 
 
 def lambert_w_exp(A):

@@ -139,7 +139,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   else sdca_prox_params_default(&p);
   if (static_cast<int>(op) < 0 || op > SDCA_PROX_TWO_SIMPLEX_SORT)
     return fail(SDCA_ERR_PROX, "unknown prox operator %d", static_cast<int>(op));
-  if (op == SDCA_PROX_TOPK_ENTROPY_BIASED || op == SDCA_PROX_TWO_SIMPLEX_SORT)
+  if (op == SDCA_PROX_TOPK_ENTROPY_BIASED)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "prox operator %d is not implemented on the GPU",
                 static_cast<int>(op));
   const bool biased = op == SDCA_PROX_KNAPSACK_LE_BIASED || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
@@ -159,7 +159,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
                       op == SDCA_PROX_TOPK_CONE_BIASED;
   if (uses_k && (p.k < 1 || p.k > m))
     return fail(SDCA_ERR_ARG_RANGE, "k must be in [1, %lld] (got %lld)", (long long)m, (long long)p.k);
-  if (op == SDCA_PROX_TWO_SIMPLEX) {
+  const bool two = op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT;
+  if (two) {
     if (m < 2) return fail(SDCA_ERR_ARG_RANGE, "two_simplex needs m >= 2");
     if (!col_p && (p.p < 1 || p.p > m - 1))
       return fail(SDCA_ERR_ARG_RANGE, "p must be in [1, %lld] (got %lld)", (long long)(m - 1), (long long)p.p);
@@ -179,20 +180,21 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   const bool reg_ok = m <= kRegMaxM;
   const bool topk = op == SDCA_PROX_TOPK_SIMPLEX || op == SDCA_PROX_TOPK_CONE;
   const bool knap = op == SDCA_PROX_KNAPSACK_EQ || op == SDCA_PROX_KNAPSACK_LE;
-  if (!reg_ok && !(topk || knap || biased) && op != SDCA_PROX_LAMBERT_W_EXP)
+  if (!reg_ok && !(topk || knap || biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
+      op != SDCA_PROX_TWO_SIMPLEX_SORT)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "operator %d supports m <= %lld on the GPU (got %lld)",
                 static_cast<int>(op), (long long)kRegMaxM, (long long)m);
   if ((topk || knap) && m > slow_max_m(data) && (!reg_ok || (topk && p.k > kTopkMaxK)))
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
                 (long long)m, (long long)slow_max_m(data));
-  if (biased && m > slow_max_m(data))
+  if ((biased || op == SDCA_PROX_TWO_SIMPLEX_SORT) && m > slow_max_m(data))
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
                 (long long)m, (long long)slow_max_m(data));
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const size_t bytes = static_cast<size_t>(m) * static_cast<size_t>(n) * dtype_size(data);
   const bool host = (flags & SDCA_HOST_PTR) != 0;
-  const int64_t nthr = (op == SDCA_PROX_TWO_SIMPLEX) ? 2 * n : n;
+  const int64_t nthr = two ? 2 * n : n;
   DeviceBuffer din, dout, dcolp, dthr;
   const void* d_in = in;
   void* d_out = out;
@@ -208,7 +210,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
       SDCA_HIP_TRY(hipMalloc(&dout.ptr, bytes), "hipMalloc(staging)");
       d_out = dout.ptr;
     }
-    if (col_p && op == SDCA_PROX_TWO_SIMPLEX) {
+    if (col_p && two) {
       rc = stage_in(col_p, static_cast<size_t>(n) * sizeof(int64_t), dcolp, stream);
       if (rc) return rc;
       d_colp = static_cast<const int64_t*>(dcolp.ptr);
@@ -219,7 +221,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
       d_thr = static_cast<sdca_thresholds*>(dthr.ptr);
     }
   }
-  if (op != SDCA_PROX_TWO_SIMPLEX) d_colp = nullptr;
+  if (!two) d_colp = nullptr;
 
   ProxLaunch a;
   a.op = op;
@@ -242,6 +244,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
 
   if (op == SDCA_PROX_LAMBERT_W_EXP) {
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
+  } else if (op == SDCA_PROX_TWO_SIMPLEX_SORT) {
+    SDCA_HIP_TRY(launch_two_sort(a), "two_simplex_sort kernel (workgroup per column)");
   } else if (biased || ((topk || knap) && (!reg_ok || (topk && p.k > kTopkMaxK)))) {
     // The biased operators' searches need the sorted column: one workgroup
     // per column (knapsack_le_biased.h, topk_simplex_biased.h,

@@ -21,7 +21,8 @@ enum {
   OP_LAMBERT_W_EXP = SDCA_PROX_LAMBERT_W_EXP,
   OP_KNAPSACK_LE_BIASED = SDCA_PROX_KNAPSACK_LE_BIASED,
   OP_TOPK_SIMPLEX_BIASED = SDCA_PROX_TOPK_SIMPLEX_BIASED,
-  OP_TOPK_CONE_BIASED = SDCA_PROX_TOPK_CONE_BIASED
+  OP_TOPK_CONE_BIASED = SDCA_PROX_TOPK_CONE_BIASED,
+  OP_TWO_SIMPLEX_SORT = SDCA_PROX_TWO_SIMPLEX_SORT
 };
 
 // Largest m handled by the register kernels.
@@ -50,6 +51,8 @@ hipError_t launch_knap(const ProxLaunch& a);
 hipError_t launch_topk(const ProxLaunch& a);
 hipError_t launch_ent(const ProxLaunch& a);
 hipError_t launch_ent_norm(const ProxLaunch& a);
+// Two-block simplex by sort and scan, one workgroup per column (prox_slow.hip).
+hipError_t launch_two_sort(const ProxLaunch& a);
 hipError_t launch_topkent(const ProxLaunch& a);
 hipError_t launch_two(const ProxLaunch& a);
 // Workgroup-per-column kernel over the flagged list (all_columns: every column).

@@ -351,6 +351,130 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   return hipGetLastError();
 }
 
+// Descending bitonic sort of s[0, pow2) by the whole workgroup (callers pad
+// with -inf).
+template <class D>
+__device__ void bitonic_desc(D* s, int pow2) {
+  for (int size = 2; size <= pow2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < pow2; i += blockDim.x) {
+        const int partner = i ^ stride;
+        if (partner > i) {
+          const bool desc = (i & size) == 0;
+          const D a = s[i], b = s[partner];
+          if (desc ? (a < b) : (b < a)) {
+            s[i] = b;
+            s[partner] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// thresholds_two_simplex_sort (two_simplex_sort.h:15-111) on the two sorted
+// blocks a[0, p), b[0, q): the common sum c is scanned over the breakpoints
+// where the active counts r, s grow; past the end of a block the reference
+// uses the pseudo point last - rhs.
+template <class D, class R>
+__device__ void two_sort_thresholds(const D* a, int p, const D* b, int q, R rhs, R& theta_a,
+                                    R& theta_b) {
+  const R eps = num<R>::eps() * dmax(R(1), rhs);
+  const R C = rhs;
+  R c = 0, best_c = rhs;
+  R sum_mu = static_cast<R>(a[0]), sum_nu = static_cast<R>(b[0]);
+  int r = 1, s = 1;
+  auto a_at = [&](int i) { return i < p ? static_cast<R>(a[i]) : static_cast<R>(a[p - 1]) - C; };
+  auto b_at = [&](int i) { return i < q ? static_cast<R>(b[i]) : static_cast<R>(b[q - 1]) - C; };
+  R a_r = a_at(r), b_s = b_at(s);
+  while (c < C) {
+    const R copt = (static_cast<R>(s) * sum_mu + static_cast<R>(r) * sum_nu) / static_cast<R>(r + s);
+    const R next_cr = (sum_mu + a_r) - static_cast<R>(r + 1) * a_r;
+    const R next_cs = (sum_nu + b_s) - static_cast<R>(s + 1) * b_s;
+    const R next_c = dmin(dmin(next_cr, next_cs), C);
+    if (c <= copt && copt < next_c) {
+      best_c = copt;
+      break;
+    }
+    if (next_c >= C - eps) {
+      best_c = C;
+      break;
+    }
+    if (next_cr < next_cs) {
+      sum_mu += a_r;
+      ++r;
+      a_r = a_at(r);
+    } else {
+      sum_nu += b_s;
+      ++s;
+      b_s = b_at(s);
+    }
+    c = next_c;
+  }
+  theta_a = (sum_mu - best_c) / static_cast<R>(r);
+  theta_b = (sum_nu - best_c) / static_cast<R>(s);
+}
+
+// Two-block simplex by sort and scan: one workgroup per column, both blocks
+// sorted in LDS (each padded to pow2 with -inf), one lane scans, the
+// workgroup clamps the column.
+template <class D, class R>
+__global__ void __launch_bounds__(256)
+two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, R rhs,
+                int64_t p_all, const int64_t* __restrict__ col_p,
+                sdca_thresholds* __restrict__ thr, int pow2) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  D* sa = reinterpret_cast<D*>(smem_raw);
+  D* sb = sa + pow2;
+  __shared__ R sh_ta, sh_tb;
+  const int m = static_cast<int>(m64);
+  for (int64_t j = blockIdx.x; j < n; j += gridDim.x) {
+    const int p = static_cast<int>(col_p ? col_p[j] : p_all);
+    const int q = m - p;
+    const D* col = in + j * m64;
+    for (int i = threadIdx.x; i < pow2; i += blockDim.x) {
+      sa[i] = (i < p) ? col[i] : -num<D>::inf();
+      sb[i] = (i < q) ? col[p + i] : -num<D>::inf();
+    }
+    __syncthreads();
+    bitonic_desc(sa, pow2);
+    bitonic_desc(sb, pow2);
+    if (threadIdx.x == 0) {
+      R ta, tb;
+      two_sort_thresholds<D, R>(sa, p, sb, q, rhs, ta, tb);
+      sh_ta = ta;
+      sh_tb = tb;
+      if (thr) {
+        thr[2 * j].t = static_cast<double>(ta);
+        thr[2 * j].lo = 0;
+        thr[2 * j].hi = static_cast<double>(rhs);
+        thr[2 * j + 1].t = static_cast<double>(tb);
+        thr[2 * j + 1].lo = 0;
+        thr[2 * j + 1].hi = static_cast<double>(rhs);
+      }
+    }
+    __syncthreads();
+    const D ta = static_cast<D>(sh_ta), tb = static_cast<D>(sh_tb), hi = static_cast<D>(rhs);
+    D* dst = out + j * m64;
+    for (int i = threadIdx.x; i < m; i += blockDim.x)
+      dst[i] = clamp_ref(col[i] - (i < p ? ta : tb), D(0), hi);
+    __syncthreads();
+  }
+}
+
+template <class D, class R>
+hipError_t launch_two_sort_t(const ProxLaunch& a) {
+  int half = 1;
+  while (half < a.m) half <<= 1;  // pow2 >= max(p, m - p) for every column
+  const int64_t grid = a.n < 4096 ? a.n : 4096;
+  hipLaunchKernelGGL((two_sort_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
+                     dim3(256), 2 * static_cast<size_t>(half) * sizeof(D), a.stream,
+                     static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n,
+                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, half);
+  return hipGetLastError();
+}
+
 __global__ void clear_kernel(int* p, int count) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < count) p[i] = 0;
@@ -375,6 +499,13 @@ hipError_t launch_slow(const ProxLaunch& a, bool all_columns) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_slow_t<float, float>(a, all_columns);
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_slow_t<float, double>(a, all_columns);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_slow_t<double, double>(a, all_columns);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_two_sort(const ProxLaunch& a) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_two_sort_t<float, float>(a);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_two_sort_t<float, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_two_sort_t<double, double>(a);
   return hipErrorInvalidValue;
 }
 

@@ -673,6 +673,59 @@ two_simplex(It a_first, It a_last, It b_first, It b_last, R rhs) {
                         make_thr(-t, lo, hi, b_first, y_last));
 }
 
+// The same problem by the sort-and-scan method (two_simplex_sort.h:15-111):
+// both blocks sorted in descending order, then the common sum c is located
+// on the grid of breakpoints where the number of active entries r, s grows.
+template <class R, class It>
+inline std::pair<thr<R, It>, thr<R, It>>
+two_simplex_sort(It a_first, It a_last, It b_first, It b_last, R rhs) {
+  const R lo(0), hi(rhs);
+  const R eps = std::numeric_limits<R>::epsilon()
+              * std::max(static_cast<R>(1), rhs);
+  std::sort(a_first, a_last, std::greater<R>());
+  std::sort(b_first, b_last, std::greater<R>());
+  R c = 0, C = rhs, best_c = rhs, sum_mu = *a_first, sum_nu = *b_first;
+  typename std::iterator_traits<It>::difference_type r = 1, s = 1;
+  // Past the end, a pseudo point that ends the scan.
+  auto a_at = [&](decltype(r) i) {
+    return a_first + i != a_last ? static_cast<R>(a_first[i])
+                                 : static_cast<R>(*std::prev(a_last)) - C;
+  };
+  auto b_at = [&](decltype(s) i) {
+    return b_first + i != b_last ? static_cast<R>(b_first[i])
+                                 : static_cast<R>(*std::prev(b_last)) - C;
+  };
+  R a_r = a_at(r), b_s = b_at(s);
+  while (c < C) {
+    R copt = (s * sum_mu + r * sum_nu) / static_cast<R>(r + s);
+    R next_cr = (sum_mu + a_r) - (r + 1) * a_r;
+    R next_cs = (sum_nu + b_s) - (s + 1) * b_s;
+    R next_c = std::min(std::min(next_cr, next_cs), C);
+    if (c <= copt && copt < next_c) {
+      best_c = copt;
+      break;
+    }
+    if (next_c >= C - eps) {
+      best_c = C;
+      break;
+    }
+    if (next_cr < next_cs) {
+      sum_mu += a_r;
+      ++r;
+      a_r = a_at(r);
+    } else {
+      sum_nu += b_s;
+      ++s;
+      b_s = b_at(s);
+    }
+    c = next_c;
+  }
+  R theta_a = (sum_mu - best_c) / static_cast<R>(r);
+  R theta_b = (sum_nu - best_c) / static_cast<R>(s);
+  return std::make_pair(make_thr(theta_a, lo, hi, a_first, a_first + r),
+                        make_thr(theta_b, lo, hi, b_first, b_first + s));
+}
+
 // ---------------------------------------------------------------------------
 // Clamp/map pass (proxdef.h:164-196): thresholds are cast to Data first.
 // ---------------------------------------------------------------------------

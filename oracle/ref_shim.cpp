@@ -84,6 +84,15 @@ void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_param
     case SDCA_PROX_TOPK_SIMPLEX_BIASED:
       sdca::prox_topk_simplex_biased(m, first, last, aux, k, rhs, rho); break;
     case SDCA_PROX_TOPK_CONE_BIASED: sdca::prox_topk_cone_biased(m, first, last, aux, k, rho); break;
+    case SDCA_PROX_TWO_SIMPLEX_SORT:
+      if (!col_p) {
+        sdca::prox_two_simplex_sort(m, static_cast<std::ptrdiff_t>(p->p), first, last, aux, rhs);
+      } else {
+        for (int64_t j = 0; first + j * m < last; ++j)
+          sdca::prox_two_simplex_sort(m, static_cast<std::ptrdiff_t>(col_p[j]), first + j * m,
+                                      first + (j + 1) * m, aux, rhs);
+      }
+      break;
     default: break;
   }
 }
@@ -132,6 +141,16 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
         std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])
                                   : static_cast<std::ptrdiff_t>(p->p);
         auto t = sdca::thresholds_two_simplex(aux, aux + pj, aux + pj, al, rhs);
+        sdca::prox(t.first, col, col + pj);
+        sdca::prox(t.second, col + pj, col + m);
+        put(out, 2 * j, t.first);
+        put(out, 2 * j + 1, t.second);
+        break;
+      }
+      case SDCA_PROX_TWO_SIMPLEX_SORT: {
+        std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])
+                                  : static_cast<std::ptrdiff_t>(p->p);
+        auto t = sdca::thresholds_two_simplex_sort(aux, aux + pj, aux + pj, al, rhs);
         sdca::prox(t.first, col, col + pj);
         sdca::prox(t.second, col + pj, col + m);
         put(out, 2 * j, t.first);

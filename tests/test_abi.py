@@ -61,7 +61,7 @@ def test_prox_operator_and_precision_checks():
         sd.prox(42, x)
     assert e.value.status == 7  # LIBSDCA:prox
     with pytest.raises(sd.SdcaError) as e:
-        sd.prox("two_simplex_sort", x)
+        sd.prox("topk_entropy_biased", x)
     assert e.value.status == 4  # not on this path
     with pytest.raises(sd.SdcaError) as e:
         sd.prox("topk_simplex", x, result="long double")

@@ -439,3 +439,24 @@ def test_knapsack_le_biased_optimality(oracle, lo, hi, rhs, rho):
             r = a - x - rho * x.sum()
             best = lp_max_box_budget(r, lo, hi, rhs)
             assert best <= np.dot(r, x) + tol * max(1.0, np.abs(x).sum()), "LP over the set"
+
+
+def test_two_simplex_sort_against_variable_fixing(oracle):
+    """two_simplex_sort (two_simplex_sort.h, a sort-and-scan method) and
+    two_simplex (two_simplex.h, variable fixing) solve the same problem by
+    independent algorithms: they agree wherever the optimum is non-zero.
+    Where the optimum is x = y = 0 (the unconstrained common sum is
+    negative), the reference's scan ends at c = rhs instead; the oracle
+    reproduces that, and this test pins that it is exactly that case."""
+    rng = np.random.default_rng(9)
+    for m in (2, 5, 40):
+        x = rng.standard_normal((1000, m)) * 2
+        for p in sorted({1, max(1, m // 2), m - 1}):
+            srt, kiw = x.copy(), x.copy()
+            oracle.prox("two_simplex_sort", srt, result=F64, params=binding.make_params(p=p))
+            oracle.prox("two_simplex", kiw, result=F64, params=binding.make_params(p=p))
+            zero = kiw.sum(axis=1) <= 1e-12
+            assert np.abs(srt[~zero] - kiw[~zero]).max() <= 1e-12 * max(1.0, np.abs(x).max())
+            if zero.any():
+                assert np.allclose(srt[zero][:, :p].sum(axis=1), 1.0)
+                assert np.allclose(srt[zero][:, p:].sum(axis=1), 1.0)

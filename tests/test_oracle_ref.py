@@ -41,6 +41,8 @@ OPS = [
     ("topk_simplex_biased", dict(k=3, rhs=2.5, rho=2.0)),
     ("topk_cone_biased", dict(k=1, rho=1.0)),
     ("topk_cone_biased", dict(k=3, rho=0.25)),
+    ("two_simplex_sort", dict(p=1)),
+    ("two_simplex_sort", dict(p=3, rhs=2.0)),
 ]
 DTYPES = [(np.float32, 0), (np.float32, 1), (np.float64, 1), (np.float64, 0)]
 
@@ -65,7 +67,7 @@ def columns(m, dtype, seed):
 @pytest.mark.parametrize("m", [1, 2, 5, 10, 31, 100])
 @pytest.mark.parametrize("op,kw", OPS)
 def test_prox_bit_exact(oracle, reference, op, kw, m, dtype, result):
-    if op == "two_simplex" and (m < 2 or kw["p"] >= m):
+    if op in ("two_simplex", "two_simplex_sort") and (m < 2 or kw["p"] >= m):
         pytest.skip("p must be in [1, m-1]")
     if op in ("topk_simplex", "topk_cone", "topk_entropy", "topk_simplex_biased",
               "topk_cone_biased") and kw["k"] > m:
@@ -85,14 +87,15 @@ def test_prox_bit_exact(oracle, reference, op, kw, m, dtype, result):
         assert np.array_equal(ta, tb, equal_nan=True), f"{op}: thresholds differ"
 
 
-def test_prox_per_column_split_bit_exact(oracle, reference):
+@pytest.mark.parametrize("op", ["two_simplex", "two_simplex_sort"])
+def test_prox_per_column_split_bit_exact(oracle, reference, op):
     rng = np.random.default_rng(3)
     x = inputs.normal(500, 40, np.float32, 4)
     col_p = rng.integers(1, 6, 500)
     a, b = x.copy(), x.copy()
     params = binding.make_params(rhs=1.0)
-    oracle.prox("two_simplex", a, params=params, col_p=col_p)
-    reference.prox("two_simplex", b, params=params, col_p=col_p)
+    oracle.prox(op, a, params=params, col_p=col_p)
+    reference.prox(op, b, params=params, col_p=col_p)
     assert np.array_equal(a, b)
 
 

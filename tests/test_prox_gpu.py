@@ -289,3 +289,23 @@ def test_biased(cuda, oracle, op, kw, m, dtype, result):
     for name, x in cases(m, dtype, 110 + m):
         got, thr = run_gpu(op, x, result, cuda, **kw)
         parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [2, 10, 159, 200, 1000, 3000])
+def test_two_simplex_sort(cuda, oracle, m, dtype, result):
+    """The sort-and-scan two-block simplex (one workgroup per column), with a
+    per-column and a common split p."""
+    n = 120
+    rng = np.random.default_rng(150 + m)
+    col_p = rng.integers(1, min(m - 1, 5) + 1, n)
+    for rhs in [1.0, 2.0]:
+        for name, x in [("normal", inputs.normal(n, m, dtype, 151 + m)),
+                        ("mixed", inputs.mixed_signs(n, m, dtype, 152 + m, -2, 2))]:
+            got, _ = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, col_p=col_p)
+            parity(oracle, "two_simplex_sort", x, got, result,
+                   f"two_simplex_sort rhs={rhs} {name} m={m}", rhs=rhs, col_p=col_p)
+            p = max(1, m // 3)
+            got, _ = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, p=p)
+            parity(oracle, "two_simplex_sort", x, got, result,
+                   f"two_simplex_sort p={p} rhs={rhs} {name} m={m}", rhs=rhs, p=p)
