@@ -21,7 +21,7 @@ OPS = {
     "knapsack_eq": 0, "knapsack_le": 1, "topk_simplex": 2, "topk_cone": 3,
     "entropy": 4, "entropy_norm": 5, "topk_entropy": 6, "two_simplex": 7,
     "lambert_w_exp": 8, "knapsack_le_biased": 9, "topk_simplex_biased": 10,
-    "topk_cone_biased": 11, "two_simplex_sort": 13,
+    "topk_cone_biased": 11, "topk_entropy_biased": 12, "two_simplex_sort": 13,
 }
 OBJECTIVES = {
     "hinge_topk": 0, "hinge_topk_smooth": 1, "topk_hinge": 2,

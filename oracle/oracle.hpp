@@ -47,13 +47,16 @@ template <class R, class It>
 struct thr {
   R t, lo, hi;
   It first, last;
-  int kind;
+  int kind;       // 3 = map_a * lambert_w_exp (a_lambert_w_exp_map, functor.h:30-38)
+  double map_a;   // the map's constant, already rounded to Data
 };
 
 template <class R, class It>
-inline thr<R, It> make_thr(R t, R lo, R hi, It first, It last, int kind = 0) {
+inline thr<R, It> make_thr(R t, R lo, R hi, It first, It last, int kind = 0,
+                           double map_a = 1) {
   thr<R, It> r;
   r.t = t; r.lo = lo; r.hi = hi; r.first = first; r.last = last; r.kind = kind;
+  r.map_a = map_a;
   return r;
 }
 
@@ -612,6 +615,127 @@ inline thr<R, It> topk_entropy(It first, It last, std::ptrdiff_t k) {
   return make_thr(t, lo, hi, mf, last, 1);
 }
 
+// Biased top-k entropy (topk_entropy_biased.h:9-260):
+//   min 0.5 alpha (<x,x> + s^2) + <x, log x> + (1 - s) log(1 - s) - <a, x>,
+//   <1,x> = s <= 1, 0 <= x_i <= s / k;  x = clamp(W(exp(a - t)) / alpha).
+// ---------------------------------------------------------------------------
+// f0..f3 += sum over [first, last) of W(exp(a + t)) and its derivatives
+// (lambert.h:253-332).
+template <class R, class It>
+inline void lw_sums(It first, It last, R t, R& f0, R& f1) {
+  for (It a = first; a != last; ++a) {
+    R v = lambert_w_exp(static_cast<R>(*a) + t);
+    f0 += v;
+    f1 += v / (1 + v);
+  }
+}
+template <class R, class It>
+inline void lw_sums(It first, It last, R t, R& f0, R& f1, R& f2, R& f3) {
+  for (It a = first; a != last; ++a) {
+    R v = lambert_w_exp(static_cast<R>(*a) + t);
+    R d = 1 + v;
+    R d3 = d * d * d;
+    f0 += v;
+    f1 += v / d;
+    f2 += v / d3;
+    f3 += v * (1 - 2 * v) / (d3 * d * d);
+  }
+}
+
+// One Householder step for W(exp(alpha - t)) + sum_i W(exp(a_i - t)) = alpha
+// (topk_entropy_biased.h:9-38); s = sum_i W(exp(a_i - t)) / alpha.
+template <class R, class It>
+inline void alpha_sum_w_exp_step4(It first, It last, R alpha, R& s, R& t) {
+  R f0(0), f1(0), f2(0), f3(0);
+  lw_sums(first, last, -t, f0, f1, f2, f3);
+  s = f0 / alpha;
+  lw_sums(&alpha, &alpha + 1, -t, f0, f1, f2, f3);
+  f0 -= alpha;
+  R f02 = f0 * f2, f11 = f1 * f1;
+  R den = 6 * f1 * (f02 - f11) - f0 * (f0 * f3);
+  if (std::abs(den) > 64 * std::numeric_limits<R>::min()) t -= 3 * f0 * (2 * f11 - f02) / den;
+}
+
+// Newton step on the KKT system in (s, t) for a given U
+// (topk_entropy_biased.h:64-117).
+template <class R, class It>
+inline void topk_entropy_biased_newton(It first, It last, R K, R U, R C0, R C1, R C2, R C3,
+                                       R C4, R C5, R& s, R& t) {
+  R S0(0), S1(0);
+  lw_sums(first, last, -t, S0, S1);
+  R E = S0 + t * S1;
+  R z, Az, Bz;
+  if (s < static_cast<R>(0.5)) {
+    z = s;
+    Az = K * (z * (U + std::log1p(-z) + z / (1 - z)) - U * x_log_x(z)) - C0 * z;
+    Bz = z * (C2 + K / (1 - z)) + C1;
+  } else {
+    z = 1 - s;
+    Az = K * (z * (U - U * std::log1p(-z) - 1) + x_log_x(z) + 1) - C0 * z;
+    Bz = z * (C2 + C1 / (1 - z)) + K;
+  }
+  R Dz = C3 * z - Bz * S1;
+  if (std::abs(Dz) > 64 * std::numeric_limits<R>::min()) {
+    s = (C4 * E * z - Az * S1) / Dz;
+    t = (C5 * Az - E * Bz) / Dz;
+  }
+}
+
+template <class R, class It>
+inline thr<R, It> topk_entropy_biased(It first, It last, std::ptrdiff_t k, R alpha) {
+  typedef typename std::iterator_traits<It>::value_type D;
+  It max_el = std::max_element(first, last);
+  R max = static_cast<R>(*max_el);
+  const R eps = 16 * std::numeric_limits<R>::epsilon() * std::max(static_cast<R>(1), max);
+  R s(0), t(max);
+  // U empty (topk_entropy_biased.h:48-61, 211-215).
+  for (std::size_t iter = 0; iter < 32; ++iter) {
+    R t1(t);
+    alpha_sum_w_exp_step4(first, last, alpha, s, t);
+    if (std::abs(t1 - t) <= std::numeric_limits<R>::epsilon()) break;
+  }
+  const R lo(0), K(static_cast<R>(k));
+  const double map_a = static_cast<double>(1 / static_cast<D>(alpha));
+  if (k == 1) return make_thr(t, lo, s, first, last, 3, map_a);
+  const R alpha_k(alpha / K);
+  R tt = t + std::max(alpha_k * s + std::log(alpha_k * s), exp_min_arg<R>::get());
+  if (max - eps <= tt) return make_thr(t, lo, s / K, first, last, 3, map_a);
+  // U not empty: grow U by the largest remaining element (:235-259).
+  std::swap(*first, *max_el);
+  const R log_k = std::log(K), log_alpha = std::log(alpha);
+  R min_u(max), sum_u(max);
+  It mf = first + 1;
+  for (std::ptrdiff_t num_u = 1; mf != last;) {
+    max_el = std::max_element(mf, last);
+    max = static_cast<R>(*max_el);
+    s = static_cast<R>(0.999);
+    t = max;
+    {  // topk_entropy_biased_kkt_iterate (:144-176)
+      const R U = static_cast<R>(num_u);
+      const R lb(0), ub(1), eps16 = 16 * std::numeric_limits<R>::epsilon();
+      const R C1 = U * K, C2 = (K + U) * alpha, C3 = (K - U) * (U - 1) * alpha;
+      const R C4 = K * (U - 1), C5 = (1 - U / K) * alpha;
+      const R C0 = C4 * log_alpha - C1 * log_k - sum_u;
+      for (std::size_t iter = 0; iter < 32; ++iter) {
+        R s1(s), t1(t);
+        s = std::min(std::max(lb, s), ub);
+        topk_entropy_biased_newton(mf, last, K, U, C0, C1, C2, C3, C4, C5, s, t);
+        if (std::abs(s1 - s) + std::abs(t1 - t) <= eps16) break;
+      }
+      s = std::min(std::max(lb, s), ub);
+    }
+    tt = t + std::max(alpha_k * s + std::log(alpha_k * s), exp_min_arg<R>::get());
+    if (max - eps <= tt && tt <= min_u + eps) break;
+    if (++num_u > k) break;
+    min_u = max;
+    sum_u += max;
+    std::swap(*mf, *max_el);
+    ++mf;
+  }
+  return make_thr(t, lo, s / K, first, last, 3, map_a);
+}
+
+// ---------------------------------------------------------------------------
 // Two-block simplex, <1,x> = <1,y> <= rhs (two_simplex.h:18-119).
 template <class R, class It>
 inline std::pair<thr<R, It>, thr<R, It>>
@@ -738,6 +862,7 @@ inline void clamp(const thr<R, It>& th, It first, It last) {
     D v = *x - t;
     if (th.kind == 1) v = std::exp(v);
     else if (th.kind == 2) v = lambert_w_exp(v);
+    else if (th.kind == 3) v = static_cast<D>(th.map_a) * lambert_w_exp(v);
     *x = std::max(lo, std::min(v, hi));
   }
 }

@@ -90,6 +90,8 @@ int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
         case SDCA_PROX_TOPK_SIMPLEX_BIASED:
           t = orc::topk_simplex_biased<R>(a, a_end, k, rhs, rho); break;
         case SDCA_PROX_TOPK_CONE_BIASED: t = orc::topk_cone_biased<R>(a, a_end, k, rho); break;
+        case SDCA_PROX_TOPK_ENTROPY_BIASED:
+          t = orc::topk_entropy_biased<R>(a, a_end, k, static_cast<R>(p->alpha)); break;
         default: break;
       }
       orc::clamp(t, col, col + m);

@@ -84,6 +84,8 @@ void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_param
     case SDCA_PROX_TOPK_SIMPLEX_BIASED:
       sdca::prox_topk_simplex_biased(m, first, last, aux, k, rhs, rho); break;
     case SDCA_PROX_TOPK_CONE_BIASED: sdca::prox_topk_cone_biased(m, first, last, aux, k, rho); break;
+    case SDCA_PROX_TOPK_ENTROPY_BIASED:
+      sdca::prox_topk_entropy_biased(m, first, last, aux, k, static_cast<R>(p->alpha)); break;
     case SDCA_PROX_TWO_SIMPLEX_SORT:
       if (!col_p) {
         sdca::prox_two_simplex_sort(m, static_cast<std::ptrdiff_t>(p->p), first, last, aux, rhs);
@@ -146,6 +148,10 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
         put(out, 2 * j, t.first);
         put(out, 2 * j + 1, t.second);
         break;
+      }
+      case SDCA_PROX_TOPK_ENTROPY_BIASED: {
+        auto t = sdca::thresholds_topk_entropy_biased(aux, al, k, static_cast<R>(p->alpha));
+        sdca::prox(t, col, col + m); put(out, j, t); break;
       }
       case SDCA_PROX_TWO_SIMPLEX_SORT: {
         std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])

@@ -35,6 +35,7 @@ PROX_CASES = [
     ("knapsack_le_biased", dict(lo=0.0, hi=1.0, rhs=1.0, rho=0.5), [10, 33]),
     ("topk_simplex_biased", dict(k=5, rhs=1.0, rho=0.5), [10, 100]),
     ("topk_cone_biased", dict(k=5, rho=0.5), [10, 100]),
+    ("topk_entropy_biased", dict(k=3, alpha=0.7), [10, 64]),
     ("two_simplex_sort", dict(p=2, rhs=1.0), [10, 33]),
 ]
 DTYPES = [("f32f32", np.float32, 0), ("f32f64", np.float32, 1), ("f64f64", np.float64, 1)]

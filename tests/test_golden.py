@@ -24,6 +24,7 @@ PARAMS = {
     "two_simplex": dict(p=2, rhs=1.0), "lambert_w_exp": dict(),
     "knapsack_le_biased": dict(lo=0.0, hi=1.0, rhs=1.0, rho=0.5),
     "topk_simplex_biased": dict(k=5, rhs=1.0, rho=0.5), "topk_cone_biased": dict(k=5, rho=0.5),
+    "topk_entropy_biased": dict(k=3, alpha=0.7),
     "two_simplex_sort": dict(p=2, rhs=1.0),
 }
 MC = [("hinge_topk", 1.0, 1.0, 5), ("hinge_topk_smooth", 1.0, 1.0, 5), ("topk_hinge", 1.0, 1.0, 3),

@@ -16,6 +16,10 @@ result by a property that characterises it independently.
   inverse identities of the reference tests (test/prox/lambert.cpp:5-157).
 * The two-block simplex and top-k entropy against scipy's SLSQP on small
   problems, plus the regression vector of test/prox/two_simplex.cpp:55-64.
+* Biased top-k entropy: k = 1 against a bisection with scipy's W, k > 1
+  against SLSQP where no entry sits at the cap; where one does, the
+  reference's result is feasible but not the minimiser, and that deviation
+  is recorded (the oracle follows the reference there, bit for bit).
 * Evaluation: losses against closed forms (max over the projection set of
   <h,p> - |p|^2/2 = (|h|^2 - |h - P(h)|^2) / 2), counts against numpy.
 """
@@ -460,3 +464,71 @@ def test_two_simplex_sort_against_variable_fixing(oracle):
             if zero.any():
                 assert np.allclose(srt[zero][:, :p].sum(axis=1), 1.0)
                 assert np.allclose(srt[zero][:, p:].sum(axis=1), 1.0)
+
+
+def biased_entropy_objective(x, a, alpha):
+    s = x.sum()
+    xl = np.where(x > 0, x * np.log(np.maximum(x, 1e-300)), 0.0)
+    return 0.5 * alpha * (x @ x + s * s) + xl.sum() + (1 - s) * np.log(max(1 - s, 1e-300)) - a @ x
+
+
+@pytest.mark.parametrize("alpha", [0.5, 1.0, 3.0])
+def test_topk_entropy_biased_k1_bisection(oracle, alpha):
+    """k = 1 (topk_entropy_biased.h:211-222): t solves
+    W(e^(alpha - t)) + sum_i W(e^(a_i - t)) = alpha, x = W(e^(a - t)) / alpha;
+    t from a float64 bisection with scipy's W, x also against SLSQP."""
+    X = np.concatenate([inputs.normal(20, 12, np.float64, 95, 2.0),
+                        inputs.uniform(10, 12, np.float64, 96, -20, 5)])
+    P, thr = prox(oracle, "topk_entropy_biased", X, k=1, alpha=alpha)
+    for a, x, th in zip(X, P, thr):
+        g = lambda t: (w_exp(alpha - t) + sum(w_exp(v - t) for v in a)) - alpha
+        t = bisect(g, -60.0, 60.0)
+        assert abs(th[0] - t) <= 1e-10 * max(1, abs(t))
+        assert np.allclose(x, np.array([w_exp(v - t) for v in a]) / alpha, rtol=1e-10, atol=1e-300)
+        assert th[2] == pytest.approx(x.sum(), rel=1e-12)  # hi = s
+    a, x = X[0], P[0]
+    cons = [{"type": "ineq", "fun": lambda z: 1 - z.sum()},
+            {"type": "ineq", "fun": lambda z: z.sum() - z}]
+    sol = scipy.optimize.minimize(biased_entropy_objective, np.full(len(a), 0.5 / len(a)),
+                                  args=(a, alpha), method="SLSQP", bounds=[(0, 1)] * len(a),
+                                  constraints=cons, options={"ftol": 1e-15, "maxiter": 500})
+    assert np.allclose(x, sol.x, atol=1e-5)
+
+
+@pytest.mark.parametrize("k,alpha", [(2, 1.0), (3, 0.5), (3, 2.0), (2, 0.1)])
+def test_topk_entropy_biased_slsqp(oracle, k, alpha):
+    """min 0.5 alpha (<x,x> + s^2) + <x, log x> + (1 - s) log(1 - s) - <a, x>
+    over s = sum x <= 1, 0 <= x_i <= s / k (topk_entropy_biased.h:179-200).
+
+    Every result is feasible (the reference's own check,
+    test/prox/topk_entropy_biased.cpp:5-18).  Where no entry sits at the cap
+    (the set U of topk_entropy_biased.h:224-230 is empty) the result is the
+    minimiser: no worse than SLSQP's and within 1e-5 of it.  Where U is not
+    empty, the reference's two-equation system (topk_entropy_biased.h:120-176)
+    is not the stationarity system of this problem and its x is feasible but
+    not the minimiser; the oracle reproduces that result bit for bit (checked
+    against the compiled reference), and this test records the deviation so
+    that a change in it is noticed."""
+    X = np.concatenate([inputs.normal(6, 7, np.float64, 97, 2.0),
+                        inputs.label_shifted(6, 7, np.float64, 98),
+                        inputs.normal(10, 7, np.float64, 99, 0.5)])
+    X[:4, :2] += 6.0  # two dominant entries: U non-empty
+    P, thr = prox(oracle, "topk_entropy_biased", X, k=k, alpha=alpha)
+    n_empty = n_capped = 0
+    for a, x, th in zip(X, P, thr):
+        s = x.sum()
+        assert s <= 1 + 1e-12 and np.all(x >= 0) and np.all(x <= s / k + 1e-12)
+        cons = [{"type": "ineq", "fun": lambda z: 1 - z.sum()},
+                {"type": "ineq", "fun": lambda z: z.sum() / k - z}]
+        sol = scipy.optimize.minimize(biased_entropy_objective, np.full(len(a), 0.5 / len(a)),
+                                      args=(a, alpha), method="SLSQP", bounds=[(0, 1)] * len(a),
+                                      constraints=cons, options={"ftol": 1e-15, "maxiter": 1000})
+        unclamped = np.array([w_exp(v - th[0]) for v in a]) / alpha
+        if np.all(unclamped <= th[2] * (1 + 1e-9)):
+            n_empty += 1
+            assert biased_entropy_objective(x, a, alpha) <= sol.fun + 1e-9
+            assert np.allclose(x, sol.x, atol=1e-5), (a, x, sol.x)
+        else:
+            n_capped += 1
+            assert biased_entropy_objective(x, a, alpha) > sol.fun + 1e-6
+    assert n_empty >= 9 and n_capped >= 7

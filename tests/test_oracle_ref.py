@@ -41,6 +41,9 @@ OPS = [
     ("topk_simplex_biased", dict(k=3, rhs=2.5, rho=2.0)),
     ("topk_cone_biased", dict(k=1, rho=1.0)),
     ("topk_cone_biased", dict(k=3, rho=0.25)),
+    ("topk_entropy_biased", dict(k=1, alpha=1.0)),
+    ("topk_entropy_biased", dict(k=3, alpha=0.5)),
+    ("topk_entropy_biased", dict(k=5, alpha=2.0)),
     ("two_simplex_sort", dict(p=1)),
     ("two_simplex_sort", dict(p=3, rhs=2.0)),
 ]
@@ -70,7 +73,7 @@ def test_prox_bit_exact(oracle, reference, op, kw, m, dtype, result):
     if op in ("two_simplex", "two_simplex_sort") and (m < 2 or kw["p"] >= m):
         pytest.skip("p must be in [1, m-1]")
     if op in ("topk_simplex", "topk_cone", "topk_entropy", "topk_simplex_biased",
-              "topk_cone_biased") and kw["k"] > m:
+              "topk_cone_biased", "topk_entropy_biased") and kw["k"] > m:
         pytest.skip("k > m")
     if op in ("knapsack_eq",) and (kw.get("hi", 1.0) * m < kw.get("rhs", 1.0) or kw.get("lo", 0.0) * m > kw.get("rhs", 1.0)):
         pytest.skip("infeasible")
