@@ -62,8 +62,7 @@ typedef enum sdca_prox_op {
   SDCA_PROX_KNAPSACK_LE_BIASED = 9,   /* knapsack_le_biased.h:165-180 (uses rho) */
   SDCA_PROX_TOPK_SIMPLEX_BIASED = 10, /* topk_simplex_biased.h:105-119 (uses rho) */
   SDCA_PROX_TOPK_CONE_BIASED = 11,    /* topk_cone_biased.h:145-158 (uses rho) */
-  /* Not on this path yet: returns SDCA_ERR_NOT_IMPLEMENTED. */
-  SDCA_PROX_TOPK_ENTROPY_BIASED = 12,
+  SDCA_PROX_TOPK_ENTROPY_BIASED = 12, /* topk_entropy_biased.h:302-315 (uses k, alpha) */
   SDCA_PROX_TWO_SIMPLEX_SORT = 13     /* two_simplex_sort.h:175-190 (uses p / col_p) */
 } sdca_prox_op;
 

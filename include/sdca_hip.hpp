@@ -186,6 +186,18 @@ inline void prox_topk_cone_biased(std::ptrdiff_t dim, Data* first, Data* last, D
   detail::run<Result>(SDCA_PROX_TOPK_CONE_BIASED, dim, first, last, p);
 }
 
+// topk_entropy_biased.h:302-315 (Result is deduced from alpha, as in the
+// reference)
+template <typename Result = double, typename Data>
+inline void prox_topk_entropy_biased(std::ptrdiff_t dim, Data* first, Data* last,
+                                     Data* /*aux*/, const std::ptrdiff_t k = 1,
+                                     const Result alpha = 1) {
+  sdca_prox_params p = detail::params();
+  p.k = k;
+  p.alpha = static_cast<double>(alpha);
+  detail::run<Result>(SDCA_PROX_TOPK_ENTROPY_BIASED, dim, first, last, p);
+}
+
 // two_simplex_sort.h:175-190
 template <typename Result = double, typename Data>
 inline void prox_two_simplex_sort(std::ptrdiff_t dim, std::ptrdiff_t p_split, Data* first,

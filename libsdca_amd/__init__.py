@@ -193,9 +193,9 @@ def _rows(dim, A):
 
 # The reference's batched overloads (`dim` first).  Result follows the
 # reference: deduced from the floating parameter's type in C++; here the
-# element type unless `result` is given.  prox_topk_cone / prox_topk_entropy
-# default to double, as their C++ templates do (topk_cone.h:187-199,
-# topk_entropy.h:106-118).
+# element type unless `result` is given.  prox_topk_cone, prox_topk_entropy
+# and prox_topk_entropy_biased default to double, as their C++ templates do
+# (topk_cone.h:187-199, topk_entropy.h:106-118, topk_entropy_biased.h:302-315).
 def prox_knapsack_eq(dim, A, lo=0.0, hi=1.0, rhs=1.0, result=None):
     return prox("knapsack_eq", _rows(dim, A), lo=lo, hi=hi, rhs=rhs, result=result)
 
@@ -238,6 +238,10 @@ def prox_topk_simplex_biased(dim, A, k=1, rhs=1.0, rho=1.0, result=None):
 
 def prox_topk_cone_biased(dim, A, k=1, rho=1.0, result=None):
     return prox("topk_cone_biased", _rows(dim, A), k=k, rho=rho, result=result)
+
+
+def prox_topk_entropy_biased(dim, A, k=1, alpha=1.0, result="double"):
+    return prox("topk_entropy_biased", _rows(dim, A), k=k, alpha=alpha, result=result)
 
 
 def prox_two_simplex_sort(dim, p, A, rhs=1.0, result=None):

@@ -139,9 +139,6 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   else sdca_prox_params_default(&p);
   if (static_cast<int>(op) < 0 || op > SDCA_PROX_TWO_SIMPLEX_SORT)
     return fail(SDCA_ERR_PROX, "unknown prox operator %d", static_cast<int>(op));
-  if (op == SDCA_PROX_TOPK_ENTROPY_BIASED)
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "prox operator %d is not implemented on the GPU",
-                static_cast<int>(op));
   const bool biased = op == SDCA_PROX_KNAPSACK_LE_BIASED || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
                       op == SDCA_PROX_TOPK_CONE_BIASED;
   int rc = check_dtypes(data, result);
@@ -156,7 +153,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   if (!(p.alpha > 0)) return fail(SDCA_ERR_ARG_RANGE, "alpha must be > 0 (got %g)", p.alpha);
   const bool uses_k = op == SDCA_PROX_TOPK_SIMPLEX || op == SDCA_PROX_TOPK_CONE ||
                       op == SDCA_PROX_TOPK_ENTROPY || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
-                      op == SDCA_PROX_TOPK_CONE_BIASED;
+                      op == SDCA_PROX_TOPK_CONE_BIASED || op == SDCA_PROX_TOPK_ENTROPY_BIASED;
   if (uses_k && (p.k < 1 || p.k > m))
     return fail(SDCA_ERR_ARG_RANGE, "k must be in [1, %lld] (got %lld)", (long long)m, (long long)p.k);
   const bool two = op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT;
@@ -180,14 +177,15 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   const bool reg_ok = m <= kRegMaxM;
   const bool topk = op == SDCA_PROX_TOPK_SIMPLEX || op == SDCA_PROX_TOPK_CONE;
   const bool knap = op == SDCA_PROX_KNAPSACK_EQ || op == SDCA_PROX_KNAPSACK_LE;
-  if (!reg_ok && !(topk || knap || biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
+  const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED;
+  if (!reg_ok && !(topk || knap || biased || ent_biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
       op != SDCA_PROX_TWO_SIMPLEX_SORT)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "operator %d supports m <= %lld on the GPU (got %lld)",
                 static_cast<int>(op), (long long)kRegMaxM, (long long)m);
   if ((topk || knap) && m > slow_max_m(data) && (!reg_ok || (topk && p.k > kTopkMaxK)))
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
                 (long long)m, (long long)slow_max_m(data));
-  if ((biased || op == SDCA_PROX_TWO_SIMPLEX_SORT) && m > slow_max_m(data))
+  if ((biased || ent_biased || op == SDCA_PROX_TWO_SIMPLEX_SORT) && m > slow_max_m(data))
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
                 (long long)m, (long long)slow_max_m(data));
 
@@ -235,6 +233,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   a.hi = p.hi;
   a.rhs = p.rhs;
   a.rho = p.rho;
+  a.alpha = p.alpha;
   a.k = p.k;
   a.p = p.p;
   a.col_p = d_colp;
@@ -246,6 +245,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
   } else if (op == SDCA_PROX_TWO_SIMPLEX_SORT) {
     SDCA_HIP_TRY(launch_two_sort(a), "two_simplex_sort kernel (workgroup per column)");
+  } else if (ent_biased) {
+    SDCA_HIP_TRY(launch_ent_biased(a), "topk_entropy_biased kernel (wave per column)");
   } else if (biased || ((topk || knap) && (!reg_ok || (topk && p.k > kTopkMaxK)))) {
     // The biased operators' searches need the sorted column: one workgroup
     // per column (knapsack_le_biased.h, topk_simplex_biased.h,

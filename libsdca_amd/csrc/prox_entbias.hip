@@ -1,0 +1,270 @@
+// Biased top-k entropy prox (topk_entropy_biased.h:179-268), one wave per
+// column:
+//   x = clamp(W(exp(a - t)) / alpha, 0, s / k)
+// with (s, t) from the reference's two solves - the order-4 Householder
+// iteration on W(e^(alpha - t)) + sum_i W(e^(a_i - t)) = alpha while no entry
+// is capped (:9-61), then, while the feasibility test fails, the set U of
+// capped entries grows by the largest remaining entry and (s, t) come from
+// the Newton iteration on the two-equation system of :120-176.
+//
+// Each pass of either iteration is a sum of W(e^(a_i - t)) and its
+// derivatives over the column: the column sits in LDS, each lane sums a
+// stride-64 share, and a butterfly reduction gives every lane the totals, so
+// the scalar updates run uniformly on all 64 lanes and no barrier beyond the
+// wave is needed.  Entries moved into U are overwritten with -inf in LDS,
+// where W(e^-inf) = 0 drops them from every later sum; the final clamp reads
+// the column again from global memory.
+#include "common.hpp"
+#include "prox_impl.hpp"
+#include "prox_launch.hpp"
+
+namespace sdca_gpu {
+
+namespace {
+
+constexpr int kEbMaxWaves = 4;
+
+// f0 = sum_i W(e^(s_i + t)), f1 = sum_i W / (1 + W) (lambert.h:253-271).
+template <class D, class R>
+__device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1) {
+  R a0(0), a1(0);
+  for (int i = lane; i < m; i += 64) {
+    const R v = lambert_w_exp(static_cast<R>(s[i]) + t);
+    a0 += v;
+    a1 += div_near(v, R(1) + v);
+  }
+  f0 = group_sum<64>(a0);
+  f1 = group_sum<64>(a1);
+}
+
+// f0..f3: W and its first three derivatives in t (lambert.h:308-332).
+template <class D, class R>
+__device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, R& f2, R& f3) {
+  R a0(0), a1(0), a2(0), a3(0);
+  for (int i = lane; i < m; i += 64) {
+    const R v = lambert_w_exp(static_cast<R>(s[i]) + t);
+    const R d = R(1) + v;
+    const R d3 = d * d * d;
+    a0 += v;
+    a1 += div_near(v, d);
+    a2 += div_near(v, d3);
+    a3 += div_near(v * (R(1) - R(2) * v), d3 * d * d);
+  }
+  f0 = group_sum<64>(a0);
+  f1 = group_sum<64>(a1);
+  f2 = group_sum<64>(a2);
+  f3 = group_sum<64>(a3);
+}
+
+// Largest entry of the LDS column and the lowest index holding it (an index
+// below m for m >= 1, also when every entry is -inf).
+template <class D>
+__device__ inline void wave_argmax(const D* s, int m, int lane, D& mx, int& idx) {
+  D best = -num<D>::inf();
+  int at = m;
+  for (int i = lane; i < m; i += 64) {
+    const D v = s[i];
+    if (v > best || at == m) {
+      best = v;
+      at = i;
+    }
+  }
+  mx = group_max<64>(best);
+  idx = group_min<64>(best == mx ? at : m);
+}
+
+template <class R>
+__device__ inline R log_w_inverse_or_min(R w) {
+  // max(lambert_w_exp_inverse(w), exp_min_arg) (lambert.h:210-214, log_exp.h:27-52)
+  const R v = w + dlog(w);
+  return (v < num<R>::exp_min_arg()) ? num<R>::exp_min_arg() : v;
+}
+
+// Thresholds (t, 0, hi) of one column whose copy is in s[0, m); entries of U
+// are overwritten with -inf.
+template <class D, class R>
+__device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_out,
+                                   R& hi_out) {
+  const R eps_r = num<R>::eps();
+  const R tiny = R(64) * num<R>::min_normal();
+  D mx_d;
+  int mx_i;
+  wave_argmax(s, m, lane, mx_d, mx_i);
+  R max = static_cast<R>(mx_d);
+  const R eps = R(16) * eps_r * (max > R(1) ? max : R(1));
+
+  // U empty: Householder on alpha_sum_w_exp (topk_entropy_biased.h:9-61),
+  // from the reference's start t = max with its steps and stopping test.
+  // g(t) = W(e^(alpha - t)) + sum_i W(e^(a_i - t)) - alpha is convex and
+  // decreasing with its root in [-log alpha, log((e^alpha + m e^max) / alpha)]
+  // (W(e^x) <= e^x), and every pass narrows that bracket by the sign of g.
+  // A step that leaves the bracket is replaced by the Newton step, or by
+  // bisection when that leaves it too.  Far below the root the order-4
+  // correction can point the wrong way; the reference then wanders and, if it
+  // has not come back within its 32 steps, returns an iterate that is not a
+  // root (and that depends on the rounding of its sums).  Steps inside the
+  // bracket are the reference's own, so wherever the reference settles both
+  // reach the same root; elsewhere this solve still reaches it, within 64
+  // passes.
+  R sv(0), t(max);
+  R br_lo = -dlog(alpha), br_hi;
+  {
+    const R top = (alpha > max) ? alpha : max;
+    br_hi = top + dlog(dexp(alpha - top) + static_cast<R>(m) * dexp(max - top)) - dlog(alpha);
+  }
+  for (int iter = 0; iter < 64; ++iter) {
+    const R t1 = t;
+    R f0, f1, f2, f3;
+    lw_sums4(s, m, lane, -t, f0, f1, f2, f3);
+    sv = f0 / alpha;
+    {
+      const R v = lambert_w_exp(alpha - t);
+      const R d = R(1) + v;
+      const R d3 = d * d * d;
+      f0 += v;
+      f1 += v / d;
+      f2 += v / d3;
+      f3 += v * (R(1) - R(2) * v) / (d3 * d * d);
+    }
+    f0 -= alpha;
+    if (f0 > R(0)) br_lo = (t > br_lo) ? t : br_lo;
+    else if (f0 < R(0)) br_hi = (t < br_hi) ? t : br_hi;
+    const R f02 = f0 * f2, f11 = f1 * f1;
+    const R den = R(6) * f1 * (f02 - f11) - f0 * (f0 * f3);
+    R step = (fabs(den) > tiny) ? R(3) * f0 * (R(2) * f11 - f02) / den : R(0);
+    R tn = t - step;
+    // Inside the bracket, or a correction below the resolution of t.
+    bool ok = isfinite(tn) && ((tn > br_lo && tn < br_hi) || (step != R(0) && tn == t));
+    if (!ok) {
+      step = (f1 > R(0)) ? -f0 / f1 : R(0);  // Newton: f1 = -g'(t)
+      tn = t - step;
+      ok = isfinite(tn) && ((tn > br_lo && tn < br_hi) || (step != R(0) && tn == t));
+      if (!ok) tn = br_lo + (br_hi - br_lo) * R(0.5);
+    }
+    t = tn;
+    if (fabs(t1 - t) <= eps_r) break;
+  }
+  const R K = static_cast<R>(k);
+  t_out = t;
+  if (k == 1) {
+    hi_out = sv;
+    return;
+  }
+  const R alpha_k = alpha / K;
+  R tt = t + log_w_inverse_or_min(alpha_k * sv);
+  if (max - eps <= tt) {
+    hi_out = sv / K;
+    return;
+  }
+
+  // U not empty (topk_entropy_biased.h:224-266).
+  if (lane == 0) s[mx_i] = -num<D>::inf();
+  wave_lds_sync();
+  const R log_k = dlog(K), log_alpha = dlog(alpha);
+  R min_u(max), sum_u(max);
+  int num_u = 1;
+  for (int remaining = m - 1; remaining > 0;) {
+    wave_argmax(s, m, lane, mx_d, mx_i);
+    max = static_cast<R>(mx_d);
+    sv = R(0.999);
+    t = max;
+    {  // Newton on the KKT system (topk_entropy_biased.h:64-176)
+      const R U = static_cast<R>(num_u);
+      const R C1 = U * K, C2 = (K + U) * alpha, C3 = (K - U) * (U - R(1)) * alpha;
+      const R C4 = K * (U - R(1)), C5 = (R(1) - U / K) * alpha;
+      const R C0 = C4 * log_alpha - C1 * log_k - sum_u;
+      const R tol = R(16) * eps_r;
+      for (int iter = 0; iter < 32; ++iter) {
+        const R s1 = sv, t1 = t;
+        sv = (sv < R(0)) ? R(0) : ((sv > R(1)) ? R(1) : sv);
+        R S0, S1;
+        lw_sums2(s, m, lane, -t, S0, S1);
+        const R E = S0 + t * S1;
+        R z, Az, Bz;
+        if (sv < R(0.5)) {
+          z = sv;
+          Az = K * (z * (U + dlog1p(-z) + z / (R(1) - z)) - U * x_log_x(z)) - C0 * z;
+          Bz = z * (C2 + K / (R(1) - z)) + C1;
+        } else {
+          z = R(1) - sv;
+          Az = K * (z * (U - U * dlog1p(-z) - R(1)) + x_log_x(z) + R(1)) - C0 * z;
+          Bz = z * (C2 + C1 / (R(1) - z)) + K;
+        }
+        const R Dz = C3 * z - Bz * S1;
+        if (fabs(Dz) > tiny) {
+          sv = (C4 * E * z - Az * S1) / Dz;
+          t = (C5 * Az - E * Bz) / Dz;
+        }
+        if (fabs(s1 - sv) + fabs(t1 - t) <= tol) break;
+      }
+      sv = (sv < R(0)) ? R(0) : ((sv > R(1)) ? R(1) : sv);
+    }
+    tt = t + log_w_inverse_or_min(alpha_k * sv);
+    if (max - eps <= tt && tt <= min_u + eps) break;
+    if (++num_u > k) break;
+    min_u = max;
+    sum_u += max;
+    if (lane == 0) s[mx_i] = -num<D>::inf();
+    wave_lds_sync();
+    --remaining;
+  }
+  t_out = t;
+  hi_out = sv / K;
+}
+
+template <class D, class R>
+__global__ void __launch_bounds__(64 * kEbMaxWaves)
+entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, int k,
+               R alpha, sdca_thresholds* __restrict__ thr, int stride_elems) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int waves = blockDim.x >> 6;
+  D* s = reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
+  const int m = static_cast<int>(m64);
+  const D map_a = D(1) / static_cast<D>(alpha);  // a_lambert_w_exp_map (functor.h:33-38)
+  for (int64_t j = static_cast<int64_t>(blockIdx.x) * waves + wave; j < n;
+       j += static_cast<int64_t>(gridDim.x) * waves) {
+    const D* col = in + j * m64;
+    for (int i = lane; i < m; i += 64) s[i] = col[i];
+    wave_lds_sync();
+    R t, hi;
+    entbias_thresholds<D, R>(s, m, lane, k, alpha, t, hi);
+    if (thr && lane == 0) {
+      thr[j].t = static_cast<double>(t);
+      thr[j].lo = 0;
+      thr[j].hi = static_cast<double>(hi);
+    }
+    const D td = static_cast<D>(t), hd = static_cast<D>(hi);
+    D* dst = out + j * m64;
+    for (int i = lane; i < m; i += 64)
+      dst[i] = clamp_ref(map_a * lambert_w_exp(col[i] - td), D(0), hd);
+    wave_lds_sync();  // every lane is done with s before the next column's copy
+  }
+}
+
+template <class D, class R>
+hipError_t launch_t(const ProxLaunch& a) {
+  const int stride = static_cast<int>((a.m + 3) & ~int64_t(3));  // 16-byte aligned slices
+  const size_t per_wave = static_cast<size_t>(stride) * sizeof(D);
+  int waves = kEbMaxWaves;
+  while (waves > 1 && waves * per_wave > 65536) waves >>= 1;
+  int64_t grid = (a.n + waves - 1) / waves;
+  if (grid > 16384) grid = 16384;
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL((entbias_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
+                     waves * per_wave, a.stream, static_cast<const D*>(a.in),
+                     static_cast<D*>(a.out), a.m, a.n, static_cast<int>(a.k),
+                     static_cast<R>(a.alpha), a.thr, stride);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_ent_biased(const ProxLaunch& a) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_t<float, float>(a);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_t<float, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_t<double, double>(a);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace sdca_gpu

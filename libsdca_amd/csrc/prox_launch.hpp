@@ -38,7 +38,7 @@ struct ProxLaunch {
   int64_t m, n;
   const void* in;
   void* out;
-  double lo, hi, rhs, rho;
+  double lo, hi, rhs, rho, alpha;
   int64_t k, p;
   const int64_t* col_p;     // device, or NULL
   sdca_thresholds* thr;     // device, or NULL
@@ -53,6 +53,8 @@ hipError_t launch_ent(const ProxLaunch& a);
 hipError_t launch_ent_norm(const ProxLaunch& a);
 // Two-block simplex by sort and scan, one workgroup per column (prox_slow.hip).
 hipError_t launch_two_sort(const ProxLaunch& a);
+// Biased top-k entropy, one wave per column (prox_entbias.hip).
+hipError_t launch_ent_biased(const ProxLaunch& a);
 hipError_t launch_topkent(const ProxLaunch& a);
 hipError_t launch_two(const ProxLaunch& a);
 // Workgroup-per-column kernel over the flagged list (all_columns: every column).

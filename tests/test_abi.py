@@ -61,8 +61,14 @@ def test_prox_operator_and_precision_checks():
         sd.prox(42, x)
     assert e.value.status == 7  # LIBSDCA:prox
     with pytest.raises(sd.SdcaError) as e:
-        sd.prox("topk_entropy_biased", x)
-    assert e.value.status == 4  # not on this path
+        sd.prox("topk_entropy_biased", np.zeros((2, 8193), np.float32))
+    assert e.value.status == 4  # above the workgroup-per-column limit
+    with pytest.raises(sd.SdcaError) as e:
+        sd.prox("topk_entropy_biased", x, k=6)
+    assert e.value.status == 2
+    with pytest.raises(sd.SdcaError) as e:
+        sd.prox("topk_entropy_biased", x, alpha=0.0)
+    assert e.value.status == 2
     with pytest.raises(sd.SdcaError) as e:
         sd.prox("topk_simplex", x, result="long double")
     assert e.value.status == 4
@@ -114,6 +120,7 @@ int main() {
   sdca::hip::prox_knapsack_le_biased(10, d, d + b.size(), bux.data(), 0.0, 1.0, 1.0, 0.5);
   sdca::hip::prox_topk_simplex_biased(100, f, f + a.size(), aux.data(), 5, 1.0f, 0.5f);
   sdca::hip::prox_topk_cone_biased(100, f, f + a.size(), aux.data(), 5, 0.5f);
+  sdca::hip::prox_topk_entropy_biased(100, f, f + a.size(), aux.data(), 5, 0.5f);
   std::vector<sdca_objective> objs(1);
   objs[0].kind = SDCA_OBJ_ENTROPY; objs[0].c = 1; objs[0].gamma = 1; objs[0].k = 1;
   std::vector<int64_t> y(4, 0);

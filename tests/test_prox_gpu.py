@@ -52,10 +52,13 @@ def run_oracle(oracle, op, x, result, nthreads=1, **kw):
 LONG_DOUBLE = 2
 
 
-def parity(oracle, op, x, got, result, what, nthreads=1, **kw):
-    """Check got (GPU) against the oracle at the Result type and in long double."""
+def parity(oracle, op, x, got, result, what, nthreads=1, keep=None, **kw):
+    """Check got (GPU) against the oracle at the Result type and in long double
+    (over the columns `keep` selects, all by default)."""
     ref, _ = run_oracle(oracle, op, x, result, nthreads, **dict(kw))
     exact, _ = run_oracle(oracle, op, x, LONG_DOUBLE, nthreads, **dict(kw))
+    if keep is not None:
+        x, got, ref, exact = x[keep], got[keep], ref[keep], exact[keep]
     scale = np.maximum(1.0, np.abs(x.astype(np.float64)).max(axis=1, keepdims=True))
     g = got.astype(np.float64)
     r = ref.astype(np.float64)
@@ -309,3 +312,68 @@ def test_two_simplex_sort(cuda, oracle, m, dtype, result):
             got, _ = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, p=p)
             parity(oracle, "two_simplex_sort", x, got, result,
                    f"two_simplex_sort p={p} rhs={rhs} {name} m={m}", rhs=rhs, p=p)
+
+
+def entbias_settled(oracle, x, alpha, result):
+    """Columns on which the reference's uncapped solve ends on a root.
+
+    That solve (topk_entropy_biased.h:48-61) does not depend on k, so its
+    iterate t is the threshold of the k = 1 result.  It should be a root of
+    g(t) = W(e^(alpha - t)) + sum_i W(e^(a_i - t)) - alpha.  From a start far
+    below the root (every entry far below zero) the order-4 correction can
+    point away from it, and the reference returns its 32nd iterate.  Where that
+    path hinges on the rounding of the sums, no other summation order can
+    reproduce the iterate, so those columns have no parity target and are left
+    out.  A settled iterate has |g| at rounding level (that of t itself
+    included: |g'(t)| * 8 eps |t|); the cut at 1e-3 of the sum's size above it
+    is far from both that and an unsettled iterate's |g| ~ alpha.
+    """
+    _, thr = run_oracle(oracle, "topk_entropy_biased", x, result, 8, k=1, alpha=alpha)
+    return entbias_is_root(oracle, x, alpha, result, thr[:, 0])
+
+
+def entbias_is_root(oracle, x, alpha, result, t):
+    """|g(t)| at rounding level, column by column (g as in entbias_settled)."""
+    z = np.concatenate([x.astype(np.float64) - t[:, None],
+                        (alpha - t)[:, None]], axis=1)
+    oracle.prox("lambert_w_exp", z)
+    total = z.sum(axis=1)
+    slope = (z / (1 + z)).sum(axis=1)
+    eps = np.finfo(np.float32 if result == F32 else np.float64).eps
+    return np.abs(total - alpha) <= 1e-3 * (alpha + total) + 8 * eps * np.abs(t) * slope
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [1, 5, 17, 64, 100, 1000])
+@pytest.mark.parametrize("k,alpha", [(1, 1.0), (3, 0.5), (5, 2.0)])
+def test_topk_entropy_biased(cuda, oracle, k, alpha, m, dtype, result):
+    """Biased top-k entropy, one wave per column (both the uncapped
+    Householder solve and the growing capped set)."""
+    if k > m:
+        pytest.skip("k > m")
+    for name, x in cases(m, dtype, 170 + m):
+        if name == "label+2":
+            x = x.copy()
+            x[: len(x) // 2, :2] += 6.0  # dominant entries: the capped branch
+        keep = entbias_settled(oracle, x, alpha, result)
+        assert keep.mean() >= 0.95, f"{name}: {np.count_nonzero(~keep)} unsettled columns"
+        if not keep.all():
+            print(f"topk_entropy_biased {name} m={m}: {np.count_nonzero(~keep)} of {len(keep)} "
+                  f"columns where the reference's uncapped solve ends unsettled")
+        got, thr = run_gpu("topk_entropy_biased", x, result, cuda, k=k, alpha=alpha)
+        parity(oracle, "topk_entropy_biased", x, got, result,
+               f"topk_entropy_biased k={k} alpha={alpha} {name} m={m}", nthreads=8, keep=keep,
+               k=k, alpha=alpha)
+        if k == 1 and not keep.all():
+            # Where the reference stops short, the GPU's threshold is a root.
+            assert entbias_is_root(oracle, x[~keep], alpha, result, thr[~keep, 0]).all()
+
+
+@pytest.mark.parametrize("dtype,result,m", [(np.float32, F32, 8192), (np.float64, F64, 4096)])
+def test_topk_entropy_biased_largest_m(cuda, oracle, dtype, result, m):
+    x = inputs.normal(16, m, dtype, 180, 2.0)
+    x[:8, :3] += 8.0
+    assert entbias_settled(oracle, x, 1.5, result).all()
+    got, _ = run_gpu("topk_entropy_biased", x, result, cuda, k=4, alpha=1.5)
+    parity(oracle, "topk_entropy_biased", x, got, result, f"topk_entropy_biased m={m}",
+           nthreads=8, k=4, alpha=1.5)
