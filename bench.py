@@ -64,6 +64,27 @@ CONFIGS = {
                    gen="normal", seed=4105, col_p=True,
                    desc="batched two-block simplex prox, m=200, n=500,000, fp32, N(0,1), "
                         "per-column p in [1,5]"),
+    # The operators next to the path, on the same inputs as above.
+    "c2sbias": dict(op="topk_simplex_biased", m=100, n=4_000_000, dtype="f32", result="f32", k=5,
+                    rhs=1.0, rho=1.0, gen="label_shifted", seed=102,
+                    desc="batched biased top-k simplex prox (rho=1), m=100, n=4,000,000, k=5, "
+                         "rhs=1, fp32, N(0,1) with the label row +2"),
+    "c2cbias": dict(op="topk_cone_biased", m=100, n=4_000_000, dtype="f32", result="f32", k=5,
+                    rho=1.0, gen="label_shifted", seed=102,
+                    desc="batched biased top-k cone prox (rho=1), m=100, n=4,000,000, k=5, "
+                         "fp32, N(0,1) with the label row +2"),
+    "c1lebias": dict(op="knapsack_le_biased", m=10, n=100_000, dtype="f64", result="f64", lo=0.0,
+                     hi=1.0, rhs=1.0, rho=1.0, gen="normal", seed=101, rotate=40,
+                     desc="batched biased knapsack_le prox (lo=0 hi=1 rhs=1 rho=1), m=10, "
+                          "n=100,000, fp64, N(0,1)"),
+    "c5sort": dict(op="two_simplex_sort", m=200, n=500_000, dtype="f32", result="f32", rhs=1.0,
+                   gen="normal", seed=4105, col_p=True,
+                   desc="batched two-block simplex prox by sort and scan, m=200, n=500,000, "
+                        "fp32, N(0,1), per-column p in [1,5]"),
+    "c3ebias": dict(op="topk_entropy_biased", m=1000, n=200_000, dtype="f64", result="f64", k=5,
+                    alpha=1.0, gen="uniform10", seed=103,
+                    desc="batched biased top-k entropy prox (k=5, alpha=1), m=1000, n=200,000, "
+                         "fp64, U(-10,10)"),
     "c4": dict(op="eval", d=4096, m=1000, n=100_000, dtype="f32", result="f32", seed=104,
                objs=[("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)],
                desc="evaluation pass, fp32: X d=4096 x n=100,000 (N(0,1), unit columns), "
@@ -155,7 +176,7 @@ def make_input(cfg, torch, dev):
 
 def kwargs_of(cfg):
     kw = {}
-    for key in ("lo", "hi", "rhs", "k"):
+    for key in ("lo", "hi", "rhs", "rho", "alpha", "k"):
         if key in cfg:
             kw[key] = cfg[key]
     return kw

@@ -109,6 +109,14 @@ def library():
         if not os.path.exists(LIB_PATH):
             raise SdcaError(6, f"{LIB_PATH} is missing: build it with "
                                "`python -c 'import __graft_entry__ as g; g.build()'`")
+        # torch ships its own HIP runtime under the same soname; loading torch
+        # first makes the library bind to it, so that a process that uses both
+        # holds one runtime (two runtimes in one process leave the second
+        # without a device).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = ctypes.CDLL(LIB_PATH)
         lib.sdca_prox.restype = ctypes.c_int
         lib.sdca_prox.argtypes = [

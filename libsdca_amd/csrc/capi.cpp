@@ -177,6 +177,13 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   const bool reg_ok = m <= kRegMaxM;
   const bool topk = op == SDCA_PROX_TOPK_SIMPLEX || op == SDCA_PROX_TOPK_CONE;
   const bool knap = op == SDCA_PROX_KNAPSACK_EQ || op == SDCA_PROX_KNAPSACK_LE;
+  // The biased simplex and knapsack run in the register kernel up to the
+  // equality knapsack and its test; columns that need the sorted search are
+  // deferred to the workgroup-per-column kernel through the column list.
+  const bool reg_biased =
+      op == SDCA_PROX_TOPK_SIMPLEX_BIASED || op == SDCA_PROX_KNAPSACK_LE_BIASED;
+  const bool topk_like = topk || op == SDCA_PROX_TOPK_SIMPLEX_BIASED;
+  const bool listed = topk || reg_biased;
   const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED;
   if (!reg_ok && !(topk || knap || biased || ent_biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
       op != SDCA_PROX_TWO_SIMPLEX_SORT)
@@ -247,10 +254,10 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     SDCA_HIP_TRY(launch_two_sort(a), "two_simplex_sort kernel (workgroup per column)");
   } else if (ent_biased) {
     SDCA_HIP_TRY(launch_ent_biased(a), "topk_entropy_biased kernel (wave per column)");
-  } else if (biased || ((topk || knap) && (!reg_ok || (topk && p.k > kTopkMaxK)))) {
-    // The biased operators' searches need the sorted column: one workgroup
-    // per column (knapsack_le_biased.h, topk_simplex_biased.h,
-    // topk_cone_biased.h).
+  } else if (op == SDCA_PROX_TOPK_CONE_BIASED ||
+             ((topk || knap || reg_biased) && (!reg_ok || (topk_like && p.k > kTopkMaxK)))) {
+    // The biased cone's search needs the sorted column (topk_cone_biased.h),
+    // as do columns beyond the register kernel: one workgroup per column.
     SDCA_HIP_TRY(launch_slow(a, true), "prox kernel (workgroup per column)");
   } else {
     // Deferred-column list: [count, done, column ids...].  The deferred-column
@@ -258,7 +265,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     // clear is launched only for a new list or after a call that did not
     // reach that kernel.
     Workspace* wsr = nullptr;
-    if (topk) {
+    if (listed) {
       void* ws = nullptr;
       rc = workspace(stream, 0, static_cast<size_t>(n + 2) * sizeof(int), &ws, &wsr);
       if (rc) return rc;
@@ -269,9 +276,11 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     hipError_t e = hipSuccess;
     switch (op) {
       case SDCA_PROX_KNAPSACK_EQ:
-      case SDCA_PROX_KNAPSACK_LE: e = launch_knap(a); break;
+      case SDCA_PROX_KNAPSACK_LE:
+      case SDCA_PROX_KNAPSACK_LE_BIASED: e = launch_knap(a); break;
       case SDCA_PROX_TOPK_SIMPLEX:
-      case SDCA_PROX_TOPK_CONE: e = launch_topk(a); break;
+      case SDCA_PROX_TOPK_CONE:
+      case SDCA_PROX_TOPK_SIMPLEX_BIASED: e = launch_topk(a); break;
       case SDCA_PROX_ENTROPY:
       case SDCA_PROX_ENTROPY_NORM: e = launch_ent(a); break;
       case SDCA_PROX_TOPK_ENTROPY: e = launch_topkent(a); break;
@@ -279,7 +288,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
       default: break;
     }
     SDCA_HIP_TRY(e, "prox kernel");
-    if (topk) {
+    if (listed) {
       SDCA_HIP_TRY(launch_slow(a, false), "prox kernel (deferred columns)");
       wsr->list_zeroed = true;
     }

@@ -18,7 +18,10 @@ hipError_t launch_one(const ProxLaunch& a) {
   pp.lo = static_cast<R>(a.lo);
   pp.hi = static_cast<R>(a.hi);
   pp.rhs = static_cast<R>(a.rhs);
-  pp.rho = R(0);
+  // rho enters the register kernel only through the biased simplex and
+  // knapsack (the other operators take rho = 0).
+  pp.rho = (a.op == OP_TOPK_SIMPLEX_BIASED || a.op == OP_KNAPSACK_LE_BIASED)
+               ? static_cast<R>(a.rho) : R(0);
   pp.k = static_cast<int>(a.k);
   pp.op = a.op;
   pp.p = static_cast<int>(a.p);

@@ -179,6 +179,71 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
   return st;
 }
 
+// The root of t / rho = sum_i clamp(a_i - t, lo, hi): the solution of
+// knapsack_le_biased_search (knapsack_le_biased.h:10-92) when the sum
+// constraint is inactive.  That search walks the sorted column for the
+// partition (U at hi, M inside, L at lo) with
+//   t = (lo |L| + hi |U| + sum_M a) / (1 / rho + |M|);
+// here the partition comes from variable fixing as in knapsack_eq_regs (the
+// left side is increasing in t, so a positive clamp excess at the trial t
+// means the root is below it and the values above hi + t end at hi; a
+// negative one fixes those at lo).  Each trial t is formed as above from the
+// sum over the values still free, not updated from the previous one: that
+// keeps the large fixed values out of the final sum, as the reference's
+// sum over M does.
+template <int G, int C, class D, class R>
+__device__ inline R knapsack_biased_regs(const D (&v)[C], int m, R total, R lo, R hi, R rhs,
+                                         R rho_inv) {
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  const R qnan = num<R>::quiet_nan();
+  int n_l = 0, n_u = 0;
+  R s_free = total;
+  R w[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(v[c]);
+    w[c] = (x > -num<R>::inf()) ? x : qnan;
+  }
+  R t = 0;
+  for (int iter = 0; iter <= m; ++iter) {
+    const int n_m = m - n_l - n_u;
+    t = (lo * static_cast<R>(n_l) + hi * static_cast<R>(n_u) + s_free) /
+        (rho_inv + static_cast<R>(n_m));
+    if (n_m == 0) break;
+    const R c_lo = lo + t, c_hi = hi + t;
+    R s_lo = 0, s_hi = 0;
+    int n_lh = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const bool lo_c = w[c] <= c_lo;
+      const bool hi_c = w[c] > c_hi;
+      s_lo += lo_c ? w[c] : R(0);
+      s_hi += hi_c ? w[c] : R(0);
+      n_lh += (lo_c ? 1 : 0) + (hi_c ? 0x10000 : 0);
+    }
+    s_lo = group_sum<G>(s_lo);
+    s_hi = group_sum<G>(s_hi);
+    n_lh = group_sum<G>(n_lh);
+    const int n_lo = n_lh & 0xffff, n_hi = n_lh >> 16;
+    const R infeas = s_hi + s_lo - (static_cast<R>(n_hi) * hi + static_cast<R>(n_lo) * lo) -
+                     static_cast<R>(n_hi + n_lo) * t;
+    const bool fix_hi = n_hi > 0 && infeas > eps;
+    const bool fix_lo = !fix_hi && n_lo > 0 && infeas < -eps;
+    if (!fix_hi && !fix_lo) break;
+    R sf = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const bool fixed = fix_hi ? (w[c] > c_hi) : (w[c] <= c_lo);
+      w[c] = fixed ? qnan : w[c];
+      sf += (w[c] == w[c]) ? w[c] : R(0);
+    }
+    s_free = group_sum<G>(sf);
+    if (fix_hi) n_u += n_hi;
+    else n_l += n_lo;
+  }
+  return t;
+}
+
 // Make LDS writes of this wave visible to its own later reads.
 __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -194,7 +259,9 @@ template <int G, int C, class D, class R>
 __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
                                         const ProxParamsT<R>& pp) {
   const R lo = pp.lo, hi = pp.hi, rhs = pp.rhs;
-  if (pp.op == OP_KNAPSACK_LE) {
+  // knapsack_le_biased with rho = 0 is knapsack_le (knapsack_le_biased.h:113-115).
+  const bool biased = pp.op == OP_KNAPSACK_LE_BIASED && pp.rho != R(0);
+  if (pp.op == OP_KNAPSACK_LE || (pp.op == OP_KNAPSACK_LE_BIASED && !biased)) {
     const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
     R s_mid = 0;
     int n_hi = 0, n_mid = 0;
@@ -213,6 +280,15 @@ __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
   }
   const R total = total_sum<G, C, D, R>(v, nvalid);
   KnapState<R> st = knapsack_eq_regs<G, C, D, R>(v, m, nvalid, total, lo, hi, rhs);
+  if (biased) {
+    // knapsack_le_biased.h:117-128: the equality solution stands if
+    // t >= rho rhs - eps; otherwise the sum constraint is inactive.
+    const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+    if (!(st.t >= pp.rho * rhs - eps))
+      return make_thr<R>(knapsack_biased_regs<G, C, D, R>(v, m, total, lo, hi, rhs,
+                                                          R(1) / pp.rho),
+                         lo, hi);
+  }
   return make_thr<R>(st.t, lo, hi);
 }
 
@@ -350,16 +426,19 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
     if (i == k) next = static_cast<R>(top[i]);
   }
   const R largest = static_cast<R>(top[0]);
-  // topk_cone_special_cases (topk_cone.h:18-55)
+  // topk_cone_special_cases (topk_cone.h:18-55), whose divisor is k, or
+  // k + rho k^2 for the biased simplex (topk_simplex_biased.h:50-51).
+  const bool biased = pp.op == OP_TOPK_SIMPLEX_BIASED;
   if (sum_k <= eps16) return make_thr<R>(R(0), R(0), R(0));
-  const R hi_c = sum_k / K;
+  const R hi_c = sum_k / (biased ? K + pp.rho * K * K : K);
   const R t_c = kth - hi_c;
   const bool constant = (k == m) || (t_c >= next - eps16);
   if (pp.op == OP_TOPK_CONE) {
     if (constant) return make_thr<R>(t_c, R(0), hi_c);
     return cone_search_u0<G, C, D, R>(v, K, largest);
   }
-  // thresholds_topk_simplex (topk_simplex.h:39-68)
+  // thresholds_topk_simplex (topk_simplex.h:39-68) and
+  // thresholds_topk_simplex_biased (topk_simplex_biased.h:40-71)
   const R rhs = pp.rhs;
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   if (constant && !(K * hi_c > rhs + eps)) return make_thr<R>(t_c, R(0), hi_c);
@@ -367,15 +446,28 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   KnapState<R> st = topk_knapsack<G, C, L, D, R>(v, top, m, nvalid, kth, hi, rhs, lds_col,
                                                   lds_dummy);
   if (!constant) {
-    // is_topk_simplex_lt (topk_simplex.h:9-27) over U = [first, t.first)
+    // is_topk_simplex_lt (topk_simplex.h:9-27), is_topk_simplex_biased_lt
+    // (topk_simplex_biased.h:9-28), over U = [first, t.first)
     bool lt;
-    if (st.n_u == 0) {
-      lt = st.t < -eps;
+    if (biased) {
+      if (st.n_u == 0) {
+        lt = st.t < pp.rho * rhs - eps;
+      } else {
+        const R num_u = static_cast<R>(st.n_u);
+        lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * (num_u + pp.rho * K * K) - eps;
+      }
+      // The biased cone search (topk_cone_biased.h:58-137) runs on the
+      // sorted column in the workgroup-per-column kernel.
+      if (lt) return slow_thr<R>();
     } else {
-      const R num_u = static_cast<R>(st.n_u);
-      lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * num_u - eps;
+      if (st.n_u == 0) {
+        lt = st.t < -eps;
+      } else {
+        const R num_u = static_cast<R>(st.n_u);
+        lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * num_u - eps;
+      }
+      if (lt) return cone_search_u0<G, C, D, R>(v, K, largest);
     }
-    if (lt) return cone_search_u0<G, C, D, R>(v, K, largest);
   }
   return make_thr<R>(st.t, R(0), hi);
 }
