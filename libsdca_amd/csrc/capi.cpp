@@ -177,12 +177,13 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   const bool reg_ok = m <= kRegMaxM;
   const bool topk = op == SDCA_PROX_TOPK_SIMPLEX || op == SDCA_PROX_TOPK_CONE;
   const bool knap = op == SDCA_PROX_KNAPSACK_EQ || op == SDCA_PROX_KNAPSACK_LE;
-  // The biased simplex and knapsack run in the register kernel up to the
-  // equality knapsack and its test; columns that need the sorted search are
-  // deferred to the workgroup-per-column kernel through the column list.
-  const bool reg_biased =
-      op == SDCA_PROX_TOPK_SIMPLEX_BIASED || op == SDCA_PROX_KNAPSACK_LE_BIASED;
-  const bool topk_like = topk || op == SDCA_PROX_TOPK_SIMPLEX_BIASED;
+  // The biased simplex, cone and knapsack run in the register kernel;
+  // columns whose search needs more of the sorted column are deferred to the
+  // workgroup-per-column kernel through the column list.
+  const bool reg_biased = op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
+                          op == SDCA_PROX_TOPK_CONE_BIASED || op == SDCA_PROX_KNAPSACK_LE_BIASED;
+  const bool topk_like =
+      topk || op == SDCA_PROX_TOPK_SIMPLEX_BIASED || op == SDCA_PROX_TOPK_CONE_BIASED;
   const bool listed = topk || reg_biased;
   const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED;
   if (!reg_ok && !(topk || knap || biased || ent_biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
@@ -254,10 +255,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     SDCA_HIP_TRY(launch_two_sort(a), "two_simplex_sort kernel (workgroup per column)");
   } else if (ent_biased) {
     SDCA_HIP_TRY(launch_ent_biased(a), "topk_entropy_biased kernel (wave per column)");
-  } else if (op == SDCA_PROX_TOPK_CONE_BIASED ||
-             ((topk || knap || reg_biased) && (!reg_ok || (topk_like && p.k > kTopkMaxK)))) {
-    // The biased cone's search needs the sorted column (topk_cone_biased.h),
-    // as do columns beyond the register kernel: one workgroup per column.
+  } else if ((topk || knap || reg_biased) && (!reg_ok || (topk_like && p.k > kTopkMaxK))) {
+    // Columns beyond the register kernel: one workgroup per sorted column.
     SDCA_HIP_TRY(launch_slow(a, true), "prox kernel (workgroup per column)");
   } else {
     // Deferred-column list: [count, done, column ids...].  The deferred-column
@@ -280,7 +279,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
       case SDCA_PROX_KNAPSACK_LE_BIASED: e = launch_knap(a); break;
       case SDCA_PROX_TOPK_SIMPLEX:
       case SDCA_PROX_TOPK_CONE:
-      case SDCA_PROX_TOPK_SIMPLEX_BIASED: e = launch_topk(a); break;
+      case SDCA_PROX_TOPK_SIMPLEX_BIASED:
+      case SDCA_PROX_TOPK_CONE_BIASED: e = launch_topk(a); break;
       case SDCA_PROX_ENTROPY:
       case SDCA_PROX_ENTROPY_NORM: e = launch_ent(a); break;
       case SDCA_PROX_TOPK_ENTROPY: e = launch_topkent(a); break;

@@ -20,7 +20,8 @@ hipError_t launch_one(const ProxLaunch& a) {
   pp.rhs = static_cast<R>(a.rhs);
   // rho enters the register kernel only through the biased simplex and
   // knapsack (the other operators take rho = 0).
-  pp.rho = (a.op == OP_TOPK_SIMPLEX_BIASED || a.op == OP_KNAPSACK_LE_BIASED)
+  pp.rho = (a.op == OP_TOPK_SIMPLEX_BIASED || a.op == OP_TOPK_CONE_BIASED ||
+            a.op == OP_KNAPSACK_LE_BIASED)
                ? static_cast<R>(a.rho) : R(0);
   pp.k = static_cast<int>(a.k);
   pp.op = a.op;

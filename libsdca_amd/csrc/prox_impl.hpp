@@ -328,6 +328,93 @@ __device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
   return slow_thr<R>();
 }
 
+// thresholds_topk_cone_biased_search (topk_cone_biased.h:9-80) on the sorted
+// top list: the reference's scan over U = the u largest and M = the next
+// ones, with its incremental sums in its order, so each trial t and hi are
+// the reference's values.
+//
+// For a given U the scan takes M = top[u, e) for growing e and accepts the
+// first e whose t satisfies the four conditions, among them t <= min(M) + eps.
+// Each step moves t to a weighted mean of t and the entry added,
+//   t' = (D t + nu a_e) / (D + nu),
+// so once t >= min(M) it stays there, and for any M reaching past the list,
+//   t' - min(M) >= D (t - top[L-1]) / (D + (m - L) nu)
+// with t and D taken at the end of the list.  When that bound clears eps
+// (plus rounding) no M beyond the list can be accepted, and the scan goes on
+// to the next U as the reference's would; otherwise the column is deferred.
+//
+// The scans for different U are independent: lane g of the group runs
+// u = g, g + G, ... (setting up sum_U, k - |U| and |U| + rho k^2 by the
+// reference's own sequence of updates), and the outcome is that of the
+// smallest u whose scan accepts or cannot be certified.
+template <int G, int L, class D, class R>
+__device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R rho) {
+  const R eps = R(16) * num<R>::eps();
+  const int g = static_cast<int>(threadIdx.x) % G;
+  int found_u = k + 1;
+  int found_kind = 0;  // 1: accepted, 2: deferred
+  R found_t = 0, found_hi = 0;
+#pragma unroll 1
+  for (int u = g; u <= k; u += G) {
+    R k_u = static_cast<R>(k);
+    R nu_rho = rho * static_cast<R>(k) * static_cast<R>(k);
+    R min_u = num<R>::inf();
+    R sum_u = 0;
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      if (i < u) {
+        min_u = static_cast<R>(top[i]);
+        sum_u += min_u;
+        k_u -= R(1);
+        nu_rho += R(1);
+      }
+    }
+    R min_m = num<R>::inf(), max_m = -num<R>::inf();
+    R sum_m = 0, num_m_sum_u = 0;
+    R den = k_u * k_u;
+    const R k_u_sum_u = k_u * sum_u;
+    int kind = 0;
+    R rt = 0, rhi = 0;
+#pragma unroll 1
+    for (int e = u;; ++e) {  // M = top[u, e)
+      const R t = (nu_rho * sum_m - k_u_sum_u) / den;
+      const R hi = (num_m_sum_u + k_u * sum_m) / den;
+      const R tt = hi + t;
+      const bool pass = max_m - eps <= tt && tt <= min_u + eps && t <= min_m + eps;
+      if (e == m) {
+        if (pass) { kind = 1; rt = t; rhi = hi; }
+        break;
+      }
+      if (e >= L) {
+        if (pass) { kind = 2; break; }  // the last test needs top[e]
+        const R last = static_cast<R>(top[L - 1]);
+        const R tol = R(2) * eps + R(8) * num<R>::eps() * dmax(fabs(t), fabs(last));
+        if (!(den * (t - last) > tol * (den + static_cast<R>(m - L) * nu_rho))) kind = 2;
+        break;
+      }
+      if (pass && static_cast<R>(top[e]) - eps <= t) { kind = 1; rt = t; rhi = hi; break; }
+      min_m = static_cast<R>(top[e]);
+      max_m = static_cast<R>(top[u]);
+      sum_m += min_m;
+      num_m_sum_u += sum_u;
+      den += nu_rho;
+    }
+    if (kind != 0) {
+      found_u = u;
+      found_kind = kind;
+      found_t = rt;
+      found_hi = rhi;
+      break;
+    }
+  }
+  const int u_min = group_min<G>(found_u);
+  if (u_min > k) return make_thr<R>(R(0), R(0), R(0));  // the reference's default
+  const int src = (static_cast<int>(threadIdx.x) & 63) - g + u_min % G;
+  const int kind = __shfl(found_kind, src, 64);
+  if (kind == 2) return slow_thr<R>();
+  return make_thr<R>(__shfl(found_t, src, 64), R(0), __shfl(found_hi, src, 64));
+}
+
 // Candidate slots per lane for the top-k simplex's knapsack: the group holds
 // up to G * kCandSlots<G> candidates in registers; columns with more run the
 // variable fixing over all register slots instead.
@@ -428,7 +515,7 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   const R largest = static_cast<R>(top[0]);
   // topk_cone_special_cases (topk_cone.h:18-55), whose divisor is k, or
   // k + rho k^2 for the biased simplex (topk_simplex_biased.h:50-51).
-  const bool biased = pp.op == OP_TOPK_SIMPLEX_BIASED;
+  const bool biased = pp.op == OP_TOPK_SIMPLEX_BIASED || pp.op == OP_TOPK_CONE_BIASED;
   if (sum_k <= eps16) return make_thr<R>(R(0), R(0), R(0));
   const R hi_c = sum_k / (biased ? K + pp.rho * K * K : K);
   const R t_c = kth - hi_c;
@@ -436,6 +523,10 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   if (pp.op == OP_TOPK_CONE) {
     if (constant) return make_thr<R>(t_c, R(0), hi_c);
     return cone_search_u0<G, C, D, R>(v, K, largest);
+  }
+  if (pp.op == OP_TOPK_CONE_BIASED) {  // thresholds_topk_cone_biased (topk_cone_biased.h:98-113)
+    if (constant) return make_thr<R>(t_c, R(0), hi_c);
+    return cone_biased_regs<G, L, D, R>(top, m, k, pp.rho);
   }
   // thresholds_topk_simplex (topk_simplex.h:39-68) and
   // thresholds_topk_simplex_biased (topk_simplex_biased.h:40-71)
