@@ -184,7 +184,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
                           op == SDCA_PROX_TOPK_CONE_BIASED || op == SDCA_PROX_KNAPSACK_LE_BIASED;
   const bool topk_like =
       topk || op == SDCA_PROX_TOPK_SIMPLEX_BIASED || op == SDCA_PROX_TOPK_CONE_BIASED;
-  const bool listed = topk || reg_biased;
+  const bool listed = topk || reg_biased || op == SDCA_PROX_TWO_SIMPLEX_SORT;
   const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED;
   if (!reg_ok && !(topk || knap || biased || ent_biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
       op != SDCA_PROX_TWO_SIMPLEX_SORT)
@@ -251,8 +251,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
 
   if (op == SDCA_PROX_LAMBERT_W_EXP) {
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
-  } else if (op == SDCA_PROX_TWO_SIMPLEX_SORT) {
-    SDCA_HIP_TRY(launch_two_sort(a), "two_simplex_sort kernel (workgroup per column)");
+  } else if (op == SDCA_PROX_TWO_SIMPLEX_SORT && !reg_ok) {
+    SDCA_HIP_TRY(launch_two_sort(a, true), "two_simplex_sort kernel (workgroup per column)");
   } else if (ent_biased) {
     SDCA_HIP_TRY(launch_ent_biased(a), "topk_entropy_biased kernel (wave per column)");
   } else if ((topk || knap || reg_biased) && (!reg_ok || (topk_like && p.k > kTopkMaxK))) {
@@ -284,11 +284,15 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
       case SDCA_PROX_ENTROPY:
       case SDCA_PROX_ENTROPY_NORM: e = launch_ent(a); break;
       case SDCA_PROX_TOPK_ENTROPY: e = launch_topkent(a); break;
-      case SDCA_PROX_TWO_SIMPLEX: e = launch_two(a); break;
+      case SDCA_PROX_TWO_SIMPLEX:
+      case SDCA_PROX_TWO_SIMPLEX_SORT: e = launch_two(a); break;
       default: break;
     }
     SDCA_HIP_TRY(e, "prox kernel");
-    if (listed) {
+    if (op == SDCA_PROX_TWO_SIMPLEX_SORT) {
+      SDCA_HIP_TRY(launch_two_sort(a, false), "two_simplex_sort kernel (deferred columns)");
+      wsr->list_zeroed = true;
+    } else if (listed) {
       SDCA_HIP_TRY(launch_slow(a, false), "prox kernel (deferred columns)");
       wsr->list_zeroed = true;
     }

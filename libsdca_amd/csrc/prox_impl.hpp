@@ -902,6 +902,7 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
   for (int c = 0; c < C; ++c) in_a[c] = (g + G * c) < p;
   R cuts[2];
   R res[2];
+  R maxs[2];
   int cnt[2];
   // Phase 1: each block on its own simplex <1, x> = rhs, by the reference's
   // iteration t = (sum(S) - rhs) / |S|, S <- {x in S : x > t} until S stays.
@@ -918,6 +919,7 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
       mx = (in_a[c] == (b == 0) && x > mx) ? x : mx;
     }
     mx = group_max<G>(mx);
+    maxs[b] = mx;
     R cut = mx - rhs;
     R sb = 0;
     int nb = 0;
@@ -960,6 +962,12 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
     r.t2 = s;
     return r;
   }
+  // two_simplex_sort (two_simplex_sort.h:15-111) solves the same problem by a
+  // scan over both sorted blocks and agrees with the above wherever the
+  // common sum is positive; where the optimum is x = y = 0 its scan ends at
+  // the sum rhs instead.  Such columns (and those within a margin of it)
+  // are deferred to the sort-and-scan kernel.
+  const bool sort_op = pp.op == OP_TWO_SIMPLEX_SORT;
   // Phase 2: joint variable fixing with s = -t.
   int mc = cnt[0] + cnt[1];
   {
@@ -1009,6 +1017,10 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
     } else {
       break;
     }
+  }
+  if (sort_op) {
+    const R margin = R(1e-3) * dmax(R(1), fabs(t));
+    if (maxs[0] - t <= margin || maxs[1] + t <= margin) return slow_thr<R>();
   }
   ColThr<R> r = make_thr<R>(t, R(0), rhs);
   r.t2 = -t;

@@ -52,7 +52,7 @@ hipError_t launch_topk(const ProxLaunch& a);
 hipError_t launch_ent(const ProxLaunch& a);
 hipError_t launch_ent_norm(const ProxLaunch& a);
 // Two-block simplex by sort and scan, one workgroup per column (prox_slow.hip).
-hipError_t launch_two_sort(const ProxLaunch& a);
+hipError_t launch_two_sort(const ProxLaunch& a, bool all_columns);
 // Biased top-k entropy, one wave per column (prox_entbias.hip).
 hipError_t launch_ent_biased(const ProxLaunch& a);
 hipError_t launch_topkent(const ProxLaunch& a);

@@ -423,13 +423,16 @@ template <class D, class R>
 __global__ void __launch_bounds__(256)
 two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, R rhs,
                 int64_t p_all, const int64_t* __restrict__ col_p,
-                sdca_thresholds* __restrict__ thr, int pow2) {
+                sdca_thresholds* __restrict__ thr, int* __restrict__ slow, int all_columns,
+                int pow2) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* sa = reinterpret_cast<D*>(smem_raw);
   D* sb = sa + pow2;
   __shared__ R sh_ta, sh_tb;
   const int m = static_cast<int>(m64);
-  for (int64_t j = blockIdx.x; j < n; j += gridDim.x) {
+  const int64_t count = all_columns ? n : static_cast<int64_t>(slow[0]);
+  for (int64_t w = blockIdx.x; w < count; w += gridDim.x) {
+    const int64_t j = all_columns ? w : static_cast<int64_t>(slow[2 + w]);
     const int p = static_cast<int>(col_p ? col_p[j] : p_all);
     const int q = m - p;
     const D* col = in + j * m64;
@@ -461,17 +464,29 @@ two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int6
       dst[i] = clamp_ref(col[i] - (i < p ? ta : tb), D(0), hi);
     __syncthreads();
   }
+  // List mode: the last of the workgroups that took a column zeroes the
+  // list's counters for the next call (as in prox_slow_kernel).
+  const int64_t workers = count < static_cast<int64_t>(gridDim.x) ? count : gridDim.x;
+  if (!all_columns && static_cast<int64_t>(blockIdx.x) < workers && threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(slow + 1, 1) == static_cast<int>(workers) - 1) {
+      atomicExch(slow, 0);
+      atomicExch(slow + 1, 0);
+    }
+  }
 }
 
 template <class D, class R>
-hipError_t launch_two_sort_t(const ProxLaunch& a) {
+hipError_t launch_two_sort_t(const ProxLaunch& a, bool all_columns) {
   int half = 1;
   while (half < a.m) half <<= 1;  // pow2 >= max(p, m - p) for every column
-  const int64_t grid = a.n < 4096 ? a.n : 4096;
+  const int64_t cap = all_columns ? 4096 : 512;
+  const int64_t grid = a.n < cap ? a.n : cap;
   hipLaunchKernelGGL((two_sort_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
                      dim3(256), 2 * static_cast<size_t>(half) * sizeof(D), a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n,
-                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, half);
+                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, a.slow, all_columns ? 1 : 0,
+                     half);
   return hipGetLastError();
 }
 
@@ -502,10 +517,10 @@ hipError_t launch_slow(const ProxLaunch& a, bool all_columns) {
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_two_sort(const ProxLaunch& a) {
-  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_two_sort_t<float, float>(a);
-  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_two_sort_t<float, double>(a);
-  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_two_sort_t<double, double>(a);
+hipError_t launch_two_sort(const ProxLaunch& a, bool all_columns) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_two_sort_t<float, float>(a, all_columns);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_two_sort_t<float, double>(a, all_columns);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_two_sort_t<double, double>(a, all_columns);
   return hipErrorInvalidValue;
 }
 

@@ -297,14 +297,18 @@ def test_biased(cuda, oracle, op, kw, m, dtype, result):
 @pytest.mark.parametrize("dtype,result", DTYPES)
 @pytest.mark.parametrize("m", [2, 10, 159, 200, 1000, 3000])
 def test_two_simplex_sort(cuda, oracle, m, dtype, result):
-    """The sort-and-scan two-block simplex (one workgroup per column), with a
-    per-column and a common split p."""
+    """The sort-and-scan two-block simplex (the register kernel, with the
+    columns whose optimum is zero deferred to the sort-and-scan kernel, and
+    that kernel alone for m > 2048), with a per-column and a common split p."""
     n = 120
     rng = np.random.default_rng(150 + m)
     col_p = rng.integers(1, min(m - 1, 5) + 1, n)
     for rhs in [1.0, 2.0]:
+        neg = -np.abs(inputs.normal(n, m, dtype, 153 + m)) - dtype(0.1)  # optimum x = y = 0
+        neg[::2] = inputs.normal(n // 2, m, dtype, 154 + m)  # interleaved with ordinary columns
         for name, x in [("normal", inputs.normal(n, m, dtype, 151 + m)),
-                        ("mixed", inputs.mixed_signs(n, m, dtype, 152 + m, -2, 2))]:
+                        ("mixed", inputs.mixed_signs(n, m, dtype, 152 + m, -2, 2)),
+                        ("zero-optimum", np.ascontiguousarray(neg))]:
             got, _ = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, col_p=col_p)
             parity(oracle, "two_simplex_sort", x, got, result,
                    f"two_simplex_sort rhs={rhs} {name} m={m}", rhs=rhs, col_p=col_p)
