@@ -22,6 +22,7 @@ OPS = {
     "entropy": 4, "entropy_norm": 5, "topk_entropy": 6, "two_simplex": 7,
     "lambert_w_exp": 8, "knapsack_le_biased": 9, "topk_simplex_biased": 10,
     "topk_cone_biased": 11, "topk_entropy_biased": 12, "two_simplex_sort": 13,
+    "two_entropy": 14,
 }
 OBJECTIVES = {
     "hinge_topk": 0, "hinge_topk_smooth": 1, "topk_hinge": 2,
@@ -128,7 +129,7 @@ class Library:
         params = params or make_params()
         thr = None
         if thresholds:
-            cnt = 2 * n if op in ("two_simplex", "two_simplex_sort") else n
+            cnt = 2 * n if op in ("two_simplex", "two_simplex_sort", "two_entropy") else n
             thr = np.zeros((cnt, 3), dtype=np.float64)
         cp = None
         if col_p is not None:

@@ -736,6 +736,122 @@ inline thr<R, It> topk_entropy_biased(It first, It last, std::ptrdiff_t k, R alp
 }
 
 // ---------------------------------------------------------------------------
+// Two-block entropic projection (two_entropy.h:9-231):
+//   x = W(exp(a - t)) / alpha,  y = W(exp(b - t - c)) / alpha,  c = alpha / |a|,
+// with t the root of sum_i W(e^(a_i - t)) + sum_j W(e^(b_j - t - c)) = alpha.
+// ---------------------------------------------------------------------------
+template <class R, class It>
+inline R two_w_step4(It af, It al, It bf, It bl, R alpha, R c, R& t) {  // :15-38
+  R f0(0), f1(0), f2(0), f3(0);
+  lw_sums(af, al, -t, f0, f1, f2, f3);
+  lw_sums(bf, bl, -t - c, f0, f1, f2, f3);
+  f0 -= alpha;
+  R f02 = f0 * f2, f11 = f1 * f1;
+  R den = 6 * f1 * (f02 - f11) - f0 * (f0 * f3);
+  if (std::abs(den) > 64 * std::numeric_limits<R>::min()) t -= 3 * f0 * (2 * f11 - f02) / den;
+  return f0;
+}
+
+template <class R, class It>
+inline R two_w_value(It af, It al, It bf, It bl, R alpha, R c, R t) {  // :45-58
+  R f0(0);
+  for (It a = af; a != al; ++a) f0 += lambert_w_exp(static_cast<R>(*a) + (-t));
+  for (It b = bf; b != bl; ++b) f0 += lambert_w_exp(static_cast<R>(*b) + (-t - c));
+  return f0 - alpha;
+}
+
+template <class R, class It>
+inline void two_w_bisection(It af, It al, It bf, It bl, R alpha, R c, R eps,
+                            std::size_t max_num_iter, R& t, R& lb, R& ub, R& lf, R& uf) {  // :65-96
+  for (std::size_t iter = 0; iter < max_num_iter; ++iter) {
+    t = (lb + ub) / 2;
+    R f1 = two_w_value(af, al, bf, bl, alpha, c, t);
+    if (eps < f1 && f1 < lf) {
+      lf = f1;
+      lb = t;
+    } else if (uf < f1 && f1 < -eps) {
+      uf = f1;
+      ub = t;
+    } else {
+      break;
+    }
+  }
+  t = (lb + ub) / 2;
+}
+
+template <class R, class It>
+inline std::pair<thr<R, It>, thr<R, It>> two_entropy(It af, It al, It bf, It bl, R alpha) {
+  typedef typename std::iterator_traits<It>::value_type D;
+  const std::size_t max_num_iter = 32;
+  const R eps = std::numeric_limits<R>::epsilon();
+  const R num_a = static_cast<R>(std::distance(af, al));
+  const R num_b = static_cast<R>(std::distance(bf, bl));
+  const R max_a = static_cast<R>(*std::max_element(af, al));
+  const R max_b = static_cast<R>(*std::max_element(bf, bl));
+  const R sum_a = std::accumulate(af, al, static_cast<R>(0));
+  const R sum_b = std::accumulate(bf, bl, static_cast<R>(0));
+  const R c = alpha / num_a;
+  const R max = std::max(max_a, max_b - c);
+  // Bracket guards (:159-163).
+  R lb = std::numeric_limits<R>::lowest();
+  R ub = max - 64 * exp_min_arg<R>::get();
+  R lf = std::numeric_limits<R>::max();
+  R uf = std::numeric_limits<R>::lowest();
+  // Two guesses, each followed by one step (:165-175).
+  R t01 = max - std::log(alpha);
+  R t1(t01);
+  R f1 = two_w_step4(af, al, bf, bl, alpha, c, t1);
+  R t02 = (sum_a + sum_b - num_b * c - alpha) / (num_a + num_b);
+  R t2(t02);
+  R f2 = two_w_step4(af, al, bf, bl, alpha, c, t2);
+  if (f1 > f2) {
+    std::swap(t01, t02);
+    std::swap(t1, t2);
+    std::swap(f1, f2);
+  }
+  R t;
+  if (f1 > 0) {
+    lb = t01;
+    lf = f1;
+    t = t1;
+  } else if (f2 < 0) {
+    ub = t02;
+    uf = f2;
+    t = t2;
+  } else {
+    lb = t02;
+    ub = t01;
+    lf = f2;
+    uf = f1;
+    t = std::max(lb, std::min(std::abs(f1) < std::abs(f2) ? t1 : t2, ub));
+    // The bisection count, converted to size_t as the reference converts it
+    // (this file is compiled by the same compiler as the reference shim).
+    const R log2_inv = static_cast<R>(1.4426950408889634);
+    std::size_t num_iter = std::min(max_num_iter,
+                                    static_cast<std::size_t>(std::log(ub - lb) * log2_inv));
+    two_w_bisection(af, al, bf, bl, alpha, c, eps, num_iter, t, lb, ub, lf, uf);
+  }
+  // Householder steps kept inside the bracket (:207-220).
+  for (std::size_t iter = 0; iter < max_num_iter; ++iter) {
+    t1 = t;
+    f1 = two_w_step4(af, al, bf, bl, alpha, c, t);
+    if (0 <= f1 && f1 < lf) {
+      lb = t1;
+      lf = f1;
+    } else if (uf < f1 && f1 <= 0) {
+      ub = t1;
+      uf = f1;
+    }
+    t = std::max(lb, std::min(t, ub));
+    if (std::abs(t1 - t) <= eps) break;
+  }
+  const R lo(0), hi(1);
+  const double map_a = static_cast<double>(1 / static_cast<D>(alpha));
+  return std::make_pair(make_thr(t, lo, hi, af, al, 3, map_a),
+                        make_thr(t + c, lo, hi, bf, bl, 3, map_a));
+}
+
+// ---------------------------------------------------------------------------
 // Two-block simplex, <1,x> = <1,y> <= rhs (two_simplex.h:18-119).
 template <class R, class It>
 inline std::pair<thr<R, It>, thr<R, It>>

@@ -60,11 +60,14 @@ int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
       std::copy(col, col + m, aux.begin());
       D* a = aux.data();
       D* a_end = a + m;
-      if (op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT) {
+      if (op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT ||
+          op == SDCA_PROX_TWO_ENTROPY) {
         std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])
                                   : static_cast<std::ptrdiff_t>(p->p);
         auto t = op == SDCA_PROX_TWO_SIMPLEX ? orc::two_simplex(a, a + pj, a + pj, a_end, rhs)
-                                             : orc::two_simplex_sort(a, a + pj, a + pj, a_end, rhs);
+               : op == SDCA_PROX_TWO_SIMPLEX_SORT
+                   ? orc::two_simplex_sort(a, a + pj, a + pj, a_end, rhs)
+                   : orc::two_entropy(a, a + pj, a + pj, a_end, static_cast<R>(p->alpha));
         // The two-block batch loop (proxdef.h:301-324): the thresholds'
         // iterators point into aux, the clamp runs over the column.
         orc::thr<R, D*> t1 = t.first, t2 = t.second;

@@ -86,6 +86,14 @@ void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_param
     case SDCA_PROX_TOPK_CONE_BIASED: sdca::prox_topk_cone_biased(m, first, last, aux, k, rho); break;
     case SDCA_PROX_TOPK_ENTROPY_BIASED:
       sdca::prox_topk_entropy_biased(m, first, last, aux, k, static_cast<R>(p->alpha)); break;
+    case SDCA_PROX_TWO_ENTROPY:
+      // The reference has the per-column form only (two_entropy.h:272-283).
+      for (int64_t j = 0; first + j * m < last; ++j)
+        sdca::prox_two_entropy(col_p ? static_cast<std::ptrdiff_t>(col_p[j])
+                                     : static_cast<std::ptrdiff_t>(p->p),
+                               first + j * m, first + (j + 1) * m, aux,
+                               static_cast<R>(p->alpha));
+      break;
     case SDCA_PROX_TWO_SIMPLEX_SORT:
       if (!col_p) {
         sdca::prox_two_simplex_sort(m, static_cast<std::ptrdiff_t>(p->p), first, last, aux, rhs);
@@ -152,6 +160,17 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
       case SDCA_PROX_TOPK_ENTROPY_BIASED: {
         auto t = sdca::thresholds_topk_entropy_biased(aux, al, k, static_cast<R>(p->alpha));
         sdca::prox(t, col, col + m); put(out, j, t); break;
+      }
+      case SDCA_PROX_TWO_ENTROPY: {
+        std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])
+                                  : static_cast<std::ptrdiff_t>(p->p);
+        auto t = sdca::thresholds_two_entropy(aux, aux + pj, aux + pj, al,
+                                              static_cast<R>(p->alpha));
+        sdca::prox(t.first, col, col + pj);
+        sdca::prox(t.second, col + pj, col + m);
+        put(out, 2 * j, t.first);
+        put(out, 2 * j + 1, t.second);
+        break;
       }
       case SDCA_PROX_TWO_SIMPLEX_SORT: {
         std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])

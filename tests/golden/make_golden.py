@@ -37,6 +37,7 @@ PROX_CASES = [
     ("topk_cone_biased", dict(k=5, rho=0.5), [10, 100]),
     ("topk_entropy_biased", dict(k=3, alpha=0.7), [10, 64]),
     ("two_simplex_sort", dict(p=2, rhs=1.0), [10, 33]),
+    ("two_entropy", dict(p=2, alpha=0.7), [10, 33]),
 ]
 DTYPES = [("f32f32", np.float32, 0), ("f32f64", np.float32, 1), ("f64f64", np.float64, 1)]
 MC = [("hinge_topk", 1.0, 1.0, 5), ("hinge_topk_smooth", 1.0, 1.0, 5), ("topk_hinge", 1.0, 1.0, 3),

@@ -25,7 +25,7 @@ PARAMS = {
     "knapsack_le_biased": dict(lo=0.0, hi=1.0, rhs=1.0, rho=0.5),
     "topk_simplex_biased": dict(k=5, rhs=1.0, rho=0.5), "topk_cone_biased": dict(k=5, rho=0.5),
     "topk_entropy_biased": dict(k=3, alpha=0.7),
-    "two_simplex_sort": dict(p=2, rhs=1.0),
+    "two_simplex_sort": dict(p=2, rhs=1.0), "two_entropy": dict(p=2, alpha=0.7),
 }
 MC = [("hinge_topk", 1.0, 1.0, 5), ("hinge_topk_smooth", 1.0, 1.0, 5), ("topk_hinge", 1.0, 1.0, 3),
       ("topk_hinge_smooth", 0.5, 0.7, 3), ("entropy", 1.0, 1.0, 1), ("entropy_topk", 2.0, 1.0, 3)]

@@ -532,3 +532,36 @@ def test_topk_entropy_biased_slsqp(oracle, k, alpha):
             n_capped += 1
             assert biased_entropy_objective(x, a, alpha) > sol.fun + 1e-6
     assert n_empty >= 9 and n_capped >= 7
+
+
+@pytest.mark.parametrize("p,alpha", [(1, 1.0), (3, 0.3), (2, 4.0)])
+def test_two_entropy_root_and_slsqp(oracle, p, alpha):
+    """two_entropy (two_entropy.h:109-231): the threshold t is the root of
+    sum_i W(e^(a_i - t)) + sum_j W(e^(b_j - t - c)) = alpha, c = alpha / p
+    (float64 bisection with scipy's W), the second record is t + c, and
+    (x, y) minimises 0.5 alpha |x - a/alpha - 1/p|^2 + <x, log x>
+    + 0.5 alpha |y - b/alpha|^2 + <y, log y> over <1,x> + <1,y> = 1, x, y >= 0
+    (SLSQP)."""
+    X = np.concatenate([inputs.normal(8, 7, np.float64, 93, 2.0),
+                        inputs.uniform(6, 7, np.float64, 94, -20, 5)])
+    P, thr = prox(oracle, "two_entropy", X, p=p, alpha=alpha)
+    c = alpha / p
+    for j, (v, z) in enumerate(zip(X, P)):
+        a, b = v[:p], v[p:]
+        g = lambda t: (sum(w_exp(q - t) for q in a) + sum(w_exp(q - t - c) for q in b)) - alpha
+        t = bisect(g, -80.0, 80.0)
+        assert abs(thr[2 * j, 0] - t) <= 1e-10 * max(1, abs(t))
+        assert thr[2 * j + 1, 0] == pytest.approx(thr[2 * j, 0] + c, rel=1e-15, abs=1e-15)
+        assert z.sum() == pytest.approx(1.0, abs=1e-12)
+
+        def f(w):
+            wl = np.where(w > 0, w * np.log(np.maximum(w, 1e-300)), 0.0)
+            return (0.5 * alpha * np.sum((w[:p] - a / alpha - 1 / p) ** 2)
+                    + 0.5 * alpha * np.sum((w[p:] - b / alpha) ** 2) + wl.sum())
+        if j < 4:
+            sol = scipy.optimize.minimize(f, np.full(len(v), 1.0 / len(v)), method="SLSQP",
+                                          bounds=[(0, 1)] * len(v),
+                                          constraints=[{"type": "eq", "fun": lambda w: w.sum() - 1}],
+                                          options={"ftol": 1e-15, "maxiter": 1000})
+            assert f(z) <= sol.fun + 1e-9
+            assert np.allclose(z, sol.x, atol=1e-5)

@@ -46,6 +46,9 @@ OPS = [
     ("topk_entropy_biased", dict(k=5, alpha=2.0)),
     ("two_simplex_sort", dict(p=1)),
     ("two_simplex_sort", dict(p=3, rhs=2.0)),
+    ("two_entropy", dict(p=1, alpha=1.0)),
+    ("two_entropy", dict(p=3, alpha=0.3)),
+    ("two_entropy", dict(p=2, alpha=4.0)),
 ]
 DTYPES = [(np.float32, 0), (np.float32, 1), (np.float64, 1), (np.float64, 0)]
 
@@ -70,7 +73,7 @@ def columns(m, dtype, seed):
 @pytest.mark.parametrize("m", [1, 2, 5, 10, 31, 100])
 @pytest.mark.parametrize("op,kw", OPS)
 def test_prox_bit_exact(oracle, reference, op, kw, m, dtype, result):
-    if op in ("two_simplex", "two_simplex_sort") and (m < 2 or kw["p"] >= m):
+    if op in ("two_simplex", "two_simplex_sort", "two_entropy") and (m < 2 or kw["p"] >= m):
         pytest.skip("p must be in [1, m-1]")
     if op in ("topk_simplex", "topk_cone", "topk_entropy", "topk_simplex_biased",
               "topk_cone_biased", "topk_entropy_biased") and kw["k"] > m:
@@ -90,7 +93,7 @@ def test_prox_bit_exact(oracle, reference, op, kw, m, dtype, result):
         assert np.array_equal(ta, tb, equal_nan=True), f"{op}: thresholds differ"
 
 
-@pytest.mark.parametrize("op", ["two_simplex", "two_simplex_sort"])
+@pytest.mark.parametrize("op", ["two_simplex", "two_simplex_sort", "two_entropy"])
 def test_prox_per_column_split_bit_exact(oracle, reference, op):
     rng = np.random.default_rng(3)
     x = inputs.normal(500, 40, np.float32, 4)
