@@ -81,6 +81,10 @@ CONFIGS = {
                    gen="normal", seed=4105, col_p=True,
                    desc="batched two-block simplex prox by sort and scan, m=200, n=500,000, "
                         "fp32, N(0,1), per-column p in [1,5]"),
+    "c5ent": dict(op="two_entropy", m=200, n=500_000, dtype="f32", result="f32", alpha=1.0,
+                  gen="normal", seed=4105, col_p=True,
+                  desc="batched two-block entropic prox (alpha=1), m=200, n=500,000, fp32, "
+                       "N(0,1), per-column p in [1,5]"),
     "c3ebias": dict(op="topk_entropy_biased", m=1000, n=200_000, dtype="f64", result="f64", k=5,
                     alpha=1.0, gen="uniform10", seed=103,
                     desc="batched biased top-k entropy prox (k=5, alpha=1), m=1000, n=200,000, "

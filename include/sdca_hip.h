@@ -63,7 +63,9 @@ typedef enum sdca_prox_op {
   SDCA_PROX_TOPK_SIMPLEX_BIASED = 10, /* topk_simplex_biased.h:105-119 (uses rho) */
   SDCA_PROX_TOPK_CONE_BIASED = 11,    /* topk_cone_biased.h:145-158 (uses rho) */
   SDCA_PROX_TOPK_ENTROPY_BIASED = 12, /* topk_entropy_biased.h:302-315 (uses k, alpha) */
-  SDCA_PROX_TWO_SIMPLEX_SORT = 13     /* two_simplex_sort.h:175-190 (uses p / col_p) */
+  SDCA_PROX_TWO_SIMPLEX_SORT = 13,    /* two_simplex_sort.h:175-190 (uses p / col_p) */
+  SDCA_PROX_TWO_ENTROPY = 14          /* prox_two_entropy(p, first, last, aux, alpha),
+                                         two_entropy.h:272-283, batched (uses p / col_p, alpha) */
 } sdca_prox_op;
 
 /* Operator parameters; defaults as in mex_prox.cpp:121-127. */

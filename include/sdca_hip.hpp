@@ -208,6 +208,18 @@ inline void prox_two_simplex_sort(std::ptrdiff_t dim, std::ptrdiff_t p_split, Da
   detail::run<Result>(SDCA_PROX_TWO_SIMPLEX_SORT, dim, first, last, p);
 }
 
+// prox_two_entropy(p, first, last, aux, alpha) (two_entropy.h:272-283) over
+// the dim-sized columns of [first, last); the reference has the per-column
+// form only, this is its batch in the argument order of prox_two_simplex.
+template <typename Result = double, typename Data>
+inline void prox_two_entropy(std::ptrdiff_t dim, std::ptrdiff_t p_split, Data* first, Data* last,
+                             Data* /*aux*/, const Result alpha = 1) {
+  sdca_prox_params p = detail::params();
+  p.p = p_split;
+  p.alpha = static_cast<double>(alpha);
+  detail::run<Result>(SDCA_PROX_TWO_ENTROPY, dim, first, last, p);
+}
+
 // apply(dim, first, last, lambert_w_exp_map<Data>()) (proxdef.h:386-400)
 template <typename Data>
 inline void apply_lambert_w_exp(std::ptrdiff_t dim, Data* first, Data* last) {

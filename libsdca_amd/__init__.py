@@ -13,6 +13,12 @@ operator table (src/matlab/mex_prox.cpp:145-172):
     prox_entropy_norm(dim, A, hi=1, rhs=1)
     prox_topk_entropy(dim, A, k=1)
     prox_two_simplex(dim, p, A, rhs=1)
+    prox_knapsack_le_biased(dim, A, lo=0, hi=1, rhs=1, rho=1)
+    prox_topk_simplex_biased(dim, A, k=1, rhs=1, rho=1)
+    prox_topk_cone_biased(dim, A, k=1, rho=1)
+    prox_topk_entropy_biased(dim, A, k=1, alpha=1)
+    prox_two_simplex_sort(dim, p, A, rhs=1)
+    prox_two_entropy(dim, p, A, alpha=1)
     lambert_w_exp(A)
 
 `A` holds n columns of length dim, contiguous (a C-contiguous (n, dim) array
@@ -30,7 +36,9 @@ import numpy as np
 __all__ = [
     "SdcaError", "library", "prox", "prox_knapsack_eq", "prox_knapsack_le",
     "prox_topk_simplex", "prox_topk_cone", "prox_entropy", "prox_entropy_norm",
-    "prox_topk_entropy", "prox_two_simplex", "lambert_w_exp", "OPS", "F32", "F64",
+    "prox_topk_entropy", "prox_two_simplex", "prox_knapsack_le_biased",
+    "prox_topk_simplex_biased", "prox_topk_cone_biased", "prox_topk_entropy_biased",
+    "prox_two_simplex_sort", "prox_two_entropy", "lambert_w_exp", "OPS", "F32", "F64",
     "OBJECTIVES", "objective", "scores", "eval_features", "eval_scores",
 ]
 
@@ -45,7 +53,7 @@ OPS = {
     "topk_cone": 3, "entropy": 4, "entropy_norm": 5, "topk_entropy": 6,
     "two_simplex": 7, "lambert_w_exp": 8, "knapsack_le_biased": 9,
     "topk_simplex_biased": 10, "topk_cone_biased": 11,
-    "topk_entropy_biased": 12, "two_simplex_sort": 13,
+    "topk_entropy_biased": 12, "two_simplex_sort": 13, "two_entropy": 14,
 }
 STATUS = {
     0: "OK", 1: "ARG_NULL", 2: "ARG_RANGE", 3: "PRECISION", 4: "NOT_IMPLEMENTED",
@@ -155,7 +163,7 @@ def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
          alpha=1.0, k=1, p=1, col_p=None, thresholds=False):
     """Batched prox over the rows of A (each row is one column of the
     reference's dim x n matrix).  Returns out (A itself when out is None) and,
-    with thresholds=True, an (n, 3) (or (2n, 3) for two_simplex) array of
+    with thresholds=True, an (n, 3) (or (2n, 3) for the two-block operators) array of
     (t, lo, hi) per column/block."""
     lib = library()
     code = OPS[op] if isinstance(op, str) else int(op)
@@ -170,7 +178,8 @@ def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
     if out is None:
         out = A
     params = ProxParams(lo, hi, rhs, rho, alpha, int(k), int(p))
-    nthr = 2 * n if code in (OPS["two_simplex"], OPS["two_simplex_sort"]) else n
+    nthr = 2 * n if code in (OPS["two_simplex"], OPS["two_simplex_sort"],
+                             OPS["two_entropy"]) else n
     if _is_torch(A):
         import torch
         if not A.is_cuda or not A.is_contiguous() or not out.is_contiguous():
@@ -250,6 +259,12 @@ def prox_topk_cone_biased(dim, A, k=1, rho=1.0, result=None):
 
 def prox_topk_entropy_biased(dim, A, k=1, alpha=1.0, result="double"):
     return prox("topk_entropy_biased", _rows(dim, A), k=k, alpha=alpha, result=result)
+
+
+def prox_two_entropy(dim, p, A, alpha=1.0, result=None):
+    """Batched form of prox_two_entropy(p, first, last, aux, alpha)
+    (two_entropy.h:272-283), which the reference has per column only."""
+    return prox("two_entropy", _rows(dim, A), p=p, alpha=alpha, result=result)
 
 
 def prox_two_simplex_sort(dim, p, A, rhs=1.0, result=None):

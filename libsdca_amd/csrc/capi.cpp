@@ -137,7 +137,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   sdca_prox_params p;
   if (params) p = *params;
   else sdca_prox_params_default(&p);
-  if (static_cast<int>(op) < 0 || op > SDCA_PROX_TWO_SIMPLEX_SORT)
+  if (static_cast<int>(op) < 0 || op > SDCA_PROX_TWO_ENTROPY)
     return fail(SDCA_ERR_PROX, "unknown prox operator %d", static_cast<int>(op));
   const bool biased = op == SDCA_PROX_KNAPSACK_LE_BIASED || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
                       op == SDCA_PROX_TOPK_CONE_BIASED;
@@ -156,12 +156,14 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
                       op == SDCA_PROX_TOPK_CONE_BIASED || op == SDCA_PROX_TOPK_ENTROPY_BIASED;
   if (uses_k && (p.k < 1 || p.k > m))
     return fail(SDCA_ERR_ARG_RANGE, "k must be in [1, %lld] (got %lld)", (long long)m, (long long)p.k);
-  const bool two = op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT;
+  const bool two = op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT ||
+                   op == SDCA_PROX_TWO_ENTROPY;
   if (two) {
     if (m < 2) return fail(SDCA_ERR_ARG_RANGE, "two_simplex needs m >= 2");
     if (!col_p && (p.p < 1 || p.p > m - 1))
       return fail(SDCA_ERR_ARG_RANGE, "p must be in [1, %lld] (got %lld)", (long long)(m - 1), (long long)p.p);
-    if (!(p.rhs > 0)) return fail(SDCA_ERR_ARG_RANGE, "two_simplex needs rhs > 0 (got %g)", p.rhs);
+    if (op != SDCA_PROX_TWO_ENTROPY && !(p.rhs > 0))
+      return fail(SDCA_ERR_ARG_RANGE, "two_simplex needs rhs > 0 (got %g)", p.rhs);
     if (col_p && (flags & SDCA_HOST_PTR)) {
       for (int64_t j = 0; j < n; ++j)
         if (col_p[j] < 1 || col_p[j] > m - 1)
@@ -185,7 +187,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   const bool topk_like =
       topk || op == SDCA_PROX_TOPK_SIMPLEX_BIASED || op == SDCA_PROX_TOPK_CONE_BIASED;
   const bool listed = topk || reg_biased || op == SDCA_PROX_TWO_SIMPLEX_SORT;
-  const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED;
+  // The Lambert-map operators solved one wave per column (prox_entbias.hip).
+  const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED || op == SDCA_PROX_TWO_ENTROPY;
   if (!reg_ok && !(topk || knap || biased || ent_biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
       op != SDCA_PROX_TWO_SIMPLEX_SORT)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "operator %d supports m <= %lld on the GPU (got %lld)",
@@ -253,6 +256,8 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
   } else if (op == SDCA_PROX_TWO_SIMPLEX_SORT && !reg_ok) {
     SDCA_HIP_TRY(launch_two_sort(a, true), "two_simplex_sort kernel (workgroup per column)");
+  } else if (op == SDCA_PROX_TWO_ENTROPY) {
+    SDCA_HIP_TRY(launch_two_ent(a), "two_entropy kernel (wave per column)");
   } else if (ent_biased) {
     SDCA_HIP_TRY(launch_ent_biased(a), "topk_entropy_biased kernel (wave per column)");
   } else if ((topk || knap || reg_biased) && (!reg_ok || (topk_like && p.k > kTopkMaxK))) {

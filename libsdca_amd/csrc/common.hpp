@@ -16,6 +16,7 @@ template <> struct num<float> {
   __device__ __host__ static constexpr float inf() { return __builtin_huge_valf(); }
   __device__ __host__ static constexpr float quiet_nan() { return __builtin_nanf(""); }
   __device__ __host__ static constexpr float min_normal() { return 1.17549435082228750797e-38f; }
+  __device__ __host__ static constexpr float max_finite() { return 3.40282346638528859812e+38f; }
   // exp_traits<float>::min_arg (math/log_exp.h:46-52)
   __device__ __host__ static constexpr float exp_min_arg() { return -8.733654022216796875000000e+01f; }
 };
@@ -24,6 +25,7 @@ template <> struct num<double> {
   __device__ __host__ static constexpr double inf() { return __builtin_huge_val(); }
   __device__ __host__ static constexpr double quiet_nan() { return __builtin_nan(""); }
   __device__ __host__ static constexpr double min_normal() { return 2.2250738585072013831e-308; }
+  __device__ __host__ static constexpr double max_finite() { return 1.7976931348623157081e+308; }
   // exp_traits<double>::min_arg = log(DBL_MIN) (math/log_exp.h:27-34)
   __device__ __host__ static constexpr double exp_min_arg() { return -0x1.6232bdd7abcd2p+9; }
 };

@@ -1,19 +1,24 @@
-// Biased top-k entropy prox (topk_entropy_biased.h:179-268), one wave per
-// column:
-//   x = clamp(W(exp(a - t)) / alpha, 0, s / k)
-// with (s, t) from the reference's two solves - the order-4 Householder
-// iteration on W(e^(alpha - t)) + sum_i W(e^(a_i - t)) = alpha while no entry
-// is capped (:9-61), then, while the feasibility test fails, the set U of
-// capped entries grows by the largest remaining entry and (s, t) come from
-// the Newton iteration on the two-equation system of :120-176.
+// Lambert-map operators solved one wave per column, with the column in LDS:
 //
-// Each pass of either iteration is a sum of W(e^(a_i - t)) and its
-// derivatives over the column: the column sits in LDS, each lane sums a
-// stride-64 share, and a butterfly reduction gives every lane the totals, so
-// the scalar updates run uniformly on all 64 lanes and no barrier beyond the
-// wave is needed.  Entries moved into U are overwritten with -inf in LDS,
-// where W(e^-inf) = 0 drops them from every later sum; the final clamp reads
-// the column again from global memory.
+// * Biased top-k entropy (topk_entropy_biased.h:179-268):
+//     x = clamp(W(exp(a - t)) / alpha, 0, s / k)
+//   with (s, t) from the reference's two solves - the order-4 Householder
+//   iteration on W(e^(alpha - t)) + sum_i W(e^(a_i - t)) = alpha while no
+//   entry is capped (:9-61), then, while the feasibility test fails, the set
+//   U of capped entries grows by the largest remaining entry and (s, t) come
+//   from the Newton iteration on the two-equation system of :120-176.
+// * Two-block entropy (two_entropy.h:109-231):
+//     x = W(exp(a - t)) / alpha,  y = W(exp(b - t - alpha / p)) / alpha,
+//   with t from the reference's two guesses, bisection and bracketed
+//   Householder steps on sum W(e^(a - t)) + sum W(e^(b - t - c)) = alpha.
+//
+// Each pass of these iterations is a sum of W(e^(x_i + shift)) and its
+// derivatives over the column: each lane sums a stride-64 share, and a
+// butterfly reduction gives every lane the totals, so the scalar updates run
+// uniformly on all 64 lanes and no barrier beyond the wave is needed.
+// Entries moved into U are overwritten with -inf in LDS, where W(e^-inf) = 0
+// drops them from every later sum; the final clamp reads the column again
+// from global memory.
 #include "common.hpp"
 #include "prox_impl.hpp"
 #include "prox_launch.hpp"
@@ -23,6 +28,15 @@ namespace sdca_gpu {
 namespace {
 
 constexpr int kEbMaxWaves = 4;
+
+// f0 = sum_i W(e^(s_i + t_i)) with t_i = ta for i < p and tb beyond
+// (sum_lambert_w_exp, lambert.h:220-237).
+template <class D, class R>
+__device__ inline R lw_sum0(const D* s, int m, int p, int lane, R ta, R tb) {
+  R a0(0);
+  for (int i = lane; i < m; i += 64) a0 += lambert_w_exp(static_cast<R>(s[i]) + (i < p ? ta : tb));
+  return group_sum<64>(a0);
+}
 
 // f0 = sum_i W(e^(s_i + t)), f1 = sum_i W / (1 + W) (lambert.h:253-271).
 template <class D, class R>
@@ -37,12 +51,18 @@ __device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1) 
   f1 = group_sum<64>(a1);
 }
 
-// f0..f3: W and its first three derivatives in t (lambert.h:308-332).
+// f0..f3: W and its first three derivatives in t (lambert.h:308-332), with
+// the shift ta for entries below p and tb beyond.
 template <class D, class R>
-__device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, R& f2, R& f3) {
+__device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, R& f2, R& f3,
+                                int p = -1, R tb = R(0)) {
+  if (p < 0) {
+    p = m;
+    tb = t;
+  }
   R a0(0), a1(0), a2(0), a3(0);
   for (int i = lane; i < m; i += 64) {
-    const R v = lambert_w_exp(static_cast<R>(s[i]) + t);
+    const R v = lambert_w_exp(static_cast<R>(s[i]) + (i < p ? t : tb));
     const R d = R(1) + v;
     const R d3 = d * d * d;
     a0 += v;
@@ -242,6 +262,173 @@ entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64
   }
 }
 
+// One order-4 Householder step on the two-block sum (two_entropy.h:15-38);
+// returns f(t) at the old t.
+template <class D, class R>
+__device__ inline R two_w_step4(const D* s, int m, int p, int lane, R alpha, R c, R& t) {
+  R f0, f1, f2, f3;
+  lw_sums4(s, m, lane, -t, f0, f1, f2, f3, p, -t - c);
+  f0 -= alpha;
+  const R f02 = f0 * f2, f11 = f1 * f1;
+  const R den = R(6) * f1 * (f02 - f11) - f0 * (f0 * f3);
+  if (fabs(den) > R(64) * num<R>::min_normal()) t -= R(3) * f0 * (R(2) * f11 - f02) / den;
+  return f0;
+}
+
+// The reference's bisection count, static_cast<std::size_t>(log(ub - lb) /
+// log 2) capped at 32, with the conversion as the reference's x86-64 build
+// performs it: truncation toward zero, and a value at or below -1 (or NaN)
+// wrapping to a huge count, hence 32.
+template <class R>
+__device__ inline int bisection_count(R v) {
+  if (!(v > R(-1))) return 32;
+  if (v >= R(32)) return 32;
+  return (v > R(0)) ? static_cast<int>(v) : 0;
+}
+
+// Thresholds t (block a) and t + c (block b) of one column in s[0, m), split p.
+template <class D, class R>
+__device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R& t_out,
+                                  R& c_out) {
+  const R eps = num<R>::eps();
+  const R num_a = static_cast<R>(p), num_b = static_cast<R>(m - p);
+  R max_a = -num<R>::inf(), max_b = -num<R>::inf(), sum_a = 0, sum_b = 0;
+  for (int i = lane; i < m; i += 64) {
+    const R x = static_cast<R>(s[i]);
+    if (i < p) {
+      max_a = (x > max_a) ? x : max_a;
+      sum_a += x;
+    } else {
+      max_b = (x > max_b) ? x : max_b;
+      sum_b += x;
+    }
+  }
+  max_a = group_max<64>(max_a);
+  max_b = group_max<64>(max_b);
+  sum_a = group_sum<64>(sum_a);
+  sum_b = group_sum<64>(sum_b);
+  const R c = alpha / num_a;
+  const R max = (max_a > max_b - c) ? max_a : max_b - c;
+  // Bracket guards (two_entropy.h:159-163).
+  R lb = -num<R>::max_finite();
+  R ub = max - R(64) * num<R>::exp_min_arg();
+  R lf = num<R>::max_finite();
+  R uf = -num<R>::max_finite();
+  // Two guesses, each followed by one step (:165-175).
+  R t01 = max - dlog(alpha);
+  R t1 = t01;
+  R f1 = two_w_step4(s, m, p, lane, alpha, c, t1);
+  R t02 = (sum_a + sum_b - num_b * c - alpha) / (num_a + num_b);
+  R t2 = t02;
+  R f2 = two_w_step4(s, m, p, lane, alpha, c, t2);
+  if (f1 > f2) {
+    R x = t01; t01 = t02; t02 = x;
+    x = t1; t1 = t2; t2 = x;
+    x = f1; f1 = f2; f2 = x;
+  }
+  R t;
+  if (f1 > R(0)) {
+    lb = t01;
+    lf = f1;
+    t = t1;
+  } else if (f2 < R(0)) {
+    ub = t02;
+    uf = f2;
+    t = t2;
+  } else {
+    lb = t02;
+    ub = t01;
+    lf = f2;
+    uf = f1;
+    const R g = (fabs(f1) < fabs(f2)) ? t1 : t2;
+    t = (lb > ((g < ub) ? g : ub)) ? lb : ((g < ub) ? g : ub);
+    // Bisection (:75-96, 193-203).
+    const int num_iter = bisection_count(dlog(ub - lb) * static_cast<R>(1.4426950408889634));
+    for (int iter = 0; iter < num_iter; ++iter) {
+      t = (lb + ub) / R(2);
+      const R fv = lw_sum0(s, m, p, lane, -t, -t - c) - alpha;
+      if (eps < fv && fv < lf) {
+        lf = fv;
+        lb = t;
+      } else if (uf < fv && fv < -eps) {
+        uf = fv;
+        ub = t;
+      } else {
+        break;
+      }
+    }
+    t = (lb + ub) / R(2);
+  }
+  // Householder steps kept inside the bracket (:207-220).
+  for (int iter = 0; iter < 32; ++iter) {
+    t1 = t;
+    f1 = two_w_step4(s, m, p, lane, alpha, c, t);
+    if (R(0) <= f1 && f1 < lf) {
+      lb = t1;
+      lf = f1;
+    } else if (uf < f1 && f1 <= R(0)) {
+      ub = t1;
+      uf = f1;
+    }
+    t = (lb > ((t < ub) ? t : ub)) ? lb : ((t < ub) ? t : ub);
+    if (fabs(t1 - t) <= eps) break;
+  }
+  t_out = t;
+  c_out = c;
+}
+
+template <class D, class R>
+__global__ void __launch_bounds__(64 * kEbMaxWaves)
+twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
+              int64_t p_all, const int64_t* __restrict__ col_p, R alpha,
+              sdca_thresholds* __restrict__ thr, int stride_elems) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int waves = blockDim.x >> 6;
+  D* s = reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
+  const int m = static_cast<int>(m64);
+  const D map_a = D(1) / static_cast<D>(alpha);  // a_lambert_w_exp_map (functor.h:33-38)
+  for (int64_t j = static_cast<int64_t>(blockIdx.x) * waves + wave; j < n;
+       j += static_cast<int64_t>(gridDim.x) * waves) {
+    const int p = static_cast<int>(col_p ? col_p[j] : p_all);
+    const D* col = in + j * m64;
+    for (int i = lane; i < m; i += 64) s[i] = col[i];
+    wave_lds_sync();
+    R t, c;
+    twoent_thresholds<D, R>(s, m, p, lane, alpha, t, c);
+    const R tb = t + c;
+    if (thr && lane == 0) {
+      thr[2 * j].t = static_cast<double>(t);
+      thr[2 * j].lo = 0;
+      thr[2 * j].hi = 1;
+      thr[2 * j + 1].t = static_cast<double>(tb);
+      thr[2 * j + 1].lo = 0;
+      thr[2 * j + 1].hi = 1;
+    }
+    const D ta_d = static_cast<D>(t), tb_d = static_cast<D>(tb);
+    D* dst = out + j * m64;
+    for (int i = lane; i < m; i += 64)
+      dst[i] = clamp_ref(map_a * lambert_w_exp(col[i] - (i < p ? ta_d : tb_d)), D(0), D(1));
+    wave_lds_sync();
+  }
+}
+
+template <class D, class R>
+hipError_t launch_twoent_t(const ProxLaunch& a) {
+  const int stride = static_cast<int>((a.m + 3) & ~int64_t(3));
+  const size_t per_wave = static_cast<size_t>(stride) * sizeof(D);
+  int waves = kEbMaxWaves;
+  while (waves > 1 && waves * per_wave > 65536) waves >>= 1;
+  int64_t grid = (a.n + waves - 1) / waves;
+  if (grid > 16384) grid = 16384;
+  if (grid < 1) grid = 1;
+  hipLaunchKernelGGL((twoent_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
+                     waves * per_wave, a.stream, static_cast<const D*>(a.in),
+                     static_cast<D*>(a.out), a.m, a.n, a.p, a.col_p, static_cast<R>(a.alpha),
+                     a.thr, stride);
+  return hipGetLastError();
+}
+
 template <class D, class R>
 hipError_t launch_t(const ProxLaunch& a) {
   const int stride = static_cast<int>((a.m + 3) & ~int64_t(3));  // 16-byte aligned slices
@@ -259,6 +446,13 @@ hipError_t launch_t(const ProxLaunch& a) {
 }
 
 }  // namespace
+
+hipError_t launch_two_ent(const ProxLaunch& a) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_twoent_t<float, float>(a);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_twoent_t<float, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_twoent_t<double, double>(a);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_ent_biased(const ProxLaunch& a) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_t<float, float>(a);

@@ -55,6 +55,8 @@ hipError_t launch_ent_norm(const ProxLaunch& a);
 hipError_t launch_two_sort(const ProxLaunch& a, bool all_columns);
 // Biased top-k entropy, one wave per column (prox_entbias.hip).
 hipError_t launch_ent_biased(const ProxLaunch& a);
+// Two-block entropy, one wave per column (prox_entbias.hip).
+hipError_t launch_two_ent(const ProxLaunch& a);
 hipError_t launch_topkent(const ProxLaunch& a);
 hipError_t launch_two(const ProxLaunch& a);
 // Workgroup-per-column kernel over the flagged list (all_columns: every column).

@@ -121,6 +121,7 @@ int main() {
   sdca::hip::prox_topk_simplex_biased(100, f, f + a.size(), aux.data(), 5, 1.0f, 0.5f);
   sdca::hip::prox_topk_cone_biased(100, f, f + a.size(), aux.data(), 5, 0.5f);
   sdca::hip::prox_topk_entropy_biased(100, f, f + a.size(), aux.data(), 5, 0.5f);
+  sdca::hip::prox_two_entropy(100, 3, f, f + a.size(), aux.data(), 0.5f);
   std::vector<sdca_objective> objs(1);
   objs[0].kind = SDCA_OBJ_ENTROPY; objs[0].c = 1; objs[0].gamma = 1; objs[0].k = 1;
   std::vector<int64_t> y(4, 0);

@@ -381,3 +381,24 @@ def test_topk_entropy_biased_largest_m(cuda, oracle, dtype, result, m):
     got, _ = run_gpu("topk_entropy_biased", x, result, cuda, k=4, alpha=1.5)
     parity(oracle, "topk_entropy_biased", x, got, result, f"topk_entropy_biased m={m}",
            nthreads=8, k=4, alpha=1.5)
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [2, 5, 17, 100, 200, 1000])
+@pytest.mark.parametrize("alpha", [1.0, 0.3, 4.0])
+def test_two_entropy(cuda, oracle, alpha, m, dtype, result):
+    """The two-block entropic projection of the multilabel entropy dual, one
+    wave per column, with a per-column and a common split p."""
+    n = 150
+    rng = np.random.default_rng(190 + m)
+    col_p = rng.integers(1, min(m - 1, 5) + 1, n)
+    for name, x in [("normal", inputs.normal(n, m, dtype, 191 + m)),
+                    ("mixed", inputs.mixed_signs(n, m, dtype, 192 + m, -2, 2)),
+                    ("uniform", inputs.uniform(n, m, dtype, 193 + m, -10, 10))]:
+        got, thr = run_gpu("two_entropy", x, result, cuda, alpha=alpha, col_p=col_p)
+        parity(oracle, "two_entropy", x, got, result, f"two_entropy alpha={alpha} {name} m={m}",
+               nthreads=8, alpha=alpha, col_p=col_p)
+        p = max(1, m // 3)
+        got, _ = run_gpu("two_entropy", x, result, cuda, alpha=alpha, p=p)
+        parity(oracle, "two_entropy", x, got, result,
+               f"two_entropy p={p} alpha={alpha} {name} m={m}", nthreads=8, alpha=alpha, p=p)
