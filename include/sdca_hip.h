@@ -65,7 +65,7 @@ typedef enum sdca_prox_op {
   SDCA_PROX_TOPK_ENTROPY_BIASED = 12, /* topk_entropy_biased.h:302-315 (uses k, alpha) */
   SDCA_PROX_TWO_SIMPLEX_SORT = 13,    /* two_simplex_sort.h:175-190 (uses p / col_p) */
   SDCA_PROX_TWO_ENTROPY = 14          /* prox_two_entropy(p, first, last, aux, alpha),
-                                         two_entropy.h:272-283, batched (uses p / col_p, alpha) */
+                                         two_entropy.h:280-292, batched (uses p / col_p, alpha) */
 } sdca_prox_op;
 
 /* Operator parameters; defaults as in mex_prox.cpp:121-127. */

@@ -208,7 +208,7 @@ inline void prox_two_simplex_sort(std::ptrdiff_t dim, std::ptrdiff_t p_split, Da
   detail::run<Result>(SDCA_PROX_TWO_SIMPLEX_SORT, dim, first, last, p);
 }
 
-// prox_two_entropy(p, first, last, aux, alpha) (two_entropy.h:272-283) over
+// prox_two_entropy(p, first, last, aux, alpha) (two_entropy.h:280-292) over
 // the dim-sized columns of [first, last); the reference has the per-column
 // form only, this is its batch in the argument order of prox_two_simplex.
 template <typename Result = double, typename Data>

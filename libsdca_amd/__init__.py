@@ -263,7 +263,7 @@ def prox_topk_entropy_biased(dim, A, k=1, alpha=1.0, result="double"):
 
 def prox_two_entropy(dim, p, A, alpha=1.0, result=None):
     """Batched form of prox_two_entropy(p, first, last, aux, alpha)
-    (two_entropy.h:272-283), which the reference has per column only."""
+    (two_entropy.h:280-292), which the reference has per column only."""
     return prox("two_entropy", _rows(dim, A), p=p, alpha=alpha, result=result)
 
 

@@ -87,7 +87,7 @@ void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_param
     case SDCA_PROX_TOPK_ENTROPY_BIASED:
       sdca::prox_topk_entropy_biased(m, first, last, aux, k, static_cast<R>(p->alpha)); break;
     case SDCA_PROX_TWO_ENTROPY:
-      // The reference has the per-column form only (two_entropy.h:272-283).
+      // The reference has the per-column form only (two_entropy.h:280-292).
       for (int64_t j = 0; first + j * m < last; ++j)
         sdca::prox_two_entropy(col_p ? static_cast<std::ptrdiff_t>(col_p[j])
                                      : static_cast<std::ptrdiff_t>(p->p),
