@@ -175,6 +175,36 @@ int sdca_eval_scores(const sdca_objective* objs, int n_obj,
                      sdca_eval_record* records, double* accuracy,
                      double* per_example, unsigned flags, void* stream);
 
+/*
+ * flags bit of the evaluation calls: evaluate a test set (eval_test,
+ * eval/types.h:128-172, finished as eval/core.h:98-132): only the primal loss
+ * (times the loss coefficient), the top-k accuracy or the rank loss are
+ * computed; the dual variables of the examples, W0 and the regularizers are
+ * not used, and the other record fields are 0.
+ */
+#define SDCA_EVAL_TEST 2u
+
+/*
+ * Whole-dataset evaluation for kernel input: evaluate_dataset (eval.h:15-51)
+ * with kernel_input (data/input.h:44-76).  scores_i = A K_i
+ * (eval/scores.h:30-47) for all i at once on the matrix cores, with
+ *   K: n_train x n kernel matrix, column-major;
+ *   A: m x n_train dual variables, column-major.
+ * A training set (n == n_train) also gets each example's dual loss from its
+ * column of A and the dual regularizer sum_i 0.5 <a_i, s_i>
+ * (eval/regularizer.h:81-98, objective_base.h:92-105) in both regularizer
+ * terms; there is no primal regularizer.  With SDCA_EVAL_TEST, the records
+ * of a test set (K is n_train x n_test).  Other arguments as in
+ * sdca_eval_features.
+ */
+int sdca_eval_kernel(const sdca_objective* objs, int n_obj,
+                     sdca_dtype data, sdca_dtype result,
+                     int64_t n_train, int64_t m, int64_t n,
+                     const void* K, const void* A, const int64_t* labels,
+                     const int64_t* offsets, sdca_eval_record* records,
+                     double* accuracy, double* per_example,
+                     unsigned flags, void* stream);
+
 /* scores = W' X on the matrix cores (eval/scores.h:21-26 for all i at once). */
 int sdca_scores(sdca_dtype data, int64_t d, int64_t m, int64_t n,
                 const void* X, const void* W, void* S,

@@ -233,23 +233,9 @@ struct eval_record {
   std::vector<double> accuracy;  // multiclass: top-(i+1) accuracy after partial_sum / n
 };
 
-// evaluate_dataset (eval.h:15-51) for feature_input: X is d x n and W is
-// d x m, column-major (num_dimensions fastest), labels 0-based; offsets is
-// empty for multiclass and holds the n + 1 CSR offsets for multilabel.
-// A (m x n dual variables) and W0 (prox mode) may be null.
-template <typename Data, typename Result = double>
-inline std::vector<eval_record> evaluate_features(
-    const std::vector<sdca_objective>& objectives, std::int64_t d, std::int64_t m,
-    std::int64_t n, const Data* X, const Data* W, const std::vector<std::int64_t>& labels,
-    const std::vector<std::int64_t>& offsets = std::vector<std::int64_t>(),
-    const Data* A = nullptr, const Data* W0 = nullptr) {
-  std::vector<sdca_eval_record> recs(objectives.size());
-  std::vector<double> acc(static_cast<size_t>(m), 0.0);
-  detail::check(sdca_eval_features(
-      objectives.data(), static_cast<int>(objectives.size()), detail::dtype<Data>::value,
-      detail::dtype<Result>::value, d, m, n, X, W, A, W0, labels.data(),
-      offsets.empty() ? nullptr : offsets.data(), recs.data(),
-      offsets.empty() ? acc.data() : nullptr, nullptr, SDCA_HOST_PTR, nullptr));
+namespace detail {
+inline std::vector<eval_record> records(const std::vector<sdca_eval_record>& recs,
+                                        const std::vector<double>& acc, bool multiclass) {
   std::vector<eval_record> out(recs.size());
   for (size_t i = 0; i < recs.size(); ++i) {
     out[i].primal = recs[i].primal;
@@ -259,9 +245,51 @@ inline std::vector<eval_record> evaluate_features(
     out[i].primal_regularizer = recs[i].primal_regularizer;
     out[i].dual_regularizer = recs[i].dual_regularizer;
     out[i].rank_loss = recs[i].rank_loss;
-    if (offsets.empty()) out[i].accuracy = acc;
+    if (multiclass) out[i].accuracy = acc;
   }
   return out;
+}
+}  // namespace detail
+
+// evaluate_dataset (eval.h:15-51) for feature_input: X is d x n and W is
+// d x m, column-major (num_dimensions fastest), labels 0-based; offsets is
+// empty for multiclass and holds the n + 1 CSR offsets for multilabel.
+// A (m x n dual variables) and W0 (prox mode) may be null.  test = true
+// evaluates a test set (eval_test: primal loss and accuracy / rank loss).
+template <typename Data, typename Result = double>
+inline std::vector<eval_record> evaluate_features(
+    const std::vector<sdca_objective>& objectives, std::int64_t d, std::int64_t m,
+    std::int64_t n, const Data* X, const Data* W, const std::vector<std::int64_t>& labels,
+    const std::vector<std::int64_t>& offsets = std::vector<std::int64_t>(),
+    const Data* A = nullptr, const Data* W0 = nullptr, bool test = false) {
+  std::vector<sdca_eval_record> recs(objectives.size());
+  std::vector<double> acc(static_cast<size_t>(m), 0.0);
+  detail::check(sdca_eval_features(
+      objectives.data(), static_cast<int>(objectives.size()), detail::dtype<Data>::value,
+      detail::dtype<Result>::value, d, m, n, X, W, A, W0, labels.data(),
+      offsets.empty() ? nullptr : offsets.data(), recs.data(),
+      offsets.empty() ? acc.data() : nullptr, nullptr,
+      SDCA_HOST_PTR | (test ? SDCA_EVAL_TEST : 0u), nullptr));
+  return detail::records(recs, acc, offsets.empty());
+}
+
+// evaluate_dataset for kernel_input (data/input.h:44-76): K is n_train x n
+// and A (the dual variables) m x n_train, column-major; scores_i = A K_i
+// (eval/scores.h:30-47).  A training set has n == n_train.
+template <typename Data, typename Result = double>
+inline std::vector<eval_record> evaluate_kernel(
+    const std::vector<sdca_objective>& objectives, std::int64_t n_train, std::int64_t m,
+    std::int64_t n, const Data* K, const Data* A, const std::vector<std::int64_t>& labels,
+    const std::vector<std::int64_t>& offsets = std::vector<std::int64_t>(), bool test = false) {
+  std::vector<sdca_eval_record> recs(objectives.size());
+  std::vector<double> acc(static_cast<size_t>(m), 0.0);
+  detail::check(sdca_eval_kernel(
+      objectives.data(), static_cast<int>(objectives.size()), detail::dtype<Data>::value,
+      detail::dtype<Result>::value, n_train, m, n, K, A, labels.data(),
+      offsets.empty() ? nullptr : offsets.data(), recs.data(),
+      offsets.empty() ? acc.data() : nullptr, nullptr,
+      SDCA_HOST_PTR | (test ? SDCA_EVAL_TEST : 0u), nullptr));
+  return detail::records(recs, acc, offsets.empty());
 }
 
 }  // namespace hip

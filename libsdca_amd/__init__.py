@@ -39,7 +39,7 @@ __all__ = [
     "prox_topk_entropy", "prox_two_simplex", "prox_knapsack_le_biased",
     "prox_topk_simplex_biased", "prox_topk_cone_biased", "prox_topk_entropy_biased",
     "prox_two_simplex_sort", "prox_two_entropy", "lambert_w_exp", "OPS", "F32", "F64",
-    "OBJECTIVES", "objective", "scores", "eval_features", "eval_scores",
+    "OBJECTIVES", "objective", "scores", "eval_features", "eval_kernel", "eval_scores",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -314,8 +314,11 @@ def scores(X, W, out=None):
     return S
 
 
+EVAL_TEST = 2  # SDCA_EVAL_TEST
+
+
 def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_example, torch_mode,
-          data, tail_args=()):
+          data, tail_args=(), test=False):
     lib = library()
     res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
     objarr = _objs(objs)
@@ -336,6 +339,8 @@ def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_exampl
         if per_example:
             pe = np.zeros((n, len(objs), 2), dtype=np.float64)
         flags, stream = HOST_PTR, None
+    if test:
+        flags |= EVAL_TEST
     fn = getattr(lib, fn_name)
     fn.restype = ctypes.c_int
     args = [objarr, ctypes.c_int(len(objs)), ctypes.c_int(data), ctypes.c_int(res)]
@@ -349,18 +354,35 @@ def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_exampl
 
 
 def eval_features(objs, X, W, labels, A=None, W0=None, offsets=None, result=None,
-                  per_example=False):
+                  per_example=False, test=False):
     """evaluate_dataset for feature input.  objs: list of objective(...).
     Returns (records, accuracy, per_example): one eval record per objective
     (primal, dual, primal_loss, dual_loss, primal/dual regularizer, rank_loss),
     the top-(i+1) accuracies (multiclass) and optionally the (n, n_obj, 2)
-    per-example (primal, dual) losses before the loss coefficient."""
+    per-example (primal, dual) losses before the loss coefficient.
+    test=True gives a test set's records (eval_test: primal loss and
+    accuracy / rank loss only)."""
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(W.shape[0])
     lead = (X, [ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
                 ctypes.c_void_p(_ptr(X)), ctypes.c_void_p(_ptr(W))])
     return _eval("sdca_eval_features", objs, lead, m, n, labels, offsets, A, result, per_example,
-                 _is_torch(X), _dtype_code(X), tail_args=(ctypes.c_void_p(_ptr(W0)),))
+                 _is_torch(X), _dtype_code(X), tail_args=(ctypes.c_void_p(_ptr(W0)),), test=test)
+
+
+def eval_kernel(objs, K, A, labels, offsets=None, result=None, per_example=False, test=False):
+    """evaluate_dataset for kernel input (data/input.h:44-76): K is (n, n_train),
+    row i the kernel column K_i of example i; A is (n_train, m), the dual
+    variables (rows are the reference's columns); scores_i = A K_i.  For a
+    training set (n == n_train) the dual losses come from A's rows and the
+    dual regularizer is sum_i 0.5 <a_i, s_i>; test=True gives a test set's
+    records."""
+    n, n_train = int(K.shape[0]), int(K.shape[1])
+    m = int(A.shape[1])
+    lead = (K, [ctypes.c_int64(n_train), ctypes.c_int64(m), ctypes.c_int64(n),
+                ctypes.c_void_p(_ptr(K))])
+    return _eval("sdca_eval_kernel", objs, lead, m, n, labels, offsets, A, result, per_example,
+                 _is_torch(K), _dtype_code(K), test=test)
 
 
 def eval_scores(objs, S, labels, A=None, offsets=None, primal_regularizer=0.0,

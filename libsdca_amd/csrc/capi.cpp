@@ -392,13 +392,22 @@ int check_labels(const int64_t* labels, const int64_t* offsets, int64_t m, int64
 
 // The shared part of sdca_eval_scores / sdca_eval_features: epilogue,
 // reductions and eval_end (eval/core.h:43-95) on device pointers.
+//   dA_reg: non-NULL for the kernel-input training evaluation: the dual
+//           regularizer sum_i 0.5 <a_i, s_i> of A (m x n) and the scores;
+//   test:   eval_test records (primal loss, accuracy / rank loss only).
 int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, int64_t m,
                    int64_t n, const void* dS, const void* dA, const int64_t* dlabels,
                    const int64_t* doffsets, const void* dW, const void* dW0, int64_t dm,
-                   double preg_in, double dreg_in, sdca_eval_record* records, double* accuracy,
-                   double* per_example, bool per_example_host, hipStream_t stream) {
+                   const void* dA_reg, bool test, double preg_in, double dreg_in,
+                   sdca_eval_record* records, double* accuracy, double* per_example,
+                   bool per_example_host, hipStream_t stream) {
   using namespace sdca_gpu;
   const bool multilabel = doffsets != nullptr;
+  if (test) {
+    dA = nullptr;
+    dW = nullptr;
+    dA_reg = nullptr;
+  }
   // Scratch layout: per-example losses, counts, rank, slow list, sums, hist, reg.
   const size_t pe_bytes = static_cast<size_t>(n) * n_obj * 2 * sizeof(double);
   const size_t cnt_bytes = static_cast<size_t>(n) * sizeof(int);
@@ -407,9 +416,10 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   const size_t sums_bytes = (2 * kMaxObjectives + 2) * sizeof(double);
   const size_t hist_bytes = static_cast<size_t>(m) * sizeof(unsigned long long);
   const size_t reg_bytes = (2 * 512 + 2) * sizeof(double);
+  const size_t dreg_bytes = dA_reg ? (static_cast<size_t>(n) + 1) * sizeof(double) : 0;
   auto align = [](size_t b) { return (b + 255) / 256 * 256; };
   const size_t total = align(pe_bytes) + align(cnt_bytes) + align(rank_bytes) + align(slow_bytes) +
-                       align(sums_bytes) + align(hist_bytes) + align(reg_bytes);
+                       align(sums_bytes) + align(hist_bytes) + align(reg_bytes) + align(dreg_bytes);
   void* ws = nullptr;
   int rc = workspace(stream, 2, total, &ws);
   if (rc) return rc;
@@ -420,7 +430,8 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   int* d_slow = reinterpret_cast<int*>(p); p += align(slow_bytes);
   double* d_sums = reinterpret_cast<double*>(p); p += align(sums_bytes);
   unsigned long long* d_hist = reinterpret_cast<unsigned long long*>(p); p += align(hist_bytes);
-  double* d_reg = reinterpret_cast<double*>(p);
+  double* d_reg = reinterpret_cast<double*>(p); p += align(reg_bytes);
+  double* d_dreg = reinterpret_cast<double*>(p);  // n per-example terms, then the sum
 
   EvalLaunch a;
   a.data = data;
@@ -451,6 +462,9 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
                "evaluation reduction kernels");
   if (dW) SDCA_HIP_TRY(launch_regularizer(data, dW, dW0, dm, d_reg + 2, d_reg, stream),
                        "regularizer kernel");
+  if (dA_reg)
+    SDCA_HIP_TRY(launch_dual_regularizer(data, result, dA_reg, dS, m, n, d_dreg, d_dreg + n, stream),
+                 "dual regularizer kernel");
 
   std::vector<double> sums(2 * kMaxObjectives + 2, 0.0), reg(2, 0.0);
   std::vector<unsigned long long> hist(static_cast<size_t>(m), 0ull);
@@ -461,6 +475,9 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
                  "hipMemcpyAsync(D2H)");
   if (dW) SDCA_HIP_TRY(hipMemcpyAsync(reg.data(), d_reg, 2 * sizeof(double), hipMemcpyDeviceToHost,
                                       stream), "hipMemcpyAsync(D2H)");
+  double dual_reg = 0;
+  if (dA_reg) SDCA_HIP_TRY(hipMemcpyAsync(&dual_reg, d_dreg + n, sizeof(double),
+                                          hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
   if (per_example) {
     SDCA_HIP_TRY(hipMemcpyAsync(per_example, d_pe, pe_bytes,
                                 per_example_host ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice,
@@ -475,15 +492,25 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
     preg = reg[0] - (dW0 ? reg[1] : 0.0);
     dreg = reg[0];
   }
+  if (dA_reg) {  // regularizers_dual adds the same term to both (objective_base.h:92-105)
+    preg = dual_reg;
+    dreg = dual_reg;
+  }
   for (int o = 0; o < n_obj; ++o) {
     sdca_eval_record& r = records[o];
     r.primal_loss = loss_coeff(objs[o]) * sums[2 * o];
+    r.rank_loss = multilabel ? sums[2 * kMaxObjectives] / static_cast<double>(n) : 0.0;
+    if (test) {
+      // eval_test holds the primal loss and the accuracy / rank loss only.
+      r.dual_loss = r.primal_regularizer = r.dual_regularizer = r.dual = 0.0;
+      r.primal = r.primal_loss;
+      continue;
+    }
     r.dual_loss = sums[2 * o + 1];
     r.primal_regularizer = preg;
     r.dual_regularizer = dreg;
     r.primal = r.primal_loss + preg;
     r.dual = r.dual_loss - dreg;
-    r.rank_loss = multilabel ? sums[2 * kMaxObjectives] / static_cast<double>(n) : 0.0;
   }
   if (!multilabel && accuracy) {
     unsigned long long run = 0;
@@ -535,12 +562,14 @@ int sdca_scores(sdca_dtype data, int64_t d, int64_t m, int64_t n, const void* X,
   return SDCA_OK;
 }
 
+// Feature input (X, W), kernel input (kernel: X = K, W = A, d = n_train) or
+// given scores (S).
 static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,
                        int64_t d, int64_t m, int64_t n, const void* X, const void* W,
                        const void* S, const void* A, const void* W0, const int64_t* labels,
                        const int64_t* offsets, double preg, double dreg,
                        sdca_eval_record* records, double* accuracy, double* per_example,
-                       unsigned flags, void* stream_ptr) {
+                       unsigned flags, void* stream_ptr, bool kernel = false) {
   using namespace sdca_gpu;
   g_last_error.clear();
   int rc = check_dtypes(data, result);
@@ -572,7 +601,7 @@ static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, s
     if (X && (rc = stage_in(X, es * d * n, dx, stream))) return rc;
     if (W && (rc = stage_in(W, es * d * m, dw, stream))) return rc;
     if (S && (rc = stage_in(S, es * m * n, ds, stream))) return rc;
-    if (A && (rc = stage_in(A, es * m * n, da, stream))) return rc;
+    if (A && (rc = stage_in(A, es * m * (kernel ? d : n), da, stream))) return rc;
     if (W0 && (rc = stage_in(W0, es * d * m, dw0, stream))) return rc;
     if ((rc = stage_in(labels, sizeof(int64_t) * nlab, dl, stream))) return rc;
     if (offsets && (rc = stage_in(offsets, sizeof(int64_t) * (n + 1), doff, stream))) return rc;
@@ -583,6 +612,15 @@ static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, s
     pW0 = W0 ? dw0.ptr : nullptr;
     pl = static_cast<const int64_t*>(dl.ptr);
     poff = offsets ? static_cast<const int64_t*>(doff.ptr) : nullptr;
+  }
+  const bool test = (flags & SDCA_EVAL_TEST) != 0;
+  if (kernel) {
+    // scores_i = A K_i (eval/scores.h:30-47) as W' X with W = A' (n_train x m,
+    // column-major), transposed once into the stream's workspace.
+    void* wt = nullptr;
+    if ((rc = workspace(stream, 3, es * static_cast<size_t>(m) * static_cast<size_t>(d), &wt))) return rc;
+    SDCA_HIP_TRY(launch_transpose(data, pA, wt, d, m, stream), "transpose kernel");
+    pW = wt;
   }
   if (!pS) {
     // scores = W' X into the stream's workspace
@@ -597,9 +635,10 @@ static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, s
                                           n, m, d, stream), "scores kernel");
     pS = sbuf;
   }
-  return eval_on_device(objs, n_obj, data, result, m, n, pS, pA, pl, poff, X ? pW : nullptr,
-                        X ? pW0 : nullptr, d * m, preg, dreg, records, accuracy, per_example, host,
-                        stream);
+  return eval_on_device(objs, n_obj, data, result, m, n, pS, pA, pl, poff,
+                        (X && !kernel) ? pW : nullptr, (X && !kernel) ? pW0 : nullptr, d * m,
+                        kernel ? pA : nullptr, test, preg, dreg, records, accuracy, per_example,
+                        host, stream);
 }
 
 int sdca_eval_features(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,
@@ -611,6 +650,21 @@ int sdca_eval_features(const sdca_objective* objs, int n_obj, sdca_dtype data, s
   if (d < 1) return fail(SDCA_ERR_ARG_RANGE, "d must be >= 1 (got %lld)", (long long)d);
   return eval_common(objs, n_obj, data, result, d, m, n, X, W, nullptr, A, W0, labels, offsets,
                      0.0, 0.0, records, accuracy, per_example, flags, stream);
+}
+
+int sdca_eval_kernel(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,
+                     int64_t n_train, int64_t m, int64_t n, const void* K, const void* A,
+                     const int64_t* labels, const int64_t* offsets, sdca_eval_record* records,
+                     double* accuracy, double* per_example, unsigned flags, void* stream) {
+  if (!K || !A) return fail(SDCA_ERR_ARG_NULL, "K and A must not be NULL");
+  if (n_train < 1) return fail(SDCA_ERR_ARG_RANGE, "n_train must be >= 1 (got %lld)", (long long)n_train);
+  if (!(flags & SDCA_EVAL_TEST) && n != n_train)
+    return fail(SDCA_ERR_ARG_RANGE,
+                "a training set's kernel is n_train x n_train (got n_train %lld, n %lld)",
+                (long long)n_train, (long long)n);
+  return eval_common(objs, n_obj, data, result, n_train, m, n, K, nullptr, nullptr, A, nullptr,
+                     labels, offsets, 0.0, 0.0, records, accuracy, per_example, flags, stream,
+                     true);
 }
 
 int sdca_eval_scores(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,

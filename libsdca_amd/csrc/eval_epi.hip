@@ -914,6 +914,61 @@ __global__ void regularizer_final(const double* __restrict__ partials, int nb, d
   }
 }
 
+// out (cols x rows, row-major) = in (rows x cols, row-major)^T through a
+// padded 32 x 32 LDS tile: both the reads and the writes are coalesced.
+template <class D>
+__global__ void __launch_bounds__(256)
+transpose_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t rows, int64_t cols) {
+  __shared__ D tile[32][33];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 32, c0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    if (r < rows && c < cols) tile[k][tx] = in[r * cols + c];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (r < rows && c < cols) out[c * rows + r] = tile[tx][k];
+  }
+}
+
+// Per-example dual regularizer of the kernel-input evaluation,
+// static_cast<Result>(dot(a_i, s_i)) / 2 (objective_base.h:92-105), one wave
+// per example; the dot is accumulated in double and rounded to Data as the
+// Data-typed BLAS dot returns it.
+template <class D, class R>
+__global__ void __launch_bounds__(256)
+dualreg_kernel(const D* __restrict__ A, const D* __restrict__ S, int64_t m, int64_t n,
+               double* __restrict__ per_example) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const D* a = A + i * m;
+  const D* sc = S + i * m;
+  double acc = 0;
+  for (int64_t c = lane; c < m; c += 64) acc += static_cast<double>(a[c]) * static_cast<double>(sc[c]);
+  acc = group_sum<64>(acc);
+  if (lane == 0)
+    per_example[i] = static_cast<double>(static_cast<R>(static_cast<D>(acc)) / R(2));
+}
+
+// Deterministic sum of x[0, n) into *out: one workgroup, fixed strided order
+// and a fixed LDS tree.
+__global__ void __launch_bounds__(256)
+sum_kernel(const double* __restrict__ x, int64_t n, double* __restrict__ out) {
+  __shared__ double part[256];
+  double acc = 0;
+  for (int64_t i = threadIdx.x; i < n; i += 256) acc += x[i];
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = part[0];
+}
+
 __global__ void __launch_bounds__(256)
 gemm_f64_kernel(const double* __restrict__ X, const double* __restrict__ W, double* __restrict__ S,
                 int64_t n, int64_t m, int64_t d) {
@@ -981,6 +1036,38 @@ hipError_t launch_regularizer(int data, const void* W, const void* W0, int64_t c
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(regularizer_final, dim3(1), dim3(64), 0, stream, partials,
                      static_cast<int>(blocks), out);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose(int data, const void* in, void* out, int64_t rows, int64_t cols,
+                            hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((cols + 31) / 32), static_cast<unsigned>((rows + 31) / 32));
+  if (data == SDCA_F32)
+    hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, stream,
+                       static_cast<const float*>(in), static_cast<float*>(out), rows, cols);
+  else
+    hipLaunchKernelGGL(transpose_kernel<double>, grid, dim3(256), 0, stream,
+                       static_cast<const double*>(in), static_cast<double*>(out), rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_dual_regularizer(int data, int result, const void* A, const void* S, int64_t m,
+                                   int64_t n, double* per_example, double* out,
+                                   hipStream_t stream) {
+  const unsigned blocks = static_cast<unsigned>((n + 3) / 4);
+  if (data == SDCA_F32 && result == SDCA_F32)
+    hipLaunchKernelGGL((dualreg_kernel<float, float>), dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const float*>(A), static_cast<const float*>(S), m, n, per_example);
+  else if (data == SDCA_F32)
+    hipLaunchKernelGGL((dualreg_kernel<float, double>), dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const float*>(A), static_cast<const float*>(S), m, n, per_example);
+  else
+    hipLaunchKernelGGL((dualreg_kernel<double, double>), dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const double*>(A), static_cast<const double*>(S), m, n,
+                       per_example);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(sum_kernel, dim3(1), dim3(256), 0, stream, per_example, n, out);
   return hipGetLastError();
 }
 

@@ -59,6 +59,15 @@ hipError_t launch_eval_reduce(const EvalLaunch& a, double* sums, double* rank_su
 hipError_t launch_regularizer(int data, const void* W, const void* W0, int64_t count,
                               double* partials, double* out, hipStream_t stream);
 
+// out (cols x rows) = in (rows x cols)^T, both row-major.
+hipError_t launch_transpose(int data, const void* in, void* out, int64_t rows, int64_t cols,
+                            hipStream_t stream);
+// *out = sum_i static_cast<Result>(dot(A_i, S_i)) / 2 over n examples of m
+// entries; `per_example` holds n doubles.
+hipError_t launch_dual_regularizer(int data, int result, const void* A, const void* S, int64_t m,
+                                   int64_t n, double* per_example, double* out,
+                                   hipStream_t stream);
+
 }  // namespace sdca_gpu
 
 #endif

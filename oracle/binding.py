@@ -189,6 +189,20 @@ class Library:
         assert rc == 0
         return S
 
+    def dual_regularizer(self, A, S, result=None):
+        """Kernel-input dual regularizer: A, S (n, m) -> (preg, dreg)."""
+        data = _dt(A)
+        result = data if result is None else result
+        preg = ctypes.c_double()
+        dreg = ctypes.c_double()
+        f = self.lib.oracle_dual_regularizer
+        f.restype = ctypes.c_int
+        rc = f(ctypes.c_int(data), ctypes.c_int(result), ctypes.c_int64(A.shape[1]),
+               ctypes.c_int64(A.shape[0]), ctypes.c_void_p(A.ctypes.data),
+               ctypes.c_void_p(S.ctypes.data), ctypes.byref(preg), ctypes.byref(dreg))
+        assert rc == 0
+        return preg.value, dreg.value
+
     def regularizers(self, W, W0=None, result=None):
         data = _dt(W)
         result = data if result is None else result

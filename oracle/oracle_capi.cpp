@@ -237,6 +237,22 @@ void regularizers(int64_t dm, const D* W, const D* W0, double& preg, double& dre
   dreg = static_cast<double>(dr);
 }
 
+// Dual regularizer of the kernel-input evaluation: the per-example
+// regularizers_dual (objective_base.h:92-105, reached from the loop of
+// eval.h:36-41 through eval/regularizer.h:81-98), 0.5 <a_i, s_i> added to
+// both terms, summed over the examples in order.
+template <class D, class R>
+void dual_regularizer(int64_t m, int64_t n, const D* A, const D* S, double& preg, double& dreg) {
+  R pr = 0, dr = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    R regul = static_cast<R>(orc::blas_dot<D>(m, A + i * m, S + i * m)) / 2;
+    pr += regul;
+    dr += regul;
+  }
+  preg = static_cast<double>(pr);
+  dreg = static_cast<double>(dr);
+}
+
 // scores = W' X as column dot products in the Data type.
 template <class D>
 void scores_impl(int64_t d, int64_t m, int64_t n, const D* X, const D* W, D* S,
@@ -318,6 +334,19 @@ int oracle_regularizers(int data, int result, int64_t dm, const void* W, const v
     regularizers<float, double>(dm, static_cast<const float*>(W), static_cast<const float*>(W0), *preg, *dreg);
   else if (data == SDCA_F64 && result == SDCA_F64)
     regularizers<double, double>(dm, static_cast<const double*>(W), static_cast<const double*>(W0), *preg, *dreg);
+  else
+    return SDCA_ERR_PRECISION;
+  return 0;
+}
+
+int oracle_dual_regularizer(int data, int result, int64_t m, int64_t n, const void* A,
+                            const void* S, double* preg, double* dreg) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    dual_regularizer<float, float>(m, n, static_cast<const float*>(A), static_cast<const float*>(S), *preg, *dreg);
+  else if (data == SDCA_F32 && result == SDCA_F64)
+    dual_regularizer<float, double>(m, n, static_cast<const float*>(A), static_cast<const float*>(S), *preg, *dreg);
+  else if (data == SDCA_F64 && result == SDCA_F64)
+    dual_regularizer<double, double>(m, n, static_cast<const double*>(A), static_cast<const double*>(S), *preg, *dreg);
   else
     return SDCA_ERR_PRECISION;
   return 0;

@@ -21,7 +21,8 @@ def declared_functions():
 
 def test_header_declares_entry_points():
     names = declared_functions()
-    for want in ("sdca_prox", "sdca_eval_features", "sdca_eval_scores", "sdca_scores",
+    for want in ("sdca_prox", "sdca_eval_features", "sdca_eval_kernel", "sdca_eval_scores",
+                 "sdca_scores",
                  "sdca_last_error", "sdca_prox_params_default", "sdca_abi_version"):
         assert want in names
 
@@ -128,7 +129,11 @@ int main() {
   std::vector<float> X(3 * 4), W(3 * 5);
   std::vector<sdca::hip::eval_record> r =
       sdca::hip::evaluate_features<float>(objs, 3, 5, 4, X.data(), W.data(), y);
-  return r.empty();
+  std::vector<float> K(4 * 4), A(5 * 4);
+  std::vector<sdca::hip::eval_record> rk =
+      sdca::hip::evaluate_kernel<float>(objs, 4, 5, 4, K.data(), A.data(), y,
+                                        std::vector<int64_t>(), true);
+  return r.empty() || rk.empty();
 }
 """
 

@@ -220,3 +220,103 @@ def test_eval_host_pointers(oracle):
     assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n)
     for r, o in zip(recs, o_recs):
         assert abs(r["primal"] - o["primal"]) <= 1e-4 * max(1, abs(o["primal"]))
+
+
+def gram(rng, n_rows, n_cols_from, d, dtype):
+    """Kernel columns K_i = X_train x_i of unit-norm features: (n, n_train)."""
+    Xt = rng.standard_normal((n_cols_from, d))
+    Xt /= np.linalg.norm(Xt, axis=1, keepdims=True)
+    Xq = rng.standard_normal((n_rows, d))
+    Xq /= np.linalg.norm(Xq, axis=1, keepdims=True)
+    return (Xq @ Xt.T).astype(dtype), Xt
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float32, F64), (np.float64, F64)])
+@pytest.mark.parametrize("m,multilabel", [(10, False), (300, False), (40, True)])
+def test_eval_kernel_training_set(cuda, oracle, dtype, result, m, multilabel):
+    """Kernel input (eval/scores.h:30-47): scores_i = A K_i on the matrix cores
+    (A transposed once), the dual losses from A's columns, and the dual
+    regularizer sum_i 0.5 <a_i, s_i> in both terms (eval/regularizer.h:81-98).
+    The epilogue and the regularizer are checked against the oracle on the
+    GPU's own scores, the scores against float64."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(700 + m)
+    n = 700
+    K, _ = gram(rng, n, n, 48, dtype)
+    A = (rng.standard_normal((n, m)) * 0.05).astype(dtype)
+    if multilabel:
+        y, off = multilabel_labels(rng, n, m)
+        objs = ML_OBJS
+    else:
+        y, off = rng.integers(0, m, n), None
+        objs = [o for o in MC_OBJS if o[3] < m]
+    tK, tA = torch.from_numpy(K).to(cuda), torch.from_numpy(A).to(cuda)
+    res = "float" if result == F32 else "double"
+    recs, acc, pe = sd.eval_kernel(objs, tK, tA, y, offsets=off, result=res, per_example=True)
+    S = sd.scores(tK, tA.T.contiguous())
+    torch.cuda.synchronize()
+    S, pe = S.cpu().numpy(), pe.cpu().numpy()
+    # Scores against float64: the d-term forward error bound with d = n_train.
+    S64 = K.astype(np.float64) @ A.astype(np.float64)
+    eps = np.finfo(dtype).eps
+    bound = np.sqrt(n) * eps * (np.abs(K).astype(np.float64) @ np.abs(A).astype(np.float64)) + 1e-30
+    assert (np.abs(S - S64) <= 4 * bound).all()
+    preg, dreg = oracle.dual_regularizer(A, S, result=result)
+    o_recs, o_acc, o_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, off, preg=preg, dreg=dreg,
+                                             result=result, per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, off, result=LONG_DOUBLE,
+                                    per_example=True)
+    rtol = RTOL[F32 if (dtype == np.float32 or result == F32) else F64]
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], rtol, "kernel primal", x_pe[:, :, 0])
+    compare_per_example(pe[:, :, 1], o_pe[:, :, 1], rtol, "kernel dual", x_pe[:, :, 1])
+    if not multilabel:
+        assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n)
+    closed = 0.5 * np.trace(A.astype(np.float64).T @ K.astype(np.float64) @ A.astype(np.float64))
+    for r, o in zip(recs, o_recs):
+        assert r["primal_regularizer"] == r["dual_regularizer"]
+        assert abs(r["dual_regularizer"] - preg) <= max(rtol, 1e-9) * 10 * max(1, abs(preg))
+        assert abs(r["dual_regularizer"] - closed) <= 1e-4 * max(1, abs(closed))
+        for f in ("primal", "dual", "primal_loss", "dual_loss", "rank_loss"):
+            assert abs(r[f] - o[f]) <= 1e-4 * max(1, abs(o[f])), (f, r[f], o[f])
+
+
+@pytest.mark.parametrize("multilabel", [False, True])
+def test_eval_test_sets(cuda, oracle, multilabel):
+    """eval_test records (eval/types.h:128-172, eval/core.h:98-132) for
+    feature and kernel input: the primal loss times the loss coefficient and
+    the accuracy or rank loss, the other fields zero."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(41 + multilabel)
+    n_train, n_test, m, d = 500, 350, 30, 64
+    K, Xt = gram(rng, n_test, n_train, d, np.float32)
+    A = (rng.standard_normal((n_train, m)) * 0.05).astype(np.float32)
+    Xq = rng.standard_normal((n_test, d)).astype(np.float32)
+    W = (rng.standard_normal((m, d)) * 0.1).astype(np.float32)
+    if multilabel:
+        y, off = multilabel_labels(rng, n_test, m)
+        objs = ML_OBJS
+    else:
+        y, off = rng.integers(0, m, n_test), None
+        objs = MC_OBJS
+    tK, tA = torch.from_numpy(K).to(cuda), torch.from_numpy(A).to(cuda)
+    tX, tW = torch.from_numpy(Xq).to(cuda), torch.from_numpy(W).to(cuda)
+    for name, run, S in [
+        ("kernel", lambda: sd.eval_kernel(objs, tK, tA, y, offsets=off, test=True),
+         lambda: sd.scores(tK, tA.T.contiguous())),
+        ("features", lambda: sd.eval_features(objs, tX, tW, y, offsets=off, test=True),
+         lambda: sd.scores(tX, tW))]:
+        recs, acc, _ = run()
+        Sg = S()
+        torch.cuda.synchronize()
+        Sg = Sg.cpu().numpy()
+        o_recs, o_acc, _ = oracle.eval_scores(oracle_objs(objs), Sg, None, y, off)
+        if not multilabel:
+            assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n_test), name
+        for r, o in zip(recs, o_recs):
+            assert abs(r["primal_loss"] - o["primal_loss"]) <= 1e-4 * max(1, abs(o["primal_loss"]))
+            assert r["primal"] == r["primal_loss"]
+            assert r["rank_loss"] == pytest.approx(o["rank_loss"], rel=1e-6, abs=1e-9)
+            for f in ("dual", "dual_loss", "primal_regularizer", "dual_regularizer"):
+                assert r[f] == 0.0, (name, f)

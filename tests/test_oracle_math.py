@@ -565,3 +565,19 @@ def test_two_entropy_root_and_slsqp(oracle, p, alpha):
                                           options={"ftol": 1e-15, "maxiter": 1000})
             assert f(z) <= sol.fun + 1e-9
             assert np.allclose(z, sol.x, atol=1e-5)
+
+
+def test_kernel_input_dual_regularizer(oracle):
+    """Kernel-input evaluation (eval/scores.h:30-47, eval/regularizer.h:81-98):
+    scores s_i = A K_i, and the summed 0.5 <a_i, s_i> equals the closed form
+    0.5 trace(A K A^T), computed from K directly in float64."""
+    rng = np.random.default_rng(60)
+    n, m, d = 40, 7, 12
+    Xf = rng.standard_normal((n, d))
+    K = Xf @ Xf.T                        # Gram matrix, symmetric
+    A = rng.standard_normal((n, m)) * 0.1
+    S = oracle.scores(np.ascontiguousarray(K), np.ascontiguousarray(A.T))   # (n, m): S[i] = A K_i
+    assert np.allclose(S, K @ A, rtol=1e-12, atol=1e-12)
+    preg, dreg = oracle.dual_regularizer(np.ascontiguousarray(A), S)
+    closed = 0.5 * np.trace(A.T @ K @ A)
+    assert preg == pytest.approx(closed, rel=1e-12) and dreg == preg
