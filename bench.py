@@ -94,6 +94,12 @@ CONFIGS = {
                desc="evaluation pass, fp32: X d=4096 x n=100,000 (N(0,1), unit columns), "
                     "W d x m=1000 (N(0,0.01^2)), scores W'X, smooth top-5 hinge (gamma=1) and "
                     "softmax cross-entropy with c=1 (lambda=1/n), top-1/top-5 accuracy"),
+    "c4kernel": dict(op="eval", kernel=True, d=4096, m=1000, n=20_000, dtype="f32", result="f32",
+                     seed=106, objs=[("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)],
+                     desc="kernel-input evaluation pass, fp32: K = X'X (n = n_train = 20,000 "
+                          "unit-norm N(0,1) features of d = 4096), dual variables A m=1000 x n "
+                          "(N(0,0.01^2)), scores A K_i, smooth top-5 hinge (gamma=1) and softmax "
+                          "cross-entropy with c=1, top-1/top-5 accuracy, dual regularizer"),
     "c5eval": dict(op="eval", d=1024, m=200, n=500_000, dtype="f32", result="f32", seed=105,
                    multilabel=True,
                    objs=[("l2_multilabel_hinge_smooth", 1.0, 1.0, 1),
@@ -231,6 +237,14 @@ def make_eval_input(cfg, torch, dev):
     n, m, d = cfg["n"], cfg["m"], cfg["d"]
     X = torch.randn((n, d), generator=g, device=dev, dtype=torch.float32)
     X /= X.norm(dim=1, keepdim=True)
+    if cfg.get("kernel"):
+        # Kernel input: the Gram matrix of the features (n x n, symmetric) and
+        # dual variables A (rows are the reference's columns).
+        K = (X @ X.T).contiguous()
+        del X
+        A = torch.randn((n, m), generator=g, device=dev, dtype=torch.float32) * 0.01
+        labels = torch.randint(0, m, (n,), generator=g, device=dev)
+        return K, A, labels, None
     W = torch.randn((m, d), generator=g, device=dev, dtype=torch.float32) * 0.01
     if cfg.get("multilabel"):
         # 1-5 distinct sorted labels per example, drawn uniformly without replacement.
@@ -254,7 +268,11 @@ def bench_eval(cfg, args, torch, sd):
     objs = cfg["objs"]
     stream = torch.cuda.current_stream()
 
+    kernel = bool(cfg.get("kernel"))
+
     def step():
+        if kernel:  # X = K (n x n_train), W = A (n_train x m)
+            return sd.eval_kernel(objs, X, W, labels, offsets=offsets)
         return sd.eval_features(objs, X, W, labels, offsets=offsets)
 
     for _ in range(args.warmup):
@@ -269,18 +287,20 @@ def bench_eval(cfg, args, torch, sd):
     # The dominant kernel is the score GEMM: time it on its own, event-timed
     # on the stream it runs on.
     S = torch.empty((cfg["n"], cfg["m"]), dtype=torch.float32, device=dev)
+    Wg = W.T.contiguous() if kernel else W   # the GEMM's W operand: A' for kernel input
     for _ in range(2):
-        sd.scores(X, W, out=S)
+        sd.scores(X, Wg, out=S)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
     torch.cuda.synchronize()
     for a, b in ev:
         a.record(stream)
-        sd.scores(X, W, out=S)
+        sd.scores(X, Wg, out=S)
         b.record(stream)
     torch.cuda.synchronize()
     gemm_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
-    flops = 2.0 * cfg["n"] * cfg["m"] * cfg["d"]
+    inner = cfg["n"] if kernel else cfg["d"]  # contraction length: n_train or d
+    flops = 2.0 * cfg["n"] * cfg["m"] * inner
     achieved = flops / (gemm_ms / 1e3) / 1e12
     value = cfg["n"] / (ms_per_step / 1e3)
     extra = {"records": recs}
@@ -301,22 +321,26 @@ def bench_eval(cfg, args, torch, sd):
         "dtype": cfg["dtype"],
         "data": "synthetic (seeded on the device)",
         "config": {"workload": cfg["desc"], "d": cfg["d"], "m": cfg["m"], "n": cfg["n"],
+                   "input": "kernel" if kernel else "features",
                    "objectives": [o[0] for o in objs]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS,
                      "traffic": traffic_of(args.config),
-                     "note": f"score GEMM 2 n m d = {flops:.3e} flop / mean event-timed launch "
+                     "note": f"score GEMM 2 n m {'n_train' if kernel else 'd'} = {flops:.3e} "
+                             f"flop / mean event-timed launch "
                              f"{gemm_ms:.3f} ms; full pass {ms_per_step:.3f} ms"},
         "eval": extra,
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline_eval(cfg, X, W, labels, offsets, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline_eval(cfg, X, W, labels, offsets, args.cpu_seconds,
+                                                   kernel)
     print(json.dumps(result))
 
 
-def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds):
+def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds, kernel=False):
     """The oracle's evaluation (gemv loop + epilogue, single thread, as the
-    reference's evaluate_dataset runs) on a bounded sample of examples."""
+    reference's evaluate_dataset runs) on a bounded sample of examples; for
+    kernel input X is K and W is A, and the dual regularizer is included."""
     import numpy as np
     from oracle import binding
     lib = binding.oracle()
@@ -324,7 +348,8 @@ def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds):
              "l2_multilabel_hinge_smooth": "multilabel_hinge_smooth",
              "l2_multilabel_entropy": "multilabel_entropy"}
     objs = [(oname[o[0]], o[1], o[2], o[3]) for o in cfg["objs"]]
-    Wh = W.cpu().numpy()
+    Wh = np.ascontiguousarray(W.T.cpu().numpy()) if kernel else W.cpu().numpy()
+    Ah = W.cpu().numpy() if kernel else None
     lab = labels.cpu().numpy()
     off = None if offsets is None else offsets.cpu().numpy()
 
@@ -332,7 +357,10 @@ def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds):
         Xs = X[:ne].cpu().numpy()
         t0 = time.perf_counter()
         S = lib.scores(Xs, Wh)
-        if off is None:
+        if kernel:
+            lib.dual_regularizer(Ah[:ne], S)
+            lib.eval_scores(objs, S, Ah[:ne], lab[:ne])
+        elif off is None:
             lib.eval_scores(objs, S, None, lab[:ne])
         else:
             lib.eval_scores(objs, S, None, lab[: off[ne]], off[: ne + 1])
