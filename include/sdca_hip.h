@@ -205,6 +205,16 @@ int sdca_eval_kernel(const sdca_objective* objs, int n_obj,
                      double* accuracy, double* per_example,
                      unsigned flags, void* stream);
 
+/*
+ * W = W0 + X A' (W = X A' when W0 is NULL) on the matrix cores: the primal
+ * recomputation of eval_recompute_primal (eval/core.h:148-182), which the
+ * reference runs before each evaluation when built with SDCA_ACCURATE_MATH.
+ *   X: d x n features, A: m x n dual variables, W0, W: d x m, column-major.
+ */
+int sdca_recompute_primal(sdca_dtype data, int64_t d, int64_t m, int64_t n,
+                          const void* X, const void* A, const void* W0, void* W,
+                          unsigned flags, void* stream);
+
 /* scores = W' X on the matrix cores (eval/scores.h:21-26 for all i at once). */
 int sdca_scores(sdca_dtype data, int64_t d, int64_t m, int64_t n,
                 const void* X, const void* W, void* S,

@@ -292,6 +292,15 @@ inline std::vector<eval_record> evaluate_kernel(
   return detail::records(recs, acc, offsets.empty());
 }
 
+// W = W0 + X A' (eval_recompute_primal, eval/core.h:148-182): X is d x n,
+// A m x n, W0 (may be null) and W d x m, column-major.
+template <typename Data>
+inline void recompute_primal(std::int64_t d, std::int64_t m, std::int64_t n, const Data* X,
+                             const Data* A, const Data* W0, Data* W) {
+  detail::check(sdca_recompute_primal(detail::dtype<Data>::value, d, m, n, X, A, W0, W,
+                                      SDCA_HOST_PTR, nullptr));
+}
+
 }  // namespace hip
 }  // namespace sdca
 

@@ -40,6 +40,7 @@ __all__ = [
     "prox_topk_simplex_biased", "prox_topk_cone_biased", "prox_topk_entropy_biased",
     "prox_two_simplex_sort", "prox_two_entropy", "lambert_w_exp", "OPS", "F32", "F64",
     "OBJECTIVES", "objective", "scores", "eval_features", "eval_kernel", "eval_scores",
+    "recompute_primal",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -312,6 +313,31 @@ def scores(X, W, out=None):
                           ctypes.c_void_p(X.ctypes.data), ctypes.c_void_p(W.ctypes.data),
                           ctypes.c_void_p(S.ctypes.data), ctypes.c_uint(HOST_PTR), None))
     return S
+
+
+def recompute_primal(X, A, W0=None, out=None):
+    """W = W0 + A^T X (the reference's W = W0 + X A' of eval_recompute_primal,
+    eval/core.h:148-182): X (n, d) features, A (n, m) dual variables, W0 and
+    the result (m, d)."""
+    lib = library()
+    n, d = int(X.shape[0]), int(X.shape[1])
+    m = int(A.shape[1])
+    data = _dtype_code(X)
+    lib.sdca_recompute_primal.restype = ctypes.c_int
+    if _is_torch(X):
+        import torch
+        W = out if out is not None else torch.empty((m, d), dtype=X.dtype, device=X.device)
+        check(lib.sdca_recompute_primal(data, ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+                                        ctypes.c_void_p(X.data_ptr()), ctypes.c_void_p(A.data_ptr()),
+                                        ctypes.c_void_p(_ptr(W0)), ctypes.c_void_p(W.data_ptr()),
+                                        ctypes.c_uint(0), _stream_ptr()))
+        return W
+    W = out if out is not None else np.zeros((m, d), dtype=X.dtype)
+    check(lib.sdca_recompute_primal(data, ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+                                    ctypes.c_void_p(X.ctypes.data), ctypes.c_void_p(A.ctypes.data),
+                                    ctypes.c_void_p(_ptr(W0)), ctypes.c_void_p(W.ctypes.data),
+                                    ctypes.c_uint(HOST_PTR), None))
+    return W
 
 
 EVAL_TEST = 2  # SDCA_EVAL_TEST

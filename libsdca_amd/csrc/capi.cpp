@@ -564,6 +564,55 @@ int sdca_scores(sdca_dtype data, int64_t d, int64_t m, int64_t n, const void* X,
 
 // Feature input (X, W), kernel input (kernel: X = K, W = A, d = n_train) or
 // given scores (S).
+int sdca_recompute_primal(sdca_dtype data, int64_t d, int64_t m, int64_t n, const void* X,
+                          const void* A, const void* W0, void* W, unsigned flags, void* stream_ptr) {
+  using namespace sdca_gpu;
+  g_last_error.clear();
+  int rc = check_dtypes(data, data);
+  if (rc) return rc;
+  if (d < 1 || m < 1 || n < 1) return fail(SDCA_ERR_ARG_RANGE, "need d, m, n >= 1");
+  if (!X || !A || !W) return fail(SDCA_ERR_ARG_NULL, "X, A and W must not be NULL");
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const size_t es = dtype_size(data);
+  DeviceBuffer dx, da, dw0, dw;
+  const void* pX = X;
+  const void* pA = A;
+  const void* pW0 = W0;
+  void* pW = W;
+  if (flags & SDCA_HOST_PTR) {
+    if ((rc = stage_in(X, es * d * n, dx, stream))) return rc;
+    if ((rc = stage_in(A, es * m * n, da, stream))) return rc;
+    if (W0 && (rc = stage_in(W0, es * d * m, dw0, stream))) return rc;
+    SDCA_HIP_TRY(hipMalloc(&dw.ptr, es * d * m), "hipMalloc(staging)");
+    pX = dx.ptr;
+    pA = da.ptr;
+    pW0 = W0 ? dw0.ptr : nullptr;
+    pW = dw.ptr;
+  }
+  // W (m x d row-major) = A' (m x n) X (n x d): the score GEMM with both
+  // operands transposed once so that the contraction over n runs along rows.
+  void* ws = nullptr;
+  if ((rc = workspace(stream, 3, es * static_cast<size_t>(n) * static_cast<size_t>(m + d), &ws)))
+    return rc;
+  void* At = ws;
+  void* Xt = static_cast<char*>(ws) + es * static_cast<size_t>(n) * static_cast<size_t>(m);
+  SDCA_HIP_TRY(launch_transpose(data, pA, At, n, m, stream), "transpose kernel");
+  SDCA_HIP_TRY(launch_transpose(data, pX, Xt, n, d, stream), "transpose kernel");
+  if (data == SDCA_F32)
+    SDCA_HIP_TRY(launch_scores_gemm(static_cast<const float*>(At), static_cast<const float*>(Xt),
+                                    static_cast<float*>(pW), m, d, n, stream), "GEMM kernel");
+  else
+    SDCA_HIP_TRY(launch_scores_gemm_f64(static_cast<const double*>(At),
+                                        static_cast<const double*>(Xt), static_cast<double*>(pW),
+                                        m, d, n, stream), "GEMM kernel");
+  if (pW0) SDCA_HIP_TRY(launch_add(data, pW, pW0, d * m, stream), "add kernel");
+  if (flags & SDCA_HOST_PTR) {
+    SDCA_HIP_TRY(hipMemcpyAsync(W, pW, es * d * m, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
+    SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  }
+  return SDCA_OK;
+}
+
 static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, sdca_dtype result,
                        int64_t d, int64_t m, int64_t n, const void* X, const void* W,
                        const void* S, const void* A, const void* W0, const int64_t* labels,

@@ -969,6 +969,14 @@ sum_kernel(const double* __restrict__ x, int64_t n, double* __restrict__ out) {
   if (threadIdx.x == 0) *out = part[0];
 }
 
+template <class D>
+__global__ void __launch_bounds__(256)
+add_kernel(D* __restrict__ y, const D* __restrict__ x, int64_t count) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    y[i] = x[i] + y[i];
+}
+
 __global__ void __launch_bounds__(256)
 gemm_f64_kernel(const double* __restrict__ X, const double* __restrict__ W, double* __restrict__ S,
                 int64_t n, int64_t m, int64_t d) {
@@ -1048,6 +1056,19 @@ hipError_t launch_transpose(int data, const void* in, void* out, int64_t rows, i
   else
     hipLaunchKernelGGL(transpose_kernel<double>, grid, dim3(256), 0, stream,
                        static_cast<const double*>(in), static_cast<double*>(out), rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(int data, void* y, const void* x, int64_t count, hipStream_t stream) {
+  int64_t blocks = (count + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  if (data == SDCA_F32)
+    hipLaunchKernelGGL(add_kernel<float>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       static_cast<float*>(y), static_cast<const float*>(x), count);
+  else
+    hipLaunchKernelGGL(add_kernel<double>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       static_cast<double*>(y), static_cast<const double*>(x), count);
   return hipGetLastError();
 }
 

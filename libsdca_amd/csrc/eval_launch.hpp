@@ -62,6 +62,8 @@ hipError_t launch_regularizer(int data, const void* W, const void* W0, int64_t c
 // out (cols x rows) = in (rows x cols)^T, both row-major.
 hipError_t launch_transpose(int data, const void* in, void* out, int64_t rows, int64_t cols,
                             hipStream_t stream);
+// y[i] = x[i] + y[i].
+hipError_t launch_add(int data, void* y, const void* x, int64_t count, hipStream_t stream);
 // *out = sum_i static_cast<Result>(dot(A_i, S_i)) / 2 over n examples of m
 // entries; `per_example` holds n doubles.
 hipError_t launch_dual_regularizer(int data, int result, const void* A, const void* S, int64_t m,

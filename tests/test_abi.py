@@ -133,6 +133,8 @@ int main() {
   std::vector<sdca::hip::eval_record> rk =
       sdca::hip::evaluate_kernel<float>(objs, 4, 5, 4, K.data(), A.data(), y,
                                         std::vector<int64_t>(), true);
+  std::vector<float> Wn(3 * 5);
+  sdca::hip::recompute_primal<float>(3, 5, 4, X.data(), A.data(), W.data(), Wn.data());
   return r.empty() || rk.empty();
 }
 """

@@ -320,3 +320,31 @@ def test_eval_test_sets(cuda, oracle, multilabel):
             assert r["rank_loss"] == pytest.approx(o["rank_loss"], rel=1e-6, abs=1e-9)
             for f in ("dual", "dual_loss", "primal_regularizer", "dual_regularizer"):
                 assert r[f] == 0.0, (name, f)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("n,m,d", [(3000, 300, 1000), (517, 37, 100), (64, 2, 1)])
+@pytest.mark.parametrize("with_w0", [False, True])
+def test_recompute_primal(cuda, dtype, n, m, d, with_w0):
+    """W = W0 + X A' (eval/core.h:148-182) against float64, within the
+    n-term dot forward error sqrt(n) eps (sum |x_q a_q| + |w0|)."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(n + m + d)
+    X = rng.standard_normal((n, d)).astype(dtype)
+    A = (rng.standard_normal((n, m)) * 0.1).astype(dtype)
+    W0 = (rng.standard_normal((m, d)) * 0.01).astype(dtype) if with_w0 else None
+    W = sd.recompute_primal(torch.from_numpy(X).to(cuda), torch.from_numpy(A).to(cuda),
+                            None if W0 is None else torch.from_numpy(W0).to(cuda))
+    torch.cuda.synchronize()
+    W = W.cpu().numpy()
+    want = A.astype(np.float64).T @ X.astype(np.float64)
+    mag = np.abs(A.astype(np.float64)).T @ np.abs(X.astype(np.float64))
+    if W0 is not None:
+        want += W0
+        mag += np.abs(W0)
+    eps = np.finfo(dtype).eps
+    assert (np.abs(W - want) <= 4 * np.sqrt(n) * eps * mag + 1e-30).all()
+    if dtype == np.float32 and n == 517:
+        Wh = sd.recompute_primal(X, A, W0)  # host pointers through the staging
+        assert np.array_equal(Wh, W)
