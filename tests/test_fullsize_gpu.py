@@ -285,3 +285,124 @@ def test_c5_eval_full(cuda, oracle):
                                     per_example=True, nthreads=THREADS)
     got = pe.index_select(0, torch.from_numpy(idx).to(cuda)).cpu().numpy()
     compare_per_example(got[:, :, 0], o_pe[:, :, 0], 1e-5, "c5 primal", exact=x_pe[:, :, 0])
+
+
+def test_c2_biased_simplex_full(cuda, oracle):
+    """Biased top-k simplex (rho=1) on the C2 input, m=100, n=4,000,000, fp32:
+    every column, plus 0 <= x <= sum(x)/k and sum(x) <= rhs."""
+    cfg, x, _ = bench_input("c2sbias", cuda)
+    out = run(cfg, x)
+    o = out.double()
+    s = o.sum(dim=1)
+    sc = scale_of(x.double())
+    assert (out >= 0).all()
+    assert (o.amax(dim=1) <= s / cfg["k"] + 1e-5 * sc).all()
+    assert (s <= cfg["rhs"] + 1e-5 * sc).all()
+    chunked_parity(oracle, cfg, x, out)
+
+
+def test_c2_biased_cone_full(cuda, oracle):
+    """Biased top-k cone (rho=1) on the C2 input: every column, plus
+    0 <= x <= sum(x)/k."""
+    cfg, x, _ = bench_input("c2cbias", cuda)
+    out = run(cfg, x)
+    o = out.double()
+    sc = scale_of(x.double())
+    assert (out >= 0).all()
+    assert (o.amax(dim=1) <= o.sum(dim=1) / cfg["k"] + 1e-5 * sc).all()
+    chunked_parity(oracle, cfg, x, out)
+
+
+def test_c1_biased_knapsack_full(cuda, oracle):
+    """Biased knapsack_le (rho=1) on the C1 input, m=10, n=100,000, fp64: every
+    column, plus lo <= x <= hi and sum(x) <= rhs."""
+    cfg, x, _ = bench_input("c1lebias", cuda)
+    out = run(cfg, x)
+    assert ((out >= cfg["lo"]) & (out <= cfg["hi"])).all()
+    assert (out.sum(dim=1) <= cfg["rhs"] + 1e-12 * 10).all()
+    chunked_parity(oracle, cfg, x, out)
+
+
+def test_c5_two_simplex_sort_full(cuda, oracle):
+    """Sort-based two-block simplex on the C5 input, m=200, n=500,000, fp32,
+    per-column p: every column, plus sum(x_P) = sum(x_N) <= rhs."""
+    import torch
+    cfg, x, col_p = bench_input("c5sort", cuda)
+    out = run(cfg, x, col_p)
+    o = out.double()
+    ar = torch.arange(x.shape[1], device=cuda)[None, :]
+    pos = ar < col_p[:, None]
+    sp = torch.where(pos, o, 0).sum(dim=1)
+    sn = torch.where(pos, 0, o).sum(dim=1)
+    s = scale_of(x.double())
+    assert (out >= 0).all()
+    assert ((sp - sn).abs() <= 1e-5 * s).all()
+    assert (sp <= cfg["rhs"] + 1e-5 * s).all()
+    chunked_parity(oracle, cfg, x, out, col_p)
+
+
+@pytest.mark.timeout(300)
+def test_c5_two_entropy_full(cuda, oracle):
+    """Two-block entropy (alpha=1) on the C5 input, m=200, n=500,000, fp32,
+    per-column p: every column, plus x >= 0 and sum(x) = 1."""
+    cfg, x, col_p = bench_input("c5ent", cuda)
+    out = run(cfg, x, col_p)
+    assert (out >= 0).all()
+    assert ((out.double().sum(dim=1) - 1).abs() <= 1e-5 * 200).all()
+    chunked_parity(oracle, cfg, x, out, col_p)
+
+
+@pytest.mark.timeout(300)
+def test_c3_biased_entropy_full(cuda, oracle):
+    """Biased top-k entropy (k=5, alpha=1) on the C3 input, m=1000, n=200,000,
+    fp64: 0 <= x <= sum(x)/k and sum(x) <= 1 on every column; the oracle on a
+    seeded sample of 4,000 columns (all settled on this input)."""
+    import torch
+    from tests.test_prox_gpu import entbias_settled
+    cfg, x, _ = bench_input("c3ebias", cuda)
+    out = run(cfg, x)
+    o = out.double()
+    s = o.sum(dim=1)
+    assert (out >= 0).all()
+    assert (o.amax(dim=1) <= s / cfg["k"] + 1e-12 * 1000).all()
+    assert (s <= 1 + 1e-12 * 1000).all()
+    idx = torch.from_numpy(np.sort(np.random.default_rng(8).choice(x.shape[0], 4000, replace=False))).to(cuda)
+    xs = x.index_select(0, idx).cpu().numpy()
+    got = out.index_select(0, idx).cpu().numpy()
+    assert entbias_settled(oracle, xs, cfg["alpha"], F64).all()
+    parity(oracle, "topk_entropy_biased", xs, got, F64, "topk_entropy_biased sample", THREADS,
+           k=cfg["k"], alpha=cfg["alpha"])
+
+
+@pytest.mark.timeout(300)
+def test_c4_kernel_eval_full(cuda, oracle):
+    """Kernel-input evaluation n = n_train = 20,000, m=1000, fp32: the top-k
+    accuracy recomputed exactly from the GPU's own scores A K_i, the dual
+    regularizer against the oracle on those scores, and the per-example
+    losses of a 2,000-example sample against the oracle."""
+    import torch
+    import bench
+    import libsdca_amd as sd
+    cfg = bench.CONFIGS["c4kernel"]
+    K, A, labels, _ = bench.make_eval_input(cfg, torch, cuda)
+    objs = cfg["objs"]
+    recs, acc, pe = sd.eval_kernel(objs, K, A, labels, per_example=True)
+    S = sd.scores(K, A.T.contiguous())
+    torch.cuda.synchronize()
+    sy = S.gather(1, labels[:, None])
+    cnt = (S >= sy).sum(dim=1) - 1  # classes other than the label scoring >= it
+    hist = torch.bincount(cnt, minlength=cfg["m"]).cpu().numpy()
+    assert np.allclose(acc, np.cumsum(hist) / cfg["n"], rtol=0, atol=1e-12)
+    Sh, Ah = S.cpu().numpy(), A.cpu().numpy()
+    preg, dreg = oracle.dual_regularizer(Ah, Sh)
+    for r in recs:
+        assert abs(r["dual_regularizer"] - dreg) <= 1e-5 * max(1, abs(dreg))
+    idx = np.sort(np.random.default_rng(9).choice(cfg["n"], 2000, replace=False))
+    lab = labels.cpu().numpy()[idx]
+    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Sh[idx], Ah[idx], lab, per_example=True,
+                                    nthreads=THREADS)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), Sh[idx], Ah[idx], lab, result=LONG_DOUBLE,
+                                    per_example=True, nthreads=THREADS)
+    pe = pe.cpu().numpy()[idx]
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], 1e-5, "kernel eval primal", x_pe[:, :, 0])
+    compare_per_example(pe[:, :, 1], o_pe[:, :, 1], 1e-5, "kernel eval dual", x_pe[:, :, 1])
