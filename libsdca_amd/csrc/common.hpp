@@ -144,6 +144,33 @@ __device__ inline double lambert_w_exp(double x) {
   return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
 }
 
+// The same function for inputs spread over all the intervals (the elementwise
+// map over arbitrary x): the branches (0, 4], (4, 2^59] and (-20, 0] each
+// start with one step lw_step5(w0, y0) from their own (w0, y0) = (x, 1),
+// (x - log x, x), (e0, exp_approx(x - e0)) with e0 = exp_approx(x); here that
+// step has one call site with per-lane arguments, so a wave spanning several
+// intervals pays for it once.  Each lane computes exactly the operations of
+// lambert_w_exp, so the results are identical; inside the iterations, where
+// a wave's arguments mostly share an interval, lambert_w_exp is faster.
+__device__ inline double lambert_w_exp_mixed(double x) {
+  const int br = x > 0.0 ? (x <= 4.0 ? 0 : (x <= 576460752303423488.0 ? 1 : 2))
+                         : (x > -20.0 ? 3 : (x > -36.0 ? 4 : 5));
+  double w0 = x, y0 = 1.0;
+  if (br == 1) {
+    w0 = x - log(x);
+    y0 = x;
+  } else if (br == 3 || br == 4) {
+    w0 = exp_approx(x);
+    if (br == 3) y0 = exp_approx(x - w0);
+  }
+  double w = (br == 4) ? w0 : 0.0;
+  if (br == 0 || br == 1 || br == 3) w = lw_step5(w0, y0);
+  const double e = exp(br == 5 ? x : x - w);
+  const double r = lw_step5(w, e);
+  return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
+}
+__device__ inline float lambert_w_exp_mixed(float x) { return lambert_w_exp(x); }
+
 // ---------------------------------------------------------------------------
 // Cross-lane exchange lane <-> lane ^ OFF inside a wave: DPP quad
 // permutations for OFF = 1, 2 (a VALU operand modifier, no LDS traffic),

@@ -500,7 +500,7 @@ __global__ void __launch_bounds__(256) lambert_kernel(const D* __restrict__ in, 
                                                       int64_t count) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride)
-    out[i] = lambert_w_exp(in[i]);
+    out[i] = lambert_w_exp_mixed(in[i]);
 }
 
 }  // namespace
