@@ -669,13 +669,14 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
   // Householder iterations of order 4 (entropy_norm.h:84-102).
   const R ub = lds_masked_max<G, C, D, R>(x, bits) - num<R>::exp_min_arg();
   const R eps16 = R(16) * num<R>::eps();
+  bool warm = false;
   if constexpr (sizeof(R) == 8) {
     // The iteration converges to the root of sum W(exp(x - t)) = rhs from
     // any start near it, and its stopping rule |dt| <= 16 eps is checked in
     // double below; single-precision steps (about a third of the cost) bring
-    // t within ~1e-6 first, so the double loop needs two Lambert passes
-    // instead of about five.  The single-precision estimate is used only if
-    // its own steps settled.
+    // t to single precision first (three passes on U(-10, 10) columns), so
+    // the double loop needs one Lambert pass instead of about five.  The
+    // single-precision estimate is used only if its own steps settled.
     float tf = static_cast<float>(t);
     const float ubf = static_cast<float>(ub);
     bool settled = false;
@@ -704,12 +705,16 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
       const float f02 = f0 * f2, f11 = f1 * f1;
       tf = tc - 3.0f * f0 * (2.0f * f11 - f02) / (6.0f * f1 * (f02 - f11) - f0 * (f0 * f3));
       if (!(fabsf(tf) <= 3.0e38f)) break;
-      if (fabsf(prev - tf) <= 4.0e-6f * fmaxf(1.0f, fabsf(tf))) {
+      // A step of at most 3e-3 (relative) leaves an order-4 correction of
+      // ~1e-9 for the next one: below single precision, so the pass that
+      // would confirm it is skipped.
+      if (fabsf(prev - tf) <= 3.0e-3f * fmaxf(1.0f, fabsf(tf))) {
         settled = true;
         break;
       }
     }
     if (settled) t = static_cast<R>(tf);
+    warm = settled;
   }
   for (int iter = 0; iter < 32; ++iter) {
     const R prev = t;
@@ -739,6 +744,12 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
     const R f02 = f0 * f2, f11 = f1 * f1;
     t = tc - R(3) * f0 * (R(2) * f11 - f02) / (R(6) * f1 * (f02 - f11) - f0 * (f0 * f3));
     if (fabs(prev - t) <= eps16) break;
+    // From a settled single-precision start the first double step moves t by
+    // about the single-precision rounding (~1e-8); when it moves by at most
+    // 1e-6 the order-4 step's next correction is ~1e-24, far below the 1e-12
+    // the results are held to, so the pass that would only confirm it is
+    // skipped.
+    if (warm && iter == 0 && fabs(prev - t) <= R(1e-6) * dmax(R(1), fabs(t))) break;
   }
   return t;
 }
