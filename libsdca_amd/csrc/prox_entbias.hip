@@ -100,6 +100,47 @@ __device__ inline R log_w_inverse_or_min(R w) {
   return (v < num<R>::exp_min_arg()) ? num<R>::exp_min_arg() : v;
 }
 
+// One pass of the uncapped solve: the order-4 Householder step on
+// g(t) = W(e^(alpha - t)) + sum_i W(e^(a_i - t)) - alpha
+// (topk_entropy_biased.h:9-38), with [lo, hi] the root bracket narrowed by
+// the sign of g(t); a step that leaves it becomes the Newton step, or the
+// bisection when that leaves it too.  *s_out (if given) receives
+// sum_i W(e^(a_i - t)) / alpha at the pass's t, as the reference's s.
+// Returns false if g(t) or the step is not finite.
+template <class D, class R>
+__device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, R& lo, R& hi,
+                                    R* s_out) {
+  R f0, f1, f2, f3;
+  lw_sums4(s, m, lane, -t, f0, f1, f2, f3);
+  if (s_out) *s_out = f0 / alpha;
+  {
+    const R v = lambert_w_exp(alpha - t);
+    const R d = R(1) + v;
+    const R d3 = d * d * d;
+    f0 += v;
+    f1 += v / d;
+    f2 += v / d3;
+    f3 += v * (R(1) - R(2) * v) / (d3 * d * d);
+  }
+  f0 -= alpha;
+  if (f0 > R(0)) lo = (t > lo) ? t : lo;
+  else if (f0 < R(0)) hi = (t < hi) ? t : hi;
+  const R f02 = f0 * f2, f11 = f1 * f1;
+  const R den = R(6) * f1 * (f02 - f11) - f0 * (f0 * f3);
+  R step = (fabs(den) > R(64) * num<R>::min_normal()) ? R(3) * f0 * (R(2) * f11 - f02) / den : R(0);
+  R tn = t - step;
+  // Inside the bracket, or a correction below the resolution of t.
+  bool ok = isfinite(tn) && ((tn > lo && tn < hi) || (step != R(0) && tn == t));
+  if (!ok) {
+    step = (f1 > R(0)) ? -f0 / f1 : R(0);  // Newton: f1 = -g'(t)
+    tn = t - step;
+    ok = isfinite(tn) && ((tn > lo && tn < hi) || (step != R(0) && tn == t));
+    if (!ok) tn = lo + (hi - lo) * R(0.5);
+  }
+  t = tn;
+  return isfinite(f0) && isfinite(tn);
+}
+
 // Thresholds (t, 0, hi) of one column whose copy is in s[0, m); entries of U
 // are overwritten with -inf.
 template <class D, class R>
@@ -132,36 +173,27 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     const R top = (alpha > max) ? alpha : max;
     br_hi = top + dlog(dexp(alpha - top) + static_cast<R>(m) * dexp(max - top)) - dlog(alpha);
   }
+  if constexpr (sizeof(R) == 8) {
+    // The same guarded iteration in single precision first (a Lambert pass
+    // costs about a third): it ends once a step moves t by at most 3e-3
+    // (relative), where the next order-4 correction is below single
+    // precision, and the double loop then starts within ~1e-7 of the root
+    // and needs two passes instead of about five.  Its estimate is used
+    // only if it ended so.
+    float tf = static_cast<float>(t);
+    float lo_f = static_cast<float>(br_lo), hi_f = static_cast<float>(br_hi);
+    const float alpha_f = static_cast<float>(alpha);
+    bool settled = false;
+    for (int iter = 0; iter < 16 && !settled; ++iter) {
+      const float t1 = tf;
+      bool ok = guarded_step<D, float>(s, m, lane, alpha_f, tf, lo_f, hi_f, nullptr);
+      settled = ok && fabsf(t1 - tf) <= 3.0e-3f * fmaxf(1.0f, fabsf(tf));
+    }
+    if (settled) t = static_cast<R>(tf);
+  }
   for (int iter = 0; iter < 64; ++iter) {
     const R t1 = t;
-    R f0, f1, f2, f3;
-    lw_sums4(s, m, lane, -t, f0, f1, f2, f3);
-    sv = f0 / alpha;
-    {
-      const R v = lambert_w_exp(alpha - t);
-      const R d = R(1) + v;
-      const R d3 = d * d * d;
-      f0 += v;
-      f1 += v / d;
-      f2 += v / d3;
-      f3 += v * (R(1) - R(2) * v) / (d3 * d * d);
-    }
-    f0 -= alpha;
-    if (f0 > R(0)) br_lo = (t > br_lo) ? t : br_lo;
-    else if (f0 < R(0)) br_hi = (t < br_hi) ? t : br_hi;
-    const R f02 = f0 * f2, f11 = f1 * f1;
-    const R den = R(6) * f1 * (f02 - f11) - f0 * (f0 * f3);
-    R step = (fabs(den) > tiny) ? R(3) * f0 * (R(2) * f11 - f02) / den : R(0);
-    R tn = t - step;
-    // Inside the bracket, or a correction below the resolution of t.
-    bool ok = isfinite(tn) && ((tn > br_lo && tn < br_hi) || (step != R(0) && tn == t));
-    if (!ok) {
-      step = (f1 > R(0)) ? -f0 / f1 : R(0);  // Newton: f1 = -g'(t)
-      tn = t - step;
-      ok = isfinite(tn) && ((tn > br_lo && tn < br_hi) || (step != R(0) && tn == t));
-      if (!ok) tn = br_lo + (br_hi - br_lo) * R(0.5);
-    }
-    t = tn;
+    guarded_step<D, R>(s, m, lane, alpha, t, br_lo, br_hi, &sv);
     if (fabs(t1 - t) <= eps_r) break;
   }
   const R K = static_cast<R>(k);
