@@ -35,6 +35,21 @@ def decades(n, m, dtype, seed, pow_from, pow_to, sign=1.0):
     return x.astype(dtype)
 
 
+def decade_blocks(n, m, dtype, seed, pow_from, pow_to, block=25):
+    """Columns made of consecutive blocks of `block` entries, block b drawn
+    from decade pow_from + (b // 2) % (pow_to - pow_from) with sign + for
+    even b and - for odd b: the concatenated vectors of the reference tests
+    (test_populate_real called per decade with coeff = +1 then -1, e.g.
+    test/prox/topk_simplex.cpp and test/prox/knapsack_eq.cpp)."""
+    rng = np.random.default_rng(seed)
+    b = np.arange(m) // block
+    p = pow_from + (b // 2) % (pow_to - pow_from)
+    sign = np.where(b % 2 == 0, 1.0, -1.0)
+    u = rng.uniform(0, 1, (n, m))
+    x = sign * (10.0 ** p) * (1.0 + 9.0 * u)
+    return x.astype(dtype)
+
+
 def mixed_signs(n, m, dtype, seed, pow_from, pow_to):
     rng = np.random.default_rng(seed)
     s = rng.choice([-1.0, 1.0], (n, m))

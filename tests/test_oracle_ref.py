@@ -63,6 +63,7 @@ def columns(m, dtype, seed):
         inputs.mixed_signs(n, m, dtype, seed + 4, -3, 3),
         np.cumsum(inputs.uniform(n, m, dtype, seed + 5, 0, 1), axis=1).astype(dtype),
         inputs.uniform(n, m, dtype, seed + 6, -10, 10),
+        inputs.decade_blocks(n, m, dtype, seed + 8, -3, 3, block=max(1, min(25, m // 4))),
     ]
     if m >= 1:
         parts.append(inputs.edge_columns(m, dtype, seed + 7))

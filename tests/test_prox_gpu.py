@@ -93,6 +93,8 @@ def cases(m, dtype, seed):
     yield "pos", inputs.decades(n, m, dtype, seed + 2, -3, 3)
     yield "neg", inputs.decades(n, m, dtype, seed + 3, -3, 3, sign=-1.0)
     yield "mixed", inputs.mixed_signs(n, m, dtype, seed + 4, -3, 3)
+    yield "decade blocks", inputs.decade_blocks(n, m, dtype, seed + 6, -3, 3,
+                                                block=max(1, min(25, m // 4)))
     yield "edge", inputs.edge_columns(m, dtype, seed + 5)
 
 
