@@ -417,9 +417,11 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   const size_t hist_bytes = static_cast<size_t>(m) * sizeof(unsigned long long);
   const size_t reg_bytes = (2 * 512 + 2) * sizeof(double);
   const size_t dreg_bytes = dA_reg ? (static_cast<size_t>(n) + 1) * sizeof(double) : 0;
+  const size_t red_bytes = static_cast<size_t>(eval_reduce_scratch(n_obj)) * sizeof(double);
   auto align = [](size_t b) { return (b + 255) / 256 * 256; };
   const size_t total = align(pe_bytes) + align(cnt_bytes) + align(rank_bytes) + align(slow_bytes) +
-                       align(sums_bytes) + align(hist_bytes) + align(reg_bytes) + align(dreg_bytes);
+                       align(sums_bytes) + align(hist_bytes) + align(reg_bytes) + align(dreg_bytes) +
+                       align(red_bytes);
   void* ws = nullptr;
   int rc = workspace(stream, 2, total, &ws);
   if (rc) return rc;
@@ -432,6 +434,8 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   unsigned long long* d_hist = reinterpret_cast<unsigned long long*>(p); p += align(hist_bytes);
   double* d_reg = reinterpret_cast<double*>(p); p += align(reg_bytes);
   double* d_dreg = reinterpret_cast<double*>(p);  // n per-example terms, then the sum
+  p += align(dreg_bytes);
+  double* d_red = reinterpret_cast<double*>(p);
 
   EvalLaunch a;
   a.data = data;
@@ -458,7 +462,7 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   SDCA_HIP_TRY(launch_eval_epilogue(a), "evaluation epilogue kernel");
   if (!multilabel) SDCA_HIP_TRY(launch_eval_slow(a), "evaluation epilogue (deferred examples)");
   SDCA_HIP_TRY(launch_eval_reduce(a, d_sums, multilabel ? d_sums + 2 * kMaxObjectives : nullptr,
-                                  multilabel ? nullptr : d_hist),
+                                  multilabel ? nullptr : d_hist, d_red),
                "evaluation reduction kernels");
   if (dW) SDCA_HIP_TRY(launch_regularizer(data, dW, dW0, dm, d_reg + 2, d_reg, stream),
                        "regularizer kernel");

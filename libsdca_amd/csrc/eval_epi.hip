@@ -838,29 +838,58 @@ hipError_t launch_slow_typed(const EvalLaunch& a) {
   return hipGetLastError();
 }
 
-// Deterministic sums: one workgroup per output, fixed strided order plus a
-// fixed LDS tree.
+// Deterministic sums in two levels: workgroup b sums examples
+// [b chunk, (b + 1) chunk) of every output (2 n_obj loss sums, then the rank
+// loss) in a fixed strided order and LDS tree, and one workgroup sums the
+// partials in a fixed tree.  The chunking depends on n only, so the totals do
+// not depend on scheduling.
+constexpr int kReduceBlocks = 1024;
+
 __global__ void __launch_bounds__(256)
-reduce_kernel(const double* __restrict__ per_example, int64_t n, int n_obj,
-              const double* __restrict__ rank, double* __restrict__ sums,
-              double* __restrict__ rank_sum) {
+reduce_partial_kernel(const double* __restrict__ per_example, int64_t n, int n_obj,
+                      const double* __restrict__ rank, int64_t chunk,
+                      double* __restrict__ partials) {
   __shared__ double part[256];
-  const int out = blockIdx.x;  // 0 .. 2 n_obj - 1: (objective, primal/dual); 2 n_obj: rank
-  double acc = 0;
-  if (out < 2 * n_obj) {
-    for (int64_t i = threadIdx.x; i < n; i += 256) acc += per_example[i * 2 * n_obj + out];
-  } else if (rank) {
-    for (int64_t i = threadIdx.x; i < n; i += 256) acc += rank[i];
-  }
-  part[threadIdx.x] = acc;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (static_cast<int>(threadIdx.x) < w) part[threadIdx.x] += part[threadIdx.x + w];
+  const int outs = 2 * n_obj + 1;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t b1 = (b0 + chunk < n) ? b0 + chunk : n;
+  for (int out = 0; out < outs; ++out) {
+    double acc = 0;
+    if (out < 2 * n_obj) {
+      for (int64_t i = b0 + threadIdx.x; i < b1; i += 256) acc += per_example[i * 2 * n_obj + out];
+    } else if (rank) {
+      for (int64_t i = b0 + threadIdx.x; i < b1; i += 256) acc += rank[i];
+    }
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+      if (static_cast<int>(threadIdx.x) < w) part[threadIdx.x] += part[threadIdx.x + w];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) partials[static_cast<int64_t>(blockIdx.x) * outs + out] = part[0];
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    if (out < 2 * n_obj) sums[out] = part[0];
-    else if (rank_sum) *rank_sum = part[0];
+}
+
+__global__ void __launch_bounds__(256)
+reduce_final_kernel(const double* __restrict__ partials, int nb, int n_obj,
+                    double* __restrict__ sums, double* __restrict__ rank_sum) {
+  __shared__ double part[256];
+  const int outs = 2 * n_obj + 1;
+  for (int out = 0; out < outs; ++out) {
+    double acc = 0;
+    for (int b = threadIdx.x; b < nb; b += 256) acc += partials[static_cast<int64_t>(b) * outs + out];
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+      if (static_cast<int>(threadIdx.x) < w) part[threadIdx.x] += part[threadIdx.x + w];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      if (out < 2 * n_obj) sums[out] = part[0];
+      else if (rank_sum) *rank_sum = part[0];
+    }
+    __syncthreads();
   }
 }
 
@@ -902,15 +931,28 @@ regularizer_kernel(const D* __restrict__ W, const D* __restrict__ W0, int64_t co
   }
 }
 
-__global__ void regularizer_final(const double* __restrict__ partials, int nb, double* out) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) {
-    double a0 = 0, a1 = 0;
-    for (int b = 0; b < nb; ++b) {
-      a0 += partials[2 * b];
-      a1 += partials[2 * b + 1];
+// Sums the per-workgroup partials in a fixed strided order and LDS tree.
+__global__ void __launch_bounds__(256)
+regularizer_final(const double* __restrict__ partials, int nb, double* out) {
+  __shared__ double p0[256], p1[256];
+  double a0 = 0, a1 = 0;
+  for (int b = threadIdx.x; b < nb; b += 256) {
+    a0 += partials[2 * b];
+    a1 += partials[2 * b + 1];
+  }
+  p0[threadIdx.x] = a0;
+  p1[threadIdx.x] = a1;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) {
+      p0[threadIdx.x] += p0[threadIdx.x + w];
+      p1[threadIdx.x] += p1[threadIdx.x + w];
     }
-    out[0] = 0.5 * a0;
-    out[1] = a1;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[0] = 0.5 * p0[0];
+    out[1] = p1[0];
   }
 }
 
@@ -1006,11 +1048,24 @@ hipError_t launch_eval_slow(const EvalLaunch& a) {
   return hipErrorInvalidValue;
 }
 
+int64_t eval_reduce_scratch(int n_obj) {
+  return static_cast<int64_t>(kReduceBlocks) * (2 * n_obj + 1);
+}
+
 hipError_t launch_eval_reduce(const EvalLaunch& a, double* sums, double* rank_sum,
-                              unsigned long long* hist) {
-  hipLaunchKernelGGL(reduce_kernel, dim3(2 * a.objs.n + 1), dim3(256), 0, a.stream,
-                     a.per_example, a.n, a.objs.n, a.rank, sums, rank_sum);
+                              unsigned long long* hist, double* partials) {
+  const int64_t chunk_min = 2048;
+  int64_t nb = (a.n + chunk_min - 1) / chunk_min;
+  if (nb > kReduceBlocks) nb = kReduceBlocks;
+  if (nb < 1) nb = 1;
+  const int64_t chunk = (a.n + nb - 1) / nb;
+  hipLaunchKernelGGL(reduce_partial_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream,
+                     a.per_example, a.n, a.objs.n, a.rank, chunk, partials);
   hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(256), 0, a.stream, partials,
+                     static_cast<int>(nb), a.objs.n, sums, rank_sum);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (hist && a.counts) {
     hipLaunchKernelGGL(zero_u64_kernel, dim3(static_cast<unsigned>((a.m + 255) / 256)), dim3(256), 0,
@@ -1042,7 +1097,7 @@ hipError_t launch_regularizer(int data, const void* W, const void* W0, int64_t c
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(regularizer_final, dim3(1), dim3(64), 0, stream, partials,
+  hipLaunchKernelGGL(regularizer_final, dim3(1), dim3(256), 0, stream, partials,
                      static_cast<int>(blocks), out);
   return hipGetLastError();
 }

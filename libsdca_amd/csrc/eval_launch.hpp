@@ -52,9 +52,11 @@ hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, i
 hipError_t launch_eval_epilogue(const EvalLaunch& a);
 hipError_t launch_eval_slow(const EvalLaunch& a);
 // Deterministic reductions: sums[o*2+{0,1}] = sum_i per_example; rank sum;
-// hist[c] = #{i: counts[i] == c}.
+// hist[c] = #{i: counts[i] == c}.  `partials` holds eval_reduce_scratch(n_obj)
+// doubles.
+int64_t eval_reduce_scratch(int n_obj);
 hipError_t launch_eval_reduce(const EvalLaunch& a, double* sums, double* rank_sum,
-                              unsigned long long* hist);
+                              unsigned long long* hist, double* partials);
 // 0.5 <W, W> and <W0, W> in double (out[0], out[1]); `partials` holds 1024 doubles.
 hipError_t launch_regularizer(int data, const void* W, const void* W0, int64_t count,
                               double* partials, double* out, hipStream_t stream);
