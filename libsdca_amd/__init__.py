@@ -155,6 +155,51 @@ def _dtype_code(x):
     return {np.dtype(np.float32): F32, np.dtype(np.float64): F64}.get(x.dtype, -1)
 
 
+def _need(x, name, shape, like):
+    """Checks that x can be handed to the C ABI beside `like`: the same kind
+    (numpy array, or tensor on like's device), like's element type, the given
+    shape, contiguous.  The library reads and writes through raw pointers, so
+    a mismatch here would otherwise become an out-of-bounds access."""
+    if x is None:
+        return
+    if _is_torch(x) != _is_torch(like):
+        raise SdcaError(2, f"{name}: numpy arrays and torch tensors cannot be mixed in one call")
+    if _is_torch(x):
+        if x.device != like.device:
+            raise SdcaError(2, f"{name} is on {x.device}, expected {like.device}")
+        contiguous = x.is_contiguous()
+    else:
+        contiguous = x.flags.c_contiguous
+    if x.dtype != like.dtype:
+        raise SdcaError(3, f"{name} has element type {x.dtype}, expected {like.dtype}")
+    if tuple(int(v) for v in x.shape) != tuple(shape):
+        raise SdcaError(2, f"{name} has shape {tuple(x.shape)}, expected {tuple(shape)}")
+    if not contiguous:
+        raise SdcaError(2, f"{name} must be contiguous")
+
+
+def _label_arrays(labels, offsets, n, like):
+    """int64 label (and CSR offset) arrays of the kind of `like`, with the
+    lengths the C ABI reads: n labels, or n + 1 offsets and offsets[n] labels."""
+    if _is_torch(like):
+        import torch
+        lab = torch.as_tensor(labels, dtype=torch.int64, device=like.device).contiguous().reshape(-1)
+        off = None if offsets is None else torch.as_tensor(
+            offsets, dtype=torch.int64, device=like.device).contiguous().reshape(-1)
+    else:
+        lab = np.ascontiguousarray(labels, dtype=np.int64).reshape(-1)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64).reshape(-1)
+    if off is None:
+        if lab.shape[0] != n:
+            raise SdcaError(8, f"{lab.shape[0]} labels for {n} examples")
+    else:
+        if off.shape[0] != n + 1:
+            raise SdcaError(8, f"{off.shape[0]} offsets for {n} examples (need n + 1)")
+        if int(off[-1]) != lab.shape[0]:
+            raise SdcaError(8, f"offsets end at {int(off[-1])} but {lab.shape[0]} labels are given")
+    return lab, off
+
+
 def _stream_ptr():
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -175,28 +220,36 @@ def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
                                         "long double": LONG_DOUBLE}.get(result, result))
     if A.ndim == 1:
         A = A.reshape(1, -1)
+        if out is not None:
+            out = out.reshape(1, -1)
+    if A.ndim != 2:
+        raise SdcaError(2, f"A must be 1-D or 2-D (got {A.ndim} dimensions)")
     n, m = int(A.shape[0]), int(A.shape[1])
     if out is None:
         out = A
+    _need(A, "A", (n, m), A)
+    _need(out, "out", (n, m), A)
     params = ProxParams(lo, hi, rhs, rho, alpha, int(k), int(p))
     nthr = 2 * n if code in (OPS["two_simplex"], OPS["two_simplex_sort"],
                              OPS["two_entropy"]) else n
     if _is_torch(A):
         import torch
-        if not A.is_cuda or not A.is_contiguous() or not out.is_contiguous():
-            raise SdcaError(2, "torch inputs must be contiguous CUDA tensors")
+        if not A.is_cuda:
+            raise SdcaError(2, "torch inputs must be CUDA tensors")
         thr = torch.zeros((nthr, 3), dtype=torch.float64, device=A.device) if thresholds else None
         cp = None
         if col_p is not None:
-            cp = torch.as_tensor(col_p, dtype=torch.int64, device=A.device).contiguous()
+            cp = torch.as_tensor(col_p, dtype=torch.int64, device=A.device).contiguous().reshape(-1)
+            if cp.shape[0] != n:
+                raise SdcaError(2, f"col_p has {cp.shape[0]} entries for {n} columns")
         check(lib.sdca_prox(code, data, res, m, n, A.data_ptr(), out.data_ptr(),
                             ctypes.byref(params), cp.data_ptr() if cp is not None else None,
                             thr.data_ptr() if thr is not None else None, 0, _stream_ptr()))
         return (out, thr) if thresholds else out
-    if not A.flags.c_contiguous or not out.flags.c_contiguous:
-        raise SdcaError(2, "numpy inputs must be C-contiguous")
     thr = np.zeros((nthr, 3), dtype=np.float64) if thresholds else None
-    cp = None if col_p is None else np.ascontiguousarray(col_p, dtype=np.int64)
+    cp = None if col_p is None else np.ascontiguousarray(col_p, dtype=np.int64).reshape(-1)
+    if cp is not None and cp.shape[0] != n:
+        raise SdcaError(2, f"col_p has {cp.shape[0]} entries for {n} columns")
     check(lib.sdca_prox(code, data, res, m, n, A.ctypes.data, out.ctypes.data,
                         ctypes.byref(params), cp.ctypes.data if cp is not None else None,
                         thr.ctypes.data if thr is not None else None, HOST_PTR, None))
@@ -301,6 +354,9 @@ def scores(X, W, out=None):
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(W.shape[0])
     data = _dtype_code(X)
+    _need(X, "X", (n, d), X)
+    _need(W, "W", (m, d), X)
+    _need(out, "out", (n, m), X)
     if _is_torch(X):
         import torch
         S = out if out is not None else torch.empty((n, m), dtype=X.dtype, device=X.device)
@@ -323,6 +379,10 @@ def recompute_primal(X, A, W0=None, out=None):
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(A.shape[1])
     data = _dtype_code(X)
+    _need(X, "X", (n, d), X)
+    _need(A, "A", (n, m), X)
+    _need(W0, "W0", (m, d), X)
+    _need(out, "out", (m, d), X)
     lib.sdca_recompute_primal.restype = ctypes.c_int
     if _is_torch(X):
         import torch
@@ -351,17 +411,14 @@ def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_exampl
     recs = (EvalRecord * len(objs))()
     acc = np.zeros(m, dtype=np.float64)
     pe = None
+    lab, off = _label_arrays(labels, offsets, n, lead_args[0])
     if torch_mode:
         import torch
         dev = lead_args[0].device
-        lab = torch.as_tensor(labels, dtype=torch.int64, device=dev).contiguous()
-        off = None if offsets is None else torch.as_tensor(offsets, dtype=torch.int64, device=dev).contiguous()
         if per_example:
             pe = torch.zeros((n, len(objs), 2), dtype=torch.float64, device=dev)
         flags, stream = 0, _stream_ptr()
     else:
-        lab = np.ascontiguousarray(labels, dtype=np.int64)
-        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
         if per_example:
             pe = np.zeros((n, len(objs), 2), dtype=np.float64)
         flags, stream = HOST_PTR, None
@@ -390,6 +447,10 @@ def eval_features(objs, X, W, labels, A=None, W0=None, offsets=None, result=None
     accuracy / rank loss only)."""
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(W.shape[0])
+    _need(X, "X", (n, d), X)
+    _need(W, "W", (m, d), X)
+    _need(A, "A", (n, m), X)
+    _need(W0, "W0", (m, d), X)
     lead = (X, [ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
                 ctypes.c_void_p(_ptr(X)), ctypes.c_void_p(_ptr(W))])
     return _eval("sdca_eval_features", objs, lead, m, n, labels, offsets, A, result, per_example,
@@ -405,6 +466,8 @@ def eval_kernel(objs, K, A, labels, offsets=None, result=None, per_example=False
     records."""
     n, n_train = int(K.shape[0]), int(K.shape[1])
     m = int(A.shape[1])
+    _need(K, "K", (n, n_train), K)
+    _need(A, "A", (n_train, m), K)
     lead = (K, [ctypes.c_int64(n_train), ctypes.c_int64(m), ctypes.c_int64(n),
                 ctypes.c_void_p(_ptr(K))])
     return _eval("sdca_eval_kernel", objs, lead, m, n, labels, offsets, A, result, per_example,
@@ -415,22 +478,20 @@ def eval_scores(objs, S, labels, A=None, offsets=None, primal_regularizer=0.0,
                 dual_regularizer=0.0, result=None, per_example=False):
     """The per-example part of evaluate_dataset on precomputed scores S."""
     n, m = int(S.shape[0]), int(S.shape[1])
-    lead = (S, [ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(_ptr(S))])
+    _need(S, "S", (n, m), S)
+    _need(A, "A", (n, m), S)
     lib = library()
     res = _dtype_code(S) if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
     torch_mode = _is_torch(S)
     objarr = _objs(objs)
     recs = (EvalRecord * len(objs))()
     acc = np.zeros(m, dtype=np.float64)
+    lab, off = _label_arrays(labels, offsets, n, S)
     if torch_mode:
         import torch
-        lab = torch.as_tensor(labels, dtype=torch.int64, device=S.device).contiguous()
-        off = None if offsets is None else torch.as_tensor(offsets, dtype=torch.int64, device=S.device).contiguous()
         pe = torch.zeros((n, len(objs), 2), dtype=torch.float64, device=S.device) if per_example else None
         flags, stream = 0, _stream_ptr()
     else:
-        lab = np.ascontiguousarray(labels, dtype=np.int64)
-        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
         pe = np.zeros((n, len(objs), 2), dtype=np.float64) if per_example else None
         flags, stream = HOST_PTR, None
     lib.sdca_eval_scores.restype = ctypes.c_int

@@ -1,7 +1,7 @@
 // C ABI of the MI355X batched prox + evaluation path (include/sdca_hip.h):
 // argument validation with the Matlab front end's rules
 // (src/matlab/mex_prox.cpp:132-136), host staging for SDCA_HOST_PTR, the
-// per-(device, stream) workspace cache and the kernel dispatch.
+// per-(device, stream, host thread) workspace cache and the kernel dispatch.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -11,6 +11,8 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
+#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -46,9 +48,13 @@ int hip_fail(hipError_t e, const char* what) {
 
 size_t dtype_size(int dt) { return dt == SDCA_F32 ? 4 : 8; }
 
-// Device scratch, one set per (device, stream) so that concurrent streams
-// never share it.  Buffers only grow; growth frees the old buffer after the
-// device is idle (hipFree synchronises).
+// Device scratch, one set per (device, stream, host thread): concurrent
+// streams never share it, and neither do host threads that enqueue on the
+// same stream (growing a shared set could free a buffer that another
+// thread's call has taken but not yet launched on).  Buffers only grow;
+// growth frees the old buffer after the stream is idle.  A stream under
+// graph capture cannot grow it (the wait and the allocation are not
+// capturable): warm the stream up with one call of the same size first.
 struct Workspace {
   void* ptr[4] = {nullptr, nullptr, nullptr, nullptr};
   size_t cap[4] = {0, 0, 0, 0};
@@ -58,7 +64,7 @@ struct Workspace {
 };
 
 std::mutex g_ws_mutex;
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::map<std::tuple<int, hipStream_t, std::thread::id>, Workspace> g_ws;
 
 // Returns slot `slot` of the calling stream's workspace with at least `bytes`
 // (and, with `ws`, the stream's workspace record).
@@ -66,9 +72,15 @@ int workspace(hipStream_t stream, int slot, size_t bytes, void** out, Workspace*
   int dev = 0;
   SDCA_HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  Workspace& w = g_ws[std::make_pair(dev, stream)];
+  Workspace& w = g_ws[std::make_tuple(dev, stream, std::this_thread::get_id())];
   if (ws) *ws = &w;
   if (w.cap[slot] < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    SDCA_HIP_TRY(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(SDCA_ERR_HIP,
+                  "the stream is being captured and its scratch must grow to %zu bytes: run the "
+                  "call once on this stream before the capture", bytes);
     if (slot == 0) w.list_zeroed = false;
     if (w.ptr[slot]) {
       SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
@@ -412,7 +424,8 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   const size_t pe_bytes = static_cast<size_t>(n) * n_obj * 2 * sizeof(double);
   const size_t cnt_bytes = static_cast<size_t>(n) * sizeof(int);
   const size_t rank_bytes = static_cast<size_t>(n) * sizeof(double);
-  const size_t slow_bytes = (1 + 2 * static_cast<size_t>(n) * n_obj) * sizeof(int);
+  // [label-check flag, deferred count, (example, objective) pairs]
+  const size_t slow_bytes = (2 + 2 * static_cast<size_t>(n) * n_obj) * sizeof(int);
   const size_t sums_bytes = (2 * kMaxObjectives + 2) * sizeof(double);
   const size_t hist_bytes = static_cast<size_t>(m) * sizeof(unsigned long long);
   const size_t reg_bytes = (2 * 512 + 2) * sizeof(double);
@@ -429,7 +442,9 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   double* d_pe = reinterpret_cast<double*>(p); p += align(pe_bytes);
   int* d_cnt = reinterpret_cast<int*>(p); p += align(cnt_bytes);
   double* d_rank = reinterpret_cast<double*>(p); p += align(rank_bytes);
-  int* d_slow = reinterpret_cast<int*>(p); p += align(slow_bytes);
+  int* d_bad = reinterpret_cast<int*>(p);  // label check of the epilogue kernels
+  int* d_slow = d_bad + 1;
+  p += align(slow_bytes);
   double* d_sums = reinterpret_cast<double*>(p); p += align(sums_bytes);
   unsigned long long* d_hist = reinterpret_cast<unsigned long long*>(p); p += align(hist_bytes);
   double* d_reg = reinterpret_cast<double*>(p); p += align(reg_bytes);
@@ -457,8 +472,9 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   a.counts = multilabel ? nullptr : d_cnt;
   a.rank = multilabel ? d_rank : nullptr;
   a.slow = d_slow;
+  a.bad = d_bad;
   a.stream = stream;
-  SDCA_HIP_TRY(launch_clear(d_slow, 1, stream), "clear kernel");
+  SDCA_HIP_TRY(launch_clear(d_bad, 2, stream), "clear kernel");  // flag and deferred count
   SDCA_HIP_TRY(launch_eval_epilogue(a), "evaluation epilogue kernel");
   if (!multilabel) SDCA_HIP_TRY(launch_eval_slow(a), "evaluation epilogue (deferred examples)");
   SDCA_HIP_TRY(launch_eval_reduce(a, d_sums, multilabel ? d_sums + 2 * kMaxObjectives : nullptr,
@@ -479,6 +495,9 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
                  "hipMemcpyAsync(D2H)");
   if (dW) SDCA_HIP_TRY(hipMemcpyAsync(reg.data(), d_reg, 2 * sizeof(double), hipMemcpyDeviceToHost,
                                       stream), "hipMemcpyAsync(D2H)");
+  int bad_labels = 0;
+  SDCA_HIP_TRY(hipMemcpyAsync(&bad_labels, d_bad, sizeof(int), hipMemcpyDeviceToHost, stream),
+               "hipMemcpyAsync(D2H)");
   double dual_reg = 0;
   if (dA_reg) SDCA_HIP_TRY(hipMemcpyAsync(&dual_reg, d_dreg + n, sizeof(double),
                                           hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
@@ -488,6 +507,11 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
                                 stream), "hipMemcpyAsync(per_example)");
   }
   SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  if (bad_labels)
+    return fail(SDCA_ERR_LABELS,
+                multilabel ? "invalid labels or offsets: the first offset must be 0, and every "
+                             "example needs 1 to m - 1 distinct, sorted labels in [0, m)"
+                           : "a label is outside [0, m)");
 
   // eval_end: primal_loss *= coeff; primal = loss + reg; dual = loss - reg;
   // accuracy = partial_sum(hist) / n; rank_loss /= n (eval/core.h:43-95).

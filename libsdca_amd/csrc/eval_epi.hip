@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(64)
 eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
                        const int64_t* __restrict__ labels, int64_t m64, int64_t n, EvalObjs objs,
                        double* __restrict__ per_example, int* __restrict__ counts,
-                       int* __restrict__ slow) {
+                       int* __restrict__ slow, int* __restrict__ bad) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* lds = reinterpret_cast<D*>(smem_raw);
   constexpr int B = 64 / G;
@@ -220,7 +220,13 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
   D* const lds_dummy = lds + B * m + threadIdx.x;
 
   const D* srow = S + ii * m64;
-  const int y = static_cast<int>(labels[ii]);
+  // Device-resident labels reach the kernel unchecked: a label outside
+  // [0, m) raises *bad (the call then fails with the reference's label
+  // error, data/output.h:169-182) and is read as 0, so no load leaves the row.
+  const int64_t yl = labels[ii];
+  const bool bad_y = yl < 0 || yl >= m64;
+  if (active && bad_y && g == 0) bad[0] = 1;
+  const int y = bad_y ? 0 : static_cast<int>(yl);
   const D sy = srow[y];
   const int nvalid = (m - g + G - 1) / G;
   D s[C];
@@ -493,7 +499,7 @@ __global__ void __launch_bounds__(64)
 eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
                        const int64_t* __restrict__ labels, const int64_t* __restrict__ offsets,
                        int64_t m64, int64_t n, EvalObjs objs, double* __restrict__ per_example,
-                       double* __restrict__ rank) {
+                       double* __restrict__ rank, int* __restrict__ bad) {
   constexpr int B = 64 / G;
   const int m = static_cast<int>(m64);
   const int lc = static_cast<int>(threadIdx.x) / G;
@@ -501,8 +507,26 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
   const int64_t i = static_cast<int64_t>(blockIdx.x) * B + lc;
   const bool active = i < n;
   const int64_t ii = active ? i : 0;
+  // The CSR rules of data/output.h:185-208, checked here for device-resident
+  // labels: the first offset is 0, the labels of an example lie inside
+  // [0, offsets[n]) with 1..m-1 of them, sorted, distinct and in [0, m).  An
+  // example that breaks them raises *bad and is evaluated as the valid
+  // example {label 0}, so that no load leaves the label array.
   const int64_t off0 = offsets[ii];
-  const int p = static_cast<int>(offsets[ii + 1] - off0);
+  const int64_t off1 = offsets[ii + 1];
+  bool ok = off0 >= 0 && (ii > 0 || off0 == 0) && off1 <= offsets[n] && off1 - off0 >= 1 &&
+            off1 - off0 <= m64 - 1;
+  if (ok) {
+    int64_t prev = -1;
+    for (int64_t q = off0; q < off1; ++q) {
+      const int64_t lab = labels[q];
+      ok = ok && lab > prev && lab < m64;
+      prev = lab;
+    }
+  }
+  if (active && !ok && g == 0) bad[0] = 1;
+  const int p = ok ? static_cast<int>(off1 - off0) : 1;
+  auto label_at = [&](int q) -> int { return ok ? static_cast<int>(labels[off0 + q]) : 0; };
   const int nvalid = (m - g + G - 1) / G;
   const D* srow = S + ii * m64;
   D s[C];
@@ -513,14 +537,14 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
     pos[c] = false;
   }
   for (int q = 0; q < p; ++q) {
-    const int lab = static_cast<int>(labels[off0 + q]);
+    const int lab = label_at(q);
 #pragma unroll
     for (int c = 0; c < C; ++c) pos[c] = pos[c] || (g + G * c == lab);
   }
   // Rank loss (eval/primal.h:70-79): for each positive, the negatives >= it.
   R rl = 0;
   for (int q = 0; q < p; ++q) {
-    const int lab = static_cast<int>(labels[off0 + q]);
+    const int lab = label_at(q);
     const D sp = srow[lab];
     int cn = 0;
 #pragma unroll
@@ -750,7 +774,8 @@ eval_slow_kernel(const D* __restrict__ S, const int64_t* __restrict__ labels, in
     const int64_t i = slow[1 + 2 * w];
     const int o = slow[2 + 2 * w];
     const D* srow = S + i * m64;
-    const int y = static_cast<int>(labels[i]);
+    const int64_t yl = labels[i];
+    const int y = (yl < 0 || yl >= m64) ? 0 : static_cast<int>(yl);  // flagged by the epilogue
     const D shift1 = D(1) - srow[y];
     // h over j != y, compacted: positions after y move down by one.
     for (int q = threadIdx.x; q < pow2; q += blockDim.x) {
@@ -792,7 +817,7 @@ hipError_t launch_mc(const EvalLaunch& a) {
   hipLaunchKernelGGL((eval_multiclass_kernel<G, C, KM, D, R>), dim3(static_cast<unsigned>(blocks)),
                      dim3(64), shmem, a.stream, static_cast<const D*>(a.S),
                      static_cast<const D*>(a.A), a.labels, a.m, a.n, a.objs, a.per_example,
-                     a.counts, a.slow);
+                     a.counts, a.slow, a.bad);
   return hipGetLastError();
 }
 
@@ -802,7 +827,7 @@ hipError_t launch_ml(const EvalLaunch& a) {
   const int64_t blocks = (a.n + B - 1) / B;
   hipLaunchKernelGGL((eval_multilabel_kernel<G, C, D, R>), dim3(static_cast<unsigned>(blocks)),
                      dim3(64), 0, a.stream, static_cast<const D*>(a.S), static_cast<const D*>(a.A),
-                     a.labels, a.offsets, a.m, a.n, a.objs, a.per_example, a.rank);
+                     a.labels, a.offsets, a.m, a.n, a.objs, a.per_example, a.rank, a.bad);
   return hipGetLastError();
 }
 

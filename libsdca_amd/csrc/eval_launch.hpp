@@ -39,6 +39,7 @@ struct EvalLaunch {
   int* counts;             // device: n (multiclass top-k counts), or NULL
   double* rank;            // device: n (multilabel rank loss per example), or NULL
   int* slow;               // device: [0] = count, then (example, objective) pairs
+  int* bad;                // device: set to 1 by an example with invalid labels
   hipStream_t stream;
 };
 

@@ -156,3 +156,45 @@ def test_cpp_header_compiles_and_links(tmp_path):
            "-Wl,--allow-shlib-undefined"]
     out = subprocess.run(cmd, capture_output=True, text=True)
     assert out.returncode == 0, out.stderr
+
+
+def test_wrapper_shape_and_type_checks():
+    """The Python layer hands raw pointers to the C ABI: arrays whose shape,
+    element type or layout does not match are refused before any call."""
+    import libsdca_amd as sd
+    x = np.zeros((3, 5), np.float32)
+    bad_out = [np.zeros((3, 4), np.float32), np.zeros((3, 5), np.float64),
+               np.zeros((5, 3), np.float32).T]
+    for out in bad_out:
+        with pytest.raises(sd.SdcaError):
+            sd.prox("topk_simplex", x, out=out, k=2)
+    with pytest.raises(sd.SdcaError):
+        sd.prox("two_simplex", x, col_p=[1, 2], p=1)  # one entry per column
+    X = np.zeros((4, 3), np.float32)
+    W = np.zeros((5, 3), np.float32)
+    obj = [sd.objective("l2_entropy")]
+    for kw in (dict(W=np.zeros((5, 2), np.float32)), dict(W=np.zeros((5, 3), np.float64)),
+               dict(A=np.zeros((4, 4), np.float32)), dict(W0=np.zeros((4, 3), np.float32))):
+        args = dict(W=W, A=None, W0=None)
+        args.update(kw)
+        with pytest.raises(sd.SdcaError):
+            sd.eval_features(obj, X, args["W"], [0, 1, 2, 3], A=args["A"], W0=args["W0"])
+    with pytest.raises(sd.SdcaError) as e:
+        sd.eval_features(obj, X, W, [0, 1, 2])  # one label short
+    assert e.value.status == 8
+    ml = [sd.objective("l2_multilabel_entropy")]
+    with pytest.raises(sd.SdcaError) as e:
+        sd.eval_features(ml, X, W, [0, 1, 2, 3, 4], offsets=[0, 2, 3, 4])  # n + 1 offsets needed
+    assert e.value.status == 8
+    with pytest.raises(sd.SdcaError) as e:
+        sd.eval_features(ml, X, W, [0, 1, 2, 3, 4], offsets=[0, 2, 3, 4, 6])  # ends past the labels
+    assert e.value.status == 8
+    with pytest.raises(sd.SdcaError):
+        sd.eval_kernel(obj, np.zeros((4, 4), np.float32), np.zeros((3, 5), np.float32), [0, 1, 2, 3])
+    with pytest.raises(sd.SdcaError):
+        sd.scores(X, np.zeros((5, 4), np.float32))
+    with pytest.raises(sd.SdcaError):
+        sd.recompute_primal(X, np.zeros((3, 5), np.float32))
+    torch = pytest.importorskip("torch")
+    with pytest.raises(sd.SdcaError):
+        sd.scores(X, torch.zeros((5, 3)))  # numpy and torch mixed

@@ -348,3 +348,58 @@ def test_recompute_primal(cuda, dtype, n, m, d, with_w0):
     if dtype == np.float32 and n == 517:
         Wh = sd.recompute_primal(X, A, W0)  # host pointers through the staging
         assert np.array_equal(Wh, W)
+
+
+@pytest.mark.parametrize("m", [10, 300])
+def test_device_labels_are_checked(cuda, m):
+    """Device-resident labels are not visible to the host checks: the
+    epilogue kernels check them (data/output.h:169-208) and the call fails
+    with the label status instead of reading outside the score rows."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(m)
+    n = 700
+    S = torch.from_numpy((rng.standard_normal((n, m)) * 2).astype(np.float32)).to(cuda)
+    y = rng.integers(0, m, n)
+    good, _, _ = sd.eval_scores(MC_OBJS, S, torch.from_numpy(y).to(cuda))
+    for at, v in [(0, m), (n // 2, -1), (n - 1, m + 1000), (n - 1, 2**40)]:
+        yb = y.copy()
+        yb[at] = v
+        with pytest.raises(sd.SdcaError) as e:
+            sd.eval_scores(MC_OBJS, S, torch.from_numpy(yb).to(cuda))
+        assert e.value.status == 8, (at, v)
+        again, _, _ = sd.eval_scores(MC_OBJS, S, torch.from_numpy(y).to(cuda))
+        assert again == good
+
+
+def test_device_multilabel_offsets_are_checked(cuda):
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(5)
+    n, m = 400, 20
+    S = torch.from_numpy((rng.standard_normal((n, m)) * 2).astype(np.float32)).to(cuda)
+    lab, off = multilabel_labels(rng, n, m)
+    good, _, _ = sd.eval_scores(ML_OBJS, S, torch.from_numpy(lab).to(cuda),
+                                offsets=torch.from_numpy(off).to(cuda))
+    p0 = int(off[1] - off[0])
+    cases = []
+    bl = lab.copy(); bl[0] = m; cases.append(("label >= m", bl, off))  # noqa: E702
+    bl = lab.copy(); bl[-1] = -3; cases.append(("negative label", bl, off))  # noqa: E702
+    i = int(np.argmax(np.diff(off) >= 2))
+    bl = lab.copy(); bl[off[i]], bl[off[i] + 1] = bl[off[i] + 1], bl[off[i]]  # noqa: E702
+    cases.append(("unsorted", bl, off))
+    bl = lab.copy(); bl[off[i] + 1] = bl[off[i]]; cases.append(("repeated", bl, off))  # noqa: E702
+    bo = off.copy(); bo[1] = bo[0]; cases.append(("example without labels", lab, bo))  # noqa: E702
+    bo = off.copy(); bo[1] = bo[2] + 7; cases.append(("offsets decrease", lab, bo))  # noqa: E702
+    bo = off.copy(); bo[0] = 1 if p0 >= 2 else -1; cases.append(("first offset", lab, bo))  # noqa: E702
+    many = np.arange(m, dtype=np.int64)
+    cases.append(("m labels", np.concatenate([many, lab[off[1]:]]),
+                  np.concatenate([[0], off[1:] - off[1] + m])))
+    for what, bl, bo in cases:
+        with pytest.raises(sd.SdcaError) as e:
+            sd.eval_scores(ML_OBJS, S, torch.from_numpy(bl).to(cuda),
+                           offsets=torch.from_numpy(bo).to(cuda))
+        assert e.value.status == 8, what
+    again, _, _ = sd.eval_scores(ML_OBJS, S, torch.from_numpy(lab).to(cuda),
+                                 offsets=torch.from_numpy(off).to(cuda))
+    assert again == good

@@ -59,3 +59,68 @@ def test_prox_graph_replays_match_eager(cuda, op, kw, m):
         sd.prox(op, xs[0], out=tmp, **kw)
         torch.cuda.synchronize()
         assert torch.equal(tmp, eager[0])
+
+
+def test_capture_on_a_cold_stream_is_refused(cuda):
+    """Scratch cannot grow inside a capture (its wait and allocation are not
+    capturable); the call says so instead of invalidating the capture."""
+    import torch
+    import libsdca_amd as sd
+    x = torch.from_numpy(inputs.mixed_signs(4096, 100, np.float32, 310, -2, 2)).to(cuda)
+    o = torch.empty_like(x)
+    gs = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(sd.SdcaError, match="captured"):
+        with torch.cuda.graph(g, stream=gs):
+            sd.prox("topk_simplex", x, out=o, k=5, rhs=1.0)
+    torch.cuda.synchronize()
+    sd.prox("topk_simplex", x, out=o, k=5, rhs=1.0)  # the library still works afterwards
+    ref = torch.empty_like(x)
+    sd.prox("topk_simplex", x, out=ref, k=5, rhs=1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)
+
+
+def test_host_threads_sharing_a_stream(cuda):
+    """Two host threads that enqueue on one stream, each growing its scratch,
+    give what one thread gives: each thread has its own scratch, so a
+    growth never frees a buffer the other thread's call is about to use."""
+    import threading
+    import torch
+    import libsdca_amd as sd
+    sizes = [1000, 8000, 30000, 120000]
+    xs = [torch.from_numpy(inputs.mixed_signs(n, 100, np.float32, 320 + i, -2, 2)).to(cuda)
+          for i, n in enumerate(sizes)]
+    expect = []
+    for x in xs:
+        o = torch.empty_like(x)
+        sd.prox("topk_cone", x, out=o, k=5)
+        expect.append(o)
+    torch.cuda.synchronize()
+    got = {}
+    errors = []
+
+    def worker(t):
+        try:
+            torch.cuda.set_device(cuda)
+            order = sizes if t == 0 else sizes[::-1]
+            outs = []
+            for n in order:
+                i = sizes.index(n)
+                o = torch.empty_like(xs[i])
+                sd.prox("topk_cone", xs[i], out=o, k=5)
+                outs.append((i, o))
+            got[t] = outs
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for t in range(2):
+        for i, o in got[t]:
+            assert torch.equal(o, expect[i]), f"thread {t}, size {sizes[i]}"
