@@ -103,12 +103,36 @@ struct KnapState {
 // false for NaN, so a slot costs two compares and the fixing of a set is one
 // select.  The low and high counts travel in one integer (n_lo + 2^16 n_hi;
 // at most m <= 2048 each) through the group sum.
-template <int G, int C, class D, class R>
+//
+// WL: the working copy lives in the column's own LDS slots (wl = the lane's
+// first slot, slot c at wl[G c]; padding slots are neither read nor written,
+// their stores go to the lane's dummy word) instead of C more registers.
+// The caller must not need the LDS copy of the column afterwards.
+template <int G, int C, class D, class R, bool WL = false>
 __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nvalid, R total,
                                                 R lo, R hi, R rhs, R hi_cut0 = num<R>::inf(),
-                                                int n_u0 = 0, R sum_u0 = 0) {
+                                                int n_u0 = 0, R sum_u0 = 0, D* wl = nullptr,
+                                                D* wl_dummy = nullptr) {
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   const R qnan = num<R>::quiet_nan();
+  R w[WL ? 1 : C];
+  constexpr int UW = WL ? 1 : C;  // the LDS loops stay rolled (their registers are the point)
+  auto get = [&](int c) -> R {
+    if constexpr (WL) {
+      const R x = static_cast<R>(wl[G * c]);
+      return c < nvalid ? x : qnan;
+    } else {
+      return w[c];
+    }
+  };
+  auto put = [&](int c, R x) {
+    if constexpr (WL) {
+      D* dst = c < nvalid ? wl + G * c : wl_dummy;
+      *dst = static_cast<D>(x);
+    } else {
+      w[c] = x;
+    }
+  };
   int mc = m - n_u0;
   R t = div_near(total - sum_u0 - rhs + static_cast<R>(n_u0) * hi, static_cast<R>(mc));
   KnapState<R> st;
@@ -118,22 +142,22 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
   st.c_hi = num<R>::inf();
   st.n_u = n_u0;
   st.sum_u = sum_u0;
-  R w[C];
-#pragma unroll
+#pragma unroll UW
   for (int c = 0; c < C; ++c) {
     const R x = static_cast<R>(v[c]);
-    w[c] = (x > -num<R>::inf() && !(x > hi_cut0)) ? x : qnan;
+    put(c, (x > -num<R>::inf() && !(x > hi_cut0)) ? x : qnan);
   }
   for (int iter = 0; iter <= m; ++iter) {
     const R c_lo = lo + t, c_hi = hi + t;
     R s_lo = 0, s_hi = 0;
     int n_lh = 0;
-#pragma unroll
+#pragma unroll UW
     for (int c = 0; c < C; ++c) {
-      const bool lo_c = w[c] <= c_lo;
-      const bool hi_c = w[c] > c_hi;
-      s_lo += lo_c ? w[c] : R(0);
-      s_hi += hi_c ? w[c] : R(0);
+      const R wc = get(c);
+      const bool lo_c = wc <= c_lo;
+      const bool hi_c = wc > c_hi;
+      s_lo += lo_c ? wc : R(0);
+      s_hi += hi_c ? wc : R(0);
       n_lh += (lo_c ? 1 : 0) + (hi_c ? 0x10000 : 0);
     }
     s_lo = group_sum<G>(s_lo);
@@ -164,10 +188,11 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
       next = static_cast<R>(mc) * t - s_lo + sl;
       mc -= n_lo;
     }
-#pragma unroll
+#pragma unroll UW
     for (int c = 0; c < C; ++c) {
-      const bool fixed = fix_hi ? (w[c] > c_hi) : (w[c] <= c_lo);
-      w[c] = fixed ? qnan : w[c];
+      const R wc = get(c);
+      const bool fixed = fix_hi ? (wc > c_hi) : (wc <= c_lo);
+      put(c, fixed ? qnan : wc);
     }
     if (mc > 0) {
       t = div_near(next, static_cast<R>(mc));
@@ -489,7 +514,13 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
     }
   }
   const R all = total_sum<G, C, D, R>(v, nvalid);
-  return knapsack_eq_regs<G, C, D, R>(v, m, nvalid, all, R(0), hi, rhs);
+  // The fixing over every slot is rare here (more than G * kCandSlots
+  // candidates): its working copy goes to the column's LDS slots, which keeps
+  // the kernel's register peak at the candidate path's.
+  return knapsack_eq_regs<G, C, D, R, (G > 1)>(v, m, nvalid, all, R(0), hi, rhs,
+                                               num<R>::inf(), 0, R(0),
+                                               lds_col + static_cast<int>(threadIdx.x) % G,
+                                               lds_dummy);
 }
 
 template <int G, int C, int KM, class D, class R>
@@ -1118,6 +1149,9 @@ __device__ inline void tile_store(D* __restrict__ dst, const D* __restrict__ src
 // ---------------------------------------------------------------------------
 template <int FAM, int KM, class D, class R, int G, int C, int BT, bool FULL>
 __global__ void __launch_bounds__(BT)
+#ifdef SDCA_WAVES_PER_EU
+__attribute__((amdgpu_waves_per_eu(SDCA_WAVES_PER_EU)))
+#endif
 prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
                     int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
                     sdca_thresholds* __restrict__ thr, int* __restrict__ slow) {

@@ -127,6 +127,22 @@ def test_topk(cuda, oracle, op, k, m, dtype, result):
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", MS)
+@pytest.mark.parametrize("k,rhs", [(5, 30.0), (2, 7.0), (11, 400.0)])
+def test_topk_simplex_many_candidates(cuda, oracle, k, rhs, m, dtype, result):
+    """A large rhs (hi = rhs / k) makes most of the column candidates for the
+    knapsack: the variable fixing then runs over every slot, with its working
+    copy in the column's LDS slots instead of the candidate registers."""
+    if k > m:
+        pytest.skip("k > m")
+    kw = dict(k=k, rhs=rhs)
+    for name, x in cases(m, dtype, 40 + m + k):
+        got, _ = run_gpu("topk_simplex", x, result, cuda, **kw)
+        parity(oracle, "topk_simplex", x, got, result, f"topk_simplex k={k} rhs={rhs} {name} m={m}",
+               **kw)
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
 @pytest.mark.parametrize("m", [1, 10, 100, 200, 1000, 2048])
 @pytest.mark.parametrize("op,kw", [
     ("entropy", dict(hi=1.0, rhs=1.0)),
