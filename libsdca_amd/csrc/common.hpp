@@ -30,7 +30,51 @@ template <> struct num<double> {
   __device__ __host__ static constexpr double exp_min_arg() { return -0x1.6232bdd7abcd2p+9; }
 };
 
+// e^x in double.  x = k ln2 + r with k = rint(x / ln2), by Cody and Waite's
+// two-constant reduction (ln2 = L1 + L2, L1 holding 32 significant bits so
+// that k L1 is exact for |k| < 2^21); e^r from its Taylor series to degree 13
+// (|r| <= ln2 / 2 leaves a truncation error below 0.05 ulp), by Horner's rule
+// in FMA; 2^k applied by ldexp, which also rounds the subnormal and
+// overflowing results.  Within about 1 ulp of e^x, in 26 vector
+// instructions against the device library's 47 (gfx950).  Clamping x to [-745.5, 709.9] keeps k in
+// range (outside it e^x rounds to 0 or overflows anyway); NaN passes through.
+//
+// a * b + c with the constant c read from a scalar register pair.  Written
+// as fma(), a constant addend is copied into a vector register pair (two
+// moves) before each v_fmac_f64; as an operand of v_fma_f64 it costs two
+// scalar moves instead.
+__device__ inline double fma_sconst(double a, double b, double c) {
+  double d;
+  asm("v_fma_f64 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "s"(c));
+  return d;
+}
+
+__device__ inline double exp_fast(double x) {
+  const double xc = fmin(fmax(x, -745.5), 709.9);
+  const double k = rint(xc * 0x1.71547652b82fep+0);
+  double r = fma(-k, 0x1.62e42fee00000p-1, xc);
+  r = fma(-k, 0x1.a39ef35793c76p-33, r);
+  double p = r * (1.0 / 6227020800.0) + 1.0 / 479001600.0;  // 1 / 13!, 1 / 12!
+  p = fma_sconst(p, r, 1.0 / 39916800.0);
+  p = fma_sconst(p, r, 1.0 / 3628800.0);
+  p = fma_sconst(p, r, 1.0 / 362880.0);
+  p = fma_sconst(p, r, 1.0 / 40320.0);
+  p = fma_sconst(p, r, 1.0 / 5040.0);
+  p = fma_sconst(p, r, 1.0 / 720.0);
+  p = fma_sconst(p, r, 1.0 / 120.0);
+  p = fma_sconst(p, r, 1.0 / 24.0);
+  p = fma_sconst(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  const double y = ldexp(p, static_cast<int>(k));
+  return x != x ? x : y;
+}
+
 __device__ inline float dexp(float x) { return expf(x); }
+// The exp map's kernels keep the device library's exp: with exp_fast the
+// C3-size exp map ran 2 % slower (its time is not in the exponentials),
+// while the Lambert evaluations below gain 2-13 % from it.
 __device__ inline double dexp(double x) { return exp(x); }
 __device__ inline float dlog(float x) { return logf(x); }
 __device__ inline double dlog(double x) { return log(x); }
@@ -139,7 +183,7 @@ __device__ inline double lambert_w_exp(double x) {
     w = exp_approx(x);
     if (br == 3) w = lw_step5(w, exp_approx(x - w));
   }
-  const double e = exp(br == 5 ? x : x - w);
+  const double e = exp_fast(br == 5 ? x : x - w);
   const double r = lw_step5(w, e);
   return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
 }
@@ -165,7 +209,7 @@ __device__ inline double lambert_w_exp_mixed(double x) {
   }
   double w = (br == 4) ? w0 : 0.0;
   if (br == 0 || br == 1 || br == 3) w = lw_step5(w0, y0);
-  const double e = exp(br == 5 ? x : x - w);
+  const double e = exp_fast(br == 5 ? x : x - w);
   const double r = lw_step5(w, e);
   return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
 }

@@ -79,10 +79,11 @@ __device__ inline SetStats<R> knap_sets(const D (&h)[C], const KnapState<R>& st,
 
 // Smooth top-k hinge loss (l2_hinge_topk.h:162-179) of the m' = m - 1 values
 // h (padding and the label's slot hold -inf).  Returns false when the
-// example needs the full topk_cone_search.
+// example needs the full topk_cone_search.  lds_col is the example's row of
+// m words in LDS, used as scratch; nvalid counts the lane's slots inside it.
 template <int G, int C, int KM, class D, class R>
-__device__ inline bool smooth_topk_hinge(const D (&h)[C], int mp, int k, R gamma, D* lds_col,
-                                         D* lds_dummy, R& loss) {
+__device__ inline bool smooth_topk_hinge(const D (&h)[C], int mp, int nvalid, int k, R gamma,
+                                         D* lds_col, D* lds_dummy, R& loss) {
   constexpr int L = KM + 1;
   const R K = static_cast<R>(k);
   const R eps16 = R(16) * num<R>::eps();
@@ -117,8 +118,10 @@ __device__ inline bool smooth_topk_hinge(const D (&h)[C], int mp, int k, R gamma
     return true;
   }
   const R hi = gamma / K;
-  KnapState<R> st = topk_knapsack<G, C, L, D, R>(h, top, mp, C, kth, hi, gamma, lds_col,
-                                                  lds_dummy);
+  // Scores of an untrained model put every h within hi of the k-th largest:
+  // the fixing over all slots is common here and stays in registers.
+  KnapState<R> st = topk_knapsack<G, C, L, D, R, false>(h, top, mp, nvalid, kth, hi, gamma,
+                                                         lds_col, lds_dummy);
   if (!constant) {
     bool lt;
     if (st.n_u == 0) {
@@ -291,7 +294,8 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
         break;
       }
       case SDCA_OBJ_HINGE_TOPK_SMOOTH: {
-        deferred = !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, k, gamma, lds_col, lds_dummy, primal);
+        deferred = !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, nvalid, k, gamma, lds_col,
+                                                      lds_dummy, primal);
         break;
       }
       case SDCA_OBJ_TOPK_HINGE_SMOOTH: {

@@ -458,8 +458,13 @@ constexpr int kCandSlots = (G <= 2) ? 8 : (G <= 4) ? SDCA_CAND_G4 : (G <= 16) ? 
 // the column's LDS slots into kCandSlots registers per lane (candidate i to
 // lane i % G), and the register variable fixing runs on them with group sums.
 // The cut is widened by a few ulps so that rounding of hi = rhs / k cannot
-// drop a contributor.
-template <int G, int C, int L, class D, class R>
+// drop a contributor.  lds_col is scratch: the column's LDS words, slot c of
+// lane g at lds_col[g + G c] for c < nvalid (nothing outside them is touched
+// but the lane's own dummy word).  LDS_FALLBACK: when there are too many
+// candidates for the registers, the fixing over every slot keeps its working
+// copy in those LDS words (for callers where that case is rare and the
+// registers set the occupancy) rather than in C more registers.
+template <int G, int C, int L, class D, class R, bool LDS_FALLBACK>
 __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L], int m,
                                              int nvalid, R kth, R hi, R rhs, D* lds_col,
                                              D* lds_dummy) {
@@ -514,13 +519,9 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
     }
   }
   const R all = total_sum<G, C, D, R>(v, nvalid);
-  // The fixing over every slot is rare here (more than G * kCandSlots
-  // candidates): its working copy goes to the column's LDS slots, which keeps
-  // the kernel's register peak at the candidate path's.
-  return knapsack_eq_regs<G, C, D, R, (G > 1)>(v, m, nvalid, all, R(0), hi, rhs,
-                                               num<R>::inf(), 0, R(0),
-                                               lds_col + static_cast<int>(threadIdx.x) % G,
-                                               lds_dummy);
+  return knapsack_eq_regs<G, C, D, R, (LDS_FALLBACK && G > 1)>(
+      v, m, nvalid, all, R(0), hi, rhs, num<R>::inf(), 0, R(0),
+      lds_col + static_cast<int>(threadIdx.x) % G, lds_dummy);
 }
 
 template <int G, int C, int KM, class D, class R>
@@ -565,8 +566,10 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   if (constant && !(K * hi_c > rhs + eps)) return make_thr<R>(t_c, R(0), hi_c);
   const R hi = rhs / K;
-  KnapState<R> st = topk_knapsack<G, C, L, D, R>(v, top, m, nvalid, kth, hi, rhs, lds_col,
-                                                  lds_dummy);
+  // More than G * kCandSlots candidates is rare for the prox inputs: the LDS
+  // working copy keeps the kernel's register peak at the candidate path's.
+  KnapState<R> st = topk_knapsack<G, C, L, D, R, true>(v, top, m, nvalid, kth, hi, rhs, lds_col,
+                                                        lds_dummy);
   if (!constant) {
     // is_topk_simplex_lt (topk_simplex.h:9-27), is_topk_simplex_biased_lt
     // (topk_simplex_biased.h:9-28), over U = [first, t.first)
@@ -1149,9 +1152,6 @@ __device__ inline void tile_store(D* __restrict__ dst, const D* __restrict__ src
 // ---------------------------------------------------------------------------
 template <int FAM, int KM, class D, class R, int G, int C, int BT, bool FULL>
 __global__ void __launch_bounds__(BT)
-#ifdef SDCA_WAVES_PER_EU
-__attribute__((amdgpu_waves_per_eu(SDCA_WAVES_PER_EU)))
-#endif
 prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
                     int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
                     sdca_thresholds* __restrict__ thr, int* __restrict__ slow) {

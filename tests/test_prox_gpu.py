@@ -213,6 +213,23 @@ def test_lambert_w_exp(cuda, oracle, dtype):
     assert err.max() <= tol, f"max rel err {err.max():.3e}"
 
 
+@pytest.mark.parametrize("lo,hi", [(-708.0, -36.0), (-745.5, -708.0)])
+def test_exp_through_lambert_tail(cuda, lo, hi):
+    """On (-746, -36] the double Lambert map returns e^x itself
+    (math/lambert.h:153): the kernels' double exponential, held here to
+    2 ulp of numpy's (1 ulp of the smallest subnormal below 2^-1022)."""
+    rng = np.random.default_rng(61)
+    x = rng.uniform(lo, hi, (1, 200000))
+    x[0, :3] = [lo, hi, np.nextafter(hi, 0.0)]
+    got, _ = run_gpu_plain("lambert_w_exp", x, cuda)
+    want = np.exp(x)
+    ulp = np.spacing(want)
+    err = np.abs(got - want) / ulp
+    normal = want >= np.finfo(np.float64).tiny
+    assert err[normal].max(initial=0.0) <= 2.0, f"max {err[normal].max():.2f} ulp"
+    assert err[~normal].max(initial=0.0) <= 1.0, f"subnormal max {err[~normal].max():.2f} ulp"
+
+
 def run_gpu_plain(op, x, cuda):
     import torch
     import libsdca_amd as sd
