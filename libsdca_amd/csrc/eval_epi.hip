@@ -377,12 +377,13 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
 }
 
 // Two-block simplex sets (two_simplex.h:18-119) with block a = the slots in
-// `in_a`: the projection of (a, b) onto {x, y >= 0, <1,x> = <1,y> <= rhs}.
+// `in_a_bits`: the projection of (a, b) onto {x, y >= 0, <1,x> = <1,y> <= rhs}.
 // Returns the smooth multilabel loss <h, p> - <p, p> / 2 summed over both
 // blocks (lo = 0 and U is empty in both, so only the free sets count).
 template <int G, int C, class D, class R>
-__device__ inline R smooth_two_simplex_loss(const D (&v)[C], const bool (&in_a)[C], int p, int mn,
+__device__ inline R smooth_two_simplex_loss(const D (&v)[C], unsigned in_a_bits, int p, int mn,
                                             R rhs) {
+  auto in_a = [&](int c) -> bool { return (in_a_bits >> c) & 1u; };
   const R eps = num<R>::eps() * dmax(R(1), rhs);
   R cuts[2];
   R res[2];
@@ -396,7 +397,7 @@ __device__ inline R smooth_two_simplex_loss(const D (&v)[C], const bool (&in_a)[
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const R x = static_cast<R>(v[c]);
-        s += (in_a[c] == (b == 0) && x > cut) ? x : R(0);
+        s += (in_a(c) == (b == 0) && x > cut) ? x : R(0);
       }
       s = group_sum<G>(s);
       tb = (s - rhs) / static_cast<R>(cnt[b]);
@@ -404,7 +405,7 @@ __device__ inline R smooth_two_simplex_loss(const D (&v)[C], const bool (&in_a)[
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const R x = static_cast<R>(v[c]);
-        above += (in_a[c] == (b == 0) && x > cut && x > tb) ? 1 : 0;
+        above += (in_a(c) == (b == 0) && x > cut && x > tb) ? 1 : 0;
       }
       above = group_sum<G>(above);
       if (above == cnt[b]) break;
@@ -421,8 +422,8 @@ __device__ inline R smooth_two_simplex_loss(const D (&v)[C], const bool (&in_a)[
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const R x = static_cast<R>(v[c]);
-      sa += (in_a[c] && x > cuts[0]) ? x : R(0);
-      sb += (!in_a[c] && x > cuts[1]) ? x : R(0);
+      sa += (in_a(c) && x > cuts[0]) ? x : R(0);
+      sb += (!in_a(c) && x > cuts[1]) ? x : R(0);
     }
     sa = group_sum<G>(sa);
     sb = group_sum<G>(sb);
@@ -434,8 +435,8 @@ __device__ inline R smooth_two_simplex_loss(const D (&v)[C], const bool (&in_a)[
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const R x = static_cast<R>(v[c]);
-        const bool lx = in_a[c] && x > cuts[0] && !(x > t);
-        const bool ly = !in_a[c] && x > cuts[1] && !(x > mt);
+        const bool lx = in_a(c) && x > cuts[0] && !(x > t);
+        const bool ly = !in_a(c) && x > cuts[1] && !(x > mt);
         sum_x += lx ? x : R(0);
         n_x += lx ? 1 : 0;
         sum_y += ly ? x : R(0);
@@ -474,8 +475,8 @@ __device__ inline R smooth_two_simplex_loss(const D (&v)[C], const bool (&in_a)[
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const R x = static_cast<R>(v[c]);
-    const bool fa = in_a[c] && x > cuts[0];
-    const bool fb = !in_a[c] && x > cuts[1];
+    const bool fa = in_a(c) && x > cuts[0];
+    const bool fb = !in_a(c) && x > cuts[1];
     sm[0] += fa ? x : R(0);
     dm[0] += fa ? x * x : R(0);
     nm[0] += fa ? 1 : 0;
@@ -534,17 +535,16 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
   const int nvalid = (m - g + G - 1) / G;
   const D* srow = S + ii * m64;
   D s[C];
-  bool pos[C];
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
-    s[c] = (c < nvalid) ? srow[g + G * c] : -num<D>::inf();
-    pos[c] = false;
-  }
+  for (int c = 0; c < C; ++c) s[c] = (c < nvalid) ? srow[g + G * c] : -num<D>::inf();
+  // Positives of this lane as a slot mask: label j sits in slot (j - g) / G
+  // of lane g when j - g is a multiple of G.
+  unsigned posb = 0;
   for (int q = 0; q < p; ++q) {
-    const int lab = label_at(q);
-#pragma unroll
-    for (int c = 0; c < C; ++c) pos[c] = pos[c] || (g + G * c == lab);
+    const int rel = label_at(q) - g;
+    if (rel >= 0 && rel % G == 0) posb |= 1u << (rel / G);
   }
+  auto pos = [&](int c) -> bool { return (posb >> c) & 1u; };
   // Rank loss (eval/primal.h:70-79): for each positive, the negatives >= it.
   R rl = 0;
   for (int q = 0; q < p; ++q) {
@@ -552,15 +552,36 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
     const D sp = srow[lab];
     int cn = 0;
 #pragma unroll
-    for (int c = 0; c < C; ++c) cn += (c < nvalid && !pos[c] && s[c] >= sp) ? 1 : 0;
+    for (int c = 0; c < C; ++c) cn += (c < nvalid && !pos(c) && s[c] >= sp) ? 1 : 0;
     rl += static_cast<R>(group_sum<G>(cn));
   }
   const R rank_i = rl / static_cast<R>(p * (m - p));
   if (active && g == 0) rank[i] = static_cast<double>(rank_i);
 
-  D a[C];
+  // The dual terms that do not depend on the objective, from one pass over
+  // the example's row of A (l2_multilabel_hinge.h:87-96, :194-208,
+  // l2_multilabel_entropy.h:89-109): sum over positives and negatives, the
+  // squared norm and the negatives' sum of x log x at -a.  A is NULL for a
+  // test set, whose records hold no dual terms.
+  const D* arow = A ? A + ii * m64 : nullptr;
+  R s_pos = 0, s_neg = 0, sq = 0, xl_neg = 0;
+  if (A) {
 #pragma unroll
-  for (int c = 0; c < C; ++c) a[c] = (A && c < nvalid) ? A[ii * m64 + g + G * c] : D(0);
+    for (int c = 0; c < C; ++c) {
+      if (c < nvalid) {
+        const R x = static_cast<R>(arow[g + G * c]);
+        s_pos += pos(c) ? x : R(0);
+        s_neg += pos(c) ? R(0) : x;
+        sq += x * x;
+        xl_neg += pos(c) ? R(0) : x_log_x(-x);
+      }
+    }
+    s_pos = group_sum<G>(s_pos);
+    s_neg = group_sum<G>(s_neg);
+    sq = group_sum<G>(sq);
+    xl_neg = group_sum<G>(xl_neg);
+  }
+  const R pr = static_cast<R>(p);
 
   for (int o = 0; o < objs.n; ++o) {
     const EvalObj ob = objs.o[o];
@@ -572,8 +593,8 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
 #pragma unroll
         for (int c = 0; c < C; ++c) {
           if (c < nvalid) {
-            mn = pos[c] ? ((s[c] < mn) ? s[c] : mn) : mn;
-            mx = !pos[c] ? ((mx < s[c]) ? s[c] : mx) : mx;
+            mn = pos(c) ? ((s[c] < mn) ? s[c] : mn) : mn;
+            mx = !pos(c) ? ((mx < s[c]) ? s[c] : mx) : mx;
           }
         }
         mn = group_min<G>(mn);
@@ -586,14 +607,14 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
         D v[C];
 #pragma unroll
         for (int c = 0; c < C; ++c)
-          v[c] = (c < nvalid) ? (pos[c] ? half - s[c] : s[c] + half) : -num<D>::inf();
-        primal = smooth_two_simplex_loss<G, C, D, R>(v, pos, p, m - p, gamma);
+          v[c] = (c < nvalid) ? (pos(c) ? half - s[c] : s[c] + half) : -num<D>::inf();
+        primal = smooth_two_simplex_loss<G, C, D, R>(v, posb, p, m - p, gamma);
         break;
       }
       case SDCA_OBJ_MULTILABEL_ENTROPY: {  // l2_multilabel_entropy.h:72-86
         R sp = 0;
 #pragma unroll
-        for (int c = 0; c < C; ++c) sp += (c < nvalid && pos[c]) ? static_cast<R>(s[c]) : R(0);
+        for (int c = 0; c < C; ++c) sp += (c < nvalid && pos(c)) ? static_cast<R>(s[c]) : R(0);
         sp = group_sum<G>(sp);
         primal = lse_all<G, C, D, R>(s, nvalid) - sp / static_cast<R>(p);
         break;
@@ -601,32 +622,22 @@ eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
       default:
         break;
     }
-    R s_pos = 0, s_neg = 0, sq = 0, xl_pos = 0, xl_neg = 0;
-    const R pr = static_cast<R>(p);
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      if (c < nvalid) {
-        const R x = static_cast<R>(a[c]);
-        s_pos += pos[c] ? x : R(0);
-        s_neg += pos[c] ? R(0) : x;
-        sq += x * x;
-        xl_pos += pos[c] ? x_log_x(c_ - pr * x) : R(0);
-        xl_neg += pos[c] ? R(0) : x_log_x(-x);
-      }
-    }
-    s_pos = group_sum<G>(s_pos);
-    s_neg = group_sum<G>(s_neg);
-    sq = group_sum<G>(sq);
-    xl_pos = group_sum<G>(xl_pos);
-    xl_neg = group_sum<G>(xl_neg);
     switch (ob.kind) {
       case SDCA_OBJ_MULTILABEL_HINGE: dual = s_pos; break;  // l2_multilabel_hinge.h:87-96
       case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:                 // l2_multilabel_hinge.h:194-208
         dual = R(0.5) * (s_pos - s_neg - (gamma / c_) * sq);
         break;
-      case SDCA_OBJ_MULTILABEL_ENTROPY:                      // l2_multilabel_entropy.h:89-109
+      case SDCA_OBJ_MULTILABEL_ENTROPY: {                    // l2_multilabel_entropy.h:89-109
+        // x log x at c - p a_j over the positives, from their labels (every
+        // lane of the group the same, in label order).
+        R xl_pos = 0;
+        for (int q = 0; q < p; ++q) {
+          const R x = arow ? static_cast<R>(arow[label_at(q)]) : R(0);
+          xl_pos += x_log_x(c_ - pr * x);
+        }
         dual = -xl_pos / pr - xl_neg + x_log_x(c_) + dlog(pr) * (c_ - s_pos);
         break;
+      }
       default: break;
     }
     if (active && g == 0) {
