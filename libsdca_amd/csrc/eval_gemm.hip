@@ -35,14 +35,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int BK = 16;  // reduction slab
 
 // Loads the slab [k0, k0 + BK) of rows [r0, r0 + ROWS) of a (rows x d)
-// matrix into float4 registers (ROWS * 4 float4 per slab, NV per thread);
-// rows past `rows` and columns past d read as zero.
-template <int ROWS, int NV>
+// matrix into float4 registers (ROWS * 4 float4 per slab, NV per thread of
+// NT); rows past `rows` and columns past d read as zero.
+template <int ROWS, int NV, int NT>
 __device__ inline void load_slab(const float* __restrict__ src, int64_t rows, int64_t d,
                                  int64_t r0, int64_t k0, bool vec, f32x4 (&r)[NV]) {
 #pragma unroll
   for (int h = 0; h < NV; ++h) {
-    const int f = static_cast<int>(threadIdx.x) + 256 * h;  // float4 index in the slab
+    const int f = static_cast<int>(threadIdx.x) + NT * h;  // float4 index in the slab
     const int row = f >> 2, q = f & 3;
     const int64_t gr = r0 + row;
     const int64_t gk = k0 + 4 * q;
@@ -62,11 +62,11 @@ __device__ inline void load_slab(const float* __restrict__ src, int64_t rows, in
 }
 
 // Stores the float4 of a slab into LDS transposed to [k][row].
-template <int ROWS, int NV>
+template <int ROWS, int NV, int NT>
 __device__ inline void store_slab(float* __restrict__ lds, int ld, const f32x4 (&r)[NV]) {
 #pragma unroll
   for (int h = 0; h < NV; ++h) {
-    const int f = static_cast<int>(threadIdx.x) + 256 * h;
+    const int f = static_cast<int>(threadIdx.x) + NT * h;
     const int row = f >> 2, q = f & 3;
     if (f < ROWS * 4) {
 #pragma unroll
@@ -75,20 +75,19 @@ __device__ inline void store_slab(float* __restrict__ lds, int ld, const f32x4 (
   }
 }
 
-// One BM x BN tile of S per 256-thread workgroup: the four waves form a
-// WM x WN grid, each wave a (BM / WM) x (BN / WN) block of 32 x 32
-// accumulators.
+// One BM x BN tile of S per workgroup of WM x WN waves, each wave a
+// (BM / WM) x (BN / WN) block of 32 x 32 accumulators.
 template <int BM, int BN, int WM, int WN>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * WM * WN)
 scores_gemm_kernel(const float* __restrict__ X, const float* __restrict__ W,
                    float* __restrict__ S, int64_t n, int64_t m, int64_t d,
                    int64_t tiles_m, int64_t tiles_n_padded, int vec) {
-  static_assert(WM * WN == 4, "four waves");
+  constexpr int NT = 64 * WM * WN;           // threads
   constexpr int TM = BM / WM, TN = BN / WN;  // rows, columns of a wave's block
   static_assert(TM % 32 == 0 && TN % 32 == 0, "32 x 32 accumulators");
   constexpr int FM = TM / 32, FN = TN / 32;
   constexpr int LDA = BM + 4, LDB = BN + 4;  // padded LDS rows (floats)
-  constexpr int NVA = (BM * 4 + 255) / 256, NVB = (BN * 4 + 255) / 256;
+  constexpr int NVA = (BM * 4 + NT - 1) / NT, NVB = (BN * 4 + NT - 1) / NT;
   __shared__ __align__(16) float As[2][BK * LDA];
   __shared__ __align__(16) float Bs[2][BK * LDB];
 
@@ -118,10 +117,10 @@ scores_gemm_kernel(const float* __restrict__ X, const float* __restrict__ W,
 
   const bool vv = vec != 0;
   f32x4 ra[NVA], rb[NVB];
-  load_slab<BM, NVA>(X, n, d, i0, 0, vv, ra);
-  load_slab<BN, NVB>(W, m, d, j0, 0, vv, rb);
-  store_slab<BM, NVA>(As[0], LDA, ra);
-  store_slab<BN, NVB>(Bs[0], LDB, rb);
+  load_slab<BM, NVA, NT>(X, n, d, i0, 0, vv, ra);
+  load_slab<BN, NVB, NT>(W, m, d, j0, 0, vv, rb);
+  store_slab<BM, NVA, NT>(As[0], LDA, ra);
+  store_slab<BN, NVB, NT>(Bs[0], LDB, rb);
   __syncthreads();
 
   const int64_t nslabs = (d + BK - 1) / BK;
@@ -129,8 +128,8 @@ scores_gemm_kernel(const float* __restrict__ X, const float* __restrict__ W,
     const int cur = static_cast<int>(s & 1);
     const bool more = s + 1 < nslabs;
     if (more) {
-      load_slab<BM, NVA>(X, n, d, i0, (s + 1) * BK, vv, ra);
-      load_slab<BN, NVB>(W, m, d, j0, (s + 1) * BK, vv, rb);
+      load_slab<BM, NVA, NT>(X, n, d, i0, (s + 1) * BK, vv, ra);
+      load_slab<BN, NVB, NT>(W, m, d, j0, (s + 1) * BK, vv, rb);
     }
     const float* as = As[cur];
     const float* bs = Bs[cur];
@@ -149,8 +148,8 @@ scores_gemm_kernel(const float* __restrict__ X, const float* __restrict__ W,
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
     }
     if (more) {
-      store_slab<BM, NVA>(As[cur ^ 1], LDA, ra);
-      store_slab<BN, NVB>(Bs[cur ^ 1], LDB, rb);
+      store_slab<BM, NVA, NT>(As[cur ^ 1], LDA, ra);
+      store_slab<BN, NVB, NT>(Bs[cur ^ 1], LDB, rb);
     }
     __syncthreads();
   }
@@ -181,7 +180,7 @@ hipError_t launch_tiles(const float* X, const float* W, float* S, int64_t n, int
   const int vec = (d % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(W) & 15) == 0) ? 1 : 0;
   hipLaunchKernelGGL((scores_gemm_kernel<BM, BN, WM, WN>), dim3(static_cast<unsigned>(grid)),
-                     dim3(256), 0, stream, X, W, S, n, m, d, tiles_m, tiles_n_padded, vec);
+                     dim3(64 * WM * WN), 0, stream, X, W, S, n, m, d, tiles_m, tiles_n_padded, vec);
   return hipGetLastError();
 }
 
