@@ -1176,10 +1176,11 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   // compile-time offset, so every slot access is one LDS instruction.
   D* const col = tile + lc * m;
   D* const mine = col + g;
-  // Unless FULL, the tile has G*C words of slack after the B*m elements, so
-  // every slot read stays inside the allocation and the loop needs no branch;
-  // past that sit BT per-lane dummy words for predicated stores.
-  D* const lds_dummy = tile + B * m + (FULL ? 0 : G * C) + threadIdx.x;
+  // Unless FULL, the tile has G*C - m words of slack after the B*m elements
+  // (the last column's slot reads end there), so every slot read stays
+  // inside the allocation and the loop needs no branch; past that sit BT
+  // per-lane dummy words for predicated stores.
+  D* const lds_dummy = tile + B * m + (FULL ? 0 : G * C - m) + threadIdx.x;
   D v[C];
   if (FULL && ncols == B) {
 #pragma unroll
