@@ -87,3 +87,30 @@ def test_random_eval_case(cuda, oracle, i):
     else:
         for r, o in zip(recs, o_recs):
             assert abs(r["rank_loss"] - o["rank_loss"]) <= 1e-6 * max(1, abs(o["rank_loss"])), what
+
+
+@pytest.mark.parametrize("i", range(40))
+def test_random_scores_gemm(cuda, i):
+    """S = X W^T for random n, m (both class-tile widths: 128, and 224 where it
+    pads m less, e.g. m in (128, 224] or (384, 448]), d (odd included, which
+    takes the unvectorised loads) and fp32/fp64, against an fp64 product
+    with the sqrt(d) eps bound of test_eval_gpu.test_scores_gemm."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(4000 + i)
+    n = int(rng.integers(1, 2000))
+    m = int(rng.choice([int(rng.integers(1, 2049)), int(rng.integers(129, 225)),
+                        int(rng.integers(385, 449))]))
+    d = int(rng.choice([int(rng.integers(1, 3000)), 4 * int(rng.integers(1, 600))]))
+    dtype = np.float64 if i % 5 == 4 else np.float32
+    X = rng.standard_normal((n, d)).astype(dtype)
+    W = (rng.standard_normal((m, d)) * 0.01).astype(dtype)
+    print(f"case {i}: n={n} m={m} d={d} {np.dtype(dtype).name}", flush=True)
+    S = sd.scores(torch.from_numpy(X).to(cuda), torch.from_numpy(W).to(cuda))
+    torch.cuda.synchronize()
+    got = S.cpu().numpy().astype(np.float64)
+    want = X.astype(np.float64) @ W.astype(np.float64).T
+    eps = np.finfo(dtype).eps
+    bound = np.sqrt(d) * eps * (np.abs(X).astype(np.float64) @ np.abs(W).astype(np.float64).T)
+    err = np.abs(got - want)
+    assert (err <= 4 * bound + 1e-30).all(), f"case {i}: max err/bound {(err / (bound + 1e-30)).max():.2f}"
