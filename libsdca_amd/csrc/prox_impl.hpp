@@ -937,14 +937,17 @@ __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
 // b = rows [p, m); the sets kept by the reference's partitions are
 // {x > x_cut} and {y > y_cut}.
 // ---------------------------------------------------------------------------
-template <int G, int C, class D, class R>
-__device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const ProxParamsT<R>& pp) {
+// CA: the slots that may hold rows of block a (slot c holds row g + G c, so
+// c < ceil(p / G)); the passes over block a visit only those, and the joint
+// passes treat the others as block b alone.
+template <int G, int C, int CA, class D, class R>
+__device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
+                                             const ProxParamsT<R>& pp) {
   const R rhs = pp.rhs;
   const R eps = num<R>::eps() * dmax(R(1), rhs);
   const int g = static_cast<int>(threadIdx.x) % G;
-  bool in_a[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) in_a[c] = (g + G * c) < p;
+  // Recomputed where used (one compare) rather than held as C lane masks.
+  auto in_a = [&](int c) -> bool { return c < CA && (g + G * c) < p; };
   R cuts[2];
   R res[2];
   R maxs[2];
@@ -960,8 +963,9 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
     R mx = -num<R>::inf();
 #pragma unroll
     for (int c = 0; c < C; ++c) {
+      if (b == 0 && c >= CA) continue;
       const R x = static_cast<R>(v[c]);
-      mx = (in_a[c] == (b == 0) && x > mx) ? x : mx;
+      mx = (in_a(c) == (b == 0) && x > mx) ? x : mx;
     }
     mx = group_max<G>(mx);
     maxs[b] = mx;
@@ -970,8 +974,9 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
     int nb = 0;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
+      if (b == 0 && c >= CA) continue;
       const R x = static_cast<R>(v[c]);
-      const bool in = in_a[c] == (b == 0) && x > cut;
+      const bool in = in_a(c) == (b == 0) && x > cut;
       sb += in ? x : R(0);
       nb += in ? 1 : 0;
     }
@@ -984,8 +989,9 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
       int n2 = 0;
 #pragma unroll
       for (int c = 0; c < C; ++c) {
+        if (b == 0 && c >= CA) continue;
         const R x = static_cast<R>(v[c]);
-        const bool in = in_a[c] == (b == 0) && x > cut && x > tb;
+        const bool in = in_a(c) == (b == 0) && x > cut && x > tb;
         s2 += in ? x : R(0);
         n2 += in ? 1 : 0;
       }
@@ -1020,8 +1026,8 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const R x = static_cast<R>(v[c]);
-      if (in_a[c] && x > cuts[0]) sa += x;
-      if (!in_a[c] && x > cuts[1]) sb += x;
+      if (in_a(c) && x > cuts[0]) sa += x;
+      if (!in_a(c) && x > cuts[1]) sb += x;
     }
     sa = group_sum<G>(sa);
     sb = group_sum<G>(sb);
@@ -1034,7 +1040,7 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const R x = static_cast<R>(v[c]);
-      if (in_a[c]) {
+      if (in_a(c)) {
         if (x > cuts[0] && !(x > t)) { sum_x += x; ++n_x; }
       } else {
         if (x > cuts[1] && !(x > mt)) { sum_y += x; ++n_y; }
@@ -1070,6 +1076,19 @@ __device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const Prox
   ColThr<R> r = make_thr<R>(t, R(0), rhs);
   r.t2 = -t;
   return r;
+}
+
+// Two-block simplex of one column per lane group.  When no column of the
+// wave has more than G rows in block a (the multilabel duals: p <= 5 of
+// m = 200 rows), block a lies in slot 0 of every lane and the passes over it
+// are one slot long; the results are the same as the general form's.
+template <int G, int C, class D, class R>
+__device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const ProxParamsT<R>& pp) {
+  if constexpr (C > 1) {
+    const int a_slots = __builtin_amdgcn_readfirstlane(group_max<64>((p + G - 1) / G));
+    if (a_slots <= 1) return two_family_slots<G, C, 1, D, R>(v, m, p, pp);
+  }
+  return two_family_slots<G, C, C, D, R>(v, m, p, pp);
 }
 
 // ---------------------------------------------------------------------------
