@@ -342,7 +342,11 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   pp.p = static_cast<int>(a.p);
   int pow2 = 1;
   while (pow2 < a.m) pow2 <<= 1;
-  const int64_t cap = all_columns ? 4096 : 512;
+  // List mode: the list is a small fraction of the n columns and usually
+  // empty; the grid grows with n (about one workgroup per 1024 columns,
+  // 512 to 4096), so that a long list finds workgroups on every CU while
+  // an empty one on a small batch costs little to launch.
+  const int64_t cap = all_columns ? 4096 : std::min<int64_t>(4096, std::max<int64_t>(512, a.n / 1024));
   const int64_t grid = a.n < cap ? a.n : cap;
   hipLaunchKernelGGL((prox_slow_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
                      dim3(256), static_cast<size_t>(pow2) * sizeof(D), a.stream,
@@ -480,7 +484,11 @@ template <class D, class R>
 hipError_t launch_two_sort_t(const ProxLaunch& a, bool all_columns) {
   int half = 1;
   while (half < a.m) half <<= 1;  // pow2 >= max(p, m - p) for every column
-  const int64_t cap = all_columns ? 4096 : 512;
+  // List mode: the list is a small fraction of the n columns and usually
+  // empty; the grid grows with n (about one workgroup per 1024 columns,
+  // 512 to 4096), so that a long list finds workgroups on every CU while
+  // an empty one on a small batch costs little to launch.
+  const int64_t cap = all_columns ? 4096 : std::min<int64_t>(4096, std::max<int64_t>(512, a.n / 1024));
   const int64_t grid = a.n < cap ? a.n : cap;
   hipLaunchKernelGGL((two_sort_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
                      dim3(256), 2 * static_cast<size_t>(half) * sizeof(D), a.stream,
