@@ -11,6 +11,8 @@
 // with the same sums - and the workgroup clamps the column from global memory.
 // Columns come from a device list written by the register kernel, so no host
 // round trip is needed; every workgroup exits after the list is drained.
+#include <algorithm>
+
 #include "common.hpp"
 #include "prox_impl.hpp"
 #include "prox_launch.hpp"
