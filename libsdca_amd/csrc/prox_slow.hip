@@ -12,6 +12,7 @@
 // Columns come from a device list written by the register kernel, so no host
 // round trip is needed; every workgroup exits after the list is drained.
 #include <algorithm>
+#include <climits>
 
 #include "common.hpp"
 #include "prox_impl.hpp"
@@ -85,17 +86,40 @@ __device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
   return st;
 }
 
+// The U/M searches below try |U| = 0, 1, 2, ... in turn and return the
+// first |U| whose scan over M accepts.  Called by all 64 lanes of a wave:
+// lane l scans |U| = l, l + 64, ... (each setting up its U by the
+// reference's own sequence of updates, so every trial value is the
+// reference's), and the smallest accepting |U| of the wave is the answer.
+// Returns its (t, hi) in every lane; found = false gives the default.
+template <class R>
+__device__ inline bool wave_first_accept(int u_found, R& t, R& hi) {
+  const int best = group_min<64>(u_found);
+  if (best == INT_MAX) return false;
+  t = __shfl(t, best & 63, 64);
+  hi = __shfl(hi, best & 63, 64);
+  return true;
+}
+
 // topk_cone_search (topk_cone.h:58-133) and its biased form
 // thresholds_topk_cone_biased_search (topk_cone_biased.h:9-106) on the sorted
 // column: the latter starts the |U| + rho k^2 term at rho k^2 (rho = 0 gives
 // the former's steps exactly).
 template <class D, class R>
 __device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R& hi_out) {
-  R k_u = static_cast<R>(k);
-  R min_u = num<R>::inf();
-  R num_u = rho * static_cast<R>(k) * static_cast<R>(k), sum_u = 0;
   const R eps = R(16) * num<R>::eps();
-  for (int mf = 0;;) {
+  int found = INT_MAX;
+  R ft = 0, fh = 0;
+  for (int mf = static_cast<int>(threadIdx.x) & 63; mf <= k && found == INT_MAX; mf += 64) {
+    R k_u = static_cast<R>(k);
+    R min_u = num<R>::inf();
+    R num_u = rho * static_cast<R>(k) * static_cast<R>(k), sum_u = 0;
+    for (int i = 0; i < mf; ++i) {
+      min_u = static_cast<R>(s[i]);
+      sum_u += min_u;
+      k_u -= R(1);
+      num_u += R(1);
+    }
     R min_m = num<R>::inf();
     R max_m = -num<R>::inf();
     R sum_m = 0, num_m_sum_u = 0;
@@ -107,9 +131,10 @@ __device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R&
       const R tt = hi + t;
       if (max_m - eps <= tt && tt <= min_u + eps) {
         if (t <= min_m + eps && (ml == m || static_cast<R>(s[ml]) - eps <= t)) {
-          t_out = t;
-          hi_out = hi;
-          return;
+          found = mf;
+          ft = t;
+          fh = hi;
+          break;
         }
       }
       if (ml == m) break;
@@ -120,15 +145,10 @@ __device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R&
       den += num_u;
       ++ml;
     }
-    if (mf == k) break;
-    min_u = static_cast<R>(s[mf]);
-    sum_u += min_u;
-    k_u -= R(1);
-    num_u += R(1);
-    ++mf;
   }
-  t_out = 0;
-  hi_out = 0;
+  if (!wave_first_accept(found, ft, fh)) ft = fh = 0;
+  t_out = ft;
+  hi_out = fh;
 }
 
 // thresholds_knapsack_le_biased_search (knapsack_le_biased.h:10-92) on the
@@ -141,8 +161,13 @@ __device__ void knapsack_le_biased_sorted(const D* s, int m, R lo, R hi, R rhs, 
   const R rho_rhs = rho * rhs;
   const R rho_inv = R(1) / rho;
   const R num_x = static_cast<R>(m);
-  R num_u = 0, min_u = num<R>::inf();
-  for (int mf = 0;;) {
+  int found = INT_MAX;
+  R ft = 0, unused = 0;
+  for (int mf = static_cast<int>(threadIdx.x) & 63; mf <= m && found == INT_MAX; mf += 64) {
+    // |U| = mf: the reference reaches it with num_u counted up by ones and
+    // min_u = s[mf - 1].
+    const R num_u = static_cast<R>(mf);
+    const R min_u = mf > 0 ? static_cast<R>(s[mf - 1]) : num<R>::inf();
     R min_m = num<R>::inf();
     R max_m = -num<R>::inf();
     R num_m = 0, sum_m = 0;
@@ -154,10 +179,9 @@ __device__ void knapsack_le_biased_sorted(const D* s, int m, R lo, R hi, R rhs, 
         if (max_m - eps <= tt && tt <= min_u + eps) {
           tt = lo + t;
           if (tt <= min_m + eps && (ml == m || static_cast<R>(s[ml]) - eps <= tt)) {
-            t_out = t;
-            lo_out = lo;
-            hi_out = hi;
-            return;
+            found = mf;
+            ft = t;
+            break;
           }
         }
       }
@@ -169,14 +193,16 @@ __device__ void knapsack_le_biased_sorted(const D* s, int m, R lo, R hi, R rhs, 
       num_m += R(1);
       ++ml;
     }
-    if (mf == m) break;
-    min_u = static_cast<R>(s[mf]);
-    num_u += R(1);
-    ++mf;
   }
-  t_out = 0;
-  lo_out = 0;
-  hi_out = 0;
+  if (wave_first_accept(found, ft, unused)) {
+    t_out = ft;
+    lo_out = lo;
+    hi_out = hi;
+  } else {
+    t_out = 0;
+    lo_out = 0;
+    hi_out = 0;
+  }
 }
 
 template <class D, class R>
@@ -297,16 +323,20 @@ prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int
         __syncthreads();
       }
     }
-    if (threadIdx.x == 0) {
+    // The first wave computes the thresholds: the scalar parts in every lane
+    // alike, the U/M searches split over its lanes.
+    if (threadIdx.x < 64) {
       R t, lo, hi;
       thresholds_sorted<D, R>(s, m, pp.op, pp.lo, pp.hi, pp.rhs, pp.rho, pp.k, t, lo, hi);
-      sh_t = t;
-      sh_lo = lo;
-      sh_hi = hi;
-      if (thr) {
-        thr[j].t = static_cast<double>(t);
-        thr[j].lo = static_cast<double>(lo);
-        thr[j].hi = static_cast<double>(hi);
+      if (threadIdx.x == 0) {
+        sh_t = t;
+        sh_lo = lo;
+        sh_hi = hi;
+        if (thr) {
+          thr[j].t = static_cast<double>(t);
+          thr[j].lo = static_cast<double>(lo);
+          thr[j].hi = static_cast<double>(hi);
+        }
       }
     }
     __syncthreads();
