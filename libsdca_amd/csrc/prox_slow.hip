@@ -380,8 +380,12 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   // an empty one on a small batch costs little to launch.
   const int64_t cap = all_columns ? 4096 : std::min<int64_t>(4096, std::max<int64_t>(512, a.n / 1024));
   const int64_t grid = a.n < cap ? a.n : cap;
+  // One wave per workgroup for short columns (the sort's stages then need
+  // no cross-wave barrier and four times as many columns are in flight),
+  // four waves beyond 256 rows.
+  const int threads = pow2 <= 256 ? 64 : 256;
   hipLaunchKernelGGL((prox_slow_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
-                     dim3(256), static_cast<size_t>(pow2) * sizeof(D), a.stream,
+                     dim3(threads), static_cast<size_t>(pow2) * sizeof(D), a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
                      a.thr, a.slow, all_columns ? 1 : 0, pow2);
   return hipGetLastError();
