@@ -340,8 +340,29 @@ __device__ inline void top_merge_step(D (&top)[L]) {
   D other[L];
 #pragma unroll
   for (int i = 0; i < L; ++i) other[i] = xor_lane<OFF>(top[i]);
+  if constexpr (L == 16) {
+    // Two descending lists: c_i = max(a_i, b_(L-1-i)) holds the L largest of
+    // both and falls then rises (bitonic); a bitonic half-cleaner network
+    // sorts it descending.  80 compare-selects instead of the 256 of
+    // inserting the other list entry by entry.
 #pragma unroll
-  for (int i = 0; i < L; ++i) top_insert(top, other[i]);
+    for (int i = 0; i < L; ++i) top[i] = (top[i] < other[L - 1 - i]) ? other[L - 1 - i] : top[i];
+#pragma unroll
+    for (int stride = L / 2; stride > 0; stride >>= 1) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        if ((i & stride) == 0) {
+          const D a = top[i], b = top[i + stride];
+          const bool swap = a < b;
+          top[i] = swap ? b : a;
+          top[i + stride] = swap ? a : b;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < L; ++i) top_insert(top, other[i]);
+  }
 }
 template <int G, int L, class D>
 __device__ inline void top_merge(D (&top)[L]) {
