@@ -335,6 +335,62 @@ __device__ inline void top_insert(double (&top)[L], double x, double = 0) {
 
 // Merge the top lists of the G lanes of a group (every lane ends with the
 // top L values of the union, as a multiset).
+// Max and min for the sorting networks: for float the median of (a, b, ±inf)
+// with an opaque infinity (pinf, made once per network), one v_med3_f32 and
+// no NaN-quieting of the operands (which fmaxf/fminf add).
+__device__ inline float net_max(float a, float b, float pinf) {
+  return __builtin_amdgcn_fmed3f(a, b, pinf);
+}
+__device__ inline float net_min(float a, float b, float pinf) {
+  return __builtin_amdgcn_fmed3f(a, b, -pinf);
+}
+__device__ inline double net_max(double a, double b, double) { return (a < b) ? b : a; }
+__device__ inline double net_min(double a, double b, double) { return (b < a) ? b : a; }
+__device__ inline float net_inf(float) { return opaque_inf(); }
+__device__ inline double net_inf(double) { return __builtin_inf(); }
+
+// Sorts a bitonic sequence of L (a power of two) values descending by
+// half-cleaner stages of max/min pairs.
+template <int L, class D>
+__device__ inline void bitonic_clean_desc(D (&x)[L]) {
+  const D pinf = net_inf(D(0));
+#pragma unroll
+  for (int stride = L / 2; stride > 0; stride >>= 1) {
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      if ((i & stride) == 0) {
+        const D a = x[i], b = x[i + stride];
+        x[i] = net_max(a, b, pinf);
+        x[i + stride] = net_min(a, b, pinf);
+      }
+    }
+  }
+}
+
+// Sorts L (a power of two) values descending by Batcher's bitonic network.
+template <int L, class D>
+__device__ inline void bitonic_sort_desc(D (&x)[L]) {
+  const D pinf = net_inf(D(0));
+#pragma unroll
+  for (int size = 2; size <= L; size <<= 1) {
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride >>= 1) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        if ((i & stride) == 0) {
+          const D a = x[i], b = x[i + stride];
+          // descending runs where (i & size) == 0, ascending otherwise, so
+          // that each merge sees a bitonic sequence; the last pass (size = L)
+          // is all descending.
+          const bool desc = (i & size) == 0;
+          x[i] = desc ? net_max(a, b, pinf) : net_min(a, b, pinf);
+          x[i + stride] = desc ? net_min(a, b, pinf) : net_max(a, b, pinf);
+        }
+      }
+    }
+  }
+}
+
 template <int OFF, int L, class D>
 __device__ inline void top_merge_step(D (&top)[L]) {
   D other[L];
@@ -343,22 +399,12 @@ __device__ inline void top_merge_step(D (&top)[L]) {
   if constexpr (L == 16) {
     // Two descending lists: c_i = max(a_i, b_(L-1-i)) holds the L largest of
     // both and falls then rises (bitonic); a bitonic half-cleaner network
-    // sorts it descending.  80 compare-selects instead of the 256 of
-    // inserting the other list entry by entry.
+    // sorts it descending.  80 max/min instead of the 256 med3 of inserting
+    // the other list entry by entry.
+    const D pinf = net_inf(D(0));
 #pragma unroll
-    for (int i = 0; i < L; ++i) top[i] = (top[i] < other[L - 1 - i]) ? other[L - 1 - i] : top[i];
-#pragma unroll
-    for (int stride = L / 2; stride > 0; stride >>= 1) {
-#pragma unroll
-      for (int i = 0; i < L; ++i) {
-        if ((i & stride) == 0) {
-          const D a = top[i], b = top[i + stride];
-          const bool swap = a < b;
-          top[i] = swap ? b : a;
-          top[i + stride] = swap ? a : b;
-        }
-      }
-    }
+    for (int i = 0; i < L; ++i) top[i] = net_max(top[i], other[L - 1 - i], pinf);
+    bitonic_clean_desc<L>(top);
   } else {
 #pragma unroll
     for (int i = 0; i < L; ++i) top_insert(top, other[i]);

@@ -534,8 +534,18 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   D top[L];
 #pragma unroll
   for (int i = 0; i < L; ++i) top[i] = -num<D>::inf();
+  if constexpr (L == 16 && C >= 16) {
+    // The first 16 slots by a sorting network (80 max/min pairs), the rest
+    // by insertion: 304 operations instead of 16 med3 for every slot.
 #pragma unroll
-  for (int c = 0; c < C; ++c) top_insert(top, v[c]);  // -inf padding leaves it unchanged
+    for (int i = 0; i < L; ++i) top[i] = v[i];
+    bitonic_sort_desc<L>(top);
+#pragma unroll
+    for (int c = L; c < C; ++c) top_insert(top, v[c]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < C; ++c) top_insert(top, v[c]);  // -inf padding leaves it unchanged
+  }
   top_merge<G>(top);
   R sum_k = 0, kth = static_cast<R>(top[0]), next = -num<R>::inf();
 #pragma unroll
