@@ -1208,7 +1208,8 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   // Unless FULL, the tile has G*C - m words of slack after the B*m elements
   // (the last column's slot reads end there), so every slot read stays
   // inside the allocation and the loop needs no branch; past that sit BT
-  // per-lane dummy words for predicated stores.
+  // per-lane dummy words for predicated stores (not allocated for the
+  // entropic families, which never store through them).
   D* const lds_dummy = tile + B * m + (FULL ? 0 : G * C - m) + threadIdx.x;
   D v[C];
   if (FULL && ncols == B) {
