@@ -82,7 +82,14 @@ def draw_case(i):
 @pytest.mark.parametrize("i", range(N_CASES))
 def test_random_case(cuda, oracle, i):
     op, m, n, result, x, kw = draw_case(i)
-    what = f"case {i}: {op} m={m} n={n} {x.dtype.name}->{'f32' if result == 0 else 'f64'} {kw}"
+    host = i % 5 == 0  # every fifth case through the host-pointer staging path
+    what = (f"case {i}: {op} m={m} n={n} {x.dtype.name}->{'f32' if result == 0 else 'f64'} {kw}"
+            f"{' (host pointers)' if host else ''}")
     print(what, flush=True)
-    got, _ = run_gpu(op, x, result, cuda, **kw)
+    if host:
+        import libsdca_amd as sd
+        got = x.copy()
+        sd.prox(op, got, result=result, **kw)
+    else:
+        got, _ = run_gpu(op, x, result, cuda, **kw)
     parity(oracle, op, x, got, result, what, **kw)
