@@ -93,3 +93,46 @@ def test_random_case(cuda, oracle, i):
     else:
         got, _ = run_gpu(op, x, result, cuda, **kw)
     parity(oracle, op, x, got, result, what, **kw)
+
+
+N_LAMBERT = 40
+
+
+@pytest.mark.parametrize("i", range(N_LAMBERT))
+def test_random_lambert_map_case(cuda, oracle, i):
+    """Seeded random cases of the two Lambert-map operators (biased top-k
+    entropy, two-block entropy), with the biased one held to parity on the
+    columns where the reference's uncapped solve settles (and to a root
+    elsewhere) as in tests/test_prox_gpu.py."""
+    from tests.test_prox_gpu import entbias_is_root, entbias_settled
+    rng = np.random.default_rng(5000 + i)
+    op = "topk_entropy_biased" if i % 2 == 0 else "two_entropy"
+    m = int(np.clip(int(rng.choice([64, 100, 200, 256, 1000, 1024])) + rng.integers(-2, 2), 2, 2048))
+    n = int(rng.integers(1, 120))
+    dtype, result = DTYPES[int(rng.integers(0, len(DTYPES)))]
+    alpha = float(rng.choice([0.5, 1.0, 2.0]))
+    family = int(rng.integers(0, 3))
+    if family == 0:
+        x = inputs.normal(n, m, dtype, 6000 + i, 2.0)
+    elif family == 1:
+        x = inputs.mixed_signs(n, m, dtype, 6000 + i, -2, 2)
+    else:
+        x = inputs.uniform(n, m, dtype, 6000 + i, -10.0, 10.0)
+    what = f"case {i}: {op} m={m} n={n} {x.dtype.name}->{'f32' if result == 0 else 'f64'} alpha={alpha}"
+    print(what, flush=True)
+    if op == "topk_entropy_biased":
+        k = int(min(rng.choice([1, 2, 5]), m))
+        keep = entbias_settled(oracle, x, alpha, result)
+        got, thr = run_gpu(op, x, result, cuda, k=k, alpha=alpha)
+        parity(oracle, op, x, got, result, what + f" k={k}", nthreads=8, keep=keep, k=k,
+               alpha=alpha)
+        if k == 1 and not keep.all():
+            assert entbias_is_root(oracle, x[~keep], alpha, result, thr[~keep, 0]).all(), what
+    else:
+        kw = dict(alpha=alpha)
+        if rng.random() < 0.5:
+            kw["col_p"] = rng.integers(1, min(m - 1, 7) + 1, n)
+        else:
+            kw["p"] = int(rng.integers(1, m))
+        got, _ = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, what, nthreads=8, **kw)
