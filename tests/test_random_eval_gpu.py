@@ -114,3 +114,65 @@ def test_random_scores_gemm(cuda, i):
     bound = np.sqrt(d) * eps * (np.abs(X).astype(np.float64) @ np.abs(W).astype(np.float64).T)
     err = np.abs(got - want)
     assert (err <= 4 * bound + 1e-30).all(), f"case {i}: max err/bound {(err / (bound + 1e-30)).max():.2f}"
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_recompute_primal(cuda, i):
+    """W = W0 + X A' (eval/core.h:148-182) for random n, m (both GEMM tile
+    widths), d, fp32/fp64, with and without W0, against float64 within the
+    n-term dot bound of test_eval_gpu.test_recompute_primal."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(7000 + i)
+    n = int(rng.integers(1, 1500))
+    m = int(rng.choice([int(rng.integers(1, 1100)), int(rng.integers(129, 225))]))
+    d = int(rng.integers(1, 700))
+    dtype = np.float64 if i % 4 == 3 else np.float32
+    X = rng.standard_normal((n, d)).astype(dtype)
+    A = (rng.standard_normal((n, m)) * 0.1).astype(dtype)
+    W0 = (rng.standard_normal((m, d)) * 0.01).astype(dtype) if i % 2 else None
+    print(f"case {i}: n={n} m={m} d={d} {np.dtype(dtype).name} W0={W0 is not None}", flush=True)
+    W = sd.recompute_primal(torch.from_numpy(X).to(cuda), torch.from_numpy(A).to(cuda),
+                            None if W0 is None else torch.from_numpy(W0).to(cuda))
+    torch.cuda.synchronize()
+    W = W.cpu().numpy()
+    want = A.astype(np.float64).T @ X.astype(np.float64)
+    mag = np.abs(A.astype(np.float64)).T @ np.abs(X.astype(np.float64))
+    if W0 is not None:
+        want += W0
+        mag += np.abs(W0)
+    eps = np.finfo(dtype).eps
+    assert (np.abs(W - want) <= 4 * np.sqrt(n) * eps * mag + 1e-30).all(), f"case {i}"
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_eval_kernel(cuda, oracle, i):
+    """Kernel-input evaluation (scores_i = A K_i) for random n_train, n
+    (training set or test set), m and objectives: the per-example losses
+    against the oracle's evaluation of the float64 scores' rounding, as the
+    fixed cases in test_eval_gpu do."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(8000 + i)
+    n_train = int(rng.integers(2, 600))
+    test = i % 3 == 2
+    n = int(rng.integers(1, 400)) if test else n_train
+    m = int(rng.choice([3, 10, 64, 200, int(rng.integers(2, 1025))]))
+    objs = [("l2_entropy", 1.0, 1.0, 1), ("l2_hinge_topk_smooth", 1.0, 1.0, int(min(3, m - 1)))]
+    K = rng.standard_normal((n, n_train)).astype(np.float32) * 0.1
+    A = (rng.standard_normal((n_train, m)) * 0.05).astype(np.float32)
+    y = rng.integers(0, m, n)
+    print(f"case {i}: n_train={n_train} n={n} m={m} test={test}", flush=True)
+    recs, acc, pe = sd.eval_kernel(objs, torch.from_numpy(K).to(cuda), torch.from_numpy(A).to(cuda),
+                                   y, per_example=True, test=test)
+    torch.cuda.synchronize()
+    pe = pe.cpu().numpy()
+    # The GPU's scores: the same contraction, recomputed here to feed the oracle.
+    S = sd.scores(torch.from_numpy(K).to(cuda),
+                  torch.from_numpy(np.ascontiguousarray(A.T)).to(cuda)).cpu().numpy()
+    o_recs, o_acc, o_pe = oracle.eval_scores(oracle_objs(objs), S, None, y, result=F32,
+                                             per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), S, None, y, result=LONG_DOUBLE,
+                                    per_example=True)
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], RTOL[F32], f"case {i} primal", x_pe[:, :, 0])
+    assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n), f"case {i}: accuracy"
