@@ -175,6 +175,60 @@ class Library:
             return np.array([self._lw32(float(v)) for v in np.ravel(x)], dtype=np.float32)
         return np.array([self._lw64(float(v)) for v in np.ravel(x)], dtype=np.float64)
 
+    # Only the reference shim has these three.
+    def evaluate_dataset(self, objs, X, W, A, labels, offsets=None, W0=None, result=None,
+                         nthreads=1):
+        """The reference's evaluate_dataset (solver/eval.h:15-51) over a
+        feature input: X (n, d), W and W0 (m, d), A (n, m), all C-contiguous
+        (the reference's column-major d x n, d x m, m x n).  A is swapped in
+        place and restored, as the reference does.  Returns (records, accuracy)."""
+        n, d = X.shape
+        m = W.shape[0]
+        data = _dt(X)
+        result = data if result is None else result
+        objarr = make_objectives(objs)
+        recs = (EvalRecord * len(objs))()
+        acc = np.zeros(m, dtype=np.float64)
+        labels = np.ascontiguousarray(labels, dtype=np.int64)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
+        f = self.lib.ref_evaluate_dataset
+        f.restype = ctypes.c_int
+        rc = f(objarr, ctypes.c_int(len(objs)), ctypes.c_int(data), ctypes.c_int(result),
+               ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+               ctypes.c_void_p(X.ctypes.data), ctypes.c_void_p(W.ctypes.data),
+               ctypes.c_void_p(W0.ctypes.data if W0 is not None else None),
+               ctypes.c_void_p(A.ctypes.data), ctypes.c_void_p(labels.ctypes.data),
+               ctypes.c_void_p(off.ctypes.data if off is not None else None), recs,
+               ctypes.c_void_p(acc.ctypes.data), ctypes.c_int(nthreads))
+        if rc != 0:
+            raise RuntimeError(f"ref_evaluate_dataset failed: {rc}")
+        return [{f_: getattr(r, f_) for f_, _ in EvalRecord._fields_} for r in recs], acc
+
+    def blas_scores(self, X, W):
+        """The reference's scores W' x_i (eval/scores.h:9-27, cblas_sgemv) of
+        every example: X (n, d), W (m, d) float32 -> S (n, m)."""
+        n, d = X.shape
+        m = W.shape[0]
+        S = np.zeros((n, m), dtype=np.float32)
+        f = self.lib.ref_blas_sgemv_t
+        f.restype = None
+        for i in range(n):
+            f(ctypes.c_int(d), ctypes.c_int(m), ctypes.c_void_p(W.ctypes.data),
+              ctypes.c_void_p(X[i].ctypes.data), ctypes.c_void_p(S[i].ctypes.data))
+        return S
+
+    def blas_dot(self, x, y):
+        """The reference's sdca_blas_dot (math/blas.h:191-219)."""
+        x = np.ascontiguousarray(x)
+        y = np.ascontiguousarray(y, dtype=x.dtype)
+        if x.dtype == np.float32:
+            f = self.lib.ref_blas_sdot
+            f.restype = ctypes.c_float
+        else:
+            f = self.lib.ref_blas_ddot
+            f.restype = ctypes.c_double
+        return f(ctypes.c_int(x.size), ctypes.c_void_p(x.ctypes.data), ctypes.c_void_p(y.ctypes.data))
+
     # Only the restatement has these two.
     def scores(self, X, W, nthreads=1):
         """X: (n, d), W: (m, d) C-contiguous -> S (n, m)."""

@@ -4,10 +4,15 @@
 // never committed.  It exists to pin the oracle restatement and to time the
 // reference CPU path for the bench's cpu_baseline.
 //
-// What is not built: the BLAS-backed parts of the evaluation (the scores
-// gemv, the regularizer dot products and the smooth objectives' dual losses,
-// math/blas.h:191-319) need an external CBLAS library, which this build does
-// not link; those entries report NaN and are pinned by closed forms instead.
+// The BLAS-backed parts of the evaluation (the scores gemv, the regularizer
+// dot products and the smooth objectives' dual losses, math/blas.h:191-319)
+// go through the reference's own CBLAS prototypes (include/cblas.h, selected
+// by -DBLAS_DEFAULT_LOCAL_HEADER, blas.h:15-16) to Intel MKL's single dynamic
+// library (libmkl_rt, LP64: blas_int = int as blas.h:29-30 expects), the
+// reference's first-choice BLAS (cmake/SelectBLAS.cmake:34-89).  MKL runs
+// with its sequential threading layer: the reference's evaluation is
+// single-threaded, and the harness-parallel timing splits examples over
+// std::threads instead.
 #include <cmath>
 #include <cstdint>
 #include <limits>
@@ -15,6 +20,8 @@
 #include <vector>
 
 #include "sdca/prox.h"
+#include "sdca/solver/context.h"
+#include "sdca/solver/eval.h"
 #include "sdca/solver/eval/dual.h"
 #include "sdca/solver/eval/primal.h"
 #include "sdca/solver/eval/types.h"
@@ -325,11 +332,11 @@ int eval_impl(const sdca_objective* objs, int n_obj, int64_t m, int64_t n, const
       case SDCA_OBJ_HINGE_TOPK:
         SDCA_REF_EVAL(false, true, (sdca::l2_hinge_topk<D, R>(c, k))); break;
       case SDCA_OBJ_HINGE_TOPK_SMOOTH:
-        SDCA_REF_EVAL(false, false, (sdca::l2_hinge_topk_smooth<D, R>(c, g, k))); break;
+        SDCA_REF_EVAL(false, true, (sdca::l2_hinge_topk_smooth<D, R>(c, g, k))); break;
       case SDCA_OBJ_TOPK_HINGE:
         SDCA_REF_EVAL(false, true, (sdca::l2_topk_hinge<D, R>(c, k))); break;
       case SDCA_OBJ_TOPK_HINGE_SMOOTH:
-        SDCA_REF_EVAL(false, false, (sdca::l2_topk_hinge_smooth<D, R>(c, g, k))); break;
+        SDCA_REF_EVAL(false, true, (sdca::l2_topk_hinge_smooth<D, R>(c, g, k))); break;
       case SDCA_OBJ_ENTROPY:
         SDCA_REF_EVAL(false, true, (sdca::l2_entropy<D, R>(c))); break;
       case SDCA_OBJ_ENTROPY_TOPK:
@@ -337,7 +344,7 @@ int eval_impl(const sdca_objective* objs, int n_obj, int64_t m, int64_t n, const
       case SDCA_OBJ_MULTILABEL_HINGE:
         SDCA_REF_EVAL(true, true, (sdca::l2_multilabel_hinge<D, R>(c))); break;
       case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
-        SDCA_REF_EVAL(true, false, (sdca::l2_multilabel_hinge_smooth<D, R>(c, g))); break;
+        SDCA_REF_EVAL(true, true, (sdca::l2_multilabel_hinge_smooth<D, R>(c, g))); break;
       case SDCA_OBJ_MULTILABEL_ENTROPY:
         SDCA_REF_EVAL(true, true, (sdca::l2_multilabel_entropy<D, R>(c))); break;
       default: return SDCA_ERR_ARG_RANGE;
@@ -353,6 +360,168 @@ int eval_impl(const sdca_objective* objs, int n_obj, int64_t m, int64_t n, const
     std::partial_sum(hist.begin(), hist.end(), hist.begin());
     R coeff(1 / static_cast<R>(n));
     for (int64_t j = 0; j < m; ++j) accuracy[j] = static_cast<double>(hist[j] * coeff);
+  }
+  return 0;
+}
+
+
+// MKL's threading layer is chosen before its first call: sequential, so that
+// one reference evaluation runs on one core as the shipped solver does.
+extern "C" int MKL_Set_Threading_Layer(int);
+struct MklSequential {
+  MklSequential() { MKL_Set_Threading_Layer(1 /* MKL_THREADING_SEQUENTIAL */); }
+} g_mkl_sequential;
+
+// One eval_train record of the reference, in double.
+template <class Ev>
+void record_out(const Ev& e, sdca_eval_record* r) {
+  r->primal = static_cast<double>(e.primal);
+  r->dual = static_cast<double>(e.dual);
+  r->primal_loss = static_cast<double>(e.primal_loss);
+  r->dual_loss = static_cast<double>(e.dual_loss);
+  r->primal_regularizer = static_cast<double>(e.primal_regularizer);
+  r->dual_regularizer = static_cast<double>(e.dual_regularizer);
+}
+template <class R>
+double rank_of(const sdca::eval_train<R, sdca::multiclass_output>&) { return 0.0; }
+template <class R>
+double rank_of(const sdca::eval_train<R, sdca::multilabel_output>& e) {
+  return static_cast<double>(e.rank_loss);
+}
+template <class R>
+const std::vector<R>* accuracy_of(const sdca::eval_train<R, sdca::multiclass_output>& e) {
+  return &e.accuracy;
+}
+template <class R>
+const std::vector<R>* accuracy_of(const sdca::eval_train<R, sdca::multilabel_output>&) {
+  return nullptr;
+}
+
+sdca::multiclass_output make_out(std::false_type, int64_t m, const int64_t* labels,
+                                 const int64_t*, int64_t b, int64_t e) {
+  std::vector<sdca::size_type> lab(labels + b, labels + e);
+  return sdca::multiclass_output(static_cast<sdca::size_type>(m), lab);
+}
+sdca::multilabel_output make_out(std::true_type, int64_t m, const int64_t* labels,
+                                 const int64_t* offsets, int64_t b, int64_t e) {
+  std::vector<sdca::size_type> lab(labels + offsets[b], labels + offsets[e]);
+  std::vector<sdca::size_type> off;
+  for (int64_t i = b; i <= e; ++i)
+    off.push_back(static_cast<sdca::size_type>(offsets[i] - offsets[b]));
+  return sdca::multilabel_output(static_cast<sdca::size_type>(m), lab, off);
+}
+
+// The reference's whole evaluation pass, sdca::evaluate_dataset
+// (solver/eval.h:15-51), over examples [b, e) of a feature input: a
+// solver_context over that slice, with W as its primal variables (W0 as the
+// initial ones, prox mode) and A as its dual variables.  The reference swaps
+// entries of A and restores them (eval/dual.h:35-43): A is borrowed mutable.
+template <class D, class R, class Out, template <class, class> class Obj>
+void evaluate_slice(Obj<D, R> obj, int64_t d, int64_t m, int64_t b, int64_t e, const D* X,
+                    D* W, const D* W0, D* A, const int64_t* labels, const int64_t* offsets,
+                    sdca_eval_record* rec, std::vector<double>* acc) {
+  typedef sdca::solver_context<D, R, sdca::feature_input, Out, Obj> Ctx;
+  typename Ctx::train_set_type set(
+      sdca::feature_input<D>(static_cast<sdca::size_type>(d),
+                             static_cast<sdca::size_type>(e - b), X + d * b),
+      make_out(std::integral_constant<bool, std::is_same<Out, sdca::multilabel_output>::value>(),
+               m, labels, offsets, b, e));
+  Ctx ctx(std::move(set), std::move(obj), A + m * b, W, W0);
+  sdca::solver_scratch<D, sdca::feature_input> scratch;
+  scratch.scores.resize(static_cast<size_t>(m));
+  sdca::evaluate_dataset(ctx, ctx.train, scratch);
+  const auto& ev = ctx.train.evals.back();
+  record_out(ev, rec);
+  rec->rank_loss = rank_of(ev);
+  if (acc) {
+    const auto* a = accuracy_of(ev);
+    if (a) acc->assign(a->begin(), a->end());
+  }
+}
+
+// evaluate_dataset on nthreads slices of the examples (harness-parallel:
+// each thread runs the reference on its own slice; nthreads = 1 is the
+// reference as shipped).  The slices' records are merged as one pass would
+// have formed them: loss terms add, regularizers are those of the whole W,
+// accuracies and rank losses are averaged with the slices' weights.
+template <class D, class R, class Out, template <class, class> class Obj>
+void evaluate_all(const Obj<D, R>& obj, int64_t d, int64_t m, int64_t n, const D* X, D* W,
+                  const D* W0, D* A, const int64_t* labels, const int64_t* offsets,
+                  sdca_eval_record* rec, double* accuracy, int nthreads) {
+  if (nthreads < 1) nthreads = 1;
+  if (n < 2 * nthreads) nthreads = 1;
+  const int64_t chunk = (n + nthreads - 1) / nthreads;
+  std::vector<sdca_eval_record> part(static_cast<size_t>(nthreads));
+  std::vector<std::vector<double>> acc(static_cast<size_t>(nthreads));
+  std::vector<int64_t> lo(static_cast<size_t>(nthreads)), hi(static_cast<size_t>(nthreads));
+  std::vector<std::thread> pool;
+  for (int w = 0; w < nthreads; ++w) {
+    lo[w] = std::min(n, w * chunk);
+    hi[w] = std::min(n, lo[w] + chunk);
+    auto job = [&, w]() {
+      if (lo[w] < hi[w])
+        evaluate_slice<D, R, Out, Obj>(obj, d, m, lo[w], hi[w], X, W, W0, A, labels, offsets,
+                                       &part[w], &acc[w]);
+    };
+    if (nthreads == 1) job();
+    else pool.emplace_back(job);
+  }
+  for (auto& t : pool) t.join();
+  if (nthreads == 1) {
+    *rec = part[0];
+    if (accuracy && !acc[0].empty())
+      for (int64_t j = 0; j < m; ++j) accuracy[j] = acc[0][j];
+    return;
+  }
+  sdca_eval_record r = part[0];
+  r.primal_loss = r.dual_loss = r.rank_loss = 0;
+  std::vector<double> a(static_cast<size_t>(m), 0.0);
+  for (int w = 0; w < nthreads; ++w) {
+    if (lo[w] >= hi[w]) continue;
+    const double wt = static_cast<double>(hi[w] - lo[w]) / static_cast<double>(n);
+    r.primal_loss += part[w].primal_loss;
+    r.dual_loss += part[w].dual_loss;
+    r.rank_loss += part[w].rank_loss * wt;
+    for (size_t j = 0; j < acc[w].size(); ++j) a[j] += acc[w][j] * wt;
+  }
+  r.primal = r.primal_loss + r.primal_regularizer;
+  r.dual = r.dual_loss - r.dual_regularizer;
+  *rec = r;
+  if (accuracy && !acc[0].empty())
+    for (int64_t j = 0; j < m; ++j) accuracy[j] = a[j];
+}
+
+#define SDCA_REF_EVALUATE(OUT, OBJ)                                                         \
+  evaluate_all<D, R, OUT>(OBJ, d, m, n, X, W, W0, A, labels, offsets, &rec[o],            \
+                          o == 0 ? accuracy : nullptr, nthreads)
+
+template <class D, class R>
+int evaluate_impl(const sdca_objective* objs, int n_obj, int64_t d, int64_t m, int64_t n,
+                  const D* X, D* W, const D* W0, D* A, const int64_t* labels,
+                  const int64_t* offsets, sdca_eval_record* rec, double* accuracy,
+                  int nthreads) {
+  typedef sdca::multiclass_output MC;
+  typedef sdca::multilabel_output ML;
+  for (int o = 0; o < n_obj; ++o) {
+    const sdca_objective& ob = objs[o];
+    const R c = static_cast<R>(ob.c), g = static_cast<R>(ob.gamma);
+    const sdca::size_type k = static_cast<sdca::size_type>(ob.k);
+    switch (ob.kind) {
+      case SDCA_OBJ_HINGE_TOPK: SDCA_REF_EVALUATE(MC, (sdca::l2_hinge_topk<D, R>(c, k))); break;
+      case SDCA_OBJ_HINGE_TOPK_SMOOTH:
+        SDCA_REF_EVALUATE(MC, (sdca::l2_hinge_topk_smooth<D, R>(c, g, k))); break;
+      case SDCA_OBJ_TOPK_HINGE: SDCA_REF_EVALUATE(MC, (sdca::l2_topk_hinge<D, R>(c, k))); break;
+      case SDCA_OBJ_TOPK_HINGE_SMOOTH:
+        SDCA_REF_EVALUATE(MC, (sdca::l2_topk_hinge_smooth<D, R>(c, g, k))); break;
+      case SDCA_OBJ_ENTROPY: SDCA_REF_EVALUATE(MC, (sdca::l2_entropy<D, R>(c))); break;
+      case SDCA_OBJ_ENTROPY_TOPK: SDCA_REF_EVALUATE(MC, (sdca::l2_entropy_topk<D, R>(c, k))); break;
+      case SDCA_OBJ_MULTILABEL_HINGE: SDCA_REF_EVALUATE(ML, (sdca::l2_multilabel_hinge<D, R>(c))); break;
+      case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
+        SDCA_REF_EVALUATE(ML, (sdca::l2_multilabel_hinge_smooth<D, R>(c, g))); break;
+      case SDCA_OBJ_MULTILABEL_ENTROPY:
+        SDCA_REF_EVALUATE(ML, (sdca::l2_multilabel_entropy<D, R>(c))); break;
+      default: return SDCA_ERR_ARG_RANGE;
+    }
   }
   return 0;
 }
@@ -390,6 +559,37 @@ int ref_eval_scores(const sdca_objective* objs, int n_obj, int data, int result,
     return eval_impl<double, double>(objs, n_obj, m, n, static_cast<const double*>(S),
         static_cast<const double*>(A), labels, offsets, preg, dreg, rec, accuracy, per_example);
   return SDCA_ERR_PRECISION;
+}
+
+// The reference's evaluate_dataset over a feature input (see evaluate_all).
+// X: d x n, W (and W0, NULL outside prox mode): d x m, A: m x n (borrowed
+// mutable, restored), all column-major; offsets NULL for multiclass labels.
+int ref_evaluate_dataset(const sdca_objective* objs, int n_obj, int data, int result,
+                         int64_t d, int64_t m, int64_t n, const void* X, void* W,
+                         const void* W0, void* A, const int64_t* labels,
+                         const int64_t* offsets, sdca_eval_record* rec, double* accuracy,
+                         int nthreads) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return evaluate_impl<float, float>(objs, n_obj, d, m, n, static_cast<const float*>(X),
+        static_cast<float*>(W), static_cast<const float*>(W0), static_cast<float*>(A), labels,
+        offsets, rec, accuracy, nthreads);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return evaluate_impl<float, double>(objs, n_obj, d, m, n, static_cast<const float*>(X),
+        static_cast<float*>(W), static_cast<const float*>(W0), static_cast<float*>(A), labels,
+        offsets, rec, accuracy, nthreads);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return evaluate_impl<double, double>(objs, n_obj, d, m, n, static_cast<const double*>(X),
+        static_cast<double*>(W), static_cast<const double*>(W0), static_cast<double*>(A), labels,
+        offsets, rec, accuracy, nthreads);
+  return SDCA_ERR_PRECISION;
+}
+
+// The reference's BLAS dot (math/blas.h:191-219) and the scores of one
+// example (eval/scores.h:9-27), for the pins of the restatement's models.
+float ref_blas_sdot(int n, const float* x, const float* y) { return sdca::sdca_blas_dot(n, x, y); }
+double ref_blas_ddot(int n, const double* x, const double* y) { return sdca::sdca_blas_dot(n, x, y); }
+void ref_blas_sgemv_t(int d, int m, const float* W, const float* x, float* s) {
+  sdca::sdca_blas_gemv(d, m, W, x, s, CblasTrans);
 }
 
 double ref_lambert_w_exp_f64(double x) { return sdca::lambert_w_exp(x); }

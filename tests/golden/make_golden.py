@@ -5,7 +5,8 @@ compiled from /root/reference's own headers by oracle/Makefile).  Every
 fixture holds seeded inputs and the reference's outputs: projected columns
 and threshold records for each prox operator and (Data, Result) pair, and the
 per-example primal losses, dual losses and top-k histogram of the evaluation
-objectives.  tests/test_golden.py checks the oracle against them, so the
+objectives, and whole evaluate_dataset passes (solver/eval.h:15-51) over a
+small feature input with the scores the reference's CBLAS (MKL) produced.  tests/test_golden.py checks the oracle against them, so the
 oracle stays pinned where the reference tree is absent.
 
     python tests/golden/make_golden.py
@@ -101,6 +102,37 @@ def main():
         out[key + "/labels"], out[key + "/offsets"] = np.array(lab), np.array(off)
         out[key + "/primal"], out[key + "/dual"] = pe[:, :, 0], pe[:, :, 1]
         out[key + "/rank"] = np.array([r["rank_loss"] for r in recs])
+    fields = ["primal", "dual", "primal_loss", "dual_loss", "primal_regularizer",
+              "dual_regularizer", "rank_loss"]
+    for tag, dtype, result in DTYPES:
+        for ml in (False, True):
+            rng = np.random.default_rng(700 + ml)
+            n, d, m = 96, 48, 24
+            X = rng.standard_normal((n, d)).astype(dtype)
+            W = (rng.standard_normal((m, d)) * 0.5).astype(dtype)
+            W0 = (rng.standard_normal((m, d)) * 0.1).astype(dtype)
+            A = (rng.standard_normal((n, m)) * 0.05).astype(dtype)
+            key = f"eval/dataset/{'multilabel' if ml else 'multiclass'}/{tag}"
+            if ml:
+                off, lab = [0], []
+                for _ in range(n):
+                    p = int(rng.integers(1, 6))
+                    lab += sorted(rng.choice(m, p, replace=False).tolist())
+                    off.append(len(lab))
+                lab, off = np.array(lab), np.array(off)
+                out[key + "/labels"], out[key + "/offsets"] = lab, off
+                objs = ML
+            else:
+                lab, off = rng.integers(0, m, n), None
+                out[key + "/y"] = lab
+                objs = MC
+            recs, acc = ref.evaluate_dataset(objs, X, W, A, lab, off, W0=W0, result=result)
+            out[key + "/X"], out[key + "/W"], out[key + "/W0"], out[key + "/A"] = X, W, W0, A
+            out[key + "/records"] = np.array([[r[f] for f in fields] for r in recs])
+            if not ml:
+                out[key + "/acc"] = acc
+            if dtype == np.float32:
+                out[key + "/S"] = ref.blas_scores(X, W)
     path = os.path.join(HERE, "reference_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path}: {len(out)} arrays, {os.path.getsize(path) / 1024:.0f} KiB")

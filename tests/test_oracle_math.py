@@ -343,38 +343,59 @@ def test_eval_multilabel_closed_forms(oracle):
     assert abs(recs[0]["rank_loss"] - rank / n) <= 1e-12
 
 
-def test_eval_smooth_dual_losses(oracle):
-    """The three dual losses whose reference code calls CBLAS (so the
-    reference shim cannot evaluate them here): A_0 - gamma/(2c) sum_{j>=1} A_j^2
-    for both smooth multiclass hinges (l2_hinge_topk.h:182-192,
-    l2_topk_hinge.h:186-196) and (sum_P A - sum_N A - (gamma/c) |A|^2) / 2 for
-    the smooth multilabel hinge (l2_multilabel_hinge.h:194-208), with the
-    ground truth / positives moved to the front first (data/output.h:42-71,
-    120-165)."""
-    rng = np.random.default_rng(102)
-    n, m, c, gamma = 150, 30, 1.7, 0.6
-    S = rng.standard_normal((n, m))
-    A = rng.standard_normal((n, m)) * 0.1
+@pytest.mark.parametrize("c,gamma,k", [(1.0, 1.0, 5), (1.7, 0.6, 3), (0.3, 2.5, 1)])
+def test_eval_smooth_fenchel_young(oracle, c, gamma, k):
+    """Fenchel-Young equality for the three smooth objectives: at the optimal
+    dual variables a = -grad of the example's loss, the loss equals
+    dual_loss(a) - <a, s> (SDCA's primal and dual share it:
+    c L(s) + c L*(-a/c) = -<a, s>).  With p = the projection of the primal
+    loss (top-k simplex rhs = gamma for l2_hinge_topk_smooth, knapsack_le
+    [0, gamma/k], gamma for l2_topk_hinge_smooth, two-simplex rhs = gamma on
+    (1/2 - s_P, 1/2 + s_N) for l2_multilabel_hinge_smooth), the gradient is
+    a_j = -(c/gamma) p_j, a_y = (c/gamma) sum p (multiclass) and
+    a_P = (c/gamma) p_P, a_N = -(c/gamma) p_N (multilabel).  A dropped term,
+    a wrong sign or a wrong gamma/c factor in either loss breaks it."""
+    rng = np.random.default_rng(int(10 * c + k))
+    n, m = 120, 30
+    S = rng.standard_normal((n, m)) * 1.5
     y = rng.integers(0, m, n)
-    objs = [("hinge_topk_smooth", c, gamma, 3), ("topk_hinge_smooth", c, gamma, 3)]
-    _, _, pe = oracle.eval_scores(objs, S, A, y, result=F64, per_example=True)
-    for i in range(n):
-        rest = np.delete(A[i], y[i])
-        want = A[i, y[i]] - gamma / (2 * c) * (rest @ rest)
-        assert abs(pe[i, 0, 1] - want) <= 1e-13 and abs(pe[i, 1, 1] - want) <= 1e-13
+    coef = c / gamma
+    objs = [("hinge_topk_smooth", c, gamma, k), ("topk_hinge_smooth", c, gamma, k)]
+    _, _, pe = oracle.eval_scores(objs, S, np.zeros_like(S), y, result=F64, per_example=True)
+    for o, (op, kw) in enumerate([("topk_simplex", dict(k=k, rhs=gamma)),
+                                  ("knapsack_le", dict(lo=0.0, hi=gamma / k, rhs=gamma))]):
+        A = np.zeros((n, m))
+        for i in range(n):
+            rest = np.delete(np.arange(m), y[i])
+            h = 1.0 + S[i, rest] - S[i, y[i]]
+            p, _ = prox(oracle, op, h, **kw)
+            A[i, rest] = -coef * p[0]
+            A[i, y[i]] = coef * p[0].sum()
+        _, _, pd = oracle.eval_scores([objs[o]], S, A, y, result=F64, per_example=True)
+        lhs = coef * pe[:, o, 0]
+        rhs = pd[:, 0, 1] - (A * S).sum(axis=1)
+        assert np.abs(lhs - rhs).max() <= 1e-12 * max(1.0, np.abs(lhs).max()), objs[o][0]
+        assert (lhs > 0).mean() > 0.5  # not a trivial all-zero check
     off, lab = [0], []
     for _ in range(n):
         p = int(rng.integers(1, 6))
         lab += sorted(rng.choice(m, p, replace=False).tolist())
         off.append(len(lab))
-    _, _, pe = oracle.eval_scores([("multilabel_hinge_smooth", c, gamma, 1)], S, A, lab, off,
-                                  result=F64, per_example=True)
+    ml = [("multilabel_hinge_smooth", c, gamma, 1)]
+    _, _, pe = oracle.eval_scores(ml, S, np.zeros_like(S), lab, off, result=F64, per_example=True)
+    A = np.zeros((n, m))
     for i in range(n):
         P = np.array(lab[off[i]:off[i + 1]])
-        mask = np.zeros(m, bool)
-        mask[P] = True
-        want = 0.5 * (A[i, mask].sum() - A[i, ~mask].sum() - gamma / c * (A[i] @ A[i]))
-        assert abs(pe[i, 0, 1] - want) <= 1e-13
+        N = np.setdiff1d(np.arange(m), P)
+        v = np.concatenate([0.5 - S[i, P], 0.5 + S[i, N]])
+        pv, _ = prox(oracle, "two_simplex", v, p=len(P), rhs=gamma)
+        A[i, P] = coef * pv[0, :len(P)]
+        A[i, N] = -coef * pv[0, len(P):]
+    _, _, pd = oracle.eval_scores(ml, S, A, lab, off, result=F64, per_example=True)
+    lhs = coef * pe[:, 0, 0]
+    rhs = pd[:, 0, 1] - (A * S).sum(axis=1)
+    assert np.abs(lhs - rhs).max() <= 1e-12 * max(1.0, np.abs(lhs).max())
+    assert (lhs > 0).mean() > 0.5
 
 
 # ---------------------------------------------------------------------------
