@@ -94,7 +94,12 @@ void sdca_prox_params_default(sdca_prox_params* params);
  *   result: the reference's Result template argument (internal precision);
  *   in/out: m*n elements each; out == in works in place like the reference;
  *   col_p:  for the two-block operators, optional per-column split p (n int64
- *           values in [1, m-1]); NULL uses params->p for every column;
+ *           values in [1, m-1]); NULL uses params->p for every column.  Host
+ *           values (SDCA_HOST_PTR) outside that range are rejected with
+ *           SDCA_ERR_ARG_RANGE; device values are not read back by the host
+ *           (the call stays asynchronous): the kernels bring an out-of-range
+ *           value into [1, m-1], so no access leaves the column, and that
+ *           column's result is the projection for the clamped split;
  *   thresholds: optional, n records (2n for the two-block operator) with the
  *           computed thresholds, in double.
  * The reference's `aux` scratch has no counterpart: scratch lives in

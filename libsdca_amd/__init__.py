@@ -206,11 +206,14 @@ def _stream_ptr():
 
 
 def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
-         alpha=1.0, k=1, p=1, col_p=None, thresholds=False):
+         alpha=1.0, k=1, p=1, col_p=None, thresholds=False, check_col_p=True):
     """Batched prox over the rows of A (each row is one column of the
     reference's dim x n matrix).  Returns out (A itself when out is None) and,
     with thresholds=True, an (n, 3) (or (2n, 3) for the two-block operators) array of
-    (t, lo, hi) per column/block."""
+    (t, lo, hi) per column/block.  A device col_p is checked against
+    [1, dim - 1] here (one synchronisation) unless check_col_p=False, for
+    callers that validated it already (the kernels clamp it into range
+    either way)."""
     lib = library()
     code = OPS[op] if isinstance(op, str) else int(op)
     data = _dtype_code(A)
@@ -242,6 +245,10 @@ def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
             cp = torch.as_tensor(col_p, dtype=torch.int64, device=A.device).contiguous().reshape(-1)
             if cp.shape[0] != n:
                 raise SdcaError(2, f"col_p has {cp.shape[0]} entries for {n} columns")
+            if check_col_p and n > 0:
+                lo_p, hi_p = torch.aminmax(cp)
+                if int(lo_p) < 1 or int(hi_p) > m - 1:
+                    raise SdcaError(2, f"col_p must lie in [1, {m - 1}] (got {int(lo_p)}..{int(hi_p)})")
         check(lib.sdca_prox(code, data, res, m, n, A.data_ptr(), out.data_ptr(),
                             ctypes.byref(params), cp.data_ptr() if cp is not None else None,
                             thr.data_ptr() if thr is not None else None, 0, _stream_ptr()))

@@ -87,6 +87,14 @@ __device__ inline double dmin(double a, double b) { return fmin(a, b); }
 
 // std::max(lo, std::min(x, hi)) with the argument order of proxdef.h:177:
 // min(x, hi) returns x unless hi < x; max(lo, y) returns lo unless lo < y.
+// The split p of a two-block column: the C ABI requires 1 <= p <= m - 1;
+// device-resident per-column splits are not read back by the host, so an
+// out-of-range value is brought into that range here and no access leaves
+// the column or its LDS copy.
+__device__ inline int clamp_split(int64_t p, int m) {
+  return static_cast<int>(p < 1 ? 1 : (p > m - 1 ? m - 1 : p));
+}
+
 template <class D>
 __device__ inline D clamp_ref(D x, D lo, D hi) {
   D y = (hi < x) ? hi : x;

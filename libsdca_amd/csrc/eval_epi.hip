@@ -36,6 +36,44 @@ struct SetStats {
   int n_u, n_m;
 };
 
+// The threshold of a knapsack with lo = 0 formed from its final sets,
+// t = (sum_M h + |U| hi - rhs) / |M| (knapsack_eq.h:87-106 with
+// SDCA_ACCURATE_MATH): the iteration's own t carries the rounding of its
+// incremental updates, which the loss would inherit.  Without free values t
+// is any point between the sets and the loss does not depend on it.
+template <class R>
+__device__ inline R set_threshold(R t_iter, R hi, R rhs, const SetStats<R>& st) {
+  if (st.n_m == 0) return t_iter;
+  return (st.sum_m + hi * static_cast<R>(st.n_u) - rhs) / static_cast<R>(st.n_m);
+}
+
+// <h, p> - <p, p> / 2 at p = clamp(h - t, 0, hi), the projection of a knapsack
+// whose sum constraint sum(p) = rhs is active, formed entry by entry and
+// minus t (sum(p) - rhs).  The loss as a function of t has slope -|M| t at
+// the root (|M| the free count), so the rounding of t alone (half an ulp of
+// t ~ 1 in float, times |M| ~ 200 at m = 1000) would move it by 1e-5; the
+// added term is zero at the exact root and cancels that slope, leaving an
+// error of order |M| dt^2.  The sums over (h, p), each term at most hi in
+// size, avoid the cancellation of the set-sum form below (t sum_M h against
+// sum_M h^2, both ~|M|).
+template <int G, int C, class D, class R>
+__device__ inline R clamp_loss(const D (&h)[C], R t, R hi, R rhs) {
+  R hp = 0, pp = 0, sp = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const R x = static_cast<R>(h[c]);
+    const bool ok = x > -num<R>::inf();
+    const R p = ok ? clamp_ref(x - t, R(0), hi) : R(0);
+    hp += ok ? x * p : R(0);
+    pp += p * p;
+    sp += p;
+  }
+  hp = group_sum<G>(hp);
+  pp = group_sum<G>(pp);
+  sp = group_sum<G>(sp);
+  return hp - R(0.5) * pp - t * (sp - rhs);
+}
+
 // <h, p> - <p, p> / 2 from the threshold sets with lo = 0
 // (dot_x_prox - dot_prox_prox / 2, proxdef.h:332-370).
 template <class R>
@@ -148,7 +186,7 @@ __device__ inline bool smooth_topk_hinge(const D (&h)[C], int mp, int nvalid, in
   // The candidate cut used by topk_knapsack: values at or below it are in L.
   const R cut = kth - hi - (fabs(kth) + hi) * (R(16) * num<R>::eps());
   const SetStats<R> ss = knap_sets<G, C, D, R>(h, st, cut);
-  loss = smooth_loss(st.t, hi, ss);
+  loss = clamp_loss<G, C, D, R>(h, set_threshold(st.t, hi, gamma, ss), hi, gamma);
   return true;
 }
 
@@ -192,7 +230,7 @@ __device__ inline R smooth_topk_hinge_beta(const D (&h)[C], int mp, int k, R gam
   total = group_sum<G>(total);
   KnapState<R> st = knapsack_eq_regs<G, C, D, R>(h, mp, C, total, lo, hi, rhs);
   const SetStats<R> ss = knap_sets<G, C, D, R>(h, st, -num<R>::inf());
-  return smooth_loss(st.t, hi, ss);
+  return clamp_loss<G, C, D, R>(h, set_threshold(st.t, hi, rhs, ss), hi, rhs);
 }
 
 template <int G, int C, class D, class R>

@@ -422,7 +422,7 @@ twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_
   const D map_a = D(1) / static_cast<D>(alpha);  // a_lambert_w_exp_map (functor.h:33-38)
   for (int64_t j = static_cast<int64_t>(blockIdx.x) * waves + wave; j < n;
        j += static_cast<int64_t>(gridDim.x) * waves) {
-    const int p = static_cast<int>(col_p ? col_p[j] : p_all);
+    const int p = clamp_split(col_p ? col_p[j] : p_all, m);
     const D* col = in + j * m64;
     for (int i = lane; i < m; i += 64) s[i] = col[i];
     wave_lds_sync();

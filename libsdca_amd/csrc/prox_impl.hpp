@@ -87,7 +87,8 @@ __device__ inline R total_sum(const D (&v)[C], int nvalid) {
 // ---------------------------------------------------------------------------
 template <class R>
 struct KnapState {
-  R t;
+  R t;               // the iteration's last t (knapsack_eq.h:79-84): branch tests use it
+  R t_acc;           // t recomputed from the final free set (the threshold applied)
   R lo_cut, hi_cut;  // fixed sets: x <= lo_cut at lo, x > hi_cut at hi
   R c_lo, c_hi;      // final candidate cuts inside the free interval
   int n_u;           // |U| = number at hi (fixed + final candidates)
@@ -135,6 +136,8 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
   };
   int mc = m - n_u0;
   R t = div_near(total - sum_u0 - rhs + static_cast<R>(n_u0) * hi, static_cast<R>(mc));
+  R t_acc = t;
+  bool have_acc = false;
   KnapState<R> st;
   st.lo_cut = -num<R>::inf();
   st.hi_cut = hi_cut0;
@@ -174,6 +177,27 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
       st.c_hi = c_hi;
       st.n_u += n_hi;
       st.sum_u += s_hi;
+      // The iteration's t carries the rounding of its incremental updates
+      // (m t - sum + n hi is a difference of large sums, then divided by the
+      // shrinking free count: in float at m = 100 that is ~1e-5 of t).  The
+      // threshold applied is formed once more from the final free set F,
+      // t = (sum_F a + |U| hi + |L| lo - rhs) / |F|, as the reference's
+      // SDCA_ACCURATE_MATH build does (knapsack_eq.h:87-106, Lemma 5.3 of
+      // Kiwiel's paper); the branch tests keep the iteration's t.
+      const int n_f = mc - n_lo - n_hi;
+      if (n_f > 0) {
+        R s_f = 0;
+#pragma unroll UW
+        for (int c = 0; c < C; ++c) {
+          const R wc = get(c);
+          s_f += (wc > c_lo && !(wc > c_hi)) ? wc : R(0);
+        }
+        s_f = group_sum<G>(s_f);
+        const int n_l = m - st.n_u - n_f;
+        t_acc = div_near(s_f + static_cast<R>(st.n_u) * hi + static_cast<R>(n_l) * lo - rhs,
+                         static_cast<R>(n_f));
+        have_acc = true;
+      }
       break;
     }
     R next;
@@ -201,6 +225,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
     }
   }
   st.t = t;
+  st.t_acc = have_acc ? t_acc : t;
   return st;
 }
 
@@ -314,7 +339,7 @@ __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
                                                           R(1) / pp.rho),
                          lo, hi);
   }
-  return make_thr<R>(st.t, lo, hi);
+  return make_thr<R>(st.t_acc, lo, hi);
 }
 
 // ---------------------------------------------------------------------------
@@ -604,7 +629,7 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
       if (lt) return cone_search_u0<G, C, D, R>(v, K, largest);
     }
   }
-  return make_thr<R>(st.t, R(0), hi);
+  return make_thr<R>(st.t_acc, R(0), hi);
 }
 
 // ---------------------------------------------------------------------------
@@ -1237,7 +1262,7 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   } else if constexpr (FAM == FAM_TOPKENT) {
     th = topkent_family<G, C, D, R>(v, m, nvalid, pp);
   } else {
-    if (col_p && active) p = static_cast<int>(col_p[j]);
+    if (col_p && active) p = clamp_split(col_p[j], m);
     th = two_family<G, C, D, R>(v, m, p, pp);
   }
 

@@ -81,6 +81,11 @@ __device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
     }
   }
   st.t = t;
+  // The threshold applied is formed once more from the final free range
+  // (knapsack_eq.h:87-106, SDCA_ACCURATE_MATH), as in the register kernel.
+  st.t_acc = (l > f) ? (sum_range<R>(s, f, l) + static_cast<R>(f) * hi +
+                        static_cast<R>(m - l) * lo - rhs) / static_cast<R>(l - f)
+                     : t;
   st.n_u = f;
   st.sum_u = sum_range<R>(s, 0, f);
   return st;
@@ -214,9 +219,9 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
     lo_out = lo;
     hi_out = hi;
     const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
-    const R t = knapsack_sorted<D, R>(s, m, lo, hi, rhs).t;
-    if (t >= rho * rhs - eps) {
-      t_out = t;
+    const KnapState<R> st = knapsack_sorted<D, R>(s, m, lo, hi, rhs);
+    if (st.t >= rho * rhs - eps) {
+      t_out = st.t_acc;
       return;
     }
     knapsack_le_biased_sorted<D, R>(s, m, lo, hi, rhs, rho, t_out, lo_out, hi_out);
@@ -239,7 +244,7 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
         return;
       }
     }
-    t_out = knapsack_sorted<D, R>(s, m, lo, hi, rhs).t;
+    t_out = knapsack_sorted<D, R>(s, m, lo, hi, rhs).t_acc;
     return;
   }
   const R K = static_cast<R>(k);
@@ -286,7 +291,7 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
       return;
     }
   }
-  t_out = st.t;
+  t_out = st.t_acc;
   hi_out = rhs / K;
 }
 
@@ -473,7 +478,7 @@ two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int6
   const int64_t count = all_columns ? n : static_cast<int64_t>(slow[0]);
   for (int64_t w = blockIdx.x; w < count; w += gridDim.x) {
     const int64_t j = all_columns ? w : static_cast<int64_t>(slow[2 + w]);
-    const int p = static_cast<int>(col_p ? col_p[j] : p_all);
+    const int p = clamp_split(col_p ? col_p[j] : p_all, m);
     const int q = m - p;
     const D* col = in + j * m64;
     for (int i = threadIdx.x; i < pow2; i += blockDim.x) {

@@ -11,9 +11,9 @@
 
 Tolerance for per-example losses, relative to max(1, |loss|): rtol = 1e-5
 when the arithmetic (Result) type or the data type is float and 1e-12 when
-both are double, plus the reference's own rounding error E, measured per
-batch as max |ref - exact| with "exact" the oracle in long double:
-|gpu - ref| <= rtol + 3 E and |gpu - exact| <= rtol + 2 E.  As for the prox
+both are double, plus the reference's own rounding error E_i of that example
+and objective, |ref - exact| / s with "exact" the oracle in long double:
+|gpu - ref| / s <= rtol + 3 E_i and |gpu - exact| / s <= rtol + 2 E_i.  As for the prox
 operators, E is needed because the smooth losses go through a Kiwiel
 projection of m - 1 values: in float the reference's own loss at m = 1000 is
 ~1e-2 away from the long-double value, and any other summation order rounds
@@ -75,21 +75,31 @@ LONG_DOUBLE = 2
 
 
 def compare_per_example(got, want, rtol, what, exact=None):
-    """Per objective (last axis): |got - want| / s <= rtol + 3 E, and with the
-    long-double values `exact`, |got - exact| / s <= rtol + 2 E."""
+    """Entry by entry (example i, objective o), with s = max(1, |want|) and
+    E_io = |want - exact| / s the reference's own error on that entry:
+    |got - want| / s <= rtol + 3 E_io and |got - exact| / s <= rtol + 2 E_io.
+    The count of entries above a flat rtol is printed."""
     scale = np.maximum(1.0, np.abs(want))
     err = np.abs(got - want) / scale
-    E = np.zeros(want.shape[-1])
+    E = np.zeros_like(want)
     if exact is not None:
-        E = np.nanmax(np.abs(want - exact) / scale, axis=0)
+        E = np.abs(want - exact) / scale
+        E = np.where(np.isnan(E), 0.0, E)
     ok = np.isnan(want) | (err <= rtol + 3 * E)
     bad = np.argwhere(~ok)
-    assert bad.size == 0, (f"{what}: {len(bad)} entries differ, max scaled err "
-                           f"{np.nanmax(err):.3e} (E per objective {E}); first {bad[0]}: got "
-                           f"{got[tuple(bad[0])]} want {want[tuple(bad[0])]}")
+    assert bad.size == 0, (f"{what}: {len(bad)} entries differ beyond rtol + 3 E_io, max scaled "
+                           f"err {np.nanmax(err):.3e}; first {bad[0]}: got "
+                           f"{got[tuple(bad[0])]} want {want[tuple(bad[0])]} "
+                           f"(E_io {E[tuple(bad[0])]:.3e})")
     if exact is not None:
-        e_gpu = np.nanmax(np.abs(got - exact) / scale, axis=0)
-        assert (e_gpu <= rtol + 2 * E).all(), f"{what}: GPU error vs exact {e_gpu} > rtol + 2E ({E})"
+        e_gpu = np.abs(got - exact) / scale
+        bad = np.argwhere(~(np.isnan(want) | (e_gpu <= rtol + 2 * E)))
+        assert bad.size == 0, (f"{what}: GPU error vs exact {e_gpu[tuple(bad[0])]:.3e} > rtol + 2 E_io "
+                               f"({E[tuple(bad[0])]:.3e}) in {len(bad)} entries")
+    over = int(np.count_nonzero(err[~np.isnan(want)] > rtol))
+    if over:
+        print(f"{what}: {over} of {err.size} entries above a flat {rtol:g}, each within "
+              f"rtol + 3 E_io")
 
 
 @pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float32, F64), (np.float64, F64)])

@@ -239,6 +239,89 @@ def test_c4_eval_full(cuda, oracle):
 
 
 @pytest.mark.timeout(300)
+def test_c4_scores_and_counts_vs_fp64(cuda):
+    """C4 end to end against float64 host scores (the count parity of the
+    evaluation pass): on a 4,000-example sample, every GPU score lies within
+    the fp32 d-term dot-product bound of the float64 product, and each
+    example's count #{j != y : s_j >= s_y} (and so its top-1 / top-5 hit)
+    from the GPU's scores equals the one from the float64 scores, except on
+    examples with a near tie - some |s_j - s_y| (float64) within the two
+    scores' rounding bounds - which are listed with both results."""
+    import torch
+    import bench
+    import libsdca_amd as sd
+    cfg = bench.CONFIGS["c4"]
+    X, W, labels, _ = bench.make_eval_input(cfg, torch, cuda)
+    S = sd.scores(X, W)
+    torch.cuda.synchronize()
+    n, m = S.shape
+    d = X.shape[1]
+    idx = np.sort(np.random.default_rng(13).choice(n, 4000, replace=False))
+    it = torch.from_numpy(idx).to(cuda)
+    Xs = X.index_select(0, it).double().cpu().numpy()
+    Wh = W.double().cpu().numpy()
+    S64 = Xs @ Wh.T
+    bound = 4 * np.sqrt(d) * np.finfo(np.float32).eps * (np.abs(Xs) @ np.abs(Wh).T) + 1e-30
+    got = S.index_select(0, it).double().cpu().numpy()
+    assert (np.abs(got - S64) <= bound).all(), f"max err/bound {(np.abs(got - S64) / bound).max():.2f}"
+    y = labels.index_select(0, it).cpu().numpy()
+    r = np.arange(len(idx))
+    gap = S64 - S64[r, y][:, None]
+    near = (np.abs(gap) <= bound + bound[r, y][:, None])
+    near[r, y] = False
+    near_tie = near.any(axis=1)
+    cnt_gpu = (got >= got[r, y][:, None]).sum(axis=1) - 1
+    cnt_64 = (S64 >= S64[r, y][:, None]).sum(axis=1) - 1
+    differ = cnt_gpu != cnt_64
+    assert not (differ & ~near_tie).any(), f"counts differ away from ties: {np.flatnonzero(differ & ~near_tie)[:8]}"
+    for k in (1, 5):
+        hit_gpu, hit_64 = cnt_gpu < k, cnt_64 < k
+        assert not ((hit_gpu != hit_64) & ~near_tie).any(), f"top-{k} differs away from ties"
+    print(f"c4 counts vs fp64: {int(near_tie.sum())} near-tie examples of {len(idx)}, "
+          f"{int(differ.sum())} with a different count; top-1 {float((cnt_64 < 1).mean()):.4f}, "
+          f"top-5 {float((cnt_64 < 5).mean()):.4f} (fp64)")
+    for i in np.flatnonzero(near_tie)[:20]:
+        print(f"  near tie: example {idx[i]} count gpu {cnt_gpu[i]} fp64 {cnt_64[i]}")
+
+
+@pytest.mark.timeout(300)
+def test_c4_eval_with_duals_full(cuda, oracle):
+    """The C4 pass with dual variables A ~ N(0, 0.01^2) (m x n, the A != 0
+    variant that exercises the dual losses; seed 3104): per-example primal and
+    dual losses of 4,000 examples against the oracle on the GPU's own scores,
+    and the dual-loss totals against the per-example sums."""
+    import torch
+    import bench
+    import libsdca_amd as sd
+    cfg = bench.CONFIGS["c4"]
+    X, W, labels, _ = bench.make_eval_input(cfg, torch, cuda)
+    n, m = cfg["n"], cfg["m"]
+    g = torch.Generator(device=cuda)
+    g.manual_seed(3104)
+    A = torch.randn((n, m), generator=g, device=cuda, dtype=torch.float32) * 0.01
+    objs = cfg["objs"]
+    recs, acc, pe = sd.eval_features(objs, X, W, labels, A=A, per_example=True)
+    S = sd.scores(X, W)
+    torch.cuda.synchronize()
+    idx = np.sort(np.random.default_rng(14).choice(n, 4000, replace=False))
+    it = torch.from_numpy(idx).to(cuda)
+    Ss = S.index_select(0, it).cpu().numpy()
+    As = A.index_select(0, it).cpu().numpy()
+    ys = labels.index_select(0, it).cpu().numpy()
+    _, _, o_pe = oracle.eval_scores(oracle_objs(objs), Ss, As, ys, result=F32, per_example=True,
+                                    nthreads=THREADS)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), Ss, As, ys, result=LONG_DOUBLE,
+                                    per_example=True, nthreads=THREADS)
+    got = pe.index_select(0, it).cpu().numpy()
+    compare_per_example(got[:, :, 0], o_pe[:, :, 0], 1e-5, "c4+A primal", exact=x_pe[:, :, 0])
+    compare_per_example(got[:, :, 1], o_pe[:, :, 1], 1e-5, "c4+A dual", exact=x_pe[:, :, 1])
+    tot = pe.sum(dim=0).cpu().numpy()
+    for o in range(len(objs)):
+        want = tot[o, 1]
+        assert abs(recs[o]["dual_loss"] - want) <= 1e-9 * max(1.0, abs(want)), (o, recs[o]["dual_loss"], want)
+
+
+@pytest.mark.timeout(300)
 def test_c5_eval_full(cuda, oracle):
     """Multilabel evaluation d=1024, m=200, n=500,000: rank loss recomputed on
     every example from the GPU's own scores, per-example losses of 5,000

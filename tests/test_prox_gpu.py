@@ -50,34 +50,148 @@ def run_oracle(oracle, op, x, result, nthreads=1, **kw):
 
 
 LONG_DOUBLE = 2
+# Operators whose threshold record carries a map (generalized thresholds,
+# proxdef.h:69-161): x <- clamp(map(x - t), lo, hi).
+MAPPED = {"entropy", "entropy_norm", "topk_entropy", "topk_entropy_biased", "two_entropy"}
+TWO_BLOCK = {"two_simplex", "two_simplex_sort", "two_entropy"}
 
 
-def parity(oracle, op, x, got, result, what, nthreads=1, keep=None, **kw):
+def record_blocks(op, n, m, kw):
+    """(column, first row, last row) of each threshold record: one per
+    column, or blocks [0, p) and [p, m) of each column for the two-block
+    operators (proxdef.h:301-324)."""
+    if op not in TWO_BLOCK:
+        return [(j, 0, m) for j in range(n)]
+    col_p, p = kw.get("col_p"), kw.get("p", 1)
+    out = []
+    for j in range(n):
+        pj = int(col_p[j]) if col_p is not None else int(p)
+        out += [(j, 0, pj), (j, pj, m)]
+    return out
+
+
+def apply_record(oracle, op, z, t, lo, hi, kw):
+    """clamp(map(z - t), lo, hi) in float64 with the map of the operator's
+    threshold record (math/functor.h:14-38)."""
+    u = np.asarray(z, dtype=np.float64) - t
+    if op in ("entropy", "topk_entropy"):
+        with np.errstate(over="ignore"):
+            u = np.exp(u)
+    elif op in ("entropy_norm", "topk_entropy_biased", "two_entropy"):
+        w = np.ascontiguousarray(u[None, :])
+        oracle.prox("lambert_w_exp", w)
+        u = w[0]
+        if op != "entropy_norm":
+            u = u / kw.get("alpha", 1.0)
+    return np.maximum(lo, np.minimum(u, hi))
+
+
+def check_thresholds(oracle, op, x, got, ref, thr_g, thr_r, thr_e, scale, err_col, rtol, what,
+                     kw, keep_cols):
+    """The GPU's threshold records against the oracle's, and the sets they
+    induce.  Per record (one per column, two per column for the two-block
+    operators):
+      * the record reproduces the reference's result: applying the GPU's
+        (t, lo, hi) with the operator's map to the input gives every entry of
+        the reference's output within the column's value tolerance
+        (rtol + 3 E_j) s_j.  Where the reference leaves an entry free this
+        pins t to that tolerance; where every entry sits at a bound (t is then
+        any point of an interval) it pins t to the interval;
+      * it is the record the GPU applied: it reproduces the GPU's own output
+        to rounding;
+      * membership - each entry at hi, at lo or free, read from the outputs -
+        equals the reference's, except for entries inside the band that the
+        two records' actual difference spans (plus 8 ulps): the entries tied
+        with a threshold.  Their count is printed.  For the top-k operators
+        the hi set is the top-k index set, which must be the reference's."""
+    n, m = x.shape
+    dt = x.dtype.type
+    u = float(np.finfo(x.dtype).eps)
+    mapped = op in MAPPED
+    moved = 0
+    for b, (j, a0, a1) in enumerate(record_blocks(op, n, m, kw)):
+        if not keep_cols[j] or a1 <= a0:
+            continue
+        tg, lg, hg = (float(v) for v in thr_g[b])
+        tr, lr, hr = (float(v) for v in thr_r[b])
+        s = float(scale[j, 0])
+        xs = x[j, a0:a1]
+        outr = ref[j, a0:a1].astype(np.float64)
+        outg = got[j, a0:a1].astype(np.float64)
+        # rounding of the map's argument x - t in the data type
+        ulps = 8 * u * (np.abs(xs.astype(np.float64)) + abs(tg) + 1.0) * \
+            np.maximum(1.0, np.abs(outr))
+        tol = (rtol + 3 * float(err_col[j])) * s
+        rep = apply_record(oracle, op, xs, tg, lg, hg, kw)
+        off = np.abs(rep - outr)
+        assert (off <= tol + ulps).all(), (
+            f"{what}: record {b} (column {j}) = ({tg!r}, {lg!r}, {hg!r}) does not reproduce the "
+            f"reference's result (reference record ({tr!r}, {lr!r}, {hr!r})): "
+            f"max |apply - ref| {off.max():.3e} > {tol:.3e}")
+        own = np.abs(rep - outg)
+        assert (own <= ulps).all(), (
+            f"{what}: record {b} (column {j}) is not the one applied to the GPU's output "
+            f"(max |apply - got| {own.max():.3e})")
+        hi_r, hi_g = outr == float(dt(hr)), outg == float(dt(hg))
+        lo_r, lo_g = (outr == float(dt(lr))) & ~hi_r, (outg == float(dt(lg))) & ~hi_g
+        cls_r = hi_r.astype(int) - lo_r.astype(int)
+        cls_g = hi_g.astype(int) - lo_g.astype(int)
+        diff = cls_r != cls_g
+        if diff.any():
+            shift = abs(tg - tr) + abs(hg - hr) + abs(lg - lr)
+            band = shift * (max(1.0, abs(hr)) if mapped else 1.0) + \
+                8 * u * max(1.0, float(np.abs(xs).max()), abs(tr), abs(hr))
+            far = diff & (np.abs(outg - outr) > band)
+            assert not far.any(), (
+                f"{what}: record {b} (column {j}): {int(far.sum())} entries change set "
+                f"outside the threshold band {band:.3e}: rows {np.flatnonzero(far)[:8] + a0}")
+            moved += int(diff.sum())
+    if moved:
+        print(f"{what}: {moved} entries change set within the band of their threshold")
+
+
+def parity(oracle, op, x, got, result, what, nthreads=1, keep=None, thr=None, **kw):
     """Check got (GPU) against the oracle at the Result type and in long double
-    (over the columns `keep` selects, all by default)."""
-    ref, _ = run_oracle(oracle, op, x, result, nthreads, **dict(kw))
-    exact, _ = run_oracle(oracle, op, x, LONG_DOUBLE, nthreads, **dict(kw))
-    if keep is not None:
-        x, got, ref, exact = x[keep], got[keep], ref[keep], exact[keep]
-    scale = np.maximum(1.0, np.abs(x.astype(np.float64)).max(axis=1, keepdims=True))
-    g = got.astype(np.float64)
-    r = ref.astype(np.float64)
-    e = exact.astype(np.float64)
+    (over the columns `keep` selects, all by default), column by column:
+    E_j is column j's own reference error |ref - exact| / s_j, and every
+    entry of column j must satisfy |gpu - ref| / s_j <= rtol + 3 E_j and
+    |gpu - exact| / s_j <= rtol + 2 E_j.  With the GPU's threshold records
+    (`thr`), those and the sets they induce are checked too
+    (check_thresholds)."""
+    want_thr = thr is not None and op != "lambert_w_exp"
+    ref, thr_r = run_oracle(oracle, op, x, result, nthreads, **dict(kw))
+    exact, thr_e = run_oracle(oracle, op, x, LONG_DOUBLE, nthreads, **dict(kw))
+    n = x.shape[0]
+    keep_cols = np.ones(n, bool) if keep is None else np.asarray(keep, bool)
+    xs, gs, rs, es = x[keep_cols], got[keep_cols], ref[keep_cols], exact[keep_cols]
+    scale_all = np.maximum(1.0, np.abs(x.astype(np.float64)).max(axis=1, keepdims=True))
+    scale = scale_all[keep_cols]
+    g = gs.astype(np.float64)
+    r = rs.astype(np.float64)
+    e = es.astype(np.float64)
     d_ref = np.abs(g - r) / scale
     err_gpu = np.abs(g - e) / scale
-    err_ref = float((np.abs(r - e) / scale).max())
+    err_col = (np.abs(r - e) / scale).max(axis=1) if r.size else np.zeros(0)
     # Outputs are stored in the Data type: float data caps the precision.
     rtol = max(RTOL[result], RTOL[F32] if x.dtype == np.float32 else RTOL[F64])
-    bad = np.argwhere(d_ref > rtol + 3 * err_ref)
+    bad = np.argwhere(d_ref > rtol + 3 * err_col[:, None])
     assert bad.size == 0, (
-        f"{what}: {len(np.unique(bad[:, 0]))} columns differ from the reference, max scaled "
-        f"err {d_ref.max():.3e} (reference error E={err_ref:.3e}); column {bad[0, 0]}: "
-        f"got {got[bad[0, 0]][:6]} want {ref[bad[0, 0]][:6]}")
-    assert err_gpu.max() <= rtol + 2 * err_ref, (
-        f"{what}: GPU error vs exact {err_gpu.max():.3e} exceeds rtol + 2E "
-        f"(E={err_ref:.3e})")
-    if d_ref.max() > rtol:
-        print(f"{what}: max |gpu-ref|/s {d_ref.max():.2e} within rtol + 3E, E={err_ref:.2e}")
+        f"{what}: {len(np.unique(bad[:, 0]))} columns differ from the reference beyond "
+        f"rtol + 3 E_j; column {bad[0, 0]}: scaled err {d_ref[bad[0, 0]].max():.3e}, "
+        f"E_j={err_col[bad[0, 0]]:.3e}; got {gs[bad[0, 0]][:6]} want {rs[bad[0, 0]][:6]}")
+    bad = np.argwhere(err_gpu > rtol + 2 * err_col[:, None])
+    assert bad.size == 0, (
+        f"{what}: GPU error vs exact {err_gpu[bad[0, 0]].max():.3e} exceeds rtol + 2 E_j "
+        f"(E_j={err_col[bad[0, 0]]:.3e}) in {len(np.unique(bad[:, 0]))} columns")
+    over = int((d_ref.max(axis=1) > rtol).sum()) if d_ref.size else 0
+    if over:
+        print(f"{what}: {over} of {len(d_ref)} columns above a flat {rtol:g} "
+              f"(max |gpu-ref|/s {d_ref.max():.2e}), each within its own rtol + 3 E_j")
+    if want_thr:
+        err_all = np.zeros(n)
+        err_all[keep_cols] = err_col
+        check_thresholds(oracle, op, x, got, ref, np.asarray(thr), thr_r, thr_e, scale_all,
+                         err_all, rtol, what, kw, keep_cols)
 
 
 DTYPES = [(np.float32, F32), (np.float32, F64), (np.float64, F64)]
@@ -109,8 +223,8 @@ def test_knapsack(cuda, oracle, op, kw, m, dtype, result):
     if kw["hi"] * m < kw["rhs"] or kw["lo"] * m > kw["rhs"]:
         pytest.skip("infeasible bounds for this m")
     for name, x in cases(m, dtype, 10 + m):
-        got, _ = run_gpu(op, x, result, cuda, **kw)
-        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
+        got, thr = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -122,8 +236,8 @@ def test_topk(cuda, oracle, op, k, m, dtype, result):
         pytest.skip("k > m")
     kw = dict(k=k, rhs=1.0)
     for name, x in cases(m, dtype, 20 + m + k):
-        got, _ = run_gpu(op, x, result, cuda, **kw)
-        parity(oracle, op, x, got, result, f"{op} k={k} {name} m={m}", **kw)
+        got, thr = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, f"{op} k={k} {name} m={m}", **kw, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -137,9 +251,9 @@ def test_topk_simplex_many_candidates(cuda, oracle, k, rhs, m, dtype, result):
         pytest.skip("k > m")
     kw = dict(k=k, rhs=rhs)
     for name, x in cases(m, dtype, 40 + m + k):
-        got, _ = run_gpu("topk_simplex", x, result, cuda, **kw)
+        got, thr = run_gpu("topk_simplex", x, result, cuda, **kw)
         parity(oracle, "topk_simplex", x, got, result, f"topk_simplex k={k} rhs={rhs} {name} m={m}",
-               **kw)
+               **kw, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -157,8 +271,8 @@ def test_entropic(cuda, oracle, op, kw, m, dtype, result):
     for name, x in [("uniform", inputs.uniform(n, m, dtype, 30 + m, -10, 10)),
                     ("normal", inputs.normal(n, m, dtype, 31 + m, 3.0)),
                     ("edge", inputs.edge_columns(m, dtype, 32 + m))]:
-        got, _ = run_gpu(op, x, result, cuda, **kw)
-        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
+        got, thr = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -171,8 +285,8 @@ def test_topk_entropy(cuda, oracle, k, m, dtype, result):
     for name, x in [("normal", inputs.normal(n, m, dtype, 40 + m, 2.0)),
                     ("label+2", inputs.label_shifted(n, m, dtype, 41 + m)),
                     ("edge", inputs.edge_columns(m, dtype, 42 + m))]:
-        got, _ = run_gpu("topk_entropy", x, result, cuda, k=k)
-        parity(oracle, "topk_entropy", x, got, result, f"topk_entropy k={k} {name} m={m}", k=k)
+        got, thr = run_gpu("topk_entropy", x, result, cuda, k=k)
+        parity(oracle, "topk_entropy", x, got, result, f"topk_entropy k={k} {name} m={m}", k=k, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -184,18 +298,18 @@ def test_two_simplex(cuda, oracle, m, dtype, result):
     for rhs in [1.0, 2.0]:
         for name, x in [("normal", inputs.normal(n, m, dtype, 51 + m)),
                         ("mixed", inputs.mixed_signs(n, m, dtype, 52 + m, -2, 2))]:
-            got, _ = run_gpu("two_simplex", x, result, cuda, rhs=rhs, col_p=col_p)
-            parity(oracle, "two_simplex", x, got, result, f"two_simplex rhs={rhs} {name} m={m}", rhs=rhs, col_p=col_p)
+            got, thr = run_gpu("two_simplex", x, result, cuda, rhs=rhs, col_p=col_p)
+            parity(oracle, "two_simplex", x, got, result, f"two_simplex rhs={rhs} {name} m={m}", rhs=rhs, col_p=col_p, thr=thr)
             # scalar p for every column
-            got, _ = run_gpu("two_simplex", x, result, cuda, rhs=rhs, p=1)
-            parity(oracle, "two_simplex", x, got, result, f"two_simplex p=1 rhs={rhs} {name} m={m}", rhs=rhs, p=1)
+            got, thr = run_gpu("two_simplex", x, result, cuda, rhs=rhs, p=1)
+            parity(oracle, "two_simplex", x, got, result, f"two_simplex p=1 rhs={rhs} {name} m={m}", rhs=rhs, p=1, thr=thr)
 
 
 def test_two_simplex_regression_vector(cuda, oracle):
     """The hard-coded vector of test/prox/two_simplex.cpp:55-64 (p=1, rhs=2)."""
     x = np.array([[-0.49371069182389915] + [0.49371069182390021] * 158], dtype=np.float64)
-    got, _ = run_gpu("two_simplex", x, F64, cuda, rhs=2.0, p=1)
-    parity(oracle, "two_simplex", x, got, F64, "two_simplex regression vector", rhs=2.0, p=1)
+    got, thr = run_gpu("two_simplex", x, F64, cuda, rhs=2.0, p=1)
+    parity(oracle, "two_simplex", x, got, F64, "two_simplex regression vector", rhs=2.0, p=1, thr=thr)
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
@@ -272,8 +386,8 @@ def test_deferred_list_reuse(cuda, oracle):
         if n != 4000:
             x[np.arange(n), rng.integers(0, 50, n)] += 40.0
         for op in ("topk_cone", "topk_simplex"):
-            got, _ = run_gpu(op, x, F32, cuda, k=5)
-            parity(oracle, op, x, got, F32, f"{op} n={n}", k=5)
+            got, thr = run_gpu(op, x, F32, cuda, k=5)
+            parity(oracle, op, x, got, F32, f"{op} n={n}", k=5, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -291,8 +405,8 @@ def test_large_m_workgroup_per_column(cuda, oracle, op, kw, m, dtype, result):
     for name, x in [("normal", inputs.normal(n, m, dtype, 90 + m)),
                     ("label+2", inputs.label_shifted(n, m, dtype, 91 + m)),
                     ("edge", inputs.edge_columns(m, dtype, 92 + m))]:
-        got, _ = run_gpu(op, x, result, cuda, **kw)
-        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
+        got, thr = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw, thr=thr)
 
 
 def test_large_m_limits(cuda):
@@ -326,7 +440,7 @@ def test_biased(cuda, oracle, op, kw, m, dtype, result):
         pytest.skip("k > m")
     for name, x in cases(m, dtype, 110 + m):
         got, thr = run_gpu(op, x, result, cuda, **kw)
-        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw)
+        parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -344,13 +458,13 @@ def test_two_simplex_sort(cuda, oracle, m, dtype, result):
         for name, x in [("normal", inputs.normal(n, m, dtype, 151 + m)),
                         ("mixed", inputs.mixed_signs(n, m, dtype, 152 + m, -2, 2)),
                         ("zero-optimum", np.ascontiguousarray(neg))]:
-            got, _ = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, col_p=col_p)
+            got, thr = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, col_p=col_p)
             parity(oracle, "two_simplex_sort", x, got, result,
-                   f"two_simplex_sort rhs={rhs} {name} m={m}", rhs=rhs, col_p=col_p)
+                   f"two_simplex_sort rhs={rhs} {name} m={m}", rhs=rhs, col_p=col_p, thr=thr)
             p = max(1, m // 3)
-            got, _ = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, p=p)
+            got, thr = run_gpu("two_simplex_sort", x, result, cuda, rhs=rhs, p=p)
             parity(oracle, "two_simplex_sort", x, got, result,
-                   f"two_simplex_sort p={p} rhs={rhs} {name} m={m}", rhs=rhs, p=p)
+                   f"two_simplex_sort p={p} rhs={rhs} {name} m={m}", rhs=rhs, p=p, thr=thr)
 
 
 def entbias_settled(oracle, x, alpha, result):
@@ -402,7 +516,7 @@ def test_topk_entropy_biased(cuda, oracle, k, alpha, m, dtype, result):
         got, thr = run_gpu("topk_entropy_biased", x, result, cuda, k=k, alpha=alpha)
         parity(oracle, "topk_entropy_biased", x, got, result,
                f"topk_entropy_biased k={k} alpha={alpha} {name} m={m}", nthreads=8, keep=keep,
-               k=k, alpha=alpha)
+               k=k, alpha=alpha, thr=thr)
         if k == 1 and not keep.all():
             # Where the reference stops short, the GPU's threshold is a root.
             assert entbias_is_root(oracle, x[~keep], alpha, result, thr[~keep, 0]).all()
@@ -413,9 +527,9 @@ def test_topk_entropy_biased_largest_m(cuda, oracle, dtype, result, m):
     x = inputs.normal(16, m, dtype, 180, 2.0)
     x[:8, :3] += 8.0
     assert entbias_settled(oracle, x, 1.5, result).all()
-    got, _ = run_gpu("topk_entropy_biased", x, result, cuda, k=4, alpha=1.5)
+    got, thr = run_gpu("topk_entropy_biased", x, result, cuda, k=4, alpha=1.5)
     parity(oracle, "topk_entropy_biased", x, got, result, f"topk_entropy_biased m={m}",
-           nthreads=8, k=4, alpha=1.5)
+           nthreads=8, k=4, alpha=1.5, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -432,8 +546,37 @@ def test_two_entropy(cuda, oracle, alpha, m, dtype, result):
                     ("uniform", inputs.uniform(n, m, dtype, 193 + m, -10, 10))]:
         got, thr = run_gpu("two_entropy", x, result, cuda, alpha=alpha, col_p=col_p)
         parity(oracle, "two_entropy", x, got, result, f"two_entropy alpha={alpha} {name} m={m}",
-               nthreads=8, alpha=alpha, col_p=col_p)
+               nthreads=8, alpha=alpha, col_p=col_p, thr=thr)
         p = max(1, m // 3)
-        got, _ = run_gpu("two_entropy", x, result, cuda, alpha=alpha, p=p)
+        got, thr = run_gpu("two_entropy", x, result, cuda, alpha=alpha, p=p)
         parity(oracle, "two_entropy", x, got, result,
-               f"two_entropy p={p} alpha={alpha} {name} m={m}", nthreads=8, alpha=alpha, p=p)
+               f"two_entropy p={p} alpha={alpha} {name} m={m}", nthreads=8, alpha=alpha, p=p, thr=thr)
+
+
+@pytest.mark.parametrize("op,m", [("two_simplex", 40), ("two_simplex_sort", 40),
+                                  ("two_simplex_sort", 3000), ("two_entropy", 40)])
+def test_col_p_out_of_range(cuda, oracle, op, m):
+    """Per-column splits outside [1, m - 1]: rejected by the host checks
+    (host pointers in the C ABI, torch tensors in the Python layer); handed
+    to the kernels anyway (check_col_p=False), each is brought into range on
+    the device, so the call stays in bounds and the column gets the
+    projection for the clamped split."""
+    import torch
+    import libsdca_amd as sd
+    n = 64
+    x = inputs.normal(n, m, np.float32, 31 + m)
+    col_p = np.full(n, 3, dtype=np.int64)
+    col_p[::4] = 0
+    col_p[1::4] = m
+    col_p[2::4] = -5
+    t = torch.from_numpy(x).to(cuda)
+    tp = torch.from_numpy(col_p).to(cuda)
+    with pytest.raises(sd.SdcaError):
+        sd.prox(op, t.clone(), col_p=tp)
+    with pytest.raises(sd.SdcaError):
+        sd.prox(op, x.copy(), col_p=col_p)
+    got, thr = sd.prox(op, t, col_p=tp, thresholds=True, check_col_p=False)
+    torch.cuda.synchronize()
+    clamped = np.clip(col_p, 1, m - 1)
+    parity(oracle, op, x, got.cpu().numpy(), F32, f"{op} m={m} clamped splits", nthreads=8,
+           col_p=clamped, thr=thr.cpu().numpy())

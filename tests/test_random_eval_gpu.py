@@ -176,3 +176,24 @@ def test_random_eval_kernel(cuda, oracle, i):
                                     per_example=True)
     compare_per_example(pe[:, :, 0], o_pe[:, :, 0], RTOL[F32], f"case {i} primal", x_pe[:, :, 0])
     assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n), f"case {i}: accuracy"
+    if test:
+        for r in recs:
+            assert r["dual_loss"] == 0 and r["dual_regularizer"] == 0, f"case {i}"
+        return
+    # A training set: the dual losses from A's rows, the dual regularizer
+    # sum_i 0.5 <a_i, s_i> in both terms, and the totals, against the oracle
+    # on the GPU's scores and the regularizer against float64 A K.
+    preg, dreg = oracle.dual_regularizer(A, S, result=F32)
+    o_recs, _, o_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, preg=preg, dreg=dreg,
+                                         result=F32, per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, result=LONG_DOUBLE,
+                                    per_example=True)
+    compare_per_example(pe[:, :, 1], o_pe[:, :, 1], RTOL[F32], f"case {i} dual", x_pe[:, :, 1])
+    A64 = A.astype(np.float64)
+    closed = 0.5 * float(((K.astype(np.float64) @ A64) * A64).sum())
+    mag = 0.5 * float(((np.abs(K).astype(np.float64) @ np.abs(A64)) * np.abs(A64)).sum())
+    for r, o in zip(recs, o_recs):
+        assert r["primal_regularizer"] == r["dual_regularizer"], f"case {i}"
+        assert abs(r["dual_regularizer"] - closed) <= 1e-5 * max(1.0, mag), f"case {i}"
+        for f in ("dual_loss", "primal", "dual"):
+            assert abs(r[f] - o[f]) <= 1e-4 * max(1.0, abs(o[f])), (i, f, r[f], o[f])
