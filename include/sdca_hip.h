@@ -110,6 +110,27 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result,
               const sdca_prox_params* params, const int64_t* col_p,
               sdca_thresholds* thresholds, unsigned flags, void* stream);
 
+/*
+ * sdca_prox without any device allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as sdca_prox with device pointers (there is no flags argument:
+ * host staging would allocate).  The deferred-column list of the top-k,
+ * biased and sort-based two-simplex operators lives in a fixed device array
+ * of the library, one per device, held until the process ends: those
+ * operators take at most sdca_prox_noalloc_max_columns() columns (4,194,304)
+ * per call and return SDCA_ERR_ARG_RANGE beyond; the other operators use no
+ * scratch and take any n.  Every call on a device shares that array: calls
+ * that overlap on one device (concurrent streams or host threads) race.
+ */
+int sdca_prox_noalloc(sdca_prox_op op, sdca_dtype data, sdca_dtype result,
+                      int64_t m, int64_t n, const void* in, void* out,
+                      const sdca_prox_params* params, const int64_t* col_p,
+                      sdca_thresholds* thresholds, void* stream);
+
+/* Largest n that sdca_prox_noalloc takes for the listed operators. */
+int64_t sdca_prox_noalloc_max_columns(void);
+
 /* Objectives of the evaluation pass (objective.h:55-160). */
 typedef enum sdca_objective_kind {
   SDCA_OBJ_HINGE_TOPK = 0,             /* l2_hinge_topk.h:11-88 */

@@ -144,7 +144,23 @@ void sdca_prox_params_default(sdca_prox_params* p) {
 int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, int64_t n,
               const void* in, void* out, const sdca_prox_params* params, const int64_t* col_p,
               sdca_thresholds* thresholds, unsigned flags, void* stream_ptr) {
-  using namespace sdca_gpu;
+  return sdca_gpu::prox_entry(op, data, result, m, n, in, out, params, col_p, thresholds, flags,
+                              stream_ptr, nullptr, 0);
+}
+
+}  // extern "C"
+
+namespace sdca_gpu {
+
+int set_error(int code, const char* message) { return fail(code, "%s", message); }
+
+int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, const void* in,
+               void* out, const sdca_prox_params* params, const int64_t* col_p,
+               sdca_thresholds* thresholds, unsigned flags, void* stream_ptr, int* fixed_list,
+               int64_t fixed_list_ints) {
+  const sdca_prox_op op = static_cast<sdca_prox_op>(op_in);
+  const sdca_dtype data = static_cast<sdca_dtype>(data_in);
+  const sdca_dtype result = static_cast<sdca_dtype>(result_in);
   g_last_error.clear();
   sdca_prox_params p;
   if (params) p = *params;
@@ -216,6 +232,19 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   const size_t bytes = static_cast<size_t>(m) * static_cast<size_t>(n) * dtype_size(data);
   const bool host = (flags & SDCA_HOST_PTR) != 0;
   const int64_t nthr = two ? 2 * n : n;
+  if (fixed_list) {
+    // The entry point without allocation: device pointers only (host
+    // staging allocates), and the deferred-column list [count, done,
+    // column ids] must fit the caller-provided scratch.
+    if (host)
+      return fail(SDCA_ERR_ARG_RANGE,
+                  "sdca_prox_noalloc takes device pointers only (SDCA_HOST_PTR stages through "
+                  "allocated device buffers)");
+    if (listed && n + 2 > fixed_list_ints)
+      return fail(SDCA_ERR_ARG_RANGE,
+                  "sdca_prox_noalloc: n = %lld columns exceed its fixed scratch of %lld columns "
+                  "for this operator", (long long)n, (long long)(fixed_list_ints - 2));
+  }
   DeviceBuffer din, dout, dcolp, dthr;
   const void* d_in = in;
   void* d_out = out;
@@ -281,7 +310,14 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
     // clear is launched only for a new list or after a call that did not
     // reach that kernel.
     Workspace* wsr = nullptr;
-    if (listed) {
+    Workspace fixed_ws;  // the fixed scratch's stand-in record (its state is not kept)
+    if (listed && fixed_list) {
+      // The fixed scratch is shared by every call on the device: its two
+      // counters are cleared by a kernel on this stream before each use.
+      a.slow = fixed_list;
+      wsr = &fixed_ws;
+      SDCA_HIP_TRY(launch_clear(a.slow, 2, stream), "clear kernel");
+    } else if (listed) {
       void* ws = nullptr;
       rc = workspace(stream, 0, static_cast<size_t>(n + 2) * sizeof(int), &ws, &wsr);
       if (rc) return rc;
@@ -325,8 +361,7 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
   return SDCA_OK;
 }
 
-
-}  // extern "C"
+}  // namespace sdca_gpu
 
 namespace {
 

@@ -68,6 +68,16 @@ hipError_t launch_lambert(const ProxLaunch& a);
 // Zero the slow-column counter.
 hipError_t launch_clear(int* p, int count, hipStream_t stream);
 
+// sdca_prox (capi.cpp) with an optional caller-provided deferred-column list
+// of fixed_list_ints ints in place of the per-stream workspace: with it the
+// call allocates nothing (device pointers only).
+int prox_entry(int op, int data, int result, int64_t m, int64_t n, const void* in, void* out,
+               const sdca_prox_params* params, const int64_t* col_p,
+               sdca_thresholds* thresholds, unsigned flags, void* stream, int* fixed_list,
+               int64_t fixed_list_ints);
+// Records a failure message for sdca_last_error() on this thread; returns code.
+int set_error(int code, const char* message);
+
 }  // namespace sdca_gpu
 
 #endif
