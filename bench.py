@@ -19,10 +19,16 @@ cone on the headline input), c3 (entropy f64 m=1000 n=2e5), c3norm
 m=1000 n=1e5: examples/s, roofline on the fp32 MFMA score GEMM), c5eval
 (multilabel evaluation d=1024 m=200 n=5e5).
 
+The default run (c2) also times the whole C4 evaluation pass under the same
+clock and nests it as "c4" (examples/s, an MFMA roofline for the score GEMM
+and for the whole pass, its own cpu_baseline); --no-c4 skips it.
+
 cpu_baseline: the reference's own prox loop (oracle/_ref, built from the
 reference headers with -O3) - or the oracle restatement when that library is
 absent - on a bounded sample of the same input, single-threaded as shipped,
-on the host cores of the GPU box.
+on the host cores of the GPU box, plus "all_cores": the same loop
+harness-parallel over the box's CPU share (16 threads).  For the evaluation
+pass: the reference's evaluate_dataset with MKL as its CBLAS.
 """
 import argparse
 import json
@@ -109,16 +115,22 @@ CONFIGS = {
                         "cross-entropy with c=1, rank loss"),
 }
 MFMA_F32_PEAK_TFLOPS = 157.3
+CPU_THREADS = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 50 untimed steps (about 30 ms of C2 work): the clocks settle; after 5
+    # the first timed steps still ran ~5 % slow.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c4", action="store_true",
+                    help="default run: skip the nested C4 evaluation-pass measurement")
+    ap.add_argument("--c4-steps", type=int, default=5)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain device copy of the headline input's size instead "
                          "(the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -214,6 +226,13 @@ def cpu_baseline(cfg, x_sample, col_p_sample, seconds):
         lib.prox(op, work, result=res, params=params, col_p=cp)
         return time.perf_counter() - t0
 
+    def timed_par(ncols):
+        work = x_sample[:ncols].copy()
+        cp = None if col_p_sample is None else col_p_sample[:ncols]
+        t0 = time.perf_counter()
+        lib.prox(op, work, result=res, params=params, col_p=cp, nthreads=CPU_THREADS)
+        return time.perf_counter() - t0
+
     probe = max(1, min(n_avail, 2000))
     per_col = timed(probe) / probe
     ncols = int(min(n_avail, max(probe, seconds / max(per_col, 1e-12))))
@@ -226,9 +245,21 @@ def cpu_baseline(cfg, x_sample, col_p_sample, seconds):
         return {"value": pts / elapsed, "unit": "points/s", "cores": 1, "kind": kind,
                 "sample": f"{x_sample.shape[1]} points of the same input x {passes} passes, "
                           f"1 thread, {elapsed:.1f} s"}
+    # harness-parallel: columns split over the host cores (the reference's
+    # functions are re-entrant; each thread has its own aux), the same
+    # columns per thread as the single-thread sample where the input allows
+    npar = int(min(n_avail, ncols * CPU_THREADS))
+    elapsed_p, passes_p = 0.0, 0
+    while elapsed_p < 0.5 * seconds and passes_p < 200:
+        elapsed_p += timed_par(npar)
+        passes_p += 1
     return {"value": ncols * passes / elapsed, "unit": "columns/s", "cores": 1, "kind": kind,
             "sample": f"first {ncols} columns of the same input x {passes} passes, 1 thread, "
-                      f"{elapsed:.1f} s"}
+                      f"{elapsed:.1f} s",
+            "all_cores": {"value": npar * passes_p / elapsed_p, "unit": "columns/s",
+                          "cores": CPU_THREADS,
+                          "sample": f"first {npar} columns x {passes_p} passes over "
+                                    f"{CPU_THREADS} threads, {elapsed_p:.1f} s, harness-parallel"}}
 
 
 def make_eval_input(cfg, torch, dev):
@@ -262,7 +293,11 @@ def make_eval_input(cfg, torch, dev):
     return X, W, labels, None
 
 
-def bench_eval(cfg, args, torch, sd):
+def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
+    """Times the evaluation pass of `cfg`; returns the result dict."""
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    config_name = args.config if config_name is None else config_name
     dev = torch.device("cuda:0")
     X, W, labels, offsets = make_eval_input(cfg, torch, dev)
     objs = cfg["objs"]
@@ -275,33 +310,33 @@ def bench_eval(cfg, args, torch, sd):
             return sd.eval_kernel(objs, X, W, labels, offsets=offsets)
         return sd.eval_features(objs, X, W, labels, offsets=offsets)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         recs, acc, _ = step()  # each call ends with a host synchronisation
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / args.steps
+    ms_per_step = wall * 1e3 / steps
     # The dominant kernel is the score GEMM: time it on its own, event-timed
     # on the stream it runs on.
     S = torch.empty((cfg["n"], cfg["m"]), dtype=torch.float32, device=dev)
     Wg = W.T.contiguous() if kernel else W   # the GEMM's W operand: A' for kernel input
     for _ in range(2):
         sd.scores(X, Wg, out=S)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    for a, b in ev:
-        a.record(stream)
+    e0.record(stream)
+    for _ in range(steps):
         sd.scores(X, Wg, out=S)
-        b.record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
-    gemm_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    gemm_ms = e0.elapsed_time(e1) / steps
     inner = cfg["n"] if kernel else cfg["d"]  # contraction length: n_train or d
     flops = 2.0 * cfg["n"] * cfg["m"] * inner
     achieved = flops / (gemm_ms / 1e3) / 1e12
+    achieved_pass = flops / (ms_per_step / 1e3) / 1e12
     value = cfg["n"] / (ms_per_step / 1e3)
     extra = {"records": recs}
     if not cfg.get("multilabel"):
@@ -312,8 +347,8 @@ def bench_eval(cfg, args, torch, sd):
         "value": value,
         "unit": "examples/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -325,54 +360,84 @@ def bench_eval(cfg, args, torch, sd):
                    "objectives": [o[0] for o in objs]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS,
-                     "traffic": traffic_of(args.config),
+                     "traffic": traffic_of(config_name),
                      "note": f"score GEMM 2 n m {'n_train' if kernel else 'd'} = {flops:.3e} "
                              f"flop / mean event-timed launch "
                              f"{gemm_ms:.3f} ms; full pass {ms_per_step:.3f} ms"},
+        "roofline_pass": {"bound": "mfma", "achieved": achieved_pass,
+                          "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                          "frac": achieved_pass / MFMA_F32_PEAK_TFLOPS,
+                          "note": "the same flops over the whole pass (GEMM, epilogue, "
+                                  "reductions, records) on the host clock"},
         "eval": extra,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_eval(cfg, X, W, labels, offsets, args.cpu_seconds,
                                                    kernel)
-    print(json.dumps(result))
+    return result
 
 
 def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds, kernel=False):
-    """The oracle's evaluation (gemv loop + epilogue, single thread, as the
-    reference's evaluate_dataset runs) on a bounded sample of examples; for
-    kernel input X is K and W is A, and the dual regularizer is included."""
+    """The reference's evaluate_dataset (solver/eval.h:15-51, oracle/_ref:
+    the reference headers with Intel MKL as their CBLAS) on a bounded sample
+    of the same examples: one thread as shipped, and harness-parallel over
+    the host cores (examples split over threads, records merged).  Kernel
+    input, or a box without the reference build, falls back to the oracle's
+    restatement (gemv loop plus epilogue, kind "port")."""
     import numpy as np
     from oracle import binding
-    lib = binding.oracle()
     oname = {"l2_hinge_topk_smooth": "hinge_topk_smooth", "l2_entropy": "entropy",
              "l2_multilabel_hinge_smooth": "multilabel_hinge_smooth",
              "l2_multilabel_entropy": "multilabel_entropy"}
     objs = [(oname[o[0]], o[1], o[2], o[3]) for o in cfg["objs"]]
-    Wh = np.ascontiguousarray(W.T.cpu().numpy()) if kernel else W.cpu().numpy()
-    Ah = W.cpu().numpy() if kernel else None
     lab = labels.cpu().numpy()
     off = None if offsets is None else offsets.cpu().numpy()
+    ref = None if kernel else binding.reference()
+    if ref is not None:
+        Wh = W.cpu().numpy()
 
-    def run(ne):
-        Xs = X[:ne].cpu().numpy()
-        t0 = time.perf_counter()
-        S = lib.scores(Xs, Wh)
-        if kernel:
-            lib.dual_regularizer(Ah[:ne], S)
-            lib.eval_scores(objs, S, Ah[:ne], lab[:ne])
-        elif off is None:
-            lib.eval_scores(objs, S, None, lab[:ne])
-        else:
-            lib.eval_scores(objs, S, None, lab[: off[ne]], off[: ne + 1])
-        return time.perf_counter() - t0
+        def run(ne, nthreads):
+            Xs = X[:ne].cpu().numpy()
+            A = np.zeros((ne, cfg["m"]), dtype=np.float32)  # cold start: A = 0
+            ls = lab[:ne] if off is None else lab[: off[ne]]
+            os_ = None if off is None else off[: ne + 1]
+            t0 = time.perf_counter()
+            ref.evaluate_dataset(objs, Xs, Wh, A, ls, os_, nthreads=nthreads)
+            return time.perf_counter() - t0
+        kind = "reference"
+        what = "the reference's evaluate_dataset (MKL sgemv scores), all objectives"
+    else:
+        lib = binding.oracle()
+        Wh = np.ascontiguousarray(W.T.cpu().numpy()) if kernel else W.cpu().numpy()
+        Ah = W.cpu().numpy() if kernel else None
+
+        def run(ne, nthreads):
+            Xs = X[:ne].cpu().numpy()
+            t0 = time.perf_counter()
+            S = lib.scores(Xs, Wh, nthreads=nthreads)
+            if kernel:
+                lib.dual_regularizer(Ah[:ne], S)
+                lib.eval_scores(objs, S, Ah[:ne], lab[:ne], nthreads=nthreads)
+            elif off is None:
+                lib.eval_scores(objs, S, None, lab[:ne], nthreads=nthreads)
+            else:
+                lib.eval_scores(objs, S, None, lab[: off[ne]], off[: ne + 1], nthreads=nthreads)
+            return time.perf_counter() - t0
+        kind = "port"
+        what = "the oracle's restated gemv loop and epilogue"
 
     probe = 200
-    dt = run(probe)
+    dt = run(probe, 1)
     ne = int(min(cfg["n"], max(probe, seconds / max(dt / probe, 1e-9))))
-    dt = run(ne)
-    return {"value": ne / dt, "unit": "examples/s", "cores": 1, "kind": "port",
-            "sample": f"first {ne} examples, 1 thread ({dt:.1f} s): the oracle's per-example "
-                      f"gemv loop plus the restated epilogue (the reference's BLAS is not built here)"}
+    dt = run(ne, 1)
+    # harness-parallel: the same work per thread as the single-thread sample
+    nep = int(min(cfg["n"], ne * CPU_THREADS))
+    dtp = run(nep, CPU_THREADS)
+    return {"value": ne / dt, "unit": "examples/s", "cores": 1, "kind": kind,
+            "sample": f"first {ne} examples, 1 thread ({dt:.1f} s): {what}",
+            "all_cores": {"value": nep / dtp, "unit": "examples/s", "cores": CPU_THREADS,
+                          "sample": f"first {nep} examples over {CPU_THREADS} threads "
+                                    f"({dtp:.1f} s), harness-parallel"}}
 
 
 def main():
@@ -391,7 +456,7 @@ def main():
         return
     cfg = CONFIGS[args.config]
     if cfg["op"] == "eval":
-        bench_eval(cfg, args, torch, sd)
+        print(json.dumps(bench_eval(cfg, args, torch, sd)))
         return
     dev = torch.device("cuda:0")
     x, col_p = make_input(cfg, torch, dev)
@@ -439,18 +504,19 @@ def main():
         for i in range(args.warmup):
             step(i)
         torch.cuda.synchronize()
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        torch.cuda.synchronize()
+        # One pair of events on the kernels' stream brackets the K timed
+        # steps: the mean launch duration is their span / K.  (An event pair
+        # per step adds its own stream packets between the steps: about 30 us
+        # of the 0.55 ms C2 step.)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        start.record(stream)
         for i in range(args.steps):
-            starts[i].record(stream)
             step(i)
-            ends[i].record(stream)
+        end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-        avg_ms = sum(launch_ms) / len(launch_ms)
+        avg_ms = start.elapsed_time(end) / args.steps
     ms_per_step = wall * 1e3 / args.steps
 
     esz = 4 if cfg["dtype"] == "f32" else 8
@@ -483,7 +549,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_of(args.config),
                      "note": f"algorithmic {bytes_per_unit} B per unit x {units} units per launch "
-                             f"/ mean event-timed launch {avg_ms:.4f} ms"
+                             f"/ mean launch {avg_ms:.4f} ms (HIP events on the kernels' stream "
+                             f"around the {args.steps} timed steps; a step is the column kernel "
+                             f"and the deferred-column kernel)"
                              + (" (the K steps replayed from one captured HIP graph)" if graph else "")},
     }
     if not args.no_cpu:
@@ -495,6 +563,17 @@ def main():
         cps = None if col_p is None else col_p[: sample.shape[0]].cpu().numpy()
         result["cpu_baseline"] = cpu_baseline(cfg, np.ascontiguousarray(sample), cps,
                                               args.cpu_seconds)
+        del sample
+    if args.config == "c2" and not args.no_c4:
+        # The second north-star workload under the same clock: the whole C4
+        # evaluation pass, nested (the headline value stays the prox's).
+        del xs, x, out
+        torch.cuda.empty_cache()
+        ev = bench_eval(CONFIGS["c4"], args, torch, sd, steps=args.c4_steps, warmup=3,
+                        config_name="c4")
+        result["c4"] = {key: ev[key] for key in ("value", "unit", "ms_per_step", "steps", "warmup",
+                                                 "dtype", "config", "roofline", "roofline_pass",
+                                                 "eval", "cpu_baseline") if key in ev}
     print(json.dumps(result))
 
 

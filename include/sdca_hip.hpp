@@ -19,6 +19,7 @@
 #ifndef SDCA_HIP_HPP
 #define SDCA_HIP_HPP
 
+#include <cstddef>
 #include <cstdint>
 #include <iterator>
 #include <stdexcept>
@@ -290,6 +291,220 @@ inline std::vector<eval_record> evaluate_kernel(
       offsets.empty() ? acc.data() : nullptr, nullptr,
       SDCA_HOST_PTR | (test ? SDCA_EVAL_TEST : 0u), nullptr));
   return detail::records(recs, acc, offsets.empty());
+}
+
+// ---------------------------------------------------------------------------
+// evaluate_dataset with the reference's own signature (solver/eval.h:15-51):
+// the same template parameters and arguments, reading the reference's
+// solver_context (ctx.primal_variables, ctx.dual_variables,
+// ctx.primal_initial, ctx.objective; context.h:32-37) and dataset (d.in,
+// d.out, d.evals), and appending the record eval_end would (eval/core.h:43-132).
+// The reference's types are only declared here: this header is included
+// next to the reference's solver headers, which define them.
+// ---------------------------------------------------------------------------
+}  // namespace hip
+
+template <typename Data> struct feature_input;
+template <typename Data> struct kernel_input;
+struct multiclass_output;
+struct multilabel_output;
+template <typename Result, typename Output> struct eval_train;
+template <typename Result, typename Output> struct eval_test;
+template <typename Data, template <typename> class Input> struct solver_scratch;
+template <typename Data, typename Result> struct l2_hinge_topk;
+template <typename Data, typename Result> struct l2_hinge_topk_smooth;
+template <typename Data, typename Result> struct l2_topk_hinge;
+template <typename Data, typename Result> struct l2_topk_hinge_smooth;
+template <typename Data, typename Result> struct l2_entropy;
+template <typename Data, typename Result> struct l2_entropy_topk;
+template <typename Data, typename Result> struct l2_multilabel_hinge;
+template <typename Data, typename Result> struct l2_multilabel_hinge_smooth;
+template <typename Data, typename Result> struct l2_multilabel_entropy;
+
+namespace hip {
+namespace detail {
+
+inline sdca_objective make_objective(int kind, double c, double gamma, std::size_t k) {
+  sdca_objective o;
+  o.kind = kind;
+  o.reserved = 0;
+  o.c = c;
+  o.gamma = gamma;
+  o.k = static_cast<std::int64_t>(k);
+  return o;
+}
+
+// The C ABI's description of each reference objective (its public c,
+// gamma, k members; objective/*.h).
+template <typename Objective> struct objective_of {
+  static_assert(sizeof(Objective) == 0,
+                "sdca::hip::evaluate_dataset: objective not on the GPU evaluation path");
+};
+template <typename D, typename R> struct objective_of<sdca::l2_hinge_topk<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_HINGE_TOPK, static_cast<double>(o.c), 1.0, o.k);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_hinge_topk_smooth<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_HINGE_TOPK_SMOOTH, static_cast<double>(o.c),
+                          static_cast<double>(o.gamma), o.k);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_topk_hinge<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_TOPK_HINGE, static_cast<double>(o.c), 1.0, o.k);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_topk_hinge_smooth<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_TOPK_HINGE_SMOOTH, static_cast<double>(o.c),
+                          static_cast<double>(o.gamma), o.k);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_entropy<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_ENTROPY, static_cast<double>(o.c), 1.0, 1);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_entropy_topk<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_ENTROPY_TOPK, static_cast<double>(o.c), 1.0, o.k);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_multilabel_hinge<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_MULTILABEL_HINGE, static_cast<double>(o.c), 1.0, 1);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_multilabel_hinge_smooth<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_MULTILABEL_HINGE_SMOOTH, static_cast<double>(o.c),
+                          static_cast<double>(o.gamma), 1);
+  }
+};
+template <typename D, typename R> struct objective_of<sdca::l2_multilabel_entropy<D, R>> {
+  template <typename O> static sdca_objective get(const O& o) {
+    return make_objective(SDCA_OBJ_MULTILABEL_ENTROPY, static_cast<double>(o.c), 1.0, 1);
+  }
+};
+
+// Labels of the reference's outputs (data/output.h:15-166) as int64 arrays.
+template <typename Output>
+inline void labels_of(const Output& out, std::vector<std::int64_t>& labels,
+                      std::vector<std::int64_t>& offsets, std::true_type /*multilabel*/) {
+  labels.assign(out.labels.begin(), out.labels.end());
+  offsets.assign(out.offsets.begin(), out.offsets.end());
+}
+template <typename Output>
+inline void labels_of(const Output& out, std::vector<std::int64_t>& labels,
+                      std::vector<std::int64_t>& offsets, std::false_type) {
+  labels.assign(out.labels.begin(), out.labels.end());
+  offsets.clear();
+}
+
+// The C ABI call for a feature input (scores W' x_i) or a kernel input
+// (scores A K_i).
+template <typename Data, typename Context>
+inline int eval_call(const sdca::feature_input<Data>& in, const Context& ctx,
+                     const sdca_objective& ob, sdca_dtype result, std::int64_t m,
+                     std::int64_t n, const std::vector<std::int64_t>& labels,
+                     const std::vector<std::int64_t>& offsets, sdca_eval_record* rec,
+                     double* acc, bool test) {
+  return sdca_eval_features(&ob, 1, dtype<Data>::value, result,
+                            static_cast<std::int64_t>(in.num_dimensions), m, n, in.features,
+                            ctx.primal_variables, test ? nullptr : ctx.dual_variables,
+                            test ? nullptr : ctx.primal_initial, labels.data(),
+                            offsets.empty() ? nullptr : offsets.data(), rec, acc, nullptr,
+                            SDCA_HOST_PTR | (test ? SDCA_EVAL_TEST : 0u), nullptr);
+}
+template <typename Data, typename Context>
+inline int eval_call(const sdca::kernel_input<Data>& in, const Context& ctx,
+                     const sdca_objective& ob, sdca_dtype result, std::int64_t m,
+                     std::int64_t n, const std::vector<std::int64_t>& labels,
+                     const std::vector<std::int64_t>& offsets, sdca_eval_record* rec,
+                     double* acc, bool test) {
+  return sdca_eval_kernel(&ob, 1, dtype<Data>::value, result,
+                          static_cast<std::int64_t>(in.num_train_examples), m, n, in.kernel,
+                          ctx.dual_variables, labels.data(),
+                          offsets.empty() ? nullptr : offsets.data(), rec, acc, nullptr,
+                          SDCA_HOST_PTR | (test ? SDCA_EVAL_TEST : 0u), nullptr);
+}
+
+// The fields eval_end sets on a training record (eval/core.h:43-95):
+// epoch and timings from the context, then the objective's terms.
+template <typename Eval, typename Context>
+inline void fill_train(Eval& e, const Context& ctx, const sdca_eval_record& r) {
+  typedef typename Context::result_type Result;
+  e.epoch = ctx.epoch;
+  e.solve_time_cpu = ctx.solve_time.cpu.elapsed_now();
+  e.solve_time_wall = ctx.solve_time.wall.elapsed_now();
+  e.eval_time_cpu = ctx.eval_time.cpu.elapsed_now();
+  e.eval_time_wall = ctx.eval_time.wall.elapsed_now();
+  e.primal = static_cast<Result>(r.primal);
+  e.dual = static_cast<Result>(r.dual);
+  e.primal_loss = static_cast<Result>(r.primal_loss);
+  e.dual_loss = static_cast<Result>(r.dual_loss);
+  e.primal_regularizer = static_cast<Result>(r.primal_regularizer);
+  e.dual_regularizer = static_cast<Result>(r.dual_regularizer);
+}
+
+// Filling the appended record as eval_end does (eval/core.h:43-132).
+template <typename Result, typename Context>
+inline void fill(sdca::eval_train<Result, sdca::multiclass_output>& e, const Context& ctx,
+                 const sdca_eval_record& r, const std::vector<double>& acc) {
+  fill_train(e, ctx, r);
+  e.accuracy.assign(acc.begin(), acc.end());
+}
+template <typename Result, typename Context>
+inline void fill(sdca::eval_train<Result, sdca::multilabel_output>& e, const Context& ctx,
+                 const sdca_eval_record& r, const std::vector<double>&) {
+  fill_train(e, ctx, r);
+  e.rank_loss = static_cast<Result>(r.rank_loss);
+}
+template <typename Result, typename Context>
+inline void fill(sdca::eval_test<Result, sdca::multiclass_output>& e, const Context&,
+                 const sdca_eval_record& r, const std::vector<double>& acc) {
+  e.primal_loss = static_cast<Result>(r.primal_loss);
+  e.accuracy.assign(acc.begin(), acc.end());
+}
+template <typename Result, typename Context>
+inline void fill(sdca::eval_test<Result, sdca::multilabel_output>& e, const Context&,
+                 const sdca_eval_record& r, const std::vector<double>&) {
+  e.primal_loss = static_cast<Result>(r.primal_loss);
+  e.rank_loss = static_cast<Result>(r.rank_loss);
+}
+template <typename Eval> struct is_test : std::false_type {};
+template <typename R, typename O> struct is_test<sdca::eval_test<R, O>> : std::true_type {};
+
+}  // namespace detail
+
+// evaluate_dataset (solver/eval.h:15-51) on the GPU: feature or kernel
+// input, multiclass or multilabel output, training set (eval_train) or test
+// set (eval_test), with the objective of ctx.  Host arrays are staged
+// through device memory.  The reference's logging of the record
+// (reporting::eval_created) and its SDCA_ACCURATE_MATH primal
+// recomputation are not done here (recompute_primal does the latter).
+template <typename Data, template <typename> class Input, typename Dataset, typename Context>
+inline void evaluate_dataset(const Context& ctx, Dataset& d,
+                             sdca::solver_scratch<Data, Input>& /*scratch*/,
+                             std::size_t /*id*/ = 0) {
+  typedef typename Context::result_type Result;
+  typedef typename Dataset::eval_type Eval;
+  typedef typename Dataset::output_type Output;
+  const bool test = detail::is_test<Eval>::value;
+  const std::int64_t m = static_cast<std::int64_t>(d.num_classes());
+  const std::int64_t n = static_cast<std::int64_t>(d.num_examples());
+  std::vector<std::int64_t> labels, offsets;
+  detail::labels_of(d.out, labels, offsets,
+                    std::integral_constant<bool, std::is_same<Output, sdca::multilabel_output>::value>());
+  const sdca_objective ob = detail::objective_of<typename Context::objective_type>::get(ctx.objective);
+  sdca_eval_record rec;
+  std::vector<double> acc(static_cast<std::size_t>(m), 0.0);
+  detail::check(detail::eval_call(d.in, ctx, ob, detail::dtype<Result>::value, m, n, labels,
+                                  offsets, &rec, offsets.empty() ? acc.data() : nullptr, test));
+  d.evals.resize(d.evals.size() + 1);
+  detail::fill(d.evals.back(), ctx, rec, acc);
 }
 
 // W = W0 + X A' (eval_recompute_primal, eval/core.h:148-182): X is d x n,

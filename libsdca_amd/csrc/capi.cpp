@@ -112,13 +112,17 @@ int stage_in(const void* host, size_t bytes, DeviceBuffer& buf, hipStream_t stre
   return SDCA_OK;
 }
 
-int check_dtypes(int data, int result) {
+// The prox operators take every (data, result) pair of the Matlab front
+// end's precision dispatch (mex_prox.cpp:179-201) except long double; the
+// evaluation pass takes (f32, f32), (f32, f64) and (f64, f64).
+int check_dtypes(int data, int result, bool prox = false) {
   if (data == SDCA_LONG_DOUBLE || result == SDCA_LONG_DOUBLE)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "long double precision is not supported on the GPU");
   if ((data != SDCA_F32 && data != SDCA_F64) || (result != SDCA_F32 && result != SDCA_F64))
     return fail(SDCA_ERR_PRECISION, "unknown precision (data %d, result %d)", data, result);
-  if (data == SDCA_F64 && result == SDCA_F32)
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "double data with single precision result is not supported");
+  if (!prox && data == SDCA_F64 && result == SDCA_F32)
+    return fail(SDCA_ERR_NOT_IMPLEMENTED,
+                "the evaluation pass takes no double data with a single precision result");
   return SDCA_OK;
 }
 
@@ -169,7 +173,7 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
     return fail(SDCA_ERR_PROX, "unknown prox operator %d", static_cast<int>(op));
   const bool biased = op == SDCA_PROX_KNAPSACK_LE_BIASED || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
                       op == SDCA_PROX_TOPK_CONE_BIASED;
-  int rc = check_dtypes(data, result);
+  int rc = check_dtypes(data, result, true);
   if (rc) return rc;
   if (m < 1) return fail(SDCA_ERR_ARG_RANGE, "m must be >= 1 (got %lld)", (long long)m);
   if (n < 0) return fail(SDCA_ERR_ARG_RANGE, "n must be >= 0 (got %lld)", (long long)n);
@@ -576,10 +580,17 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
     r.dual = r.dual_loss - dreg;
   }
   if (!multilabel && accuracy) {
+    // eval_end: partial_sum of the counts, then scaled by coeff = 1 / n, both
+    // in the Result type (eval/core.h:65-68), so the fractions are the
+    // reference's to the last bit.
     unsigned long long run = 0;
+    const double coeff_d = 1.0 / static_cast<double>(n);
+    const float coeff_f = 1.0f / static_cast<float>(n);
     for (int64_t j = 0; j < m; ++j) {
       run += hist[j];
-      accuracy[j] = static_cast<double>(run) / static_cast<double>(n);
+      accuracy[j] = result == SDCA_F32
+                        ? static_cast<double>(static_cast<float>(run) * coeff_f)
+                        : static_cast<double>(run) * coeff_d;
     }
   }
   return SDCA_OK;

@@ -70,7 +70,10 @@ hipError_t launch_by_m(const ProxLaunch& a) {
 #ifndef SDCA_M100_G
 #define SDCA_M100_G 4
 #endif
-  if (a.m <= 100) return launch_one<FAM, KM, D, R, SDCA_M100_G, 100 / SDCA_M100_G>(a);
+#ifndef SDCA_M100_C
+#define SDCA_M100_C (100 / SDCA_M100_G)
+#endif
+  if (a.m <= 100) return launch_one<FAM, KM, D, R, SDCA_M100_G, SDCA_M100_C>(a);
   if (a.m <= 128) return launch_one<FAM, KM, D, R, 4, 32>(a);
   if (a.m <= 200) return launch_one<FAM, KM, D, R, 8, 25>(a);
   if (a.m <= 256) return launch_one<FAM, KM, D, R, 16, 16>(a);
@@ -84,6 +87,7 @@ hipError_t launch_by_type(const ProxLaunch& a) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_by_m<FAM, KM, float, float>(a);
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_by_m<FAM, KM, float, double>(a);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_by_m<FAM, KM, double, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_by_m<FAM, KM, double, float>(a);
   return hipErrorInvalidValue;
 }
 

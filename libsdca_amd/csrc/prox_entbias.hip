@@ -483,6 +483,7 @@ hipError_t launch_two_ent(const ProxLaunch& a) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_twoent_t<float, float>(a);
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_twoent_t<float, double>(a);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_twoent_t<double, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_twoent_t<double, float>(a);
   return hipErrorInvalidValue;
 }
 
@@ -490,6 +491,7 @@ hipError_t launch_ent_biased(const ProxLaunch& a) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_t<float, float>(a);
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_t<float, double>(a);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_t<double, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_t<double, float>(a);
   return hipErrorInvalidValue;
 }
 

@@ -1311,7 +1311,10 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
         // The cached exp(x - mx0) may have underflowed where exp(x - t) does
         // not when t < mx0 (after fixing, or for a large rhs); then the map
         // is evaluated directly.
-        if (!th.slow && escale <= R(1)) {
+        // Double data with a float Result: the map is evaluated in the data
+        // type, as the reference's prox does (proxdef.h:181-196), not from
+        // the float cache.
+        if (!th.slow && escale <= R(1) && sizeof(R) >= sizeof(D)) {
 #pragma unroll
           for (int c = 0; c < C; ++c) {
             if (c < nvalid)

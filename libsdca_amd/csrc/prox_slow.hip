@@ -381,9 +381,11 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   while (pow2 < a.m) pow2 <<= 1;
   // List mode: the list is a small fraction of the n columns and usually
   // empty; the grid grows with n (about one workgroup per 1024 columns,
-  // 512 to 4096), so that a long list finds workgroups on every CU while
-  // an empty one on a small batch costs little to launch.
-  const int64_t cap = all_columns ? 4096 : std::min<int64_t>(4096, std::max<int64_t>(512, a.n / 1024));
+  // 512 to 1024: four per CU), so that a long list finds workgroups on
+  // every CU while an empty one costs little to launch (the launch of 3906
+  // workgroups for an empty C2 list took 0.5 % of the step; 1024 runs the
+  // biased cone's deferred columns as fast).
+  const int64_t cap = all_columns ? 4096 : std::min<int64_t>(1024, std::max<int64_t>(512, a.n / 1024));
   const int64_t grid = a.n < cap ? a.n : cap;
   // One wave per workgroup for short columns (the sort's stages then need
   // no cross-wave barrier and four times as many columns are in flight),
@@ -563,6 +565,7 @@ hipError_t launch_slow(const ProxLaunch& a, bool all_columns) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_slow_t<float, float>(a, all_columns);
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_slow_t<float, double>(a, all_columns);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_slow_t<double, double>(a, all_columns);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_slow_t<double, float>(a, all_columns);
   return hipErrorInvalidValue;
 }
 
@@ -570,6 +573,7 @@ hipError_t launch_two_sort(const ProxLaunch& a, bool all_columns) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_two_sort_t<float, float>(a, all_columns);
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_two_sort_t<float, double>(a, all_columns);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_two_sort_t<double, double>(a, all_columns);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_two_sort_t<double, float>(a, all_columns);
   return hipErrorInvalidValue;
 }
 

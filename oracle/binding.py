@@ -58,6 +58,9 @@ def build(with_reference=True):
     subprocess.check_call(["make", "-s", "-B", "-C", HERE, "all"])
     if with_reference and os.path.isdir(os.path.join(REFERENCE_TREE, "include")):
         subprocess.check_call(["make", "-s", "-B", "-C", HERE, "ref"])
+        # needs the product library, built first by __graft_entry__.build()
+        if os.path.exists(os.path.join(HERE, "..", "libsdca_amd", "libsdca_hip.so")):
+            subprocess.check_call(["make", "-s", "-B", "-C", HERE, "dropin"])
 
 
 _libs = {}

@@ -76,6 +76,9 @@ def test_prox_operator_and_precision_checks():
     with pytest.raises(sd.SdcaError) as e:
         sd.prox("two_simplex", x, p=5)
     assert e.value.status == 2
+    with pytest.raises(sd.SdcaError) as e:  # the evaluation takes no (double, float) pair
+        sd.eval_scores([sd.objective("l2_entropy")], np.zeros((3, 5)), [0, 1, 2], result="float")
+    assert e.value.status == 4
     with pytest.raises(sd.SdcaError) as e:
         sd.prox("two_simplex", x, col_p=[1, 9, 1])
     assert e.value.status == 2

@@ -70,9 +70,10 @@ def record_blocks(op, n, m, kw):
     return out
 
 
-def apply_record(oracle, op, z, t, lo, hi, kw):
+def apply_record(oracle, op, z, t, lo, hi, kw, result=F64):
     """clamp(map(z - t), lo, hi) in float64 with the map of the operator's
-    threshold record (math/functor.h:14-38)."""
+    threshold record (math/functor.h:14-38); alpha of the a_lambert map is
+    the Result-type value the reference forms 1 / alpha from."""
     u = np.asarray(z, dtype=np.float64) - t
     if op in ("entropy", "topk_entropy"):
         with np.errstate(over="ignore"):
@@ -82,12 +83,13 @@ def apply_record(oracle, op, z, t, lo, hi, kw):
         oracle.prox("lambert_w_exp", w)
         u = w[0]
         if op != "entropy_norm":
-            u = u / kw.get("alpha", 1.0)
+            alpha = kw.get("alpha", 1.0)
+            u = u / float(np.float32(alpha) if result == F32 else alpha)
     return np.maximum(lo, np.minimum(u, hi))
 
 
 def check_thresholds(oracle, op, x, got, ref, thr_g, thr_r, thr_e, scale, err_col, rtol, what,
-                     kw, keep_cols):
+                     kw, keep_cols, result=F64):
     """The GPU's threshold records against the oracle's, and the sets they
     induce.  Per record (one per column, two per column for the two-block
     operators):
@@ -122,7 +124,7 @@ def check_thresholds(oracle, op, x, got, ref, thr_g, thr_r, thr_e, scale, err_co
         ulps = 8 * u * (np.abs(xs.astype(np.float64)) + abs(tg) + 1.0) * \
             np.maximum(1.0, np.abs(outr))
         tol = (rtol + 3 * float(err_col[j])) * s
-        rep = apply_record(oracle, op, xs, tg, lg, hg, kw)
+        rep = apply_record(oracle, op, xs, tg, lg, hg, kw, result)
         off = np.abs(rep - outr)
         assert (off <= tol + ulps).all(), (
             f"{what}: record {b} (column {j}) = ({tg!r}, {lg!r}, {hg!r}) does not reproduce the "
@@ -191,10 +193,12 @@ def parity(oracle, op, x, got, result, what, nthreads=1, keep=None, thr=None, **
         err_all = np.zeros(n)
         err_all[keep_cols] = err_col
         check_thresholds(oracle, op, x, got, ref, np.asarray(thr), thr_r, thr_e, scale_all,
-                         err_all, rtol, what, kw, keep_cols)
+                         err_all, rtol, what, kw, keep_cols, result)
 
 
-DTYPES = [(np.float32, F32), (np.float32, F64), (np.float64, F64)]
+# Every (Data, Result) pair of the Matlab front end's precision dispatch
+# (mex_prox.cpp:179-201) but long double.
+DTYPES = [(np.float32, F32), (np.float32, F64), (np.float64, F64), (np.float64, F32)]
 # One m per register configuration (G lanes x C slots), plus the sizes of the
 # benchmark configurations.
 MS = [1, 3, 10, 16, 17, 64, 100, 101, 128, 150, 200, 512, 999, 1000, 2048]
