@@ -305,10 +305,10 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
 
     kernel = bool(cfg.get("kernel"))
 
-    def step():
+    def step(fused=False):
         if kernel:  # X = K (n x n_train), W = A (n_train x m)
             return sd.eval_kernel(objs, X, W, labels, offsets=offsets)
-        return sd.eval_features(objs, X, W, labels, offsets=offsets)
+        return sd.eval_features(objs, X, W, labels, offsets=offsets, fused=fused)
 
     for _ in range(warmup):
         step()
@@ -319,6 +319,21 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / steps
+    # The fused form of the same pass (scores and epilogue in one kernel,
+    # scores not stored; SDCA_EVAL_FUSED), timed the same way after the
+    # measured steps where it applies: the default two-kernel form is the
+    # faster on MI355X, and the records must be bit-identical.
+    fused_ms = None
+    if not kernel and not cfg.get("multilabel"):
+        step(fused=True)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            recs_f, _, _ = step(fused=True)
+        torch.cuda.synchronize()
+        fused_ms = (time.perf_counter() - t1) * 1e3 / steps
+        if recs_f != recs:
+            raise RuntimeError("fused and two-kernel evaluation records differ")
     # The dominant kernel is the score GEMM: time it on its own, event-timed
     # on the stream it runs on.
     S = torch.empty((cfg["n"], cfg["m"]), dtype=torch.float32, device=dev)
@@ -338,7 +353,7 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
     achieved = flops / (gemm_ms / 1e3) / 1e12
     achieved_pass = flops / (ms_per_step / 1e3) / 1e12
     value = cfg["n"] / (ms_per_step / 1e3)
-    extra = {"records": recs}
+    extra = {"records": recs, "fused_form_ms_per_step": fused_ms}
     if not cfg.get("multilabel"):
         extra["top1"] = float(acc[0])
         extra["top5"] = float(acc[4])

@@ -211,6 +211,20 @@ int sdca_eval_scores(const sdca_objective* objs, int n_obj,
 #define SDCA_EVAL_TEST 2u
 
 /*
+ * flags bit of sdca_eval_features: the fused form where it applies (fp32
+ * data, multiclass, m <= 1024, the smooth top-k hinge and / or the softmax
+ * cross-entropy, no dual variables): one kernel computes the scores on the
+ * matrix cores and evaluates the examples from LDS without storing the
+ * scores, instead of the default two-kernel form (scores written to a
+ * device buffer by the GEMM, then the per-example kernel).  Both forms give
+ * bit-identical records.  The default is the two-kernel form: on MI355X it
+ * is the faster (the fused kernel holds 32 examples x all classes per
+ * workgroup, is limited to 2 waves per SIMD by its registers and re-reads W
+ * per 32 examples).
+ */
+#define SDCA_EVAL_FUSED 4u
+
+/*
  * Whole-dataset evaluation for kernel input: evaluate_dataset (eval.h:15-51)
  * with kernel_input (data/input.h:44-76).  scores_i = A K_i
  * (eval/scores.h:30-47) for all i at once on the matrix cores, with

@@ -410,8 +410,11 @@ def recompute_primal(X, A, W0=None, out=None):
 EVAL_TEST = 2  # SDCA_EVAL_TEST
 
 
+EVAL_FUSED = 4  # SDCA_EVAL_FUSED
+
+
 def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_example, torch_mode,
-          data, tail_args=(), test=False):
+          data, tail_args=(), test=False, fused=False):
     lib = library()
     res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
     objarr = _objs(objs)
@@ -431,6 +434,8 @@ def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_exampl
         flags, stream = HOST_PTR, None
     if test:
         flags |= EVAL_TEST
+    if fused:
+        flags |= EVAL_FUSED
     fn = getattr(lib, fn_name)
     fn.restype = ctypes.c_int
     args = [objarr, ctypes.c_int(len(objs)), ctypes.c_int(data), ctypes.c_int(res)]
@@ -444,14 +449,15 @@ def _eval(fn_name, objs, lead_args, m, n, labels, offsets, A, result, per_exampl
 
 
 def eval_features(objs, X, W, labels, A=None, W0=None, offsets=None, result=None,
-                  per_example=False, test=False):
+                  per_example=False, test=False, fused=False):
     """evaluate_dataset for feature input.  objs: list of objective(...).
     Returns (records, accuracy, per_example): one eval record per objective
     (primal, dual, primal_loss, dual_loss, primal/dual regularizer, rank_loss),
     the top-(i+1) accuracies (multiclass) and optionally the (n, n_obj, 2)
     per-example (primal, dual) losses before the loss coefficient.
     test=True gives a test set's records (eval_test: primal loss and
-    accuracy / rank loss only)."""
+    accuracy / rank loss only).  fused=True runs the one-kernel form where it
+    applies (SDCA_EVAL_FUSED; bit-identical results, slower on MI355X)."""
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(W.shape[0])
     _need(X, "X", (n, d), X)
@@ -461,7 +467,8 @@ def eval_features(objs, X, W, labels, A=None, W0=None, offsets=None, result=None
     lead = (X, [ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
                 ctypes.c_void_p(_ptr(X)), ctypes.c_void_p(_ptr(W))])
     return _eval("sdca_eval_features", objs, lead, m, n, labels, offsets, A, result, per_example,
-                 _is_torch(X), _dtype_code(X), tail_args=(ctypes.c_void_p(_ptr(W0)),), test=test)
+                 _is_torch(X), _dtype_code(X), tail_args=(ctypes.c_void_p(_ptr(W0)),), test=test,
+                 fused=fused)
 
 
 def eval_kernel(objs, K, A, labels, offsets=None, result=None, per_example=False, test=False):

@@ -451,7 +451,8 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
                    const int64_t* doffsets, const void* dW, const void* dW0, int64_t dm,
                    const void* dA_reg, bool test, double preg_in, double dreg_in,
                    sdca_eval_record* records, double* accuracy, double* per_example,
-                   bool per_example_host, hipStream_t stream) {
+                   bool per_example_host, hipStream_t stream, const float* fused_X = nullptr,
+                   const float* fused_W = nullptr, int64_t fused_d = 0) {
   using namespace sdca_gpu;
   const bool multilabel = doffsets != nullptr;
   if (test) {
@@ -514,7 +515,15 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
   a.bad = d_bad;
   a.stream = stream;
   SDCA_HIP_TRY(launch_clear(d_bad, 2, stream), "clear kernel");  // flag and deferred count
-  SDCA_HIP_TRY(launch_eval_epilogue(a), "evaluation epilogue kernel");
+  if (fused_X) {
+    // Scores and epilogue in one kernel; dS receives only the rows of
+    // deferred examples, which the deferred-example kernel reads.
+    SDCA_HIP_TRY(launch_eval_fused(fused_X, fused_W, a, fused_d,
+                                   static_cast<float*>(const_cast<void*>(dS))),
+                 "fused evaluation kernel");
+  } else {
+    SDCA_HIP_TRY(launch_eval_epilogue(a), "evaluation epilogue kernel");
+  }
   if (!multilabel) SDCA_HIP_TRY(launch_eval_slow(a), "evaluation epilogue (deferred examples)");
   SDCA_HIP_TRY(launch_eval_reduce(a, d_sums, multilabel ? d_sums + 2 * kMaxObjectives : nullptr,
                                   multilabel ? nullptr : d_hist, d_red),
@@ -744,6 +753,30 @@ static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, s
     if ((rc = workspace(stream, 3, es * static_cast<size_t>(m) * static_cast<size_t>(d), &wt))) return rc;
     SDCA_HIP_TRY(launch_transpose(data, pA, wt, d, m, stream), "transpose kernel");
     pW = wt;
+  }
+  bool fused = false;
+  if (!pS && !kernel && data == SDCA_F32 && (flags & SDCA_EVAL_FUSED)) {
+    EvalLaunch probe;
+    probe.data = data;
+    probe.result = result;
+    probe.m = m;
+    probe.n = n;
+    probe.A = test ? nullptr : pA;
+    probe.offsets = poff;
+    probe.objs.n = n_obj;
+    for (int o = 0; o < n_obj; ++o) {
+      probe.objs.o[o].kind = objs[o].kind;
+      probe.objs.o[o].k = static_cast<int>(objs[o].k);
+    }
+    fused = eval_fused_supported(probe, d);
+  }
+  if (fused) {
+    // The fused kernel's buffer for the score rows of deferred examples.
+    void* sbuf = nullptr;
+    if ((rc = workspace(stream, 1, es * static_cast<size_t>(m) * static_cast<size_t>(n), &sbuf))) return rc;
+    return eval_on_device(objs, n_obj, data, result, m, n, sbuf, pA, pl, poff, pW, pW0, d * m,
+                          nullptr, test, preg, dreg, records, accuracy, per_example, host, stream,
+                          static_cast<const float*>(pX), static_cast<const float*>(pW), d);
   }
   if (!pS) {
     // scores = W' X into the stream's workspace

@@ -30,6 +30,9 @@ namespace sdca_gpu {
 
 namespace {
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <class R>
 struct SetStats {
   R sum_u, sum_m, dot_m;
@@ -242,25 +245,31 @@ __device__ inline R lse_all(const D (&v)[C], int nvalid) {
   return mx + dlog1p(lse_sum_excl<G, C, D, R>(v, mask, mx));
 }
 
-template <int G, int C, int KM, class D, class R>
-__global__ void __launch_bounds__(64)
-eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
-                       const int64_t* __restrict__ labels, int64_t m64, int64_t n, EvalObjs objs,
-                       double* __restrict__ per_example, int* __restrict__ counts,
-                       int* __restrict__ slow, int* __restrict__ bad) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  D* lds = reinterpret_cast<D*>(smem_raw);
-  constexpr int B = 64 / G;
-  const int m = static_cast<int>(m64);
-  const int lc = static_cast<int>(threadIdx.x) / G;
-  const int g = static_cast<int>(threadIdx.x) % G;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * B + lc;
-  const bool active = i < n;
-  const int64_t ii = active ? i : 0;  // inactive groups compute on example 0, store nothing
-  D* const lds_col = lds + lc * m;
-  D* const lds_dummy = lds + B * m + threadIdx.x;
-
-  const D* srow = S + ii * m64;
+// The per-example part of the multiclass evaluation (eval.h:36-47) for
+// example i (active: a real example; inactive groups compute on example 0
+// and store nothing), its m scores at srow (global memory, or the LDS tile
+// of the fused kernel), g the lane's index in its group of G.  lds_col is
+// the example's row of m words of LDS scratch (it may be the scores' own
+// row: they are read into registers first), lds_dummy the lane's dummy word.
+// save_row (or NULL): where the example's scores are written when one of its
+// objectives is deferred to eval_slow_kernel, which reads them from global
+// memory (the fused kernel keeps scores out of it otherwise).  Returns true
+// when some objective of the example was deferred.
+// MASK: the objective kinds compiled in (bit sdca_objective_kind; the
+// others are skipped), HAS_A: whether dual variables may be given.  The fused
+// kernel instantiates the set it runs to keep its registers down.
+constexpr unsigned kAllMulticlass = 0x3fu;
+template <int G, int C, int KM, class D, class R, unsigned MASK = kAllMulticlass,
+          bool HAS_A = true>
+__device__ __forceinline__ bool eval_example_mc(const D* srow, const D* __restrict__ A,
+                                                const int64_t* __restrict__ labels, int m,
+                                                int64_t i, int64_t ii, bool active, int g,
+                                                const EvalObjs& objs,
+                                                double* __restrict__ per_example,
+                                                int* __restrict__ counts, int* __restrict__ slow,
+                                                int* __restrict__ bad, D* lds_col, D* lds_dummy,
+                                                D* save_row = nullptr) {
+  const int64_t m64 = m;
   // Device-resident labels reach the kernel unchecked: a label outside
   // [0, m) raises *bad (the call then fails with the reference's label
   // error, data/output.h:169-182) and is read as 0, so no load leaves the row.
@@ -287,7 +296,7 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
   // Dual variables of the example.
   D a[C];
   D ay = 0;
-  if (A) {
+  if (HAS_A && A) {
     const D* arow = A + ii * m64;
     ay = arow[y];
 #pragma unroll
@@ -297,6 +306,7 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
     for (int c = 0; c < C; ++c) a[c] = 0;
   }
 
+  bool any_deferred = false;
   for (int o = 0; o < objs.n; ++o) {
     const EvalObj ob = objs.o[o];
     const R c_ = static_cast<R>(ob.c), gamma = static_cast<R>(ob.gamma);
@@ -314,6 +324,7 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
     switch (ob.kind) {
       case SDCA_OBJ_HINGE_TOPK:
       case SDCA_OBJ_TOPK_HINGE: {
+        if constexpr ((MASK & ((1u << SDCA_OBJ_HINGE_TOPK) | (1u << SDCA_OBJ_TOPK_HINGE))) == 0) break;
         constexpr int L = KM + 1;
         D top[L];
 #pragma unroll
@@ -332,19 +343,23 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
         break;
       }
       case SDCA_OBJ_HINGE_TOPK_SMOOTH: {
+        if constexpr ((MASK & (1u << SDCA_OBJ_HINGE_TOPK_SMOOTH)) == 0) break;
         deferred = !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, nvalid, k, gamma, lds_col,
                                                       lds_dummy, primal);
         break;
       }
       case SDCA_OBJ_TOPK_HINGE_SMOOTH: {
+        if constexpr ((MASK & (1u << SDCA_OBJ_TOPK_HINGE_SMOOTH)) == 0) break;
         primal = smooth_topk_hinge_beta<G, C, D, R>(h, m - 1, k, gamma);
         break;
       }
       case SDCA_OBJ_ENTROPY: {
+        if constexpr ((MASK & (1u << SDCA_OBJ_ENTROPY)) == 0) break;
         primal = lse_all<G, C, D, R>(s, nvalid) - static_cast<R>(sy);
         break;
       }
       case SDCA_OBJ_ENTROPY_TOPK: {
+        if constexpr ((MASK & (1u << SDCA_OBJ_ENTROPY_TOPK)) == 0) break;
         // a_j = s_j - s_y (l2_entropy_topk.h:78-80), then the top-k entropy thresholds
         const D shift0 = -sy;
         D v[C];
@@ -375,6 +390,10 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
     switch (ob.kind) {
       case SDCA_OBJ_HINGE_TOPK_SMOOTH:
       case SDCA_OBJ_TOPK_HINGE_SMOOTH: {  // l2_hinge_topk.h:182-192
+        if constexpr (!HAS_A) {
+          dual = 0;
+          break;
+        }
         R sq = 0;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
@@ -388,6 +407,11 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
       }
       case SDCA_OBJ_ENTROPY:
       case SDCA_OBJ_ENTROPY_TOPK: {  // l2_entropy.h:94-114, l2_entropy_topk.h:97-107
+        if constexpr (!HAS_A) {
+          // A = 0: c log c - x log x(c) - sum x log x(0) = 0
+          dual = x_log_x(c_) - x_log_x(c_);
+          break;
+        }
         R acc = 0;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
@@ -411,7 +435,34 @@ eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
         slow[2 + 2 * pos] = o;
       }
     }
+    any_deferred = any_deferred || deferred;
   }
+  if (save_row && active && any_deferred) {
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      if (c < nvalid) save_row[g + G * c] = s[c];
+  }
+  return any_deferred;
+}
+
+template <int G, int C, int KM, class D, class R>
+__global__ void __launch_bounds__(64)
+eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
+                       const int64_t* __restrict__ labels, int64_t m64, int64_t n, EvalObjs objs,
+                       double* __restrict__ per_example, int* __restrict__ counts,
+                       int* __restrict__ slow, int* __restrict__ bad) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  D* lds = reinterpret_cast<D*>(smem_raw);
+  constexpr int B = 64 / G;
+  const int m = static_cast<int>(m64);
+  const int lc = static_cast<int>(threadIdx.x) / G;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * B + lc;
+  const bool active = i < n;
+  const int64_t ii = active ? i : 0;  // inactive groups compute on example 0, store nothing
+  eval_example_mc<G, C, KM, D, R>(S + ii * m64, A, labels, m, i, ii, active, g, objs,
+                                  per_example, counts, slow, bad, lds + lc * m,
+                                  lds + B * m + threadIdx.x);
 }
 
 // Two-block simplex sets (two_simplex.h:18-119) with block a = the slots in
@@ -862,6 +913,230 @@ eval_slow_kernel(const D* __restrict__ S, const int64_t* __restrict__ labels, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused evaluation pass (feature input, fp32 data, multiclass): scores
+// W' x_i on the matrix cores and the per-example epilogue in one kernel, the
+// scores never stored.  A workgroup of four waves owns E = 32 examples and
+// every class (m <= 1024, padded to 4 NBW 32): wave w accumulates the
+// 32 x (32 NBW) block of classes [32 NBW w, 32 NBW (w + 1)) in NBW
+// v_mfma_f32_32x32x2f32 accumulators (16 NBW fp32 per lane).  The reduction
+// runs in slabs of 8 with the next slab prefetched into registers while the
+// current one is multiplied out of LDS ([k][row], padded rows), and visits k
+// in the same pairs and operand lanes as the unfused scores_gemm_kernel, so
+// every score is bit-identical to the unfused path's.  Then, for each half
+// of the 32 examples, the accumulators are written to the LDS the slabs used
+// (16 x m scores) and each wave runs the per-example epilogue
+// (eval_example_mc) on four of them with one example per wave (G = 64),
+// while the other workgroup of its CU (two fit: 68 KB of LDS each) keeps the
+// matrix cores busy.  W (16 MB at C4) is re-read by every workgroup from the
+// L2 / Infinity Cache: 32 examples per read give 16 flop per byte.
+// ---------------------------------------------------------------------------
+constexpr int kFusedE = 32;   // examples per workgroup
+constexpr int kFusedBK = 8;   // reduction slab
+
+template <int NBW>
+struct FusedShape {
+  static constexpr int BN = 4 * NBW * 32;         // padded classes
+  static constexpr int LDA = kFusedE + 4, LDB = BN + 4;
+  static constexpr int FLOATS = 2 * kFusedBK * LDA + 2 * kFusedBK * LDB;
+  static constexpr int NVA = (kFusedE * kFusedBK / 4 + 255) / 256;
+  static constexpr int NVB = (BN * kFusedBK / 4 + 255) / 256;
+};
+
+// The slab [k0, k0 + 8) of rows [r0, r0 + ROWS) of a (rows x d) matrix into
+// float4 registers (two per row); rows past `rows` and columns past d read 0.
+template <int ROWS, int NV>
+__device__ inline void fused_load(const float* __restrict__ src, int64_t rows, int64_t d,
+                                  int64_t r0, int64_t k0, bool vec, f32x4 (&r)[NV]) {
+#pragma unroll
+  for (int h = 0; h < NV; ++h) {
+    const int f = static_cast<int>(threadIdx.x) + 256 * h;
+    const int row = f >> 1, q = f & 1;
+    const int64_t gr = r0 + row;
+    const int64_t gk = k0 + 4 * q;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (f < ROWS * 2 && gr < rows) {
+      const float* p = src + gr * d + gk;
+      if (vec && gk + 4 <= d) {
+        v = *reinterpret_cast<const f32x4*>(p);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gk + e < d) v[e] = p[e];
+      }
+    }
+    r[h] = v;
+  }
+}
+
+// The float4 of a slab into LDS transposed to [k][row].
+template <int ROWS, int NV>
+__device__ inline void fused_store(float* __restrict__ lds, int ld, const f32x4 (&r)[NV]) {
+#pragma unroll
+  for (int h = 0; h < NV; ++h) {
+    const int f = static_cast<int>(threadIdx.x) + 256 * h;
+    const int row = f >> 1, q = f & 1;
+    if (f < ROWS * 2) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lds[(4 * q + e) * ld + row] = r[h][e];
+    }
+  }
+}
+
+template <int NBW, int G, int C, int KM, class R, unsigned MASK, bool HAS_A>
+__global__ void __launch_bounds__(256, 2)
+eval_fused_mc_kernel(const float* __restrict__ X, const float* __restrict__ W,
+                     const float* __restrict__ A, const int64_t* __restrict__ labels, int64_t n,
+                     int64_t m64, int64_t d, EvalObjs objs, double* __restrict__ per_example,
+                     int* __restrict__ counts, int* __restrict__ slow, int* __restrict__ bad,
+                     float* __restrict__ s_deferred, int vec) {
+  typedef FusedShape<NBW> Sh;
+  __shared__ __align__(16) float smem[Sh::FLOATS];
+  float* const As0 = smem;
+  float* const Bs0 = smem + 2 * kFusedBK * Sh::LDA;
+  const int m = static_cast<int>(m64);
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kFusedE;
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int lr = lane & 31, lk = lane >> 5;
+  const int c0 = wave * NBW * 32;  // first class of this wave's block
+
+  f32x16 acc[NBW];
+#pragma unroll
+  for (int b = 0; b < NBW; ++b)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[b][e] = 0.f;
+
+  const bool vv = vec != 0;
+  f32x4 ra[Sh::NVA], rb[Sh::NVB];
+  fused_load<kFusedE, Sh::NVA>(X, n, d, i0, 0, vv, ra);
+  fused_load<Sh::BN, Sh::NVB>(W, m64, d, 0, 0, vv, rb);
+  fused_store<kFusedE, Sh::NVA>(As0, Sh::LDA, ra);
+  fused_store<Sh::BN, Sh::NVB>(Bs0, Sh::LDB, rb);
+  __syncthreads();
+  const int64_t nslabs = (d + kFusedBK - 1) / kFusedBK;
+  for (int64_t sl = 0; sl < nslabs; ++sl) {
+    const int cur = static_cast<int>(sl & 1);
+    const bool more = sl + 1 < nslabs;
+    if (more) {
+      fused_load<kFusedE, Sh::NVA>(X, n, d, i0, (sl + 1) * kFusedBK, vv, ra);
+      fused_load<Sh::BN, Sh::NVB>(W, m64, d, 0, (sl + 1) * kFusedBK, vv, rb);
+    }
+    const float* as = As0 + cur * kFusedBK * Sh::LDA;
+    const float* bs = Bs0 + cur * kFusedBK * Sh::LDB;
+#pragma unroll
+    for (int kk = 0; kk < kFusedBK; kk += 2) {
+      const int kr = kk + lk;
+      const float av = as[kr * Sh::LDA + lr];
+      float bv[NBW];
+#pragma unroll
+      for (int b = 0; b < NBW; ++b) bv[b] = bs[kr * Sh::LDB + c0 + 32 * b + lr];
+#pragma unroll
+      for (int b = 0; b < NBW; ++b)
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv[b], acc[b], 0, 0, 0);
+    }
+    if (more) {
+      fused_store<kFusedE, Sh::NVA>(As0 + (cur ^ 1) * kFusedBK * Sh::LDA, Sh::LDA, ra);
+      fused_store<Sh::BN, Sh::NVB>(Bs0 + (cur ^ 1) * kFusedBK * Sh::LDB, Sh::LDB, rb);
+    }
+    __syncthreads();
+  }
+
+  // Accumulator r of lane l holds example 8 (r / 4) + 4 (l / 32) + r % 4 and
+  // class l % 32 of its block: r < 8 are examples 0-15, r >= 8 are 16-31.
+  float* const ss = smem;                           // 16 x m scores
+  float* const dummies = smem + kFusedE / 2 * m;    // one word per thread
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int b = 0; b < NBW; ++b) {
+      const int col = c0 + 32 * b + lr;
+      if (col < m) {
+#pragma unroll
+        for (int r = 8 * half; r < 8 * half + 8; ++r) {
+          const int row = 8 * (r / 4) + 4 * lk + (r % 4) - 16 * half;
+          ss[row * m + col] = acc[b][r];
+        }
+      }
+    }
+    __syncthreads();
+    // Groups of G lanes per example, as the two-kernel epilogue uses for
+    // this m (so the per-example sums run in the same order): a wave pass
+    // covers 64 / G examples, the four waves 256 / G.
+    constexpr int B = 64 / G;
+    constexpr int PASSES = (kFusedE / 2 + 4 * B - 1) / (4 * B);
+#pragma unroll 1
+    for (int q = 0; q < PASSES; ++q) {
+      const int row0 = (q * 4 + wave) * B;  // first example of this wave pass
+      if (row0 >= kFusedE / 2) break;       // wave-uniform
+      // B divides 16, so every group of the pass has its own row of the
+      // half; past n a group computes on its (zero) row and stores nothing.
+      const int row = row0 + lane / G;
+      const int64_t i = i0 + 16 * half + row;
+      const bool active = i < n;
+      const int64_t ii = active ? i : 0;
+      float* const srow = ss + row * m;
+      eval_example_mc<G, C, KM, float, R, MASK, HAS_A>(
+          srow, A, labels, m, i, ii, active, lane % G, objs, per_example, counts, slow, bad,
+          srow, dummies + threadIdx.x, s_deferred + ii * m64);
+    }
+    __syncthreads();
+  }
+}
+
+template <int NBW, class R, unsigned MASK, bool HAS_A>
+hipError_t launch_fused_set(const float* X, const float* W, const EvalLaunch& a, int64_t d,
+                            float* s_deferred, bool km8) {
+  const int64_t grid = (a.n + kFusedE - 1) / kFusedE;
+  const int vec = (d % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(W) & 15) == 0) ? 1 : 0;
+  // (G, C) as launch_typed picks for the two-kernel epilogue.
+#define SDCA_FUSED_LAUNCH(G_, KM_)                                                          \
+  hipLaunchKernelGGL((eval_fused_mc_kernel<NBW, G_, 16, KM_, R, MASK, HAS_A>),             \
+                     dim3(static_cast<unsigned>(grid)), dim3(256), 0, a.stream, X, W,       \
+                     static_cast<const float*>(a.A), a.labels, a.n, a.m, d, a.objs,         \
+                     a.per_example, a.counts, a.slow, a.bad, s_deferred, vec)
+  if (a.m <= 64) {
+    if (!km8) SDCA_FUSED_LAUNCH(4, 5); else SDCA_FUSED_LAUNCH(4, 8);
+  } else if (a.m <= 256) {
+    if (!km8) SDCA_FUSED_LAUNCH(16, 5); else SDCA_FUSED_LAUNCH(16, 8);
+  } else {
+    if (!km8) SDCA_FUSED_LAUNCH(64, 5); else SDCA_FUSED_LAUNCH(64, 8);
+  }
+#undef SDCA_FUSED_LAUNCH
+  return hipGetLastError();
+}
+
+// The objective sets with their own instantiation: the smooth top-k hinge
+// with the softmax cross-entropy (the C4 pair), either alone, without
+// dual variables (a cold start); anything else takes the general form.
+constexpr unsigned kSmoothEntropy =
+    (1u << SDCA_OBJ_HINGE_TOPK_SMOOTH) | (1u << SDCA_OBJ_ENTROPY);
+
+template <int NBW, class R>
+hipError_t launch_fused_nbw(const float* X, const float* W, const EvalLaunch& a, int64_t d,
+                            float* s_deferred) {
+  int kmax = 1;
+  unsigned kinds = 0;
+  for (int o = 0; o < a.objs.n; ++o) {
+    kmax = a.objs.o[o].k > kmax ? a.objs.o[o].k : kmax;
+    kinds |= 1u << a.objs.o[o].kind;
+  }
+  const bool km8 = kmax > 5;
+  if (a.A || (kinds & ~kSmoothEntropy) != 0) return hipErrorInvalidValue;
+  return launch_fused_set<NBW, R, kSmoothEntropy, false>(X, W, a, d, s_deferred, km8);
+}
+
+template <class R>
+hipError_t launch_fused_typed(const float* X, const float* W, const EvalLaunch& a, int64_t d,
+                              float* s_deferred) {
+  // Classes per wave in blocks of 32: the fewest that cover m (m <= 1024).
+  if (a.m <= 128) return launch_fused_nbw<1, R>(X, W, a, d, s_deferred);
+  if (a.m <= 256) return launch_fused_nbw<2, R>(X, W, a, d, s_deferred);
+  if (a.m <= 512) return launch_fused_nbw<4, R>(X, W, a, d, s_deferred);
+  return launch_fused_nbw<8, R>(X, W, a, d, s_deferred);
+}
+
 template <class D, class R, int G, int C, int KM>
 hipError_t launch_mc(const EvalLaunch& a) {
   constexpr int B = 64 / G;
@@ -1124,6 +1399,25 @@ hipError_t launch_eval_slow(const EvalLaunch& a) {
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_slow_typed<float, double>(a);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_slow_typed<double, double>(a);
   return hipErrorInvalidValue;
+}
+
+bool eval_fused_supported(const EvalLaunch& a, int64_t d) {
+  (void)d;
+  if (!(a.data == SDCA_F32 && (a.result == SDCA_F32 || a.result == SDCA_F64) && !a.offsets &&
+        a.m >= 2 && a.m <= 1024))
+    return false;
+  // The general objective set needs more registers than two workgroups per
+  // CU allow (it spills); it keeps the two-kernel form.
+  unsigned kinds = 0;
+  for (int o = 0; o < a.objs.n; ++o) kinds |= 1u << a.objs.o[o].kind;
+  return !a.A && (kinds & ~kSmoothEntropy) == 0;
+}
+
+hipError_t launch_eval_fused(const float* X, const float* W, const EvalLaunch& a, int64_t d,
+                             float* s_deferred) {
+  if (!eval_fused_supported(a, d)) return hipErrorInvalidValue;
+  if (a.result == SDCA_F32) return launch_fused_typed<float>(X, W, a, d, s_deferred);
+  return launch_fused_typed<double>(X, W, a, d, s_deferred);
 }
 
 int64_t eval_reduce_scratch(int n_obj) {

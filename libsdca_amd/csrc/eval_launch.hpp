@@ -49,6 +49,13 @@ hipError_t launch_scores_gemm(const float* X, const float* W, float* S, int64_t 
 // The same contraction in double (plain FMA kernel).
 hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, int64_t n,
                                   int64_t m, int64_t d, hipStream_t stream);
+// The fused pass (scores on the matrix cores and the multiclass epilogue in
+// one kernel, scores not stored): fp32 feature input, m <= 1024.  Deferred
+// examples get their score row written to s_deferred (n x m) for
+// launch_eval_slow, which then reads it as S.
+bool eval_fused_supported(const EvalLaunch& a, int64_t d);
+hipError_t launch_eval_fused(const float* X, const float* W, const EvalLaunch& a, int64_t d,
+                             float* s_deferred);
 // Per-example epilogue (losses, counts, rank loss) and its deferred examples.
 hipError_t launch_eval_epilogue(const EvalLaunch& a);
 hipError_t launch_eval_slow(const EvalLaunch& a);

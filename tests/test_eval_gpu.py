@@ -413,3 +413,62 @@ def test_device_multilabel_offsets_are_checked(cuda):
     again, _, _ = sd.eval_scores(ML_OBJS, S, torch.from_numpy(lab).to(cuda),
                                  offsets=torch.from_numpy(off).to(cuda))
     assert again == good
+
+
+def dominant_class_inputs(rng, n, m, frac=0.25):
+    """X, W with d = m and W = 10 I, so s_ij = 10 x_ij; a fraction of the
+    examples get one class far above the label and the rest far below it
+    (h = 6 for that class, -9 for the others): the smooth top-k hinge's
+    top-k simplex then needs the reference's topk_cone_search with U
+    non-empty, which the per-example kernels defer to eval_slow_kernel."""
+    X = (rng.standard_normal((n, m)) * 0.05).astype(np.float32)
+    y = rng.integers(0, m, n)
+    idx = np.flatnonzero(rng.random(n) < frac)
+    for i in idx:
+        j1 = (y[i] + 1 + rng.integers(0, m - 1)) % m
+        X[i, :] = -0.5
+        X[i, y[i]] = 0.5
+        X[i, j1] = 1.0
+    W = (np.eye(m) * 10.0).astype(np.float32)
+    return X, W, y
+
+
+@pytest.mark.parametrize("m", [2, 10, 100, 128, 129, 200, 257, 513, 1000, 1024])
+@pytest.mark.parametrize("objs", [[("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)],
+                                  [("l2_entropy", 2.0, 1.0, 1)],
+                                  [("l2_hinge_topk_smooth", 0.5, 0.7, 8)],
+                                  [("l2_hinge_topk_smooth", 1.0, 1.0, 1)]])
+@pytest.mark.parametrize("result", ["float", "double"])
+def test_fused_matches_unfused(cuda, m, objs, result):
+    """The fused pass (scores and epilogue in one kernel, scores not stored)
+    against the two-kernel form: the scores are formed by the same MFMA
+    sequence, so every per-example loss, count-derived accuracy and record
+    must be bit-identical.  n is not a multiple of the 32-example workgroup,
+    d not of the 8-wide slab or of 4 (the scalar load path) in half the
+    cases, and some examples take the deferred top-k cone search (their
+    score rows are the only ones the fused kernel writes)."""
+    import torch
+    import libsdca_amd as sd
+    objs = [o for o in objs if o[3] <= m - 1]
+    if not objs:
+        pytest.skip("k > m - 1")
+    rng = np.random.default_rng(m + len(objs))
+    n = 1000 + m % 7
+    if m <= 1024 and m % 2 == 0:
+        X, W, y = dominant_class_inputs(rng, n, m)
+    else:
+        d = 37 if m % 3 else 64
+        X = rng.standard_normal((n, d)).astype(np.float32)
+        X /= np.linalg.norm(X, axis=1, keepdims=True)
+        W = (rng.standard_normal((m, d)) * 0.5).astype(np.float32)
+        y = rng.integers(0, m, n)
+    tX, tW = torch.from_numpy(X).to(cuda), torch.from_numpy(W).to(cuda)
+    for test in (False, True):
+        r_f, a_f, p_f = sd.eval_features(objs, tX, tW, y, result=result, per_example=True, test=test,
+                                         fused=True)
+        r_u, a_u, p_u = sd.eval_features(objs, tX, tW, y, result=result, per_example=True, test=test)
+        torch.cuda.synchronize()
+        assert torch.equal(p_f, p_u), f"m={m} test={test}: per-example losses differ"
+        assert np.array_equal(a_f, a_u), f"m={m} test={test}: accuracy differs"
+        for a, b in zip(r_f, r_u):
+            assert a == b, f"m={m} test={test}: records differ"
