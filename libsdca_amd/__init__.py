@@ -44,8 +44,7 @@ __all__ = [
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-# SDCA_HIP_LIBRARY selects another build of the same library (tuning builds).
-LIB_PATH = os.environ.get("SDCA_HIP_LIBRARY", os.path.join(HERE, "libsdca_hip.so"))
+LIB_PATH = os.path.join(HERE, "libsdca_hip.so")
 
 F32, F64, LONG_DOUBLE = 0, 1, 2
 HOST_PTR = 1

@@ -9,10 +9,7 @@ namespace sdca_gpu {
 
 template <int FAM, int KM, class D, class R, int G, int C>
 hipError_t launch_one(const ProxLaunch& a) {
-#ifndef SDCA_PROX_BT
-#define SDCA_PROX_BT 64
-#endif
-  constexpr int BT = SDCA_PROX_BT;  // threads per workgroup (default: one wave)
+  constexpr int BT = 64;  // threads per workgroup: one wave
   constexpr int B = BT / G;
   ProxParamsT<R> pp;
   pp.lo = static_cast<R>(a.lo);
@@ -62,18 +59,9 @@ hipError_t launch_one(const ProxLaunch& a) {
 // m = 200 on eight).
 template <int FAM, int KM, class D, class R>
 hipError_t launch_by_m(const ProxLaunch& a) {
-#ifndef SDCA_M16_G
-#define SDCA_M16_G 1
-#endif
-  if (a.m <= 16) return launch_one<FAM, KM, D, R, SDCA_M16_G, 16 / SDCA_M16_G>(a);
+  if (a.m <= 16) return launch_one<FAM, KM, D, R, 1, 16>(a);
   if (a.m <= 64) return launch_one<FAM, KM, D, R, 4, 16>(a);
-#ifndef SDCA_M100_G
-#define SDCA_M100_G 4
-#endif
-#ifndef SDCA_M100_C
-#define SDCA_M100_C (100 / SDCA_M100_G)
-#endif
-  if (a.m <= 100) return launch_one<FAM, KM, D, R, SDCA_M100_G, SDCA_M100_C>(a);
+  if (a.m <= 100) return launch_one<FAM, KM, D, R, 4, 25>(a);
   if (a.m <= 128) return launch_one<FAM, KM, D, R, 4, 32>(a);
   if (a.m <= 200) return launch_one<FAM, KM, D, R, 8, 25>(a);
   if (a.m <= 256) return launch_one<FAM, KM, D, R, 16, 16>(a);

@@ -469,10 +469,7 @@ __device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R 
 // up to G * kCandSlots<G> candidates in registers; columns with more run the
 // variable fixing over all register slots instead.
 template <int G>
-#ifndef SDCA_CAND_G4
-#define SDCA_CAND_G4 4
-#endif
-constexpr int kCandSlots = (G <= 2) ? 8 : (G <= 4) ? SDCA_CAND_G4 : (G <= 16) ? 2 : 1;
+constexpr int kCandSlots = (G <= 2) ? 8 : (G <= 4) ? 4 : (G <= 16) ? 2 : 1;
 
 // Variable fixing for the top-k simplex's knapsack (lo = 0, hi = rhs / k):
 // its root t* satisfies sum_i clamp(a_i - t*, 0, hi) = k hi, hence
