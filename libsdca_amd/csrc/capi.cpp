@@ -409,9 +409,6 @@ int check_objectives(const sdca_objective* objs, int n_obj, int64_t m, bool mult
       if (ob.k < 1 || ob.k > m - 1)
         return fail(SDCA_ERR_ARG_RANGE, "k must be in [1, %lld] (got %lld)", (long long)(m - 1),
                     (long long)ob.k);
-      if (ob.k > sdca_gpu::kEvalMaxK)
-        return fail(SDCA_ERR_NOT_IMPLEMENTED, "top-k objectives support k <= %lld on the GPU",
-                    (long long)sdca_gpu::kEvalMaxK);
     }
   }
   return SDCA_OK;

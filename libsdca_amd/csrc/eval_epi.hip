@@ -193,6 +193,91 @@ __device__ inline bool smooth_topk_hinge(const D (&h)[C], int mp, int nvalid, in
   return true;
 }
 
+// The k + 1 largest of h for k above the register list (KM): k + 1 passes of
+// a group argmax, each removing one element (ties are taken one at a time,
+// as nth_element's order does).  sum_k: the k largest; sum_pos: the positive
+// ones among them; kth, next: the k-th and (k+1)-th; largest: the first.
+template <int G, int C, class D, class R>
+__device__ inline void topk_scan(const D (&h)[C], int k, R& sum_k, R& sum_pos, R& kth, R& next,
+                                 R& largest) {
+  bool rest[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) rest[c] = static_cast<R>(h[c]) > -num<R>::inf();
+  const int g = static_cast<int>(threadIdx.x) % G;
+  sum_k = sum_pos = 0;
+  kth = next = largest = -num<R>::inf();
+  for (int q = 0; q <= k; ++q) {
+    R mx;
+    int owner, slot;
+    masked_argmax<G, C, D, R>(h, rest, mx, owner, slot);
+    if (q == 0) largest = mx;
+    if (q < k) {
+      sum_k += mx;
+      sum_pos += mx > R(0) ? mx : R(0);
+      if (q == k - 1) kth = mx;
+    } else {
+      next = mx;
+    }
+    if (g == owner) {
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (c == slot) rest[c] = false;
+    }
+  }
+}
+
+// smooth_topk_hinge for k above the register list: the same special cases
+// (topk_cone.h:18-55) from topk_scan, the knapsack over every slot, the same
+// cone-search test and deferral.
+template <int G, int C, class D, class R>
+__device__ inline bool smooth_topk_hinge_bigk(const D (&h)[C], int mp, int nvalid, int k, R gamma,
+                                              R& loss) {
+  const R K = static_cast<R>(k);
+  const R eps16 = R(16) * num<R>::eps();
+  R sum_k, sum_pos, kth, next, largest;
+  topk_scan<G, C, D, R>(h, k, sum_k, sum_pos, kth, next, largest);
+  if (sum_k <= eps16) {
+    loss = 0;
+    return true;
+  }
+  const R hi_c = sum_k / K;
+  const R t_c = kth - hi_c;
+  const bool constant = (k == mp) || (t_c >= next - eps16);
+  const R eps = num<R>::eps() * dmax(R(1), fabs(gamma));
+  if (constant && !(K * hi_c > gamma + eps)) {
+    loss = hi_c * sum_k - R(0.5) * (hi_c * hi_c * K);
+    return true;
+  }
+  const R hi = gamma / K;
+  const R total = total_sum<G, C, D, R>(h, nvalid);
+  KnapState<R> st = knapsack_eq_regs<G, C, D, R>(h, mp, nvalid, total, R(0), hi, gamma);
+  if (!constant) {
+    bool lt;
+    if (st.n_u == 0) {
+      lt = st.t < -eps;
+    } else {
+      const R num_u = static_cast<R>(st.n_u);
+      lt = K * (st.sum_u + (K - num_u) * st.t) < gamma * num_u - eps;
+    }
+    if (lt) {
+      ColThr<R> cs = cone_search_u0<G, C, D, R>(h, K, largest);
+      if (cs.slow) return false;
+      R dot = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(h[c]);
+        dot += (x > eps16) ? x * x : R(0);
+      }
+      dot = group_sum<G>(dot);
+      loss = R(0.5) * dot;
+      return true;
+    }
+  }
+  const SetStats<R> ss = knap_sets<G, C, D, R>(h, st, -num<R>::inf());
+  loss = clamp_loss<G, C, D, R>(h, set_threshold(st.t, hi, gamma, ss), hi, gamma);
+  return true;
+}
+
 // Smooth top-k hinge beta (l2_topk_hinge.h:166-183): knapsack_le(h, 0, gamma/k, gamma).
 template <int G, int C, class D, class R>
 __device__ inline R smooth_topk_hinge_beta(const D (&h)[C], int mp, int k, R gamma) {
@@ -325,6 +410,13 @@ __device__ __forceinline__ bool eval_example_mc(const D* srow, const D* __restri
       case SDCA_OBJ_HINGE_TOPK:
       case SDCA_OBJ_TOPK_HINGE: {
         if constexpr ((MASK & ((1u << SDCA_OBJ_HINGE_TOPK) | (1u << SDCA_OBJ_TOPK_HINGE))) == 0) break;
+        dual = static_cast<R>(ay);
+        if (k > KM) {  // l2_hinge_topk.h:71-86, l2_topk_hinge.h:72-87 by passes
+          R sum_k, sum_pos, kth, next, largest;
+          topk_scan<G, C, D, R>(h, k, sum_k, sum_pos, kth, next, largest);
+          primal = (ob.kind == SDCA_OBJ_HINGE_TOPK) ? dmax(R(0), sum_k) : sum_pos;
+          break;
+        }
         constexpr int L = KM + 1;
         D top[L];
 #pragma unroll
@@ -344,8 +436,9 @@ __device__ __forceinline__ bool eval_example_mc(const D* srow, const D* __restri
       }
       case SDCA_OBJ_HINGE_TOPK_SMOOTH: {
         if constexpr ((MASK & (1u << SDCA_OBJ_HINGE_TOPK_SMOOTH)) == 0) break;
-        deferred = !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, nvalid, k, gamma, lds_col,
-                                                      lds_dummy, primal);
+        deferred = k > KM ? !smooth_topk_hinge_bigk<G, C, D, R>(h, m - 1, nvalid, k, gamma, primal)
+                          : !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, nvalid, k, gamma, lds_col,
+                                                               lds_dummy, primal);
         break;
       }
       case SDCA_OBJ_TOPK_HINGE_SMOOTH: {
@@ -855,6 +948,22 @@ __device__ R smooth_topk_sorted(const D* s, int mp, int k, R gamma) {
       ++mf;
     }
     if (!found) return R(0);  // default zero thresholds
+  }
+  if (!lt) {
+    // The knapsack's root: the threshold formed from the final free range
+    // and the loss summed entry by entry minus t (sum p - gamma), as the
+    // register epilogue does (set_threshold, clamp_loss).
+    if (l > f)
+      t = (sorted_sum<D, R>(s, f, l) + static_cast<R>(f) * hi - gamma) / static_cast<R>(l - f);
+    double hp = 0, pp = 0, sp = 0;
+    for (int q = 0; q < mp; ++q) {
+      const R x = static_cast<R>(s[q]);
+      const R p = clamp_ref(x - t, R(0), hi);
+      hp += static_cast<double>(x * p);
+      pp += static_cast<double>(p * p);
+      sp += static_cast<double>(p);
+    }
+    return static_cast<R>(hp) - R(0.5) * static_cast<R>(pp) - t * (static_cast<R>(sp) - gamma);
   }
   SetStats<R> st;
   st.sum_u = sorted_sum<D, R>(s, 0, f);
@@ -1372,18 +1481,7 @@ add_kernel(D* __restrict__ y, const D* __restrict__ x, int64_t count) {
     y[i] = x[i] + y[i];
 }
 
-__global__ void __launch_bounds__(256)
-gemm_f64_kernel(const double* __restrict__ X, const double* __restrict__ W, double* __restrict__ S,
-                int64_t n, int64_t m, int64_t d) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= n * m) return;
-  const int64_t i = idx / m, j = idx % m;
-  const double* x = X + i * d;
-  const double* w = W + j * d;
-  double acc = 0;
-  for (int64_t q = 0; q < d; ++q) acc += w[q] * x[q];
-  S[idx] = acc;
-}
+
 
 }  // namespace
 
@@ -1519,12 +1617,6 @@ hipError_t launch_dual_regularizer(int data, int result, const void* A, const vo
   return hipGetLastError();
 }
 
-hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, int64_t n,
-                                  int64_t m, int64_t d, hipStream_t stream) {
-  const int64_t total = n * m;
-  hipLaunchKernelGGL(gemm_f64_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
-                     stream, X, W, S, n, m, d);
-  return hipGetLastError();
-}
+
 
 }  // namespace sdca_gpu

@@ -184,7 +184,155 @@ hipError_t launch_tiles(const float* X, const float* W, float* S, int64_t n, int
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// fp64 scores on the matrix cores: v_mfma_f64_16x16x4f64 (78.6 TFLOP/s
+// dense on MI355X, the same as the fp64 vector peak; the MFMA form needs no
+// VALU issue).  A 256-thread workgroup computes a 64 x 64 tile of S as
+// 2 x 2 waves of 32 x 32, each 2 x 2 accumulators of 16 x 16 (4 doubles per
+// lane each).  K advances in slabs of 8: 16-byte loads (two doubles) into
+// registers while the previous slab is multiplied out of LDS stored as
+// [k][row] (+2 padding), where the operand of lane l (row l % 16, k l / 16)
+// is a conflict-free ds_read_b64.
+// ---------------------------------------------------------------------------
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+constexpr int BK64 = 8;
+
+template <int ROWS>
+__device__ inline void load_slab64(const double* __restrict__ src, int64_t rows, int64_t d,
+                                   int64_t r0, int64_t k0, bool vec, f64x2 (&r)[ROWS * 4 / 256]) {
+  constexpr int NV = ROWS * 4 / 256;  // (ROWS x 8 doubles) / 2 per load / 256 threads
+#pragma unroll
+  for (int h = 0; h < NV; ++h) {
+    const int f = static_cast<int>(threadIdx.x) + 256 * h;  // double2 index in the slab
+    const int row = f >> 2, q = f & 3;
+    const int64_t gr = r0 + row;
+    const int64_t gk = k0 + 2 * q;
+    f64x2 v = {0.0, 0.0};
+    if (gr < rows) {
+      const double* p = src + gr * d + gk;
+      if (vec && gk + 2 <= d) {
+        v = *reinterpret_cast<const f64x2*>(p);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          if (gk + e < d) v[e] = p[e];
+      }
+    }
+    r[h] = v;
+  }
+}
+
+template <int ROWS>
+__device__ inline void store_slab64(double* __restrict__ lds, int ld,
+                                    const f64x2 (&r)[ROWS * 4 / 256]) {
+  constexpr int NV = ROWS * 4 / 256;
+#pragma unroll
+  for (int h = 0; h < NV; ++h) {
+    const int f = static_cast<int>(threadIdx.x) + 256 * h;
+    const int row = f >> 2, q = f & 3;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) lds[(2 * q + e) * ld + row] = r[h][e];
+  }
+}
+
+__global__ void __launch_bounds__(256)
+scores_gemm_f64_kernel(const double* __restrict__ X, const double* __restrict__ W,
+                       double* __restrict__ S, int64_t n, int64_t m, int64_t d, int64_t tiles_m,
+                       int64_t tiles_n_padded, int vec) {
+  constexpr int BM = 64, BN = 64;
+  constexpr int LD = 64 + 2;
+  __shared__ __align__(16) double As[2][BK64 * LD];
+  __shared__ __align__(16) double Bs[2][BK64 * LD];
+  // XCD-aware order as in scores_gemm_kernel.
+  const int64_t w = blockIdx.x;
+  const int64_t xcd = w % 8, slot = w / 8;
+  const int64_t eb = (slot / tiles_m) * 8 + xcd;
+  const int64_t cb = slot % tiles_m;
+  if (eb >= tiles_n_padded) return;
+  const int64_t i0 = eb * BM, j0 = cb * BN;
+  if (i0 >= n) return;
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int lr = lane & 15, lk = lane >> 4;
+
+  f64x4 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[a][b][e] = 0.0;
+
+  const bool vv = vec != 0;
+  f64x2 ra[BM * 4 / 256], rb[BN * 4 / 256];
+  load_slab64<BM>(X, n, d, i0, 0, vv, ra);
+  load_slab64<BN>(W, m, d, j0, 0, vv, rb);
+  store_slab64<BM>(As[0], LD, ra);
+  store_slab64<BN>(Bs[0], LD, rb);
+  __syncthreads();
+  const int64_t nslabs = (d + BK64 - 1) / BK64;
+  for (int64_t s = 0; s < nslabs; ++s) {
+    const int cur = static_cast<int>(s & 1);
+    const bool more = s + 1 < nslabs;
+    if (more) {
+      load_slab64<BM>(X, n, d, i0, (s + 1) * BK64, vv, ra);
+      load_slab64<BN>(W, m, d, j0, (s + 1) * BK64, vv, rb);
+    }
+    const double* as = As[cur];
+    const double* bs = Bs[cur];
+#pragma unroll
+    for (int kk = 0; kk < BK64; kk += 4) {
+      const int kr = kk + lk;
+      double av[2], bv[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) av[a] = as[kr * LD + wr * 32 + 16 * a + lr];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) bv[b] = bs[kr * LD + wc * 32 + 16 * b + lr];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
+    }
+    if (more) {
+      store_slab64<BM>(As[cur ^ 1], LD, ra);
+      store_slab64<BN>(Bs[cur ^ 1], LD, rb);
+    }
+    __syncthreads();
+  }
+  // Accumulator e of lane l holds row l / 16 + 4 e and column l % 16 of its
+  // 16 x 16 block (operands: lane l carries A[l % 16][l / 16] and
+  // B[l / 16][l % 16]).
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int64_t col = j0 + wc * 32 + 16 * b + lr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t row = i0 + wr * 32 + 16 * a + lk + 4 * e;
+        if (row < n && col < m) S[row * m + col] = acc[a][b][e];
+      }
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, int64_t n,
+                                  int64_t m, int64_t d, hipStream_t stream) {
+  const int64_t tiles_m = (m + 63) / 64;
+  const int64_t tiles_n = (n + 63) / 64;
+  const int64_t tiles_n_padded = (tiles_n + 7) / 8 * 8;
+  const int64_t grid = tiles_n_padded * tiles_m;
+  const int vec = (d % 2 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(W) & 15) == 0) ? 1 : 0;
+  hipLaunchKernelGGL(scores_gemm_f64_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                     stream, X, W, S, n, m, d, tiles_m, tiles_n_padded, vec);
+  return hipGetLastError();
+}
 
 hipError_t launch_scores_gemm(const float* X, const float* W, float* S, int64_t n, int64_t m,
                               int64_t d, hipStream_t stream) {

@@ -10,7 +10,8 @@
 namespace sdca_gpu {
 
 constexpr int kMaxObjectives = 8;
-// Top-k objectives keep k <= kEvalMaxK in registers.
+// Top-k objectives keep a register list of the k + 1 largest for
+// k <= kEvalMaxK; larger k takes k + 1 passes of a group argmax.
 constexpr int64_t kEvalMaxK = 8;
 // Largest m the per-example kernels hold in registers.
 constexpr int64_t kEvalMaxM = 2048;
@@ -46,7 +47,7 @@ struct EvalLaunch {
 // S = X W^T for fp32 on the matrix cores; X: n x d, W: m x d, S: n x m (row-major).
 hipError_t launch_scores_gemm(const float* X, const float* W, float* S, int64_t n, int64_t m,
                               int64_t d, hipStream_t stream);
-// The same contraction in double (plain FMA kernel).
+// The same contraction in double on the matrix cores (v_mfma_f64_16x16x4f64).
 hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, int64_t n,
                                   int64_t m, int64_t d, hipStream_t stream);
 // The fused pass (scores on the matrix cores and the multiclass epilogue in

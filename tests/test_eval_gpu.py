@@ -472,3 +472,43 @@ def test_fused_matches_unfused(cuda, m, objs, result):
         assert np.array_equal(a_f, a_u), f"m={m} test={test}: accuracy differs"
         for a, b in zip(r_f, r_u):
             assert a == b, f"m={m} test={test}: records differ"
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float32, F64), (np.float64, F64)])
+@pytest.mark.parametrize("m", [12, 100, 300, 1000])
+@pytest.mark.parametrize("k", [9, 11, 40])
+def test_epilogue_large_k(cuda, oracle, dtype, result, m, k):
+    """Top-k objectives with k above the register list (8): the k + 1
+    largest by passes of a group argmax, the smooth top-k hinge's knapsack
+    over every slot (l2_hinge_topk.h:71-86, 162-179; l2_topk_hinge.h:72-87,
+    166-183; l2_entropy_topk.h:74-94), against the oracle per example, with
+    and without dual variables; untrained and spread scores."""
+    import torch
+    import libsdca_amd as sd
+    if k > m - 1:
+        pytest.skip("k > m - 1")
+    rng = np.random.default_rng(m * 7 + k)
+    n = 400
+    for spread in (0.01, 3.0):
+        S = (rng.standard_normal((n, m)) * spread).astype(dtype)
+        y = rng.integers(0, m, n)
+        S[: n // 10, 0] = S[np.arange(n // 10), y[: n // 10]]  # ties with the label
+        A = (rng.standard_normal((n, m)) * 0.01).astype(dtype)
+        objs = [("l2_hinge_topk", 1.0, 1.0, k), ("l2_hinge_topk_smooth", 1.0, 1.0, k),
+                ("l2_topk_hinge", 0.7, 1.0, k), ("l2_topk_hinge_smooth", 1.0, 0.5, k),
+                ("l2_entropy_topk", 1.0, 1.0, k)]
+        recs, acc, pe = sd.eval_scores(objs, torch.from_numpy(S).to(cuda), y,
+                                       A=torch.from_numpy(A).to(cuda), result=result,
+                                       per_example=True)
+        torch.cuda.synchronize()
+        pe = pe.cpu().numpy()
+        _, o_acc, o_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, result=result,
+                                            per_example=True)
+        _, _, x_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, result=LONG_DOUBLE,
+                                        per_example=True)
+        rtol = max(RTOL[result], RTOL[F32] if dtype == np.float32 else RTOL[F64])
+        compare_per_example(pe[:, :, 0], o_pe[:, :, 0], rtol, f"large k={k} m={m} primal",
+                            x_pe[:, :, 0])
+        compare_per_example(pe[:, :, 1], o_pe[:, :, 1], rtol, f"large k={k} m={m} dual",
+                            x_pe[:, :, 1])
+        assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n)
