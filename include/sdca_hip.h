@@ -103,7 +103,9 @@ void sdca_prox_params_default(sdca_prox_params* params);
  *   thresholds: optional, n records (2n for the two-block operator) with the
  *           computed thresholds, in double.
  * The reference's `aux` scratch has no counterpart: scratch lives in
- * registers and LDS.
+ * registers and LDS.  A column is held by one workgroup: m is at most 32768
+ * for fp32 data and 16384 for fp64 (128 KiB of column); larger m returns
+ * SDCA_ERR_NOT_IMPLEMENTED (the elementwise LAMBERT_W_EXP takes any size).
  */
 int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result,
               int64_t m, int64_t n, const void* in, void* out,
@@ -176,7 +178,9 @@ typedef struct sdca_eval_record {
  *           partial_sum and 1/n, eval/core.h:65-68), multiclass only;
  *   per_example: optional, n * n_obj * 2 doubles: (primal, dual) loss of
  *           each example and objective before the loss coefficient.
- * The objectives must all be multiclass or all multilabel.
+ * The objectives must all be multiclass or all multilabel.  m is at most
+ * 32768 for fp32 data and 16384 for fp64 (an example's scores are held by
+ * one workgroup); larger m returns SDCA_ERR_NOT_IMPLEMENTED.
  */
 int sdca_eval_features(const sdca_objective* objs, int n_obj,
                        sdca_dtype data, sdca_dtype result,

@@ -171,8 +171,6 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
   else sdca_prox_params_default(&p);
   if (static_cast<int>(op) < 0 || op > SDCA_PROX_TWO_ENTROPY)
     return fail(SDCA_ERR_PROX, "unknown prox operator %d", static_cast<int>(op));
-  const bool biased = op == SDCA_PROX_KNAPSACK_LE_BIASED || op == SDCA_PROX_TOPK_SIMPLEX_BIASED ||
-                      op == SDCA_PROX_TOPK_CONE_BIASED;
   int rc = check_dtypes(data, result, true);
   if (rc) return rc;
   if (m < 1) return fail(SDCA_ERR_ARG_RANGE, "m must be >= 1 (got %lld)", (long long)m);
@@ -221,16 +219,13 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
   const bool listed = topk || reg_biased || op == SDCA_PROX_TWO_SIMPLEX_SORT;
   // The Lambert-map operators solved one wave per column (prox_entbias.hip).
   const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED || op == SDCA_PROX_TWO_ENTROPY;
-  if (!reg_ok && !(topk || knap || biased || ent_biased) && op != SDCA_PROX_LAMBERT_W_EXP &&
-      op != SDCA_PROX_TWO_SIMPLEX_SORT)
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "operator %d supports m <= %lld on the GPU (got %lld)",
-                static_cast<int>(op), (long long)kRegMaxM, (long long)m);
-  if ((topk || knap) && m > slow_max_m(data) && (!reg_ok || (topk && p.k > kTopkMaxK)))
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
-                (long long)m, (long long)slow_max_m(data));
-  if ((biased || ent_biased || op == SDCA_PROX_TWO_SIMPLEX_SORT) && m > slow_max_m(data))
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "m = %lld is above the supported %lld for this operator",
-                (long long)m, (long long)slow_max_m(data));
+  // Above kRegMaxM rows a column is held by one workgroup, in LDS (the
+  // sorted-column, wave-per-column and workgroup-per-column kernels).
+  if (op != SDCA_PROX_LAMBERT_W_EXP && m > max_rows(data))
+    return fail(SDCA_ERR_NOT_IMPLEMENTED,
+                "m = %lld is above the %lld rows (%lld KiB per column) the GPU kernels hold for "
+                "this element type", (long long)m, (long long)max_rows(data),
+                (long long)(kMaxColumnBytes / 1024));
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const size_t bytes = static_cast<size_t>(m) * static_cast<size_t>(n) * dtype_size(data);
@@ -705,9 +700,10 @@ static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, s
   if (rc) return rc;
   if (m < 2) return fail(SDCA_ERR_ARG_RANGE, "m must be >= 2 (got %lld)", (long long)m);
   if (n < 1) return fail(SDCA_ERR_ARG_RANGE, "n must be >= 1 (got %lld)", (long long)n);
-  if (m > kEvalMaxM)
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "the evaluation supports m <= %lld on the GPU",
-                (long long)kEvalMaxM);
+  if (m > max_rows(data))
+    return fail(SDCA_ERR_NOT_IMPLEMENTED,
+                "the evaluation supports m <= %lld for this element type on the GPU",
+                (long long)max_rows(data));
   if (n > INT32_MAX / 2) return fail(SDCA_ERR_ARG_RANGE, "n too large");
   const bool multilabel = offsets != nullptr;
   if ((rc = check_objectives(objs, n_obj, m, multilabel))) return rc;

@@ -256,9 +256,58 @@ __device__ inline double xor_lane(double v) {
 // ---------------------------------------------------------------------------
 // Reductions over a group of G adjacent lanes of a wave (G a power of two,
 // groups aligned to G).  Every lane of the group receives the result.
+//
+// G > 64: the group is the whole workgroup (blockDim.x == G, at most 16
+// waves).  Each wave reduces in registers, lane 0 of every wave puts its
+// result in LDS, and every thread combines the wave results in wave order,
+// so all threads hold the same bits and branch alike on them.  Every thread
+// of the workgroup must make the same sequence of these calls (they contain
+// barriers).
 // ---------------------------------------------------------------------------
+constexpr int kMaxGroupWaves = 16;
+
+// LDS words for the workgroup-wide reductions, one array per element type.
+template <class T>
+__device__ inline T* group_lds_words() {
+  __shared__ T words[kMaxGroupWaves];
+  return words;
+}
+
+// Make LDS writes of this wave visible to its own later reads.
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// Barrier between LDS writes and reads of a group: the wave's own ordering
+// for groups inside a wave, a workgroup barrier for a workgroup-wide group.
+template <int G>
+__device__ inline void group_lds_sync() {
+  if constexpr (G > 64) {
+    __syncthreads();
+  } else {
+    wave_lds_sync();
+  }
+}
+
+template <int G, class T, class Op>
+__device__ inline T workgroup_combine(T x, Op op) {
+  static_assert(G % 64 == 0 && G / 64 <= kMaxGroupWaves, "workgroup group of 2..16 waves");
+  T* words = group_lds_words<T>();
+  __syncthreads();  // the previous combine's readers are done with the words
+  if ((threadIdx.x & 63) == 0) words[threadIdx.x >> 6] = x;
+  __syncthreads();
+  T r = words[0];
+#pragma unroll
+  for (int w = 1; w < G / 64; ++w) r = op(r, words[w]);
+  return r;
+}
+
 template <int G, class T>
 __device__ inline T group_sum(T x) {
+  if constexpr (G > 64) {
+    return workgroup_combine<G>(group_sum<64>(x), [](T a, T b) { return a + b; });
+  }
   if constexpr (G >= 64) x += xor_lane<32>(x);
   if constexpr (G >= 32) x += xor_lane<16>(x);
   if constexpr (G >= 16) x += xor_lane<8>(x);
@@ -279,6 +328,9 @@ __device__ inline T min_step(T x) {
 }
 template <int G, class T>
 __device__ inline T group_max(T x) {
+  if constexpr (G > 64) {
+    return workgroup_combine<G>(group_max<64>(x), [](T a, T b) { return (b > a) ? b : a; });
+  }
   if constexpr (G >= 64) x = max_step<32>(x);
   if constexpr (G >= 32) x = max_step<16>(x);
   if constexpr (G >= 16) x = max_step<8>(x);
@@ -289,6 +341,9 @@ __device__ inline T group_max(T x) {
 }
 template <int G, class T>
 __device__ inline T group_min(T x) {
+  if constexpr (G > 64) {
+    return workgroup_combine<G>(group_min<64>(x), [](T a, T b) { return (b < a) ? b : a; });
+  }
   if constexpr (G >= 64) x = min_step<32>(x);
   if constexpr (G >= 32) x = min_step<16>(x);
   if constexpr (G >= 16) x = min_step<8>(x);
@@ -300,16 +355,30 @@ __device__ inline T group_min(T x) {
 // Exclusive prefix sum over the group (lane order g = 0..G-1).
 template <int G>
 __device__ inline int group_exclusive_scan(int x, int g) {
+  if constexpr (G > 64) {
+    // The wave's own scan plus the totals of the waves before it.
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int ex = group_exclusive_scan<64>(x, lane);
+    int* words = group_lds_words<int>();
+    __syncthreads();
+    if (lane == 63) words[wave] = ex + x;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += words[w];
+    return base + ex;
+  }
   int incl = x;
+  const int lane = static_cast<int>(threadIdx.x) & 63;
   if constexpr (G >= 2) { int y = xor_lane<1>(incl); if (g & 1) incl += y; }
   // After step s every lane holds the inclusive sum of its aligned block of
   // 2^(s+1) lanes restricted to lanes <= itself; the xor partner supplies the
   // lower half's total.
-  if constexpr (G >= 4) { int t = __shfl(incl, (threadIdx.x & ~3) | 1, 64); if (g & 2) incl += t; }
-  if constexpr (G >= 8) { int t = __shfl(incl, (threadIdx.x & ~7) | 3, 64); if (g & 4) incl += t; }
-  if constexpr (G >= 16) { int t = __shfl(incl, (threadIdx.x & ~15) | 7, 64); if (g & 8) incl += t; }
-  if constexpr (G >= 32) { int t = __shfl(incl, (threadIdx.x & ~31) | 15, 64); if (g & 16) incl += t; }
-  if constexpr (G >= 64) { int t = __shfl(incl, (threadIdx.x & ~63) | 31, 64); if (g & 32) incl += t; }
+  if constexpr (G >= 4) { int t = __shfl(incl, (lane & ~3) | 1, 64); if (g & 2) incl += t; }
+  if constexpr (G >= 8) { int t = __shfl(incl, (lane & ~7) | 3, 64); if (g & 4) incl += t; }
+  if constexpr (G >= 16) { int t = __shfl(incl, (lane & ~15) | 7, 64); if (g & 8) incl += t; }
+  if constexpr (G >= 32) { int t = __shfl(incl, (lane & ~31) | 15, 64); if (g & 16) incl += t; }
+  if constexpr (G >= 64) { int t = __shfl(incl, 31, 64); if (g & 32) incl += t; }
   return incl - x;
 }
 
@@ -420,6 +489,26 @@ __device__ inline void top_merge_step(D (&top)[L]) {
 }
 template <int G, int L, class D>
 __device__ inline void top_merge(D (&top)[L]) {
+  if constexpr (G > 64) {
+    // Each wave's list through LDS; every thread merges them in wave order.
+    static_assert(G % 64 == 0 && G / 64 <= kMaxGroupWaves, "workgroup group of 2..16 waves");
+    __shared__ D lists[kMaxGroupWaves][L];
+    top_merge<64, L, D>(top);
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) lists[wave][i] = top[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < L; ++i) top[i] = lists[0][i];
+    for (int w = 1; w < G / 64; ++w) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) top_insert(top, lists[w][i]);
+    }
+    return;
+  }
   if constexpr (G >= 64) top_merge_step<32>(top);
   if constexpr (G >= 32) top_merge_step<16>(top);
   if constexpr (G >= 16) top_merge_step<8>(top);

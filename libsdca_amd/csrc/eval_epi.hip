@@ -342,10 +342,12 @@ __device__ inline R lse_all(const D (&v)[C], int nvalid) {
 // when some objective of the example was deferred.
 // MASK: the objective kinds compiled in (bit sdca_objective_kind; the
 // others are skipped), HAS_A: whether dual variables may be given.  The fused
-// kernel instantiates the set it runs to keep its registers down.
+// kernel instantiates the set it runs to keep its registers down.  BIGK:
+// top-k objectives with k above the register list (KM) are compiled in (the
+// launch picks this variant only for them: the passes cost registers).
 constexpr unsigned kAllMulticlass = 0x3fu;
 template <int G, int C, int KM, class D, class R, unsigned MASK = kAllMulticlass,
-          bool HAS_A = true>
+          bool HAS_A = true, bool BIGK = false>
 __device__ __forceinline__ bool eval_example_mc(const D* srow, const D* __restrict__ A,
                                                 const int64_t* __restrict__ labels, int m,
                                                 int64_t i, int64_t ii, bool active, int g,
@@ -411,11 +413,13 @@ __device__ __forceinline__ bool eval_example_mc(const D* srow, const D* __restri
       case SDCA_OBJ_TOPK_HINGE: {
         if constexpr ((MASK & ((1u << SDCA_OBJ_HINGE_TOPK) | (1u << SDCA_OBJ_TOPK_HINGE))) == 0) break;
         dual = static_cast<R>(ay);
-        if (k > KM) {  // l2_hinge_topk.h:71-86, l2_topk_hinge.h:72-87 by passes
-          R sum_k, sum_pos, kth, next, largest;
-          topk_scan<G, C, D, R>(h, k, sum_k, sum_pos, kth, next, largest);
-          primal = (ob.kind == SDCA_OBJ_HINGE_TOPK) ? dmax(R(0), sum_k) : sum_pos;
-          break;
+        if constexpr (BIGK) {
+          if (k > KM) {  // l2_hinge_topk.h:71-86, l2_topk_hinge.h:72-87 by passes
+            R sum_k, sum_pos, kth, next, largest;
+            topk_scan<G, C, D, R>(h, k, sum_k, sum_pos, kth, next, largest);
+            primal = (ob.kind == SDCA_OBJ_HINGE_TOPK) ? dmax(R(0), sum_k) : sum_pos;
+            break;
+          }
         }
         constexpr int L = KM + 1;
         D top[L];
@@ -436,9 +440,14 @@ __device__ __forceinline__ bool eval_example_mc(const D* srow, const D* __restri
       }
       case SDCA_OBJ_HINGE_TOPK_SMOOTH: {
         if constexpr ((MASK & (1u << SDCA_OBJ_HINGE_TOPK_SMOOTH)) == 0) break;
-        deferred = k > KM ? !smooth_topk_hinge_bigk<G, C, D, R>(h, m - 1, nvalid, k, gamma, primal)
-                          : !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, nvalid, k, gamma, lds_col,
-                                                               lds_dummy, primal);
+        if constexpr (BIGK) {
+          if (k > KM) {
+            deferred = !smooth_topk_hinge_bigk<G, C, D, R>(h, m - 1, nvalid, k, gamma, primal);
+            break;
+          }
+        }
+        deferred = !smooth_topk_hinge<G, C, KM, D, R>(h, m - 1, nvalid, k, gamma, lds_col,
+                                                      lds_dummy, primal);
         break;
       }
       case SDCA_OBJ_TOPK_HINGE_SMOOTH: {
@@ -538,22 +547,25 @@ __device__ __forceinline__ bool eval_example_mc(const D* srow, const D* __restri
   return any_deferred;
 }
 
-template <int G, int C, int KM, class D, class R>
-__global__ void __launch_bounds__(64)
+// BT threads per workgroup: one wave of 64 / G examples, or (G = BT) one
+// example per workgroup for m above one wave's registers.
+template <int G, int C, int KM, class D, class R, int BT = 64, bool BIGK = false>
+__global__ void __launch_bounds__(BT)
 eval_multiclass_kernel(const D* __restrict__ S, const D* __restrict__ A,
                        const int64_t* __restrict__ labels, int64_t m64, int64_t n, EvalObjs objs,
                        double* __restrict__ per_example, int* __restrict__ counts,
                        int* __restrict__ slow, int* __restrict__ bad) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* lds = reinterpret_cast<D*>(smem_raw);
-  constexpr int B = 64 / G;
+  constexpr int B = BT / G;
   const int m = static_cast<int>(m64);
   const int lc = static_cast<int>(threadIdx.x) / G;
   const int g = static_cast<int>(threadIdx.x) % G;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * B + lc;
   const bool active = i < n;
   const int64_t ii = active ? i : 0;  // inactive groups compute on example 0, store nothing
-  eval_example_mc<G, C, KM, D, R>(S + ii * m64, A, labels, m, i, ii, active, g, objs,
+  eval_example_mc<G, C, KM, D, R, kAllMulticlass, true, BIGK>(S + ii * m64, A, labels, m, i, ii,
+                                                              active, g, objs,
                                   per_example, counts, slow, bad, lds + lc * m,
                                   lds + B * m + threadIdx.x);
 }
@@ -681,13 +693,13 @@ __device__ inline R smooth_two_simplex_loss(const D (&v)[C], unsigned in_a_bits,
   return loss;
 }
 
-template <int G, int C, class D, class R>
-__global__ void __launch_bounds__(64)
+template <int G, int C, class D, class R, int BT = 64>
+__global__ void __launch_bounds__(BT)
 eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
                        const int64_t* __restrict__ labels, const int64_t* __restrict__ offsets,
                        int64_t m64, int64_t n, EvalObjs objs, double* __restrict__ per_example,
                        double* __restrict__ rank, int* __restrict__ bad) {
-  constexpr int B = 64 / G;
+  constexpr int B = BT / G;
   const int m = static_cast<int>(m64);
   const int lc = static_cast<int>(threadIdx.x) / G;
   const int g = static_cast<int>(threadIdx.x) % G;
@@ -1246,30 +1258,54 @@ hipError_t launch_fused_typed(const float* X, const float* W, const EvalLaunch& 
   return launch_fused_nbw<8, R>(X, W, a, d, s_deferred);
 }
 
-template <class D, class R, int G, int C, int KM>
+template <class D, class R, int G, int C, int KM, int BT = 64, bool BIGK = false>
 hipError_t launch_mc(const EvalLaunch& a) {
-  constexpr int B = 64 / G;
+  constexpr int B = BT / G;
+  if (a.m > static_cast<int64_t>(G) * C) return hipErrorInvalidValue;
   const int64_t blocks = (a.n + B - 1) / B;
-  const size_t shmem = (static_cast<size_t>(B) * a.m + 64) * sizeof(D);
-  hipLaunchKernelGGL((eval_multiclass_kernel<G, C, KM, D, R>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(64), shmem, a.stream, static_cast<const D*>(a.S),
-                     static_cast<const D*>(a.A), a.labels, a.m, a.n, a.objs, a.per_example,
-                     a.counts, a.slow, a.bad);
+  // B rows of scratch and BT dummy words.
+  const size_t shmem = (static_cast<size_t>(B) * a.m + BT) * sizeof(D);
+  hipLaunchKernelGGL((eval_multiclass_kernel<G, C, KM, D, R, BT, BIGK>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
+                     static_cast<const D*>(a.S), static_cast<const D*>(a.A), a.labels, a.m, a.n,
+                     a.objs, a.per_example, a.counts, a.slow, a.bad);
   return hipGetLastError();
 }
 
-template <class D, class R, int G, int C>
+template <class D, class R, int G, int C, int BT = 64>
 hipError_t launch_ml(const EvalLaunch& a) {
-  constexpr int B = 64 / G;
+  constexpr int B = BT / G;
+  if (a.m > static_cast<int64_t>(G) * C) return hipErrorInvalidValue;
   const int64_t blocks = (a.n + B - 1) / B;
-  hipLaunchKernelGGL((eval_multilabel_kernel<G, C, D, R>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(64), 0, a.stream, static_cast<const D*>(a.S), static_cast<const D*>(a.A),
+  hipLaunchKernelGGL((eval_multilabel_kernel<G, C, D, R, BT>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(BT), 0, a.stream, static_cast<const D*>(a.S), static_cast<const D*>(a.A),
                      a.labels, a.offsets, a.m, a.n, a.objs, a.per_example, a.rank, a.bad);
   return hipGetLastError();
 }
 
+// Rows above kRegMaxM: one example per workgroup (kWideThreads threads, the
+// largest fp32 rows kMaxWideThreads), C slots per thread; every top-k
+// variant compiled in.
+template <class D, class R>
+hipError_t launch_wide(const EvalLaunch& a) {
+  constexpr int G = kWideThreads, G2 = kMaxWideThreads;
+  if (a.offsets) {
+    if (a.m <= 8 * G) return launch_ml<D, R, G, 8, G>(a);
+    if (a.m <= 16 * G) return launch_ml<D, R, G, 16, G>(a);
+    if (a.m <= 32 * G) return launch_ml<D, R, G, 32, G>(a);
+    if constexpr (sizeof(D) == 4) return launch_ml<D, R, G2, 32, G2>(a);
+    return hipErrorInvalidValue;
+  }
+  if (a.m <= 8 * G) return launch_mc<D, R, G, 8, 8, G, true>(a);
+  if (a.m <= 16 * G) return launch_mc<D, R, G, 16, 8, G, true>(a);
+  if (a.m <= 32 * G) return launch_mc<D, R, G, 32, 8, G, true>(a);
+  if constexpr (sizeof(D) == 4) return launch_mc<D, R, G2, 32, 8, G2, true>(a);
+  return hipErrorInvalidValue;
+}
+
 template <class D, class R>
 hipError_t launch_typed(const EvalLaunch& a) {
+  if (a.m > kRegMaxM) return launch_wide<D, R>(a);
   if (a.offsets) {
     if (a.m <= 64) return launch_ml<D, R, 4, 16>(a);
     if (a.m <= 256) return launch_ml<D, R, 16, 16>(a);
@@ -1278,6 +1314,12 @@ hipError_t launch_typed(const EvalLaunch& a) {
   }
   int kmax = 1;
   for (int o = 0; o < a.objs.n; ++o) kmax = a.objs.o[o].k > kmax ? a.objs.o[o].k : kmax;
+  if (kmax > kEvalMaxK) {
+    if (a.m <= 64) return launch_mc<D, R, 4, 16, 8, 64, true>(a);
+    if (a.m <= 256) return launch_mc<D, R, 16, 16, 8, 64, true>(a);
+    if (a.m <= 1024) return launch_mc<D, R, 64, 16, 8, 64, true>(a);
+    return launch_mc<D, R, 64, 32, 8, 64, true>(a);
+  }
   if (kmax <= 5) {
     if (a.m <= 64) return launch_mc<D, R, 4, 16, 5>(a);
     if (a.m <= 256) return launch_mc<D, R, 16, 16, 5>(a);
@@ -1507,7 +1549,10 @@ bool eval_fused_supported(const EvalLaunch& a, int64_t d) {
   // The general objective set needs more registers than two workgroups per
   // CU allow (it spills); it keeps the two-kernel form.
   unsigned kinds = 0;
-  for (int o = 0; o < a.objs.n; ++o) kinds |= 1u << a.objs.o[o].kind;
+  for (int o = 0; o < a.objs.n; ++o) {
+    kinds |= 1u << a.objs.o[o].kind;
+    if (a.objs.o[o].k > kEvalMaxK) return false;  // the register top list only
+  }
   return !a.A && (kinds & ~kSmoothEntropy) == 0;
 }
 

@@ -13,8 +13,6 @@ constexpr int kMaxObjectives = 8;
 // Top-k objectives keep a register list of the k + 1 largest for
 // k <= kEvalMaxK; larger k takes k + 1 passes of a group argmax.
 constexpr int64_t kEvalMaxK = 8;
-// Largest m the per-example kernels hold in registers.
-constexpr int64_t kEvalMaxM = 2048;
 
 // One objective as the kernels see it.
 struct EvalObj {

@@ -7,9 +7,10 @@
 
 namespace sdca_gpu {
 
-template <int FAM, int KM, class D, class R, int G, int C>
+template <int FAM, int KM, class D, class R, int G, int C, int BT = 64>
 hipError_t launch_one(const ProxLaunch& a) {
-  constexpr int BT = 64;  // threads per workgroup: one wave
+  // BT threads per workgroup: one wave, or (G = BT) one column per
+  // workgroup.
   constexpr int B = BT / G;
   ProxParamsT<R> pp;
   pp.lo = static_cast<R>(a.lo);
@@ -39,19 +40,36 @@ hipError_t launch_one(const ProxLaunch& a) {
   const size_t shmem =
       (static_cast<size_t>(B) * static_cast<size_t>(a.m) + slack + dummies) * sizeof(D);
   // m == G * C (the configuration's exact size) gets the variant without
-  // per-slot validity tests.
-  if (full) {
-    hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, true>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
-                       static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
-                       a.col_p, a.thr, a.slow);
-  } else {
-    hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, false>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
-                       static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
-                       a.col_p, a.thr, a.slow);
+  // per-slot validity tests (for one-wave workgroups: the wide
+  // configurations are for rare sizes and keep one variant).
+  if constexpr (BT == 64) {
+    if (full) {
+      hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, true>),
+                         dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
+                         static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
+                         a.col_p, a.thr, a.slow);
+      return hipGetLastError();
+    }
   }
+  hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, false>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
+                     static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
+                     a.col_p, a.thr, a.slow);
   return hipGetLastError();
+}
+
+// Columns above kRegMaxM rows: one workgroup per column (kWideThreads
+// threads, kMaxWideThreads for the largest fp32 columns), C slots per
+// thread; the column (at most kMaxColumnBytes) is staged in LDS and the
+// group reductions combine the waves through LDS.
+template <int FAM, int KM, class D, class R>
+hipError_t launch_wide(const ProxLaunch& a) {
+  constexpr int G = kWideThreads, G2 = kMaxWideThreads;
+  if (a.m <= 8 * G) return launch_one<FAM, KM, D, R, G, 8, G>(a);
+  if (a.m <= 16 * G) return launch_one<FAM, KM, D, R, G, 16, G>(a);
+  if (a.m <= 32 * G) return launch_one<FAM, KM, D, R, G, 32, G>(a);
+  if constexpr (sizeof(D) == 4) return launch_one<FAM, KM, D, R, G2, 32, G2>(a);
+  return hipErrorInvalidValue;
 }
 
 // m -> (G lanes per column, C slots per lane): the fewest lanes whose C
@@ -59,6 +77,11 @@ hipError_t launch_one(const ProxLaunch& a) {
 // m = 200 on eight).
 template <int FAM, int KM, class D, class R>
 hipError_t launch_by_m(const ProxLaunch& a) {
+  // The knapsack and top-k families take the sorted-column kernel above
+  // kRegMaxM rows.
+  if constexpr (FAM == FAM_ENT || FAM == FAM_TOPKENT || FAM == FAM_TWO) {
+    if (a.m > kRegMaxM) return launch_wide<FAM, KM, D, R>(a);
+  }
   if (a.m <= 16) return launch_one<FAM, KM, D, R, 1, 16>(a);
   if (a.m <= 64) return launch_one<FAM, KM, D, R, 4, 16>(a);
   if (a.m <= 100) return launch_one<FAM, KM, D, R, 4, 25>(a);

@@ -294,13 +294,6 @@ __device__ inline R knapsack_biased_regs(const D (&v)[C], int m, R total, R lo, 
   return t;
 }
 
-// Make LDS writes of this wave visible to its own later reads.
-__device__ inline void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // ---------------------------------------------------------------------------
 // Knapsack family: knapsack_eq (knapsack_eq.h:25-109) and knapsack_le
 // (knapsack_le.h:17-44).
@@ -502,6 +495,8 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
     if (total <= G * CC) {
       // Branch-free compaction: every slot is stored, non-candidates to the
       // lane's own dummy word (distinct per lane, so no bank serialisation).
+      // (For a workgroup-wide group the scan's barriers also order these
+      // stores after the other waves' reads of an earlier compaction.)
       int pos = group_exclusive_scan<G>(cn, g);
 #pragma unroll
       for (int c = 0; c < C; ++c) {
@@ -510,7 +505,7 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
         *dst = v[c];
         pos += pr ? 1 : 0;
       }
-      wave_lds_sync();
+      group_lds_sync<G>();
       // Candidate i sits at lds_col[i]; lane g takes i = g, g + G, ...  The
       // reads stay inside the tile: G * CC <= 16 <= m for G = 4 and 2, and
       // G * CC <= G <= m for larger G.

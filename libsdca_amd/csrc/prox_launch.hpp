@@ -25,8 +25,23 @@ enum {
   OP_TWO_SIMPLEX_SORT = SDCA_PROX_TWO_SIMPLEX_SORT
 };
 
-// Largest m handled by the register kernels.
+// Largest m handled by the one-wave register kernels.
 constexpr int64_t kRegMaxM = 2048;
+// Threads of the workgroup that holds one column above kRegMaxM rows, with
+// up to 32 slots per thread (up to 16384 rows; 256 registers per thread at
+// two waves per SIMD), and for the fp32 columns beyond that.
+constexpr int kWideThreads = 512;
+constexpr int kMaxWideThreads = 1024;
+// Largest column (m times the element size) any kernel holds in LDS: the
+// sorted-column, wave-per-column and workgroup-per-column kernels stage
+// whole columns (160 KiB of LDS per workgroup on gfx950, less the dummy
+// words and reduction scratch).
+constexpr int64_t kMaxColumnBytes = 128 * 1024;
+// Largest m of the prox operators (and of the evaluation) for an element
+// type: 32768 rows in fp32, 16384 in fp64.
+inline int64_t max_rows(int data) {
+  return kMaxColumnBytes / (data == SDCA_F32 ? 4 : 8);
+}
 // Top-k operators keep k <= kTopkMaxK in registers; larger k takes the
 // workgroup-per-column kernel.
 constexpr int64_t kTopkMaxK = 8;
@@ -61,8 +76,6 @@ hipError_t launch_topkent(const ProxLaunch& a);
 hipError_t launch_two(const ProxLaunch& a);
 // Workgroup-per-column kernel over the flagged list (all_columns: every column).
 hipError_t launch_slow(const ProxLaunch& a, bool all_columns);
-// Largest m the workgroup-per-column kernel accepts for this element type.
-int64_t slow_max_m(int data);
 // Elementwise lambert_w_exp over m*n elements.
 hipError_t launch_lambert(const ProxLaunch& a);
 // Zero the slow-column counter.

@@ -398,18 +398,26 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   return hipGetLastError();
 }
 
-// Descending bitonic sort of s[0, pow2) by the whole workgroup (callers pad
-// with -inf).
+// Descending sort of s[0, len) by the whole workgroup, without padding:
+// Batcher's bitonic network in the form whose merges all run one way (the
+// first stage of a merge of size `size` compares i with its mirror
+// i ^ (size - 1), the later stages i with i ^ stride), over the next power
+// of two.  Positions at or beyond len stand for -inf: such a position is
+// always the larger index of its comparators, where a descending comparator
+// leaves -inf in place, so those comparators are skipped and the array
+// holds only the len values.
 template <class D>
-__device__ void bitonic_desc(D* s, int pow2) {
+__device__ void sort_desc_unpadded(D* s, int len) {
+  int pow2 = 1;
+  while (pow2 < len) pow2 <<= 1;
   for (int size = 2; size <= pow2; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < pow2; i += blockDim.x) {
-        const int partner = i ^ stride;
-        if (partner > i) {
-          const bool desc = (i & size) == 0;
+      const int mask = (stride == (size >> 1)) ? size - 1 : stride;
+      for (int i = threadIdx.x; i < len; i += blockDim.x) {
+        const int partner = i ^ mask;
+        if (partner > i && partner < len) {
           const D a = s[i], b = s[partner];
-          if (desc ? (a < b) : (b < a)) {
+          if (a < b) {
             s[i] = b;
             s[partner] = a;
           }
@@ -463,18 +471,16 @@ __device__ void two_sort_thresholds(const D* a, int p, const D* b, int q, R rhs,
   theta_b = (sum_nu - best_c) / static_cast<R>(s);
 }
 
-// Two-block simplex by sort and scan: one workgroup per column, both blocks
-// sorted in LDS (each padded to pow2 with -inf), one lane scans, the
+// Two-block simplex by sort and scan: one workgroup per column, the column
+// in LDS (m words) with each block sorted in place, one lane scans, the
 // workgroup clamps the column.
 template <class D, class R>
 __global__ void __launch_bounds__(256)
 two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, R rhs,
                 int64_t p_all, const int64_t* __restrict__ col_p,
-                sdca_thresholds* __restrict__ thr, int* __restrict__ slow, int all_columns,
-                int pow2) {
+                sdca_thresholds* __restrict__ thr, int* __restrict__ slow, int all_columns) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* sa = reinterpret_cast<D*>(smem_raw);
-  D* sb = sa + pow2;
   __shared__ R sh_ta, sh_tb;
   const int m = static_cast<int>(m64);
   const int64_t count = all_columns ? n : static_cast<int64_t>(slow[0]);
@@ -483,13 +489,11 @@ two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int6
     const int p = clamp_split(col_p ? col_p[j] : p_all, m);
     const int q = m - p;
     const D* col = in + j * m64;
-    for (int i = threadIdx.x; i < pow2; i += blockDim.x) {
-      sa[i] = (i < p) ? col[i] : -num<D>::inf();
-      sb[i] = (i < q) ? col[p + i] : -num<D>::inf();
-    }
+    D* sb = sa + p;
+    for (int i = threadIdx.x; i < m; i += blockDim.x) sa[i] = col[i];
     __syncthreads();
-    bitonic_desc(sa, pow2);
-    bitonic_desc(sb, pow2);
+    sort_desc_unpadded(sa, p);
+    sort_desc_unpadded(sb, q);
     if (threadIdx.x == 0) {
       R ta, tb;
       two_sort_thresholds<D, R>(sa, p, sb, q, rhs, ta, tb);
@@ -525,8 +529,6 @@ two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int6
 
 template <class D, class R>
 hipError_t launch_two_sort_t(const ProxLaunch& a, bool all_columns) {
-  int half = 1;
-  while (half < a.m) half <<= 1;  // pow2 >= max(p, m - p) for every column
   // List mode: the list is a small fraction of the n columns and usually
   // empty; the grid grows with n (about one workgroup per 1024 columns,
   // 512 to 4096), so that a long list finds workgroups on every CU while
@@ -534,10 +536,9 @@ hipError_t launch_two_sort_t(const ProxLaunch& a, bool all_columns) {
   const int64_t cap = all_columns ? 4096 : std::min<int64_t>(4096, std::max<int64_t>(512, a.n / 1024));
   const int64_t grid = a.n < cap ? a.n : cap;
   hipLaunchKernelGGL((two_sort_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
-                     dim3(256), 2 * static_cast<size_t>(half) * sizeof(D), a.stream,
+                     dim3(256), static_cast<size_t>(a.m) * sizeof(D), a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n,
-                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, a.slow, all_columns ? 1 : 0,
-                     half);
+                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, a.slow, all_columns ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -555,11 +556,6 @@ __global__ void __launch_bounds__(256) lambert_kernel(const D* __restrict__ in, 
 }
 
 }  // namespace
-
-int64_t slow_max_m(int data) {
-  // Sorted column in at most 32 KiB of LDS.
-  return data == SDCA_F32 ? 8192 : 4096;
-}
 
 hipError_t launch_slow(const ProxLaunch& a, bool all_columns) {
   if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_slow_t<float, float>(a, all_columns);

@@ -512,3 +512,107 @@ def test_epilogue_large_k(cuda, oracle, dtype, result, m, k):
         compare_per_example(pe[:, :, 1], o_pe[:, :, 1], rtol, f"large k={k} m={m} dual",
                             x_pe[:, :, 1])
         assert np.allclose(acc, o_acc, rtol=0, atol=0.5 / n)
+
+
+# Largest m per element type: 128 KiB of scores per example.
+MAX_ROWS = {np.float32: 32768, np.float64: 16384}
+
+
+def wide_scores(rng, n, m, dtype):
+    """Scores with ties against the label, and a quarter of the examples with
+    one class far above the label and the rest far below it (the smooth top-k
+    hinge's cone search with U non-empty: the deferred-example kernel)."""
+    S = (rng.standard_normal((n, m)) * 2).astype(dtype)
+    y = rng.integers(0, m, n)
+    S[: n // 10, 0] = S[np.arange(n // 10), y[: n // 10]]
+    for i in range(n // 10, n // 10 + n // 4):
+        S[i, :] = -5.0
+        S[i, y[i]] = 5.0
+        S[i, (y[i] + 1 + int(rng.integers(0, m - 1))) % m] = 10.0
+    return S, y
+
+
+def check_wide_multiclass(cuda, oracle, dtype, result, m, n, with_a, seed):
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(seed)
+    S, y = wide_scores(rng, n, m, dtype)
+    A = None
+    if with_a:
+        A = -np.abs(rng.standard_normal((n, m)) * 0.01).astype(dtype)
+        A[np.arange(n), y] = np.abs(A[np.arange(n), y])
+    objs = MC_OBJS + [("l2_hinge_topk_smooth", 1.0, 1.0, 12), ("l2_topk_hinge", 1.0, 1.0, 20)]
+    recs, acc, pe = sd.eval_scores(objs, torch.from_numpy(S).to(cuda), y,
+                                   A=None if A is None else torch.from_numpy(A).to(cuda),
+                                   result=result, per_example=True)
+    torch.cuda.synchronize()
+    pe = pe.cpu().numpy()
+    _, o_acc, o_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, result=result,
+                                        per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(objs), S, A, y, result=LONG_DOUBLE,
+                                    per_example=True)
+    rtol = max(RTOL[result], RTOL[F32] if dtype == np.float32 else RTOL[F64])
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], rtol, f"wide primal m={m}", x_pe[:, :, 0])
+    compare_per_example(pe[:, :, 1], o_pe[:, :, 1], rtol, f"wide dual m={m}", x_pe[:, :, 1])
+    assert np.array_equal(np.rint(acc * n), np.rint(o_acc * n)), \
+        f"m={m}: top-k counts differ: {acc[:5]} vs {o_acc[:5]}"
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float32, F64), (np.float64, F64)])
+@pytest.mark.parametrize("m", [3000, 5000])
+@pytest.mark.parametrize("with_a", [False, True])
+def test_epilogue_wide_multiclass(cuda, oracle, dtype, result, m, with_a):
+    """m above one wave's registers: one example per workgroup (group sums
+    through LDS), every multiclass objective incl. k above the register list,
+    deferred examples at these sizes (eval.h:36-47, l2_hinge_topk.h:71-86,
+    162-179, l2_topk_hinge.h:72-87, 166-183, l2_entropy.h:77-91,
+    l2_entropy_topk.h:74-94)."""
+    check_wide_multiclass(cuda, oracle, dtype, result, m, 120, with_a, m + 17)
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float64, F64)])
+def test_epilogue_widest_multiclass(cuda, oracle, dtype, result):
+    """The largest rows (32768 fp32, 16384 fp64) and a configuration step."""
+    for m in (MAX_ROWS[dtype], 8192, 8193):
+        check_wide_multiclass(cuda, oracle, dtype, result, m, 16, True, m + 19)
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float64, F64)])
+@pytest.mark.parametrize("m", [3000, 5000, "max"])
+def test_epilogue_wide_multilabel(cuda, oracle, dtype, result, m):
+    import torch
+    import libsdca_amd as sd
+    m = MAX_ROWS[dtype] if m == "max" else m
+    rng = np.random.default_rng(m + 23)
+    n = 60
+    S = (rng.standard_normal((n, m)) * 2).astype(dtype)
+    lab, off = multilabel_labels(rng, n, m, pmax=40)
+    A = (rng.standard_normal((n, m)) * 0.01).astype(dtype)
+    recs, _, pe = sd.eval_scores(ML_OBJS, torch.from_numpy(S).to(cuda), lab,
+                                 A=torch.from_numpy(A).to(cuda), offsets=off, result=result,
+                                 per_example=True)
+    torch.cuda.synchronize()
+    pe = pe.cpu().numpy()
+    o_recs, _, o_pe = oracle.eval_scores(oracle_objs(ML_OBJS), S, A, lab, off, result=result,
+                                         per_example=True)
+    _, _, x_pe = oracle.eval_scores(oracle_objs(ML_OBJS), S, A, lab, off, result=LONG_DOUBLE,
+                                    per_example=True)
+    rtol = RTOL[result]
+    compare_per_example(pe[:, :, 0], o_pe[:, :, 0], rtol, f"wide multilabel primal m={m}",
+                        x_pe[:, :, 0])
+    compare_per_example(pe[:, :, 1], o_pe[:, :, 1], rtol, f"wide multilabel dual m={m}",
+                        x_pe[:, :, 1])
+    for r, o in zip(recs, o_recs):
+        assert abs(r["rank_loss"] - o["rank_loss"]) <= 1e-6 * max(1, abs(o["rank_loss"]))
+
+
+def test_eval_rows_limit(cuda):
+    """Rows above 128 KiB per example are refused with SDCA_ERR_NOT_IMPLEMENTED."""
+    import torch
+    import libsdca_amd as sd
+    for dt, npdt in ((torch.float32, np.float32), (torch.float64, np.float64)):
+        m = MAX_ROWS[npdt] + 1
+        S = torch.zeros((2, m), dtype=dt, device=cuda)
+        with pytest.raises(sd.SdcaError) as e:
+            sd.eval_scores([("l2_entropy", 1.0, 1.0, 1)], S, np.zeros(2, np.int64))
+        assert e.value.status == 4

@@ -413,17 +413,109 @@ def test_large_m_workgroup_per_column(cuda, oracle, op, kw, m, dtype, result):
         parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw, thr=thr)
 
 
+# Largest m per element type: 128 KiB of column in LDS.
+MAX_ROWS = {np.float32: 32768, np.float64: 16384}
+ALL_OPS = ["knapsack_eq", "knapsack_le", "topk_simplex", "topk_cone", "entropy", "entropy_norm",
+           "topk_entropy", "two_simplex", "knapsack_le_biased", "topk_simplex_biased",
+           "topk_cone_biased", "two_simplex_sort", "topk_entropy_biased", "two_entropy"]
+
+
 def test_large_m_limits(cuda):
-    """Sizes past the workgroup-per-column kernel's LDS, and the operators
-    without it, are refused with SDCA_ERR_NOT_IMPLEMENTED (4)."""
+    """Columns above 128 KiB (32768 fp32 rows, 16384 fp64 rows) are refused by
+    every operator with SDCA_ERR_NOT_IMPLEMENTED (4); the elementwise Lambert
+    map has no column."""
     import torch
     import libsdca_amd as sd
-    for op, m, dt in [("topk_simplex", 8193, torch.float32), ("knapsack_eq", 4097, torch.float64),
-                      ("entropy", 2049, torch.float64), ("two_simplex", 2049, torch.float32)]:
-        x = torch.zeros((3, m), dtype=dt, device=cuda)
-        with pytest.raises(sd.SdcaError) as e:
-            sd.prox(op, x, k=5, p=1)
-        assert e.value.status == 4, op
+    for dt, npdt in ((torch.float32, np.float32), (torch.float64, np.float64)):
+        m = MAX_ROWS[npdt] + 1
+        x = torch.zeros((2, m), dtype=dt, device=cuda)
+        for op in ALL_OPS:
+            with pytest.raises(sd.SdcaError) as e:
+                sd.prox(op, x, k=5, p=1)
+            assert e.value.status == 4, op
+        sd.prox("lambert_w_exp", x)
+
+
+# One wide case per operator family: (op, kwargs, inputs).  col_p: a
+# per-column split drawn in [1, m - 1].
+WIDE = [
+    ("entropy", dict(hi=1.0, rhs=1.0), "uniform"),
+    ("entropy", dict(hi=0.1, rhs=0.5), "normal"),
+    ("entropy_norm", dict(hi=1.0, rhs=1.0), "uniform"),
+    ("entropy_norm", dict(hi=0.2, rhs=0.9), "normal"),
+    ("topk_entropy", dict(k=3), "normal"),
+    ("topk_entropy", dict(k=12), "label+2"),
+    ("two_simplex", dict(rhs=1.0, p="third"), "normal"),
+    ("two_simplex", dict(rhs=2.0, col_p=True), "label+2"),
+    ("two_simplex_sort", dict(rhs=1.0, col_p=True), "normal"),
+    ("two_simplex_sort", dict(rhs=1.0, p="third"), "negative"),
+    ("two_entropy", dict(alpha=1.0, col_p=True), "normal"),
+    ("knapsack_eq", dict(lo=0.0, hi=1.0, rhs=1.0), "normal"),
+    ("knapsack_le", dict(lo=-0.5, hi=0.3, rhs=2.0), "label+2"),
+    ("topk_simplex", dict(k=5, rhs=1.0), "label+2"),
+    ("topk_cone", dict(k=3), "normal"),
+    ("knapsack_le_biased", dict(lo=0.0, hi=1.0, rhs=1.0, rho=1.0), "normal"),
+    ("topk_simplex_biased", dict(k=5, rhs=1.0, rho=0.5), "label+2"),
+    ("topk_cone_biased", dict(k=3, rho=0.25), "normal"),
+]
+
+
+def wide_input(kind, n, m, dtype, seed):
+    if kind == "uniform":
+        return inputs.uniform(n, m, dtype, seed, -10, 10)
+    if kind == "label+2":
+        return inputs.label_shifted(n, m, dtype, seed)
+    if kind == "negative":  # the two-simplex optimum x = y = 0
+        return (-np.abs(inputs.normal(n, m, dtype, seed)) - 0.1).astype(dtype)
+    return inputs.normal(n, m, dtype, seed, 2.0)
+
+
+def wide_case(cuda, oracle, op, kw, kind, m, dtype, result, n):
+    kw = dict(kw)
+    seed = 300 + m + len(op)
+    x = wide_input(kind, n, m, dtype, seed)
+    if kw.get("p") == "third":
+        kw["p"] = m // 3
+    if kw.pop("col_p", False):
+        kw["col_p"] = np.random.default_rng(seed).integers(1, m, n)
+    got, thr = run_gpu(op, x, result, cuda, **kw)
+    parity(oracle, op, x, got, result, f"{op} {kind} m={m}", nthreads=8, thr=thr, **kw)
+    return x
+
+
+@pytest.mark.parametrize("dtype,result", DTYPES)
+@pytest.mark.parametrize("m", [3000, 5000])
+@pytest.mark.parametrize("op,kw,kind", WIDE)
+def test_wide_columns(cuda, oracle, op, kw, kind, m, dtype, result):
+    """Columns above one wave's registers (m > 2048): the register families
+    with one workgroup per column (group sums through LDS), the sorted-column
+    and wave-per-column kernels, every (Data, Result) pair, against the
+    oracle (prox/entropy.h:19-53, topk_entropy.h:20-76, two_simplex.h:18-119,
+    knapsack_eq.h:25-109, topk_simplex.h:39-68, ...)."""
+    wide_case(cuda, oracle, op, kw, kind, m, dtype, result, 24)
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float64, F64),
+                                          (np.float32, F64)])
+@pytest.mark.parametrize("op,kw,kind", WIDE)
+def test_widest_columns(cuda, oracle, op, kw, kind, dtype, result):
+    """The largest columns (128 KiB: 32768 fp32 rows, 16384 fp64 rows), and
+    the sizes around a configuration step (8192 = 16 slots of 512 threads)."""
+    for m in (MAX_ROWS[dtype], 8192, 8193):
+        wide_case(cuda, oracle, op, kw, kind, m, dtype, result, 6)
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float64, F64)])
+def test_wide_topk_entropy_biased(cuda, oracle, dtype, result):
+    """The biased top-k entropy (wave per column) at 5000 rows and the
+    largest column."""
+    for m in (5000, MAX_ROWS[dtype]):
+        x = inputs.normal(8, m, dtype, 181, 2.0)
+        x[:4, :3] += 8.0
+        assert entbias_settled(oracle, x, 1.5, result).all()
+        got, thr = run_gpu("topk_entropy_biased", x, result, cuda, k=4, alpha=1.5)
+        parity(oracle, "topk_entropy_biased", x, got, result, f"topk_entropy_biased m={m}",
+               nthreads=8, k=4, alpha=1.5, thr=thr)
 
 
 @pytest.mark.parametrize("dtype,result", DTYPES)
@@ -527,7 +619,7 @@ def test_topk_entropy_biased(cuda, oracle, k, alpha, m, dtype, result):
 
 
 @pytest.mark.parametrize("dtype,result,m", [(np.float32, F32, 8192), (np.float64, F64, 4096)])
-def test_topk_entropy_biased_largest_m(cuda, oracle, dtype, result, m):
+def test_topk_entropy_biased_large_m(cuda, oracle, dtype, result, m):
     x = inputs.normal(16, m, dtype, 180, 2.0)
     x[:8, :3] += 8.0
     assert entbias_settled(oracle, x, 1.5, result).all()
