@@ -58,6 +58,10 @@ size_t dtype_size(int dt) { return dt == SDCA_F32 ? 4 : 8; }
 struct Workspace {
   void* ptr[4] = {nullptr, nullptr, nullptr, nullptr};
   size_t cap[4] = {0, 0, 0, 0};
+  // Pinned host block for the evaluation's results: copies into it are
+  // asynchronous, so the call waits once for all of them.
+  void* host = nullptr;
+  size_t host_cap = 0;
   // The deferred-column list's two counters are zero (the deferred-column
   // kernel of the last call on this stream was launched and resets them).
   bool list_zeroed = false;
@@ -93,6 +97,28 @@ int workspace(hipStream_t stream, int slot, size_t bytes, void** out, Workspace*
     w.cap[slot] = want;
   }
   *out = w.ptr[slot];
+  return SDCA_OK;
+}
+
+// The calling stream's pinned host block of at least `bytes` (grown like
+// the device slots).
+int host_block(hipStream_t stream, size_t bytes, void** out) {
+  int dev = 0;
+  SDCA_HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  Workspace& w = g_ws[std::make_tuple(dev, stream, std::this_thread::get_id())];
+  if (w.host_cap < bytes) {
+    if (w.host) {
+      SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      SDCA_HIP_TRY(hipHostFree(w.host), "hipHostFree");
+      w.host = nullptr;
+      w.host_cap = 0;
+    }
+    const size_t want = bytes + bytes / 4 + 256;
+    SDCA_HIP_TRY(hipHostMalloc(&w.host, want, hipHostMallocDefault), "hipHostMalloc");
+    w.host_cap = want;
+  }
+  *out = w.host;
   return SDCA_OK;
 }
 
@@ -526,20 +552,27 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
     SDCA_HIP_TRY(launch_dual_regularizer(data, result, dA_reg, dS, m, n, d_dreg, d_dreg + n, stream),
                  "dual regularizer kernel");
 
-  std::vector<double> sums(2 * kMaxObjectives + 2, 0.0), reg(2, 0.0);
-  std::vector<unsigned long long> hist(static_cast<size_t>(m), 0ull);
-  SDCA_HIP_TRY(hipMemcpyAsync(sums.data(), d_sums, sums_bytes, hipMemcpyDeviceToHost, stream),
+  // The small results go to the stream's pinned block (asynchronous
+  // copies, one wait): [sums | reg (2) | dual_reg | bad label flag | hist].
+  void* hb = nullptr;
+  if ((rc = host_block(stream, sums_bytes + 4 * sizeof(double) + hist_bytes, &hb))) return rc;
+  double* h_sums = static_cast<double*>(hb);
+  double* h_reg = h_sums + (2 * kMaxObjectives + 2);
+  double* h_dual_reg = h_reg + 2;
+  int* h_bad = reinterpret_cast<int*>(h_dual_reg + 1);
+  unsigned long long* h_hist = reinterpret_cast<unsigned long long*>(h_dual_reg + 2);
+  h_reg[0] = h_reg[1] = 0;
+  *h_dual_reg = 0;
+  SDCA_HIP_TRY(hipMemcpyAsync(h_sums, d_sums, sums_bytes, hipMemcpyDeviceToHost, stream),
                "hipMemcpyAsync(D2H)");
   if (!multilabel && accuracy)
-    SDCA_HIP_TRY(hipMemcpyAsync(hist.data(), d_hist, hist_bytes, hipMemcpyDeviceToHost, stream),
+    SDCA_HIP_TRY(hipMemcpyAsync(h_hist, d_hist, hist_bytes, hipMemcpyDeviceToHost, stream),
                  "hipMemcpyAsync(D2H)");
-  if (dW) SDCA_HIP_TRY(hipMemcpyAsync(reg.data(), d_reg, 2 * sizeof(double), hipMemcpyDeviceToHost,
+  if (dW) SDCA_HIP_TRY(hipMemcpyAsync(h_reg, d_reg, 2 * sizeof(double), hipMemcpyDeviceToHost,
                                       stream), "hipMemcpyAsync(D2H)");
-  int bad_labels = 0;
-  SDCA_HIP_TRY(hipMemcpyAsync(&bad_labels, d_bad, sizeof(int), hipMemcpyDeviceToHost, stream),
+  SDCA_HIP_TRY(hipMemcpyAsync(h_bad, d_bad, sizeof(int), hipMemcpyDeviceToHost, stream),
                "hipMemcpyAsync(D2H)");
-  double dual_reg = 0;
-  if (dA_reg) SDCA_HIP_TRY(hipMemcpyAsync(&dual_reg, d_dreg + n, sizeof(double),
+  if (dA_reg) SDCA_HIP_TRY(hipMemcpyAsync(h_dual_reg, d_dreg + n, sizeof(double),
                                           hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
   if (per_example) {
     SDCA_HIP_TRY(hipMemcpyAsync(per_example, d_pe, pe_bytes,
@@ -547,6 +580,12 @@ int eval_on_device(const sdca_objective* objs, int n_obj, int data, int result, 
                                 stream), "hipMemcpyAsync(per_example)");
   }
   SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  const std::vector<double> sums(h_sums, h_sums + 2 * kMaxObjectives + 2);
+  const std::vector<double> reg(h_reg, h_reg + 2);
+  std::vector<unsigned long long> hist(static_cast<size_t>(m), 0ull);
+  if (!multilabel && accuracy) hist.assign(h_hist, h_hist + m);
+  const int bad_labels = *h_bad;
+  const double dual_reg = *h_dual_reg;
   if (bad_labels)
     return fail(SDCA_ERR_LABELS,
                 multilabel ? "invalid labels or offsets: the first offset must be 0, and every "
