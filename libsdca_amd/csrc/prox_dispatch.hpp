@@ -37,8 +37,12 @@ hipError_t launch_one(const ProxLaunch& a) {
   // need no dummy words: at m = 1000 in fp64 that keeps a wave's LDS at
   // 8 KB, 5 waves per SIMD (the register limit) instead of 4.5.
   const size_t dummies = (FAM == FAM_ENT || FAM == FAM_TOPKENT) ? 0 : BT;
-  const size_t shmem =
+  size_t shmem =
       (static_cast<size_t>(B) * static_cast<size_t>(a.m) + slack + dummies) * sizeof(D);
+  // The Lambert map keeps its last W values in an LDS array of R.
+  if constexpr (FAM == FAM_ENT && KM == 1 && sizeof(R) >= sizeof(D) && BT == 64)
+    shmem = w_lds_offset<D, R>(B, a.m, slack) +
+            (static_cast<size_t>(B) * static_cast<size_t>(a.m) + slack) * sizeof(R);
   // m == G * C (the configuration's exact size) gets the variant without
   // per-slot validity tests (for one-wave workgroups: the wide
   // configurations are for rare sizes and keep one variant).

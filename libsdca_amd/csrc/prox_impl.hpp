@@ -699,36 +699,56 @@ __device__ inline R lds_lse_sum_excl(const D* x, unsigned bits, R mx) {
 }
 
 // solve_sum_w_exp (entropy_norm.h:110-134) over the free slots (count of
-// them in the column).
+// them in the column).  With wl (the lane's slots of an LDS array of R), the
+// last Householder pass leaves W(exp(x - tc)) of every free slot there and
+// tc in *tw: the output map is then a short Taylor step from them.
 template <int G, int C, class D, class R>
-__device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int count, R rhs) {
-  R s = 0;
+__device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int count, R rhs,
+                                                 R* wl = nullptr, R* tw = nullptr) {
+  // Start.  W(e^y) <= e^y, so the root lies at or below
+  // t_lse = log sum exp(x) - log(rhs), and within about e^(max - t_lse) of it
+  // when every free value sits well below t_lse (small W, W(e^y) ~ e^y).
+  // There the iteration starts from t_lse: one single-precision step settles
+  // it on U(-10, 10) columns, against three from the reference's heuristic
+  // start (below), which the other columns keep.  The root, and the
+  // stopping rule that ends on it, are the same.
+  const R mx = lds_masked_max<G, C, D, R>(x, bits);
+  float se = 0.0f;
 #pragma unroll 4
-  for (int c = 0; c < C; ++c) s += ((bits >> c) & 1u) ? static_cast<R>(x[G * c]) : R(0);
-  s = group_sum<G>(s);
-  R t = (s - rhs) / static_cast<R>(count);
-  // Heuristic refinement: U = {a > t} shrinks while it stays non-trivial.
-  R u_cut = -num<R>::inf();
-  int u_count = count;
-  for (int it = 0; it < count + 1; ++it) {
-    R su = 0;
-    int cu = 0;
+  for (int c = 0; c < C; ++c)
+    se += ((bits >> c) & 1u) ? expf(static_cast<float>(static_cast<R>(x[G * c]) - mx)) : 0.0f;
+  se = group_sum<G>(se);
+  const R t_lse = mx + static_cast<R>(logf(se)) - dlog(rhs);
+  R t = t_lse;
+  if (!(mx - t_lse <= R(-1))) {
+    R s = 0;
 #pragma unroll 4
-    for (int c = 0; c < C; ++c) {
-      const R y = static_cast<R>(x[G * c]);
-      const bool in = ((bits >> c) & 1u) && y > u_cut && y > t;
-      su += in ? y : R(0);
-      cu += in ? 1 : 0;
+    for (int c = 0; c < C; ++c) s += ((bits >> c) & 1u) ? static_cast<R>(x[G * c]) : R(0);
+    s = group_sum<G>(s);
+    t = (s - rhs) / static_cast<R>(count);
+    // Heuristic refinement: U = {a > t} shrinks while it stays non-trivial.
+    R u_cut = -num<R>::inf();
+    int u_count = count;
+    for (int it = 0; it < count + 1; ++it) {
+      R su = 0;
+      int cu = 0;
+#pragma unroll 4
+      for (int c = 0; c < C; ++c) {
+        const R y = static_cast<R>(x[G * c]);
+        const bool in = ((bits >> c) & 1u) && y > u_cut && y > t;
+        su += in ? y : R(0);
+        cu += in ? 1 : 0;
+      }
+      su = group_sum<G>(su);
+      cu = group_sum<G>(cu);
+      if (cu == u_count || cu == 0) break;
+      u_cut = dmax(u_cut, t);
+      u_count = cu;
+      t = (su - rhs) / static_cast<R>(cu);
     }
-    su = group_sum<G>(su);
-    cu = group_sum<G>(cu);
-    if (cu == u_count || cu == 0) break;
-    u_cut = dmax(u_cut, t);
-    u_count = cu;
-    t = (su - rhs) / static_cast<R>(cu);
   }
   // Householder iterations of order 4 (entropy_norm.h:84-102).
-  const R ub = lds_masked_max<G, C, D, R>(x, bits) - num<R>::exp_min_arg();
+  const R ub = mx - num<R>::exp_min_arg();
   const R eps16 = R(16) * num<R>::eps();
   bool warm = false;
   if constexpr (sizeof(R) == 8) {
@@ -781,11 +801,13 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
     const R prev = t;
     const R tc = dmin(t, ub);
     const R mt = -tc;
+    if (tw) *tw = tc;
     R f0 = 0, f1 = 0, f2 = 0, f3 = 0;
 #pragma unroll 1
     for (int c = 0; c < C; ++c) {
       if ((bits >> c) & 1u) {
         const R w = lambert_w_exp(static_cast<R>(x[G * c]) + mt);
+        if (wl) wl[G * c] = w;
         // The derivative sums steer the step only (the root is f0 = rhs),
         // so they share one reciprocal of 1 + w.
         const R rd = div_near(R(1), R(1) + w);
@@ -822,10 +844,15 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
 // writes e_c * exp(mx0 - t) instead of evaluating exp(x_c - t) again (the
 // same value to a few ulps; with t >= mx0 an underflowed e_c means an
 // underflowed result).
+// NORM with wl: the last solve's W values stay in wl (see
+// lds_solve_sum_w_exp); *wbits receives the slots whose value belongs to
+// the returned threshold (the free slots, 0 if the threshold came otherwise)
+// and *tw the point tc they were evaluated at.
 template <bool NORM, int G, int C, class D, class R>
 __device__ __forceinline__ ColThr<R> ent_family(const D* x, int m, int nvalid,
                                                 const ProxParamsT<R>& pp, R (&e)[C],
-                                                R& scale) {
+                                                R& scale, R* wl = nullptr, R* tw = nullptr,
+                                                unsigned* wbits = nullptr) {
   const R hi = pp.hi, rhs = pp.rhs;
   const R eps = R(16) * num<R>::eps() * dmax(R(1), rhs);
   const R u = NORM ? hi + dlog(hi) + eps : dlog(hi) + eps;
@@ -856,7 +883,8 @@ __device__ __forceinline__ ColThr<R> ent_family(const D* x, int m, int nvalid,
   // (entropy.h:30-49, entropy_norm.h:157-178).
   for (int iter = 0; iter <= m; ++iter) {
     if constexpr (NORM) {
-      t = lds_solve_sum_w_exp<G, C, D, R>(x, freeb, m - nfixed, r);
+      t = lds_solve_sum_w_exp<G, C, D, R>(x, freeb, m - nfixed, r, wl, tw);
+      if (wbits) *wbits = freeb;
     } else if (iter > 0) {
       const R mx = lds_masked_max<G, C, D, R>(x, freeb);
       t = mx + dlog1p(lds_lse_sum_excl<G, C, D, R>(x, freeb, mx)) - dlog(r);
@@ -871,6 +899,8 @@ __device__ __forceinline__ ColThr<R> ent_family(const D* x, int m, int nvalid,
     }
     cnt = group_sum<G>(cnt);
     if (cnt == 0) break;
+    // The solve's W values no longer belong to the final threshold.
+    if (wbits) *wbits = 0u;
     r -= hi * static_cast<R>(cnt);
     nfixed += cnt;
     if (nfixed == m) break;
@@ -1192,6 +1222,18 @@ __device__ inline void tile_store(D* __restrict__ dst, const D* __restrict__ src
   }
 }
 
+// The Lambert map's LDS array of W values: after the tile of B m + slack
+// words of D (8-byte aligned), the same shape in R.
+template <class D, class R>
+__device__ __host__ inline size_t w_lds_offset(int B, int64_t m, int64_t slack) {
+  return ((static_cast<size_t>(B) * static_cast<size_t>(m) + static_cast<size_t>(slack)) *
+              sizeof(D) + 7) & ~static_cast<size_t>(7);
+}
+template <class D, class R>
+__device__ inline R* w_lds(unsigned char* smem, int B, int m, int slack) {
+  return reinterpret_cast<R*>(smem + w_lds_offset<D, R>(B, m, slack));
+}
+
 // ---------------------------------------------------------------------------
 // The batched kernel.  Block = BT threads (one wave) = BT / G columns of G
 // lanes each.  FULL: m == G * C, so every slot of an active lane is valid.
@@ -1245,12 +1287,20 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   // exp(x - mx0) per slot and exp(mx0 - t) from the exp-map family.
   R ecache[C];
   R escale = 0;
+  // The Lambert map's last W values (an LDS array of R after the tile, for
+  // Result types at least as wide as the data: otherwise the map is
+  // evaluated in the data type) and the point they were taken at.  One-wave
+  // workgroups only: a workgroup-wide column has no LDS to spare.
+  constexpr bool kWReuse = FAM == FAM_ENT && KM == 1 && sizeof(R) >= sizeof(D) && BT == 64;
+  R* const wl = kWReuse ? w_lds<D, R>(smem_raw, B, m, FULL ? 0 : G * C - m) + lc * m + g : nullptr;
+  R tw = 0;
+  unsigned wbits = 0;
   if constexpr (FAM == FAM_KNAP) {
     th = knap_family<G, C, D, R>(v, m, nvalid, pp);
   } else if constexpr (FAM == FAM_TOPK) {
     th = topk_family<G, C, KM, D, R>(v, m, nvalid, pp, col, lds_dummy);
   } else if constexpr (FAM == FAM_ENT) {
-    th = ent_family<KM == 1, G, C, D, R>(mine, m, nvalid, pp, ecache, escale);
+    th = ent_family<KM == 1, G, C, D, R>(mine, m, nvalid, pp, ecache, escale, wl, &tw, &wbits);
   } else if constexpr (FAM == FAM_TOPKENT) {
     th = topkent_family<G, C, D, R>(v, m, nvalid, pp);
   } else {
@@ -1314,6 +1364,38 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
           }
         } else {
           write_rolled([&](D x) { return clamp_ref(dexp(x - t1), lo1, hi1); });
+        }
+      } else if constexpr (kWReuse) {
+        // W(exp(x - t)) = W(exp((x - tc) - dt)) from w = W(exp(x - tc)) by
+        // its Taylor series in dt = t - tc: the derivatives of W(e^y) are
+        // g1 = w / (1 + w), g2 = w / (1 + w)^3 and g3 = w (1 - 2w) / (1 + w)^5,
+        // and for |dt| <= 1e-4 (a settled iteration's last step is ~1e-6)
+        // the fourth-order term is below 1e-17 w.  Slots outside the last
+        // solve's free set (fixed at hi by an earlier pass), and columns whose
+        // last step was larger, evaluate the map.
+        if (!th.slow) {
+          const R dt = th.t - tw;
+          const unsigned tay = fabs(dt) <= R(1e-4) ? wbits : 0u;
+          const R hdt2 = R(0.5) * dt * dt;
+          const R sdt3 = hdt2 * dt * R(1.0 / 3.0);
+#pragma unroll 2
+          for (int c = 0; c < C; ++c) {
+            if (c < nvalid) {
+              D y;
+              if ((tay >> c) & 1u) {
+                const R w = wl[G * c];
+                const R rd = div_near(R(1), R(1) + w);
+                const R rd2 = rd * rd;
+                const R g1 = w * rd;
+                const R g2 = g1 * rd2;
+                const R g3 = g2 * (R(1) - R(2) * w) * rd2;
+                y = static_cast<D>(w - dt * g1 + hdt2 * g2 - sdt3 * g3);
+              } else {
+                y = lambert_w_exp(mine[G * c] - t1);
+              }
+              mine[G * c] = clamp_ref(y, lo1, hi1);
+            }
+          }
         }
       } else {
         write_rolled([&](D x) { return clamp_ref(lambert_w_exp(x - t1), lo1, hi1); });
