@@ -196,6 +196,22 @@ __device__ inline double lambert_w_exp(double x) {
   return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
 }
 
+// W(exp(y - dt)) from w = W(exp(y)) by the Taylor series in dt: the
+// derivatives of W(e^y) are g1 = w / (1 + w), g2 = w / (1 + w)^3 and
+// g3 = w (1 - 2w) / (1 + w)^5, so for |dt| <= 1e-4 the omitted fourth-order
+// term is below 1e-17 w.  Callers keep |dt| within that.
+template <class R>
+__device__ inline R lambert_w_exp_shift(R w, R dt) {
+  const R rd = div_near(R(1), R(1) + w);
+  const R rd2 = rd * rd;
+  const R g1 = w * rd;
+  const R g2 = g1 * rd2;
+  const R g3 = g2 * (R(1) - R(2) * w) * rd2;
+  const R hdt2 = R(0.5) * dt * dt;
+  return w - dt * g1 + hdt2 * g2 - (hdt2 * dt * R(1.0 / 3.0)) * g3;
+}
+constexpr double kLambertShiftMax = 1e-4;
+
 // The same function for inputs spread over all the intervals (the elementwise
 // map over arbitrary x): the branches (0, 4], (4, 2^59] and (-20, 0] each
 // start with one step lw_step5(w0, y0) from their own (w0, y0) = (x, 1),

@@ -31,6 +31,8 @@ constexpr int kEbMaxWaves = 4;
 
 // f0 = sum_i W(e^(s_i + t_i)) with t_i = ta for i < p and tb beyond
 // (sum_lambert_w_exp, lambert.h:220-237).
+// wout (optional, the wave's LDS array of R): each pass leaves its W values
+// there, for the output map.
 template <class D, class R>
 __device__ inline R lw_sum0(const D* s, int m, int p, int lane, R ta, R tb) {
   R a0(0);
@@ -40,10 +42,12 @@ __device__ inline R lw_sum0(const D* s, int m, int p, int lane, R ta, R tb) {
 
 // f0 = sum_i W(e^(s_i + t)), f1 = sum_i W / (1 + W) (lambert.h:253-271).
 template <class D, class R>
-__device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1) {
+__device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1,
+                                R* wout = nullptr) {
   R a0(0), a1(0);
   for (int i = lane; i < m; i += 64) {
     const R v = lambert_w_exp(static_cast<R>(s[i]) + t);
+    if (wout) wout[i] = v;
     a0 += v;
     a1 += div_near(v, R(1) + v);
   }
@@ -55,7 +59,7 @@ __device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1) 
 // the shift ta for entries below p and tb beyond.
 template <class D, class R>
 __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, R& f2, R& f3,
-                                int p = -1, R tb = R(0)) {
+                                int p = -1, R tb = R(0), R* wout = nullptr) {
   if (p < 0) {
     p = m;
     tb = t;
@@ -63,6 +67,7 @@ __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, 
   R a0(0), a1(0), a2(0), a3(0);
   for (int i = lane; i < m; i += 64) {
     const R v = lambert_w_exp(static_cast<R>(s[i]) + (i < p ? t : tb));
+    if (wout) wout[i] = v;
     const R d = R(1) + v;
     const R d3 = d * d * d;
     a0 += v;
@@ -107,12 +112,19 @@ __device__ inline R log_w_inverse_or_min(R w) {
 // bisection when that leaves it too.  *s_out (if given) receives
 // sum_i W(e^(a_i - t)) / alpha at the pass's t, as the reference's s.
 // Returns false if g(t) or the step is not finite.
+// ds_out (if given) receives the first two t-derivatives of that s with
+// the sign of a step down in t: sum_i W / (1 + W) / alpha and
+// sum_i W / (1 + W)^3 / alpha.
 template <class D, class R>
 __device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, R& lo, R& hi,
-                                    R* s_out) {
+                                    R* s_out, R* wout = nullptr, R* ds_out = nullptr) {
   R f0, f1, f2, f3;
-  lw_sums4(s, m, lane, -t, f0, f1, f2, f3);
+  lw_sums4(s, m, lane, -t, f0, f1, f2, f3, -1, R(0), wout);
   if (s_out) *s_out = f0 / alpha;
+  if (ds_out) {
+    ds_out[0] = f1 / alpha;
+    ds_out[1] = f2 / alpha;
+  }
   {
     const R v = lambert_w_exp(alpha - t);
     const R d = R(1) + v;
@@ -141,11 +153,29 @@ __device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, 
   return isfinite(f0) && isfinite(tn);
 }
 
+// Upper bound of the root of sum_i W(e^(x_i - t)) = rhs over the values
+// x_i = s[i] + (i < p ? 0 : -c) (and the extra value e, if finite), and
+// whether it is close: W(e^y) <= e^y, so the root lies at or below
+// t_lse = log sum exp(x) - log(rhs), within about e^(max - t_lse) of it when
+// every value sits below t_lse (small W, W(e^y) ~ e^y).  Single precision:
+// a start for the iterations, which end on the root whatever their start.
+template <class D, class R>
+__device__ inline bool lse_start(const D* s, int m, int p, R c, R e, R mx, R rhs, int lane,
+                                 R& t_lse) {
+  float se = (e > -num<R>::inf()) ? expf(static_cast<float>(e - mx)) : 0.0f;
+  for (int i = lane; i < m; i += 64)
+    se += expf(static_cast<float>(static_cast<R>(s[i]) - (i < p ? R(0) : c) - mx));
+  se = group_sum<64>(se);
+  t_lse = mx + static_cast<R>(logf(se)) - dlog(rhs);
+  return mx - t_lse <= R(-1);
+}
+
 // Thresholds (t, 0, hi) of one column whose copy is in s[0, m); entries of U
-// are overwritten with -inf.
+// are overwritten with -inf.  With wl (the wave's LDS array of R), the last
+// pass's W values are left there and *tw receives the t they were taken at.
 template <class D, class R>
 __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_out,
-                                   R& hi_out) {
+                                   R& hi_out, R* wl = nullptr, R* tw = nullptr) {
   const R eps_r = num<R>::eps();
   const R tiny = R(64) * num<R>::min_normal();
   D mx_d;
@@ -173,13 +203,24 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     const R top = (alpha > max) ? alpha : max;
     br_hi = top + dlog(dexp(alpha - top) + static_cast<R>(m) * dexp(max - top)) - dlog(alpha);
   }
+  // Where every value lies well below the log-sum-exp bound, the iteration
+  // starts there (one single-precision pass instead of about three from
+  // t = max on U(-10, 10) columns); the bracket is kept as it is.
+  {
+    R t_lse;
+    const R top = (alpha > max) ? alpha : max;
+    if (lse_start<D, R>(s, m, m, R(0), alpha, top, alpha, lane, t_lse) && t_lse > br_lo &&
+        t_lse < br_hi)
+      t = t_lse;
+  }
+  bool warm = false;
   if constexpr (sizeof(R) == 8) {
     // The same guarded iteration in single precision first (a Lambert pass
     // costs about a third): it ends once a step moves t by at most 3e-3
     // (relative), where the next order-4 correction is below single
     // precision, and the double loop then starts within ~1e-7 of the root
-    // and needs two passes instead of about five.  Its estimate is used
-    // only if it ended so.
+    // and needs one or two passes instead of about five.  Its estimate is
+    // used only if it ended so.
     float tf = static_cast<float>(t);
     float lo_f = static_cast<float>(br_lo), hi_f = static_cast<float>(br_hi);
     const float alpha_f = static_cast<float>(alpha);
@@ -190,11 +231,23 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
       settled = ok && fabsf(t1 - tf) <= 3.0e-3f * fmaxf(1.0f, fabsf(tf));
     }
     if (settled) t = static_cast<R>(tf);
+    warm = settled;
   }
   for (int iter = 0; iter < 64; ++iter) {
     const R t1 = t;
-    guarded_step<D, R>(s, m, lane, alpha, t, br_lo, br_hi, &sv);
+    if (tw) *tw = t;
+    R ds[2];
+    const bool ok = guarded_step<D, R>(s, m, lane, alpha, t, br_lo, br_hi, &sv, wl, ds);
     if (fabs(t1 - t) <= eps_r) break;
+    // From a settled single-precision start a first step of at most 1e-6
+    // leaves an order-4 correction of ~1e-24: the confirming pass is
+    // skipped, and s (the pass's sum at t1) is carried to the final t by its
+    // Taylor series (third-order term ~1e-18 s).
+    if (warm && ok && iter == 0 && fabs(t1 - t) <= R(1e-6) * dmax(R(1), fabs(t))) {
+      const R dt = t - t1;
+      sv += -dt * ds[0] + R(0.5) * dt * dt * ds[1];
+      break;
+    }
   }
   const R K = static_cast<R>(k);
   t_out = t;
@@ -230,7 +283,8 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
         const R s1 = sv, t1 = t;
         sv = (sv < R(0)) ? R(0) : ((sv > R(1)) ? R(1) : sv);
         R S0, S1;
-        lw_sums2(s, m, lane, -t, S0, S1);
+        if (tw) *tw = t;
+        lw_sums2(s, m, lane, -t, S0, S1, wl);
         const R E = S0 + t * S1;
         R z, Az, Bz;
         if (sv < R(0.5)) {
@@ -264,14 +318,21 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
   hi_out = sv / K;
 }
 
+// reuse: each wave also has an LDS array of R (after the waves' columns)
+// where the last pass leaves its W values, and the output map is a Taylor
+// step from them (lambert_w_exp_shift) instead of a new evaluation.
 template <class D, class R>
 __global__ void __launch_bounds__(64 * kEbMaxWaves)
 entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, int k,
-               R alpha, sdca_thresholds* __restrict__ thr, int stride_elems) {
+               R alpha, sdca_thresholds* __restrict__ thr, int stride_elems, int reuse) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
   D* s = reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
+  R* const wl = reuse ? reinterpret_cast<R*>(smem_raw + static_cast<size_t>(waves) *
+                                                            stride_elems * sizeof(D)) +
+                            static_cast<int64_t>(wave) * stride_elems
+                      : nullptr;
   const int m = static_cast<int>(m64);
   const D map_a = D(1) / static_cast<D>(alpha);  // a_lambert_w_exp_map (functor.h:33-38)
   for (int64_t j = static_cast<int64_t>(blockIdx.x) * waves + wave; j < n;
@@ -279,8 +340,8 @@ entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64
     const D* col = in + j * m64;
     for (int i = lane; i < m; i += 64) s[i] = col[i];
     wave_lds_sync();
-    R t, hi;
-    entbias_thresholds<D, R>(s, m, lane, k, alpha, t, hi);
+    R t, hi, tw = 0;
+    entbias_thresholds<D, R>(s, m, lane, k, alpha, t, hi, wl, &tw);
     if (thr && lane == 0) {
       thr[j].t = static_cast<double>(t);
       thr[j].lo = 0;
@@ -288,8 +349,14 @@ entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64
     }
     const D td = static_cast<D>(t), hd = static_cast<D>(hi);
     D* dst = out + j * m64;
-    for (int i = lane; i < m; i += 64)
-      dst[i] = clamp_ref(map_a * lambert_w_exp(col[i] - td), D(0), hd);
+    // Entries moved into U hold -inf in s (and W = 0 in wl): the map.
+    const R dt = t - tw;
+    const bool tay = wl && fabs(dt) <= R(kLambertShiftMax);
+    for (int i = lane; i < m; i += 64) {
+      const D y = (tay && s[i] != -num<D>::inf()) ? static_cast<D>(lambert_w_exp_shift(wl[i], dt))
+                                                   : lambert_w_exp(col[i] - td);
+      dst[i] = clamp_ref(map_a * y, D(0), hd);
+    }
     wave_lds_sync();  // every lane is done with s before the next column's copy
   }
 }
@@ -297,9 +364,10 @@ entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64
 // One order-4 Householder step on the two-block sum (two_entropy.h:15-38);
 // returns f(t) at the old t.
 template <class D, class R>
-__device__ inline R two_w_step4(const D* s, int m, int p, int lane, R alpha, R c, R& t) {
+__device__ inline R two_w_step4(const D* s, int m, int p, int lane, R alpha, R c, R& t,
+                                R* wout = nullptr) {
   R f0, f1, f2, f3;
-  lw_sums4(s, m, lane, -t, f0, f1, f2, f3, p, -t - c);
+  lw_sums4(s, m, lane, -t, f0, f1, f2, f3, p, -t - c, wout);
   f0 -= alpha;
   const R f02 = f0 * f2, f11 = f1 * f1;
   const R den = R(6) * f1 * (f02 - f11) - f0 * (f0 * f3);
@@ -319,9 +387,10 @@ __device__ inline int bisection_count(R v) {
 }
 
 // Thresholds t (block a) and t + c (block b) of one column in s[0, m), split p.
+// With wl, the last pass's W values are left there and *tw receives its t.
 template <class D, class R>
 __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R& t_out,
-                                  R& c_out) {
+                                  R& c_out, R* wl = nullptr, R* tw = nullptr) {
   const R eps = num<R>::eps();
   const R num_a = static_cast<R>(p), num_b = static_cast<R>(m - p);
   R max_a = -num<R>::inf(), max_b = -num<R>::inf(), sum_a = 0, sum_b = 0;
@@ -346,55 +415,64 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
   R ub = max - R(64) * num<R>::exp_min_arg();
   R lf = num<R>::max_finite();
   R uf = -num<R>::max_finite();
-  // Two guesses, each followed by one step (:165-175).
-  R t01 = max - dlog(alpha);
-  R t1 = t01;
-  R f1 = two_w_step4(s, m, p, lane, alpha, c, t1);
-  R t02 = (sum_a + sum_b - num_b * c - alpha) / (num_a + num_b);
-  R t2 = t02;
-  R f2 = two_w_step4(s, m, p, lane, alpha, c, t2);
-  if (f1 > f2) {
-    R x = t01; t01 = t02; t02 = x;
-    x = t1; t1 = t2; t2 = x;
-    x = f1; f1 = f2; f2 = x;
-  }
-  R t;
-  if (f1 > R(0)) {
-    lb = t01;
-    lf = f1;
-    t = t1;
-  } else if (f2 < R(0)) {
-    ub = t02;
-    uf = f2;
-    t = t2;
+  R t, t1, f1;
+  // Where every value lies well below the log-sum-exp bound, the steps below
+  // start there (two or three passes on U(-10, 10) columns instead of the
+  // reference's two guesses and its bisection); they end on the same root.
+  R t_lse;
+  if (lse_start<D, R>(s, m, p, c, -num<R>::inf(), max, alpha, lane, t_lse)) {
+    t = t_lse;
   } else {
-    lb = t02;
-    ub = t01;
-    lf = f2;
-    uf = f1;
-    const R g = (fabs(f1) < fabs(f2)) ? t1 : t2;
-    t = (lb > ((g < ub) ? g : ub)) ? lb : ((g < ub) ? g : ub);
-    // Bisection (:75-96, 193-203).
-    const int num_iter = bisection_count(dlog(ub - lb) * static_cast<R>(1.4426950408889634));
-    for (int iter = 0; iter < num_iter; ++iter) {
-      t = (lb + ub) / R(2);
-      const R fv = lw_sum0(s, m, p, lane, -t, -t - c) - alpha;
-      if (eps < fv && fv < lf) {
-        lf = fv;
-        lb = t;
-      } else if (uf < fv && fv < -eps) {
-        uf = fv;
-        ub = t;
-      } else {
-        break;
-      }
+    // Two guesses, each followed by one step (:165-175).
+    R t01 = max - dlog(alpha);
+    t1 = t01;
+    f1 = two_w_step4(s, m, p, lane, alpha, c, t1);
+    R t02 = (sum_a + sum_b - num_b * c - alpha) / (num_a + num_b);
+    R t2 = t02;
+    R f2 = two_w_step4(s, m, p, lane, alpha, c, t2);
+    if (f1 > f2) {
+      R x = t01; t01 = t02; t02 = x;
+      x = t1; t1 = t2; t2 = x;
+      x = f1; f1 = f2; f2 = x;
     }
-    t = (lb + ub) / R(2);
+    if (f1 > R(0)) {
+      lb = t01;
+      lf = f1;
+      t = t1;
+    } else if (f2 < R(0)) {
+      ub = t02;
+      uf = f2;
+      t = t2;
+    } else {
+      lb = t02;
+      ub = t01;
+      lf = f2;
+      uf = f1;
+      const R g = (fabs(f1) < fabs(f2)) ? t1 : t2;
+      t = (lb > ((g < ub) ? g : ub)) ? lb : ((g < ub) ? g : ub);
+      // Bisection (:75-96, 193-203).
+      const int num_iter = bisection_count(dlog(ub - lb) * static_cast<R>(1.4426950408889634));
+      for (int iter = 0; iter < num_iter; ++iter) {
+        t = (lb + ub) / R(2);
+        const R fv = lw_sum0(s, m, p, lane, -t, -t - c) - alpha;
+        if (eps < fv && fv < lf) {
+          lf = fv;
+          lb = t;
+        } else if (uf < fv && fv < -eps) {
+          uf = fv;
+          ub = t;
+        } else {
+          break;
+        }
+      }
+      t = (lb + ub) / R(2);
+    }
   }
   // Householder steps kept inside the bracket (:207-220).
   for (int iter = 0; iter < 32; ++iter) {
     t1 = t;
-    f1 = two_w_step4(s, m, p, lane, alpha, c, t);
+    if (tw) *tw = t;
+    f1 = two_w_step4(s, m, p, lane, alpha, c, t, wl);
     if (R(0) <= f1 && f1 < lf) {
       lb = t1;
       lf = f1;
@@ -413,11 +491,15 @@ template <class D, class R>
 __global__ void __launch_bounds__(64 * kEbMaxWaves)
 twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
               int64_t p_all, const int64_t* __restrict__ col_p, R alpha,
-              sdca_thresholds* __restrict__ thr, int stride_elems) {
+              sdca_thresholds* __restrict__ thr, int stride_elems, int reuse) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
   D* s = reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
+  R* const wl = reuse ? reinterpret_cast<R*>(smem_raw + static_cast<size_t>(waves) *
+                                                            stride_elems * sizeof(D)) +
+                            static_cast<int64_t>(wave) * stride_elems
+                      : nullptr;
   const int m = static_cast<int>(m64);
   const D map_a = D(1) / static_cast<D>(alpha);  // a_lambert_w_exp_map (functor.h:33-38)
   for (int64_t j = static_cast<int64_t>(blockIdx.x) * waves + wave; j < n;
@@ -426,8 +508,8 @@ twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_
     const D* col = in + j * m64;
     for (int i = lane; i < m; i += 64) s[i] = col[i];
     wave_lds_sync();
-    R t, c;
-    twoent_thresholds<D, R>(s, m, p, lane, alpha, t, c);
+    R t, c, tw = 0;
+    twoent_thresholds<D, R>(s, m, p, lane, alpha, t, c, wl, &tw);
     const R tb = t + c;
     if (thr && lane == 0) {
       thr[2 * j].t = static_cast<double>(t);
@@ -439,16 +521,33 @@ twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_
     }
     const D ta_d = static_cast<D>(t), tb_d = static_cast<D>(tb);
     D* dst = out + j * m64;
-    for (int i = lane; i < m; i += 64)
-      dst[i] = clamp_ref(map_a * lambert_w_exp(col[i] - (i < p ? ta_d : tb_d)), D(0), D(1));
+    const R dt = t - tw;  // both blocks' arguments moved by it
+    const bool tay = wl && fabs(dt) <= R(kLambertShiftMax);
+    for (int i = lane; i < m; i += 64) {
+      const D y = tay ? static_cast<D>(lambert_w_exp_shift(wl[i], dt))
+                      : lambert_w_exp(col[i] - (i < p ? ta_d : tb_d));
+      dst[i] = clamp_ref(map_a * y, D(0), D(1));
+    }
     wave_lds_sync();
   }
+}
+
+// LDS per wave: the column in D and, where it fits (64 KiB per workgroup)
+// and the Result type is at least as wide as the data (otherwise the map is
+// evaluated in the data type), the array of W values in R.
+template <class D, class R>
+size_t eb_per_wave(int stride, bool& reuse) {
+  const size_t col = static_cast<size_t>(stride) * sizeof(D);
+  const size_t w = static_cast<size_t>(stride) * sizeof(R);
+  reuse = sizeof(R) >= sizeof(D) && col + w <= 65536;
+  return reuse ? col + w : col;
 }
 
 template <class D, class R>
 hipError_t launch_twoent_t(const ProxLaunch& a) {
   const int stride = static_cast<int>((a.m + 3) & ~int64_t(3));
-  const size_t per_wave = static_cast<size_t>(stride) * sizeof(D);
+  bool reuse = false;
+  const size_t per_wave = eb_per_wave<D, R>(stride, reuse);
   int waves = kEbMaxWaves;
   while (waves > 1 && waves * per_wave > 65536) waves >>= 1;
   int64_t grid = (a.n + waves - 1) / waves;
@@ -457,14 +556,15 @@ hipError_t launch_twoent_t(const ProxLaunch& a) {
   hipLaunchKernelGGL((twoent_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
                      waves * per_wave, a.stream, static_cast<const D*>(a.in),
                      static_cast<D*>(a.out), a.m, a.n, a.p, a.col_p, static_cast<R>(a.alpha),
-                     a.thr, stride);
+                     a.thr, stride, reuse ? 1 : 0);
   return hipGetLastError();
 }
 
 template <class D, class R>
 hipError_t launch_t(const ProxLaunch& a) {
   const int stride = static_cast<int>((a.m + 3) & ~int64_t(3));  // 16-byte aligned slices
-  const size_t per_wave = static_cast<size_t>(stride) * sizeof(D);
+  bool reuse = false;
+  const size_t per_wave = eb_per_wave<D, R>(stride, reuse);
   int waves = kEbMaxWaves;
   while (waves > 1 && waves * per_wave > 65536) waves >>= 1;
   int64_t grid = (a.n + waves - 1) / waves;
@@ -473,7 +573,7 @@ hipError_t launch_t(const ProxLaunch& a) {
   hipLaunchKernelGGL((entbias_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
                      waves * per_wave, a.stream, static_cast<const D*>(a.in),
                      static_cast<D*>(a.out), a.m, a.n, static_cast<int>(a.k),
-                     static_cast<R>(a.alpha), a.thr, stride);
+                     static_cast<R>(a.alpha), a.thr, stride, reuse ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -1366,30 +1366,19 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
           write_rolled([&](D x) { return clamp_ref(dexp(x - t1), lo1, hi1); });
         }
       } else if constexpr (kWReuse) {
-        // W(exp(x - t)) = W(exp((x - tc) - dt)) from w = W(exp(x - tc)) by
-        // its Taylor series in dt = t - tc: the derivatives of W(e^y) are
-        // g1 = w / (1 + w), g2 = w / (1 + w)^3 and g3 = w (1 - 2w) / (1 + w)^5,
-        // and for |dt| <= 1e-4 (a settled iteration's last step is ~1e-6)
-        // the fourth-order term is below 1e-17 w.  Slots outside the last
-        // solve's free set (fixed at hi by an earlier pass), and columns whose
-        // last step was larger, evaluate the map.
+        // W(exp(x - t)) = W(exp((x - tc) - dt)) from w = W(exp(x - tc)),
+        // dt = t - tc (a settled iteration's last step, ~1e-6).  Slots
+        // outside the last solve's free set (fixed at hi by an earlier pass),
+        // and columns whose last step was larger, evaluate the map.
         if (!th.slow) {
           const R dt = th.t - tw;
-          const unsigned tay = fabs(dt) <= R(1e-4) ? wbits : 0u;
-          const R hdt2 = R(0.5) * dt * dt;
-          const R sdt3 = hdt2 * dt * R(1.0 / 3.0);
+          const unsigned tay = fabs(dt) <= R(kLambertShiftMax) ? wbits : 0u;
 #pragma unroll 2
           for (int c = 0; c < C; ++c) {
             if (c < nvalid) {
               D y;
               if ((tay >> c) & 1u) {
-                const R w = wl[G * c];
-                const R rd = div_near(R(1), R(1) + w);
-                const R rd2 = rd * rd;
-                const R g1 = w * rd;
-                const R g2 = g1 * rd2;
-                const R g3 = g2 * (R(1) - R(2) * w) * rd2;
-                y = static_cast<D>(w - dt * g1 + hdt2 * g2 - sdt3 * g3);
+                y = static_cast<D>(lambert_w_exp_shift(wl[G * c], dt));
               } else {
                 y = lambert_w_exp(mine[G * c] - t1);
               }
