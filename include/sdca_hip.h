@@ -250,6 +250,39 @@ int sdca_eval_kernel(const sdca_objective* objs, int n_obj,
                      unsigned flags, void* stream);
 
 /*
+ * One epoch of the SDCA solver on feature input (replaces one pass of the
+ * example loop of solver::solve, solver.h:44-47: update_variables for each
+ * example, update.h:52-85, with the objective's update_dual_variables) for
+ * the multiclass objectives (kind 0..5).  Per example i in `order`: scores
+ * W' x_i, the dual update of a_i, and W -= x_i (a_old - a_new)' when
+ * sum |a_old - a_new| exceeds epsilon.  The examples run in blocks whose
+ * scores come from the matrix cores; the updates are the sequential loop's
+ * (results equal up to the rounding of the scores' sums).
+ *   X: d x n features, W: d x m primal and A: m x n dual variables, all
+ *      column-major (each example's / class's values contiguous); W and A
+ *      are updated in place;
+ *   labels: n labels in [0, m); order: count example indices in [0, n), or
+ *      NULL for 0..count-1; norms: n values ||x_i||^2 in the data type, or
+ *      NULL (computed, scratch.h:27-41).
+ * Device pointers; (data, result) one of (F32, F32), (F32, F64), (F64, F64);
+ * m at most 16384 (fp32) or 8192 (fp64).  Returns SDCA_ERR_LABELS (after
+ * the epoch, which read such entries as 0) for an index or label out of
+ * range.
+ */
+int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result,
+                        int64_t d, int64_t m, int64_t n, const void* X, void* W, void* A,
+                        const int64_t* labels, const int64_t* order, int64_t count,
+                        const void* norms, void* stream);
+
+/*
+ * The reference solver's example order for epoch `epoch` (0-based) of a
+ * solve over n examples (solver.h:75-92, 108-112: a default-seeded
+ * std::minstd_rand, std::shuffle of 0..n-1 once per epoch): n indices into
+ * the host array `order`.  Host only.
+ */
+int sdca_epoch_order(int64_t n, int64_t epoch, int64_t* order);
+
+/*
  * W = W0 + X A' (W = X A' when W0 is NULL) on the matrix cores: the primal
  * recomputation of eval_recompute_primal (eval/core.h:148-182), which the
  * reference runs before each evaluation when built with SDCA_ACCURATE_MATH.

@@ -377,6 +377,57 @@ def scores(X, W, out=None):
     return S
 
 
+def epoch_order(n, epoch):
+    """The reference solver's example order for epoch `epoch` (0-based) of a
+    solve over n examples (solver.h:75-112): int64 numpy array."""
+    lib = library()
+    out = np.zeros(int(n), dtype=np.int64)
+    lib.sdca_epoch_order.restype = ctypes.c_int
+    rc = lib.sdca_epoch_order(ctypes.c_int64(int(n)), ctypes.c_int64(int(epoch)),
+                              ctypes.c_void_p(out.ctypes.data))
+    if rc != 0:
+        raise SdcaError(rc, lib.sdca_last_error().decode())
+    return out
+
+
+def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None):
+    """One SDCA epoch on feature input (update_variables for each example of
+    `order`, update.h:52-85) for a multiclass objective (name, c, gamma, k):
+    X (n, d), W (m, d), A (n, m) CUDA tensors, W and A updated in place and
+    returned.  order: example indices (None: 0..n-1), e.g. epoch_order(n, e);
+    norms: (n,) squared row norms of X, or None."""
+    lib = library()
+    if not _is_torch(X) or not X.is_cuda:
+        raise SdcaError(2, "epoch_features takes CUDA tensors")
+    import torch
+    n, d = int(X.shape[0]), int(X.shape[1])
+    m = int(W.shape[0])
+    _need(X, "X", (n, d), X)
+    _need(W, "W", (m, d), X)
+    _need(A, "A", (n, m), X)
+    _need(norms, "norms", (n,), X)
+    data = _dtype_code(X)
+    res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
+    lab = torch.as_tensor(labels, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
+    if lab.shape[0] != n:
+        raise SdcaError(2, f"labels: expected {n} entries, got {lab.shape[0]}")
+    od = None
+    if order is not None:
+        od = torch.as_tensor(order, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
+    count = n if od is None else int(od.shape[0])
+    objarr = _objs([obj])
+    lib.sdca_epoch_features.restype = ctypes.c_int
+    rc = lib.sdca_epoch_features(objarr, ctypes.c_int(data), ctypes.c_int(res), ctypes.c_int64(d),
+                                 ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(_ptr(X)),
+                                 ctypes.c_void_p(_ptr(W)), ctypes.c_void_p(_ptr(A)),
+                                 ctypes.c_void_p(_ptr(lab)), ctypes.c_void_p(_ptr(od)),
+                                 ctypes.c_int64(count), ctypes.c_void_p(_ptr(norms)),
+                                 _stream_ptr())
+    if rc != 0:
+        raise SdcaError(rc, lib.sdca_last_error().decode())
+    return W, A
+
+
 def recompute_primal(X, A, W0=None, out=None):
     """W = W0 + A^T X (the reference's W = W0 + X A' of eval_recompute_primal,
     eval/core.h:148-182): X (n, d) features, A (n, m) dual variables, W0 and

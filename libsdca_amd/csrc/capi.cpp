@@ -4,7 +4,10 @@
 // per-(device, stream, host thread) workspace cache and the kernel dispatch.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
+#include <numeric>
+#include <random>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -17,6 +20,7 @@
 #include <vector>
 
 #include "../../include/sdca_hip.h"
+#include "epoch_launch.hpp"
 #include "eval_launch.hpp"
 #include "prox_launch.hpp"
 
@@ -56,8 +60,8 @@ size_t dtype_size(int dt) { return dt == SDCA_F32 ? 4 : 8; }
 // graph capture cannot grow it (the wait and the allocation are not
 // capturable): warm the stream up with one call of the same size first.
 struct Workspace {
-  void* ptr[4] = {nullptr, nullptr, nullptr, nullptr};
-  size_t cap[4] = {0, 0, 0, 0};
+  void* ptr[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+  size_t cap[5] = {0, 0, 0, 0, 0};
   // Pinned host block for the evaluation's results: copies into it are
   // asynchronous, so the call waits once for all of them.
   void* host = nullptr;
@@ -864,6 +868,84 @@ int sdca_eval_scores(const sdca_objective* objs, int n_obj, sdca_dtype data, sdc
   return eval_common(objs, n_obj, data, result, 0, m, n, nullptr, nullptr, S, A, nullptr, labels,
                      offsets, primal_regularizer, dual_regularizer, records, accuracy, per_example,
                      flags, stream);
+}
+
+int sdca_epoch_order(int64_t n, int64_t epoch, int64_t* order) {
+  g_last_error.clear();
+  if (n < 0 || epoch < 0) return fail(SDCA_ERR_ARG_RANGE, "n and epoch must be >= 0");
+  if (n > 0 && !order) return fail(SDCA_ERR_ARG_NULL, "order must not be NULL");
+  // solver.h:75-92: a default-seeded minstd_rand at the start of the solve,
+  // the examples 0..n-1, one std::shuffle per epoch (solver.h:108-112).
+  std::minstd_rand generator;
+  generator.seed();
+  std::vector<int64_t> examples(static_cast<size_t>(n));
+  std::iota(examples.begin(), examples.end(), int64_t(0));
+  for (int64_t e = 0; e <= epoch; ++e) std::shuffle(examples.begin(), examples.end(), generator);
+  std::copy(examples.begin(), examples.end(), order);
+  return SDCA_OK;
+}
+
+int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result, int64_t d,
+                        int64_t m, int64_t n, const void* X, void* W, void* A,
+                        const int64_t* labels, const int64_t* order, int64_t count,
+                        const void* norms, void* stream_ptr) {
+  using namespace sdca_gpu;
+  g_last_error.clear();
+  if (!obj) return fail(SDCA_ERR_ARG_NULL, "obj must not be NULL");
+  if (obj->kind < SDCA_OBJ_HINGE_TOPK || obj->kind > SDCA_OBJ_ENTROPY_TOPK)
+    return fail(SDCA_ERR_NOT_IMPLEMENTED,
+                "the epoch supports the multiclass objectives (kind 0..5; got %d)",
+                static_cast<int>(obj->kind));
+  if (!((data == SDCA_F32 && (result == SDCA_F32 || result == SDCA_F64)) ||
+        (data == SDCA_F64 && result == SDCA_F64)))
+    return fail(SDCA_ERR_PRECISION,
+                "the epoch takes (float, float), (float, double) or (double, double)");
+  if (d < 1 || m < 2 || n < 1 || count < 0)
+    return fail(SDCA_ERR_ARG_RANGE, "need d >= 1, m >= 2, n >= 1, count >= 0");
+  if (m > epoch_max_m(data))
+    return fail(SDCA_ERR_NOT_IMPLEMENTED, "the epoch supports m <= %lld for this element type",
+                (long long)epoch_max_m(data));
+  if (n > INT32_MAX || d > INT32_MAX) return fail(SDCA_ERR_ARG_RANGE, "matrix too large");
+  if (!order && count > n)
+    return fail(SDCA_ERR_ARG_RANGE, "count (%lld) > n (%lld) without an order",
+                (long long)count, (long long)n);
+  int rc = check_objectives(obj, 1, m, false);
+  if (rc) return rc;
+  if (!X || !W || !A || !labels) return fail(SDCA_ERR_ARG_NULL, "X, W, A and labels must not be NULL");
+  if (count == 0) return SDCA_OK;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  void* ws = nullptr;
+  if ((rc = workspace(stream, 4, epoch_workspace_bytes(data, d, m, n, norms != nullptr), &ws)))
+    return rc;
+  EpochLaunch a;
+  a.data = data;
+  a.result = result;
+  a.kind = obj->kind;
+  a.c = obj->c;
+  a.gamma = obj->gamma;
+  a.k = static_cast<int>(obj->k);
+  a.d = d;
+  a.m = m;
+  a.n = n;
+  a.X = X;
+  a.W = W;
+  a.A = A;
+  a.labels = labels;
+  a.order = order;
+  a.count = count;
+  a.norms = norms;
+  a.ws = ws;
+  a.stream = stream;
+  int* flag = nullptr;
+  SDCA_HIP_TRY(launch_epoch(a, &flag), "SDCA epoch kernels");
+  int bad = 0;
+  SDCA_HIP_TRY(hipMemcpyAsync(&bad, flag, sizeof(int), hipMemcpyDeviceToHost, stream),
+               "hipMemcpyAsync(D2H)");
+  SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  if (bad)
+    return fail(SDCA_ERR_LABELS,
+                "an example index outside [0, n) or a label outside [0, m) (read as 0)");
+  return SDCA_OK;
 }
 
 }  // extern "C"

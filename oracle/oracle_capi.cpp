@@ -6,6 +6,8 @@
 // oracle_eval_scores   per-example part of evaluate_dataset (eval.h:36-47) on given scores
 // oracle_eval_features evaluate_dataset for feature input, with the scores
 //                      gemv (eval/scores.h:21-26) as a plain loop
+// oracle_epoch_features one SDCA epoch on feature input (solver.h:39-51,
+//                      update.h:52-85) over a given example order
 //
 // Host pointers only.  `nthreads` > 1 splits columns / examples over
 // std::threads, each with its own scratch (the reference is single-threaded;
@@ -13,6 +15,7 @@
 #include <cstring>
 #include <thread>
 
+#include "oracle_epoch.hpp"
 #include "oracle_eval.hpp"
 
 namespace {
@@ -350,6 +353,31 @@ int oracle_dual_regularizer(int data, int result, int64_t m, int64_t n, const vo
   else
     return SDCA_ERR_PRECISION;
   return 0;
+}
+
+// X: n x d, W: m x d, A: n x m updated in place; order: count indices or
+// NULL; reverse: the scores' dot products accumulated in Data, last term
+// first.  Returns -1 for an objective without a multiclass update.
+int oracle_epoch_features(const sdca_objective* obj, int data, int result, int64_t d, int64_t m,
+                          int64_t n, const void* X, void* W, void* A, const int64_t* labels,
+                          const int64_t* order, int64_t count, int reverse) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return orc::epoch<float, float>(*obj, d, m, n, static_cast<const float*>(X),
+                                    static_cast<float*>(W), static_cast<float*>(A), labels, order,
+                                    count, reverse != 0);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return orc::epoch<float, double>(*obj, d, m, n, static_cast<const float*>(X),
+                                     static_cast<float*>(W), static_cast<float*>(A), labels,
+                                     order, count, reverse != 0);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return orc::epoch<double, double>(*obj, d, m, n, static_cast<const double*>(X),
+                                      static_cast<double*>(W), static_cast<double*>(A), labels,
+                                      order, count, reverse != 0);
+  if (data == SDCA_F64 && result == SDCA_LONG_DOUBLE)
+    return orc::epoch<double, long double>(*obj, d, m, n, static_cast<const double*>(X),
+                                           static_cast<double*>(W), static_cast<double*>(A),
+                                           labels, order, count, reverse != 0);
+  return -2;
 }
 
 double oracle_lambert_w_exp_f64(double x) { return orc::lambert_w_exp(x); }

@@ -21,6 +21,7 @@
 
 #include "sdca/prox.h"
 #include "sdca/solver/context.h"
+#include "sdca/solver.h"
 #include "sdca/solver/eval.h"
 #include "sdca/solver/eval/dual.h"
 #include "sdca/solver/eval/primal.h"
@@ -526,9 +527,77 @@ int evaluate_impl(const sdca_objective* objs, int n_obj, int64_t d, int64_t m, i
   return 0;
 }
 
+// One epoch of the reference's example loop (solver.h:44-47) over `order`
+// (NULL: 0..n-1): sdca::update_variables (update.h:52-85) on a
+// solver_context over the whole training set, W and A updated in place.
+// With epochs > 0 instead, the reference's own solve() runs that many epochs
+// (its generator and std::shuffle give the order, solver.h:75-112) with no
+// evaluation between epochs.
+template <class D, class R, template <class, class> class Obj>
+void epoch_run(Obj<D, R> obj, int64_t d, int64_t m, int64_t n, const D* X, D* W, D* A,
+               const int64_t* labels, const int64_t* order, int64_t count, int64_t epochs) {
+  typedef sdca::solver_context<D, R, sdca::feature_input, sdca::multiclass_output, Obj> Ctx;
+  typename Ctx::train_set_type set(
+      sdca::feature_input<D>(static_cast<sdca::size_type>(d), static_cast<sdca::size_type>(n), X),
+      make_out(std::false_type(), m, labels, nullptr, 0, n));
+  Ctx ctx(std::move(set), std::move(obj), A, W);
+  if (epochs > 0) {
+    sdca::logging::set_level(sdca::logging::level::none);
+    ctx.criteria.max_epoch = static_cast<sdca::size_type>(epochs);
+    ctx.criteria.eval_epoch = 0;
+    ctx.criteria.eval_on_start = false;
+    auto solver = sdca::make_solver(ctx);
+    solver.solve();
+    return;
+  }
+  sdca::solver_scratch<D, sdca::feature_input> scratch;
+  scratch.init(ctx.train);
+  for (int64_t q = 0; q < count; ++q)
+    sdca::update_variables(static_cast<sdca::size_type>(order ? order[q] : q), ctx, scratch);
+}
+
+#define SDCA_REF_EPOCH(OBJ)                                                               \
+  epoch_run<D, R>(OBJ, d, m, n, X, W, A, labels, order, count, epochs)
+
+template <class D, class R>
+int epoch_impl(const sdca_objective& ob, int64_t d, int64_t m, int64_t n, const D* X, D* W,
+               D* A, const int64_t* labels, const int64_t* order, int64_t count,
+               int64_t epochs) {
+  const R c = static_cast<R>(ob.c), g = static_cast<R>(ob.gamma);
+  const sdca::size_type k = static_cast<sdca::size_type>(ob.k);
+  switch (ob.kind) {
+    case SDCA_OBJ_HINGE_TOPK: SDCA_REF_EPOCH((sdca::l2_hinge_topk<D, R>(c, k))); break;
+    case SDCA_OBJ_HINGE_TOPK_SMOOTH: SDCA_REF_EPOCH((sdca::l2_hinge_topk_smooth<D, R>(c, g, k))); break;
+    case SDCA_OBJ_TOPK_HINGE: SDCA_REF_EPOCH((sdca::l2_topk_hinge<D, R>(c, k))); break;
+    case SDCA_OBJ_TOPK_HINGE_SMOOTH: SDCA_REF_EPOCH((sdca::l2_topk_hinge_smooth<D, R>(c, g, k))); break;
+    case SDCA_OBJ_ENTROPY: SDCA_REF_EPOCH((sdca::l2_entropy<D, R>(c))); break;
+    case SDCA_OBJ_ENTROPY_TOPK: SDCA_REF_EPOCH((sdca::l2_entropy_topk<D, R>(c, k))); break;
+    default: return SDCA_ERR_ARG_RANGE;
+  }
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+// The reference's SDCA epoch on feature input (see epoch_run): X d x n,
+// W d x m, A m x n, column-major (each example's / class's values
+// contiguous), W and A updated in place.
+int ref_epoch_features(const sdca_objective* obj, int data, int result, int64_t d, int64_t m,
+                       int64_t n, const void* X, void* W, void* A, const int64_t* labels,
+                       const int64_t* order, int64_t count, int64_t epochs) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return epoch_impl<float, float>(*obj, d, m, n, static_cast<const float*>(X),
+        static_cast<float*>(W), static_cast<float*>(A), labels, order, count, epochs);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return epoch_impl<float, double>(*obj, d, m, n, static_cast<const float*>(X),
+        static_cast<float*>(W), static_cast<float*>(A), labels, order, count, epochs);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return epoch_impl<double, double>(*obj, d, m, n, static_cast<const double*>(X),
+        static_cast<double*>(W), static_cast<double*>(A), labels, order, count, epochs);
+  return SDCA_ERR_PRECISION;
+}
 
 int ref_prox(int op, int data, int result, int64_t m, int64_t n, void* x,
              const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* out,

@@ -1,0 +1,147 @@
+"""GPU parity of the SDCA epoch (sdca_epoch_features) against the oracle.
+
+The epoch's arithmetic is the sequential loop's (update.h:52-85 per example,
+in the reference solver's order from sdca_epoch_order) except for the order
+of the sums in the scores: the GPU forms them from a block GEMM and the
+block's earlier rank-1 updates.  Each case runs two epochs from zero on the
+GPU and in the oracle (restatement pinned to the reference's own epoch in
+tests/test_epoch_oracle.py) and requires every entry of W and A within
+4 times the spread of the oracle's two roundings of the scores (exact dot
+products against Data accumulation) plus 8 ulps of the largest magnitude:
+a different rounding of the scores must not move the epoch further than
+another valid rounding does.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+OBJS = [("hinge_topk", 1.0, 1.0, 3), ("hinge_topk_smooth", 1.0, 0.5, 3),
+        ("topk_hinge", 1.0, 1.0, 2), ("topk_hinge_smooth", 0.7, 0.5, 2),
+        ("entropy", 1.0, 1.0, 1), ("entropy_topk", 1.5, 1.0, 3)]
+PAIRS = [(np.float32, 0), (np.float32, 1), (np.float64, 1)]
+ORACLE_NAME = {"hinge_topk": "l2_hinge_topk", "hinge_topk_smooth": "l2_hinge_topk_smooth",
+               "topk_hinge": "l2_topk_hinge", "topk_hinge_smooth": "l2_topk_hinge_smooth",
+               "entropy": "l2_entropy", "entropy_topk": "l2_entropy_topk"}
+
+
+def problem(dtype, n, d, m, seed):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((n, d))
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    X[3] = 0.0  # norm2 = 0: the example changes nothing
+    y = rng.integers(0, m, n)
+    y[:2] = [0, m - 1]
+    return X.astype(dtype), y
+
+
+def oracle_epochs(oracle, obj, X, y, m, result, orders, reverse=False):
+    n, d = X.shape
+    W = np.zeros((m, d), X.dtype)
+    A = np.zeros((n, m), X.dtype)
+    for order in orders:
+        oracle.epoch_features(obj, X, W, A, y, order, result=result, reverse=reverse)
+    return W, A
+
+
+def gpu_epochs(cuda, obj, X, y, m, result, orders):
+    import torch
+    import libsdca_amd as sd
+    n, d = X.shape
+    Xt = torch.from_numpy(X).to(cuda)
+    W = torch.zeros((m, d), dtype=Xt.dtype, device=cuda)
+    A = torch.zeros((n, m), dtype=Xt.dtype, device=cuda)
+    name = (ORACLE_NAME[obj[0]],) + tuple(obj[1:])
+    for order in orders:
+        sd.epoch_features(name, Xt, W, A, y, order=order, result=result)
+    torch.cuda.synchronize()
+    return W.cpu().numpy(), A.cpu().numpy()
+
+
+def check(oracle, cuda, obj, dtype, result, n, d, m, seed, epochs=2):
+    import libsdca_amd as sd
+    X, y = problem(dtype, n, d, m, seed)
+    orders = [sd.epoch_order(n, e) for e in range(epochs)]
+    Wg, Ag = gpu_epochs(cuda, obj, X, y, m, result, orders)
+    Wo, Ao = oracle_epochs(oracle, obj, X, y, m, result, orders)
+    Wv, Av = oracle_epochs(oracle, obj, X, y, m, result, orders, reverse=True)
+    eps = np.finfo(dtype).eps
+    for name, g, o, v in (("W", Wg, Wo, Wv), ("A", Ag, Ao, Av)):
+        spread = float(np.abs(o - v).max())
+        tol = 4 * spread + 8 * eps * max(1.0, float(np.abs(o).max()))
+        err = float(np.abs(g - o).max())
+        print(f"{obj[0]} {np.dtype(dtype).name}/{result} n={n} d={d} m={m} {name}: "
+              f"|gpu - oracle| {err:.2e}, spread {spread:.2e}")
+        assert err <= tol, f"{obj[0]} m={m} {name}: |gpu - oracle| {err:.3e} > {tol:.3e}"
+    assert np.abs(Ao).max() > 0.01
+    assert not Ag[3].any()
+    return Wg, Ag
+
+
+@pytest.mark.parametrize("dtype,result", PAIRS)
+@pytest.mark.parametrize("obj", OBJS)
+@pytest.mark.parametrize("m", [2, 20, 257])
+def test_epoch(cuda, oracle, obj, dtype, result, m):
+    if obj[3] > m - 1:
+        pytest.skip("k > m - 1")
+    check(oracle, cuda, obj, dtype, result, 300, 64, m, 7 + m)
+
+
+@pytest.mark.parametrize("obj", [OBJS[1], OBJS[3], OBJS[4], OBJS[5]])
+def test_epoch_c4_like(cuda, oracle, obj):
+    """A block-heavy shape (4,000 examples in 125 blocks, m = 1000)."""
+    check(oracle, cuda, obj, np.float32, 0, 4000, 256, 1000, 99, epochs=1)
+
+
+def test_epoch_partial_order_and_bad_index(cuda, oracle):
+    """count < n with an explicit order (a prefix of the epoch's order), and
+    an index out of range: reported as SDCA_ERR_LABELS after the call, which
+    read it as example 0 (no access leaves the arrays)."""
+    import torch
+    import libsdca_amd as sd
+    obj = OBJS[1]
+    X, y = problem(np.float32, 200, 32, 10, 5)
+    order = sd.epoch_order(200, 0)[:77]
+    Wg, Ag = gpu_epochs(cuda, obj, X, y, 10, 0, [order])
+    Wo, Ao = oracle_epochs(oracle, obj, X, y, 10, 0, [order])
+    assert np.abs(Wg - Wo).max() <= 1e-5 and np.abs(Ag - Ao).max() <= 1e-5
+    untouched = np.setdiff1d(np.arange(200), order)
+    assert not Ag[untouched].any()
+    Xt = torch.from_numpy(X).to(cuda)
+    W = torch.zeros((10, 32), device=cuda)
+    A = torch.zeros((200, 10), device=cuda)
+    with pytest.raises(sd.SdcaError) as e:
+        sd.epoch_features(("l2_hinge_topk", 1.0, 1.0, 1), Xt, W, A, y, order=[0, 5, 200, 7])
+    assert e.value.status == 8
+    bad = y.copy()
+    bad[4] = 10
+    with pytest.raises(sd.SdcaError) as e:
+        sd.epoch_features(("l2_hinge_topk", 1.0, 1.0, 1), Xt, W, A, bad, order=[4])
+    assert e.value.status == 8
+
+
+def test_epoch_duality_gap_closes(cuda):
+    """Size-independent property: the relative duality gap of the evaluation
+    pass falls over epochs (SDCA's dual ascent) on a separable-ish problem."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(3)
+    n, d, m = 3000, 128, 50
+    centers = rng.standard_normal((m, d)) * 2
+    y = rng.integers(0, m, n)
+    X = centers[y] + rng.standard_normal((n, d))
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    Xt = torch.from_numpy(X.astype(np.float32)).to(cuda)
+    W = torch.zeros((m, d), device=cuda)
+    A = torch.zeros((n, m), device=cuda)
+    c = 1.0 / (1e-3 * n)  # c = 1 / (lambda n)
+    obj = ("l2_hinge_topk_smooth", c, 1.0, 1)
+    gaps = []
+    for e in range(4):
+        sd.epoch_features(obj, Xt, W, A, y, order=sd.epoch_order(n, e))
+        recs, _, _ = sd.eval_features([obj], Xt, W, y, A=A, result="double")
+        r = recs[0]
+        gaps.append((r["primal"] - r["dual"]) / max(abs(r["primal"]), abs(r["dual"])))
+    print("relative gaps", gaps)
+    assert all(g > -1e-5 for g in gaps)
+    assert gaps[-1] < gaps[0] and gaps[-1] < 0.5 * gaps[0]

@@ -1,0 +1,75 @@
+"""The SDCA epoch's oracle and example order against the reference itself.
+
+* The order: sdca_epoch_order (the C ABI, host only) gives the reference
+  solver's shuffled order of each epoch (solver.h:75-112).  Pinned by running
+  the reference's own solve() for several epochs (oracle/_ref) and, from the
+  same start, the reference's update_variables over our orders one epoch at
+  a time: the same code on the same order must give identical W and A.
+* The restatement (oracle/oracle_epoch.hpp) against the reference's
+  update_variables (update.h:52-85) with MKL for its BLAS calls, for the six
+  multiclass objectives and the three precision pairs, two epochs: every
+  entry of W and A within 4 times the spread of the restatement's two
+  roundings of the scores (exact dot products, and Data accumulation from
+  the last term) plus 8 ulps of the largest magnitude - the reference's own
+  BLAS rounds the scores in a third, unpinned order.
+"""
+import numpy as np
+import pytest
+
+OBJS = [("hinge_topk", 1.0, 1.0, 3), ("hinge_topk_smooth", 1.0, 0.5, 3),
+        ("topk_hinge", 1.0, 1.0, 2), ("topk_hinge_smooth", 0.7, 0.5, 2),
+        ("entropy", 1.0, 1.0, 1), ("entropy_topk", 1.5, 1.0, 3)]
+PAIRS = [(np.float32, 0), (np.float32, 1), (np.float64, 1)]
+
+
+def problem(dtype, n=80, d=24, m=12, seed=0):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((n, d))
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    X[3] = 0.0  # norm2 = 0: the reference skips the example
+    y = rng.integers(0, m, n)
+    return X.astype(dtype), y, m
+
+
+def run(lib, obj, X, y, m, result, orders, reverse=False):
+    n, d = X.shape
+    W = np.zeros((m, d), X.dtype)
+    A = np.zeros((n, m), X.dtype)
+    for order in orders:
+        lib.epoch_features(obj, X, W, A, y, order, result=result, reverse=reverse)
+    return W, A
+
+
+def test_epoch_order_is_the_reference_solvers(reference):
+    import libsdca_amd as sd
+    X, y, m = problem(np.float64)
+    n, d = X.shape
+    obj = ("hinge_topk_smooth", 1.0, 0.5, 3)
+    W1, A1 = np.zeros((m, d)), np.zeros((n, m))
+    reference.epoch_features(obj, X, W1, A1, y, epochs=3)
+    orders = [sd.epoch_order(n, e) for e in range(3)]
+    W2, A2 = run(reference, obj, X, y, m, 1, orders)
+    assert np.array_equal(W1, W2) and np.array_equal(A1, A2)
+    assert sorted(orders[1]) == list(range(n)) and not np.array_equal(orders[0], orders[1])
+
+
+@pytest.mark.parametrize("dtype,result", PAIRS)
+@pytest.mark.parametrize("obj", OBJS)
+def test_epoch_restatement_vs_reference(oracle, reference, obj, dtype, result):
+    import libsdca_amd as sd
+    X, y, m = problem(dtype, seed=len(obj[0]))
+    n = X.shape[0]
+    orders = [sd.epoch_order(n, e) for e in range(2)]
+    Wr, Ar = run(reference, obj, X, y, m, result, orders)
+    Wo, Ao = run(oracle, obj, X, y, m, result, orders)
+    Wv, Av = run(oracle, obj, X, y, m, result, orders, reverse=True)
+    eps = np.finfo(dtype).eps
+    for name, r, o, v in (("W", Wr, Wo, Wv), ("A", Ar, Ao, Av)):
+        spread = float(np.abs(o - v).max())
+        tol = 4 * spread + 8 * eps * max(1.0, float(np.abs(r).max()))
+        err = float(np.abs(o - r).max())
+        assert err <= tol, f"{obj[0]} {name}: |oracle - ref| {err:.3e} > {tol:.3e}"
+    # the epoch moved the variables (a vacuous comparison pins nothing)
+    assert np.abs(Ar).max() > 0.01 and np.abs(Wr).max() > 0.01
+    # the skipped example's duals stay at zero (update.h:62)
+    assert not Ar[3].any()
