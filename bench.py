@@ -17,7 +17,8 @@ cone on the headline input), c3 (entropy f64 m=1000 n=2e5), c3norm
 (entropy_norm f64), lambert (W(exp(x)) f64 on 10M points), c5prox
 (two_simplex f32 m=200 n=5e5, per-column p), c4 (evaluation pass d=4096
 m=1000 n=1e5: examples/s, roofline on the fp32 MFMA score GEMM), c5eval
-(multilabel evaluation d=1024 m=200 n=5e5).
+(multilabel evaluation d=1024 m=200 n=5e5), c4epoch (one SDCA epoch on the C4
+data: examples/s, the reference's own epoch loop as cpu_baseline).
 
 The default run (c2) also times the whole C4 evaluation pass under the same
 clock and nests it as "c4" (examples/s, an MFMA roofline for the score GEMM
@@ -100,6 +101,11 @@ CONFIGS = {
                desc="evaluation pass, fp32: X d=4096 x n=100,000 (N(0,1), unit columns), "
                     "W d x m=1000 (N(0,0.01^2)), scores W'X, smooth top-5 hinge (gamma=1) and "
                     "softmax cross-entropy with c=1 (lambda=1/n), top-1/top-5 accuracy"),
+    "c4epoch": dict(op="epoch", d=4096, m=1000, n=100_000, dtype="f32", result="f32", seed=104,
+                    obj=("l2_hinge_topk_smooth", 1.0, 1.0, 5), steps=2, warmup=1,
+                    desc="one SDCA epoch (update_variables over the reference solver's shuffled "
+                         "order), fp32: X d=4096 x n=100,000 (N(0,1), unit columns), m=1000, "
+                         "smooth top-5 hinge (gamma=1, c=1), W and A from zero"),
     "c4kernel": dict(op="eval", kernel=True, d=4096, m=1000, n=20_000, dtype="f32", result="f32",
                      seed=106, objs=[("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)],
                      desc="kernel-input evaluation pass, fp32: K = X'X (n = n_train = 20,000 "
@@ -121,10 +127,11 @@ CPU_THREADS = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    # 50 untimed steps (about 30 ms of C2 work): the clocks settle; after 5
-    # the first timed steps still ran ~5 % slow.
-    ap.add_argument("--warmup", type=int, default=50)
+    # Defaults 20 and 50 (the epoch configuration: 2 and 1).  50 untimed
+    # steps (about 30 ms of C2 work): the clocks settle; after 5 the first
+    # timed steps still ran ~5 % slow.
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -394,6 +401,82 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
     return result
 
 
+def bench_epoch(cfg, args, torch, sd):
+    """Times SDCA epochs (sdca_epoch_features) over the reference solver's
+    orders: `warmup` untimed epochs from W = 0, A = 0, then `steps` timed ones
+    (each call ends with a host synchronisation); value = examples per second."""
+    import numpy as np
+    steps = cfg["steps"] if args.steps is None else args.steps
+    warmup = cfg["warmup"] if args.warmup is None else args.warmup
+    dev = torch.device("cuda:0")
+    X, _, labels, _ = make_eval_input(cfg, torch, dev)
+    n, m, d = cfg["n"], cfg["m"], cfg["d"]
+    W = torch.zeros((m, d), dtype=torch.float32, device=dev)
+    A = torch.zeros((n, m), dtype=torch.float32, device=dev)
+    norms = (X * X).sum(dim=1).contiguous()
+    orders = [torch.from_numpy(sd.epoch_order(n, e)).to(dev) for e in range(warmup + steps)]
+    res = "float" if cfg["result"] == "f32" else "double"
+    for e in range(warmup):
+        sd.epoch_features(cfg["obj"], X, W, A, labels, order=orders[e], norms=norms, result=res)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e in range(warmup, warmup + steps):
+        sd.epoch_features(cfg["obj"], X, W, A, labels, order=orders[e], norms=norms, result=res)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    recs, _, _ = sd.eval_features([cfg["obj"]], X, W, labels, A=A, result="double")
+    r = recs[0]
+    gap = (r["primal"] - r["dual"]) / max(abs(r["primal"]), abs(r["dual"]))
+    result = {
+        "metric": "SDCA epoch examples/s", "value": n / (ms / 1e3), "unit": "examples/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": cfg["dtype"], "data": "synthetic (seeded on the device)",
+        "config": {"workload": cfg["desc"], "d": d, "m": m, "n": n,
+                   "objective": list(cfg["obj"])},
+        "roofline": None,
+        "note": "latency-bound: the dual updates run in order in one workgroup per block of "
+                "32 examples (profiles/ has the per-kernel split); relative duality gap after "
+                f"{warmup + steps} epochs: {gap:.4g}",
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_epoch(cfg, X, labels, sd, args.cpu_seconds)
+    return result
+
+
+def cpu_baseline_epoch(cfg, X, labels, sd, seconds):
+    """The reference's own epoch loop (sdca::update_variables, oracle/_ref with
+    MKL) from W = 0, A = 0 over the first examples of epoch 0's order, one
+    thread as shipped (the loop is sequential)."""
+    import numpy as np
+    from oracle import binding
+    ref = binding.reference()
+    if ref is None:
+        return None
+    oname = {"l2_hinge_topk_smooth": "hinge_topk_smooth"}
+    obj = (oname[cfg["obj"][0]],) + tuple(cfg["obj"][1:])
+    n, m, d = cfg["n"], cfg["m"], cfg["d"]
+    Xh = X.cpu().numpy()
+    lab = labels.cpu().numpy()
+    order = sd.epoch_order(n, 0)
+
+    def run(count):
+        W = np.zeros((m, d), np.float32)
+        A = np.zeros((n, m), np.float32)
+        t0 = time.perf_counter()
+        ref.epoch_features(obj, Xh, W, A, lab, order[:count],
+                           result=0 if cfg["result"] == "f32" else 1)
+        return time.perf_counter() - t0
+
+    count = 64
+    t = run(count)
+    count = max(64, min(n, int(count * seconds / max(t, 1e-3))))
+    t = run(count)
+    return {"value": count / t, "unit": "examples/s", "cores": 1, "kind": "reference",
+            "sample": f"the first {count} examples of epoch 0's order from W = 0, A = 0, "
+                      f"1 thread ({t:.1f} s): the reference's update_variables with MKL"}
+
+
 def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds, kernel=False):
     """The reference's evaluate_dataset (solver/eval.h:15-51, oracle/_ref:
     the reference headers with Intel MKL as their CBLAS) on a bounded sample
@@ -468,10 +551,16 @@ def main():
 
     import libsdca_amd as sd
 
+    cfg = CONFIGS[args.config]
+    if cfg["op"] == "epoch" and not args.copy_calibration:
+        print(json.dumps(bench_epoch(cfg, args, torch, sd)))
+        return
+    # The epoch has its own defaults; every other workload takes 20 / 50.
+    args.steps = 20 if args.steps is None else args.steps
+    args.warmup = 50 if args.warmup is None else args.warmup
     if args.copy_calibration:
         copy_calibration(args, torch)
         return
-    cfg = CONFIGS[args.config]
     if cfg["op"] == "eval":
         print(json.dumps(bench_eval(cfg, args, torch, sd)))
         return

@@ -11,8 +11,10 @@
 //   sum W(e^(a - t)) + sum W(e^(b - t - c)) = alpha.
 //
 // Each pass is a sum of W(e^(x_i + shift)) and its derivatives over the
-// column: each lane sums a stride-64 share, and a butterfly reduction gives
-// every lane the totals, so the scalar updates run uniformly on all 64 lanes.
+// column: each of the NT threads (one wave, or a whole workgroup of NT)
+// sums a stride-NT share, and the group reduction gives every thread the
+// totals, so the scalar updates run uniformly on all of them.  `lane` is the
+// thread's index in the group.
 // Used by the wave-per-column prox kernels and the SDCA epoch.
 #ifndef SDCA_HIP_PROX_LAMBERT_WAVE_HPP
 #define SDCA_HIP_PROX_LAMBERT_WAVE_HPP
@@ -26,31 +28,31 @@ namespace sdca_gpu {
 // (sum_lambert_w_exp, lambert.h:220-237).
 // wout (optional, the wave's LDS array of R): each pass leaves its W values
 // there, for the output map.
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ inline R lw_sum0(const D* s, int m, int p, int lane, R ta, R tb) {
   R a0(0);
-  for (int i = lane; i < m; i += 64) a0 += lambert_w_exp(static_cast<R>(s[i]) + (i < p ? ta : tb));
-  return group_sum<64>(a0);
+  for (int i = lane; i < m; i += NT) a0 += lambert_w_exp(static_cast<R>(s[i]) + (i < p ? ta : tb));
+  return group_sum<NT>(a0);
 }
 
 // f0 = sum_i W(e^(s_i + t)), f1 = sum_i W / (1 + W) (lambert.h:253-271).
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1,
                                 R* wout = nullptr) {
   R a0(0), a1(0);
-  for (int i = lane; i < m; i += 64) {
+  for (int i = lane; i < m; i += NT) {
     const R v = lambert_w_exp(static_cast<R>(s[i]) + t);
     if (wout) wout[i] = v;
     a0 += v;
     a1 += div_near(v, R(1) + v);
   }
-  f0 = group_sum<64>(a0);
-  f1 = group_sum<64>(a1);
+  f0 = group_sum<NT>(a0);
+  f1 = group_sum<NT>(a1);
 }
 
 // f0..f3: W and its first three derivatives in t (lambert.h:308-332), with
 // the shift ta for entries below p and tb beyond.
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, R& f2, R& f3,
                                 int p = -1, R tb = R(0), R* wout = nullptr) {
   if (p < 0) {
@@ -58,7 +60,7 @@ __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, 
     tb = t;
   }
   R a0(0), a1(0), a2(0), a3(0);
-  for (int i = lane; i < m; i += 64) {
+  for (int i = lane; i < m; i += NT) {
     const R v = lambert_w_exp(static_cast<R>(s[i]) + (i < p ? t : tb));
     if (wout) wout[i] = v;
     const R d = R(1) + v;
@@ -68,27 +70,27 @@ __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, 
     a2 += div_near(v, d3);
     a3 += div_near(v * (R(1) - R(2) * v), d3 * d * d);
   }
-  f0 = group_sum<64>(a0);
-  f1 = group_sum<64>(a1);
-  f2 = group_sum<64>(a2);
-  f3 = group_sum<64>(a3);
+  f0 = group_sum<NT>(a0);
+  f1 = group_sum<NT>(a1);
+  f2 = group_sum<NT>(a2);
+  f3 = group_sum<NT>(a3);
 }
 
 // Largest entry of the LDS column and the lowest index holding it (an index
 // below m for m >= 1, also when every entry is -inf).
-template <class D>
+template <class D, int NT = 64>
 __device__ inline void wave_argmax(const D* s, int m, int lane, D& mx, int& idx) {
   D best = -num<D>::inf();
   int at = m;
-  for (int i = lane; i < m; i += 64) {
+  for (int i = lane; i < m; i += NT) {
     const D v = s[i];
     if (v > best || at == m) {
       best = v;
       at = i;
     }
   }
-  mx = group_max<64>(best);
-  idx = group_min<64>(best == mx ? at : m);
+  mx = group_max<NT>(best);
+  idx = group_min<NT>(best == mx ? at : m);
 }
 
 template <class R>
@@ -108,11 +110,11 @@ __device__ inline R log_w_inverse_or_min(R w) {
 // ds_out (if given) receives the first two t-derivatives of that s with
 // the sign of a step down in t: sum_i W / (1 + W) / alpha and
 // sum_i W / (1 + W)^3 / alpha.
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, R& lo, R& hi,
                                     R* s_out, R* wout = nullptr, R* ds_out = nullptr) {
   R f0, f1, f2, f3;
-  lw_sums4(s, m, lane, -t, f0, f1, f2, f3, -1, R(0), wout);
+  lw_sums4<D, R, NT>(s, m, lane, -t, f0, f1, f2, f3, -1, R(0), wout);
   if (s_out) *s_out = f0 / alpha;
   if (ds_out) {
     ds_out[0] = f1 / alpha;
@@ -152,13 +154,13 @@ __device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, 
 // t_lse = log sum exp(x) - log(rhs), within about e^(max - t_lse) of it when
 // every value sits below t_lse (small W, W(e^y) ~ e^y).  Single precision:
 // a start for the iterations, which end on the root whatever their start.
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ inline bool lse_start(const D* s, int m, int p, R c, R e, R mx, R rhs, int lane,
                                  R& t_lse) {
   float se = (e > -num<R>::inf()) ? expf(static_cast<float>(e - mx)) : 0.0f;
-  for (int i = lane; i < m; i += 64)
+  for (int i = lane; i < m; i += NT)
     se += expf(static_cast<float>(static_cast<R>(s[i]) - (i < p ? R(0) : c) - mx));
-  se = group_sum<64>(se);
+  se = group_sum<NT>(se);
   t_lse = mx + static_cast<R>(logf(se)) - dlog(rhs);
   return mx - t_lse <= R(-1);
 }
@@ -166,14 +168,14 @@ __device__ inline bool lse_start(const D* s, int m, int p, R c, R e, R mx, R rhs
 // Thresholds (t, 0, hi) of one column whose copy is in s[0, m); entries of U
 // are overwritten with -inf.  With wl (the wave's LDS array of R), the last
 // pass's W values are left there and *tw receives the t they were taken at.
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_out,
                                    R& hi_out, R* wl = nullptr, R* tw = nullptr) {
   const R eps_r = num<R>::eps();
   const R tiny = R(64) * num<R>::min_normal();
   D mx_d;
   int mx_i;
-  wave_argmax(s, m, lane, mx_d, mx_i);
+  wave_argmax<D, NT>(s, m, lane, mx_d, mx_i);
   R max = static_cast<R>(mx_d);
   const R eps = R(16) * eps_r * (max > R(1) ? max : R(1));
 
@@ -202,7 +204,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
   {
     R t_lse;
     const R top = (alpha > max) ? alpha : max;
-    if (lse_start<D, R>(s, m, m, R(0), alpha, top, alpha, lane, t_lse) && t_lse > br_lo &&
+    if (lse_start<D, R, NT>(s, m, m, R(0), alpha, top, alpha, lane, t_lse) && t_lse > br_lo &&
         t_lse < br_hi)
       t = t_lse;
   }
@@ -220,7 +222,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     bool settled = false;
     for (int iter = 0; iter < 16 && !settled; ++iter) {
       const float t1 = tf;
-      bool ok = guarded_step<D, float>(s, m, lane, alpha_f, tf, lo_f, hi_f, nullptr);
+      bool ok = guarded_step<D, float, NT>(s, m, lane, alpha_f, tf, lo_f, hi_f, nullptr);
       settled = ok && fabsf(t1 - tf) <= 3.0e-3f * fmaxf(1.0f, fabsf(tf));
     }
     if (settled) t = static_cast<R>(tf);
@@ -230,7 +232,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     const R t1 = t;
     if (tw) *tw = t;
     R ds[2];
-    const bool ok = guarded_step<D, R>(s, m, lane, alpha, t, br_lo, br_hi, &sv, wl, ds);
+    const bool ok = guarded_step<D, R, NT>(s, m, lane, alpha, t, br_lo, br_hi, &sv, wl, ds);
     if (fabs(t1 - t) <= eps_r) break;
     // From a settled single-precision start a first step of at most 1e-6
     // leaves an order-4 correction of ~1e-24: the confirming pass is
@@ -257,12 +259,12 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
 
   // U not empty (topk_entropy_biased.h:224-266).
   if (lane == 0) s[mx_i] = -num<D>::inf();
-  wave_lds_sync();
+  group_lds_sync<NT>();
   const R log_k = dlog(K), log_alpha = dlog(alpha);
   R min_u(max), sum_u(max);
   int num_u = 1;
   for (int remaining = m - 1; remaining > 0;) {
-    wave_argmax(s, m, lane, mx_d, mx_i);
+    wave_argmax<D, NT>(s, m, lane, mx_d, mx_i);
     max = static_cast<R>(mx_d);
     sv = R(0.999);
     t = max;
@@ -277,7 +279,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
         sv = (sv < R(0)) ? R(0) : ((sv > R(1)) ? R(1) : sv);
         R S0, S1;
         if (tw) *tw = t;
-        lw_sums2(s, m, lane, -t, S0, S1, wl);
+        lw_sums2<D, R, NT>(s, m, lane, -t, S0, S1, wl);
         const R E = S0 + t * S1;
         R z, Az, Bz;
         if (sv < R(0.5)) {
@@ -304,7 +306,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     min_u = max;
     sum_u += max;
     if (lane == 0) s[mx_i] = -num<D>::inf();
-    wave_lds_sync();
+    group_lds_sync<NT>();
     --remaining;
   }
   t_out = t;
@@ -313,11 +315,11 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
 
 // One order-4 Householder step on the two-block sum (two_entropy.h:15-38);
 // returns f(t) at the old t.
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ inline R two_w_step4(const D* s, int m, int p, int lane, R alpha, R c, R& t,
                                 R* wout = nullptr) {
   R f0, f1, f2, f3;
-  lw_sums4(s, m, lane, -t, f0, f1, f2, f3, p, -t - c, wout);
+  lw_sums4<D, R, NT>(s, m, lane, -t, f0, f1, f2, f3, p, -t - c, wout);
   f0 -= alpha;
   const R f02 = f0 * f2, f11 = f1 * f1;
   const R den = R(6) * f1 * (f02 - f11) - f0 * (f0 * f3);
@@ -338,13 +340,13 @@ __device__ inline int bisection_count(R v) {
 
 // Thresholds t (block a) and t + c (block b) of one column in s[0, m), split p.
 // With wl, the last pass's W values are left there and *tw receives its t.
-template <class D, class R>
+template <class D, class R, int NT = 64>
 __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R& t_out,
                                   R& c_out, R* wl = nullptr, R* tw = nullptr) {
   const R eps = num<R>::eps();
   const R num_a = static_cast<R>(p), num_b = static_cast<R>(m - p);
   R max_a = -num<R>::inf(), max_b = -num<R>::inf(), sum_a = 0, sum_b = 0;
-  for (int i = lane; i < m; i += 64) {
+  for (int i = lane; i < m; i += NT) {
     const R x = static_cast<R>(s[i]);
     if (i < p) {
       max_a = (x > max_a) ? x : max_a;
@@ -354,10 +356,10 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
       sum_b += x;
     }
   }
-  max_a = group_max<64>(max_a);
-  max_b = group_max<64>(max_b);
-  sum_a = group_sum<64>(sum_a);
-  sum_b = group_sum<64>(sum_b);
+  max_a = group_max<NT>(max_a);
+  max_b = group_max<NT>(max_b);
+  sum_a = group_sum<NT>(sum_a);
+  sum_b = group_sum<NT>(sum_b);
   const R c = alpha / num_a;
   const R max = (max_a > max_b - c) ? max_a : max_b - c;
   // Bracket guards (two_entropy.h:159-163).
@@ -370,16 +372,16 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
   // start there (two or three passes on U(-10, 10) columns instead of the
   // reference's two guesses and its bisection); they end on the same root.
   R t_lse;
-  if (lse_start<D, R>(s, m, p, c, -num<R>::inf(), max, alpha, lane, t_lse)) {
+  if (lse_start<D, R, NT>(s, m, p, c, -num<R>::inf(), max, alpha, lane, t_lse)) {
     t = t_lse;
   } else {
     // Two guesses, each followed by one step (:165-175).
     R t01 = max - dlog(alpha);
     t1 = t01;
-    f1 = two_w_step4(s, m, p, lane, alpha, c, t1);
+    f1 = two_w_step4<D, R, NT>(s, m, p, lane, alpha, c, t1);
     R t02 = (sum_a + sum_b - num_b * c - alpha) / (num_a + num_b);
     R t2 = t02;
-    R f2 = two_w_step4(s, m, p, lane, alpha, c, t2);
+    R f2 = two_w_step4<D, R, NT>(s, m, p, lane, alpha, c, t2);
     if (f1 > f2) {
       R x = t01; t01 = t02; t02 = x;
       x = t1; t1 = t2; t2 = x;
@@ -404,7 +406,7 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
       const int num_iter = bisection_count(dlog(ub - lb) * static_cast<R>(1.4426950408889634));
       for (int iter = 0; iter < num_iter; ++iter) {
         t = (lb + ub) / R(2);
-        const R fv = lw_sum0(s, m, p, lane, -t, -t - c) - alpha;
+        const R fv = lw_sum0<D, R, NT>(s, m, p, lane, -t, -t - c) - alpha;
         if (eps < fv && fv < lf) {
           lf = fv;
           lb = t;
@@ -422,7 +424,7 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
   for (int iter = 0; iter < 32; ++iter) {
     t1 = t;
     if (tw) *tw = t;
-    f1 = two_w_step4(s, m, p, lane, alpha, c, t, wl);
+    f1 = two_w_step4<D, R, NT>(s, m, p, lane, alpha, c, t, wl);
     if (R(0) <= f1 && f1 < lf) {
       lb = t1;
       lf = f1;

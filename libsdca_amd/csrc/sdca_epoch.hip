@@ -35,6 +35,9 @@ namespace sdca_gpu {
 namespace {
 
 constexpr int kEpochThreads = 256;
+// LDS of the block kernel (gfx950: 160 KiB per workgroup), less the static
+// arrays.
+constexpr size_t kEpochLdsBytes = 150 * 1024;
 constexpr int kRankJ = 8;  // classes per workgroup of the rank-B update
 
 struct EpochObj {
@@ -42,6 +45,13 @@ struct EpochObj {
   int k;
   double c, gamma;
 };
+
+// Words of the thresholds' column in LDS: m values, or G C for the register
+// form, whose LDS scratch is the slot layout of the whole workgroup.
+__host__ __device__ inline int epoch_column_words(int m, int C) {
+  const int w = kEpochThreads * C > m ? kEpochThreads * C : m;
+  return (w + 3) & ~3;
+}
 
 // ||x_i||^2 in the data type (scratch.h:37-40), one wave per example.
 template <class D>
@@ -75,19 +85,30 @@ gather_kernel(const D* __restrict__ X, const int64_t* __restrict__ order, int64_
   for (int64_t l = threadIdx.x; l < d; l += 256) dst[l] = src[l];
 }
 
-// The block's examples in order (one workgroup).  S: nb x m scores at W_B,
-// G: nb x nb Gram matrix (leading dimension nb), Delta: nb x m.
-template <class D, class R>
+// The block's examples in order (one workgroup of G threads, all of which
+// run every step, including the thresholds).  S: nb x m scores at W_B: after
+// example k, row k' > k loses G_{kk'} delta_k (each thread owns the same
+// classes j in every row, so the rows it reads are the ones it wrote); the
+// rows live in LDS when s_lds (copied in first), else in S itself.
+// Gm: nb x nb Gram matrix, Delta: nb x m.  C, KM: the register form of the
+// simplex / knapsack thresholds for m - 1 <= G C values (C = 0: the
+// sorted-column form only) and k <= KM.
+template <class D, class R, int C, int KM>
 __global__ void __launch_bounds__(kEpochThreads)
-epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm, const int64_t* __restrict__ idx,
+epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* __restrict__ idx,
                    int nb, const D* __restrict__ norms, const int64_t* __restrict__ labels,
-                   D* __restrict__ A, D* __restrict__ Delta, EpochObj ob, int m,
+                   D* __restrict__ A, D* __restrict__ Delta, EpochObj ob, int m, int s_lds,
                    int* __restrict__ bad) {
   constexpr int G = kEpochThreads;
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int cw = epoch_column_words(m, C);
   D* const v = reinterpret_cast<D*>(smem_raw);  // the example's vector, m values
-  D* const cb = v + ((m + 3) & ~3);             // the column the thresholds read
+  D* const cb = v + ((m + 3) & ~3);             // the column the thresholds read (cw words)
+  D* const dummy = cb + cw;                     // G per-thread dummy words
+  D* const Sx = s_lds ? dummy + G : S;          // the block's running scores
   __shared__ R sh_t, sh_lo, sh_hi;
+  __shared__ int sh_slow;
+  __shared__ D g_row[kEpochBlock];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   const int kind = ob.kind;
@@ -95,14 +116,20 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm, const int6
   const bool hinge = kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH;
   const bool smooth = kind == SDCA_OBJ_HINGE_TOPK_SMOOTH || kind == SDCA_OBJ_TOPK_HINGE_SMOOTH;
   const bool simplex = kind == SDCA_OBJ_HINGE_TOPK || kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
+  const int op = simplex ? OP_TOPK_SIMPLEX_BIASED : OP_KNAPSACK_LE_BIASED;
+  const R knap_hi = simplex ? R(0) : c / static_cast<R>(ob.k);
+  if (s_lds) {
+    for (int64_t e = tid; e < static_cast<int64_t>(nb) * m; e += G) Sx[e] = S[e];
+    __syncthreads();
+  }
   for (int k = 0; k < nb; ++k) {
     const int64_t i = idx[k];
     const D norm2 = norms[i];
     D* const arow = A + i * m;
     D* const drow = Delta + static_cast<int64_t>(k) * m;
+    const D* const srow = Sx + static_cast<int64_t>(k) * m;
     if (!(norm2 > D(0))) {  // update.h:62: the example changes nothing
       for (int j = tid; j < m; j += G) drow[j] = D(0);
-      __syncthreads();
       continue;
     }
     int64_t yl = labels[i];
@@ -119,11 +146,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm, const int6
       pa = smooth ? static_cast<D>(rho) / norm2 : D(1) / norm2;
       pb = smooth ? -static_cast<D>(rho) : D(-1);
     }
-    for (int j = tid; j < m; j += G) {
-      D s = S[static_cast<int64_t>(k) * m + j];
-      for (int q = 0; q < k; ++q) s -= Gm[q * nb + k] * Delta[static_cast<int64_t>(q) * m + j];
-      v[j] = pa * s + pb * arow[j];
-    }
+    for (int j = tid; j < m; j += G) v[j] = pa * srow[j] + pb * arow[j];
     __syncthreads();
     const D vy = v[y];
     if (kind == SDCA_OBJ_ENTROPY) {
@@ -131,17 +154,10 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm, const int6
       for (int j = tid; j < m; j += G) cb[j == y ? 0 : (j < y ? j + 1 : j)] = v[j];
       __syncthreads();
       const R alpha = c * static_cast<R>(norm2);
-      if (tid < 64) {
-        R t, c2;
-        twoent_thresholds<D, R>(cb, m, 1, lane, alpha, t, c2);
-        if (lane == 0) {
-          sh_t = t;
-          sh_lo = t + c2;
-        }
-      }
-      __syncthreads();
+      R t, c2;
+      twoent_thresholds<D, R, G>(cb, m, 1, tid, alpha, t, c2);
       const D map_a = D(1) / static_cast<D>(alpha);
-      const D ta = static_cast<D>(sh_t), tb = static_cast<D>(sh_lo);
+      const D ta = static_cast<D>(t), tb = static_cast<D>(t + c2);
       const D na = static_cast<D>(-c), nbias = static_cast<D>(c / R(1));
       for (int j = tid; j < m; j += G) {
         const D x = clamp_ref(map_a * lambert_w_exp(v[j] - (j == y ? ta : tb)), D(0), D(1));
@@ -161,22 +177,57 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm, const int6
       __syncthreads();
       const int mp = m - 1;
       if (hinge) {
-        sort_desc_unpadded(cb, mp);
-        if (tid < 64) {
-          R t, lo, hi;
-          thresholds_sorted<D, R>(cb, mp, simplex ? OP_TOPK_SIMPLEX_BIASED : OP_KNAPSACK_LE_BIASED,
-                                  R(0), simplex ? R(0) : c / static_cast<R>(ob.k), c, rho, ob.k, t,
-                                  lo, hi);
-          if (lane == 0) {
-            sh_t = t;
-            sh_lo = lo;
-            sh_hi = hi;
+        bool sorted_form = true;
+        if constexpr (C > 0) {
+          // The register form over the whole workgroup (slot c of thread g
+          // = entry g + G c), which defers to the sorted form only where the
+          // reference's biased cone search is needed
+          // (topk_simplex_biased.h:57-66).
+          D vr[C];
+          const int nvalid = (mp - tid + G - 1) / G;
+#pragma unroll
+          for (int q = 0; q < C; ++q) vr[q] = (q < nvalid) ? cb[tid + G * q] : -num<D>::inf();
+          ProxParamsT<R> pp;
+          pp.lo = R(0);
+          pp.hi = knap_hi;
+          pp.rhs = c;
+          pp.rho = rho;
+          pp.k = ob.k;
+          pp.op = op;
+          pp.p = 0;
+          const ColThr<R> th = simplex
+              ? topk_family<G, C, KM, D, R>(vr, mp, nvalid, pp, cb, dummy + tid)
+              : knap_family<G, C, D, R>(vr, mp, nvalid, pp);
+          if (tid == 0) {
+            sh_slow = th.slow ? 1 : 0;
+            sh_t = th.t;
+            sh_lo = th.lo;
+            sh_hi = th.hi;
+          }
+          __syncthreads();
+          sorted_form = sh_slow != 0;
+          if (sorted_form) {  // cb served as scratch: compact it again
+            for (int j = tid; j < m; j += G)
+              if (j != y) cb[j < y ? j : j - 1] = v[j];
+            __syncthreads();
           }
         }
-      } else if (tid < 64) {  // prox_topk_entropy_biased, alpha = c norm2
+        if (sorted_form) {
+          sort_desc_unpadded(cb, mp);
+          if (tid < 64) {
+            R t, lo, hi;
+            thresholds_sorted<D, R>(cb, mp, op, R(0), knap_hi, c, rho, ob.k, t, lo, hi);
+            if (lane == 0) {
+              sh_t = t;
+              sh_lo = lo;
+              sh_hi = hi;
+            }
+          }
+        }
+      } else {  // prox_topk_entropy_biased, alpha = c norm2
         R t, hi;
-        entbias_thresholds<D, R>(cb, mp, lane, ob.k, c * static_cast<R>(norm2), t, hi);
-        if (lane == 0) {
+        entbias_thresholds<D, R, G>(cb, mp, tid, ob.k, c * static_cast<R>(norm2), t, hi);
+        if (tid == 0) {
           sh_t = t;
           sh_lo = R(0);
           sh_hi = hi;
@@ -215,11 +266,98 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm, const int6
       arow[j] = an;
       part += fabs(dl);
     }
-    const D asum = group_sum<G>(part);
-    if (!(asum > num<D>::eps()))
+    const D asum = group_sum<G>(part);  // also orders v's last reads before the next writes
+    if (asum > num<D>::eps() && k + 1 < nb) {
+      // The later rows of the block see this update: S_k' -= G_kk' delta_k.
+      if (tid < nb) g_row[tid] = Gm[k * nb + tid];
+      __syncthreads();
+      for (int j = tid; j < m; j += G) {
+        const D dl = drow[j];
+        for (int q = k + 1; q < nb; ++q) Sx[static_cast<int64_t>(q) * m + j] -= g_row[q] * dl;
+      }
+    } else if (!(asum > num<D>::eps())) {
       for (int j = tid; j < m; j += G) drow[j] = D(0);
-    __syncthreads();  // a_i and delta_k before the next example reads them
+    }
+    __syncthreads();
   }
+}
+
+// The block's skinny products P = X_B Y' (nb <= kEpochBlock rows; Y: M x d,
+// the primal variables or X_B itself), split over the features: workgroup
+// (bx, ks) has four waves of JW classes each over features
+// [ks kc, (ks + 1) kc), lane l taking features l, l + 64, ...; the partial
+// sums of the splits are added in split order by skinny_sum_kernel.
+template <class D, int JW>
+__global__ void __launch_bounds__(256)
+skinny_partial_kernel(const D* __restrict__ XB, const D* __restrict__ Y, D* __restrict__ P,
+                      int nb, int64_t M, int64_t d, int64_t kc) {
+  const int wave = static_cast<int>(threadIdx.x) >> 6, lane = static_cast<int>(threadIdx.x) & 63;
+  const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * JW;
+  const int64_t l0 = static_cast<int64_t>(blockIdx.y) * kc;
+  const int64_t l1 = (l0 + kc < d) ? l0 + kc : d;
+  D acc[JW][kEpochBlock];
+#pragma unroll
+  for (int jw = 0; jw < JW; ++jw)
+#pragma unroll
+    for (int e = 0; e < kEpochBlock; ++e) acc[jw][e] = D(0);
+  for (int64_t l = l0 + lane; l < l1; l += 64) {
+    D y[JW];
+#pragma unroll
+    for (int jw = 0; jw < JW; ++jw) y[jw] = (j0 + jw < M) ? Y[(j0 + jw) * d + l] : D(0);
+#pragma unroll
+    for (int e = 0; e < kEpochBlock; ++e) {
+      if (e < nb) {
+        const D x = XB[static_cast<int64_t>(e) * d + l];
+#pragma unroll
+        for (int jw = 0; jw < JW; ++jw) acc[jw][e] += x * y[jw];
+      }
+    }
+  }
+  D* const out = P + static_cast<int64_t>(blockIdx.y) * kEpochBlock * M;
+#pragma unroll
+  for (int jw = 0; jw < JW; ++jw) {
+#pragma unroll
+    for (int e = 0; e < kEpochBlock; ++e) {
+      const D s = group_sum<64>(acc[jw][e]);
+      if (lane == 0 && e < nb && j0 + jw < M) out[static_cast<int64_t>(e) * M + j0 + jw] = s;
+    }
+  }
+}
+
+template <class D>
+__global__ void __launch_bounds__(256)
+skinny_sum_kernel(const D* __restrict__ P, D* __restrict__ out, int nb, int64_t M, int ksplit) {
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (o >= static_cast<int64_t>(nb) * M) return;
+  const int64_t e = o / M, j = o % M;
+  D s = P[e * M + j];
+  for (int ks = 1; ks < ksplit; ++ks) s += P[(static_cast<int64_t>(ks) * kEpochBlock + e) * M + j];
+  out[o] = s;
+}
+
+// Feature split of the skinny products: chunks of at least 512 features, at
+// most kSkinnySplits of them.
+constexpr int kSkinnySplits = 8;
+inline int64_t skinny_chunk(int64_t d) {
+  const int64_t c = (d + kSkinnySplits - 1) / kSkinnySplits;
+  return c < 512 ? 512 : c;
+}
+
+template <class D>
+hipError_t launch_skinny(const D* XB, const D* Y, D* out, D* P, int nb, int64_t M, int64_t d,
+                         hipStream_t stream) {
+  constexpr int JW = sizeof(D) == 4 ? 4 : 2;
+  const int64_t kc = skinny_chunk(d);
+  const int ksplit = static_cast<int>((d + kc - 1) / kc);
+  const dim3 grid(static_cast<unsigned>((M + 4 * JW - 1) / (4 * JW)), static_cast<unsigned>(ksplit));
+  hipLaunchKernelGGL((skinny_partial_kernel<D, JW>), grid, dim3(256), 0, stream, XB, Y, P, nb, M,
+                     d, kc);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t total = static_cast<int64_t>(nb) * M;
+  hipLaunchKernelGGL((skinny_sum_kernel<D>), dim3(static_cast<unsigned>((total + 255) / 256)),
+                     dim3(256), 0, stream, P, out, nb, M, ksplit);
+  return hipGetLastError();
 }
 
 // W -= delta_B' X_B: each element takes the block's rank-1 updates in order,
@@ -254,6 +392,43 @@ rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __re
   }
 }
 
+template <class D, class R, int C, int KM>
+hipError_t launch_block(D* S, const D* Gm, const int64_t* idx, int nb, const D* norms,
+                        const EpochLaunch& a, D* Delta, const EpochObj& ob, int* bad) {
+  const int m = static_cast<int>(a.m);
+  size_t lds = (static_cast<size_t>((m + 3) & ~3) + epoch_column_words(m, C) + kEpochThreads) *
+               sizeof(D);
+  // The block's scores in LDS where they fit (the running update then costs
+  // LDS instead of global round trips).
+  const size_t s_bytes = static_cast<size_t>(nb) * static_cast<size_t>(m) * sizeof(D);
+  const int s_lds = lds + s_bytes <= kEpochLdsBytes ? 1 : 0;
+  if (s_lds) lds += s_bytes;
+  hipLaunchKernelGGL((epoch_block_kernel<D, R, C, KM>), dim3(1), dim3(kEpochThreads), lds,
+                     a.stream, S, Gm, idx, nb, norms, a.labels, static_cast<D*>(a.A), Delta, ob,
+                     m, s_lds, bad);
+  return hipGetLastError();
+}
+
+// The block kernel's register form for m - 1 values and k (C = 0: the
+// sorted-column form only).
+template <class D, class R>
+hipError_t launch_block_for(D* S, const D* Gm, const int64_t* idx, int nb, const D* norms,
+                            const EpochLaunch& a, D* Delta, const EpochObj& ob, int* bad) {
+  const int64_t mp = a.m - 1;
+  const bool simplex = a.kind == SDCA_OBJ_HINGE_TOPK || a.kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
+  const bool big_k = simplex && a.k > 8;
+  if (mp > 2048 || big_k || a.kind > SDCA_OBJ_TOPK_HINGE_SMOOTH)
+    return launch_block<D, R, 0, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+  if (!simplex || a.k <= 5) {
+    if (mp <= 256) return launch_block<D, R, 1, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+    if (mp <= 1024) return launch_block<D, R, 4, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+    return launch_block<D, R, 8, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+  }
+  if (mp <= 256) return launch_block<D, R, 1, 8>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+  if (mp <= 1024) return launch_block<D, R, 4, 8>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+  return launch_block<D, R, 8, 8>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+}
+
 template <class D, class R>
 hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   const int64_t d = a.d, m = a.m, n = a.n;
@@ -268,13 +443,13 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   D* S = XB + B * d;
   D* Gm = S + B * m;
   D* Delta = Gm + B * B;
-  D* norms_ws = Delta + B * m;
+  D* P = Delta + B * m;  // the skinny products' partial sums
+  D* norms_ws = P + kSkinnySplits * B * (m > B ? m : B);
   *flag_dev = bad;
   hipError_t e = launch_clear(bad, 1, a.stream);
   if (e != hipSuccess) return e;
   const D* X = static_cast<const D*>(a.X);
   D* W = static_cast<D*>(a.W);
-  D* A = static_cast<D*>(a.A);
   const D* norms = static_cast<const D*>(a.norms);
   if (!norms) {
     hipLaunchKernelGGL((norms_kernel<D>), dim3(static_cast<unsigned>((n + 3) / 4)), dim3(256), 0,
@@ -287,7 +462,6 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   ob.k = a.k;
   ob.c = a.c;
   ob.gamma = a.gamma;
-  const size_t lds = 2 * static_cast<size_t>((m + 3) & ~int64_t(3)) * sizeof(D);
   const dim3 rank_grid(static_cast<unsigned>((d + 255) / 256),
                        static_cast<unsigned>((m + kRankJ - 1) / kRankJ));
   for (int64_t q0 = 0; q0 < a.count; q0 += B) {
@@ -295,16 +469,10 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
     hipLaunchKernelGGL((gather_kernel<D>), dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream,
                        X, a.order, q0, n, d, XB, idx, bad);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if constexpr (sizeof(D) == 4) {
-      if ((e = launch_scores_gemm(XB, W, S, nb, m, d, a.stream)) != hipSuccess) return e;
-      if ((e = launch_scores_gemm(XB, XB, Gm, nb, nb, d, a.stream)) != hipSuccess) return e;
-    } else {
-      if ((e = launch_scores_gemm_f64(XB, W, S, nb, m, d, a.stream)) != hipSuccess) return e;
-      if ((e = launch_scores_gemm_f64(XB, XB, Gm, nb, nb, d, a.stream)) != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL((epoch_block_kernel<D, R>), dim3(1), dim3(kEpochThreads), lds, a.stream, S,
-                       Gm, idx, nb, norms, a.labels, A, Delta, ob, static_cast<int>(m), bad);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = launch_skinny<D>(XB, W, S, P, nb, m, d, a.stream)) != hipSuccess) return e;
+    if ((e = launch_skinny<D>(XB, XB, Gm, P, nb, nb, d, a.stream)) != hipSuccess) return e;
+    if ((e = launch_block_for<D, R>(S, Gm, idx, nb, norms, a, Delta, ob, bad)) != hipSuccess)
+      return e;
     hipLaunchKernelGGL((rank_update_kernel<D>), rank_grid, dim3(256), 0, a.stream, W, Delta, XB,
                        nb, m, d);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -317,9 +485,10 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
 size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool norms_given) {
   const size_t es = data == SDCA_F32 ? 4 : 8;
   const size_t B = kEpochBlock;
+  const size_t mb = static_cast<size_t>(m) > B ? static_cast<size_t>(m) : B;
   return 256 + B * sizeof(int64_t) +
          es * (B * static_cast<size_t>(d) + 2 * B * static_cast<size_t>(m) + B * B +
-               (norms_given ? 0 : static_cast<size_t>(n)));
+               kSkinnySplits * B * mb + (norms_given ? 0 : static_cast<size_t>(n)));
 }
 
 int64_t epoch_max_m(int data) {
