@@ -240,9 +240,11 @@ __device__ inline double lambert_w_exp_mixed(double x) {
 __device__ inline float lambert_w_exp_mixed(float x) { return lambert_w_exp(x); }
 
 // ---------------------------------------------------------------------------
-// Cross-lane exchange lane <-> lane ^ OFF inside a wave: DPP quad
-// permutations for OFF = 1, 2 (a VALU operand modifier, no LDS traffic),
-// ds_swizzle in xor mode for OFF = 4, 8, 16, ds_bpermute for 32.
+// Cross-lane exchange lane <-> lane ^ OFF inside a wave, all by VALU
+// operations (no LDS traffic): DPP quad permutations for OFF = 1, 2; DPP row
+// shifts by 4 (left for lanes with bit 2 clear, right for the others) for 4;
+// DPP row rotation by 8 for 8; v_permlane16_swap / v_permlane32_swap for 16
+// and 32.
 // ---------------------------------------------------------------------------
 template <int OFF>
 __device__ inline int xor_lane(int v) {
@@ -250,10 +252,26 @@ __device__ inline int xor_lane(int v) {
     return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
   } else if constexpr (OFF == 2) {
     return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-  } else if constexpr (OFF < 32) {
-    return __builtin_amdgcn_ds_swizzle(v, (OFF << 10) | 0x1F);  // and 0x1F, xor OFF
+  } else if constexpr (OFF == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, false);  // row_shl:4
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    return (__lane_id() & 4) ? dn : up;
+  } else if constexpr (OFF == 8) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
   } else {
-    return __shfl_xor(v, OFF, 64);
+    // The swap with both operands v leaves rows (r0, r0, r2, r2) in the
+    // first result and (r1, r1, r3, r3) in the second (16-lane rows; for
+    // the 32-lane swap, halves (h0, h0) and (h1, h1)).
+    static_assert(OFF == 16 || OFF == 32, "partner levels 1..32");
+    const unsigned u = static_cast<unsigned>(v);
+    const bool upper = (__lane_id() & OFF) != 0;
+    if constexpr (OFF == 16) {
+      const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      return static_cast<int>(upper ? p[0] : p[1]);
+    } else {
+      const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      return static_cast<int>(upper ? p[0] : p[1]);
+    }
   }
 }
 template <int OFF>
@@ -332,6 +350,47 @@ __device__ inline T group_sum(T x) {
   if constexpr (G >= 2) x += xor_lane<1>(x);
   return x;
 }
+// Several group sums in one exchange: each value reduced as group_sum<G>
+// would, the workgroup-wide ones through one pair of barriers for all of
+// them (the same wave-order sums, so the same bits as separate calls).
+template <class T>
+__device__ inline void slot_put(unsigned long long& slot, T x) {
+  static_assert(sizeof(T) <= sizeof(unsigned long long), "8-byte slots");
+  __builtin_memcpy(&slot, &x, sizeof(T));
+}
+template <class T>
+__device__ inline T slot_get(const unsigned long long& slot) {
+  T x;
+  __builtin_memcpy(&x, &slot, sizeof(T));
+  return x;
+}
+template <int G, class T>
+__device__ inline T slot_sum(const unsigned long long (*slots)[8], int i) {
+  T r = slot_get<T>(slots[0][i]);
+#pragma unroll
+  for (int w = 1; w < G / 64; ++w) r = r + slot_get<T>(slots[w][i]);
+  return r;
+}
+template <int G, class... T>
+__device__ inline void group_sums(T&... x) {
+  static_assert(sizeof...(T) <= 8, "at most 8 values per exchange");
+  if constexpr (G > 64) {
+    __shared__ unsigned long long slots[kMaxGroupWaves][8];
+    ((x = group_sum<64>(x)), ...);
+    __syncthreads();  // the previous exchange's readers are done with the slots
+    if ((threadIdx.x & 63) == 0) {
+      const int w = static_cast<int>(threadIdx.x) >> 6;
+      int i = 0;
+      ((slot_put(slots[w][i++], x)), ...);
+    }
+    __syncthreads();
+    int i = 0;
+    ((x = slot_sum<G, T>(slots, i++)), ...);
+  } else {
+    ((x = group_sum<G>(x)), ...);
+  }
+}
+
 template <int OFF, class T>
 __device__ inline T max_step(T x) {
   T y = xor_lane<OFF>(x);
@@ -385,6 +444,19 @@ __device__ inline int group_exclusive_scan(int x, int g) {
     return base + ex;
   }
   int incl = x;
+  if constexpr (G >= 16) {
+    // Inclusive scan of each 16-lane row by DPP row shifts (a lane whose
+    // source lies before its row reads 0), then the row totals carried by
+    // row_bcast:15 (into rows 1 and 3) and, for 64 lanes, row_bcast:31
+    // (into rows 2 and 3).
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);  // row_shr:1
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
+    if constexpr (G >= 32) incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);
+    if constexpr (G >= 64) incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xC, 0xF, false);
+    return incl - x;
+  }
   const int lane = static_cast<int>(threadIdx.x) & 63;
   if constexpr (G >= 2) { int y = xor_lane<1>(incl); if (g & 1) incl += y; }
   // After step s every lane holds the inclusive sum of its aligned block of

@@ -163,9 +163,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
       s_hi += hi_c ? wc : R(0);
       n_lh += (lo_c ? 1 : 0) + (hi_c ? 0x10000 : 0);
     }
-    s_lo = group_sum<G>(s_lo);
-    s_hi = group_sum<G>(s_hi);
-    n_lh = group_sum<G>(n_lh);
+    group_sums<G>(s_lo, s_hi, n_lh);
     const int n_lo = n_lh & 0xffff, n_hi = n_lh >> 16;
     const R sh = static_cast<R>(n_hi) * hi;
     const R sl = static_cast<R>(n_lo) * lo;
@@ -271,9 +269,7 @@ __device__ inline R knapsack_biased_regs(const D (&v)[C], int m, R total, R lo, 
       s_hi += hi_c ? w[c] : R(0);
       n_lh += (lo_c ? 1 : 0) + (hi_c ? 0x10000 : 0);
     }
-    s_lo = group_sum<G>(s_lo);
-    s_hi = group_sum<G>(s_hi);
-    n_lh = group_sum<G>(n_lh);
+    group_sums<G>(s_lo, s_hi, n_lh);
     const int n_lo = n_lh & 0xffff, n_hi = n_lh >> 16;
     const R infeas = s_hi + s_lo - (static_cast<R>(n_hi) * hi + static_cast<R>(n_lo) * lo) -
                      static_cast<R>(n_hi + n_lo) * t;
@@ -314,9 +310,7 @@ __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
       if (x >= hi) ++n_hi;
       else if (x > lo) { s_mid += x; ++n_mid; }
     }
-    s_mid = group_sum<G>(s_mid);
-    n_hi = group_sum<G>(n_hi);
-    n_mid = group_sum<G>(n_mid);
+    group_sums<G>(s_mid, n_hi, n_mid);
     const int n_lo = m - n_hi - n_mid;
     const R s = s_mid + hi * static_cast<R>(n_hi) + lo * static_cast<R>(n_lo);
     if (!(s > rhs + eps)) return make_thr<R>(R(0), lo, hi);
@@ -358,9 +352,7 @@ __device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
     n_p += pos ? 1 : 0;
     n_z += (!pos && x >= -eps16) ? 1 : 0;
   }
-  s_p = group_sum<G>(s_p);
-  n_p = group_sum<G>(n_p);
-  n_z = group_sum<G>(n_z);
+  group_sums<G>(s_p, n_p, n_z);
   if (n_z > 0) return slow_thr<R>();
   const R den = K * K;
   const R t = (R(0) * s_p - K * R(0)) / den;
@@ -739,8 +731,7 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
         su += in ? y : R(0);
         cu += in ? 1 : 0;
       }
-      su = group_sum<G>(su);
-      cu = group_sum<G>(cu);
+      group_sums<G>(su, cu);
       if (cu == u_count || cu == 0) break;
       u_cut = dmax(u_cut, t);
       u_count = cu;
@@ -778,10 +769,7 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
           f3 += w * (1.0f - 2.0f * w) * (rd3 * rd2);
         }
       }
-      f0 = group_sum<G>(f0);
-      f1 = group_sum<G>(f1);
-      f2 = group_sum<G>(f2);
-      f3 = group_sum<G>(f3);
+      group_sums<G>(f0, f1, f2, f3);
       f0 -= static_cast<float>(rhs);
       const float f02 = f0 * f2, f11 = f1 * f1;
       tf = tc - 3.0f * f0 * (2.0f * f11 - f02) / (6.0f * f1 * (f02 - f11) - f0 * (f0 * f3));
@@ -819,10 +807,7 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
         f3 += w * (R(1) - R(2) * w) * (rd3 * rd2);
       }
     }
-    f0 = group_sum<G>(f0);
-    f1 = group_sum<G>(f1);
-    f2 = group_sum<G>(f2);
-    f3 = group_sum<G>(f3);
+    group_sums<G>(f0, f1, f2, f3);
     f0 -= rhs;
     const R f02 = f0 * f2, f11 = f1 * f1;
     t = tc - R(3) * f0 * (R(2) * f11 - f02) / (R(6) * f1 * (f02 - f11) - f0 * (f0 * f3));
@@ -1037,8 +1022,7 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
       sb += in ? x : R(0);
       nb += in ? 1 : 0;
     }
-    sb = group_sum<G>(sb);
-    nb = group_sum<G>(nb);
+    group_sums<G>(sb, nb);
     R tb = 0;
     for (int it = 0; it <= m; ++it) {
       tb = div_near(sb - rhs, static_cast<R>(nb));
@@ -1052,8 +1036,7 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
         s2 += in ? x : R(0);
         n2 += in ? 1 : 0;
       }
-      s2 = group_sum<G>(s2);
-      n2 = group_sum<G>(n2);
+      group_sums<G>(s2, n2);
       if (n2 == nb) break;
       cut = dmax(cut, tb);
       sb = s2;
@@ -1086,8 +1069,7 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
       if (in_a(c) && x > cuts[0]) sa += x;
       if (!in_a(c) && x > cuts[1]) sb += x;
     }
-    sa = group_sum<G>(sa);
-    sb = group_sum<G>(sb);
+    group_sums<G>(sa, sb);
     t = (+sa - sb) / static_cast<R>(mc);
   }
   for (int it = 0; it <= m; ++it) {
@@ -1103,10 +1085,7 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
         if (x > cuts[1] && !(x > mt)) { sum_y += x; ++n_y; }
       }
     }
-    sum_x = group_sum<G>(sum_x);
-    sum_y = group_sum<G>(sum_y);
-    n_x = group_sum<G>(n_x);
-    n_y = group_sum<G>(n_y);
+    group_sums<G>(sum_x, sum_y, n_x, n_y);
     const R infeas = sum_x - sum_y - static_cast<R>(n_x + n_y) * t;
     R next;
     if (n_y > 0 && infeas > eps) {

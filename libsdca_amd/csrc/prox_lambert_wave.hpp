@@ -46,8 +46,9 @@ __device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1,
     a0 += v;
     a1 += div_near(v, R(1) + v);
   }
-  f0 = group_sum<NT>(a0);
-  f1 = group_sum<NT>(a1);
+  group_sums<NT>(a0, a1);
+  f0 = a0;
+  f1 = a1;
 }
 
 // f0..f3: W and its first three derivatives in t (lambert.h:308-332), with
@@ -70,10 +71,11 @@ __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, 
     a2 += div_near(v, d3);
     a3 += div_near(v * (R(1) - R(2) * v), d3 * d * d);
   }
-  f0 = group_sum<NT>(a0);
-  f1 = group_sum<NT>(a1);
-  f2 = group_sum<NT>(a2);
-  f3 = group_sum<NT>(a3);
+  group_sums<NT>(a0, a1, a2, a3);
+  f0 = a0;
+  f1 = a1;
+  f2 = a2;
+  f3 = a3;
 }
 
 // Largest entry of the LDS column and the lowest index holding it (an index
@@ -358,8 +360,7 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
   }
   max_a = group_max<NT>(max_a);
   max_b = group_max<NT>(max_b);
-  sum_a = group_sum<NT>(sum_a);
-  sum_b = group_sum<NT>(sum_b);
+  group_sums<NT>(sum_a, sum_b);
   const R c = alpha / num_a;
   const R max = (max_a > max_b - c) ? max_a : max_b - c;
   // Bracket guards (two_entropy.h:159-163).

@@ -37,14 +37,24 @@ namespace {
 constexpr int kEpochThreads = 256;
 // LDS of the block kernel (gfx950: 160 KiB per workgroup), less the static
 // arrays.
-constexpr size_t kEpochLdsBytes = 150 * 1024;
+constexpr size_t kEpochLdsBytes = 144 * 1024;
 constexpr int kRankJ = 8;  // classes per workgroup of the rank-B update
+// Delta rows whose loads the score corrections issue together (their
+// registers: kFixRows x PF values).
+constexpr int kFixRows = 8;
 
 struct EpochObj {
   int kind;
   int k;
   double c, gamma;
 };
+
+// The block's delta rows in LDS: for the row sizes where kEpochBlock rows of
+// m <= kEpochThreads PF values always fit next to the column buffers.
+template <class D>
+__host__ __device__ constexpr bool epoch_delta_in_lds(int PF) {
+  return PF > 0 && (sizeof(D) == 4 ? PF <= 4 : PF <= 1);
+}
 
 // Words of the thresholds' column in LDS: m values, or G C for the register
 // form, whose LDS scratch is the slot layout of the whole workgroup.
@@ -67,50 +77,72 @@ norms_kernel(const D* __restrict__ X, int64_t n, int64_t d, D* __restrict__ norm
   if (lane == 0) norms[i] = s;
 }
 
-// Rows of the block (one workgroup per row) and their example indices.  An
-// index outside [0, n) raises *bad and is read as 0.
-template <class D>
-__global__ void __launch_bounds__(256)
-gather_kernel(const D* __restrict__ X, const int64_t* __restrict__ order, int64_t q0, int64_t n,
-              int64_t d, D* __restrict__ XB, int64_t* __restrict__ idx, int* __restrict__ bad) {
-  const int k = blockIdx.x;
-  int64_t i = order ? order[q0 + k] : q0 + k;
-  if (i < 0 || i >= n) {
-    if (threadIdx.x == 0) bad[0] = 1;
-    i = 0;
+// Example index at position q of the order (q itself without one).  An
+// index outside [0, n) reads as 0 (the block kernel raises the flag).
+__device__ inline int64_t block_row(const int64_t* order, int64_t q, int64_t n) {
+  const int64_t i = order ? order[q] : q;
+  return (i >= 0 && i < n) ? i : 0;
+}
+
+// The thread's columns j = tid + G q for every q < PF (m <= G PF), with
+// ok = j < m: the loops stay branch-free (exec-masked branches around each
+// slot cost more than the slot's work), so loads read the clamped column
+// j < m ? j : m - 1 and the stores of slots past m go to the thread's dummy
+// word.  PF = 0: every j = tid (mod G) below m, q = 0, ok = true.
+template <int PF, class F>
+__device__ __forceinline__ void for_cols(int tid, int m, F&& f) {
+  if constexpr (PF > 0) {
+#pragma unroll
+    for (int q = 0; q < PF; ++q) {
+      const int j = tid + kEpochThreads * q;
+      f(j, q, j < m);
+    }
+  } else {
+    for (int j = tid; j < m; j += kEpochThreads) f(j, 0, true);
   }
-  if (threadIdx.x == 0) idx[k] = i;
-  const D* src = X + i * d;
-  D* dst = XB + static_cast<int64_t>(k) * d;
-  for (int64_t l = threadIdx.x; l < d; l += 256) dst[l] = src[l];
 }
 
 // The block's examples in order (one workgroup of G threads, all of which
-// run every step, including the thresholds).  S: nb x m scores at W_B: after
-// example k, row k' > k loses G_{kk'} delta_k (each thread owns the same
-// classes j in every row, so the rows it reads are the ones it wrote); the
-// rows live in LDS when s_lds (copied in first), else in S itself.
-// Gm: nb x nb Gram matrix, Delta: nb x m.  C, KM: the register form of the
-// simplex / knapsack thresholds for m - 1 <= G C values (C = 0: the
-// sorted-column form only) and k <= KM.
-template <class D, class R, int C, int KM>
+// run every step, including the thresholds).  S: nb x m scores at W_B;
+// example k's scores are S_k - sum_{k' < k} G_{k'k} delta_{k'} over the
+// earlier examples that changed W, in the order of the sequential updates
+// (each thread owns the same classes j in every row, so the delta entries it
+// reads are the ones it wrote).  The block's delta rows live in LDS where
+// kEpochBlock rows always fit (DL), else in Delta (nb x m), which holds them
+// for the rank update in any case.  Gm: nb x nb Gram matrix.  gdummy: G
+// words of global memory, the threads' sinks for stores past m.  C, KM: the
+// register form of the simplex / knapsack thresholds for m - 1 <= G C values
+// (C = 0: the sorted-column form only) and k <= KM.  PF > 0 (m <= G PF):
+// each thread keeps its entries of the example's vector, of a_i and of S_k
+// in registers, the next example's a_i and S_k loaded while this one runs;
+// PF = 0 keeps the vector in LDS and reads a_i and S_k as it goes.
+template <class D, class R, int C, int KM, int PF>
 __global__ void __launch_bounds__(kEpochThreads)
-epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* __restrict__ idx,
-                   int nb, const D* __restrict__ norms, const int64_t* __restrict__ labels,
-                   D* __restrict__ A, D* __restrict__ Delta, EpochObj ob, int m, int s_lds,
-                   int* __restrict__ bad) {
+epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
+                   const int64_t* __restrict__ order, int64_t q0, int64_t n, int nb,
+                   const D* __restrict__ norms, const int64_t* __restrict__ labels,
+                   D* __restrict__ A, D* __restrict__ Delta, D* __restrict__ gdummy, EpochObj ob,
+                   int m, int* __restrict__ bad) {
   constexpr int G = kEpochThreads;
+  constexpr int PQ = PF > 0 ? PF : 1;
+  constexpr bool DL = epoch_delta_in_lds<D>(PF);
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int cw = epoch_column_words(m, C);
-  D* const v = reinterpret_cast<D*>(smem_raw);  // the example's vector, m values
+  D* const v = reinterpret_cast<D*>(smem_raw);  // the example's vector (PF = 0), m values
   D* const cb = v + ((m + 3) & ~3);             // the column the thresholds read (cw words)
   D* const dummy = cb + cw;                     // G per-thread dummy words
-  D* const Sx = s_lds ? dummy + G : S;          // the block's running scores
+  D* const Dx = DL ? dummy + G : Delta;         // the block's delta rows
   __shared__ R sh_t, sh_lo, sh_hi;
   __shared__ int sh_slow;
-  __shared__ D g_row[kEpochBlock];
+  __shared__ D sh_vy;
+  __shared__ D g_all[kEpochBlock * kEpochBlock];
+  __shared__ D sh_norm[kEpochBlock];
+  __shared__ int64_t sh_i[kEpochBlock];
+  __shared__ int sh_y[kEpochBlock];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
+  D* const ld = dummy + tid;   // LDS sink
+  D* const gd = gdummy + tid;  // global sink
   const int kind = ob.kind;
   const R c = static_cast<R>(ob.c), gamma = static_cast<R>(ob.gamma);
   const bool hinge = kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH;
@@ -118,26 +150,78 @@ epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* _
   const bool simplex = kind == SDCA_OBJ_HINGE_TOPK || kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
   const int op = simplex ? OP_TOPK_SIMPLEX_BIASED : OP_KNAPSACK_LE_BIASED;
   const R knap_hi = simplex ? R(0) : c / static_cast<R>(ob.k);
-  if (s_lds) {
-    for (int64_t e = tid; e < static_cast<int64_t>(nb) * m; e += G) Sx[e] = S[e];
-    __syncthreads();
-  }
-  for (int k = 0; k < nb; ++k) {
-    const int64_t i = idx[k];
-    const D norm2 = norms[i];
-    D* const arow = A + i * m;
-    D* const drow = Delta + static_cast<int64_t>(k) * m;
-    const D* const srow = Sx + static_cast<int64_t>(k) * m;
-    if (!(norm2 > D(0))) {  // update.h:62: the example changes nothing
-      for (int j = tid; j < m; j += G) drow[j] = D(0);
-      continue;
+  // The block's indices, norms, labels and Gram matrix in LDS.
+  // An index outside [0, n) or a label outside [0, m) raises *bad and is
+  // read as 0.
+  if (tid < nb) {
+    int64_t i = order ? order[q0 + tid] : q0 + tid;
+    if (i < 0 || i >= n) {
+      bad[0] = 1;
+      i = 0;
     }
     int64_t yl = labels[i];
     if (yl < 0 || yl >= m) {
-      if (tid == 0) bad[0] = 1;
+      bad[0] = 1;
       yl = 0;
     }
-    const int y = static_cast<int>(yl);
+    sh_i[tid] = i;
+    sh_norm[tid] = norms[i];
+    sh_y[tid] = static_cast<int>(yl);
+  }
+  for (int e = tid; e < nb * nb; e += G) g_all[e] = Gm[e];
+  __syncthreads();
+  // PF > 0: the next example's a_i and S row are loaded into anext / snext
+  // one example ahead and copied at the top of its step, where nothing newer
+  // is in flight (so the wait for them waits for nothing else).
+  D acur[PQ], anext[PQ], scur[PQ], snext[PQ], vr[PQ];
+  if constexpr (PF > 0) {
+    const D* a0 = A + sh_i[0] * m;
+    for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+      const int jc = ok ? j : m - 1;
+      anext[q] = a0[jc];
+      snext[q] = S[jc];
+    });
+  }
+  // The example's vector entry of slot (j, q): registers or LDS.
+  auto getv = [&](int j, int q) -> D {
+    if constexpr (PF > 0) return vr[q];
+    else return v[j];
+  };
+  auto setv = [&](int j, int q, D x) {
+    if constexpr (PF > 0) vr[q] = x;
+    else v[j] = x;
+  };
+  unsigned changed = 0;  // bit k': example k' changed W
+  for (int k = 0; k < nb; ++k) {
+    const int64_t i = sh_i[k];
+    const D norm2 = sh_norm[k];
+    const int y = sh_y[k];
+    D* const arow = A + i * m;
+    D* const drow = Delta + static_cast<int64_t>(k) * m;
+    const D* const srow = S + static_cast<int64_t>(k) * m;
+    const bool has_next = k + 1 < nb;
+    if constexpr (PF > 0) {
+#pragma unroll
+      for (int q = 0; q < PF; ++q) {
+        acur[q] = anext[q];
+        scur[q] = snext[q];
+      }
+      // The next example's a as A holds it now (replaced below when it is
+      // this example, the only one whose update is still to come).
+      if (has_next) {
+        const D* an = A + sh_i[k + 1] * m;
+        const D* sn = srow + m;
+        for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+          const int jc = ok ? j : m - 1;
+          anext[q] = an[jc];
+          snext[q] = sn[jc];
+        });
+      }
+    }
+    if (!(norm2 > D(0))) {  // update.h:62: the example changes nothing
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) { *(ok ? drow + j : gd) = D(0); });
+      continue;
+    }
     // 1. The vector to project: axpby(pa, scores, pb, a_old).
     R rho = R(1);
     D pa = D(1), pb = -norm2;  // the entropic objectives
@@ -146,12 +230,56 @@ epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* _
       pa = smooth ? static_cast<D>(rho) / norm2 : D(1) / norm2;
       pb = smooth ? -static_cast<D>(rho) : D(-1);
     }
-    for (int j = tid; j < m; j += G) v[j] = pa * srow[j] + pb * arow[j];
+    if constexpr (PF > 0) {
+      // The corrections row by row in increasing r, kFixRows rows' loads at
+      // a time (the same sequence of subtractions per entry).
+      unsigned rem = changed & ((1u << k) - 1u);
+      while (rem != 0u) {
+        int rr[kFixRows];
+        D g[kFixRows];
+#pragma unroll
+        for (int b = 0; b < kFixRows; ++b) {
+          rr[b] = rem != 0u ? __builtin_ctz(rem) : -1;
+          rem &= rem - 1u;
+          g[b] = rr[b] >= 0 ? g_all[rr[b] * nb + k] : D(0);
+        }
+        D dv[kFixRows][PQ];
+#pragma unroll
+        for (int b = 0; b < kFixRows; ++b) {
+          const D* drr = Dx + static_cast<int64_t>(rr[b] >= 0 ? rr[b] : 0) * m;
+          for_cols<PF>(tid, m, [&](int j, int q, bool ok) { dv[b][q] = drr[ok ? j : m - 1]; });
+        }
+#pragma unroll
+        for (int b = 0; b < kFixRows; ++b) {
+          if (rr[b] >= 0) {
+#pragma unroll
+            for (int q = 0; q < PF; ++q) scur[q] -= g[b] * dv[b][q];
+          }
+        }
+      }
+    }
+    for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+      D sc, ao;
+      if constexpr (PF > 0) {
+        sc = scur[q];
+        ao = acur[q];
+      } else {
+        sc = srow[j];
+        for (int r = 0; r < k; ++r)
+          if ((changed >> r) & 1u) sc -= g_all[r * nb + k] * Dx[static_cast<int64_t>(r) * m + j];
+        ao = arow[j];
+      }
+      const D x = pa * sc + pb * ao;
+      setv(j, q, x);
+      if constexpr (PF > 0) *((ok && j == y) ? &sh_vy : ld) = x;
+    });
     __syncthreads();
-    const D vy = v[y];
+    const D vy = PF > 0 ? sh_vy : v[y];
     if (kind == SDCA_OBJ_ENTROPY) {
       // prox_two_entropy over (label | the rest), alpha = c norm2
-      for (int j = tid; j < m; j += G) cb[j == y ? 0 : (j < y ? j + 1 : j)] = v[j];
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+        *(ok ? cb + (j == y ? 0 : (j < y ? j + 1 : j)) : ld) = getv(j, q);
+      });
       __syncthreads();
       const R alpha = c * static_cast<R>(norm2);
       R t, c2;
@@ -159,21 +287,20 @@ epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* _
       const D map_a = D(1) / static_cast<D>(alpha);
       const D ta = static_cast<D>(t), tb = static_cast<D>(t + c2);
       const D na = static_cast<D>(-c), nbias = static_cast<D>(c / R(1));
-      for (int j = tid; j < m; j += G) {
-        const D x = clamp_ref(map_a * lambert_w_exp(v[j] - (j == y ? ta : tb)), D(0), D(1));
-        v[j] = (j == y) ? na * x + nbias : na * x;
-      }
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+        const D x = clamp_ref(map_a * lambert_w_exp(getv(j, q) - (j == y ? ta : tb)), D(0), D(1));
+        setv(j, q, (j == y) ? na * x + nbias : na * x);
+      });
     } else {
       // The off-label entries shifted by (pa - v_y) (hinge) or -v_y (top-k
       // entropy), compacted into cb.
       const D shift = hinge ? pa - vy : -vy;
-      for (int j = tid; j < m; j += G) {
-        if (j != y) {
-          const D x = v[j] + shift;
-          v[j] = x;
-          cb[j < y ? j : j - 1] = x;
-        }
-      }
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+        const bool off = j != y;
+        const D x = getv(j, q) + shift;
+        if (off) setv(j, q, x);
+        *((ok && off) ? cb + (j < y ? j : j - 1) : ld) = x;
+      });
       __syncthreads();
       const int mp = m - 1;
       if (hinge) {
@@ -183,10 +310,13 @@ epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* _
           // = entry g + G c), which defers to the sorted form only where the
           // reference's biased cone search is needed
           // (topk_simplex_biased.h:57-66).
-          D vr[C];
+          D vq[C];
           const int nvalid = (mp - tid + G - 1) / G;
 #pragma unroll
-          for (int q = 0; q < C; ++q) vr[q] = (q < nvalid) ? cb[tid + G * q] : -num<D>::inf();
+          for (int q = 0; q < C; ++q) {
+            const D x = cb[tid + G * q];
+            vq[q] = (q < nvalid) ? x : -num<D>::inf();
+          }
           ProxParamsT<R> pp;
           pp.lo = R(0);
           pp.hi = knap_hi;
@@ -196,8 +326,8 @@ epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* _
           pp.op = op;
           pp.p = 0;
           const ColThr<R> th = simplex
-              ? topk_family<G, C, KM, D, R>(vr, mp, nvalid, pp, cb, dummy + tid)
-              : knap_family<G, C, D, R>(vr, mp, nvalid, pp);
+              ? topk_family<G, C, KM, D, R>(vq, mp, nvalid, pp, cb, ld)
+              : knap_family<G, C, D, R>(vq, mp, nvalid, pp);
           if (tid == 0) {
             sh_slow = th.slow ? 1 : 0;
             sh_t = th.t;
@@ -207,8 +337,9 @@ epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* _
           __syncthreads();
           sorted_form = sh_slow != 0;
           if (sorted_form) {  // cb served as scratch: compact it again
-            for (int j = tid; j < m; j += G)
-              if (j != y) cb[j < y ? j : j - 1] = v[j];
+            for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+              *((ok && j != y) ? cb + (j < y ? j : j - 1) : ld) = getv(j, q);
+            });
             __syncthreads();
           }
         }
@@ -237,126 +368,255 @@ epoch_block_kernel(D* __restrict__ S, const D* __restrict__ Gm, const int64_t* _
       const D t = static_cast<D>(sh_t), lo = static_cast<D>(sh_lo), hi = static_cast<D>(sh_hi);
       const D map_a = hinge ? D(1) : D(1) / static_cast<D>(c * static_cast<R>(norm2));
       R part = 0;
-      for (int j = tid; j < m; j += G) {
-        if (j != y) {
-          const D x = hinge ? clamp_ref(v[j] - t, lo, hi)
-                            : clamp_ref(map_a * lambert_w_exp(v[j] - t), D(0), hi);
-          v[j] = x;
-          part += static_cast<R>(x);
-        }
-      }
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+        const bool off = j != y;
+        const D x0 = getv(j, q);
+        const D x = hinge ? clamp_ref(x0 - t, lo, hi)
+                          : clamp_ref(map_a * lambert_w_exp(x0 - t), D(0), hi);
+        if (off) setv(j, q, x);
+        part += (ok && off) ? static_cast<R>(x) : R(0);
+      });
       const R sum = group_sum<G>(part);
       // 3. Recover the variables: the label's entry from the sum, the others
       // negated (and scaled by c for the top-k entropy).
       const D scale = hinge ? D(-1) : static_cast<D>(-c);
-      for (int j = tid; j < m; j += G) {
-        if (j == y) {
-          v[j] = hinge ? static_cast<D>(dmin(c, sum)) : static_cast<D>(c * dmin(R(1), sum));
-        } else {
-          v[j] = v[j] * scale;
-        }
-      }
+      const D ay = hinge ? static_cast<D>(dmin(c, sum)) : static_cast<D>(c * dmin(R(1), sum));
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+        setv(j, q, (j == y) ? ay : getv(j, q) * scale);
+      });
     }
     // a_old - a_new (sdca_blas_axpy with -1), its 1-norm, a_i <- a_new.
     D part = 0;
-    for (int j = tid; j < m; j += G) {
-      const D an = v[j];
-      const D dl = arow[j] + D(-1) * an;
-      drow[j] = dl;
-      arow[j] = an;
-      part += fabs(dl);
-    }
+    for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+      const D an = getv(j, q);
+      const D dl = (PF > 0 ? acur[q] : arow[j]) + D(-1) * an;
+      *(ok ? drow + j : gd) = dl;
+      *(ok ? arow + j : gd) = an;
+      if constexpr (DL) *(ok ? Dx + static_cast<int64_t>(k) * m + j : ld) = dl;
+      part += ok ? fabs(dl) : D(0);
+    });
     const D asum = group_sum<G>(part);  // also orders v's last reads before the next writes
-    if (asum > num<D>::eps() && k + 1 < nb) {
-      // The later rows of the block see this update: S_k' -= G_kk' delta_k.
-      if (tid < nb) g_row[tid] = Gm[k * nb + tid];
-      __syncthreads();
-      for (int j = tid; j < m; j += G) {
-        const D dl = drow[j];
-        for (int q = k + 1; q < nb; ++q) Sx[static_cast<int64_t>(q) * m + j] -= g_row[q] * dl;
+    if (asum > num<D>::eps()) {
+      changed |= 1u << k;  // the later examples' scores see this update
+    } else {
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) { *(ok ? drow + j : gd) = D(0); });
+    }
+    if constexpr (PF > 0) {
+      if (has_next && sh_i[k + 1] == i) {
+#pragma unroll
+        for (int q = 0; q < PF; ++q) anext[q] = vr[q];
       }
-    } else if (!(asum > num<D>::eps())) {
-      for (int j = tid; j < m; j += G) drow[j] = D(0);
     }
     __syncthreads();
   }
 }
 
-// The block's skinny products P = X_B Y' (nb <= kEpochBlock rows; Y: M x d,
-// the primal variables or X_B itself), split over the features: workgroup
-// (bx, ks) has four waves of JW classes each over features
-// [ks kc, (ks + 1) kc), lane l taking features l, l + 64, ...; the partial
-// sums of the splits are added in split order by skinny_sum_kernel.
-template <class D, int JW>
+typedef float ep_f32x16 __attribute__((ext_vector_type(16)));
+typedef double ep_f64x4 __attribute__((ext_vector_type(4)));
+
+// The block's score and Gram products on the matrix cores.  Column c of the
+// product is w_c (c < M) or x_{c - M} (M <= c < M + nb, the Gram matrix), row
+// e is x_e, the block's e-th example.  Workgroup (tile, ks) takes 32 columns
+// (tile tiles_w: the Gram matrix) over the features [ks kc, (ks + 1) kc),
+// its four waves 32 features in turn; the waves' sums are added in wave
+// order into P[ks][e][c] (Mt = M + nb columns), or, with one split, straight
+// into S (nb x M) and Gm (nb x nb).
+//   fp32: v_mfma_f32_32x32x2f32; lane l holds example / column l % 32 at
+//         features 16 (l / 32) .. + 15 of the wave's 32;
+//   fp64: 2 x 2 v_mfma_f64_16x16x4f64; lane l holds examples / columns
+//         l % 16 and 16 + l % 16 at features 8 (l / 16) .. + 7.
+template <class D>
 __global__ void __launch_bounds__(256)
-skinny_partial_kernel(const D* __restrict__ XB, const D* __restrict__ Y, D* __restrict__ P,
-                      int nb, int64_t M, int64_t d, int64_t kc) {
+skinny_mfma_kernel(const D* __restrict__ X, const int64_t* __restrict__ order, int64_t q0,
+                   int64_t n, const D* __restrict__ W, int nb, int64_t M, int64_t d, int64_t kc,
+                   int tiles_w, int vec, D* __restrict__ P, D* __restrict__ S,
+                   D* __restrict__ Gm) {
+  constexpr int LD = 33;
+  __shared__ D red[4][32 * LD];
   const int wave = static_cast<int>(threadIdx.x) >> 6, lane = static_cast<int>(threadIdx.x) & 63;
-  const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * JW;
-  const int64_t l0 = static_cast<int64_t>(blockIdx.y) * kc;
+  const bool gram = static_cast<int>(blockIdx.x) == tiles_w;
+  const int64_t j0 = gram ? 0 : static_cast<int64_t>(blockIdx.x) * 32;
+  const int64_t cols = gram ? nb : M;
+  const int64_t ks = blockIdx.y;
+  const int64_t l0 = ks * kc;
   const int64_t l1 = (l0 + kc < d) ? l0 + kc : d;
-  D acc[JW][kEpochBlock];
+  if constexpr (sizeof(D) == 4) {
+    const int r = lane & 31, h = lane >> 5;
+    const bool xr = r < nb, yr = j0 + r < cols;
+    const D* xrow = X + (xr ? block_row(order, q0 + r, n) : 0) * d;
+    const D* yrow = gram ? X + (yr ? block_row(order, q0 + r, n) : 0) * d
+                         : W + (yr ? j0 + r : 0) * d;
+    ep_f32x16 acc;
 #pragma unroll
-  for (int jw = 0; jw < JW; ++jw)
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    for (int64_t f0 = l0 + 32 * wave; f0 < l1; f0 += 128) {
+      const int64_t fb = f0 + 16 * h;
+      float a[16], b[16];
+      if (vec && fb + 16 <= l1) {
 #pragma unroll
-    for (int e = 0; e < kEpochBlock; ++e) acc[jw][e] = D(0);
-  for (int64_t l = l0 + lane; l < l1; l += 64) {
-    D y[JW];
+        for (int u = 0; u < 4; ++u) {
+          const float4 xa = xr ? *reinterpret_cast<const float4*>(xrow + fb + 4 * u)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 yb = yr ? *reinterpret_cast<const float4*>(yrow + fb + 4 * u)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+          a[4 * u] = xa.x; a[4 * u + 1] = xa.y; a[4 * u + 2] = xa.z; a[4 * u + 3] = xa.w;
+          b[4 * u] = yb.x; b[4 * u + 1] = yb.y; b[4 * u + 2] = yb.z; b[4 * u + 3] = yb.w;
+        }
+      } else {
 #pragma unroll
-    for (int jw = 0; jw < JW; ++jw) y[jw] = (j0 + jw < M) ? Y[(j0 + jw) * d + l] : D(0);
+        for (int u = 0; u < 16; ++u) {
+          const bool ok = fb + u < l1;
+          a[u] = (xr && ok) ? xrow[fb + u] : 0.0f;
+          b[u] = (yr && ok) ? yrow[fb + u] : 0.0f;
+        }
+      }
 #pragma unroll
-    for (int e = 0; e < kEpochBlock; ++e) {
-      if (e < nb) {
-        const D x = XB[static_cast<int64_t>(e) * d + l];
+      for (int u = 0; u < 16; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b[u], acc, 0, 0, 0);
+    }
+    // Accumulator i of lane l: row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
 #pragma unroll
-        for (int jw = 0; jw < JW; ++jw) acc[jw][e] += x * y[jw];
+    for (int i = 0; i < 16; ++i) red[wave][(8 * (i >> 2) + 4 * h + (i & 3)) * LD + r] = acc[i];
+  } else {
+    const int r = lane & 15, g = lane >> 4;
+    const D* xrow[2];
+    const D* yrow[2];
+    bool xr[2], yr[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int e = 16 * a + r;
+      xr[a] = e < nb;
+      yr[a] = j0 + e < cols;
+      xrow[a] = X + (xr[a] ? block_row(order, q0 + e, n) : 0) * d;
+      yrow[a] = gram ? X + (yr[a] ? block_row(order, q0 + e, n) : 0) * d
+                     : W + (yr[a] ? j0 + e : 0) * d;
+    }
+    ep_f64x4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[a][b][i] = 0.0;
+    for (int64_t f0 = l0 + 32 * wave; f0 < l1; f0 += 128) {
+      const int64_t fb = f0 + 8 * g;
+      double xa[2][8], yb[2][8];
+      if (vec && fb + 8 <= l1) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const double2 x2 = xr[a] ? *reinterpret_cast<const double2*>(xrow[a] + fb + 2 * u)
+                                     : make_double2(0.0, 0.0);
+            const double2 y2 = yr[a] ? *reinterpret_cast<const double2*>(yrow[a] + fb + 2 * u)
+                                     : make_double2(0.0, 0.0);
+            xa[a][2 * u] = x2.x; xa[a][2 * u + 1] = x2.y;
+            yb[a][2 * u] = y2.x; yb[a][2 * u + 1] = y2.y;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const bool ok = fb + u < l1;
+            xa[a][u] = (xr[a] && ok) ? xrow[a][fb + u] : 0.0;
+            yb[a][u] = (yr[a] && ok) ? yrow[a][fb + u] : 0.0;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(xa[a][u], yb[b][u], acc[a][b], 0, 0, 0);
+    }
+    // Accumulator i of lane l: row l / 16 + 4 i, column l % 16 of its tile.
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][(16 * a + g + 4 * i) * LD + 16 * b + r] = acc[a][b][i];
+  }
+  __syncthreads();
+  const bool direct = gridDim.y == 1;
+  const int64_t Mt = M + nb;
+  for (int o = static_cast<int>(threadIdx.x); o < 32 * 32; o += 256) {
+    const int e = o >> 5, cc = o & 31;
+    D s = red[0][e * LD + cc];
+    s += red[1][e * LD + cc];
+    s += red[2][e * LD + cc];
+    s += red[3][e * LD + cc];
+    const int64_t col = j0 + cc;
+    if (e < nb && col < cols) {
+      if (direct) {
+        if (gram) Gm[e * nb + col] = s;
+        else S[e * M + col] = s;
+      } else {
+        P[(ks * kEpochBlock + e) * Mt + (gram ? M + col : col)] = s;
       }
     }
   }
-  D* const out = P + static_cast<int64_t>(blockIdx.y) * kEpochBlock * M;
-#pragma unroll
-  for (int jw = 0; jw < JW; ++jw) {
-#pragma unroll
-    for (int e = 0; e < kEpochBlock; ++e) {
-      const D s = group_sum<64>(acc[jw][e]);
-      if (lane == 0 && e < nb && j0 + jw < M) out[static_cast<int64_t>(e) * M + j0 + jw] = s;
-    }
-  }
 }
 
+// The splits' sums in split order, into S and Gm.
 template <class D>
 __global__ void __launch_bounds__(256)
-skinny_sum_kernel(const D* __restrict__ P, D* __restrict__ out, int nb, int64_t M, int ksplit) {
+skinny_sum_kernel(const D* __restrict__ P, D* __restrict__ S, D* __restrict__ Gm, int nb,
+                  int64_t M, int ksplit) {
+  const int64_t Mt = M + nb;
   const int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (o >= static_cast<int64_t>(nb) * M) return;
-  const int64_t e = o / M, j = o % M;
-  D s = P[e * M + j];
-  for (int ks = 1; ks < ksplit; ++ks) s += P[(static_cast<int64_t>(ks) * kEpochBlock + e) * M + j];
-  out[o] = s;
+  if (o >= static_cast<int64_t>(nb) * Mt) return;
+  const int64_t e = o / Mt, c = o % Mt;
+  D s = P[e * Mt + c];
+  for (int ks = 1; ks < ksplit; ++ks) s += P[(static_cast<int64_t>(ks) * kEpochBlock + e) * Mt + c];
+  if (c < M) S[e * M + c] = s;
+  else Gm[e * nb + (c - M)] = s;
 }
 
-// Feature split of the skinny products: chunks of at least 512 features, at
-// most kSkinnySplits of them.
-constexpr int kSkinnySplits = 8;
-inline int64_t skinny_chunk(int64_t d) {
-  const int64_t c = (d + kSkinnySplits - 1) / kSkinnySplits;
-  return c < 512 ? 512 : c;
+// Feature split of the skinny products: about kSkinnyGroups workgroups over
+// the column tiles, splits of whole 128-feature steps, at most
+// kSkinnyMaxSplits of them.
+constexpr int kSkinnyGroups = 512;
+constexpr int kSkinnyMaxSplits = 32;
+struct SkinnyPlan {
+  int tiles_w;
+  int ksplit;
+  int64_t kc;
+};
+inline SkinnyPlan skinny_plan(int64_t d, int64_t m) {
+  SkinnyPlan p;
+  p.tiles_w = static_cast<int>((m + 31) / 32);
+  const int64_t tiles = p.tiles_w + 1;
+  const int64_t steps = (d + 127) / 128;
+  int64_t ks = (kSkinnyGroups + tiles - 1) / tiles;
+  if (ks > steps) ks = steps;
+  if (ks > kSkinnyMaxSplits) ks = kSkinnyMaxSplits;
+  if (ks < 1) ks = 1;
+  p.kc = ((steps + ks - 1) / ks) * 128;
+  p.ksplit = static_cast<int>((d + p.kc - 1) / p.kc);
+  if (p.ksplit < 1) p.ksplit = 1;
+  return p;
 }
 
 template <class D>
-hipError_t launch_skinny(const D* XB, const D* Y, D* out, D* P, int nb, int64_t M, int64_t d,
-                         hipStream_t stream) {
-  constexpr int JW = sizeof(D) == 4 ? 4 : 2;
-  const int64_t kc = skinny_chunk(d);
-  const int ksplit = static_cast<int>((d + kc - 1) / kc);
-  const dim3 grid(static_cast<unsigned>((M + 4 * JW - 1) / (4 * JW)), static_cast<unsigned>(ksplit));
-  hipLaunchKernelGGL((skinny_partial_kernel<D, JW>), grid, dim3(256), 0, stream, XB, Y, P, nb, M,
-                     d, kc);
+hipError_t launch_skinny(const EpochLaunch& a, int64_t q0, int nb, D* S, D* Gm, D* P,
+                         const SkinnyPlan& pl) {
+  const D* X = static_cast<const D*>(a.X);
+  const D* W = static_cast<const D*>(a.W);
+  constexpr int64_t vw = 16 / sizeof(D);
+  const int vec = (a.d % vw == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
+                  (reinterpret_cast<uintptr_t>(W) % 16 == 0);
+  const dim3 grid(static_cast<unsigned>(pl.tiles_w + 1), static_cast<unsigned>(pl.ksplit));
+  hipLaunchKernelGGL((skinny_mfma_kernel<D>), grid, dim3(256), 0, a.stream, X, a.order, q0, a.n, W,
+                     nb, a.m, a.d, pl.kc, pl.tiles_w, vec, P, S, Gm);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int64_t total = static_cast<int64_t>(nb) * M;
+  if (e != hipSuccess || pl.ksplit == 1) return e;
+  const int64_t total = static_cast<int64_t>(nb) * (a.m + nb);
   hipLaunchKernelGGL((skinny_sum_kernel<D>), dim3(static_cast<unsigned>((total + 255) / 256)),
-                     dim3(256), 0, stream, P, out, nb, M, ksplit);
+                     dim3(256), 0, a.stream, P, S, Gm, nb, a.m, pl.ksplit);
   return hipGetLastError();
 }
 
@@ -365,20 +625,24 @@ hipError_t launch_skinny(const D* XB, const D* Y, D* out, D* P, int nb, int64_t 
 // consecutive features of kRankJ classes.
 template <class D>
 __global__ void __launch_bounds__(256)
-rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __restrict__ XB,
-                   int nb, int64_t m, int64_t d) {
+rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __restrict__ X,
+                   const int64_t* __restrict__ order, int64_t q0, int64_t n, int nb, int64_t m,
+                   int64_t d) {
   __shared__ D dl[kEpochBlock][kRankJ];
+  __shared__ int64_t rows[kEpochBlock];
   const int64_t j0 = static_cast<int64_t>(blockIdx.y) * kRankJ;
   for (int e = threadIdx.x; e < kEpochBlock * kRankJ; e += 256) {
     const int k = e / kRankJ, jj = e % kRankJ;
     dl[k][jj] = (k < nb && j0 + jj < m) ? Delta[static_cast<int64_t>(k) * m + j0 + jj] : D(0);
   }
+  if (threadIdx.x < kEpochBlock)
+    rows[threadIdx.x] = threadIdx.x < nb ? block_row(order, q0 + threadIdx.x, n) : 0;
   __syncthreads();
   const int64_t l = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (l >= d) return;
   D xk[kEpochBlock];
 #pragma unroll
-  for (int k = 0; k < kEpochBlock; ++k) xk[k] = (k < nb) ? XB[static_cast<int64_t>(k) * d + l] : D(0);
+  for (int k = 0; k < kEpochBlock; ++k) xk[k] = (k < nb) ? X[rows[k] * d + l] : D(0);
 #pragma unroll
   for (int jj = 0; jj < kRankJ; ++jj) {
     const int64_t j = j0 + jj;
@@ -392,59 +656,68 @@ rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __re
   }
 }
 
-template <class D, class R, int C, int KM>
-hipError_t launch_block(D* S, const D* Gm, const int64_t* idx, int nb, const D* norms,
-                        const EpochLaunch& a, D* Delta, const EpochObj& ob, int* bad) {
+template <class D, class R, int C, int KM, int PF>
+hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* norms,
+                        const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob, int* bad) {
   const int m = static_cast<int>(a.m);
   size_t lds = (static_cast<size_t>((m + 3) & ~3) + epoch_column_words(m, C) + kEpochThreads) *
                sizeof(D);
-  // The block's scores in LDS where they fit (the running update then costs
-  // LDS instead of global round trips).
-  const size_t s_bytes = static_cast<size_t>(nb) * static_cast<size_t>(m) * sizeof(D);
-  const int s_lds = lds + s_bytes <= kEpochLdsBytes ? 1 : 0;
-  if (s_lds) lds += s_bytes;
-  hipLaunchKernelGGL((epoch_block_kernel<D, R, C, KM>), dim3(1), dim3(kEpochThreads), lds,
-                     a.stream, S, Gm, idx, nb, norms, a.labels, static_cast<D*>(a.A), Delta, ob,
-                     m, s_lds, bad);
+  // The block's delta rows in LDS where they always fit (the score
+  // corrections then read LDS instead of global memory).
+  if constexpr (epoch_delta_in_lds<D>(PF))
+    lds += static_cast<size_t>(kEpochBlock) * static_cast<size_t>(m) * sizeof(D);
+  if (lds > kEpochLdsBytes) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((epoch_block_kernel<D, R, C, KM, PF>), dim3(1), dim3(kEpochThreads), lds,
+                     a.stream, S, Gm, a.order, q0, a.n, nb, norms, a.labels,
+                     static_cast<D*>(a.A), Delta, gdummy, ob, m, bad);
   return hipGetLastError();
 }
 
-// The block kernel's register form for m - 1 values and k (C = 0: the
-// sorted-column form only).
+// The block kernel for m and k: register slots per thread PF = C from m
+// (m <= 256, 1024, 2048), and the register form of the thresholds (C > 0)
+// for the simplex and knapsack objectives with k <= 8.
 template <class D, class R>
-hipError_t launch_block_for(D* S, const D* Gm, const int64_t* idx, int nb, const D* norms,
-                            const EpochLaunch& a, D* Delta, const EpochObj& ob, int* bad) {
-  const int64_t mp = a.m - 1;
+hipError_t launch_block_for(const D* S, const D* Gm, int64_t q0, int nb, const D* norms,
+                            const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob,
+                            int* bad) {
+  const int64_t m = a.m;
   const bool simplex = a.kind == SDCA_OBJ_HINGE_TOPK || a.kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
-  const bool big_k = simplex && a.k > 8;
-  if (mp > 2048 || big_k || a.kind > SDCA_OBJ_TOPK_HINGE_SMOOTH)
-    return launch_block<D, R, 0, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
-  if (!simplex || a.k <= 5) {
-    if (mp <= 256) return launch_block<D, R, 1, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
-    if (mp <= 1024) return launch_block<D, R, 4, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
-    return launch_block<D, R, 8, 5>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+  const bool regs = a.kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH && !(simplex && a.k > 8);
+  const bool k5 = !simplex || a.k <= 5;
+  const int pf = m <= 256 ? 1 : m <= 1024 ? 4 : m <= 2048 ? 8 : 0;
+  if (pf == 0) return launch_block<D, R, 0, 5, 0>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+  if (!regs) {
+    if (pf == 1) return launch_block<D, R, 0, 5, 1>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+    if (pf == 4) return launch_block<D, R, 0, 5, 4>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+    return launch_block<D, R, 0, 5, 8>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
   }
-  if (mp <= 256) return launch_block<D, R, 1, 8>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
-  if (mp <= 1024) return launch_block<D, R, 4, 8>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
-  return launch_block<D, R, 8, 8>(S, Gm, idx, nb, norms, a, Delta, ob, bad);
+  if (k5) {
+    if (pf == 1) return launch_block<D, R, 1, 5, 1>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+    if (pf == 4) return launch_block<D, R, 4, 5, 4>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+    return launch_block<D, R, 8, 5, 8>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+  }
+  if (pf == 1) return launch_block<D, R, 1, 8, 1>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+  if (pf == 4) return launch_block<D, R, 4, 8, 4>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+  return launch_block<D, R, 8, 8, 8>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
 }
 
 template <class D, class R>
 hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   const int64_t d = a.d, m = a.m, n = a.n;
   const int64_t B = kEpochBlock;
-  // Workspace: [flag (256 B) | idx | XB | S | G | Delta | norms]
+  const SkinnyPlan pl = skinny_plan(d, m);
+  // Workspace: [flag (256 B) | the threads' store sinks | S | G | Delta | P |
+  // norms]
   char* p = static_cast<char*>(a.ws);
   int* bad = reinterpret_cast<int*>(p);
   p += 256;
-  int64_t* idx = reinterpret_cast<int64_t*>(p);
-  p += B * sizeof(int64_t);
-  D* XB = reinterpret_cast<D*>(p);
-  D* S = XB + B * d;
+  D* gdummy = reinterpret_cast<D*>(p);
+  p += kEpochThreads * sizeof(double);
+  D* S = reinterpret_cast<D*>(p);
   D* Gm = S + B * m;
   D* Delta = Gm + B * B;
   D* P = Delta + B * m;  // the skinny products' partial sums
-  D* norms_ws = P + kSkinnySplits * B * (m > B ? m : B);
+  D* norms_ws = P + static_cast<int64_t>(pl.ksplit) * B * (m + B);
   *flag_dev = bad;
   hipError_t e = launch_clear(bad, 1, a.stream);
   if (e != hipSuccess) return e;
@@ -466,15 +739,11 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
                        static_cast<unsigned>((m + kRankJ - 1) / kRankJ));
   for (int64_t q0 = 0; q0 < a.count; q0 += B) {
     const int nb = static_cast<int>(a.count - q0 < B ? a.count - q0 : B);
-    hipLaunchKernelGGL((gather_kernel<D>), dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream,
-                       X, a.order, q0, n, d, XB, idx, bad);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = launch_skinny<D>(XB, W, S, P, nb, m, d, a.stream)) != hipSuccess) return e;
-    if ((e = launch_skinny<D>(XB, XB, Gm, P, nb, nb, d, a.stream)) != hipSuccess) return e;
-    if ((e = launch_block_for<D, R>(S, Gm, idx, nb, norms, a, Delta, ob, bad)) != hipSuccess)
+    if ((e = launch_skinny<D>(a, q0, nb, S, Gm, P, pl)) != hipSuccess) return e;
+    if ((e = launch_block_for<D, R>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad)) != hipSuccess)
       return e;
-    hipLaunchKernelGGL((rank_update_kernel<D>), rank_grid, dim3(256), 0, a.stream, W, Delta, XB,
-                       nb, m, d);
+    hipLaunchKernelGGL((rank_update_kernel<D>), rank_grid, dim3(256), 0, a.stream, W, Delta, X,
+                       a.order, q0, n, nb, m, d);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;
@@ -485,10 +754,10 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
 size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool norms_given) {
   const size_t es = data == SDCA_F32 ? 4 : 8;
   const size_t B = kEpochBlock;
-  const size_t mb = static_cast<size_t>(m) > B ? static_cast<size_t>(m) : B;
-  return 256 + B * sizeof(int64_t) +
-         es * (B * static_cast<size_t>(d) + 2 * B * static_cast<size_t>(m) + B * B +
-               kSkinnySplits * B * mb + (norms_given ? 0 : static_cast<size_t>(n)));
+  const size_t splits = static_cast<size_t>(skinny_plan(d, m).ksplit);
+  return 256 + kEpochThreads * sizeof(double) + es * (2 * B * static_cast<size_t>(m) + B * B +
+                     splits * B * (static_cast<size_t>(m) + B) +
+                     (norms_given ? 0 : static_cast<size_t>(n)));
 }
 
 int64_t epoch_max_m(int data) {
