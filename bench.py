@@ -22,7 +22,8 @@ data: examples/s, the reference's own epoch loop as cpu_baseline).
 
 The default run (c2) also times the whole C4 evaluation pass under the same
 clock and nests it as "c4" (examples/s, an MFMA roofline for the score GEMM
-and for the whole pass, its own cpu_baseline); --no-c4 skips it.
+and for the whole pass, its own cpu_baseline); --no-c4 skips it.  It nests
+one SDCA epoch on the C4 shape as "c4epoch" likewise (--no-epoch skips it).
 
 cpu_baseline: the reference's own prox loop (oracle/_ref, built from the
 reference headers with -O3) - or the oracle restatement when that library is
@@ -137,6 +138,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c4", action="store_true",
                     help="default run: skip the nested C4 evaluation-pass measurement")
+    ap.add_argument("--no-epoch", action="store_true",
+                    help="default run: skip the nested SDCA epoch measurement")
+    ap.add_argument("--epoch-steps", type=int, default=2)
+    ap.add_argument("--epoch-warmup", type=int, default=1)
     ap.add_argument("--c4-steps", type=int, default=10)
     # GPU clocks keep rising over the first few dozen passes of 8 ms.
     ap.add_argument("--c4-warmup", type=int, default=15)
@@ -401,13 +406,15 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
     return result
 
 
-def bench_epoch(cfg, args, torch, sd):
+def bench_epoch(cfg, args, torch, sd, steps=None, warmup=None):
     """Times SDCA epochs (sdca_epoch_features) over the reference solver's
     orders: `warmup` untimed epochs from W = 0, A = 0, then `steps` timed ones
     (each call ends with a host synchronisation); value = examples per second."""
     import numpy as np
-    steps = cfg["steps"] if args.steps is None else args.steps
-    warmup = cfg["warmup"] if args.warmup is None else args.warmup
+    if steps is None:
+        steps = cfg["steps"] if args.steps is None else args.steps
+    if warmup is None:
+        warmup = cfg["warmup"] if args.warmup is None else args.warmup
     dev = torch.device("cuda:0")
     X, _, labels, _ = make_eval_input(cfg, torch, dev)
     n, m, d = cfg["n"], cfg["m"], cfg["d"]
@@ -680,6 +687,15 @@ def main():
         result["c4"] = {key: ev[key] for key in ("value", "unit", "ms_per_step", "steps", "warmup",
                                                  "dtype", "config", "roofline", "roofline_pass",
                                                  "eval", "cpu_baseline") if key in ev}
+    if args.config == "c2" and not args.no_epoch:
+        # The epoch row (the solver's inner loop over the prox operators) on
+        # the C4 shape, nested likewise, with its own step counts.
+        torch.cuda.empty_cache()
+        ep = bench_epoch(CONFIGS["c4epoch"], args, torch, sd, steps=args.epoch_steps,
+                         warmup=args.epoch_warmup)
+        result["c4epoch"] = {key: ep[key] for key in ("value", "unit", "ms_per_step", "steps",
+                                                      "warmup", "dtype", "config", "roofline",
+                                                      "note", "cpu_baseline") if key in ep}
     print(json.dumps(result))
 
 

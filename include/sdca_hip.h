@@ -264,19 +264,20 @@ int sdca_eval_kernel(const sdca_objective* objs, int n_obj,
  *   labels: n labels in [0, m); order: count example indices in [0, n), or
  *      NULL for 0..count-1; norms: n values ||x_i||^2 in the data type, or
  *      NULL (computed, scratch.h:27-41).
- * Device pointers; (data, result) one of (F32, F32), (F32, F64), (F64, F64);
- * m at most 16384 (fp32) or 8192 (fp64).  Returns SDCA_ERR_LABELS (after
- * the epoch, which read such entries as 0) for an index or label out of
- * range.
+ * Device pointers on `stream` (flags 0), or host arrays with SDCA_HOST_PTR
+ * (staged through device memory for the call, W and A copied back); (data,
+ * result) one of (F32, F32), (F32, F64), (F64, F64); m at most 16384 (fp32)
+ * or 8192 (fp64).  Returns SDCA_ERR_LABELS (after the epoch, which read such
+ * entries as 0) for an index or label out of range.
  */
 int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result,
                         int64_t d, int64_t m, int64_t n, const void* X, void* W, void* A,
                         const int64_t* labels, const int64_t* order, int64_t count,
-                        const void* norms, void* stream);
+                        const void* norms, unsigned flags, void* stream);
 
 /*
  * The reference solver's example order for epoch `epoch` (0-based) of a
- * solve over n examples (solver.h:75-92, 108-112: a default-seeded
+ * solve over n examples (solver.h:59, 75-79, 96-100: a default-seeded
  * std::minstd_rand, std::shuffle of 0..n-1 once per epoch): n indices into
  * the host array `order`.  Host only.
  */

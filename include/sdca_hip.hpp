@@ -507,6 +507,38 @@ inline void evaluate_dataset(const Context& ctx, Dataset& d,
   detail::fill(d.evals.back(), ctx, rec, acc);
 }
 
+// One epoch of solve()'s example loop (solver.h:43-47) on the GPU:
+// update_variables (solver/update.h:52-85) for each example index in
+// [first, last) - the solver's examples_ after begin_epoch's shuffle - for a
+// feature input with multiclass output and one of the six multiclass
+// objectives (another objective fails with SDCA_ERR_NOT_IMPLEMENTED).
+// ctx.primal_variables and ctx.dual_variables are updated in place, through
+// host staging per call; scratch.norms (scratch.h:27-41) are used when
+// filled.  The maintainer's switch in solve():
+//   begin_epoch();
+//   sdca::hip::update_epoch(ctx_, scratch_, examples_.begin(), examples_.end());
+//   end_epoch();
+template <typename Data, typename Context, typename Iterator>
+inline void update_epoch(Context& ctx, sdca::solver_scratch<Data, sdca::feature_input>& scratch,
+                         Iterator first, Iterator last) {
+  typedef typename Context::result_type Result;
+  const auto& d = ctx.train;
+  const std::int64_t m = static_cast<std::int64_t>(d.num_classes());
+  const std::int64_t n = static_cast<std::int64_t>(d.num_examples());
+  const std::int64_t dim = static_cast<std::int64_t>(d.in.num_dimensions);
+  std::vector<std::int64_t> labels(d.out.labels.begin(), d.out.labels.end());
+  std::vector<std::int64_t> order;
+  for (Iterator it = first; it != last; ++it) order.push_back(static_cast<std::int64_t>(*it));
+  const sdca_objective ob = detail::objective_of<typename Context::objective_type>::get(ctx.objective);
+  const Data* norms = scratch.norms.size() == static_cast<std::size_t>(n) ? scratch.norms.data()
+                                                                         : nullptr;
+  detail::check(sdca_epoch_features(&ob, detail::dtype<Data>::value, detail::dtype<Result>::value,
+                                    dim, m, n, d.in.features, ctx.primal_variables,
+                                    ctx.dual_variables, labels.data(), order.data(),
+                                    static_cast<std::int64_t>(order.size()), norms,
+                                    SDCA_HOST_PTR, nullptr));
+}
+
 // W = W0 + X A' (eval_recompute_primal, eval/core.h:148-182): X is d x n,
 // A m x n, W0 (may be null) and W d x m, column-major.
 template <typename Data>

@@ -393,36 +393,55 @@ def epoch_order(n, epoch):
 def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None):
     """One SDCA epoch on feature input (update_variables for each example of
     `order`, update.h:52-85) for a multiclass objective (name, c, gamma, k):
-    X (n, d), W (m, d), A (n, m) CUDA tensors, W and A updated in place and
-    returned.  order: example indices (None: 0..n-1), e.g. epoch_order(n, e);
-    norms: (n,) squared row norms of X, or None."""
+    X (n, d), W (m, d), A (n, m), W and A updated in place and returned.
+    CUDA tensors run on torch's current stream; numpy arrays (C-contiguous,
+    X's dtype) go through the host-staging path.  order: example indices
+    (None: 0..n-1), e.g. epoch_order(n, e); norms: (n,) squared row norms of
+    X, or None."""
     lib = library()
-    if not _is_torch(X) or not X.is_cuda:
-        raise SdcaError(2, "epoch_features takes CUDA tensors")
-    import torch
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(W.shape[0])
-    _need(X, "X", (n, d), X)
-    _need(W, "W", (m, d), X)
-    _need(A, "A", (n, m), X)
-    _need(norms, "norms", (n,), X)
-    data = _dtype_code(X)
-    res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
-    lab = torch.as_tensor(labels, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
-    if lab.shape[0] != n:
-        raise SdcaError(2, f"labels: expected {n} entries, got {lab.shape[0]}")
-    od = None
-    if order is not None:
-        od = torch.as_tensor(order, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
-    count = n if od is None else int(od.shape[0])
     objarr = _objs([obj])
     lib.sdca_epoch_features.restype = ctypes.c_int
+    if _is_torch(X):
+        if not X.is_cuda:
+            raise SdcaError(2, "epoch_features takes CUDA tensors or numpy arrays")
+        import torch
+        _need(X, "X", (n, d), X)
+        _need(W, "W", (m, d), X)
+        _need(A, "A", (n, m), X)
+        _need(norms, "norms", (n,), X)
+        lab = torch.as_tensor(labels, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
+        od = None
+        if order is not None:
+            od = torch.as_tensor(order, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
+        flags, stream = 0, _stream_ptr()
+        ptr = _ptr
+    else:
+        for name, a, shape in (("X", X, (n, d)), ("W", W, (m, d)), ("A", A, (n, m)),
+                               ("norms", norms, (n,))):
+            if a is None:
+                continue
+            if (not isinstance(a, np.ndarray) or a.dtype != X.dtype or tuple(a.shape) != shape
+                    or not a.flags.c_contiguous):
+                raise SdcaError(2, f"{name}: expected a C-contiguous {X.dtype} array {shape}")
+        lab = np.ascontiguousarray(labels, dtype=np.int64).reshape(-1)
+        od = None if order is None else np.ascontiguousarray(order, dtype=np.int64).reshape(-1)
+        flags, stream = HOST_PTR, None
+
+        def ptr(a):
+            return None if a is None else a.ctypes.data
+    data = _dtype_code(X)
+    res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
+    if lab.shape[0] != n:
+        raise SdcaError(2, f"labels: expected {n} entries, got {lab.shape[0]}")
+    count = n if od is None else int(od.shape[0])
     rc = lib.sdca_epoch_features(objarr, ctypes.c_int(data), ctypes.c_int(res), ctypes.c_int64(d),
-                                 ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(_ptr(X)),
-                                 ctypes.c_void_p(_ptr(W)), ctypes.c_void_p(_ptr(A)),
-                                 ctypes.c_void_p(_ptr(lab)), ctypes.c_void_p(_ptr(od)),
-                                 ctypes.c_int64(count), ctypes.c_void_p(_ptr(norms)),
-                                 _stream_ptr())
+                                 ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(ptr(X)),
+                                 ctypes.c_void_p(ptr(W)), ctypes.c_void_p(ptr(A)),
+                                 ctypes.c_void_p(ptr(lab)), ctypes.c_void_p(ptr(od)),
+                                 ctypes.c_int64(count), ctypes.c_void_p(ptr(norms)),
+                                 ctypes.c_uint(flags), stream)
     if rc != 0:
         raise SdcaError(rc, lib.sdca_last_error().decode())
     return W, A

@@ -888,7 +888,7 @@ int sdca_epoch_order(int64_t n, int64_t epoch, int64_t* order) {
 int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result, int64_t d,
                         int64_t m, int64_t n, const void* X, void* W, void* A,
                         const int64_t* labels, const int64_t* order, int64_t count,
-                        const void* norms, void* stream_ptr) {
+                        const void* norms, unsigned flags, void* stream_ptr) {
   using namespace sdca_gpu;
   g_last_error.clear();
   if (!obj) return fail(SDCA_ERR_ARG_NULL, "obj must not be NULL");
@@ -914,6 +914,17 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   if (!X || !W || !A || !labels) return fail(SDCA_ERR_ARG_NULL, "X, W, A and labels must not be NULL");
   if (count == 0) return SDCA_OK;
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const bool host = (flags & SDCA_HOST_PTR) != 0;
+  const size_t es = dtype_size(data);
+  DeviceBuffer dx, dw, da, dl, dord, dnorm;
+  if (host) {
+    if ((rc = stage_in(X, es * d * n, dx, stream))) return rc;
+    if ((rc = stage_in(W, es * d * m, dw, stream))) return rc;
+    if ((rc = stage_in(A, es * m * n, da, stream))) return rc;
+    if ((rc = stage_in(labels, sizeof(int64_t) * n, dl, stream))) return rc;
+    if (order && (rc = stage_in(order, sizeof(int64_t) * count, dord, stream))) return rc;
+    if (norms && (rc = stage_in(norms, es * n, dnorm, stream))) return rc;
+  }
   void* ws = nullptr;
   if ((rc = workspace(stream, 4, epoch_workspace_bytes(data, d, m, n, norms != nullptr), &ws)))
     return rc;
@@ -927,17 +938,23 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   a.d = d;
   a.m = m;
   a.n = n;
-  a.X = X;
-  a.W = W;
-  a.A = A;
-  a.labels = labels;
-  a.order = order;
+  a.X = host ? dx.ptr : X;
+  a.W = host ? dw.ptr : W;
+  a.A = host ? da.ptr : A;
+  a.labels = host ? static_cast<const int64_t*>(dl.ptr) : labels;
+  a.order = host && order ? static_cast<const int64_t*>(dord.ptr) : order;
   a.count = count;
-  a.norms = norms;
+  a.norms = host && norms ? dnorm.ptr : norms;
   a.ws = ws;
   a.stream = stream;
   int* flag = nullptr;
   SDCA_HIP_TRY(launch_epoch(a, &flag), "SDCA epoch kernels");
+  if (host) {
+    SDCA_HIP_TRY(hipMemcpyAsync(W, dw.ptr, es * d * m, hipMemcpyDeviceToHost, stream),
+                 "hipMemcpyAsync(D2H)");
+    SDCA_HIP_TRY(hipMemcpyAsync(A, da.ptr, es * m * n, hipMemcpyDeviceToHost, stream),
+                 "hipMemcpyAsync(D2H)");
+  }
   int bad = 0;
   SDCA_HIP_TRY(hipMemcpyAsync(&bad, flag, sizeof(int), hipMemcpyDeviceToHost, stream),
                "hipMemcpyAsync(D2H)");

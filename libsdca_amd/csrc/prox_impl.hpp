@@ -533,7 +533,12 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
       lds_col + static_cast<int>(threadIdx.x) % G, lds_dummy);
 }
 
-template <int G, int C, int KM, class D, class R>
+// LDS_FALLBACK: the variable fixing over every slot (more candidates than
+// the candidate registers hold) keeps its working copy in the column's LDS
+// slots (the column kernels, whose registers set the occupancy) or in C
+// registers (false: the epoch's single workgroup, where that case is common
+// in the first epoch and registers are plentiful).
+template <int G, int C, int KM, class D, class R, bool LDS_FALLBACK = true>
 __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
                                         const ProxParamsT<R>& pp, D* lds_col, D* lds_dummy) {
   const int k = pp.k;
@@ -587,8 +592,8 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   const R hi = rhs / K;
   // More than G * kCandSlots candidates is rare for the prox inputs: the LDS
   // working copy keeps the kernel's register peak at the candidate path's.
-  KnapState<R> st = topk_knapsack<G, C, L, D, R, true>(v, top, m, nvalid, kth, hi, rhs, lds_col,
-                                                        lds_dummy);
+  KnapState<R> st = topk_knapsack<G, C, L, D, R, LDS_FALLBACK>(v, top, m, nvalid, kth, hi, rhs,
+                                                                lds_col, lds_dummy);
   if (!constant) {
     // is_topk_simplex_lt (topk_simplex.h:9-27), is_topk_simplex_biased_lt
     // (topk_simplex_biased.h:9-28), over U = [first, t.first)

@@ -326,7 +326,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
           pp.op = op;
           pp.p = 0;
           const ColThr<R> th = simplex
-              ? topk_family<G, C, KM, D, R>(vq, mp, nvalid, pp, cb, ld)
+              ? topk_family<G, C, KM, D, R, false>(vq, mp, nvalid, pp, cb, ld)
               : knap_family<G, C, D, R>(vq, mp, nvalid, pp);
           if (tid == 0) {
             sh_slow = th.slow ? 1 : 0;

@@ -108,9 +108,72 @@ int run_features(const Obj<float, double>& obj, int64_t d, int64_t m, int64_t n,
   return 0;
 }
 
+// One epoch over `order` with one objective: the reference's own loop of
+// update_variables (solver.h:43-47, solver/update.h:52-85) on ctx_ref,
+// sdca::hip::update_epoch on ctx_gpu, both from the given W and A.
+template <template <class, class> class Obj>
+int run_epoch(const Obj<float, double>& obj, int64_t d, int64_t m, int64_t n, const float* X,
+              const int64_t* labels, const int64_t* order, int64_t count, float* W_gpu,
+              float* A_gpu, float* W_ref, float* A_ref) {
+  typedef sdca::solver_context<float, double, sdca::feature_input, sdca::multiclass_output, Obj>
+      Ctx;
+  auto make = [&](float* A, float* W) {
+    return Ctx(sdca::make_dataset_train<double>(
+                   sdca::make_input_feature(static_cast<sdca::size_type>(d),
+                                            static_cast<sdca::size_type>(n), X),
+                   output(std::false_type(), m, labels, nullptr, n)),
+               Obj<float, double>(obj), A, W, nullptr);
+  };
+  Ctx ctx_ref = make(A_ref, W_ref);
+  Ctx ctx_gpu = make(A_gpu, W_gpu);
+  sdca::solver_scratch<float, sdca::feature_input> scratch;
+  scratch.init(ctx_ref.train);
+  std::vector<sdca::size_type> examples(order, order + count);
+  for (auto i : examples) sdca::update_variables(i, ctx_ref, scratch);
+  try {
+    sdca::hip::update_epoch(ctx_gpu, scratch, examples.begin(), examples.end());
+  } catch (const sdca::hip::error& e) {
+    return e.status();
+  }
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+// kind: a multiclass sdca_objective_kind (0..5).  W_* (m x d) and A_* (n x m)
+// hold the starting point and receive each side's result.  Returns 0, or the
+// drop-in's error status.
+int dropin_update_epoch(int kind, double c, double gamma, int64_t k, int64_t d, int64_t m,
+                        int64_t n, const float* X, const int64_t* labels, const int64_t* order,
+                        int64_t count, float* W_gpu, float* A_gpu, float* W_ref,
+                        float* A_ref) {
+  const sdca::size_type kk = static_cast<sdca::size_type>(k);
+  switch (kind) {
+    case SDCA_OBJ_HINGE_TOPK:
+      return run_epoch(sdca::l2_hinge_topk<float, double>(c, kk), d, m, n, X, labels, order,
+                       count, W_gpu, A_gpu, W_ref, A_ref);
+    case SDCA_OBJ_HINGE_TOPK_SMOOTH:
+      return run_epoch(sdca::l2_hinge_topk_smooth<float, double>(c, gamma, kk), d, m, n, X,
+                       labels, order, count, W_gpu, A_gpu, W_ref, A_ref);
+    case SDCA_OBJ_TOPK_HINGE:
+      return run_epoch(sdca::l2_topk_hinge<float, double>(c, kk), d, m, n, X, labels, order,
+                       count, W_gpu, A_gpu, W_ref, A_ref);
+    case SDCA_OBJ_TOPK_HINGE_SMOOTH:
+      return run_epoch(sdca::l2_topk_hinge_smooth<float, double>(c, gamma, kk), d, m, n, X,
+                       labels, order, count, W_gpu, A_gpu, W_ref, A_ref);
+    case SDCA_OBJ_ENTROPY:
+      return run_epoch(sdca::l2_entropy<float, double>(c), d, m, n, X, labels, order, count,
+                       W_gpu, A_gpu, W_ref, A_ref);
+    case SDCA_OBJ_ENTROPY_TOPK:
+      return run_epoch(sdca::l2_entropy_topk<float, double>(c, kk), d, m, n, X, labels, order,
+                       count, W_gpu, A_gpu, W_ref, A_ref);
+    default:
+      return -2;
+  }
+}
+
 
 // kind: sdca_objective_kind; multilabel when offsets != NULL.  rec_*: 14
 // doubles (training record, then test record: primal, dual, primal_loss,

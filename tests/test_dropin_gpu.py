@@ -134,3 +134,51 @@ def test_prox_dropin(cuda, oracle, dropin, op, dtype, m, k):
     from oracle import binding
     oracle.prox(name, want, result=result, params=binding.make_params(**kw))
     assert np.array_equal(r, want)
+
+
+EPOCH_OBJS = [("l2_hinge_topk", 1.0, 1.0, 3), ("l2_hinge_topk_smooth", 1.0, 0.5, 3),
+              ("l2_topk_hinge", 1.0, 1.0, 2), ("l2_topk_hinge_smooth", 0.7, 0.5, 2),
+              ("l2_entropy", 1.0, 1.0, 1), ("l2_entropy_topk", 1.5, 1.0, 3)]
+ORACLE_EPOCH = {"l2_hinge_topk": "hinge_topk", "l2_hinge_topk_smooth": "hinge_topk_smooth",
+                "l2_topk_hinge": "topk_hinge", "l2_topk_hinge_smooth": "topk_hinge_smooth",
+                "l2_entropy": "entropy", "l2_entropy_topk": "entropy_topk"}
+
+
+@pytest.mark.parametrize("obj", EPOCH_OBJS)
+def test_dropin_update_epoch(dropin, oracle, obj):
+    """sdca::hip::update_epoch (host staging through the C ABI) against the
+    reference's own loop of update_variables over the solver's order, on
+    copies of one reference context (float data, double results), two epochs
+    from a non-zero start.  The scores round differently on each side (MKL's
+    sgemv, the block GEMM), so the bound is the sum of the two pinned ones
+    (reference vs restatement, restatement vs GPU: 4 spreads of the
+    restatement's two roundings plus 8 ulps each)."""
+    import libsdca_amd as sd
+    rng = np.random.default_rng(17)
+    n, d, m = 150, 24, 11
+    X = rng.standard_normal((n, d))
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    X = X.astype(np.float32)
+    y = rng.integers(0, m, n).astype(np.int64)
+    W0 = np.zeros((m, d), np.float32)
+    A0 = np.zeros((n, m), np.float32)
+    Wg, Ag, Wr, Ar = W0.copy(), A0.copy(), W0.copy(), A0.copy()
+    orders = [sd.epoch_order(n, e) for e in range(2)]
+    for order in orders:
+        rc = dropin.dropin_update_epoch(
+            ctypes.c_int(KIND[obj[0]]), ctypes.c_double(obj[1]), ctypes.c_double(obj[2]),
+            ctypes.c_int64(obj[3]), ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
+            ptr(X), ptr(y), ptr(order), ctypes.c_int64(len(order)), ptr(Wg), ptr(Ag), ptr(Wr),
+            ptr(Ar))
+        assert rc == 0, rc
+    name = (ORACLE_EPOCH[obj[0]],) + tuple(obj[1:])
+    Wo, Ao, Wv, Av = W0.copy(), A0.copy(), W0.copy(), A0.copy()
+    for order in orders:
+        oracle.epoch_features(name, X, Wo, Ao, y, order, result=1)
+        oracle.epoch_features(name, X, Wv, Av, y, order, result=1, reverse=True)
+    eps = np.finfo(np.float32).eps
+    for what, g, r, o, v in (("W", Wg, Wr, Wo, Wv), ("A", Ag, Ar, Ao, Av)):
+        tol = 8 * float(np.abs(o - v).max()) + 16 * eps * max(1.0, float(np.abs(o).max()))
+        err = float(np.abs(g - r).max())
+        assert err <= tol, f"{obj[0]} {what}: |drop-in - reference| {err:.3e} > {tol:.3e}"
+    assert np.abs(Ar).max() > 0.01

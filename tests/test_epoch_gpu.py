@@ -145,3 +145,42 @@ def test_epoch_duality_gap_closes(cuda):
     print("relative gaps", gaps)
     assert all(g > -1e-5 for g in gaps)
     assert gaps[-1] < gaps[0] and gaps[-1] < 0.5 * gaps[0]
+
+
+@pytest.mark.parametrize("obj", [OBJS[1], OBJS[2], OBJS[4], OBJS[5]])
+@pytest.mark.parametrize("m", [1500, 3000])
+def test_epoch_wide_rows(cuda, oracle, obj, m):
+    """Rows above 1024 classes (eight register slots per thread, delta rows in
+    global memory) and above 2048 (the vector in LDS, no register slots)."""
+    check(oracle, cuda, obj, np.float32, 0, 160, 48, m, 31 + m)
+
+
+@pytest.mark.parametrize("dtype,result", [(np.float32, 1), (np.float64, 1)])
+def test_epoch_wide_rows_double(cuda, oracle, dtype, result):
+    check(oracle, cuda, OBJS[1], dtype, result, 160, 48, 1500, 77)
+
+
+def test_epoch_large_k(cuda, oracle):
+    """k > 8 for the top-k hinge: the sorted-column thresholds for every
+    example."""
+    check(oracle, cuda, ("hinge_topk", 1.0, 1.0, 11), np.float32, 0, 200, 32, 40, 13)
+
+
+def test_epoch_repeated_examples(cuda, oracle):
+    """An order that repeats examples, next to each other inside a block and
+    across a block boundary (positions 31 and 32): each occurrence must see the
+    previous one's update of a_i and W, as in the sequential loop."""
+    import libsdca_amd as sd
+    n, m = 120, 15
+    X, y = problem(np.float32, n, 24, m, 21)
+    base = [int(i) for i in sd.epoch_order(n, 0)]
+    order = base[:31] + [base[30], base[30]] + base[31:50] + [base[49]] * 3 + base[50:90]
+    for obj in (OBJS[1], OBJS[4]):
+        Wg, Ag = gpu_epochs(cuda, obj, X, y, m, 0, [np.array(order, np.int64)])
+        Wo, Ao = oracle_epochs(oracle, obj, X, y, m, 0, [np.array(order, np.int64)])
+        Wv, Av = oracle_epochs(oracle, obj, X, y, m, 0, [np.array(order, np.int64)],
+                               reverse=True)
+        eps = np.finfo(np.float32).eps
+        for g, o, v in ((Wg, Wo, Wv), (Ag, Ao, Av)):
+            tol = 4 * float(np.abs(o - v).max()) + 8 * eps * max(1.0, float(np.abs(o).max()))
+            assert float(np.abs(g - o).max()) <= tol
