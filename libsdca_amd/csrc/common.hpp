@@ -196,6 +196,35 @@ __device__ inline double lambert_w_exp(double x) {
   return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
 }
 
+// The same values with every branch's initial part computed and the
+// lane's own selected (no divergent branches): for callers that evaluate a
+// few independent points per thread in one latency chain, where branches
+// around each point would serialise them.
+__device__ inline float lambert_w_exp_nb(float x) {
+  const int br = x > -1.0f ? (x <= 8.0f ? 0 : (x <= 536870912.0f ? 1 : 2))
+                           : (x > -18.0f ? 3 : 4);
+  const float w0 = lw_step5(x, 1.0f);
+  const float w1 = x - logf(x);
+  const float w3 = exp_approx(x);
+  const float w = br == 0 ? w0 : (br == 1 ? w1 : (br == 3 ? w3 : 0.0f));
+  const float e = expf(br == 4 ? x : x - w);
+  const float r = lw_step5(w, br == 1 ? x : e);
+  return br == 2 ? x : (br == 4 ? ((x > -104.0f) ? e : 0.0f) : r);
+}
+
+__device__ inline double lambert_w_exp_nb(double x) {
+  const int br = x > 0.0 ? (x <= 4.0 ? 0 : (x <= 576460752303423488.0 ? 1 : 2))
+                         : (x > -20.0 ? 3 : (x > -36.0 ? 4 : 5));
+  const double w0 = lw_step5(x, 1.0);
+  const double w1 = lw_step5(x - log(x), x);
+  const double w4 = exp_approx(x);
+  const double w3 = lw_step5(w4, exp_approx(x - w4));
+  const double w = br == 0 ? w0 : (br == 1 ? w1 : (br == 3 ? w3 : (br == 4 ? w4 : 0.0)));
+  const double e = exp_fast(br == 5 ? x : x - w);
+  const double r = lw_step5(w, e);
+  return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
+}
+
 // W(exp(y - dt)) from w = W(exp(y)) by the Taylor series in dt: the
 // derivatives of W(e^y) are g1 = w / (1 + w), g2 = w / (1 + w)^3 and
 // g3 = w (1 - 2w) / (1 + w)^5, so for |dt| <= 1e-4 the omitted fourth-order

@@ -28,10 +28,30 @@ namespace sdca_gpu {
 // (sum_lambert_w_exp, lambert.h:220-237).
 // wout (optional, the wave's LDS array of R): each pass leaves its W values
 // there, for the output map.
+// NT > 64 (a whole workgroup on one column: a few entries per thread, one
+// wave per SIMD, the passes latency-bound) takes the thread's entries four at
+// a time with the branch-free W so that their chains overlap: loads read a
+// clamped index, entries past m add zero, and the sums keep their order.
+constexpr int kLwBlock = 4;
+
 template <class D, class R, int NT = 64>
 __device__ inline R lw_sum0(const D* s, int m, int p, int lane, R ta, R tb) {
   R a0(0);
-  for (int i = lane; i < m; i += NT) a0 += lambert_w_exp(static_cast<R>(s[i]) + (i < p ? ta : tb));
+  if constexpr (NT > 64) {
+    for (int i0 = lane; i0 < m; i0 += kLwBlock * NT) {
+      R v[kLwBlock];
+#pragma unroll
+      for (int u = 0; u < kLwBlock; ++u) {
+        const int i = i0 + u * NT;
+        const int ic = i < m ? i : m - 1;
+        v[u] = lambert_w_exp_nb(static_cast<R>(s[ic]) + (ic < p ? ta : tb));
+      }
+#pragma unroll
+      for (int u = 0; u < kLwBlock; ++u) a0 += (i0 + u * NT < m) ? v[u] : R(0);
+    }
+  } else {
+    for (int i = lane; i < m; i += NT) a0 += lambert_w_exp(static_cast<R>(s[i]) + (i < p ? ta : tb));
+  }
   return group_sum<NT>(a0);
 }
 
@@ -40,11 +60,30 @@ template <class D, class R, int NT = 64>
 __device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1,
                                 R* wout = nullptr) {
   R a0(0), a1(0);
-  for (int i = lane; i < m; i += NT) {
-    const R v = lambert_w_exp(static_cast<R>(s[i]) + t);
-    if (wout) wout[i] = v;
-    a0 += v;
-    a1 += div_near(v, R(1) + v);
+  if constexpr (NT > 64) {
+    for (int i0 = lane; i0 < m; i0 += kLwBlock * NT) {
+      R v[kLwBlock];
+#pragma unroll
+      for (int u = 0; u < kLwBlock; ++u) {
+        const int i = i0 + u * NT;
+        v[u] = lambert_w_exp_nb(static_cast<R>(s[i < m ? i : m - 1]) + t);
+      }
+#pragma unroll
+      for (int u = 0; u < kLwBlock; ++u) {
+        const int i = i0 + u * NT;
+        const bool ok = i < m;
+        if (wout && ok) wout[i] = v[u];
+        a0 += ok ? v[u] : R(0);
+        a1 += ok ? div_near(v[u], R(1) + v[u]) : R(0);
+      }
+    }
+  } else {
+    for (int i = lane; i < m; i += NT) {
+      const R v = lambert_w_exp(static_cast<R>(s[i]) + t);
+      if (wout) wout[i] = v;
+      a0 += v;
+      a1 += div_near(v, R(1) + v);
+    }
   }
   group_sums<NT>(a0, a1);
   f0 = a0;
@@ -61,15 +100,39 @@ __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, 
     tb = t;
   }
   R a0(0), a1(0), a2(0), a3(0);
-  for (int i = lane; i < m; i += NT) {
-    const R v = lambert_w_exp(static_cast<R>(s[i]) + (i < p ? t : tb));
-    if (wout) wout[i] = v;
-    const R d = R(1) + v;
-    const R d3 = d * d * d;
-    a0 += v;
-    a1 += div_near(v, d);
-    a2 += div_near(v, d3);
-    a3 += div_near(v * (R(1) - R(2) * v), d3 * d * d);
+  if constexpr (NT > 64) {
+    for (int i0 = lane; i0 < m; i0 += kLwBlock * NT) {
+      R v[kLwBlock];
+#pragma unroll
+      for (int u = 0; u < kLwBlock; ++u) {
+        const int i = i0 + u * NT;
+        const int ic = i < m ? i : m - 1;
+        v[u] = lambert_w_exp_nb(static_cast<R>(s[ic]) + (ic < p ? t : tb));
+      }
+#pragma unroll
+      for (int u = 0; u < kLwBlock; ++u) {
+        const int i = i0 + u * NT;
+        const bool ok = i < m;
+        if (wout && ok) wout[i] = v[u];
+        const R d = R(1) + v[u];
+        const R d3 = d * d * d;
+        a0 += ok ? v[u] : R(0);
+        a1 += ok ? div_near(v[u], d) : R(0);
+        a2 += ok ? div_near(v[u], d3) : R(0);
+        a3 += ok ? div_near(v[u] * (R(1) - R(2) * v[u]), d3 * d * d) : R(0);
+      }
+    }
+  } else {
+    for (int i = lane; i < m; i += NT) {
+      const R v = lambert_w_exp(static_cast<R>(s[i]) + (i < p ? t : tb));
+      if (wout) wout[i] = v;
+      const R d = R(1) + v;
+      const R d3 = d * d * d;
+      a0 += v;
+      a1 += div_near(v, d);
+      a2 += div_near(v, d3);
+      a3 += div_near(v * (R(1) - R(2) * v), d3 * d * d);
+    }
   }
   group_sums<NT>(a0, a1, a2, a3);
   f0 = a0;
@@ -112,9 +175,12 @@ __device__ inline R log_w_inverse_or_min(R w) {
 // ds_out (if given) receives the first two t-derivatives of that s with
 // the sign of a step down in t: sum_i W / (1 + W) / alpha and
 // sum_i W / (1 + W)^3 / alpha.
+// noise_out (if given) is set when |g(t)| is within 16 ulps of the sum it
+// is formed from: the step is then below what the sums' rounding resolves.
 template <class D, class R, int NT = 64>
 __device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, R& lo, R& hi,
-                                    R* s_out, R* wout = nullptr, R* ds_out = nullptr) {
+                                    R* s_out, R* wout = nullptr, R* ds_out = nullptr,
+                                    bool* noise_out = nullptr) {
   R f0, f1, f2, f3;
   lw_sums4<D, R, NT>(s, m, lane, -t, f0, f1, f2, f3, -1, R(0), wout);
   if (s_out) *s_out = f0 / alpha;
@@ -131,6 +197,7 @@ __device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, 
     f2 += v / d3;
     f3 += v * (R(1) - R(2) * v) / (d3 * d * d);
   }
+  if (noise_out) *noise_out = fabs(f0 - alpha) <= R(16) * num<R>::eps() * (fabs(f0) + alpha);
   f0 -= alpha;
   if (f0 > R(0)) lo = (t > lo) ? t : lo;
   else if (f0 < R(0)) hi = (t < hi) ? t : hi;
@@ -170,7 +237,11 @@ __device__ inline bool lse_start(const D* s, int m, int p, R c, R e, R mx, R rhs
 // Thresholds (t, 0, hi) of one column whose copy is in s[0, m); entries of U
 // are overwritten with -inf.  With wl (the wave's LDS array of R), the last
 // pass's W values are left there and *tw receives the t they were taken at.
-template <class D, class R, int NT = 64>
+// NOISE_STOP (the epoch's solves): the uncapped iteration also ends once
+// g(t) is at the rounding level of its sums (the reference's test, a step
+// of at most epsilon, then waits for t to stop moving between neighbouring
+// floats, which takes several more passes and lands within that level too).
+template <class D, class R, int NT = 64, bool NOISE_STOP = false>
 __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_out,
                                    R& hi_out, R* wl = nullptr, R* tw = nullptr) {
   const R eps_r = num<R>::eps();
@@ -203,12 +274,18 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
   // Where every value lies well below the log-sum-exp bound, the iteration
   // starts there (one single-precision pass instead of about three from
   // t = max on U(-10, 10) columns); the bracket is kept as it is.
+  // The epoch's solves (NOISE_STOP) start there whenever it lies inside the
+  // bracket: an upper bound of the root, nearer to it than t = max on their
+  // columns (about three passes instead of five).
   {
     R t_lse;
     const R top = (alpha > max) ? alpha : max;
-    if (lse_start<D, R, NT>(s, m, m, R(0), alpha, top, alpha, lane, t_lse) && t_lse > br_lo &&
-        t_lse < br_hi)
+    const bool close = lse_start<D, R, NT>(s, m, m, R(0), alpha, top, alpha, lane, t_lse);
+    if (close && t_lse > br_lo && t_lse < br_hi) {
       t = t_lse;
+    } else if (NOISE_STOP && t_lse > br_lo) {
+      t = (t_lse < br_hi) ? t_lse : br_hi;  // equal values put t_lse on br_hi
+    }
   }
   bool warm = false;
   if constexpr (sizeof(R) == 8) {
@@ -234,8 +311,11 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     const R t1 = t;
     if (tw) *tw = t;
     R ds[2];
-    const bool ok = guarded_step<D, R, NT>(s, m, lane, alpha, t, br_lo, br_hi, &sv, wl, ds);
+    bool noise = false;
+    const bool ok = guarded_step<D, R, NT>(s, m, lane, alpha, t, br_lo, br_hi, &sv, wl, ds,
+                                           NOISE_STOP ? &noise : nullptr);
     if (fabs(t1 - t) <= eps_r) break;
+    if (NOISE_STOP && ok && noise) break;
     // From a settled single-precision start a first step of at most 1e-6
     // leaves an order-4 correction of ~1e-24: the confirming pass is
     // skipped, and s (the pass's sum at t1) is carried to the final t by its
@@ -342,7 +422,9 @@ __device__ inline int bisection_count(R v) {
 
 // Thresholds t (block a) and t + c (block b) of one column in s[0, m), split p.
 // With wl, the last pass's W values are left there and *tw receives its t.
-template <class D, class R, int NT = 64>
+// NOISE_STOP: as for entbias_thresholds, the Householder steps also end
+// once f(t) is at the rounding level of its sums.
+template <class D, class R, int NT = 64, bool NOISE_STOP = false>
 __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R& t_out,
                                   R& c_out, R* wl = nullptr, R* tw = nullptr) {
   const R eps = num<R>::eps();
@@ -435,6 +517,7 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
     }
     t = (lb > ((t < ub) ? t : ub)) ? lb : ((t < ub) ? t : ub);
     if (fabs(t1 - t) <= eps) break;
+    if (NOISE_STOP && fabs(f1) <= R(16) * eps * (fabs(f1 + alpha) + alpha)) break;
   }
   t_out = t;
   c_out = c;

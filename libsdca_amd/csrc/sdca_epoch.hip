@@ -283,12 +283,12 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
       __syncthreads();
       const R alpha = c * static_cast<R>(norm2);
       R t, c2;
-      twoent_thresholds<D, R, G>(cb, m, 1, tid, alpha, t, c2);
+      twoent_thresholds<D, R, G, true>(cb, m, 1, tid, alpha, t, c2);
       const D map_a = D(1) / static_cast<D>(alpha);
       const D ta = static_cast<D>(t), tb = static_cast<D>(t + c2);
       const D na = static_cast<D>(-c), nbias = static_cast<D>(c / R(1));
       for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
-        const D x = clamp_ref(map_a * lambert_w_exp(getv(j, q) - (j == y ? ta : tb)), D(0), D(1));
+        const D x = clamp_ref(map_a * lambert_w_exp_nb(getv(j, q) - (j == y ? ta : tb)), D(0), D(1));
         setv(j, q, (j == y) ? na * x + nbias : na * x);
       });
     } else {
@@ -357,7 +357,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
         }
       } else {  // prox_topk_entropy_biased, alpha = c norm2
         R t, hi;
-        entbias_thresholds<D, R, G>(cb, mp, tid, ob.k, c * static_cast<R>(norm2), t, hi);
+        entbias_thresholds<D, R, G, true>(cb, mp, tid, ob.k, c * static_cast<R>(norm2), t, hi);
         if (tid == 0) {
           sh_t = t;
           sh_lo = R(0);
@@ -372,7 +372,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
         const bool off = j != y;
         const D x0 = getv(j, q);
         const D x = hinge ? clamp_ref(x0 - t, lo, hi)
-                          : clamp_ref(map_a * lambert_w_exp(x0 - t), D(0), hi);
+                          : clamp_ref(map_a * lambert_w_exp_nb(x0 - t), D(0), hi);
         if (off) setv(j, q, x);
         part += (ok && off) ? static_cast<R>(x) : R(0);
       });
