@@ -269,18 +269,30 @@ __device__ inline double lambert_w_exp_mixed(double x) {
 __device__ inline float lambert_w_exp_mixed(float x) { return lambert_w_exp(x); }
 
 // ---------------------------------------------------------------------------
-// Cross-lane exchange lane <-> lane ^ OFF inside a wave, all by VALU
-// operations (no LDS traffic): DPP quad permutations for OFF = 1, 2; DPP row
-// shifts by 4 (left for lanes with bit 2 clear, right for the others) for 4;
-// DPP row rotation by 8 for 8; v_permlane16_swap / v_permlane32_swap for 16
-// and 32.
+// Cross-lane exchange lane <-> lane ^ OFF inside a wave.  OFF = 1, 2: DPP
+// quad permutations (a VALU operand modifier).  Beyond, two forms:
+//  * VALU = false: ds_swizzle in xor mode for 4, 8, 16 and ds_bpermute for
+//    32.  They run on the LDS pipe, beside the VALU work: the form for the
+//    column kernels, whose many waves per SIMD are throughput-bound;
+//  * VALU = true: DPP row shifts by 4 (left for lanes with bit 2 clear,
+//    right for the others), DPP row rotation by 8, v_permlane16_swap /
+//    v_permlane32_swap for 16 and 32.  No LDS round trip (67 against about
+//    400 ns for a 64-lane sum chain): the form for one workgroup running a
+//    column alone, one wave per SIMD, latency-bound.
+// Both give lane ^ OFF, so a reduction has the same bits either way.
 // ---------------------------------------------------------------------------
-template <int OFF>
+template <int OFF, bool VALU = false>
 __device__ inline int xor_lane(int v) {
   if constexpr (OFF == 1) {
     return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
   } else if constexpr (OFF == 2) {
     return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (!VALU) {
+    if constexpr (OFF < 32) {
+      return __builtin_amdgcn_ds_swizzle(v, (OFF << 10) | 0x1F);  // and 0x1F, xor OFF
+    } else {
+      return __shfl_xor(v, OFF, 64);
+    }
   } else if constexpr (OFF == 4) {
     const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, false);  // row_shl:4
     const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
@@ -303,15 +315,15 @@ __device__ inline int xor_lane(int v) {
     }
   }
 }
-template <int OFF>
+template <int OFF, bool VALU = false>
 __device__ inline float xor_lane(float v) {
-  return __int_as_float(xor_lane<OFF>(__float_as_int(v)));
+  return __int_as_float(xor_lane<OFF, VALU>(__float_as_int(v)));
 }
-template <int OFF>
+template <int OFF, bool VALU = false>
 __device__ inline double xor_lane(double v) {
   const long long b = __double_as_longlong(v);
-  const int lo = xor_lane<OFF>(static_cast<int>(b & 0xffffffffll));
-  const int hi = xor_lane<OFF>(static_cast<int>(b >> 32));
+  const int lo = xor_lane<OFF, VALU>(static_cast<int>(b & 0xffffffffll));
+  const int hi = xor_lane<OFF, VALU>(static_cast<int>(b >> 32));
   return __longlong_as_double((static_cast<long long>(hi) << 32) |
                               (static_cast<long long>(static_cast<unsigned>(lo))));
 }
@@ -366,18 +378,24 @@ __device__ inline T workgroup_combine(T x, Op op) {
   return r;
 }
 
+// The lanes' part of a reduction over G <= 64 lanes (VALU: the exchange form).
+template <int G, bool VALU, class T>
+__device__ inline T lanes_sum(T x) {
+  if constexpr (G >= 64) x += xor_lane<32, VALU>(x);
+  if constexpr (G >= 32) x += xor_lane<16, VALU>(x);
+  if constexpr (G >= 16) x += xor_lane<8, VALU>(x);
+  if constexpr (G >= 8) x += xor_lane<4, VALU>(x);
+  if constexpr (G >= 4) x += xor_lane<2, VALU>(x);
+  if constexpr (G >= 2) x += xor_lane<1, VALU>(x);
+  return x;
+}
 template <int G, class T>
 __device__ inline T group_sum(T x) {
   if constexpr (G > 64) {
-    return workgroup_combine<G>(group_sum<64>(x), [](T a, T b) { return a + b; });
+    return workgroup_combine<G>(lanes_sum<64, true>(x), [](T a, T b) { return a + b; });
+  } else {
+    return lanes_sum<G, false>(x);
   }
-  if constexpr (G >= 64) x += xor_lane<32>(x);
-  if constexpr (G >= 32) x += xor_lane<16>(x);
-  if constexpr (G >= 16) x += xor_lane<8>(x);
-  if constexpr (G >= 8) x += xor_lane<4>(x);
-  if constexpr (G >= 4) x += xor_lane<2>(x);
-  if constexpr (G >= 2) x += xor_lane<1>(x);
-  return x;
 }
 // Several group sums in one exchange: each value reduced as group_sum<G>
 // would, the workgroup-wide ones through one pair of barriers for all of
@@ -405,7 +423,7 @@ __device__ inline void group_sums(T&... x) {
   static_assert(sizeof...(T) <= 8, "at most 8 values per exchange");
   if constexpr (G > 64) {
     __shared__ unsigned long long slots[kMaxGroupWaves][8];
-    ((x = group_sum<64>(x)), ...);
+    ((x = lanes_sum<64, true>(x)), ...);
     __syncthreads();  // the previous exchange's readers are done with the slots
     if ((threadIdx.x & 63) == 0) {
       const int w = static_cast<int>(threadIdx.x) >> 6;
@@ -420,42 +438,67 @@ __device__ inline void group_sums(T&... x) {
   }
 }
 
-template <int OFF, class T>
+template <int OFF, bool VALU, class T>
 __device__ inline T max_step(T x) {
-  T y = xor_lane<OFF>(x);
+  T y = xor_lane<OFF, VALU>(x);
   return (y > x) ? y : x;
 }
-template <int OFF, class T>
+template <int OFF, bool VALU, class T>
 __device__ inline T min_step(T x) {
-  T y = xor_lane<OFF>(x);
+  T y = xor_lane<OFF, VALU>(x);
   return (y < x) ? y : x;
+}
+template <int G, bool VALU, class T>
+__device__ inline T lanes_max(T x) {
+  if constexpr (G >= 64) x = max_step<32, VALU>(x);
+  if constexpr (G >= 32) x = max_step<16, VALU>(x);
+  if constexpr (G >= 16) x = max_step<8, VALU>(x);
+  if constexpr (G >= 8) x = max_step<4, VALU>(x);
+  if constexpr (G >= 4) x = max_step<2, VALU>(x);
+  if constexpr (G >= 2) x = max_step<1, VALU>(x);
+  return x;
+}
+template <int G, bool VALU, class T>
+__device__ inline T lanes_min(T x) {
+  if constexpr (G >= 64) x = min_step<32, VALU>(x);
+  if constexpr (G >= 32) x = min_step<16, VALU>(x);
+  if constexpr (G >= 16) x = min_step<8, VALU>(x);
+  if constexpr (G >= 8) x = min_step<4, VALU>(x);
+  if constexpr (G >= 4) x = min_step<2, VALU>(x);
+  if constexpr (G >= 2) x = min_step<1, VALU>(x);
+  return x;
 }
 template <int G, class T>
 __device__ inline T group_max(T x) {
   if constexpr (G > 64) {
-    return workgroup_combine<G>(group_max<64>(x), [](T a, T b) { return (b > a) ? b : a; });
+    return workgroup_combine<G>(lanes_max<64, true>(x), [](T a, T b) { return (b > a) ? b : a; });
+  } else {
+    return lanes_max<G, false>(x);
   }
-  if constexpr (G >= 64) x = max_step<32>(x);
-  if constexpr (G >= 32) x = max_step<16>(x);
-  if constexpr (G >= 16) x = max_step<8>(x);
-  if constexpr (G >= 8) x = max_step<4>(x);
-  if constexpr (G >= 4) x = max_step<2>(x);
-  if constexpr (G >= 2) x = max_step<1>(x);
-  return x;
 }
 template <int G, class T>
 __device__ inline T group_min(T x) {
   if constexpr (G > 64) {
-    return workgroup_combine<G>(group_min<64>(x), [](T a, T b) { return (b < a) ? b : a; });
+    return workgroup_combine<G>(lanes_min<64, true>(x), [](T a, T b) { return (b < a) ? b : a; });
+  } else {
+    return lanes_min<G, false>(x);
   }
-  if constexpr (G >= 64) x = min_step<32>(x);
-  if constexpr (G >= 32) x = min_step<16>(x);
-  if constexpr (G >= 16) x = min_step<8>(x);
-  if constexpr (G >= 8) x = min_step<4>(x);
-  if constexpr (G >= 4) x = min_step<2>(x);
-  if constexpr (G >= 2) x = min_step<1>(x);
-  return x;
 }
+// Exclusive prefix sum over the wave by DPP alone: each 16-lane row by row
+// shifts (a lane whose source lies before its row reads 0), then the row
+// totals carried by row_bcast:15 (into rows 1 and 3) and row_bcast:31 (into
+// rows 2 and 3).  For the workgroup-wide scan (latency-bound).
+__device__ inline int wave_exclusive_scan_dpp(int x) {
+  int incl = x;
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);  // row_shr:1
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return incl - x;
+}
+
 // Exclusive prefix sum over the group (lane order g = 0..G-1).
 template <int G>
 __device__ inline int group_exclusive_scan(int x, int g) {
@@ -463,7 +506,7 @@ __device__ inline int group_exclusive_scan(int x, int g) {
     // The wave's own scan plus the totals of the waves before it.
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
-    const int ex = group_exclusive_scan<64>(x, lane);
+    const int ex = wave_exclusive_scan_dpp(x);
     int* words = group_lds_words<int>();
     __syncthreads();
     if (lane == 63) words[wave] = ex + x;
@@ -473,19 +516,6 @@ __device__ inline int group_exclusive_scan(int x, int g) {
     return base + ex;
   }
   int incl = x;
-  if constexpr (G >= 16) {
-    // Inclusive scan of each 16-lane row by DPP row shifts (a lane whose
-    // source lies before its row reads 0), then the row totals carried by
-    // row_bcast:15 (into rows 1 and 3) and, for 64 lanes, row_bcast:31
-    // (into rows 2 and 3).
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);  // row_shr:1
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
-    if constexpr (G >= 32) incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);
-    if constexpr (G >= 64) incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xC, 0xF, false);
-    return incl - x;
-  }
   const int lane = static_cast<int>(threadIdx.x) & 63;
   if constexpr (G >= 2) { int y = xor_lane<1>(incl); if (g & 1) incl += y; }
   // After step s every lane holds the inclusive sum of its aligned block of
@@ -585,11 +615,11 @@ __device__ inline void bitonic_sort_desc(D (&x)[L]) {
   }
 }
 
-template <int OFF, int L, class D>
+template <int OFF, bool VALU, int L, class D>
 __device__ inline void top_merge_step(D (&top)[L]) {
   D other[L];
 #pragma unroll
-  for (int i = 0; i < L; ++i) other[i] = xor_lane<OFF>(top[i]);
+  for (int i = 0; i < L; ++i) other[i] = xor_lane<OFF, VALU>(top[i]);
   if constexpr (L == 16) {
     // Two descending lists: c_i = max(a_i, b_(L-1-i)) holds the L largest of
     // both and falls then rises (bitonic); a bitonic half-cleaner network
@@ -610,7 +640,12 @@ __device__ inline void top_merge(D (&top)[L]) {
     // Each wave's list through LDS; every thread merges them in wave order.
     static_assert(G % 64 == 0 && G / 64 <= kMaxGroupWaves, "workgroup group of 2..16 waves");
     __shared__ D lists[kMaxGroupWaves][L];
-    top_merge<64, L, D>(top);
+    top_merge_step<32, true>(top);
+    top_merge_step<16, true>(top);
+    top_merge_step<8, true>(top);
+    top_merge_step<4, true>(top);
+    top_merge_step<2, true>(top);
+    top_merge_step<1, true>(top);
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     __syncthreads();
     if ((threadIdx.x & 63) == 0) {
@@ -626,12 +661,12 @@ __device__ inline void top_merge(D (&top)[L]) {
     }
     return;
   }
-  if constexpr (G >= 64) top_merge_step<32>(top);
-  if constexpr (G >= 32) top_merge_step<16>(top);
-  if constexpr (G >= 16) top_merge_step<8>(top);
-  if constexpr (G >= 8) top_merge_step<4>(top);
-  if constexpr (G >= 4) top_merge_step<2>(top);
-  if constexpr (G >= 2) top_merge_step<1>(top);
+  if constexpr (G >= 64) top_merge_step<32, false>(top);
+  if constexpr (G >= 32) top_merge_step<16, false>(top);
+  if constexpr (G >= 16) top_merge_step<8, false>(top);
+  if constexpr (G >= 8) top_merge_step<4, false>(top);
+  if constexpr (G >= 4) top_merge_step<2, false>(top);
+  if constexpr (G >= 2) top_merge_step<1, false>(top);
 }
 
 }  // namespace sdca_gpu
