@@ -253,27 +253,32 @@ int sdca_eval_kernel(const sdca_objective* objs, int n_obj,
  * One epoch of the SDCA solver on feature input (replaces one pass of the
  * example loop of solver::solve, solver.h:44-47: update_variables for each
  * example, update.h:52-85, with the objective's update_dual_variables) for
- * the multiclass objectives (kind 0..5).  Per example i in `order`: scores
- * W' x_i, the dual update of a_i, and W -= x_i (a_old - a_new)' when
+ * the nine objectives: the six multiclass ones (kind 0..5) and the three
+ * multilabel ones (kind 6..8).  Per example i in `order`: scores W' x_i,
+ * the dual update of a_i, and W -= x_i (a_old - a_new)' when
  * sum |a_old - a_new| exceeds epsilon.  The examples run in blocks whose
  * scores come from the matrix cores; the updates are the sequential loop's
  * (results equal up to the rounding of the scores' sums).
  *   X: d x n features, W: d x m primal and A: m x n dual variables, all
  *      column-major (each example's / class's values contiguous); W and A
  *      are updated in place;
- *   labels: n labels in [0, m); order: count example indices in [0, n), or
- *      NULL for 0..count-1; norms: n values ||x_i||^2 in the data type, or
- *      NULL (computed, scratch.h:27-41).
+ *   labels: n labels in [0, m) (multiclass, offsets NULL), or CSR labels
+ *      with offsets (n + 1 row starts; multilabel: 1..m-1 distinct sorted
+ *      labels per example, output.h:184-206);
+ *   order: count example indices in [0, n), or NULL for 0..count-1;
+ *   norms: n values ||x_i||^2 in the data type, or NULL (computed,
+ *      scratch.h:27-41).
  * Device pointers on `stream` (flags 0), or host arrays with SDCA_HOST_PTR
  * (staged through device memory for the call, W and A copied back); (data,
  * result) one of (F32, F32), (F32, F64), (F64, F64); m at most 16384 (fp32)
- * or 8192 (fp64).  Returns SDCA_ERR_LABELS (after the epoch, which read such
- * entries as 0) for an index or label out of range.
+ * or 8192 (fp64), 2048 for the multilabel hinges.  Returns SDCA_ERR_LABELS
+ * (after the epoch) for an index or multiclass label out of range (read as
+ * 0) or a multilabel example whose labels break those rules (skipped).
  */
 int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result,
                         int64_t d, int64_t m, int64_t n, const void* X, void* W, void* A,
-                        const int64_t* labels, const int64_t* order, int64_t count,
-                        const void* norms, unsigned flags, void* stream);
+                        const int64_t* labels, const int64_t* offsets, const int64_t* order,
+                        int64_t count, const void* norms, unsigned flags, void* stream);
 
 /*
  * The reference solver's example order for epoch `epoch` (0-based) of a

@@ -510,8 +510,7 @@ inline void evaluate_dataset(const Context& ctx, Dataset& d,
 // One epoch of solve()'s example loop (solver.h:43-47) on the GPU:
 // update_variables (solver/update.h:52-85) for each example index in
 // [first, last) - the solver's examples_ after begin_epoch's shuffle - for a
-// feature input with multiclass output and one of the six multiclass
-// objectives (another objective fails with SDCA_ERR_NOT_IMPLEMENTED).
+// feature input with multiclass or multilabel output and its objective.
 // ctx.primal_variables and ctx.dual_variables are updated in place, through
 // host staging per call; scratch.norms (scratch.h:27-41) are used when
 // filled.  The maintainer's switch in solve():
@@ -526,7 +525,10 @@ inline void update_epoch(Context& ctx, sdca::solver_scratch<Data, sdca::feature_
   const std::int64_t m = static_cast<std::int64_t>(d.num_classes());
   const std::int64_t n = static_cast<std::int64_t>(d.num_examples());
   const std::int64_t dim = static_cast<std::int64_t>(d.in.num_dimensions);
-  std::vector<std::int64_t> labels(d.out.labels.begin(), d.out.labels.end());
+  typedef typename Context::output_type Output;
+  std::vector<std::int64_t> labels, offsets;
+  detail::labels_of(d.out, labels, offsets,
+                    std::integral_constant<bool, std::is_same<Output, sdca::multilabel_output>::value>());
   std::vector<std::int64_t> order;
   for (Iterator it = first; it != last; ++it) order.push_back(static_cast<std::int64_t>(*it));
   const sdca_objective ob = detail::objective_of<typename Context::objective_type>::get(ctx.objective);
@@ -534,7 +536,8 @@ inline void update_epoch(Context& ctx, sdca::solver_scratch<Data, sdca::feature_
                                                                          : nullptr;
   detail::check(sdca_epoch_features(&ob, detail::dtype<Data>::value, detail::dtype<Result>::value,
                                     dim, m, n, d.in.features, ctx.primal_variables,
-                                    ctx.dual_variables, labels.data(), order.data(),
+                                    ctx.dual_variables, labels.data(),
+                                    offsets.empty() ? nullptr : offsets.data(), order.data(),
                                     static_cast<std::int64_t>(order.size()), norms,
                                     SDCA_HOST_PTR, nullptr));
 }

@@ -390,14 +390,15 @@ def epoch_order(n, epoch):
     return out
 
 
-def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None):
+def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None, offsets=None):
     """One SDCA epoch on feature input (update_variables for each example of
     `order`, update.h:52-85) for a multiclass objective (name, c, gamma, k):
     X (n, d), W (m, d), A (n, m), W and A updated in place and returned.
     CUDA tensors run on torch's current stream; numpy arrays (C-contiguous,
     X's dtype) go through the host-staging path.  order: example indices
     (None: 0..n-1), e.g. epoch_order(n, e); norms: (n,) squared row norms of
-    X, or None."""
+    X, or None; offsets: (n + 1,) CSR row starts into labels for the
+    multilabel objectives."""
     lib = library()
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(W.shape[0])
@@ -412,6 +413,9 @@ def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None):
         _need(A, "A", (n, m), X)
         _need(norms, "norms", (n,), X)
         lab = torch.as_tensor(labels, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
+        off = None
+        if offsets is not None:
+            off = torch.as_tensor(offsets, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
         od = None
         if order is not None:
             od = torch.as_tensor(order, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
@@ -426,6 +430,7 @@ def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None):
                     or not a.flags.c_contiguous):
                 raise SdcaError(2, f"{name}: expected a C-contiguous {X.dtype} array {shape}")
         lab = np.ascontiguousarray(labels, dtype=np.int64).reshape(-1)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64).reshape(-1)
         od = None if order is None else np.ascontiguousarray(order, dtype=np.int64).reshape(-1)
         flags, stream = HOST_PTR, None
 
@@ -433,13 +438,16 @@ def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None):
             return None if a is None else a.ctypes.data
     data = _dtype_code(X)
     res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
-    if lab.shape[0] != n:
+    if off is None and lab.shape[0] != n:
         raise SdcaError(2, f"labels: expected {n} entries, got {lab.shape[0]}")
+    if off is not None and off.shape[0] != n + 1:
+        raise SdcaError(8, f"{off.shape[0]} offsets for {n} examples (need n + 1)")
     count = n if od is None else int(od.shape[0])
     rc = lib.sdca_epoch_features(objarr, ctypes.c_int(data), ctypes.c_int(res), ctypes.c_int64(d),
                                  ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(ptr(X)),
                                  ctypes.c_void_p(ptr(W)), ctypes.c_void_p(ptr(A)),
-                                 ctypes.c_void_p(ptr(lab)), ctypes.c_void_p(ptr(od)),
+                                 ctypes.c_void_p(ptr(lab)), ctypes.c_void_p(ptr(off)),
+                                 ctypes.c_void_p(ptr(od)),
                                  ctypes.c_int64(count), ctypes.c_void_p(ptr(norms)),
                                  ctypes.c_uint(flags), stream)
     if rc != 0:

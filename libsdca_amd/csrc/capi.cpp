@@ -887,15 +887,21 @@ int sdca_epoch_order(int64_t n, int64_t epoch, int64_t* order) {
 
 int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result, int64_t d,
                         int64_t m, int64_t n, const void* X, void* W, void* A,
-                        const int64_t* labels, const int64_t* order, int64_t count,
-                        const void* norms, unsigned flags, void* stream_ptr) {
+                        const int64_t* labels, const int64_t* offsets, const int64_t* order,
+                        int64_t count, const void* norms, unsigned flags, void* stream_ptr) {
   using namespace sdca_gpu;
   g_last_error.clear();
   if (!obj) return fail(SDCA_ERR_ARG_NULL, "obj must not be NULL");
-  if (obj->kind < SDCA_OBJ_HINGE_TOPK || obj->kind > SDCA_OBJ_ENTROPY_TOPK)
-    return fail(SDCA_ERR_NOT_IMPLEMENTED,
-                "the epoch supports the multiclass objectives (kind 0..5; got %d)",
+  if (obj->kind < SDCA_OBJ_HINGE_TOPK || obj->kind > SDCA_OBJ_MULTILABEL_ENTROPY)
+    return fail(SDCA_ERR_NOT_IMPLEMENTED, "unknown objective kind %d",
                 static_cast<int>(obj->kind));
+  const bool multilabel = obj->kind >= SDCA_OBJ_MULTILABEL_HINGE;
+  if (multilabel && !offsets)
+    return fail(SDCA_ERR_ARG_NULL, "the multilabel objectives need label offsets");
+  if ((obj->kind == SDCA_OBJ_MULTILABEL_HINGE || obj->kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH) &&
+      m > kEpochMaxMultilabelHingeM)
+    return fail(SDCA_ERR_NOT_IMPLEMENTED, "the multilabel hinge epoch supports m <= %lld",
+                (long long)kEpochMaxMultilabelHingeM);
   if (!((data == SDCA_F32 && (result == SDCA_F32 || result == SDCA_F64)) ||
         (data == SDCA_F64 && result == SDCA_F64)))
     return fail(SDCA_ERR_PRECISION,
@@ -909,19 +915,22 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   if (!order && count > n)
     return fail(SDCA_ERR_ARG_RANGE, "count (%lld) > n (%lld) without an order",
                 (long long)count, (long long)n);
-  int rc = check_objectives(obj, 1, m, false);
+  int rc = check_objectives(obj, 1, m, multilabel);
   if (rc) return rc;
   if (!X || !W || !A || !labels) return fail(SDCA_ERR_ARG_NULL, "X, W, A and labels must not be NULL");
   if (count == 0) return SDCA_OK;
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const bool host = (flags & SDCA_HOST_PTR) != 0;
   const size_t es = dtype_size(data);
-  DeviceBuffer dx, dw, da, dl, dord, dnorm;
+  DeviceBuffer dx, dw, da, dl, doff, dord, dnorm;
   if (host) {
     if ((rc = stage_in(X, es * d * n, dx, stream))) return rc;
     if ((rc = stage_in(W, es * d * m, dw, stream))) return rc;
     if ((rc = stage_in(A, es * m * n, da, stream))) return rc;
-    if ((rc = stage_in(labels, sizeof(int64_t) * n, dl, stream))) return rc;
+    const int64_t nlab = multilabel ? offsets[n] : n;
+    if (nlab < 0) return fail(SDCA_ERR_LABELS, "offsets[n] < 0");
+    if ((rc = stage_in(labels, sizeof(int64_t) * nlab, dl, stream))) return rc;
+    if (multilabel && (rc = stage_in(offsets, sizeof(int64_t) * (n + 1), doff, stream))) return rc;
     if (order && (rc = stage_in(order, sizeof(int64_t) * count, dord, stream))) return rc;
     if (norms && (rc = stage_in(norms, es * n, dnorm, stream))) return rc;
   }
@@ -942,6 +951,7 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   a.W = host ? dw.ptr : W;
   a.A = host ? da.ptr : A;
   a.labels = host ? static_cast<const int64_t*>(dl.ptr) : labels;
+  a.offsets = !multilabel ? nullptr : host ? static_cast<const int64_t*>(doff.ptr) : offsets;
   a.order = host && order ? static_cast<const int64_t*>(dord.ptr) : order;
   a.count = count;
   a.norms = host && norms ? dnorm.ptr : norms;
@@ -961,7 +971,8 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
   if (bad)
     return fail(SDCA_ERR_LABELS,
-                "an example index outside [0, n) or a label outside [0, m) (read as 0)");
+                "an example index outside [0, n), a label outside [0, m) (read as 0), or a "
+                "multilabel example whose labels are not 1..m-1 distinct sorted ones (skipped)");
   return SDCA_OK;
 }
 

@@ -16,14 +16,15 @@ constexpr int kEpochBlock = 32;
 struct EpochLaunch {
   int data;    // sdca_dtype of X, W, A
   int result;  // sdca_dtype of the dual update's internal arithmetic
-  int kind;    // sdca_objective_kind (multiclass)
+  int kind;    // sdca_objective_kind
   double c, gamma;
   int k;
   int64_t d, m, n;
   const void* X;          // n x d
   void* W;                // m x d, updated
   void* A;                // n x m, updated
-  const int64_t* labels;  // n
+  const int64_t* labels;  // n (multiclass), or offsets[n] (multilabel)
+  const int64_t* offsets; // n + 1 CSR row starts into labels (multilabel), or NULL
   const int64_t* order;   // count example indices, or NULL for 0..count-1
   int64_t count;
   const void* norms;      // n squared norms, or NULL (computed into the workspace)
@@ -37,8 +38,10 @@ size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool nor
 // Enqueues the epoch; the bad-input flag (an example index or a label out of
 // range: such entries are read as 0) is left in *flag_dev for the caller.
 hipError_t launch_epoch(const EpochLaunch& a, int** flag_dev);
-// Largest m of the epoch for an element type (two rows of m values in LDS).
+// Largest m of the epoch for an element type (two rows of m values in LDS),
+// and for the multilabel hinges (the two-block simplex in registers).
 int64_t epoch_max_m(int data);
+constexpr int64_t kEpochMaxMultilabelHingeM = 2048;
 
 }  // namespace sdca_gpu
 

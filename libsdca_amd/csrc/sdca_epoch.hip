@@ -1,10 +1,13 @@
 // One SDCA epoch on feature input: the example loop of solver.h:39-51 over a
 // given order, each step update_variables (update.h:52-85) with the
-// objective's update_dual_variables, for the six multiclass objectives:
+// objective's update_dual_variables, for the six multiclass objectives
 //   l2_hinge_topk(_smooth)   prox_topk_simplex_biased  (l2_hinge_topk.h:44-68, 132-159)
 //   l2_topk_hinge(_smooth)   prox_knapsack_le_biased   (l2_topk_hinge.h:46-69, 137-163)
 //   l2_entropy               prox_two_entropy          (l2_entropy.h:48-74)
 //   l2_entropy_topk          prox_topk_entropy_biased  (l2_entropy_topk.h:47-71)
+// and the three multilabel ones, labels first (output.h:121-164):
+//   l2_multilabel_hinge(_smooth)  prox_two_simplex  (l2_multilabel_hinge.h:40-66, 137-166)
+//   l2_multilabel_entropy         prox_two_entropy  (l2_multilabel_entropy.h:43-69)
 //
 // The loop is sequential through W (each example's scores depend on every
 // earlier update), so it runs blocked, with the same arithmetic as the
@@ -121,8 +124,9 @@ __global__ void __launch_bounds__(kEpochThreads)
 epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
                    const int64_t* __restrict__ order, int64_t q0, int64_t n, int nb,
                    const D* __restrict__ norms, const int64_t* __restrict__ labels,
-                   D* __restrict__ A, D* __restrict__ Delta, D* __restrict__ gdummy, EpochObj ob,
-                   int m, int* __restrict__ bad) {
+                   const int64_t* __restrict__ offsets, D* __restrict__ A,
+                   D* __restrict__ Delta, D* __restrict__ gdummy, EpochObj ob, int m,
+                   int* __restrict__ bad) {
   constexpr int G = kEpochThreads;
   constexpr int PQ = PF > 0 ? PF : 1;
   constexpr bool DL = epoch_delta_in_lds<D>(PF);
@@ -132,13 +136,17 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
   D* const cb = v + ((m + 3) & ~3);             // the column the thresholds read (cw words)
   D* const dummy = cb + cw;                     // G per-thread dummy words
   D* const Dx = DL ? dummy + G : Delta;         // the block's delta rows
+  // the example's labels (multilabel), m ints after the D words
+  int* const lab = reinterpret_cast<int*>(dummy + G + (DL ? kEpochBlock * m : 0));
   __shared__ R sh_t, sh_lo, sh_hi;
   __shared__ int sh_slow;
   __shared__ D sh_vy;
   __shared__ D g_all[kEpochBlock * kEpochBlock];
   __shared__ D sh_norm[kEpochBlock];
   __shared__ int64_t sh_i[kEpochBlock];
-  __shared__ int sh_y[kEpochBlock];
+  __shared__ int sh_y[kEpochBlock];   // multiclass: the label; multilabel: the label count
+  __shared__ int64_t sh_off[kEpochBlock];
+  __shared__ int sh_badex;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
   D* const ld = dummy + tid;   // LDS sink
@@ -146,23 +154,37 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
   const int kind = ob.kind;
   const R c = static_cast<R>(ob.c), gamma = static_cast<R>(ob.gamma);
   const bool hinge = kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH;
+  const bool ml = kind >= SDCA_OBJ_MULTILABEL_HINGE;
   const bool smooth = kind == SDCA_OBJ_HINGE_TOPK_SMOOTH || kind == SDCA_OBJ_TOPK_HINGE_SMOOTH;
   const bool simplex = kind == SDCA_OBJ_HINGE_TOPK || kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
   const int op = simplex ? OP_TOPK_SIMPLEX_BIASED : OP_KNAPSACK_LE_BIASED;
   const R knap_hi = simplex ? R(0) : c / static_cast<R>(ob.k);
   // The block's indices, norms, labels and Gram matrix in LDS.
   // An index outside [0, n) or a label outside [0, m) raises *bad and is
-  // read as 0.
+  // read as 0; a multilabel example with a label count outside [1, m - 1]
+  // (or, below, labels that are not distinct, sorted and in [0, m)) raises
+  // it and is skipped (validate_labels_and_offsets, output.h:184-206).
+  if (tid == 0) sh_badex = -1;
   if (tid < nb) {
     int64_t i = order ? order[q0 + tid] : q0 + tid;
     if (i < 0 || i >= n) {
       bad[0] = 1;
       i = 0;
     }
-    int64_t yl = labels[i];
-    if (yl < 0 || yl >= m) {
-      bad[0] = 1;
-      yl = 0;
+    int64_t yl;
+    if (ml) {
+      sh_off[tid] = offsets[i];
+      yl = offsets[i + 1] - offsets[i];
+      if (yl < 1 || yl >= m) {
+        bad[0] = 1;
+        yl = 0;
+      }
+    } else {
+      yl = labels[i];
+      if (yl < 0 || yl >= m) {
+        bad[0] = 1;
+        yl = 0;
+      }
     }
     sh_i[tid] = i;
     sh_norm[tid] = norms[i];
@@ -195,7 +217,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
   for (int k = 0; k < nb; ++k) {
     const int64_t i = sh_i[k];
     const D norm2 = sh_norm[k];
-    const int y = sh_y[k];
+    const int y = sh_y[k];  // multilabel: the label count nl
     D* const arow = A + i * m;
     D* const drow = Delta + static_cast<int64_t>(k) * m;
     const D* const srow = S + static_cast<int64_t>(k) * m;
@@ -218,7 +240,20 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
         });
       }
     }
-    if (!(norm2 > D(0))) {  // update.h:62: the example changes nothing
+    if (ml && y > 0) {
+      // The example's labels into LDS, checked distinct, sorted, in range.
+      const int64_t o0 = sh_off[k];
+      for (int q = tid; q < y; q += G) {
+        const int64_t l = labels[o0 + q];
+        const bool okl = l >= 0 && l < m && (q == 0 || l > labels[o0 + q - 1]);
+        if (!okl) {
+          bad[0] = 1;
+          sh_badex = k;
+        }
+        lab[q] = okl ? static_cast<int>(l) : 0;
+      }
+    }
+    if (!(norm2 > D(0)) || (ml && y == 0)) {  // update.h:62: the example changes nothing
       for_cols<PF>(tid, m, [&](int j, int q, bool ok) { *(ok ? drow + j : gd) = D(0); });
       continue;
     }
@@ -229,6 +264,13 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
       rho = smooth ? static_cast<R>(norm2) / (static_cast<R>(norm2) + gamma / c) : R(1);
       pa = smooth ? static_cast<D>(rho) / norm2 : D(1) / norm2;
       pb = smooth ? -static_cast<D>(rho) : D(-1);
+    } else if (kind == SDCA_OBJ_MULTILABEL_HINGE) {  // l2_multilabel_hinge.h:50-54
+      pa = D(1) / norm2;
+      pb = D(-1);
+    } else if (kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH) {  // l2_multilabel_hinge.h:147-153
+      const R gdc = gamma / c;
+      pa = static_cast<D>(R(1) / (static_cast<R>(norm2) + gdc));
+      pb = -static_cast<D>(static_cast<R>(norm2) / (static_cast<R>(norm2) + gdc));
     }
     if constexpr (PF > 0) {
       // The corrections row by row in increasing r, kFixRows rows' loads at
@@ -274,8 +316,83 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
       if constexpr (PF > 0) *((ok && j == y) ? &sh_vy : ld) = x;
     });
     __syncthreads();
+    if (ml && sh_badex == k) {  // labels not valid: the example is skipped
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) { *(ok ? drow + j : gd) = D(0); });
+      __syncthreads();
+      continue;
+    }
     const D vy = PF > 0 ? sh_vy : v[y];
-    if (kind == SDCA_OBJ_ENTROPY) {
+    if (ml) {
+      // The labels first (output.h:121-164): label r of the example (the
+      // r-th smallest) to row r, the other rows after them in index order;
+      // the two-block prox, then the recovery.
+      const int nl = y;
+      auto rank_of = [&](int j, bool& is_lab) {
+        int lo = 0, hi = nl;  // the count of labels below j
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (lab[mid] < j) lo = mid + 1;
+          else hi = mid;
+        }
+        is_lab = lo < nl && lab[lo] == j;
+        return lo;
+      };
+      const bool ent = kind == SDCA_OBJ_MULTILABEL_ENTROPY;
+      const D half = pa / D(2);
+      for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+        bool is_lab;
+        const int r = rank_of(j, is_lab);
+        const D x = getv(j, q);
+        const D xx = ent ? x : (is_lab ? half - x : half + x);
+        setv(j, q, xx);
+        *(ok ? cb + (is_lab ? r : nl + j - r) : ld) = xx;
+      });
+      __syncthreads();
+      if (ent) {  // prox_two_entropy, alpha = c norm2 (l2_multilabel_entropy.h:55-68)
+        const R alpha = c * static_cast<R>(norm2);
+        R t, c2;
+        twoent_thresholds<D, R, G, true>(cb, m, nl, tid, alpha, t, c2);
+        const D map_a = D(1) / static_cast<D>(alpha);
+        const D ta = static_cast<D>(t), tb = static_cast<D>(t + c2);
+        const D na = static_cast<D>(-c), nbias = static_cast<D>(c / static_cast<R>(nl));
+        for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+          bool is_lab;
+          rank_of(j, is_lab);
+          const D x = clamp_ref(map_a * lambert_w_exp_nb(getv(j, q) - (is_lab ? ta : tb)), D(0),
+                                D(1));
+          setv(j, q, is_lab ? na * x + nbias : na * x);
+        });
+      } else {  // prox_two_simplex, rhs c (l2_multilabel_hinge.h:59-65)
+        D ta = D(0), tb = D(0);  // the two blocks' thresholds
+        if constexpr (C > 0) {
+          D vq[C];
+          const int nvalid = (m - tid + G - 1) / G;
+#pragma unroll
+          for (int q = 0; q < C; ++q) {
+            const D x = cb[tid + G * q];
+            vq[q] = (q < nvalid) ? x : -num<D>::inf();
+          }
+          ProxParamsT<R> pp;
+          pp.lo = R(0);
+          pp.hi = c;
+          pp.rhs = c;
+          pp.rho = R(0);
+          pp.k = 1;
+          pp.op = OP_TWO_SIMPLEX;
+          pp.p = nl;
+          const ColThr<R> th = two_family_slots<G, C, C, D, R>(vq, m, nl, pp);
+          ta = static_cast<D>(th.t);
+          tb = static_cast<D>(th.t2);
+        }
+        const D hc = static_cast<D>(c);
+        for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+          bool is_lab;
+          rank_of(j, is_lab);
+          const D x = getv(j, q);
+          setv(j, q, is_lab ? clamp_ref(x - ta, D(0), hc) : D(-1) * clamp_ref(x - tb, D(0), hc));
+        });
+      }
+    } else if (kind == SDCA_OBJ_ENTROPY) {
       // prox_two_entropy over (label | the rest), alpha = c norm2
       for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
         *(ok ? cb + (j == y ? 0 : (j < y ? j + 1 : j)) : ld) = getv(j, q);
@@ -666,9 +783,10 @@ hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* no
   // corrections then read LDS instead of global memory).
   if constexpr (epoch_delta_in_lds<D>(PF))
     lds += static_cast<size_t>(kEpochBlock) * static_cast<size_t>(m) * sizeof(D);
+  lds += static_cast<size_t>(m) * sizeof(int);  // the example's labels (multilabel)
   if (lds > kEpochLdsBytes) return hipErrorInvalidValue;
   hipLaunchKernelGGL((epoch_block_kernel<D, R, C, KM, PF>), dim3(1), dim3(kEpochThreads), lds,
-                     a.stream, S, Gm, a.order, q0, a.n, nb, norms, a.labels,
+                     a.stream, S, Gm, a.order, q0, a.n, nb, norms, a.labels, a.offsets,
                      static_cast<D*>(a.A), Delta, gdummy, ob, m, bad);
   return hipGetLastError();
 }
@@ -682,7 +800,12 @@ hipError_t launch_block_for(const D* S, const D* Gm, int64_t q0, int nb, const D
                             int* bad) {
   const int64_t m = a.m;
   const bool simplex = a.kind == SDCA_OBJ_HINGE_TOPK || a.kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
-  const bool regs = a.kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH && !(simplex && a.k > 8);
+  // The register forms: the simplex / knapsack thresholds of the multiclass
+  // hinges (k <= 8 for the simplex) and the two-block simplex of the
+  // multilabel hinges.
+  const bool regs = (a.kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH && !(simplex && a.k > 8)) ||
+                    a.kind == SDCA_OBJ_MULTILABEL_HINGE ||
+                    a.kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH;
   const bool k5 = !simplex || a.k <= 5;
   const int pf = m <= 256 ? 1 : m <= 1024 ? 4 : m <= 2048 ? 8 : 0;
   if (pf == 0) return launch_block<D, R, 0, 5, 0>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);

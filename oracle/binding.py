@@ -208,14 +208,15 @@ class Library:
         return [{f_: getattr(r, f_) for f_, _ in EvalRecord._fields_} for r in recs], acc
 
     def epoch_features(self, obj, X, W, A, labels, order=None, result=None, epochs=0,
-                       reverse=False):
+                       reverse=False, offsets=None):
         """One SDCA epoch on feature input (solver.h:39-51, update.h:52-85)
         over `order` (None: 0..n-1): X (n, d), W (m, d), A (n, m)
         C-contiguous; W and A are updated in place (and returned).  The
         reference shim runs sdca::update_variables; with epochs > 0 instead
         the reference's own solve() for that many epochs (its shuffled
         order).  The restatement takes reverse=True for its second rounding
-        of the scores."""
+        of the scores.  offsets: CSR row starts into labels (n + 1) for the
+        multilabel objectives."""
         n, d = X.shape
         m = W.shape[0]
         data = _dt(X)
@@ -223,11 +224,13 @@ class Library:
         objarr = make_objectives([obj])
         labels = np.ascontiguousarray(labels, dtype=np.int64)
         od = None if order is None else np.ascontiguousarray(order, dtype=np.int64)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
         count = n if od is None else od.size
         common = (objarr, ctypes.c_int(data), ctypes.c_int(result), ctypes.c_int64(d),
                   ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(X.ctypes.data),
                   ctypes.c_void_p(W.ctypes.data), ctypes.c_void_p(A.ctypes.data),
                   ctypes.c_void_p(labels.ctypes.data),
+                  ctypes.c_void_p(off.ctypes.data if off is not None else None),
                   ctypes.c_void_p(od.ctypes.data if od is not None else None),
                   ctypes.c_int64(count))
         if hasattr(self.lib, "ref_epoch_features"):

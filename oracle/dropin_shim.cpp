@@ -111,17 +111,17 @@ int run_features(const Obj<float, double>& obj, int64_t d, int64_t m, int64_t n,
 // One epoch over `order` with one objective: the reference's own loop of
 // update_variables (solver.h:43-47, solver/update.h:52-85) on ctx_ref,
 // sdca::hip::update_epoch on ctx_gpu, both from the given W and A.
-template <template <class, class> class Obj>
+template <class Out, template <class, class> class Obj>
 int run_epoch(const Obj<float, double>& obj, int64_t d, int64_t m, int64_t n, const float* X,
-              const int64_t* labels, const int64_t* order, int64_t count, float* W_gpu,
-              float* A_gpu, float* W_ref, float* A_ref) {
-  typedef sdca::solver_context<float, double, sdca::feature_input, sdca::multiclass_output, Obj>
-      Ctx;
+              const int64_t* labels, const int64_t* offsets, const int64_t* order,
+              int64_t count, float* W_gpu, float* A_gpu, float* W_ref, float* A_ref) {
+  typedef std::integral_constant<bool, std::is_same<Out, sdca::multilabel_output>::value> ML;
+  typedef sdca::solver_context<float, double, sdca::feature_input, Out, Obj> Ctx;
   auto make = [&](float* A, float* W) {
     return Ctx(sdca::make_dataset_train<double>(
                    sdca::make_input_feature(static_cast<sdca::size_type>(d),
                                             static_cast<sdca::size_type>(n), X),
-                   output(std::false_type(), m, labels, nullptr, n)),
+                   output(ML(), m, labels, offsets, n)),
                Obj<float, double>(obj), A, W, nullptr);
   };
   Ctx ctx_ref = make(A_ref, W_ref);
@@ -142,33 +142,45 @@ int run_epoch(const Obj<float, double>& obj, int64_t d, int64_t m, int64_t n, co
 
 extern "C" {
 
-// kind: a multiclass sdca_objective_kind (0..5).  W_* (m x d) and A_* (n x m)
-// hold the starting point and receive each side's result.  Returns 0, or the
+// kind: an sdca_objective_kind (multilabel ones with offsets, n + 1 CSR row
+// starts).  W_* (m x d) and A_* (n x m) hold the starting point and receive
+// each side's result.  Returns 0, or the
 // drop-in's error status.
 int dropin_update_epoch(int kind, double c, double gamma, int64_t k, int64_t d, int64_t m,
-                        int64_t n, const float* X, const int64_t* labels, const int64_t* order,
-                        int64_t count, float* W_gpu, float* A_gpu, float* W_ref,
-                        float* A_ref) {
+                        int64_t n, const float* X, const int64_t* labels,
+                        const int64_t* offsets, const int64_t* order, int64_t count,
+                        float* W_gpu, float* A_gpu, float* W_ref, float* A_ref) {
+  typedef sdca::multiclass_output MC;
+  typedef sdca::multilabel_output ML;
   const sdca::size_type kk = static_cast<sdca::size_type>(k);
   switch (kind) {
+    case SDCA_OBJ_MULTILABEL_HINGE:
+      return run_epoch<ML>(sdca::l2_multilabel_hinge<float, double>(c), d, m, n, X, labels,
+                           offsets, order, count, W_gpu, A_gpu, W_ref, A_ref);
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
+      return run_epoch<ML>(sdca::l2_multilabel_hinge_smooth<float, double>(c, gamma), d, m, n, X,
+                           labels, offsets, order, count, W_gpu, A_gpu, W_ref, A_ref);
+    case SDCA_OBJ_MULTILABEL_ENTROPY:
+      return run_epoch<ML>(sdca::l2_multilabel_entropy<float, double>(c), d, m, n, X, labels,
+                           offsets, order, count, W_gpu, A_gpu, W_ref, A_ref);
     case SDCA_OBJ_HINGE_TOPK:
-      return run_epoch(sdca::l2_hinge_topk<float, double>(c, kk), d, m, n, X, labels, order,
-                       count, W_gpu, A_gpu, W_ref, A_ref);
+      return run_epoch<MC>(sdca::l2_hinge_topk<float, double>(c, kk), d, m, n, X,
+                           labels, nullptr, order, count, W_gpu, A_gpu, W_ref, A_ref);
     case SDCA_OBJ_HINGE_TOPK_SMOOTH:
-      return run_epoch(sdca::l2_hinge_topk_smooth<float, double>(c, gamma, kk), d, m, n, X,
-                       labels, order, count, W_gpu, A_gpu, W_ref, A_ref);
+      return run_epoch<MC>(sdca::l2_hinge_topk_smooth<float, double>(c, gamma, kk), d, m, n, X,
+                           labels, nullptr, order, count, W_gpu, A_gpu, W_ref, A_ref);
     case SDCA_OBJ_TOPK_HINGE:
-      return run_epoch(sdca::l2_topk_hinge<float, double>(c, kk), d, m, n, X, labels, order,
-                       count, W_gpu, A_gpu, W_ref, A_ref);
+      return run_epoch<MC>(sdca::l2_topk_hinge<float, double>(c, kk), d, m, n, X,
+                           labels, nullptr, order, count, W_gpu, A_gpu, W_ref, A_ref);
     case SDCA_OBJ_TOPK_HINGE_SMOOTH:
-      return run_epoch(sdca::l2_topk_hinge_smooth<float, double>(c, gamma, kk), d, m, n, X,
-                       labels, order, count, W_gpu, A_gpu, W_ref, A_ref);
+      return run_epoch<MC>(sdca::l2_topk_hinge_smooth<float, double>(c, gamma, kk), d, m, n, X,
+                           labels, nullptr, order, count, W_gpu, A_gpu, W_ref, A_ref);
     case SDCA_OBJ_ENTROPY:
-      return run_epoch(sdca::l2_entropy<float, double>(c), d, m, n, X, labels, order, count,
-                       W_gpu, A_gpu, W_ref, A_ref);
+      return run_epoch<MC>(sdca::l2_entropy<float, double>(c), d, m, n, X,
+                           labels, nullptr, order, count, W_gpu, A_gpu, W_ref, A_ref);
     case SDCA_OBJ_ENTROPY_TOPK:
-      return run_epoch(sdca::l2_entropy_topk<float, double>(c, kk), d, m, n, X, labels, order,
-                       count, W_gpu, A_gpu, W_ref, A_ref);
+      return run_epoch<MC>(sdca::l2_entropy_topk<float, double>(c, kk), d, m, n, X,
+                           labels, nullptr, order, count, W_gpu, A_gpu, W_ref, A_ref);
     default:
       return -2;
   }

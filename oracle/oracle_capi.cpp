@@ -360,23 +360,24 @@ int oracle_dual_regularizer(int data, int result, int64_t m, int64_t n, const vo
 // first.  Returns -1 for an objective without a multiclass update.
 int oracle_epoch_features(const sdca_objective* obj, int data, int result, int64_t d, int64_t m,
                           int64_t n, const void* X, void* W, void* A, const int64_t* labels,
-                          const int64_t* order, int64_t count, int reverse) {
+                          const int64_t* offsets, const int64_t* order, int64_t count,
+                          int reverse) {
   if (data == SDCA_F32 && result == SDCA_F32)
     return orc::epoch<float, float>(*obj, d, m, n, static_cast<const float*>(X),
-                                    static_cast<float*>(W), static_cast<float*>(A), labels, order,
-                                    count, reverse != 0);
+                                    static_cast<float*>(W), static_cast<float*>(A), labels, offsets,
+                                    order, count, reverse != 0);
   if (data == SDCA_F32 && result == SDCA_F64)
     return orc::epoch<float, double>(*obj, d, m, n, static_cast<const float*>(X),
                                      static_cast<float*>(W), static_cast<float*>(A), labels,
-                                     order, count, reverse != 0);
+                                     offsets, order, count, reverse != 0);
   if (data == SDCA_F64 && result == SDCA_F64)
     return orc::epoch<double, double>(*obj, d, m, n, static_cast<const double*>(X),
                                       static_cast<double*>(W), static_cast<double*>(A), labels,
-                                      order, count, reverse != 0);
+                                      offsets, order, count, reverse != 0);
   if (data == SDCA_F64 && result == SDCA_LONG_DOUBLE)
     return orc::epoch<double, long double>(*obj, d, m, n, static_cast<const double*>(X),
                                            static_cast<double*>(W), static_cast<double*>(A),
-                                           labels, order, count, reverse != 0);
+                                           labels, offsets, order, count, reverse != 0);
   return -2;
 }
 

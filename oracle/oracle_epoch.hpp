@@ -16,6 +16,11 @@
 //   l2_topk_hinge_smooth   l2_topk_hinge.h:137-163
 //   l2_entropy             l2_entropy.h:48-74       (prox_two_entropy, alpha c norm2)
 //   l2_entropy_topk        l2_entropy_topk.h:47-71  (prox_topk_entropy_biased)
+// and the three multilabel ones, on the labels-first view
+// (output.h:121-164, multilabel move_front / move_back):
+//   l2_multilabel_hinge         l2_multilabel_hinge.h:40-66    (prox_two_simplex, rhs c)
+//   l2_multilabel_hinge_smooth  l2_multilabel_hinge.h:137-166
+//   l2_multilabel_entropy       l2_multilabel_entropy.h:43-69  (prox_two_entropy, alpha c norm2)
 // BLAS calls are modelled as in oracle_eval.hpp: dot products exact and
 // rounded once to Data (blas_dot), axpby and scal elementwise in Data, ger
 // as w - x_l y_j per element.  `reverse` accumulates the score dot
@@ -114,13 +119,66 @@ inline bool update_dual(const sdca_objective& ob, std::ptrdiff_t m, D norm2, D* 
   }
 }
 
-// One epoch over `order` (count entries; NULL: 0..n-1).  X: n x d, W: m x d,
+// The multilabel objectives' update_dual_variables on v = a_i with its nl
+// labels first (m entries) and scores s (same order).  The two-block prox
+// runs on copies of the blocks (proxdef.h:259-276) and clamps v.
+template <class D, class R>
+inline bool update_dual_ml(const sdca_objective& ob, std::ptrdiff_t m, std::ptrdiff_t nl, D norm2,
+                           D* v, D* s) {
+  const R c = static_cast<R>(ob.c), gamma = static_cast<R>(ob.gamma);
+  D* pos_first = v;
+  D* pos_last = v + nl;
+  D* neg_first = v + nl;
+  D* neg_last = v + m;
+  switch (ob.kind) {
+    case SDCA_OBJ_MULTILABEL_HINGE:
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH: {
+      D a, b;
+      if (ob.kind == SDCA_OBJ_MULTILABEL_HINGE) {
+        a = D(1) / norm2;
+        b = D(1);
+      } else {
+        const R gamma_div_c = gamma / c;
+        a = static_cast<D>(R(1) / (static_cast<R>(norm2) + gamma_div_c));
+        b = static_cast<D>(static_cast<R>(norm2) / (static_cast<R>(norm2) + gamma_div_c));
+      }
+      for (std::ptrdiff_t j = 0; j < m; ++j) v[j] = a * s[j] + (-b) * v[j];
+      a /= 2;
+      for (D* x = pos_first; x != pos_last; ++x) *x = a - *x;
+      for (D* x = neg_first; x != neg_last; ++x) *x = a + *x;
+      std::vector<D> pa(pos_first, pos_last), na(neg_first, neg_last);
+      auto tt = two_simplex(pa.data(), pa.data() + nl, na.data(), na.data() + (m - nl), c);
+      clamp(tt.first, pos_first, pos_last);
+      clamp(tt.second, neg_first, neg_last);
+      for (D* x = neg_first; x != neg_last; ++x) *x *= D(-1);
+      return true;
+    }
+    case SDCA_OBJ_MULTILABEL_ENTROPY: {
+      for (std::ptrdiff_t j = 0; j < m; ++j) v[j] = D(1) * s[j] + (-norm2) * v[j];
+      const R alpha = c * static_cast<R>(norm2);
+      std::vector<D> pa(pos_first, pos_last), na(neg_first, neg_last);
+      auto tt = two_entropy(pa.data(), pa.data() + nl, na.data(), na.data() + (m - nl), alpha);
+      clamp(tt.first, pos_first, pos_last);
+      clamp(tt.second, neg_first, neg_last);
+      const D a = static_cast<D>(-c), b = static_cast<D>(c / static_cast<R>(nl));
+      for (D* x = pos_first; x != pos_last; ++x) *x = a * *x + b;
+      for (D* x = neg_first; x != neg_last; ++x) *x *= a;
+      return true;
+    }
+    default:
+      return false;
+  }
+}
+
+// One epoch over `order` (count entries; NULL: 0..n-1); offsets (n + 1,
+// CSR into labels) for the multilabel objectives, NULL for the multiclass
+// ones.  X: n x d, W: m x d,
 // A: n x m (each example's / class's values contiguous, as the reference's
 // column-major d x n, d x m and m x n matrices).
 template <class D, class R>
 inline int epoch(const sdca_objective& ob, std::ptrdiff_t d, std::ptrdiff_t m, std::ptrdiff_t n,
-                 const D* X, D* W, D* A, const int64_t* labels, const int64_t* order,
-                 std::ptrdiff_t count, bool reverse) {
+                 const D* X, D* W, D* A, const int64_t* labels, const int64_t* offsets,
+                 const int64_t* order, std::ptrdiff_t count, bool reverse) {
   std::vector<D> norms(static_cast<size_t>(n)), scores(static_cast<size_t>(m)),
       copy(static_cast<size_t>(m));
   for (std::ptrdiff_t i = 0; i < n; ++i) norms[i] = blas_dot(d, X + d * i, X + d * i);
@@ -132,11 +190,22 @@ inline int epoch(const sdca_objective& ob, std::ptrdiff_t d, std::ptrdiff_t m, s
     for (std::ptrdiff_t j = 0; j < m; ++j) scores[j] = dot_order(d, W + d * j, x, reverse);
     D* v = A + m * i;
     std::copy(v, v + m, copy.begin());
-    const std::ptrdiff_t y = static_cast<std::ptrdiff_t>(labels[i]);
-    std::swap(v[0], v[y]);
-    std::swap(scores[0], scores[y]);
-    if (!update_dual<D, R>(ob, m, norm2, v, scores.data())) return -1;
-    std::swap(v[0], v[y]);
+    if (offsets) {
+      // multilabel move_front / move_back (output.h:121-164)
+      const int64_t o0 = offsets[i], nl = offsets[i + 1] - offsets[i];
+      for (int64_t q = 0; q < nl; ++q) {
+        std::swap(v[q], v[labels[o0 + q]]);
+        std::swap(scores[q], scores[labels[o0 + q]]);
+      }
+      if (!update_dual_ml<D, R>(ob, m, nl, norm2, v, scores.data())) return -1;
+      for (int64_t q = nl - 1; q >= 0; --q) std::swap(v[q], v[labels[o0 + q]]);
+    } else {
+      const std::ptrdiff_t y = static_cast<std::ptrdiff_t>(labels[i]);
+      std::swap(v[0], v[y]);
+      std::swap(scores[0], scores[y]);
+      if (!update_dual<D, R>(ob, m, norm2, v, scores.data())) return -1;
+      std::swap(v[0], v[y]);
+    }
     // var_copy = a_old - a_new; diff = asum
     long double asum = 0;
     for (std::ptrdiff_t j = 0; j < m; ++j) {

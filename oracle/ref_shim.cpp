@@ -533,13 +533,15 @@ int evaluate_impl(const sdca_objective* objs, int n_obj, int64_t d, int64_t m, i
 // With epochs > 0 instead, the reference's own solve() runs that many epochs
 // (its generator and std::shuffle give the order, solver.h:75-112) with no
 // evaluation between epochs.
-template <class D, class R, template <class, class> class Obj>
+template <class Out, class D, class R, template <class, class> class Obj>
 void epoch_run(Obj<D, R> obj, int64_t d, int64_t m, int64_t n, const D* X, D* W, D* A,
-               const int64_t* labels, const int64_t* order, int64_t count, int64_t epochs) {
-  typedef sdca::solver_context<D, R, sdca::feature_input, sdca::multiclass_output, Obj> Ctx;
+               const int64_t* labels, const int64_t* offsets, const int64_t* order,
+               int64_t count, int64_t epochs) {
+  typedef sdca::solver_context<D, R, sdca::feature_input, Out, Obj> Ctx;
   typename Ctx::train_set_type set(
       sdca::feature_input<D>(static_cast<sdca::size_type>(d), static_cast<sdca::size_type>(n), X),
-      make_out(std::false_type(), m, labels, nullptr, 0, n));
+      make_out(std::integral_constant<bool, std::is_same<Out, sdca::multilabel_output>::value>(),
+               m, labels, offsets, 0, n));
   Ctx ctx(std::move(set), std::move(obj), A, W);
   if (epochs > 0) {
     sdca::logging::set_level(sdca::logging::level::none);
@@ -557,12 +559,16 @@ void epoch_run(Obj<D, R> obj, int64_t d, int64_t m, int64_t n, const D* X, D* W,
 }
 
 #define SDCA_REF_EPOCH(OBJ)                                                               \
-  epoch_run<D, R>(OBJ, d, m, n, X, W, A, labels, order, count, epochs)
+  epoch_run<sdca::multiclass_output, D, R>(OBJ, d, m, n, X, W, A, labels, nullptr, order,   \
+                                           count, epochs)
+#define SDCA_REF_EPOCH_ML(OBJ)                                                            \
+  epoch_run<sdca::multilabel_output, D, R>(OBJ, d, m, n, X, W, A, labels, offsets, order,   \
+                                           count, epochs)
 
 template <class D, class R>
 int epoch_impl(const sdca_objective& ob, int64_t d, int64_t m, int64_t n, const D* X, D* W,
-               D* A, const int64_t* labels, const int64_t* order, int64_t count,
-               int64_t epochs) {
+               D* A, const int64_t* labels, const int64_t* offsets, const int64_t* order,
+               int64_t count, int64_t epochs) {
   const R c = static_cast<R>(ob.c), g = static_cast<R>(ob.gamma);
   const sdca::size_type k = static_cast<sdca::size_type>(ob.k);
   switch (ob.kind) {
@@ -572,6 +578,12 @@ int epoch_impl(const sdca_objective& ob, int64_t d, int64_t m, int64_t n, const 
     case SDCA_OBJ_TOPK_HINGE_SMOOTH: SDCA_REF_EPOCH((sdca::l2_topk_hinge_smooth<D, R>(c, g, k))); break;
     case SDCA_OBJ_ENTROPY: SDCA_REF_EPOCH((sdca::l2_entropy<D, R>(c))); break;
     case SDCA_OBJ_ENTROPY_TOPK: SDCA_REF_EPOCH((sdca::l2_entropy_topk<D, R>(c, k))); break;
+    case SDCA_OBJ_MULTILABEL_HINGE:
+      SDCA_REF_EPOCH_ML((sdca::l2_multilabel_hinge<D, R>(c))); break;
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
+      SDCA_REF_EPOCH_ML((sdca::l2_multilabel_hinge_smooth<D, R>(c, g))); break;
+    case SDCA_OBJ_MULTILABEL_ENTROPY:
+      SDCA_REF_EPOCH_ML((sdca::l2_multilabel_entropy<D, R>(c))); break;
     default: return SDCA_ERR_ARG_RANGE;
   }
   return 0;
@@ -583,19 +595,21 @@ extern "C" {
 
 // The reference's SDCA epoch on feature input (see epoch_run): X d x n,
 // W d x m, A m x n, column-major (each example's / class's values
-// contiguous), W and A updated in place.
+// contiguous), W and A updated in place; offsets (n + 1, CSR into labels)
+// for the multilabel objectives, NULL for the multiclass ones.
 int ref_epoch_features(const sdca_objective* obj, int data, int result, int64_t d, int64_t m,
                        int64_t n, const void* X, void* W, void* A, const int64_t* labels,
-                       const int64_t* order, int64_t count, int64_t epochs) {
+                       const int64_t* offsets, const int64_t* order, int64_t count,
+                       int64_t epochs) {
   if (data == SDCA_F32 && result == SDCA_F32)
     return epoch_impl<float, float>(*obj, d, m, n, static_cast<const float*>(X),
-        static_cast<float*>(W), static_cast<float*>(A), labels, order, count, epochs);
+        static_cast<float*>(W), static_cast<float*>(A), labels, offsets, order, count, epochs);
   if (data == SDCA_F32 && result == SDCA_F64)
     return epoch_impl<float, double>(*obj, d, m, n, static_cast<const float*>(X),
-        static_cast<float*>(W), static_cast<float*>(A), labels, order, count, epochs);
+        static_cast<float*>(W), static_cast<float*>(A), labels, offsets, order, count, epochs);
   if (data == SDCA_F64 && result == SDCA_F64)
     return epoch_impl<double, double>(*obj, d, m, n, static_cast<const double*>(X),
-        static_cast<double*>(W), static_cast<double*>(A), labels, order, count, epochs);
+        static_cast<double*>(W), static_cast<double*>(A), labels, offsets, order, count, epochs);
   return SDCA_ERR_PRECISION;
 }
 

@@ -138,18 +138,17 @@ def test_prox_dropin(cuda, oracle, dropin, op, dtype, m, k):
 
 EPOCH_OBJS = [("l2_hinge_topk", 1.0, 1.0, 3), ("l2_hinge_topk_smooth", 1.0, 0.5, 3),
               ("l2_topk_hinge", 1.0, 1.0, 2), ("l2_topk_hinge_smooth", 0.7, 0.5, 2),
-              ("l2_entropy", 1.0, 1.0, 1), ("l2_entropy_topk", 1.5, 1.0, 3)]
-ORACLE_EPOCH = {"l2_hinge_topk": "hinge_topk", "l2_hinge_topk_smooth": "hinge_topk_smooth",
-                "l2_topk_hinge": "topk_hinge", "l2_topk_hinge_smooth": "topk_hinge_smooth",
-                "l2_entropy": "entropy", "l2_entropy_topk": "entropy_topk"}
+              ("l2_entropy", 1.0, 1.0, 1), ("l2_entropy_topk", 1.5, 1.0, 3),
+              ("l2_multilabel_hinge", 1.0, 1.0, 1), ("l2_multilabel_hinge_smooth", 0.7, 0.5, 1),
+              ("l2_multilabel_entropy", 1.0, 1.0, 1)]
 
 
 @pytest.mark.parametrize("obj", EPOCH_OBJS)
 def test_dropin_update_epoch(dropin, oracle, obj):
     """sdca::hip::update_epoch (host staging through the C ABI) against the
     reference's own loop of update_variables over the solver's order, on
-    copies of one reference context (float data, double results), two epochs
-    from a non-zero start.  The scores round differently on each side (MKL's
+    copies of one reference context (float data, double results; multiclass
+    or multilabel output), two epochs from zero.  The scores round differently on each side (MKL's
     sgemv, the block GEMM), so the bound is the sum of the two pinned ones
     (reference vs restatement, restatement vs GPU: 4 spreads of the
     restatement's two roundings plus 8 ulps each)."""
@@ -159,7 +158,14 @@ def test_dropin_update_epoch(dropin, oracle, obj):
     X = rng.standard_normal((n, d))
     X /= np.linalg.norm(X, axis=1, keepdims=True)
     X = X.astype(np.float32)
-    y = rng.integers(0, m, n).astype(np.int64)
+    multilabel = "multilabel" in obj[0]
+    if multilabel:
+        counts = rng.integers(1, 4, n)
+        y = np.concatenate([np.sort(rng.choice(m, c, replace=False)) for c in counts]).astype(np.int64)
+        off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    else:
+        y = rng.integers(0, m, n).astype(np.int64)
+        off = None
     W0 = np.zeros((m, d), np.float32)
     A0 = np.zeros((n, m), np.float32)
     Wg, Ag, Wr, Ar = W0.copy(), A0.copy(), W0.copy(), A0.copy()
@@ -168,14 +174,14 @@ def test_dropin_update_epoch(dropin, oracle, obj):
         rc = dropin.dropin_update_epoch(
             ctypes.c_int(KIND[obj[0]]), ctypes.c_double(obj[1]), ctypes.c_double(obj[2]),
             ctypes.c_int64(obj[3]), ctypes.c_int64(d), ctypes.c_int64(m), ctypes.c_int64(n),
-            ptr(X), ptr(y), ptr(order), ctypes.c_int64(len(order)), ptr(Wg), ptr(Ag), ptr(Wr),
-            ptr(Ar))
+            ptr(X), ptr(y), ptr(off), ptr(order), ctypes.c_int64(len(order)), ptr(Wg), ptr(Ag),
+            ptr(Wr), ptr(Ar))
         assert rc == 0, rc
-    name = (ORACLE_EPOCH[obj[0]],) + tuple(obj[1:])
+    name = (obj[0][3:],) + tuple(obj[1:])
     Wo, Ao, Wv, Av = W0.copy(), A0.copy(), W0.copy(), A0.copy()
     for order in orders:
-        oracle.epoch_features(name, X, Wo, Ao, y, order, result=1)
-        oracle.epoch_features(name, X, Wv, Av, y, order, result=1, reverse=True)
+        oracle.epoch_features(name, X, Wo, Ao, y, order, result=1, offsets=off)
+        oracle.epoch_features(name, X, Wv, Av, y, order, result=1, reverse=True, offsets=off)
     eps = np.finfo(np.float32).eps
     for what, g, r, o, v in (("W", Wg, Wr, Wo, Wv), ("A", Ag, Ar, Ao, Av)):
         tol = 8 * float(np.abs(o - v).max()) + 16 * eps * max(1.0, float(np.abs(o).max()))

@@ -184,3 +184,98 @@ def test_epoch_repeated_examples(cuda, oracle):
         for g, o, v in ((Wg, Wo, Wv), (Ag, Ao, Av)):
             tol = 4 * float(np.abs(o - v).max()) + 8 * eps * max(1.0, float(np.abs(o).max()))
             assert float(np.abs(g - o).max()) <= tol
+
+
+ML_OBJS = [("l2_multilabel_hinge", 1.0, 1.0, 1), ("l2_multilabel_hinge_smooth", 0.7, 0.5, 1),
+           ("l2_multilabel_entropy", 1.0, 1.0, 1)]
+
+
+def ml_labels(rng, n, m, max_labels=4):
+    """Sorted, distinct labels per example, 1..min(max_labels, m - 1) each,
+    as CSR (labels, offsets)."""
+    counts = rng.integers(1, min(max_labels, m - 1) + 1, n)
+    labels = np.concatenate([np.sort(rng.choice(m, c, replace=False)) for c in counts])
+    return labels.astype(np.int64), np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+
+
+def check_ml(oracle, cuda, obj, dtype, result, n, d, m, seed, epochs=2, max_labels=4):
+    import torch
+    import libsdca_amd as sd
+    X, _ = problem(dtype, n, d, m, seed)
+    lab, off = ml_labels(np.random.default_rng(seed + 1), n, m, max_labels)
+    orders = [sd.epoch_order(n, e) for e in range(epochs)]
+    Xt = torch.from_numpy(X).to(cuda)
+    Wt = torch.zeros((m, d), dtype=Xt.dtype, device=cuda)
+    At = torch.zeros((n, m), dtype=Xt.dtype, device=cuda)
+    for order in orders:
+        sd.epoch_features(obj, Xt, Wt, At, lab, order=order, result=result, offsets=off)
+    torch.cuda.synchronize()
+    Wg, Ag = Wt.cpu().numpy(), At.cpu().numpy()
+    name = (obj[0][3:],) + tuple(obj[1:])
+    res = []
+    for reverse in (False, True):
+        W = np.zeros((m, d), X.dtype)
+        A = np.zeros((n, m), X.dtype)
+        for order in orders:
+            oracle.epoch_features(name, X, W, A, lab, order, result=result, reverse=reverse,
+                                  offsets=off)
+        res.append((W, A))
+    (Wo, Ao), (Wv, Av) = res
+    eps = np.finfo(dtype).eps
+    for what, g, o, v in (("W", Wg, Wo, Wv), ("A", Ag, Ao, Av)):
+        spread = float(np.abs(o - v).max())
+        tol = 4 * spread + 8 * eps * max(1.0, float(np.abs(o).max()))
+        err = float(np.abs(g - o).max())
+        print(f"{obj[0]} {np.dtype(dtype).name}/{result} m={m} {what}: |gpu - oracle| "
+              f"{err:.2e}, spread {spread:.2e}")
+        assert err <= tol, f"{obj[0]} m={m} {what}: |gpu - oracle| {err:.3e} > {tol:.3e}"
+    assert np.abs(Ao).max() > 0.01
+    assert not Ag[3].any()
+
+
+@pytest.mark.parametrize("dtype,result", PAIRS)
+@pytest.mark.parametrize("obj", ML_OBJS)
+@pytest.mark.parametrize("m", [3, 20, 257])
+def test_epoch_multilabel(cuda, oracle, obj, dtype, result, m):
+    check_ml(oracle, cuda, obj, dtype, result, 300, 64, m, 5 + m)
+
+
+@pytest.mark.parametrize("obj", ML_OBJS)
+def test_epoch_multilabel_wide(cuda, oracle, obj):
+    """m = 1500 (eight register slots per thread) with up to 40 labels per
+    example; the entropy also at m = 3000 (the vector in LDS).  fp32 data
+    with fp64 arithmetic: in fp32 arithmetic the two-block projection's own
+    sums over ~1500 rows round differently on the GPU (tree order) than in
+    the reference (sequential), by more than the scores' rounding spread
+    that the criterion measures; the fp32 pair is covered up to m = 257."""
+    check_ml(oracle, cuda, obj, np.float32, 1, 160, 48, 1500, 41, max_labels=40)
+    if obj[0] == "l2_multilabel_entropy":
+        check_ml(oracle, cuda, obj, np.float32, 1, 120, 32, 3000, 43, max_labels=40)
+
+
+def test_epoch_multilabel_errors(cuda):
+    """Label rules (1..m-1 distinct sorted labels per example): a broken
+    example is skipped and reported as SDCA_ERR_LABELS after the epoch; the
+    multilabel hinges refuse m > 2048."""
+    import torch
+    import libsdca_amd as sd
+    n, d, m = 40, 16, 9
+    X, _ = problem(np.float32, n, d, m, 3)
+    rows = [[1, 4] if i % 2 else [0, 3, 7] for i in range(n)]
+    rows[5] = [6, 2]  # not sorted
+    lab = np.array([l for r in rows for l in r], np.int64)
+    off = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int64)
+    Xt = torch.from_numpy(X).to(cuda)
+    W = torch.zeros((m, d), device=cuda)
+    A = torch.zeros((n, m), device=cuda)
+    with pytest.raises(sd.SdcaError) as e:
+        sd.epoch_features(ML_OBJS[0], Xt, W, A, lab, offsets=off)
+    assert e.value.status == 8
+    assert not A[5].any()  # skipped
+    assert A.abs().max() > 0
+    with pytest.raises(sd.SdcaError) as e:
+        Xw = torch.zeros((4, 8), device=cuda)
+        sd.epoch_features(ML_OBJS[1], Xw, torch.zeros((2049, 8), device=cuda),
+                          torch.zeros((4, 2049), device=cuda), [0, 1, 2, 3],
+                          offsets=[0, 1, 2, 3, 4])
+    assert e.value.status == 4

@@ -73,3 +73,68 @@ def test_epoch_restatement_vs_reference(oracle, reference, obj, dtype, result):
     assert np.abs(Ar).max() > 0.01 and np.abs(Wr).max() > 0.01
     # the skipped example's duals stay at zero (update.h:62)
     assert not Ar[3].any()
+
+
+ML_OBJS = [("multilabel_hinge", 1.0, 1.0, 1), ("multilabel_hinge_smooth", 0.7, 0.5, 1),
+           ("multilabel_entropy", 1.0, 1.0, 1)]
+
+
+def ml_labels(rng, n, m, max_labels=4):
+    """Sorted, distinct labels per example (validate_labels, output.h:169-208),
+    1..max_labels of them, as CSR."""
+    counts = rng.integers(1, max_labels + 1, n)
+    labels = np.concatenate([np.sort(rng.choice(m, c, replace=False)) for c in counts])
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    return labels.astype(np.int64), offsets
+
+
+def run_ml(lib, obj, X, lab, off, m, result, orders, reverse=False):
+    n, d = X.shape
+    W = np.zeros((m, d), X.dtype)
+    A = np.zeros((n, m), X.dtype)
+    for order in orders:
+        lib.epoch_features(obj, X, W, A, lab, order, result=result, reverse=reverse, offsets=off)
+    return W, A
+
+
+@pytest.mark.parametrize("dtype,result", PAIRS)
+@pytest.mark.parametrize("obj", ML_OBJS)
+def test_epoch_multilabel_restatement_vs_reference(oracle, reference, obj, dtype, result):
+    """The multilabel objectives' epoch (labels first by the reference's
+    swaps, the two-block prox, move_back) against the reference's own
+    update_variables, two epochs, the same spread criterion."""
+    import libsdca_amd as sd
+    X, _, m = problem(dtype, seed=11 + len(obj[0]))
+    n = X.shape[0]
+    lab, off = ml_labels(np.random.default_rng(5), n, m)
+    orders = [sd.epoch_order(n, e) for e in range(2)]
+    Wr, Ar = run_ml(reference, obj, X, lab, off, m, result, orders)
+    Wo, Ao = run_ml(oracle, obj, X, lab, off, m, result, orders)
+    Wv, Av = run_ml(oracle, obj, X, lab, off, m, result, orders, reverse=True)
+    eps = np.finfo(dtype).eps
+    for name, r, o, v in (("W", Wr, Wo, Wv), ("A", Ar, Ao, Av)):
+        spread = float(np.abs(o - v).max())
+        tol = 4 * spread + 8 * eps * max(1.0, float(np.abs(r).max()))
+        err = float(np.abs(o - r).max())
+        assert err <= tol, f"{obj[0]} {name}: |oracle - ref| {err:.3e} > {tol:.3e}"
+    assert np.abs(Ar).max() > 0.01 and np.abs(Wr).max() > 0.01
+    assert not Ar[3].any()
+
+
+def test_epoch_multilabel_dual_feasible(oracle):
+    """Mathematics: after an epoch every example's multilabel hinge duals
+    satisfy the constraints of the two-simplex dual (a_label >= 0, the rest
+    <= 0, sum(a_label) = -sum(rest) <= c), whatever the order."""
+    import libsdca_amd as sd
+    X, _, m = problem(np.float64, seed=3)
+    n = X.shape[0]
+    lab, off = ml_labels(np.random.default_rng(9), n, m)
+    c = 0.8
+    _, A = run_ml(oracle, ("multilabel_hinge", c, 1.0, 1), X, lab, off, m, 1,
+                  [sd.epoch_order(n, 0)])
+    for i in range(n):
+        pos = lab[off[i]:off[i + 1]]
+        neg = np.setdiff1d(np.arange(m), pos)
+        assert (A[i, pos] >= -1e-12).all() and (A[i, neg] <= 1e-12).all()
+        assert abs(A[i, pos].sum() + A[i, neg].sum()) <= 1e-9
+        assert A[i, pos].sum() <= c + 1e-9
