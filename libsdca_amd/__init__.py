@@ -392,7 +392,7 @@ def epoch_order(n, epoch):
 
 def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None, offsets=None):
     """One SDCA epoch on feature input (update_variables for each example of
-    `order`, update.h:52-85) for a multiclass objective (name, c, gamma, k):
+    `order`, update.h:52-85) for an objective (name, c, gamma, k):
     X (n, d), W (m, d), A (n, m), W and A updated in place and returned.
     CUDA tensors run on torch's current stream; numpy arrays (C-contiguous,
     X's dtype) go through the host-staging path.  order: example indices
