@@ -38,6 +38,11 @@ namespace sdca_gpu {
 namespace {
 
 constexpr int kEpochThreads = 256;
+// The block kernel's objective families (one instantiation each, so that a
+// kernel holds only its own solve): the multiclass hinges (kinds 0..3), the
+// multiclass entropy, the top-k entropy, the multilabel hinges, the
+// multilabel entropy.
+constexpr int kFamHinge = 0, kFamEnt = 1, kFamTopkEnt = 2, kFamMlHinge = 3, kFamMlEnt = 4;
 // LDS of the block kernel (gfx950: 160 KiB per workgroup), less the static
 // arrays.
 constexpr size_t kEpochLdsBytes = 144 * 1024;
@@ -119,7 +124,7 @@ __device__ __forceinline__ void for_cols(int tid, int m, F&& f) {
 // each thread keeps its entries of the example's vector, of a_i and of S_k
 // in registers, the next example's a_i and S_k loaded while this one runs;
 // PF = 0 keeps the vector in LDS and reads a_i and S_k as it goes.
-template <class D, class R, int C, int KM, int PF>
+template <class D, class R, int FK, int C, int KM, int PF>
 __global__ void __launch_bounds__(kEpochThreads)
 epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
                    const int64_t* __restrict__ order, int64_t q0, int64_t n, int nb,
@@ -153,8 +158,8 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
   D* const gd = gdummy + tid;  // global sink
   const int kind = ob.kind;
   const R c = static_cast<R>(ob.c), gamma = static_cast<R>(ob.gamma);
-  const bool hinge = kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH;
-  const bool ml = kind >= SDCA_OBJ_MULTILABEL_HINGE;
+  constexpr bool hinge = FK == kFamHinge;
+  constexpr bool ml = FK == kFamMlHinge || FK == kFamMlEnt;
   const bool smooth = kind == SDCA_OBJ_HINGE_TOPK_SMOOTH || kind == SDCA_OBJ_TOPK_HINGE_SMOOTH;
   const bool simplex = kind == SDCA_OBJ_HINGE_TOPK || kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
   const int op = simplex ? OP_TOPK_SIMPLEX_BIASED : OP_KNAPSACK_LE_BIASED;
@@ -322,7 +327,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
       continue;
     }
     const D vy = PF > 0 ? sh_vy : v[y];
-    if (ml) {
+    if constexpr (ml) {
       // The labels first (output.h:121-164): label r of the example (the
       // r-th smallest) to row r, the other rows after them in index order;
       // the two-block prox, then the recovery.
@@ -337,7 +342,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
         is_lab = lo < nl && lab[lo] == j;
         return lo;
       };
-      const bool ent = kind == SDCA_OBJ_MULTILABEL_ENTROPY;
+      constexpr bool ent = FK == kFamMlEnt;
       const D half = pa / D(2);
       for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
         bool is_lab;
@@ -348,7 +353,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
         *(ok ? cb + (is_lab ? r : nl + j - r) : ld) = xx;
       });
       __syncthreads();
-      if (ent) {  // prox_two_entropy, alpha = c norm2 (l2_multilabel_entropy.h:55-68)
+      if constexpr (ent) {  // prox_two_entropy, alpha = c norm2 (l2_multilabel_entropy.h:55-68)
         const R alpha = c * static_cast<R>(norm2);
         R t, c2;
         twoent_thresholds<D, R, G, true>(cb, m, nl, tid, alpha, t, c2);
@@ -392,7 +397,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
           setv(j, q, is_lab ? clamp_ref(x - ta, D(0), hc) : D(-1) * clamp_ref(x - tb, D(0), hc));
         });
       }
-    } else if (kind == SDCA_OBJ_ENTROPY) {
+    } else if constexpr (FK == kFamEnt) {
       // prox_two_entropy over (label | the rest), alpha = c norm2
       for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
         *(ok ? cb + (j == y ? 0 : (j < y ? j + 1 : j)) : ld) = getv(j, q);
@@ -420,7 +425,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
       });
       __syncthreads();
       const int mp = m - 1;
-      if (hinge) {
+      if constexpr (hinge) {
         bool sorted_form = true;
         if constexpr (C > 0) {
           // The register form over the whole workgroup (slot c of thread g
@@ -773,7 +778,7 @@ rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __re
   }
 }
 
-template <class D, class R, int C, int KM, int PF>
+template <class D, class R, int FK, int C, int KM, int PF>
 hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* norms,
                         const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob, int* bad) {
   const int m = static_cast<int>(a.m);
@@ -785,43 +790,64 @@ hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* no
     lds += static_cast<size_t>(kEpochBlock) * static_cast<size_t>(m) * sizeof(D);
   lds += static_cast<size_t>(m) * sizeof(int);  // the example's labels (multilabel)
   if (lds > kEpochLdsBytes) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((epoch_block_kernel<D, R, C, KM, PF>), dim3(1), dim3(kEpochThreads), lds,
+  hipLaunchKernelGGL((epoch_block_kernel<D, R, FK, C, KM, PF>), dim3(1), dim3(kEpochThreads), lds,
                      a.stream, S, Gm, a.order, q0, a.n, nb, norms, a.labels, a.offsets,
                      static_cast<D*>(a.A), Delta, gdummy, ob, m, bad);
   return hipGetLastError();
 }
 
-// The block kernel for m and k: register slots per thread PF = C from m
-// (m <= 256, 1024, 2048), and the register form of the thresholds (C > 0)
-// for the simplex and knapsack objectives with k <= 8.
+// The block kernel for the objective's family, m and k: register slots per
+// thread PF from m (m <= 256, 1024, 2048), and the register forms (C = PF)
+// of the multiclass hinges' simplex / knapsack thresholds (k <= 8 for the
+// simplex) and of the multilabel hinges' two-block simplex.
 template <class D, class R>
 hipError_t launch_block_for(const D* S, const D* Gm, int64_t q0, int nb, const D* norms,
                             const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob,
                             int* bad) {
   const int64_t m = a.m;
-  const bool simplex = a.kind == SDCA_OBJ_HINGE_TOPK || a.kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
-  // The register forms: the simplex / knapsack thresholds of the multiclass
-  // hinges (k <= 8 for the simplex) and the two-block simplex of the
-  // multilabel hinges.
-  const bool regs = (a.kind <= SDCA_OBJ_TOPK_HINGE_SMOOTH && !(simplex && a.k > 8)) ||
-                    a.kind == SDCA_OBJ_MULTILABEL_HINGE ||
-                    a.kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH;
-  const bool k5 = !simplex || a.k <= 5;
   const int pf = m <= 256 ? 1 : m <= 1024 ? 4 : m <= 2048 ? 8 : 0;
-  if (pf == 0) return launch_block<D, R, 0, 5, 0>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-  if (!regs) {
-    if (pf == 1) return launch_block<D, R, 0, 5, 1>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-    if (pf == 4) return launch_block<D, R, 0, 5, 4>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-    return launch_block<D, R, 0, 5, 8>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+#define SDCA_EPOCH_BLOCK(FK, C, KM, PF) \
+  launch_block<D, R, FK, C, KM, PF>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad)
+  // Families without a register form: one variant per PF.
+#define SDCA_EPOCH_BY_PF(FK)                                      \
+  (pf == 0 ? SDCA_EPOCH_BLOCK(FK, 0, 5, 0)                        \
+           : pf == 1 ? SDCA_EPOCH_BLOCK(FK, 0, 5, 1)              \
+                     : pf == 4 ? SDCA_EPOCH_BLOCK(FK, 0, 5, 4) : SDCA_EPOCH_BLOCK(FK, 0, 5, 8))
+  hipError_t e;
+  switch (a.kind) {
+    case SDCA_OBJ_ENTROPY:
+      e = SDCA_EPOCH_BY_PF(kFamEnt);
+      break;
+    case SDCA_OBJ_ENTROPY_TOPK:
+      e = SDCA_EPOCH_BY_PF(kFamTopkEnt);
+      break;
+    case SDCA_OBJ_MULTILABEL_ENTROPY:
+      e = SDCA_EPOCH_BY_PF(kFamMlEnt);
+      break;
+    case SDCA_OBJ_MULTILABEL_HINGE:
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:  // m <= 2048 (checked by the caller)
+      e = pf == 1 ? SDCA_EPOCH_BLOCK(kFamMlHinge, 1, 5, 1)
+                  : pf == 4 ? SDCA_EPOCH_BLOCK(kFamMlHinge, 4, 5, 4)
+                            : SDCA_EPOCH_BLOCK(kFamMlHinge, 8, 5, 8);
+      break;
+    default: {
+      const bool simplex = a.kind == SDCA_OBJ_HINGE_TOPK || a.kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
+      if (pf == 0 || (simplex && a.k > 8)) {
+        e = SDCA_EPOCH_BY_PF(kFamHinge);
+      } else if (!simplex || a.k <= 5) {
+        e = pf == 1 ? SDCA_EPOCH_BLOCK(kFamHinge, 1, 5, 1)
+                    : pf == 4 ? SDCA_EPOCH_BLOCK(kFamHinge, 4, 5, 4)
+                              : SDCA_EPOCH_BLOCK(kFamHinge, 8, 5, 8);
+      } else {
+        e = pf == 1 ? SDCA_EPOCH_BLOCK(kFamHinge, 1, 8, 1)
+                    : pf == 4 ? SDCA_EPOCH_BLOCK(kFamHinge, 4, 8, 4)
+                              : SDCA_EPOCH_BLOCK(kFamHinge, 8, 8, 8);
+      }
+    }
   }
-  if (k5) {
-    if (pf == 1) return launch_block<D, R, 1, 5, 1>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-    if (pf == 4) return launch_block<D, R, 4, 5, 4>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-    return launch_block<D, R, 8, 5, 8>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-  }
-  if (pf == 1) return launch_block<D, R, 1, 8, 1>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-  if (pf == 4) return launch_block<D, R, 4, 8, 4>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
-  return launch_block<D, R, 8, 8, 8>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad);
+#undef SDCA_EPOCH_BY_PF
+#undef SDCA_EPOCH_BLOCK
+  return e;
 }
 
 template <class D, class R>
