@@ -491,3 +491,54 @@ def test_c4_kernel_eval_full(cuda, oracle):
     pe = pe.cpu().numpy()[idx]
     compare_per_example(pe[:, :, 0], o_pe[:, :, 0], 1e-5, "kernel eval primal", x_pe[:, :, 0])
     compare_per_example(pe[:, :, 1], o_pe[:, :, 1], 1e-5, "kernel eval dual", x_pe[:, :, 1])
+
+
+def test_c4_epoch_full(cuda):
+    """One SDCA epoch at the bench's c4epoch size (d=4096, m=1000, n=100,000,
+    smooth top-5 hinge from W = 0, A = 0) and two size-independent
+    properties that any correct epoch keeps:
+      * W = A' X exactly in exact arithmetic (every update adds
+        x_i (a_new - a_old)'; eval_recompute_primal, eval/core.h:148-182,
+        relies on it): 64 classes of W against a float64 product, within
+        32 sqrt(n) eps of the classes' largest magnitude, well below one
+        example's contribution (about |W| / sqrt(n)), so a missed or doubled
+        update shows;
+      * the dual constraints of the top-k hinge (l2_hinge_topk.h:44-68): the
+        label's variable a_y = -sum of the others' (or at most c), a_y >= 0,
+        the others <= 0 and >= -a_y / k (within rounding), on every example."""
+    import torch
+    import bench
+    import libsdca_amd as sd
+    cfg = bench.CONFIGS["c4epoch"]
+    X, _, labels, _ = bench.make_eval_input(cfg, torch, cuda)
+    n, m, d = cfg["n"], cfg["m"], cfg["d"]
+    W = torch.zeros((m, d), dtype=torch.float32, device=cuda)
+    A = torch.zeros((n, m), dtype=torch.float32, device=cuda)
+    sd.epoch_features(cfg["obj"], X, W, A, labels, order=sd.epoch_order(n, 0))
+    torch.cuda.synchronize()
+    cls = torch.arange(0, m, m // 64, device=cuda)[:64]
+    Wref = (A[:, cls].double().T @ X.double())
+    eps = float(np.finfo(np.float32).eps)
+    err = float((W[cls].double() - Wref).abs().max())
+    tol = 8 * np.sqrt(n) * eps * float(Wref.abs().max())
+    print(f"epoch W vs A'X: max |W - A'X| {err:.3e}, tol {tol:.3e}, max|W| {float(Wref.abs().max()):.3e}")
+    assert err <= tol
+    c, k = cfg["obj"][1], cfg["obj"][3]
+    A64 = A.double()
+    y = labels.long()
+    ay = A64.gather(1, y[:, None])[:, 0]
+    others = A64.sum(dim=1) - ay
+    mask = torch.ones_like(A64, dtype=torch.bool)
+    mask[torch.arange(n, device=cuda), y] = False
+    tiny = 8 * eps * max(1.0, float(ay.abs().max()))
+    assert float(ay.min()) >= -tiny and float(ay.max()) <= c + tiny
+    off = A64[mask]
+    assert float(off.max()) <= tiny
+    # a_y = min(c, sum p) with p = -a_j the projected entries, each p_j at
+    # most sum(p) / k; a_y is an fp32 sum of the m - 1 entries, within
+    # 4 sqrt(m) ulps of the exact one with a wide margin
+    sp = -others
+    sum_tol = 4 * np.sqrt(m) * eps * (sp.abs() + eps)
+    assert bool(((ay - torch.clamp(sp, max=c)).abs() <= sum_tol + tiny).all())
+    assert bool((A64 >= -(sp[:, None] / k) - tiny - sum_tol[:, None]).all())
+    assert float(ay.max()) > 0.01
