@@ -1043,8 +1043,9 @@ eval_slow_kernel(const D* __restrict__ S, const int64_t* __restrict__ labels, in
 // v_mfma_f32_32x32x2f32 accumulators (16 NBW fp32 per lane).  The reduction
 // runs in slabs of 8 with the next slab prefetched into registers while the
 // current one is multiplied out of LDS ([k][row], padded rows), and visits k
-// in the same pairs and operand lanes as the unfused scores_gemm_kernel, so
-// every score is bit-identical to the unfused path's.  Then, for each half
+// in the same pairs and operand lanes as the unfused score GEMMs (step t of
+// each group of 8 sums k = 8g + t and 8g + 4 + t), so every score is
+// bit-identical to the unfused path's.  Then, for each half
 // of the 32 examples, the accumulators are written to the LDS the slabs used
 // (16 x m scores) and each wave runs the per-example epilogue
 // (eval_example_mc) on four of them with one example per wave (G = 64),
@@ -1147,7 +1148,10 @@ eval_fused_mc_kernel(const float* __restrict__ X, const float* __restrict__ W,
     const float* bs = Bs0 + cur * kFusedBK * Sh::LDB;
 #pragma unroll
     for (int kk = 0; kk < kFusedBK; kk += 2) {
-      const int kr = kk + lk;
+      // MFMA step kk / 2 of the slab's group of 8 sums k = kk / 2 (lanes
+      // 0-31) and k = 4 + kk / 2 (lanes 32-63): the k order of every score
+      // GEMM here.
+      const int kr = 4 * lk + (kk >> 1);
       const float av = as[kr * Sh::LDA + lr];
       float bv[NBW];
 #pragma unroll
