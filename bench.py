@@ -16,7 +16,8 @@ Other workloads (--config): c1 (knapsack_eq f64 m=10 n=1e5), c2cone (top-k
 cone on the headline input), c3 (entropy f64 m=1000 n=2e5), c3norm
 (entropy_norm f64), lambert (W(exp(x)) f64 on 10M points), c5prox
 (two_simplex f32 m=200 n=5e5, per-column p), c4 (evaluation pass d=4096
-m=1000 n=1e5: examples/s, roofline on the fp32 MFMA score GEMM), c5eval
+m=1000 n=1e5: examples/s, roofline on the fp32 MFMA score GEMM), c4f64 (the
+same pass in double: roofline on the fp64 MFMA score GEMM), c5eval
 (multilabel evaluation d=1024 m=200 n=5e5), c4epoch (one SDCA epoch on the C4
 data: examples/s, the reference's own epoch loop as cpu_baseline).
 
@@ -102,6 +103,11 @@ CONFIGS = {
                desc="evaluation pass, fp32: X d=4096 x n=100,000 (N(0,1), unit columns), "
                     "W d x m=1000 (N(0,0.01^2)), scores W'X, smooth top-5 hinge (gamma=1) and "
                     "softmax cross-entropy with c=1 (lambda=1/n), top-1/top-5 accuracy"),
+    "c4f64": dict(op="eval", d=4096, m=1000, n=100_000, dtype="f64", result="f64", seed=104,
+                  objs=[("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)],
+                  desc="evaluation pass, fp64: the C4 input in double (X d=4096 x n=100,000, "
+                       "W d x m=1000), scores W'X on the fp64 matrix cores, smooth top-5 hinge "
+                       "(gamma=1) and softmax cross-entropy with c=1, top-1/top-5 accuracy"),
     "c4epoch": dict(op="epoch", d=4096, m=1000, n=100_000, dtype="f32", result="f32", seed=104,
                     obj=("l2_hinge_topk_smooth", 1.0, 1.0, 5), steps=2, warmup=1,
                     desc="one SDCA epoch (update_variables over the reference solver's shuffled "
@@ -122,6 +128,7 @@ CONFIGS = {
                         "cross-entropy with c=1, rank loss"),
 }
 MFMA_F32_PEAK_TFLOPS = 157.3
+MFMA_F64_PEAK_TFLOPS = 78.6
 CPU_THREADS = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
 
 
@@ -304,6 +311,8 @@ def make_eval_input(cfg, torch, dev):
         offsets[1:] = torch.cumsum(p, 0)
         return X, W, labels, offsets
     labels = torch.randint(0, m, (n,), generator=g, device=dev)
+    if cfg["dtype"] == "f64":  # the same values in double
+        X, W = X.double(), W.double()
     return X, W, labels, None
 
 
@@ -338,7 +347,7 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
     # measured steps where it applies: the default two-kernel form is the
     # faster on MI355X, and the records must be bit-identical.
     fused_ms = None
-    if not kernel and not cfg.get("multilabel"):
+    if not kernel and not cfg.get("multilabel") and cfg["dtype"] == "f32":
         step(fused=True)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
@@ -350,7 +359,7 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
             raise RuntimeError("fused and two-kernel evaluation records differ")
     # The dominant kernel is the score GEMM: time it on its own, event-timed
     # on the stream it runs on.
-    S = torch.empty((cfg["n"], cfg["m"]), dtype=torch.float32, device=dev)
+    S = torch.empty((cfg["n"], cfg["m"]), dtype=X.dtype, device=dev)
     Wg = W.T.contiguous() if kernel else W   # the GEMM's W operand: A' for kernel input
     for _ in range(5):
         sd.scores(X, Wg, out=S)
@@ -366,6 +375,7 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
     flops = 2.0 * cfg["n"] * cfg["m"] * inner
     achieved = flops / (gemm_ms / 1e3) / 1e12
     achieved_pass = flops / (ms_per_step / 1e3) / 1e12
+    peak = MFMA_F64_PEAK_TFLOPS if cfg["dtype"] == "f64" else MFMA_F32_PEAK_TFLOPS
     value = cfg["n"] / (ms_per_step / 1e3)
     extra = {"records": recs, "fused_form_ms_per_step": fused_ms}
     if not cfg.get("multilabel"):
@@ -387,15 +397,15 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
         "config": {"workload": cfg["desc"], "d": cfg["d"], "m": cfg["m"], "n": cfg["n"],
                    "input": "kernel" if kernel else "features",
                    "objectives": [o[0] for o in objs]},
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak,
+                     "unit": "TFLOP/s", "frac": achieved / peak,
                      "traffic": traffic_of(config_name),
                      "note": f"score GEMM 2 n m {'n_train' if kernel else 'd'} = {flops:.3e} "
                              f"flop / mean event-timed launch "
                              f"{gemm_ms:.3f} ms; full pass {ms_per_step:.3f} ms"},
         "roofline_pass": {"bound": "mfma", "achieved": achieved_pass,
-                          "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                          "frac": achieved_pass / MFMA_F32_PEAK_TFLOPS,
+                          "peak": peak, "unit": "TFLOP/s",
+                          "frac": achieved_pass / peak,
                           "note": "the same flops over the whole pass (GEMM, epilogue, "
                                   "reductions, records) on the host clock"},
         "eval": extra,
@@ -505,14 +515,15 @@ def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds, kernel=False):
 
         def run(ne, nthreads):
             Xs = X[:ne].cpu().numpy()
-            A = np.zeros((ne, cfg["m"]), dtype=np.float32)  # cold start: A = 0
+            A = np.zeros((ne, cfg["m"]), dtype=Xs.dtype)  # cold start: A = 0
             ls = lab[:ne] if off is None else lab[: off[ne]]
             os_ = None if off is None else off[: ne + 1]
             t0 = time.perf_counter()
             ref.evaluate_dataset(objs, Xs, Wh, A, ls, os_, nthreads=nthreads)
             return time.perf_counter() - t0
         kind = "reference"
-        what = "the reference's evaluate_dataset (MKL sgemv scores), all objectives"
+        what = (f"the reference's evaluate_dataset (MKL {'d' if cfg['dtype'] == 'f64' else 's'}"
+                "gemv scores), all objectives")
     else:
         lib = binding.oracle()
         Wh = np.ascontiguousarray(W.T.cpu().numpy()) if kernel else W.cpu().numpy()
