@@ -43,6 +43,21 @@ hipError_t launch_one(const ProxLaunch& a) {
   if constexpr (FAM == FAM_ENT && KM == 1 && sizeof(R) >= sizeof(D) && BT == 64)
     shmem = w_lds_offset<D, R>(B, a.m, slack) +
             (static_cast<size_t>(B) * static_cast<size_t>(a.m) + slack) * sizeof(R);
+  // The plain top-k operators stream their tiles with little work per
+  // column, and HBM serves them faster with fewer tiles in flight: their
+  // workgroups reserve LDS in proportion to the tile (1.6x for the simplex,
+  // 3.2x for the cone), which caps a CU at ~100 KB (~50 KB) of tiles.  At
+  // m = 100 in fp32 (6.4 KB tiles) that is 4 (2) waves per SIMD instead of
+  // 6: 73.1 -> 73.8 % (68.3 -> 71.8 %) of the HBM peak on one box.  The
+  // biased operators and the two-simplex, which compute more per column,
+  // run slower with fewer waves and keep their natural occupancy.
+  if constexpr (FAM == FAM_TOPK && BT == 64) {
+    const size_t tile = static_cast<size_t>(B) * static_cast<size_t>(a.m) * sizeof(D);
+    size_t reserve = 0;
+    if (a.op == OP_TOPK_SIMPLEX) reserve = tile * 8 / 5;
+    if (a.op == OP_TOPK_CONE) reserve = tile * 16 / 5;
+    if (shmem < reserve) shmem = reserve;
+  }
   // m == G * C (the configuration's exact size) gets the variant without
   // per-slot validity tests (for one-wave workgroups: the wide
   // configurations are for rare sizes and keep one variant).
