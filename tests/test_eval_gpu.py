@@ -152,7 +152,7 @@ def test_epilogue_multiclass(cuda, oracle, dtype, result, m, with_a):
 
 
 @pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float64, F64)])
-@pytest.mark.parametrize("m", [3, 20, 200, 1000])
+@pytest.mark.parametrize("m", [3, 20, 150, 200, 1000])
 def test_epilogue_multilabel(cuda, oracle, dtype, result, m):
     import torch
     import libsdca_amd as sd
