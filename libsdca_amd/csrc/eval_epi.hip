@@ -1328,14 +1328,22 @@ hipError_t launch_typed(const EvalLaunch& a) {
     if (a.m <= 1024) return launch_mc<D, R, 64, 16, 8, 64, true>(a);
     return launch_mc<D, R, 64, 32, 8, 64, true>(a);
   }
+  // Double rows of 513-1024 classes: one example per two-wave workgroup, 8
+  // slots per lane.  Sixteen double slots per lane of one wave need 352
+  // registers (one wave per SIMD, with spills); eight need 229 (two waves):
+  // the C4 epilogue in double takes 2.38 ms against 2.85 ms.  (fp32 data
+  // keeps one wave per example: its fused pass forms the same sums.)
+  constexpr bool kWideDouble = sizeof(D) == 8;
   if (kmax <= 5) {
     if (a.m <= 64) return launch_mc<D, R, 4, 16, 5>(a);
     if (a.m <= 256) return launch_mc<D, R, 16, 16, 5>(a);
+    if (kWideDouble && a.m > 512 && a.m <= 1024) return launch_mc<D, R, 128, 8, 5, 128>(a);
     if (a.m <= 1024) return launch_mc<D, R, 64, 16, 5>(a);
     return launch_mc<D, R, 64, 32, 5>(a);
   }
   if (a.m <= 64) return launch_mc<D, R, 4, 16, 8>(a);
   if (a.m <= 256) return launch_mc<D, R, 16, 16, 8>(a);
+  if (kWideDouble && a.m > 512 && a.m <= 1024) return launch_mc<D, R, 128, 8, 8, 128>(a);
   if (a.m <= 1024) return launch_mc<D, R, 64, 16, 8>(a);
   return launch_mc<D, R, 64, 32, 8>(a);
 }
