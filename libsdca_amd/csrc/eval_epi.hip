@@ -1328,22 +1328,35 @@ hipError_t launch_typed(const EvalLaunch& a) {
     if (a.m <= 1024) return launch_mc<D, R, 64, 16, 8, 64, true>(a);
     return launch_mc<D, R, 64, 32, 8, 64, true>(a);
   }
-  // Double rows of 513-1024 classes: one example per two-wave workgroup, 8
-  // slots per lane.  Sixteen double slots per lane of one wave need 352
-  // registers (one wave per SIMD, with spills); eight need 229 (two waves):
-  // the C4 epilogue in double takes 2.38 ms against 2.85 ms.  (fp32 data
-  // keeps one wave per example: its fused pass forms the same sums.)
-  constexpr bool kWideDouble = sizeof(D) == 8;
+  // Double data: twice the lanes of the float mapping at half the slots
+  // (rows of 513-1024 classes: one example per two-wave workgroup).  Sixteen
+  // double slots per lane need 350 registers (one wave per SIMD, with
+  // spills); eight need 180-230 (two waves).  The epilogue in double takes
+  // 2.18 / 1.90 / 0.93 / 0.90 / 2.38 ms against 2.57 / 2.35 / 1.31 / 2.25 /
+  // 2.85 ms at m = 50 / 100 / 200 / 400 / 1000 (the last at the C4 shape).
+  // (fp32 data keeps its mapping: its fused pass forms the same sums.)
+  if constexpr (sizeof(D) == 8) {
+    if (a.m <= 1024) {
+      if (kmax <= 5) {
+        if (a.m <= 64) return launch_mc<D, R, 8, 8, 5>(a);
+        if (a.m <= 256) return launch_mc<D, R, 32, 8, 5>(a);
+        if (a.m <= 512) return launch_mc<D, R, 64, 8, 5>(a);
+        return launch_mc<D, R, 128, 8, 5, 128>(a);
+      }
+      if (a.m <= 64) return launch_mc<D, R, 8, 8, 8>(a);
+      if (a.m <= 256) return launch_mc<D, R, 32, 8, 8>(a);
+      if (a.m <= 512) return launch_mc<D, R, 64, 8, 8>(a);
+      return launch_mc<D, R, 128, 8, 8, 128>(a);
+    }
+  }
   if (kmax <= 5) {
     if (a.m <= 64) return launch_mc<D, R, 4, 16, 5>(a);
     if (a.m <= 256) return launch_mc<D, R, 16, 16, 5>(a);
-    if (kWideDouble && a.m > 512 && a.m <= 1024) return launch_mc<D, R, 128, 8, 5, 128>(a);
     if (a.m <= 1024) return launch_mc<D, R, 64, 16, 5>(a);
     return launch_mc<D, R, 64, 32, 5>(a);
   }
   if (a.m <= 64) return launch_mc<D, R, 4, 16, 8>(a);
   if (a.m <= 256) return launch_mc<D, R, 16, 16, 8>(a);
-  if (kWideDouble && a.m > 512 && a.m <= 1024) return launch_mc<D, R, 128, 8, 8, 128>(a);
   if (a.m <= 1024) return launch_mc<D, R, 64, 16, 8>(a);
   return launch_mc<D, R, 64, 32, 8>(a);
 }
