@@ -698,8 +698,11 @@ __device__ inline R smooth_two_simplex_loss(const D (&v)[C], unsigned in_a_bits,
   return loss;
 }
 
-template <int G, int C, class D, class R, int BT = 64>
-__global__ void __launch_bounds__(BT)
+// WPE: as eval_multiclass_kernel's.  The float kernel on 8 lanes x 25 slots
+// (C5) asks for 4 waves per SIMD: 127 registers instead of 134, no spills,
+// its epilogue 0.51 ms instead of 0.58 ms.
+template <int G, int C, class D, class R, int BT = 64, int WPE = 1>
+__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(WPE)))
 eval_multilabel_kernel(const D* __restrict__ S, const D* __restrict__ A,
                        const int64_t* __restrict__ labels, const int64_t* __restrict__ offsets,
                        int64_t m64, int64_t n, EvalObjs objs, double* __restrict__ per_example,
@@ -1287,7 +1290,8 @@ hipError_t launch_ml(const EvalLaunch& a) {
   constexpr int B = BT / G;
   if (a.m > static_cast<int64_t>(G) * C) return hipErrorInvalidValue;
   const int64_t blocks = (a.n + B - 1) / B;
-  hipLaunchKernelGGL((eval_multilabel_kernel<G, C, D, R, BT>), dim3(static_cast<unsigned>(blocks)),
+  constexpr int WPE = (sizeof(D) == 4 && sizeof(R) == 4 && BT == 64 && G == 8 && C == 25) ? 4 : 1;
+  hipLaunchKernelGGL((eval_multilabel_kernel<G, C, D, R, BT, WPE>), dim3(static_cast<unsigned>(blocks)),
                      dim3(BT), 0, a.stream, static_cast<const D*>(a.S), static_cast<const D*>(a.A),
                      a.labels, a.offsets, a.m, a.n, a.objs, a.per_example, a.rank, a.bad);
   return hipGetLastError();
