@@ -127,6 +127,17 @@ CONFIGS = {
                         "positive labels per example, smooth multilabel hinge and multilabel "
                         "cross-entropy with c=1, rank loss"),
 }
+# Nested in the default (c2) run: the other configurations of the path.
+NESTED_PROX = ("c1", "c3", "c3norm", "lambert", "c5prox")
+NESTED_EVAL = ("c5eval",)
+PROX_KEYS = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline",
+             "launch_floor", "cpu_baseline")
+EVAL_KEYS = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline",
+             "roofline_pass", "eval", "cpu_baseline")
+# Operators whose step is two launches: the column kernel and the kernel
+# that finishes the columns it deferred (an empty list for most inputs).
+LISTED_OPS = ("topk_simplex", "topk_cone", "topk_simplex_biased", "topk_cone_biased",
+              "knapsack_le_biased", "two_simplex_sort")
 MFMA_F32_PEAK_TFLOPS = 157.3
 MFMA_F64_PEAK_TFLOPS = 78.6
 CPU_THREADS = min(16, os.cpu_count() or 1)  # the GPU box's CPU share
@@ -147,6 +158,12 @@ def parse():
                     help="default run: skip the nested C4 evaluation-pass measurement")
     ap.add_argument("--no-epoch", action="store_true",
                     help="default run: skip the nested SDCA epoch measurement")
+    ap.add_argument("--no-nested", action="store_true",
+                    help="default run: skip the nested c1, c3, c3norm, lambert, c5prox and "
+                         "c5eval measurements")
+    ap.add_argument("--nested-steps", type=int, default=20)
+    ap.add_argument("--nested-warmup", type=int, default=20)
+    ap.add_argument("--nested-cpu-seconds", type=float, default=3.0)
     ap.add_argument("--epoch-steps", type=int, default=2)
     ap.add_argument("--epoch-warmup", type=int, default=1)
     ap.add_argument("--c4-steps", type=int, default=10)
@@ -217,6 +234,21 @@ def make_input(cfg, torch, dev):
     return x.contiguous(), col_p
 
 
+def units_of(cfg):
+    """(units per step, unit name, algorithmic HBM bytes per unit): one read
+    and one write of each column (+ its int64 split point), or of each
+    point for the elementwise map."""
+    esz = 4 if cfg["dtype"] == "f32" else 8
+    if cfg["op"] == "lambert_w_exp":
+        return cfg["m"] * cfg["n"], "points/s", 2 * esz
+    return cfg["n"], "columns/s", 2 * cfg["m"] * esz + (8 if cfg.get("col_p") else 0)
+
+
+def units_bytes(cfg):
+    units, _, per = units_of(cfg)
+    return units * per
+
+
 def kwargs_of(cfg):
     kw = {}
     for key in ("lo", "hi", "rhs", "rho", "alpha", "k"):
@@ -261,11 +293,6 @@ def cpu_baseline(cfg, x_sample, col_p_sample, seconds):
     while elapsed < 0.8 * seconds and passes < 200:
         elapsed += timed(ncols)
         passes += 1
-    if op == "lambert_w_exp":
-        pts = ncols * x_sample.shape[1] * passes
-        return {"value": pts / elapsed, "unit": "points/s", "cores": 1, "kind": kind,
-                "sample": f"{x_sample.shape[1]} points of the same input x {passes} passes, "
-                          f"1 thread, {elapsed:.1f} s"}
     # harness-parallel: columns split over the host cores (the reference's
     # functions are re-entrant; each thread has its own aux), the same
     # columns per thread as the single-thread sample where the input allows
@@ -274,12 +301,16 @@ def cpu_baseline(cfg, x_sample, col_p_sample, seconds):
     while elapsed_p < 0.5 * seconds and passes_p < 200:
         elapsed_p += timed_par(npar)
         passes_p += 1
-    return {"value": ncols * passes / elapsed, "unit": "columns/s", "cores": 1, "kind": kind,
-            "sample": f"first {ncols} columns of the same input x {passes} passes, 1 thread, "
+    if op == "lambert_w_exp":  # rows of the sample are runs of points
+        per, unit, what = x_sample.shape[1], "points/s", f"runs of {x_sample.shape[1]} points"
+    else:
+        per, unit, what = 1, "columns/s", "columns"
+    return {"value": ncols * per * passes / elapsed, "unit": unit, "cores": 1, "kind": kind,
+            "sample": f"first {ncols} {what} of the same input x {passes} passes, 1 thread, "
                       f"{elapsed:.1f} s",
-            "all_cores": {"value": npar * passes_p / elapsed_p, "unit": "columns/s",
+            "all_cores": {"value": npar * per * passes_p / elapsed_p, "unit": unit,
                           "cores": CPU_THREADS,
-                          "sample": f"first {npar} columns x {passes_p} passes over "
+                          "sample": f"first {npar} {what} x {passes_p} passes over "
                                     f"{CPU_THREADS} threads, {elapsed_p:.1f} s, harness-parallel"}}
 
 
@@ -316,8 +347,10 @@ def make_eval_input(cfg, torch, dev):
     return X, W, labels, None
 
 
-def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
+def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None,
+               cpu_seconds=None):
     """Times the evaluation pass of `cfg`; returns the result dict."""
+    cpu_seconds = args.cpu_seconds if cpu_seconds is None else cpu_seconds
     steps = args.steps if steps is None else steps
     warmup = args.warmup if warmup is None else warmup
     config_name = args.config if config_name is None else config_name
@@ -411,7 +444,7 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None):
         "eval": extra,
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline_eval(cfg, X, W, labels, offsets, args.cpu_seconds,
+        result["cpu_baseline"] = cpu_baseline_eval(cfg, X, W, labels, offsets, cpu_seconds,
                                                    kernel)
     return result
 
@@ -558,30 +591,10 @@ def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds, kernel=False):
                                     f"({dtp:.1f} s), harness-parallel"}}
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(prox columns and evaluation examples shard across GPUs with no exchange "
-              "other than a final sum of the evaluation records)", file=sys.stderr)
-        sys.exit(2)
-    import torch
-
-    import libsdca_amd as sd
-
-    cfg = CONFIGS[args.config]
-    if cfg["op"] == "epoch" and not args.copy_calibration:
-        print(json.dumps(bench_epoch(cfg, args, torch, sd)))
-        return
-    # The epoch has its own defaults; every other workload takes 20 / 50.
-    args.steps = 20 if args.steps is None else args.steps
-    args.warmup = 50 if args.warmup is None else args.warmup
-    if args.copy_calibration:
-        copy_calibration(args, torch)
-        return
-    if cfg["op"] == "eval":
-        print(json.dumps(bench_eval(cfg, args, torch, sd)))
-        return
+def bench_prox(cfg, args, torch, sd, steps, warmup, config_name, cpu_seconds):
+    """Times the batched prox of `cfg` (W untimed steps, then K steps timed on
+    the host clock and by one event pair on the kernels' stream); returns the
+    result dict, with the cpu_baseline unless --no-cpu."""
     dev = torch.device("cuda:0")
     x, col_p = make_input(cfg, torch, dev)
     rotate = cfg.get("rotate", 1)
@@ -606,12 +619,12 @@ def main():
         # exists before the capture, and replayed as one launch.
         gs = torch.cuda.Stream()
         with torch.cuda.stream(gs):
-            for i in range(args.warmup):
+            for i in range(warmup):
                 step(i)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=gs):
-            for i in range(args.steps):
+            for i in range(steps):
                 step(i)
         torch.cuda.synchronize()
         g.replay()  # untimed
@@ -623,9 +636,33 @@ def main():
         end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        avg_ms = start.elapsed_time(end) / args.steps
+        avg_ms = start.elapsed_time(end) / steps
+        # The launch floor of that graph: per step, as many launches of a
+        # kernel with no work (a one-element fill) as the step makes (one
+        # column kernel, plus the deferred-column kernel for the listed
+        # operators), captured and replayed the same way.
+        launches = 2 if cfg["op"] in LISTED_OPS else 1
+        tiny = torch.zeros(1, device=dev)
+        gf = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gf, stream=gs):
+            for i in range(steps * launches):
+                tiny.fill_(float(i & 1))
+        torch.cuda.synchronize()
+        gf.replay()  # untimed
+        torch.cuda.synchronize()
+        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        f0.record(stream)
+        gf.replay()
+        f1.record(stream)
+        torch.cuda.synchronize()
+        floor_ms = f0.elapsed_time(f1) / steps
+        floor = {"ms_per_step": floor_ms, "launches_per_step": launches,
+                 "frac_at_floor": units_bytes(cfg) / (floor_ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+                 "note": "the same K-step graph with each launch replaced by a one-element "
+                         "fill kernel: the step time no kernel of this launch count goes "
+                         "below, and the HBM fraction the workload would reach at it"}
     else:
-        for i in range(args.warmup):
+        for i in range(warmup):
             step(i)
         torch.cuda.synchronize()
         # One pair of events on the kernels' stream brackets the K timed
@@ -635,23 +672,15 @@ def main():
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         start.record(stream)
-        for i in range(args.steps):
+        for i in range(steps):
             step(i)
         end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        avg_ms = start.elapsed_time(end) / args.steps
-    ms_per_step = wall * 1e3 / args.steps
+        avg_ms = start.elapsed_time(end) / steps
+    ms_per_step = wall * 1e3 / steps
 
-    esz = 4 if cfg["dtype"] == "f32" else 8
-    if cfg["op"] == "lambert_w_exp":
-        units = cfg["m"] * cfg["n"]
-        unit = "points/s"
-        bytes_per_unit = 2 * esz
-    else:
-        units = cfg["n"]
-        unit = "columns/s"
-        bytes_per_unit = 2 * cfg["m"] * esz + (8 if cfg.get("col_p") else 0)
+    units, unit, bytes_per_unit = units_of(cfg)
     value = units / (ms_per_step / 1e3)
     achieved = units * bytes_per_unit / (avg_ms / 1e3) / 1e9
 
@@ -660,8 +689,8 @@ def main():
         "value": value,
         "unit": unit,
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -671,33 +700,77 @@ def main():
         "config": {"workload": cfg["desc"], "op": cfg["op"], "m": cfg["m"], "n": cfg["n"],
                    "result": cfg["result"], **kw, **({"hip_graph": True} if graph else {})},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_of(args.config),
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_of(config_name),
                      "note": f"algorithmic {bytes_per_unit} B per unit x {units} units per launch "
                              f"/ mean launch {avg_ms:.4f} ms (HIP events on the kernels' stream "
-                             f"around the {args.steps} timed steps; a step is the column kernel "
-                             f"and the deferred-column kernel)"
+                             f"around the {steps} timed steps; a step is the column kernel"
+                             + (" and the deferred-column kernel)" if cfg["op"] in LISTED_OPS
+                                else ")")
                              + (" (the K steps replayed from one captured HIP graph)" if graph else "")},
     }
+    if graph:
+        result["launch_floor"] = floor
     if not args.no_cpu:
         import numpy as np
         if cfg["op"] == "lambert_w_exp":
-            sample = x.reshape(-1)[:1_000_000].cpu().numpy().reshape(1, -1)
+            # 64 runs of 62,500 points: split over the threads for all_cores
+            sample = x.reshape(-1)[:4_000_000].cpu().numpy().reshape(64, -1)
         else:
             sample = x[: min(cfg["n"], 4_000_000)].cpu().numpy()
         cps = None if col_p is None else col_p[: sample.shape[0]].cpu().numpy()
         result["cpu_baseline"] = cpu_baseline(cfg, np.ascontiguousarray(sample), cps,
-                                              args.cpu_seconds)
+                                              cpu_seconds)
         del sample
+    return result
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(prox columns and evaluation examples shard across GPUs with no exchange "
+              "other than a final sum of the evaluation records)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import libsdca_amd as sd
+
+    cfg = CONFIGS[args.config]
+    if cfg["op"] == "epoch" and not args.copy_calibration:
+        print(json.dumps(bench_epoch(cfg, args, torch, sd)))
+        return
+    # The epoch has its own defaults; every other workload takes 20 / 50.
+    args.steps = 20 if args.steps is None else args.steps
+    args.warmup = 50 if args.warmup is None else args.warmup
+    if args.copy_calibration:
+        copy_calibration(args, torch)
+        return
+    if cfg["op"] == "eval":
+        print(json.dumps(bench_eval(cfg, args, torch, sd)))
+        return
+    result = bench_prox(cfg, args, torch, sd, args.steps, args.warmup, args.config,
+                        args.cpu_seconds)
     if args.config == "c2" and not args.no_c4:
         # The second north-star workload under the same clock: the whole C4
         # evaluation pass, nested (the headline value stays the prox's).
-        del xs, x, out
         torch.cuda.empty_cache()
         ev = bench_eval(CONFIGS["c4"], args, torch, sd, steps=args.c4_steps,
                         warmup=args.c4_warmup, config_name="c4")
-        result["c4"] = {key: ev[key] for key in ("value", "unit", "ms_per_step", "steps", "warmup",
-                                                 "dtype", "config", "roofline", "roofline_pass",
-                                                 "eval", "cpu_baseline") if key in ev}
+        result["c4"] = {key: ev[key] for key in EVAL_KEYS if key in ev}
+    if args.config == "c2" and not args.no_nested:
+        # The other configurations of the path, each under the same clock with
+        # its own roofline and a shorter cpu_baseline sample.
+        for name in NESTED_PROX:
+            torch.cuda.empty_cache()
+            r = bench_prox(CONFIGS[name], args, torch, sd, args.nested_steps,
+                           args.nested_warmup, name, args.nested_cpu_seconds)
+            result[name] = {key: r[key] for key in PROX_KEYS if key in r}
+        for name in NESTED_EVAL:
+            torch.cuda.empty_cache()
+            ev = bench_eval(CONFIGS[name], args, torch, sd, steps=args.c4_steps,
+                            warmup=args.c4_warmup, config_name=name,
+                            cpu_seconds=args.nested_cpu_seconds)
+            result[name] = {key: ev[key] for key in EVAL_KEYS if key in ev}
     if args.config == "c2" and not args.no_epoch:
         # The epoch row (the solver's inner loop over the prox operators) on
         # the C4 shape, nested likewise, with its own step counts.

@@ -196,6 +196,10 @@ def _label_arrays(labels, offsets, n, like):
             raise SdcaError(8, f"{off.shape[0]} offsets for {n} examples (need n + 1)")
         if int(off[-1]) != lab.shape[0]:
             raise SdcaError(8, f"offsets end at {int(off[-1])} but {lab.shape[0]} labels are given")
+        if int(off[0]) != 0:
+            raise SdcaError(8, f"offsets start at {int(off[0])}, not 0")
+        if n > 0 and bool((off[1:] < off[:-1]).any()):
+            raise SdcaError(8, "offsets decrease")
     return lab, off
 
 
@@ -412,10 +416,6 @@ def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None, of
         _need(W, "W", (m, d), X)
         _need(A, "A", (n, m), X)
         _need(norms, "norms", (n,), X)
-        lab = torch.as_tensor(labels, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
-        off = None
-        if offsets is not None:
-            off = torch.as_tensor(offsets, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
         od = None
         if order is not None:
             od = torch.as_tensor(order, dtype=torch.int64, device=X.device).contiguous().reshape(-1)
@@ -429,8 +429,6 @@ def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None, of
             if (not isinstance(a, np.ndarray) or a.dtype != X.dtype or tuple(a.shape) != shape
                     or not a.flags.c_contiguous):
                 raise SdcaError(2, f"{name}: expected a C-contiguous {X.dtype} array {shape}")
-        lab = np.ascontiguousarray(labels, dtype=np.int64).reshape(-1)
-        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64).reshape(-1)
         od = None if order is None else np.ascontiguousarray(order, dtype=np.int64).reshape(-1)
         flags, stream = HOST_PTR, None
 
@@ -438,10 +436,8 @@ def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None, of
             return None if a is None else a.ctypes.data
     data = _dtype_code(X)
     res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
-    if off is None and lab.shape[0] != n:
-        raise SdcaError(2, f"labels: expected {n} entries, got {lab.shape[0]}")
-    if off is not None and off.shape[0] != n + 1:
-        raise SdcaError(8, f"{off.shape[0]} offsets for {n} examples (need n + 1)")
+    # n labels, or n + 1 offsets from 0, non-decreasing, ending at len(labels)
+    lab, off = _label_arrays(labels, offsets, n, X)
     count = n if od is None else int(od.shape[0])
     rc = lib.sdca_epoch_features(objarr, ctypes.c_int(data), ctypes.c_int(res), ctypes.c_int64(d),
                                  ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(ptr(X)),

@@ -898,19 +898,16 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   const bool multilabel = obj->kind >= SDCA_OBJ_MULTILABEL_HINGE;
   if (multilabel && !offsets)
     return fail(SDCA_ERR_ARG_NULL, "the multilabel objectives need label offsets");
-  if ((obj->kind == SDCA_OBJ_MULTILABEL_HINGE || obj->kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH) &&
-      m > kEpochMaxMultilabelHingeM)
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "the multilabel hinge epoch supports m <= %lld",
-                (long long)kEpochMaxMultilabelHingeM);
   if (!((data == SDCA_F32 && (result == SDCA_F32 || result == SDCA_F64)) ||
         (data == SDCA_F64 && result == SDCA_F64)))
     return fail(SDCA_ERR_PRECISION,
                 "the epoch takes (float, float), (float, double) or (double, double)");
   if (d < 1 || m < 2 || n < 1 || count < 0)
     return fail(SDCA_ERR_ARG_RANGE, "need d >= 1, m >= 2, n >= 1, count >= 0");
-  if (m > epoch_max_m(data))
-    return fail(SDCA_ERR_NOT_IMPLEMENTED, "the epoch supports m <= %lld for this element type",
-                (long long)epoch_max_m(data));
+  if (m > epoch_max_m(data, obj->kind))
+    return fail(SDCA_ERR_NOT_IMPLEMENTED,
+                "the epoch supports m <= %lld for this element type and objective",
+                (long long)epoch_max_m(data, obj->kind));
   if (n > INT32_MAX || d > INT32_MAX) return fail(SDCA_ERR_ARG_RANGE, "matrix too large");
   if (!order && count > n)
     return fail(SDCA_ERR_ARG_RANGE, "count (%lld) > n (%lld) without an order",
@@ -923,12 +920,19 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   const bool host = (flags & SDCA_HOST_PTR) != 0;
   const size_t es = dtype_size(data);
   DeviceBuffer dx, dw, da, dl, doff, dord, dnorm;
+  if (host && multilabel) {
+    // The CSR structure bounds the labels staged below (offsets[n] of them);
+    // the labels' values are checked per example on the device.
+    if (offsets[0] != 0) return fail(SDCA_ERR_LABELS, "The first offset must be 0.");
+    for (int64_t i = 0; i < n; ++i)
+      if (offsets[i + 1] < offsets[i])
+        return fail(SDCA_ERR_LABELS, "offsets decrease at example %lld", (long long)i);
+  }
   if (host) {
     if ((rc = stage_in(X, es * d * n, dx, stream))) return rc;
     if ((rc = stage_in(W, es * d * m, dw, stream))) return rc;
     if ((rc = stage_in(A, es * m * n, da, stream))) return rc;
     const int64_t nlab = multilabel ? offsets[n] : n;
-    if (nlab < 0) return fail(SDCA_ERR_LABELS, "offsets[n] < 0");
     if ((rc = stage_in(labels, sizeof(int64_t) * nlab, dl, stream))) return rc;
     if (multilabel && (rc = stage_in(offsets, sizeof(int64_t) * (n + 1), doff, stream))) return rc;
     if (order && (rc = stage_in(order, sizeof(int64_t) * count, dord, stream))) return rc;

@@ -180,7 +180,8 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
     if (ml) {
       sh_off[tid] = offsets[i];
       yl = offsets[i + 1] - offsets[i];
-      if (yl < 1 || yl >= m) {
+      // a negative start is as broken as a bad count: skipped, never read
+      if (yl < 1 || yl >= m || offsets[i] < 0) {
         bad[0] = 1;
         yl = 0;
       }
@@ -778,17 +779,24 @@ rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __re
   }
 }
 
+// Dynamic LDS of the block kernel: the example's vector (m words), the
+// thresholds' column, the per-thread dummy words, the block's delta rows
+// where they always fit (the score corrections then read LDS instead of
+// global memory) and, for the multilabel families, the example's labels.
+__host__ inline size_t block_lds_bytes(size_t es, int m, int C, bool delta_in_lds, bool ml) {
+  size_t lds = (static_cast<size_t>((m + 3) & ~3) + epoch_column_words(m, C) + kEpochThreads) * es;
+  if (delta_in_lds) lds += static_cast<size_t>(kEpochBlock) * static_cast<size_t>(m) * es;
+  if (ml) lds += static_cast<size_t>(m) * sizeof(int);
+  return lds;
+}
+
 template <class D, class R, int FK, int C, int KM, int PF>
 hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* norms,
                         const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob, int* bad) {
   const int m = static_cast<int>(a.m);
-  size_t lds = (static_cast<size_t>((m + 3) & ~3) + epoch_column_words(m, C) + kEpochThreads) *
-               sizeof(D);
-  // The block's delta rows in LDS where they always fit (the score
-  // corrections then read LDS instead of global memory).
-  if constexpr (epoch_delta_in_lds<D>(PF))
-    lds += static_cast<size_t>(kEpochBlock) * static_cast<size_t>(m) * sizeof(D);
-  lds += static_cast<size_t>(m) * sizeof(int);  // the example's labels (multilabel)
+  constexpr bool ml = FK == kFamMlHinge || FK == kFamMlEnt;
+  const size_t lds = block_lds_bytes(sizeof(D), m, C, epoch_delta_in_lds<D>(PF), ml);
+  // epoch_max_m keeps every accepted m inside the budget.
   if (lds > kEpochLdsBytes) return hipErrorInvalidValue;
   hipLaunchKernelGGL((epoch_block_kernel<D, R, FK, C, KM, PF>), dim3(1), dim3(kEpochThreads), lds,
                      a.stream, S, Gm, a.order, q0, a.n, nb, norms, a.labels, a.offsets,
@@ -909,9 +917,23 @@ size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool nor
                      (norms_given ? 0 : static_cast<size_t>(n)));
 }
 
-int64_t epoch_max_m(int data) {
-  // v and the thresholds' column, each m values, in at most 128 KiB of LDS
-  return kMaxColumnBytes / (2 * (data == SDCA_F32 ? 4 : 8));
+int64_t epoch_max_m(int data, int kind) {
+  // The vector and the thresholds' column, each m values, in at most
+  // 128 KiB; and the block kernel's LDS (block_lds_bytes, with the labels of
+  // a multilabel example) within kEpochLdsBytes.  Above 2048 rows the block
+  // kernel keeps everything in LDS (PF = 0, C = 0, no delta rows), and that
+  // is the largest of its forms for a given m.
+  const size_t es = data == SDCA_F32 ? 4 : 8;
+  const bool ml = kind >= SDCA_OBJ_MULTILABEL_HINGE;
+  if (kind == SDCA_OBJ_MULTILABEL_HINGE || kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH)
+    return kEpochMaxMultilabelHingeM;
+  int64_t lo = 2, hi = static_cast<int64_t>(kMaxColumnBytes / (2 * es));
+  while (lo < hi) {  // the largest m in [2, hi] whose block kernel fits
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (block_lds_bytes(es, static_cast<int>(mid), 0, false, ml) <= kEpochLdsBytes) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
 }
 
 hipError_t launch_epoch(const EpochLaunch& a, int** flag_dev) {

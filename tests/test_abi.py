@@ -201,3 +201,39 @@ def test_wrapper_shape_and_type_checks():
     torch = pytest.importorskip("torch")
     with pytest.raises(sd.SdcaError):
         sd.scores(X, torch.zeros((5, 3)))  # numpy and torch mixed
+
+
+def test_epoch_label_structure_checks():
+    """The epoch refuses label arrays whose CSR structure would make it read
+    outside them, before touching the device: labels shorter than the
+    offsets say, offsets that do not start at 0 or that decrease (the Python
+    layer), and the same offsets handed to the C ABI directly."""
+    import libsdca_amd as sd
+    n, d, m = 4, 3, 6
+    X = np.zeros((n, d), np.float32)
+    W = np.zeros((m, d), np.float32)
+    A = np.zeros((n, m), np.float32)
+    ml = ("l2_multilabel_entropy", 1.0, 1.0, 1)
+    for labels, offsets in (([0, 1, 2], [0, 1, 2, 3, 4]),       # one label short
+                            ([0, 1, 2, 3], [-1, 1, 2, 3, 4]),   # negative start
+                            ([0, 1, 2, 3], [1, 1, 2, 3, 4]),    # does not start at 0
+                            ([0, 1, 2, 3], [0, 2, 1, 3, 4])):   # decreasing
+        with pytest.raises(sd.SdcaError) as e:
+            sd.epoch_features(ml, X, W, A, labels, offsets=offsets)
+        assert e.value.status == 8, (labels, offsets)
+    with pytest.raises(sd.SdcaError) as e:
+        sd.epoch_features(("l2_hinge_topk", 1.0, 1.0, 1), X, W, A, [0, 1, 2])  # one label short
+    assert e.value.status == 8
+    lib = sd.library()
+    obj = sd._objs([ml])
+    lab = np.array([0, 1, 2, 3], np.int64)
+    for off in ([-1, 1, 2, 3, 4], [0, 2, 1, 3, 4]):
+        o = np.array(off, np.int64)
+        rc = lib.sdca_epoch_features(obj, ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int64(d),
+                                     ctypes.c_int64(m), ctypes.c_int64(n),
+                                     ctypes.c_void_p(X.ctypes.data), ctypes.c_void_p(W.ctypes.data),
+                                     ctypes.c_void_p(A.ctypes.data),
+                                     ctypes.c_void_p(lab.ctypes.data),
+                                     ctypes.c_void_p(o.ctypes.data), None, ctypes.c_int64(n),
+                                     None, ctypes.c_uint(1), None)
+        assert rc == 8, lib.sdca_last_error()

@@ -279,3 +279,34 @@ def test_epoch_multilabel_errors(cuda):
                           torch.zeros((4, 2049), device=cuda), [0, 1, 2, 3],
                           offsets=[0, 1, 2, 3, 4])
     assert e.value.status == 4
+
+
+@pytest.mark.parametrize("dtype,result,m", [(np.float32, 0, 16384), (np.float64, 1, 8192)])
+def test_epoch_at_max_m(cuda, oracle, dtype, result, m):
+    """The largest m the C ABI accepts for a multiclass objective (the block
+    kernel's LDS at its limit); one more is refused before any launch."""
+    import torch
+    import libsdca_amd as sd
+    check(oracle, cuda, OBJS[1], dtype, result, 40, 16, m, 17, epochs=1)
+    Xt = torch.zeros((4, 8), dtype=torch.float32 if dtype == np.float32 else torch.float64,
+                     device=cuda)
+    with pytest.raises(sd.SdcaError) as e:
+        sd.epoch_features(("l2_hinge_topk_smooth", 1.0, 0.5, 3), Xt,
+                          torch.zeros((m + 1, 8), dtype=Xt.dtype, device=cuda),
+                          torch.zeros((4, m + 1), dtype=Xt.dtype, device=cuda), [0, 1, 2, 3])
+    assert e.value.status == 4
+
+
+def test_epoch_multilabel_entropy_at_max_m(cuda, oracle):
+    """The multilabel entropy keeps the example's labels in LDS too: its
+    largest m in fp32 is 12200, one more is refused before any launch."""
+    import torch
+    import libsdca_amd as sd
+    check_ml(oracle, cuda, ML_OBJS[2], np.float32, 1, 24, 16, 12200, 45, epochs=1,
+             max_labels=6)
+    with pytest.raises(sd.SdcaError) as e:
+        sd.epoch_features(ML_OBJS[2], torch.zeros((4, 8), device=cuda),
+                          torch.zeros((12201, 8), device=cuda),
+                          torch.zeros((4, 12201), device=cuda), [0, 1, 2, 3],
+                          offsets=[0, 1, 2, 3, 4])
+    assert e.value.status == 4
