@@ -95,7 +95,12 @@ twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_
     for (int i = lane; i < m; i += 64) s[i] = col[i];
     wave_lds_sync();
     R t, c, tw = 0;
-    twoent_thresholds<D, R>(s, m, p, lane, alpha, t, c, wl, &tw);
+    // The Householder steps end once f(t) is at the rounding level of its
+    // sums (NOISE_STOP): the reference's own test, a step of at most
+    // epsilon, then waits for t to stop moving between neighbouring floats
+    // (about ten passes on N(0,1) columns at m = 200 against two or three),
+    // and lands within that level too.
+    twoent_thresholds<D, R, 64, true>(s, m, p, lane, alpha, t, c, wl, &tw);
     const R tb = t + c;
     if (thr && lane == 0) {
       thr[2 * j].t = static_cast<double>(t);
@@ -108,7 +113,7 @@ twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_
     const D ta_d = static_cast<D>(t), tb_d = static_cast<D>(tb);
     D* dst = out + j * m64;
     const R dt = t - tw;  // both blocks' arguments moved by it
-    const bool tay = wl && fabs(dt) <= R(kLambertShiftMax);
+    const bool tay = wl && fabs(dt) <= lw_shift_max<R>();
     for (int i = lane; i < m; i += 64) {
       const D y = tay ? static_cast<D>(lambert_w_exp_shift(wl[i], dt))
                       : lambert_w_exp(col[i] - (i < p ? ta_d : tb_d));

@@ -90,11 +90,38 @@ __device__ inline void lw_sums2(const D* s, int m, int lane, R t, R& f0, R& f1,
   f1 = a1;
 }
 
+// Largest move dt of the shift for which a pass takes W(e^(y - dt)) from
+// the previous pass's W(e^y) by the Taylor step lambert_w_exp_shift instead
+// of a new evaluation: the omitted fourth-order term is below dt^4 w / 24,
+// 4e-10 w for float at 1e-2 and 4e-18 w for double at 1e-4, under the
+// rounding of the sums either way.
+template <class R>
+__device__ constexpr R lw_shift_max() {
+  return sizeof(R) == 4 ? R(1e-2) : R(kLambertShiftMax);
+}
+
+// The terms of the derivative sums of one W value: W / (1 + W),
+// W / (1 + W)^3 and W (1 - 2W) / (1 + W)^5 from one reciprocal of 1 + W
+// (they steer the steps; the root is where the sum of W equals its target).
+template <class R>
+__device__ inline void lw_terms(R v, R& a1, R& a2, R& a3) {
+  const R rd = div_near(R(1), R(1) + v);
+  const R rd2 = rd * rd;
+  const R rd3 = rd2 * rd;
+  a1 = v * rd;
+  a2 = v * rd3;
+  a3 = v * (R(1) - R(2) * v) * (rd3 * rd2);
+}
+
 // f0..f3: W and its first three derivatives in t (lambert.h:308-332), with
 // the shift ta for entries below p and tb beyond.
+// win (optional, with wout the same LDS array): W of every entry at shifts
+// larger by wdt (|wdt| <= lw_shift_max), from the previous pass; this pass
+// then takes each W by the Taylor step from it instead of a new evaluation.
 template <class D, class R, int NT = 64>
 __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, R& f2, R& f3,
-                                int p = -1, R tb = R(0), R* wout = nullptr) {
+                                int p = -1, R tb = R(0), R* wout = nullptr,
+                                const R* win = nullptr, R wdt = R(0)) {
   if (p < 0) {
     p = m;
     tb = t;
@@ -107,31 +134,33 @@ __device__ inline void lw_sums4(const D* s, int m, int lane, R t, R& f0, R& f1, 
       for (int u = 0; u < kLwBlock; ++u) {
         const int i = i0 + u * NT;
         const int ic = i < m ? i : m - 1;
-        v[u] = lambert_w_exp_nb(static_cast<R>(s[ic]) + (ic < p ? t : tb));
+        v[u] = win ? lambert_w_exp_shift(win[ic], wdt)
+                   : lambert_w_exp_nb(static_cast<R>(s[ic]) + (ic < p ? t : tb));
       }
 #pragma unroll
       for (int u = 0; u < kLwBlock; ++u) {
         const int i = i0 + u * NT;
         const bool ok = i < m;
         if (wout && ok) wout[i] = v[u];
-        const R d = R(1) + v[u];
-        const R d3 = d * d * d;
+        R b1, b2, b3;
+        lw_terms(v[u], b1, b2, b3);
         a0 += ok ? v[u] : R(0);
-        a1 += ok ? div_near(v[u], d) : R(0);
-        a2 += ok ? div_near(v[u], d3) : R(0);
-        a3 += ok ? div_near(v[u] * (R(1) - R(2) * v[u]), d3 * d * d) : R(0);
+        a1 += ok ? b1 : R(0);
+        a2 += ok ? b2 : R(0);
+        a3 += ok ? b3 : R(0);
       }
     }
   } else {
     for (int i = lane; i < m; i += NT) {
-      const R v = lambert_w_exp(static_cast<R>(s[i]) + (i < p ? t : tb));
+      const R v = win ? lambert_w_exp_shift(win[i], wdt)
+                      : lambert_w_exp(static_cast<R>(s[i]) + (i < p ? t : tb));
       if (wout) wout[i] = v;
-      const R d = R(1) + v;
-      const R d3 = d * d * d;
+      R b1, b2, b3;
+      lw_terms(v, b1, b2, b3);
       a0 += v;
-      a1 += div_near(v, d);
-      a2 += div_near(v, d3);
-      a3 += div_near(v * (R(1) - R(2) * v), d3 * d * d);
+      a1 += b1;
+      a2 += b2;
+      a3 += b3;
     }
   }
   group_sums<NT>(a0, a1, a2, a3);
@@ -397,11 +426,12 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
 
 // One order-4 Householder step on the two-block sum (two_entropy.h:15-38);
 // returns f(t) at the old t.
+// win / wdt: as for lw_sums4 (the previous pass's W, taken at t - wdt).
 template <class D, class R, int NT = 64>
 __device__ inline R two_w_step4(const D* s, int m, int p, int lane, R alpha, R c, R& t,
-                                R* wout = nullptr) {
+                                R* wout = nullptr, const R* win = nullptr, R wdt = R(0)) {
   R f0, f1, f2, f3;
-  lw_sums4<D, R, NT>(s, m, lane, -t, f0, f1, f2, f3, p, -t - c, wout);
+  lw_sums4<D, R, NT>(s, m, lane, -t, f0, f1, f2, f3, p, -t - c, wout, win, wdt);
   f0 -= alpha;
   const R f02 = f0 * f2, f11 = f1 * f1;
   const R den = R(6) * f1 * (f02 - f11) - f0 * (f0 * f3);
@@ -503,11 +533,18 @@ __device__ void twoent_thresholds(const D* s, int m, int p, int lane, R alpha, R
       t = (lb + ub) / R(2);
     }
   }
-  // Householder steps kept inside the bracket (:207-220).
+  // Householder steps kept inside the bracket (:207-220).  With wl, a pass
+  // whose t moved by at most lw_shift_max from the previous pass's takes its
+  // W values by the Taylor step from that pass's (left in wl).
+  bool have_w = false;
+  R t_w = 0;
   for (int iter = 0; iter < 32; ++iter) {
     t1 = t;
     if (tw) *tw = t;
-    f1 = two_w_step4<D, R, NT>(s, m, p, lane, alpha, c, t, wl);
+    const bool shift = have_w && fabs(t1 - t_w) <= lw_shift_max<R>();
+    f1 = two_w_step4<D, R, NT>(s, m, p, lane, alpha, c, t, wl, shift ? wl : nullptr, t1 - t_w);
+    have_w = wl != nullptr;
+    t_w = t1;
     if (R(0) <= f1 && f1 < lf) {
       lb = t1;
       lf = f1;

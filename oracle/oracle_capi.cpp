@@ -12,6 +12,7 @@
 // Host pointers only.  `nthreads` > 1 splits columns / examples over
 // std::threads, each with its own scratch (the reference is single-threaded;
 // the split is a harness-level partition for the CPU baseline timing).
+#include <type_traits>
 #include <cstring>
 #include <thread>
 
@@ -248,7 +249,16 @@ template <class D, class R>
 void dual_regularizer(int64_t m, int64_t n, const D* A, const D* S, double& preg, double& dreg) {
   R pr = 0, dr = 0;
   for (int64_t i = 0; i < n; ++i) {
-    R regul = static_cast<R>(orc::blas_dot<D>(m, A + i * m, S + i * m)) / 2;
+    // The reference's dot in the data type (blas.h); for a long double
+    // result the exact-arithmetic check: the dot accumulated in long double.
+    R dot = 0;
+    if (std::is_same<R, long double>::value) {
+      for (int64_t j = 0; j < m; ++j)
+        dot += static_cast<R>(A[i * m + j]) * static_cast<R>(S[i * m + j]);
+    } else {
+      dot = static_cast<R>(orc::blas_dot<D>(m, A + i * m, S + i * m));
+    }
+    R regul = dot / 2;
     pr += regul;
     dr += regul;
   }
@@ -350,6 +360,8 @@ int oracle_dual_regularizer(int data, int result, int64_t m, int64_t n, const vo
     dual_regularizer<float, double>(m, n, static_cast<const float*>(A), static_cast<const float*>(S), *preg, *dreg);
   else if (data == SDCA_F64 && result == SDCA_F64)
     dual_regularizer<double, double>(m, n, static_cast<const double*>(A), static_cast<const double*>(S), *preg, *dreg);
+  else if (data == SDCA_F32 && result == SDCA_LONG_DOUBLE)
+    dual_regularizer<float, long double>(m, n, static_cast<const float*>(A), static_cast<const float*>(S), *preg, *dreg);
   else
     return SDCA_ERR_PRECISION;
   return 0;
