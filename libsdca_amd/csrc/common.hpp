@@ -225,6 +225,36 @@ __device__ inline double lambert_w_exp_nb(double x) {
   return br == 2 ? x : (br == 5 ? ((x > -746.0) ? e : 0.0) : r);
 }
 
+// a * b + c, the constant c from a scalar register for double (fma_sconst).
+__device__ inline double fma_c(double a, double b, double c) { return fma_sconst(a, b, c); }
+__device__ inline float fma_c(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
+// W(z) for 0 <= z <= 0.06 by its series z - z^2 + 3/2 z^3 - 8/3 z^4
+// + 125/24 z^5 (relative error below 11 z^5 < 1e-5): a start for lw_step5.
+template <class R>
+__device__ inline R lambert_w_series5(R z) {
+  R p = fma_c(z, R(125.0 / 24.0), R(-8.0 / 3.0));
+  p = fma_c(p, z, R(1.5));
+  p = fma_c(p, z, R(-1));
+  p = fma_c(p, z, R(1));
+  return p * z;
+}
+
+// e^-v for 0 <= v <= 0.06: the Taylor polynomial of degree 9 (the omitted
+// term is below 0.06^10 / 10! < 2e-19).
+template <class R>
+__device__ inline R exp_neg_small(R v) {
+  R p = fma_c(v, R(-1.0 / 362880.0), R(1.0 / 40320.0));
+  p = fma_c(p, v, R(-1.0 / 5040.0));
+  p = fma_c(p, v, R(1.0 / 720.0));
+  p = fma_c(p, v, R(-1.0 / 120.0));
+  p = fma_c(p, v, R(1.0 / 24.0));
+  p = fma_c(p, v, R(-1.0 / 6.0));
+  p = fma_c(p, v, R(0.5));
+  p = fma_c(p, v, R(-1));
+  return fma_c(p, v, R(1));
+}
+
 // W(exp(y - dt)) from w = W(exp(y)) by the Taylor series in dt: the
 // derivatives of W(e^y) are g1 = w / (1 + w), g2 = w / (1 + w)^3 and
 // g3 = w (1 - 2w) / (1 + w)^5, so for |dt| <= 1e-4 the omitted fourth-order

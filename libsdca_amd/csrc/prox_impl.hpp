@@ -710,14 +710,90 @@ __device__ __forceinline__ R lds_solve_sum_w_exp(const D* x, unsigned bits, int 
   // start (below), which the other columns keep.  The root, and the
   // stopping rule that ends on it, are the same.
   const R mx = lds_masked_max<G, C, D, R>(x, bits);
-  float se = 0.0f;
+  // sum_i e_i with e_i = exp(x_i - mx), and for a double Result the power
+  // sums S_k = sum_i e_i^k, k = 2..5, of the series start below.
+  float se = 0.0f, s2 = 0.0f, s3 = 0.0f, s4 = 0.0f, s5 = 0.0f;
 #pragma unroll 4
-  for (int c = 0; c < C; ++c)
-    se += ((bits >> c) & 1u) ? expf(static_cast<float>(static_cast<R>(x[G * c]) - mx)) : 0.0f;
-  se = group_sum<G>(se);
+  for (int c = 0; c < C; ++c) {
+    const float e =
+        ((bits >> c) & 1u) ? expf(static_cast<float>(static_cast<R>(x[G * c]) - mx)) : 0.0f;
+    se += e;
+    if constexpr (sizeof(R) == 8) {
+      const float e2 = e * e;
+      s2 += e2;
+      s3 += e2 * e;
+      s4 += e2 * e2;
+      s5 += e2 * (e2 * e);
+    }
+  }
+  if constexpr (sizeof(R) == 8) group_sums<G>(se, s2, s3, s4, s5);
+  else se = group_sum<G>(se);
   const R t_lse = mx + static_cast<R>(logf(se)) - dlog(rhs);
   R t = t_lse;
-  if (!(mx - t_lse <= R(-1))) {
+  bool started = false;
+  if constexpr (sizeof(R) == 8) {
+    // Series start.  Where every value sits at least 3 below t_lse, every
+    // argument z_i = exp(x_i - t) at the root is at most ~0.05, inside the
+    // radius 1/e of W(z) = z - z^2 + 3/2 z^3 - 8/3 z^4 + 125/24 z^5 - ...
+    // With u = exp(mx - t), sum_i W(z_i) = sum_k c_k S_k u^k: the root of
+    // the five-term model (Newton in u from rhs / S_1, the log-sum-exp bound)
+    // is within ~11 u^5 (relative) of the true one.  One double pass at that
+    // t0 then evaluates every W(z_i) exactly (the series value corrected by
+    // the reference's order-5 step, lambert.h:31-42, whose error after one
+    // step is the fifth power of the series' ~1e-5) and the order-4
+    // Householder step of entropy_norm.h:84-102 lands on the root to double
+    // precision: one pass at ~80 instructions per element instead of a
+    // single- and a double-precision Lambert pass (~190).  Other columns,
+    // and a step larger than the start's error allows, take the general
+    // path below; the root is the same.
+    if (wl != nullptr && mx - t_lse <= R(-3)) {
+      const R S1 = se, S2 = s2, S3 = s3, S4 = s4, S5 = s5;
+      R u = rhs / S1;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const R g =
+            u * (S1 + u * (-S2 + u * (R(1.5) * S3 + u * (R(-8.0 / 3.0) * S4 +
+                                                         u * (R(125.0 / 24.0) * S5))))) - rhs;
+        const R gp = S1 + u * (R(-2) * S2 + u * (R(4.5) * S3 + u * (R(-32.0 / 3.0) * S4 +
+                                                                      u * (R(625.0 / 24.0) * S5))));
+        u -= g / gp;
+      }
+      const R t0 = mx - dlog(u);
+      R f0 = 0, f1 = 0, f2 = 0, f3 = 0;
+#pragma unroll 1
+      for (int c = 0; c < C; ++c) {
+        if ((bits >> c) & 1u) {
+          const R z = exp_fast(static_cast<R>(x[G * c]) - t0);
+          const R w0 = lambert_w_series5(z);
+          const R w = lw_step5(w0, z * exp_neg_small(w0));
+          wl[G * c] = w;
+          const R rd = div_near(R(1), R(1) + w);
+          const R rd2 = rd * rd;
+          const R rd3 = rd2 * rd;
+          f0 += w;
+          f1 += w * rd;
+          f2 += w * rd3;
+          f3 += w * (R(1) - R(2) * w) * (rd3 * rd2);
+        }
+      }
+      group_sums<G>(f0, f1, f2, f3);
+      f0 -= rhs;
+      const R f02 = f0 * f2, f11 = f1 * f1;
+      const R t1 =
+          t0 - R(3) * f0 * (R(2) * f11 - f02) / (R(6) * f1 * (f02 - f11) - f0 * (f0 * f3));
+      // The start's error (~1e-6 here) bounds the step; a step of at most
+      // 3e-5 leaves an order-4 correction below 1e-18.
+      if (isfinite(t1) && fabs(t1 - t0) <= R(3e-5) * dmax(R(1), fabs(t1))) {
+        if (tw) *tw = t0;
+        return t1;
+      }
+      if (isfinite(t1)) {
+        t = t1;
+        started = true;
+      }
+    }
+  }
+  if (!started && !(mx - t_lse <= R(-1))) {
     R s = 0;
 #pragma unroll 4
     for (int c = 0; c < C; ++c) s += ((bits >> c) & 1u) ? static_cast<R>(x[G * c]) : R(0);

@@ -279,6 +279,24 @@ def test_entropic(cuda, oracle, op, kw, m, dtype, result):
         parity(oracle, op, x, got, result, f"{op} {name} m={m}", **kw, thr=thr)
 
 
+@pytest.mark.parametrize("dtype,result", [(np.float64, F64), (np.float32, F64)])
+@pytest.mark.parametrize("m", [600, 1000, 2000])
+@pytest.mark.parametrize("hi,rhs", [(1.0, 1.0), (1.0, 2.4), (1.0, 2.6), (1.0, 0.05), (0.0015, 1.0),
+                                    (0.01, 0.5)])
+def test_entropy_norm_series_regime(cuda, oracle, hi, rhs, m, dtype, result):
+    """The Lambert-map projection where every value sits at least 3 below
+    the log-sum-exp bound (the series start of the double-precision solve):
+    U(-10, 10) columns, rhs from well inside that regime to its edge
+    (rhs 2.4 and 2.6 put max - t_lse near -3 at m = 1000) and beyond, and
+    small hi, whose fixing passes solve again over the remaining values."""
+    if hi * m < rhs:
+        pytest.skip("infeasible bounds for this m")
+    x = inputs.uniform(200, m, dtype, 60 + m, -10, 10)
+    got, thr = run_gpu("entropy_norm", x, result, cuda, hi=hi, rhs=rhs)
+    parity(oracle, "entropy_norm", x, got, result, f"entropy_norm series hi={hi} rhs={rhs} m={m}",
+           hi=hi, rhs=rhs, thr=thr)
+
+
 @pytest.mark.parametrize("dtype,result", DTYPES)
 @pytest.mark.parametrize("m", [2, 10, 100, 999])
 @pytest.mark.parametrize("k", [1, 3, 5, 12])
