@@ -158,6 +158,9 @@ def parse():
                     help="default run: skip the nested C4 evaluation-pass measurement")
     ap.add_argument("--no-epoch", action="store_true",
                     help="default run: skip the nested SDCA epoch measurement")
+    ap.add_argument("--trace-steps", action="store_true",
+                    help="also record an event after every timed step and print the per-step "
+                         "durations (per_step_ms)")
     ap.add_argument("--no-nested", action="store_true",
                     help="default run: skip the nested c1, c3, c3norm, lambert, c5prox and "
                          "c5eval measurements")
@@ -670,14 +673,24 @@ def bench_prox(cfg, args, torch, sd, steps, warmup, config_name, cpu_seconds):
         # per step adds its own stream packets between the steps: about 30 us
         # of the 0.55 ms C2 step.)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # --trace-steps: an event after every step as well, for the per-step
+        # durations (the transient after a cold start); the mean stays the
+        # span of the K steps / K.
+        marks = ([torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+                 if args.trace_steps else None)
         t0 = time.perf_counter()
         start.record(stream)
         for i in range(steps):
             step(i)
+            if marks:
+                marks[i].record(stream)
         end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         avg_ms = start.elapsed_time(end) / steps
+        if marks:
+            per_step = [start.elapsed_time(marks[0])] + [
+                marks[i - 1].elapsed_time(marks[i]) for i in range(1, steps)]
     ms_per_step = wall * 1e3 / steps
 
     units, unit, bytes_per_unit = units_of(cfg)
@@ -710,6 +723,8 @@ def bench_prox(cfg, args, torch, sd, steps, warmup, config_name, cpu_seconds):
     }
     if graph:
         result["launch_floor"] = floor
+    if not graph and args.trace_steps:
+        result["per_step_ms"] = [round(v, 4) for v in per_step]
     if not args.no_cpu:
         import numpy as np
         if cfg["op"] == "lambert_w_exp":

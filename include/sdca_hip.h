@@ -103,8 +103,10 @@ void sdca_prox_params_default(sdca_prox_params* params);
  *   thresholds: optional, n records (2n for the two-block operator) with the
  *           computed thresholds, in double.
  * The reference's `aux` scratch has no counterpart: scratch lives in
- * registers and LDS.  A column is held by one workgroup: m is at most 32768
- * for fp32 data and 16384 for fp64 (128 KiB of column); larger m returns
+ * registers and LDS.  A column is held by one workgroup, in LDS up to 32768
+ * rows of fp32 data and 16384 of fp64 (128 KiB of column).  Beyond that the
+ * KNAPSACK_EQ, KNAPSACK_LE, ENTROPY and ENTROPY_NORM operators stream the
+ * column from global memory (any m); the other operators return
  * SDCA_ERR_NOT_IMPLEMENTED (the elementwise LAMBERT_W_EXP takes any size).
  */
 int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result,

@@ -251,10 +251,14 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
   const bool ent_biased = op == SDCA_PROX_TOPK_ENTROPY_BIASED || op == SDCA_PROX_TWO_ENTROPY;
   // Above kRegMaxM rows a column is held by one workgroup, in LDS (the
   // sorted-column, wave-per-column and workgroup-per-column kernels).
-  if (op != SDCA_PROX_LAMBERT_W_EXP && m > max_rows(data))
+  // Above that, the knapsack and entropic operators stream the column from
+  // global memory; the others refuse.
+  const bool streamed = m > max_rows(data) && stream_supported(op);
+  if (op != SDCA_PROX_LAMBERT_W_EXP && m > max_rows(data) && !streamed)
     return fail(SDCA_ERR_NOT_IMPLEMENTED,
                 "m = %lld is above the %lld rows (%lld KiB per column) the GPU kernels hold for "
-                "this element type", (long long)m, (long long)max_rows(data),
+                "this operator and element type (knapsack_eq, knapsack_le, entropy and "
+                "entropy_norm take any m)", (long long)m, (long long)max_rows(data),
                 (long long)(kMaxColumnBytes / 1024));
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
@@ -324,6 +328,8 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
 
   if (op == SDCA_PROX_LAMBERT_W_EXP) {
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
+  } else if (streamed) {
+    SDCA_HIP_TRY(launch_stream(a), "prox kernel (column streamed from global memory)");
   } else if (op == SDCA_PROX_TWO_SIMPLEX_SORT && !reg_ok) {
     SDCA_HIP_TRY(launch_two_sort(a, true), "two_simplex_sort kernel (workgroup per column)");
   } else if (op == SDCA_PROX_TWO_ENTROPY) {

@@ -43,20 +43,21 @@ hipError_t launch_one(const ProxLaunch& a) {
   if constexpr (FAM == FAM_ENT && KM == 1 && sizeof(R) >= sizeof(D) && BT == 64)
     shmem = w_lds_offset<D, R>(B, a.m, slack) +
             (static_cast<size_t>(B) * static_cast<size_t>(a.m) + slack) * sizeof(R);
-  // The plain top-k operators stream their tiles with little work per
-  // column, and HBM serves them faster with fewer tiles in flight: their
-  // workgroups reserve LDS in proportion to the tile (1.6x for the simplex,
-  // 3.2x for the cone), which caps a CU at ~100 KB (~50 KB) of tiles.  At
-  // m = 100 in fp32 (6.4 KB tiles) that is 4 (2) waves per SIMD instead of
-  // 6: 73.1 -> 73.8 % (68.3 -> 71.8 %) of the HBM peak on one box.  The
-  // biased operators and the two-simplex, which compute more per column,
-  // run slower with fewer waves and keep their natural occupancy.
+  // The top-k cone streams its tiles with little work per column, and HBM
+  // serves them faster with fewer tiles in flight: its workgroups reserve
+  // LDS at 3.2x the tile, which caps a CU at ~50 KB of tiles (at m = 100 in
+  // fp32, 2 waves per SIMD instead of 6: 68.3 -> 71.8 % of the HBM peak on
+  // one box).  The top-k simplex keeps its natural 6 waves per SIMD: a cap
+  // at 4 gained ~1.5 % in steady state but lost ~4 % over the first few
+  // dozen launches after a cold start, when the shader clock is reduced and
+  // the kernel, whose vector issue is ~78 % of its memory time, needs every
+  // wave (cold starts measured in the first 25 launches: 0.59 ms per launch
+  // with 6 waves, 0.61-0.62 ms with 4).  The biased operators and the
+  // two-simplex, which compute more per column, keep their natural
+  // occupancy too.
   if constexpr (FAM == FAM_TOPK && BT == 64) {
     const size_t tile = static_cast<size_t>(B) * static_cast<size_t>(a.m) * sizeof(D);
-    size_t reserve = 0;
-    if (a.op == OP_TOPK_SIMPLEX) reserve = tile * 8 / 5;
-    if (a.op == OP_TOPK_CONE) reserve = tile * 16 / 5;
-    if (shmem < reserve) shmem = reserve;
+    if (a.op == OP_TOPK_CONE && shmem < tile * 16 / 5) shmem = tile * 16 / 5;
   }
   // m == G * C (the configuration's exact size) gets the variant without
   // per-slot validity tests (for one-wave workgroups: the wide

@@ -76,6 +76,12 @@ hipError_t launch_topkent(const ProxLaunch& a);
 hipError_t launch_two(const ProxLaunch& a);
 // Workgroup-per-column kernel over the flagged list (all_columns: every column).
 hipError_t launch_slow(const ProxLaunch& a, bool all_columns);
+// Columns above max_rows(data) for the operators whose thresholds come from
+// sweeps alone (knapsack_eq, knapsack_le, entropy, entropy_norm): one
+// workgroup per column, the column re-read from global memory per sweep
+// (prox_stream.hip).
+bool stream_supported(int op);
+hipError_t launch_stream(const ProxLaunch& a);
 // Elementwise lambert_w_exp over m*n elements.
 hipError_t launch_lambert(const ProxLaunch& a);
 // Zero the slow-column counter.

@@ -386,6 +386,10 @@ int oracle_epoch_features(const sdca_objective* obj, int data, int result, int64
     return orc::epoch<double, double>(*obj, d, m, n, static_cast<const double*>(X),
                                       static_cast<double*>(W), static_cast<double*>(A), labels,
                                       offsets, order, count, reverse != 0);
+  if (data == SDCA_F32 && result == SDCA_LONG_DOUBLE)
+    return orc::epoch<float, long double>(*obj, d, m, n, static_cast<const float*>(X),
+                                          static_cast<float*>(W), static_cast<float*>(A), labels,
+                                          offsets, order, count, reverse != 0);
   if (data == SDCA_F64 && result == SDCA_LONG_DOUBLE)
     return orc::epoch<double, long double>(*obj, d, m, n, static_cast<const double*>(X),
                                            static_cast<double*>(W), static_cast<double*>(A),

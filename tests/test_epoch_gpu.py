@@ -285,18 +285,52 @@ def test_epoch_multilabel_errors(cuda):
 def test_epoch_at_max_m(cuda, oracle, dtype, result, m):
     """The largest m the C ABI accepts for a multiclass objective (the block
     kernel's LDS at its limit, set by the data type); one more is refused
-    before any launch.  Double arithmetic: from W = A = 0 the first
-    example's m - 1 off-label values are all equal, and the reference's
-    sequential float sums over 16,383 of them carry ~m eps ~ 1e-3 relative
-    error, far above the scores' rounding spread this criterion measures
-    (the wide multilabel case below runs in double for the same reason)."""
+    before any launch.  The epoch starts from a small random W (A = 0): from
+    W = 0 the first example's m - 1 off-label values are all equal, a tie
+    whose branch in the top-k special cases turns on the last bit of sums
+    over thousands of equal terms (summed in another order by the
+    reference), which this criterion, the scores' rounding spread, does not
+    measure.  Double arithmetic for the same reason."""
     import torch
     import libsdca_amd as sd
-    check(oracle, cuda, OBJS[1], dtype, result, 40, 16, m, 17, epochs=1)
-    Xt = torch.zeros((4, 8), dtype=torch.float32 if dtype == np.float32 else torch.float64,
-                     device=cuda)
+    n, d = 40, 16
+    X, y = problem(dtype, n, d, m, 17)
+    W0 = (np.random.default_rng(18).standard_normal((m, d)) * 0.01).astype(dtype)
+    order = sd.epoch_order(n, 0)
+    # Above 2048 classes the thresholds come from the sorted row with
+    # compensated sums, where the reference's sequential sums over thousands
+    # of terms carry an error of their own (E, against the same epoch in
+    # long double): the bar adds it, as the prox parity tests do.
+    Xt = torch.from_numpy(X).to(cuda)
+    Wt = torch.from_numpy(W0.copy()).to(cuda)
+    At = torch.zeros((n, m), dtype=Xt.dtype, device=cuda)
+    obj = OBJS[1]
+    sd.epoch_features((ORACLE_NAME[obj[0]],) + tuple(obj[1:]), Xt, Wt, At, y, order=order,
+                      result=result)
+    torch.cuda.synchronize()
+    Wg, Ag = Wt.cpu().numpy(), At.cpu().numpy()
+    res = []
+    for reverse, res_t in ((False, result), (True, result), (False, 2)):
+        W = W0.copy()
+        A = np.zeros((n, m), dtype)
+        oracle.epoch_features(obj, X, W, A, y, order, result=res_t, reverse=reverse)
+        res.append((W, A))
+    (Wo, Ao), (Wv, Av), (Wx, Ax) = res
+    eps = np.finfo(dtype).eps
+    for name, g, o, v, xx in (("W", Wg, Wo, Wv, Wx), ("A", Ag, Ao, Av, Ax)):
+        spread = float(np.abs(o - v).max())
+        E = float(np.abs(o - xx).max())
+        base = 4 * spread + 8 * eps * max(1.0, float(np.abs(o).max()))
+        err = float(np.abs(g - o).max())
+        err_x = float(np.abs(g - xx).max())
+        print(f"max m={m} {np.dtype(dtype).name}/{result} {name}: |gpu - oracle| {err:.2e}, "
+              f"|gpu - exact| {err_x:.2e}, spread {spread:.2e}, reference error {E:.2e}")
+        assert err <= base + 3 * E, f"m={m} {name}: |gpu - oracle| {err:.3e}"
+        assert err_x <= base + 2 * E, f"m={m} {name}: |gpu - exact| {err_x:.3e}"
+    assert np.abs(Ao).max() > 0.01
+    Xz = torch.zeros((4, 8), dtype=Xt.dtype, device=cuda)
     with pytest.raises(sd.SdcaError) as e:
-        sd.epoch_features(("l2_hinge_topk_smooth", 1.0, 0.5, 3), Xt,
+        sd.epoch_features(("l2_hinge_topk_smooth", 1.0, 0.5, 3), Xz,
                           torch.zeros((m + 1, 8), dtype=Xt.dtype, device=cuda),
                           torch.zeros((4, m + 1), dtype=Xt.dtype, device=cuda), [0, 1, 2, 3])
     assert e.value.status == 4

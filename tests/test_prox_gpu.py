@@ -438,20 +438,57 @@ ALL_OPS = ["knapsack_eq", "knapsack_le", "topk_simplex", "topk_cone", "entropy",
            "topk_cone_biased", "two_simplex_sort", "topk_entropy_biased", "two_entropy"]
 
 
+STREAMED = ("knapsack_eq", "knapsack_le", "entropy", "entropy_norm")
+
+
 def test_large_m_limits(cuda):
-    """Columns above 128 KiB (32768 fp32 rows, 16384 fp64 rows) are refused by
-    every operator with SDCA_ERR_NOT_IMPLEMENTED (4); the elementwise Lambert
-    map has no column."""
+    """Columns above 128 KiB (32768 fp32 rows, 16384 fp64 rows) are refused
+    with SDCA_ERR_NOT_IMPLEMENTED (4) by the operators that hold a column in
+    LDS; the knapsack and entropic operators stream it (their parity is in
+    test_streamed_columns) and the elementwise Lambert map has no column."""
     import torch
     import libsdca_amd as sd
     for dt, npdt in ((torch.float32, np.float32), (torch.float64, np.float64)):
         m = MAX_ROWS[npdt] + 1
         x = torch.zeros((2, m), dtype=dt, device=cuda)
         for op in ALL_OPS:
+            if op in STREAMED:
+                sd.prox(op, x, k=5, p=1, hi=1.0, rhs=1.0)
+                continue
             with pytest.raises(sd.SdcaError) as e:
                 sd.prox(op, x, k=5, p=1)
             assert e.value.status == 4, op
         sd.prox("lambert_w_exp", x)
+
+
+@pytest.mark.parametrize("dtype,result,m", [(np.float32, F32, 40_000), (np.float32, F64, 40_000),
+                                            (np.float64, F64, 20_000), (np.float64, F32, 20_000),
+                                            (np.float32, F32, 100_000)])
+@pytest.mark.parametrize("op,kw", [
+    ("knapsack_eq", dict(lo=0.0, hi=1.0, rhs=1.0)),
+    ("knapsack_eq", dict(lo=-0.5, hi=0.01, rhs=3.0)),
+    ("knapsack_le", dict(lo=0.0, hi=0.001, rhs=1.0)),
+    ("knapsack_le", dict(lo=0.0, hi=1.0, rhs=100.0)),
+    ("entropy", dict(hi=1.0, rhs=1.0)),
+    ("entropy", dict(hi=1e-4, rhs=0.5)),
+    ("entropy_norm", dict(hi=1.0, rhs=1.0)),
+    ("entropy_norm", dict(hi=1e-4, rhs=0.9)),
+])
+def test_streamed_columns(cuda, oracle, op, kw, m, dtype, result):
+    """Columns beyond the 128 KiB an LDS copy holds (m = 40,000 and 100,000
+    fp32, 20,000 fp64): the knapsack and entropic operators stream each
+    column from global memory, one workgroup per column, against the
+    oracle; bounds that fix many entries (small hi) included."""
+    if kw.get("hi", 1.0) * m < kw.get("rhs", 1.0) or (op == "knapsack_eq" and
+                                                      kw["lo"] * m > kw["rhs"]):
+        pytest.skip("infeasible bounds for this m")
+    n = 6
+    for name, x in [("normal", inputs.normal(n, m, dtype, 70 + m % 97, 2.0)),
+                    ("uniform", inputs.uniform(n, m, dtype, 71 + m % 97, -10, 10))]:
+        print(f"{op} {kw} {name} m={m}", flush=True)
+        got, thr = run_gpu(op, x, result, cuda, **kw)
+        parity(oracle, op, x, got, result, f"{op} streamed {name} m={m}", nthreads=6, **kw,
+               thr=thr)
 
 
 # One wide case per operator family: (op, kwargs, inputs).  col_p: a

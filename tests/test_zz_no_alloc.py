@@ -96,3 +96,52 @@ def test_noalloc_rejects_oversized(cuda):
                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 2
     assert "fixed scratch" in lib.sdca_last_error().decode()
+
+
+def test_noalloc_allocates_nothing_on_a_fresh_stream(cuda):
+    """The property the entry point exists for: its first call on a stream
+    the library has never used allocates no device memory (the free memory
+    the driver reports is unchanged), where sdca_prox's first call on such a
+    stream allocates that stream's deferred-column list (the control, which
+    shows the measurement can see an allocation of that size).  Each stream
+    runs one torch kernel first: the runtime sets up a new stream's hardware
+    queue (2 MiB of device memory) at its first launch, whoever launches."""
+    import torch
+    sd, lib = _abi()
+    n, m = 2_000_000, 100
+    x = torch.from_numpy(inputs.label_shifted(n, m, np.float32, 905)).to(cuda)
+    params = sd.ProxParams(0.0, 1.0, 1.0, 1.0, 1.0, 5, 1)
+    code = sd.OPS["topk_simplex"]
+    # Load the kernels' code first (the runtime's own one-time cost of any
+    # first launch), on a stream of its own.
+    warm = torch.cuda.Stream()
+    _run(lib, lib.sdca_prox_noalloc, code, x[:1000].contiguous(), params,
+         ctypes.c_void_p(warm.cuda_stream))
+    out = torch.empty_like(x)
+    thr = torch.zeros((n, 3), dtype=torch.float64, device=cuda)
+    torch.cuda.synchronize()
+
+    def free_after(fn, stream):
+        torch.cuda.synchronize()
+        before = torch.cuda.mem_get_info()[0]
+        rc = fn(code, 0, 0, m, n, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                ctypes.byref(params), None, ctypes.c_void_p(thr.data_ptr()),
+                *([ctypes.c_uint(0)] if fn is lib.sdca_prox else []),
+                ctypes.c_void_p(stream.cuda_stream))
+        assert rc == 0, lib.sdca_last_error().decode()
+        torch.cuda.synchronize()
+        return before - torch.cuda.mem_get_info()[0]
+
+    def new_stream():
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            torch.zeros(1, device=cuda).add_(1.0)
+        torch.cuda.synchronize()
+        return st
+
+    fresh = new_stream()
+    assert free_after(lib.sdca_prox_noalloc, fresh) == 0
+    control = new_stream()
+    grown = free_after(lib.sdca_prox, control)
+    print(f"sdca_prox on a fresh stream took {grown} bytes")
+    assert grown >= 4 * n  # its list of n column indices
