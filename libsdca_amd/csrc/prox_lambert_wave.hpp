@@ -255,12 +255,61 @@ __device__ inline bool guarded_step(const D* s, int m, int lane, R alpha, R& t, 
 template <class D, class R, int NT = 64>
 __device__ inline bool lse_start(const D* s, int m, int p, R c, R e, R mx, R rhs, int lane,
                                  R& t_lse) {
-  float se = (e > -num<R>::inf()) ? expf(static_cast<float>(e - mx)) : 0.0f;
+  // the extra value once (by the group's first thread), the column's values
+  // by their threads
+  float se = (lane == 0 && e > -num<R>::inf()) ? expf(static_cast<float>(e - mx)) : 0.0f;
   for (int i = lane; i < m; i += NT)
     se += expf(static_cast<float>(static_cast<R>(s[i]) - (i < p ? R(0) : c) - mx));
   se = group_sum<NT>(se);
   t_lse = mx + static_cast<R>(logf(se)) - dlog(rhs);
   return mx - t_lse <= R(-1);
+}
+
+// The series start of a Lambert-map solve over the column s[0, m) and the
+// extra value e (if finite), with mx the largest of them: where every value
+// sits at least 3 below the log-sum-exp bound t_lse of sum W(e^(x - t)) =
+// rhs, every argument at the root is at most ~0.05 and
+// sum W(e^(x - t)) = sum_k c_k S_k u^k (u = e^(mx - t), S_k the power sums
+// of e^(x - mx), W's series c = 1, -1, 3/2, -8/3, 125/24); t0 is the root
+// of that five-term model by Newton in u from rhs / S_1, within ~11 u^5
+// (relative) of the true one (as lds_solve_sum_w_exp in prox_impl.hpp).
+// Returns whether the start applies.
+template <class D, class R, int NT = 64>
+__device__ inline bool series_start(const D* s, int m, R e, R mx, R rhs, int lane, R& t0) {
+  float s1 = 0.0f, s2 = 0.0f, s3 = 0.0f, s4 = 0.0f, s5 = 0.0f;
+  auto add = [&](float v) {
+    const float v2 = v * v;
+    s1 += v;
+    s2 += v2;
+    s3 += v2 * v;
+    s4 += v2 * v2;
+    s5 += v2 * (v2 * v);
+  };
+  if (lane == 0 && e > -num<R>::inf()) add(expf(static_cast<float>(e - mx)));
+  for (int i = lane; i < m; i += NT) add(expf(static_cast<float>(static_cast<R>(s[i]) - mx)));
+  group_sums<NT>(s1, s2, s3, s4, s5);
+  const R t_lse = mx + static_cast<R>(logf(s1)) - dlog(rhs);
+  if (!(mx - t_lse <= R(-3))) return false;
+  const R S1 = s1, S2 = s2, S3 = s3, S4 = s4, S5 = s5;
+  R u = rhs / S1;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const R g = u * (S1 + u * (-S2 + u * (R(1.5) * S3 + u * (R(-8.0 / 3.0) * S4 +
+                                                             u * (R(125.0 / 24.0) * S5))))) - rhs;
+    const R gp = S1 + u * (R(-2) * S2 + u * (R(4.5) * S3 + u * (R(-32.0 / 3.0) * S4 +
+                                                                  u * (R(625.0 / 24.0) * S5))));
+    u -= g / gp;
+  }
+  t0 = mx - dlog(u);
+  return isfinite(t0);
+}
+
+// W(e^x) for x whose e^x is at most ~0.06: the series value corrected by
+// the reference's order-5 step (lambert.h:31-42), exact to double rounding.
+__device__ inline double lambert_w_exp_small(double x) {
+  const double z = exp_fast(x);
+  const double w0 = lambert_w_series5(z);
+  return lw_step5(w0, z * exp_neg_small(w0));
 }
 
 // Thresholds (t, 0, hi) of one column whose copy is in s[0, m); entries of U
@@ -317,6 +366,49 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     }
   }
   bool warm = false;
+  bool solved = false;
+  if constexpr (sizeof(R) == 8 && NT == 64) {
+    // Series start (every value, alpha included, at least 3 below the
+    // log-sum-exp bound, as on U(-10, 10) columns): one double pass at the
+    // series root t0 with every W from the series and the order-5 step,
+    // then the order-4 Householder step; accepted when it stays inside the
+    // bracket and moves t by at most 3e-5 (the next correction is then below
+    // 1e-18).  s at t0 is carried to the final t by its Taylor series, as
+    // after the warm start below.
+    const R top = (alpha > max) ? alpha : max;
+    R t0;
+    if (wl && series_start<D, R, NT>(s, m, alpha, top, alpha, lane, t0) && t0 > br_lo &&
+        t0 < br_hi) {
+      R f0 = 0, f1 = 0, f2 = 0, f3 = 0;
+      for (int i = lane; i < m; i += NT) {
+        const R w = lambert_w_exp_small(static_cast<R>(s[i]) - t0);
+        wl[i] = w;
+        R b1, b2, b3;
+        lw_terms(w, b1, b2, b3);
+        f0 += w;
+        f1 += b1;
+        f2 += b2;
+        f3 += b3;
+      }
+      group_sums<NT>(f0, f1, f2, f3);
+      const R s0 = f0 / alpha, d0 = f1 / alpha, d1 = f2 / alpha;
+      const R v = lambert_w_exp_small(alpha - t0);
+      R b1, b2, b3;
+      lw_terms(v, b1, b2, b3);
+      const R g = f0 + v - alpha;
+      const R g1 = f1 + b1, g2 = f2 + b2, g3 = f3 + b3;
+      const R g02 = g * g2, g11 = g1 * g1;
+      const R t1 = t0 - R(3) * g * (R(2) * g11 - g02) / (R(6) * g1 * (g02 - g11) - g * (g * g3));
+      if (isfinite(t1) && t1 > br_lo && t1 < br_hi &&
+          fabs(t1 - t0) <= R(3e-5) * dmax(R(1), fabs(t1))) {
+        const R dt = t1 - t0;
+        sv = s0 - dt * d0 + R(0.5) * dt * dt * d1;
+        if (tw) *tw = t0;
+        t = t1;
+        solved = true;
+      }
+    }
+  }
   if constexpr (sizeof(R) == 8) {
     // The same guarded iteration in single precision first (a Lambert pass
     // costs about a third): it ends once a step moves t by at most 3e-3
@@ -328,7 +420,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     float lo_f = static_cast<float>(br_lo), hi_f = static_cast<float>(br_hi);
     const float alpha_f = static_cast<float>(alpha);
     bool settled = false;
-    for (int iter = 0; iter < 16 && !settled; ++iter) {
+    for (int iter = 0; iter < 16 && !settled && !solved; ++iter) {
       const float t1 = tf;
       bool ok = guarded_step<D, float, NT>(s, m, lane, alpha_f, tf, lo_f, hi_f, nullptr);
       settled = ok && fabsf(t1 - tf) <= 3.0e-3f * fmaxf(1.0f, fabsf(tf));
@@ -336,7 +428,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     if (settled) t = static_cast<R>(tf);
     warm = settled;
   }
-  for (int iter = 0; iter < 64; ++iter) {
+  for (int iter = 0; iter < 64 && !solved; ++iter) {
     const R t1 = t;
     if (tw) *tw = t;
     R ds[2];
