@@ -313,10 +313,13 @@ __device__ inline float lambert_w_exp_mixed(float x) { return lambert_w_exp(x); 
 // ---------------------------------------------------------------------------
 template <int OFF, bool VALU = false>
 __device__ inline int xor_lane(int v) {
+  // bound_ctrl (last argument) set: a lane whose source is outside its row
+  // reads 0, as the old value 0 would give, and the compiler needs no move
+  // of 0 into the destination first.
   if constexpr (OFF == 1) {
-    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
   } else if constexpr (OFF == 2) {
-    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
   } else if constexpr (!VALU) {
     if constexpr (OFF < 32) {
       return __builtin_amdgcn_ds_swizzle(v, (OFF << 10) | 0x1F);  // and 0x1F, xor OFF
@@ -324,11 +327,11 @@ __device__ inline int xor_lane(int v) {
       return __shfl_xor(v, OFF, 64);
     }
   } else if constexpr (OFF == 4) {
-    const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, false);  // row_shl:4
-    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, true);  // row_shl:4
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
     return (__lane_id() & 4) ? dn : up;
   } else if constexpr (OFF == 8) {
-    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, true);  // row_ror:8
   } else {
     // The swap with both operands v leaves rows (r0, r0, r2, r2) in the
     // first result and (r1, r1, r3, r3) in the second (16-lane rows; for
@@ -585,6 +588,47 @@ __device__ inline void top_insert(double (&top)[L], double x, double = 0) {
     top[i] = (top[i] < lo) ? lo : top[i];
   }
   top[0] = (top[0] < x) ? x : top[0];
+}
+
+// Insertion of the (N+1)-th value into a list whose entries N.. are still
+// -inf: levels above N stay -inf and level N takes min(top[N-1], x), so the
+// insertion costs N + 1 operations instead of L.
+template <int N, int L>
+__device__ inline void top_insert_first(float (&top)[L], float x, float pinf) {
+  static_assert(N < L, "a level of the list");
+  if constexpr (N > 0) {
+    top[N] = __builtin_amdgcn_fmed3f(top[N - 1], x, -pinf);
+#pragma unroll
+    for (int i = N - 1; i >= 1; --i) top[i] = __builtin_amdgcn_fmed3f(top[i - 1], top[i], x);
+  }
+  top[0] = __builtin_amdgcn_fmed3f(top[0], x, pinf);
+}
+template <int N, int L>
+__device__ inline void top_insert_first(double (&top)[L], double x, double) {
+  static_assert(N < L, "a level of the list");
+  if constexpr (N > 0) {
+    top[N] = (top[N - 1] < x) ? top[N - 1] : x;
+#pragma unroll
+    for (int i = N - 1; i >= 1; --i) {
+      double lo = (top[i - 1] < x) ? top[i - 1] : x;
+      top[i] = (top[i] < lo) ? lo : top[i];
+    }
+  }
+  top[0] = (top[0] < x) ? x : top[0];
+}
+
+// The top list (entries -inf on entry) of the slots v[N..C): the first L
+// slots by top_insert_first, the rest by top_insert.
+template <int N, int L, int C, class D>
+__device__ inline void top_fill(D (&top)[L], const D (&v)[C], D pinf) {
+  if constexpr (N < C) {
+    if constexpr (N < L) {
+      top_insert_first<N>(top, v[N], pinf);
+    } else {
+      top_insert(top, v[N], pinf);
+    }
+    top_fill<N + 1>(top, v, pinf);
+  }
 }
 
 // Merge the top lists of the G lanes of a group (every lane ends with the

@@ -161,7 +161,7 @@ __device__ inline bool smooth_topk_hinge(const D (&h)[C], int mp, int nvalid, in
   const R hi = gamma / K;
   // Scores of an untrained model put every h within hi of the k-th largest:
   // the fixing over all slots is common here and stays in registers.
-  KnapState<R> st = topk_knapsack<G, C, L, D, R, false>(h, top, mp, nvalid, kth, hi, gamma,
+  KnapState<R> st = topk_knapsack<G, C, L, D, R, false>(h, top, mp, nvalid, k, kth, hi, gamma,
                                                          lds_col, lds_dummy);
   if (!constant) {
     bool lt;

@@ -138,6 +138,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
   R t = div_near(total - sum_u0 - rhs + static_cast<R>(n_u0) * hi, static_cast<R>(mc));
   R t_acc = t;
   bool have_acc = false;
+  int n_f = 0;
   KnapState<R> st;
   st.lo_cut = -num<R>::inf();
   st.hi_cut = hi_cut0;
@@ -175,27 +176,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
       st.c_hi = c_hi;
       st.n_u += n_hi;
       st.sum_u += s_hi;
-      // The iteration's t carries the rounding of its incremental updates
-      // (m t - sum + n hi is a difference of large sums, then divided by the
-      // shrinking free count: in float at m = 100 that is ~1e-5 of t).  The
-      // threshold applied is formed once more from the final free set F,
-      // t = (sum_F a + |U| hi + |L| lo - rhs) / |F|, as the reference's
-      // SDCA_ACCURATE_MATH build does (knapsack_eq.h:87-106, Lemma 5.3 of
-      // Kiwiel's paper); the branch tests keep the iteration's t.
-      const int n_f = mc - n_lo - n_hi;
-      if (n_f > 0) {
-        R s_f = 0;
-#pragma unroll UW
-        for (int c = 0; c < C; ++c) {
-          const R wc = get(c);
-          s_f += (wc > c_lo && !(wc > c_hi)) ? wc : R(0);
-        }
-        s_f = group_sum<G>(s_f);
-        const int n_l = m - st.n_u - n_f;
-        t_acc = div_near(s_f + static_cast<R>(st.n_u) * hi + static_cast<R>(n_l) * lo - rhs,
-                         static_cast<R>(n_f));
-        have_acc = true;
-      }
+      n_f = mc - n_lo - n_hi;
       break;
     }
     R next;
@@ -221,6 +202,31 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
     } else {
       break;
     }
+  }
+  // The iteration's t carries the rounding of its incremental updates
+  // (m t - sum + n hi is a difference of large sums, then divided by the
+  // shrinking free count: in float at m = 100 that is ~1e-5 of t).  The
+  // threshold applied is formed once more from the final free set F (the
+  // free values between the last pass's candidate cuts),
+  // t = (sum_F a + |U| hi + |L| lo - rhs) / |F|, as the reference's
+  // SDCA_ACCURATE_MATH build does (knapsack_eq.h:87-106, Lemma 5.3 of
+  // Kiwiel's paper); the branch tests keep the iteration's t.  It runs once
+  // after the loop, for every column of the wave together, rather than in
+  // the pass where each column ends.  n_f is the same on every lane of a
+  // group (it comes from group sums), so the group sum below sees its
+  // whole group.
+  if (n_f > 0) {
+    R s_f = 0;
+#pragma unroll UW
+    for (int c = 0; c < C; ++c) {
+      const R wc = get(c);
+      s_f += (wc > st.c_lo && !(wc > st.c_hi)) ? wc : R(0);
+    }
+    s_f = group_sum<G>(s_f);
+    const int n_l = m - st.n_u - n_f;
+    t_acc = div_near(s_f + static_cast<R>(st.n_u) * hi + static_cast<R>(n_l) * lo - rhs,
+                     static_cast<R>(n_f));
+    have_acc = true;
   }
   st.t = t;
   st.t_acc = have_acc ? t_acc : t;
@@ -456,6 +462,231 @@ __device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R 
 template <int G>
 constexpr int kCandSlots = (G <= 2) ? 8 : (G <= 4) ? 4 : (G <= 16) ? 2 : 1;
 
+// Lane J's value of a quad (the group of four lanes a lane belongs to).
+template <int J, class T>
+__device__ inline T quad_lane(T v) {
+  if constexpr (sizeof(T) == 8) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b & 0xffffffffll), J * 0x55,
+                                               0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), J * 0x55, 0xF, 0xF,
+                                               true);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) |
+                                static_cast<long long>(static_cast<unsigned>(lo)));
+  } else {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), J * 0x55, 0xF, 0xF, true));
+  }
+}
+
+// max(a, b) where bound is +inf, min(a, b) where it is -inf.
+__device__ inline float max_or_min(float a, float b, float bound) {
+  return __builtin_amdgcn_fmed3f(a, b, bound);
+}
+__device__ inline double max_or_min(double a, double b, double bound) {
+  return (bound > 0) ? ((a < b) ? b : a) : ((b < a) ? b : a);
+}
+
+// Descending bitonic sort of the N = G * CC values of a group of G = 4
+// lanes (a quad), element i = g CC + c in slot c of lane g: strides
+// below CC exchange slots of a lane, strides CC and 2 CC exchange lanes by
+// quad permutations.  Every compare-exchange keeps the larger value at the
+// lower index where its block sorts descending, the smaller where it sorts
+// ascending (Batcher's network); a lane's direction is the same for all its
+// slots in each pass, so each exchange is one median with a bound of +inf
+// (keep the larger) or -inf (keep the smaller).
+template <int G, int CC, class D>
+__device__ inline void group_sort_desc(D (&x)[CC], int g) {
+  constexpr int N = G * CC;
+  static_assert(G == 4, "quads");
+  static_assert((CC & (CC - 1)) == 0, "slots a power of two");
+  const D pinf = net_inf(D(0));
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride >>= 1) {
+      if (stride < CC) {
+#pragma unroll
+        for (int c = 0; c < CC; ++c) {
+          if ((c & stride) == 0) {
+            const bool desc = size == N || ((g * CC + c) & size) == 0;
+            const D b = desc ? pinf : -pinf;
+            const D lo = x[c], hi = x[c + stride];
+            x[c] = max_or_min(lo, hi, b);
+            x[c + stride] = max_or_min(lo, hi, -b);
+          }
+        }
+      } else {
+        const int lanes = stride / CC;  // 1 or 2: the partner is lane g ^ lanes
+        const bool desc = size == N || ((g * CC) & size) == 0;
+        const bool lower = (g & lanes) == 0;
+        const D b = (lower == desc) ? pinf : -pinf;
+#pragma unroll
+        for (int c = 0; c < CC; ++c) {
+          const D y = (lanes == 1) ? xor_lane<1>(x[c]) : xor_lane<2>(x[c]);
+          x[c] = max_or_min(x[c], y, b);
+        }
+      }
+    }
+  }
+}
+
+// The exact root of the top-k simplex's knapsack from its sorted
+// candidates, for groups of 4 lanes: the <= N = G * CC candidates (every
+// value above a_(k) - hi - slack; the rest end at 0) at lds_col[0, total)
+// are sorted descending across the group, a_0 >= a_1 >= ...  With
+// f(t) = sum_i clamp(a_i - t, 0, hi), the root t* of f(t) = rhs has
+// U = ranks [0, u) at hi, M = ranks [u, e) free and the rest at 0, where
+//   * e is the first rank with f(a_e) >= rhs (a_e <= t*, f decreasing),
+//     from prefix sums and the sorted top list every lane holds, each lane
+//     testing its own ranks at once;
+//   * u is the U count for which t_u = (sum_M a + u hi - rhs) / (e - u)
+//     (t = (sum_F a + |U| hi + |L| lo - rhs) / |F|, knapsack_eq.h:87-106)
+//     puts a_(u-1) at or above t_u + hi and a_u below it; u < k.
+// That is the partition Kiwiel's variable fixing ends with
+// (knapsack_eq.h:25-109), found with a fixed instruction count instead of a
+// data-dependent number of passes (a wave pays for the slowest of its
+// columns).  The sum over M is taken once more directly for the threshold
+// applied.  Where M is empty (every one of the k largest at hi: f is flat
+// at k hi over [a_k, a_(k-1) - hi]), any t of that interval gives the same
+// projection; the record takes its midpoint.  The f tests allow eps
+// (= eps max(1, |rhs|), the fixing's own tolerance) for the rounding of
+// k hi against rhs.  Returns false, for the variable fixing to decide, when
+// no u fits (ties with a threshold at rounding level), hi <= 0 or a value
+// is not finite.
+template <int G, int CC, int L, class D, class R>
+__device__ inline bool topk_sorted_root(const D* lds_col, int total, const D (&top)[L], int k,
+                                        R hi, R rhs, KnapState<R>& st) {
+  constexpr int N = G * CC;
+  const int g = static_cast<int>(threadIdx.x) % G;
+  const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
+  D x[CC];
+#pragma unroll
+  for (int c = 0; c < CC; ++c) {
+    const int i = g * CC + c;
+    const D v = lds_col[i];
+    x[c] = (i < total) ? v : -num<D>::inf();
+  }
+  group_sort_desc<G, CC>(x, g);
+  // Exclusive prefix sums: within the lane (ex), then the lanes before it
+  // (base), every lane adding the lane totals in the same order.
+  R ex[CC];
+  R tot = 0;
+#pragma unroll
+  for (int c = 0; c < CC; ++c) {
+    ex[c] = tot;
+    tot += (g * CC + c < total) ? static_cast<R>(x[c]) : R(0);
+  }
+  const R t0 = quad_lane<0>(tot), t1 = quad_lane<1>(tot), t2 = quad_lane<2>(tot),
+          t3 = quad_lane<3>(tot);
+  const R base = (g >= 1 ? t0 : R(0)) + (g >= 2 ? t1 : R(0)) + (g >= 3 ? t2 : R(0));
+  const R all = ((t0 + t1) + t2) + t3;
+  // The f test on the lane's ranks; e = the first passing rank (ranks at or
+  // past total hold the values below the cut, which pass).  With
+  // f(a_r) = sum_{i<r} (a_i - a_r) - sum_{i<r} max(a_i - hi - a_r, 0), the
+  // second sum runs over the values above a_r + hi: the k largest cover it
+  // unless more than k values lie there, and then f(a_r) >= k hi passes
+  // either way.
+  R thj[L - 1];
+#pragma unroll
+  for (int j = 0; j < L - 1; ++j)
+    thj[j] = (j < k) ? static_cast<R>(top[j]) - hi : -num<R>::inf();
+  const R target = rhs - eps;
+  int e = N;
+#pragma unroll
+  for (int c = CC - 1; c >= 0; --c) {
+    const int r = g * CC + c;
+    const R a = static_cast<R>(x[c]);
+    R over = 0;
+#pragma unroll
+    for (int j = 0; j < L - 1; ++j) over += dmax(thj[j] - a, R(0));
+    const R f = ((base + ex[c]) - static_cast<R>(r) * a) - over;
+    const bool pass = r >= total || f >= target;
+    e = pass ? r : e;
+  }
+  e = group_min<G>(e);
+  if (e > total) e = total;
+  // Prefix sums of the k largest from the top list: pk[j] = sum of top[0, j).
+  R pk[L];
+  pk[0] = 0;
+#pragma unroll
+  for (int j = 1; j < L; ++j) pk[j] = pk[j - 1] + static_cast<R>(top[j - 1]);
+  // sum of ranks [0, e) and a_e: the owner lane's, summed over the group
+  // (the other lanes give 0; a_e = -inf past the candidates).
+  R pe = 0, ae = 0;
+#pragma unroll
+  for (int c = 0; c < CC; ++c) {
+    const bool own = g * CC + c == e;
+    pe = own ? base + ex[c] : pe;
+    ae = own ? static_cast<R>(x[c]) : ae;
+  }
+  group_sums<G>(pe, ae);
+  if (e >= N) {
+    pe = all;
+    ae = -num<R>::inf();
+  }
+  // u: the smallest U count whose t_u = num / (e - u) puts a_(u-1) at or
+  // above t_u + hi and a_u below it (compared without the division).
+  int u = -1;
+#pragma unroll
+  for (int j = L - 2; j >= 0; --j) {
+    if (j < k && j < e) {
+      const R den = static_cast<R>(e - j);
+      const R num_j = (pe - pk[j]) + static_cast<R>(j) * hi - rhs;
+      const bool above = j == 0 || (static_cast<R>(top[j > 0 ? j - 1 : 0]) - hi) * den >= num_j;
+      const bool below = (static_cast<R>(top[j]) - hi) * den < num_j;
+      u = (above && below) ? j : u;
+    }
+  }
+  const bool usable = hi > 0 && static_cast<R>(top[0]) < num<R>::inf();
+  st.lo_cut = -num<R>::inf();
+  st.hi_cut = num<R>::inf();
+  if (u >= 0) {
+    // The threshold applied, from the sum over M taken directly; the sets
+    // as value cuts (U = values above a_u, M = the rest above a_e).
+    R sm = 0;
+#pragma unroll
+    for (int c = 0; c < CC; ++c) {
+      const int r = g * CC + c;
+      sm += (r >= u && r < e) ? static_cast<R>(x[c]) : R(0);
+    }
+    sm = group_sum<G>(sm);
+    const R t = div_near(sm + static_cast<R>(u) * hi - rhs, static_cast<R>(e - u));
+    R su = 0, au = 0;
+#pragma unroll
+    for (int j = 0; j < L - 1; ++j) {
+      su = (j == u) ? pk[j] : su;
+      au = (j == u) ? static_cast<R>(top[j]) : au;
+    }
+    st.t = t;
+    st.t_acc = t;
+    st.n_u = u;
+    st.sum_u = su;
+    st.c_hi = au;
+    st.c_lo = ae;
+    return usable;
+  }
+  // M empty: the k largest at hi, the rest (a_k = the largest of them) at 0.
+  R kth = 0, ak = -num<R>::inf(), sk = 0;
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    kth = (j == k - 1) ? static_cast<R>(top[j]) : kth;
+    ak = (j == k) ? static_cast<R>(top[j]) : ak;
+    sk = (j == k) ? pk[j] : sk;
+  }
+  if (e == k && ak <= kth - hi) {
+    const R t = (ak > -num<R>::inf()) ? R(0.5) * ak + R(0.5) * (kth - hi) : kth - hi;
+    st.t = t;
+    st.t_acc = t;
+    st.n_u = k;
+    st.sum_u = sk;
+    st.c_hi = ak;
+    st.c_lo = ak;
+    return usable;
+  }
+  return false;
+}
+
 // Variable fixing for the top-k simplex's knapsack (lo = 0, hi = rhs / k):
 // its root t* satisfies sum_i clamp(a_i - t*, 0, hi) = k hi, hence
 // a_(k) - hi <= t* < a_(k) (the k largest each give hi at t = a_(k) - hi;
@@ -473,31 +704,61 @@ constexpr int kCandSlots = (G <= 2) ? 8 : (G <= 4) ? 4 : (G <= 16) ? 2 : 1;
 // registers set the occupancy) rather than in C more registers.
 template <int G, int C, int L, class D, class R, bool LDS_FALLBACK>
 __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L], int m,
-                                             int nvalid, R kth, R hi, R rhs, D* lds_col,
-                                             D* lds_dummy) {
+                                             int nvalid, int k, R kth, R hi, R rhs, D* lds_col,
+                                             D* lds_dummy, bool lane_lists = false) {
   const R slack = (fabs(kth) + hi) * (R(16) * num<R>::eps());
   const R cut = kth - hi - slack;
   if constexpr (G > 1) {
     constexpr int CC = kCandSlots<G>;
-    int cn = 0;
-#pragma unroll
-    for (int c = 0; c < C; ++c) cn += (static_cast<R>(v[c]) > cut) ? 1 : 0;
     const int g = static_cast<int>(threadIdx.x) % G;
+    // lane_lists: each lane's own top-L list (sorted, before the group
+    // merge) sits at lds_col[g L, g L + L).  A lane whose L-th largest is at
+    // or below the cut holds all its candidates there, as a prefix of the
+    // list: they are counted and compacted from L words instead of C slots.
+    D own[L];
+    int cn = 0;
+    bool from_lists = false;
+    if (lane_lists) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        own[i] = lds_col[g * L + i];
+        cn += (static_cast<R>(own[i]) > cut) ? 1 : 0;
+      }
+      from_lists = group_min<G>(static_cast<R>(own[L - 1]) > cut ? 0 : 1) == 1;
+    }
+    if (!from_lists) {
+      cn = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) cn += (static_cast<R>(v[c]) > cut) ? 1 : 0;
+    }
     const int total = group_sum<G>(cn);
     if (total <= G * CC) {
       // Branch-free compaction: every slot is stored, non-candidates to the
       // lane's own dummy word (distinct per lane, so no bank serialisation).
       // (For a workgroup-wide group the scan's barriers also order these
-      // stores after the other waves' reads of an earlier compaction.)
+      // stores after the other waves' reads of an earlier compaction.)  The
+      // lists were read above, before these stores overwrite them.
       int pos = group_exclusive_scan<G>(cn, g);
+      if (from_lists) {
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const bool pr = static_cast<R>(v[c]) > cut;
-        D* dst = pr ? lds_col + pos : lds_dummy;
-        *dst = v[c];
-        pos += pr ? 1 : 0;
+        for (int i = 0; i < L; ++i) {
+          D* dst = (i < cn) ? lds_col + pos + i : lds_dummy;
+          *dst = own[i];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const bool pr = static_cast<R>(v[c]) > cut;
+          D* dst = pr ? lds_col + pos : lds_dummy;
+          *dst = v[c];
+          pos += pr ? 1 : 0;
+        }
       }
       group_lds_sync<G>();
+      if constexpr (G == 4) {
+        KnapState<R> st;
+        if (topk_sorted_root<G, CC, L, D, R>(lds_col, total, top, k, hi, rhs, st)) return st;
+      }
       // Candidate i sits at lds_col[i]; lane g takes i = g, g + G, ...  The
       // reads stay inside the tile: G * CC <= 16 <= m for G = 4 and 2, and
       // G * CC <= G <= m for larger G.
@@ -557,8 +818,16 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
 #pragma unroll
     for (int c = L; c < C; ++c) top_insert(top, v[c]);
   } else {
+    top_fill<0>(top, v, net_inf(D(0)));  // -inf padding leaves it unchanged
+  }
+  // Groups of four lanes keep each lane's own list in the column's LDS words
+  // (free once the slots are in registers) for the candidate compaction of
+  // the knapsack below.
+  const bool lane_lists = G == 4 && m >= G * L;
+  if (lane_lists) {
+    const int g = static_cast<int>(threadIdx.x) % G;
 #pragma unroll
-    for (int c = 0; c < C; ++c) top_insert(top, v[c]);  // -inf padding leaves it unchanged
+    for (int i = 0; i < L; ++i) lds_col[g * L + i] = top[i];
   }
   top_merge<G>(top);
   R sum_k = 0, kth = static_cast<R>(top[0]), next = -num<R>::inf();
@@ -592,8 +861,9 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   const R hi = rhs / K;
   // More than G * kCandSlots candidates is rare for the prox inputs: the LDS
   // working copy keeps the kernel's register peak at the candidate path's.
-  KnapState<R> st = topk_knapsack<G, C, L, D, R, LDS_FALLBACK>(v, top, m, nvalid, kth, hi, rhs,
-                                                                lds_col, lds_dummy);
+  KnapState<R> st = topk_knapsack<G, C, L, D, R, LDS_FALLBACK>(v, top, m, nvalid, k, kth, hi,
+                                                                rhs, lds_col, lds_dummy,
+                                                                lane_lists);
   if (!constant) {
     // is_topk_simplex_lt (topk_simplex.h:9-27), is_topk_simplex_biased_lt
     // (topk_simplex_biased.h:9-28), over U = [first, t.first)
@@ -1295,30 +1565,23 @@ __device__ inline R* w_lds(unsigned char* smem, int B, int m, int slack) {
 }
 
 // ---------------------------------------------------------------------------
-// The batched kernel.  Block = BT threads (one wave) = BT / G columns of G
-// lanes each.  FULL: m == G * C, so every slot of an active lane is valid.
+// One tile of the batched kernel, once its B*m words are in LDS: the
+// threshold search per column and the map, written back to the tile in
+// place.  Block = BT threads (one wave) = BT / G columns of G lanes each.
+// FULL: m == G * C, so every slot of an active lane is valid.
 // ---------------------------------------------------------------------------
 template <int FAM, int KM, class D, class R, int G, int C, int BT, bool FULL>
-__global__ void __launch_bounds__(BT)
-prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
-                    int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
-                    sdca_thresholds* __restrict__ thr, int* __restrict__ slow) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
+__device__ __forceinline__ void columns_tile(unsigned char* smem_raw, int m, int64_t col0,
+                                             int ncols, const ProxParamsT<R>& pp,
+                                             const int64_t* __restrict__ col_p,
+                                             sdca_thresholds* __restrict__ thr,
+                                             int* __restrict__ slow) {
   D* tile = reinterpret_cast<D*>(smem_raw);
   constexpr int B = BT / G;
-  // Most 16-byte transfers per thread: B m sizeof(D) / (16 BT) <= C sizeof(D) / 16.
-  constexpr int NV = (C * static_cast<int>(sizeof(D)) + 15) / 16;
-  const int m = FULL ? G * C : static_cast<int>(m64);
-  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * B;
-  const int ncols = static_cast<int>(min(static_cast<int64_t>(B), n - col0));
-  const int64_t count = static_cast<int64_t>(ncols) * m;
   const int lc = static_cast<int>(threadIdx.x) / G;
   const int g = static_cast<int>(threadIdx.x) % G;
   const bool active = lc < ncols;
   const int64_t j = col0 + lc;
-
-  tile_load<NV, BT>(tile, in + col0 * m, count);
-  __syncthreads();
   const int nvalid = active ? (FULL ? C : (m - g + G - 1) / G) : 0;
   // Slot c of this lane is tile word lc * m + g + G c: a per-lane base and a
   // compile-time offset, so every slot access is one LDS instruction.
@@ -1478,6 +1741,27 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
       }
     }
   }
+}
+
+// The batched kernel: a workgroup takes one tile (B columns): load, search,
+// map, store.
+template <int FAM, int KM, class D, class R, int G, int C, int BT, bool FULL>
+__global__ void __launch_bounds__(BT)
+prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
+                    int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
+                    sdca_thresholds* __restrict__ thr, int* __restrict__ slow) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  D* tile = reinterpret_cast<D*>(smem_raw);
+  constexpr int B = BT / G;
+  // Most 16-byte transfers per thread: B m sizeof(D) / (16 BT) <= C sizeof(D) / 16.
+  constexpr int NV = (C * static_cast<int>(sizeof(D)) + 15) / 16;
+  const int m = FULL ? G * C : static_cast<int>(m64);
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * B;
+  const int ncols = static_cast<int>(min(static_cast<int64_t>(B), n - col0));
+  const int64_t count = static_cast<int64_t>(ncols) * m;
+  tile_load<NV, BT>(tile, in + col0 * m, count);
+  __syncthreads();
+  columns_tile<FAM, KM, D, R, G, C, BT, FULL>(smem_raw, m, col0, ncols, pp, col_p, thr, slow);
   __syncthreads();
   tile_store<NV, BT>(out + col0 * m, tile, count);
 }
