@@ -22,6 +22,7 @@ hipError_t launch_one(const ProxLaunch& a) {
             a.op == OP_KNAPSACK_LE_BIASED)
                ? static_cast<R>(a.rho) : R(0);
   pp.k = static_cast<int>(a.k);
+  pp.rhs_k = (a.k > 0) ? pp.rhs / static_cast<R>(a.k) : R(0);
   pp.op = a.op;
   pp.p = static_cast<int>(a.p);
   const int64_t blocks = (a.n + B - 1) / B;

@@ -34,6 +34,7 @@ enum Family { FAM_KNAP = 0, FAM_TOPK = 1, FAM_ENT = 2, FAM_TOPKENT = 3, FAM_TWO 
 template <class R>
 struct ProxParamsT {
   R lo, hi, rhs;
+  R rhs_k;  // rhs / k in R, formed once on the host (the top-k simplex's upper bound)
   R rho;  // biased operators only (0 for the others)
   int k;
   int op;
@@ -858,7 +859,7 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   const R rhs = pp.rhs;
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   if (constant && !(K * hi_c > rhs + eps)) return make_thr<R>(t_c, R(0), hi_c);
-  const R hi = rhs / K;
+  const R hi = pp.rhs_k;  // rhs / K (topk_simplex.h:56)
   // More than G * kCandSlots candidates is rare for the prox inputs: the LDS
   // working copy keeps the kernel's register peak at the candidate path's.
   KnapState<R> st = topk_knapsack<G, C, L, D, R, LDS_FALLBACK>(v, top, m, nvalid, k, kth, hi,
@@ -1520,15 +1521,28 @@ __device__ inline void tile_load(D* __restrict__ dst, const D* __restrict__ src,
   const int last = static_cast<int>(bytes / 16) - 1;
   const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
   u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+  const int tid = static_cast<int>(threadIdx.x);
   u32x4 r[NV];
+  if (last >= (NV - 1) * BT - 1) {
+    // Every load but the last in range for every lane (whole tiles): one
+    // base address with constant offsets, the clamp on the last load only.
+#pragma unroll
+    for (int i = 0; i < NV - 1; ++i) r[i] = __builtin_nontemporal_load(s4 + i * BT + tid);
+    const int idx = min((NV - 1) * BT + tid, last);
+    r[NV - 1] = __builtin_nontemporal_load(s4 + idx);
+#pragma unroll
+    for (int i = 0; i < NV - 1; ++i) d4[i * BT + tid] = r[i];
+    d4[idx] = r[NV - 1];
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = min(i * BT + static_cast<int>(threadIdx.x), last);
+    const int idx = min(i * BT + tid, last);
     r[i] = __builtin_nontemporal_load(s4 + idx);
   }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = min(i * BT + static_cast<int>(threadIdx.x), last);
+    const int idx = min(i * BT + tid, last);
     d4[idx] = r[i];
   }
 }
@@ -1545,9 +1559,18 @@ __device__ inline void tile_store(D* __restrict__ dst, const D* __restrict__ src
   const int last = static_cast<int>(bytes / 16) - 1;
   const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
   u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+  const int tid = static_cast<int>(threadIdx.x);
+  if (last >= (NV - 1) * BT - 1) {
+#pragma unroll
+    for (int i = 0; i < NV - 1; ++i)
+      __builtin_nontemporal_store(s4[i * BT + tid], d4 + i * BT + tid);
+    const int idx = min((NV - 1) * BT + tid, last);
+    __builtin_nontemporal_store(s4[idx], d4 + idx);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = min(i * BT + static_cast<int>(threadIdx.x), last);
+    const int idx = min(i * BT + tid, last);
     __builtin_nontemporal_store(s4[idx], d4 + idx);
   }
 }

@@ -446,6 +446,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
           pp.rhs = c;
           pp.rho = rho;
           pp.k = ob.k;
+          pp.rhs_k = (ob.k > 0) ? c / static_cast<R>(ob.k) : R(0);
           pp.op = op;
           pp.p = 0;
           const ColThr<R> th = simplex
