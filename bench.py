@@ -381,7 +381,10 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None,
     # The fused form of the same pass (scores and epilogue in one kernel,
     # scores not stored; SDCA_EVAL_FUSED), timed the same way after the
     # measured steps where it applies: the default two-kernel form is the
-    # faster on MI355X, and the records must be bit-identical.
+    # faster on MI355X.  Its records must equal the two-kernel form's to the
+    # rounding of the scores (bit for bit below 2^32 multiply-adds, where
+    # both take the scores from the same MFMA sequence; above, the
+    # two-kernel form's come from hipBLASLt).
     fused_ms = None
     if not kernel and not cfg.get("multilabel") and cfg["dtype"] == "f32":
         step(fused=True)
@@ -391,8 +394,12 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None,
             recs_f, _, _ = step(fused=True)
         torch.cuda.synchronize()
         fused_ms = (time.perf_counter() - t1) * 1e3 / steps
-        if recs_f != recs:
-            raise RuntimeError("fused and two-kernel evaluation records differ")
+        for a, b in zip(recs_f, recs):
+            for key in a:
+                x, y = float(a[key]), float(b[key])
+                if abs(x - y) > 1e-5 * max(1.0, abs(y)):
+                    raise RuntimeError(f"fused and two-kernel evaluation records differ: {key} "
+                                       f"{x!r} against {y!r}")
     # The dominant kernel is the score GEMM: time it on its own, event-timed
     # on the stream it runs on.
     S = torch.empty((cfg["n"], cfg["m"]), dtype=X.dtype, device=dev)

@@ -60,8 +60,10 @@ size_t dtype_size(int dt) { return dt == SDCA_F32 ? 4 : 8; }
 // graph capture cannot grow it (the wait and the allocation are not
 // capturable): warm the stream up with one call of the same size first.
 struct Workspace {
-  void* ptr[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
-  size_t cap[5] = {0, 0, 0, 0, 0};
+  // Slots: 0 deferred-column list, 1 scores, 2 evaluation scratch,
+  // 3 transposes, 4 epoch, 5 the library GEMM's workspace.
+  void* ptr[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  size_t cap[6] = {0, 0, 0, 0, 0, 0};
   // Pinned host block for the evaluation's results: copies into it are
   // asynchronous, so the call waits once for all of them.
   void* host = nullptr;
@@ -101,6 +103,36 @@ int workspace(hipStream_t stream, int slot, size_t bytes, void** out, Workspace*
     w.cap[slot] = want;
   }
   *out = w.ptr[slot];
+  return SDCA_OK;
+}
+
+// The library GEMM's workspace (slot 5) for an fp32 score GEMM of n m d:
+// none below the library's threshold, and under graph capture only one the
+// stream already has (the GEMM then takes an algorithm within it, or the
+// MFMA kernel).
+int gemm_workspace(hipStream_t stream, int64_t n, int64_t m, int64_t d, void** ws,
+                   size_t* bytes) {
+  using sdca_gpu::blas_shape;
+  using sdca_gpu::kBlasWorkspaceBytes;
+  *ws = nullptr;
+  *bytes = 0;
+  if (!blas_shape(n, m, d)) return SDCA_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  SDCA_HIP_TRY(hipStreamIsCapturing(stream, &cs), "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone) {
+    int dev = 0;
+    SDCA_HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    Workspace& w = g_ws[std::make_tuple(dev, stream, std::this_thread::get_id())];
+    if (w.cap[5] >= kBlasWorkspaceBytes) {
+      *ws = w.ptr[5];
+      *bytes = kBlasWorkspaceBytes;
+    }
+    return SDCA_OK;
+  }
+  const int rc = workspace(stream, 5, kBlasWorkspaceBytes, ws);
+  if (rc) return rc;
+  *bytes = kBlasWorkspaceBytes;
   return SDCA_OK;
 }
 
@@ -673,10 +705,14 @@ int sdca_scores(sdca_dtype data, int64_t d, int64_t m, int64_t n, const void* X,
     pW = dw.ptr;
     pS = ds.ptr;
   }
-  if (data == SDCA_F32)
+  if (data == SDCA_F32) {
+    void* gws = nullptr;
+    size_t gws_bytes = 0;
+    if ((rc = gemm_workspace(stream, n, m, d, &gws, &gws_bytes))) return rc;
     SDCA_HIP_TRY(launch_scores_gemm(static_cast<const float*>(pX), static_cast<const float*>(pW),
-                                    static_cast<float*>(pS), n, m, d, stream), "scores kernel");
-  else
+                                    static_cast<float*>(pS), n, m, d, stream, gws, gws_bytes),
+                 "scores kernel");
+  } else
     SDCA_HIP_TRY(launch_scores_gemm_f64(static_cast<const double*>(pX), static_cast<const double*>(pW),
                                         static_cast<double*>(pS), n, m, d, stream), "scores kernel");
   if (flags & SDCA_HOST_PTR) {
@@ -722,10 +758,14 @@ int sdca_recompute_primal(sdca_dtype data, int64_t d, int64_t m, int64_t n, cons
   void* Xt = static_cast<char*>(ws) + es * static_cast<size_t>(n) * static_cast<size_t>(m);
   SDCA_HIP_TRY(launch_transpose(data, pA, At, n, m, stream), "transpose kernel");
   SDCA_HIP_TRY(launch_transpose(data, pX, Xt, n, d, stream), "transpose kernel");
-  if (data == SDCA_F32)
+  if (data == SDCA_F32) {
+    void* gws = nullptr;
+    size_t gws_bytes = 0;
+    if ((rc = gemm_workspace(stream, m, d, n, &gws, &gws_bytes))) return rc;
     SDCA_HIP_TRY(launch_scores_gemm(static_cast<const float*>(At), static_cast<const float*>(Xt),
-                                    static_cast<float*>(pW), m, d, n, stream), "GEMM kernel");
-  else
+                                    static_cast<float*>(pW), m, d, n, stream, gws, gws_bytes),
+                 "GEMM kernel");
+  } else
     SDCA_HIP_TRY(launch_scores_gemm_f64(static_cast<const double*>(At),
                                         static_cast<const double*>(Xt), static_cast<double*>(pW),
                                         m, d, n, stream), "GEMM kernel");
@@ -824,10 +864,14 @@ static int eval_common(const sdca_objective* objs, int n_obj, sdca_dtype data, s
     // scores = W' X into the stream's workspace
     void* sbuf = nullptr;
     if ((rc = workspace(stream, 1, es * static_cast<size_t>(m) * static_cast<size_t>(n), &sbuf))) return rc;
-    if (data == SDCA_F32)
+    if (data == SDCA_F32) {
+      void* gws = nullptr;
+      size_t gws_bytes = 0;
+      if ((rc = gemm_workspace(stream, n, m, d, &gws, &gws_bytes))) return rc;
       SDCA_HIP_TRY(launch_scores_gemm(static_cast<const float*>(pX), static_cast<const float*>(pW),
-                                      static_cast<float*>(sbuf), n, m, d, stream), "scores kernel");
-    else
+                                      static_cast<float*>(sbuf), n, m, d, stream, gws, gws_bytes),
+                   "scores kernel");
+    } else
       SDCA_HIP_TRY(launch_scores_gemm_f64(static_cast<const double*>(pX),
                                           static_cast<const double*>(pW), static_cast<double*>(sbuf),
                                           n, m, d, stream), "scores kernel");

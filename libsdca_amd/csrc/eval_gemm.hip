@@ -16,7 +16,8 @@
 // K order (every fp32 score GEMM here, fused or not): k runs in groups of 8;
 // MFMA step t (0..3) of group g sums k = 8g + t (lanes 0-31) and
 // k = 8g + 4 + t (lanes 32-63), groups in increasing order, so every score
-// is the same float whichever kernel forms it.
+// is the same float whichever of these kernels forms it.  (From 2^32
+// multiply-adds on, the unfused product goes to hipBLASLt: eval_blas.cpp.)
 // Fast form (d % 16 == 0, 16-byte aligned operands; scores_gemm_fast_kernel):
 // K advances in slabs of 16 held in LDS as [row][k] (rows padded to 20
 // floats), so a lane's operands for four MFMA steps are one conflict-free
@@ -635,14 +636,25 @@ hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, i
   return hipGetLastError();
 }
 
-hipError_t launch_scores_gemm(const float* X, const float* W, float* S, int64_t n, int64_t m,
-                              int64_t d, hipStream_t stream) {
+hipError_t launch_scores_gemm_mfma(const float* X, const float* W, float* S, int64_t n,
+                                   int64_t m, int64_t d, hipStream_t stream) {
   // Class tiles of 128 (2 x 2 waves of 64 x 64) or 224 (4 x 1 waves of
   // 32 x 224), whichever pads m less: m = 200 fills 89 % of one 224-wide
   // tile against 78 % of two 128-wide ones.
   const int64_t pad128 = (m + 127) / 128 * 128, pad224 = (m + 223) / 224 * 224;
   if (pad224 < pad128) return launch_tiles<128, 224, 4, 1>(X, W, S, n, m, d, stream);
   return launch_tiles<128, 128, 2, 2>(X, W, S, n, m, d, stream);
+}
+
+// Large products go to hipBLASLt (92.9 % of the fp32 MFMA peak at the C4
+// shape against this file's 78-84 %); below kBlasMinMacs, and wherever the
+// library declines, the MFMA kernel keeps the fused pass's k order, so the
+// two-kernel pass gives the fused pass's bits there.
+hipError_t launch_scores_gemm(const float* X, const float* W, float* S, int64_t n, int64_t m,
+                              int64_t d, hipStream_t stream, void* blas_ws, size_t blas_ws_bytes) {
+  if (blas_shape(n, m, d) && blas_scores_gemm(X, W, S, n, m, d, stream, blas_ws, blas_ws_bytes))
+    return hipSuccess;
+  return launch_scores_gemm_mfma(X, W, S, n, m, d, stream);
 }
 
 }  // namespace sdca_gpu

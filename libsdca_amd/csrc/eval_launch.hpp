@@ -43,8 +43,25 @@ struct EvalLaunch {
 };
 
 // S = X W^T for fp32 on the matrix cores; X: n x d, W: m x d, S: n x m (row-major).
+// From kBlasMinMacs multiply-adds (n m d) on, through hipBLASLt when it has
+// an algorithm for the shape within the caller's workspace (blas_ws, at
+// most kBlasWorkspaceBytes; none: only algorithms without one), else the
+// hand-written MFMA kernel.
+constexpr int64_t kBlasMinMacs = int64_t(1) << 32;
+constexpr size_t kBlasWorkspaceBytes = size_t(32) << 20;
+inline bool blas_shape(int64_t n, int64_t m, int64_t d) {
+  return n > 0 && m > 0 && d > 0 && n * m >= kBlasMinMacs / d;
+}
 hipError_t launch_scores_gemm(const float* X, const float* W, float* S, int64_t n, int64_t m,
-                              int64_t d, hipStream_t stream);
+                              int64_t d, hipStream_t stream, void* blas_ws = nullptr,
+                              size_t blas_ws_bytes = 0);
+// The hand-written MFMA kernel alone (the fused pass's k order).
+hipError_t launch_scores_gemm_mfma(const float* X, const float* W, float* S, int64_t n,
+                                   int64_t m, int64_t d, hipStream_t stream);
+// The same product through hipBLASLt; false (S untouched or to be
+// overwritten) when the library declines the shape or fails.
+bool blas_scores_gemm(const float* X, const float* W, float* S, int64_t n, int64_t m, int64_t d,
+                      hipStream_t stream, void* ws, size_t ws_bytes);
 // The same contraction in double on the matrix cores (v_mfma_f64_16x16x4f64).
 hipError_t launch_scores_gemm_f64(const double* X, const double* W, double* S, int64_t n,
                                   int64_t m, int64_t d, hipStream_t stream);

@@ -55,7 +55,9 @@ def multilabel_labels(rng, n, m, pmax=5):
 
 
 @pytest.mark.parametrize("n,m,d", [(3000, 300, 1000), (517, 1000, 4096), (1000, 200, 1024),
-                                   (64, 5, 37), (130, 129, 16)])
+                                   (64, 5, 37), (130, 129, 16),
+                                   # from 2^32 multiply-adds on: the hipBLASLt path
+                                   (2000, 1000, 2200), (4099, 257, 4097)])
 def test_scores_gemm(cuda, n, m, d):
     import torch
     import libsdca_amd as sd
@@ -472,6 +474,33 @@ def test_fused_matches_unfused(cuda, m, objs, result):
         assert np.array_equal(a_f, a_u), f"m={m} test={test}: accuracy differs"
         for a, b in zip(r_f, r_u):
             assert a == b, f"m={m} test={test}: records differ"
+
+
+@pytest.mark.parametrize("result", ["float", "double"])
+def test_fused_against_library_scores(cuda, result):
+    """Above 2^32 multiply-adds the two-kernel pass takes its scores from
+    hipBLASLt, whose k order is not the fused kernel's: the per-example
+    losses then agree to the rounding of the scores (float scores of
+    d = 1100 unit-norm features: relative 1e-5 of max(1, |loss|)), and the
+    top-k accuracies to the rare example whose k-th and (k+1)-th scores
+    tie at that rounding."""
+    import torch
+    import libsdca_amd as sd
+    rng = np.random.default_rng(7)
+    n, m, d = 4000, 1000, 1100
+    X = rng.standard_normal((n, d)).astype(np.float32)
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    W = (rng.standard_normal((m, d)) * 0.5).astype(np.float32)
+    y = rng.integers(0, m, n)
+    objs = [("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)]
+    tX, tW = torch.from_numpy(X).to(cuda), torch.from_numpy(W).to(cuda)
+    r_f, a_f, p_f = sd.eval_features(objs, tX, tW, y, result=result, per_example=True, fused=True)
+    r_u, a_u, p_u = sd.eval_features(objs, tX, tW, y, result=result, per_example=True)
+    torch.cuda.synchronize()
+    pf, pu = p_f.cpu().numpy(), p_u.cpu().numpy()
+    err = np.abs(pf - pu) / np.maximum(1.0, np.abs(pu))
+    assert err.max() <= 1e-5, f"per-example losses differ by {err.max():.3e}"
+    assert np.abs(np.asarray(a_f) - np.asarray(a_u)).max() <= 2.0 / n, "accuracies differ"
 
 
 @pytest.mark.parametrize("dtype,result", [(np.float32, F32), (np.float32, F64), (np.float64, F64)])
