@@ -382,9 +382,9 @@ def bench_eval(cfg, args, torch, sd, steps=None, warmup=None, config_name=None,
     # scores not stored; SDCA_EVAL_FUSED), timed the same way after the
     # measured steps where it applies: the default two-kernel form is the
     # faster on MI355X.  Its records must equal the two-kernel form's to the
-    # rounding of the scores (bit for bit below 2^32 multiply-adds, where
-    # both take the scores from the same MFMA sequence; above, the
-    # two-kernel form's come from hipBLASLt).
+    # rounding of the scores (bit for bit below 2^32 multiply-adds or 512
+    # classes, where both take the scores from the same MFMA sequence;
+    # above, the two-kernel form's come from hipBLASLt).
     fused_ms = None
     if not kernel and not cfg.get("multilabel") and cfg["dtype"] == "f32":
         step(fused=True)

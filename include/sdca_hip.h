@@ -223,9 +223,10 @@ int sdca_eval_scores(const sdca_objective* objs, int n_obj,
  * matrix cores and evaluates the examples from LDS without storing the
  * scores, instead of the default two-kernel form (scores written to a
  * device buffer by the GEMM, then the per-example kernel).  Below 2^32
- * multiply-adds (n m d) both forms give bit-identical records; from there
- * on the two-kernel form takes its scores from hipBLASLt, whose summation
- * order differs, and the records agree to the rounding of the scores.
+ * multiply-adds (n m d) or 512 classes both forms give bit-identical
+ * records; from there on the two-kernel form takes its scores from
+ * hipBLASLt, whose summation order differs, and the records agree to the
+ * rounding of the scores.
  * The default is the two-kernel form: on MI355X it
  * is the faster (the fused kernel holds 32 examples x all classes per
  * workgroup, is limited to 2 waves per SIMD by its registers and re-reads W

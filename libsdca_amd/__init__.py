@@ -531,8 +531,8 @@ def eval_features(objs, X, W, labels, A=None, W0=None, offsets=None, result=None
     test=True gives a test set's records (eval_test: primal loss and
     accuracy / rank loss only).  fused=True runs the one-kernel form where it
     applies (SDCA_EVAL_FUSED; slower on MI355X; bit-identical results below
-    2^32 multiply-adds n m d, equal to score rounding above, where the
-    two-kernel form's scores come from hipBLASLt)."""
+    2^32 multiply-adds n m d or 512 classes, equal to score rounding above,
+    where the two-kernel form's scores come from hipBLASLt)."""
     n, d = int(X.shape[0]), int(X.shape[1])
     m = int(W.shape[0])
     _need(X, "X", (n, d), X)

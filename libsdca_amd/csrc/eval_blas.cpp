@@ -101,12 +101,14 @@ bool lookup(int dev, int64_t n, int64_t m, int64_t d, size_t ws_max, const Descs
   hipblasLtMatmulPreference_t pref = nullptr;
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
   const uint64_t max_bytes = ws_max;
-  hipblasLtMatmulHeuristicResult_t res[1];
+  // The first of the heuristic's ranked list (asked for several: asked
+  // for one, it ranked differently at the C5 shape).
+  hipblasLtMatmulHeuristicResult_t res[8];
   int count = 0;
   if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                             &max_bytes, sizeof(max_bytes)) ==
           HIPBLAS_STATUS_SUCCESS &&
-      hipblasLtMatmulAlgoGetHeuristic(*h, ds.desc, ds.la, ds.lb, ds.lc, ds.lc, pref, 1, res,
+      hipblasLtMatmulAlgoGetHeuristic(*h, ds.desc, ds.la, ds.lb, ds.lc, ds.lc, pref, 8, res,
                                       &count) == HIPBLAS_STATUS_SUCCESS &&
       count > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= ws_max) {
     s.algo = res[0].algo;

@@ -1054,7 +1054,7 @@ eval_slow_kernel(const D* __restrict__ S, const int64_t* __restrict__ labels, in
 // in the same pairs and operand lanes as the unfused score GEMMs (step t of
 // each group of 8 sums k = 8g + t and 8g + 4 + t), so every score is
 // bit-identical to the unfused path's wherever that path uses the MFMA
-// score kernel (below 2^32 multiply-adds).  Then, for each half
+// score kernel (below 2^32 multiply-adds or 512 classes).  Then, for each half
 // of the 32 examples, the accumulators are written to the LDS the slabs used
 // (16 x m scores) and each wave runs the per-example epilogue
 // (eval_example_mc) on four of them with one example per wave (G = 64),

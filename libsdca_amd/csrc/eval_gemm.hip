@@ -17,7 +17,8 @@
 // MFMA step t (0..3) of group g sums k = 8g + t (lanes 0-31) and
 // k = 8g + 4 + t (lanes 32-63), groups in increasing order, so every score
 // is the same float whichever of these kernels forms it.  (From 2^32
-// multiply-adds on, the unfused product goes to hipBLASLt: eval_blas.cpp.)
+// multiply-adds and 512 classes on, the unfused product goes to hipBLASLt:
+// eval_blas.cpp.)
 // Fast form (d % 16 == 0, 16-byte aligned operands; scores_gemm_fast_kernel):
 // K advances in slabs of 16 held in LDS as [row][k] (rows padded to 20
 // floats), so a lane's operands for four MFMA steps are one conflict-free

@@ -56,8 +56,9 @@ def multilabel_labels(rng, n, m, pmax=5):
 
 @pytest.mark.parametrize("n,m,d", [(3000, 300, 1000), (517, 1000, 4096), (1000, 200, 1024),
                                    (64, 5, 37), (130, 129, 16),
-                                   # from 2^32 multiply-adds on: the hipBLASLt path
-                                   (2000, 1000, 2200), (4099, 257, 4097)])
+                                   # from 2^32 multiply-adds and 512 classes on: the
+                                   # hipBLASLt path
+                                   (2000, 1000, 2200), (4099, 600, 1800)])
 def test_scores_gemm(cuda, n, m, d):
     import torch
     import libsdca_amd as sd
@@ -478,12 +479,12 @@ def test_fused_matches_unfused(cuda, m, objs, result):
 
 @pytest.mark.parametrize("result", ["float", "double"])
 def test_fused_against_library_scores(cuda, result):
-    """Above 2^32 multiply-adds the two-kernel pass takes its scores from
-    hipBLASLt, whose k order is not the fused kernel's: the per-example
-    losses then agree to the rounding of the scores (float scores of
-    d = 1100 unit-norm features: relative 1e-5 of max(1, |loss|)), and the
-    top-k accuracies to the rare example whose k-th and (k+1)-th scores
-    tie at that rounding."""
+    """From 2^32 multiply-adds and 512 classes on the two-kernel pass takes
+    its scores from hipBLASLt, whose k order is not the fused kernel's: the
+    per-example losses then agree to the rounding of the scores (float
+    scores of d = 1100 unit-norm features: relative 1e-5 of max(1, |loss|)),
+    and the top-k accuracies to the rare example whose k-th and (k+1)-th
+    scores tie at that rounding."""
     import torch
     import libsdca_amd as sd
     rng = np.random.default_rng(7)
