@@ -289,6 +289,27 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
                         int64_t count, const void* norms, unsigned flags, void* stream);
 
 /*
+ * One epoch of the SDCA solver on kernel input (replaces one pass of the
+ * example loop of solver::solve, solver.h:44-47, with the kernel form of
+ * update_variables, update.h:88-107): per example i in `order`, norm2 =
+ * K_ii (no update when it is <= 0), scores A k_i over the current dual
+ * variables of all examples (eval_scores, solver/eval/scores.h:28-45), and the
+ * objective's dual update of a_i.  Every update reaches the later
+ * examples' scores (there is no primal matrix and no epsilon test).  The
+ * examples run in blocks whose scores come from the matrix cores and whose
+ * Gram matrix is read from K; results equal the sequential loop's up to
+ * the rounding of the scores' sums.
+ *   K: the n x n training kernel matrix (symmetric; column i = k_i);
+ *   A: m x n dual variables, column-major, updated in place;
+ *   labels, offsets, order, count, flags, stream, (data, result) and the
+ *   limits on m and the SDCA_ERR_LABELS return: as sdca_epoch_features.
+ */
+int sdca_epoch_kernel(const sdca_objective* obj, sdca_dtype data, sdca_dtype result,
+                      int64_t m, int64_t n, const void* K, void* A,
+                      const int64_t* labels, const int64_t* offsets, const int64_t* order,
+                      int64_t count, unsigned flags, void* stream);
+
+/*
  * The reference solver's example order for epoch `epoch` (0-based) of a
  * solve over n examples (solver.h:59, 75-79, 96-100: a default-seeded
  * std::minstd_rand, std::shuffle of 0..n-1 once per epoch): n indices into

@@ -542,6 +542,30 @@ inline void update_epoch(Context& ctx, sdca::solver_scratch<Data, sdca::feature_
                                     SDCA_HOST_PTR, nullptr));
 }
 
+// The same epoch for a kernel input: update_variables' kernel form
+// (solver/update.h:88-107) for each example index in [first, last);
+// ctx.dual_variables is updated in place.
+template <typename Data, typename Context, typename Iterator>
+inline void update_epoch(Context& ctx, sdca::solver_scratch<Data, sdca::kernel_input>&,
+                         Iterator first, Iterator last) {
+  typedef typename Context::result_type Result;
+  const auto& d = ctx.train;
+  const std::int64_t m = static_cast<std::int64_t>(d.num_classes());
+  const std::int64_t n = static_cast<std::int64_t>(d.num_examples());
+  typedef typename Context::output_type Output;
+  std::vector<std::int64_t> labels, offsets;
+  detail::labels_of(d.out, labels, offsets,
+                    std::integral_constant<bool, std::is_same<Output, sdca::multilabel_output>::value>());
+  std::vector<std::int64_t> order;
+  for (Iterator it = first; it != last; ++it) order.push_back(static_cast<std::int64_t>(*it));
+  const sdca_objective ob = detail::objective_of<typename Context::objective_type>::get(ctx.objective);
+  detail::check(sdca_epoch_kernel(&ob, detail::dtype<Data>::value, detail::dtype<Result>::value, m,
+                                  n, d.in.kernel, ctx.dual_variables, labels.data(),
+                                  offsets.empty() ? nullptr : offsets.data(), order.data(),
+                                  static_cast<std::int64_t>(order.size()), SDCA_HOST_PTR,
+                                  nullptr));
+}
+
 // W = W0 + X A' (eval_recompute_primal, eval/core.h:148-182): X is d x n,
 // A m x n, W0 (may be null) and W d x m, column-major.
 template <typename Data>

@@ -40,7 +40,7 @@ __all__ = [
     "prox_topk_simplex_biased", "prox_topk_cone_biased", "prox_topk_entropy_biased",
     "prox_two_simplex_sort", "prox_two_entropy", "lambert_w_exp", "OPS", "F32", "F64",
     "OBJECTIVES", "objective", "scores", "eval_features", "eval_kernel", "eval_scores",
-    "recompute_primal",
+    "recompute_primal", "epoch_order", "epoch_features", "epoch_kernel",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -449,6 +449,53 @@ def epoch_features(obj, X, W, A, labels, order=None, norms=None, result=None, of
     if rc != 0:
         raise SdcaError(rc, lib.sdca_last_error().decode())
     return W, A
+
+
+def epoch_kernel(obj, K, A, labels, order=None, result=None, offsets=None):
+    """One SDCA epoch on kernel input (the kernel form of update_variables,
+    update.h:88-107, for each example of `order`) for an objective (name, c,
+    gamma, k): K (n, n) the symmetric training kernel matrix, A (n, m)
+    updated in place and returned.  CUDA tensors run on torch's current
+    stream; numpy arrays (C-contiguous, K's dtype) go through the
+    host-staging path.  order, result and offsets: as epoch_features."""
+    lib = library()
+    n = int(K.shape[0])
+    m = int(A.shape[1])
+    objarr = _objs([obj])
+    lib.sdca_epoch_kernel.restype = ctypes.c_int
+    if _is_torch(K):
+        if not K.is_cuda:
+            raise SdcaError(2, "epoch_kernel takes CUDA tensors or numpy arrays")
+        import torch
+        _need(K, "K", (n, n), K)
+        _need(A, "A", (n, m), K)
+        od = None
+        if order is not None:
+            od = torch.as_tensor(order, dtype=torch.int64, device=K.device).contiguous().reshape(-1)
+        flags, stream = 0, _stream_ptr()
+        ptr = _ptr
+    else:
+        for name, a, shape in (("K", K, (n, n)), ("A", A, (n, m))):
+            if (not isinstance(a, np.ndarray) or a.dtype != K.dtype or tuple(a.shape) != shape
+                    or not a.flags.c_contiguous):
+                raise SdcaError(2, f"{name}: expected a C-contiguous {K.dtype} array {shape}")
+        od = None if order is None else np.ascontiguousarray(order, dtype=np.int64).reshape(-1)
+        flags, stream = HOST_PTR, None
+
+        def ptr(a):
+            return None if a is None else a.ctypes.data
+    data = _dtype_code(K)
+    res = data if result is None else ({"float": F32, "single": F32, "double": F64}.get(result, result))
+    lab, off = _label_arrays(labels, offsets, n, K)
+    count = n if od is None else int(od.shape[0])
+    rc = lib.sdca_epoch_kernel(objarr, ctypes.c_int(data), ctypes.c_int(res), ctypes.c_int64(m),
+                               ctypes.c_int64(n), ctypes.c_void_p(ptr(K)), ctypes.c_void_p(ptr(A)),
+                               ctypes.c_void_p(ptr(lab)), ctypes.c_void_p(ptr(off)),
+                               ctypes.c_void_p(ptr(od)), ctypes.c_int64(count),
+                               ctypes.c_uint(flags), stream)
+    if rc != 0:
+        raise SdcaError(rc, lib.sdca_last_error().decode())
+    return A
 
 
 def recompute_primal(X, A, W0=None, out=None):

@@ -935,12 +935,17 @@ int sdca_epoch_order(int64_t n, int64_t epoch, int64_t* order) {
   return SDCA_OK;
 }
 
-int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result, int64_t d,
-                        int64_t m, int64_t n, const void* X, void* W, void* A,
-                        const int64_t* labels, const int64_t* offsets, const int64_t* order,
-                        int64_t count, const void* norms, unsigned flags, void* stream_ptr) {
+}  // extern "C"
+
+namespace {
+
+// The epoch on feature input (X: n x d, W: m x d) or, with `kernel`, on
+// kernel input (X: the n x n kernel matrix, d = n, W and norms unused).
+int epoch_common(const sdca_objective* obj, sdca_dtype data, sdca_dtype result, int64_t d,
+                 int64_t m, int64_t n, const void* X, void* W, void* A, const int64_t* labels,
+                 const int64_t* offsets, const int64_t* order, int64_t count, const void* norms,
+                 unsigned flags, void* stream_ptr, bool kernel) {
   using namespace sdca_gpu;
-  g_last_error.clear();
   if (!obj) return fail(SDCA_ERR_ARG_NULL, "obj must not be NULL");
   if (obj->kind < SDCA_OBJ_HINGE_TOPK || obj->kind > SDCA_OBJ_MULTILABEL_ENTROPY)
     return fail(SDCA_ERR_NOT_IMPLEMENTED, "unknown objective kind %d",
@@ -964,7 +969,10 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
                 (long long)count, (long long)n);
   int rc = check_objectives(obj, 1, m, multilabel);
   if (rc) return rc;
-  if (!X || !W || !A || !labels) return fail(SDCA_ERR_ARG_NULL, "X, W, A and labels must not be NULL");
+  if (!X || (!W && !kernel) || !A || !labels)
+    return fail(SDCA_ERR_ARG_NULL,
+                kernel ? "K, A and labels must not be NULL" : "X, W, A and labels must not be NULL");
+  if (kernel) norms = nullptr;
   if (count == 0) return SDCA_OK;
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const bool host = (flags & SDCA_HOST_PTR) != 0;
@@ -980,7 +988,7 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   }
   if (host) {
     if ((rc = stage_in(X, es * d * n, dx, stream))) return rc;
-    if ((rc = stage_in(W, es * d * m, dw, stream))) return rc;
+    if (!kernel && (rc = stage_in(W, es * d * m, dw, stream))) return rc;
     if ((rc = stage_in(A, es * m * n, da, stream))) return rc;
     const int64_t nlab = multilabel ? offsets[n] : n;
     if ((rc = stage_in(labels, sizeof(int64_t) * nlab, dl, stream))) return rc;
@@ -989,7 +997,8 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
     if (norms && (rc = stage_in(norms, es * n, dnorm, stream))) return rc;
   }
   void* ws = nullptr;
-  if ((rc = workspace(stream, 4, epoch_workspace_bytes(data, d, m, n, norms != nullptr), &ws)))
+  if ((rc = workspace(stream, 4, epoch_workspace_bytes(data, d, m, n, norms != nullptr, kernel),
+                      &ws)))
     return rc;
   EpochLaunch a;
   a.data = data;
@@ -1002,20 +1011,22 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
   a.m = m;
   a.n = n;
   a.X = host ? dx.ptr : X;
-  a.W = host ? dw.ptr : W;
+  a.W = kernel ? nullptr : host ? dw.ptr : W;
   a.A = host ? da.ptr : A;
   a.labels = host ? static_cast<const int64_t*>(dl.ptr) : labels;
   a.offsets = !multilabel ? nullptr : host ? static_cast<const int64_t*>(doff.ptr) : offsets;
   a.order = host && order ? static_cast<const int64_t*>(dord.ptr) : order;
   a.count = count;
   a.norms = host && norms ? dnorm.ptr : norms;
+  a.kernel = kernel;
   a.ws = ws;
   a.stream = stream;
   int* flag = nullptr;
   SDCA_HIP_TRY(launch_epoch(a, &flag), "SDCA epoch kernels");
   if (host) {
-    SDCA_HIP_TRY(hipMemcpyAsync(W, dw.ptr, es * d * m, hipMemcpyDeviceToHost, stream),
-                 "hipMemcpyAsync(D2H)");
+    if (!kernel)
+      SDCA_HIP_TRY(hipMemcpyAsync(W, dw.ptr, es * d * m, hipMemcpyDeviceToHost, stream),
+                   "hipMemcpyAsync(D2H)");
     SDCA_HIP_TRY(hipMemcpyAsync(A, da.ptr, es * m * n, hipMemcpyDeviceToHost, stream),
                  "hipMemcpyAsync(D2H)");
   }
@@ -1028,6 +1039,28 @@ int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype r
                 "an example index outside [0, n), a label outside [0, m) (read as 0), or a "
                 "multilabel example whose labels are not 1..m-1 distinct sorted ones (skipped)");
   return SDCA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sdca_epoch_features(const sdca_objective* obj, sdca_dtype data, sdca_dtype result, int64_t d,
+                        int64_t m, int64_t n, const void* X, void* W, void* A,
+                        const int64_t* labels, const int64_t* offsets, const int64_t* order,
+                        int64_t count, const void* norms, unsigned flags, void* stream_ptr) {
+  g_last_error.clear();
+  return epoch_common(obj, data, result, d, m, n, X, W, A, labels, offsets, order, count, norms,
+                      flags, stream_ptr, false);
+}
+
+int sdca_epoch_kernel(const sdca_objective* obj, sdca_dtype data, sdca_dtype result, int64_t m,
+                      int64_t n, const void* K, void* A, const int64_t* labels,
+                      const int64_t* offsets, const int64_t* order, int64_t count,
+                      unsigned flags, void* stream_ptr) {
+  g_last_error.clear();
+  return epoch_common(obj, data, result, n, m, n, K, nullptr, A, labels, offsets, order, count,
+                      nullptr, flags, stream_ptr, true);
 }
 
 }  // extern "C"

@@ -28,13 +28,16 @@ struct EpochLaunch {
   const int64_t* order;   // count example indices, or NULL for 0..count-1
   int64_t count;
   const void* norms;      // n squared norms, or NULL (computed into the workspace)
+  bool kernel;            // kernel input: X is the n x n kernel matrix (d = n), W unused
   void* ws;               // epoch_workspace_bytes(...) bytes
   hipStream_t stream;
 };
 
-// Workspace bytes of one call (the block buffers, the norms when not given,
-// the index list and the bad-input flag).
-size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool norms_given);
+// Workspace bytes of one call (the block buffers, the norms when not given
+// or taken from K's diagonal, the transposed dual variables for kernel
+// input, the index list and the bad-input flag).
+size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool norms_given,
+                             bool kernel = false);
 // Enqueues the epoch; the bad-input flag (an example index or a label out of
 // range: such entries are read as 0) is left in *flag_dev for the caller.
 hipError_t launch_epoch(const EpochLaunch& a, int** flag_dev);

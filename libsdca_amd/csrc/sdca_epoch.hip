@@ -55,6 +55,10 @@ struct EpochObj {
   int kind;
   int k;
   double c, gamma;
+  // Kernel input: every update reaches the later examples' scores (the
+  // reference reads A itself, update.h:88-107), not only those above
+  // epsilon (the W update's test, update.h:78-84).
+  int kernel;
 };
 
 // The block's delta rows in LDS: for the row sizes where kEpochBlock rows of
@@ -90,6 +94,40 @@ norms_kernel(const D* __restrict__ X, int64_t n, int64_t d, D* __restrict__ norm
 __device__ inline int64_t block_row(const int64_t* order, int64_t q, int64_t n) {
   const int64_t i = order ? order[q] : q;
   return (i >= 0 && i < n) ? i : 0;
+}
+
+// Kernel input (update.h:88-107), the training set's n x n kernel matrix K
+// (row i = K_i, the reference's column i): norm2 = K_ii.
+template <class D>
+__global__ void __launch_bounds__(256)
+kernel_diag_kernel(const D* __restrict__ K, int64_t n, D* __restrict__ norms) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) norms[i] = K[i * n + i];
+}
+
+// Kernel input: the block's Gram matrix is K itself, Gm[e][f] = K[i_e][i_f]
+// (x_e . x_f of the feature form).
+template <class D>
+__global__ void __launch_bounds__(256)
+kernel_gram_kernel(const D* __restrict__ K, const int64_t* __restrict__ order, int64_t q0,
+                   int64_t n, int nb, D* __restrict__ Gm) {
+  const int o = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (o >= nb * nb) return;
+  const int e = o / nb, f = o % nb;
+  Gm[o] = K[block_row(order, q0 + e, n) * n + block_row(order, q0 + f, n)];
+}
+
+// Kernel input: the transposed copy At (m x n) that the score products read
+// as their W takes the block's updated dual variables, At[c][i] = A[i][c].
+template <class D>
+__global__ void __launch_bounds__(256)
+kernel_at_kernel(const D* __restrict__ A, D* __restrict__ At, const int64_t* __restrict__ order,
+                 int64_t q0, int64_t n, int nb, int64_t m) {
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (o >= static_cast<int64_t>(nb) * m) return;
+  const int64_t k = o / m, c = o % m;
+  const int64_t i = block_row(order, q0 + k, n);
+  At[c * n + i] = A[i * m + c];
 }
 
 // The thread's columns j = tid + G q for every q < PF (m <= G PF), with
@@ -520,7 +558,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
       part += ok ? fabs(dl) : D(0);
     });
     const D asum = group_sum<G>(part);  // also orders v's last reads before the next writes
-    if (asum > num<D>::eps()) {
+    if (asum > num<D>::eps() || ob.kernel) {
       changed |= 1u << k;  // the later examples' scores see this update
     } else {
       for_cols<PF>(tid, m, [&](int j, int q, bool ok) { *(ok ? drow + j : gd) = D(0); });
@@ -733,11 +771,16 @@ hipError_t launch_skinny(const EpochLaunch& a, int64_t q0, int nb, D* S, D* Gm, 
   constexpr int64_t vw = 16 / sizeof(D);
   const int vec = (a.d % vw == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
                   (reinterpret_cast<uintptr_t>(W) % 16 == 0);
-  const dim3 grid(static_cast<unsigned>(pl.tiles_w + 1), static_cast<unsigned>(pl.ksplit));
+  // Kernel input takes its Gram matrix from K (kernel_gram_kernel): no Gram
+  // tile.
+  const dim3 grid(static_cast<unsigned>(pl.tiles_w + (a.kernel ? 0 : 1)),
+                  static_cast<unsigned>(pl.ksplit));
   hipLaunchKernelGGL((skinny_mfma_kernel<D>), grid, dim3(256), 0, a.stream, X, a.order, q0, a.n, W,
                      nb, a.m, a.d, pl.kc, pl.tiles_w, vec, P, S, Gm);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || pl.ksplit == 1) return e;
+  // (With kernel input the sums of the absent Gram columns land in Gm and
+  // are overwritten by the Gram matrix read from K after this.)
   const int64_t total = static_cast<int64_t>(nb) * (a.m + nb);
   hipLaunchKernelGGL((skinny_sum_kernel<D>), dim3(static_cast<unsigned>((total + 255) / 256)),
                      dim3(256), 0, a.stream, P, S, Gm, nb, a.m, pl.ksplit);
@@ -865,7 +908,7 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   const int64_t B = kEpochBlock;
   const SkinnyPlan pl = skinny_plan(d, m);
   // Workspace: [flag (256 B) | the threads' store sinks | S | G | Delta | P |
-  // norms]
+  // norms | At (kernel input)]
   char* p = static_cast<char*>(a.ws);
   int* bad = reinterpret_cast<int*>(p);
   p += 256;
@@ -876,13 +919,22 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   D* Delta = Gm + B * B;
   D* P = Delta + B * m;  // the skinny products' partial sums
   D* norms_ws = P + static_cast<int64_t>(pl.ksplit) * B * (m + B);
+  D* At = norms_ws + n;
   *flag_dev = bad;
   hipError_t e = launch_clear(bad, 1, a.stream);
   if (e != hipSuccess) return e;
   const D* X = static_cast<const D*>(a.X);
   D* W = static_cast<D*>(a.W);
   const D* norms = static_cast<const D*>(a.norms);
-  if (!norms) {
+  EpochLaunch ak = a;  // kernel input: the score products' W is At
+  if (a.kernel) {
+    hipLaunchKernelGGL((kernel_diag_kernel<D>), dim3(static_cast<unsigned>((n + 255) / 256)),
+                       dim3(256), 0, a.stream, X, n, norms_ws);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    norms = norms_ws;
+    if ((e = launch_transpose(a.data, a.A, At, n, m, a.stream)) != hipSuccess) return e;
+    ak.W = At;
+  } else if (!norms) {
     hipLaunchKernelGGL((norms_kernel<D>), dim3(static_cast<unsigned>((n + 3) / 4)), dim3(256), 0,
                        a.stream, X, n, d, norms_ws);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -893,15 +945,28 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   ob.k = a.k;
   ob.c = a.c;
   ob.gamma = a.gamma;
+  ob.kernel = a.kernel ? 1 : 0;
   const dim3 rank_grid(static_cast<unsigned>((d + 255) / 256),
                        static_cast<unsigned>((m + kRankJ - 1) / kRankJ));
   for (int64_t q0 = 0; q0 < a.count; q0 += B) {
     const int nb = static_cast<int>(a.count - q0 < B ? a.count - q0 : B);
-    if ((e = launch_skinny<D>(a, q0, nb, S, Gm, P, pl)) != hipSuccess) return e;
+    if ((e = launch_skinny<D>(ak, q0, nb, S, Gm, P, pl)) != hipSuccess) return e;
+    if (a.kernel) {
+      hipLaunchKernelGGL((kernel_gram_kernel<D>), dim3(static_cast<unsigned>((nb * nb + 255) / 256)),
+                         dim3(256), 0, a.stream, X, a.order, q0, n, nb, Gm);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     if ((e = launch_block_for<D, R>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad)) != hipSuccess)
       return e;
-    hipLaunchKernelGGL((rank_update_kernel<D>), rank_grid, dim3(256), 0, a.stream, W, Delta, X,
-                       a.order, q0, n, nb, m, d);
+    if (a.kernel) {
+      const int64_t cnt = static_cast<int64_t>(nb) * m;
+      hipLaunchKernelGGL((kernel_at_kernel<D>), dim3(static_cast<unsigned>((cnt + 255) / 256)),
+                         dim3(256), 0, a.stream, static_cast<const D*>(a.A), At, a.order, q0, n,
+                         nb, m);
+    } else {
+      hipLaunchKernelGGL((rank_update_kernel<D>), rank_grid, dim3(256), 0, a.stream, W, Delta, X,
+                         a.order, q0, n, nb, m, d);
+    }
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;
@@ -909,13 +974,15 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
 
 }  // namespace
 
-size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool norms_given) {
+size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool norms_given,
+                             bool kernel) {
   const size_t es = data == SDCA_F32 ? 4 : 8;
   const size_t B = kEpochBlock;
   const size_t splits = static_cast<size_t>(skinny_plan(d, m).ksplit);
   return 256 + kEpochThreads * sizeof(double) + es * (2 * B * static_cast<size_t>(m) + B * B +
                      splits * B * (static_cast<size_t>(m) + B) +
-                     (norms_given ? 0 : static_cast<size_t>(n)));
+                     (norms_given && !kernel ? 0 : static_cast<size_t>(n)) +
+                     (kernel ? static_cast<size_t>(m) * static_cast<size_t>(n) : 0));
 }
 
 int64_t epoch_max_m(int data, int kind) {

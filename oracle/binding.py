@@ -246,6 +246,43 @@ class Library:
             raise RuntimeError(f"epoch_features failed: {rc}")
         return W, A
 
+    def epoch_kernel(self, obj, K, A, labels, order=None, result=None, epochs=0, reverse=False,
+                     offsets=None):
+        """One SDCA epoch on kernel input (update.h:88-107) over `order`
+        (None: 0..n-1): K (n, n) the training set's kernel matrix (row i =
+        K_i), A (n, m) C-contiguous, updated in place (and returned).  The
+        reference shim runs sdca::update_variables on a kernel_input
+        context; with epochs > 0 instead the reference's own solve().  The
+        restatement takes reverse=True for its second rounding of the
+        scores."""
+        n = K.shape[0]
+        m = A.shape[1]
+        data = _dt(K)
+        result = data if result is None else result
+        objarr = make_objectives([obj])
+        labels = np.ascontiguousarray(labels, dtype=np.int64)
+        od = None if order is None else np.ascontiguousarray(order, dtype=np.int64)
+        off = None if offsets is None else np.ascontiguousarray(offsets, dtype=np.int64)
+        count = n if od is None else od.size
+        common = (objarr, ctypes.c_int(data), ctypes.c_int(result), ctypes.c_int64(m),
+                  ctypes.c_int64(n), ctypes.c_void_p(K.ctypes.data),
+                  ctypes.c_void_p(A.ctypes.data), ctypes.c_void_p(labels.ctypes.data),
+                  ctypes.c_void_p(off.ctypes.data if off is not None else None),
+                  ctypes.c_void_p(od.ctypes.data if od is not None else None),
+                  ctypes.c_int64(count))
+        if hasattr(self.lib, "ref_epoch_kernel"):
+            f = self.lib.ref_epoch_kernel
+            f.restype = ctypes.c_int
+            rc = f(*common, ctypes.c_int64(epochs))
+        else:
+            assert epochs == 0
+            f = self.lib.oracle_epoch_kernel
+            f.restype = ctypes.c_int
+            rc = f(*common, ctypes.c_int(1 if reverse else 0))
+        if rc != 0:
+            raise RuntimeError(f"epoch_kernel failed: {rc}")
+        return A
+
     def blas_scores(self, X, W):
         """The reference's scores W' x_i (eval/scores.h:9-27, cblas_sgemv) of
         every example: X (n, d), W (m, d) float32 -> S (n, m)."""

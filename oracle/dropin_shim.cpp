@@ -138,9 +138,77 @@ int run_epoch(const Obj<float, double>& obj, int64_t d, int64_t m, int64_t n, co
   return 0;
 }
 
+// The same on kernel input (solver/update.h:88-107): K n x n, A updated.
+template <class Out, template <class, class> class Obj>
+int run_epoch_kernel(const Obj<float, double>& obj, int64_t m, int64_t n, const float* K,
+                     const int64_t* labels, const int64_t* offsets, const int64_t* order,
+                     int64_t count, float* A_gpu, float* A_ref) {
+  typedef std::integral_constant<bool, std::is_same<Out, sdca::multilabel_output>::value> ML;
+  typedef sdca::solver_context<float, double, sdca::kernel_input, Out, Obj> Ctx;
+  auto make = [&](float* A) {
+    typename Ctx::train_set_type set(
+        sdca::kernel_input<float>(static_cast<sdca::size_type>(n),
+                                  static_cast<sdca::size_type>(n), K),
+        output(ML(), m, labels, offsets, n));
+    return Ctx(std::move(set), Obj<float, double>(obj), A);
+  };
+  Ctx ctx_ref = make(A_ref);
+  Ctx ctx_gpu = make(A_gpu);
+  sdca::solver_scratch<float, sdca::kernel_input> scratch;
+  scratch.init(ctx_ref.train);
+  std::vector<sdca::size_type> examples(order, order + count);
+  for (auto i : examples) sdca::update_variables(i, ctx_ref, scratch);
+  try {
+    sdca::hip::update_epoch(ctx_gpu, scratch, examples.begin(), examples.end());
+  } catch (const sdca::hip::error& e) {
+    return e.status();
+  }
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+// dropin_update_epoch on kernel input: K (n x n) in place of X, no W.
+int dropin_update_epoch_kernel(int kind, double c, double gamma, int64_t k, int64_t m, int64_t n,
+                               const float* K, const int64_t* labels, const int64_t* offsets,
+                               const int64_t* order, int64_t count, float* A_gpu, float* A_ref) {
+  typedef sdca::multiclass_output MC;
+  typedef sdca::multilabel_output ML;
+  const sdca::size_type kk = static_cast<sdca::size_type>(k);
+  switch (kind) {
+    case SDCA_OBJ_MULTILABEL_HINGE:
+      return run_epoch_kernel<ML>(sdca::l2_multilabel_hinge<float, double>(c), m, n, K, labels,
+                                  offsets, order, count, A_gpu, A_ref);
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
+      return run_epoch_kernel<ML>(sdca::l2_multilabel_hinge_smooth<float, double>(c, gamma), m,
+                                  n, K, labels, offsets, order, count, A_gpu, A_ref);
+    case SDCA_OBJ_MULTILABEL_ENTROPY:
+      return run_epoch_kernel<ML>(sdca::l2_multilabel_entropy<float, double>(c), m, n, K, labels,
+                                  offsets, order, count, A_gpu, A_ref);
+    case SDCA_OBJ_HINGE_TOPK:
+      return run_epoch_kernel<MC>(sdca::l2_hinge_topk<float, double>(c, kk), m, n, K, labels,
+                                  nullptr, order, count, A_gpu, A_ref);
+    case SDCA_OBJ_HINGE_TOPK_SMOOTH:
+      return run_epoch_kernel<MC>(sdca::l2_hinge_topk_smooth<float, double>(c, gamma, kk), m, n,
+                                  K, labels, nullptr, order, count, A_gpu, A_ref);
+    case SDCA_OBJ_TOPK_HINGE:
+      return run_epoch_kernel<MC>(sdca::l2_topk_hinge<float, double>(c, kk), m, n, K, labels,
+                                  nullptr, order, count, A_gpu, A_ref);
+    case SDCA_OBJ_TOPK_HINGE_SMOOTH:
+      return run_epoch_kernel<MC>(sdca::l2_topk_hinge_smooth<float, double>(c, gamma, kk), m, n,
+                                  K, labels, nullptr, order, count, A_gpu, A_ref);
+    case SDCA_OBJ_ENTROPY:
+      return run_epoch_kernel<MC>(sdca::l2_entropy<float, double>(c), m, n, K, labels, nullptr,
+                                  order, count, A_gpu, A_ref);
+    case SDCA_OBJ_ENTROPY_TOPK:
+      return run_epoch_kernel<MC>(sdca::l2_entropy_topk<float, double>(c, kk), m, n, K, labels,
+                                  nullptr, order, count, A_gpu, A_ref);
+    default:
+      return -2;
+  }
+}
 
 // kind: an sdca_objective_kind (multilabel ones with offsets, n + 1 CSR row
 // starts).  W_* (m x d) and A_* (n x m) hold the starting point and receive

@@ -8,6 +8,7 @@
 //                      gemv (eval/scores.h:21-26) as a plain loop
 // oracle_epoch_features one SDCA epoch on feature input (solver.h:39-51,
 //                      update.h:52-85) over a given example order
+// oracle_epoch_kernel  the same on kernel input (update.h:88-107)
 //
 // Host pointers only.  `nthreads` > 1 splits columns / examples over
 // std::threads, each with its own scratch (the reference is single-threaded;
@@ -394,6 +395,34 @@ int oracle_epoch_features(const sdca_objective* obj, int data, int result, int64
     return orc::epoch<double, long double>(*obj, d, m, n, static_cast<const double*>(X),
                                            static_cast<double*>(W), static_cast<double*>(A),
                                            labels, offsets, order, count, reverse != 0);
+  return -2;
+}
+
+// One SDCA epoch on kernel input: K n x n (row i = K_i), A n x m updated in
+// place; the rest as oracle_epoch_features.
+int oracle_epoch_kernel(const sdca_objective* obj, int data, int result, int64_t m, int64_t n,
+                        const void* K, void* A, const int64_t* labels, const int64_t* offsets,
+                        const int64_t* order, int64_t count, int reverse) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return orc::epoch_kernel<float, float>(*obj, m, n, static_cast<const float*>(K),
+                                           static_cast<float*>(A), labels, offsets, order, count,
+                                           reverse != 0);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return orc::epoch_kernel<float, double>(*obj, m, n, static_cast<const float*>(K),
+                                            static_cast<float*>(A), labels, offsets, order, count,
+                                            reverse != 0);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return orc::epoch_kernel<double, double>(*obj, m, n, static_cast<const double*>(K),
+                                             static_cast<double*>(A), labels, offsets, order,
+                                             count, reverse != 0);
+  if (data == SDCA_F32 && result == SDCA_LONG_DOUBLE)
+    return orc::epoch_kernel<float, long double>(*obj, m, n, static_cast<const float*>(K),
+                                                 static_cast<float*>(A), labels, offsets, order,
+                                                 count, reverse != 0);
+  if (data == SDCA_F64 && result == SDCA_LONG_DOUBLE)
+    return orc::epoch_kernel<double, long double>(*obj, m, n, static_cast<const double*>(K),
+                                                  static_cast<double*>(A), labels, offsets, order,
+                                                  count, reverse != 0);
   return -2;
 }
 

@@ -170,6 +170,31 @@ inline bool update_dual_ml(const sdca_objective& ob, std::ptrdiff_t m, std::ptrd
   }
 }
 
+// The objective's update of example i (update_dual_variables,
+// update.h:12-49): the label (multiclass) or the labels (multilabel, output.h:121-164)
+// moved to the front of v = a_i and of the scores, the update, and v's
+// entries moved back.  Returns false for an objective without an update.
+template <class D, class R>
+inline bool update_example(const sdca_objective& ob, std::ptrdiff_t m, const int64_t* labels,
+                           const int64_t* offsets, std::ptrdiff_t i, D norm2, D* v, D* scores) {
+  if (offsets) {
+    const int64_t o0 = offsets[i], nl = offsets[i + 1] - offsets[i];
+    for (int64_t q = 0; q < nl; ++q) {
+      std::swap(v[q], v[labels[o0 + q]]);
+      std::swap(scores[q], scores[labels[o0 + q]]);
+    }
+    if (!update_dual_ml<D, R>(ob, m, nl, norm2, v, scores)) return false;
+    for (int64_t q = nl - 1; q >= 0; --q) std::swap(v[q], v[labels[o0 + q]]);
+  } else {
+    const std::ptrdiff_t y = static_cast<std::ptrdiff_t>(labels[i]);
+    std::swap(v[0], v[y]);
+    std::swap(scores[0], scores[y]);
+    if (!update_dual<D, R>(ob, m, norm2, v, scores)) return false;
+    std::swap(v[0], v[y]);
+  }
+  return true;
+}
+
 // One epoch over `order` (count entries; NULL: 0..n-1); offsets (n + 1,
 // CSR into labels) for the multilabel objectives, NULL for the multiclass
 // ones.  X: n x d, W: m x d,
@@ -190,22 +215,7 @@ inline int epoch(const sdca_objective& ob, std::ptrdiff_t d, std::ptrdiff_t m, s
     for (std::ptrdiff_t j = 0; j < m; ++j) scores[j] = dot_order(d, W + d * j, x, reverse);
     D* v = A + m * i;
     std::copy(v, v + m, copy.begin());
-    if (offsets) {
-      // multilabel move_front / move_back (output.h:121-164)
-      const int64_t o0 = offsets[i], nl = offsets[i + 1] - offsets[i];
-      for (int64_t q = 0; q < nl; ++q) {
-        std::swap(v[q], v[labels[o0 + q]]);
-        std::swap(scores[q], scores[labels[o0 + q]]);
-      }
-      if (!update_dual_ml<D, R>(ob, m, nl, norm2, v, scores.data())) return -1;
-      for (int64_t q = nl - 1; q >= 0; --q) std::swap(v[q], v[labels[o0 + q]]);
-    } else {
-      const std::ptrdiff_t y = static_cast<std::ptrdiff_t>(labels[i]);
-      std::swap(v[0], v[y]);
-      std::swap(scores[0], scores[y]);
-      if (!update_dual<D, R>(ob, m, norm2, v, scores.data())) return -1;
-      std::swap(v[0], v[y]);
-    }
+    if (!update_example<D, R>(ob, m, labels, offsets, i, norm2, v, scores.data())) return -1;
     // var_copy = a_old - a_new; diff = asum
     long double asum = 0;
     for (std::ptrdiff_t j = 0; j < m; ++j) {
@@ -219,6 +229,31 @@ inline int epoch(const sdca_objective& ob, std::ptrdiff_t d, std::ptrdiff_t m, s
         for (std::ptrdiff_t l = 0; l < d; ++l) w[l] = w[l] - x[l] * yj;
       }
     }
+  }
+  return 0;
+}
+
+// One epoch on kernel input (update.h:88-107) over `order`: K is the
+// training set's n x n kernel matrix (row i = K_i, the reference's column
+// i), A: n x m updated in place.  norm2 = K_ii; scores = A' K_i, the gemv of
+// eval/scores.h:30-47 over the n training examples (reverse: accumulated in
+// Data from the last example, else exact); only the dual variables change.
+template <class D, class R>
+inline int epoch_kernel(const sdca_objective& ob, std::ptrdiff_t m, std::ptrdiff_t n, const D* K,
+                        D* A, const int64_t* labels, const int64_t* offsets,
+                        const int64_t* order, std::ptrdiff_t count, bool reverse) {
+  std::vector<D> scores(static_cast<size_t>(m)), column(static_cast<size_t>(n));
+  for (std::ptrdiff_t q = 0; q < count; ++q) {
+    const std::ptrdiff_t i = order ? static_cast<std::ptrdiff_t>(order[q]) : q;
+    const D* ki = K + n * i;
+    const D norm2 = ki[i];
+    if (norm2 <= 0) continue;
+    for (std::ptrdiff_t j = 0; j < m; ++j) {
+      for (std::ptrdiff_t l = 0; l < n; ++l) column[l] = A[m * l + j];
+      scores[j] = dot_order(n, column.data(), ki, reverse);
+    }
+    if (!update_example<D, R>(ob, m, labels, offsets, i, norm2, A + m * i, scores.data()))
+      return -1;
   }
   return 0;
 }

@@ -558,12 +558,70 @@ void epoch_run(Obj<D, R> obj, int64_t d, int64_t m, int64_t n, const D* X, D* W,
     sdca::update_variables(static_cast<sdca::size_type>(order ? order[q] : q), ctx, scratch);
 }
 
+// The same on kernel input (update.h:88-107): K n x n column-major (column
+// i = K_i), A m x n updated in place, no primal variables.
+template <class Out, class D, class R, template <class, class> class Obj>
+void epoch_kernel_run(Obj<D, R> obj, int64_t m, int64_t n, const D* K, D* A,
+                      const int64_t* labels, const int64_t* offsets, const int64_t* order,
+                      int64_t count, int64_t epochs) {
+  typedef sdca::solver_context<D, R, sdca::kernel_input, Out, Obj> Ctx;
+  typename Ctx::train_set_type set(
+      sdca::kernel_input<D>(static_cast<sdca::size_type>(n), static_cast<sdca::size_type>(n), K),
+      make_out(std::integral_constant<bool, std::is_same<Out, sdca::multilabel_output>::value>(),
+               m, labels, offsets, 0, n));
+  Ctx ctx(std::move(set), std::move(obj), A);
+  if (epochs > 0) {
+    sdca::logging::set_level(sdca::logging::level::none);
+    ctx.criteria.max_epoch = static_cast<sdca::size_type>(epochs);
+    ctx.criteria.eval_epoch = 0;
+    ctx.criteria.eval_on_start = false;
+    auto solver = sdca::make_solver(ctx);
+    solver.solve();
+    return;
+  }
+  sdca::solver_scratch<D, sdca::kernel_input> scratch;
+  scratch.init(ctx.train);
+  for (int64_t q = 0; q < count; ++q)
+    sdca::update_variables(static_cast<sdca::size_type>(order ? order[q] : q), ctx, scratch);
+}
+
 #define SDCA_REF_EPOCH(OBJ)                                                               \
   epoch_run<sdca::multiclass_output, D, R>(OBJ, d, m, n, X, W, A, labels, nullptr, order,   \
                                            count, epochs)
 #define SDCA_REF_EPOCH_ML(OBJ)                                                            \
   epoch_run<sdca::multilabel_output, D, R>(OBJ, d, m, n, X, W, A, labels, offsets, order,   \
                                            count, epochs)
+
+#define SDCA_REF_EPOCH_K(OBJ)                                                             \
+  epoch_kernel_run<sdca::multiclass_output, D, R>(OBJ, m, n, K, A, labels, nullptr, order, \
+                                                  count, epochs)
+#define SDCA_REF_EPOCH_K_ML(OBJ)                                                          \
+  epoch_kernel_run<sdca::multilabel_output, D, R>(OBJ, m, n, K, A, labels, offsets, order, \
+                                                  count, epochs)
+
+template <class D, class R>
+int epoch_kernel_impl(const sdca_objective& ob, int64_t m, int64_t n, const D* K, D* A,
+                      const int64_t* labels, const int64_t* offsets, const int64_t* order,
+                      int64_t count, int64_t epochs) {
+  const R c = static_cast<R>(ob.c), g = static_cast<R>(ob.gamma);
+  const sdca::size_type k = static_cast<sdca::size_type>(ob.k);
+  switch (ob.kind) {
+    case SDCA_OBJ_HINGE_TOPK: SDCA_REF_EPOCH_K((sdca::l2_hinge_topk<D, R>(c, k))); break;
+    case SDCA_OBJ_HINGE_TOPK_SMOOTH: SDCA_REF_EPOCH_K((sdca::l2_hinge_topk_smooth<D, R>(c, g, k))); break;
+    case SDCA_OBJ_TOPK_HINGE: SDCA_REF_EPOCH_K((sdca::l2_topk_hinge<D, R>(c, k))); break;
+    case SDCA_OBJ_TOPK_HINGE_SMOOTH: SDCA_REF_EPOCH_K((sdca::l2_topk_hinge_smooth<D, R>(c, g, k))); break;
+    case SDCA_OBJ_ENTROPY: SDCA_REF_EPOCH_K((sdca::l2_entropy<D, R>(c))); break;
+    case SDCA_OBJ_ENTROPY_TOPK: SDCA_REF_EPOCH_K((sdca::l2_entropy_topk<D, R>(c, k))); break;
+    case SDCA_OBJ_MULTILABEL_HINGE:
+      SDCA_REF_EPOCH_K_ML((sdca::l2_multilabel_hinge<D, R>(c))); break;
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
+      SDCA_REF_EPOCH_K_ML((sdca::l2_multilabel_hinge_smooth<D, R>(c, g))); break;
+    case SDCA_OBJ_MULTILABEL_ENTROPY:
+      SDCA_REF_EPOCH_K_ML((sdca::l2_multilabel_entropy<D, R>(c))); break;
+    default: return SDCA_ERR_ARG_RANGE;
+  }
+  return 0;
+}
 
 template <class D, class R>
 int epoch_impl(const sdca_objective& ob, int64_t d, int64_t m, int64_t n, const D* X, D* W,
@@ -610,6 +668,23 @@ int ref_epoch_features(const sdca_objective* obj, int data, int result, int64_t 
   if (data == SDCA_F64 && result == SDCA_F64)
     return epoch_impl<double, double>(*obj, d, m, n, static_cast<const double*>(X),
         static_cast<double*>(W), static_cast<double*>(A), labels, offsets, order, count, epochs);
+  return SDCA_ERR_PRECISION;
+}
+
+// The reference's SDCA epoch on kernel input (see epoch_kernel_run): K n x n
+// (symmetric; column i = K_i), A m x n column-major, updated in place.
+int ref_epoch_kernel(const sdca_objective* obj, int data, int result, int64_t m, int64_t n,
+                     const void* K, void* A, const int64_t* labels, const int64_t* offsets,
+                     const int64_t* order, int64_t count, int64_t epochs) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return epoch_kernel_impl<float, float>(*obj, m, n, static_cast<const float*>(K),
+        static_cast<float*>(A), labels, offsets, order, count, epochs);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return epoch_kernel_impl<float, double>(*obj, m, n, static_cast<const float*>(K),
+        static_cast<float*>(A), labels, offsets, order, count, epochs);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return epoch_kernel_impl<double, double>(*obj, m, n, static_cast<const double*>(K),
+        static_cast<double*>(A), labels, offsets, order, count, epochs);
   return SDCA_ERR_PRECISION;
 }
 

@@ -188,3 +188,44 @@ def test_dropin_update_epoch(dropin, oracle, obj):
         err = float(np.abs(g - r).max())
         assert err <= tol, f"{obj[0]} {what}: |drop-in - reference| {err:.3e} > {tol:.3e}"
     assert np.abs(Ar).max() > 0.01
+
+
+@pytest.mark.parametrize("obj", EPOCH_OBJS)
+def test_dropin_update_epoch_kernel(dropin, oracle, obj):
+    """The kernel_input overload of sdca::hip::update_epoch against the
+    reference's own loop of update_variables on a kernel input
+    (solver/update.h:88-107), a Gaussian kernel, two epochs from zero, with
+    the bound of the feature form's drop-in test."""
+    import libsdca_amd as sd
+    rng = np.random.default_rng(19)
+    n, d, m = 150, 8, 11
+    X = rng.standard_normal((n, d))
+    X /= np.linalg.norm(X, axis=1, keepdims=True)
+    sq = (X * X).sum(1)
+    K = np.exp(-0.5 * np.maximum(sq[:, None] + sq[None, :] - 2 * X @ X.T, 0.0)).astype(np.float32)
+    multilabel = "multilabel" in obj[0]
+    if multilabel:
+        counts = rng.integers(1, 4, n)
+        y = np.concatenate([np.sort(rng.choice(m, c, replace=False)) for c in counts]).astype(np.int64)
+        off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    else:
+        y = rng.integers(0, m, n).astype(np.int64)
+        off = None
+    Ag, Ar = np.zeros((n, m), np.float32), np.zeros((n, m), np.float32)
+    orders = [sd.epoch_order(n, e) for e in range(2)]
+    for order in orders:
+        rc = dropin.dropin_update_epoch_kernel(
+            ctypes.c_int(KIND[obj[0]]), ctypes.c_double(obj[1]), ctypes.c_double(obj[2]),
+            ctypes.c_int64(obj[3]), ctypes.c_int64(m), ctypes.c_int64(n), ptr(K), ptr(y), ptr(off),
+            ptr(order), ctypes.c_int64(len(order)), ptr(Ag), ptr(Ar))
+        assert rc == 0, rc
+    name = (obj[0][3:],) + tuple(obj[1:])
+    Ao, Av = np.zeros((n, m), np.float32), np.zeros((n, m), np.float32)
+    for order in orders:
+        oracle.epoch_kernel(name, K, Ao, y, order, result=1, offsets=off)
+        oracle.epoch_kernel(name, K, Av, y, order, result=1, reverse=True, offsets=off)
+    eps = np.finfo(np.float32).eps
+    tol = 8 * float(np.abs(Ao - Av).max()) + 16 * eps * max(1.0, float(np.abs(Ao).max()))
+    err = float(np.abs(Ag - Ar).max())
+    assert err <= tol, f"{obj[0]} A: |drop-in - reference| {err:.3e} > {tol:.3e}"
+    assert np.abs(Ar).max() > 0.01

@@ -138,3 +138,62 @@ def test_epoch_multilabel_dual_feasible(oracle):
         assert (A[i, pos] >= -1e-12).all() and (A[i, neg] <= 1e-12).all()
         assert abs(A[i, pos].sum() + A[i, neg].sum()) <= 1e-9
         assert A[i, pos].sum() <= c + 1e-9
+
+
+def run_kernel(lib, obj, K, y, m, result, orders, reverse=False, offsets=None):
+    n = K.shape[0]
+    A = np.zeros((n, m), K.dtype)
+    for order in orders:
+        lib.epoch_kernel(obj, K, A, y, order, result=result, reverse=reverse, offsets=offsets)
+    return A
+
+
+@pytest.mark.parametrize("dtype,result", PAIRS)
+@pytest.mark.parametrize("obj", OBJS + ML_OBJS)
+def test_epoch_kernel_restatement_vs_reference(oracle, reference, obj, dtype, result):
+    """The kernel-input epoch (update.h:88-107: norm2 = K_ii, scores = A' K_i,
+    no primal update) of the restatement against the reference's own
+    update_variables on a kernel_input context, two epochs, the spread
+    criterion of the feature epoch; K = X X' of unit rows, with one zero row
+    (K_ii = 0: the reference skips the example)."""
+    import libsdca_amd as sd
+    X, y, m = problem(dtype, seed=21 + len(obj[0]))
+    K = (X.astype(np.float64) @ X.astype(np.float64).T).astype(dtype)
+    n = K.shape[0]
+    off = None
+    if obj in ML_OBJS:
+        y, off = ml_labels(np.random.default_rng(7), n, m)
+    orders = [sd.epoch_order(n, e) for e in range(2)]
+    Ar = run_kernel(reference, obj, K, y, m, result, orders, offsets=off)
+    Ao = run_kernel(oracle, obj, K, y, m, result, orders, offsets=off)
+    Av = run_kernel(oracle, obj, K, y, m, result, orders, reverse=True, offsets=off)
+    eps = np.finfo(dtype).eps
+    spread = float(np.abs(Ao - Av).max())
+    tol = 4 * spread + 8 * eps * max(1.0, float(np.abs(Ar).max()))
+    err = float(np.abs(Ao - Ar).max())
+    assert err <= tol, f"{obj[0]}: |oracle - ref| {err:.3e} > {tol:.3e}"
+    assert np.abs(Ar).max() > 0.01
+    assert not Ar[3].any()
+
+
+@pytest.mark.parametrize("obj", OBJS[:1] + OBJS[4:5] + ML_OBJS[:1])
+def test_epoch_kernel_equals_feature_epoch(oracle, obj):
+    """Mathematics: with K = X X' the kernel-input epoch is the feature
+    epoch (scores W' x_i = A' X x_i = A' K_i with W = X' A, and norm2 =
+    ||x_i||^2 = K_ii): the dual variables agree to the rounding of the
+    scores, in double with the restatement's exact dot products."""
+    import libsdca_amd as sd
+    X, y, m = problem(np.float64, seed=31)
+    K = X @ X.T
+    n, d = X.shape
+    off = None
+    if obj in ML_OBJS:
+        y, off = ml_labels(np.random.default_rng(9), n, m)
+    orders = [sd.epoch_order(n, e) for e in range(2)]
+    W = np.zeros((m, d))
+    A = np.zeros((n, m))
+    for order in orders:
+        oracle.epoch_features(obj, X, W, A, y, order, result=1, offsets=off)
+    Ak = run_kernel(oracle, obj, K, y, m, 1, orders, offsets=off)
+    assert np.abs(A).max() > 0.01
+    assert np.abs(Ak - A).max() <= 1e-12 * max(1.0, float(np.abs(A).max()))
