@@ -19,12 +19,14 @@ cone on the headline input), c3 (entropy f64 m=1000 n=2e5), c3norm
 m=1000 n=1e5: examples/s, roofline on the fp32 MFMA score GEMM), c4f64 (the
 same pass in double: roofline on the fp64 MFMA score GEMM), c5eval
 (multilabel evaluation d=1024 m=200 n=5e5), c4epoch (one SDCA epoch on the C4
-data: examples/s, the reference's own epoch loop as cpu_baseline).
+data: examples/s, the reference's own epoch loop as cpu_baseline), c4kepoch
+(one SDCA epoch on kernel input, K of n = 20,000 examples, m = 1000).
 
 The default run (c2) also times the whole C4 evaluation pass under the same
 clock and nests it as "c4" (examples/s, an MFMA roofline for the score GEMM
 and for the whole pass, its own cpu_baseline); --no-c4 skips it.  It nests
-one SDCA epoch on the C4 shape as "c4epoch" likewise (--no-epoch skips it).
+one SDCA epoch on the C4 shape as "c4epoch" and one on kernel input as
+"c4kepoch" likewise (--no-epoch skips both).
 
 cpu_baseline: the reference's own prox loop (oracle/_ref, built from the
 reference headers with -O3) - or the oracle restatement when that library is
@@ -113,6 +115,12 @@ CONFIGS = {
                     desc="one SDCA epoch (update_variables over the reference solver's shuffled "
                          "order), fp32: X d=4096 x n=100,000 (N(0,1), unit columns), m=1000, "
                          "smooth top-5 hinge (gamma=1, c=1), W and A from zero"),
+    "c4kepoch": dict(op="epoch", kernel=True, d=4096, m=1000, n=20_000, dtype="f32", result="f32",
+                     seed=107, obj=("l2_hinge_topk_smooth", 1.0, 1.0, 5), steps=2, warmup=1,
+                     desc="one SDCA epoch on kernel input (the kernel form of update_variables "
+                          "over the reference solver's shuffled order), fp32: K = X'X (n = "
+                          "20,000 unit-norm N(0,1) features of d = 4096), m=1000, smooth top-5 "
+                          "hinge (gamma=1, c=1), A from zero"),
     "c4kernel": dict(op="eval", kernel=True, d=4096, m=1000, n=20_000, dtype="f32", result="f32",
                      seed=106, objs=[("l2_hinge_topk_smooth", 1.0, 1.0, 5), ("l2_entropy", 1.0, 1.0, 1)],
                      desc="kernel-input evaluation pass, fp32: K = X'X (n = n_train = 20,000 "
@@ -130,6 +138,8 @@ CONFIGS = {
 # Nested in the default (c2) run: the other configurations of the path.
 NESTED_PROX = ("c1", "c3", "c3norm", "lambert", "c5prox")
 NESTED_EVAL = ("c5eval",)
+EPOCH_KEYS = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline",
+              "note", "cpu_baseline")
 PROX_KEYS = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline",
              "launch_floor", "cpu_baseline")
 EVAL_KEYS = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline",
@@ -469,22 +479,37 @@ def bench_epoch(cfg, args, torch, sd, steps=None, warmup=None):
     if warmup is None:
         warmup = cfg["warmup"] if args.warmup is None else args.warmup
     dev = torch.device("cuda:0")
-    X, _, labels, _ = make_eval_input(cfg, torch, dev)
+    kernel = bool(cfg.get("kernel"))
+    X, _, labels, _ = make_eval_input(cfg, torch, dev)  # X = K (n x n) for kernel input
     n, m, d = cfg["n"], cfg["m"], cfg["d"]
-    W = torch.zeros((m, d), dtype=torch.float32, device=dev)
     A = torch.zeros((n, m), dtype=torch.float32, device=dev)
-    norms = (X * X).sum(dim=1).contiguous()
+    if kernel:
+        W = norms = None
+    else:
+        W = torch.zeros((m, d), dtype=torch.float32, device=dev)
+        norms = (X * X).sum(dim=1).contiguous()
     orders = [torch.from_numpy(sd.epoch_order(n, e)).to(dev) for e in range(warmup + steps)]
     res = "float" if cfg["result"] == "f32" else "double"
+
+    def epoch(e):
+        if kernel:
+            sd.epoch_kernel(cfg["obj"], X, A, labels, order=orders[e], result=res)
+        else:
+            sd.epoch_features(cfg["obj"], X, W, A, labels, order=orders[e], norms=norms,
+                              result=res)
+
     for e in range(warmup):
-        sd.epoch_features(cfg["obj"], X, W, A, labels, order=orders[e], norms=norms, result=res)
+        epoch(e)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for e in range(warmup, warmup + steps):
-        sd.epoch_features(cfg["obj"], X, W, A, labels, order=orders[e], norms=norms, result=res)
+        epoch(e)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    recs, _, _ = sd.eval_features([cfg["obj"]], X, W, labels, A=A, result="double")
+    if kernel:
+        recs, _, _ = sd.eval_kernel([cfg["obj"]], X, A, labels, result="double")
+    else:
+        recs, _, _ = sd.eval_features([cfg["obj"]], X, W, labels, A=A, result="double")
     r = recs[0]
     gap = (r["primal"] - r["dual"]) / max(abs(r["primal"]), abs(r["dual"]))
     result = {
@@ -493,7 +518,7 @@ def bench_epoch(cfg, args, torch, sd, steps=None, warmup=None):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": cfg["dtype"], "data": "synthetic (seeded on the device)",
         "config": {"workload": cfg["desc"], "d": d, "m": m, "n": n,
-                   "objective": list(cfg["obj"])},
+                   "input": "kernel" if kernel else "features", "objective": list(cfg["obj"])},
         "roofline": None,
         "note": "latency-bound: the dual updates run in order in one workgroup per block of "
                 "32 examples (profiles/ has the per-kernel split); relative duality gap after "
@@ -516,16 +541,20 @@ def cpu_baseline_epoch(cfg, X, labels, sd, seconds):
     oname = {"l2_hinge_topk_smooth": "hinge_topk_smooth"}
     obj = (oname[cfg["obj"][0]],) + tuple(cfg["obj"][1:])
     n, m, d = cfg["n"], cfg["m"], cfg["d"]
-    Xh = X.cpu().numpy()
+    kernel = bool(cfg.get("kernel"))
+    Xh = X.cpu().numpy()  # K for kernel input
     lab = labels.cpu().numpy()
     order = sd.epoch_order(n, 0)
+    res = 0 if cfg["result"] == "f32" else 1
 
     def run(count):
-        W = np.zeros((m, d), np.float32)
         A = np.zeros((n, m), np.float32)
         t0 = time.perf_counter()
-        ref.epoch_features(obj, Xh, W, A, lab, order[:count],
-                           result=0 if cfg["result"] == "f32" else 1)
+        if kernel:
+            ref.epoch_kernel(obj, Xh, A, lab, order[:count], result=res)
+        else:
+            W = np.zeros((m, d), np.float32)
+            ref.epoch_features(obj, Xh, W, A, lab, order[:count], result=res)
         return time.perf_counter() - t0
 
     count = 64
@@ -533,8 +562,10 @@ def cpu_baseline_epoch(cfg, X, labels, sd, seconds):
     count = max(64, min(n, int(count * seconds / max(t, 1e-3))))
     t = run(count)
     return {"value": count / t, "unit": "examples/s", "cores": 1, "kind": "reference",
-            "sample": f"the first {count} examples of epoch 0's order from W = 0, A = 0, "
-                      f"1 thread ({t:.1f} s): the reference's update_variables with MKL"}
+            "sample": f"the first {count} examples of epoch 0's order from "
+                      f"{'A = 0' if kernel else 'W = 0, A = 0'}, 1 thread ({t:.1f} s): the "
+                      f"reference's update_variables ({'kernel' if kernel else 'feature'} "
+                      "input) with MKL"}
 
 
 def cpu_baseline_eval(cfg, X, W, labels, offsets, seconds, kernel=False):
@@ -799,9 +830,11 @@ def main():
         torch.cuda.empty_cache()
         ep = bench_epoch(CONFIGS["c4epoch"], args, torch, sd, steps=args.epoch_steps,
                          warmup=args.epoch_warmup)
-        result["c4epoch"] = {key: ep[key] for key in ("value", "unit", "ms_per_step", "steps",
-                                                      "warmup", "dtype", "config", "roofline",
-                                                      "note", "cpu_baseline") if key in ep}
+        result["c4epoch"] = {key: ep[key] for key in EPOCH_KEYS if key in ep}
+        torch.cuda.empty_cache()
+        ep = bench_epoch(CONFIGS["c4kepoch"], args, torch, sd, steps=args.epoch_steps,
+                         warmup=args.epoch_warmup)
+        result["c4kepoch"] = {key: ep[key] for key in EPOCH_KEYS if key in ep}
     print(json.dumps(result))
 
 
