@@ -80,6 +80,58 @@ typedef struct sdca_thresholds {
   double t, lo, hi;
 } sdca_thresholds;
 
+/* Which return of the operator's threshold function produced a record. */
+typedef enum sdca_prox_branch {
+  /* the operator's own solve: knapsack_eq's variable fixing
+     (knapsack_eq.h:25-109), the entropy and Lambert solves (entropy.h:30-52,
+     entropy_norm.h:157-180, two_entropy.h:131-231); for the two-block
+     simplex, common sum rhs (two_simplex.h:44-67 phase 1;
+     two_simplex_sort.h:84-87) */
+  SDCA_BRANCH_SEARCH = 0,
+  /* knapsack_le: the clamp at t = 0 meets the sum (knapsack_le.h:40-43) */
+  SDCA_BRANCH_INACTIVE = 1,
+  /* top-k: the k largest sum to <= 16 eps, all zero (topk_cone.h:34-41) */
+  SDCA_BRANCH_ZERO = 2,
+  /* top-k: the k largest at hi, nothing free (topk_cone.h:43-52,
+     topk_simplex.h:53-58) */
+  SDCA_BRANCH_CONSTANT = 3,
+  /* the equality knapsack's solution reached from another operator:
+     knapsack_le active (knapsack_le.h:39-40), the top-k simplex with
+     hi = rhs / k (topk_simplex.h:55-65), knapsack_le_biased's equality
+     solution (knapsack_le_biased.h:117-120) */
+  SDCA_BRANCH_KNAPSACK = 4,
+  /* a U/M scan accepted a partition: topk_cone_search (topk_cone.h:104),
+     the biased cone (topk_cone_biased.h:57), knapsack_le_biased's search
+     (knapsack_le_biased.h:62) */
+  SDCA_BRANCH_SCAN = 5,
+  /* a U/M scan accepted nothing: the default zero record (topk_cone.h:131,
+     topk_cone_biased.h:85, knapsack_le_biased.h:89) */
+  SDCA_BRANCH_DEFAULT = 6,
+  /* top-k entropy: U empty (topk_entropy.h:38-41; biased:
+     topk_entropy_biased.h:219-233) */
+  SDCA_BRANCH_U_EMPTY = 7,
+  /* top-k entropy: U grown (topk_entropy.h:43-75; biased:
+     topk_entropy_biased.h:235-269) */
+  SDCA_BRANCH_U_GROWN = 8,
+  /* two-block simplex: common sum below rhs (two_simplex.h:69-117 phase 2;
+     two_simplex_sort.h:78-81) */
+  SDCA_BRANCH_BELOW_RHS = 9
+} sdca_prox_branch;
+
+/* The sets of a record: the reference's record carries iterators first and
+ * last over its permuted copy of the column (proxdef.h:29-67), [begin,
+ * first) at hi, [first, last) free, [last, end) at lo; n_hi = first - begin,
+ * n_mid = last - first, as the reference's own threshold function leaves
+ * them (for example (k, 0) when the k largest are at hi, (0, m) for the top-k
+ * entropy with U empty and for every biased top-k entropy record, (0, |kept|)
+ * for the two-block simplex).  branch: an sdca_prox_branch. */
+typedef struct sdca_prox_sets {
+  int64_t n_hi;
+  int64_t n_mid;
+  int32_t branch;
+  int32_t reserved;
+} sdca_prox_sets;
+
 #define SDCA_DEVICE_PTR 0u
 #define SDCA_HOST_PTR 1u
 
@@ -113,6 +165,22 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result,
               int64_t m, int64_t n, const void* in, void* out,
               const sdca_prox_params* params, const int64_t* col_p,
               sdca_thresholds* thresholds, unsigned flags, void* stream);
+
+/*
+ * sdca_prox that also returns each record's sets and branch (the
+ * reference's first / last, proxdef.h:29-67): sets holds n records (2n for
+ * the two-block operators, block a then b), host or device memory as the
+ * other arrays; NULL gives sdca_prox.  Not for SDCA_PROX_LAMBERT_W_EXP (no
+ * records).  The sets are the GPU's own partition; next to the reference
+ * they can differ only by entries tied with a threshold at rounding level,
+ * and the branch only where the reference's own epsilon tests are decided at
+ * rounding level.
+ */
+int sdca_prox_with_sets(sdca_prox_op op, sdca_dtype data, sdca_dtype result,
+                        int64_t m, int64_t n, const void* in, void* out,
+                        const sdca_prox_params* params, const int64_t* col_p,
+                        sdca_thresholds* thresholds, sdca_prox_sets* sets,
+                        unsigned flags, void* stream);
 
 /*
  * sdca_prox without any device allocation.  No counterpart in the reference:

@@ -40,7 +40,7 @@ __all__ = [
     "prox_topk_simplex_biased", "prox_topk_cone_biased", "prox_topk_entropy_biased",
     "prox_two_simplex_sort", "prox_two_entropy", "lambert_w_exp", "OPS", "F32", "F64",
     "OBJECTIVES", "objective", "scores", "eval_features", "eval_kernel", "eval_scores",
-    "recompute_primal", "epoch_order", "epoch_features", "epoch_kernel",
+    "recompute_primal", "epoch_order", "epoch_features", "epoch_kernel", "BRANCHES",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -54,6 +54,12 @@ OPS = {
     "two_simplex": 7, "lambert_w_exp": 8, "knapsack_le_biased": 9,
     "topk_simplex_biased": 10, "topk_cone_biased": 11,
     "topk_entropy_biased": 12, "two_simplex_sort": 13, "two_entropy": 14,
+}
+# sdca_prox_branch (include/sdca_hip.h): the return of the threshold
+# function that produced a record.
+BRANCHES = {
+    0: "search", 1: "inactive", 2: "zero", 3: "constant", 4: "knapsack", 5: "scan",
+    6: "default", 7: "u_empty", 8: "u_grown", 9: "below_rhs",
 }
 STATUS = {
     0: "OK", 1: "ARG_NULL", 2: "ARG_RANGE", 3: "PRECISION", 4: "NOT_IMPLEMENTED",
@@ -127,6 +133,7 @@ def library():
             pass
         lib = ctypes.CDLL(LIB_PATH)
         lib.sdca_prox.restype = ctypes.c_int
+        lib.sdca_prox_with_sets.restype = ctypes.c_int
         lib.sdca_prox.argtypes = [
             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
             ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ProxParams), ctypes.c_void_p,
@@ -209,14 +216,16 @@ def _stream_ptr():
 
 
 def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
-         alpha=1.0, k=1, p=1, col_p=None, thresholds=False, check_col_p=True):
+         alpha=1.0, k=1, p=1, col_p=None, thresholds=False, check_col_p=True, sets=False):
     """Batched prox over the rows of A (each row is one column of the
     reference's dim x n matrix).  Returns out (A itself when out is None) and,
     with thresholds=True, an (n, 3) (or (2n, 3) for the two-block operators) array of
-    (t, lo, hi) per column/block.  A device col_p is checked against
-    [1, dim - 1] here (one synchronisation) unless check_col_p=False, for
-    callers that validated it already (the kernels clamp it into range
-    either way)."""
+    (t, lo, hi) per column/block; with sets=True also an int64 array of the
+    same shape of (n_hi, n_mid, branch) per record (sdca_prox_with_sets: the
+    sizes of the record's set at hi and free set, and its sdca_prox_branch).
+    A device col_p is checked against [1, dim - 1] here (one
+    synchronisation) unless check_col_p=False, for callers that validated it
+    already (the kernels clamp it into range either way)."""
     lib = library()
     code = OPS[op] if isinstance(op, str) else int(op)
     data = _dtype_code(A)
@@ -243,6 +252,9 @@ def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
         if not A.is_cuda:
             raise SdcaError(2, "torch inputs must be CUDA tensors")
         thr = torch.zeros((nthr, 3), dtype=torch.float64, device=A.device) if thresholds else None
+        # sdca_prox_sets is {int64, int64, int32, int32}: the third int64 word
+        # reads as the branch (the reserved half is 0).
+        st = torch.zeros((nthr, 3), dtype=torch.int64, device=A.device) if sets else None
         cp = None
         if col_p is not None:
             cp = torch.as_tensor(col_p, dtype=torch.int64, device=A.device).contiguous().reshape(-1)
@@ -252,18 +264,40 @@ def prox(op, A, out=None, result=None, lo=0.0, hi=1.0, rhs=1.0, rho=1.0,
                 lo_p, hi_p = torch.aminmax(cp)
                 if int(lo_p) < 1 or int(hi_p) > m - 1:
                     raise SdcaError(2, f"col_p must lie in [1, {m - 1}] (got {int(lo_p)}..{int(hi_p)})")
-        check(lib.sdca_prox(code, data, res, m, n, A.data_ptr(), out.data_ptr(),
-                            ctypes.byref(params), cp.data_ptr() if cp is not None else None,
-                            thr.data_ptr() if thr is not None else None, 0, _stream_ptr()))
-        return (out, thr) if thresholds else out
+        if st is not None:
+            check(lib.sdca_prox_with_sets(
+                code, data, res, ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(A.data_ptr()),
+                ctypes.c_void_p(out.data_ptr()), ctypes.byref(params),
+                ctypes.c_void_p(cp.data_ptr() if cp is not None else None),
+                ctypes.c_void_p(thr.data_ptr() if thr is not None else None),
+                ctypes.c_void_p(st.data_ptr()), ctypes.c_uint(0), _stream_ptr()))
+        else:
+            check(lib.sdca_prox(code, data, res, m, n, A.data_ptr(), out.data_ptr(),
+                                ctypes.byref(params), cp.data_ptr() if cp is not None else None,
+                                thr.data_ptr() if thr is not None else None, 0, _stream_ptr()))
+        return _prox_result(out, thr, st, thresholds, sets)
     thr = np.zeros((nthr, 3), dtype=np.float64) if thresholds else None
+    st = np.zeros((nthr, 3), dtype=np.int64) if sets else None
     cp = None if col_p is None else np.ascontiguousarray(col_p, dtype=np.int64).reshape(-1)
     if cp is not None and cp.shape[0] != n:
         raise SdcaError(2, f"col_p has {cp.shape[0]} entries for {n} columns")
-    check(lib.sdca_prox(code, data, res, m, n, A.ctypes.data, out.ctypes.data,
-                        ctypes.byref(params), cp.ctypes.data if cp is not None else None,
-                        thr.ctypes.data if thr is not None else None, HOST_PTR, None))
-    return (out, thr) if thresholds else out
+    if st is not None:
+        check(lib.sdca_prox_with_sets(
+            code, data, res, ctypes.c_int64(m), ctypes.c_int64(n), ctypes.c_void_p(A.ctypes.data),
+            ctypes.c_void_p(out.ctypes.data), ctypes.byref(params),
+            ctypes.c_void_p(cp.ctypes.data if cp is not None else None),
+            ctypes.c_void_p(thr.ctypes.data if thr is not None else None),
+            ctypes.c_void_p(st.ctypes.data), ctypes.c_uint(HOST_PTR), None))
+    else:
+        check(lib.sdca_prox(code, data, res, m, n, A.ctypes.data, out.ctypes.data,
+                            ctypes.byref(params), cp.ctypes.data if cp is not None else None,
+                            thr.ctypes.data if thr is not None else None, HOST_PTR, None))
+    return _prox_result(out, thr, st, thresholds, sets)
+
+
+def _prox_result(out, thr, st, thresholds, sets):
+    res = (out,) + ((thr,) if thresholds else ()) + ((st,) if sets else ())
+    return res if len(res) > 1 else out
 
 
 def _rows(dim, A):

@@ -214,6 +214,14 @@ int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m, in
                               stream_ptr, nullptr, 0);
 }
 
+int sdca_prox_with_sets(sdca_prox_op op, sdca_dtype data, sdca_dtype result, int64_t m,
+                        int64_t n, const void* in, void* out, const sdca_prox_params* params,
+                        const int64_t* col_p, sdca_thresholds* thresholds, sdca_prox_sets* sets,
+                        unsigned flags, void* stream_ptr) {
+  return sdca_gpu::prox_entry(op, data, result, m, n, in, out, params, col_p, thresholds, flags,
+                              stream_ptr, nullptr, 0, sets);
+}
+
 }  // extern "C"
 
 namespace sdca_gpu {
@@ -223,7 +231,7 @@ int set_error(int code, const char* message) { return fail(code, "%s", message);
 int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, const void* in,
                void* out, const sdca_prox_params* params, const int64_t* col_p,
                sdca_thresholds* thresholds, unsigned flags, void* stream_ptr, int* fixed_list,
-               int64_t fixed_list_ints) {
+               int64_t fixed_list_ints, sdca_prox_sets* sets) {
   const sdca_prox_op op = static_cast<sdca_prox_op>(op_in);
   const sdca_dtype data = static_cast<sdca_dtype>(data_in);
   const sdca_dtype result = static_cast<sdca_dtype>(result_in);
@@ -265,6 +273,8 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
   }
   if ((op == SDCA_PROX_ENTROPY || op == SDCA_PROX_ENTROPY_NORM) && (!(p.hi > 0) || !(p.rhs > 0)))
     return fail(SDCA_ERR_ARG_RANGE, "entropic projections need hi > 0 and rhs > 0");
+  if (sets && op == SDCA_PROX_LAMBERT_W_EXP)
+    return fail(SDCA_ERR_ARG_RANGE, "lambert_w_exp has no threshold records (sets must be NULL)");
   if (n == 0) return SDCA_OK;
   if (!in || !out) return fail(SDCA_ERR_ARG_NULL, "in and out must not be NULL");
 
@@ -310,11 +320,12 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
                   "sdca_prox_noalloc: n = %lld columns exceed its fixed scratch of %lld columns "
                   "for this operator", (long long)n, (long long)(fixed_list_ints - 2));
   }
-  DeviceBuffer din, dout, dcolp, dthr;
+  DeviceBuffer din, dout, dcolp, dthr, dsets;
   const void* d_in = in;
   void* d_out = out;
   const int64_t* d_colp = col_p;
   sdca_thresholds* d_thr = thresholds;
+  sdca_prox_sets* d_sets = sets;
   if (host) {
     rc = stage_in(in, bytes, din, stream);
     if (rc) return rc;
@@ -334,6 +345,11 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
       SDCA_HIP_TRY(hipMalloc(&dthr.ptr, static_cast<size_t>(nthr) * sizeof(sdca_thresholds)),
                    "hipMalloc(staging)");
       d_thr = static_cast<sdca_thresholds*>(dthr.ptr);
+    }
+    if (sets) {
+      SDCA_HIP_TRY(hipMalloc(&dsets.ptr, static_cast<size_t>(nthr) * sizeof(sdca_prox_sets)),
+                   "hipMalloc(staging)");
+      d_sets = static_cast<sdca_prox_sets*>(dsets.ptr);
     }
   }
   if (!two) d_colp = nullptr;
@@ -355,6 +371,7 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
   a.p = p.p;
   a.col_p = d_colp;
   a.thr = d_thr;
+  a.sets = d_sets;
   a.slow = nullptr;
   a.stream = stream;
 
@@ -422,6 +439,9 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
     SDCA_HIP_TRY(hipMemcpyAsync(out, d_out, bytes, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
     if (thresholds)
       SDCA_HIP_TRY(hipMemcpyAsync(thresholds, d_thr, static_cast<size_t>(nthr) * sizeof(sdca_thresholds),
+                                  hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
+    if (sets)
+      SDCA_HIP_TRY(hipMemcpyAsync(sets, d_sets, static_cast<size_t>(nthr) * sizeof(sdca_prox_sets),
                                   hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(D2H)");
     SDCA_HIP_TRY(hipStreamSynchronize(stream), "hipStreamSynchronize");
   }

@@ -68,14 +68,14 @@ hipError_t launch_one(const ProxLaunch& a) {
       hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, true>),
                          dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
                          static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
-                         a.col_p, a.thr, a.slow);
+                         a.col_p, a.thr, a.slow, a.sets);
       return hipGetLastError();
     }
   }
   hipLaunchKernelGGL((prox_columns_kernel<FAM, KM, D, R, G, C, BT, false>),
                      dim3(static_cast<unsigned>(blocks)), dim3(BT), shmem, a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
-                     a.col_p, a.thr, a.slow);
+                     a.col_p, a.thr, a.slow, a.sets);
   return hipGetLastError();
 }
 

@@ -36,7 +36,8 @@ constexpr int kEbMaxWaves = 4;
 template <class D, class R>
 __global__ void __launch_bounds__(64 * kEbMaxWaves)
 entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, int k,
-               R alpha, sdca_thresholds* __restrict__ thr, int stride_elems, int reuse) {
+               R alpha, sdca_thresholds* __restrict__ thr, int stride_elems, int reuse,
+               sdca_prox_sets* __restrict__ sets) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
@@ -53,12 +54,16 @@ entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64
     for (int i = lane; i < m; i += 64) s[i] = col[i];
     wave_lds_sync();
     R t, hi, tw = 0;
-    entbias_thresholds<D, R>(s, m, lane, k, alpha, t, hi, wl, &tw);
+    int branch = SDCA_BRANCH_U_EMPTY;
+    entbias_thresholds<D, R>(s, m, lane, k, alpha, t, hi, wl, &tw, &branch);
     if (thr && lane == 0) {
       thr[j].t = static_cast<double>(t);
       thr[j].lo = 0;
       thr[j].hi = static_cast<double>(hi);
     }
+    // The reference's record keeps (first, last) in every branch
+    // (topk_entropy_biased.h:224, 232, 269).
+    if (sets && lane == 0) sets[j] = sdca_prox_sets{0, m, branch, 0};
     const D td = static_cast<D>(t), hd = static_cast<D>(hi);
     D* dst = out + j * m64;
     // Entries moved into U hold -inf in s (and W = 0 in wl): the map.
@@ -77,7 +82,8 @@ template <class D, class R>
 __global__ void __launch_bounds__(64 * kEbMaxWaves)
 twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
               int64_t p_all, const int64_t* __restrict__ col_p, R alpha,
-              sdca_thresholds* __restrict__ thr, int stride_elems, int reuse) {
+              sdca_thresholds* __restrict__ thr, int stride_elems, int reuse,
+              sdca_prox_sets* __restrict__ sets) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
@@ -109,6 +115,11 @@ twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_
       thr[2 * j + 1].t = static_cast<double>(tb);
       thr[2 * j + 1].lo = 0;
       thr[2 * j + 1].hi = 1;
+    }
+    // Both blocks free in the reference's record (two_entropy.h:228-230).
+    if (sets && lane == 0) {
+      sets[2 * j] = sdca_prox_sets{0, p, SDCA_BRANCH_SEARCH, 0};
+      sets[2 * j + 1] = sdca_prox_sets{0, m - p, SDCA_BRANCH_SEARCH, 0};
     }
     const D ta_d = static_cast<D>(t), tb_d = static_cast<D>(tb);
     D* dst = out + j * m64;
@@ -147,7 +158,7 @@ hipError_t launch_twoent_t(const ProxLaunch& a) {
   hipLaunchKernelGGL((twoent_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
                      waves * per_wave, a.stream, static_cast<const D*>(a.in),
                      static_cast<D*>(a.out), a.m, a.n, a.p, a.col_p, static_cast<R>(a.alpha),
-                     a.thr, stride, reuse ? 1 : 0);
+                     a.thr, stride, reuse ? 1 : 0, a.sets);
   return hipGetLastError();
 }
 
@@ -164,7 +175,7 @@ hipError_t launch_t(const ProxLaunch& a) {
   hipLaunchKernelGGL((entbias_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
                      waves * per_wave, a.stream, static_cast<const D*>(a.in),
                      static_cast<D*>(a.out), a.m, a.n, static_cast<int>(a.k),
-                     static_cast<R>(a.alpha), a.thr, stride, reuse ? 1 : 0);
+                     static_cast<R>(a.alpha), a.thr, stride, reuse ? 1 : 0, a.sets);
   return hipGetLastError();
 }
 

@@ -48,6 +48,12 @@ struct ColThr {
   R t2, lo2, hi2;  // second block (two-block operator)
   int kind;        // elementwise map of the clamp: 0 identity, 1 exp, 2 W(exp)
   bool slow;       // column deferred to the workgroup-per-column kernel
+  // The record's sets (sdca_prox_sets) and the branch that produced it:
+  // n_hi < 0 leaves them to be counted from the column by the record's cuts
+  // (x > t + hi at hi, x > t + lo free); n_mid2 is block b's free count (its
+  // n_hi is 0).
+  int branch;
+  int n_hi, n_mid, n_mid2;
 };
 
 template <class R>
@@ -57,6 +63,19 @@ __device__ inline ColThr<R> make_thr(R t, R lo, R hi, int kind = 0) {
   r.t2 = t; r.lo2 = lo; r.hi2 = hi;
   r.kind = kind;
   r.slow = false;
+  r.branch = SDCA_BRANCH_SEARCH;
+  r.n_hi = -1;
+  r.n_mid = 0;
+  r.n_mid2 = 0;
+  return r;
+}
+
+// r with its branch and, when n_hi >= 0, its sets.
+template <class R>
+__device__ inline ColThr<R> tag_thr(ColThr<R> r, int branch, int n_hi = -1, int n_mid = 0) {
+  r.branch = branch;
+  r.n_hi = n_hi;
+  r.n_mid = n_mid;
   return r;
 }
 
@@ -94,6 +113,7 @@ struct KnapState {
   R c_lo, c_hi;      // final candidate cuts inside the free interval
   int n_u;           // |U| = number at hi (fixed + final candidates)
   R sum_u;           // sum over U
+  int n_f;           // |F| = number free at the end
 };
 
 // The fixing may start with the n_u0 values above hi_cut0 (sum sum_u0)
@@ -231,6 +251,7 @@ __device__ inline KnapState<R> knapsack_eq_regs(const D (&v)[C], int m, int nval
   }
   st.t = t;
   st.t_acc = have_acc ? t_acc : t;
+  st.n_f = n_f;
   return st;
 }
 
@@ -320,7 +341,7 @@ __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
     group_sums<G>(s_mid, n_hi, n_mid);
     const int n_lo = m - n_hi - n_mid;
     const R s = s_mid + hi * static_cast<R>(n_hi) + lo * static_cast<R>(n_lo);
-    if (!(s > rhs + eps)) return make_thr<R>(R(0), lo, hi);
+    if (!(s > rhs + eps)) return tag_thr(make_thr<R>(R(0), lo, hi), SDCA_BRANCH_INACTIVE, n_hi, n_mid);
   }
   const R total = total_sum<G, C, D, R>(v, nvalid);
   KnapState<R> st = knapsack_eq_regs<G, C, D, R>(v, m, nvalid, total, lo, hi, rhs);
@@ -329,11 +350,14 @@ __device__ inline ColThr<R> knap_family(const D (&v)[C], int m, int nvalid,
     // t >= rho rhs - eps; otherwise the sum constraint is inactive.
     const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
     if (!(st.t >= pp.rho * rhs - eps))
-      return make_thr<R>(knapsack_biased_regs<G, C, D, R>(v, m, total, lo, hi, rhs,
-                                                          R(1) / pp.rho),
-                         lo, hi);
+      return tag_thr(make_thr<R>(knapsack_biased_regs<G, C, D, R>(v, m, total, lo, hi, rhs,
+                                                                  R(1) / pp.rho),
+                                 lo, hi),
+                     SDCA_BRANCH_SCAN);
   }
-  return make_thr<R>(st.t_acc, lo, hi);
+  return tag_thr(make_thr<R>(st.t_acc, lo, hi),
+                 pp.op == OP_KNAPSACK_EQ ? SDCA_BRANCH_SEARCH : SDCA_BRANCH_KNAPSACK, st.n_u,
+                 st.n_f);
 }
 
 // ---------------------------------------------------------------------------
@@ -366,7 +390,7 @@ __device__ inline ColThr<R> cone_search_u0(const D (&v)[C], R K, R largest) {
   const R hi = (R(0) + K * s_p) / den;
   const R max_m = (n_p > 0) ? largest : -num<R>::inf();
   const R tt = hi + t;
-  if (max_m - eps16 <= tt) return make_thr<R>(t, R(0), hi);
+  if (max_m - eps16 <= tt) return tag_thr(make_thr<R>(t, R(0), hi), SDCA_BRANCH_SCAN, 0, n_p);
   return slow_thr<R>();
 }
 
@@ -395,6 +419,7 @@ __device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R 
   const int g = static_cast<int>(threadIdx.x) % G;
   int found_u = k + 1;
   int found_kind = 0;  // 1: accepted, 2: deferred
+  int found_e = 0;     // M = top[u, e)
   R found_t = 0, found_hi = 0;
 #pragma unroll 1
   for (int u = g; u <= k; u += G) {
@@ -415,7 +440,7 @@ __device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R 
     R sum_m = 0, num_m_sum_u = 0;
     R den = k_u * k_u;
     const R k_u_sum_u = k_u * sum_u;
-    int kind = 0;
+    int kind = 0, re = u;
     R rt = 0, rhi = 0;
 #pragma unroll 1
     for (int e = u;; ++e) {  // M = top[u, e)
@@ -424,7 +449,7 @@ __device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R 
       const R tt = hi + t;
       const bool pass = max_m - eps <= tt && tt <= min_u + eps && t <= min_m + eps;
       if (e == m) {
-        if (pass) { kind = 1; rt = t; rhi = hi; }
+        if (pass) { kind = 1; rt = t; rhi = hi; re = e; }
         break;
       }
       if (e >= L) {
@@ -434,7 +459,7 @@ __device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R 
         if (!(den * (t - last) > tol * (den + static_cast<R>(m - L) * nu_rho))) kind = 2;
         break;
       }
-      if (pass && static_cast<R>(top[e]) - eps <= t) { kind = 1; rt = t; rhi = hi; break; }
+      if (pass && static_cast<R>(top[e]) - eps <= t) { kind = 1; rt = t; rhi = hi; re = e; break; }
       min_m = static_cast<R>(top[e]);
       max_m = static_cast<R>(top[u]);
       sum_m += min_m;
@@ -446,15 +471,18 @@ __device__ inline ColThr<R> cone_biased_regs(const D (&top)[L], int m, int k, R 
       found_kind = kind;
       found_t = rt;
       found_hi = rhi;
+      found_e = re;
       break;
     }
   }
   const int u_min = group_min<G>(found_u);
-  if (u_min > k) return make_thr<R>(R(0), R(0), R(0));  // the reference's default
+  if (u_min > k)  // the reference's default
+    return tag_thr(make_thr<R>(R(0), R(0), R(0)), SDCA_BRANCH_DEFAULT, 0, 0);
   const int src = (static_cast<int>(threadIdx.x) & 63) - g + u_min % G;
   const int kind = __shfl(found_kind, src, 64);
   if (kind == 2) return slow_thr<R>();
-  return make_thr<R>(__shfl(found_t, src, 64), R(0), __shfl(found_hi, src, 64));
+  return tag_thr(make_thr<R>(__shfl(found_t, src, 64), R(0), __shfl(found_hi, src, 64)),
+                 SDCA_BRANCH_SCAN, u_min, __shfl(found_e, src, 64) - u_min);
 }
 
 // Candidate slots per lane for the top-k simplex's knapsack: the group holds
@@ -665,6 +693,7 @@ __device__ inline bool topk_sorted_root(const D* lds_col, int total, const D (&t
     st.sum_u = su;
     st.c_hi = au;
     st.c_lo = ae;
+    st.n_f = e - u;
     return usable;
   }
   // M empty: the k largest at hi, the rest (a_k = the largest of them) at 0.
@@ -683,6 +712,7 @@ __device__ inline bool topk_sorted_root(const D* lds_col, int total, const D (&t
     st.sum_u = sk;
     st.c_hi = ak;
     st.c_lo = ak;
+    st.n_f = 0;
     return usable;
   }
   return false;
@@ -842,23 +872,24 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
   // topk_cone_special_cases (topk_cone.h:18-55), whose divisor is k, or
   // k + rho k^2 for the biased simplex (topk_simplex_biased.h:50-51).
   const bool biased = pp.op == OP_TOPK_SIMPLEX_BIASED || pp.op == OP_TOPK_CONE_BIASED;
-  if (sum_k <= eps16) return make_thr<R>(R(0), R(0), R(0));
+  if (sum_k <= eps16) return tag_thr(make_thr<R>(R(0), R(0), R(0)), SDCA_BRANCH_ZERO, 0, 0);
   const R hi_c = sum_k / (biased ? K + pp.rho * K * K : K);
   const R t_c = kth - hi_c;
   const bool constant = (k == m) || (t_c >= next - eps16);
   if (pp.op == OP_TOPK_CONE) {
-    if (constant) return make_thr<R>(t_c, R(0), hi_c);
+    if (constant) return tag_thr(make_thr<R>(t_c, R(0), hi_c), SDCA_BRANCH_CONSTANT, k, 0);
     return cone_search_u0<G, C, D, R>(v, K, largest);
   }
   if (pp.op == OP_TOPK_CONE_BIASED) {  // thresholds_topk_cone_biased (topk_cone_biased.h:98-113)
-    if (constant) return make_thr<R>(t_c, R(0), hi_c);
+    if (constant) return tag_thr(make_thr<R>(t_c, R(0), hi_c), SDCA_BRANCH_CONSTANT, k, 0);
     return cone_biased_regs<G, L, D, R>(top, m, k, pp.rho);
   }
   // thresholds_topk_simplex (topk_simplex.h:39-68) and
   // thresholds_topk_simplex_biased (topk_simplex_biased.h:40-71)
   const R rhs = pp.rhs;
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
-  if (constant && !(K * hi_c > rhs + eps)) return make_thr<R>(t_c, R(0), hi_c);
+  if (constant && !(K * hi_c > rhs + eps))
+    return tag_thr(make_thr<R>(t_c, R(0), hi_c), SDCA_BRANCH_CONSTANT, k, 0);
   const R hi = pp.rhs_k;  // rhs / K (topk_simplex.h:56)
   // More than G * kCandSlots candidates is rare for the prox inputs: the LDS
   // working copy keeps the kernel's register peak at the candidate path's.
@@ -889,7 +920,7 @@ __device__ inline ColThr<R> topk_family(const D (&v)[C], int m, int nvalid,
       if (lt) return cone_search_u0<G, C, D, R>(v, K, largest);
     }
   }
-  return make_thr<R>(st.t_acc, R(0), hi);
+  return tag_thr(make_thr<R>(st.t_acc, R(0), hi), SDCA_BRANCH_KNAPSACK, st.n_u, st.n_f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1247,7 +1278,7 @@ __device__ __forceinline__ ColThr<R> ent_family(const D* x, int m, int nvalid,
     }
   }
   if constexpr (!NORM) scale = dexp(mx0 - t);
-  return make_thr<R>(t, R(0), hi, NORM ? 2 : 1);
+  return tag_thr(make_thr<R>(t, R(0), hi, NORM ? 2 : 1), SDCA_BRANCH_SEARCH, nfixed, m - nfixed);
 }
 
 // ---------------------------------------------------------------------------
@@ -1274,7 +1305,6 @@ template <int G, int C, class D, class R>
 __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
                                            const ProxParamsT<R>& pp, int* n_u_out = nullptr,
                                            R* sum_u_out = nullptr) {
-  (void)m;
   const int k = pp.k;
   const R eps = R(16) * num<R>::eps();
   const R K = static_cast<R>(k);
@@ -1291,7 +1321,8 @@ __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
   R log_z_1 = isfinite(l1) ? mx + dlog1p(z + l1) : R(0);
   if (n_u_out) *n_u_out = 0;
   if (sum_u_out) *sum_u_out = R(0);
-  if (k <= 1 || mx - eps <= log_z - dlog(K)) return make_thr<R>(log_z_1, R(0), R(1), 1);
+  if (k <= 1 || mx - eps <= log_z - dlog(K))
+    return tag_thr(make_thr<R>(log_z_1, R(0), R(1), 1), SDCA_BRANCH_U_EMPTY, 0, m);
   R sum_u = 0, k_u = K;
   int n_u = 0;
   for (int num_u = 1; num_u < k; ++num_u) {
@@ -1323,7 +1354,7 @@ __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
     t = mx + dlog1p(z + a) - dlog(k_u / K);
     hi = (R(1) + z) / ((R(1) + z + a) * K);
   }
-  return make_thr<R>(t, R(0), hi, 1);
+  return tag_thr(make_thr<R>(t, R(0), hi, 1), SDCA_BRANCH_U_GROWN, n_u, m - n_u);
 }
 
 // ---------------------------------------------------------------------------
@@ -1401,8 +1432,9 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
   R t = res[0];
   const R s = res[1];
   if (t + s >= -eps) {
-    ColThr<R> r = make_thr<R>(t, R(0), rhs);
+    ColThr<R> r = tag_thr(make_thr<R>(t, R(0), rhs), SDCA_BRANCH_SEARCH, 0, cnt[0]);
     r.t2 = s;
+    r.n_mid2 = cnt[1];
     return r;
   }
   // two_simplex_sort (two_simplex_sort.h:15-111) solves the same problem by a
@@ -1411,8 +1443,10 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
   // the sum rhs instead.  Such columns (and those within a margin of it)
   // are deferred to the sort-and-scan kernel.
   const bool sort_op = pp.op == OP_TWO_SIMPLEX_SORT;
-  // Phase 2: joint variable fixing with s = -t.
+  // Phase 2: joint variable fixing with s = -t; ca, cb: the blocks' kept
+  // counts.
   int mc = cnt[0] + cnt[1];
+  int ca = cnt[0], cb = cnt[1];
   {
     R sa = 0, sb = 0;
 #pragma unroll
@@ -1444,11 +1478,15 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
       cuts[1] = dmax(cuts[1], mt);
       next = static_cast<R>(mc) * t + sum_y;
       mc -= n_y;
+      cb -= n_y;
     } else if (n_x > 0 && infeas < -eps) {
       cuts[0] = dmax(cuts[0], t);
       next = static_cast<R>(mc) * t - sum_x;
       mc -= n_x;
+      ca -= n_x;
     } else {
+      ca -= n_x;  // two_simplex.h:100-103: both blocks keep {x > t}, {y > -t}
+      cb -= n_y;
       break;
     }
     if (mc > 0) {
@@ -1461,8 +1499,9 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
     const R margin = R(1e-3) * dmax(R(1), fabs(t));
     if (maxs[0] - t <= margin || maxs[1] + t <= margin) return slow_thr<R>();
   }
-  ColThr<R> r = make_thr<R>(t, R(0), rhs);
+  ColThr<R> r = tag_thr(make_thr<R>(t, R(0), rhs), SDCA_BRANCH_BELOW_RHS, 0, ca);
   r.t2 = -t;
+  r.n_mid2 = cb;
   return r;
 }
 
@@ -1598,7 +1637,8 @@ __device__ __forceinline__ void columns_tile(unsigned char* smem_raw, int m, int
                                              int ncols, const ProxParamsT<R>& pp,
                                              const int64_t* __restrict__ col_p,
                                              sdca_thresholds* __restrict__ thr,
-                                             int* __restrict__ slow) {
+                                             int* __restrict__ slow,
+                                             sdca_prox_sets* __restrict__ sets) {
   D* tile = reinterpret_cast<D*>(smem_raw);
   constexpr int B = BT / G;
   const int lc = static_cast<int>(threadIdx.x) / G;
@@ -1744,7 +1784,35 @@ __device__ __forceinline__ void columns_tile(unsigned char* smem_raw, int m, int
     } else {
       write_slots([&](int c) { return clamp_med3(v[c] - t1, lo1, he1); });
     }
+    // The record's sets: from the search where it knows them, else counted
+    // by the record's cuts over the slots (the input values).
+    int set_hi = th.n_hi, set_mid = th.n_mid;
+    if constexpr (FAM == FAM_KNAP || FAM == FAM_TOPK) {
+      if (sets && !th.slow && set_hi < 0) {
+        const R chi = th.t + th.hi, clo = th.t + th.lo;
+        int nh = 0, nm = 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const R x = static_cast<R>(v[c]);
+          const bool ok = FULL || c < nvalid;
+          const bool h = ok && x > chi;
+          nh += h ? 1 : 0;
+          nm += (ok && !h && x > clo) ? 1 : 0;
+        }
+        group_sums<G>(nh, nm);
+        set_hi = nh;
+        set_mid = nm;
+      }
+    }
     if (g == 0) {
+      if (sets && !th.slow) {
+        if (FAM == FAM_TWO) {
+          sets[2 * j] = sdca_prox_sets{0, th.n_mid, th.branch, 0};
+          sets[2 * j + 1] = sdca_prox_sets{0, th.n_mid2, th.branch, 0};
+        } else {
+          sets[j] = sdca_prox_sets{set_hi, set_mid, th.branch, 0};
+        }
+      }
       if (th.slow) {
         const int pos = atomicAdd(slow, 1);
         slow[2 + pos] = static_cast<int>(j);
@@ -1772,7 +1840,8 @@ template <int FAM, int KM, class D, class R, int G, int C, int BT, bool FULL>
 __global__ void __launch_bounds__(BT)
 prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
                     int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
-                    sdca_thresholds* __restrict__ thr, int* __restrict__ slow) {
+                    sdca_thresholds* __restrict__ thr, int* __restrict__ slow,
+                    sdca_prox_sets* __restrict__ sets) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* tile = reinterpret_cast<D*>(smem_raw);
   constexpr int B = BT / G;
@@ -1784,7 +1853,8 @@ prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
   const int64_t count = static_cast<int64_t>(ncols) * m;
   tile_load<NV, BT>(tile, in + col0 * m, count);
   __syncthreads();
-  columns_tile<FAM, KM, D, R, G, C, BT, FULL>(smem_raw, m, col0, ncols, pp, col_p, thr, slow);
+  columns_tile<FAM, KM, D, R, G, C, BT, FULL>(smem_raw, m, col0, ncols, pp, col_p, thr, slow,
+                                              sets);
   __syncthreads();
   tile_store<NV, BT>(out + col0 * m, tile, count);
 }

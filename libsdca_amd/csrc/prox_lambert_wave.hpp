@@ -321,7 +321,8 @@ __device__ inline double lambert_w_exp_small(double x) {
 // floats, which takes several more passes and lands within that level too).
 template <class D, class R, int NT = 64, bool NOISE_STOP = false>
 __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_out,
-                                   R& hi_out, R* wl = nullptr, R* tw = nullptr) {
+                                   R& hi_out, R* wl = nullptr, R* tw = nullptr,
+                                   int* branch = nullptr) {
   const R eps_r = num<R>::eps();
   const R tiny = R(64) * num<R>::min_normal();
   D mx_d;
@@ -449,6 +450,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
   }
   const R K = static_cast<R>(k);
   t_out = t;
+  if (branch) *branch = SDCA_BRANCH_U_EMPTY;
   if (k == 1) {
     hi_out = sv;
     return;
@@ -459,6 +461,7 @@ __device__ void entbias_thresholds(D* s, int m, int lane, int k, R alpha, R& t_o
     hi_out = sv / K;
     return;
   }
+  if (branch) *branch = SDCA_BRANCH_U_GROWN;
 
   // U not empty (topk_entropy_biased.h:224-266).
   if (lane == 0) s[mx_i] = -num<D>::inf();

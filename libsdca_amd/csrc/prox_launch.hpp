@@ -57,6 +57,7 @@ struct ProxLaunch {
   int64_t k, p;
   const int64_t* col_p;     // device, or NULL
   sdca_thresholds* thr;     // device, or NULL
+  sdca_prox_sets* sets;     // device, or NULL (one per threshold record)
   int* slow;                // device: [0] = count, [1..n] = column list
   hipStream_t stream;
 };
@@ -93,7 +94,7 @@ hipError_t launch_clear(int* p, int count, hipStream_t stream);
 int prox_entry(int op, int data, int result, int64_t m, int64_t n, const void* in, void* out,
                const sdca_prox_params* params, const int64_t* col_p,
                sdca_thresholds* thresholds, unsigned flags, void* stream, int* fixed_list,
-               int64_t fixed_list_ints);
+               int64_t fixed_list_ints, sdca_prox_sets* sets = nullptr);
 // Records a failure message for sdca_last_error() on this thread; returns code.
 int set_error(int code, const char* message);
 

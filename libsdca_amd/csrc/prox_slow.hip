@@ -27,7 +27,8 @@ template <class D, class R>
 __global__ void __launch_bounds__(256)
 prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
                  ProxParamsT<R> pp, sdca_thresholds* __restrict__ thr,
-                 int* __restrict__ slow, int all_columns, int pow2) {
+                 int* __restrict__ slow, int all_columns, int pow2,
+                 sdca_prox_sets* __restrict__ sets) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* s = reinterpret_cast<D*>(smem_raw);
   __shared__ R sh_t, sh_lo, sh_hi;
@@ -60,7 +61,9 @@ prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int
     // alike, the U/M searches split over its lanes.
     if (threadIdx.x < 64) {
       R t, lo, hi;
-      thresholds_sorted<D, R>(s, m, pp.op, pp.lo, pp.hi, pp.rhs, pp.rho, pp.k, t, lo, hi);
+      int branch, n_hi, n_mid;
+      thresholds_sorted<D, R>(s, m, pp.op, pp.lo, pp.hi, pp.rhs, pp.rho, pp.k, t, lo, hi,
+                              branch, n_hi, n_mid);
       if (threadIdx.x == 0) {
         sh_t = t;
         sh_lo = lo;
@@ -70,6 +73,7 @@ prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int
           thr[j].lo = static_cast<double>(lo);
           thr[j].hi = static_cast<double>(hi);
         }
+        if (sets) sets[j] = sdca_prox_sets{n_hi, n_mid, branch, 0};
       }
     }
     __syncthreads();
@@ -122,7 +126,7 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   hipLaunchKernelGGL((prox_slow_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
                      dim3(threads), static_cast<size_t>(pow2) * sizeof(D), a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
-                     a.thr, a.slow, all_columns ? 1 : 0, pow2);
+                     a.thr, a.slow, all_columns ? 1 : 0, pow2, a.sets);
   return hipGetLastError();
 }
 
@@ -130,9 +134,11 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
 // blocks a[0, p), b[0, q): the common sum c is scanned over the breakpoints
 // where the active counts r, s grow; past the end of a block the reference
 // uses the pseudo point last - rhs.
+// Also returns the active counts r, s (the records' free sets) and the
+// branch: SDCA_BRANCH_BELOW_RHS when the optimum falls inside the scan.
 template <class D, class R>
 __device__ void two_sort_thresholds(const D* a, int p, const D* b, int q, R rhs, R& theta_a,
-                                    R& theta_b) {
+                                    R& theta_b, int& r_out, int& s_out, int& branch) {
   const R eps = num<R>::eps() * dmax(R(1), rhs);
   const R C = rhs;
   R c = 0, best_c = rhs;
@@ -141,6 +147,7 @@ __device__ void two_sort_thresholds(const D* a, int p, const D* b, int q, R rhs,
   auto a_at = [&](int i) { return i < p ? static_cast<R>(a[i]) : static_cast<R>(a[p - 1]) - C; };
   auto b_at = [&](int i) { return i < q ? static_cast<R>(b[i]) : static_cast<R>(b[q - 1]) - C; };
   R a_r = a_at(r), b_s = b_at(s);
+  branch = SDCA_BRANCH_SEARCH;
   while (c < C) {
     const R copt = (static_cast<R>(s) * sum_mu + static_cast<R>(r) * sum_nu) / static_cast<R>(r + s);
     const R next_cr = (sum_mu + a_r) - static_cast<R>(r + 1) * a_r;
@@ -148,6 +155,7 @@ __device__ void two_sort_thresholds(const D* a, int p, const D* b, int q, R rhs,
     const R next_c = dmin(dmin(next_cr, next_cs), C);
     if (c <= copt && copt < next_c) {
       best_c = copt;
+      branch = SDCA_BRANCH_BELOW_RHS;
       break;
     }
     if (next_c >= C - eps) {
@@ -167,6 +175,8 @@ __device__ void two_sort_thresholds(const D* a, int p, const D* b, int q, R rhs,
   }
   theta_a = (sum_mu - best_c) / static_cast<R>(r);
   theta_b = (sum_nu - best_c) / static_cast<R>(s);
+  r_out = r;
+  s_out = s;
 }
 
 // Two-block simplex by sort and scan: one workgroup per column, the column
@@ -176,7 +186,8 @@ template <class D, class R>
 __global__ void __launch_bounds__(256)
 two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, R rhs,
                 int64_t p_all, const int64_t* __restrict__ col_p,
-                sdca_thresholds* __restrict__ thr, int* __restrict__ slow, int all_columns) {
+                sdca_thresholds* __restrict__ thr, int* __restrict__ slow, int all_columns,
+                sdca_prox_sets* __restrict__ sets) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   D* sa = reinterpret_cast<D*>(smem_raw);
   __shared__ R sh_ta, sh_tb;
@@ -194,7 +205,12 @@ two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int6
     sort_desc_unpadded(sb, q);
     if (threadIdx.x == 0) {
       R ta, tb;
-      two_sort_thresholds<D, R>(sa, p, sb, q, rhs, ta, tb);
+      int ra, rb, branch;
+      two_sort_thresholds<D, R>(sa, p, sb, q, rhs, ta, tb, ra, rb, branch);
+      if (sets) {
+        sets[2 * j] = sdca_prox_sets{0, ra, branch, 0};
+        sets[2 * j + 1] = sdca_prox_sets{0, rb, branch, 0};
+      }
       sh_ta = ta;
       sh_tb = tb;
       if (thr) {
@@ -236,7 +252,8 @@ hipError_t launch_two_sort_t(const ProxLaunch& a, bool all_columns) {
   hipLaunchKernelGGL((two_sort_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
                      dim3(256), static_cast<size_t>(a.m) * sizeof(D), a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n,
-                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, a.slow, all_columns ? 1 : 0);
+                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, a.slow, all_columns ? 1 : 0,
+                     a.sets);
   return hipGetLastError();
 }
 

@@ -80,6 +80,7 @@ __device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
                         static_cast<R>(m - l) * lo - rhs) / static_cast<R>(l - f)
                      : t;
   st.n_u = f;
+  st.n_f = l - f;
   st.sum_u = sum_range<R>(s, 0, f);
   return st;
 }
@@ -89,13 +90,16 @@ __device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
 // lane l scans |U| = l, l + 64, ... (each setting up its U by the
 // reference's own sequence of updates, so every trial value is the
 // reference's), and the smallest accepting |U| of the wave is the answer.
-// Returns its (t, hi) in every lane; found = false gives the default.
+// Returns its (t, hi) and the end e of its M = [u, e) in every lane, u in
+// u_found; found = false gives the default.
 template <class R>
-__device__ inline bool wave_first_accept(int u_found, R& t, R& hi) {
+__device__ inline bool wave_first_accept(int& u_found, R& t, R& hi, int& e) {
   const int best = group_min<64>(u_found);
   if (best == INT_MAX) return false;
   t = __shfl(t, best & 63, 64);
   hi = __shfl(hi, best & 63, 64);
+  e = __shfl(e, best & 63, 64);
+  u_found = best;
   return true;
 }
 
@@ -104,9 +108,10 @@ __device__ inline bool wave_first_accept(int u_found, R& t, R& hi) {
 // column: the latter starts the |U| + rho k^2 term at rho k^2 (rho = 0 gives
 // the former's steps exactly).
 template <class D, class R>
-__device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R& hi_out) {
+__device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R& hi_out,
+                                   int& branch, int& n_hi, int& n_mid) {
   const R eps = R(16) * num<R>::eps();
-  int found = INT_MAX;
+  int found = INT_MAX, fe = 0;
   R ft = 0, fh = 0;
   for (int mf = static_cast<int>(threadIdx.x) & 63; mf <= k && found == INT_MAX; mf += 64) {
     R k_u = static_cast<R>(k);
@@ -130,6 +135,7 @@ __device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R&
       if (max_m - eps <= tt && tt <= min_u + eps) {
         if (t <= min_m + eps && (ml == m || static_cast<R>(s[ml]) - eps <= t)) {
           found = mf;
+          fe = ml;
           ft = t;
           fh = hi;
           break;
@@ -144,7 +150,15 @@ __device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R&
       ++ml;
     }
   }
-  if (!wave_first_accept(found, ft, fh)) ft = fh = 0;
+  if (wave_first_accept(found, ft, fh, fe)) {
+    branch = SDCA_BRANCH_SCAN;
+    n_hi = found;
+    n_mid = fe - found;
+  } else {
+    ft = fh = 0;
+    branch = SDCA_BRANCH_DEFAULT;
+    n_hi = n_mid = 0;
+  }
   t_out = ft;
   hi_out = fh;
 }
@@ -154,12 +168,13 @@ __device__ void cone_search_sorted(const D* s, int m, int k, R rho, R& t_out, R&
 // satisfies the reference's interval tests; default 0.
 template <class D, class R>
 __device__ void knapsack_le_biased_sorted(const D* s, int m, R lo, R hi, R rhs, R rho,
-                                          R& t_out, R& lo_out, R& hi_out) {
+                                          R& t_out, R& lo_out, R& hi_out, int& branch,
+                                          int& n_hi, int& n_mid) {
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
   const R rho_rhs = rho * rhs;
   const R rho_inv = R(1) / rho;
   const R num_x = static_cast<R>(m);
-  int found = INT_MAX;
+  int found = INT_MAX, fe = 0;
   R ft = 0, unused = 0;
   for (int mf = static_cast<int>(threadIdx.x) & 63; mf <= m && found == INT_MAX; mf += 64) {
     // |U| = mf: the reference reaches it with num_u counted up by ones and
@@ -178,6 +193,7 @@ __device__ void knapsack_le_biased_sorted(const D* s, int m, R lo, R hi, R rhs, 
           tt = lo + t;
           if (tt <= min_m + eps && (ml == m || static_cast<R>(s[ml]) - eps <= tt)) {
             found = mf;
+            fe = ml;
             ft = t;
             break;
           }
@@ -192,20 +208,29 @@ __device__ void knapsack_le_biased_sorted(const D* s, int m, R lo, R hi, R rhs, 
       ++ml;
     }
   }
-  if (wave_first_accept(found, ft, unused)) {
+  if (wave_first_accept(found, ft, unused, fe)) {
     t_out = ft;
     lo_out = lo;
     hi_out = hi;
+    branch = SDCA_BRANCH_SCAN;
+    n_hi = found;
+    n_mid = fe - found;
   } else {
     t_out = 0;
     lo_out = 0;
     hi_out = 0;
+    branch = SDCA_BRANCH_DEFAULT;
+    n_hi = n_mid = 0;
   }
 }
 
+// The record of the column's threshold function, with its branch
+// (sdca_prox_branch) and sets: n_hi, n_mid are positions in the sorted
+// column.
 template <class D, class R>
 __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, R rho, int k,
-                                  R& t_out, R& lo_out, R& hi_out) {
+                                  R& t_out, R& lo_out, R& hi_out, int& branch, int& n_hi,
+                                  int& n_mid) {
   if (op == OP_KNAPSACK_LE_BIASED && rho != R(0)) {
     // knapsack_le_biased.h:102-130: the equality solution if its t is at
     // least rho rhs, else the search.
@@ -215,9 +240,13 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
     const KnapState<R> st = knapsack_sorted<D, R>(s, m, lo, hi, rhs);
     if (st.t >= rho * rhs - eps) {
       t_out = st.t_acc;
+      branch = SDCA_BRANCH_KNAPSACK;
+      n_hi = st.n_u;
+      n_mid = st.n_f;
       return;
     }
-    knapsack_le_biased_sorted<D, R>(s, m, lo, hi, rhs, rho, t_out, lo_out, hi_out);
+    knapsack_le_biased_sorted<D, R>(s, m, lo, hi, rhs, rho, t_out, lo_out, hi_out, branch, n_hi,
+                                    n_mid);
     return;
   }
   if (op == OP_KNAPSACK_EQ || op == OP_KNAPSACK_LE || op == OP_KNAPSACK_LE_BIASED) {
@@ -226,18 +255,25 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
     if (op != OP_KNAPSACK_EQ) {  // knapsack_le, and knapsack_le_biased with rho = 0
       // knapsack_le.h:30-46 on the sorted column
       const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
-      int n_hi = 0;
-      while (n_hi < m && static_cast<R>(s[n_hi]) >= hi) ++n_hi;
-      int e_mid = n_hi;
+      int e_hi = 0;
+      while (e_hi < m && static_cast<R>(s[e_hi]) >= hi) ++e_hi;
+      int e_mid = e_hi;
       while (e_mid < m && static_cast<R>(s[e_mid]) > lo) ++e_mid;
-      const R sum = sum_range<R>(s, n_hi, e_mid) + hi * static_cast<R>(n_hi)
+      const R sum = sum_range<R>(s, e_hi, e_mid) + hi * static_cast<R>(e_hi)
                   + lo * static_cast<R>(m - e_mid);
       if (!(sum > rhs + eps)) {
         t_out = 0;
+        branch = SDCA_BRANCH_INACTIVE;
+        n_hi = e_hi;
+        n_mid = e_mid - e_hi;
         return;
       }
     }
-    t_out = knapsack_sorted<D, R>(s, m, lo, hi, rhs).t_acc;
+    const KnapState<R> st = knapsack_sorted<D, R>(s, m, lo, hi, rhs);
+    t_out = st.t_acc;
+    branch = op == OP_KNAPSACK_EQ ? SDCA_BRANCH_SEARCH : SDCA_BRANCH_KNAPSACK;
+    n_hi = st.n_u;
+    n_mid = st.n_f;
     return;
   }
   const R K = static_cast<R>(k);
@@ -245,6 +281,8 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
   const R sum_k = sum_range<R>(s, 0, k);
   if (sum_k <= eps16) {
     t_out = 0; lo_out = 0; hi_out = 0;
+    branch = SDCA_BRANCH_ZERO;
+    n_hi = n_mid = 0;
     return;
   }
   // topk_cone_special_cases with divisor K (+ rho K^2 for the biased forms,
@@ -257,8 +295,11 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
     if (constant) {
       t_out = t_c;
       hi_out = hi_c;
+      branch = SDCA_BRANCH_CONSTANT;
+      n_hi = k;
+      n_mid = 0;
     } else {
-      cone_search_sorted<D, R>(s, m, k, rho, t_out, hi_out);
+      cone_search_sorted<D, R>(s, m, k, rho, t_out, hi_out, branch, n_hi, n_mid);
     }
     return;
   }
@@ -266,6 +307,9 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
   if (constant && !(K * hi_c > rhs + eps)) {
     t_out = t_c;
     hi_out = hi_c;
+    branch = SDCA_BRANCH_CONSTANT;
+    n_hi = k;
+    n_mid = 0;
     return;
   }
   KnapState<R> st = knapsack_sorted<D, R>(s, m, R(0), rhs / K, rhs);
@@ -280,12 +324,15 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
       lt = K * (st.sum_u + (K - num_u) * st.t) < rhs * (num_u + rho * K * K) - eps;
     }
     if (lt) {
-      cone_search_sorted<D, R>(s, m, k, rho, t_out, hi_out);
+      cone_search_sorted<D, R>(s, m, k, rho, t_out, hi_out, branch, n_hi, n_mid);
       return;
     }
   }
   t_out = st.t_acc;
   hi_out = rhs / K;
+  branch = SDCA_BRANCH_KNAPSACK;
+  n_hi = st.n_u;
+  n_mid = st.n_f;
 }
 
 // Descending sort of s[0, len) by the whole workgroup, without padding:

@@ -33,9 +33,11 @@ struct Column {
 
 // Kiwiel's variable fixing (knapsack_eq.h:25-109) over the column's values
 // in (w_lo, w_hi]; returns the threshold applied, recomputed from the final
-// free set (the register kernels' t_acc).
+// free set (the register kernels' t_acc), and the final counts at hi and
+// free in n_u_out, n_f_out.
 template <class D, class R>
-__device__ R stream_knapsack_eq(const Column<D, R>& col, R lo, R hi, R rhs) {
+__device__ R stream_knapsack_eq(const Column<D, R>& col, R lo, R hi, R rhs, int64_t& n_u_out,
+                                int64_t& n_f_out) {
   constexpr int G = kStreamThreads;
   const int tid = static_cast<int>(threadIdx.x);
   const int64_t m = col.m;
@@ -67,6 +69,8 @@ __device__ R stream_knapsack_eq(const Column<D, R>& col, R lo, R hi, R rhs) {
     if (!fix_hi && !fix_lo) {
       n_u += n_hi;
       const int64_t n_f = mc - n_lo - n_hi;
+      n_u_out = n_u;
+      n_f_out = n_f;
       if (n_f <= 0) return t;
       R s_f = 0;
       for (int64_t i = tid; i < m; i += G) {
@@ -92,6 +96,8 @@ __device__ R stream_knapsack_eq(const Column<D, R>& col, R lo, R hi, R rhs) {
     if (mc <= 0) break;
     t = div_near(next, static_cast<R>(mc));
   }
+  n_u_out = n_u;
+  n_f_out = 0;
   return t;
 }
 
@@ -299,7 +305,8 @@ __device__ R stream_solve_sum_w_exp(const Column<D, R>& col, R w_hi, int64_t cou
 template <int OPK, class D, class R>
 __global__ void __launch_bounds__(kStreamThreads)
 stream_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m, int64_t n,
-              ProxParamsT<R> pp, sdca_thresholds* __restrict__ thr) {
+              ProxParamsT<R> pp, sdca_thresholds* __restrict__ thr,
+              sdca_prox_sets* __restrict__ sets) {
   constexpr int G = kStreamThreads;
   const int tid = static_cast<int>(threadIdx.x);
   for (int64_t j = blockIdx.x; j < n; j += gridDim.x) {
@@ -307,6 +314,8 @@ stream_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m, int64_t 
     D* const y = out + j * m;
     R t = 0, lo = pp.lo, hi = pp.hi;
     bool series = false;
+    int64_t set_hi = 0, set_mid = 0;
+    int branch = SDCA_BRANCH_SEARCH;
     if constexpr (OPK == SK_KNAP_EQ || OPK == SK_KNAP_LE) {
       bool active = true;
       if constexpr (OPK == SK_KNAP_LE) {
@@ -324,8 +333,11 @@ stream_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m, int64_t 
         const int64_t n_lo = m - n_hi - n_mid;
         const R s = s_mid + hi * static_cast<R>(n_hi) + lo * static_cast<R>(n_lo);
         active = s > pp.rhs + eps;
+        branch = active ? SDCA_BRANCH_KNAPSACK : SDCA_BRANCH_INACTIVE;
+        set_hi = n_hi;
+        set_mid = n_mid;
       }
-      if (active) t = stream_knapsack_eq(col, lo, hi, pp.rhs);
+      if (active) t = stream_knapsack_eq(col, lo, hi, pp.rhs, set_hi, set_mid);
     } else {
       // entropy.h:30-49, entropy_norm.h:157-178
       constexpr bool NORM = OPK == SK_ENT_NORM;
@@ -367,6 +379,8 @@ stream_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m, int64_t 
           break;
         }
       }
+      set_hi = nfixed;
+      set_mid = m - nfixed;
     }
     // The clamp / map pass (proxdef.h:164-196), t, lo, hi cast to Data.
     const D td = static_cast<D>(t), lod = static_cast<D>(lo), hid = static_cast<D>(hi);
@@ -398,6 +412,7 @@ stream_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m, int64_t 
       thr[j].lo = static_cast<double>(lo);
       thr[j].hi = static_cast<double>(hi);
     }
+    if (sets && tid == 0) sets[j] = sdca_prox_sets{set_hi, set_mid, branch, 0};
     __syncthreads();  // the next column's sweeps reuse the reduction scratch
   }
 }
@@ -415,7 +430,7 @@ hipError_t launch_t(const ProxLaunch& a) {
   const int64_t grid = a.n < 8192 ? a.n : 8192;
   hipLaunchKernelGGL((stream_kernel<OPK, D, R>), dim3(static_cast<unsigned>(grid)),
                      dim3(kStreamThreads), 0, a.stream, static_cast<const D*>(a.in),
-                     static_cast<D*>(a.out), a.m, a.n, pp, a.thr);
+                     static_cast<D*>(a.out), a.m, a.n, pp, a.thr, a.sets);
   return hipGetLastError();
 }
 

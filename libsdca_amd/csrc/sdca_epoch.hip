@@ -509,7 +509,9 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
           sort_desc_unpadded(cb, mp);
           if (tid < 64) {
             R t, lo, hi;
-            thresholds_sorted<D, R>(cb, mp, op, R(0), knap_hi, c, rho, ob.k, t, lo, hi);
+            int branch, n_hi, n_mid;  // (not used by the epoch)
+            thresholds_sorted<D, R>(cb, mp, op, R(0), knap_hi, c, rho, ob.k, t, lo, hi, branch,
+                                    n_hi, n_mid);
             if (lane == 0) {
               sh_t = t;
               sh_lo = lo;

@@ -32,6 +32,10 @@ OBJECTIVES = {
 }
 
 
+# sdca_prox_sets (include/sdca_hip.h)
+SETS_DTYPE = np.dtype([("n_hi", "<i8"), ("n_mid", "<i8"), ("branch", "<i4"), ("reserved", "<i4")])
+
+
 class ProxParams(ctypes.Structure):
     _fields_ = [("lo", ctypes.c_double), ("hi", ctypes.c_double),
                 ("rhs", ctypes.c_double), ("rho", ctypes.c_double),
@@ -144,6 +148,33 @@ class Library:
         if rc != 0:
             raise RuntimeError(f"{self.prefix}_prox failed: {rc}")
         return thr
+
+    def prox_sets(self, op, x, result=None, params=None, col_p=None, nthreads=1):
+        """prox with each record's thresholds and sets: returns (thr, sets),
+        thr (records, 3) = (t, lo, hi), sets (records, 3) int64 = (n_hi,
+        n_mid, branch): first - begin and last - first of the threshold
+        function's record (proxdef.h:29-67), and the return that produced it
+        (-1 from the reference, which does not record it)."""
+        assert x.flags.c_contiguous
+        n, m = x.shape
+        data = _dt(x)
+        result = data if result is None else result
+        params = params or make_params()
+        cnt = 2 * n if op in ("two_simplex", "two_simplex_sort", "two_entropy") else n
+        thr = np.zeros((cnt, 3), dtype=np.float64)
+        raw = np.zeros(cnt, dtype=SETS_DTYPE)
+        cp = None if col_p is None else np.ascontiguousarray(col_p, dtype=np.int64)
+        f = getattr(self.lib, f"{self.prefix}_prox_sets")
+        f.restype = ctypes.c_int
+        rc = f(ctypes.c_int(OPS[op]), ctypes.c_int(data), ctypes.c_int(result), ctypes.c_int64(m),
+               ctypes.c_int64(n), ctypes.c_void_p(x.ctypes.data), ctypes.byref(params),
+               ctypes.c_void_p(cp.ctypes.data if cp is not None else None),
+               ctypes.c_void_p(thr.ctypes.data), ctypes.c_void_p(raw.ctypes.data),
+               ctypes.c_int(nthreads))
+        if rc != 0:
+            raise RuntimeError(f"{self.prefix}_prox_sets failed: {rc}")
+        sets = np.stack([raw["n_hi"], raw["n_mid"], raw["branch"].astype(np.int64)], axis=1)
+        return thr, sets
 
     def eval_scores(self, objs, S, A, labels, offsets=None, preg=0.0, dreg=0.0,
                     result=None, per_example=False, nthreads=1):

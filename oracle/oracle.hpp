@@ -41,15 +41,29 @@ namespace orc {
 // Threshold record (proxdef.h:29-67).  Over the permuted scratch copy,
 // [begin, first) is fixed at hi, [first, last) is free and [last, end) is
 // fixed at lo.  `kind` selects the elementwise map of the clamp pass
-// (proxdef.h:164-196): 0 = identity, 1 = exp, 2 = lambert_w_exp.
+// (proxdef.h:164-196): 0 = identity, 1 = exp, 2 = lambert_w_exp.  `branch`
+// names the return of the reference's threshold function that produced the
+// record (an sdca_prox_branch value of the C ABI).
 // ---------------------------------------------------------------------------
+enum : int {
+  B_SEARCH = 0, B_INACTIVE = 1, B_ZERO = 2, B_CONSTANT = 3, B_KNAPSACK = 4, B_SCAN = 5,
+  B_DEFAULT = 6, B_U_EMPTY = 7, B_U_GROWN = 8, B_BELOW_RHS = 9
+};
+
 template <class R, class It>
 struct thr {
   R t, lo, hi;
   It first, last;
   int kind;       // 3 = map_a * lambert_w_exp (a_lambert_w_exp_map, functor.h:30-38)
   double map_a;   // the map's constant, already rounded to Data
+  int branch;
 };
+
+template <class T>
+inline T tagged(T t, int branch) {
+  t.branch = branch;
+  return t;
+}
 
 template <class R, class It>
 inline thr<R, It> make_thr(R t, R lo, R hi, It first, It last, int kind = 0,
@@ -57,6 +71,7 @@ inline thr<R, It> make_thr(R t, R lo, R hi, It first, It last, int kind = 0,
   thr<R, It> r;
   r.t = t; r.lo = lo; r.hi = hi; r.first = first; r.last = last; r.kind = kind;
   r.map_a = map_a;
+  r.branch = B_SEARCH;
   return r;
 }
 
@@ -225,8 +240,8 @@ inline thr<R, It> knapsack_le(It first, It last, R lo, R hi, R rhs) {
   R s = std::accumulate(mid_first, mid_last, static_cast<R>(0))
       + hi * static_cast<R>(std::distance(first, mid_first))
       + lo * static_cast<R>(std::distance(mid_last, last));
-  if (s > rhs + eps) return knapsack_eq(first, last, lo, hi, rhs);
-  return make_thr(static_cast<R>(0), lo, hi, mid_first, mid_last);
+  if (s > rhs + eps) return tagged(knapsack_eq(first, last, lo, hi, rhs), B_KNAPSACK);
+  return tagged(make_thr(static_cast<R>(0), lo, hi, mid_first, mid_last), B_INACTIVE);
 }
 
 // ---------------------------------------------------------------------------
@@ -243,15 +258,15 @@ inline proj cone_special_cases(It first, It last, std::ptrdiff_t k, R div,
   const R eps = 16 * std::numeric_limits<R>::epsilon();
   R sum_k = std::accumulate(first, k_last, static_cast<R>(0));
   if (sum_k <= eps) {
-    out = make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
-                   first, first);
+    out = tagged(make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                          first, first), B_ZERO);
     return proj::zero;
   }
   R hi = sum_k / div;
   R t = static_cast<R>(*(k_last - 1)) - hi;
   if (k == std::distance(first, last) ||
       t >= static_cast<R>(*std::max_element(k_last, last)) - eps) {
-    out = make_thr(t, static_cast<R>(0), hi, k_last, k_last);
+    out = tagged(make_thr(t, static_cast<R>(0), hi, k_last, k_last), B_CONSTANT);
     return proj::constant;
   }
   return proj::general;
@@ -279,7 +294,7 @@ inline thr<R, It> cone_search(It first, It last, std::ptrdiff_t k) {
       if (max_m - eps <= tt && tt <= min_u + eps) {
         if (t <= min_m + eps &&
             ((ml == last) || static_cast<R>(*ml) - eps <= t)) {
-          return make_thr(t, static_cast<R>(0), hi, mf, ml);
+          return tagged(make_thr(t, static_cast<R>(0), hi, mf, ml), B_SCAN);
         }
       }
       if (ml == last) break;
@@ -297,8 +312,8 @@ inline thr<R, It> cone_search(It first, It last, std::ptrdiff_t k) {
     ++num_u;
     ++mf;
   }
-  return make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
-                  first, first);
+  return tagged(make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                         first, first), B_DEFAULT);
 }
 
 template <class R, class It>
@@ -330,10 +345,11 @@ inline thr<R, It> topk_simplex(It first, It last, std::ptrdiff_t k, R rhs) {
     case proj::zero:
       break;
     case proj::constant:
-      if (K * out.hi > rhs + eps) return knapsack_eq(first, last, lo, rhs / K, rhs);
+      if (K * out.hi > rhs + eps)
+        return tagged(knapsack_eq(first, last, lo, rhs / K, rhs), B_KNAPSACK);
       break;
     case proj::general: {
-      thr<R, It> t = knapsack_eq(first, last, lo, rhs / K, rhs);
+      thr<R, It> t = tagged(knapsack_eq(first, last, lo, rhs / K, rhs), B_KNAPSACK);
       if (topk_simplex_lt(first, t.first, t.t, K, rhs, eps))
         return cone_search<R>(first, last, k);
       return t;
@@ -369,7 +385,7 @@ inline thr<R, It> cone_biased_search(It first, It last, std::ptrdiff_t k, R rho)
       if (max_m - eps <= tt && tt <= min_u + eps) {
         if (t <= min_m + eps &&
             ((ml == last) || static_cast<R>(*ml) - eps <= t)) {
-          return make_thr(t, static_cast<R>(0), hi, mf, ml);
+          return tagged(make_thr(t, static_cast<R>(0), hi, mf, ml), B_SCAN);
         }
       }
       if (ml == last) break;
@@ -387,8 +403,8 @@ inline thr<R, It> cone_biased_search(It first, It last, std::ptrdiff_t k, R rho)
     ++nu_rho;
     ++mf;
   }
-  return make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
-                  first, first);
+  return tagged(make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                         first, first), B_DEFAULT);
 }
 
 template <class R, class It>
@@ -418,10 +434,11 @@ inline thr<R, It> topk_simplex_biased(It first, It last, std::ptrdiff_t k, R rhs
     case proj::zero:
       break;
     case proj::constant:
-      if (K * out.hi > rhs + eps) return knapsack_eq(first, last, lo, rhs / K, rhs);
+      if (K * out.hi > rhs + eps)
+        return tagged(knapsack_eq(first, last, lo, rhs / K, rhs), B_KNAPSACK);
       break;
     case proj::general: {
-      thr<R, It> t = knapsack_eq(first, last, lo, rhs / K, rhs);
+      thr<R, It> t = tagged(knapsack_eq(first, last, lo, rhs / K, rhs), B_KNAPSACK);
       if (topk_simplex_biased_lt(first, t.first, t.t, K, rhs, rho, eps))
         return cone_biased_search<R>(first, last, k, rho);
       return t;
@@ -457,7 +474,7 @@ inline thr<R, It> knapsack_le_biased_search(It first, It last, R lo, R hi, R rhs
           tt = lo + t;
           if (tt <= min_m + eps &&
               ((ml == last) || static_cast<R>(*ml) - eps <= tt)) {
-            return make_thr(t, lo, hi, mf, ml);
+            return tagged(make_thr(t, lo, hi, mf, ml), B_SCAN);
           }
         }
       }
@@ -474,8 +491,8 @@ inline thr<R, It> knapsack_le_biased_search(It first, It last, R lo, R hi, R rhs
     ++num_u;
     ++mf;
   }
-  return make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
-                  first, first);
+  return tagged(make_thr(static_cast<R>(0), static_cast<R>(0), static_cast<R>(0),
+                         first, first), B_DEFAULT);
 }
 
 template <class R, class It>
@@ -484,7 +501,7 @@ inline thr<R, It> knapsack_le_biased(It first, It last, R lo, R hi, R rhs, R rho
   const R eps = std::numeric_limits<R>::epsilon()
               * std::max(static_cast<R>(1), std::abs(rhs));
   thr<R, It> t = knapsack_eq(first, last, lo, hi, rhs);
-  if (t.t >= rho * rhs - eps) return t;
+  if (t.t >= rho * rhs - eps) return tagged(t, B_KNAPSACK);
   return knapsack_le_biased_search(first, last, lo, hi, rhs, rho);
 }
 
@@ -587,7 +604,7 @@ inline thr<R, It> topk_entropy(It first, It last, std::ptrdiff_t k) {
   lse_both(first, last, mx, log_z, log_z_1);
   R t(log_z_1), lo(0), hi(1);
   if (k <= 1 || static_cast<R>(*mx) - eps <= log_z - std::log(K))
-    return make_thr(t, lo, hi, first, last, 1);
+    return tagged(make_thr(t, lo, hi, first, last, 1), B_U_EMPTY);
   R min_u(0), sum_u(0), k_u(K), z(0);
   It mf = first;
   for (std::ptrdiff_t num_u = 1; num_u < k; ++num_u) {
@@ -612,7 +629,7 @@ inline thr<R, It> topk_entropy(It first, It last, std::ptrdiff_t k) {
     t = mxv + std::log1p(z + a) - std::log(k_u / K);
     hi = (1 + z) / ((1 + z + a) * K);
   }
-  return make_thr(t, lo, hi, mf, last, 1);
+  return tagged(make_thr(t, lo, hi, mf, last, 1), B_U_GROWN);
 }
 
 // Biased top-k entropy (topk_entropy_biased.h:9-260):
@@ -696,10 +713,10 @@ inline thr<R, It> topk_entropy_biased(It first, It last, std::ptrdiff_t k, R alp
   }
   const R lo(0), K(static_cast<R>(k));
   const double map_a = static_cast<double>(1 / static_cast<D>(alpha));
-  if (k == 1) return make_thr(t, lo, s, first, last, 3, map_a);
+  if (k == 1) return tagged(make_thr(t, lo, s, first, last, 3, map_a), B_U_EMPTY);
   const R alpha_k(alpha / K);
   R tt = t + std::max(alpha_k * s + std::log(alpha_k * s), exp_min_arg<R>::get());
-  if (max - eps <= tt) return make_thr(t, lo, s / K, first, last, 3, map_a);
+  if (max - eps <= tt) return tagged(make_thr(t, lo, s / K, first, last, 3, map_a), B_U_EMPTY);
   // U not empty: grow U by the largest remaining element (:235-259).
   std::swap(*first, *max_el);
   const R log_k = std::log(K), log_alpha = std::log(alpha);
@@ -732,7 +749,7 @@ inline thr<R, It> topk_entropy_biased(It first, It last, std::ptrdiff_t k, R alp
     std::swap(*mf, *max_el);
     ++mf;
   }
-  return make_thr(t, lo, s / K, first, last, 3, map_a);
+  return tagged(make_thr(t, lo, s / K, first, last, 3, map_a), B_U_GROWN);
 }
 
 // ---------------------------------------------------------------------------
@@ -909,8 +926,8 @@ two_simplex(It a_first, It a_last, It b_first, It b_last, R rhs) {
       break;
     }
   }
-  return std::make_pair(make_thr(t, lo, hi, a_first, x_last),
-                        make_thr(-t, lo, hi, b_first, y_last));
+  return std::make_pair(tagged(make_thr(t, lo, hi, a_first, x_last), B_BELOW_RHS),
+                        tagged(make_thr(-t, lo, hi, b_first, y_last), B_BELOW_RHS));
 }
 
 // The same problem by the sort-and-scan method (two_simplex_sort.h:15-111):
@@ -936,6 +953,7 @@ two_simplex_sort(It a_first, It a_last, It b_first, It b_last, R rhs) {
                                  : static_cast<R>(*std::prev(b_last)) - C;
   };
   R a_r = a_at(r), b_s = b_at(s);
+  int branch = B_SEARCH;  // common sum rhs unless the scan stops inside
   while (c < C) {
     R copt = (s * sum_mu + r * sum_nu) / static_cast<R>(r + s);
     R next_cr = (sum_mu + a_r) - (r + 1) * a_r;
@@ -943,6 +961,7 @@ two_simplex_sort(It a_first, It a_last, It b_first, It b_last, R rhs) {
     R next_c = std::min(std::min(next_cr, next_cs), C);
     if (c <= copt && copt < next_c) {
       best_c = copt;
+      branch = B_BELOW_RHS;
       break;
     }
     if (next_c >= C - eps) {
@@ -962,8 +981,8 @@ two_simplex_sort(It a_first, It a_last, It b_first, It b_last, R rhs) {
   }
   R theta_a = (sum_mu - best_c) / static_cast<R>(r);
   R theta_b = (sum_nu - best_c) / static_cast<R>(s);
-  return std::make_pair(make_thr(theta_a, lo, hi, a_first, a_first + r),
-                        make_thr(theta_b, lo, hi, b_first, b_first + s));
+  return std::make_pair(tagged(make_thr(theta_a, lo, hi, a_first, a_first + r), branch),
+                        tagged(make_thr(theta_b, lo, hi, b_first, b_first + s), branch));
 }
 
 // ---------------------------------------------------------------------------

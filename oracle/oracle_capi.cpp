@@ -3,6 +3,8 @@
 // the product library).
 //
 // oracle_prox          batch loop prox(dim, first, last, aux, ...) (proxdef.h:279-324)
+// oracle_prox_sets     the same, also returning each record's sets (first / last
+//                      over aux) and the branch that produced it
 // oracle_eval_scores   per-example part of evaluate_dataset (eval.h:36-47) on given scores
 // oracle_eval_features evaluate_dataset for feature input, with the scores
 //                      gemv (eval/scores.h:21-26) as a plain loop
@@ -46,9 +48,21 @@ void store_thr(sdca_thresholds* out, int64_t j, const orc::thr<R, D*>& t) {
   out[j].hi = static_cast<double>(t.hi);
 }
 
+// n_hi = first - begin, n_mid = last - first over the block's scratch copy
+// starting at `begin` (proxdef.h:29-67).
+template <class D, class R>
+void store_sets(sdca_prox_sets* out, int64_t j, const orc::thr<R, D*>& t, const D* begin) {
+  if (!out) return;
+  out[j].n_hi = static_cast<int64_t>(t.first - begin);
+  out[j].n_mid = static_cast<int64_t>(t.last - t.first);
+  out[j].branch = t.branch;
+  out[j].reserved = 0;
+}
+
 template <class D, class R>
 int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
-              const int64_t* col_p, sdca_thresholds* thr_out, int nthreads) {
+              const int64_t* col_p, sdca_thresholds* thr_out, int nthreads,
+              sdca_prox_sets* sets_out = nullptr) {
   const R lo = static_cast<R>(p->lo), hi = static_cast<R>(p->hi),
           rhs = static_cast<R>(p->rhs), rho = static_cast<R>(p->rho);
   const std::ptrdiff_t k = static_cast<std::ptrdiff_t>(p->k);
@@ -82,6 +96,8 @@ int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
           store_thr<D, R>(thr_out, 2 * j, t1);
           store_thr<D, R>(thr_out, 2 * j + 1, t2);
         }
+        store_sets<D, R>(sets_out, 2 * j, t1, a);
+        store_sets<D, R>(sets_out, 2 * j + 1, t2, a + pj);
         continue;
       }
       orc::thr<R, D*> t;
@@ -104,6 +120,7 @@ int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
       }
       orc::clamp(t, col, col + m);
       store_thr<D, R>(thr_out, j, t);
+      store_sets<D, R>(sets_out, j, t, a);
     }
   });
   return 0;
@@ -299,6 +316,24 @@ int oracle_prox(int op, int data, int result, int64_t m, int64_t n, void* x,
     return prox_impl<float, long double>(op, m, n, static_cast<float*>(x), p, col_p, thr_out, nthreads);
   if (data == SDCA_F64 && result == SDCA_LONG_DOUBLE)
     return prox_impl<double, long double>(op, m, n, static_cast<double*>(x), p, col_p, thr_out, nthreads);
+  return SDCA_ERR_PRECISION;
+}
+
+int oracle_prox_sets(int op, int data, int result, int64_t m, int64_t n, void* x,
+                     const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* thr_out,
+                     sdca_prox_sets* sets_out, int nthreads) {
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return prox_impl<float, float>(op, m, n, static_cast<float*>(x), p, col_p, thr_out, nthreads,
+                                   sets_out);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return prox_impl<float, double>(op, m, n, static_cast<float*>(x), p, col_p, thr_out,
+                                    nthreads, sets_out);
+  if (data == SDCA_F64 && result == SDCA_F32)
+    return prox_impl<double, float>(op, m, n, static_cast<double*>(x), p, col_p, thr_out,
+                                    nthreads, sets_out);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return prox_impl<double, double>(op, m, n, static_cast<double*>(x), p, col_p, thr_out,
+                                     nthreads, sets_out);
   return SDCA_ERR_PRECISION;
 }
 

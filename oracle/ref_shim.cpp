@@ -60,6 +60,18 @@ void put(sdca_thresholds* out, int64_t j, const T& th) {
   out[j].hi = static_cast<double>(th.hi);
 }
 
+// The record's sets as the reference leaves them (proxdef.h:29-67): first
+// and last over the block's scratch copy starting at `begin`.  The branch is
+// not part of the reference's record (-1).
+template <class T, class D>
+void put_sets(sdca_prox_sets* out, int64_t j, const T& th, const D* begin) {
+  if (!out) return;
+  out[j].n_hi = static_cast<int64_t>(th.first - begin);
+  out[j].n_mid = static_cast<int64_t>(th.last - th.first);
+  out[j].branch = -1;
+  out[j].reserved = 0;
+}
+
 // The reference's own batched entry points (the Matlab dispatch,
 // src/matlab/mex_prox.cpp:145-172), on columns [b, e).
 template <class D, class R>
@@ -118,7 +130,8 @@ void batched(int op, int64_t m, D* first, D* last, D* aux, const sdca_prox_param
 // Per-column loop with the threshold records (same steps as proxdef.h:279-298).
 template <class D, class R>
 void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
-                     const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* out) {
+                     const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* out,
+                     sdca_prox_sets* sets) {
   const R lo = static_cast<R>(p->lo), hi = static_cast<R>(p->hi), rhs = static_cast<R>(p->rhs);
   const R rho = static_cast<R>(p->rho);
   const std::ptrdiff_t k = static_cast<std::ptrdiff_t>(p->k);
@@ -129,31 +142,31 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
     switch (op) {
       case SDCA_PROX_KNAPSACK_EQ: {
         auto t = sdca::thresholds_knapsack_eq(aux, al, lo, hi, rhs);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_KNAPSACK_LE: {
         auto t = sdca::thresholds_knapsack_le(aux, al, lo, hi, rhs);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_TOPK_SIMPLEX: {
         auto t = sdca::thresholds_topk_simplex(aux, al, k, rhs);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_TOPK_CONE: {
         auto t = sdca::thresholds_topk_cone<R>(aux, al, k);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_ENTROPY: {
         auto t = sdca::thresholds_entropy(aux, al, hi, rhs);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_ENTROPY_NORM: {
         auto t = sdca::thresholds_entropy_norm(aux, al, hi, rhs);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_TOPK_ENTROPY: {
         auto t = sdca::thresholds_topk_entropy<R>(aux, al, k);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_TWO_SIMPLEX: {
         std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])
@@ -163,11 +176,13 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
         sdca::prox(t.second, col + pj, col + m);
         put(out, 2 * j, t.first);
         put(out, 2 * j + 1, t.second);
+        put_sets(sets, 2 * j, t.first, aux);
+        put_sets(sets, 2 * j + 1, t.second, aux + pj);
         break;
       }
       case SDCA_PROX_TOPK_ENTROPY_BIASED: {
         auto t = sdca::thresholds_topk_entropy_biased(aux, al, k, static_cast<R>(p->alpha));
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_TWO_ENTROPY: {
         std::ptrdiff_t pj = col_p ? static_cast<std::ptrdiff_t>(col_p[j])
@@ -178,6 +193,8 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
         sdca::prox(t.second, col + pj, col + m);
         put(out, 2 * j, t.first);
         put(out, 2 * j + 1, t.second);
+        put_sets(sets, 2 * j, t.first, aux);
+        put_sets(sets, 2 * j + 1, t.second, aux + pj);
         break;
       }
       case SDCA_PROX_TWO_SIMPLEX_SORT: {
@@ -188,19 +205,21 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
         sdca::prox(t.second, col + pj, col + m);
         put(out, 2 * j, t.first);
         put(out, 2 * j + 1, t.second);
+        put_sets(sets, 2 * j, t.first, aux);
+        put_sets(sets, 2 * j + 1, t.second, aux + pj);
         break;
       }
       case SDCA_PROX_KNAPSACK_LE_BIASED: {
         auto t = sdca::thresholds_knapsack_le_biased(aux, al, lo, hi, rhs, rho);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_TOPK_SIMPLEX_BIASED: {
         auto t = sdca::thresholds_topk_simplex_biased(aux, al, k, rhs, rho);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       case SDCA_PROX_TOPK_CONE_BIASED: {
         auto t = sdca::thresholds_topk_cone_biased(aux, al, k, rho);
-        sdca::prox(t, col, col + m); put(out, j, t); break;
+        sdca::prox(t, col, col + m); put(out, j, t); put_sets(sets, j, t, aux); break;
       }
       default: break;
     }
@@ -209,7 +228,8 @@ void with_thresholds(int op, int64_t m, int64_t b, int64_t e, D* x, D* aux,
 
 template <class D, class R>
 int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
-              const int64_t* col_p, sdca_thresholds* out, int nthreads) {
+              const int64_t* col_p, sdca_thresholds* out, int nthreads,
+              sdca_prox_sets* sets = nullptr) {
   if (op == SDCA_PROX_LAMBERT_W_EXP) {
     parallel_for(n, nthreads, [&](int64_t b, int64_t e) {
       batched<D, R>(op, m, x + b * m, x + e * m, nullptr, p, nullptr);
@@ -219,7 +239,7 @@ int prox_impl(int op, int64_t m, int64_t n, D* x, const sdca_prox_params* p,
   parallel_for(n, nthreads, [&](int64_t b, int64_t e) {
     std::vector<D> aux(static_cast<size_t>(m));
     if (out) {
-      with_thresholds<D, R>(op, m, b, e, x, aux.data(), p, col_p, out);
+      with_thresholds<D, R>(op, m, b, e, x, aux.data(), p, col_p, out, sets);
     } else {
       batched<D, R>(op, m, x + b * m, x + e * m, aux.data(), p, col_p ? col_p + b : nullptr);
     }
@@ -699,6 +719,26 @@ int ref_prox(int op, int data, int result, int64_t m, int64_t n, void* x,
     return prox_impl<double, float>(op, m, n, static_cast<double*>(x), p, col_p, out, nthreads);
   if (data == SDCA_F64 && result == SDCA_F64)
     return prox_impl<double, double>(op, m, n, static_cast<double*>(x), p, col_p, out, nthreads);
+  return SDCA_ERR_PRECISION;
+}
+
+// ref_prox with the sets of each record (thresholds required).
+int ref_prox_sets(int op, int data, int result, int64_t m, int64_t n, void* x,
+                  const sdca_prox_params* p, const int64_t* col_p, sdca_thresholds* out,
+                  sdca_prox_sets* sets, int nthreads) {
+  if (!out) return SDCA_ERR_ARG_NULL;
+  if (data == SDCA_F32 && result == SDCA_F32)
+    return prox_impl<float, float>(op, m, n, static_cast<float*>(x), p, col_p, out, nthreads,
+                                   sets);
+  if (data == SDCA_F32 && result == SDCA_F64)
+    return prox_impl<float, double>(op, m, n, static_cast<float*>(x), p, col_p, out, nthreads,
+                                    sets);
+  if (data == SDCA_F64 && result == SDCA_F32)
+    return prox_impl<double, float>(op, m, n, static_cast<double*>(x), p, col_p, out, nthreads,
+                                    sets);
+  if (data == SDCA_F64 && result == SDCA_F64)
+    return prox_impl<double, double>(op, m, n, static_cast<double*>(x), p, col_p, out,
+                                     nthreads, sets);
   return SDCA_ERR_PRECISION;
 }
 
