@@ -43,9 +43,8 @@ size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool nor
 hipError_t launch_epoch(const EpochLaunch& a, int** flag_dev);
 // Largest m of the epoch for an element type and objective kind (two rows
 // of m values and, multilabel, the example's labels in the block kernel's
-// LDS; the multilabel hinges: the two-block simplex in registers).
+// LDS).
 int64_t epoch_max_m(int data, int kind);
-constexpr int64_t kEpochMaxMultilabelHingeM = 2048;
 
 }  // namespace sdca_gpu
 

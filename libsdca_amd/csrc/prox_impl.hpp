@@ -1505,6 +1505,122 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
   return r;
 }
 
+// two_family_slots over a column held in memory (LDS or global) instead of
+// register slots, thread g of the group taking entries g, g + G, ... (the
+// slot layout's order, so the sums are the same): the same passes, for
+// columns beyond the register slots.  Block a = entries [0, p).
+template <int G, class D, class R>
+__device__ inline ColThr<R> two_family_array(const D* x, int m, int p, const ProxParamsT<R>& pp) {
+  const R rhs = pp.rhs;
+  const R eps = num<R>::eps() * dmax(R(1), rhs);
+  const int g = static_cast<int>(threadIdx.x) % G;
+  R cuts[2];
+  R res[2];
+  int cnt[2];
+  // Phase 1 per block: S starts at {x > max - rhs} and shrinks to
+  // {x in S : x > t} until it stays (two_simplex.h:44-67).
+  for (int b = 0; b < 2; ++b) {
+    const int j0 = b == 0 ? 0 : p, j1 = b == 0 ? p : m;
+    R mx = -num<R>::inf();
+    for (int j = j0 + g; j < j1; j += G) {
+      const R v = static_cast<R>(x[j]);
+      mx = v > mx ? v : mx;
+    }
+    mx = group_max<G>(mx);
+    R cut = mx - rhs;
+    R sb = 0;
+    int nb = 0;
+    for (int j = j0 + g; j < j1; j += G) {
+      const R v = static_cast<R>(x[j]);
+      const bool in = v > cut;
+      sb += in ? v : R(0);
+      nb += in ? 1 : 0;
+    }
+    group_sums<G>(sb, nb);
+    R tb = 0;
+    for (int it = 0; it <= m; ++it) {
+      tb = div_near(sb - rhs, static_cast<R>(nb));
+      R s2 = 0;
+      int n2 = 0;
+      for (int j = j0 + g; j < j1; j += G) {
+        const R v = static_cast<R>(x[j]);
+        const bool in = v > cut && v > tb;
+        s2 += in ? v : R(0);
+        n2 += in ? 1 : 0;
+      }
+      group_sums<G>(s2, n2);
+      if (n2 == nb) break;
+      cut = dmax(cut, tb);
+      sb = s2;
+      nb = n2;
+    }
+    cuts[b] = cut;
+    cnt[b] = nb;
+    res[b] = tb;
+  }
+  R t = res[0];
+  const R s = res[1];
+  if (t + s >= -eps) {
+    ColThr<R> r = tag_thr(make_thr<R>(t, R(0), rhs), SDCA_BRANCH_SEARCH, 0, cnt[0]);
+    r.t2 = s;
+    r.n_mid2 = cnt[1];
+    return r;
+  }
+  // Phase 2: joint variable fixing with s = -t (two_simplex.h:69-117).
+  int mc = cnt[0] + cnt[1];
+  int ca = cnt[0], cb = cnt[1];
+  {
+    R sa = 0, sbb = 0;
+    for (int j = g; j < m; j += G) {
+      const R v = static_cast<R>(x[j]);
+      if (j < p && v > cuts[0]) sa += v;
+      if (j >= p && v > cuts[1]) sbb += v;
+    }
+    group_sums<G>(sa, sbb);
+    t = (+sa - sbb) / static_cast<R>(mc);
+  }
+  for (int it = 0; it <= m; ++it) {
+    R sum_x = 0, sum_y = 0;
+    int n_x = 0, n_y = 0;
+    const R mt = -t;
+    for (int j = g; j < m; j += G) {
+      const R v = static_cast<R>(x[j]);
+      if (j < p) {
+        if (v > cuts[0] && !(v > t)) { sum_x += v; ++n_x; }
+      } else {
+        if (v > cuts[1] && !(v > mt)) { sum_y += v; ++n_y; }
+      }
+    }
+    group_sums<G>(sum_x, sum_y, n_x, n_y);
+    const R infeas = sum_x - sum_y - static_cast<R>(n_x + n_y) * t;
+    R next;
+    if (n_y > 0 && infeas > eps) {
+      cuts[1] = dmax(cuts[1], mt);
+      next = static_cast<R>(mc) * t + sum_y;
+      mc -= n_y;
+      cb -= n_y;
+    } else if (n_x > 0 && infeas < -eps) {
+      cuts[0] = dmax(cuts[0], t);
+      next = static_cast<R>(mc) * t - sum_x;
+      mc -= n_x;
+      ca -= n_x;
+    } else {
+      ca -= n_x;
+      cb -= n_y;
+      break;
+    }
+    if (mc > 0) {
+      t = next / static_cast<R>(mc);
+    } else {
+      break;
+    }
+  }
+  ColThr<R> r = tag_thr(make_thr<R>(t, R(0), rhs), SDCA_BRANCH_BELOW_RHS, 0, ca);
+  r.t2 = -t;
+  r.n_mid2 = cb;
+  return r;
+}
+
 // Two-block simplex of one column per lane group.  When no column of the
 // wave has more than G rows in block a (the multilabel duals: p <= 5 of
 // m = 200 rows), block a lies in slot 0 of every lane and the passes over it

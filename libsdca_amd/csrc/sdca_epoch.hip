@@ -408,6 +408,14 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
         });
       } else {  // prox_two_simplex, rhs c (l2_multilabel_hinge.h:59-65)
         D ta = D(0), tb = D(0);  // the two blocks' thresholds
+        ProxParamsT<R> pp;
+        pp.lo = R(0);
+        pp.hi = c;
+        pp.rhs = c;
+        pp.rho = R(0);
+        pp.k = 1;
+        pp.op = OP_TWO_SIMPLEX;
+        pp.p = nl;
         if constexpr (C > 0) {
           D vq[C];
           const int nvalid = (m - tid + G - 1) / G;
@@ -416,15 +424,13 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
             const D x = cb[tid + G * q];
             vq[q] = (q < nvalid) ? x : -num<D>::inf();
           }
-          ProxParamsT<R> pp;
-          pp.lo = R(0);
-          pp.hi = c;
-          pp.rhs = c;
-          pp.rho = R(0);
-          pp.k = 1;
-          pp.op = OP_TWO_SIMPLEX;
-          pp.p = nl;
           const ColThr<R> th = two_family_slots<G, C, C, D, R>(vq, m, nl, pp);
+          ta = static_cast<D>(th.t);
+          tb = static_cast<D>(th.t2);
+        } else {
+          // Rows beyond the register slots: the same passes over the LDS
+          // column.
+          const ColThr<R> th = two_family_array<G, D, R>(cb, m, nl, pp);
           ta = static_cast<D>(th.t);
           tb = static_cast<D>(th.t2);
         }
@@ -879,10 +885,11 @@ hipError_t launch_block_for(const D* S, const D* Gm, int64_t q0, int nb, const D
       e = SDCA_EPOCH_BY_PF(kFamMlEnt);
       break;
     case SDCA_OBJ_MULTILABEL_HINGE:
-    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:  // m <= 2048 (checked by the caller)
-      e = pf == 1 ? SDCA_EPOCH_BLOCK(kFamMlHinge, 1, 5, 1)
-                  : pf == 4 ? SDCA_EPOCH_BLOCK(kFamMlHinge, 4, 5, 4)
-                            : SDCA_EPOCH_BLOCK(kFamMlHinge, 8, 5, 8);
+    case SDCA_OBJ_MULTILABEL_HINGE_SMOOTH:
+      e = pf == 0 ? SDCA_EPOCH_BLOCK(kFamMlHinge, 0, 5, 0)
+                  : pf == 1 ? SDCA_EPOCH_BLOCK(kFamMlHinge, 1, 5, 1)
+                            : pf == 4 ? SDCA_EPOCH_BLOCK(kFamMlHinge, 4, 5, 4)
+                                      : SDCA_EPOCH_BLOCK(kFamMlHinge, 8, 5, 8);
       break;
     default: {
       const bool simplex = a.kind == SDCA_OBJ_HINGE_TOPK || a.kind == SDCA_OBJ_HINGE_TOPK_SMOOTH;
@@ -995,8 +1002,6 @@ int64_t epoch_max_m(int data, int kind) {
   // is the largest of its forms for a given m.
   const size_t es = data == SDCA_F32 ? 4 : 8;
   const bool ml = kind >= SDCA_OBJ_MULTILABEL_HINGE;
-  if (kind == SDCA_OBJ_MULTILABEL_HINGE || kind == SDCA_OBJ_MULTILABEL_HINGE_SMOOTH)
-    return kEpochMaxMultilabelHingeM;
   int64_t lo = 2, hi = static_cast<int64_t>(kMaxColumnBytes / (2 * es));
   while (lo < hi) {  // the largest m in [2, hi] whose block kernel fits
     const int64_t mid = (lo + hi + 1) / 2;

@@ -243,20 +243,20 @@ def test_epoch_multilabel(cuda, oracle, obj, dtype, result, m):
 @pytest.mark.parametrize("obj", ML_OBJS)
 def test_epoch_multilabel_wide(cuda, oracle, obj):
     """m = 1500 (eight register slots per thread) with up to 40 labels per
-    example; the entropy also at m = 3000 (the vector in LDS).  fp32 data
+    example, and m = 3000 (the vector in LDS; for the hinges the two-block
+    simplex over the LDS column).  fp32 data
     with fp64 arithmetic: in fp32 arithmetic the two-block projection's own
     sums over ~1500 rows round differently on the GPU (tree order) than in
     the reference (sequential), by more than the scores' rounding spread
     that the criterion measures; the fp32 pair is covered up to m = 257."""
     check_ml(oracle, cuda, obj, np.float32, 1, 160, 48, 1500, 41, max_labels=40)
-    if obj[0] == "l2_multilabel_entropy":
-        check_ml(oracle, cuda, obj, np.float32, 1, 120, 32, 3000, 43, max_labels=40)
+    check_ml(oracle, cuda, obj, np.float32, 1, 120, 32, 3000, 43, max_labels=40)
 
 
 def test_epoch_multilabel_errors(cuda):
     """Label rules (1..m-1 distinct sorted labels per example): a broken
     example is skipped and reported as SDCA_ERR_LABELS after the epoch; the
-    multilabel hinges refuse m > 2048."""
+    multilabel hinges refuse m > 12200 (fp32), the labels' LDS bound."""
     import torch
     import libsdca_amd as sd
     n, d, m = 40, 16, 9
@@ -275,8 +275,8 @@ def test_epoch_multilabel_errors(cuda):
     assert A.abs().max() > 0
     with pytest.raises(sd.SdcaError) as e:
         Xw = torch.zeros((4, 8), device=cuda)
-        sd.epoch_features(ML_OBJS[1], Xw, torch.zeros((2049, 8), device=cuda),
-                          torch.zeros((4, 2049), device=cuda), [0, 1, 2, 3],
+        sd.epoch_features(ML_OBJS[1], Xw, torch.zeros((12201, 8), device=cuda),
+                          torch.zeros((4, 12201), device=cuda), [0, 1, 2, 3],
                           offsets=[0, 1, 2, 3, 4])
     assert e.value.status == 4
 
@@ -336,15 +336,16 @@ def test_epoch_at_max_m(cuda, oracle, dtype, result, m):
     assert e.value.status == 4
 
 
-def test_epoch_multilabel_entropy_at_max_m(cuda, oracle):
-    """The multilabel entropy keeps the example's labels in LDS too: its
-    largest m in fp32 is 12200, one more is refused before any launch."""
+@pytest.mark.parametrize("obj", ML_OBJS)
+def test_epoch_multilabel_at_max_m(cuda, oracle, obj):
+    """The multilabel objectives keep the example's labels in LDS too: their
+    largest m in fp32 is 12200 (the hinges' two-block simplex over the LDS
+    column there), one more is refused before any launch."""
     import torch
     import libsdca_amd as sd
-    check_ml(oracle, cuda, ML_OBJS[2], np.float32, 1, 24, 16, 12200, 45, epochs=1,
-             max_labels=6)
+    check_ml(oracle, cuda, obj, np.float32, 1, 24, 16, 12200, 45, epochs=1, max_labels=6)
     with pytest.raises(sd.SdcaError) as e:
-        sd.epoch_features(ML_OBJS[2], torch.zeros((4, 8), device=cuda),
+        sd.epoch_features(obj, torch.zeros((4, 8), device=cuda),
                           torch.zeros((12201, 8), device=cuda),
                           torch.zeros((4, 12201), device=cuda), [0, 1, 2, 3],
                           offsets=[0, 1, 2, 3, 4])
