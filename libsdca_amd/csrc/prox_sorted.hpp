@@ -4,8 +4,10 @@
 // (knapsack_eq.h:25-109) whose partitions are contiguous ranges of the sorted
 // column, the top-k simplex test (topk_simplex.h:9-68), the O(k m) searches
 // topk_cone_search (topk_cone.h:58-133) and knapsack_le_biased_search - run
-// by one wave, in the reference's order and with its sums.  Used by the
-// workgroup-per-column prox kernel and the SDCA epoch.
+// by one wave, with the reference's tests in its order; the partitions are
+// found by binary search and the range sums by the wave's 64 lanes
+// (compensated), the scans' incremental sums in the reference's order.  Used
+// by the workgroup-per-column prox kernel and the SDCA epoch.
 #ifndef SDCA_HIP_PROX_SORTED_HPP
 #define SDCA_HIP_PROX_SORTED_HPP
 
@@ -15,22 +17,54 @@
 
 namespace sdca_gpu {
 
-// Sums over ranges of the sorted column.  Summing a sorted sequence in order
-// is the worst case for rounding (all positives, then the cancelling
-// negatives), so the sum is compensated (Neumaier) in double.
+// Sums over ranges of the sorted column, by the 64 lanes of a wave (every
+// lane calls it and receives the sum).  Summing a sorted sequence is the
+// worst case for rounding (all positives, then the cancelling negatives), so
+// each lane's strided part is compensated (Neumaier) in double and the
+// lanes' (sum, compensation) pairs are combined the same way, lane ^ 32,
+// ^ 16, ... (every lane ends with the same bits).
+template <int OFF>
+__device__ inline void neumaier_xor(double& acc, double& comp) {
+  const double a2 = xor_lane<OFF, true>(acc), c2 = xor_lane<OFF, true>(comp);
+  const double t = acc + a2;
+  comp += c2 + ((fabs(acc) >= fabs(a2)) ? (acc - t) + a2 : (a2 - t) + acc);
+  acc = t;
+}
 template <class R, class D>
 __device__ R sum_range(const D* s, int b, int e) {
   double acc = 0, comp = 0;
-  for (int i = b; i < e; ++i) {
+  for (int i = b + (static_cast<int>(threadIdx.x) & 63); i < e; i += 64) {
     const double x = static_cast<double>(static_cast<R>(s[i]));
     const double t = acc + x;
     comp += (fabs(acc) >= fabs(x)) ? (acc - t) + x : (x - t) + acc;
     acc = t;
   }
+  neumaier_xor<32>(acc, comp);
+  neumaier_xor<16>(acc, comp);
+  neumaier_xor<8>(acc, comp);
+  neumaier_xor<4>(acc, comp);
+  neumaier_xor<2>(acc, comp);
+  neumaier_xor<1>(acc, comp);
   return static_cast<R>(acc + comp);
 }
 
-// Kiwiel variable fixing on a column sorted in descending order.
+// The first index of [b, e) whose value fails x > c (x >= c with GE) in a
+// column sorted in descending order, e if none: the end of the prefix the
+// reference's partitions put first (binary search; the same in every lane).
+template <class R, class D, bool GE = false>
+__device__ inline int prefix_end(const D* s, int b, int e, R c) {
+  while (b < e) {
+    const int mid = b + ((e - b) >> 1);
+    const R x = static_cast<R>(s[mid]);
+    if (GE ? x >= c : x > c) b = mid + 1;
+    else e = mid;
+  }
+  return b;
+}
+
+// Kiwiel variable fixing on a column sorted in descending order, by the 64
+// lanes of a wave: its partitions are the sorted column's prefixes (found by
+// binary search), its sums range sums.
 template <class D, class R>
 __device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
   const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
@@ -42,10 +76,8 @@ __device__ KnapState<R> knapsack_sorted(const D* s, int m, R lo, R hi, R rhs) {
   st.sum_u = 0;
   for (int iter = 0; iter <= m; ++iter) {
     const R c_lo = lo + t, c_hi = hi + t;
-    int p_lo = f;  // first free index with !(x > c_lo)
-    while (p_lo < l && static_cast<R>(s[p_lo]) > c_lo) ++p_lo;
-    int p_hi = f;  // end of the prefix with x > c_hi (within [f, p_lo))
-    while (p_hi < p_lo && static_cast<R>(s[p_hi]) > c_hi) ++p_hi;
+    const int p_lo = prefix_end<R>(s, f, l, c_lo);     // first free index with !(x > c_lo)
+    const int p_hi = prefix_end<R>(s, f, p_lo, c_hi);  // end of the prefix with x > c_hi
     const R s_lo = sum_range<R>(s, p_lo, l);
     const int n_lo = l - p_lo;
     const R s_hi = sum_range<R>(s, f, p_hi);
@@ -255,10 +287,8 @@ __device__ void thresholds_sorted(const D* s, int m, int op, R lo, R hi, R rhs, 
     if (op != OP_KNAPSACK_EQ) {  // knapsack_le, and knapsack_le_biased with rho = 0
       // knapsack_le.h:30-46 on the sorted column
       const R eps = num<R>::eps() * dmax(R(1), fabs(rhs));
-      int e_hi = 0;
-      while (e_hi < m && static_cast<R>(s[e_hi]) >= hi) ++e_hi;
-      int e_mid = e_hi;
-      while (e_mid < m && static_cast<R>(s[e_mid]) > lo) ++e_mid;
+      const int e_hi = prefix_end<R, D, true>(s, 0, m, hi);
+      const int e_mid = prefix_end<R>(s, e_hi, m, lo);
       const R sum = sum_range<R>(s, e_hi, e_mid) + hi * static_cast<R>(e_hi)
                   + lo * static_cast<R>(m - e_mid);
       if (!(sum > rhs + eps)) {
