@@ -3,12 +3,13 @@
 // knapsack operators for m beyond the register kernel.
 //
 // The column is sorted in LDS (bitonic, descending, the order the reference's
-// std::sort(greater) produces), then one lane runs the reference's sequential
+// std::sort(greater) produces), then the first wave runs the reference's
 // steps on the sorted values - the special cases (topk_cone.h:18-55), the
 // Kiwiel loop (knapsack_eq.h:25-109) whose partitions are contiguous ranges
-// of the sorted column, the top-k simplex test (topk_simplex.h:9-68) and the
-// O(k m) search topk_cone_search (topk_cone.h:58-133) in the same order and
-// with the same sums - and the workgroup clamps the column from global memory.
+// of the sorted column (binary searches, range sums over the wave), the
+// top-k simplex test (topk_simplex.h:9-68) and the O(k m) search
+// topk_cone_search (topk_cone.h:58-133) in the same order - and the
+// workgroup clamps the column from global memory.
 // Columns come from a device list written by the register kernel, so no host
 // round trip is needed; every workgroup exits after the list is drained.
 #include <algorithm>
