@@ -344,10 +344,10 @@ int sdca_eval_kernel(const sdca_objective* objs, int n_obj,
  *      scratch.h:27-41).
  * Device pointers on `stream` (flags 0), or host arrays with SDCA_HOST_PTR
  * (staged through device memory for the call, W and A copied back); (data,
- * result) one of (F32, F32), (F32, F64), (F64, F64); m at most 16384 (fp32)
- * or 8192 (fp64) for the multiclass objectives, 12200 (fp32) or 7268 (fp64)
- * for the multilabel ones (larger m: SDCA_ERR_NOT_IMPLEMENTED before
- * anything is enqueued).  Returns SDCA_ERR_LABELS
+ * result) one of (F32, F32), (F32, F64), (F64, F64); m at most 524280 (larger
+ * m: SDCA_ERR_NOT_IMPLEMENTED before anything is enqueued; the example's
+ * vectors stay in LDS up to 16384 (fp32) / 8192 (fp64) classes, 12200 /
+ * 7268 multilabel, and move to device memory beyond).  Returns SDCA_ERR_LABELS
  * (after the epoch) for an index or multiclass label out of range (read as
  * 0) or a multilabel example whose labels break those rules (skipped).
  */

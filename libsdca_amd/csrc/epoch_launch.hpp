@@ -41,9 +41,9 @@ size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool nor
 // Enqueues the epoch; the bad-input flag (an example index or a label out of
 // range: such entries are read as 0) is left in *flag_dev for the caller.
 hipError_t launch_epoch(const EpochLaunch& a, int** flag_dev);
-// Largest m of the epoch for an element type and objective kind (two rows
-// of m values and, multilabel, the example's labels in the block kernel's
-// LDS).
+// Largest m of the epoch for an element type and objective kind (the block
+// kernel's rows go to global memory beyond its LDS; the rank update's grid
+// bounds m).
 int64_t epoch_max_m(int data, int kind);
 
 }  // namespace sdca_gpu

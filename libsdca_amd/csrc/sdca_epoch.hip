@@ -161,26 +161,33 @@ __device__ __forceinline__ void for_cols(int tid, int m, F&& f) {
 // (C = 0: the sorted-column form only) and k <= KM.  PF > 0 (m <= G PF):
 // each thread keeps its entries of the example's vector, of a_i and of S_k
 // in registers, the next example's a_i and S_k loaded while this one runs;
-// PF = 0 keeps the vector in LDS and reads a_i and S_k as it goes.
-template <class D, class R, int FK, int C, int KM, int PF>
+// PF = 0 keeps the vector in LDS and reads a_i and S_k as it goes.  GV
+// (PF = 0, rows beyond the LDS): the vector, the thresholds' column and the
+// labels live in gv (global memory, the workspace; L2-resident at the sizes
+// where LDS ends), the same code reading them there.
+template <class D, class R, int FK, int C, int KM, int PF, bool GV = false>
 __global__ void __launch_bounds__(kEpochThreads)
 epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
                    const int64_t* __restrict__ order, int64_t q0, int64_t n, int nb,
                    const D* __restrict__ norms, const int64_t* __restrict__ labels,
                    const int64_t* __restrict__ offsets, D* __restrict__ A,
                    D* __restrict__ Delta, D* __restrict__ gdummy, EpochObj ob, int m,
-                   int* __restrict__ bad) {
+                   int* __restrict__ bad, D* __restrict__ gv) {
   constexpr int G = kEpochThreads;
   constexpr int PQ = PF > 0 ? PF : 1;
   constexpr bool DL = epoch_delta_in_lds<D>(PF);
+  static_assert(!GV || (PF == 0 && !DL), "global vectors for the PF = 0 form");
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int cw = epoch_column_words(m, C);
-  D* const v = reinterpret_cast<D*>(smem_raw);  // the example's vector (PF = 0), m values
-  D* const cb = v + ((m + 3) & ~3);             // the column the thresholds read (cw words)
-  D* const dummy = cb + cw;                     // G per-thread dummy words
-  D* const Dx = DL ? dummy + G : Delta;         // the block's delta rows
+  // the example's vector (PF = 0), m values
+  D* const v = GV ? gv : reinterpret_cast<D*>(smem_raw);
+  D* const cb = v + ((m + 3) & ~3);  // the column the thresholds read (cw words)
+  // G per-thread dummy words (always in LDS)
+  D* const dummy = GV ? reinterpret_cast<D*>(smem_raw) : cb + cw;
+  D* const Dx = DL ? dummy + G : Delta;  // the block's delta rows
   // the example's labels (multilabel), m ints after the D words
-  int* const lab = reinterpret_cast<int*>(dummy + G + (DL ? kEpochBlock * m : 0));
+  int* const lab = GV ? reinterpret_cast<int*>(cb + cw)
+                      : reinterpret_cast<int*>(dummy + G + (DL ? kEpochBlock * m : 0));
   __shared__ R sh_t, sh_lo, sh_hi;
   __shared__ int sh_slow;
   __shared__ D sh_vy;
@@ -844,15 +851,27 @@ __host__ inline size_t block_lds_bytes(size_t es, int m, int C, bool delta_in_ld
 
 template <class D, class R, int FK, int C, int KM, int PF>
 hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* norms,
-                        const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob, int* bad) {
+                        const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob, int* bad,
+                        D* gv) {
   const int m = static_cast<int>(a.m);
   constexpr bool ml = FK == kFamMlHinge || FK == kFamMlEnt;
   const size_t lds = block_lds_bytes(sizeof(D), m, C, epoch_delta_in_lds<D>(PF), ml);
-  // epoch_max_m keeps every accepted m inside the budget.
-  if (lds > kEpochLdsBytes) return hipErrorInvalidValue;
+  if (lds > kEpochLdsBytes) {
+    // Rows beyond the LDS: the PF = 0 form with its vectors in gv (the
+    // workspace holds epoch_gv_words(m) words there).
+    if constexpr (PF == 0 && C == 0) {
+      hipLaunchKernelGGL((epoch_block_kernel<D, R, FK, C, KM, PF, true>), dim3(1),
+                         dim3(kEpochThreads), kEpochThreads * sizeof(D), a.stream, S, Gm,
+                         a.order, q0, a.n, nb, norms, a.labels, a.offsets, static_cast<D*>(a.A),
+                         Delta, gdummy, ob, m, bad, gv);
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   hipLaunchKernelGGL((epoch_block_kernel<D, R, FK, C, KM, PF>), dim3(1), dim3(kEpochThreads), lds,
                      a.stream, S, Gm, a.order, q0, a.n, nb, norms, a.labels, a.offsets,
-                     static_cast<D*>(a.A), Delta, gdummy, ob, m, bad);
+                     static_cast<D*>(a.A), Delta, gdummy, ob, m, bad, gv);
   return hipGetLastError();
 }
 
@@ -863,11 +882,11 @@ hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* no
 template <class D, class R>
 hipError_t launch_block_for(const D* S, const D* Gm, int64_t q0, int nb, const D* norms,
                             const EpochLaunch& a, D* Delta, D* gdummy, const EpochObj& ob,
-                            int* bad) {
+                            int* bad, D* gv) {
   const int64_t m = a.m;
   const int pf = m <= 256 ? 1 : m <= 1024 ? 4 : m <= 2048 ? 8 : 0;
 #define SDCA_EPOCH_BLOCK(FK, C, KM, PF) \
-  launch_block<D, R, FK, C, KM, PF>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad)
+  launch_block<D, R, FK, C, KM, PF>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad, gv)
   // Families without a register form: one variant per PF.
 #define SDCA_EPOCH_BY_PF(FK)                                      \
   (pf == 0 ? SDCA_EPOCH_BLOCK(FK, 0, 5, 0)                        \
@@ -929,6 +948,9 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
   D* P = Delta + B * m;  // the skinny products' partial sums
   D* norms_ws = P + static_cast<int64_t>(pl.ksplit) * B * (m + B);
   D* At = norms_ws + n;
+  // The block kernel's vectors when the rows exceed its LDS (16-byte aligned).
+  D* gv = reinterpret_cast<D*>((reinterpret_cast<uintptr_t>(At + (a.kernel ? m * n : 0)) + 15) &
+                               ~static_cast<uintptr_t>(15));
   *flag_dev = bad;
   hipError_t e = launch_clear(bad, 1, a.stream);
   if (e != hipSuccess) return e;
@@ -965,7 +987,8 @@ hipError_t launch_epoch_t(const EpochLaunch& a, int** flag_dev) {
                          dim3(256), 0, a.stream, X, a.order, q0, n, nb, Gm);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if ((e = launch_block_for<D, R>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad)) != hipSuccess)
+    if ((e = launch_block_for<D, R>(S, Gm, q0, nb, norms, a, Delta, gdummy, ob, bad, gv)) !=
+        hipSuccess)
       return e;
     if (a.kernel) {
       const int64_t cnt = static_cast<int64_t>(nb) * m;
@@ -988,27 +1011,24 @@ size_t epoch_workspace_bytes(int data, int64_t d, int64_t m, int64_t n, bool nor
   const size_t es = data == SDCA_F32 ? 4 : 8;
   const size_t B = kEpochBlock;
   const size_t splits = static_cast<size_t>(skinny_plan(d, m).ksplit);
+  (void)norms_given;  // the n norm words are kept in the layout either way
+  const size_t mm = static_cast<size_t>((m + 3) & ~int64_t(3));
+  // the block kernel's vectors beyond its LDS: the vector and the column
+  // (mm values each) and the labels (m ints), 16-byte aligned
+  const size_t gv = 16 + 2 * mm * es + 4 * static_cast<size_t>(m);
   return 256 + kEpochThreads * sizeof(double) + es * (2 * B * static_cast<size_t>(m) + B * B +
-                     splits * B * (static_cast<size_t>(m) + B) +
-                     (norms_given && !kernel ? 0 : static_cast<size_t>(n)) +
-                     (kernel ? static_cast<size_t>(m) * static_cast<size_t>(n) : 0));
+                     splits * B * (static_cast<size_t>(m) + B) + static_cast<size_t>(n) +
+                     (kernel ? static_cast<size_t>(m) * static_cast<size_t>(n) : 0)) + gv;
 }
 
 int64_t epoch_max_m(int data, int kind) {
-  // The vector and the thresholds' column, each m values, in at most
-  // 128 KiB; and the block kernel's LDS (block_lds_bytes, with the labels of
-  // a multilabel example) within kEpochLdsBytes.  Above 2048 rows the block
-  // kernel keeps everything in LDS (PF = 0, C = 0, no delta rows), and that
-  // is the largest of its forms for a given m.
-  const size_t es = data == SDCA_F32 ? 4 : 8;
-  const bool ml = kind >= SDCA_OBJ_MULTILABEL_HINGE;
-  int64_t lo = 2, hi = static_cast<int64_t>(kMaxColumnBytes / (2 * es));
-  while (lo < hi) {  // the largest m in [2, hi] whose block kernel fits
-    const int64_t mid = (lo + hi + 1) / 2;
-    if (block_lds_bytes(es, static_cast<int>(mid), 0, false, ml) <= kEpochLdsBytes) lo = mid;
-    else hi = mid - 1;
-  }
-  return lo;
+  // Rows beyond the block kernel's LDS run with its vectors in global
+  // memory, so no row count is refused for the layout; the rank update's
+  // grid (kRankJ classes per workgroup row, at most 65535 rows) sets the
+  // bound.
+  (void)data;
+  (void)kind;
+  return static_cast<int64_t>(65535) * kRankJ;
 }
 
 hipError_t launch_epoch(const EpochLaunch& a, int** flag_dev) {

@@ -255,8 +255,8 @@ def test_epoch_multilabel_wide(cuda, oracle, obj):
 
 def test_epoch_multilabel_errors(cuda):
     """Label rules (1..m-1 distinct sorted labels per example): a broken
-    example is skipped and reported as SDCA_ERR_LABELS after the epoch; the
-    multilabel hinges refuse m > 12200 (fp32), the labels' LDS bound."""
+    example is skipped and reported as SDCA_ERR_LABELS after the epoch; m
+    above 524280 is refused."""
     import torch
     import libsdca_amd as sd
     n, d, m = 40, 16, 9
@@ -275,17 +275,20 @@ def test_epoch_multilabel_errors(cuda):
     assert A.abs().max() > 0
     with pytest.raises(sd.SdcaError) as e:
         Xw = torch.zeros((4, 8), device=cuda)
-        sd.epoch_features(ML_OBJS[1], Xw, torch.zeros((12201, 8), device=cuda),
-                          torch.zeros((4, 12201), device=cuda), [0, 1, 2, 3],
+        sd.epoch_features(ML_OBJS[1], Xw, torch.zeros((524281, 8), device=cuda),
+                          torch.zeros((4, 524281), device=cuda), [0, 1, 2, 3],
                           offsets=[0, 1, 2, 3, 4])
     assert e.value.status == 4
 
 
-@pytest.mark.parametrize("dtype,result,m", [(np.float32, 1, 16384), (np.float64, 1, 8192)])
-def test_epoch_at_max_m(cuda, oracle, dtype, result, m):
-    """The largest m the C ABI accepts for a multiclass objective (the block
-    kernel's LDS at its limit, set by the data type); one more is refused
-    before any launch.  The epoch starts from a small random W (A = 0): from
+@pytest.mark.parametrize("dtype,result,m", [(np.float32, 1, 16384), (np.float32, 1, 16385),
+                                            (np.float32, 1, 40000), (np.float64, 1, 8192),
+                                            (np.float64, 1, 8193), (np.float64, 1, 20000)])
+def test_epoch_wide_rows_lds_and_global(cuda, oracle, dtype, result, m):
+    """Rows at the block kernel's LDS limit (16384 fp32, 8192 fp64) and
+    beyond it, where its vectors live in global memory; the C ABI refuses
+    m above 524280 (the rank update's grid) before any launch.  The epoch
+    starts from a small random W (A = 0): from
     W = 0 the first example's m - 1 off-label values are all equal, a tie
     whose branch in the top-k special cases turns on the last bit of sums
     over thousands of equal terms (summed in another order by the
@@ -328,25 +331,21 @@ def test_epoch_at_max_m(cuda, oracle, dtype, result, m):
         assert err <= base + 3 * E, f"m={m} {name}: |gpu - oracle| {err:.3e}"
         assert err_x <= base + 2 * E, f"m={m} {name}: |gpu - exact| {err_x:.3e}"
     assert np.abs(Ao).max() > 0.01
-    Xz = torch.zeros((4, 8), dtype=Xt.dtype, device=cuda)
-    with pytest.raises(sd.SdcaError) as e:
-        sd.epoch_features(("l2_hinge_topk_smooth", 1.0, 0.5, 3), Xz,
-                          torch.zeros((m + 1, 8), dtype=Xt.dtype, device=cuda),
-                          torch.zeros((4, m + 1), dtype=Xt.dtype, device=cuda), [0, 1, 2, 3])
-    assert e.value.status == 4
+    if m == 40000:
+        Xz = torch.zeros((4, 8), dtype=Xt.dtype, device=cuda)
+        with pytest.raises(sd.SdcaError) as e:
+            sd.epoch_features(("l2_hinge_topk_smooth", 1.0, 0.5, 3), Xz,
+                              torch.zeros((524281, 8), dtype=Xt.dtype, device=cuda),
+                              torch.zeros((4, 524281), dtype=Xt.dtype, device=cuda),
+                              [0, 1, 2, 3])
+        assert e.value.status == 4
 
 
 @pytest.mark.parametrize("obj", ML_OBJS)
-def test_epoch_multilabel_at_max_m(cuda, oracle, obj):
-    """The multilabel objectives keep the example's labels in LDS too: their
-    largest m in fp32 is 12200 (the hinges' two-block simplex over the LDS
-    column there), one more is refused before any launch."""
-    import torch
-    import libsdca_amd as sd
-    check_ml(oracle, cuda, obj, np.float32, 1, 24, 16, 12200, 45, epochs=1, max_labels=6)
-    with pytest.raises(sd.SdcaError) as e:
-        sd.epoch_features(obj, torch.zeros((4, 8), device=cuda),
-                          torch.zeros((12201, 8), device=cuda),
-                          torch.zeros((4, 12201), device=cuda), [0, 1, 2, 3],
-                          offsets=[0, 1, 2, 3, 4])
-    assert e.value.status == 4
+def test_epoch_multilabel_wide_rows(cuda, oracle, obj):
+    """The multilabel objectives keep the example's labels in LDS too: at
+    m = 12200 fp32 the block kernel's LDS is full (the hinges' two-block
+    simplex over the LDS column), at 12201 and 30000 its vectors and labels
+    are in global memory."""
+    for m, seed in ((12200, 45), (12201, 46), (30000, 47)):
+        check_ml(oracle, cuda, obj, np.float32, 1, 24, 16, m, seed, epochs=1, max_labels=6)

@@ -130,7 +130,8 @@ def test_epoch_kernel_host_staging(cuda, oracle):
 def test_epoch_kernel_order_repeats_and_errors(cuda, oracle):
     """A partial order that repeats examples inside a block and across a
     block boundary; examples outside the order keep a_i = 0; an index out of
-    range and a label out of range are reported as SDCA_ERR_LABELS."""
+    range and a label out of range are reported as SDCA_ERR_LABELS; m above
+    524280 is refused."""
     import torch
     import libsdca_amd as sd
     n, m = 120, 15
@@ -153,7 +154,7 @@ def test_epoch_kernel_order_repeats_and_errors(cuda, oracle):
         sd.epoch_kernel(("l2_hinge_topk", 1.0, 1.0, 1), Kt, A, bad, order=[4])
     assert e.value.status == 8
     with pytest.raises(sd.SdcaError) as e:
-        sd.epoch_kernel(("l2_hinge_topk", 1.0, 1.0, 1), Kt, torch.zeros((n, 16385), device=cuda), y)
+        sd.epoch_kernel(("l2_hinge_topk", 1.0, 1.0, 1), Kt, torch.zeros((n, 524281), device=cuda), y)
     assert e.value.status == 4
 
 
@@ -167,6 +168,15 @@ def test_epoch_kernel_multilabel(cuda, oracle, obj, dtype, result):
     orders = [sd.epoch_order(n, e) for e in range(2)]
     Ag, _ = compare(oracle, cuda, obj, K, lab, m, result, orders, offsets=off, label="multilabel")
     assert not Ag[3].any()
+
+
+@pytest.mark.parametrize("obj", [OBJS[1], OBJS[4], OBJS[5]])
+def test_epoch_kernel_rows_beyond_lds(cuda, oracle, obj):
+    """m = 20,000 fp32: the block kernel's vectors in global memory."""
+    import libsdca_amd as sd
+    n, m = 48, 20000
+    K, y = kernel_problem(np.float32, n, 16, m, 71, kind="gauss")
+    compare(oracle, cuda, obj, K, y, m, 1, [sd.epoch_order(n, 0)], label="global rows")
 
 
 @pytest.mark.parametrize("obj", [OBJS[1], OBJS[4]])
