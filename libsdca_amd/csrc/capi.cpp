@@ -61,9 +61,10 @@ size_t dtype_size(int dt) { return dt == SDCA_F32 ? 4 : 8; }
 // capturable): warm the stream up with one call of the same size first.
 struct Workspace {
   // Slots: 0 deferred-column list, 1 scores, 2 evaluation scratch,
-  // 3 transposes, 4 epoch, 5 the library GEMM's workspace.
-  void* ptr[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-  size_t cap[6] = {0, 0, 0, 0, 0, 0};
+  // 3 transposes, 4 epoch, 5 the library GEMM's workspace, 6 the column
+  // slices of the prox beyond the LDS copy.
+  void* ptr[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  size_t cap[7] = {0, 0, 0, 0, 0, 0, 0};
   // Pinned host block for the evaluation's results: copies into it are
   // asynchronous, so the call waits once for all of them.
   void* host = nullptr;
@@ -294,14 +295,23 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
   // Above kRegMaxM rows a column is held by one workgroup, in LDS (the
   // sorted-column, wave-per-column and workgroup-per-column kernels).
   // Above that, the knapsack and entropic operators stream the column from
-  // global memory; the others refuse.
-  const bool streamed = m > max_rows(data) && stream_supported(op);
-  if (op != SDCA_PROX_LAMBERT_W_EXP && m > max_rows(data) && !streamed)
+  // global memory, the top-k, biased-knapsack and two-block simplex
+  // operators work on the column in device memory (sorted in a scratch
+  // slice, or read in place); the Lambert-map entropic ones refuse.
+  const bool wide = m > max_rows(data);
+  const bool streamed = wide && stream_supported(op);
+  const bool global_sorted = wide && (topk || reg_biased);
+  const bool global_two = wide && (op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT);
+  if (op != SDCA_PROX_LAMBERT_W_EXP && wide && !streamed && !global_sorted && !global_two)
     return fail(SDCA_ERR_NOT_IMPLEMENTED,
                 "m = %lld is above the %lld rows (%lld KiB per column) the GPU kernels hold for "
-                "this operator and element type (knapsack_eq, knapsack_le, entropy and "
-                "entropy_norm take any m)", (long long)m, (long long)max_rows(data),
-                (long long)(kMaxColumnBytes / 1024));
+                "this operator and element type (topk_entropy, topk_entropy_biased and "
+                "two_entropy; the other operators take any m)", (long long)m,
+                (long long)max_rows(data), (long long)(kMaxColumnBytes / 1024));
+  if (fixed_list && (global_sorted || op == SDCA_PROX_TWO_SIMPLEX_SORT) && wide)
+    return fail(SDCA_ERR_ARG_RANGE,
+                "sdca_prox_noalloc: m = %lld is above %lld rows, where this operator needs "
+                "allocated scratch", (long long)m, (long long)max_rows(data));
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const size_t bytes = static_cast<size_t>(m) * static_cast<size_t>(n) * dtype_size(data);
@@ -377,6 +387,31 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
 
   if (op == SDCA_PROX_LAMBERT_W_EXP) {
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
+  } else if (global_sorted || (global_two && op == SDCA_PROX_TWO_SIMPLEX_SORT)) {
+    // One column slice per workgroup, as many slices as fit 512 MiB (at
+    // least one), at most one per column and 4096.
+    size_t slice = static_cast<size_t>(m) * dtype_size(data);
+    if (global_sorted) {
+      size_t pow2 = 1;
+      while (pow2 < static_cast<size_t>(m)) pow2 <<= 1;
+      slice = pow2 * dtype_size(data);
+    }
+    int64_t slices = static_cast<int64_t>((size_t(512) << 20) / slice);
+    if (slices < 1) slices = 1;
+    if (slices > n) slices = n;
+    if (slices > 4096) slices = 4096;
+    void* scratch = nullptr;
+    rc = workspace(stream, 6, static_cast<size_t>(slices) * slice, &scratch);
+    if (rc) return rc;
+    const size_t bytes_s = static_cast<size_t>(slices) * slice;
+    if (global_sorted)
+      SDCA_HIP_TRY(launch_slow_global(a, scratch, bytes_s),
+                   "prox kernel (workgroup per column, column in device memory)");
+    else
+      SDCA_HIP_TRY(launch_two_sort_global(a, scratch, bytes_s),
+                   "two_simplex_sort kernel (column in device memory)");
+  } else if (global_two) {
+    SDCA_HIP_TRY(launch_two_global(a), "two_simplex kernel (column in device memory)");
   } else if (streamed) {
     SDCA_HIP_TRY(launch_stream(a), "prox kernel (column streamed from global memory)");
   } else if (op == SDCA_PROX_TWO_SIMPLEX_SORT && !reg_ok) {

@@ -77,6 +77,15 @@ hipError_t launch_topkent(const ProxLaunch& a);
 hipError_t launch_two(const ProxLaunch& a);
 // Workgroup-per-column kernel over the flagged list (all_columns: every column).
 hipError_t launch_slow(const ProxLaunch& a, bool all_columns);
+// Columns beyond the LDS copy, every column: the sorted-column kernel with
+// each workgroup's column sorted in a slice of scratch (device memory,
+// scratch_bytes; at least one slice of the next power of two above m
+// values), the sort-based two-block simplex likewise (slices of m values),
+// and the two-block simplex with its passes over the column in device
+// memory.
+hipError_t launch_slow_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes);
+hipError_t launch_two_sort_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes);
+hipError_t launch_two_global(const ProxLaunch& a);
 // Columns above max_rows(data) for the operators whose thresholds come from
 // sweeps alone (knapsack_eq, knapsack_le, entropy, entropy_norm): one
 // workgroup per column, the column re-read from global memory per sweep

@@ -24,14 +24,16 @@ namespace sdca_gpu {
 
 namespace {
 
-template <class D, class R>
+// GV: columns beyond the LDS; each workgroup sorts its column in its own
+// pow2-word slice of gscratch (device memory) instead.
+template <class D, class R, bool GV = false>
 __global__ void __launch_bounds__(256)
 prox_slow_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
                  ProxParamsT<R> pp, sdca_thresholds* __restrict__ thr,
                  int* __restrict__ slow, int all_columns, int pow2,
-                 sdca_prox_sets* __restrict__ sets) {
+                 sdca_prox_sets* __restrict__ sets, D* __restrict__ gscratch) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  D* s = reinterpret_cast<D*>(smem_raw);
+  D* s = GV ? gscratch + static_cast<int64_t>(blockIdx.x) * pow2 : reinterpret_cast<D*>(smem_raw);
   __shared__ R sh_t, sh_lo, sh_hi;
   const int m = static_cast<int>(m64);
   const int64_t count = all_columns ? n : static_cast<int64_t>(slow[0]);
@@ -127,7 +129,34 @@ hipError_t launch_slow_t(const ProxLaunch& a, bool all_columns) {
   hipLaunchKernelGGL((prox_slow_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
                      dim3(threads), static_cast<size_t>(pow2) * sizeof(D), a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n, pp,
-                     a.thr, a.slow, all_columns ? 1 : 0, pow2, a.sets);
+                     a.thr, a.slow, all_columns ? 1 : 0, pow2, a.sets, static_cast<D*>(nullptr));
+  return hipGetLastError();
+}
+
+// Every column, each sorted in a pow2-word slice of scratch (device memory;
+// scratch_bytes of it): one workgroup per slice.
+template <class D, class R>
+hipError_t launch_slow_global_t(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  ProxParamsT<R> pp;
+  pp.lo = static_cast<R>(a.lo);
+  pp.hi = static_cast<R>(a.hi);
+  pp.rhs = static_cast<R>(a.rhs);
+  const bool biased = a.op == OP_KNAPSACK_LE_BIASED || a.op == OP_TOPK_SIMPLEX_BIASED ||
+                      a.op == OP_TOPK_CONE_BIASED;
+  pp.rho = biased ? static_cast<R>(a.rho) : R(0);
+  pp.k = static_cast<int>(a.k);
+  pp.op = a.op;
+  pp.p = static_cast<int>(a.p);
+  int64_t pow2 = 1;
+  while (pow2 < a.m) pow2 <<= 1;
+  int64_t grid = static_cast<int64_t>(scratch_bytes / (static_cast<size_t>(pow2) * sizeof(D)));
+  if (grid > a.n) grid = a.n;
+  if (grid > 4096) grid = 4096;
+  if (grid < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((prox_slow_kernel<D, R, true>), dim3(static_cast<unsigned>(grid)),
+                     dim3(256), 0, a.stream, static_cast<const D*>(a.in), static_cast<D*>(a.out),
+                     a.m, a.n, pp, a.thr, a.slow, 1, static_cast<int>(pow2), a.sets,
+                     static_cast<D*>(scratch));
   return hipGetLastError();
 }
 
@@ -183,14 +212,16 @@ __device__ void two_sort_thresholds(const D* a, int p, const D* b, int q, R rhs,
 // Two-block simplex by sort and scan: one workgroup per column, the column
 // in LDS (m words) with each block sorted in place, one lane scans, the
 // workgroup clamps the column.
-template <class D, class R>
+template <class D, class R, bool GV = false>
 __global__ void __launch_bounds__(256)
 two_sort_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, R rhs,
                 int64_t p_all, const int64_t* __restrict__ col_p,
                 sdca_thresholds* __restrict__ thr, int* __restrict__ slow, int all_columns,
-                sdca_prox_sets* __restrict__ sets) {
+                sdca_prox_sets* __restrict__ sets, D* __restrict__ gscratch) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  D* sa = reinterpret_cast<D*>(smem_raw);
+  // GV: beyond the LDS, each workgroup's column in its m-word slice of
+  // gscratch (device memory).
+  D* sa = GV ? gscratch + static_cast<int64_t>(blockIdx.x) * m64 : reinterpret_cast<D*>(smem_raw);
   __shared__ R sh_ta, sh_tb;
   const int m = static_cast<int>(m64);
   const int64_t count = all_columns ? n : static_cast<int64_t>(slow[0]);
@@ -254,7 +285,75 @@ hipError_t launch_two_sort_t(const ProxLaunch& a, bool all_columns) {
                      dim3(256), static_cast<size_t>(a.m) * sizeof(D), a.stream,
                      static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n,
                      static_cast<R>(a.rhs), a.p, a.col_p, a.thr, a.slow, all_columns ? 1 : 0,
-                     a.sets);
+                     a.sets, static_cast<D*>(nullptr));
+  return hipGetLastError();
+}
+
+template <class D, class R>
+hipError_t launch_two_sort_global_t(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  int64_t grid = static_cast<int64_t>(scratch_bytes / (static_cast<size_t>(a.m) * sizeof(D)));
+  if (grid > a.n) grid = a.n;
+  if (grid > 4096) grid = 4096;
+  if (grid < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((two_sort_kernel<D, R, true>), dim3(static_cast<unsigned>(grid)), dim3(256),
+                     0, a.stream, static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n,
+                     static_cast<R>(a.rhs), a.p, a.col_p, a.thr, a.slow, 1, a.sets,
+                     static_cast<D*>(scratch));
+  return hipGetLastError();
+}
+
+// The two-block simplex (two_simplex.h:18-119) of one column per 256-thread
+// workgroup, its passes reading the column from device memory
+// (two_family_array): columns beyond the LDS.
+template <class D, class R>
+__global__ void __launch_bounds__(256)
+two_global_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
+                  ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
+                  sdca_thresholds* __restrict__ thr, sdca_prox_sets* __restrict__ sets) {
+  const int m = static_cast<int>(m64);
+  for (int64_t j = blockIdx.x; j < n; j += gridDim.x) {
+    const int p = clamp_split(col_p ? col_p[j] : static_cast<int64_t>(pp.p), m);
+    const D* col = in + j * m64;
+    const ColThr<R> th = two_family_array<256, D, R>(col, m, p, pp);
+    if (threadIdx.x == 0) {
+      if (thr) {
+        thr[2 * j] = sdca_thresholds{static_cast<double>(th.t), static_cast<double>(th.lo),
+                                     static_cast<double>(th.hi)};
+        thr[2 * j + 1] = sdca_thresholds{static_cast<double>(th.t2), static_cast<double>(th.lo2),
+                                         static_cast<double>(th.hi2)};
+      }
+      if (sets) {
+        sets[2 * j] = sdca_prox_sets{0, th.n_mid, th.branch, 0};
+        sets[2 * j + 1] = sdca_prox_sets{0, th.n_mid2, th.branch, 0};
+      }
+    }
+    // Every read of the column is behind the solve's last group sum; the
+    // clamp may then overwrite it (in == out).
+    __syncthreads();
+    const D ta = static_cast<D>(th.t), tb = static_cast<D>(th.t2), hi = static_cast<D>(th.hi);
+    const D he = D(0) < hi ? hi : D(0);
+    D* dst = out + j * m64;
+    for (int i = threadIdx.x; i < m; i += 256)
+      dst[i] = clamp_med3(col[i] - (i < p ? ta : tb), D(0), he);
+    __syncthreads();
+  }
+}
+
+template <class D, class R>
+hipError_t launch_two_global_t(const ProxLaunch& a) {
+  ProxParamsT<R> pp;
+  pp.lo = R(0);
+  pp.hi = static_cast<R>(a.rhs);
+  pp.rhs = static_cast<R>(a.rhs);
+  pp.rho = R(0);
+  pp.k = 1;
+  pp.rhs_k = R(0);
+  pp.op = a.op;
+  pp.p = static_cast<int>(a.p);
+  const int64_t grid = a.n < 4096 ? a.n : 4096;
+  hipLaunchKernelGGL((two_global_kernel<D, R>), dim3(static_cast<unsigned>(grid > 0 ? grid : 1)),
+                     dim3(256), 0, a.stream, static_cast<const D*>(a.in), static_cast<D*>(a.out),
+                     a.m, a.n, pp, a.col_p, a.thr, a.sets);
   return hipGetLastError();
 }
 
@@ -286,6 +385,38 @@ hipError_t launch_two_sort(const ProxLaunch& a, bool all_columns) {
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_two_sort_t<float, double>(a, all_columns);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_two_sort_t<double, double>(a, all_columns);
   if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_two_sort_t<double, float>(a, all_columns);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_slow_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32)
+    return launch_slow_global_t<float, float>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64)
+    return launch_slow_global_t<float, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64)
+    return launch_slow_global_t<double, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32)
+    return launch_slow_global_t<double, float>(a, scratch, scratch_bytes);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_two_sort_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32)
+    return launch_two_sort_global_t<float, float>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64)
+    return launch_two_sort_global_t<float, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64)
+    return launch_two_sort_global_t<double, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32)
+    return launch_two_sort_global_t<double, float>(a, scratch, scratch_bytes);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_two_global(const ProxLaunch& a) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32) return launch_two_global_t<float, float>(a);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_two_global_t<float, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_two_global_t<double, double>(a);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_two_global_t<double, float>(a);
   return hipErrorInvalidValue;
 }
 

@@ -439,20 +439,26 @@ ALL_OPS = ["knapsack_eq", "knapsack_le", "topk_simplex", "topk_cone", "entropy",
 
 
 STREAMED = ("knapsack_eq", "knapsack_le", "entropy", "entropy_norm")
+# Beyond 128 KiB: sorted in a slice of device memory, or (two_simplex) read
+# there in place.
+IN_MEMORY = ("topk_simplex", "topk_cone", "knapsack_le_biased", "topk_simplex_biased",
+             "topk_cone_biased", "two_simplex", "two_simplex_sort")
 
 
 def test_large_m_limits(cuda):
-    """Columns above 128 KiB (32768 fp32 rows, 16384 fp64 rows) are refused
-    with SDCA_ERR_NOT_IMPLEMENTED (4) by the operators that hold a column in
-    LDS; the knapsack and entropic operators stream it (their parity is in
-    test_streamed_columns) and the elementwise Lambert map has no column."""
+    """Columns above 128 KiB (32768 fp32 rows, 16384 fp64 rows): the knapsack
+    and entropic operators stream them (test_streamed_columns), the top-k,
+    biased and two-block simplex operators work on them in device memory
+    (test_columns_in_device_memory), the elementwise Lambert map has no
+    column, and the Lambert-map entropic operators refuse with
+    SDCA_ERR_NOT_IMPLEMENTED (4)."""
     import torch
     import libsdca_amd as sd
     for dt, npdt in ((torch.float32, np.float32), (torch.float64, np.float64)):
         m = MAX_ROWS[npdt] + 1
         x = torch.zeros((2, m), dtype=dt, device=cuda)
         for op in ALL_OPS:
-            if op in STREAMED:
+            if op in STREAMED or op in IN_MEMORY:
                 sd.prox(op, x, k=5, p=1, hi=1.0, rhs=1.0)
                 continue
             with pytest.raises(sd.SdcaError) as e:
@@ -489,6 +495,31 @@ def test_streamed_columns(cuda, oracle, op, kw, m, dtype, result):
         got, thr = run_gpu(op, x, result, cuda, **kw)
         parity(oracle, op, x, got, result, f"{op} streamed {name} m={m}", nthreads=6, **kw,
                thr=thr)
+
+
+@pytest.mark.parametrize("dtype,result,m", [(np.float32, F32, 40_000), (np.float32, F64, 40_000),
+                                            (np.float64, F64, 20_000)])
+@pytest.mark.parametrize("op,kw,kind", [
+    ("topk_simplex", dict(k=5, rhs=1.0), "label+2"),
+    ("topk_simplex", dict(k=20, rhs=1.0), "normal"),
+    ("topk_cone", dict(k=3), "normal"),
+    ("knapsack_le_biased", dict(lo=0.0, hi=1.0, rhs=1.0, rho=1.0), "normal"),
+    ("topk_simplex_biased", dict(k=5, rhs=1.0, rho=0.5), "label+2"),
+    ("topk_cone_biased", dict(k=3, rho=0.25), "normal"),
+    ("two_simplex", dict(rhs=1.0, p="third"), "normal"),
+    ("two_simplex", dict(rhs=2.0, col_p=True), "label+2"),
+    ("two_simplex_sort", dict(rhs=1.0, col_p=True), "normal"),
+    ("two_simplex_sort", dict(rhs=1.0, p="third"), "negative"),
+])
+def test_columns_in_device_memory(cuda, oracle, op, kw, kind, m, dtype, result):
+    """Columns beyond the 128 KiB an LDS copy holds, for the operators that
+    need the sorted column or several passes over it: sorted per workgroup
+    in a slice of device memory (the sorted-column kernel, the sort-based
+    two-block simplex), or, for the two-block simplex, its passes read the
+    column in place; against the oracle (topk_simplex.h:39-68,
+    topk_cone.h:58-157, knapsack_le_biased.h:10-130, two_simplex.h:18-119,
+    two_simplex_sort.h:15-111)."""
+    wide_case(cuda, oracle, op, kw, kind, m, dtype, result, 5)
 
 
 # One wide case per operator family: (op, kwargs, inputs).  col_p: a
