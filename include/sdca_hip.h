@@ -158,10 +158,9 @@ void sdca_prox_params_default(sdca_prox_params* params);
  * registers and LDS.  A column is held by one workgroup, in LDS up to 32768
  * rows of fp32 data and 16384 of fp64 (128 KiB of column).  Beyond that the
  * KNAPSACK_EQ, KNAPSACK_LE, ENTROPY and ENTROPY_NORM operators stream the
- * column from global memory, the top-k, biased and two-block simplex
- * operators sort it in (or read it from) device memory, all for any m; the
- * TOPK_ENTROPY, TOPK_ENTROPY_BIASED and TWO_ENTROPY operators return
- * SDCA_ERR_NOT_IMPLEMENTED (the elementwise LAMBERT_W_EXP takes any size).
+ * column from global memory and the others work on it in device memory
+ * (sorted in, copied to or read from it, in a scratch of up to 512 MiB per
+ * stream): every operator takes any m.
  */
 int sdca_prox(sdca_prox_op op, sdca_dtype data, sdca_dtype result,
               int64_t m, int64_t n, const void* in, void* out,

@@ -302,13 +302,10 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
   const bool streamed = wide && stream_supported(op);
   const bool global_sorted = wide && (topk || reg_biased);
   const bool global_two = wide && (op == SDCA_PROX_TWO_SIMPLEX || op == SDCA_PROX_TWO_SIMPLEX_SORT);
-  if (op != SDCA_PROX_LAMBERT_W_EXP && wide && !streamed && !global_sorted && !global_two)
-    return fail(SDCA_ERR_NOT_IMPLEMENTED,
-                "m = %lld is above the %lld rows (%lld KiB per column) the GPU kernels hold for "
-                "this operator and element type (topk_entropy, topk_entropy_biased and "
-                "two_entropy; the other operators take any m)", (long long)m,
-                (long long)max_rows(data), (long long)(kMaxColumnBytes / 1024));
-  if (fixed_list && (global_sorted || op == SDCA_PROX_TWO_SIMPLEX_SORT) && wide)
+  const bool global_wave = wide && ent_biased;
+  const bool global_topkent = wide && op == SDCA_PROX_TOPK_ENTROPY;
+  if (fixed_list && (global_sorted || global_wave || global_topkent ||
+                     op == SDCA_PROX_TWO_SIMPLEX_SORT) && wide)
     return fail(SDCA_ERR_ARG_RANGE,
                 "sdca_prox_noalloc: m = %lld is above %lld rows, where this operator needs "
                 "allocated scratch", (long long)m, (long long)max_rows(data));
@@ -387,19 +384,23 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
 
   if (op == SDCA_PROX_LAMBERT_W_EXP) {
     SDCA_HIP_TRY(launch_lambert(a), "lambert_w_exp kernel");
-  } else if (global_sorted || (global_two && op == SDCA_PROX_TWO_SIMPLEX_SORT)) {
-    // One column slice per workgroup, as many slices as fit 512 MiB (at
-    // least one), at most one per column and 4096.
+  } else if (global_sorted || global_wave || global_topkent ||
+             (global_two && op == SDCA_PROX_TWO_SIMPLEX_SORT)) {
+    // One column slice per workgroup (per wave for the wave kernels, in
+    // whole workgroups of four), as many slices as fit 512 MiB (at least
+    // one workgroup's), at most one per column and 4096.
     size_t slice = static_cast<size_t>(m) * dtype_size(data);
+    if (global_wave) slice = static_cast<size_t>((m + 3) & ~int64_t(3)) * dtype_size(data);
     if (global_sorted) {
       size_t pow2 = 1;
       while (pow2 < static_cast<size_t>(m)) pow2 <<= 1;
       slice = pow2 * dtype_size(data);
     }
     int64_t slices = static_cast<int64_t>((size_t(512) << 20) / slice);
-    if (slices < 1) slices = 1;
     if (slices > n) slices = n;
     if (slices > 4096) slices = 4096;
+    if (global_wave) slices = (slices + 3) & ~int64_t(3);  // whole workgroups of four waves
+    if (slices < (global_wave ? 4 : 1)) slices = global_wave ? 4 : 1;
     void* scratch = nullptr;
     rc = workspace(stream, 6, static_cast<size_t>(slices) * slice, &scratch);
     if (rc) return rc;
@@ -407,6 +408,15 @@ int prox_entry(int op_in, int data_in, int result_in, int64_t m, int64_t n, cons
     if (global_sorted)
       SDCA_HIP_TRY(launch_slow_global(a, scratch, bytes_s),
                    "prox kernel (workgroup per column, column in device memory)");
+    else if (op == SDCA_PROX_TWO_ENTROPY)
+      SDCA_HIP_TRY(launch_two_ent_global(a, scratch, bytes_s),
+                   "two_entropy kernel (column in device memory)");
+    else if (op == SDCA_PROX_TOPK_ENTROPY_BIASED)
+      SDCA_HIP_TRY(launch_ent_biased_global(a, scratch, bytes_s),
+                   "topk_entropy_biased kernel (column in device memory)");
+    else if (global_topkent)
+      SDCA_HIP_TRY(launch_topkent_global(a, scratch, bytes_s),
+                   "topk_entropy kernel (column in device memory)");
     else
       SDCA_HIP_TRY(launch_two_sort_global(a, scratch, bytes_s),
                    "two_simplex_sort kernel (column in device memory)");

@@ -33,15 +33,20 @@ constexpr int kEbMaxWaves = 4;
 // reuse: each wave also has an LDS array of R (after the waves' columns)
 // where the last pass leaves its W values, and the output map is a Taylor
 // step from them (lambert_w_exp_shift) instead of a new evaluation.
-template <class D, class R>
+//
+// GV (columns beyond the LDS): each wave's column copy is its stride_elems
+// slice of gscratch (device memory) instead; reuse is 0.  The wave's own
+// accesses to it are ordered as its LDS accesses are (one wavefront).
+template <class D, class R, bool GV = false>
 __global__ void __launch_bounds__(64 * kEbMaxWaves)
 entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n, int k,
                R alpha, sdca_thresholds* __restrict__ thr, int stride_elems, int reuse,
-               sdca_prox_sets* __restrict__ sets) {
+               sdca_prox_sets* __restrict__ sets, D* __restrict__ gscratch) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
-  D* s = reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
+  D* s = GV ? gscratch + (static_cast<int64_t>(blockIdx.x) * waves + wave) * stride_elems
+            : reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
   R* const wl = reuse ? reinterpret_cast<R*>(smem_raw + static_cast<size_t>(waves) *
                                                             stride_elems * sizeof(D)) +
                             static_cast<int64_t>(wave) * stride_elems
@@ -78,16 +83,18 @@ entbias_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64
   }
 }
 
-template <class D, class R>
+template <class D, class R, bool GV = false>
 __global__ void __launch_bounds__(64 * kEbMaxWaves)
 twoent_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
               int64_t p_all, const int64_t* __restrict__ col_p, R alpha,
               sdca_thresholds* __restrict__ thr, int stride_elems, int reuse,
-              sdca_prox_sets* __restrict__ sets) {
+              sdca_prox_sets* __restrict__ sets, D* __restrict__ gscratch) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
-  D* s = reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
+  // GV: as in entbias_kernel.
+  D* s = GV ? gscratch + (static_cast<int64_t>(blockIdx.x) * waves + wave) * stride_elems
+            : reinterpret_cast<D*>(smem_raw) + static_cast<int64_t>(wave) * stride_elems;
   R* const wl = reuse ? reinterpret_cast<R*>(smem_raw + static_cast<size_t>(waves) *
                                                             stride_elems * sizeof(D)) +
                             static_cast<int64_t>(wave) * stride_elems
@@ -158,7 +165,45 @@ hipError_t launch_twoent_t(const ProxLaunch& a) {
   hipLaunchKernelGGL((twoent_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
                      waves * per_wave, a.stream, static_cast<const D*>(a.in),
                      static_cast<D*>(a.out), a.m, a.n, a.p, a.col_p, static_cast<R>(a.alpha),
-                     a.thr, stride, reuse ? 1 : 0, a.sets);
+                     a.thr, stride, reuse ? 1 : 0, a.sets, static_cast<D*>(nullptr));
+  return hipGetLastError();
+}
+
+// Columns beyond the LDS: four waves per workgroup, each with a slice of
+// scratch (as many workgroups as the scratch holds four slices, at most
+// one wave per column).
+template <class D>
+int64_t eb_global_grid(const ProxLaunch& a, size_t scratch_bytes, int stride) {
+  const int64_t slices = static_cast<int64_t>(scratch_bytes / (static_cast<size_t>(stride) *
+                                                               sizeof(D)));
+  int64_t grid = slices / kEbMaxWaves;
+  const int64_t need = (a.n + kEbMaxWaves - 1) / kEbMaxWaves;
+  if (grid > need) grid = need;
+  if (grid > 16384) grid = 16384;
+  return grid;
+}
+
+template <class D, class R>
+hipError_t launch_twoent_global_t(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  const int stride = static_cast<int>((a.m + 3) & ~int64_t(3));
+  const int64_t grid = eb_global_grid<D>(a, scratch_bytes, stride);
+  if (grid < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((twoent_kernel<D, R, true>), dim3(static_cast<unsigned>(grid)),
+                     dim3(64 * kEbMaxWaves), 0, a.stream, static_cast<const D*>(a.in),
+                     static_cast<D*>(a.out), a.m, a.n, a.p, a.col_p, static_cast<R>(a.alpha),
+                     a.thr, stride, 0, a.sets, static_cast<D*>(scratch));
+  return hipGetLastError();
+}
+
+template <class D, class R>
+hipError_t launch_entbias_global_t(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  const int stride = static_cast<int>((a.m + 3) & ~int64_t(3));
+  const int64_t grid = eb_global_grid<D>(a, scratch_bytes, stride);
+  if (grid < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((entbias_kernel<D, R, true>), dim3(static_cast<unsigned>(grid)),
+                     dim3(64 * kEbMaxWaves), 0, a.stream, static_cast<const D*>(a.in),
+                     static_cast<D*>(a.out), a.m, a.n, static_cast<int>(a.k),
+                     static_cast<R>(a.alpha), a.thr, stride, 0, a.sets, static_cast<D*>(scratch));
   return hipGetLastError();
 }
 
@@ -175,7 +220,8 @@ hipError_t launch_t(const ProxLaunch& a) {
   hipLaunchKernelGGL((entbias_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
                      waves * per_wave, a.stream, static_cast<const D*>(a.in),
                      static_cast<D*>(a.out), a.m, a.n, static_cast<int>(a.k),
-                     static_cast<R>(a.alpha), a.thr, stride, reuse ? 1 : 0, a.sets);
+                     static_cast<R>(a.alpha), a.thr, stride, reuse ? 1 : 0, a.sets,
+                     static_cast<D*>(nullptr));
   return hipGetLastError();
 }
 
@@ -186,6 +232,30 @@ hipError_t launch_two_ent(const ProxLaunch& a) {
   if (a.data == SDCA_F32 && a.result == SDCA_F64) return launch_twoent_t<float, double>(a);
   if (a.data == SDCA_F64 && a.result == SDCA_F64) return launch_twoent_t<double, double>(a);
   if (a.data == SDCA_F64 && a.result == SDCA_F32) return launch_twoent_t<double, float>(a);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_two_ent_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32)
+    return launch_twoent_global_t<float, float>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64)
+    return launch_twoent_global_t<float, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64)
+    return launch_twoent_global_t<double, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32)
+    return launch_twoent_global_t<double, float>(a, scratch, scratch_bytes);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_ent_biased_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32)
+    return launch_entbias_global_t<float, float>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64)
+    return launch_entbias_global_t<float, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64)
+    return launch_entbias_global_t<double, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32)
+    return launch_entbias_global_t<double, float>(a, scratch, scratch_bytes);
   return hipErrorInvalidValue;
 }
 

@@ -86,6 +86,14 @@ hipError_t launch_slow(const ProxLaunch& a, bool all_columns);
 hipError_t launch_slow_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes);
 hipError_t launch_two_sort_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes);
 hipError_t launch_two_global(const ProxLaunch& a);
+// The biased top-k entropy and the two-block entropy beyond the LDS: the
+// wave-per-column kernels with each wave's column copy in a slice of
+// scratch (device memory; slices of m rounded up to 4 values).
+hipError_t launch_ent_biased_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes);
+hipError_t launch_two_ent_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes);
+// The top-k entropy beyond the LDS: one workgroup per column, its copy in a
+// slice of scratch (m values).
+hipError_t launch_topkent_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes);
 // Columns above max_rows(data) for the operators whose thresholds come from
 // sweeps alone (knapsack_eq, knapsack_le, entropy, entropy_norm): one
 // workgroup per column, the column re-read from global memory per sweep

@@ -339,6 +339,114 @@ two_global_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, in
   }
 }
 
+// thresholds_topk_entropy (topk_entropy.h:20-76) of one column per
+// 256-thread workgroup, the column copied into its m-word slice of
+// gscratch (device memory), where the entries moved into U are set to -inf:
+// the steps of topkent_family (the register kernel's form) over the slice,
+// each maximum the first in index order, each log-sum-exp over the rest
+// with that maximum excluded.  Columns beyond the LDS.
+template <class D, class R>
+__device__ inline void slice_argmax(const D* s, int m, R& mx, int& at) {
+  R lm = -num<R>::inf();
+  int li = INT_MAX;
+  for (int i = threadIdx.x; i < m; i += 256) {
+    const R x = static_cast<R>(s[i]);
+    if (li == INT_MAX || x > lm) {
+      lm = x;
+      li = i;
+    }
+  }
+  mx = group_max<256>(lm);
+  at = group_min<256>((li != INT_MAX && lm == mx) ? li : INT_MAX);
+}
+
+template <class D, class R>
+__device__ inline R slice_lse_excl(const D* s, int m, R mx, int at) {
+  R z = 0;
+  for (int i = threadIdx.x; i < m; i += 256) {
+    const R x = static_cast<R>(s[i]);
+    if (i != at && x > -num<R>::inf()) z += dexp(x - mx);
+  }
+  return group_sum<256>(z);
+}
+
+template <class D, class R>
+__global__ void __launch_bounds__(256)
+topkent_global_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64, int64_t n,
+                      int k, sdca_thresholds* __restrict__ thr,
+                      sdca_prox_sets* __restrict__ sets, D* __restrict__ gscratch) {
+  const int m = static_cast<int>(m64);
+  D* const s = gscratch + static_cast<int64_t>(blockIdx.x) * m64;
+  const R eps = R(16) * num<R>::eps();
+  const R K = static_cast<R>(k);
+  for (int64_t j = blockIdx.x; j < n; j += gridDim.x) {
+    const D* col = in + j * m64;
+    for (int i = threadIdx.x; i < m; i += 256) s[i] = col[i];
+    __syncthreads();
+    R mx;
+    int at;
+    slice_argmax<D, R>(s, m, mx, at);
+    R z = slice_lse_excl<D, R>(s, m, mx, at);
+    R log_z = mx + dlog1p(z);
+    const R l1 = dexp(-mx);
+    R t, hi;
+    int branch, n_u = 0;
+    if (k <= 1 || mx - eps <= log_z - dlog(K)) {
+      t = isfinite(l1) ? mx + dlog1p(z + l1) : R(0);
+      hi = R(1);
+      branch = SDCA_BRANCH_U_EMPTY;
+    } else {
+      R sum_u = 0, k_u = K;
+      for (int num_u = 1; num_u < k; ++num_u) {
+        const R min_u = mx;
+        sum_u += min_u;
+        ++n_u;
+        // every thread has read the slice (the last group sum) before the
+        // owner of the maximum removes it
+        if (static_cast<int>(threadIdx.x) == at % 256) s[at] = -num<D>::inf();
+        __syncthreads();
+        k_u -= R(1);
+        slice_argmax<D, R>(s, m, mx, at);
+        z = slice_lse_excl<D, R>(s, m, mx, at);
+        log_z = mx + dlog1p(z);
+        const R tt = log_z - dlog(k_u);
+        if (mx - eps <= tt && tt <= min_u + eps) break;
+      }
+      const R tmp = ((K - k_u) * log_z + k_u * dlog(k_u) - sum_u) / K;
+      if (tmp > mx) {
+        const R a = (R(1) + z) * dexp(mx - tmp);
+        t = tmp + dlog1p(a * K) - dlog(k_u);
+        hi = a / (R(1) + a * K);
+      } else {
+        const R a = dexp(tmp - mx) / K;
+        t = mx + dlog1p(z + a) - dlog(k_u / K);
+        hi = (R(1) + z) / ((R(1) + z + a) * K);
+      }
+      branch = SDCA_BRANCH_U_GROWN;
+    }
+    if (threadIdx.x == 0) {
+      if (thr) thr[j] = sdca_thresholds{static_cast<double>(t), 0.0, static_cast<double>(hi)};
+      if (sets) sets[j] = sdca_prox_sets{n_u, m - n_u, branch, 0};
+    }
+    const D td = static_cast<D>(t), hd = static_cast<D>(hi);
+    D* dst = out + j * m64;
+    for (int i = threadIdx.x; i < m; i += 256) dst[i] = clamp_ref(dexp(col[i] - td), D(0), hd);
+    __syncthreads();  // the slice's last reads before the next column's copy
+  }
+}
+
+template <class D, class R>
+hipError_t launch_topkent_global_t(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  int64_t grid = static_cast<int64_t>(scratch_bytes / (static_cast<size_t>(a.m) * sizeof(D)));
+  if (grid > a.n) grid = a.n;
+  if (grid > 4096) grid = 4096;
+  if (grid < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((topkent_global_kernel<D, R>), dim3(static_cast<unsigned>(grid)), dim3(256),
+                     0, a.stream, static_cast<const D*>(a.in), static_cast<D*>(a.out), a.m, a.n,
+                     static_cast<int>(a.k), a.thr, a.sets, static_cast<D*>(scratch));
+  return hipGetLastError();
+}
+
 template <class D, class R>
 hipError_t launch_two_global_t(const ProxLaunch& a) {
   ProxParamsT<R> pp;
@@ -409,6 +517,18 @@ hipError_t launch_two_sort_global(const ProxLaunch& a, void* scratch, size_t scr
     return launch_two_sort_global_t<double, double>(a, scratch, scratch_bytes);
   if (a.data == SDCA_F64 && a.result == SDCA_F32)
     return launch_two_sort_global_t<double, float>(a, scratch, scratch_bytes);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_topkent_global(const ProxLaunch& a, void* scratch, size_t scratch_bytes) {
+  if (a.data == SDCA_F32 && a.result == SDCA_F32)
+    return launch_topkent_global_t<float, float>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F32 && a.result == SDCA_F64)
+    return launch_topkent_global_t<float, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F64)
+    return launch_topkent_global_t<double, double>(a, scratch, scratch_bytes);
+  if (a.data == SDCA_F64 && a.result == SDCA_F32)
+    return launch_topkent_global_t<double, float>(a, scratch, scratch_bytes);
   return hipErrorInvalidValue;
 }
 

@@ -442,28 +442,26 @@ STREAMED = ("knapsack_eq", "knapsack_le", "entropy", "entropy_norm")
 # Beyond 128 KiB: sorted in a slice of device memory, or (two_simplex) read
 # there in place.
 IN_MEMORY = ("topk_simplex", "topk_cone", "knapsack_le_biased", "topk_simplex_biased",
-             "topk_cone_biased", "two_simplex", "two_simplex_sort")
+             "topk_cone_biased", "two_simplex", "two_simplex_sort", "topk_entropy",
+             "topk_entropy_biased", "two_entropy")
 
 
 def test_large_m_limits(cuda):
-    """Columns above 128 KiB (32768 fp32 rows, 16384 fp64 rows): the knapsack
-    and entropic operators stream them (test_streamed_columns), the top-k,
-    biased and two-block simplex operators work on them in device memory
-    (test_columns_in_device_memory), the elementwise Lambert map has no
-    column, and the Lambert-map entropic operators refuse with
-    SDCA_ERR_NOT_IMPLEMENTED (4)."""
+    """Columns above 128 KiB (32768 fp32 rows, 16384 fp64 rows) run on every
+    operator: the knapsack and entropic operators stream them
+    (test_streamed_columns), the others work on them in device memory
+    (test_columns_in_device_memory); the elementwise Lambert map has no
+    column.  A zero column of one more row than the LDS holds must come back
+    as each operator's projection of 0 without an error."""
     import torch
     import libsdca_amd as sd
     for dt, npdt in ((torch.float32, np.float32), (torch.float64, np.float64)):
         m = MAX_ROWS[npdt] + 1
         x = torch.zeros((2, m), dtype=dt, device=cuda)
         for op in ALL_OPS:
-            if op in STREAMED or op in IN_MEMORY:
-                sd.prox(op, x, k=5, p=1, hi=1.0, rhs=1.0)
-                continue
-            with pytest.raises(sd.SdcaError) as e:
-                sd.prox(op, x, k=5, p=1)
-            assert e.value.status == 4, op
+            assert op in STREAMED or op in IN_MEMORY, op
+            y = sd.prox(op, x.clone(), k=5, p=1, hi=1.0, rhs=1.0)
+            assert torch.isfinite(y).all(), op
         sd.prox("lambert_w_exp", x)
 
 
@@ -510,16 +508,32 @@ def test_streamed_columns(cuda, oracle, op, kw, m, dtype, result):
     ("two_simplex", dict(rhs=2.0, col_p=True), "label+2"),
     ("two_simplex_sort", dict(rhs=1.0, col_p=True), "normal"),
     ("two_simplex_sort", dict(rhs=1.0, p="third"), "negative"),
+    ("topk_entropy", dict(k=3), "normal"),
+    ("topk_entropy", dict(k=12), "label+2"),
+    ("two_entropy", dict(alpha=1.0, col_p=True), "normal"),
 ])
 def test_columns_in_device_memory(cuda, oracle, op, kw, kind, m, dtype, result):
     """Columns beyond the 128 KiB an LDS copy holds, for the operators that
     need the sorted column or several passes over it: sorted per workgroup
     in a slice of device memory (the sorted-column kernel, the sort-based
     two-block simplex), or, for the two-block simplex, its passes read the
-    column in place; against the oracle (topk_simplex.h:39-68,
+    column in place; the top-k entropy and the Lambert-map wave kernels on a
+    copy in device memory; against the oracle (topk_simplex.h:39-68,
     topk_cone.h:58-157, knapsack_le_biased.h:10-130, two_simplex.h:18-119,
-    two_simplex_sort.h:15-111)."""
+    two_simplex_sort.h:15-111, topk_entropy.h:20-76, two_entropy.h:131-231)."""
     wide_case(cuda, oracle, op, kw, kind, m, dtype, result, 5)
+
+
+@pytest.mark.parametrize("dtype,result,m", [(np.float32, F32, 40_000), (np.float64, F64, 20_000)])
+def test_topk_entropy_biased_in_device_memory(cuda, oracle, dtype, result, m):
+    """The biased top-k entropy (wave per column, the column copied into
+    device memory) beyond the LDS."""
+    x = inputs.normal(8, m, dtype, 183, 2.0)
+    x[:4, :3] += 8.0
+    assert entbias_settled(oracle, x, 1.5, result).all()
+    got, thr = run_gpu("topk_entropy_biased", x, result, cuda, k=4, alpha=1.5)
+    parity(oracle, "topk_entropy_biased", x, got, result, f"topk_entropy_biased m={m}",
+           nthreads=8, k=4, alpha=1.5, thr=thr)
 
 
 # One wide case per operator family: (op, kwargs, inputs).  col_p: a
