@@ -1365,9 +1365,13 @@ __device__ inline ColThr<R> topkent_family(const D (&v)[C], int m, int nvalid,
 // CA: the slots that may hold rows of block a (slot c holds row g + G c, so
 // c < ceil(p / G)); the passes over block a visit only those, and the joint
 // passes treat the others as block b alone.
+// Candidate slots per lane for block b's phase 1 (see two_family_slots).
+constexpr int kTwoCand = 4;
+
 template <int G, int C, int CA, class D, class R>
 __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
-                                             const ProxParamsT<R>& pp) {
+                                             const ProxParamsT<R>& pp, D* lds_col = nullptr,
+                                             D* lds_dummy = nullptr) {
   const R rhs = pp.rhs;
   const R eps = num<R>::eps() * dmax(R(1), rhs);
   const int g = static_cast<int>(threadIdx.x) % G;
@@ -1395,6 +1399,67 @@ __device__ inline ColThr<R> two_family_slots(const D (&v)[C], int m, int p,
     mx = group_max<G>(mx);
     maxs[b] = mx;
     R cut = mx - rhs;
+    if constexpr (CA == 1 && G <= 64 && C >= 8) {
+      // Block b of a column whose block a sits in slot 0 (the multilabel
+      // duals): every value the iteration can keep is above max - rhs, a
+      // few of the C slots on N(0,1) columns.  They are compacted through
+      // the column's LDS words (free: the slots are in registers, and the
+      // output is written from them) into kTwoCand slots per lane, and the
+      // iteration runs on those; more candidates than that take the passes
+      // over every slot below.  The sums are the same set's, in another
+      // order.
+      if (b == 1 && lds_col != nullptr) {
+        int cn = 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          cn += (!in_a(c) && static_cast<R>(v[c]) > cut) ? 1 : 0;
+        const int total = group_sum<G>(cn);
+        if (total <= G * kTwoCand) {
+          int pos = group_exclusive_scan<G>(cn, g);
+#pragma unroll
+          for (int c = 0; c < C; ++c) {
+            const bool pr = !in_a(c) && static_cast<R>(v[c]) > cut;
+            D* dst = pr ? lds_col + pos : lds_dummy;
+            *dst = v[c];
+            pos += pr ? 1 : 0;
+          }
+          group_lds_sync<G>();
+          R cand[kTwoCand];
+          R sb = 0;
+          int nb = 0;
+#pragma unroll
+          for (int q = 0; q < kTwoCand; ++q) {
+            const int i = g + G * q;
+            const D x = lds_col[i < total ? i : 0];
+            cand[q] = i < total ? static_cast<R>(x) : -num<R>::inf();
+            sb += i < total ? cand[q] : R(0);
+            nb += i < total ? 1 : 0;
+          }
+          group_sums<G>(sb, nb);
+          R tb = 0;
+          for (int it = 0; it <= m; ++it) {
+            tb = div_near(sb - rhs, static_cast<R>(nb));
+            R s2 = 0;
+            int n2 = 0;
+#pragma unroll
+            for (int q = 0; q < kTwoCand; ++q) {
+              const bool in = cand[q] > cut && cand[q] > tb;
+              s2 += in ? cand[q] : R(0);
+              n2 += in ? 1 : 0;
+            }
+            group_sums<G>(s2, n2);
+            if (n2 == nb) break;
+            cut = dmax(cut, tb);
+            sb = s2;
+            nb = n2;
+          }
+          cuts[b] = cut;
+          cnt[b] = nb;
+          res[b] = tb;
+          continue;
+        }
+      }
+    }
     R sb = 0;
     int nb = 0;
 #pragma unroll
@@ -1626,10 +1691,11 @@ __device__ inline ColThr<R> two_family_array(const D* x, int m, int p, const Pro
 // m = 200 rows), block a lies in slot 0 of every lane and the passes over it
 // are one slot long; the results are the same as the general form's.
 template <int G, int C, class D, class R>
-__device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const ProxParamsT<R>& pp) {
+__device__ inline ColThr<R> two_family(const D (&v)[C], int m, int p, const ProxParamsT<R>& pp,
+                                       D* lds_col = nullptr, D* lds_dummy = nullptr) {
   if constexpr (C > 1) {
     const int a_slots = __builtin_amdgcn_readfirstlane(group_max<64>((p + G - 1) / G));
-    if (a_slots <= 1) return two_family_slots<G, C, 1, D, R>(v, m, p, pp);
+    if (a_slots <= 1) return two_family_slots<G, C, 1, D, R>(v, m, p, pp, lds_col, lds_dummy);
   }
   return two_family_slots<G, C, C, D, R>(v, m, p, pp);
 }
@@ -1807,7 +1873,7 @@ __device__ __forceinline__ void columns_tile(unsigned char* smem_raw, int m, int
     th = topkent_family<G, C, D, R>(v, m, nvalid, pp);
   } else {
     if (col_p && active) p = clamp_split(col_p[j], m);
-    th = two_family<G, C, D, R>(v, m, p, pp);
+    th = two_family<G, C, D, R>(v, m, p, pp, col, lds_dummy);
   }
 
   // The threshold search may have used the column's LDS slots as scratch.
@@ -1951,9 +2017,15 @@ __device__ __forceinline__ void columns_tile(unsigned char* smem_raw, int m, int
 }
 
 // The batched kernel: a workgroup takes one tile (B columns): load, search,
-// map, store.
+// map, store.  The two-block simplex of 200-row fp32 columns (the
+// multilabel duals' shape, eight lanes of 25 slots) asks for five waves per
+// SIMD: left alone the compiler takes 98 VGPRs (four waves), with the hint
+// 71, no spills, and the column kernel runs 3-7 % faster (0.1455 -> 0.141 ms
+// per 500,000 columns, 0.154 -> 0.143 ms over the first steps).
 template <int FAM, int KM, class D, class R, int G, int C, int BT, bool FULL>
-__global__ void __launch_bounds__(BT)
+__global__ void __launch_bounds__(BT) __attribute__((amdgpu_waves_per_eu(
+    (FAM == FAM_TWO && BT == 64 && G == 8 && C == 25 && sizeof(D) == 4 && sizeof(R) == 4)
+        ? 5 : 1)))
 prox_columns_kernel(const D* __restrict__ in, D* __restrict__ out, int64_t m64,
                     int64_t n, ProxParamsT<R> pp, const int64_t* __restrict__ col_p,
                     sdca_thresholds* __restrict__ thr, int* __restrict__ slow,
