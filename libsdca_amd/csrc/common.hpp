@@ -422,10 +422,68 @@ __device__ inline T lanes_sum(T x) {
   if constexpr (G >= 2) x += xor_lane<1, VALU>(x);
   return x;
 }
+// The total of the 64 lanes of a wave by gfx9's DPP row reduction: pairs
+// and quads by quad_perm, each 16-lane row by row_ror 4 and 8, rows 1 and 3
+// add the last lane of rows 0 and 2 (row_bcast:15), rows 2 and 3 the last
+// lane of the first half (row_bcast:31); lane 63 then holds the total and
+// readlane gives every lane its bits.  Six DPP adds and a readlane against
+// the butterfly's eighteen exchanges, moves and adds: the workgroup-wide
+// reductions are latency-bound chains in one wave per SIMD.
+template <int CTRL, int RM, bool B>
+__device__ inline int dpp_bits(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, RM, 0xF, B);
+}
+template <int CTRL, int RM, bool B>
+__device__ inline int dpp_add(int v) { return v + dpp_bits<CTRL, RM, B>(v); }
+template <int CTRL, int RM, bool B>
+__device__ inline float dpp_add(float v) {
+  return v + __int_as_float(dpp_bits<CTRL, RM, B>(__float_as_int(v)));
+}
+template <int CTRL, int RM, bool B>
+__device__ inline double dpp_add(double v) {
+  const long long u = __double_as_longlong(v);
+  const int lo = dpp_bits<CTRL, RM, B>(static_cast<int>(u & 0xffffffffll));
+  const int hi = dpp_bits<CTRL, RM, B>(static_cast<int>(u >> 32));
+  return v + __longlong_as_double((static_cast<long long>(hi) << 32) |
+                                  static_cast<long long>(static_cast<unsigned>(lo)));
+}
+__device__ inline int lane63(int x) { return __builtin_amdgcn_readlane(x, 63); }
+__device__ inline float lane63(float x) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+__device__ inline double lane63(double x) {
+  const long long u = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffll), 63);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(u >> 32), 63);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) |
+                              static_cast<long long>(static_cast<unsigned>(lo)));
+}
+// Lane l's value (l uniform) in every lane.
+__device__ inline float read_lane(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+__device__ inline double read_lane(double x, int l) {
+  const long long u = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffll), l);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(u >> 32), l);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) |
+                              static_cast<long long>(static_cast<unsigned>(lo)));
+}
+template <class T>
+__device__ inline T wave_total(T x) {
+  x = dpp_add<0xB1, 0xF, true>(x);    // quad_perm [1,0,3,2]
+  x = dpp_add<0x4E, 0xF, true>(x);    // quad_perm [2,3,0,1]
+  x = dpp_add<0x124, 0xF, true>(x);   // row_ror:4
+  x = dpp_add<0x128, 0xF, true>(x);   // row_ror:8
+  x = dpp_add<0x142, 0xA, false>(x);  // row_bcast:15 into rows 1 and 3
+  x = dpp_add<0x143, 0xC, false>(x);  // row_bcast:31 into rows 2 and 3
+  return lane63(x);
+}
+
 template <int G, class T>
 __device__ inline T group_sum(T x) {
   if constexpr (G > 64) {
-    return workgroup_combine<G>(lanes_sum<64, true>(x), [](T a, T b) { return a + b; });
+    return workgroup_combine<G>(wave_total(x), [](T a, T b) { return a + b; });
   } else {
     return lanes_sum<G, false>(x);
   }
@@ -456,7 +514,7 @@ __device__ inline void group_sums(T&... x) {
   static_assert(sizeof...(T) <= 8, "at most 8 values per exchange");
   if constexpr (G > 64) {
     __shared__ unsigned long long slots[kMaxGroupWaves][8];
-    ((x = lanes_sum<64, true>(x)), ...);
+    ((x = wave_total(x)), ...);
     __syncthreads();  // the previous exchange's readers are done with the slots
     if ((threadIdx.x & 63) == 0) {
       const int w = static_cast<int>(threadIdx.x) >> 6;

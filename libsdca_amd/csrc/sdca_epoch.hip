@@ -68,6 +68,13 @@ __host__ __device__ constexpr bool epoch_delta_in_lds(int PF) {
   return PF > 0 && (sizeof(D) == 4 ? PF <= 4 : PF <= 1);
 }
 
+// Words of the block's delta rows in LDS: kEpochBlock rows of m and the
+// padding that the last row's unclamped slot reads run into (the thread
+// slots cover kEpochThreads PF >= m columns).
+__host__ __device__ inline int epoch_dx_words(int m, int PF) {
+  return kEpochBlock * m + (kEpochThreads * PF > m ? kEpochThreads * PF - m : 0);
+}
+
 // Words of the thresholds' column in LDS: m values, or G C for the register
 // form, whose LDS scratch is the slot layout of the whole workgroup.
 __host__ __device__ inline int epoch_column_words(int m, int C) {
@@ -187,7 +194,7 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
   D* const Dx = DL ? dummy + G : Delta;  // the block's delta rows
   // the example's labels (multilabel), m ints after the D words
   int* const lab = GV ? reinterpret_cast<int*>(cb + cw)
-                      : reinterpret_cast<int*>(dummy + G + (DL ? kEpochBlock * m : 0));
+                      : reinterpret_cast<int*>(dummy + G + (DL ? epoch_dx_words(m, PF) : 0));
   __shared__ R sh_t, sh_lo, sh_hi;
   __shared__ int sh_slow;
   __shared__ D sh_vy;
@@ -325,8 +332,14 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
     }
     if constexpr (PF > 0) {
       // The corrections row by row in increasing r, kFixRows rows' loads at
-      // a time (the same sequence of subtractions per entry).
-      unsigned rem = changed & ((1u << k) - 1u);
+      // a time (the same sequence of subtractions per entry).  The row set
+      // is uniform: readfirstlane keeps it and the row indices in scalar
+      // registers, and G_rk comes from lane r's copy of column k of the Gram
+      // matrix (one LDS read per example) by readlane.  Rows in LDS are read
+      // unclamped (the padding after the last row holds the tail past m), so
+      // a row's slots are one address with constant offsets.
+      const D gk = g_all[(lane < nb ? lane : 0) * nb + k];
+      unsigned rem = __builtin_amdgcn_readfirstlane(changed & ((1u << k) - 1u));
       while (rem != 0u) {
         int rr[kFixRows];
         D g[kFixRows];
@@ -334,13 +347,15 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
         for (int b = 0; b < kFixRows; ++b) {
           rr[b] = rem != 0u ? __builtin_ctz(rem) : -1;
           rem &= rem - 1u;
-          g[b] = rr[b] >= 0 ? g_all[rr[b] * nb + k] : D(0);
+          g[b] = rr[b] >= 0 ? read_lane(gk, rr[b]) : D(0);
         }
         D dv[kFixRows][PQ];
 #pragma unroll
         for (int b = 0; b < kFixRows; ++b) {
           const D* drr = Dx + static_cast<int64_t>(rr[b] >= 0 ? rr[b] : 0) * m;
-          for_cols<PF>(tid, m, [&](int j, int q, bool ok) { dv[b][q] = drr[ok ? j : m - 1]; });
+          for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
+            dv[b][q] = drr[(DL || ok) ? j : m - 1];
+          });
         }
 #pragma unroll
         for (int b = 0; b < kFixRows; ++b) {
@@ -842,9 +857,10 @@ rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __re
 // thresholds' column, the per-thread dummy words, the block's delta rows
 // where they always fit (the score corrections then read LDS instead of
 // global memory) and, for the multilabel families, the example's labels.
-__host__ inline size_t block_lds_bytes(size_t es, int m, int C, bool delta_in_lds, bool ml) {
+__host__ inline size_t block_lds_bytes(size_t es, int m, int C, int PF, bool delta_in_lds,
+                                      bool ml) {
   size_t lds = (static_cast<size_t>((m + 3) & ~3) + epoch_column_words(m, C) + kEpochThreads) * es;
-  if (delta_in_lds) lds += static_cast<size_t>(kEpochBlock) * static_cast<size_t>(m) * es;
+  if (delta_in_lds) lds += static_cast<size_t>(epoch_dx_words(m, PF)) * es;
   if (ml) lds += static_cast<size_t>(m) * sizeof(int);
   return lds;
 }
@@ -855,7 +871,7 @@ hipError_t launch_block(const D* S, const D* Gm, int64_t q0, int nb, const D* no
                         D* gv) {
   const int m = static_cast<int>(a.m);
   constexpr bool ml = FK == kFamMlHinge || FK == kFamMlEnt;
-  const size_t lds = block_lds_bytes(sizeof(D), m, C, epoch_delta_in_lds<D>(PF), ml);
+  const size_t lds = block_lds_bytes(sizeof(D), m, C, PF, epoch_delta_in_lds<D>(PF), ml);
   if (lds > kEpochLdsBytes) {
     // Rows beyond the LDS: the PF = 0 form with its vectors in gv (the
     // workspace holds epoch_gv_words(m) words there).
