@@ -837,20 +837,23 @@ rank_update_kernel(D* __restrict__ W, const D* __restrict__ Delta, const D* __re
   __syncthreads();
   const int64_t l = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (l >= d) return;
+  // Every load is issued before the arithmetic (the kRankJ elements of W
+  // with the block's x values), so a thread waits for memory once.
   D xk[kEpochBlock];
 #pragma unroll
   for (int k = 0; k < kEpochBlock; ++k) xk[k] = (k < nb) ? X[rows[k] * d + l] : D(0);
+  D w[kRankJ];
+#pragma unroll
+  for (int jj = 0; jj < kRankJ; ++jj) w[jj] = (j0 + jj < m) ? W[(j0 + jj) * d + l] : D(0);
 #pragma unroll
   for (int jj = 0; jj < kRankJ; ++jj) {
-    const int64_t j = j0 + jj;
-    if (j < m) {
-      D w = W[j * d + l];
 #pragma unroll
-      for (int k = 0; k < kEpochBlock; ++k)
-        if (k < nb) w = w - xk[k] * dl[k][jj];
-      W[j * d + l] = w;
-    }
+    for (int k = 0; k < kEpochBlock; ++k)
+      if (k < nb) w[jj] = w[jj] - xk[k] * dl[k][jj];
   }
+#pragma unroll
+  for (int jj = 0; jj < kRankJ; ++jj)
+    if (j0 + jj < m) W[(j0 + jj) * d + l] = w[jj];
 }
 
 // Dynamic LDS of the block kernel: the example's vector (m words), the
