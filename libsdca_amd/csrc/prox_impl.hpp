@@ -762,7 +762,22 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
 #pragma unroll
       for (int c = 0; c < C; ++c) cn += (static_cast<R>(v[c]) > cut) ? 1 : 0;
     }
-    const int total = group_sum<G>(cn);
+    // A workgroup-wide group forms the column total in the same exchange as
+    // the count (one barrier pair instead of two when the candidates do not
+    // fit, as in the epoch's columns; the same bits as total_sum).
+    R all_wg = 0;
+    int total;
+    if constexpr (G > 64) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const R x = static_cast<R>(v[c]);
+        all_wg += (c < nvalid && x > -num<R>::inf()) ? x : R(0);
+      }
+      total = cn;
+      group_sums<G>(total, all_wg);
+    } else {
+      total = group_sum<G>(cn);
+    }
     if (total <= G * CC) {
       // Branch-free compaction: every slot is stored, non-candidates to the
       // lane's own dummy word (distinct per lane, so no bank serialisation).
@@ -817,6 +832,11 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
       }
       return knapsack_eq_regs<G, CC, D, R>(cand, total, total, csum, R(0), hi, rhs, ucut, n_u0,
                                            sum_u0);
+    }
+    if constexpr (G > 64) {
+      return knapsack_eq_regs<G, C, D, R, LDS_FALLBACK>(
+          v, m, nvalid, all_wg, R(0), hi, rhs, num<R>::inf(), 0, R(0),
+          lds_col + static_cast<int>(threadIdx.x) % G, lds_dummy);
     }
   }
   const R all = total_sum<G, C, D, R>(v, nvalid);
