@@ -762,19 +762,19 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
 #pragma unroll
       for (int c = 0; c < C; ++c) cn += (static_cast<R>(v[c]) > cut) ? 1 : 0;
     }
-    // A workgroup-wide group forms the column total in the same exchange as
-    // the count (one barrier pair instead of two when the candidates do not
-    // fit, as in the epoch's columns; the same bits as total_sum).
-    R all_wg = 0;
+    // A workgroup-wide group forms the candidates' sum in the same exchange
+    // as their count (for the fixing over more candidates than registers,
+    // below).
+    R cand_wg = 0;
     int total;
     if constexpr (G > 64) {
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const R x = static_cast<R>(v[c]);
-        all_wg += (c < nvalid && x > -num<R>::inf()) ? x : R(0);
+        cand_wg += (c < nvalid && x > cut) ? x : R(0);
       }
       total = cn;
-      group_sums<G>(total, all_wg);
+      group_sums<G>(total, cand_wg);
     } else {
       total = group_sum<G>(cn);
     }
@@ -834,8 +834,25 @@ __device__ inline KnapState<R> topk_knapsack(const D (&v)[C], const D (&top)[L],
                                            sum_u0);
     }
     if constexpr (G > 64) {
+      // More candidates than registers on a workgroup-wide group (the
+      // epoch's columns): the same fixing over the candidates in their
+      // slots, the others left out as padding (they end at the lower bound,
+      // 0), and the upper values of the top list fixed at the start, as the
+      // register path does; fewer passes than the fixing over every value.
+      D w[C];
+#pragma unroll
+      for (int c = 0; c < C; ++c) w[c] = (static_cast<R>(v[c]) > cut) ? v[c] : -num<D>::inf();
+      const R ucut = kth + hi + slack;
+      int n_u0 = 0;
+      R sum_u0 = 0;
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        const bool u = static_cast<R>(top[i]) > ucut;
+        n_u0 += u ? 1 : 0;
+        sum_u0 += u ? static_cast<R>(top[i]) : R(0);
+      }
       return knapsack_eq_regs<G, C, D, R, LDS_FALLBACK>(
-          v, m, nvalid, all_wg, R(0), hi, rhs, num<R>::inf(), 0, R(0),
+          w, total, nvalid, cand_wg, R(0), hi, rhs, ucut, n_u0, sum_u0,
           lds_col + static_cast<int>(threadIdx.x) % G, lds_dummy);
     }
   }
