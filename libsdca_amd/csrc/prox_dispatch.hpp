@@ -103,6 +103,12 @@ hipError_t launch_by_m(const ProxLaunch& a) {
   if constexpr (FAM == FAM_ENT || FAM == FAM_TOPKENT || FAM == FAM_TWO) {
     if (a.m > kRegMaxM) return launch_wide<FAM, KM, D, R>(a);
   }
+  // The knapsack family's smallest columns (C1: m = 10) in exactly ten
+  // slots: every pass of the variable fixing touches the column's own
+  // values only.
+  if constexpr (FAM == FAM_KNAP) {
+    if (a.m <= 10) return launch_one<FAM, KM, D, R, 1, 10>(a);
+  }
   if (a.m <= 16) return launch_one<FAM, KM, D, R, 1, 16>(a);
   if (a.m <= 64) return launch_one<FAM, KM, D, R, 4, 16>(a);
   if (a.m <= 100) return launch_one<FAM, KM, D, R, 4, 25>(a);
