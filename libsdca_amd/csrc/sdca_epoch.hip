@@ -338,28 +338,31 @@ epoch_block_kernel(const D* __restrict__ S, const D* __restrict__ Gm,
       // matrix (one LDS read per example) by readlane.  Rows in LDS are read
       // unclamped (the padding after the last row holds the tail past m), so
       // a row's slots are one address with constant offsets.
+      // Past the last row the index reads as 31 (ctz of the guard bit; row
+      // 31 and lane 31 exist, and its values are not used).
       const D gk = g_all[(lane < nb ? lane : 0) * nb + k];
       unsigned rem = __builtin_amdgcn_readfirstlane(changed & ((1u << k) - 1u));
-      while (rem != 0u) {
+      const int nrows = __builtin_popcount(rem);
+      for (int base = 0; base < nrows; base += kFixRows) {
         int rr[kFixRows];
         D g[kFixRows];
 #pragma unroll
         for (int b = 0; b < kFixRows; ++b) {
-          rr[b] = rem != 0u ? __builtin_ctz(rem) : -1;
+          rr[b] = __builtin_ctz(rem | 0x80000000u);
           rem &= rem - 1u;
-          g[b] = rr[b] >= 0 ? read_lane(gk, rr[b]) : D(0);
+          g[b] = read_lane(gk, rr[b]);
         }
         D dv[kFixRows][PQ];
 #pragma unroll
         for (int b = 0; b < kFixRows; ++b) {
-          const D* drr = Dx + static_cast<int64_t>(rr[b] >= 0 ? rr[b] : 0) * m;
+          const D* drr = Dx + static_cast<int64_t>(rr[b]) * m;
           for_cols<PF>(tid, m, [&](int j, int q, bool ok) {
             dv[b][q] = drr[(DL || ok) ? j : m - 1];
           });
         }
 #pragma unroll
         for (int b = 0; b < kFixRows; ++b) {
-          if (rr[b] >= 0) {
+          if (base + b < nrows) {
 #pragma unroll
             for (int q = 0; q < PF; ++q) scur[q] -= g[b] * dv[b][q];
           }
